@@ -1,0 +1,26 @@
+"""atlas_rnn_amd: MI355X-native memory-layer recurrence of atlas-rnn's Titans/OmegaNet RNN cells.
+
+The hot path (delta, window aggregation, scalar-gated momentum/state scan, retrieval, and their
+backward) runs as hand-written gfx950 HIP kernels in libatlas_mem.so behind the C ABI of
+include/atlas_mem.h. Module classes mirror atlas_pytorch.rnn_memory / omega / affine_scan.
+"""
+
+from .functional import (  # noqa: F401
+    memory_recurrence,
+    AtlasOmegaFunction,
+    atlas_omega_forward,
+    check_cuda_availability,
+    assoc_scan,
+    AssocScan,
+    window_sum,
+)
+
+__all__ = [
+    "memory_recurrence",
+    "AtlasOmegaFunction",
+    "atlas_omega_forward",
+    "check_cuda_availability",
+    "assoc_scan",
+    "AssocScan",
+    "window_sum",
+]

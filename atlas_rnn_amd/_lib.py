@@ -1,0 +1,118 @@
+"""ctypes binding of libatlas_mem.so (the C ABI in include/atlas_mem.h).
+
+The structs below mirror the header field by field. Loading fails loudly when the library
+has not been built: there is no fallback implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libatlas_mem.so")
+
+ABI_VERSION = 1
+
+OK = 0
+ERR_UNSUPPORTED = 6
+
+DT_F32 = 0
+DT_BF16 = 1
+
+GATE_NONE = 0
+GATE_TOKEN = 1
+GATE_LAG = 2
+
+MAP_OFF = 0
+MAP_ELEMENTWISE = 1
+
+# every symbol include/atlas_mem.h declares
+EXPORTED_SYMBOLS = (
+    "atlas_mem_abi_version",
+    "atlas_mem_strerror",
+    "atlas_mem_validate",
+    "atlas_mem_saved_bytes",
+    "atlas_mem_bwd_workspace_bytes",
+    "atlas_mem_fwd",
+    "atlas_mem_bwd",
+    "atlas_scan_fwd",
+    "atlas_scan_bwd",
+    "atlas_window_sum",
+    "atlas_mem_mfma_selftest",
+)
+
+
+class Problem(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_int32) for name in (
+        "abi_version", "bh", "seq_len", "d_k", "d_v", "window", "momentum", "gate_mode",
+        "map_mode", "map_degree", "has_buffer", "clamp_every", "clamp_final", "dtype")]
+
+
+class FwdArgs(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in (
+        "k", "q", "v", "lr", "decay", "beta", "gate", "S_ref", "S0", "Z0", "buffer_in",
+        "y", "S_T", "Z_T", "buffer_out")]
+
+
+class BwdArgs(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in (
+        "k", "q", "v", "lr", "decay", "beta", "gate", "S_ref", "S0", "Z0", "buffer_in",
+        "dy", "dS_T", "dZ_T", "dbuffer_out",
+        "dk", "dq", "dv", "dlr", "ddecay", "dbeta", "dgate",
+        "dS_ref", "dS0", "dZ0", "dbuffer_in")]
+
+
+_LIB = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def load(path: str | None = None) -> ctypes.CDLL:
+    """Load (once) and type the C ABI. Raises LibraryMissing if the .so is not built."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        raise LibraryMissing(
+            f"{p} is not built; run `python -m atlas_rnn_amd.build` (hipcc, gfx950). "
+            "atlas_rnn_amd has no CPU fallback.")
+    lib = ctypes.CDLL(p)
+    vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
+    P = ctypes.POINTER(Problem)
+    lib.atlas_mem_abi_version.restype = i32
+    lib.atlas_mem_abi_version.argtypes = []
+    lib.atlas_mem_strerror.restype = ctypes.c_char_p
+    lib.atlas_mem_strerror.argtypes = [i32]
+    lib.atlas_mem_validate.restype = i32
+    lib.atlas_mem_validate.argtypes = [P]
+    lib.atlas_mem_saved_bytes.restype = sz
+    lib.atlas_mem_saved_bytes.argtypes = [P]
+    lib.atlas_mem_bwd_workspace_bytes.restype = sz
+    lib.atlas_mem_bwd_workspace_bytes.argtypes = [P]
+    lib.atlas_mem_fwd.restype = i32
+    lib.atlas_mem_fwd.argtypes = [P, ctypes.POINTER(FwdArgs), vp, vp]
+    lib.atlas_mem_bwd.restype = i32
+    lib.atlas_mem_bwd.argtypes = [P, ctypes.POINTER(BwdArgs), vp, vp, sz, vp]
+    lib.atlas_scan_fwd.restype = i32
+    lib.atlas_scan_fwd.argtypes = [i32, i64, i64, i64, vp, vp, vp, vp, vp]
+    lib.atlas_scan_bwd.restype = i32
+    lib.atlas_scan_bwd.argtypes = [i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.atlas_window_sum.restype = i32
+    lib.atlas_window_sum.argtypes = [i32, i64, i64, i64, i32, i32, vp, vp, vp]
+    lib.atlas_mem_mfma_selftest.restype = i32
+    lib.atlas_mem_mfma_selftest.argtypes = [i32, vp, vp, vp, vp]
+    if lib.atlas_mem_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{p}: ABI version {lib.atlas_mem_abi_version()} != {ABI_VERSION}")
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    if status != OK:
+        msg = load().atlas_mem_strerror(status).decode()
+        raise RuntimeError(f"{what} failed: {msg} (status {status})")

@@ -1,0 +1,258 @@
+// abi.hip - extern "C" entry points of libatlas_mem.so (declared in include/atlas_mem.h).
+#include <hip/hip_runtime.h>
+
+#include "../../include/atlas_mem.h"
+#include "mem_common.h"
+#include "mem_params.h"
+
+namespace atlas {
+template <typename T, int CH, int DK, int DV> hipError_t launch_fwd(const Geom&, const FwdPtrs<T>&, hipStream_t);
+template <typename T, int CH, int DK, int DV> hipError_t launch_bwd(const Geom&, const BwdPtrs<T>&, hipStream_t);
+
+// Diagnostic tile product C = A B^T (16 x 64 inputs) through the same fragment helpers.
+template <typename T>
+__global__ __launch_bounds__(64) void k_mfma_selftest(const T* A, const T* B, float* C) {
+  __shared__ __align__(16) T sa[16][64 + 8];
+  __shared__ __align__(16) T sb[16][64 + 8];
+  const int l = threadIdx.x;
+  for (int idx = l; idx < 16 * 64; idx += 64) {
+    sa[idx / 64][idx % 64] = A[idx];
+    sb[idx / 64][idx % 64] = B[idx];
+  }
+  __syncthreads();
+  typedef MM<T> M;
+  f32x4 acc = zero4(), acc2 = zero4();
+  for (int k0 = 0; k0 < 64; k0 += M::KS) {
+    acc = M::mma(frag_ld_row<T>(&sa[0][0], 64 + 8, 0, k0), frag_ld_row<T>(&sb[0][0], 64 + 8, 0, k0), acc);
+    // strided path: read B^T through (rs = 1, cs = row stride) of a transposed view of the same data
+    acc2 = M::mma(frag_ld<T>(&sa[0][0], 64 + 8, 1, 0, k0), frag_ld<T>(B, 64, 1, 0, k0), acc2);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * (l >> 4) + r, n = l & 15;
+    C[m * 16 + n] = acc[r];
+    C[256 + m * 16 + n] = acc2[r];
+  }
+}
+}  // namespace atlas
+
+using namespace atlas;
+
+namespace {
+
+struct Plan {
+  Geom g;
+  int CH;
+  bool ok;
+  int status;
+};
+
+int chunk_cap(int dtype) { return dtype == ATLAS_DT_BF16 ? 64 : 32; }
+
+Plan make_plan(const atlas_mem_problem* p) {
+  Plan pl{};
+  pl.ok = false;
+  pl.status = ATLAS_MEM_ERR_ARG;
+  if (!p) { pl.status = ATLAS_MEM_ERR_NULL; return pl; }
+  if (p->abi_version != ATLAS_MEM_ABI_VERSION) { pl.status = ATLAS_MEM_ERR_ABI; return pl; }
+  if (p->dtype != ATLAS_DT_F32 && p->dtype != ATLAS_DT_BF16) { pl.status = ATLAS_MEM_ERR_DTYPE; return pl; }
+  if (p->bh < 1 || p->seq_len < 1 || p->window < 1 || p->window > kMaxWindow) { pl.status = ATLAS_MEM_ERR_SHAPE; return pl; }
+  if (p->d_k != p->d_v || (p->d_k != 32 && p->d_k != 64)) { pl.status = ATLAS_MEM_ERR_SHAPE; return pl; }
+  if ((p->momentum != 0 && p->momentum != 1) || p->gate_mode < 0 || p->gate_mode > 2 ||
+      p->map_mode < 0 || p->map_mode > 1 || p->map_degree < 1 || p->map_degree > 16 ||
+      (p->has_buffer != 0 && p->has_buffer != 1) || p->clamp_every < 0 ||
+      (p->clamp_final != 0 && p->clamp_final != 1)) {
+    return pl;
+  }
+  if (p->has_buffer && p->window == 1) return pl;
+  const int CH = chunk_cap(p->dtype);
+  int Lc = CH;
+  if (p->clamp_every > 0 && p->clamp_every % CH != 0) {
+    Lc = 1;
+    for (int d = CH; d >= 1; --d) {
+      if (p->clamp_every % d == 0) { Lc = d; break; }
+    }
+  }
+  const int H = p->window - 1;
+  if (Lc < H) { pl.status = ATLAS_MEM_ERR_UNSUPPORTED; return pl; }
+  Geom& g = pl.g;
+  g.BH = p->bh; g.T = p->seq_len; g.DK = p->d_k; g.DV = p->d_v;
+  g.e = p->window; g.H = H; g.Lc = Lc; g.nc = (p->seq_len + Lc - 1) / Lc;
+  g.SP = ((H + CH + 31) / 32) * 32;
+  g.momentum = p->momentum; g.gate_mode = p->gate_mode; g.map_mode = p->map_mode;
+  g.map_deg = p->map_mode == ATLAS_MAP_ELEMENTWISE ? p->map_degree : 1;
+  g.has_buf = p->has_buffer; g.clamp_every = p->clamp_every; g.clamp_final = p->clamp_final;
+  pl.CH = CH;
+  pl.ok = true;
+  pl.status = ATLAS_MEM_OK;
+  return pl;
+}
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+struct BwdLayout {
+  size_t adj, dsref, tail, halo, dw, total;
+};
+
+BwdLayout bwd_layout(const Geom& g) {
+  BwdLayout L{};
+  const size_t st = (size_t)g.DV * g.DK * sizeof(float);
+  size_t off = 0;
+  L.adj = off; off += align256((size_t)g.BH * g.nc * 2 * st);
+  L.dsref = off; off += align256((size_t)g.BH * g.nc * st);
+  L.tail = off; off += align256((size_t)g.BH * g.nc * g.H * (g.DV + g.DK) * sizeof(float));
+  L.halo = off; off += align256((size_t)g.BH * g.nc * g.H * (g.DV + g.DK) * sizeof(float));
+  L.dw = off; off += align256(g.gate_mode == ATLAS_GATE_TOKEN ? (size_t)g.BH * g.T * g.e * sizeof(float) : 0);
+  L.total = off;
+  return L;
+}
+
+bool misaligned(const void* p, size_t a) { return p && (reinterpret_cast<uintptr_t>(p) % a) != 0; }
+
+template <typename T>
+int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream_t s) {
+  FwdPtrs<T> a;
+  a.k = (const T*)x->k; a.q = (const T*)x->q; a.v = (const T*)x->v;
+  a.lr = (const T*)x->lr; a.decay = (const T*)x->decay; a.beta = (const T*)x->beta; a.gate = (const T*)x->gate;
+  a.S_ref = x->S_ref; a.S0 = x->S0; a.Z0 = x->Z0; a.buf_in = x->buffer_in;
+  a.y = (T*)x->y; a.S_T = x->S_T; a.Z_T = x->Z_T; a.buf_out = x->buffer_out; a.saved = saved;
+  const Geom& g = pl.g;
+  hipError_t err = hipErrorInvalidValue;
+  if (g.DK == 64) {
+    if constexpr (sizeof(T) == 2) err = launch_fwd<T, 64, 64, 64>(g, a, s);
+    else err = launch_fwd<T, 32, 64, 64>(g, a, s);
+  } else if (g.DK == 32) {
+    if constexpr (sizeof(T) == 2) err = launch_fwd<T, 64, 32, 32>(g, a, s);
+    else err = launch_fwd<T, 32, 32, 32>(g, a, s);
+  }
+  return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
+}
+
+template <typename T>
+int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, void* ws, hipStream_t s) {
+  const Geom& g = pl.g;
+  const BwdLayout L = bwd_layout(g);
+  unsigned char* w = static_cast<unsigned char*>(ws);
+  BwdPtrs<T> a;
+  a.k = (const T*)x->k; a.q = (const T*)x->q; a.v = (const T*)x->v;
+  a.lr = (const T*)x->lr; a.decay = (const T*)x->decay; a.beta = (const T*)x->beta; a.gate = (const T*)x->gate;
+  a.S_ref = x->S_ref; a.S0 = x->S0; a.Z0 = x->Z0; a.buf_in = x->buffer_in;
+  a.dy = (const T*)x->dy; a.dS_T = x->dS_T; a.dZ_T = x->dZ_T; a.dbuf_out = x->dbuffer_out;
+  a.dk = (T*)x->dk; a.dq = (T*)x->dq; a.dv = (T*)x->dv; a.dlr = (T*)x->dlr; a.ddecay = (T*)x->ddecay;
+  a.dbeta = (T*)x->dbeta; a.dgate = (T*)x->dgate;
+  a.dS_ref = x->dS_ref; a.dS0 = x->dS0; a.dZ0 = x->dZ0; a.dbuf_in = x->dbuffer_in;
+  a.saved = saved;
+  a.adj = reinterpret_cast<float*>(w + L.adj);
+  a.dsref_part = reinterpret_cast<float*>(w + L.dsref);
+  a.tail_part = g.H > 0 ? reinterpret_cast<float*>(w + L.tail) : nullptr;
+  a.halo_part = g.H > 0 ? reinterpret_cast<float*>(w + L.halo) : nullptr;
+  a.dw = g.gate_mode == ATLAS_GATE_TOKEN ? reinterpret_cast<float*>(w + L.dw) : nullptr;
+  hipError_t err = hipErrorInvalidValue;
+  if (g.DK == 64) {
+    if constexpr (sizeof(T) == 2) err = launch_bwd<T, 64, 64, 64>(g, a, s);
+    else err = launch_bwd<T, 32, 64, 64>(g, a, s);
+  } else if (g.DK == 32) {
+    if constexpr (sizeof(T) == 2) err = launch_bwd<T, 64, 32, 32>(g, a, s);
+    else err = launch_bwd<T, 32, 32, 32>(g, a, s);
+  }
+  return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+int atlas_mem_abi_version(void) { return ATLAS_MEM_ABI_VERSION; }
+
+const char* atlas_mem_strerror(int status) {
+  switch (status) {
+    case ATLAS_MEM_OK: return "ok";
+    case ATLAS_MEM_ERR_ABI: return "problem.abi_version does not match the library ABI version";
+    case ATLAS_MEM_ERR_SHAPE: return "unsupported sizes (need bh >= 1, seq_len >= 1, d_k == d_v in {32, 64}, 1 <= window <= 33)";
+    case ATLAS_MEM_ERR_DTYPE: return "unknown dtype code (ATLAS_DT_F32 or ATLAS_DT_BF16)";
+    case ATLAS_MEM_ERR_NULL: return "a required pointer is NULL";
+    case ATLAS_MEM_ERR_ALIGN: return "a pointer is not aligned to its element size";
+    case ATLAS_MEM_ERR_UNSUPPORTED: return "window - 1 exceeds the chunk length implied by clamp_every; split the call at clamp_every";
+    case ATLAS_MEM_ERR_WORKSPACE: return "workspace smaller than atlas_mem_bwd_workspace_bytes()";
+    case ATLAS_MEM_ERR_LAUNCH: return "a HIP kernel launch or runtime call failed";
+    case ATLAS_MEM_ERR_ARG: return "inconsistent flags (momentum/gate/map/buffer/clamp)";
+    default: return "unknown atlas_mem status";
+  }
+}
+
+int atlas_mem_validate(const atlas_mem_problem* prob) { return make_plan(prob).status; }
+
+size_t atlas_mem_saved_bytes(const atlas_mem_problem* prob) {
+  const Plan pl = make_plan(prob);
+  if (!pl.ok) return 0;
+  return (size_t)pl.g.BH * pl.g.nc * 2 * pl.g.DV * pl.g.DK * sizeof(float);
+}
+
+size_t atlas_mem_bwd_workspace_bytes(const atlas_mem_problem* prob) {
+  const Plan pl = make_plan(prob);
+  if (!pl.ok) return 0;
+  return bwd_layout(pl.g).total;
+}
+
+int atlas_mem_fwd(const atlas_mem_problem* prob, const atlas_mem_fwd_args* args, float* saved, void* stream) {
+  const Plan pl = make_plan(prob);
+  if (!pl.ok) return pl.status;
+  if (!args) return ATLAS_MEM_ERR_NULL;
+  const atlas_mem_problem& p = *prob;
+  if (!args->k || !args->q || !args->v || !args->lr || !args->decay || !args->S_ref || !args->S0 ||
+      !args->y || !args->S_T)
+    return ATLAS_MEM_ERR_NULL;
+  if (p.momentum && (!args->beta || !args->Z_T)) return ATLAS_MEM_ERR_NULL;
+  if (!p.momentum && (args->beta || args->Z_T)) return ATLAS_MEM_ERR_ARG;
+  if ((p.gate_mode != ATLAS_GATE_NONE) != (args->gate != nullptr)) return ATLAS_MEM_ERR_ARG;
+  if (p.has_buffer && !args->buffer_in) return ATLAS_MEM_ERR_NULL;
+  if (p.window > 1 && !args->buffer_out) return ATLAS_MEM_ERR_NULL;
+  const size_t es = p.dtype == ATLAS_DT_BF16 ? 2 : 4;
+  const void* tp[] = {args->k, args->q, args->v, args->lr, args->decay, args->beta, args->gate, args->y};
+  for (const void* q : tp) if (misaligned(q, es)) return ATLAS_MEM_ERR_ALIGN;
+  const void* fp[] = {args->S_ref, args->S0, args->Z0, args->buffer_in, args->S_T, args->Z_T, args->buffer_out, saved};
+  for (const void* q : fp) if (misaligned(q, 4)) return ATLAS_MEM_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return p.dtype == ATLAS_DT_BF16 ? run_fwd<bf16>(pl, args, saved, s) : run_fwd<float>(pl, args, saved, s);
+}
+
+int atlas_mem_bwd(const atlas_mem_problem* prob, const atlas_mem_bwd_args* args, const float* saved,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  const Plan pl = make_plan(prob);
+  if (!pl.ok) return pl.status;
+  if (!args || !saved || !workspace) return ATLAS_MEM_ERR_NULL;
+  const atlas_mem_problem& p = *prob;
+  if (workspace_bytes < bwd_layout(pl.g).total) return ATLAS_MEM_ERR_WORKSPACE;
+  if (!args->k || !args->q || !args->v || !args->lr || !args->decay || !args->S_ref || !args->S0 ||
+      !args->dk || !args->dq || !args->dv || !args->dlr || !args->ddecay || !args->dS_ref || !args->dS0)
+    return ATLAS_MEM_ERR_NULL;
+  if (p.momentum && (!args->beta || !args->dbeta || !args->dZ0)) return ATLAS_MEM_ERR_NULL;
+  if ((p.gate_mode != ATLAS_GATE_NONE) != (args->gate != nullptr)) return ATLAS_MEM_ERR_ARG;
+  if (p.gate_mode != ATLAS_GATE_NONE && !args->dgate) return ATLAS_MEM_ERR_NULL;
+  if (p.has_buffer && (!args->buffer_in || !args->dbuffer_in)) return ATLAS_MEM_ERR_NULL;
+  const size_t es = p.dtype == ATLAS_DT_BF16 ? 2 : 4;
+  const void* tp[] = {args->k, args->q, args->v, args->lr, args->decay, args->beta, args->gate, args->dy,
+                      args->dk, args->dq, args->dv, args->dlr, args->ddecay, args->dbeta, args->dgate};
+  for (const void* q : tp) if (misaligned(q, es)) return ATLAS_MEM_ERR_ALIGN;
+  const void* fp[] = {args->S_ref, args->S0, args->Z0, args->buffer_in, args->dS_T, args->dZ_T, args->dbuffer_out,
+                      args->dS_ref, args->dS0, args->dZ0, args->dbuffer_in, saved, workspace};
+  for (const void* q : fp) if (misaligned(q, 4)) return ATLAS_MEM_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return p.dtype == ATLAS_DT_BF16 ? run_bwd<bf16>(pl, args, saved, workspace, s)
+                                  : run_bwd<float>(pl, args, saved, workspace, s);
+}
+
+int atlas_mem_mfma_selftest(int dtype, const void* A, const void* B, float* C, void* stream) {
+  if (!A || !B || !C) return ATLAS_MEM_ERR_NULL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == ATLAS_DT_BF16) {
+    hipLaunchKernelGGL(k_mfma_selftest<bf16>, dim3(1), dim3(64), 0, s, (const bf16*)A, (const bf16*)B, C);
+  } else if (dtype == ATLAS_DT_F32) {
+    hipLaunchKernelGGL(k_mfma_selftest<float>, dim3(1), dim3(64), 0, s, (const float*)A, (const float*)B, C);
+  } else {
+    return ATLAS_MEM_ERR_DTYPE;
+  }
+  return hipGetLastError() == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
+}
+
+}  // extern "C"

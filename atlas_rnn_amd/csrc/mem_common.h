@@ -1,0 +1,115 @@
+// mem_common.h - device helpers shared by the memory-recurrence kernels (gfx950 / CDNA4).
+//
+// Matrix-core tiles: every GEMM in this library is an "NT" product
+//     C[m, n] = sum_k A[m, k] * Bt[n, k]
+// computed as 16x16 output tiles by one wave64 with
+//     bf16: v_mfma_f32_16x16x32_bf16 (k step 32, 8 bf16 per lane)
+//     fp32: v_mfma_f32_16x16x4_f32   (k step 4, 1 fp32 per lane)
+// Lane l of the wave supplies A[m0 + (l & 15)][k0 + (l >> 4) * KL + e] (e < KL) and the same
+// pattern of Bt; the accumulator lane l holds C[m0 + 4 * (l >> 4) + i][n0 + (l & 15)], i < 4.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace atlas {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+template <typename T> __device__ __forceinline__ float to_f32(T x) { return static_cast<float>(x); }
+template <typename T> __device__ __forceinline__ T from_f32(float x) { return static_cast<T>(x); }
+
+template <typename OT> struct MM;
+
+template <> struct MM<bf16> {
+  static constexpr int KS = 32;  // k per instruction
+  static constexpr int KL = 8;   // k values per lane
+  typedef bf16x8 frag;
+  static __device__ __forceinline__ f32x4 mma(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct MM<float> {
+  static constexpr int KS = 4;
+  static constexpr int KL = 1;
+  typedef float frag;
+  static __device__ __forceinline__ f32x4 mma(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+};
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// Fragment of a matrix stored with element (r, k) at p[r * rs + k * cs].
+template <typename OT, typename ST>
+__device__ __forceinline__ typename MM<OT>::frag frag_ld(const ST* p, int rs, int cs, int r0, int k0) {
+  const int l = lane_id();
+  const ST* q = p + (r0 + (l & 15)) * rs + (k0 + (l >> 4) * MM<OT>::KL) * cs;
+  typename MM<OT>::frag f;
+  if constexpr (MM<OT>::KL == 1) {
+    f = static_cast<OT>(to_f32(q[0]));
+  } else {
+#pragma unroll
+    for (int e = 0; e < MM<OT>::KL; ++e) f[e] = static_cast<OT>(to_f32(q[e * cs]));
+  }
+  return f;
+}
+
+// Row-major, k contiguous, same element type: one 16-byte load per lane for bf16.
+// Requires rs % 8 == 0 and 16-byte aligned p.
+template <typename OT>
+__device__ __forceinline__ typename MM<OT>::frag frag_ld_row(const OT* p, int rs, int r0, int k0) {
+  const int l = lane_id();
+  const OT* q = p + (r0 + (l & 15)) * rs + k0 + (l >> 4) * MM<OT>::KL;
+  if constexpr (MM<OT>::KL == 1) {
+    return q[0];
+  } else {
+    return *reinterpret_cast<const typename MM<OT>::frag*>(q);
+  }
+}
+
+// Same as frag_ld but each k value is multiplied by s[k] (fp32) before rounding to OT.
+template <typename OT, typename ST>
+__device__ __forceinline__ typename MM<OT>::frag frag_ld_kscaled(const ST* p, int rs, int cs, int r0, int k0,
+                                                                const float* s) {
+  const int l = lane_id();
+  const int kb = k0 + (l >> 4) * MM<OT>::KL;
+  const ST* q = p + (r0 + (l & 15)) * rs + kb * cs;
+  typename MM<OT>::frag f;
+  if constexpr (MM<OT>::KL == 1) {
+    f = static_cast<OT>(to_f32(q[0]) * s[kb]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < MM<OT>::KL; ++e) f[e] = static_cast<OT>(to_f32(q[e * cs]) * s[kb + e]);
+  }
+  return f;
+}
+
+// Clamp of the reference (torch.clamp(-100, 100)) and its gradient mask (min <= x <= max).
+__device__ __forceinline__ float clamp100(float x) { return fminf(fmaxf(x, -100.f), 100.f); }
+__device__ __forceinline__ float clamp_mask(float x) { return (x >= -100.f && x <= 100.f) ? 1.f : 0.f; }
+
+// Elementwise polynomial feature map sum_{i=1..g} x^i (rnn_memory.py:117-123) and its derivative.
+__device__ __forceinline__ float poly_map(float x, int g) {
+  float out = x, pw = x;
+  for (int i = 2; i <= g; ++i) { pw *= x; out += pw; }
+  return out;
+}
+__device__ __forceinline__ float poly_map_grad(float x, int g) {
+  // d/dx sum_{i=1..g} x^i = sum_{i=1..g} i x^{i-1}
+  float out = 1.f, pw = 1.f;
+  for (int i = 2; i <= g; ++i) { pw *= x; out += static_cast<float>(i) * pw; }
+  return out;
+}
+
+}  // namespace atlas

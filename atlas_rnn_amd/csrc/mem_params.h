@@ -1,0 +1,56 @@
+// mem_params.h - geometry and pointer bundles passed by value to the kernels.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace atlas {
+
+// Gate modes / map modes mirror atlas_mem.h.
+enum { GATE_NONE = 0, GATE_TOKEN = 1, GATE_LAG = 2 };
+enum { MAP_OFF = 0, MAP_ELEMENTWISE = 1 };
+
+constexpr int kMaxWindow = 33;  // e <= 33  ->  halo <= 32
+constexpr int kHaloPad = 32;    // source tile = chunk + 32 rows
+
+struct Geom {
+  int BH, T, DK, DV;
+  int e, H;         // window and halo = e - 1
+  int Lc;           // chunk length used for this call (<= CH)
+  int nc;           // number of chunks = ceil(T / Lc)
+  int SP;           // source rows per chunk tile, multiple of 32: round_up(H + CH, 32)
+  int momentum, gate_mode, map_mode, map_deg, has_buf, clamp_every, clamp_final;
+};
+
+// The end of chunk c (token t1 - 1) is a clamp point inside the sequence.
+__host__ __device__ inline bool clamp_after(const Geom& g, int t1) {
+  return g.clamp_every > 0 && t1 < g.T && (t1 % g.clamp_every) == 0;
+}
+
+template <typename T>
+struct FwdPtrs {
+  const T* k; const T* q; const T* v;
+  const T* lr; const T* decay; const T* beta; const T* gate;
+  const float* S_ref; const float* S0; const float* Z0; const float* buf_in;
+  T* y; float* S_T; float* Z_T; float* buf_out;
+  float* saved;   // [BH][nc][2][DV][DK] raw chunk-end (S, Z)
+};
+
+template <typename T>
+struct BwdPtrs {
+  const T* k; const T* q; const T* v;
+  const T* lr; const T* decay; const T* beta; const T* gate;
+  const float* S_ref; const float* S0; const float* Z0; const float* buf_in;
+  const T* dy; const float* dS_T; const float* dZ_T; const float* dbuf_out;
+  T* dk; T* dq; T* dv; T* dlr; T* ddecay; T* dbeta; T* dgate;
+  float* dS_ref; float* dS0; float* dZ0; float* dbuf_in;
+  const float* saved;  // forward states
+  // workspace
+  float* adj;          // [BH][nc][2][DV][DK]  adjoint of chunk-end (S, Z)
+  float* dsref_part;   // [BH][nc][DV][DK]
+  float* tail_part;    // [BH][nc][H][DV + DK]  partial (dv, dphi) of a chunk's last H tokens
+  float* halo_part;    // [BH][nc][H][DV + DK]  partial (dv, dphi) for the previous chunk's last H tokens
+  float* dw;           // [BH][T][e] per (target, lag) weight gradients (token mode)
+};
+
+}  // namespace atlas

@@ -1,0 +1,335 @@
+"""Autograd functions over libatlas_mem.so.
+
+* `memory_recurrence(...)`: the memory-layer recurrence of the Titans/OmegaNet RNN cells
+  (atlas_pytorch/rnn_memory.py:300-406 and :605-730), forward and backward on the GPU.
+* `AtlasOmegaFunction` / `atlas_omega_forward`: drop-in for the reference's CUDA autograd
+  function (atlas_pytorch/cuda/atlas_omega_autograd.py:87-211): window 16, per-token gate,
+  no buffer, no clamp.
+* `assoc_scan` / `window_sum`: the scalar-gated scan and window sum primitives.
+
+Every op requires ROCm GPU tensors and raises on CPU tensors; there is no fallback path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+_DTYPES = {torch.float32: _lib.DT_F32, torch.bfloat16: _lib.DT_BF16}
+
+
+def _ptr(t: Tensor | None):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_gpu(*ts: Tensor | None) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError("atlas_rnn_amd runs on ROCm GPU tensors only (got a CPU tensor); "
+                               "there is no CPU implementation in the product path")
+        dev = t.device if dev is None else dev
+    if dev is None:
+        raise RuntimeError("no tensor inputs")
+    return dev
+
+
+@dataclass(frozen=True)
+class RecurrenceConfig:
+    window: int = 1
+    map_mode: str = 'off'         # 'off' | 'elementwise'
+    map_degree: int = 1
+    clamp_every: int | None = None
+    clamp_final: bool = True
+
+
+def _problem(cfg: RecurrenceConfig, bh, T, dk, dv, momentum, gate, has_buffer, dtype) -> _lib.Problem:
+    p = _lib.Problem()
+    p.abi_version = _lib.ABI_VERSION
+    p.bh, p.seq_len, p.d_k, p.d_v = bh, T, dk, dv
+    p.window = cfg.window
+    p.momentum = int(momentum)
+    if gate is None:
+        p.gate_mode = _lib.GATE_NONE
+    else:
+        p.gate_mode = _lib.GATE_TOKEN if gate.dim() == 2 else _lib.GATE_LAG
+    elementwise = cfg.map_mode == 'elementwise' and cfg.map_degree > 1
+    p.map_mode = _lib.MAP_ELEMENTWISE if elementwise else _lib.MAP_OFF
+    p.map_degree = cfg.map_degree if elementwise else 1
+    p.has_buffer = int(has_buffer)
+    p.clamp_every = int(cfg.clamp_every or 0)
+    p.clamp_final = int(cfg.clamp_final)
+    p.dtype = _DTYPES[dtype]
+    return p
+
+
+class MemoryRecurrenceFn(torch.autograd.Function):
+    """y, S_T, Z_T, buffer_out = recurrence(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buffer).
+
+    k, q, v, lr, decay, beta, gate: same dtype (fp32 or bf16), contiguous; states fp32.
+    Z_T / buffer_out are empty tensors when momentum is off / window == 1.
+    """
+
+    @staticmethod
+    def forward(ctx, k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buf, cfg: RecurrenceConfig):
+        lib = _lib.load()
+        bh, T, dk = k.shape
+        dv = v.shape[-1]
+        momentum = beta is not None
+        prob = _problem(cfg, bh, T, dk, dv, momentum, gate, buf is not None, k.dtype)
+        _lib.check(lib.atlas_mem_validate(ctypes.byref(prob)), "atlas_mem_validate")
+        dev = k.device
+        y = torch.empty(bh, T, dv, device=dev, dtype=k.dtype)
+        S_T = torch.empty(bh, dv, dk, device=dev, dtype=torch.float32)
+        Z_T = torch.empty(bh, dv, dk, device=dev, dtype=torch.float32) if momentum else None
+        e = cfg.window
+        buf_out = torch.empty(bh, e - 1, dv, dk, device=dev, dtype=torch.float32) if e > 1 else None
+        need_bwd = any(ctx.needs_input_grad[:11])
+        saved = None
+        if need_bwd:
+            nbytes = lib.atlas_mem_saved_bytes(ctypes.byref(prob))
+            saved = torch.empty(nbytes // 4, device=dev, dtype=torch.float32)
+        a = _lib.FwdArgs(k=_ptr(k), q=_ptr(q), v=_ptr(v), lr=_ptr(lr), decay=_ptr(decay), beta=_ptr(beta),
+                         gate=_ptr(gate), S_ref=_ptr(S_ref), S0=_ptr(S0), Z0=_ptr(Z0), buffer_in=_ptr(buf),
+                         y=_ptr(y), S_T=_ptr(S_T), Z_T=_ptr(Z_T), buffer_out=_ptr(buf_out))
+        _lib.check(lib.atlas_mem_fwd(ctypes.byref(prob), ctypes.byref(a), _ptr(saved), _stream(dev)), "atlas_mem_fwd")
+        ctx.cfg = cfg
+        ctx.prob = prob
+        ctx.momentum = momentum
+        ctx.save_for_backward(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buf, saved)
+        empty = torch.empty(0, device=dev)
+        return y, S_T, (Z_T if Z_T is not None else empty), (buf_out if buf_out is not None else empty)
+
+    @staticmethod
+    def backward(ctx, dy, dS_T, dZ_T, dbuf_out):
+        lib = _lib.load()
+        k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buf, saved = ctx.saved_tensors
+        prob = ctx.prob
+        dev = k.device
+        bh, T, dk = k.shape
+        dv_ = v.shape[-1]
+        f32 = torch.float32
+        dy = dy.contiguous() if dy is not None else None
+        dS_T = dS_T.float().contiguous() if dS_T is not None else None
+        dZ_T = dZ_T.float().contiguous() if (dZ_T is not None and ctx.momentum and dZ_T.numel() > 0) else None
+        dbuf_out = dbuf_out.float().contiguous() if (dbuf_out is not None and dbuf_out.numel() > 0) else None
+        dk_ = torch.empty_like(k)
+        dq_ = torch.empty_like(q)
+        dv_t = torch.empty_like(v)
+        dlr = torch.empty_like(lr)
+        ddecay = torch.empty_like(decay)
+        dbeta = torch.empty_like(beta) if beta is not None else None
+        dgate = torch.empty_like(gate) if gate is not None else None
+        dS_ref = torch.empty(bh, dv_, dk, device=dev, dtype=f32)
+        dS0 = torch.empty(bh, dv_, dk, device=dev, dtype=f32)
+        dZ0 = torch.empty(bh, dv_, dk, device=dev, dtype=f32) if ctx.momentum else None
+        dbuf_in = torch.empty_like(buf) if buf is not None else None
+        ws_bytes = lib.atlas_mem_bwd_workspace_bytes(ctypes.byref(prob))
+        ws = torch.empty((ws_bytes + 3) // 4, device=dev, dtype=f32)
+        a = _lib.BwdArgs(k=_ptr(k), q=_ptr(q), v=_ptr(v), lr=_ptr(lr), decay=_ptr(decay), beta=_ptr(beta),
+                         gate=_ptr(gate), S_ref=_ptr(S_ref), S0=_ptr(S0), Z0=_ptr(Z0), buffer_in=_ptr(buf),
+                         dy=_ptr(dy), dS_T=_ptr(dS_T), dZ_T=_ptr(dZ_T), dbuffer_out=_ptr(dbuf_out),
+                         dk=_ptr(dk_), dq=_ptr(dq_), dv=_ptr(dv_t), dlr=_ptr(dlr), ddecay=_ptr(ddecay),
+                         dbeta=_ptr(dbeta), dgate=_ptr(dgate), dS_ref=_ptr(dS_ref), dS0=_ptr(dS0),
+                         dZ0=_ptr(dZ0), dbuffer_in=_ptr(dbuf_in))
+        _lib.check(lib.atlas_mem_bwd(ctypes.byref(prob), ctypes.byref(a), _ptr(saved), _ptr(ws),
+                                     ctypes.c_size_t(ws_bytes), _stream(dev)), "atlas_mem_bwd")
+        return (dk_, dq_, dv_t, dlr, ddecay, dbeta, dgate, dS_ref, dS0,
+                dZ0 if Z0 is not None else None, dbuf_in, None)
+
+
+def _canon(x: Tensor | None, dtype) -> Tensor | None:
+    return None if x is None else x.to(dtype).contiguous()
+
+
+def memory_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
+                      beta: Tensor | None = None, gate: Tensor | None = None,
+                      S_ref: Tensor | None = None, S0: Tensor | None = None, Z0: Tensor | None = None,
+                      buffer: Tensor | None = None, *, window: int = 1, map_mode: str = 'off',
+                      map_degree: int = 1, clamp_every: int | None = None, clamp_final: bool = True):
+    """Memory-layer recurrence over [BH, T, d] inputs (see oracle/recurrence.py for the math).
+
+    k, q: raw keys / queries [BH, T, d_k] (the elementwise polynomial map is applied inside);
+    v [BH, T, d_v]; lr (eta), decay (alpha), beta [BH, T]; gate None | [BH, T] (per-token,
+    reference omega_gate) | [BH, T, e] (per-lag); S_ref, S0, Z0 [BH, d_v, d_k];
+    buffer [BH, e-1, d_v, d_k]. Returns (y [BH,T,d_v] in the input dtype, S_T, Z_T or None,
+    buffer_out or None) with fp32 states.
+    """
+    dev = _require_gpu(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buffer)
+    dt = k.dtype if k.dtype in _DTYPES else torch.float32
+    bh, T, dk = k.shape
+    dv = v.shape[-1]
+    if S0 is None:
+        S0 = torch.zeros(bh, dv, dk, device=dev, dtype=torch.float32)
+    if S_ref is None:
+        S_ref = S0
+    e = window
+    cfg = RecurrenceConfig(window=e, map_mode=map_mode, map_degree=map_degree,
+                           clamp_every=clamp_every, clamp_final=clamp_final)
+    args = [_canon(t, dt) for t in (k, q, v, lr, decay, beta, gate)]
+    states = [_canon(t, torch.float32) for t in (S_ref, S0, Z0 if beta is not None else None,
+                                                  buffer if e > 1 else None)]
+    # window - 1 longer than the chunk implied by clamp_every: run one call per scan chunk
+    # (atlas_pytorch/rnn_memory.py:584-601), carrying S, Z and the buffer, S_ref fixed.
+    lib = _lib.load()
+    prob = _problem(cfg, bh, T, dk, dv, beta is not None, gate, states[3] is not None, dt)
+    status = lib.atlas_mem_validate(ctypes.byref(prob))
+    if status == _lib.ERR_UNSUPPORTED and clamp_every and T > clamp_every:
+        ys = []
+        S_ref_f, S, Z, B = states
+        for start in range(0, T, clamp_every):
+            end = min(T, start + clamp_every)
+            sl = slice(start, end)
+            y, S, Z, B = memory_recurrence(
+                args[0][:, sl], args[1][:, sl], args[2][:, sl], args[3][:, sl], args[4][:, sl],
+                args[5][:, sl] if args[5] is not None else None,
+                args[6][:, sl] if args[6] is not None else None,
+                S_ref_f, S, Z, B, window=e, map_mode=map_mode, map_degree=map_degree,
+                clamp_every=None, clamp_final=(end < T) or clamp_final)
+            ys.append(y)
+        return torch.cat(ys, dim=1), S, Z, B
+    _lib.check(status, "atlas_mem_validate")
+    y, S_T, Z_T, buf_out = MemoryRecurrenceFn.apply(*args, *states, cfg)
+    return y, S_T, (Z_T if beta is not None else None), (buf_out if e > 1 else None)
+
+
+class AtlasOmegaFunction:
+    """Drop-in for atlas_pytorch/cuda/atlas_omega_autograd.py:87-204.
+
+    apply(phi_k, phi_q, v, S_ref, lr, decay, beta, gate, S0, Z0) -> (y, S_T, Z_T): window 16,
+    per-token gate, momentum, zero buffer, no clamp. phi_k / phi_q are already feature-mapped.
+    Unlike the reference CUDA kernel, alpha and beta are not clamped to >= 1e-4 and states stay
+    in fp32 (the PyTorch-path semantics); y and the states are returned in phi_k's dtype.
+    """
+
+    WINDOW = 16
+
+    @staticmethod
+    def apply(phi_k, phi_q, v, S_ref, lr, decay, beta, gate, S0, Z0):
+        y, S_T, Z_T, _ = memory_recurrence(phi_k, phi_q, v, lr, decay, beta, gate, S_ref, S0, Z0, None,
+                                           window=AtlasOmegaFunction.WINDOW, clamp_final=False)
+        return y, S_T.to(phi_k.dtype), Z_T.to(phi_k.dtype)
+
+
+def atlas_omega_forward(phi_k, phi_q, v, S_ref, lr, decay, beta, gate, S0, Z0):
+    """atlas_pytorch/cuda/atlas_omega_autograd.py:207-211."""
+    return AtlasOmegaFunction.apply(phi_k, phi_q, v, S_ref, lr, decay, beta, gate, S0, Z0)
+
+
+def check_cuda_availability():
+    """atlas_pytorch/cuda/atlas_omega_autograd.py:214-228: (available, message)."""
+    if not torch.cuda.is_available():
+        return False, "no ROCm GPU visible"
+    try:
+        _lib.load()
+    except Exception as exc:  # noqa: BLE001
+        return False, f"libatlas_mem.so not loaded: {exc}"
+    props = torch.cuda.get_device_properties(0)
+    return True, f"atlas_rnn_amd ready (GPU: {props.name}, library: {_lib.LIB_PATH})"
+
+
+# ------------------------------------------------------------------------------------------
+# Scan primitives
+# ------------------------------------------------------------------------------------------
+
+class _ScanFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, gates, x, prev):
+        lib = _lib.load()
+        n, t = gates.shape
+        d = x.numel() // (n * t)
+        out = torch.empty_like(x)
+        _lib.check(lib.atlas_scan_fwd(_DTYPES[x.dtype], n, t, d, _ptr(gates), _ptr(x), _ptr(prev), _ptr(out),
+                                      _stream(x.device)), "atlas_scan_fwd")
+        ctx.save_for_backward(gates, out, prev)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        lib = _lib.load()
+        gates, out, prev = ctx.saved_tensors
+        n, t = gates.shape
+        d = out.numel() // (n * t)
+        dout = dout.contiguous()
+        dx = torch.empty_like(out)
+        dg = torch.empty_like(gates)
+        dprev = torch.empty_like(prev) if prev is not None else None
+        _lib.check(lib.atlas_scan_bwd(_DTYPES[out.dtype], n, t, d, _ptr(gates), _ptr(out), _ptr(prev),
+                                      _ptr(dout), _ptr(dx), _ptr(dg), _ptr(dprev), _stream(out.device)),
+                   "atlas_scan_bwd")
+        return dg, dx, dprev
+
+
+def assoc_scan(gates: Tensor, inputs: Tensor, prev: Tensor | None = None, remove_prev: bool | None = None) -> Tensor:
+    """AssocScan contract: out_t = gates_t * out_{t-1} + inputs_t (gates [N, T] or [N, T, 1...]
+    broadcast over the trailing dims of inputs [N, T, ...]); prev is out_{-1}. With prev and
+    remove_prev=False the result has T+1 steps and starts with prev."""
+    _require_gpu(gates, inputs, prev)
+    dt = inputs.dtype if inputs.dtype in _DTYPES else torch.float32
+    N, T = inputs.shape[:2]
+    g = gates.reshape(N, T, -1)
+    if g.shape[-1] != 1:
+        raise ValueError("gates must be scalar per (n, t)")
+    g = g.reshape(N, T).to(dt).contiguous()
+    x = inputs.to(dt).contiguous()
+    pv = prev.to(dt).contiguous() if prev is not None else None
+    out = _ScanFn.apply(g, x, pv)
+    if remove_prev is None:
+        remove_prev = prev is not None
+    if prev is not None and not remove_prev:
+        out = torch.cat([pv.unsqueeze(1), out], dim=1)
+    return out
+
+
+class AssocScan(torch.nn.Module):
+    """Module form of the scan (constructor kwargs of assoc_scan.AssocScan are accepted)."""
+
+    def __init__(self, use_accelerated: bool = False, **kwargs):
+        super().__init__()
+
+    def forward(self, gates, inputs, prev=None, remove_prev=None):
+        return assoc_scan(gates, inputs, prev=prev, remove_prev=remove_prev)
+
+
+class _WindowSumFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, window):
+        lib = _lib.load()
+        n, t = x.shape[:2]
+        d = x.numel() // (n * t)
+        y = torch.empty_like(x)
+        _lib.check(lib.atlas_window_sum(_DTYPES[x.dtype], n, t, d, window, 0, _ptr(x), _ptr(y), _stream(x.device)),
+                   "atlas_window_sum")
+        ctx.window = window
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        lib = _lib.load()
+        dy = dy.contiguous()
+        n, t = dy.shape[:2]
+        d = dy.numel() // (n * t)
+        dx = torch.empty_like(dy)
+        _lib.check(lib.atlas_window_sum(_DTYPES[dy.dtype], n, t, d, ctx.window, 1, _ptr(dy), _ptr(dx),
+                                        _stream(dy.device)), "atlas_window_sum")
+        return dx, None
+
+
+def window_sum(x: Tensor, window: int) -> Tensor:
+    """Inclusive window sum along dim 1 (the contract of _sliding_sum_along_time)."""
+    if window <= 1:
+        return x
+    _require_gpu(x)
+    dt = x.dtype if x.dtype in _DTYPES else torch.float32
+    return _WindowSumFn.apply(x.to(dt).contiguous(), int(window))

@@ -1,0 +1,176 @@
+/*
+ * atlas_mem.h - C ABI of the MI355X memory-layer recurrence library (libatlas_mem.so).
+ *
+ * One library, built ahead of time for gfx950, loaded with ctypes (or dlopen) by the
+ * host-side mirror of the reference module API. Plain pointers and sizes only; no torch types.
+ *
+ * Recurrence computed per head-batch row bh (all states fp32, row-major [d_v, d_k]):
+ *   phi_t = map(k_t), psi_t = map(q_t)                (map: identity or sum_{i=1..g} x^i)
+ *   delta_t = S_ref phi_t - v_t
+ *   g_t = sum_{j=0..e-1} w[t,j] delta_{t-j} phi_{t-j}^T   (+ carried buffer for t-j < 0)
+ *   Z_t = beta_t Z_{t-1} + g_t ;  S_t = alpha_t S_{t-1} - eta_t Z_t   (no momentum: Z_t = g_t)
+ *   y_t = S_{t-1} psi_t ;  S_T = clamp(S_{T-1}, -100, 100) ;  Z_T = Z_{T-1}
+ * With clamp_every = n > 0, S is also clamped after every token t with (t+1) % n == 0
+ * (the reference's scan_chunk_len semantics).
+ *
+ * Replaces the reference's native FFI:
+ *   forward_exact(...)   atlas_pytorch/cuda/atlas_omega.cpp:56-99   -> atlas_mem_fwd
+ *   backward_exact(...)  atlas_pytorch/cuda/atlas_omega.cpp:102-136  -> atlas_mem_bwd
+ * and the AssocScan/PyTorch path it bypassed (atlas_pytorch/rnn_memory.py:605-730,
+ * :300-406), whose semantics (fp32 state, buffer carry, clamp, any window e) it follows.
+ *
+ * Ownership: the caller allocates every buffer (outputs, the `saved` state buffer that
+ * travels from forward to backward, and the backward workspace); the library never
+ * allocates device memory. Calls are asynchronous on the given HIP stream (`stream` is a
+ * hipStream_t passed as void*; NULL = the default stream) and stream-ordered. Entry points
+ * are reentrant; concurrent calls must not share output, saved or workspace buffers.
+ *
+ * Errors: every entry point returns ATLAS_MEM_OK (0) or a nonzero code; the text is
+ * available from atlas_mem_strerror(code). Shape/dtype/pointer checks happen before any
+ * launch; a launch failure returns ATLAS_MEM_ERR_LAUNCH.
+ */
+#ifndef ATLAS_MEM_H
+#define ATLAS_MEM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ATLAS_MEM_ABI_VERSION 1
+
+enum atlas_mem_status {
+  ATLAS_MEM_OK = 0,
+  ATLAS_MEM_ERR_ABI = 1,          /* problem.abi_version != ATLAS_MEM_ABI_VERSION */
+  ATLAS_MEM_ERR_SHAPE = 2,        /* sizes out of the supported range */
+  ATLAS_MEM_ERR_DTYPE = 3,        /* unknown dtype code */
+  ATLAS_MEM_ERR_NULL = 4,         /* a required pointer is NULL */
+  ATLAS_MEM_ERR_ALIGN = 5,        /* a pointer is not 16-byte aligned */
+  ATLAS_MEM_ERR_UNSUPPORTED = 6,  /* valid request this build does not implement */
+  ATLAS_MEM_ERR_WORKSPACE = 7,    /* workspace too small */
+  ATLAS_MEM_ERR_LAUNCH = 8,       /* a HIP launch or runtime call failed */
+  ATLAS_MEM_ERR_ARG = 9           /* inconsistent flags */
+};
+
+enum atlas_mem_dtype { ATLAS_DT_F32 = 0, ATLAS_DT_BF16 = 1 };
+enum atlas_mem_gate_mode {
+  ATLAS_GATE_NONE = 0,   /* w[t,j] = 1 */
+  ATLAS_GATE_TOKEN = 1,  /* gate [bh,T]: w[t,j] = u_{t-j} (reference omega_gate); buffer holds gated products */
+  ATLAS_GATE_LAG = 2     /* gate [bh,T,e]: w[t,j] = U[t,j]; buffer holds ungated products */
+};
+enum atlas_mem_map_mode { ATLAS_MAP_OFF = 0, ATLAS_MAP_ELEMENTWISE = 1 };
+
+typedef struct atlas_mem_problem {
+  int32_t abi_version;  /* ATLAS_MEM_ABI_VERSION */
+  int32_t bh;           /* batch * heads */
+  int32_t seq_len;      /* T >= 1 */
+  int32_t d_k;          /* key/feature width: 32, 64 */
+  int32_t d_v;          /* value width (rows of S): equal to d_k in this build */
+  int32_t window;       /* omega window e, 1..33 */
+  int32_t momentum;     /* 1: Z recurrence with beta; 0: Z_t = g_t, no Z0/Z_T */
+  int32_t gate_mode;    /* atlas_mem_gate_mode */
+  int32_t map_mode;     /* atlas_mem_map_mode, applied to k and q on load */
+  int32_t map_degree;   /* g for ATLAS_MAP_ELEMENTWISE (>= 1) */
+  int32_t has_buffer;   /* 1: buffer_in [bh, e-1, d_v, d_k] supplied (otherwise zeros) */
+  int32_t clamp_every;  /* 0 or scan_chunk_len */
+  int32_t clamp_final;  /* 1: S_T = clamp(S_{T-1}) (reference PyTorch path) */
+  int32_t dtype;        /* atlas_mem_dtype of k, q, v, lr, decay, beta, gate, y and their grads */
+} atlas_mem_problem;
+
+typedef struct atlas_mem_fwd_args {
+  const void* k;            /* [bh, T, d_k] raw keys (feature map applied inside) */
+  const void* q;            /* [bh, T, d_k] raw queries */
+  const void* v;            /* [bh, T, d_v] */
+  const void* lr;           /* [bh, T] eta */
+  const void* decay;        /* [bh, T] alpha */
+  const void* beta;         /* [bh, T] momentum; NULL iff momentum == 0 */
+  const void* gate;         /* [bh, T] or [bh, T, e]; NULL iff gate_mode == NONE */
+  const float* S_ref;       /* [bh, d_v, d_k] reference state for delta */
+  const float* S0;          /* [bh, d_v, d_k] */
+  const float* Z0;          /* [bh, d_v, d_k] or NULL (zeros); ignored without momentum */
+  const float* buffer_in;   /* [bh, e-1, d_v, d_k] iff has_buffer */
+  void* y;                  /* [bh, T, d_v] out */
+  float* S_T;               /* [bh, d_v, d_k] out */
+  float* Z_T;               /* [bh, d_v, d_k] out iff momentum, else NULL */
+  float* buffer_out;        /* [bh, e-1, d_v, d_k] out iff e > 1, else NULL */
+} atlas_mem_fwd_args;
+
+typedef struct atlas_mem_bwd_args {
+  /* forward inputs, the same buffers that were passed to atlas_mem_fwd */
+  const void* k; const void* q; const void* v;
+  const void* lr; const void* decay; const void* beta; const void* gate;
+  const float* S_ref; const float* S0; const float* Z0; const float* buffer_in;
+  /* incoming gradients; NULL means zero */
+  const void* dy;           /* [bh, T, d_v] (dtype) */
+  const float* dS_T;        /* [bh, d_v, d_k] */
+  const float* dZ_T;        /* [bh, d_v, d_k] */
+  const float* dbuffer_out; /* [bh, e-1, d_v, d_k] */
+  /* gradients out (dtype unless noted); dbeta/dgate NULL iff the input is absent */
+  void* dk; void* dq; void* dv; void* dlr; void* ddecay; void* dbeta; void* dgate;
+  float* dS_ref;            /* [bh, d_v, d_k] */
+  float* dS0;               /* [bh, d_v, d_k] */
+  float* dZ0;               /* [bh, d_v, d_k] iff momentum, else NULL */
+  float* dbuffer_in;        /* [bh, e-1, d_v, d_k] iff has_buffer, else NULL */
+} atlas_mem_bwd_args;
+
+/* Library ABI version (ATLAS_MEM_ABI_VERSION of the build). */
+int atlas_mem_abi_version(void);
+
+/* Static text for a status code. */
+const char* atlas_mem_strerror(int status);
+
+/* Checks a problem description without touching the GPU. */
+int atlas_mem_validate(const atlas_mem_problem* prob);
+
+/* Bytes of the `saved` buffer written by atlas_mem_fwd and read by atlas_mem_bwd
+ * (fp32 chunk-end states). Returns 0 for an invalid problem. */
+size_t atlas_mem_saved_bytes(const atlas_mem_problem* prob);
+
+/* Bytes of scratch workspace atlas_mem_bwd needs. Returns 0 for an invalid problem. */
+size_t atlas_mem_bwd_workspace_bytes(const atlas_mem_problem* prob);
+
+/* Forward pass. Replaces forward_exact (atlas_pytorch/cuda/atlas_omega.cpp:56-99) and the
+ * PyTorch scan path (atlas_pytorch/rnn_memory.py:605-730). `saved` may be NULL when no
+ * backward will follow. */
+int atlas_mem_fwd(const atlas_mem_problem* prob, const atlas_mem_fwd_args* args,
+                  float* saved, void* stream);
+
+/* Backward pass from the forward's `saved` states. Replaces backward_exact
+ * (atlas_pytorch/cuda/atlas_omega.cpp:102-136) plus the PyTorch-side chain in
+ * AtlasOmegaFunction.backward (atlas_pytorch/cuda/atlas_omega_autograd.py:156-204). */
+int atlas_mem_bwd(const atlas_mem_problem* prob, const atlas_mem_bwd_args* args,
+                  const float* saved, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- scan primitives (row-major [n, t, d] buffers of `dtype`, gates [n, t]) -------------- */
+
+/* out_t = gates_t * out_{t-1} + x_t, out_{-1} = prev ([n, d]) or 0 when prev is NULL.
+ * Replaces assoc_scan.AssocScan.__call__(gates, inputs, prev) as called at
+ * atlas_pytorch/rnn_memory.py:363,369,698,700,705 and atlas_pytorch/omega.py:267,315
+ * (the T-output form; the caller prepends prev for remove_prev=False). */
+int atlas_scan_fwd(int dtype, int64_t n, int64_t t, int64_t d, const void* gates, const void* x,
+                   const void* prev, void* out, void* stream);
+
+/* Gradients of atlas_scan_fwd given its output `out`: dx [n,t,d], dgates [n,t], dprev [n,d]
+ * (dprev may be NULL). */
+int atlas_scan_bwd(int dtype, int64_t n, int64_t t, int64_t d, const void* gates, const void* out,
+                   const void* prev, const void* dout, void* dx, void* dgates, void* dprev, void* stream);
+
+/* Inclusive window sum along t: reverse == 0: y_t = sum_{k=max(0,t-w+1)}^{t} x_k;
+ * reverse == 1: y_t = sum_{k=t}^{min(t+w-1,T-1)} x_k (the adjoint). Replaces
+ * _sliding_sum_along_time (atlas_pytorch/rnn_memory.py:50-61) and _sliding_sum_along_n
+ * (atlas_pytorch/omega.py:24-33). */
+int atlas_window_sum(int dtype, int64_t n, int64_t t, int64_t d, int window, int reverse,
+                     const void* x, void* y, void* stream);
+
+/* Diagnostic: C[16,16] = A[16,64] * B[16,64]^T through the library's MFMA tile helpers
+ * (dtype selects bf16 or fp32 inputs; C is fp32). No reference counterpart; used by the
+ * GPU tests to check the matrix-core lane layout in isolation. */
+int atlas_mem_mfma_selftest(int dtype, const void* A, const void* B, float* C, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATLAS_MEM_H */

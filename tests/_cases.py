@@ -1,0 +1,153 @@
+"""Seeded problem generation and the two sides of a parity check (test helper).
+
+Inputs follow BASELINE.json's distributions: q, k, v ~ N(0, 1) with keys L2-normalised per
+token, alpha = sigmoid(N(2, 0.5)), eta = 0.1 * sigmoid(N(0, 1)), beta = sigmoid(N(1, 0.5)),
+per-lag gates softmax(N(0, 1)) over the window, per-token gates sigmoid(N(0, 1)).
+Inputs are drawn in fp32 on the CPU, rounded to the test dtype, and the oracle runs in fp64
+on exactly those rounded values.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from oracle import memory_recurrence_vectorised, poly_feature_map
+
+F64 = torch.float64
+
+
+@dataclass
+class Case:
+    name: str
+    BH: int
+    T: int
+    d: int
+    e: int = 1
+    gate: str | None = None          # None | 'token' | 'lag'
+    momentum: bool = True
+    buffer: bool = False
+    states: float = 0.0              # scale of random S_ref / S0 / Z0 (0 -> zeros)
+    map_degree: int = 1
+    clamp_every: int | None = None
+    clamp_final: bool = True
+    dtype: torch.dtype = torch.float32
+    seed: int = 0
+    decay_shift: float = 2.0
+    backward: bool = True
+    extra: dict = field(default_factory=dict)
+
+
+def make_inputs(c: Case) -> dict:
+    g = torch.Generator().manual_seed(1000 + c.seed)
+    r = lambda *s: torch.randn(*s, generator=g, dtype=torch.float32)
+    BH, T, d, e = c.BH, c.T, c.d, c.e
+    k = r(BH, T, d)
+    k = k / k.norm(dim=-1, keepdim=True)
+    p = dict(k=k, q=r(BH, T, d), v=r(BH, T, d),
+             decay=torch.sigmoid(r(BH, T) * 0.5 + c.decay_shift), lr=0.1 * torch.sigmoid(r(BH, T)))
+    p["beta"] = torch.sigmoid(r(BH, T) * 0.5 + 1.0) if c.momentum else None
+    if c.gate == 'token':
+        p["gate"] = torch.sigmoid(r(BH, T))
+    elif c.gate == 'lag':
+        p["gate"] = torch.softmax(r(BH, T, e), dim=-1)
+    else:
+        p["gate"] = None
+    s = c.states
+    z = lambda: torch.zeros(BH, d, d)
+    p["S_ref"] = s * r(BH, d, d) if s else z()
+    p["S0"] = s * r(BH, d, d) if s else z()
+    p["Z0"] = (s * r(BH, d, d) if s else z()) if c.momentum else None
+    p["buffer"] = (0.1 * r(BH, e - 1, d, d)) if (c.buffer and e > 1) else None
+    # upstream gradients
+    p["gy"] = r(BH, T, d)
+    p["gS"] = r(BH, d, d)
+    p["gZ"] = r(BH, d, d) if c.momentum else None
+    p["gB"] = r(BH, e - 1, d, d) if e > 1 else None
+    # round the dtype-carried tensors
+    for key in ("k", "q", "v", "decay", "lr", "beta", "gate", "gy"):
+        if p[key] is not None:
+            p[key] = p[key].to(c.dtype).to(torch.float32)
+    return p
+
+
+TENSOR_INPUTS = ("k", "q", "v", "lr", "decay", "beta", "gate", "S_ref", "S0", "Z0", "buffer")
+
+
+def _loss(out, p):
+    y, S_T, Z_T, B = out
+    loss = (y * p["gy"]).sum() + (S_T * p["gS"]).sum()
+    if Z_T is not None:
+        loss = loss + (Z_T * p["gZ"]).sum()
+    if B is not None:
+        loss = loss + (B * p["gB"]).sum()
+    return loss
+
+
+def run_oracle(c: Case, p: dict):
+    """fp64 oracle outputs and gradients (autograd through the vectorised restatement)."""
+    x = {kk: (p[kk].to(F64).clone().requires_grad_(c.backward) if p[kk] is not None else None)
+         for kk in TENSOR_INPUTS}
+    # S_ref and S0 are separate leaves here (the cell passes the same tensor for both)
+    phi_k = poly_feature_map(x["k"], c.map_degree, 'elementwise' if c.map_degree > 1 else 'off')
+    phi_q = poly_feature_map(x["q"], c.map_degree, 'elementwise' if c.map_degree > 1 else 'off')
+    out = memory_recurrence_vectorised(phi_k, phi_q, x["v"], x["lr"], x["decay"], x["beta"], x["gate"],
+                                       x["S_ref"], x["S0"], x["Z0"], x["buffer"], window=c.e,
+                                       clamp_every=c.clamp_every, clamp_final=c.clamp_final)
+    grads = {}
+    if c.backward:
+        q64 = {kk: (v.to(F64) if v is not None else None) for kk, v in p.items() if kk.startswith("g")}
+        loss = _loss(out, q64)
+        leaves = [kk for kk in TENSOR_INPUTS if x[kk] is not None]
+        gs = torch.autograd.grad(loss, [x[kk] for kk in leaves], allow_unused=True)
+        grads = {kk: (gg if gg is not None else torch.zeros_like(x[kk])) for kk, gg in zip(leaves, gs)}
+    return [o.detach() if o is not None else None for o in out], grads
+
+
+def run_gpu(c: Case, p: dict, device="cuda"):
+    from atlas_rnn_amd.functional import memory_recurrence
+    x = {}
+    for kk in TENSOR_INPUTS:
+        if p[kk] is None:
+            x[kk] = None
+            continue
+        dt = c.dtype if kk in ("k", "q", "v", "lr", "decay", "beta", "gate") else torch.float32
+        x[kk] = p[kk].to(device=device, dtype=dt).clone().requires_grad_(c.backward)
+    out = memory_recurrence(x["k"], x["q"], x["v"], x["lr"], x["decay"], x["beta"], x["gate"],
+                            x["S_ref"], x["S0"], x["Z0"], x["buffer"], window=c.e,
+                            map_mode='elementwise' if c.map_degree > 1 else 'off', map_degree=c.map_degree,
+                            clamp_every=c.clamp_every, clamp_final=c.clamp_final)
+    grads = {}
+    if c.backward:
+        gd = {kk: (v.to(device) if v is not None else None) for kk, v in p.items() if kk.startswith("g")}
+        gd["gy"] = gd["gy"].to(c.dtype)
+        loss = _loss([o.float() if o is not None else None for o in out], gd)
+        leaves = [kk for kk in TENSOR_INPUTS if x[kk] is not None]
+        gs = torch.autograd.grad(loss, [x[kk] for kk in leaves], allow_unused=True)
+        grads = {kk: (gg if gg is not None else torch.zeros_like(x[kk])) for kk, gg in zip(leaves, gs)}
+    torch.cuda.synchronize()
+    return ([o.detach().float().cpu() if o is not None else None for o in out],
+            {kk: v.float().cpu() for kk, v in grads.items()})
+
+
+def tol_for(c: Case) -> float:
+    return 1e-4 if c.dtype == torch.float32 else 2e-2
+
+
+def compare(name: str, got: torch.Tensor, ref: torch.Tensor, tol: float):
+    """Elementwise |got - ref| <= tol * |ref| + tol * max|ref| (rtol with an atol floor scaled
+    by the tensor's largest magnitude)."""
+    ref = ref.to(torch.float64)
+    got = got.to(torch.float64)
+    assert got.shape == ref.shape, f"{name}: shape {tuple(got.shape)} vs {tuple(ref.shape)}"
+    scale = ref.abs().max().item()
+    atol = tol * max(scale, 1e-30)
+    err = (got - ref).abs()
+    bad = err > (tol * ref.abs() + atol)
+    if bad.any():
+        idx = bad.nonzero()[0].tolist()
+        raise AssertionError(
+            f"{name}: {int(bad.sum())} of {bad.numel()} elements off (tol {tol}); max err "
+            f"{err.max().item():.3e} vs max|ref| {scale:.3e}; first at {idx}: got "
+            f"{got[tuple(idx)].item():.6e} ref {ref[tuple(idx)].item():.6e}")

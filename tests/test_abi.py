@@ -1,0 +1,107 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol include/atlas_mem.h
+declares, and validates problems / sizes buffers on the host."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from atlas_rnn_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "atlas_mem.h")
+
+
+def _declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(atlas_\w+)\s*\(", src)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("libatlas_mem.so is not built (run `python -m atlas_rnn_amd.build`)")
+    return _lib.load()
+
+
+def test_header_and_binding_agree():
+    assert _declared_functions() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_exports_every_declared_symbol(lib):
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version(lib):
+    assert lib.atlas_mem_abi_version() == _lib.ABI_VERSION
+    assert "#define ATLAS_MEM_ABI_VERSION 1" in open(HEADER).read()
+
+
+def _prob(**kw):
+    p = _lib.Problem(abi_version=_lib.ABI_VERSION, bh=32, seq_len=4096, d_k=64, d_v=64, window=4, momentum=1,
+                     gate_mode=_lib.GATE_LAG, map_mode=0, map_degree=1, has_buffer=0, clamp_every=0,
+                     clamp_final=1, dtype=_lib.DT_BF16)
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def test_validate_accepts_headline(lib):
+    assert lib.atlas_mem_validate(ctypes.byref(_prob())) == _lib.OK
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("abi_version", 2, 1), ("bh", 0, 2), ("seq_len", 0, 2), ("d_k", 48, 2), ("d_v", 32, 2),
+    ("window", 0, 2), ("window", 34, 2), ("dtype", 7, 3), ("momentum", 2, 9), ("gate_mode", 3, 9),
+    ("map_mode", 2, 9), ("map_degree", 0, 9), ("clamp_every", -1, 9)])
+def test_validate_rejects(lib, field, value, code):
+    assert lib.atlas_mem_validate(ctypes.byref(_prob(**{field: value}))) == code
+    assert lib.atlas_mem_saved_bytes(ctypes.byref(_prob(**{field: value}))) == 0
+
+
+def test_buffer_needs_window(lib):
+    assert lib.atlas_mem_validate(ctypes.byref(_prob(window=1, has_buffer=1))) == 9
+
+
+def test_window_longer_than_clamp_chunk_is_unsupported(lib):
+    # clamp every 4 tokens with window 8: the caller splits the call (reference chunk loop)
+    assert lib.atlas_mem_validate(ctypes.byref(_prob(window=8, clamp_every=4))) == _lib.ERR_UNSUPPORTED
+
+
+def test_sizes(lib):
+    p = _prob()
+    nc = 4096 // 64
+    assert lib.atlas_mem_saved_bytes(ctypes.byref(p)) == 32 * nc * 2 * 64 * 64 * 4
+    ws = lib.atlas_mem_bwd_workspace_bytes(ctypes.byref(p))
+    assert ws >= 32 * nc * 3 * 64 * 64 * 4
+    pf = _prob(dtype=_lib.DT_F32)   # fp32 uses 32-token chunks
+    assert lib.atlas_mem_saved_bytes(ctypes.byref(pf)) == 32 * (4096 // 32) * 2 * 64 * 64 * 4
+
+
+def test_strerror(lib):
+    for code in range(0, 10):
+        assert len(lib.atlas_mem_strerror(code)) > 0
+    assert b"unknown" in lib.atlas_mem_strerror(99)
+
+
+def test_null_pointer_errors_before_launch(lib):
+    p = _prob()
+    args = _lib.FwdArgs()
+    assert lib.atlas_mem_fwd(ctypes.byref(p), ctypes.byref(args), None, None) == 4
+    assert lib.atlas_mem_fwd(ctypes.byref(p), None, None, None) == 4
+    bargs = _lib.BwdArgs()
+    assert lib.atlas_mem_bwd(ctypes.byref(p), ctypes.byref(bargs), None, None, 0, None) == 4
+    assert lib.atlas_scan_fwd(0, 1, 4, 8, None, None, None, None, None) == 4
+    assert lib.atlas_scan_fwd(0, 0, 4, 8, None, None, None, None, None) == 2
+    assert lib.atlas_window_sum(0, 1, 4, 8, 0, 0, None, None, None) == 2
+
+
+def test_cpu_tensors_are_rejected():
+    torch = pytest.importorskip("torch")
+    from atlas_rnn_amd.functional import memory_recurrence
+    x = torch.zeros(1, 4, 32)
+    s = torch.zeros(1, 4)
+    with pytest.raises(RuntimeError, match="GPU"):
+        memory_recurrence(x, x, x, s, s)

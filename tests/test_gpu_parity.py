@@ -1,0 +1,79 @@
+"""GPU parity: libatlas_mem.so (through the C ABI) against the fp64 CPU oracle.
+
+fp32 inputs: rtol 1e-4; bf16 inputs with fp32 state: rtol 2e-2; both with an atol floor of
+tol * max|ref| per tensor (see _cases.compare). Outputs (y, S_T, Z_T, buffer_out) and the
+gradients of every input are checked.
+"""
+
+import sys
+
+import pytest
+import torch
+
+from _cases import Case, compare, make_inputs, run_gpu, run_oracle, tol_for
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+
+CASES = [
+    # BASELINE config 1 (Titans, fp32, forward) with the backward as well
+    Case("c1_titans_fp32", BH=8, T=256, d=64, e=1, gate=None, momentum=False),
+    Case("fp32_token_buffer_d32", BH=3, T=77, d=32, e=3, gate='token', momentum=True, buffer=True, states=0.2, seed=1),
+    Case("fp32_lag_buffer_clamp32", BH=2, T=100, d=64, e=4, gate='lag', momentum=True, buffer=True, states=0.2,
+         clamp_every=32, seed=2),
+    Case("fp32_nomom_map3", BH=2, T=50, d=32, e=2, gate=None, momentum=False, map_degree=3, seed=3),
+    Case("fp32_T1", BH=2, T=1, d=32, e=3, gate='token', momentum=True, buffer=True, states=0.2, seed=4),
+    Case("fp32_T_lt_window", BH=1, T=5, d=32, e=8, gate='lag', momentum=True, buffer=True, states=0.2, seed=5),
+    Case("fp32_clamp_active", BH=2, T=96, d=32, e=2, gate='token', momentum=True, states=150.0, clamp_every=32,
+         decay_shift=7.0, seed=6),
+    Case("fp32_no_final_clamp", BH=2, T=40, d=32, e=1, gate=None, momentum=True, states=150.0, clamp_final=False,
+         decay_shift=7.0, seed=7),
+    # bf16 inputs, fp32 state
+    Case("c2_reduced_bf16", BH=4, T=300, d=64, e=1, gate=None, momentum=True, dtype=BF16, seed=8),
+    Case("c3_reduced_bf16", BH=4, T=256, d=64, e=4, gate='lag', momentum=True, dtype=BF16, seed=9),
+    Case("bf16_token_buffer_d32", BH=3, T=130, d=32, e=3, gate='token', momentum=True, buffer=True, states=0.2,
+         dtype=BF16, seed=10),
+    Case("bf16_map2_nomom", BH=2, T=70, d=64, e=2, gate='token', momentum=False, map_degree=2, dtype=BF16, seed=11),
+]
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def test_mfma_tile_layout():
+    """The fragment/accumulator lane layout of the matrix-core helpers, in isolation."""
+    from atlas_rnn_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(0)
+    for dt, code, tol in ((torch.float32, _lib.DT_F32, 1e-5), (BF16, _lib.DT_BF16, 1e-5)):
+        A = torch.randn(16, 64, generator=g).to(dt)
+        B = torch.randn(16, 64, generator=g).to(dt)
+        Ad, Bd = A.cuda(), B.cuda()
+        C = torch.zeros(2, 16, 16, device="cuda")
+        _say(f"mfma selftest {dt}")
+        _lib.check(lib.atlas_mem_mfma_selftest(code, Ad.data_ptr(), Bd.data_ptr(), C.data_ptr(),
+                                               torch.cuda.current_stream().cuda_stream), "selftest")
+        torch.cuda.synchronize()
+        ref = A.double() @ B.double().T
+        assert torch.allclose(C[0].cpu().double(), ref, rtol=tol, atol=tol * ref.abs().max())
+        assert torch.allclose(C[1].cpu().double(), ref, rtol=tol, atol=tol * ref.abs().max())
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: c.name)
+def test_recurrence_parity(case):
+    _say(f"case {case.name}: BH={case.BH} T={case.T} d={case.d} e={case.e} gate={case.gate} "
+         f"mom={case.momentum} buf={case.buffer} dtype={case.dtype}")
+    p = make_inputs(case)
+    ref_out, ref_grads = run_oracle(case, p)
+    got_out, got_grads = run_gpu(case, p)
+    tol = tol_for(case)
+    for name, g, r in zip(("y", "S_T", "Z_T", "buffer_out"), got_out, ref_out):
+        if r is None:
+            assert g is None, name
+            continue
+        compare(f"{case.name}.{name}", g, r, tol)
+    for name, r in ref_grads.items():
+        compare(f"{case.name}.d{name}", got_grads[name], r, tol)
