@@ -137,7 +137,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_adjoint_walk(const Geom g, con
       for (int k0 = 0; k0 < CH; k0 += M::KS) {
         const typename M::frag fb = frag_ld<T>(&sm.psi[0][0], 1, DK + 8, n0, k0);
         aa = M::mma(frag_ld_kscaled<T>(&sm.dyT[0][0], CH + 1, 1, 0, k0, sm.acoef), fb, aa);
-        if (g.momentum) ak = M::mma(frag_ld_kscaled<T>(&sm.dyT[0][0], CH + 1, 1, 0, k0, sm.kcoef), fb, ak);
+        ak = M::mma(frag_ld_kscaled<T>(&sm.dyT[0][0], CH + 1, 1, 0, k0, sm.kcoef), fb, ak);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_chunk(const Geom g, const BwdP
     for (int t = 0; t < CH; ++t) {
       sm.u.m.wsh[t][s] = ws;
       const int j = t + H - s;
-      const float w = (j >= 0 && j < e) ? src_weight<T>(g.gate_mode, sm.ug, sm.wl, e, s, t, j) : 0.f;
+      const float w = (j >= 0 && j < e && t < L) ? src_weight<T>(g.gate_mode, sm.ug, sm.wl, e, s, t, j) : 0.f;
       wz = sm.beta[t] * wz + w;
       ws = sm.alpha[t] * ws + sm.eta[t] * wz;
     }
@@ -382,7 +382,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_chunk(const Geom g, const BwdP
       for (int k0 = 0; k0 < DK; k0 += M::KS) {
         const typename M::frag fb = frag_ld_row<T>(&sm.u.m.phi[0][0], DK + 8, n0, k0);
         as = M::mma(frag_ld<T>(dSe, DK, 1, m0, k0), fb, as);
-        if (g.momentum) az = M::mma(frag_ld<T>(dZe, DK, 1, m0, k0), fb, az);
+        az = M::mma(frag_ld<T>(dZe, DK, 1, m0, k0), fb, az);   // dZ_end == 0 without momentum
       }
       for (int k0 = 0; k0 < CH; k0 += M::KS)
         aq = M::mma(frag_ld<T>(&sm.u.m.dy[0][0], 1, DV + 8, m0, k0),
@@ -434,7 +434,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_chunk(const Geom g, const BwdP
       for (int k0 = 0; k0 < DV; k0 += M::KS) {
         const typename M::frag fa = frag_ld_row<T>(&sm.u.m.deltaT[0][0], DV + 8, m0, k0);
         a2 = M::mma(fa, frag_ld<T>(dSe, 1, DK, n0, k0), a2);
-        if (g.momentum) a1 = M::mma(fa, frag_ld<T>(dZe, 1, DK, n0, k0), a1);
+        a1 = M::mma(fa, frag_ld<T>(dZe, 1, DK, n0, k0), a1);
         a4 = M::mma(frag_ld<T>(&sm.u.m.dD[0][0], 1, SPM + 8, m0, k0), frag_ld<T>(Sref, 1, DK, n0, k0), a4);
       }
       for (int k0 = 0; k0 < CH; k0 += M::KS)
@@ -499,7 +499,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_chunk(const Geom g, const BwdP
           fs = frag_ld<T>(Sin, 1, DK, n0, k0);
         }
         as = M::mma(fa, fs, as);
-        if (Zin) az = M::mma(fa, frag_ld<T>(Zin, 1, DK, n0, k0), az);
+        az = M::mma(fa, frag_ld_or_zero<T>(Zin, 1, DK, n0, k0), az);
       }
       for (int k0 = 0; k0 < SP; k0 += M::KS)
         aq = M::mma(frag_ld_row<T>(&sm.u.m.Qp[0][0], SPM + 8, m0, k0),
@@ -590,7 +590,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_chunk(const Geom g, const BwdP
     float lz = 0.f, ls = 0.f;
     for (int t = 0; t < CH; ++t) {
       float acc = 0.f;
-      for (int j = 0; j < e; ++j) {
+      for (int j = 0; j < e && t < L; ++j) {
         const int s = t + H - j;
         acc += src_weight<T>(g.gate_mode, sm.ug, sm.wl, e, s, t, j) * sm.Lm[q][s];
       }
@@ -603,7 +603,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_chunk(const Geom g, const BwdP
     float hzs = 0.f, hss = 0.f, hzz = 0.f;
     for (int t = 0; t < CH; ++t) {
       float as = 0.f, az = 0.f;
-      for (int j = 0; j < e; ++j) {
+      for (int j = 0; j < e && t < L; ++j) {
         const int s = t + H - j;
         const float w = src_weight<T>(g.gate_mode, sm.ug, sm.wl, e, s, t, j);
         as += w * sm.hS[s];

@@ -7,6 +7,12 @@
 //     fp32: v_mfma_f32_16x16x4_f32   (k step 4, 1 fp32 per lane)
 // Lane l of the wave supplies A[m0 + (l & 15)][k0 + (l >> 4) * KL + e] (e < KL) and the same
 // pattern of Bt; the accumulator lane l holds C[m0 + 4 * (l >> 4) + i][n0 + (l & 15)], i < 4.
+//
+// Rule: an MFMA is never issued under a condition whose join is followed by a read of its
+// accumulator. With hipcc 7.2 on gfx950 such a join after a conditionally issued
+// v_mfma_f32_16x16x4_f32 got too few wait states before v_accvgpr_read, returning the value
+// from before the last MFMA. Optional terms are therefore computed unconditionally with zero
+// operands (frag_ld_or_zero) instead of being skipped.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -61,6 +67,20 @@ __device__ __forceinline__ typename MM<OT>::frag frag_ld(const ST* p, int rs, in
   } else {
 #pragma unroll
     for (int e = 0; e < MM<OT>::KL; ++e) f[e] = static_cast<OT>(to_f32(q[e * cs]));
+  }
+  return f;
+}
+
+// frag_ld, or a zero fragment when p is null (keeps the MFMA itself unconditional).
+template <typename OT, typename ST>
+__device__ __forceinline__ typename MM<OT>::frag frag_ld_or_zero(const ST* p, int rs, int cs, int r0, int k0) {
+  if (p) return frag_ld<OT>(p, rs, cs, r0, k0);
+  typename MM<OT>::frag f;
+  if constexpr (MM<OT>::KL == 1) {
+    f = static_cast<OT>(0.f);
+  } else {
+#pragma unroll
+    for (int e = 0; e < MM<OT>::KL; ++e) f[e] = static_cast<OT>(0.f);
   }
   return f;
 }

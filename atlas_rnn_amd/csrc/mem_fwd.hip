@@ -155,7 +155,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_walk(const Geom g, const FwdPt
         sm.wsh[t][s] = ws;
         const int j = t + H - s;
         float w = 0.f;
-        if (j >= 0 && j < e) {
+        if (j >= 0 && j < e && t < L) {
           w = (g.gate_mode == GATE_TOKEN) ? sm.ug[s] : (g.gate_mode == GATE_LAG ? sm.wl[t * e + j] : 1.f);
         }
         wz = sm.beta[t] * wz + w;
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_walk(const Geom g, const FwdPt
       for (int k0 = 0; k0 < DK; k0 += M::KS) {
         const typename M::frag fa = frag_ld_row<T>(&sm.psi[0][0], DK + 8, m0, k0);
         as = M::mma(fa, frag_ld<T>(&sm.S[0][0], DK + 1, 1, 0, k0), as);
-        if (g.momentum) az = M::mma(fa, frag_ld<T>(&sm.Z[0][0], DK + 1, 1, 0, k0), az);
+        az = M::mma(fa, frag_ld<T>(&sm.Z[0][0], DK + 1, 1, 0, k0), az);   // sm.Z == 0 without momentum
       }
       f32x4 yv;
 #pragma unroll
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_walk(const Geom g, const FwdPt
       for (int k0 = 0; k0 < SP; k0 += M::KS) {
         const typename M::frag fb = frag_ld<T>(&sm.phi[0][0], 1, DK + 8, n0, k0);
         au = M::mma(frag_ld_kscaled<T>(&sm.delta[0][0], SPM + 1, 1, 0, k0, sm.wsend), fb, au);
-        if (g.momentum) av = M::mma(frag_ld_kscaled<T>(&sm.delta[0][0], SPM + 1, 1, 0, k0, sm.wzend), fb, av);
+        av = M::mma(frag_ld_kscaled<T>(&sm.delta[0][0], SPM + 1, 1, 0, k0, sm.wzend), fb, av);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
