@@ -39,8 +39,13 @@ EXPORTED_SYMBOLS = (
     "atlas_scan_fwd",
     "atlas_scan_bwd",
     "atlas_window_sum",
+    "atlas_mem_profile_enable",
+    "atlas_mem_profile_read",
+    "atlas_mem_kernel_name",
     "atlas_mem_mfma_selftest",
 )
+
+NKERNELS = 6
 
 
 class Problem(ctypes.Structure):
@@ -103,6 +108,12 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_scan_bwd.argtypes = [i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.atlas_window_sum.restype = i32
     lib.atlas_window_sum.argtypes = [i32, i64, i64, i64, i32, i32, vp, vp, vp]
+    lib.atlas_mem_profile_enable.restype = i32
+    lib.atlas_mem_profile_enable.argtypes = [i32]
+    lib.atlas_mem_profile_read.restype = i32
+    lib.atlas_mem_profile_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_longlong), i32, i32]
+    lib.atlas_mem_kernel_name.restype = ctypes.c_char_p
+    lib.atlas_mem_kernel_name.argtypes = [i32]
     lib.atlas_mem_mfma_selftest.restype = i32
     lib.atlas_mem_mfma_selftest.argtypes = [i32, vp, vp, vp, vp]
     if lib.atlas_mem_abi_version() != ABI_VERSION:

@@ -1,6 +1,9 @@
 // abi.hip - extern "C" entry points of libatlas_mem.so (declared in include/atlas_mem.h).
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+#include <vector>
+
 #include "../../include/atlas_mem.h"
 #include "mem_common.h"
 #include "mem_params.h"
@@ -37,6 +40,56 @@ __global__ __launch_bounds__(64) void k_mfma_selftest(const T* A, const T* B, fl
 }  // namespace atlas
 
 using namespace atlas;
+
+// ---------------------------------------------------------------------------------------------
+// Opt-in kernel timing: when enabled, every launch is bracketed by two HIP events recorded on the
+// launch stream; atlas_mem_profile_read() waits for them and accumulates per-kernel time.
+// ---------------------------------------------------------------------------------------------
+namespace {
+struct Pending { int kid; hipEvent_t a, b; };
+struct Profiler {
+  std::mutex mu;
+  bool on = false;
+  std::vector<hipEvent_t> pool;
+  std::vector<Pending> pending;
+  hipEvent_t open[KID_COUNT] = {};
+  double ms[KID_COUNT] = {};
+  long long n[KID_COUNT] = {};
+  hipEvent_t take() {
+    if (!pool.empty()) { hipEvent_t e = pool.back(); pool.pop_back(); return e; }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+};
+Profiler& prof() { static Profiler p; return p; }
+const char* kKernelNames[KID_COUNT] = {"k_fwd_walk", "k_buffer_out", "k_bwd_adjoint_walk", "k_bwd_chunk",
+                                       "k_bwd_fixup", "k_reduce_dsref"};
+}  // namespace
+
+namespace atlas {
+void prof_begin(int kid, hipStream_t s) {
+  Profiler& P = prof();
+  if (!P.on) return;
+  std::lock_guard<std::mutex> lk(P.mu);
+  hipEvent_t e = P.take();
+  if (!e) return;
+  hipEventRecord(e, s);
+  P.open[kid] = e;
+}
+void prof_end(int kid, hipStream_t s) {
+  Profiler& P = prof();
+  if (!P.on) return;
+  std::lock_guard<std::mutex> lk(P.mu);
+  hipEvent_t a = P.open[kid];
+  if (!a) return;
+  hipEvent_t b = P.take();
+  if (!b) return;
+  hipEventRecord(b, s);
+  P.pending.push_back({kid, a, b});
+  P.open[kid] = nullptr;
+}
+}  // namespace atlas
 
 namespace {
 
@@ -240,6 +293,39 @@ int atlas_mem_bwd(const atlas_mem_problem* prob, const atlas_mem_bwd_args* args,
   hipStream_t s = static_cast<hipStream_t>(stream);
   return p.dtype == ATLAS_DT_BF16 ? run_bwd<bf16>(pl, args, saved, workspace, s)
                                   : run_bwd<float>(pl, args, saved, workspace, s);
+}
+
+int atlas_mem_profile_enable(int on) {
+  Profiler& P = prof();
+  std::lock_guard<std::mutex> lk(P.mu);
+  P.on = on != 0;
+  return ATLAS_MEM_OK;
+}
+
+int atlas_mem_profile_read(double* ms, long long* launches, int n, int reset) {
+  Profiler& P = prof();
+  std::lock_guard<std::mutex> lk(P.mu);
+  for (const Pending& q : P.pending) {
+    float t = 0.f;
+    if (hipEventSynchronize(q.b) != hipSuccess || hipEventElapsedTime(&t, q.a, q.b) != hipSuccess) return ATLAS_MEM_ERR_LAUNCH;
+    P.ms[q.kid] += t;
+    P.n[q.kid] += 1;
+    P.pool.push_back(q.a);
+    P.pool.push_back(q.b);
+  }
+  P.pending.clear();
+  for (int i = 0; i < n && i < KID_COUNT; ++i) {
+    if (ms) ms[i] = P.ms[i];
+    if (launches) launches[i] = P.n[i];
+  }
+  if (reset) {
+    for (int i = 0; i < KID_COUNT; ++i) { P.ms[i] = 0.0; P.n[i] = 0; }
+  }
+  return ATLAS_MEM_OK;
+}
+
+const char* atlas_mem_kernel_name(int kid) {
+  return (kid >= 0 && kid < KID_COUNT) ? kKernelNames[kid] : "";
 }
 
 int atlas_mem_mfma_selftest(int dtype, const void* A, const void* B, float* C, void* stream) {

@@ -772,7 +772,9 @@ hipError_t launch_bwd(const Geom& g, const BwdPtrs<T>& a, hipStream_t stream) {
     err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bwd_adjoint_walk<T, CH, DK, DV>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (err != hipSuccess) return err;
+    prof_begin(KID_BWD_ADJOINT, stream);
     hipLaunchKernelGGL((k_bwd_adjoint_walk<T, CH, DK, DV>), dim3(DV / 16, g.BH), dim3(kThreads), smem, stream, g, a);
+    prof_end(KID_BWD_ADJOINT, stream);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   {
@@ -780,13 +782,19 @@ hipError_t launch_bwd(const Geom& g, const BwdPtrs<T>& a, hipStream_t stream) {
     err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bwd_chunk<T, CH, DK, DV>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (err != hipSuccess) return err;
+    prof_begin(KID_BWD_CHUNK, stream);
     hipLaunchKernelGGL((k_bwd_chunk<T, CH, DK, DV>), dim3(g.nc, g.BH), dim3(kThreads), smem, stream, g, a);
+    prof_end(KID_BWD_CHUNK, stream);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
+  prof_begin(KID_BWD_FIXUP, stream);
   hipLaunchKernelGGL((k_bwd_fixup<T, DK, DV>), dim3(g.nc, g.BH), dim3(kThreads), 0, stream, g, a);
+  prof_end(KID_BWD_FIXUP, stream);
   if ((err = hipGetLastError()) != hipSuccess) return err;
+  prof_begin(KID_REDUCE_DSREF, stream);
   hipLaunchKernelGGL(k_reduce_dsref, dim3((DV * DK + kThreads - 1) / kThreads, g.BH), dim3(kThreads), 0, stream,
                      g, (const float*)a.dsref_part, a.dS_ref);
+  prof_end(KID_REDUCE_DSREF, stream);
   return hipGetLastError();
 }
 

@@ -336,11 +336,15 @@ hipError_t launch_fwd(const Geom& g, const FwdPtrs<T>& a, hipStream_t stream) {
   hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_walk<T, CH, DK, DV>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (err != hipSuccess) return err;
+  prof_begin(KID_FWD_WALK, stream);
   hipLaunchKernelGGL((k_fwd_walk<T, CH, DK, DV>), dim3(DV / 16, g.BH), dim3(kThreads), smem, stream, g, a);
+  prof_end(KID_FWD_WALK, stream);
   err = hipGetLastError();
   if (err != hipSuccess) return err;
   if (g.H > 0 && a.buf_out) {
+    prof_begin(KID_BUFFER_OUT, stream);
     hipLaunchKernelGGL((k_buffer_out<T, DK, DV>), dim3(g.H, g.BH), dim3(kThreads), 0, stream, g, a);
+    prof_end(KID_BUFFER_OUT, stream);
     err = hipGetLastError();
   }
   return err;

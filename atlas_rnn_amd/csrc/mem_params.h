@@ -4,6 +4,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <hip/hip_runtime.h>
+
 namespace atlas {
 
 // Gate modes / map modes mirror atlas_mem.h.
@@ -52,5 +54,13 @@ struct BwdPtrs {
   float* halo_part;    // [BH][nc][H][DV + DK]  partial (dv, dphi) for the previous chunk's last H tokens
   float* dw;           // [BH][T][e] per (target, lag) weight gradients (token mode)
 };
+
+// Opt-in per-kernel timing (atlas_mem_profile_*): brackets each launch with HIP events.
+enum KernelId {
+  KID_FWD_WALK = 0, KID_BUFFER_OUT, KID_BWD_ADJOINT, KID_BWD_CHUNK, KID_BWD_FIXUP, KID_REDUCE_DSREF,
+  KID_COUNT
+};
+void prof_begin(int kid, hipStream_t s);
+void prof_end(int kid, hipStream_t s);
 
 }  // namespace atlas

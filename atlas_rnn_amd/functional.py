@@ -333,3 +333,96 @@ def window_sum(x: Tensor, window: int) -> Tensor:
     _require_gpu(x)
     dt = x.dtype if x.dtype in _DTYPES else torch.float32
     return _WindowSumFn.apply(x.to(dt).contiguous(), int(window))
+
+
+# ------------------------------------------------------------------------------------------
+# Preallocated plan: direct C-ABI calls for a fixed problem shape
+# ------------------------------------------------------------------------------------------
+
+class RecurrencePlan:
+    """Forward/backward of one problem shape with every buffer allocated up front.
+
+    No autograd and no per-call allocation: `forward` and `backward` only launch the library
+    on the current stream. Outputs and gradients live in the plan and are overwritten by the
+    next call.
+    """
+
+    def __init__(self, bh: int, T: int, d: int, *, window: int = 1, momentum: bool = True,
+                 gate_mode: str | None = None, dtype=torch.bfloat16, map_degree: int = 1,
+                 has_buffer: bool = False, clamp_every: int | None = None, clamp_final: bool = True,
+                 device="cuda"):
+        lib = _lib.load()
+        self.lib = lib
+        self.device = torch.device(device)
+        cfg = RecurrenceConfig(window=window, map_mode='elementwise' if map_degree > 1 else 'off',
+                               map_degree=map_degree, clamp_every=clamp_every, clamp_final=clamp_final)
+        gate_stub = None
+        if gate_mode == 'token':
+            gate_stub = torch.empty(1, 1)
+        elif gate_mode == 'lag':
+            gate_stub = torch.empty(1, 1, 1)
+        self.prob = _problem(cfg, bh, T, d, d, momentum, gate_stub, has_buffer, dtype)
+        _lib.check(lib.atlas_mem_validate(ctypes.byref(self.prob)), "atlas_mem_validate")
+        dev, f32 = self.device, torch.float32
+        self.shape = (bh, T, d)
+        self.momentum, self.window, self.dtype = momentum, window, dtype
+        self.y = torch.empty(bh, T, d, device=dev, dtype=dtype)
+        self.S_T = torch.empty(bh, d, d, device=dev, dtype=f32)
+        self.Z_T = torch.empty(bh, d, d, device=dev, dtype=f32) if momentum else None
+        self.buf_out = torch.empty(bh, window - 1, d, d, device=dev, dtype=f32) if window > 1 else None
+        self.saved = torch.empty(lib.atlas_mem_saved_bytes(ctypes.byref(self.prob)) // 4, device=dev, dtype=f32)
+        self.ws_bytes = lib.atlas_mem_bwd_workspace_bytes(ctypes.byref(self.prob))
+        self.ws = torch.empty((self.ws_bytes + 3) // 4, device=dev, dtype=f32)
+        self.grads = None
+        self._inputs = None
+
+    def forward(self, k, q, v, lr, decay, beta=None, gate=None, S_ref=None, S0=None, Z0=None, buffer=None):
+        self._inputs = (k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buffer)
+        a = _lib.FwdArgs(k=_ptr(k), q=_ptr(q), v=_ptr(v), lr=_ptr(lr), decay=_ptr(decay), beta=_ptr(beta),
+                         gate=_ptr(gate), S_ref=_ptr(S_ref), S0=_ptr(S0), Z0=_ptr(Z0), buffer_in=_ptr(buffer),
+                         y=_ptr(self.y), S_T=_ptr(self.S_T), Z_T=_ptr(self.Z_T), buffer_out=_ptr(self.buf_out))
+        _lib.check(self.lib.atlas_mem_fwd(ctypes.byref(self.prob), ctypes.byref(a), _ptr(self.saved),
+                                          _stream(self.device)), "atlas_mem_fwd")
+        return self.y, self.S_T, self.Z_T, self.buf_out
+
+    def backward(self, dy, dS_T=None, dZ_T=None, dbuffer_out=None):
+        if self._inputs is None:
+            raise RuntimeError("RecurrencePlan.backward before forward")
+        k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buf = self._inputs
+        if self.grads is None:
+            f32 = torch.float32
+            bh, T, d = self.shape
+            self.grads = dict(
+                k=torch.empty_like(k), q=torch.empty_like(q), v=torch.empty_like(v), lr=torch.empty_like(lr),
+                decay=torch.empty_like(decay), beta=torch.empty_like(beta) if beta is not None else None,
+                gate=torch.empty_like(gate) if gate is not None else None,
+                S_ref=torch.empty(bh, d, d, device=self.device, dtype=f32),
+                S0=torch.empty(bh, d, d, device=self.device, dtype=f32),
+                Z0=torch.empty(bh, d, d, device=self.device, dtype=f32) if self.momentum else None,
+                buffer=torch.empty_like(buf) if buf is not None else None)
+        gr = self.grads
+        a = _lib.BwdArgs(k=_ptr(k), q=_ptr(q), v=_ptr(v), lr=_ptr(lr), decay=_ptr(decay), beta=_ptr(beta),
+                         gate=_ptr(gate), S_ref=_ptr(S_ref), S0=_ptr(S0), Z0=_ptr(Z0), buffer_in=_ptr(buf),
+                         dy=_ptr(dy), dS_T=_ptr(dS_T), dZ_T=_ptr(dZ_T), dbuffer_out=_ptr(dbuffer_out),
+                         dk=_ptr(gr["k"]), dq=_ptr(gr["q"]), dv=_ptr(gr["v"]), dlr=_ptr(gr["lr"]),
+                         ddecay=_ptr(gr["decay"]), dbeta=_ptr(gr["beta"]), dgate=_ptr(gr["gate"]),
+                         dS_ref=_ptr(gr["S_ref"]), dS0=_ptr(gr["S0"]), dZ0=_ptr(gr["Z0"]),
+                         dbuffer_in=_ptr(gr["buffer"]))
+        _lib.check(self.lib.atlas_mem_bwd(ctypes.byref(self.prob), ctypes.byref(a), _ptr(self.saved), _ptr(self.ws),
+                                          ctypes.c_size_t(self.ws_bytes), _stream(self.device)), "atlas_mem_bwd")
+        return gr
+
+
+def profile_enable(on: bool = True) -> None:
+    """Per-kernel HIP-event timing inside the library (see atlas_mem_profile_enable)."""
+    _lib.check(_lib.load().atlas_mem_profile_enable(int(on)), "atlas_mem_profile_enable")
+
+
+def profile_read(reset: bool = True) -> dict:
+    """{kernel name: (total ms, launches)} accumulated since the last reset."""
+    lib = _lib.load()
+    n = _lib.NKERNELS
+    ms = (ctypes.c_double * n)()
+    cnt = (ctypes.c_longlong * n)()
+    _lib.check(lib.atlas_mem_profile_read(ms, cnt, n, int(reset)), "atlas_mem_profile_read")
+    return {lib.atlas_mem_kernel_name(i).decode(): (ms[i], cnt[i]) for i in range(n)}

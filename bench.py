@@ -1,0 +1,187 @@
+"""Headline benchmark: OmegaNet-RNN memory-layer recurrence, forward + backward, on one MI355X.
+
+Workload (the metric's shape): B=4, H=8 (BH=32), T=4096, d_k=d_v=64,
+Omega window e=4 with per-lag softmax gates, momentum, bf16 inputs, fp32 state, chunk 64,
+S0 = S_ref = Z0 = 0, zero buffer; dy ~ N(0,1) (loss = sum y * g). Inputs are synthetic, seeded,
+and resident in HBM before the timed region. One step = one forward + one backward of the
+recurrence over the whole batch (libatlas_mem.so through its C ABI, preallocated buffers).
+
+Prints ONE JSON line (rank 0). `roofline` covers the kernel with the largest share of the timed
+region, timed live with HIP events recorded by the library on the launch stream;
+`cpu_baseline` times the CPU oracle (the fp32 torch restatement of the reference op sequence,
+forward + backward through autograd) on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+B, H, T, D, E = 4, 8, 4096, 64, 4
+BH = B * H
+TOKENS = B * T               # (b, t) positions through one memory layer, all heads
+
+
+def algorithmic_bytes(bh=BH, t=T, d=D, e=E, s_in=2, s_st=4):
+    """Compulsory HBM bytes (each input read once, each output written once) per kernel and per
+    step. Scalars per token-head: eta, alpha, beta and e lag gates."""
+    n = bh * t
+    n_sc = 3 + e
+    st = bh * d * d * s_st
+    buf = 2 * bh * (e - 1) * d * d * s_st
+    fwd = n * 3 * d * s_in + n * n_sc * s_in + n * d * s_in + 5 * st + buf
+    bwd = n * 4 * d * s_in + 2 * n * n_sc * s_in + n * 3 * d * s_in + 8 * st + buf
+    per_kernel = {
+        # forward walk: read k, q, v, scalars, S_ref/S0/Z0; write y, S_T, Z_T
+        "k_fwd_walk": n * 3 * d * s_in + n * n_sc * s_in + n * d * s_in + 5 * st,
+        "k_buffer_out": n and bh * (e - 1) * (2 * d * s_in + d * d * s_st),
+        # adjoint walk: read q, dy, alpha/eta/beta, dS_T, dZ_T; write dS0, dZ0
+        "k_bwd_adjoint_walk": n * 2 * d * s_in + n * 3 * s_in + 4 * st,
+        # per-chunk gradients: read k, q, v, dy, scalars, S_ref; write dk, dq, dv, scalar grads
+        "k_bwd_chunk": n * 4 * d * s_in + 2 * n * n_sc * s_in + n * 3 * d * s_in + st,
+        "k_bwd_fixup": 0,
+        "k_reduce_dsref": st,
+    }
+    return fwd, bwd, per_kernel
+
+
+def make_inputs(device):
+    import torch
+    g = torch.Generator().manual_seed(1003)       # seed = 1000 + config number
+    r = lambda *s: torch.randn(*s, generator=g)
+    k = r(BH, T, D)
+    k = k / k.norm(dim=-1, keepdim=True)
+    x = dict(k=k, q=r(BH, T, D), v=r(BH, T, D),
+             lr=0.1 * torch.sigmoid(r(BH, T)), decay=torch.sigmoid(r(BH, T) * 0.5 + 2.0),
+             beta=torch.sigmoid(r(BH, T) * 0.5 + 1.0), gate=torch.softmax(r(BH, T, E), dim=-1),
+             dy=r(BH, T, D))
+    out = {kk: v.to(device=device, dtype=torch.bfloat16).contiguous() for kk, v in x.items()}
+    zeros = torch.zeros(BH, D, D, device=device, dtype=torch.float32)
+    out.update(S_ref=zeros, S0=zeros, Z0=zeros)
+    return out, x
+
+
+def cpu_baseline(x_cpu, sample_t=256, reps=3):
+    """Oracle (fp32, autograd) on the first `sample_t` tokens of every (b, h): 1 warmup, median
+    of `reps`. Returns tokens/s of the sample and the thread count."""
+    import torch
+    from oracle import memory_recurrence_vectorised
+    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(cores)
+    sl = slice(0, sample_t)
+    f32 = torch.float32
+    leaves = {kk: x_cpu[kk][:, sl].to(torch.bfloat16).to(f32).clone().requires_grad_(True)
+              for kk in ("k", "q", "v", "lr", "decay", "beta", "gate")}
+    dy = x_cpu["dy"][:, sl].to(torch.bfloat16).to(f32)
+    S0 = torch.zeros(BH, D, D, requires_grad=True)
+    Z0 = torch.zeros(BH, D, D, requires_grad=True)
+    times = []
+    for i in range(reps + 1):
+        t0 = time.perf_counter()
+        y, S_T, Z_T, buf = memory_recurrence_vectorised(
+            leaves["k"], leaves["q"], leaves["v"], leaves["lr"], leaves["decay"], leaves["beta"], leaves["gate"],
+            S0, S0, Z0, None, window=E)
+        (y * dy).sum().backward()
+        dt = time.perf_counter() - t0
+        if i > 0:
+            times.append(dt)
+        for t in list(leaves.values()) + [S0, Z0]:
+            t.grad = None
+    med = statistics.median(times)
+    return B * sample_t / med, cores, med
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-tokens", type=int, default=256)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the memory-layer recurrence shards over (batch, head) rows "
+              "with no exchange, so there is no multi-GPU figure to report (use --gpus 1).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from atlas_rnn_amd.functional import RecurrencePlan, profile_enable, profile_read
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    x, x_cpu = make_inputs(dev)
+    plan = RecurrencePlan(BH, T, D, window=E, momentum=True, gate_mode='lag', dtype=torch.bfloat16, device=dev)
+
+    def step():
+        plan.forward(x["k"], x["q"], x["v"], x["lr"], x["decay"], x["beta"], x["gate"], x["S_ref"], x["S0"], x["Z0"])
+        plan.backward(x["dy"])
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    profile_enable(True)
+    profile_read(reset=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    prof = profile_read(reset=True)
+    profile_enable(False)
+
+    elapsed = t1 - t0
+    ms_per_step = 1e3 * elapsed / args.steps
+    value = TOKENS * args.steps / elapsed
+    fwd_b, bwd_b, per_kernel = algorithmic_bytes()
+    step_bytes = fwd_b + bwd_b
+    kernels = {name: {"avg_us": 1e3 * ms / max(n, 1), "launches": n, "share": ms / (1e3 * elapsed) if elapsed else 0}
+               for name, (ms, n) in prof.items() if n}
+    dom = max(kernels, key=lambda kk: kernels[kk]["avg_us"] * kernels[kk]["launches"])
+    dom_s = kernels[dom]["avg_us"] * 1e-6
+    achieved = per_kernel[dom] / dom_s / 1e9
+    roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                "algorithmic_bytes_per_launch": per_kernel[dom], "avg_launch_us": round(kernels[dom]["avg_us"], 2)}
+    step_gbs = step_bytes / (elapsed / args.steps) / 1e9
+    out = {
+        "metric": "memory-layer tokens/s fwd+bwd at H=8,d=64,T=4096; % HBM/MFMA roofline",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v with L2-normalised keys, sigmoid gates, softmax lag gates)",
+        "config": {"workload": "C3 OmegaNet-RNN memory layer: B=4 H=8 T=4096 d=64 e=4 lag gates, momentum, "
+                               "bf16 inputs, fp32 state, chunk 64", "global_batch": B, "seq_len": T,
+                   "heads": H, "d": D, "window": E, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "step_roofline": {"bytes_per_step": step_bytes, "achieved_gbs": round(step_gbs, 2),
+                          "frac": round(step_gbs / HBM_PEAK_GBS, 5)},
+        "kernels": {kk: {"avg_us": round(v["avg_us"], 2), "launches": v["launches"]} for kk, v in kernels.items()},
+    }
+    if not args.no_cpu_baseline:
+        cpu_tps, cores, med = cpu_baseline(x_cpu, sample_t=args.cpu_sample_tokens)
+        out["cpu_baseline"] = {"value": round(cpu_tps, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+                               "sample": f"oracle fp32 fwd+bwd (autograd) on tokens 0..{args.cpu_sample_tokens - 1} "
+                                         f"of all {BH} (b,h) rows, median of 3 = {med:.2f} s"}
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -164,6 +164,22 @@ int atlas_scan_bwd(int dtype, int64_t n, int64_t t, int64_t d, const void* gates
 int atlas_window_sum(int dtype, int64_t n, int64_t t, int64_t d, int window, int reverse,
                      const void* x, void* y, void* stream);
 
+/* ---- diagnostics (no reference counterpart) ------------------------------------------------ */
+
+/* Number of kernels the timing hooks distinguish (index -> atlas_mem_kernel_name). */
+#define ATLAS_MEM_NKERNELS 6
+
+/* Opt-in timing: while enabled, each kernel launch of atlas_mem_fwd/atlas_mem_bwd is bracketed
+ * by HIP events on its stream (adds two event records per launch). */
+int atlas_mem_profile_enable(int on);
+
+/* Waits for the recorded events and returns accumulated milliseconds and launch counts per kernel
+ * (arrays of n <= ATLAS_MEM_NKERNELS entries; either may be NULL); reset != 0 clears the totals. */
+int atlas_mem_profile_read(double* ms, long long* launches, int n, int reset);
+
+/* Kernel name for a timing index ("" if out of range). */
+const char* atlas_mem_kernel_name(int kid);
+
 /* Diagnostic: C[16,16] = A[16,64] * B[16,64]^T through the library's MFMA tile helpers
  * (dtype selects bf16 or fp32 inputs; C is fp32). No reference counterpart; used by the
  * GPU tests to check the matrix-core lane layout in isolation. */
