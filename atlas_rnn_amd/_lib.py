@@ -45,7 +45,7 @@ EXPORTED_SYMBOLS = (
     "atlas_mem_mfma_selftest",
 )
 
-NKERNELS = 6
+NKERNELS = 7
 
 
 class Problem(ctypes.Structure):

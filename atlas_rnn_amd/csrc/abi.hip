@@ -7,10 +7,16 @@
 #include "../../include/atlas_mem.h"
 #include "mem_common.h"
 #include "mem_params.h"
+#include "seg_common.h"
+
+#include <cstdlib>
 
 namespace atlas {
-template <typename T, int CH, int DK, int DV> hipError_t launch_fwd(const Geom&, const FwdPtrs<T>&, hipStream_t);
-template <typename T, int CH, int DK, int DV> hipError_t launch_bwd(const Geom&, const BwdPtrs<T>&, hipStream_t);
+template <typename T, int CH, int D>
+hipError_t launch_fwd_seg(const Geom&, const FwdPtrs<T>&, const SegGeom&, float*, float*, float*, hipStream_t);
+template <typename T, int CH, int D>
+hipError_t launch_bwd_seg(const Geom&, const BwdPtrs<T>&, const SegGeom&, const BwdSegPtrs&, hipStream_t);
+template <typename T, int DK, int DV> hipError_t launch_buffer_out(const Geom&, const FwdPtrs<T>&, hipStream_t);
 
 // Diagnostic tile product C = A B^T (16 x 64 inputs) through the same fragment helpers.
 template <typename T>
@@ -63,8 +69,8 @@ struct Profiler {
   }
 };
 Profiler& prof() { static Profiler p; return p; }
-const char* kKernelNames[KID_COUNT] = {"k_fwd_walk", "k_buffer_out", "k_bwd_adjoint_walk", "k_bwd_chunk",
-                                       "k_bwd_fixup", "k_reduce_dsref"};
+const char* kKernelNames[KID_COUNT] = {"k_fwd_seg_agg", "k_fwd_seg", "k_buffer_out", "k_bwd_seg_agg",
+                                       "k_bwd_seg", "k_bwd_seg_fixup", "k_seg_reduce_dsref"};
 }  // namespace
 
 namespace atlas {
@@ -94,13 +100,46 @@ void prof_end(int kid, hipStream_t s) {
 namespace {
 
 struct Plan {
-  Geom g;
+  Geom g;      // forward chunks (Lc <= 64 bf16, 32 fp32)
+  SegGeom sg;
+  Geom gb;     // backward chunks (Lb <= 32 bf16, 16 fp32; Lb divides Lc)
+  SegGeom sgb;
   int CH;
   bool ok;
   int status;
 };
 
+// Segments per head-batch row: enough (segment, bh) workgroups to cover the 256 CUs twice;
+// a single segment when S is clamped at scan_chunk_len boundaries (not affine).
+// ATLAS_MEM_SEG_CHUNKS overrides the chunks per segment (tuning).
+SegGeom make_seg(const Geom& g) {
+  SegGeom s{};
+  int G;
+  if (g.clamp_every > 0) {
+    G = g.nc;
+  } else {
+    const int want = g.BH >= 512 ? 1 : (512 + g.BH - 1) / g.BH;
+    G = (g.nc + want - 1) / want;
+    if (const char* env = std::getenv("ATLAS_MEM_SEG_CHUNKS")) {
+      const int v = std::atoi(env);
+      if (v > 0) G = v;
+    }
+  }
+  if (G < 1) G = 1;
+  if (G > g.nc) G = g.nc;
+  s.G = G;
+  s.nseg = (g.nc + G - 1) / G;
+  s.agg_stride = 2 * g.DV * g.DK + 16;
+  return s;
+}
+
 int chunk_cap(int dtype) { return dtype == ATLAS_DT_BF16 ? 64 : 32; }
+int bwd_chunk_cap(int dtype) { return dtype == ATLAS_DT_BF16 ? 32 : 16; }
+int largest_divisor_at_most(int n, int cap) {
+  for (int d = cap; d >= 1; --d)
+    if (n % d == 0) return d;
+  return 1;
+}
 
 Plan make_plan(const atlas_mem_problem* p) {
   Plan pl{};
@@ -120,14 +159,10 @@ Plan make_plan(const atlas_mem_problem* p) {
   if (p->has_buffer && p->window == 1) return pl;
   const int CH = chunk_cap(p->dtype);
   int Lc = CH;
-  if (p->clamp_every > 0 && p->clamp_every % CH != 0) {
-    Lc = 1;
-    for (int d = CH; d >= 1; --d) {
-      if (p->clamp_every % d == 0) { Lc = d; break; }
-    }
-  }
+  if (p->clamp_every > 0 && p->clamp_every % CH != 0) Lc = largest_divisor_at_most(p->clamp_every, CH);
+  const int Lb = largest_divisor_at_most(Lc, bwd_chunk_cap(p->dtype));
   const int H = p->window - 1;
-  if (Lc < H) { pl.status = ATLAS_MEM_ERR_UNSUPPORTED; return pl; }
+  if (Lb < H) { pl.status = ATLAS_MEM_ERR_UNSUPPORTED; return pl; }
   Geom& g = pl.g;
   g.BH = p->bh; g.T = p->seq_len; g.DK = p->d_k; g.DV = p->d_v;
   g.e = p->window; g.H = H; g.Lc = Lc; g.nc = (p->seq_len + Lc - 1) / Lc;
@@ -135,6 +170,17 @@ Plan make_plan(const atlas_mem_problem* p) {
   g.momentum = p->momentum; g.gate_mode = p->gate_mode; g.map_mode = p->map_mode;
   g.map_deg = p->map_mode == ATLAS_MAP_ELEMENTWISE ? p->map_degree : 1;
   g.has_buf = p->has_buffer; g.clamp_every = p->clamp_every; g.clamp_final = p->clamp_final;
+  pl.sg = make_seg(g);
+  // backward: same segments, chunks of Lb
+  Geom& gb = pl.gb;
+  gb = g;
+  gb.Lc = Lb;
+  gb.nc = (p->seq_len + Lb - 1) / Lb;
+  const int CHB = bwd_chunk_cap(p->dtype);
+  const int spr = p->dtype == ATLAS_DT_BF16 ? 32 : 16;
+  gb.SP = ((H + CHB + spr - 1) / spr) * spr;
+  pl.sgb = pl.sg;
+  pl.sgb.G = pl.sg.G * (Lc / Lb);
   pl.CH = CH;
   pl.ok = true;
   pl.status = ATLAS_MEM_OK;
@@ -143,18 +189,40 @@ Plan make_plan(const atlas_mem_problem* p) {
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-struct BwdLayout {
-  size_t adj, dsref, tail, halo, dw, total;
+// `saved` layout: segment-start states, segment aggregates (forward scratch), raw S_{T-1}.
+struct SavedLayout {
+  size_t seg, agg, final_raw, total;
 };
 
-BwdLayout bwd_layout(const Geom& g) {
+SavedLayout saved_layout(const Plan& pl) {
+  const Geom& g = pl.g;
+  SavedLayout L{};
+  const size_t st = (size_t)g.DV * g.DK * sizeof(float);
+  size_t off = 0;
+  L.seg = off; off += align256((size_t)g.BH * pl.sg.nseg * 2 * st);
+  L.agg = off; off += align256((size_t)g.BH * pl.sg.nseg * pl.sg.agg_stride * sizeof(float));
+  L.final_raw = off; off += align256((size_t)g.BH * st);
+  L.total = off;
+  return L;
+}
+
+// backward workspace: adjoint aggregates, re-walk chunk states, dS_ref partials, boundary partials,
+// token-gate (target, lag) gradients.
+struct BwdLayout {
+  size_t agg, rw, dsref, tail, halo, dw, total;
+};
+
+BwdLayout bwd_layout(const Plan& pl) {
+  const Geom& g = pl.gb;
+  const int nseg = pl.sgb.nseg;
   BwdLayout L{};
   const size_t st = (size_t)g.DV * g.DK * sizeof(float);
   size_t off = 0;
-  L.adj = off; off += align256((size_t)g.BH * g.nc * 2 * st);
-  L.dsref = off; off += align256((size_t)g.BH * g.nc * st);
-  L.tail = off; off += align256((size_t)g.BH * g.nc * g.H * (g.DV + g.DK) * sizeof(float));
-  L.halo = off; off += align256((size_t)g.BH * g.nc * g.H * (g.DV + g.DK) * sizeof(float));
+  L.agg = off; off += align256((size_t)g.BH * nseg * pl.sgb.agg_stride * sizeof(float));
+  L.rw = off; off += align256((size_t)g.BH * nseg * pl.sgb.G * 2 * st);
+  L.dsref = off; off += align256((size_t)g.BH * nseg * st);
+  L.tail = off; off += align256((size_t)g.BH * nseg * g.H * (g.DV + g.DK) * sizeof(float));
+  L.halo = off; off += align256((size_t)g.BH * nseg * g.H * (g.DV + g.DK) * sizeof(float));
   L.dw = off; off += align256(g.gate_mode == ATLAS_GATE_TOKEN ? (size_t)g.BH * g.T * g.e * sizeof(float) : 0);
   L.total = off;
   return L;
@@ -168,25 +236,35 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
   a.k = (const T*)x->k; a.q = (const T*)x->q; a.v = (const T*)x->v;
   a.lr = (const T*)x->lr; a.decay = (const T*)x->decay; a.beta = (const T*)x->beta; a.gate = (const T*)x->gate;
   a.S_ref = x->S_ref; a.S0 = x->S0; a.Z0 = x->Z0; a.buf_in = x->buffer_in;
-  a.y = (T*)x->y; a.S_T = x->S_T; a.Z_T = x->Z_T; a.buf_out = x->buffer_out; a.saved = saved;
+  const SavedLayout SL = saved_layout(pl);
+  unsigned char* sv = reinterpret_cast<unsigned char*>(saved);
+  a.y = (T*)x->y; a.S_T = x->S_T; a.Z_T = x->Z_T; a.buf_out = x->buffer_out;
+  a.saved = nullptr;
+  float* seg_states = reinterpret_cast<float*>(sv + SL.seg);
+  float* agg = reinterpret_cast<float*>(sv + SL.agg);
+  float* final_raw = reinterpret_cast<float*>(sv + SL.final_raw);
   const Geom& g = pl.g;
   hipError_t err = hipErrorInvalidValue;
   if (g.DK == 64) {
-    if constexpr (sizeof(T) == 2) err = launch_fwd<T, 64, 64, 64>(g, a, s);
-    else err = launch_fwd<T, 32, 64, 64>(g, a, s);
+    if constexpr (sizeof(T) == 2) err = launch_fwd_seg<T, 64, 64>(g, a, pl.sg, agg, seg_states, final_raw, s);
+    else err = launch_fwd_seg<T, 32, 64>(g, a, pl.sg, agg, seg_states, final_raw, s);
+    if (err == hipSuccess) err = launch_buffer_out<T, 64, 64>(g, a, s);
   } else if (g.DK == 32) {
-    if constexpr (sizeof(T) == 2) err = launch_fwd<T, 64, 32, 32>(g, a, s);
-    else err = launch_fwd<T, 32, 32, 32>(g, a, s);
+    if constexpr (sizeof(T) == 2) err = launch_fwd_seg<T, 64, 32>(g, a, pl.sg, agg, seg_states, final_raw, s);
+    else err = launch_fwd_seg<T, 32, 32>(g, a, pl.sg, agg, seg_states, final_raw, s);
+    if (err == hipSuccess) err = launch_buffer_out<T, 32, 32>(g, a, s);
   }
   return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
 }
 
 template <typename T>
 int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, void* ws, hipStream_t s) {
-  const Geom& g = pl.g;
-  const BwdLayout L = bwd_layout(g);
+  const Geom& gb = pl.gb;
+  const BwdLayout L = bwd_layout(pl);
+  const SavedLayout SL = saved_layout(pl);
   unsigned char* w = static_cast<unsigned char*>(ws);
-  BwdPtrs<T> a;
+  const unsigned char* sv = reinterpret_cast<const unsigned char*>(saved);
+  BwdPtrs<T> a{};
   a.k = (const T*)x->k; a.q = (const T*)x->q; a.v = (const T*)x->v;
   a.lr = (const T*)x->lr; a.decay = (const T*)x->decay; a.beta = (const T*)x->beta; a.gate = (const T*)x->gate;
   a.S_ref = x->S_ref; a.S0 = x->S0; a.Z0 = x->Z0; a.buf_in = x->buffer_in;
@@ -194,19 +272,22 @@ int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, voi
   a.dk = (T*)x->dk; a.dq = (T*)x->dq; a.dv = (T*)x->dv; a.dlr = (T*)x->dlr; a.ddecay = (T*)x->ddecay;
   a.dbeta = (T*)x->dbeta; a.dgate = (T*)x->dgate;
   a.dS_ref = x->dS_ref; a.dS0 = x->dS0; a.dZ0 = x->dZ0; a.dbuf_in = x->dbuffer_in;
-  a.saved = saved;
-  a.adj = reinterpret_cast<float*>(w + L.adj);
-  a.dsref_part = reinterpret_cast<float*>(w + L.dsref);
-  a.tail_part = g.H > 0 ? reinterpret_cast<float*>(w + L.tail) : nullptr;
-  a.halo_part = g.H > 0 ? reinterpret_cast<float*>(w + L.halo) : nullptr;
-  a.dw = g.gate_mode == ATLAS_GATE_TOKEN ? reinterpret_cast<float*>(w + L.dw) : nullptr;
+  BwdSegPtrs p;
+  p.seg_states = reinterpret_cast<const float*>(sv + SL.seg);
+  p.final_raw = reinterpret_cast<const float*>(sv + SL.final_raw);
+  p.adj_agg = reinterpret_cast<float*>(w + L.agg);
+  p.rw = reinterpret_cast<float*>(w + L.rw);
+  p.dsref_part = reinterpret_cast<float*>(w + L.dsref);
+  p.tail_part = gb.H > 0 ? reinterpret_cast<float*>(w + L.tail) : nullptr;
+  p.halo_part = gb.H > 0 ? reinterpret_cast<float*>(w + L.halo) : nullptr;
+  p.dw = gb.gate_mode == ATLAS_GATE_TOKEN ? reinterpret_cast<float*>(w + L.dw) : nullptr;
   hipError_t err = hipErrorInvalidValue;
-  if (g.DK == 64) {
-    if constexpr (sizeof(T) == 2) err = launch_bwd<T, 64, 64, 64>(g, a, s);
-    else err = launch_bwd<T, 32, 64, 64>(g, a, s);
-  } else if (g.DK == 32) {
-    if constexpr (sizeof(T) == 2) err = launch_bwd<T, 64, 32, 32>(g, a, s);
-    else err = launch_bwd<T, 32, 32, 32>(g, a, s);
+  if (gb.DK == 64) {
+    if constexpr (sizeof(T) == 2) err = launch_bwd_seg<T, 32, 64>(gb, a, pl.sgb, p, s);
+    else err = launch_bwd_seg<T, 16, 64>(gb, a, pl.sgb, p, s);
+  } else if (gb.DK == 32) {
+    if constexpr (sizeof(T) == 2) err = launch_bwd_seg<T, 32, 32>(gb, a, pl.sgb, p, s);
+    else err = launch_bwd_seg<T, 16, 32>(gb, a, pl.sgb, p, s);
   }
   return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
 }
@@ -238,19 +319,19 @@ int atlas_mem_validate(const atlas_mem_problem* prob) { return make_plan(prob).s
 size_t atlas_mem_saved_bytes(const atlas_mem_problem* prob) {
   const Plan pl = make_plan(prob);
   if (!pl.ok) return 0;
-  return (size_t)pl.g.BH * pl.g.nc * 2 * pl.g.DV * pl.g.DK * sizeof(float);
+  return saved_layout(pl).total;
 }
 
 size_t atlas_mem_bwd_workspace_bytes(const atlas_mem_problem* prob) {
   const Plan pl = make_plan(prob);
   if (!pl.ok) return 0;
-  return bwd_layout(pl.g).total;
+  return bwd_layout(pl).total;
 }
 
 int atlas_mem_fwd(const atlas_mem_problem* prob, const atlas_mem_fwd_args* args, float* saved, void* stream) {
   const Plan pl = make_plan(prob);
   if (!pl.ok) return pl.status;
-  if (!args) return ATLAS_MEM_ERR_NULL;
+  if (!args || !saved) return ATLAS_MEM_ERR_NULL;
   const atlas_mem_problem& p = *prob;
   if (!args->k || !args->q || !args->v || !args->lr || !args->decay || !args->S_ref || !args->S0 ||
       !args->y || !args->S_T)
@@ -275,7 +356,7 @@ int atlas_mem_bwd(const atlas_mem_problem* prob, const atlas_mem_bwd_args* args,
   if (!pl.ok) return pl.status;
   if (!args || !saved || !workspace) return ATLAS_MEM_ERR_NULL;
   const atlas_mem_problem& p = *prob;
-  if (workspace_bytes < bwd_layout(pl.g).total) return ATLAS_MEM_ERR_WORKSPACE;
+  if (workspace_bytes < bwd_layout(pl).total) return ATLAS_MEM_ERR_WORKSPACE;
   if (!args->k || !args->q || !args->v || !args->lr || !args->decay || !args->S_ref || !args->S0 ||
       !args->dk || !args->dq || !args->dv || !args->dlr || !args->ddecay || !args->dS_ref || !args->dS0)
     return ATLAS_MEM_ERR_NULL;

@@ -132,4 +132,11 @@ __device__ __forceinline__ float poly_map_grad(float x, int g) {
   return out;
 }
 
+// Load one element and apply the feature map (identity or elementwise polynomial).
+template <typename T>
+__device__ __forceinline__ float ld_map(const T* p, size_t idx, int map_mode, int deg) {
+  const float x = to_f32(p[idx]);
+  return map_mode == 1 ? poly_map(x, deg) : x;
+}
+
 }  // namespace atlas

@@ -1,0 +1,447 @@
+// seg_fwd.h - the segment walk of the forward recurrence, shared by the forward kernels and the
+// backward pass's forward re-walk.
+#pragma once
+
+#include "mem_common.h"
+#include "mem_params.h"
+#include "seg_common.h"
+
+namespace atlas {
+
+template <typename T, int CH, int D, bool FULL>
+struct SegFwdSmem {
+  static constexpr int SPM = CH + kHaloPad;
+  T phi[SPM][D + 8];
+  T phiTs[D][SPM + 8];       // Ws_end[s] * phi[s][k], stored [k][s]
+  T phiTz[D][SPM + 8];       // Wz_end[s] * phi[s][k], stored [k][s]
+  T delta[D][SPM + 8];       // delta[i][s]
+  T sref[D][D + 8];
+  ChunkScalars<CH> sc;
+  // full walk only
+  T psi[FULL ? CH : 1][D + 8];
+  T Q[FULL ? CH : 1][SPM + 8];
+  T Sb[FULL ? D : 1][D + 8];
+  T Zb[FULL ? D : 1][D + 8];
+  float wsh[FULL ? CH : 1][SPM + 1];   // Ws[s, tau-1]
+};
+
+// Per-thread register prefetch of one chunk's inputs (issued one chunk ahead).
+template <typename T, int CH, int D, bool FULL>
+struct ChunkPrefetch {
+  static constexpr int SPM = CH + kHaloPad;
+  static constexpr int NV_PHI = (SPM * D / 8 + kSegThreads - 1) / kSegThreads;
+  static constexpr int NV_PSI = FULL ? (CH * D / 8 + kSegThreads - 1) / kSegThreads : 0;
+  Vec8<T> phi[NV_PHI];
+  Vec8<T> psi[NV_PSI > 0 ? NV_PSI : 1];
+  static constexpr int NWL = (CH * kMaxWindow + kSegThreads - 1) / kSegThreads;
+  float alpha, eta, beta, ug;
+  float wl[NWL];
+
+  __device__ __forceinline__ void load(const Geom& g, const FwdPtrs<T>& a, size_t tb, int t0, int L) {
+    const int tid = threadIdx.x, H = g.H;
+#pragma unroll
+    for (int j = 0; j < NV_PHI; ++j) {
+      const int v = tid + j * kSegThreads;
+      const int s = v / (D / 8), c8 = v % (D / 8);
+      const int p = t0 - H + s;
+      const bool ok = s < g.SP && s < H + L && p >= 0;
+      phi[j] = ok ? vec8_load(a.k + (tb + p) * D + c8 * 8) : Vec8<T>::zero();
+    }
+    if constexpr (FULL) {
+#pragma unroll
+      for (int j = 0; j < NV_PSI; ++j) {
+        const int v = tid + j * kSegThreads;
+        const int t = v / (D / 8), c8 = v % (D / 8);
+        psi[j] = (t < L) ? vec8_load(a.q + (tb + t0 + t) * D + c8 * 8) : Vec8<T>::zero();
+      }
+    }
+    if (tid < CH) {
+      const bool in = tid < L;
+      alpha = in ? to_f32(a.decay[tb + t0 + tid]) : 1.f;
+      eta = in ? to_f32(a.lr[tb + t0 + tid]) : 0.f;
+      beta = in ? (g.momentum ? to_f32(a.beta[tb + t0 + tid]) : 0.f) : 1.f;
+    }
+    if (g.gate_mode == GATE_TOKEN && tid < g.SP) {
+      const int p = t0 - H + tid;
+      ug = (tid < H + L) ? (p >= 0 ? to_f32(a.gate[tb + p]) : 1.f) : 0.f;
+    } else if (g.gate_mode == GATE_LAG) {
+#pragma unroll
+      for (int j = 0; j < NWL; ++j) {
+        const int idx = tid + j * kSegThreads;
+        const int t = idx / g.e;
+        wl[j] = (idx < CH * g.e && t < L) ? to_f32(a.gate[(tb + t0) * g.e + idx]) : 0.f;
+      }
+    }
+  }
+
+  template <typename Sm>
+  __device__ __forceinline__ void store(const Geom& g, Sm& sm) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < NV_PHI; ++j) {
+      const int v = tid + j * kSegThreads;
+      const int s = v / (D / 8), c8 = v % (D / 8);
+      if (s < SPM) {
+        Vec8<T> x = phi[j];
+        if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
+        x.store(&sm.phi[s][c8 * 8]);
+      }
+    }
+    if constexpr (FULL) {
+#pragma unroll
+      for (int j = 0; j < NV_PSI; ++j) {
+        const int v = tid + j * kSegThreads;
+        const int t = v / (D / 8), c8 = v % (D / 8);
+        if (t < CH) {
+          Vec8<T> x = psi[j];
+          if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
+          x.store(&sm.psi[t][c8 * 8]);
+        }
+      }
+    }
+    if (tid < CH) { sm.sc.alpha[tid] = alpha; sm.sc.eta[tid] = eta; sm.sc.beta[tid] = beta; }
+    if (g.gate_mode == GATE_TOKEN && tid < g.SP) sm.sc.ug[tid] = ug;
+    if (g.gate_mode == GATE_LAG) {
+#pragma unroll
+      for (int j = 0; j < NWL; ++j) {
+        const int idx = tid + j * kSegThreads;
+        if (idx < CH * g.e) sm.sc.wl[idx] = wl[j];
+      }
+    }
+  }
+};
+
+enum WalkMode { WALK_AGG = 0, WALK_FULL = 1, WALK_REWALK = 2 };
+
+// Segment walk.
+//   WALK_AGG:    zero initial state; writes the segment aggregate (a, kappa, b, U, V) to agg.
+//   WALK_FULL:   folds the preceding aggregates into the start state (saved to seg_states), walks
+//                the chunks with the true state and writes y (and S_T, Z_T, the raw S_{T-1}).
+//   WALK_REWALK: starts from seg_states[seg] (saved by WALK_FULL, chunk length may differ) and
+//                writes the raw state at the start of every chunk of the segment to rw (the
+//                backward pass walks them in reverse); no y.
+template <typename T, int CH, int D, int MODE>
+__device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg, float* agg,
+                                            float* seg_states, float* rw, float* final_raw,
+                                            unsigned char* smem_raw) {
+  constexpr bool AGG = MODE == WALK_AGG;
+  constexpr bool FULL = MODE == WALK_FULL;
+  constexpr bool REWALK = MODE == WALK_REWALK;
+  typedef SegFwdSmem<T, CH, D, FULL> Sm;
+  Sm& sm = *reinterpret_cast<Sm*>(smem_raw);
+  constexpr int SPM = Sm::SPM;
+  constexpr int NTD = D / 16;                    // 16-wide tiles along D
+  typedef MM<T> M;
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const int seg = blockIdx.x, bh = blockIdx.y;
+  const int H = g.H, SP = g.SP;
+  const size_t tb = (size_t)bh * g.T;
+  const size_t sb = (size_t)bh * D * D;
+  const int c_begin = seg * sg.G, c_end = min(g.nc, c_begin + sg.G);
+
+  // ---- S_ref (bf16/fp32 operand copy)
+  for (int idx = tid; idx < D * D; idx += kSegThreads) sm.sref[idx / D][idx % D] = from_f32<T>(a.S_ref[sb + idx]);
+
+  // ---- state registers on waves 4..7: wave w owns row tile (w - 4) (and w, for D = 32, none beyond NTD)
+  constexpr int NSW = 4;   // state waves
+  const bool state_wave = wave >= 4;
+  const int mt = wave - 4;                        // row tile owned
+  const bool owns = state_wave && mt < NTD;
+  float Sr[NTD][4], Zr[NTD][4];
+#pragma unroll
+  for (int n = 0; n < NTD; ++n)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { Sr[n][r] = 0.f; Zr[n][r] = 0.f; }
+  float seg_a = 1.f, seg_k = 0.f, seg_b = 1.f;   // aggregate transition (AGG)
+  float Sraw[NTD][4];                             // raw (pre-clamp) end state of the last chunk
+#pragma unroll
+  for (int n = 0; n < NTD; ++n)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Sraw[n][r] = 0.f;
+
+  if constexpr (REWALK) {
+    if (owns) {
+      const float* ss = seg_states + ((size_t)bh * sg.nseg + seg) * 2 * D * D;
+#pragma unroll
+      for (int n = 0; n < NTD; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
+          Sr[n][r] = ss[(size_t)i * D + k];
+          Zr[n][r] = ss[(size_t)D * D + (size_t)i * D + k];
+        }
+    }
+  }
+  if constexpr (FULL) {
+    if (owns) {
+      // start from (S0, Z0) and fold the aggregates of segments 0 .. seg-1
+#pragma unroll
+      for (int n = 0; n < NTD; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
+          Sr[n][r] = a.S0[sb + (size_t)i * D + k];
+          Zr[n][r] = (g.momentum && a.Z0) ? a.Z0[sb + (size_t)i * D + k] : 0.f;
+        }
+      for (int js = 0; js < seg; ++js) {
+        const float* ag = agg + ((size_t)bh * sg.nseg + js) * sg.agg_stride;
+        const float ta = ag[2 * D * D], tk = ag[2 * D * D + 1], tbb = ag[2 * D * D + 2];
+#pragma unroll
+        for (int n = 0; n < NTD; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
+            const float U = ag[(size_t)i * D + k], V = ag[(size_t)D * D + (size_t)i * D + k];
+            const float s = Sr[n][r];
+            Sr[n][r] = ta * s - tk * Zr[n][r] + U;
+            Zr[n][r] = g.momentum ? tbb * Zr[n][r] + V : 0.f;
+          }
+      }
+      // save the segment-start state for the backward pass
+      if (seg_states) {
+        float* ss = seg_states + ((size_t)bh * sg.nseg + seg) * 2 * D * D;
+#pragma unroll
+        for (int n = 0; n < NTD; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
+            ss[(size_t)i * D + k] = Sr[n][r];
+            ss[(size_t)D * D + (size_t)i * D + k] = Zr[n][r];
+          }
+      }
+#pragma unroll
+      for (int n = 0; n < NTD; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
+          sm.Sb[i][k] = from_f32<T>(Sr[n][r]);
+          sm.Zb[i][k] = from_f32<T>(Zr[n][r]);
+        }
+    }
+  }
+
+  ChunkPrefetch<T, CH, D, FULL> pf;
+  if (c_begin < c_end) {
+    const int t0 = c_begin * g.Lc;
+    pf.load(g, a, tb, t0, min(g.T, t0 + g.Lc) - t0);
+  }
+
+  for (int c = c_begin; c < c_end; ++c) {
+    const int t0 = c * g.Lc;
+    const int t1 = min(g.T, t0 + g.Lc);
+    const int L = t1 - t0;
+    const bool bufchunk = (c == 0) && g.has_buf;
+    if constexpr (REWALK) {
+      if (owns) {
+        float* dst = rw + (size_t)(c - c_begin) * 2 * D * D;
+#pragma unroll
+        for (int n = 0; n < NTD; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
+            dst[(size_t)i * D + k] = c == c_begin ? Sr[n][r] : Sraw[n][r];
+            dst[(size_t)D * D + (size_t)i * D + k] = Zr[n][r];
+          }
+      }
+    }
+    __syncthreads();                      // previous chunk finished with the LDS inputs
+    pf.store(g, sm);
+    __syncthreads();
+    if (c + 1 < c_end) {                  // prefetch the next chunk while this one computes
+      const int n0 = (c + 1) * g.Lc;
+      pf.load(g, a, tb, n0, min(g.T, n0 + g.Lc) - n0);
+    }
+
+    // ---- P1: G1 + G2 (waves 0-5) | coefficient recurrences (waves 6-7)
+    // G2 tile tt = wave + 6 j (j < 4) stays in registers kacc[j] until the Q epilogue.
+    const int nts = SP / 16;
+    const int n_g2 = FULL ? (CH / 16) * nts : 0;
+    f32x4 kacc[4];
+    if (wave < 6) {
+      for (int tile = wave; tile < nts * NTD; tile += 6) {
+        const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;   // m: sources, n: rows i
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int k0 = 0; k0 < D; k0 += M::KS)
+          acc = M::mma(frag_ld_row<T>(&sm.phi[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.sref[0][0], D + 8, n0, k0), acc);
+        const int i = n0 + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int s = m0 + 4 * (lane >> 4) + r;
+          const int p = t0 - H + s;
+          float d = 0.f;
+          if (s < H + L && p >= 0) d = acc[r] - to_f32(a.v[(tb + p) * D + i]);
+          sm.delta[i][s] = from_f32<T>(d);
+        }
+      }
+      if constexpr (FULL) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int tt = wave + 6 * j;
+          kacc[j] = zero4();
+          if (tt < n_g2) {
+            const int m0 = (tt / nts) * 16, n0 = (tt % nts) * 16;
+            f32x4 acc = zero4();
+#pragma unroll
+            for (int k0 = 0; k0 < D; k0 += M::KS)
+              acc = M::mma(frag_ld_row<T>(&sm.psi[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.phi[0][0], D + 8, n0, k0), acc);
+            kacc[j] = acc;
+          }
+        }
+      }
+    } else {
+      chunk_coefficients<CH, FULL>(g, sm.sc, L, tid - 6 * kWave, FULL ? &sm.wsh[0][0] : nullptr, SPM + 1);
+    }
+    __syncthreads();
+
+    // ---- P2: Q epilogue (waves 0-5), scaled phi^T for G4 (all)
+    if constexpr (FULL) {
+      if (wave < 6) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int tt = wave + 6 * j;
+          if (tt < n_g2) {
+            const int m0 = (tt / nts) * 16, n0 = (tt % nts) * 16;
+            const int s = n0 + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int t = m0 + 4 * (lane >> 4) + r;
+              sm.Q[t][s] = from_f32<T>(kacc[j][r] * sm.wsh[t][s]);
+            }
+          }
+        }
+      }
+    }
+    for (int idx = tid; idx < SP * D; idx += kSegThreads) {
+      const int s = idx / D, k = idx % D;
+      const float x = to_f32(sm.phi[s][k]);
+      sm.phiTs[k][s] = from_f32<T>(sm.sc.wsend[s] * x);
+      sm.phiTz[k][s] = from_f32<T>(sm.sc.wzend[s] * x);
+    }
+    __syncthreads();
+
+    // ---- P3: G3 (waves 0-3, full walk) | G4 + state update (waves 4-7)
+    if (FULL && wave < 4) {
+      for (int tile = wave; tile < (CH / 16) * NTD; tile += 4) {
+        const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;   // m: tau, n: rows i
+        f32x4 aq = zero4(), as = zero4(), az = zero4();
+        for (int k0 = 0; k0 < SP; k0 += M::KS)
+          aq = M::mma(frag_ld_row<T>(&sm.Q[0][0], SPM + 8, m0, k0), frag_ld_row<T>(&sm.delta[0][0], SPM + 8, n0, k0), aq);
+#pragma unroll
+        for (int k0 = 0; k0 < D; k0 += M::KS) {
+          const typename M::frag fa = frag_ld_row<T>(&sm.psi[0][0], D + 8, m0, k0);
+          as = M::mma(fa, frag_ld_row<T>(&sm.Sb[0][0], D + 8, n0, k0), as);
+          az = M::mma(fa, frag_ld_row<T>(&sm.Zb[0][0], D + 8, n0, k0), az);
+        }
+        f32x4 yv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = m0 + 4 * (lane >> 4) + r;
+          yv[r] = -aq[r] + sm.sc.acoef[t] * as[r] - sm.sc.kcoef[t] * az[r];
+        }
+        if (bufchunk) {
+          for (int s = 0; s < H; ++s) {
+            const float* Bs = a.buf_in + ((size_t)bh * H + s) * D * D;
+            f32x4 ab = zero4();
+#pragma unroll
+            for (int k0 = 0; k0 < D; k0 += M::KS)
+              ab = M::mma(frag_ld_row<T>(&sm.psi[0][0], D + 8, m0, k0), frag_ld<T>(Bs, D, 1, n0, k0), ab);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int t = m0 + 4 * (lane >> 4) + r;
+              yv[r] -= sm.wsh[t][s] * ab[r];
+            }
+          }
+        }
+        const int i = n0 + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = m0 + 4 * (lane >> 4) + r;
+          if (t < L) a.y[(tb + t0 + t) * D + i] = from_f32<T>(yv[r]);
+        }
+      }
+    } else if (owns) {
+      const float a_end = sm.sc.endc[0], k_end = sm.sc.endc[1], b_end = sm.sc.endc[2];
+      const bool do_clamp = !AGG && clamp_after(g, t1);
+#pragma unroll
+      for (int n = 0; n < NTD; ++n) {
+        const int m0 = mt * 16, n0 = n * 16;
+        f32x4 au = zero4(), av = zero4();
+        for (int k0 = 0; k0 < SP; k0 += M::KS) {
+          const typename M::frag fa = frag_ld_row<T>(&sm.delta[0][0], SPM + 8, m0, k0);
+          au = M::mma(fa, frag_ld_row<T>(&sm.phiTs[0][0], SPM + 8, n0, k0), au);
+          av = M::mma(fa, frag_ld_row<T>(&sm.phiTz[0][0], SPM + 8, n0, k0), av);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = m0 + 4 * (lane >> 4) + r, k = n0 + (lane & 15);
+          float U = -au[r], V = av[r];
+          if (bufchunk) {
+            for (int s = 0; s < H; ++s) {
+              const float b = a.buf_in[(((size_t)bh * H + s) * D + i) * D + k];
+              U -= sm.sc.wsend[s] * b;
+              V += sm.sc.wzend[s] * b;
+            }
+          }
+          const float Sn = a_end * Sr[n][r] - k_end * Zr[n][r] + U;
+          const float Zn = g.momentum ? (b_end * Zr[n][r] + V) : 0.f;
+          Sraw[n][r] = Sn;
+          Sr[n][r] = do_clamp ? clamp100(Sn) : Sn;
+          Zr[n][r] = Zn;
+        }
+      }
+      if constexpr (AGG) {
+        const float na = a_end * seg_a;
+        const float nk = a_end * seg_k + k_end * seg_b;
+        seg_b = b_end * seg_b;
+        seg_a = na;
+        seg_k = nk;
+      }
+    }
+    if constexpr (FULL) {
+      __syncthreads();                    // G3 done reading Sb / Zb
+      if (owns) {
+#pragma unroll
+        for (int n = 0; n < NTD; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
+            sm.Sb[i][k] = from_f32<T>(Sr[n][r]);
+            sm.Zb[i][k] = from_f32<T>(Zr[n][r]);
+          }
+      }
+    }
+  }
+
+  // ---- segment results
+  if (owns) {
+    if constexpr (AGG) {
+      float* ag = agg + ((size_t)bh * sg.nseg + seg) * sg.agg_stride;
+#pragma unroll
+      for (int n = 0; n < NTD; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
+          ag[(size_t)i * D + k] = Sr[n][r];
+          ag[(size_t)D * D + (size_t)i * D + k] = Zr[n][r];
+        }
+      if (mt == 0 && lane == 0) {
+        ag[2 * D * D] = seg_a; ag[2 * D * D + 1] = seg_k; ag[2 * D * D + 2] = seg_b;
+      }
+    } else if (FULL && seg == sg.nseg - 1) {
+      // Sr holds the raw S_{T-1} (the last chunk of the sequence is never a clamp point)
+#pragma unroll
+      for (int n = 0; n < NTD; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
+          const size_t off = sb + (size_t)i * D + k;
+          a.S_T[off] = g.clamp_final ? clamp100(Sr[n][r]) : Sr[n][r];
+          if (g.momentum) a.Z_T[off] = Zr[n][r];
+          if (final_raw) final_raw[off] = Sr[n][r];
+        }
+    }
+  }
+}
+
+}  // namespace atlas

@@ -1,0 +1,79 @@
+// seg_fwd.hip - segment-parallel forward pass of the chunked memory recurrence (gfx950).
+//
+// The sequence of every head-batch row bh is cut into segments of G chunks (chunk length Lc).
+// Chunk-boundary states follow an affine recurrence with a scalar 2x2 transition,
+//   [S; Z]_out = [[a, -kappa], [0, b]] [S; Z]_in + [U; V],
+// so the work splits into two launches, both parallel over (segment, bh):
+//   k_fwd_seg_agg : walk the segment's chunks from a zero state -> segment aggregate
+//                   (a, kappa, b, U_seg, V_seg).
+//   k_fwd_seg     : fold the aggregates of the preceding segments into the segment-start state,
+//                   save it for the backward pass, then walk the chunks again with the true state,
+//                   producing y (and S_T, Z_T in the last segment).
+// With clamp_every > 0 the clamp at scan_chunk_len boundaries is not affine, so the caller uses a
+// single segment (an exact sequential walk over all chunks).
+//
+// Inside a chunk (tokens t0..t1-1, sources s = the chunk plus its e-1 token halo) everything is in
+// closed form (see the per-source coefficient recurrence in chunk_coefficients):
+//   G1  delta^T[s,i] = phi_s . S_ref[i,:] - v_s[i]
+//   G2  Q[tau,s]     = Ws[s,tau-1] * (psi_tau . phi_s)
+//   G3  y^T[tau,i]   = -Q delta^T + a_{tau-1} psi S_in^T - kappa_{tau-1} psi Z_in^T
+//   G4  U = -delta (Ws_end phi), V = delta (Wz_end phi)
+//   S_out = a_end S_in - kappa_end Z_in + U,   Z_out = b_end Z_in + V
+// Wave roles (8 waves): 0-5 run G1/G2 while 6-7 run the scalar coefficient recurrences; then
+// 0-3 run G3 (y) while 4-7 run G4 and keep the 64 x 64 states S, Z in registers.
+#include "mem_common.h"
+#include "mem_params.h"
+#include "seg_common.h"
+#include "seg_fwd.h"
+
+namespace atlas {
+
+template <typename T, int CH, int D>
+__global__ __launch_bounds__(kSegThreads) void k_fwd_seg_agg(const Geom g, const FwdPtrs<T> a, const SegGeom sg,
+                                                               float* agg) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  fwd_segment<T, CH, D, WALK_AGG>(g, a, sg, agg, nullptr, nullptr, nullptr, smem_raw);
+}
+
+template <typename T, int CH, int D>
+__global__ __launch_bounds__(kSegThreads) void k_fwd_seg(const Geom g, const FwdPtrs<T> a, const SegGeom sg,
+                                                           float* agg, float* seg_states, float* final_raw) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  fwd_segment<T, CH, D, WALK_FULL>(g, a, sg, agg, seg_states, nullptr, final_raw, smem_raw);
+}
+
+template <typename T, int CH, int D>
+hipError_t launch_fwd_seg(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg, float* agg, float* seg_states,
+                          float* final_raw, hipStream_t stream) {
+  hipError_t err;
+  if (sg.nseg > 1) {
+    const size_t smem = sizeof(SegFwdSmem<T, CH, D, false>);
+    err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_seg_agg<T, CH, D>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (err != hipSuccess) return err;
+    prof_begin(KID_FWD_SEG_AGG, stream);
+    hipLaunchKernelGGL((k_fwd_seg_agg<T, CH, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, agg);
+    prof_end(KID_FWD_SEG_AGG, stream);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
+  const size_t smem = sizeof(SegFwdSmem<T, CH, D, true>);
+  err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_seg<T, CH, D>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (err != hipSuccess) return err;
+  prof_begin(KID_FWD_WALK, stream);
+  hipLaunchKernelGGL((k_fwd_seg<T, CH, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, agg,
+                     seg_states, final_raw);
+  prof_end(KID_FWD_WALK, stream);
+  return hipGetLastError();
+}
+
+#define ATLAS_INST_FWD_SEG(T, CH, D) \
+  template hipError_t launch_fwd_seg<T, CH, D>(const Geom&, const FwdPtrs<T>&, const SegGeom&, float*, float*, float*, \
+                                               hipStream_t);
+
+ATLAS_INST_FWD_SEG(bf16, 64, 64)
+ATLAS_INST_FWD_SEG(float, 32, 64)
+ATLAS_INST_FWD_SEG(bf16, 64, 32)
+ATLAS_INST_FWD_SEG(float, 32, 32)
+
+}  // namespace atlas

@@ -95,11 +95,10 @@ class MemoryRecurrenceFn(torch.autograd.Function):
         Z_T = torch.empty(bh, dv, dk, device=dev, dtype=torch.float32) if momentum else None
         e = cfg.window
         buf_out = torch.empty(bh, e - 1, dv, dk, device=dev, dtype=torch.float32) if e > 1 else None
-        need_bwd = any(ctx.needs_input_grad[:11])
-        saved = None
-        if need_bwd:
-            nbytes = lib.atlas_mem_saved_bytes(ctypes.byref(prob))
-            saved = torch.empty(nbytes // 4, device=dev, dtype=torch.float32)
+        # segment-start states and aggregates: the forward writes them (it needs them for its own
+        # second pass) and the backward re-reads them
+        nbytes = lib.atlas_mem_saved_bytes(ctypes.byref(prob))
+        saved = torch.empty(nbytes // 4, device=dev, dtype=torch.float32)
         a = _lib.FwdArgs(k=_ptr(k), q=_ptr(q), v=_ptr(v), lr=_ptr(lr), decay=_ptr(decay), beta=_ptr(beta),
                          gate=_ptr(gate), S_ref=_ptr(S_ref), S0=_ptr(S0), Z0=_ptr(Z0), buffer_in=_ptr(buf),
                          y=_ptr(y), S_T=_ptr(S_T), Z_T=_ptr(Z_T), buffer_out=_ptr(buf_out))

@@ -40,15 +40,17 @@ def algorithmic_bytes(bh=BH, t=T, d=D, e=E, s_in=2, s_st=4):
     fwd = n * 3 * d * s_in + n * n_sc * s_in + n * d * s_in + 5 * st + buf
     bwd = n * 4 * d * s_in + 2 * n * n_sc * s_in + n * 3 * d * s_in + 8 * st + buf
     per_kernel = {
+        # segment aggregates (zero state): read k, v, scalars, S_ref
+        "k_fwd_seg_agg": n * 2 * d * s_in + n * n_sc * s_in + st,
         # forward walk: read k, q, v, scalars, S_ref/S0/Z0; write y, S_T, Z_T
-        "k_fwd_walk": n * 3 * d * s_in + n * n_sc * s_in + n * d * s_in + 5 * st,
-        "k_buffer_out": n and bh * (e - 1) * (2 * d * s_in + d * d * s_st),
-        # adjoint walk: read q, dy, alpha/eta/beta, dS_T, dZ_T; write dS0, dZ0
-        "k_bwd_adjoint_walk": n * 2 * d * s_in + n * 3 * s_in + 4 * st,
-        # per-chunk gradients: read k, q, v, dy, scalars, S_ref; write dk, dq, dv, scalar grads
-        "k_bwd_chunk": n * 4 * d * s_in + 2 * n * n_sc * s_in + n * 3 * d * s_in + st,
-        "k_bwd_fixup": 0,
-        "k_reduce_dsref": st,
+        "k_fwd_seg": n * 3 * d * s_in + n * n_sc * s_in + n * d * s_in + 5 * st,
+        "k_buffer_out": bh * (e - 1) * (2 * d * s_in + d * d * s_st),
+        # adjoint aggregates: read q, dy, alpha/eta/beta
+        "k_bwd_seg_agg": n * 2 * d * s_in + n * 3 * s_in,
+        # backward walk: read k, q, v, dy, scalars, S_ref, dS_T, dZ_T; write dk, dq, dv, scalar grads, dS0, dZ0
+        "k_bwd_seg": n * 4 * d * s_in + 2 * n * n_sc * s_in + n * 3 * d * s_in + 5 * st,
+        "k_bwd_seg_fixup": 0,
+        "k_seg_reduce_dsref": st,
     }
     return fwd, bwd, per_kernel
 

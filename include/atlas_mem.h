@@ -124,16 +124,16 @@ const char* atlas_mem_strerror(int status);
 /* Checks a problem description without touching the GPU. */
 int atlas_mem_validate(const atlas_mem_problem* prob);
 
-/* Bytes of the `saved` buffer written by atlas_mem_fwd and read by atlas_mem_bwd
- * (fp32 chunk-end states). Returns 0 for an invalid problem. */
+/* Bytes of the `saved` buffer atlas_mem_fwd writes (its scratch plus the fp32 states
+ * atlas_mem_bwd reuses). Returns 0 for an invalid problem. */
 size_t atlas_mem_saved_bytes(const atlas_mem_problem* prob);
 
 /* Bytes of scratch workspace atlas_mem_bwd needs. Returns 0 for an invalid problem. */
 size_t atlas_mem_bwd_workspace_bytes(const atlas_mem_problem* prob);
 
 /* Forward pass. Replaces forward_exact (atlas_pytorch/cuda/atlas_omega.cpp:56-99) and the
- * PyTorch scan path (atlas_pytorch/rnn_memory.py:605-730). `saved` may be NULL when no
- * backward will follow. */
+ * PyTorch scan path (atlas_pytorch/rnn_memory.py:605-730). `saved` (atlas_mem_saved_bytes)
+ * is required; keep it unchanged until the matching atlas_mem_bwd when a backward follows. */
 int atlas_mem_fwd(const atlas_mem_problem* prob, const atlas_mem_fwd_args* args,
                   float* saved, void* stream);
 
@@ -167,7 +167,7 @@ int atlas_window_sum(int dtype, int64_t n, int64_t t, int64_t d, int window, int
 /* ---- diagnostics (no reference counterpart) ------------------------------------------------ */
 
 /* Number of kernels the timing hooks distinguish (index -> atlas_mem_kernel_name). */
-#define ATLAS_MEM_NKERNELS 6
+#define ATLAS_MEM_NKERNELS 7
 
 /* Opt-in timing: while enabled, each kernel launch of atlas_mem_fwd/atlas_mem_bwd is bracketed
  * by HIP events on its stream (adds two event records per launch). */

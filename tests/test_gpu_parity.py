@@ -35,6 +35,13 @@ CASES = [
     Case("bf16_token_buffer_d32", BH=3, T=130, d=32, e=3, gate='token', momentum=True, buffer=True, states=0.2,
          dtype=BF16, seed=10),
     Case("bf16_map2_nomom", BH=2, T=70, d=64, e=2, gate='token', momentum=False, map_degree=2, dtype=BF16, seed=11),
+    # segment structure: a last segment shorter than the window halo, many segments with a short last
+    # chunk, the window crossing segment boundaries with the carried buffer
+    Case("bf16_short_last_segment", BH=2, T=67, d=64, e=6, gate='token', momentum=True, buffer=True, states=0.1,
+         dtype=BF16, seed=12),
+    Case("bf16_multiseg_short_chunk", BH=40, T=1100, d=32, e=16, gate='lag', momentum=True, buffer=True,
+         states=0.1, dtype=BF16, seed=13),
+    Case("fp32_multiseg", BH=40, T=300, d=32, e=5, gate='token', momentum=True, buffer=True, states=0.2, seed=14),
 ]
 
 
