@@ -45,7 +45,7 @@ EXPORTED_SYMBOLS = (
     "atlas_mem_mfma_selftest",
 )
 
-NKERNELS = 7
+NKERNELS = 9
 
 
 class Problem(ctypes.Structure):

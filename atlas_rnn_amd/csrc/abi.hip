@@ -70,7 +70,8 @@ struct Profiler {
 };
 Profiler& prof() { static Profiler p; return p; }
 const char* kKernelNames[KID_COUNT] = {"k_fwd_seg_agg", "k_fwd_seg", "k_buffer_out", "k_bwd_seg_agg",
-                                       "k_bwd_seg", "k_bwd_seg_fixup", "k_seg_reduce_dsref"};
+                                       "k_bwd_seg", "k_bwd_seg_fixup", "k_seg_reduce_dsref", "k_fwd_seg_scan",
+                                       "k_bwd_seg_scan"};
 }  // namespace
 
 namespace atlas {
@@ -166,7 +167,6 @@ Plan make_plan(const atlas_mem_problem* p) {
   Geom& g = pl.g;
   g.BH = p->bh; g.T = p->seq_len; g.DK = p->d_k; g.DV = p->d_v;
   g.e = p->window; g.H = H; g.Lc = Lc; g.nc = (p->seq_len + Lc - 1) / Lc;
-  g.SP = ((H + CH + 31) / 32) * 32;
   g.momentum = p->momentum; g.gate_mode = p->gate_mode; g.map_mode = p->map_mode;
   g.map_deg = p->map_mode == ATLAS_MAP_ELEMENTWISE ? p->map_degree : 1;
   g.has_buf = p->has_buffer; g.clamp_every = p->clamp_every; g.clamp_final = p->clamp_final;
@@ -176,9 +176,6 @@ Plan make_plan(const atlas_mem_problem* p) {
   gb = g;
   gb.Lc = Lb;
   gb.nc = (p->seq_len + Lb - 1) / Lb;
-  const int CHB = bwd_chunk_cap(p->dtype);
-  const int spr = p->dtype == ATLAS_DT_BF16 ? 32 : 16;
-  gb.SP = ((H + CHB + spr - 1) / spr) * spr;
   pl.sgb = pl.sg;
   pl.sgb.G = pl.sg.G * (Lc / Lb);
   pl.CH = CH;
@@ -209,7 +206,7 @@ SavedLayout saved_layout(const Plan& pl) {
 // backward workspace: adjoint aggregates, re-walk chunk states, dS_ref partials, boundary partials,
 // token-gate (target, lag) gradients.
 struct BwdLayout {
-  size_t agg, rw, dsref, tail, halo, dw, total;
+  size_t agg, segadj, rw, dsref, tail, halo, dw, total;
 };
 
 BwdLayout bwd_layout(const Plan& pl) {
@@ -219,6 +216,7 @@ BwdLayout bwd_layout(const Plan& pl) {
   const size_t st = (size_t)g.DV * g.DK * sizeof(float);
   size_t off = 0;
   L.agg = off; off += align256((size_t)g.BH * nseg * pl.sgb.agg_stride * sizeof(float));
+  L.segadj = off; off += align256((size_t)g.BH * nseg * 2 * st);
   L.rw = off; off += align256((size_t)g.BH * nseg * pl.sgb.G * 2 * st);
   L.dsref = off; off += align256((size_t)g.BH * nseg * st);
   L.tail = off; off += align256((size_t)g.BH * nseg * g.H * (g.DV + g.DK) * sizeof(float));
@@ -239,7 +237,6 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
   const SavedLayout SL = saved_layout(pl);
   unsigned char* sv = reinterpret_cast<unsigned char*>(saved);
   a.y = (T*)x->y; a.S_T = x->S_T; a.Z_T = x->Z_T; a.buf_out = x->buffer_out;
-  a.saved = nullptr;
   float* seg_states = reinterpret_cast<float*>(sv + SL.seg);
   float* agg = reinterpret_cast<float*>(sv + SL.agg);
   float* final_raw = reinterpret_cast<float*>(sv + SL.final_raw);
@@ -276,6 +273,7 @@ int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, voi
   p.seg_states = reinterpret_cast<const float*>(sv + SL.seg);
   p.final_raw = reinterpret_cast<const float*>(sv + SL.final_raw);
   p.adj_agg = reinterpret_cast<float*>(w + L.agg);
+  p.seg_adj = reinterpret_cast<float*>(w + L.segadj);
   p.rw = reinterpret_cast<float*>(w + L.rw);
   p.dsref_part = reinterpret_cast<float*>(w + L.dsref);
   p.tail_part = gb.H > 0 ? reinterpret_cast<float*>(w + L.tail) : nullptr;

@@ -20,7 +20,6 @@ struct Geom {
   int e, H;         // window and halo = e - 1
   int Lc;           // chunk length used for this call (<= CH)
   int nc;           // number of chunks = ceil(T / Lc)
-  int SP;           // source rows per chunk tile, multiple of 32: round_up(H + CH, 32)
   int momentum, gate_mode, map_mode, map_deg, has_buf, clamp_every, clamp_final;
 };
 
@@ -35,7 +34,6 @@ struct FwdPtrs {
   const T* lr; const T* decay; const T* beta; const T* gate;
   const float* S_ref; const float* S0; const float* Z0; const float* buf_in;
   T* y; float* S_T; float* Z_T; float* buf_out;
-  float* saved;   // [BH][nc][2][DV][DK] raw chunk-end (S, Z)
 };
 
 template <typename T>
@@ -46,19 +44,12 @@ struct BwdPtrs {
   const T* dy; const float* dS_T; const float* dZ_T; const float* dbuf_out;
   T* dk; T* dq; T* dv; T* dlr; T* ddecay; T* dbeta; T* dgate;
   float* dS_ref; float* dS0; float* dZ0; float* dbuf_in;
-  const float* saved;  // forward states
-  // workspace
-  float* adj;          // [BH][nc][2][DV][DK]  adjoint of chunk-end (S, Z)
-  float* dsref_part;   // [BH][nc][DV][DK]
-  float* tail_part;    // [BH][nc][H][DV + DK]  partial (dv, dphi) of a chunk's last H tokens
-  float* halo_part;    // [BH][nc][H][DV + DK]  partial (dv, dphi) for the previous chunk's last H tokens
-  float* dw;           // [BH][T][e] per (target, lag) weight gradients (token mode)
 };
 
 // Opt-in per-kernel timing (atlas_mem_profile_*): brackets each launch with HIP events.
 enum KernelId {
   KID_FWD_SEG_AGG = 0, KID_FWD_WALK, KID_BUFFER_OUT, KID_BWD_ADJOINT, KID_BWD_CHUNK, KID_BWD_FIXUP,
-  KID_REDUCE_DSREF, KID_COUNT
+  KID_REDUCE_DSREF, KID_FWD_SCAN, KID_BWD_SCAN, KID_COUNT
 };
 void prof_begin(int kid, hipStream_t s);
 void prof_end(int kid, hipStream_t s);

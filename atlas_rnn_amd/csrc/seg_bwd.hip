@@ -6,8 +6,10 @@
 //                   (the transposed 2x2 transition and the local chunk-start adjoint L, K):
 //                     dS_in = a dS_end + sum_t a_{t-1} dy_t psi_t^T
 //                     dZ_in = b dZ_end - kappa dS_end - sum_t kappa_{t-1} dy_t psi_t^T
-//   k_bwd_seg     : folds the aggregates of the following segments into the adjoint at the segment
-//                   end, re-walks the forward recurrence of the segment from its saved start state
+//   k_bwd_seg_scan: one thread per state element folds the aggregates from the last segment back,
+//                   writing the adjoint (dS, dZ) at every segment end.
+//   k_bwd_seg     : starts from the adjoint at its segment end,
+//                   re-walks the forward recurrence of the segment from its saved start state
 //                   (raw chunk-start states to a short-lived scratch), then walks the chunks in
 //                   reverse forming every gradient of each chunk in closed form (see k_bwd_seg's
 //                   phase comments) while carrying (dS, dZ) and the halo gradients of the previous
@@ -124,6 +126,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg_agg(const Geom g, const
 template <typename T, int CH, int D>
 struct BwdSegSmem {
   static constexpr int SPM = CH + kHaloPad;
+  static constexpr int LWR = ((CH + 2 + 15) / 16) * 16;   // rows of the phase-F GEMM operand
   static constexpr bool kStatesInLds = sizeof(T) == 2;   // fp32 reads S_in / Z_in from the re-walk scratch
   T sref[D][D + 8];
   T dSe[D][D + 8];
@@ -133,17 +136,25 @@ struct BwdSegSmem {
   T phi[SPM][D + 8];
   T psi[CH][D + 8];
   T dy[CH][D + 8];
-  T deltaT[SPM][D + 8];
-  T QT[SPM][CH + 8];       // Q^T[s][q],  Q[q][s] = Ws[s, q-1] (psi_q . phi_s)
-  T Qp[CH][SPM + 8];       // Q'[q][s] = Ws[s, q-1] (dy_q . delta_s)
-  T QpT[SPM][CH + 8];
-  T dD[D][SPM + 8];        // dDelta[i][s]
+  T deltaT[SPM][D + 8];    // v_s staged by the loads, then delta^T[s][i]
+  union {
+    struct {               // phases A-D
+      T QT[SPM][CH + 8];   // Q^T[s][q],  Q[q][s] = Ws[s, q-1] (psi_q . phi_s)
+      T Qp[CH][SPM + 8];   // Q'[q][s] = Ws[s, q-1] (dy_q . delta_s)
+      T QpT[SPM][CH + 8];
+      T dD[D][SPM + 8];    // dDelta[i][s]
+    } g;
+    struct {               // phase F
+      float Lw[LWR][CH + 1];      // window-weighted Lm rows (q < CH), hS (row CH), hZ (row CH + 1)
+      float LWs[CH + 2][CH + 1];  // Lw C^T: rows q; row CH = HWsS, row CH + 1 unused
+      float LWz[CH + 2][CH + 1];  // Lw B^T: rows q; row CH = HWzS, row CH + 1 = HWzZ
+    } f;
+  } u;
   T wsh[CH][SPM + 8];      // Ws[s, tau-1]
   float Lm[CH][SPM + 1];   // (dy_q . delta_s)(psi_q . phi_s)
-  float LWs[CH][CH + 1], LWz[CH][CH + 1];
   ChunkScalars<CH> sc;
+  DecayTab<CH> tab;
   float hS[SPM], hZ[SPM], fS[CH], fZ[CH];
-  float HWsS[CH], HWzS[CH], HWzZ[CH];
   float A1[CH + 1], K1[CH + 1], B1[CH + 1];
   float gram[4];
   float red[kSegWaves][4];
@@ -167,7 +178,9 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
   typedef MM<T> M;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int seg = blockIdx.x, bh = blockIdx.y;
-  const int H = g.H, SP = g.SP, e = g.e;
+  const int H = g.H, e = g.e;
+  constexpr int NTS = SPM / 16, NTC = CH / 16;
+  static_assert(SPM <= 64, "backward source tile: coefficient lanes 0..63, decay columns 64..64+CH");
   const size_t tb = (size_t)bh * g.T;
   const size_t sb = (size_t)bh * D * D;
   const int c_begin = seg * sg.G, c_end = min(g.nc, c_begin + sg.G);
@@ -178,36 +191,19 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
 
   // ---- 1. adjoint at the segment end (owned tiles: wave + 8 j)
   float dS[NT2][4], dZ[NT2][4], dsr[NT2][4];
-#pragma unroll
-  for (int j = 0; j < NT2; ++j) {
-    const int tile = wave + kSegWaves * j;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      dS[j][r] = 0.f; dZ[j][r] = 0.f; dsr[j][r] = 0.f;
-      if (tile < NTD * NTD) {
-        const int i = (tile / NTD) * 16 + 4 * (lane >> 4) + r, k = (tile % NTD) * 16 + (lane & 15);
-        const size_t off = sb + (size_t)i * D + k;
-        float ds = a.dS_T ? a.dS_T[off] : 0.f;
-        if (g.clamp_final) ds *= clamp_mask(p.final_raw[off]);
-        dS[j][r] = ds;
-        dZ[j][r] = (g.momentum && a.dZ_T) ? a.dZ_T[off] : 0.f;
-      }
-    }
-  }
-  for (int js = sg.nseg - 1; js > seg; --js) {
-    const float* ag = p.adj_agg + ((size_t)bh * sg.nseg + js) * sg.agg_stride;
-    const float ta = ag[2 * D * D], tk = ag[2 * D * D + 1], tbb = ag[2 * D * D + 2];
+  {
+    const float* sa = p.seg_adj + ((size_t)bh * sg.nseg + seg) * 2 * D * D;
 #pragma unroll
     for (int j = 0; j < NT2; ++j) {
       const int tile = wave + kSegWaves * j;
-      if (tile >= NTD * NTD) continue;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = (tile / NTD) * 16 + 4 * (lane >> 4) + r, k = (tile % NTD) * 16 + (lane & 15);
-        const float Lv = ag[(size_t)i * D + k], Kv = ag[(size_t)D * D + (size_t)i * D + k];
-        const float s_out = dS[j][r];
-        dS[j][r] = ta * s_out + Lv;
-        dZ[j][r] = g.momentum ? (tbb * dZ[j][r] - tk * s_out + Kv) : 0.f;
+        dS[j][r] = 0.f; dZ[j][r] = 0.f; dsr[j][r] = 0.f;
+        if (tile < NTD * NTD) {
+          const int i = (tile / NTD) * 16 + 4 * (lane >> 4) + r, k = (tile % NTD) * 16 + (lane & 15);
+          dS[j][r] = sa[(size_t)i * D + k];
+          dZ[j][r] = sa[(size_t)D * D + (size_t)i * D + k];
+        }
       }
     }
   }
@@ -217,7 +213,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
     FwdPtrs<T> fa;
     fa.k = a.k; fa.q = a.q; fa.v = a.v; fa.lr = a.lr; fa.decay = a.decay; fa.beta = a.beta; fa.gate = a.gate;
     fa.S_ref = a.S_ref; fa.S0 = a.S0; fa.Z0 = a.Z0; fa.buf_in = a.buf_in;
-    fa.y = nullptr; fa.S_T = nullptr; fa.Z_T = nullptr; fa.buf_out = nullptr; fa.saved = nullptr;
+    fa.y = nullptr; fa.S_T = nullptr; fa.Z_T = nullptr; fa.buf_out = nullptr;
     fwd_segment<T, CH, D, WALK_REWALK>(g, fa, sg, nullptr, const_cast<float*>(p.seg_states), rw, nullptr, smem_raw);
   }
   __syncthreads();
@@ -229,6 +225,11 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
 
   // ---- 3. reverse walk
   for (int c = c_end - 1; c >= c_begin; --c) {
+    // per-lane indices re-derived every chunk: keeps the compiler from hoisting every per-lane
+    // address out of the loop and holding (or spilling) them across the whole walk
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int jc = c - c_begin;
     const int t0 = c * g.Lc, t1 = min(g.T, t0 + g.Lc), L = t1 - t0;
     const bool bufchunk = (c == 0) && g.has_buf;
@@ -240,43 +241,96 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
     float* prev_carry = carry + (size_t)((c + 1) & 1) * H * 2 * D; // chunk c+1's halo -> this chunk's tail
     __syncthreads();
 
-    // ---- loads
-    for (int idx = tid; idx < SP * (D / 8); idx += kSegThreads) {
-      const int s = idx / (D / 8), c8 = idx % (D / 8);
-      const int pp = t0 - H + s;
-      Vec8<T> x = (s < H + L && pp >= 0) ? vec8_load(a.k + (tb + pp) * D + c8 * 8) : Vec8<T>::zero();
-      if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
-      x.store(&sm.phi[s][c8 * 8]);
-    }
-    for (int idx = tid; idx < CH * (D / 8); idx += kSegThreads) {
-      const int t = idx / (D / 8), c8 = idx % (D / 8);
-      Vec8<T> x = t < L ? vec8_load(a.q + (tb + t0 + t) * D + c8 * 8) : Vec8<T>::zero();
-      if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
-      x.store(&sm.psi[t][c8 * 8]);
-      const Vec8<T> dv = (t < L && a.dy) ? vec8_load(a.dy + (tb + t0 + t) * D + c8 * 8) : Vec8<T>::zero();
-      dv.store(&sm.dy[t][c8 * 8]);
-    }
-    if (tid < CH) {
-      const bool in = tid < L;
-      sm.sc.alpha[tid] = in ? to_f32(a.decay[tb + t0 + tid]) : 1.f;
-      sm.sc.eta[tid] = in ? to_f32(a.lr[tb + t0 + tid]) : 0.f;
-      sm.sc.beta[tid] = in ? (g.momentum ? to_f32(a.beta[tb + t0 + tid]) : 0.f) : 1.f;
-      sm.fS[tid] = 0.f; sm.fZ[tid] = 0.f;
-    }
-    for (int s = tid; s < SPM; s += kSegThreads) { sm.hS[s] = 0.f; sm.hZ[s] = 0.f; }
-    if (g.gate_mode == GATE_TOKEN) {
-      for (int s = tid; s < SP; s += kSegThreads) {
-        const int pp = t0 - H + s;
-        sm.sc.ug[s] = (s < H + L) ? (pp >= 0 ? to_f32(a.gate[tb + pp]) : 1.f) : 0.f;
-      }
-    } else if (g.gate_mode == GATE_LAG) {
-      for (int idx = tid; idx < CH * e; idx += kSegThreads) {
-        const int t = idx / e;
-        sm.sc.wl[idx] = (t < L) ? to_f32(a.gate[(tb + t0) * e + idx]) : 0.f;
-      }
-    }
-    // states: carried adjoint (registers) and the re-walk's chunk-start state -> LDS operands, Grams
+    // ---- loads: every global read of the chunk is issued before the first LDS write
     {
+      constexpr int NVS = (SPM * (D / 8) + kSegThreads - 1) / kSegThreads;
+      constexpr int NVT = (CH * (D / 8) + kSegThreads - 1) / kSegThreads;
+      constexpr int NWL = (CH * kMaxWindow + kSegThreads - 1) / kSegThreads;
+      Vec8<T> rk[NVS], rv[NVS], rq[NVT], rd[NVT];
+#pragma unroll
+      for (int j = 0; j < NVS; ++j) {
+        const int idx = tid + j * kSegThreads;
+        const int s = idx / (D / 8), c8 = idx % (D / 8);
+        const int pp = t0 - H + s;
+        const bool ok = s < SPM && s < H + L && pp >= 0;
+        rk[j] = ok ? vec8_load(a.k + (tb + pp) * D + c8 * 8) : Vec8<T>::zero();
+        rv[j] = ok ? vec8_load(a.v + (tb + pp) * D + c8 * 8) : Vec8<T>::zero();
+      }
+#pragma unroll
+      for (int j = 0; j < NVT; ++j) {
+        const int idx = tid + j * kSegThreads;
+        const int t = idx / (D / 8), c8 = idx % (D / 8);
+        const bool ok = t < L;
+        rq[j] = ok ? vec8_load(a.q + (tb + t0 + t) * D + c8 * 8) : Vec8<T>::zero();
+        rd[j] = (ok && a.dy) ? vec8_load(a.dy + (tb + t0 + t) * D + c8 * 8) : Vec8<T>::zero();
+      }
+      float r_al = 1.f, r_et = 0.f, r_be = 1.f, r_ug = 0.f;
+      if (tid < L) {
+        r_al = to_f32(a.decay[tb + t0 + tid]);
+        r_et = to_f32(a.lr[tb + t0 + tid]);
+        r_be = g.momentum ? to_f32(a.beta[tb + t0 + tid]) : 0.f;
+      }
+      if (g.gate_mode == GATE_TOKEN && tid < SPM) {
+        const int pp = t0 - H + tid;
+        r_ug = (tid < H + L) ? (pp >= 0 ? to_f32(a.gate[tb + pp]) : 1.f) : 0.f;
+      }
+      float r_wl[NWL];
+#pragma unroll
+      for (int j = 0; j < NWL; ++j) {
+        const int idx = tid + j * kSegThreads;
+        r_wl[j] = (g.gate_mode == GATE_LAG && idx < CH * e && idx / e < L) ? to_f32(a.gate[(tb + t0) * e + idx]) : 0.f;
+      }
+      float s_in[NT2][4], z_in[NT2][4];
+#pragma unroll
+      for (int j = 0; j < NT2; ++j) {
+        const int tile = wave + kSegWaves * j;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          s_in[j][r] = 0.f; z_in[j][r] = 0.f;
+          if (tile < NTD * NTD) {
+            const int i = (tile / NTD) * 16 + 4 * (lane >> 4) + r, k = (tile % NTD) * 16 + (lane & 15);
+            s_in[j][r] = Sin_g[(size_t)i * D + k];
+            z_in[j][r] = g.momentum ? Zin_g[(size_t)i * D + k] : 0.f;
+          }
+        }
+      }
+      // LDS stores
+#pragma unroll
+      for (int j = 0; j < NVS; ++j) {
+        const int idx = tid + j * kSegThreads;
+        const int s = idx / (D / 8), c8 = idx % (D / 8);
+        if (s < SPM) {
+          Vec8<T> x = rk[j];
+          if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
+          x.store(&sm.phi[s][c8 * 8]);
+          rv[j].store(&sm.deltaT[s][c8 * 8]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NVT; ++j) {
+        const int idx = tid + j * kSegThreads;
+        const int t = idx / (D / 8), c8 = idx % (D / 8);
+        if (t < CH) {
+          Vec8<T> x = rq[j];
+          if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
+          x.store(&sm.psi[t][c8 * 8]);
+          rd[j].store(&sm.dy[t][c8 * 8]);
+        }
+      }
+      if (tid < CH) {
+        sm.sc.alpha[tid] = r_al; sm.sc.eta[tid] = r_et; sm.sc.beta[tid] = r_be;
+        sm.fS[tid] = 0.f; sm.fZ[tid] = 0.f;
+      }
+      for (int s = tid; s < SPM; s += kSegThreads) { sm.hS[s] = 0.f; sm.hZ[s] = 0.f; }
+      if (g.gate_mode == GATE_TOKEN && tid < SPM) sm.sc.ug[tid] = r_ug;
+      if (g.gate_mode == GATE_LAG) {
+#pragma unroll
+        for (int j = 0; j < NWL; ++j) {
+          const int idx = tid + j * kSegThreads;
+          if (idx < CH * e) sm.sc.wl[idx] = r_wl[j];
+        }
+      }
+      // carried adjoint (registers) and the re-walk's chunk-start state -> LDS operands, Grams
       float gss = 0.f, gsz = 0.f, gzz = 0.f;
 #pragma unroll
       for (int j = 0; j < NT2; ++j) {
@@ -285,15 +339,14 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = (tile / NTD) * 16 + 4 * (lane >> 4) + r, k = (tile % NTD) * 16 + (lane & 15);
-          float s_in = Sin_g[(size_t)i * D + k];
-          if (clamp_in) s_in = clamp100(s_in);
-          const float z_in = g.momentum ? Zin_g[(size_t)i * D + k] : 0.f;
-          gss += dS[j][r] * s_in; gsz += dS[j][r] * z_in; gzz += dZ[j][r] * z_in;
+          const float sv = clamp_in ? clamp100(s_in[j][r]) : s_in[j][r];
+          const float zv = z_in[j][r];
+          gss += dS[j][r] * sv; gsz += dS[j][r] * zv; gzz += dZ[j][r] * zv;
           sm.dSe[i][k] = from_f32<T>(dS[j][r]);
           sm.dZe[i][k] = from_f32<T>(dZ[j][r]);
           if constexpr (SIL) {
-            sm.Sin[i][k] = from_f32<T>(s_in);
-            sm.Zin[i][k] = from_f32<T>(z_in);
+            sm.Sin[i][k] = from_f32<T>(sv);
+            sm.Zin[i][k] = from_f32<T>(zv);
           }
         }
       }
@@ -305,9 +358,9 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
     __syncthreads();
     if (tid == 0) {
       for (int q = 0; q < 3; ++q) {
-        float s = 0.f;
-        for (int w = 0; w < kSegWaves; ++w) s += sm.red[w][q];
-        sm.gram[q] = s;
+        float sum = 0.f;
+        for (int w = 0; w < kSegWaves; ++w) sum += sm.red[w][q];
+        sm.gram[q] = sum;
       }
     }
     if (bufchunk) {   // <dS_end, B_s>, <dZ_end, B_s> for the dense buffer sources
@@ -331,77 +384,67 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
     }
 
     // ---- phase A: G1 delta^T (waves 0-5) | coefficients (waves 6-7)
+    // Tile indices past the end of a tile list are clamped: the MFMAs stay unconditional and only
+    // the stores are guarded.
     if (wave < 6) {
-      for (int tile = wave; tile < (SP / 16) * NTD; tile += 6) {
+      constexpr int NT1 = NTS * NTD, PER1 = (NT1 + 5) / 6;
+#pragma unroll 1
+      for (int j = 0; j < PER1; ++j) {
+        const int tile = min(wave + 6 * j, NT1 - 1);
+        const bool valid = NT1 % 6 == 0 || wave + 6 * j < NT1;
         const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
         f32x4 acc = zero4();
 #pragma unroll
         for (int k0 = 0; k0 < D; k0 += M::KS)
           acc = M::mma(frag_ld_row<T>(&sm.phi[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.sref[0][0], D + 8, n0, k0), acc);
-        const int i = n0 + (lane & 15);
+        if (valid) {
+          const int i = n0 + (lane & 15);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int s = m0 + 4 * (lane >> 4) + r;
-          const int pp = t0 - H + s;
-          float d = 0.f;
-          if (s < H + L && pp >= 0) d = acc[r] - to_f32(a.v[(tb + pp) * D + i]);
-          sm.deltaT[s][i] = from_f32<T>(d);
+          for (int r = 0; r < 4; ++r) {
+            const int s = m0 + 4 * (lane >> 4) + r;
+            const int pp = t0 - H + s;
+            const float d = (s < H + L && pp >= 0) ? acc[r] - to_f32(sm.deltaT[s][i]) : 0.f;
+            sm.deltaT[s][i] = from_f32<T>(d);
+          }
         }
       }
     } else {
+      // ci < SPM (<= 64): per-source recurrences (Ws[s, tau-1] -> wsh, end values);
+      // ci = 64 .. 64 + CH: the columns of the decay tables (and a, kappa, b).
       const int ci = tid - 6 * kWave;
-      // per-source recurrences (Ws[s, tau-1] -> wsh, end values) and a / kappa / b with the shifted arrays
-      const float* __restrict__ al = sm.sc.alpha;
-      const float* __restrict__ et = sm.sc.eta;
-      const float* __restrict__ be = sm.sc.beta;
-      const float* __restrict__ wl = sm.sc.wl;
-      if (ci < SP) {
-        const int s = ci;
-        const float us = g.gate_mode == GATE_TOKEN ? sm.sc.ug[s] : 1.f;
-        float ws = 0.f, wz = 0.f;
-        for (int t = 0; t < CH; ++t) {
-          sm.wsh[t][s] = from_f32<T>(ws);
-          const int j = t + H - s;
-          float w = 0.f;
-          if (j >= 0 && j < e && t < L) w = (g.gate_mode == GATE_LAG) ? wl[t * e + j] : us;
-          wz = be[t] * wz + w;
-          ws = al[t] * ws + et[t] * wz;
-        }
-        sm.sc.wsend[s] = ws;
-        sm.sc.wzend[s] = wz;
-      } else if (ci == 127) {
-        float ac = 1.f, kc = 0.f, bc = 1.f;
-        sm.A1[0] = 1.f; sm.K1[0] = 0.f; sm.B1[0] = 1.f;
-        for (int t = 0; t < CH; ++t) {
-          sm.sc.acoef[t] = ac; sm.sc.kcoef[t] = kc;
-          bc = be[t] * bc; ac = al[t] * ac; kc = al[t] * kc + et[t] * bc;
-          sm.A1[t + 1] = ac; sm.K1[t + 1] = kc; sm.B1[t + 1] = bc;
-        }
-        sm.sc.endc[0] = ac; sm.sc.endc[1] = kc; sm.sc.endc[2] = bc;
+      if (ci < 64) {
+        chunk_coefficients<CH, true, false, T>(g, sm.sc, L, ci, &sm.wsh[0][0], SPM + 8);
+      } else if (ci <= 64 + CH) {
+        decay_column<CH>(sm.tab, sm.sc, ci - 64, sm.A1, sm.K1, sm.B1);
       }
     }
     __syncthreads();
     // G2 / G3: Kmat = psi phi^T, K3 = dy delta -> Q^T, Q', Q'^T, Lm
     {
-      const int nts = SP / 16;
-      for (int tile = wave; tile < (CH / 16) * nts; tile += kSegWaves) {
-        const int m0 = (tile / nts) * 16, n0 = (tile % nts) * 16;
+      constexpr int NTQ = NTC * NTS, PERQ = (NTQ + kSegWaves - 1) / kSegWaves;
+#pragma unroll 1
+      for (int j = 0; j < PERQ; ++j) {
+        const int tile = min(wave + kSegWaves * j, NTQ - 1);
+        const bool valid = NTQ % kSegWaves == 0 || wave + kSegWaves * j < NTQ;
+        const int m0 = (tile / NTS) * 16, n0 = (tile % NTS) * 16;
         f32x4 kk = zero4(), k3 = zero4();
 #pragma unroll
         for (int k0 = 0; k0 < D; k0 += M::KS) {
           kk = M::mma(frag_ld_row<T>(&sm.psi[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.phi[0][0], D + 8, n0, k0), kk);
           k3 = M::mma(frag_ld_row<T>(&sm.dy[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.deltaT[0][0], D + 8, n0, k0), k3);
         }
-        const int s = n0 + (lane & 15);
+        if (valid) {
+          const int s = n0 + (lane & 15);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = m0 + 4 * (lane >> 4) + r;
-          const float w = to_f32(sm.wsh[t][s]);
-          sm.QT[s][t] = from_f32<T>(w * kk[r]);
-          const T qp = from_f32<T>(w * k3[r]);
-          sm.Qp[t][s] = qp;
-          sm.QpT[s][t] = qp;
-          sm.Lm[t][s] = kk[r] * k3[r];
+          for (int r = 0; r < 4; ++r) {
+            const int t = m0 + 4 * (lane >> 4) + r;
+            const float w = to_f32(sm.wsh[t][s]);
+            sm.u.g.QT[s][t] = from_f32<T>(w * kk[r]);
+            const T qp = from_f32<T>(w * k3[r]);
+            sm.u.g.Qp[t][s] = qp;
+            sm.u.g.QpT[s][t] = qp;
+            sm.Lm[t][s] = kk[r] * k3[r];
+          }
         }
       }
     }
@@ -409,9 +452,12 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
 
     // ---- phase B: G4  dDelta[i, s] = Wz_end[s] (dZ_end phi_s)_i - Ws_end[s] (dS_end phi_s)_i - sum_q dy_q[i] Q[q, s]
     {
-      const int nts = SP / 16;
-      for (int tile = wave; tile < NTD * nts; tile += kSegWaves) {
-        const int m0 = (tile / nts) * 16, n0 = (tile % nts) * 16;
+      constexpr int NT4 = NTD * NTS, PER4 = (NT4 + kSegWaves - 1) / kSegWaves;
+#pragma unroll 1
+      for (int j = 0; j < PER4; ++j) {
+        const int tile = min(wave + kSegWaves * j, NT4 - 1);
+        const bool valid = NT4 % kSegWaves == 0 || wave + kSegWaves * j < NT4;
+        const int m0 = (tile / NTS) * 16, n0 = (tile % NTS) * 16;
         f32x4 az = zero4(), as = zero4(), aq = zero4();
 #pragma unroll
         for (int k0 = 0; k0 < D; k0 += M::KS) {
@@ -419,22 +465,25 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
           as = M::mma(frag_ld_row<T>(&sm.dSe[0][0], D + 8, m0, k0), fb, as);
           az = M::mma(frag_ld_row<T>(&sm.dZe[0][0], D + 8, m0, k0), fb, az);
         }
-        for (int k0 = 0; k0 < CH; k0 += M::KS)
-          aq = M::mma(frag_ld<T>(&sm.dy[0][0], 1, D + 8, m0, k0), frag_ld_row<T>(&sm.QT[0][0], CH + 8, n0, k0), aq);
-        const int s = n0 + (lane & 15);
-        const float wz = sm.sc.wzend[s], ws = sm.sc.wsend[s];
-        float hs = 0.f, hz = 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = m0 + 4 * (lane >> 4) + r;
-          const float d = to_f32(sm.deltaT[s][i]);
-          hs += d * as[r];
-          hz += d * az[r];
-          sm.dD[i][s] = from_f32<T>(wz * az[r] - ws * as[r] - aq[r]);
+        for (int k0 = 0; k0 < CH; k0 += M::KS)
+          aq = M::mma(frag_ld<T>(&sm.dy[0][0], 1, D + 8, m0, k0), frag_ld_row<T>(&sm.u.g.QT[0][0], CH + 8, n0, k0), aq);
+        if (valid) {
+          const int s = n0 + (lane & 15);
+          const float wz = sm.sc.wzend[s], ws = sm.sc.wsend[s];
+          float hs = 0.f, hz = 0.f;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = m0 + 4 * (lane >> 4) + r;
+            const float d = to_f32(sm.deltaT[s][i]);
+            hs += d * as[r];
+            hz += d * az[r];
+            sm.u.g.dD[i][s] = from_f32<T>(wz * az[r] - ws * as[r] - aq[r]);
+          }
+          hs += __shfl_xor(hs, 16); hs += __shfl_xor(hs, 32);
+          hz += __shfl_xor(hz, 16); hz += __shfl_xor(hz, 32);
+          if (lane < 16) { atomicAdd(&sm.hS[s], hs); atomicAdd(&sm.hZ[s], hz); }
         }
-        hs += __shfl_xor(hs, 16); hs += __shfl_xor(hs, 32);
-        hz += __shfl_xor(hz, 16); hz += __shfl_xor(hz, 32);
-        if (lane < 16) { atomicAdd(&sm.hS[s], hs); atomicAdd(&sm.hZ[s], hz); }
       }
     }
     __syncthreads();
@@ -446,7 +495,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         const int s = idx / D, i = idx % D;
         const int pp = t0 - H + s;
         if (pp < 0) continue;
-        float val = -to_f32(sm.dD[i][s]);
+        float val = -to_f32(sm.u.g.dD[i][s]);
         if (s < H) {
           if (first) { if (c > 0) p.halo_part[(((size_t)bh * sg.nseg + seg) * H + s) * (2 * D) + i] = val; }
           else cur_carry[s * 2 * D + i] = val;
@@ -459,82 +508,91 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
     }
 #pragma unroll
     for (int j = 0; j < NT2; ++j) {   // G6: dS_ref[i, k] += sum_s dDelta[i, s] phi_s[k]
-      const int tile = wave + kSegWaves * j;
-      if (tile >= NTD * NTD) continue;
+      const int tile = min(wave + kSegWaves * j, NTD * NTD - 1);
       const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
       f32x4 acc = zero4();
-      for (int k0 = 0; k0 < SP; k0 += M::KS)
-        acc = M::mma(frag_ld_row<T>(&sm.dD[0][0], SPM + 8, m0, k0), frag_ld<T>(&sm.phi[0][0], 1, D + 8, n0, k0), acc);
+#pragma unroll
+      for (int k0 = 0; k0 < SPM; k0 += M::KS)
+        acc = M::mma(frag_ld_row<T>(&sm.u.g.dD[0][0], SPM + 8, m0, k0), frag_ld<T>(&sm.phi[0][0], 1, D + 8, n0, k0), acc);
 #pragma unroll
       for (int r = 0; r < 4; ++r) dsr[j][r] += acc[r];
     }
-    for (int tile = wave; tile < (CH / 16) * NTD; tile += kSegWaves) {   // G7
-      const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
-      f32x4 as = zero4(), az = zero4(), aq = zero4();
+    {   // G7: dpsi[q, k] = a_{q-1} (dy_q S_in)[k] - kappa_{q-1} (dy_q Z_in)[k] - sum_s Q'[q, s] phi_s[k]
+      constexpr int NT7 = NTC * NTD, PER7 = (NT7 + kSegWaves - 1) / kSegWaves;
+#pragma unroll 1
+      for (int j = 0; j < PER7; ++j) {
+        const int tile = min(wave + kSegWaves * j, NT7 - 1);
+        const bool valid = NT7 % kSegWaves == 0 || wave + kSegWaves * j < NT7;
+        const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
+        f32x4 as = zero4(), az = zero4(), aq = zero4();
 #pragma unroll
-      for (int k0 = 0; k0 < D; k0 += M::KS) {
-        const typename M::frag fa = frag_ld_row<T>(&sm.dy[0][0], D + 8, m0, k0);
-        if constexpr (SIL) {
-          as = M::mma(fa, frag_ld<T>(&sm.Sin[0][0], 1, D + 8, n0, k0), as);
-          az = M::mma(fa, frag_ld<T>(&sm.Zin[0][0], 1, D + 8, n0, k0), az);
-        } else {
-          typename M::frag fs;
-          {
-            const int kb = k0 + (lane >> 4) * M::KL;
-            const float* q = Sin_g + (size_t)kb * D + n0 + (lane & 15);
-            if constexpr (M::KL == 1) fs = static_cast<T>(clamp_in ? clamp100(q[0]) : q[0]);
-            else {
+        for (int k0 = 0; k0 < D; k0 += M::KS) {
+          const typename M::frag fa = frag_ld_row<T>(&sm.dy[0][0], D + 8, m0, k0);
+          if constexpr (SIL) {
+            as = M::mma(fa, frag_ld<T>(&sm.Sin[0][0], 1, D + 8, n0, k0), as);
+            az = M::mma(fa, frag_ld<T>(&sm.Zin[0][0], 1, D + 8, n0, k0), az);
+          } else {
+            typename M::frag fs;
+            {
+              const int kb = k0 + (lane >> 4) * M::KL;
+              const float* q = Sin_g + (size_t)kb * D + n0 + (lane & 15);
+              if constexpr (M::KL == 1) fs = static_cast<T>(clamp_in ? clamp100(q[0]) : q[0]);
+              else {
 #pragma unroll
-              for (int ee = 0; ee < M::KL; ++ee) {
-                const float x = q[(size_t)ee * D];
-                fs[ee] = static_cast<T>(clamp_in ? clamp100(x) : x);
+                for (int ee = 0; ee < M::KL; ++ee) {
+                  const float x = q[(size_t)ee * D];
+                  fs[ee] = static_cast<T>(clamp_in ? clamp100(x) : x);
+                }
               }
             }
+            as = M::mma(fa, fs, as);
+            az = M::mma(fa, frag_ld_or_zero<T>(g.momentum ? Zin_g : nullptr, 1, D, n0, k0), az);
           }
-          as = M::mma(fa, fs, as);
-          az = M::mma(fa, frag_ld_or_zero<T>(g.momentum ? Zin_g : nullptr, 1, D, n0, k0), az);
         }
-      }
-      for (int k0 = 0; k0 < SP; k0 += M::KS)
-        aq = M::mma(frag_ld_row<T>(&sm.Qp[0][0], SPM + 8, m0, k0), frag_ld<T>(&sm.phi[0][0], 1, D + 8, n0, k0), aq);
-      const int k = n0 + (lane & 15);
-      f32x4 dpsi;
-      float fsp[4], fzp[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = m0 + 4 * (lane >> 4) + r;
-        dpsi[r] = sm.A1[t] * as[r] - sm.K1[t] * az[r] - aq[r];
-        const float ps = to_f32(sm.psi[t][k]);
-        fsp[r] = as[r] * ps;
-        fzp[r] = az[r] * ps;
-      }
-      if (bufchunk) {
-        for (int s = 0; s < H; ++s) {
-          const float* Bs = a.buf_in + ((size_t)bh * H + s) * D * D;
-          f32x4 ab = zero4();
+        for (int k0 = 0; k0 < SPM; k0 += M::KS)
+          aq = M::mma(frag_ld_row<T>(&sm.u.g.Qp[0][0], SPM + 8, m0, k0), frag_ld<T>(&sm.phi[0][0], 1, D + 8, n0, k0), aq);
+        const int k = n0 + (lane & 15);
+        f32x4 dpsi;
+        float fsp[4], fzp[4];
 #pragma unroll
-          for (int k0 = 0; k0 < D; k0 += M::KS)
-            ab = M::mma(frag_ld_row<T>(&sm.dy[0][0], D + 8, m0, k0), frag_ld<T>(Bs, 1, D, n0, k0), ab);
+        for (int r = 0; r < 4; ++r) {
+          const int t = m0 + 4 * (lane >> 4) + r;
+          dpsi[r] = sm.A1[t] * as[r] - sm.K1[t] * az[r] - aq[r];
+          const float ps = to_f32(sm.psi[t][k]);
+          fsp[r] = as[r] * ps;
+          fzp[r] = az[r] * ps;
+        }
+        if (bufchunk) {
+          for (int s = 0; s < H; ++s) {
+            const float* Bs = a.buf_in + ((size_t)bh * H + s) * D * D;
+            f32x4 ab = zero4();
+#pragma unroll
+            for (int k0 = 0; k0 < D; k0 += M::KS)
+              ab = M::mma(frag_ld_row<T>(&sm.dy[0][0], D + 8, m0, k0), frag_ld<T>(Bs, 1, D, n0, k0), ab);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int t = m0 + 4 * (lane >> 4) + r;
+              dpsi[r] -= to_f32(sm.wsh[t][s]) * ab[r];
+              float lm = ab[r] * to_f32(sm.psi[t][k]);
+              for (int off = 8; off > 0; off >>= 1) lm += __shfl_xor(lm, off);
+              if (valid && (lane & 15) == 0) atomicAdd(&sm.Lm[t][s], lm);
+            }
+          }
+        }
+        if (valid) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int t = m0 + 4 * (lane >> 4) + r;
-            dpsi[r] -= to_f32(sm.wsh[t][s]) * ab[r];
-            float lm = ab[r] * to_f32(sm.psi[t][k]);
-            for (int off = 8; off > 0; off >>= 1) lm += __shfl_xor(lm, off);
-            if ((lane & 15) == 0) atomicAdd(&sm.Lm[t][s], lm);
+            float fsv = fsp[r], fzv = fzp[r];
+            for (int off = 8; off > 0; off >>= 1) { fsv += __shfl_xor(fsv, off); fzv += __shfl_xor(fzv, off); }
+            if ((lane & 15) == 0) { atomicAdd(&sm.fS[t], fsv); atomicAdd(&sm.fZ[t], fzv); }
+            if (t < L) {
+              float outv = dpsi[r];
+              if (g.map_mode == MAP_ELEMENTWISE) outv *= poly_map_grad(to_f32(a.q[(tb + t0 + t) * D + k]), g.map_deg);
+              a.dq[(tb + t0 + t) * D + k] = from_f32<T>(outv);
+            }
           }
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = m0 + 4 * (lane >> 4) + r;
-        float fsv = fsp[r], fzv = fzp[r];
-        for (int off = 8; off > 0; off >>= 1) { fsv += __shfl_xor(fsv, off); fzv += __shfl_xor(fzv, off); }
-        if ((lane & 15) == 0) { atomicAdd(&sm.fS[t], fsv); atomicAdd(&sm.fZ[t], fzv); }
-        if (t < L) {
-          float outv = dpsi[r];
-          if (g.map_mode == MAP_ELEMENTWISE) outv *= poly_map_grad(to_f32(a.q[(tb + t0 + t) * D + k]), g.map_deg);
-          a.dq[(tb + t0 + t) * D + k] = from_f32<T>(outv);
         }
       }
     }
@@ -543,10 +601,11 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         float* dst = a.dbuf_in + ((size_t)bh * H + s) * D * D;
 #pragma unroll
         for (int j = 0; j < NT2; ++j) {
-          const int tile = wave + kSegWaves * j;
-          if (tile >= NTD * NTD) continue;
+          const int tile = min(wave + kSegWaves * j, NTD * NTD - 1);
+          const bool valid = (NTD * NTD) % kSegWaves == 0 || wave + kSegWaves * j < NTD * NTD;
           const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
           f32x4 acc = zero4();
+#pragma unroll
           for (int k0 = 0; k0 < CH; k0 += M::KS) {
             typename M::frag fa;
             const int qb = k0 + (lane >> 4) * M::KL;
@@ -559,10 +618,12 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
             }
             acc = M::mma(fa, frag_ld<T>(&sm.psi[0][0], 1, D + 8, n0, k0), acc);
           }
+          if (valid) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int i = m0 + 4 * (lane >> 4) + r, k = n0 + (lane & 15);
-            dst[(size_t)i * D + k] = sm.sc.wzend[s] * dZ[j][r] - sm.sc.wsend[s] * dS[j][r] - acc[r];
+            for (int r = 0; r < 4; ++r) {
+              const int i = m0 + 4 * (lane >> 4) + r, k = n0 + (lane & 15);
+              dst[(size_t)i * D + k] = sm.sc.wzend[s] * dZ[j][r] - sm.sc.wsend[s] * dS[j][r] - acc[r];
+            }
           }
         }
       }
@@ -572,7 +633,11 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
     // ---- phase D: G5  dphi[s, k] = Wz_end dZ_end^T delta_s - Ws_end dS_end^T delta_s - sum_q Q'[q, s] psi_q + S_ref^T dDelta_s
     {
       const int tail0 = t1 - H;
-      for (int tile = wave; tile < (SP / 16) * NTD; tile += kSegWaves) {
+      constexpr int NT5 = NTS * NTD, PER5 = (NT5 + kSegWaves - 1) / kSegWaves;
+#pragma unroll 1
+      for (int j = 0; j < PER5; ++j) {
+        const int tile = min(wave + kSegWaves * j, NT5 - 1);
+        const bool valid = NT5 % kSegWaves == 0 || wave + kSegWaves * j < NT5;
         const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
         f32x4 a1 = zero4(), a2 = zero4(), a3 = zero4(), a4 = zero4();
 #pragma unroll
@@ -580,28 +645,31 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
           const typename M::frag fa = frag_ld_row<T>(&sm.deltaT[0][0], D + 8, m0, k0);
           a1 = M::mma(fa, frag_ld<T>(&sm.dZe[0][0], 1, D + 8, n0, k0), a1);
           a2 = M::mma(fa, frag_ld<T>(&sm.dSe[0][0], 1, D + 8, n0, k0), a2);
-          a4 = M::mma(frag_ld<T>(&sm.dD[0][0], 1, SPM + 8, m0, k0), frag_ld<T>(&sm.sref[0][0], 1, D + 8, n0, k0), a4);
+          a4 = M::mma(frag_ld<T>(&sm.u.g.dD[0][0], 1, SPM + 8, m0, k0), frag_ld<T>(&sm.sref[0][0], 1, D + 8, n0, k0), a4);
         }
-        for (int k0 = 0; k0 < CH; k0 += M::KS)
-          a3 = M::mma(frag_ld_row<T>(&sm.QpT[0][0], CH + 8, m0, k0), frag_ld<T>(&sm.psi[0][0], 1, D + 8, n0, k0), a3);
-        const int k = n0 + (lane & 15);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int s = m0 + 4 * (lane >> 4) + r;
-          const int pp = t0 - H + s;
-          if (s >= H + L || pp < 0) continue;
-          float val = sm.sc.wzend[s] * a1[r] - sm.sc.wsend[s] * a2[r] - a3[r] + a4[r];
-          if (s < H) {
-            if (first) { if (c > 0) p.halo_part[(((size_t)bh * sg.nseg + seg) * H + s) * (2 * D) + D + k] = val; }
-            else cur_carry[s * 2 * D + D + k] = val;
-            continue;
-          }
-          if (pp >= tail0) val += prev_carry[(pp - tail0) * 2 * D + D + k];
-          if (pp >= seg_tail0) {
-            p.tail_part[(((size_t)bh * sg.nseg + seg) * H + (pp - seg_tail0)) * (2 * D) + D + k] = val;
-          } else {
-            if (g.map_mode == MAP_ELEMENTWISE) val *= poly_map_grad(to_f32(a.k[(tb + pp) * D + k]), g.map_deg);
-            a.dk[(tb + pp) * D + k] = from_f32<T>(val);
+        for (int k0 = 0; k0 < CH; k0 += M::KS)
+          a3 = M::mma(frag_ld_row<T>(&sm.u.g.QpT[0][0], CH + 8, m0, k0), frag_ld<T>(&sm.psi[0][0], 1, D + 8, n0, k0), a3);
+        if (valid) {
+          const int k = n0 + (lane & 15);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int s = m0 + 4 * (lane >> 4) + r;
+            const int pp = t0 - H + s;
+            if (s >= H + L || pp < 0) continue;
+            float val = sm.sc.wzend[s] * a1[r] - sm.sc.wsend[s] * a2[r] - a3[r] + a4[r];
+            if (s < H) {
+              if (first) { if (c > 0) p.halo_part[(((size_t)bh * sg.nseg + seg) * H + s) * (2 * D) + D + k] = val; }
+              else cur_carry[s * 2 * D + D + k] = val;
+              continue;
+            }
+            if (pp >= tail0) val += prev_carry[(pp - tail0) * 2 * D + D + k];
+            if (pp >= seg_tail0) {
+              p.tail_part[(((size_t)bh * sg.nseg + seg) * H + (pp - seg_tail0)) * (2 * D) + D + k] = val;
+            } else {
+              if (g.map_mode == MAP_ELEMENTWISE) val *= poly_map_grad(to_f32(a.k[(tb + pp) * D + k]), g.map_deg);
+              a.dk[(tb + pp) * D + k] = from_f32<T>(val);
+            }
           }
         }
       }
@@ -612,109 +680,120 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
       const float ae = sm.sc.endc[0], ke = sm.sc.endc[1], be = sm.sc.endc[2];
 #pragma unroll
       for (int j = 0; j < NT2; ++j) {
-        const int tile = wave + kSegWaves * j;
-        if (tile >= NTD * NTD) continue;
+        const int tile = min(wave + kSegWaves * j, NTD * NTD - 1);
+        const bool valid = (NTD * NTD) % kSegWaves == 0 || wave + kSegWaves * j < NTD * NTD;
         const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
         f32x4 aa = zero4(), ak = zero4();
+#pragma unroll
         for (int k0 = 0; k0 < CH; k0 += M::KS) {
           const typename M::frag fb = frag_ld<T>(&sm.psi[0][0], 1, D + 8, n0, k0);
           aa = M::mma(frag_ld_kscaled<T>(&sm.dy[0][0], 1, D + 8, m0, k0, sm.sc.acoef), fb, aa);
           ak = M::mma(frag_ld_kscaled<T>(&sm.dy[0][0], 1, D + 8, m0, k0, sm.sc.kcoef), fb, ak);
         }
+        if (valid) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = m0 + 4 * (lane >> 4) + r, k = n0 + (lane & 15);
-          const float lam = ae * dS[j][r] + aa[r];
-          const float mu = g.momentum ? (be * dZ[j][r] - ke * dS[j][r] - ak[r]) : 0.f;
-          const float mk = clamp_in ? clamp_mask(Sin_g[(size_t)i * D + k]) : 1.f;
-          dS[j][r] = lam * mk;
-          dZ[j][r] = mu;
-          if (c == 0) {
-            a.dS0[sb + (size_t)i * D + k] = lam;
-            if (g.momentum && a.dZ0) a.dZ0[sb + (size_t)i * D + k] = mu;
+          for (int r = 0; r < 4; ++r) {
+            const int i = m0 + 4 * (lane >> 4) + r, k = n0 + (lane & 15);
+            const float lam = ae * dS[j][r] + aa[r];
+            const float mu = g.momentum ? (be * dZ[j][r] - ke * dS[j][r] - ak[r]) : 0.f;
+            const float mk = clamp_in ? clamp_mask(Sin_g[(size_t)i * D + k]) : 1.f;
+            dS[j][r] = lam * mk;
+            dZ[j][r] = mu;
+            if (c == 0) {
+              a.dS0[sb + (size_t)i * D + k] = lam;
+              if (g.momentum && a.dZ0) a.dZ0[sb + (size_t)i * D + k] = mu;
+            }
           }
         }
       }
     }
 
     // ---- phase F: scalar gradients
-    if (tid < CH) {
-      const int q = tid;
-      float lz = 0.f, ls = 0.f;
-      for (int t = 0; t < CH; ++t) {
-        float acc = 0.f;
-        for (int j = 0; j < e && t < L; ++j) {
-          const int s = t + H - j;
-          acc += src_w<T>(g.gate_mode, sm.sc.ug[s], sm.sc.wl, e, t, j) * sm.Lm[q][s];
+    __syncthreads();   // phase D done with the union's GEMM operands
+    // F1: Lw[q][t'] = sum_j w(t', j) X_q[t' + H - j],  X_q = Lm[q] (q < CH), hS (q = CH), hZ (q = CH + 1)
+    for (int idx = tid; idx < (CH + 2) * CH; idx += kSegThreads) {
+      const int q = idx / CH, tq = idx % CH;
+      const float* X = q < CH ? &sm.Lm[q][0] : (q == CH ? sm.hS : sm.hZ);
+      float acc = 0.f;
+      if (tq < L) {
+        for (int j = 0; j < e; ++j) {
+          const int s = tq + H - j;
+          acc += src_w<T>(g.gate_mode, sm.sc.ug[s], sm.sc.wl, e, tq, j) * X[s];
         }
-        lz = sm.sc.beta[t] * lz + acc;
-        ls = sm.sc.alpha[t] * ls + sm.sc.eta[t] * lz;
-        sm.LWs[q][t] = ls;
-        sm.LWz[q][t] = lz;
       }
-    } else if (tid == CH) {
-      float hzs = 0.f, hss = 0.f, hzz = 0.f;
-      for (int t = 0; t < CH; ++t) {
-        float as = 0.f, az = 0.f;
-        for (int j = 0; j < e && t < L; ++j) {
-          const int s = t + H - j;
-          const float w = src_w<T>(g.gate_mode, sm.sc.ug[s], sm.sc.wl, e, t, j);
-          as += w * sm.hS[s];
-          az += w * sm.hZ[s];
+      sm.u.f.Lw[q][tq] = acc;
+    }
+    __syncthreads();
+    // F2: the window-weighted recurrences along the chunk as GEMMs with the decay tables:
+    //   LWz[q][t] = sum_t' B[t'+1][t] Lw[q][t'],   LWs[q][t] = sum_t' C[t'+1][t] Lw[q][t']
+    {
+      typedef MM<float> MF;
+      constexpr int NRT = Sm::LWR / 16, NCT = CH / 16;
+      for (int job = wave; job < 2 * NRT * NCT; job += kSegWaves) {
+        const int mat = job / (NRT * NCT), tile = job % (NRT * NCT);
+        const int m0 = (tile / NCT) * 16, n0 = (tile % NCT) * 16;
+        const float* tabp = mat == 0 ? &sm.tab.B[1][0] : &sm.tab.C[1][0];
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int k0 = 0; k0 < CH; k0 += MF::KS)
+          acc = MF::mma(frag_ld<float>(&sm.u.f.Lw[0][0], CH + 1, 1, m0, k0), frag_ld<float>(tabp, 1, CH + 1, n0, k0), acc);
+        float* dst = mat == 0 ? &sm.u.f.LWz[0][0] : &sm.u.f.LWs[0][0];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int q = m0 + 4 * (lane >> 4) + r;
+          if (q < CH + 2) dst[q * (CH + 1) + n0 + (lane & 15)] = acc[r];
         }
-        hzs = sm.sc.beta[t] * hzs + as;
-        hss = sm.sc.alpha[t] * hss + sm.sc.eta[t] * hzs;
-        hzz = sm.sc.beta[t] * hzz + az;
-        sm.HWsS[t] = hss; sm.HWzS[t] = hzs; sm.HWzZ[t] = hzz;
       }
     }
     __syncthreads();
-    // one thread per (target t, term): term 0 -> dalpha, 1 -> deta, 2 -> dbeta, 3 + j -> dw[t, j]
+    // F3: one wave per term (0: dalpha, 1: deta, 2: dbeta, 3 + j: dw[t, j]); lane = (q part, target t).
+    //   The running products of the step-by-step adjoint are table entries: prod alpha = A[t+1][q-1],
+    //   prod beta = B[t+1][q-1], the eta-mixed term = C[t+1][q-1] (zero for q - 1 < t).
     {
+      constexpr int NQ = kWave / CH;
+      constexpr int QPP = CH / NQ;
+      const int t = lane % CH, part = lane / CH;
       const int nterm = 3 + (g.gate_mode != GATE_NONE ? e : 0);
-      for (int idx = tid; idx < L * nterm; idx += kSegThreads) {
-        const int t = idx % L, term = idx / L;
-        const float gss = sm.gram[0], gsz = sm.gram[1], gzz = sm.gram[2];
-        const float am1 = sm.A1[t], km1 = sm.K1[t], bm1 = sm.B1[t];
-        const float b0 = sm.B1[t + 1];
-        float acc = 0.f;
-        float Ar = 1.f, Br = 1.f, Mr = sm.sc.eta[t];
+      const float gss = sm.gram[0], gsz = sm.gram[1], gzz = sm.gram[2];
+      const float am1 = sm.A1[t], km1 = sm.K1[t], bm1 = sm.B1[t], b0 = sm.B1[t + 1];
+      const float Aend = sm.tab.A[t + 1][CH - 1], Bend = sm.tab.B[t + 1][CH - 1], Cend = sm.tab.C[t + 1][CH - 1];
+      for (int term = wave; term < nterm; term += kSegWaves) {
+        const float* W = term < 2 ? &sm.tab.A[t + 1][0] : &sm.tab.C[t + 1][0];
         const int sj = term >= 3 ? t + H - (term - 3) : 0;
-        for (int q = t + 1; q < L; ++q) {
-          float v;
-          if (term == 0) {
-            const float LWs_m1 = t > 0 ? sm.LWs[q][t - 1] : 0.f;
-            v = Ar * (am1 * sm.fS[q] - km1 * sm.fZ[q] - LWs_m1);
-          } else if (term == 1) {
-            v = Ar * (b0 * sm.fZ[q] + sm.LWz[q][t]);
-          } else if (term == 2) {
-            const float LWz_m1 = t > 0 ? sm.LWz[q][t - 1] : 0.f;
-            v = Mr * (bm1 * sm.fZ[q] + LWz_m1);
-          } else {
-            v = Mr * sm.Lm[q][sj];
+        float acc = 0.f;
+#pragma unroll 4
+        for (int qq = 0; qq < QPP; ++qq) {
+          const int q = part * QPP + qq;
+          if (q >= 1) {
+            float v;
+            if (term == 0) v = am1 * sm.fS[q] - km1 * sm.fZ[q] - (t > 0 ? sm.u.f.LWs[q][t - 1] : 0.f);
+            else if (term == 1) v = b0 * sm.fZ[q] + sm.u.f.LWz[q][t];
+            else if (term == 2) v = bm1 * sm.fZ[q] + (t > 0 ? sm.u.f.LWz[q][t - 1] : 0.f);
+            else v = sm.Lm[q][sj];
+            acc += W[q - 1] * v;
           }
-          acc += v;
-          Ar *= sm.sc.alpha[q];
-          Br *= sm.sc.beta[q];
-          Mr = sm.sc.alpha[q] * Mr + sm.sc.eta[q] * Br;
         }
-        const size_t tt = tb + t0 + t;
-        if (term == 0) {
-          const float HWsS_m1 = t > 0 ? sm.HWsS[t - 1] : 0.f;
-          a.ddecay[tt] = from_f32<T>(acc + Ar * (am1 * gss - km1 * gsz - HWsS_m1));
-        } else if (term == 1) {
-          a.dlr[tt] = from_f32<T>(-(acc + Ar * (b0 * gsz + sm.HWzS[t])));
-        } else if (term == 2) {
-          if (g.momentum && a.dbeta) {
-            const float HWzS_m1 = t > 0 ? sm.HWzS[t - 1] : 0.f;
-            const float HWzZ_m1 = t > 0 ? sm.HWzZ[t - 1] : 0.f;
-            a.dbeta[tt] = from_f32<T>(Br * (bm1 * gzz + HWzZ_m1) - Mr * (bm1 * gsz + HWzS_m1) - acc);
+#pragma unroll
+        for (int off = CH; off < kWave; off <<= 1) acc += __shfl_xor(acc, off);
+        if (part == 0 && t < L) {
+          const size_t tt = tb + t0 + t;
+          if (term == 0) {
+            const float hss_m1 = t > 0 ? sm.u.f.LWs[CH][t - 1] : 0.f;
+            a.ddecay[tt] = from_f32<T>(acc + Aend * (am1 * gss - km1 * gsz - hss_m1));
+          } else if (term == 1) {
+            a.dlr[tt] = from_f32<T>(-(acc + Aend * (b0 * gsz + sm.u.f.LWz[CH][t])));
+          } else if (term == 2) {
+            if (g.momentum && a.dbeta) {
+              const float hzs_m1 = t > 0 ? sm.u.f.LWz[CH][t - 1] : 0.f;
+              const float hzz_m1 = t > 0 ? sm.u.f.LWz[CH + 1][t - 1] : 0.f;
+              a.dbeta[tt] = from_f32<T>(Bend * (bm1 * gzz + hzz_m1) - Cend * (bm1 * gsz + hzs_m1) - acc);
+            }
+          } else {
+            const int j = term - 3;
+            const float v = Bend * sm.hZ[sj] - Cend * sm.hS[sj] - acc;
+            if (g.gate_mode == GATE_LAG) a.dgate[tt * e + j] = from_f32<T>(v);
+            else p.dw[tt * e + j] = v;
           }
-        } else {
-          const int j = term - 3;
-          const float v = Br * sm.hZ[sj] - Mr * sm.hS[sj] - acc;
-          if (g.gate_mode == GATE_LAG) a.dgate[tt * e + j] = from_f32<T>(v);
-          else p.dw[tt * e + j] = v;
         }
       }
     }
@@ -730,6 +809,36 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
     for (int r = 0; r < 4; ++r) {
       const int i = (tile / NTD) * 16 + 4 * (lane >> 4) + r, k = (tile % NTD) * 16 + (lane & 15);
       dst[(size_t)i * D + k] = dsr[j][r];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// adjoint at every segment end: grid (D * D / kThreads, BH)
+//   x_{j-1} = [[a_j, 0], [-kappa_j, b_j]] x_j + [L_j; K_j], starting from (dS_T * clamp mask, dZ_T)
+// ---------------------------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(kThreads) void k_bwd_seg_scan(const Geom g, const float* dS_T, const float* dZ_T,
+                                                             const SegGeom sg, const BwdSegPtrs p) {
+  const int bh = blockIdx.y;
+  const int idx = blockIdx.x * kThreads + threadIdx.x;
+  if (idx >= D * D) return;
+  const size_t off = (size_t)bh * D * D + idx;
+  float dS = dS_T ? dS_T[off] : 0.f;
+  if (g.clamp_final) dS *= clamp_mask(p.final_raw[off]);
+  float dZ = (g.momentum && dZ_T) ? dZ_T[off] : 0.f;
+  const float* ag = p.adj_agg + (size_t)bh * sg.nseg * sg.agg_stride;
+  float* sa = p.seg_adj + (size_t)bh * sg.nseg * 2 * D * D;
+  for (int js = sg.nseg - 1; js >= 0; --js) {
+    sa[(size_t)js * 2 * D * D + idx] = dS;
+    sa[(size_t)js * 2 * D * D + D * D + idx] = dZ;
+    if (js > 0) {
+      const float* aj = ag + (size_t)js * sg.agg_stride;
+      const float ta = aj[2 * D * D], tk = aj[2 * D * D + 1], tbb = aj[2 * D * D + 2];
+      const float Lv = aj[idx], Kv = aj[D * D + idx];
+      const float s_out = dS;
+      dS = ta * s_out + Lv;
+      dZ = g.momentum ? (tbb * dZ - tk * s_out + Kv) : 0.f;
     }
   }
 }
@@ -851,6 +960,11 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
     prof_end(KID_BWD_ADJOINT, stream);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
+  prof_begin(KID_BWD_SCAN, stream);
+  hipLaunchKernelGGL((k_bwd_seg_scan<D>), dim3((D * D + kThreads - 1) / kThreads, g.BH), dim3(kThreads), 0, stream,
+                     g, a.dS_T, a.dZ_T, sg, p);
+  prof_end(KID_BWD_SCAN, stream);
+  if ((err = hipGetLastError()) != hipSuccess) return err;
   {
     const size_t smem = bwd_seg_smem_bytes<T, CH, D>(g.H);
     err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bwd_seg<T, CH, D>),

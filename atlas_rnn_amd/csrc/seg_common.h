@@ -20,6 +20,7 @@ struct BwdSegPtrs {
   const float* seg_states;   // forward segment-start states [BH][nseg][2][D][D]
   const float* final_raw;    // forward raw S_{T-1} [BH][D][D]
   float* adj_agg;            // [BH][nseg][agg_stride]: L, K, a, kappa, b
+  float* seg_adj;            // [BH][nseg][2][D][D] adjoint (dS, dZ) at each segment end
   float* rw;                 // [BH][nseg][Gb][2][D][D] raw chunk-start states of the re-walk
   float* dsref_part;         // [BH][nseg][D][D]
   float* tail_part;          // [BH][nseg][H][2D]  (dv | dphi) partial of a segment's last H tokens
@@ -77,42 +78,112 @@ struct ChunkScalars {
   float endc[4];                        // a_end, kappa_end, b_end
 };
 
+// Decay tables of one chunk, stored [c][t] with source column c = t' + 1 (column 0 is the chunk
+// start, t' = -1) and target row t:
+//   A[c][t] = prod_{u = t'+1 .. t} alpha_u,   B[c][t] = prod_{u = t'+1 .. t} beta_u,
+//   C[c][t] = response of Ws at t to a unit input into Wz at t':
+//             C[c][t'] = eta_t',  C[c][t] = alpha_t C[c][t-1] + eta_t B[c][t]   (t > t'),
+// and zero for t < t'. Column 0 holds the chunk-start coefficients a_t, b_t, kappa_t. Every linear
+// recurrence along the chunk (Wz / Ws of a source, and the adjoint recurrences of the scalar
+// gradients) is a sum over these columns, so it runs in parallel instead of step by step.
+// The pitch CH + 1 keeps row-wise and column-wise accesses free of bank conflicts.
+template <int CH>
+struct DecayTab {
+  float A[CH + 1][CH + 1], B[CH + 1][CH + 1], C[CH + 1][CH + 1];
+};
+
+// Column c (0 <= c <= CH) of the decay tables; the thread of column 0 also writes the prefix
+// coefficients A1[t] = a_{t-1}, K1[t] = kappa_{t-1}, B1[t] = b_{t-1} (t = 0..CH; A1[0] = B1[0] = 1,
+// K1[0] = 0) and sc.acoef / sc.kcoef / sc.endc.
+template <int CH>
+__device__ __forceinline__ void decay_column(DecayTab<CH>& tab, ChunkScalars<CH>& sc, int c, float* A1, float* K1,
+                                             float* B1) {
+  static_assert(CH % 8 == 0, "decay table groups");
+  const int tp = c - 1;
+  float a = 1.f, b = 1.f, m = 0.f;
+  if (c == 0) { A1[0] = 1.f; K1[0] = 0.f; B1[0] = 1.f; sc.acoef[0] = 1.f; sc.kcoef[0] = 0.f; }
+  for (int t0 = 0; t0 < CH; t0 += 8) {
+    float al8[8], et8[8], be8[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) { al8[u] = sc.alpha[t0 + u]; et8[u] = sc.eta[t0 + u]; be8[u] = sc.beta[t0 + u]; }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int t = t0 + u;
+      if (t == tp) {
+        m = et8[u];
+      } else if (t > tp) {
+        b = be8[u] * b;
+        a = al8[u] * a;
+        m = al8[u] * m + et8[u] * b;
+      }
+      const bool on = t >= tp;
+      tab.A[c][t] = on ? a : 0.f;
+      tab.B[c][t] = on ? b : 0.f;
+      tab.C[c][t] = on ? m : 0.f;
+      if (c == 0) {
+        A1[t + 1] = a; K1[t + 1] = m; B1[t + 1] = b;
+        if (t + 1 < CH) { sc.acoef[t + 1] = a; sc.kcoef[t + 1] = m; }
+      }
+    }
+  }
+  if (c == 0) { sc.endc[0] = a; sc.endc[1] = m; sc.endc[2] = b; }
+}
+
 // Coefficient recurrences of a chunk, run by 128 lanes (ci = 0..127):
-//   source s (ci < SP):  Wz[s,t] = beta_t Wz[s,t-1] + w(s,t),  Ws[s,t] = alpha_t Ws[s,t-1] + eta_t Wz[s,t]
+//   source s (ci < SPM): Wz[s,t] = beta_t Wz[s,t-1] + w(s,t),  Ws[s,t] = alpha_t Ws[s,t-1] + eta_t Wz[s,t]
 //                        (w(s,t) = window weight of source s at target t), writing Ws[s, t-1] to
-//                        wsh[t * ldw + s] when wsh != nullptr and the end values to wsend / wzend;
-//   ci == 127:           b_t = beta_t b_{t-1}, a_t = alpha_t a_{t-1}, kappa_t = alpha_t kappa_{t-1} + eta_t b_t.
-template <int CH, bool WSH>
+//                        wsh[t * ldw + s] when WSH and the end values to wsend / wzend;
+//   ci == 127 (PREFIX):  b_t = beta_t b_{t-1}, a_t = alpha_t a_{t-1}, kappa_t = alpha_t kappa_{t-1} + eta_t b_t.
+// The scalars of 8 steps are read into registers before the 8 dependent steps run, so the chain
+// waits on LDS once per group instead of once per step.
+template <int CH, bool WSH, bool PREFIX = true, typename WT = float>
 __device__ __forceinline__ void chunk_coefficients(const Geom& g, ChunkScalars<CH>& sc, int L, int ci,
-                                                   float* __restrict__ wsh, int ldw) {
+                                                   WT* __restrict__ wsh, int ldw) {
+  constexpr int SPM = CH + kHaloPad;
+  static_assert(SPM <= 127 && CH % 8 == 0, "coefficient lanes");
   const float* __restrict__ al = sc.alpha;
   const float* __restrict__ et = sc.eta;
   const float* __restrict__ be = sc.beta;
   const float* __restrict__ wl = sc.wl;
   const int H = g.H, e = g.e;
-  if (ci < g.SP) {
+  if (ci < SPM) {
     const int s = ci;
     const float us = g.gate_mode == GATE_TOKEN ? sc.ug[s] : 1.f;
+    const bool lag = g.gate_mode == GATE_LAG;
     float ws = 0.f, wz = 0.f;
-#pragma unroll 8
-    for (int t = 0; t < CH; ++t) {
-      if constexpr (WSH) wsh[t * ldw + s] = ws;
-      const int j = t + H - s;
-      float w = 0.f;
-      if (j >= 0 && j < e && t < L) w = (g.gate_mode == GATE_LAG) ? wl[t * e + j] : us;
-      wz = be[t] * wz + w;
-      ws = al[t] * ws + et[t] * wz;
+    for (int t0 = 0; t0 < CH; t0 += 8) {
+      float al8[8], et8[8], be8[8], w8[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int t = t0 + u, j = t + H - s;
+        const bool on = j >= 0 && j < e && t < L;
+        const float wv = wl[on ? t * e + j : 0];
+        al8[u] = al[t]; et8[u] = et[t]; be8[u] = be[t];
+        w8[u] = on ? (lag ? wv : us) : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if constexpr (WSH) wsh[(t0 + u) * ldw + s] = static_cast<WT>(ws);
+        wz = be8[u] * wz + w8[u];
+        ws = al8[u] * ws + et8[u] * wz;
+      }
     }
     sc.wsend[s] = ws;
     sc.wzend[s] = wz;
-  } else if (ci == 127) {
+  } else if (PREFIX && ci == 127) {
     float ac = 1.f, kc = 0.f, bc = 1.f;
-    for (int t = 0; t < CH; ++t) {
-      sc.acoef[t] = ac;
-      sc.kcoef[t] = kc;
-      bc = be[t] * bc;
-      ac = al[t] * ac;
-      kc = al[t] * kc + et[t] * bc;
+    for (int t0 = 0; t0 < CH; t0 += 8) {
+      float al8[8], et8[8], be8[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) { al8[u] = al[t0 + u]; et8[u] = et[t0 + u]; be8[u] = be[t0 + u]; }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        sc.acoef[t0 + u] = ac;
+        sc.kcoef[t0 + u] = kc;
+        bc = be8[u] * bc;
+        ac = al8[u] * ac;
+        kc = al8[u] * kc + et8[u] * bc;
+      }
     }
     sc.endc[0] = ac; sc.endc[1] = kc; sc.endc[2] = bc;
   }

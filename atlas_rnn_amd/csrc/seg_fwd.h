@@ -1,5 +1,10 @@
 // seg_fwd.h - the segment walk of the forward recurrence, shared by the forward kernels and the
 // backward pass's forward re-walk.
+//
+// Every chunk is a handful of small GEMMs separated by workgroup barriers; with 8 waves per CU the
+// barriers and LDS latency, not the matrix cores, set the pace. All tile counts and k extents are
+// therefore compile-time (the source tile always spans SPM = CH + 32 rows, padded rows are zero)
+// so that each wave's fragment loads are issued together ahead of its MFMA chains.
 #pragma once
 
 #include "mem_common.h"
@@ -14,7 +19,7 @@ struct SegFwdSmem {
   T phi[SPM][D + 8];
   T phiTs[D][SPM + 8];       // Ws_end[s] * phi[s][k], stored [k][s]
   T phiTz[D][SPM + 8];       // Wz_end[s] * phi[s][k], stored [k][s]
-  T delta[D][SPM + 8];       // delta[i][s]
+  T delta[D][SPM + 8];       // v staged by the loads as [i][s], then delta[i][s]
   T sref[D][D + 8];
   ChunkScalars<CH> sc;
   // full walk only
@@ -31,9 +36,10 @@ struct ChunkPrefetch {
   static constexpr int SPM = CH + kHaloPad;
   static constexpr int NV_PHI = (SPM * D / 8 + kSegThreads - 1) / kSegThreads;
   static constexpr int NV_PSI = FULL ? (CH * D / 8 + kSegThreads - 1) / kSegThreads : 0;
-  Vec8<T> phi[NV_PHI];
-  Vec8<T> psi[NV_PSI > 0 ? NV_PSI : 1];
   static constexpr int NWL = (CH * kMaxWindow + kSegThreads - 1) / kSegThreads;
+  Vec8<T> phi[NV_PHI];
+  Vec8<T> vv[NV_PHI];
+  Vec8<T> psi[NV_PSI > 0 ? NV_PSI : 1];
   float alpha, eta, beta, ug;
   float wl[NWL];
 
@@ -42,10 +48,18 @@ struct ChunkPrefetch {
 #pragma unroll
     for (int j = 0; j < NV_PHI; ++j) {
       const int v = tid + j * kSegThreads;
-      const int s = v / (D / 8), c8 = v % (D / 8);
-      const int p = t0 - H + s;
-      const bool ok = s < g.SP && s < H + L && p >= 0;
-      phi[j] = ok ? vec8_load(a.k + (tb + p) * D + c8 * 8) : Vec8<T>::zero();
+      {   // phi: 8 consecutive features of source s per lane
+        const int s = v / (D / 8), c8 = v % (D / 8);
+        const int p = t0 - H + s;
+        const bool ok = s < SPM && s < H + L && p >= 0;
+        phi[j] = ok ? vec8_load(a.k + (tb + p) * D + c8 * 8) : Vec8<T>::zero();
+      }
+      {   // v: consecutive lanes take consecutive sources (conflict-free transposed LDS store)
+        const int s = v % SPM, c8 = v / SPM;
+        const int p = t0 - H + s;
+        const bool ok = c8 < D / 8 && s < H + L && p >= 0;
+        vv[j] = ok ? vec8_load(a.v + (tb + p) * D + c8 * 8) : Vec8<T>::zero();
+      }
     }
     if constexpr (FULL) {
 #pragma unroll
@@ -55,22 +69,20 @@ struct ChunkPrefetch {
         psi[j] = (t < L) ? vec8_load(a.q + (tb + t0 + t) * D + c8 * 8) : Vec8<T>::zero();
       }
     }
-    if (tid < CH) {
-      const bool in = tid < L;
-      alpha = in ? to_f32(a.decay[tb + t0 + tid]) : 1.f;
-      eta = in ? to_f32(a.lr[tb + t0 + tid]) : 0.f;
-      beta = in ? (g.momentum ? to_f32(a.beta[tb + t0 + tid]) : 0.f) : 1.f;
+    alpha = 1.f; eta = 0.f; beta = 1.f; ug = 0.f;
+    if (tid < L) {
+      alpha = to_f32(a.decay[tb + t0 + tid]);
+      eta = to_f32(a.lr[tb + t0 + tid]);
+      beta = g.momentum ? to_f32(a.beta[tb + t0 + tid]) : 0.f;
     }
-    if (g.gate_mode == GATE_TOKEN && tid < g.SP) {
+    if (g.gate_mode == GATE_TOKEN && tid < SPM) {
       const int p = t0 - H + tid;
       ug = (tid < H + L) ? (p >= 0 ? to_f32(a.gate[tb + p]) : 1.f) : 0.f;
-    } else if (g.gate_mode == GATE_LAG) {
+    }
 #pragma unroll
-      for (int j = 0; j < NWL; ++j) {
-        const int idx = tid + j * kSegThreads;
-        const int t = idx / g.e;
-        wl[j] = (idx < CH * g.e && t < L) ? to_f32(a.gate[(tb + t0) * g.e + idx]) : 0.f;
-      }
+    for (int j = 0; j < NWL; ++j) {
+      const int idx = tid + j * kSegThreads;
+      wl[j] = (g.gate_mode == GATE_LAG && idx < CH * g.e && idx / g.e < L) ? to_f32(a.gate[(tb + t0) * g.e + idx]) : 0.f;
     }
   }
 
@@ -80,11 +92,20 @@ struct ChunkPrefetch {
 #pragma unroll
     for (int j = 0; j < NV_PHI; ++j) {
       const int v = tid + j * kSegThreads;
-      const int s = v / (D / 8), c8 = v % (D / 8);
-      if (s < SPM) {
-        Vec8<T> x = phi[j];
-        if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
-        x.store(&sm.phi[s][c8 * 8]);
+      {
+        const int s = v / (D / 8), c8 = v % (D / 8);
+        if (s < SPM) {
+          Vec8<T> x = phi[j];
+          if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
+          x.store(&sm.phi[s][c8 * 8]);
+        }
+      }
+      {
+        const int s = v % SPM, c8 = v / SPM;
+        if (c8 < D / 8) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sm.delta[c8 * 8 + e][s] = vv[j].v[e];
+        }
       }
     }
     if constexpr (FULL) {
@@ -100,7 +121,7 @@ struct ChunkPrefetch {
       }
     }
     if (tid < CH) { sm.sc.alpha[tid] = alpha; sm.sc.eta[tid] = eta; sm.sc.beta[tid] = beta; }
-    if (g.gate_mode == GATE_TOKEN && tid < g.SP) sm.sc.ug[tid] = ug;
+    if (g.gate_mode == GATE_TOKEN && tid < SPM) sm.sc.ug[tid] = ug;
     if (g.gate_mode == GATE_LAG) {
 #pragma unroll
       for (int j = 0; j < NWL; ++j) {
@@ -115,14 +136,17 @@ enum WalkMode { WALK_AGG = 0, WALK_FULL = 1, WALK_REWALK = 2 };
 
 // Segment walk.
 //   WALK_AGG:    zero initial state; writes the segment aggregate (a, kappa, b, U, V) to agg.
-//   WALK_FULL:   folds the preceding aggregates into the start state (saved to seg_states), walks
-//                the chunks with the true state and writes y (and S_T, Z_T, the raw S_{T-1}).
-//   WALK_REWALK: starts from seg_states[seg] (saved by WALK_FULL, chunk length may differ) and
+//   WALK_FULL:   starts from seg_states[seg] (the segment scan folded the preceding aggregates),
+//                walks the chunks with the true state and writes y (and S_T, Z_T, the raw S_{T-1}).
+//   WALK_REWALK: starts from seg_states[seg] (chunk length may differ from the forward's) and
 //                writes the raw state at the start of every chunk of the segment to rw (the
 //                backward pass walks them in reverse); no y.
+// Wave roles per chunk: P1 waves 0-5 run G1 (and G2 for the full walk) while waves 6-7 run the
+// coefficient recurrences; P3 waves 0-3 run G3 (y) while waves 4-7 run G4 and update the states,
+// which they hold in registers (wave 4 + m owns state rows 16 m .. 16 m + 15).
 template <typename T, int CH, int D, int MODE>
 __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg, float* agg,
-                                            float* seg_states, float* rw, float* final_raw,
+                                            const float* seg_states, float* rw, float* final_raw,
                                             unsigned char* smem_raw) {
   constexpr bool AGG = MODE == WALK_AGG;
   constexpr bool FULL = MODE == WALK_FULL;
@@ -131,10 +155,11 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
   Sm& sm = *reinterpret_cast<Sm*>(smem_raw);
   constexpr int SPM = Sm::SPM;
   constexpr int NTD = D / 16;                    // 16-wide tiles along D
+  constexpr int NTS = SPM / 16;                  // 16-wide tiles along the sources
   typedef MM<T> M;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int seg = blockIdx.x, bh = blockIdx.y;
-  const int H = g.H, SP = g.SP;
+  const int H = g.H;
   const size_t tb = (size_t)bh * g.T;
   const size_t sb = (size_t)bh * D * D;
   const int c_begin = seg * sg.G, c_end = min(g.nc, c_begin + sg.G);
@@ -142,8 +167,7 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
   // ---- S_ref (bf16/fp32 operand copy)
   for (int idx = tid; idx < D * D; idx += kSegThreads) sm.sref[idx / D][idx % D] = from_f32<T>(a.S_ref[sb + idx]);
 
-  // ---- state registers on waves 4..7: wave w owns row tile (w - 4) (and w, for D = 32, none beyond NTD)
-  constexpr int NSW = 4;   // state waves
+  // ---- state registers on waves 4..7: wave w owns row tile (w - 4) (for D = 32 only waves 4, 5)
   const bool state_wave = wave >= 4;
   const int mt = wave - 4;                        // row tile owned
   const bool owns = state_wave && mt < NTD;
@@ -159,7 +183,8 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
 #pragma unroll
     for (int r = 0; r < 4; ++r) Sraw[n][r] = 0.f;
 
-  if constexpr (REWALK) {
+  if constexpr (!AGG) {
+    // segment-start state (written by the segment scan)
     if (owns) {
       const float* ss = seg_states + ((size_t)bh * sg.nseg + seg) * 2 * D * D;
 #pragma unroll
@@ -169,53 +194,10 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
           const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
           Sr[n][r] = ss[(size_t)i * D + k];
           Zr[n][r] = ss[(size_t)D * D + (size_t)i * D + k];
-        }
-    }
-  }
-  if constexpr (FULL) {
-    if (owns) {
-      // start from (S0, Z0) and fold the aggregates of segments 0 .. seg-1
-#pragma unroll
-      for (int n = 0; n < NTD; ++n)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
-          Sr[n][r] = a.S0[sb + (size_t)i * D + k];
-          Zr[n][r] = (g.momentum && a.Z0) ? a.Z0[sb + (size_t)i * D + k] : 0.f;
-        }
-      for (int js = 0; js < seg; ++js) {
-        const float* ag = agg + ((size_t)bh * sg.nseg + js) * sg.agg_stride;
-        const float ta = ag[2 * D * D], tk = ag[2 * D * D + 1], tbb = ag[2 * D * D + 2];
-#pragma unroll
-        for (int n = 0; n < NTD; ++n)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
-            const float U = ag[(size_t)i * D + k], V = ag[(size_t)D * D + (size_t)i * D + k];
-            const float s = Sr[n][r];
-            Sr[n][r] = ta * s - tk * Zr[n][r] + U;
-            Zr[n][r] = g.momentum ? tbb * Zr[n][r] + V : 0.f;
+          if constexpr (FULL) {
+            sm.Sb[i][k] = from_f32<T>(Sr[n][r]);
+            sm.Zb[i][k] = from_f32<T>(Zr[n][r]);
           }
-      }
-      // save the segment-start state for the backward pass
-      if (seg_states) {
-        float* ss = seg_states + ((size_t)bh * sg.nseg + seg) * 2 * D * D;
-#pragma unroll
-        for (int n = 0; n < NTD; ++n)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
-            ss[(size_t)i * D + k] = Sr[n][r];
-            ss[(size_t)D * D + (size_t)i * D + k] = Zr[n][r];
-          }
-      }
-#pragma unroll
-      for (int n = 0; n < NTD; ++n)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
-          sm.Sb[i][k] = from_f32<T>(Sr[n][r]);
-          sm.Zb[i][k] = from_f32<T>(Zr[n][r]);
         }
     }
   }
@@ -227,6 +209,11 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
   }
 
   for (int c = c_begin; c < c_end; ++c) {
+    // per-lane indices re-derived every chunk: keeps the compiler from hoisting every per-lane
+    // address out of the loop and holding (or spilling) them across the whole walk
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int t0 = c * g.Lc;
     const int t1 = min(g.T, t0 + g.Lc);
     const int L = t1 - t0;
@@ -253,40 +240,44 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
     }
 
     // ---- P1: G1 + G2 (waves 0-5) | coefficient recurrences (waves 6-7)
-    // G2 tile tt = wave + 6 j (j < 4) stays in registers kacc[j] until the Q epilogue.
-    const int nts = SP / 16;
-    const int n_g2 = FULL ? (CH / 16) * nts : 0;
-    f32x4 kacc[4];
+    // G1: delta[i][s] = (S_ref phi_s)[i] - v_s[i];  G2 (full walk): Kmat[tau][s] = psi_tau . phi_s,
+    // kept in registers (kacc) until the Q epilogue.
+    constexpr int NT1 = NTS * NTD, PER1 = (NT1 + 5) / 6;
+    constexpr int NT2 = FULL ? (CH / 16) * NTS : 0, PER2 = (NT2 + 5) / 6;
+    f32x4 kacc[PER2 > 0 ? PER2 : 1];
+    static_assert(!FULL || NT2 > 0, "G2 tiles");
     if (wave < 6) {
-      for (int tile = wave; tile < nts * NTD; tile += 6) {
+      // tile indices past the end are clamped (MFMAs stay unconditional, only the stores are guarded)
+#pragma unroll 1
+      for (int j = 0; j < PER1; ++j) {
+        const int tile = min(wave + 6 * j, NT1 - 1);
+        const bool valid = NT1 % 6 == 0 || wave + 6 * j < NT1;
         const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;   // m: sources, n: rows i
         f32x4 acc = zero4();
 #pragma unroll
         for (int k0 = 0; k0 < D; k0 += M::KS)
           acc = M::mma(frag_ld_row<T>(&sm.phi[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.sref[0][0], D + 8, n0, k0), acc);
-        const int i = n0 + (lane & 15);
+        if (valid) {
+          const int i = n0 + (lane & 15);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int s = m0 + 4 * (lane >> 4) + r;
-          const int p = t0 - H + s;
-          float d = 0.f;
-          if (s < H + L && p >= 0) d = acc[r] - to_f32(a.v[(tb + p) * D + i]);
-          sm.delta[i][s] = from_f32<T>(d);
+          for (int r = 0; r < 4; ++r) {
+            const int s = m0 + 4 * (lane >> 4) + r;
+            const int p = t0 - H + s;
+            const float d = (s < H + L && p >= 0) ? acc[r] - to_f32(sm.delta[i][s]) : 0.f;
+            sm.delta[i][s] = from_f32<T>(d);
+          }
         }
       }
       if constexpr (FULL) {
+#pragma unroll 1
+        for (int j = 0; j < PER2; ++j) {
+          const int tt = min(wave + 6 * j, NT2 - 1);
+          const int m0 = (tt / NTS) * 16, n0 = (tt % NTS) * 16;
+          f32x4 acc = zero4();
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int tt = wave + 6 * j;
-          kacc[j] = zero4();
-          if (tt < n_g2) {
-            const int m0 = (tt / nts) * 16, n0 = (tt % nts) * 16;
-            f32x4 acc = zero4();
-#pragma unroll
-            for (int k0 = 0; k0 < D; k0 += M::KS)
-              acc = M::mma(frag_ld_row<T>(&sm.psi[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.phi[0][0], D + 8, n0, k0), acc);
-            kacc[j] = acc;
-          }
+          for (int k0 = 0; k0 < D; k0 += M::KS)
+            acc = M::mma(frag_ld_row<T>(&sm.psi[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.phi[0][0], D + 8, n0, k0), acc);
+          kacc[j] = acc;
         }
       }
     } else {
@@ -297,11 +288,11 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
     // ---- P2: Q epilogue (waves 0-5), scaled phi^T for G4 (all)
     if constexpr (FULL) {
       if (wave < 6) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
+#pragma unroll 1
+        for (int j = 0; j < PER2; ++j) {
           const int tt = wave + 6 * j;
-          if (tt < n_g2) {
-            const int m0 = (tt / nts) * 16, n0 = (tt % nts) * 16;
+          if (NT2 % 6 == 0 || tt < NT2) {
+            const int m0 = (tt / NTS) * 16, n0 = (tt % NTS) * 16;
             const int s = n0 + (lane & 15);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -312,65 +303,84 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
         }
       }
     }
-    for (int idx = tid; idx < SP * D; idx += kSegThreads) {
-      const int s = idx / D, k = idx % D;
-      const float x = to_f32(sm.phi[s][k]);
-      sm.phiTs[k][s] = from_f32<T>(sm.sc.wsend[s] * x);
-      sm.phiTz[k][s] = from_f32<T>(sm.sc.wzend[s] * x);
+    {
+      // consecutive lanes take consecutive sources: conflict-free transposed stores
+      constexpr int NPT = (SPM * D + kSegThreads - 1) / kSegThreads;
+#pragma unroll
+      for (int j = 0; j < NPT; ++j) {
+        const int idx = tid + j * kSegThreads;
+        const int s = idx % SPM, k = idx / SPM;
+        if (k < D) {
+          const float x = to_f32(sm.phi[s][k]);
+          sm.phiTs[k][s] = from_f32<T>(sm.sc.wsend[s] * x);
+          sm.phiTz[k][s] = from_f32<T>(sm.sc.wzend[s] * x);
+        }
+      }
     }
     __syncthreads();
 
     // ---- P3: G3 (waves 0-3, full walk) | G4 + state update (waves 4-7)
     if (FULL && wave < 4) {
-      for (int tile = wave; tile < (CH / 16) * NTD; tile += 4) {
-        const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;   // m: tau, n: rows i
-        f32x4 aq = zero4(), as = zero4(), az = zero4();
-        for (int k0 = 0; k0 < SP; k0 += M::KS)
-          aq = M::mma(frag_ld_row<T>(&sm.Q[0][0], SPM + 8, m0, k0), frag_ld_row<T>(&sm.delta[0][0], SPM + 8, n0, k0), aq);
+      constexpr int NT3 = (CH / 16) * NTD, PER3 = (NT3 + 3) / 4;
+      static_assert(!FULL || NT3 % 4 == 0, "G3 tiles split evenly over 4 waves");
+#pragma unroll 1
+      for (int j = 0; j < PER3; ++j) {
+        const int tile = wave + 4 * j;
+        {
+          const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;   // m: tau, n: rows i
+          f32x4 aq = zero4(), as = zero4(), az = zero4();
 #pragma unroll
-        for (int k0 = 0; k0 < D; k0 += M::KS) {
-          const typename M::frag fa = frag_ld_row<T>(&sm.psi[0][0], D + 8, m0, k0);
-          as = M::mma(fa, frag_ld_row<T>(&sm.Sb[0][0], D + 8, n0, k0), as);
-          az = M::mma(fa, frag_ld_row<T>(&sm.Zb[0][0], D + 8, n0, k0), az);
-        }
-        f32x4 yv;
+          for (int k0 = 0; k0 < SPM; k0 += M::KS)
+            aq = M::mma(frag_ld_row<T>(&sm.Q[0][0], SPM + 8, m0, k0), frag_ld_row<T>(&sm.delta[0][0], SPM + 8, n0, k0), aq);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = m0 + 4 * (lane >> 4) + r;
-          yv[r] = -aq[r] + sm.sc.acoef[t] * as[r] - sm.sc.kcoef[t] * az[r];
-        }
-        if (bufchunk) {
-          for (int s = 0; s < H; ++s) {
-            const float* Bs = a.buf_in + ((size_t)bh * H + s) * D * D;
-            f32x4 ab = zero4();
+          for (int k0 = 0; k0 < D; k0 += M::KS) {
+            const typename M::frag fa = frag_ld_row<T>(&sm.psi[0][0], D + 8, m0, k0);
+            as = M::mma(fa, frag_ld_row<T>(&sm.Sb[0][0], D + 8, n0, k0), as);
+            az = M::mma(fa, frag_ld_row<T>(&sm.Zb[0][0], D + 8, n0, k0), az);
+          }
+          f32x4 yv;
 #pragma unroll
-            for (int k0 = 0; k0 < D; k0 += M::KS)
-              ab = M::mma(frag_ld_row<T>(&sm.psi[0][0], D + 8, m0, k0), frag_ld<T>(Bs, D, 1, n0, k0), ab);
+          for (int r = 0; r < 4; ++r) {
+            const int t = m0 + 4 * (lane >> 4) + r;
+            yv[r] = -aq[r] + sm.sc.acoef[t] * as[r] - sm.sc.kcoef[t] * az[r];
+          }
+          if (bufchunk) {
+            for (int s = 0; s < H; ++s) {
+              const float* Bs = a.buf_in + ((size_t)bh * H + s) * D * D;
+              f32x4 ab = zero4();
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int t = m0 + 4 * (lane >> 4) + r;
-              yv[r] -= sm.wsh[t][s] * ab[r];
+              for (int k0 = 0; k0 < D; k0 += M::KS)
+                ab = M::mma(frag_ld_row<T>(&sm.psi[0][0], D + 8, m0, k0), frag_ld<T>(Bs, D, 1, n0, k0), ab);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int t = m0 + 4 * (lane >> 4) + r;
+                yv[r] -= sm.wsh[t][s] * ab[r];
+              }
             }
           }
-        }
-        const int i = n0 + (lane & 15);
+          const int i = n0 + (lane & 15);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = m0 + 4 * (lane >> 4) + r;
-          if (t < L) a.y[(tb + t0 + t) * D + i] = from_f32<T>(yv[r]);
+          for (int r = 0; r < 4; ++r) {
+            const int t = m0 + 4 * (lane >> 4) + r;
+            if (t < L) a.y[(tb + t0 + t) * D + i] = from_f32<T>(yv[r]);
+          }
         }
       }
     } else if (owns) {
       const float a_end = sm.sc.endc[0], k_end = sm.sc.endc[1], b_end = sm.sc.endc[2];
       const bool do_clamp = !AGG && clamp_after(g, t1);
+      const int m0 = mt * 16;
+      typename M::frag fa[SPM / M::KS];
 #pragma unroll
+      for (int kk = 0; kk < SPM / M::KS; ++kk) fa[kk] = frag_ld_row<T>(&sm.delta[0][0], SPM + 8, m0, kk * M::KS);
+#pragma unroll 1
       for (int n = 0; n < NTD; ++n) {
-        const int m0 = mt * 16, n0 = n * 16;
+        const int n0 = n * 16;
         f32x4 au = zero4(), av = zero4();
-        for (int k0 = 0; k0 < SP; k0 += M::KS) {
-          const typename M::frag fa = frag_ld_row<T>(&sm.delta[0][0], SPM + 8, m0, k0);
-          au = M::mma(fa, frag_ld_row<T>(&sm.phiTs[0][0], SPM + 8, n0, k0), au);
-          av = M::mma(fa, frag_ld_row<T>(&sm.phiTz[0][0], SPM + 8, n0, k0), av);
+#pragma unroll
+        for (int kk = 0; kk < SPM / M::KS; ++kk) {
+          au = M::mma(fa[kk], frag_ld_row<T>(&sm.phiTs[0][0], SPM + 8, n0, kk * M::KS), au);
+          av = M::mma(fa[kk], frag_ld_row<T>(&sm.phiTz[0][0], SPM + 8, n0, kk * M::KS), av);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {

@@ -6,9 +6,10 @@
 // so the work splits into two launches, both parallel over (segment, bh):
 //   k_fwd_seg_agg : walk the segment's chunks from a zero state -> segment aggregate
 //                   (a, kappa, b, U_seg, V_seg).
-//   k_fwd_seg     : fold the aggregates of the preceding segments into the segment-start state,
-//                   save it for the backward pass, then walk the chunks again with the true state,
-//                   producing y (and S_T, Z_T in the last segment).
+//   k_fwd_seg_scan: one thread per state element (i, k) of a row folds the aggregates in segment
+//                   order from (S0, Z0), writing every segment-start state (kept for the backward).
+//   k_fwd_seg     : walk the segment's chunks again from its start state, producing y (and S_T,
+//                   Z_T in the last segment).
 // With clamp_every > 0 the clamp at scan_chunk_len boundaries is not affine, so the caller uses a
 // single segment (an exact sequential walk over all chunks).
 //
@@ -35,11 +36,36 @@ __global__ __launch_bounds__(kSegThreads) void k_fwd_seg_agg(const Geom g, const
   fwd_segment<T, CH, D, WALK_AGG>(g, a, sg, agg, nullptr, nullptr, nullptr, smem_raw);
 }
 
+// grid (D * D / kThreads, BH): segment-start states  x_{j+1} = [[a_j, -kappa_j], [0, b_j]] x_j + [U_j; V_j]
+template <int D>
+__global__ __launch_bounds__(kThreads) void k_fwd_seg_scan(const Geom g, const float* S0, const float* Z0,
+                                                             const SegGeom sg, const float* agg, float* seg_states) {
+  const int bh = blockIdx.y;
+  const int idx = blockIdx.x * kThreads + threadIdx.x;
+  if (idx >= D * D) return;
+  float S = S0[(size_t)bh * D * D + idx];
+  float Z = (g.momentum && Z0) ? Z0[(size_t)bh * D * D + idx] : 0.f;
+  const float* ag = agg + (size_t)bh * sg.nseg * sg.agg_stride;
+  float* ss = seg_states + (size_t)bh * sg.nseg * 2 * D * D;
+  for (int js = 0; js < sg.nseg; ++js) {
+    ss[(size_t)js * 2 * D * D + idx] = S;
+    ss[(size_t)js * 2 * D * D + D * D + idx] = Z;
+    if (js + 1 < sg.nseg) {
+      const float* aj = ag + (size_t)js * sg.agg_stride;
+      const float ta = aj[2 * D * D], tk = aj[2 * D * D + 1], tbb = aj[2 * D * D + 2];
+      const float U = aj[idx], V = aj[D * D + idx];
+      const float Sn = ta * S - tk * Z + U;
+      Z = g.momentum ? tbb * Z + V : 0.f;
+      S = Sn;
+    }
+  }
+}
+
 template <typename T, int CH, int D>
 __global__ __launch_bounds__(kSegThreads) void k_fwd_seg(const Geom g, const FwdPtrs<T> a, const SegGeom sg,
-                                                           float* agg, float* seg_states, float* final_raw) {
+                                                           const float* seg_states, float* final_raw) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  fwd_segment<T, CH, D, WALK_FULL>(g, a, sg, agg, seg_states, nullptr, final_raw, smem_raw);
+  fwd_segment<T, CH, D, WALK_FULL>(g, a, sg, nullptr, seg_states, nullptr, final_raw, smem_raw);
 }
 
 template <typename T, int CH, int D>
@@ -56,13 +82,18 @@ hipError_t launch_fwd_seg(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg,
     prof_end(KID_FWD_SEG_AGG, stream);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
+  prof_begin(KID_FWD_SCAN, stream);
+  hipLaunchKernelGGL((k_fwd_seg_scan<D>), dim3((D * D + kThreads - 1) / kThreads, g.BH), dim3(kThreads), 0, stream,
+                     g, a.S0, a.Z0, sg, (const float*)agg, seg_states);
+  prof_end(KID_FWD_SCAN, stream);
+  if ((err = hipGetLastError()) != hipSuccess) return err;
   const size_t smem = sizeof(SegFwdSmem<T, CH, D, true>);
   err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_seg<T, CH, D>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (err != hipSuccess) return err;
   prof_begin(KID_FWD_WALK, stream);
-  hipLaunchKernelGGL((k_fwd_seg<T, CH, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, agg,
-                     seg_states, final_raw);
+  hipLaunchKernelGGL((k_fwd_seg<T, CH, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg,
+                     (const float*)seg_states, final_raw);
   prof_end(KID_FWD_WALK, stream);
   return hipGetLastError();
 }
