@@ -246,53 +246,73 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
       constexpr int NVS = (SPM * (D / 8) + kSegThreads - 1) / kSegThreads;
       constexpr int NVT = (CH * (D / 8) + kSegThreads - 1) / kSegThreads;
       constexpr int NWL = (CH * kMaxWindow + kSegThreads - 1) / kSegThreads;
+      // every load is unconditional from an in-bounds address; masks are applied when storing
+      const size_t r0 = tb + t0;
       Vec8<T> rk[NVS], rv[NVS], rq[NVT], rd[NVT];
+      unsigned okS = 0, okT = 0;
 #pragma unroll
       for (int j = 0; j < NVS; ++j) {
         const int idx = tid + j * kSegThreads;
         const int s = idx / (D / 8), c8 = idx % (D / 8);
         const int pp = t0 - H + s;
         const bool ok = s < SPM && s < H + L && pp >= 0;
-        rk[j] = ok ? vec8_load(a.k + (tb + pp) * D + c8 * 8) : Vec8<T>::zero();
-        rv[j] = ok ? vec8_load(a.v + (tb + pp) * D + c8 * 8) : Vec8<T>::zero();
+        const size_t row = ok ? tb + pp : r0;
+        rk[j] = vec8_load(a.k + row * D + c8 * 8);
+        rv[j] = vec8_load(a.v + row * D + c8 * 8);
+        okS |= (ok ? 1u : 0u) << j;
       }
+      const T* dyp = a.dy ? a.dy : a.q;
 #pragma unroll
       for (int j = 0; j < NVT; ++j) {
         const int idx = tid + j * kSegThreads;
         const int t = idx / (D / 8), c8 = idx % (D / 8);
         const bool ok = t < L;
-        rq[j] = ok ? vec8_load(a.q + (tb + t0 + t) * D + c8 * 8) : Vec8<T>::zero();
-        rd[j] = (ok && a.dy) ? vec8_load(a.dy + (tb + t0 + t) * D + c8 * 8) : Vec8<T>::zero();
+        const size_t row = ok ? r0 + t : r0;
+        rq[j] = vec8_load(a.q + row * D + c8 * 8);
+        rd[j] = vec8_load(dyp + row * D + c8 * 8);
+        okT |= ((ok ? 1u : 0u) << j);
       }
-      float r_al = 1.f, r_et = 0.f, r_be = 1.f, r_ug = 0.f;
-      if (tid < L) {
-        r_al = to_f32(a.decay[tb + t0 + tid]);
-        r_et = to_f32(a.lr[tb + t0 + tid]);
-        r_be = g.momentum ? to_f32(a.beta[tb + t0 + tid]) : 0.f;
-      }
-      if (g.gate_mode == GATE_TOKEN && tid < SPM) {
-        const int pp = t0 - H + tid;
-        r_ug = (tid < H + L) ? (pp >= 0 ? to_f32(a.gate[tb + pp]) : 1.f) : 0.f;
-      }
-      float r_wl[NWL];
+      const bool okt = tid < L;
+      const size_t rt = okt ? r0 + tid : r0;
+      const T x_al = a.decay[rt], x_et = a.lr[rt];
+      const T x_be = ((g.momentum && a.beta) ? a.beta : a.decay)[rt];
+      const T* gp = a.gate ? a.gate : a.decay;
+      const int pg = t0 - H + tid;
+      const bool okug = g.gate_mode == GATE_TOKEN && tid < SPM && tid < H + L && pg >= 0;
+      const bool padug = g.gate_mode == GATE_TOKEN && tid < SPM && tid < H + L && pg < 0;
+      const T x_ug = gp[okug ? tb + pg : r0];
+      T x_wl[NWL];
+      unsigned okW = 0;
 #pragma unroll
       for (int j = 0; j < NWL; ++j) {
         const int idx = tid + j * kSegThreads;
-        r_wl[j] = (g.gate_mode == GATE_LAG && idx < CH * e && idx / e < L) ? to_f32(a.gate[(tb + t0) * e + idx]) : 0.f;
+        const bool ok = g.gate_mode == GATE_LAG && idx < CH * e && idx / e < L;
+        x_wl[j] = gp[ok ? r0 * e + idx : r0];
+        okW |= (ok ? 1u : 0u) << j;
       }
       float s_in[NT2][4], z_in[NT2][4];
 #pragma unroll
       for (int j = 0; j < NT2; ++j) {
-        const int tile = wave + kSegWaves * j;
+        const int tile = min(wave + kSegWaves * j, NTD * NTD - 1);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          s_in[j][r] = 0.f; z_in[j][r] = 0.f;
-          if (tile < NTD * NTD) {
-            const int i = (tile / NTD) * 16 + 4 * (lane >> 4) + r, k = (tile % NTD) * 16 + (lane & 15);
-            s_in[j][r] = Sin_g[(size_t)i * D + k];
-            z_in[j][r] = g.momentum ? Zin_g[(size_t)i * D + k] : 0.f;
-          }
+          const int i = (tile / NTD) * 16 + 4 * (lane >> 4) + r, k = (tile % NTD) * 16 + (lane & 15);
+          s_in[j][r] = Sin_g[(size_t)i * D + k];
+          z_in[j][r] = Zin_g[(size_t)i * D + k];
         }
+      }
+      const float r_al = okt ? to_f32(x_al) : 1.f;
+      const float r_et = okt ? to_f32(x_et) : 0.f;
+      const float r_be = okt ? (g.momentum ? to_f32(x_be) : 0.f) : 1.f;
+      const float r_ug = okug ? to_f32(x_ug) : (padug ? 1.f : 0.f);
+      float r_wl[NWL];
+#pragma unroll
+      for (int j = 0; j < NWL; ++j) r_wl[j] = ((okW >> j) & 1u) ? to_f32(x_wl[j]) : 0.f;
+      if (!g.momentum) {
+#pragma unroll
+        for (int j = 0; j < NT2; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) z_in[j][r] = 0.f;
       }
       // LDS stores
 #pragma unroll
@@ -300,10 +320,11 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         const int idx = tid + j * kSegThreads;
         const int s = idx / (D / 8), c8 = idx % (D / 8);
         if (s < SPM) {
-          Vec8<T> x = rk[j];
+          const bool ok = (okS >> j) & 1u;
+          Vec8<T> x = ok ? rk[j] : Vec8<T>::zero();
           if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
           x.store(&sm.phi[s][c8 * 8]);
-          rv[j].store(&sm.deltaT[s][c8 * 8]);
+          (ok ? rv[j] : Vec8<T>::zero()).store(&sm.deltaT[s][c8 * 8]);
         }
       }
 #pragma unroll
@@ -311,10 +332,11 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         const int idx = tid + j * kSegThreads;
         const int t = idx / (D / 8), c8 = idx % (D / 8);
         if (t < CH) {
-          Vec8<T> x = rq[j];
+          const bool ok = (okT >> j) & 1u;
+          Vec8<T> x = ok ? rq[j] : Vec8<T>::zero();
           if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
           x.store(&sm.psi[t][c8 * 8]);
-          rd[j].store(&sm.dy[t][c8 * 8]);
+          ((ok && a.dy) ? rd[j] : Vec8<T>::zero()).store(&sm.dy[t][c8 * 8]);
         }
       }
       if (tid < CH) {

@@ -31,6 +31,10 @@ struct SegFwdSmem {
 };
 
 // Per-thread register prefetch of one chunk's inputs (issued one chunk ahead).
+// Every load is unconditional from an in-bounds address (out-of-range rows are redirected to the
+// chunk's first token, absent optional inputs to `decay`); the raw values are kept with validity
+// flags and only converted and masked in store(). A load under a condition whose value is
+// converted inside the same branch would make the wave wait for each load in turn.
 template <typename T, int CH, int D, bool FULL>
 struct ChunkPrefetch {
   static constexpr int SPM = CH + kHaloPad;
@@ -40,11 +44,15 @@ struct ChunkPrefetch {
   Vec8<T> phi[NV_PHI];
   Vec8<T> vv[NV_PHI];
   Vec8<T> psi[NV_PSI > 0 ? NV_PSI : 1];
-  float alpha, eta, beta, ug;
-  float wl[NWL];
+  T alpha, eta, beta, ug;
+  T wl[NWL];
+  unsigned ok_phi, ok_v, ok_psi, ok_wl;
+  bool ok_t, ok_ug, pad_ug;
 
   __device__ __forceinline__ void load(const Geom& g, const FwdPtrs<T>& a, size_t tb, int t0, int L) {
     const int tid = threadIdx.x, H = g.H;
+    const size_t r0 = tb + t0;                          // always a valid token row
+    ok_phi = 0; ok_v = 0; ok_psi = 0; ok_wl = 0;
 #pragma unroll
     for (int j = 0; j < NV_PHI; ++j) {
       const int v = tid + j * kSegThreads;
@@ -52,13 +60,15 @@ struct ChunkPrefetch {
         const int s = v / (D / 8), c8 = v % (D / 8);
         const int p = t0 - H + s;
         const bool ok = s < SPM && s < H + L && p >= 0;
-        phi[j] = ok ? vec8_load(a.k + (tb + p) * D + c8 * 8) : Vec8<T>::zero();
+        phi[j] = vec8_load(a.k + (ok ? tb + p : r0) * D + c8 * 8);
+        ok_phi |= (ok ? 1u : 0u) << j;
       }
       {   // v: consecutive lanes take consecutive sources (conflict-free transposed LDS store)
         const int s = v % SPM, c8 = v / SPM;
         const int p = t0 - H + s;
         const bool ok = c8 < D / 8 && s < H + L && p >= 0;
-        vv[j] = ok ? vec8_load(a.v + (tb + p) * D + c8 * 8) : Vec8<T>::zero();
+        vv[j] = vec8_load(a.v + (ok ? tb + p : r0) * D + (ok ? c8 * 8 : 0));
+        ok_v |= (ok ? 1u : 0u) << j;
       }
     }
     if constexpr (FULL) {
@@ -66,23 +76,30 @@ struct ChunkPrefetch {
       for (int j = 0; j < NV_PSI; ++j) {
         const int v = tid + j * kSegThreads;
         const int t = v / (D / 8), c8 = v % (D / 8);
-        psi[j] = (t < L) ? vec8_load(a.q + (tb + t0 + t) * D + c8 * 8) : Vec8<T>::zero();
+        const bool ok = t < L;
+        psi[j] = vec8_load(a.q + (ok ? r0 + t : r0) * D + c8 * 8);
+        ok_psi |= (ok ? 1u : 0u) << j;
       }
     }
-    alpha = 1.f; eta = 0.f; beta = 1.f; ug = 0.f;
-    if (tid < L) {
-      alpha = to_f32(a.decay[tb + t0 + tid]);
-      eta = to_f32(a.lr[tb + t0 + tid]);
-      beta = g.momentum ? to_f32(a.beta[tb + t0 + tid]) : 0.f;
-    }
-    if (g.gate_mode == GATE_TOKEN && tid < SPM) {
+    ok_t = tid < L;
+    const size_t rt = ok_t ? r0 + tid : r0;
+    alpha = a.decay[rt];
+    eta = a.lr[rt];
+    const T* bp = (g.momentum && a.beta) ? a.beta : a.decay;
+    beta = bp[rt];
+    const T* gp = a.gate ? a.gate : a.decay;
+    {
       const int p = t0 - H + tid;
-      ug = (tid < H + L) ? (p >= 0 ? to_f32(a.gate[tb + p]) : 1.f) : 0.f;
+      ok_ug = g.gate_mode == GATE_TOKEN && tid < SPM && tid < H + L && p >= 0;
+      pad_ug = g.gate_mode == GATE_TOKEN && tid < SPM && tid < H + L && p < 0;
+      ug = gp[ok_ug ? tb + p : r0];
     }
 #pragma unroll
     for (int j = 0; j < NWL; ++j) {
       const int idx = tid + j * kSegThreads;
-      wl[j] = (g.gate_mode == GATE_LAG && idx < CH * g.e && idx / g.e < L) ? to_f32(a.gate[(tb + t0) * g.e + idx]) : 0.f;
+      const bool ok = g.gate_mode == GATE_LAG && idx < CH * g.e && idx / g.e < L;
+      wl[j] = gp[ok ? r0 * g.e + idx : r0];
+      ok_wl |= (ok ? 1u : 0u) << j;
     }
   }
 
@@ -95,7 +112,7 @@ struct ChunkPrefetch {
       {
         const int s = v / (D / 8), c8 = v % (D / 8);
         if (s < SPM) {
-          Vec8<T> x = phi[j];
+          Vec8<T> x = ((ok_phi >> j) & 1u) ? phi[j] : Vec8<T>::zero();
           if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
           x.store(&sm.phi[s][c8 * 8]);
         }
@@ -103,8 +120,9 @@ struct ChunkPrefetch {
       {
         const int s = v % SPM, c8 = v / SPM;
         if (c8 < D / 8) {
+          const Vec8<T> x = ((ok_v >> j) & 1u) ? vv[j] : Vec8<T>::zero();
 #pragma unroll
-          for (int e = 0; e < 8; ++e) sm.delta[c8 * 8 + e][s] = vv[j].v[e];
+          for (int e = 0; e < 8; ++e) sm.delta[c8 * 8 + e][s] = x.v[e];
         }
       }
     }
@@ -114,19 +132,23 @@ struct ChunkPrefetch {
         const int v = tid + j * kSegThreads;
         const int t = v / (D / 8), c8 = v % (D / 8);
         if (t < CH) {
-          Vec8<T> x = psi[j];
+          Vec8<T> x = ((ok_psi >> j) & 1u) ? psi[j] : Vec8<T>::zero();
           if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
           x.store(&sm.psi[t][c8 * 8]);
         }
       }
     }
-    if (tid < CH) { sm.sc.alpha[tid] = alpha; sm.sc.eta[tid] = eta; sm.sc.beta[tid] = beta; }
-    if (g.gate_mode == GATE_TOKEN && tid < SPM) sm.sc.ug[tid] = ug;
+    if (tid < CH) {
+      sm.sc.alpha[tid] = ok_t ? to_f32(alpha) : 1.f;
+      sm.sc.eta[tid] = ok_t ? to_f32(eta) : 0.f;
+      sm.sc.beta[tid] = ok_t ? (g.momentum ? to_f32(beta) : 0.f) : 1.f;
+    }
+    if (g.gate_mode == GATE_TOKEN && tid < SPM) sm.sc.ug[tid] = ok_ug ? to_f32(ug) : (pad_ug ? 1.f : 0.f);
     if (g.gate_mode == GATE_LAG) {
 #pragma unroll
       for (int j = 0; j < NWL; ++j) {
         const int idx = tid + j * kSegThreads;
-        if (idx < CH * g.e) sm.sc.wl[idx] = wl[j];
+        if (idx < CH * g.e) sm.sc.wl[idx] = ((ok_wl >> j) & 1u) ? to_f32(wl[j]) : 0.f;
       }
     }
   }
