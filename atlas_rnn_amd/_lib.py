@@ -45,7 +45,7 @@ EXPORTED_SYMBOLS = (
     "atlas_mem_mfma_selftest",
 )
 
-NKERNELS = 9
+NKERNELS = 11
 
 
 class Problem(ctypes.Structure):

@@ -13,7 +13,8 @@
 
 namespace atlas {
 template <typename T, int CH, int D>
-hipError_t launch_fwd_seg(const Geom&, const FwdPtrs<T>&, const SegGeom&, float*, float*, float*, hipStream_t);
+hipError_t launch_fwd_seg(const Geom&, const FwdPtrs<T>&, const SegGeom&, float*, float*, float*, float*, T*,
+                          hipStream_t);
 template <typename T, int CH, int D>
 hipError_t launch_bwd_seg(const Geom&, const BwdPtrs<T>&, const SegGeom&, const BwdSegPtrs&, hipStream_t);
 template <typename T, int DK, int DV> hipError_t launch_buffer_out(const Geom&, const FwdPtrs<T>&, hipStream_t);
@@ -71,7 +72,7 @@ struct Profiler {
 Profiler& prof() { static Profiler p; return p; }
 const char* kKernelNames[KID_COUNT] = {"k_fwd_seg_agg", "k_fwd_seg", "k_buffer_out", "k_bwd_seg_agg",
                                        "k_bwd_seg", "k_bwd_seg_fixup", "k_seg_reduce_dsref", "k_fwd_seg_scan",
-                                       "k_bwd_seg_scan"};
+                                       "k_bwd_seg_scan", "k_chunk_coef_fwd", "k_chunk_coef_bwd"};
 }  // namespace
 
 namespace atlas {
@@ -105,7 +106,9 @@ struct Plan {
   SegGeom sg;
   Geom gb;     // backward chunks (Lb <= 32 bf16, 16 fp32; Lb divides Lc)
   SegGeom sgb;
-  int CH;
+  int CH;      // forward chunk capacity (kernel template), 64 bf16 / 32 fp32
+  int CHB;     // backward chunk capacity, 32 bf16 / 16 fp32
+  int esize;   // bytes per input element
   bool ok;
   int status;
 };
@@ -179,6 +182,8 @@ Plan make_plan(const atlas_mem_problem* p) {
   pl.sgb = pl.sg;
   pl.sgb.G = pl.sg.G * (Lc / Lb);
   pl.CH = CH;
+  pl.CHB = bwd_chunk_cap(p->dtype);
+  pl.esize = p->dtype == ATLAS_DT_BF16 ? 2 : 4;
   pl.ok = true;
   pl.status = ATLAS_MEM_OK;
   return pl;
@@ -188,8 +193,11 @@ size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // `saved` layout: segment-start states, segment aggregates (forward scratch), raw S_{T-1}.
 struct SavedLayout {
-  size_t seg, agg, final_raw, total;
+  size_t seg, agg, final_raw, coef, wsh, total;
 };
+
+// floats per chunk coefficient record (acoef, kcoef, endc, wsend, wzend) for chunk capacity ch
+size_t coef_rec_floats(int ch) { return (size_t)2 * ch + 4 + 2 * (ch + kHaloPad); }
 
 SavedLayout saved_layout(const Plan& pl) {
   const Geom& g = pl.g;
@@ -199,6 +207,9 @@ SavedLayout saved_layout(const Plan& pl) {
   L.seg = off; off += align256((size_t)g.BH * pl.sg.nseg * 2 * st);
   L.agg = off; off += align256((size_t)g.BH * pl.sg.nseg * pl.sg.agg_stride * sizeof(float));
   L.final_raw = off; off += align256((size_t)g.BH * st);
+  // forward scratch: per-chunk coefficient records and Ws[s, t-1] blocks
+  L.coef = off; off += align256((size_t)g.BH * g.nc * coef_rec_floats(pl.CH) * sizeof(float));
+  L.wsh = off; off += align256((size_t)g.BH * g.nc * pl.CH * (pl.CH + kHaloPad) * pl.esize);
   L.total = off;
   return L;
 }
@@ -206,7 +217,7 @@ SavedLayout saved_layout(const Plan& pl) {
 // backward workspace: adjoint aggregates, re-walk chunk states, dS_ref partials, boundary partials,
 // token-gate (target, lag) gradients.
 struct BwdLayout {
-  size_t agg, segadj, rw, dsref, tail, halo, dw, total;
+  size_t agg, segadj, rw, dsref, tail, halo, dw, coef, wsh, total;
 };
 
 BwdLayout bwd_layout(const Plan& pl) {
@@ -222,6 +233,8 @@ BwdLayout bwd_layout(const Plan& pl) {
   L.tail = off; off += align256((size_t)g.BH * nseg * g.H * (g.DV + g.DK) * sizeof(float));
   L.halo = off; off += align256((size_t)g.BH * nseg * g.H * (g.DV + g.DK) * sizeof(float));
   L.dw = off; off += align256(g.gate_mode == ATLAS_GATE_TOKEN ? (size_t)g.BH * g.T * g.e * sizeof(float) : 0);
+  L.coef = off; off += align256((size_t)g.BH * g.nc * coef_rec_floats(pl.CHB) * sizeof(float));
+  L.wsh = off; off += align256((size_t)g.BH * g.nc * pl.CHB * (pl.CHB + kHaloPad) * pl.esize);
   L.total = off;
   return L;
 }
@@ -240,15 +253,17 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
   float* seg_states = reinterpret_cast<float*>(sv + SL.seg);
   float* agg = reinterpret_cast<float*>(sv + SL.agg);
   float* final_raw = reinterpret_cast<float*>(sv + SL.final_raw);
+  float* coef = reinterpret_cast<float*>(sv + SL.coef);
+  T* wsh = reinterpret_cast<T*>(sv + SL.wsh);
   const Geom& g = pl.g;
   hipError_t err = hipErrorInvalidValue;
   if (g.DK == 64) {
-    if constexpr (sizeof(T) == 2) err = launch_fwd_seg<T, 64, 64>(g, a, pl.sg, agg, seg_states, final_raw, s);
-    else err = launch_fwd_seg<T, 32, 64>(g, a, pl.sg, agg, seg_states, final_raw, s);
+    if constexpr (sizeof(T) == 2) err = launch_fwd_seg<T, 64, 64>(g, a, pl.sg, agg, seg_states, final_raw, coef, wsh, s);
+    else err = launch_fwd_seg<T, 32, 64>(g, a, pl.sg, agg, seg_states, final_raw, coef, wsh, s);
     if (err == hipSuccess) err = launch_buffer_out<T, 64, 64>(g, a, s);
   } else if (g.DK == 32) {
-    if constexpr (sizeof(T) == 2) err = launch_fwd_seg<T, 64, 32>(g, a, pl.sg, agg, seg_states, final_raw, s);
-    else err = launch_fwd_seg<T, 32, 32>(g, a, pl.sg, agg, seg_states, final_raw, s);
+    if constexpr (sizeof(T) == 2) err = launch_fwd_seg<T, 64, 32>(g, a, pl.sg, agg, seg_states, final_raw, coef, wsh, s);
+    else err = launch_fwd_seg<T, 32, 32>(g, a, pl.sg, agg, seg_states, final_raw, coef, wsh, s);
     if (err == hipSuccess) err = launch_buffer_out<T, 32, 32>(g, a, s);
   }
   return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
@@ -279,6 +294,8 @@ int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, voi
   p.tail_part = gb.H > 0 ? reinterpret_cast<float*>(w + L.tail) : nullptr;
   p.halo_part = gb.H > 0 ? reinterpret_cast<float*>(w + L.halo) : nullptr;
   p.dw = gb.gate_mode == ATLAS_GATE_TOKEN ? reinterpret_cast<float*>(w + L.dw) : nullptr;
+  p.coef = reinterpret_cast<float*>(w + L.coef);
+  p.wsh = w + L.wsh;
   hipError_t err = hipErrorInvalidValue;
   if (gb.DK == 64) {
     if constexpr (sizeof(T) == 2) err = launch_bwd_seg<T, 32, 64>(gb, a, pl.sgb, p, s);

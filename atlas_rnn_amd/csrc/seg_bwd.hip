@@ -23,6 +23,9 @@
 
 namespace atlas {
 
+template <typename T, int CH>
+hipError_t launch_chunk_coef(const Geom& g, const T* decay, const T* lr, const T* beta, const T* gate, float* rec,
+                             T* wsh, int kid, hipStream_t stream);
 
 // ---------------------------------------------------------------------------------------------
 // adjoint aggregates
@@ -66,20 +69,10 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg_agg(const Geom g, const
       sm.psiT[k][t] = from_f32<T>(ps);
       sm.dyT[k][t] = from_f32<T>(dv);
     }
-    if (tid < CH) {
-      const bool in = tid < L;
-      sm.sc.alpha[tid] = in ? to_f32(a.decay[tb + t0 + tid]) : 1.f;
-      sm.sc.eta[tid] = in ? to_f32(a.lr[tb + t0 + tid]) : 0.f;
-      sm.sc.beta[tid] = in ? (g.momentum ? to_f32(a.beta[tb + t0 + tid]) : 0.f) : 1.f;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      float ac = 1.f, kc = 0.f, bc = 1.f;
-      for (int t = 0; t < CH; ++t) {
-        sm.sc.acoef[t] = ac; sm.sc.kcoef[t] = kc;
-        bc = sm.sc.beta[t] * bc; ac = sm.sc.alpha[t] * ac; kc = sm.sc.alpha[t] * kc + sm.sc.eta[t] * bc;
-      }
-      sm.sc.endc[0] = ac; sm.sc.endc[1] = kc; sm.sc.endc[2] = bc;
+    {   // a_{t-1}, kappa_{t-1} and the chunk transition from the chunk's coefficient record
+      constexpr int REC4 = CoefRec<CH>::SIZE / 4;
+      const float4* rc = reinterpret_cast<const float4*>(p.coef + ((size_t)bh * g.nc + c) * CoefRec<CH>::SIZE);
+      if (tid < REC4) reinterpret_cast<float4*>(&sm.sc.acoef[0])[tid] = rc[tid];
     }
     __syncthreads();
     const float ae = sm.sc.endc[0], ke = sm.sc.endc[1], be = sm.sc.endc[2];
@@ -214,7 +207,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
     fa.k = a.k; fa.q = a.q; fa.v = a.v; fa.lr = a.lr; fa.decay = a.decay; fa.beta = a.beta; fa.gate = a.gate;
     fa.S_ref = a.S_ref; fa.S0 = a.S0; fa.Z0 = a.Z0; fa.buf_in = a.buf_in;
     fa.y = nullptr; fa.S_T = nullptr; fa.Z_T = nullptr; fa.buf_out = nullptr;
-    fwd_segment<T, CH, D, WALK_REWALK>(g, fa, sg, nullptr, const_cast<float*>(p.seg_states), rw, nullptr, smem_raw);
+    fwd_segment<T, CH, D, WALK_REWALK>(g, fa, sg, nullptr, p.seg_states, rw, nullptr, p.coef, nullptr, smem_raw);
   }
   __syncthreads();
 
@@ -290,6 +283,17 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         x_wl[j] = gp[ok ? r0 * e + idx : r0];
         okW |= (ok ? 1u : 0u) << j;
       }
+      // chunk coefficient record and Ws[s, t-1] block (k_chunk_coef)
+      constexpr int REC4 = CoefRec<CH>::SIZE / 4;
+      constexpr int NV_WSH = (CH * SPM / 8 + kSegThreads - 1) / kSegThreads;
+      const float4 rec4 = reinterpret_cast<const float4*>(p.coef + ((size_t)bh * g.nc + c) * CoefRec<CH>::SIZE)[tid < REC4 ? tid : 0];
+      const T* wsh_c = reinterpret_cast<const T*>(p.wsh) + ((size_t)bh * g.nc + c) * CH * SPM;
+      Vec8<T> wsv[NV_WSH];
+#pragma unroll
+      for (int j = 0; j < NV_WSH; ++j) {
+        const int v = tid + j * kSegThreads;
+        wsv[j] = vec8_load(wsh_c + (size_t)(v < CH * SPM / 8 ? v : 0) * 8);
+      }
       float s_in[NT2][4], z_in[NT2][4];
 #pragma unroll
       for (int j = 0; j < NT2; ++j) {
@@ -321,10 +325,10 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         const int s = idx / (D / 8), c8 = idx % (D / 8);
         if (s < SPM) {
           const bool ok = (okS >> j) & 1u;
-          Vec8<T> x = ok ? rk[j] : Vec8<T>::zero();
+          Vec8<T> x = rk[j].masked(ok);
           if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
           x.store(&sm.phi[s][c8 * 8]);
-          (ok ? rv[j] : Vec8<T>::zero()).store(&sm.deltaT[s][c8 * 8]);
+          rv[j].masked(ok).store(&sm.deltaT[s][c8 * 8]);
         }
       }
 #pragma unroll
@@ -333,11 +337,17 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         const int t = idx / (D / 8), c8 = idx % (D / 8);
         if (t < CH) {
           const bool ok = (okT >> j) & 1u;
-          Vec8<T> x = ok ? rq[j] : Vec8<T>::zero();
+          Vec8<T> x = rq[j].masked(ok);
           if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
           x.store(&sm.psi[t][c8 * 8]);
-          ((ok && a.dy) ? rd[j] : Vec8<T>::zero()).store(&sm.dy[t][c8 * 8]);
+          rd[j].masked(ok && a.dy).store(&sm.dy[t][c8 * 8]);
         }
+      }
+      if (tid < REC4) reinterpret_cast<float4*>(&sm.sc.acoef[0])[tid] = rec4;
+#pragma unroll
+      for (int j = 0; j < NV_WSH; ++j) {
+        const int v = tid + j * kSegThreads;
+        if (v < CH * SPM / 8) wsv[j].store(&sm.wsh[(v * 8) / SPM][(v * 8) % SPM]);
       }
       if (tid < CH) {
         sm.sc.alpha[tid] = r_al; sm.sc.eta[tid] = r_et; sm.sc.beta[tid] = r_be;
@@ -405,15 +415,15 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
       }
     }
 
-    // ---- phase A: G1 delta^T (waves 0-5) | coefficients (waves 6-7)
+    // ---- phase A: G1 delta^T (waves 0-6) | decay table columns (wave 7)
     // Tile indices past the end of a tile list are clamped: the MFMAs stay unconditional and only
     // the stores are guarded.
-    if (wave < 6) {
-      constexpr int NT1 = NTS * NTD, PER1 = (NT1 + 5) / 6;
+    if (wave < 7) {
+      constexpr int NT1 = NTS * NTD, PER1 = (NT1 + 6) / 7;
 #pragma unroll 1
       for (int j = 0; j < PER1; ++j) {
-        const int tile = min(wave + 6 * j, NT1 - 1);
-        const bool valid = NT1 % 6 == 0 || wave + 6 * j < NT1;
+        const int tile = min(wave + 7 * j, NT1 - 1);
+        const bool valid = NT1 % 7 == 0 || wave + 7 * j < NT1;
         const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
         f32x4 acc = zero4();
 #pragma unroll
@@ -430,15 +440,8 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
           }
         }
       }
-    } else {
-      // ci < SPM (<= 64): per-source recurrences (Ws[s, tau-1] -> wsh, end values);
-      // ci = 64 .. 64 + CH: the columns of the decay tables (and a, kappa, b).
-      const int ci = tid - 6 * kWave;
-      if (ci < 64) {
-        chunk_coefficients<CH, true, false, T>(g, sm.sc, L, ci, &sm.wsh[0][0], SPM + 8);
-      } else if (ci <= 64 + CH) {
-        decay_column<CH>(sm.tab, sm.sc, ci - 64, sm.A1, sm.K1, sm.B1);
-      }
+    } else if (lane <= CH) {
+      decay_column<CH>(sm.tab, sm.sc, lane, sm.A1, sm.K1, sm.B1);
     }
     __syncthreads();
     // G2 / G3: Kmat = psi phi^T, K3 = dy delta -> Q^T, Q', Q'^T, Lm
@@ -971,7 +974,9 @@ size_t bwd_seg_smem_bytes(int H) {
 template <typename T, int CH, int D>
 hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg, const BwdSegPtrs& p,
                           hipStream_t stream) {
-  hipError_t err;
+  hipError_t err = launch_chunk_coef<T, CH>(g, a.decay, a.lr, a.beta, a.gate, p.coef, reinterpret_cast<T*>(p.wsh),
+                                            KID_BWD_COEF, stream);
+  if (err != hipSuccess) return err;
   if (sg.nseg > 1) {
     const size_t smem = sizeof(BwdAggSmem<T, CH, D>);
     err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bwd_seg_agg<T, CH, D>),

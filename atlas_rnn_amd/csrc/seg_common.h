@@ -26,6 +26,8 @@ struct BwdSegPtrs {
   float* tail_part;          // [BH][nseg][H][2D]  (dv | dphi) partial of a segment's last H tokens
   float* halo_part;          // [BH][nseg][H][2D]  partial from the segment's first chunk for the previous segment
   float* dw;                 // [BH][T][e] per (target, lag) gradients (token gates)
+  float* coef;               // [BH][nc][CoefRec] chunk coefficient records (k_chunk_coef)
+  void* wsh;                 // [BH][nc][CH][SPM] Ws[s, t-1] of every chunk (input element type)
 };
 
 // Eight consecutive elements: one 16-byte (bf16) or two 16-byte (fp32) vector accesses.
@@ -42,6 +44,16 @@ struct Vec8 {
     Vec8 r;
 #pragma unroll
     for (int e = 0; e < 8; ++e) r.v[e] = static_cast<T>(poly_map(to_f32(v[e]), deg));
+    return r;
+  }
+  // this vector if ok, zeros otherwise (word-wise selects, no aggregate temporaries)
+  __device__ __forceinline__ Vec8 masked(bool ok) const {
+    Vec8 r;
+    constexpr int NW = sizeof(v) / 4;
+    const unsigned* src = reinterpret_cast<const unsigned*>(v);
+    unsigned* dst = reinterpret_cast<unsigned*>(r.v);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) dst[w] = ok ? src[w] : 0u;
     return r;
   }
   __device__ __forceinline__ void store(T* p) const {
@@ -73,9 +85,20 @@ struct ChunkScalars {
   float alpha[CH], eta[CH], beta[CH];   // padded targets: alpha = beta = 1, eta = 0
   float ug[SPM];                        // token-mode gate of each source
   float wl[CH * kMaxWindow];            // lag-mode weights [tau][j]
-  float wsend[SPM], wzend[SPM];         // Ws[s, end], Wz[s, end]
-  float acoef[CH], kcoef[CH];           // a_{tau-1}, kappa_{tau-1}
+  // the coefficient record (same order as CoefRec, one contiguous 16-byte aligned block)
+  alignas(16) float acoef[CH];          // a_{tau-1}
+  float kcoef[CH];                      // kappa_{tau-1}
   float endc[4];                        // a_end, kappa_end, b_end
+  float wsend[SPM], wzend[SPM];         // Ws[s, end], Wz[s, end]
+};
+
+// Per-chunk coefficient record in HBM (fp32), written by k_chunk_coef for every chunk of every row:
+// acoef[CH], kcoef[CH], endc[4], wsend[SPM], wzend[SPM] - the layout of ChunkScalars from acoef on.
+template <int CH>
+struct CoefRec {
+  static constexpr int SPM = CH + kHaloPad;
+  static constexpr int SIZE = 2 * CH + 4 + 2 * SPM;   // floats
+  static_assert(SIZE % 4 == 0, "record copied as float4");
 };
 
 // Decay tables of one chunk, stored [c][t] with source column c = t' + 1 (column 0 is the chunk

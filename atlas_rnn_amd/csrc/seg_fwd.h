@@ -27,7 +27,7 @@ struct SegFwdSmem {
   T Q[FULL ? CH : 1][SPM + 8];
   T Sb[FULL ? D : 1][D + 8];
   T Zb[FULL ? D : 1][D + 8];
-  float wsh[FULL ? CH : 1][SPM + 1];   // Ws[s, tau-1]
+  T wsh[FULL ? CH : 1][SPM + 8];       // Ws[s, tau-1]
 };
 
 // Per-thread register prefetch of one chunk's inputs (issued one chunk ahead).
@@ -41,18 +41,36 @@ struct ChunkPrefetch {
   static constexpr int NV_PHI = (SPM * D / 8 + kSegThreads - 1) / kSegThreads;
   static constexpr int NV_PSI = FULL ? (CH * D / 8 + kSegThreads - 1) / kSegThreads : 0;
   static constexpr int NWL = (CH * kMaxWindow + kSegThreads - 1) / kSegThreads;
+  static constexpr int REC4 = CoefRec<CH>::SIZE / 4;
+  static constexpr int NV_WSH = FULL ? (CH * SPM / 8 + kSegThreads - 1) / kSegThreads : 0;
+  static_assert(REC4 <= kSegThreads && SPM % 8 == 0, "record / wsh prefetch");
   Vec8<T> phi[NV_PHI];
   Vec8<T> vv[NV_PHI];
   Vec8<T> psi[NV_PSI > 0 ? NV_PSI : 1];
+  Vec8<T> wsv[NV_WSH > 0 ? NV_WSH : 1];
+  float rc0, rc1, rc2, rc3;   // this thread's float4 of the coefficient record
   T alpha, eta, beta, ug;
   T wl[NWL];
   unsigned ok_phi, ok_v, ok_psi, ok_wl;
   bool ok_t, ok_ug, pad_ug;
 
-  __device__ __forceinline__ void load(const Geom& g, const FwdPtrs<T>& a, size_t tb, int t0, int L) {
+  // rec_c / wsh_c: this chunk's coefficient record and Ws[s, t-1] block (k_chunk_coef)
+  __device__ __forceinline__ void load(const Geom& g, const FwdPtrs<T>& a, size_t tb, int t0, int L,
+                                       const float* rec_c, const T* wsh_c) {
     const int tid = threadIdx.x, H = g.H;
     const size_t r0 = tb + t0;                          // always a valid token row
     ok_phi = 0; ok_v = 0; ok_psi = 0; ok_wl = 0;
+    {
+      const float4 r4 = reinterpret_cast<const float4*>(rec_c)[tid < REC4 ? tid : 0];
+      rc0 = r4.x; rc1 = r4.y; rc2 = r4.z; rc3 = r4.w;
+    }
+    if constexpr (FULL) {
+#pragma unroll
+      for (int j = 0; j < NV_WSH; ++j) {
+        const int v = tid + j * kSegThreads;
+        wsv[j] = vec8_load(wsh_c + (size_t)(v < CH * SPM / 8 ? v : 0) * 8);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < NV_PHI; ++j) {
       const int v = tid + j * kSegThreads;
@@ -112,7 +130,7 @@ struct ChunkPrefetch {
       {
         const int s = v / (D / 8), c8 = v % (D / 8);
         if (s < SPM) {
-          Vec8<T> x = ((ok_phi >> j) & 1u) ? phi[j] : Vec8<T>::zero();
+          Vec8<T> x = phi[j].masked((ok_phi >> j) & 1u);
           if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
           x.store(&sm.phi[s][c8 * 8]);
         }
@@ -120,7 +138,7 @@ struct ChunkPrefetch {
       {
         const int s = v % SPM, c8 = v / SPM;
         if (c8 < D / 8) {
-          const Vec8<T> x = ((ok_v >> j) & 1u) ? vv[j] : Vec8<T>::zero();
+          const Vec8<T> x = vv[j].masked((ok_v >> j) & 1u);
 #pragma unroll
           for (int e = 0; e < 8; ++e) sm.delta[c8 * 8 + e][s] = x.v[e];
         }
@@ -132,10 +150,18 @@ struct ChunkPrefetch {
         const int v = tid + j * kSegThreads;
         const int t = v / (D / 8), c8 = v % (D / 8);
         if (t < CH) {
-          Vec8<T> x = ((ok_psi >> j) & 1u) ? psi[j] : Vec8<T>::zero();
+          Vec8<T> x = psi[j].masked((ok_psi >> j) & 1u);
           if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
           x.store(&sm.psi[t][c8 * 8]);
         }
+      }
+    }
+    if (tid < REC4) reinterpret_cast<float4*>(&sm.sc.acoef[0])[tid] = make_float4(rc0, rc1, rc2, rc3);
+    if constexpr (FULL) {
+#pragma unroll
+      for (int j = 0; j < NV_WSH; ++j) {
+        const int v = tid + j * kSegThreads;
+        if (v < CH * SPM / 8) wsv[j].store(&sm.wsh[(v * 8) / SPM][(v * 8) % SPM]);
       }
     }
     if (tid < CH) {
@@ -163,13 +189,15 @@ enum WalkMode { WALK_AGG = 0, WALK_FULL = 1, WALK_REWALK = 2 };
 //   WALK_REWALK: starts from seg_states[seg] (chunk length may differ from the forward's) and
 //                writes the raw state at the start of every chunk of the segment to rw (the
 //                backward pass walks them in reverse); no y.
-// Wave roles per chunk: P1 waves 0-5 run G1 (and G2 for the full walk) while waves 6-7 run the
-// coefficient recurrences; P3 waves 0-3 run G3 (y) while waves 4-7 run G4 and update the states,
-// which they hold in registers (wave 4 + m owns state rows 16 m .. 16 m + 15).
+// The chunk coefficients (a, kappa, end weights, Ws[s, t-1]) come precomputed from k_chunk_coef
+// (coef: [BH][nc] records, wsh_all: [BH][nc][CH][SPM], full walk only) with the prefetch.
+// Wave roles per chunk: P1 all waves run G1 (and G2 for the full walk); P3 waves 0-3 run G3 (y)
+// while waves 4-7 run G4 and update the states, which they hold in registers (wave 4 + m owns
+// state rows 16 m .. 16 m + 15).
 template <typename T, int CH, int D, int MODE>
 __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg, float* agg,
                                             const float* seg_states, float* rw, float* final_raw,
-                                            unsigned char* smem_raw) {
+                                            const float* coef, const T* wsh_all, unsigned char* smem_raw) {
   constexpr bool AGG = MODE == WALK_AGG;
   constexpr bool FULL = MODE == WALK_FULL;
   constexpr bool REWALK = MODE == WALK_REWALK;
@@ -224,10 +252,14 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
     }
   }
 
+  constexpr int REC = CoefRec<CH>::SIZE;
+  const float* coef_row = coef + (size_t)bh * g.nc * REC;
+  const T* wsh_row = FULL ? wsh_all + (size_t)bh * g.nc * CH * SPM : nullptr;
   ChunkPrefetch<T, CH, D, FULL> pf;
   if (c_begin < c_end) {
     const int t0 = c_begin * g.Lc;
-    pf.load(g, a, tb, t0, min(g.T, t0 + g.Lc) - t0);
+    pf.load(g, a, tb, t0, min(g.T, t0 + g.Lc) - t0, coef_row + (size_t)c_begin * REC,
+            FULL ? wsh_row + (size_t)c_begin * CH * SPM : nullptr);
   }
 
   for (int c = c_begin; c < c_end; ++c) {
@@ -258,22 +290,24 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
     __syncthreads();
     if (c + 1 < c_end) {                  // prefetch the next chunk while this one computes
       const int n0 = (c + 1) * g.Lc;
-      pf.load(g, a, tb, n0, min(g.T, n0 + g.Lc) - n0);
+      pf.load(g, a, tb, n0, min(g.T, n0 + g.Lc) - n0, coef_row + (size_t)(c + 1) * REC,
+              FULL ? wsh_row + (size_t)(c + 1) * CH * SPM : nullptr);
     }
 
-    // ---- P1: G1 + G2 (waves 0-5) | coefficient recurrences (waves 6-7)
+    // ---- P1: G1 + G2 (all waves)
     // G1: delta[i][s] = (S_ref phi_s)[i] - v_s[i];  G2 (full walk): Kmat[tau][s] = psi_tau . phi_s,
     // kept in registers (kacc) until the Q epilogue.
-    constexpr int NT1 = NTS * NTD, PER1 = (NT1 + 5) / 6;
-    constexpr int NT2 = FULL ? (CH / 16) * NTS : 0, PER2 = (NT2 + 5) / 6;
+    constexpr int NGW = kSegWaves;
+    constexpr int NT1 = NTS * NTD, PER1 = (NT1 + NGW - 1) / NGW;
+    constexpr int NT2 = FULL ? (CH / 16) * NTS : 0, PER2 = (NT2 + NGW - 1) / NGW;
     f32x4 kacc[PER2 > 0 ? PER2 : 1];
     static_assert(!FULL || NT2 > 0, "G2 tiles");
-    if (wave < 6) {
+    {
       // tile indices past the end are clamped (MFMAs stay unconditional, only the stores are guarded)
 #pragma unroll 1
       for (int j = 0; j < PER1; ++j) {
-        const int tile = min(wave + 6 * j, NT1 - 1);
-        const bool valid = NT1 % 6 == 0 || wave + 6 * j < NT1;
+        const int tile = min(wave + NGW * j, NT1 - 1);
+        const bool valid = NT1 % NGW == 0 || wave + NGW * j < NT1;
         const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;   // m: sources, n: rows i
         f32x4 acc = zero4();
 #pragma unroll
@@ -291,9 +325,9 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
         }
       }
       if constexpr (FULL) {
-#pragma unroll 1
+#pragma unroll
         for (int j = 0; j < PER2; ++j) {
-          const int tt = min(wave + 6 * j, NT2 - 1);
+          const int tt = min(wave + NGW * j, NT2 - 1);
           const int m0 = (tt / NTS) * 16, n0 = (tt % NTS) * 16;
           f32x4 acc = zero4();
 #pragma unroll
@@ -302,24 +336,22 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
           kacc[j] = acc;
         }
       }
-    } else {
-      chunk_coefficients<CH, FULL>(g, sm.sc, L, tid - 6 * kWave, FULL ? &sm.wsh[0][0] : nullptr, SPM + 1);
     }
     __syncthreads();
 
-    // ---- P2: Q epilogue (waves 0-5), scaled phi^T for G4 (all)
+    // ---- P2: Q epilogue, scaled phi^T for G4 (all waves)
     if constexpr (FULL) {
-      if (wave < 6) {
-#pragma unroll 1
+      {
+#pragma unroll
         for (int j = 0; j < PER2; ++j) {
-          const int tt = wave + 6 * j;
-          if (NT2 % 6 == 0 || tt < NT2) {
+          const int tt = wave + NGW * j;
+          if (NT2 % NGW == 0 || tt < NT2) {
             const int m0 = (tt / NTS) * 16, n0 = (tt % NTS) * 16;
             const int s = n0 + (lane & 15);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int t = m0 + 4 * (lane >> 4) + r;
-              sm.Q[t][s] = from_f32<T>(kacc[j][r] * sm.wsh[t][s]);
+              sm.Q[t][s] = from_f32<T>(kacc[j][r] * to_f32(sm.wsh[t][s]));
             }
           }
         }
@@ -376,7 +408,7 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
                 const int t = m0 + 4 * (lane >> 4) + r;
-                yv[r] -= sm.wsh[t][s] * ab[r];
+                yv[r] -= to_f32(sm.wsh[t][s]) * ab[r];
               }
             }
           }

@@ -14,7 +14,7 @@
 // single segment (an exact sequential walk over all chunks).
 //
 // Inside a chunk (tokens t0..t1-1, sources s = the chunk plus its e-1 token halo) everything is in
-// closed form (see the per-source coefficient recurrence in chunk_coefficients):
+// closed form (the per-chunk coefficients, k_chunk_coef in coef.hip, are formed first):
 //   G1  delta^T[s,i] = phi_s . S_ref[i,:] - v_s[i]
 //   G2  Q[tau,s]     = Ws[s,tau-1] * (psi_tau . phi_s)
 //   G3  y^T[tau,i]   = -Q delta^T + a_{tau-1} psi S_in^T - kappa_{tau-1} psi Z_in^T
@@ -29,11 +29,15 @@
 
 namespace atlas {
 
+template <typename T, int CH>
+hipError_t launch_chunk_coef(const Geom& g, const T* decay, const T* lr, const T* beta, const T* gate, float* rec,
+                             T* wsh, int kid, hipStream_t stream);
+
 template <typename T, int CH, int D>
 __global__ __launch_bounds__(kSegThreads) void k_fwd_seg_agg(const Geom g, const FwdPtrs<T> a, const SegGeom sg,
-                                                               float* agg) {
+                                                               float* agg, const float* coef) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  fwd_segment<T, CH, D, WALK_AGG>(g, a, sg, agg, nullptr, nullptr, nullptr, smem_raw);
+  fwd_segment<T, CH, D, WALK_AGG>(g, a, sg, agg, nullptr, nullptr, nullptr, coef, nullptr, smem_raw);
 }
 
 // grid (D * D / kThreads, BH): segment-start states  x_{j+1} = [[a_j, -kappa_j], [0, b_j]] x_j + [U_j; V_j]
@@ -63,22 +67,25 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg_scan(const Geom g, const f
 
 template <typename T, int CH, int D>
 __global__ __launch_bounds__(kSegThreads) void k_fwd_seg(const Geom g, const FwdPtrs<T> a, const SegGeom sg,
-                                                           const float* seg_states, float* final_raw) {
+                                                           const float* seg_states, float* final_raw,
+                                                           const float* coef, const T* wsh) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  fwd_segment<T, CH, D, WALK_FULL>(g, a, sg, nullptr, seg_states, nullptr, final_raw, smem_raw);
+  fwd_segment<T, CH, D, WALK_FULL>(g, a, sg, nullptr, seg_states, nullptr, final_raw, coef, wsh, smem_raw);
 }
 
 template <typename T, int CH, int D>
 hipError_t launch_fwd_seg(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg, float* agg, float* seg_states,
-                          float* final_raw, hipStream_t stream) {
-  hipError_t err;
+                          float* final_raw, float* coef, T* wsh, hipStream_t stream) {
+  hipError_t err = launch_chunk_coef<T, CH>(g, a.decay, a.lr, a.beta, a.gate, coef, wsh, KID_FWD_COEF, stream);
+  if (err != hipSuccess) return err;
   if (sg.nseg > 1) {
     const size_t smem = sizeof(SegFwdSmem<T, CH, D, false>);
     err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_seg_agg<T, CH, D>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (err != hipSuccess) return err;
     prof_begin(KID_FWD_SEG_AGG, stream);
-    hipLaunchKernelGGL((k_fwd_seg_agg<T, CH, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, agg);
+    hipLaunchKernelGGL((k_fwd_seg_agg<T, CH, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, agg,
+                       (const float*)coef);
     prof_end(KID_FWD_SEG_AGG, stream);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
@@ -93,14 +100,14 @@ hipError_t launch_fwd_seg(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg,
   if (err != hipSuccess) return err;
   prof_begin(KID_FWD_WALK, stream);
   hipLaunchKernelGGL((k_fwd_seg<T, CH, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg,
-                     (const float*)seg_states, final_raw);
+                     (const float*)seg_states, final_raw, (const float*)coef, (const T*)wsh);
   prof_end(KID_FWD_WALK, stream);
   return hipGetLastError();
 }
 
 #define ATLAS_INST_FWD_SEG(T, CH, D) \
   template hipError_t launch_fwd_seg<T, CH, D>(const Geom&, const FwdPtrs<T>&, const SegGeom&, float*, float*, float*, \
-                                               hipStream_t);
+                                               float*, T*, hipStream_t);
 
 ATLAS_INST_FWD_SEG(bf16, 64, 64)
 ATLAS_INST_FWD_SEG(float, 32, 64)

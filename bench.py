@@ -51,6 +51,12 @@ def algorithmic_bytes(bh=BH, t=T, d=D, e=E, s_in=2, s_st=4):
         "k_bwd_seg": n * 4 * d * s_in + 2 * n * n_sc * s_in + n * 3 * d * s_in + 5 * st,
         "k_bwd_seg_fixup": 0,
         "k_seg_reduce_dsref": st,
+        # segment scans and chunk-coefficient passes: intermediate data only; the coefficient
+        # passes read the per-token scalars once
+        "k_fwd_seg_scan": 0,
+        "k_bwd_seg_scan": 0,
+        "k_chunk_coef_fwd": n * n_sc * s_in,
+        "k_chunk_coef_bwd": n * n_sc * s_in,
     }
     return fwd, bwd, per_kernel
 

@@ -167,7 +167,7 @@ int atlas_window_sum(int dtype, int64_t n, int64_t t, int64_t d, int window, int
 /* ---- diagnostics (no reference counterpart) ------------------------------------------------ */
 
 /* Number of kernels the timing hooks distinguish (index -> atlas_mem_kernel_name). */
-#define ATLAS_MEM_NKERNELS 9
+#define ATLAS_MEM_NKERNELS 11
 
 /* Opt-in timing: while enabled, each kernel launch of atlas_mem_fwd/atlas_mem_bwd is bracketed
  * by HIP events on its stream (adds two event records per launch). */
