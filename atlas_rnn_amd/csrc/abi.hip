@@ -13,8 +13,8 @@
 
 namespace atlas {
 template <typename T, int CH, int D>
-hipError_t launch_fwd_seg(const Geom&, const FwdPtrs<T>&, const SegGeom&, float*, float*, float*, float*, T*,
-                          hipStream_t);
+hipError_t launch_fwd_seg(const Geom&, const FwdPtrs<T>&, const SegGeom&, float*, float*, float*, float*, float*,
+                          T*, hipStream_t);
 template <typename T, int CH, int D>
 hipError_t launch_bwd_seg(const Geom&, const BwdPtrs<T>&, const SegGeom&, const BwdSegPtrs&, hipStream_t);
 template <typename T, int DK, int DV> hipError_t launch_buffer_out(const Geom&, const FwdPtrs<T>&, hipStream_t);
@@ -165,11 +165,15 @@ Plan make_plan(const atlas_mem_problem* p) {
   int Lc = CH;
   if (p->clamp_every > 0 && p->clamp_every % CH != 0) Lc = largest_divisor_at_most(p->clamp_every, CH);
   const int Lb = largest_divisor_at_most(Lc, bwd_chunk_cap(p->dtype));
+  // the forward saves the state at every backward-chunk boundary: at most one inside a chunk
+  if (Lc / Lb > 2) Lc = Lb;
   const int H = p->window - 1;
   if (Lb < H) { pl.status = ATLAS_MEM_ERR_UNSUPPORTED; return pl; }
   Geom& g = pl.g;
   g.BH = p->bh; g.T = p->seq_len; g.DK = p->d_k; g.DV = p->d_v;
   g.e = p->window; g.H = H; g.Lc = Lc; g.nc = (p->seq_len + Lc - 1) / Lc;
+  g.Lmid = Lc / Lb == 2 ? Lb : 0;
+  g.ncb = (p->seq_len + Lb - 1) / Lb;
   g.momentum = p->momentum; g.gate_mode = p->gate_mode; g.map_mode = p->map_mode;
   g.map_deg = p->map_mode == ATLAS_MAP_ELEMENTWISE ? p->map_degree : 1;
   g.has_buf = p->has_buffer; g.clamp_every = p->clamp_every; g.clamp_final = p->clamp_final;
@@ -179,6 +183,7 @@ Plan make_plan(const atlas_mem_problem* p) {
   gb = g;
   gb.Lc = Lb;
   gb.nc = (p->seq_len + Lb - 1) / Lb;
+  gb.Lmid = 0;
   pl.sgb = pl.sg;
   pl.sgb.G = pl.sg.G * (Lc / Lb);
   pl.CH = CH;
@@ -191,13 +196,14 @@ Plan make_plan(const atlas_mem_problem* p) {
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-// `saved` layout: segment-start states, segment aggregates (forward scratch), raw S_{T-1}.
+// `saved` layout: segment-start states, segment aggregates (forward scratch), raw S_{T-1}, the raw
+// state at every backward-chunk boundary (written by the forward walk, read by the backward).
 struct SavedLayout {
-  size_t seg, agg, final_raw, coef, wsh, total;
+  size_t seg, agg, final_raw, rw, coef, wsh, total;
 };
 
-// floats per chunk coefficient record (acoef, kcoef, endc, wsend, wzend) for chunk capacity ch
-size_t coef_rec_floats(int ch) { return (size_t)2 * ch + 4 + 2 * (ch + kHaloPad); }
+// floats per chunk coefficient record (acoef, kcoef, endc, wsend, wzend, wsmid, wzmid, midc)
+size_t coef_rec_floats(int ch) { return (size_t)2 * ch + 8 + 4 * (ch + kHaloPad); }
 
 SavedLayout saved_layout(const Plan& pl) {
   const Geom& g = pl.g;
@@ -207,6 +213,7 @@ SavedLayout saved_layout(const Plan& pl) {
   L.seg = off; off += align256((size_t)g.BH * pl.sg.nseg * 2 * st);
   L.agg = off; off += align256((size_t)g.BH * pl.sg.nseg * pl.sg.agg_stride * sizeof(float));
   L.final_raw = off; off += align256((size_t)g.BH * st);
+  L.rw = off; off += align256((size_t)g.BH * g.ncb * 2 * st);
   // forward scratch: per-chunk coefficient records and Ws[s, t-1] blocks
   L.coef = off; off += align256((size_t)g.BH * g.nc * coef_rec_floats(pl.CH) * sizeof(float));
   L.wsh = off; off += align256((size_t)g.BH * g.nc * pl.CH * (pl.CH + kHaloPad) * pl.esize);
@@ -217,7 +224,7 @@ SavedLayout saved_layout(const Plan& pl) {
 // backward workspace: adjoint aggregates, re-walk chunk states, dS_ref partials, boundary partials,
 // token-gate (target, lag) gradients.
 struct BwdLayout {
-  size_t agg, segadj, rw, dsref, tail, halo, dw, coef, wsh, total;
+  size_t agg, segadj, dsref, tail, halo, dw, coef, wsh, total;
 };
 
 BwdLayout bwd_layout(const Plan& pl) {
@@ -228,7 +235,6 @@ BwdLayout bwd_layout(const Plan& pl) {
   size_t off = 0;
   L.agg = off; off += align256((size_t)g.BH * nseg * pl.sgb.agg_stride * sizeof(float));
   L.segadj = off; off += align256((size_t)g.BH * nseg * 2 * st);
-  L.rw = off; off += align256((size_t)g.BH * nseg * pl.sgb.G * 2 * st);
   L.dsref = off; off += align256((size_t)g.BH * nseg * st);
   L.tail = off; off += align256((size_t)g.BH * nseg * g.H * (g.DV + g.DK) * sizeof(float));
   L.halo = off; off += align256((size_t)g.BH * nseg * g.H * (g.DV + g.DK) * sizeof(float));
@@ -253,17 +259,18 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
   float* seg_states = reinterpret_cast<float*>(sv + SL.seg);
   float* agg = reinterpret_cast<float*>(sv + SL.agg);
   float* final_raw = reinterpret_cast<float*>(sv + SL.final_raw);
+  float* rw = reinterpret_cast<float*>(sv + SL.rw);
   float* coef = reinterpret_cast<float*>(sv + SL.coef);
   T* wsh = reinterpret_cast<T*>(sv + SL.wsh);
   const Geom& g = pl.g;
   hipError_t err = hipErrorInvalidValue;
   if (g.DK == 64) {
-    if constexpr (sizeof(T) == 2) err = launch_fwd_seg<T, 64, 64>(g, a, pl.sg, agg, seg_states, final_raw, coef, wsh, s);
-    else err = launch_fwd_seg<T, 32, 64>(g, a, pl.sg, agg, seg_states, final_raw, coef, wsh, s);
+    if constexpr (sizeof(T) == 2) err = launch_fwd_seg<T, 64, 64>(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
+    else err = launch_fwd_seg<T, 32, 64>(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
     if (err == hipSuccess) err = launch_buffer_out<T, 64, 64>(g, a, s);
   } else if (g.DK == 32) {
-    if constexpr (sizeof(T) == 2) err = launch_fwd_seg<T, 64, 32>(g, a, pl.sg, agg, seg_states, final_raw, coef, wsh, s);
-    else err = launch_fwd_seg<T, 32, 32>(g, a, pl.sg, agg, seg_states, final_raw, coef, wsh, s);
+    if constexpr (sizeof(T) == 2) err = launch_fwd_seg<T, 64, 32>(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
+    else err = launch_fwd_seg<T, 32, 32>(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
     if (err == hipSuccess) err = launch_buffer_out<T, 32, 32>(g, a, s);
   }
   return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
@@ -289,7 +296,7 @@ int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, voi
   p.final_raw = reinterpret_cast<const float*>(sv + SL.final_raw);
   p.adj_agg = reinterpret_cast<float*>(w + L.agg);
   p.seg_adj = reinterpret_cast<float*>(w + L.segadj);
-  p.rw = reinterpret_cast<float*>(w + L.rw);
+  p.rw = reinterpret_cast<const float*>(sv + SL.rw);
   p.dsref_part = reinterpret_cast<float*>(w + L.dsref);
   p.tail_part = gb.H > 0 ? reinterpret_cast<float*>(w + L.tail) : nullptr;
   p.halo_part = gb.H > 0 ? reinterpret_cast<float*>(w + L.halo) : nullptr;

@@ -19,6 +19,9 @@ struct Geom {
   int BH, T, DK, DV;
   int e, H;         // window and halo = e - 1
   int Lc;           // chunk length used for this call (<= CH)
+  int Lmid;         // forward walk: token offset inside a chunk at which the backward chunks split it
+                    // (the backward chunk length when it is Lc / 2), 0 when the chunkings coincide
+  int ncb;          // forward walk: number of backward chunks (rows of the saved chunk-start states)
   int nc;           // number of chunks = ceil(T / Lc)
   int momentum, gate_mode, map_mode, map_deg, has_buf, clamp_every, clamp_final;
 };

@@ -8,9 +8,7 @@
 //                     dZ_in = b dZ_end - kappa dS_end - sum_t kappa_{t-1} dy_t psi_t^T
 //   k_bwd_seg_scan: one thread per state element folds the aggregates from the last segment back,
 //                   writing the adjoint (dS, dZ) at every segment end.
-//   k_bwd_seg     : starts from the adjoint at its segment end,
-//                   re-walks the forward recurrence of the segment from its saved start state
-//                   (raw chunk-start states to a short-lived scratch), then walks the chunks in
+//   k_bwd_seg     : starts from the adjoint at its segment end and walks the segment's chunks in
 //                   reverse forming every gradient of each chunk in closed form (see k_bwd_seg's
 //                   phase comments) while carrying (dS, dZ) and the halo gradients of the previous
 //                   chunk's last e-1 tokens.
@@ -19,7 +17,6 @@
 #include "mem_common.h"
 #include "mem_params.h"
 #include "seg_common.h"
-#include "seg_fwd.h"
 
 namespace atlas {
 
@@ -120,7 +117,7 @@ template <typename T, int CH, int D>
 struct BwdSegSmem {
   static constexpr int SPM = CH + kHaloPad;
   static constexpr int LWR = ((CH + 2 + 15) / 16) * 16;   // rows of the phase-F GEMM operand
-  static constexpr bool kStatesInLds = sizeof(T) == 2;   // fp32 reads S_in / Z_in from the re-walk scratch
+  static constexpr bool kStatesInLds = sizeof(T) == 2;   // fp32 reads S_in / Z_in from the saved chunk states
   T sref[D][D + 8];
   T dSe[D][D + 8];
   T dZe[D][D + 8];
@@ -148,10 +145,153 @@ struct BwdSegSmem {
   ChunkScalars<CH> sc;
   DecayTab<CH> tab;
   float hS[SPM], hZ[SPM], fS[CH], fZ[CH];
-  float A1[CH + 1], K1[CH + 1], B1[CH + 1];
+  float B1[CH + 1];        // b_{t-1}, t = 0..CH (a_{t-1}, kappa_{t-1} are sc.acoef / sc.kcoef)
   float gram[4];
   float red[kSegWaves][4];
   // followed by the halo carry: float carry[2][H][2 * D] (dynamic size)
+};
+
+// Register prefetch of one backward chunk's inputs (issued one chunk ahead of its use): k, v of
+// the sources, q, dy of the targets, the scalars and gates, the coefficient record, the Ws[s, t-1]
+// block and the saved chunk-start state tiles of this wave. Every load is unconditional from
+// an in-bounds address; masks are applied in store().
+template <typename T, int CH, int D>
+struct BwdPrefetch {
+  static constexpr int SPM = CH + kHaloPad;
+  static constexpr int NTD = D / 16;
+  static constexpr int NT2 = (NTD * NTD + kSegWaves - 1) / kSegWaves;
+  static constexpr int NVS = (SPM * (D / 8) + kSegThreads - 1) / kSegThreads;
+  static constexpr int NVT = (CH * (D / 8) + kSegThreads - 1) / kSegThreads;
+  static constexpr int NWL = (CH * kMaxWindow + kSegThreads - 1) / kSegThreads;
+  static constexpr int REC4 = CoefRec<CH>::SIZE / 4;
+  static constexpr int NV_WSH = (CH * SPM / 8 + kSegThreads - 1) / kSegThreads;
+  Vec8<T> rk[NVS], rv[NVS], rq[NVT], rd[NVT], wsv[NV_WSH];
+  float rc0, rc1, rc2, rc3;
+  T x_al, x_et, x_be, x_ug;
+  T x_wl[NWL];
+  unsigned okS, okT, okW;
+  bool okt, okug, padug;
+  float s_in[NT2][4], z_in[NT2][4];   // raw chunk-start state (saved by the forward), this wave's tiles
+
+  __device__ __forceinline__ void load(const Geom& g, const BwdPtrs<T>& a, const BwdSegPtrs& p, int bh, int c,
+                                       const float* Sin_g, int tid, int lane, int wave) {
+    const int H = g.H, e = g.e;
+    const size_t tb = (size_t)bh * g.T;
+    const int t0 = c * g.Lc, L = min(g.T, t0 + g.Lc) - t0;
+    const size_t r0 = tb + t0;
+    okS = 0; okT = 0; okW = 0;
+#pragma unroll
+    for (int j = 0; j < NVS; ++j) {
+      const int idx = tid + j * kSegThreads;
+      const int s = idx / (D / 8), c8 = idx % (D / 8);
+      const int pp = t0 - H + s;
+      const bool ok = s < SPM && s < H + L && pp >= 0;
+      const size_t row = ok ? tb + pp : r0;
+      rk[j] = vec8_load(a.k + row * D + c8 * 8);
+      rv[j] = vec8_load(a.v + row * D + c8 * 8);
+      okS |= (ok ? 1u : 0u) << j;
+    }
+    const T* dyp = a.dy ? a.dy : a.q;
+#pragma unroll
+    for (int j = 0; j < NVT; ++j) {
+      const int idx = tid + j * kSegThreads;
+      const int t = idx / (D / 8), c8 = idx % (D / 8);
+      const bool ok = t < L;
+      const size_t row = ok ? r0 + t : r0;
+      rq[j] = vec8_load(a.q + row * D + c8 * 8);
+      rd[j] = vec8_load(dyp + row * D + c8 * 8);
+      okT |= (ok ? 1u : 0u) << j;
+    }
+    okt = tid < L;
+    const size_t rt = okt ? r0 + tid : r0;
+    x_al = a.decay[rt];
+    x_et = a.lr[rt];
+    x_be = ((g.momentum && a.beta) ? a.beta : a.decay)[rt];
+    const T* gp = a.gate ? a.gate : a.decay;
+    const int pg = t0 - H + tid;
+    okug = g.gate_mode == GATE_TOKEN && tid < SPM && tid < H + L && pg >= 0;
+    padug = g.gate_mode == GATE_TOKEN && tid < SPM && tid < H + L && pg < 0;
+    x_ug = gp[okug ? tb + pg : r0];
+#pragma unroll
+    for (int j = 0; j < NWL; ++j) {
+      const int idx = tid + j * kSegThreads;
+      const bool ok = g.gate_mode == GATE_LAG && idx < CH * e && idx / e < L;
+      x_wl[j] = gp[ok ? r0 * e + idx : r0];
+      okW |= (ok ? 1u : 0u) << j;
+    }
+    {
+      const float4 r4 = reinterpret_cast<const float4*>(p.coef + ((size_t)bh * g.nc + c) * CoefRec<CH>::SIZE)[tid < REC4 ? tid : 0];
+      rc0 = r4.x; rc1 = r4.y; rc2 = r4.z; rc3 = r4.w;
+    }
+    const T* wsh_c = reinterpret_cast<const T*>(p.wsh) + ((size_t)bh * g.nc + c) * CH * SPM;
+#pragma unroll
+    for (int j = 0; j < NV_WSH; ++j) {
+      const int v = tid + j * kSegThreads;
+      wsv[j] = vec8_load(wsh_c + (size_t)(v < CH * SPM / 8 ? v : 0) * 8);
+    }
+    const float* Zin_g = Sin_g + (size_t)D * D;
+#pragma unroll
+    for (int j = 0; j < NT2; ++j) {
+      const int tile = min(wave + kSegWaves * j, NTD * NTD - 1);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = (tile / NTD) * 16 + 4 * (lane >> 4) + r, k = (tile % NTD) * 16 + (lane & 15);
+        s_in[j][r] = Sin_g[(size_t)i * D + k];
+        z_in[j][r] = Zin_g[(size_t)i * D + k];
+      }
+    }
+  }
+
+  // chunk inputs -> LDS (the states are consumed by the caller)
+  template <typename Sm>
+  __device__ __forceinline__ void store(const Geom& g, const BwdPtrs<T>& a, Sm& sm, int tid) {
+    const int e = g.e;
+#pragma unroll
+    for (int j = 0; j < NVS; ++j) {
+      const int idx = tid + j * kSegThreads;
+      const int s = idx / (D / 8), c8 = idx % (D / 8);
+      if (s < SPM) {
+        const bool ok = (okS >> j) & 1u;
+        Vec8<T> x = rk[j].masked(ok);
+        if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
+        x.store(&sm.phi[s][c8 * 8]);
+        rv[j].masked(ok).store(&sm.deltaT[s][c8 * 8]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NVT; ++j) {
+      const int idx = tid + j * kSegThreads;
+      const int t = idx / (D / 8), c8 = idx % (D / 8);
+      if (t < CH) {
+        const bool ok = (okT >> j) & 1u;
+        Vec8<T> x = rq[j].masked(ok);
+        if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
+        x.store(&sm.psi[t][c8 * 8]);
+        rd[j].masked(ok && a.dy).store(&sm.dy[t][c8 * 8]);
+      }
+    }
+    if (tid < REC4) reinterpret_cast<float4*>(&sm.sc.acoef[0])[tid] = make_float4(rc0, rc1, rc2, rc3);
+#pragma unroll
+    for (int j = 0; j < NV_WSH; ++j) {
+      const int v = tid + j * kSegThreads;
+      if (v < CH * SPM / 8) wsv[j].store(&sm.wsh[(v * 8) / SPM][(v * 8) % SPM]);
+    }
+    if (tid < CH) {
+      sm.sc.alpha[tid] = okt ? to_f32(x_al) : 1.f;
+      sm.sc.eta[tid] = okt ? to_f32(x_et) : 0.f;
+      sm.sc.beta[tid] = okt ? (g.momentum ? to_f32(x_be) : 0.f) : 1.f;
+      sm.fS[tid] = 0.f; sm.fZ[tid] = 0.f;
+    }
+    for (int s = tid; s < SPM; s += kSegThreads) { sm.hS[s] = 0.f; sm.hZ[s] = 0.f; }
+    if (g.gate_mode == GATE_TOKEN && tid < SPM) sm.sc.ug[tid] = okug ? to_f32(x_ug) : (padug ? 1.f : 0.f);
+    if (g.gate_mode == GATE_LAG) {
+#pragma unroll
+      for (int j = 0; j < NWL; ++j) {
+        const int idx = tid + j * kSegThreads;
+        if (idx < CH * e) sm.sc.wl[idx] = ((okW >> j) & 1u) ? to_f32(x_wl[j]) : 0.f;
+      }
+    }
+  }
 };
 
 template <typename T>
@@ -180,7 +320,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
   // the segment's last H tokens: their partial (dv, dphi) goes to tail_part (merged by the fixup with the
   // next segment's halo and the d buffer_out terms)
   const int seg_tail0 = min(g.T, c_end * g.Lc) - H;
-  float* rw = p.rw + ((size_t)bh * sg.nseg + seg) * (size_t)sg.G * 2 * D * D;
+  const float* rw = p.rw + (size_t)bh * g.nc * 2 * D * D;   // raw chunk-start states of this row
 
   // ---- 1. adjoint at the segment end (owned tiles: wave + 8 j)
   float dS[NT2][4], dZ[NT2][4], dsr[NT2][4];
@@ -201,168 +341,34 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
     }
   }
 
-  // ---- 2. forward re-walk of the segment -> raw chunk-start states in rw
-  {
-    FwdPtrs<T> fa;
-    fa.k = a.k; fa.q = a.q; fa.v = a.v; fa.lr = a.lr; fa.decay = a.decay; fa.beta = a.beta; fa.gate = a.gate;
-    fa.S_ref = a.S_ref; fa.S0 = a.S0; fa.Z0 = a.Z0; fa.buf_in = a.buf_in;
-    fa.y = nullptr; fa.S_T = nullptr; fa.Z_T = nullptr; fa.buf_out = nullptr;
-    fwd_segment<T, CH, D, WALK_REWALK>(g, fa, sg, nullptr, p.seg_states, rw, nullptr, p.coef, nullptr, smem_raw);
-  }
-  __syncthreads();
-
   Sm& sm = *reinterpret_cast<Sm*>(smem_raw);
   float* carry = reinterpret_cast<float*>(smem_raw + sizeof(Sm));   // [2][H][2D]
   for (int idx = tid; idx < D * D; idx += kSegThreads) sm.sref[idx / D][idx % D] = from_f32<T>(a.S_ref[sb + idx]);
   for (int idx = tid; idx < 2 * H * 2 * D; idx += kSegThreads) carry[idx] = 0.f;
 
   // ---- 3. reverse walk
+  BwdPrefetch<T, CH, D> pf;
+  if (c_begin < c_end) pf.load(g, a, p, bh, c_end - 1, rw + (size_t)(c_end - 1) * 2 * D * D, tid, lane, wave);
   for (int c = c_end - 1; c >= c_begin; --c) {
     // per-lane indices re-derived every chunk: keeps the compiler from hoisting every per-lane
     // address out of the loop and holding (or spilling) them across the whole walk
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
     const int lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int jc = c - c_begin;
     const int t0 = c * g.Lc, t1 = min(g.T, t0 + g.Lc), L = t1 - t0;
     const bool bufchunk = (c == 0) && g.has_buf;
     const bool clamp_in = (c > 0) && clamp_after(g, t0);
     const bool first = c == c_begin, last = c == c_end - 1;
-    const float* Sin_g = rw + (size_t)jc * 2 * D * D;   // raw
+    const float* Sin_g = rw + (size_t)c * 2 * D * D;   // raw
     const float* Zin_g = Sin_g + (size_t)D * D;
     float* cur_carry = carry + (size_t)(c & 1) * H * 2 * D;        // this chunk's halo -> chunk c-1
     float* prev_carry = carry + (size_t)((c + 1) & 1) * H * 2 * D; // chunk c+1's halo -> this chunk's tail
     __syncthreads();
 
-    // ---- loads: every global read of the chunk is issued before the first LDS write
+    // ---- loads: this chunk's inputs (prefetched one chunk ahead) -> LDS; next chunk's prefetch
     {
-      constexpr int NVS = (SPM * (D / 8) + kSegThreads - 1) / kSegThreads;
-      constexpr int NVT = (CH * (D / 8) + kSegThreads - 1) / kSegThreads;
-      constexpr int NWL = (CH * kMaxWindow + kSegThreads - 1) / kSegThreads;
-      // every load is unconditional from an in-bounds address; masks are applied when storing
-      const size_t r0 = tb + t0;
-      Vec8<T> rk[NVS], rv[NVS], rq[NVT], rd[NVT];
-      unsigned okS = 0, okT = 0;
-#pragma unroll
-      for (int j = 0; j < NVS; ++j) {
-        const int idx = tid + j * kSegThreads;
-        const int s = idx / (D / 8), c8 = idx % (D / 8);
-        const int pp = t0 - H + s;
-        const bool ok = s < SPM && s < H + L && pp >= 0;
-        const size_t row = ok ? tb + pp : r0;
-        rk[j] = vec8_load(a.k + row * D + c8 * 8);
-        rv[j] = vec8_load(a.v + row * D + c8 * 8);
-        okS |= (ok ? 1u : 0u) << j;
-      }
-      const T* dyp = a.dy ? a.dy : a.q;
-#pragma unroll
-      for (int j = 0; j < NVT; ++j) {
-        const int idx = tid + j * kSegThreads;
-        const int t = idx / (D / 8), c8 = idx % (D / 8);
-        const bool ok = t < L;
-        const size_t row = ok ? r0 + t : r0;
-        rq[j] = vec8_load(a.q + row * D + c8 * 8);
-        rd[j] = vec8_load(dyp + row * D + c8 * 8);
-        okT |= ((ok ? 1u : 0u) << j);
-      }
-      const bool okt = tid < L;
-      const size_t rt = okt ? r0 + tid : r0;
-      const T x_al = a.decay[rt], x_et = a.lr[rt];
-      const T x_be = ((g.momentum && a.beta) ? a.beta : a.decay)[rt];
-      const T* gp = a.gate ? a.gate : a.decay;
-      const int pg = t0 - H + tid;
-      const bool okug = g.gate_mode == GATE_TOKEN && tid < SPM && tid < H + L && pg >= 0;
-      const bool padug = g.gate_mode == GATE_TOKEN && tid < SPM && tid < H + L && pg < 0;
-      const T x_ug = gp[okug ? tb + pg : r0];
-      T x_wl[NWL];
-      unsigned okW = 0;
-#pragma unroll
-      for (int j = 0; j < NWL; ++j) {
-        const int idx = tid + j * kSegThreads;
-        const bool ok = g.gate_mode == GATE_LAG && idx < CH * e && idx / e < L;
-        x_wl[j] = gp[ok ? r0 * e + idx : r0];
-        okW |= (ok ? 1u : 0u) << j;
-      }
-      // chunk coefficient record and Ws[s, t-1] block (k_chunk_coef)
-      constexpr int REC4 = CoefRec<CH>::SIZE / 4;
-      constexpr int NV_WSH = (CH * SPM / 8 + kSegThreads - 1) / kSegThreads;
-      const float4 rec4 = reinterpret_cast<const float4*>(p.coef + ((size_t)bh * g.nc + c) * CoefRec<CH>::SIZE)[tid < REC4 ? tid : 0];
-      const T* wsh_c = reinterpret_cast<const T*>(p.wsh) + ((size_t)bh * g.nc + c) * CH * SPM;
-      Vec8<T> wsv[NV_WSH];
-#pragma unroll
-      for (int j = 0; j < NV_WSH; ++j) {
-        const int v = tid + j * kSegThreads;
-        wsv[j] = vec8_load(wsh_c + (size_t)(v < CH * SPM / 8 ? v : 0) * 8);
-      }
-      float s_in[NT2][4], z_in[NT2][4];
-#pragma unroll
-      for (int j = 0; j < NT2; ++j) {
-        const int tile = min(wave + kSegWaves * j, NTD * NTD - 1);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = (tile / NTD) * 16 + 4 * (lane >> 4) + r, k = (tile % NTD) * 16 + (lane & 15);
-          s_in[j][r] = Sin_g[(size_t)i * D + k];
-          z_in[j][r] = Zin_g[(size_t)i * D + k];
-        }
-      }
-      const float r_al = okt ? to_f32(x_al) : 1.f;
-      const float r_et = okt ? to_f32(x_et) : 0.f;
-      const float r_be = okt ? (g.momentum ? to_f32(x_be) : 0.f) : 1.f;
-      const float r_ug = okug ? to_f32(x_ug) : (padug ? 1.f : 0.f);
-      float r_wl[NWL];
-#pragma unroll
-      for (int j = 0; j < NWL; ++j) r_wl[j] = ((okW >> j) & 1u) ? to_f32(x_wl[j]) : 0.f;
-      if (!g.momentum) {
-#pragma unroll
-        for (int j = 0; j < NT2; ++j)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) z_in[j][r] = 0.f;
-      }
-      // LDS stores
-#pragma unroll
-      for (int j = 0; j < NVS; ++j) {
-        const int idx = tid + j * kSegThreads;
-        const int s = idx / (D / 8), c8 = idx % (D / 8);
-        if (s < SPM) {
-          const bool ok = (okS >> j) & 1u;
-          Vec8<T> x = rk[j].masked(ok);
-          if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
-          x.store(&sm.phi[s][c8 * 8]);
-          rv[j].masked(ok).store(&sm.deltaT[s][c8 * 8]);
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < NVT; ++j) {
-        const int idx = tid + j * kSegThreads;
-        const int t = idx / (D / 8), c8 = idx % (D / 8);
-        if (t < CH) {
-          const bool ok = (okT >> j) & 1u;
-          Vec8<T> x = rq[j].masked(ok);
-          if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
-          x.store(&sm.psi[t][c8 * 8]);
-          rd[j].masked(ok && a.dy).store(&sm.dy[t][c8 * 8]);
-        }
-      }
-      if (tid < REC4) reinterpret_cast<float4*>(&sm.sc.acoef[0])[tid] = rec4;
-#pragma unroll
-      for (int j = 0; j < NV_WSH; ++j) {
-        const int v = tid + j * kSegThreads;
-        if (v < CH * SPM / 8) wsv[j].store(&sm.wsh[(v * 8) / SPM][(v * 8) % SPM]);
-      }
-      if (tid < CH) {
-        sm.sc.alpha[tid] = r_al; sm.sc.eta[tid] = r_et; sm.sc.beta[tid] = r_be;
-        sm.fS[tid] = 0.f; sm.fZ[tid] = 0.f;
-      }
-      for (int s = tid; s < SPM; s += kSegThreads) { sm.hS[s] = 0.f; sm.hZ[s] = 0.f; }
-      if (g.gate_mode == GATE_TOKEN && tid < SPM) sm.sc.ug[tid] = r_ug;
-      if (g.gate_mode == GATE_LAG) {
-#pragma unroll
-        for (int j = 0; j < NWL; ++j) {
-          const int idx = tid + j * kSegThreads;
-          if (idx < CH * e) sm.sc.wl[idx] = r_wl[j];
-        }
-      }
-      // carried adjoint (registers) and the re-walk's chunk-start state -> LDS operands, Grams
+      pf.store(g, a, sm, tid);
+      // carried adjoint (registers) and the saved chunk-start state -> LDS operands, Grams
       float gss = 0.f, gsz = 0.f, gzz = 0.f;
 #pragma unroll
       for (int j = 0; j < NT2; ++j) {
@@ -371,8 +377,8 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = (tile / NTD) * 16 + 4 * (lane >> 4) + r, k = (tile % NTD) * 16 + (lane & 15);
-          const float sv = clamp_in ? clamp100(s_in[j][r]) : s_in[j][r];
-          const float zv = z_in[j][r];
+          const float sv = clamp_in ? clamp100(pf.s_in[j][r]) : pf.s_in[j][r];
+          const float zv = g.momentum ? pf.z_in[j][r] : 0.f;
           gss += dS[j][r] * sv; gsz += dS[j][r] * zv; gzz += dZ[j][r] * zv;
           sm.dSe[i][k] = from_f32<T>(dS[j][r]);
           sm.dZe[i][k] = from_f32<T>(dZ[j][r]);
@@ -386,14 +392,14 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         gss += __shfl_xor(gss, off); gsz += __shfl_xor(gsz, off); gzz += __shfl_xor(gzz, off);
       }
       if (lane == 0) { sm.red[wave][0] = gss; sm.red[wave][1] = gsz; sm.red[wave][2] = gzz; }
+      if (c - 1 >= c_begin) pf.load(g, a, p, bh, c - 1, rw + (size_t)(c - 1) * 2 * D * D, tid, lane, wave);
     }
     __syncthreads();
-    if (tid == 0) {
-      for (int q = 0; q < 3; ++q) {
-        float sum = 0.f;
-        for (int w = 0; w < kSegWaves; ++w) sum += sm.red[w][q];
-        sm.gram[q] = sum;
-      }
+    if (tid < 3) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kSegWaves; ++w) sum += sm.red[w][tid];
+      sm.gram[tid] = sum;
     }
     if (bufchunk) {   // <dS_end, B_s>, <dZ_end, B_s> for the dense buffer sources
       for (int s = 0; s < H; ++s) {
@@ -441,7 +447,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         }
       }
     } else if (lane <= CH) {
-      decay_column<CH>(sm.tab, sm.sc, lane, sm.A1, sm.K1, sm.B1);
+      decay_column<CH>(sm.tab, sm.sc, lane, sm.B1);
     }
     __syncthreads();
     // G2 / G3: Kmat = psi phi^T, K3 = dy delta -> Q^T, Q', Q'^T, Lm
@@ -583,7 +589,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = m0 + 4 * (lane >> 4) + r;
-          dpsi[r] = sm.A1[t] * as[r] - sm.K1[t] * az[r] - aq[r];
+          dpsi[r] = sm.sc.acoef[t] * as[r] - sm.sc.kcoef[t] * az[r] - aq[r];
           const float ps = to_f32(sm.psi[t][k]);
           fsp[r] = as[r] * ps;
           fzp[r] = az[r] * ps;
@@ -780,7 +786,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
       const int t = lane % CH, part = lane / CH;
       const int nterm = 3 + (g.gate_mode != GATE_NONE ? e : 0);
       const float gss = sm.gram[0], gsz = sm.gram[1], gzz = sm.gram[2];
-      const float am1 = sm.A1[t], km1 = sm.K1[t], bm1 = sm.B1[t], b0 = sm.B1[t + 1];
+      const float am1 = sm.sc.acoef[t], km1 = sm.sc.kcoef[t], bm1 = sm.B1[t], b0 = sm.B1[t + 1];
       const float Aend = sm.tab.A[t + 1][CH - 1], Bend = sm.tab.B[t + 1][CH - 1], Cend = sm.tab.C[t + 1][CH - 1];
       for (int term = wave; term < nterm; term += kSegWaves) {
         const float* W = term < 2 ? &sm.tab.A[t + 1][0] : &sm.tab.C[t + 1][0];
@@ -966,9 +972,7 @@ __global__ __launch_bounds__(kThreads) void k_seg_reduce_dsref(int nseg, int n, 
 
 template <typename T, int CH, int D>
 size_t bwd_seg_smem_bytes(int H) {
-  const size_t main_sz = sizeof(BwdSegSmem<T, CH, D>) + (size_t)2 * H * 2 * D * sizeof(float);
-  const size_t rewalk = sizeof(SegFwdSmem<T, CH, D, false>);
-  return main_sz > rewalk ? main_sz : rewalk;
+  return sizeof(BwdSegSmem<T, CH, D>) + (size_t)2 * H * 2 * D * sizeof(float);
 }
 
 template <typename T, int CH, int D>

@@ -21,7 +21,7 @@ struct BwdSegPtrs {
   const float* final_raw;    // forward raw S_{T-1} [BH][D][D]
   float* adj_agg;            // [BH][nseg][agg_stride]: L, K, a, kappa, b
   float* seg_adj;            // [BH][nseg][2][D][D] adjoint (dS, dZ) at each segment end
-  float* rw;                 // [BH][nseg][Gb][2][D][D] raw chunk-start states of the re-walk
+  const float* rw;           // [BH][nc][2][D][D] raw chunk-start states (written by the forward walk)
   float* dsref_part;         // [BH][nseg][D][D]
   float* tail_part;          // [BH][nseg][H][2D]  (dv | dphi) partial of a segment's last H tokens
   float* halo_part;          // [BH][nseg][H][2D]  partial from the segment's first chunk for the previous segment
@@ -90,14 +90,17 @@ struct ChunkScalars {
   float kcoef[CH];                      // kappa_{tau-1}
   float endc[4];                        // a_end, kappa_end, b_end
   float wsend[SPM], wzend[SPM];         // Ws[s, end], Wz[s, end]
+  float wsmid[SPM], wzmid[SPM];         // Ws[s, Lmid-1], Wz[s, Lmid-1] (zero when Lmid == 0)
+  float midc[4];                        // a, kappa, b after token Lmid-1
 };
 
 // Per-chunk coefficient record in HBM (fp32), written by k_chunk_coef for every chunk of every row:
-// acoef[CH], kcoef[CH], endc[4], wsend[SPM], wzend[SPM] - the layout of ChunkScalars from acoef on.
+// acoef[CH], kcoef[CH], endc[4], wsend[SPM], wzend[SPM], wsmid[SPM], wzmid[SPM], midc[4] - the
+// layout of ChunkScalars from acoef on.
 template <int CH>
 struct CoefRec {
   static constexpr int SPM = CH + kHaloPad;
-  static constexpr int SIZE = 2 * CH + 4 + 2 * SPM;   // floats
+  static constexpr int SIZE = 2 * CH + 8 + 4 * SPM;   // floats
   static_assert(SIZE % 4 == 0, "record copied as float4");
 };
 
@@ -116,15 +119,14 @@ struct DecayTab {
 };
 
 // Column c (0 <= c <= CH) of the decay tables; the thread of column 0 also writes the prefix
-// coefficients A1[t] = a_{t-1}, K1[t] = kappa_{t-1}, B1[t] = b_{t-1} (t = 0..CH; A1[0] = B1[0] = 1,
-// K1[0] = 0) and sc.acoef / sc.kcoef / sc.endc.
+// coefficients sc.acoef[t] = a_{t-1}, sc.kcoef[t] = kappa_{t-1}, sc.endc and B1[t] = b_{t-1}
+// (t = 0..CH, B1[0] = 1).
 template <int CH>
-__device__ __forceinline__ void decay_column(DecayTab<CH>& tab, ChunkScalars<CH>& sc, int c, float* A1, float* K1,
-                                             float* B1) {
+__device__ __forceinline__ void decay_column(DecayTab<CH>& tab, ChunkScalars<CH>& sc, int c, float* B1) {
   static_assert(CH % 8 == 0, "decay table groups");
   const int tp = c - 1;
   float a = 1.f, b = 1.f, m = 0.f;
-  if (c == 0) { A1[0] = 1.f; K1[0] = 0.f; B1[0] = 1.f; sc.acoef[0] = 1.f; sc.kcoef[0] = 0.f; }
+  if (c == 0) { B1[0] = 1.f; sc.acoef[0] = 1.f; sc.kcoef[0] = 0.f; }
   for (int t0 = 0; t0 < CH; t0 += 8) {
     float al8[8], et8[8], be8[8];
 #pragma unroll
@@ -144,7 +146,7 @@ __device__ __forceinline__ void decay_column(DecayTab<CH>& tab, ChunkScalars<CH>
       tab.B[c][t] = on ? b : 0.f;
       tab.C[c][t] = on ? m : 0.f;
       if (c == 0) {
-        A1[t + 1] = a; K1[t + 1] = m; B1[t + 1] = b;
+        B1[t + 1] = b;
         if (t + 1 < CH) { sc.acoef[t + 1] = a; sc.kcoef[t + 1] = m; }
       }
     }
@@ -157,6 +159,7 @@ __device__ __forceinline__ void decay_column(DecayTab<CH>& tab, ChunkScalars<CH>
 //                        (w(s,t) = window weight of source s at target t), writing Ws[s, t-1] to
 //                        wsh[t * ldw + s] when WSH and the end values to wsend / wzend;
 //   ci == 127 (PREFIX):  b_t = beta_t b_{t-1}, a_t = alpha_t a_{t-1}, kappa_t = alpha_t kappa_{t-1} + eta_t b_t.
+// The values after token g.Lmid - 1 are also kept (wsmid, wzmid, midc) when g.Lmid > 0.
 // The scalars of 8 steps are read into registers before the 8 dependent steps run, so the chain
 // waits on LDS once per group instead of once per step.
 template <int CH, bool WSH, bool PREFIX = true, typename WT = float>
@@ -173,7 +176,8 @@ __device__ __forceinline__ void chunk_coefficients(const Geom& g, ChunkScalars<C
     const int s = ci;
     const float us = g.gate_mode == GATE_TOKEN ? sc.ug[s] : 1.f;
     const bool lag = g.gate_mode == GATE_LAG;
-    float ws = 0.f, wz = 0.f;
+    float ws = 0.f, wz = 0.f, wsm = 0.f, wzm = 0.f;
+    const int tm = g.Lmid - 1;
     for (int t0 = 0; t0 < CH; t0 += 8) {
       float al8[8], et8[8], be8[8], w8[8];
 #pragma unroll
@@ -189,12 +193,17 @@ __device__ __forceinline__ void chunk_coefficients(const Geom& g, ChunkScalars<C
         if constexpr (WSH) wsh[(t0 + u) * ldw + s] = static_cast<WT>(ws);
         wz = be8[u] * wz + w8[u];
         ws = al8[u] * ws + et8[u] * wz;
+        wsm = (t0 + u == tm) ? ws : wsm;
+        wzm = (t0 + u == tm) ? wz : wzm;
       }
     }
     sc.wsend[s] = ws;
     sc.wzend[s] = wz;
+    sc.wsmid[s] = wsm;
+    sc.wzmid[s] = wzm;
   } else if (PREFIX && ci == 127) {
-    float ac = 1.f, kc = 0.f, bc = 1.f;
+    float ac = 1.f, kc = 0.f, bc = 1.f, am = 0.f, km = 0.f, bm = 0.f;
+    const int tm = g.Lmid - 1;
     for (int t0 = 0; t0 < CH; t0 += 8) {
       float al8[8], et8[8], be8[8];
 #pragma unroll
@@ -206,9 +215,13 @@ __device__ __forceinline__ void chunk_coefficients(const Geom& g, ChunkScalars<C
         bc = be8[u] * bc;
         ac = al8[u] * ac;
         kc = al8[u] * kc + et8[u] * bc;
+        am = (t0 + u == tm) ? ac : am;
+        km = (t0 + u == tm) ? kc : km;
+        bm = (t0 + u == tm) ? bc : bm;
       }
     }
-    sc.endc[0] = ac; sc.endc[1] = kc; sc.endc[2] = bc;
+    sc.endc[0] = ac; sc.endc[1] = kc; sc.endc[2] = bc; sc.endc[3] = 0.f;
+    sc.midc[0] = am; sc.midc[1] = km; sc.midc[2] = bm; sc.midc[3] = 0.f;
   }
 }
 

@@ -1,5 +1,4 @@
-// seg_fwd.h - the segment walk of the forward recurrence, shared by the forward kernels and the
-// backward pass's forward re-walk.
+// seg_fwd.h - the segment walk of the forward recurrence (aggregate pass and full walk).
 //
 // Every chunk is a handful of small GEMMs separated by workgroup barriers; with 8 waves per CU the
 // barriers and LDS latency, not the matrix cores, set the pace. All tile counts and k extents are
@@ -16,9 +15,8 @@ namespace atlas {
 template <typename T, int CH, int D, bool FULL>
 struct SegFwdSmem {
   static constexpr int SPM = CH + kHaloPad;
-  T phi[SPM][D + 8];
-  T phiTs[D][SPM + 8];       // Ws_end[s] * phi[s][k], stored [k][s]
-  T phiTz[D][SPM + 8];       // Wz_end[s] * phi[s][k], stored [k][s]
+  T phi[SPM][D + 8];         // phi[s][k]
+  T phiT[D][SPM + 8];        // phi^T[k][s] (G4's B operand)
   T delta[D][SPM + 8];       // v staged by the loads as [i][s], then delta[i][s]
   T sref[D][D + 8];
   ChunkScalars<CH> sc;
@@ -45,6 +43,7 @@ struct ChunkPrefetch {
   static constexpr int NV_WSH = FULL ? (CH * SPM / 8 + kSegThreads - 1) / kSegThreads : 0;
   static_assert(REC4 <= kSegThreads && SPM % 8 == 0, "record / wsh prefetch");
   Vec8<T> phi[NV_PHI];
+  Vec8<T> kt[NV_PHI];        // k again with consecutive lanes on consecutive sources (phi^T store)
   Vec8<T> vv[NV_PHI];
   Vec8<T> psi[NV_PSI > 0 ? NV_PSI : 1];
   Vec8<T> wsv[NV_WSH > 0 ? NV_WSH : 1];
@@ -81,11 +80,14 @@ struct ChunkPrefetch {
         phi[j] = vec8_load(a.k + (ok ? tb + p : r0) * D + c8 * 8);
         ok_phi |= (ok ? 1u : 0u) << j;
       }
-      {   // v: consecutive lanes take consecutive sources (conflict-free transposed LDS store)
+      {   // k (for phi^T) and v: consecutive lanes take consecutive sources (conflict-free
+          // transposed LDS stores)
         const int s = v % SPM, c8 = v / SPM;
         const int p = t0 - H + s;
         const bool ok = c8 < D / 8 && s < H + L && p >= 0;
-        vv[j] = vec8_load(a.v + (ok ? tb + p : r0) * D + (ok ? c8 * 8 : 0));
+        const size_t off = (ok ? tb + p : r0) * D + (ok ? c8 * 8 : 0);
+        kt[j] = vec8_load(a.k + off);
+        vv[j] = vec8_load(a.v + off);
         ok_v |= (ok ? 1u : 0u) << j;
       }
     }
@@ -138,9 +140,15 @@ struct ChunkPrefetch {
       {
         const int s = v % SPM, c8 = v / SPM;
         if (c8 < D / 8) {
-          const Vec8<T> x = vv[j].masked((ok_v >> j) & 1u);
+          const bool ok = (ok_v >> j) & 1u;
+          const Vec8<T> x = vv[j].masked(ok);
+          Vec8<T> y = kt[j].masked(ok);
+          if (g.map_mode == MAP_ELEMENTWISE) y = y.mapped(g.map_deg);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) sm.delta[c8 * 8 + e][s] = x.v[e];
+          for (int e = 0; e < 8; ++e) {
+            sm.delta[c8 * 8 + e][s] = x.v[e];
+            sm.phiT[c8 * 8 + e][s] = y.v[e];
+          }
         }
       }
     }
@@ -180,15 +188,27 @@ struct ChunkPrefetch {
   }
 };
 
-enum WalkMode { WALK_AGG = 0, WALK_FULL = 1, WALK_REWALK = 2 };
+enum WalkMode { WALK_AGG = 0, WALK_FULL = 1 };
+
+// Fragment f with its k values scaled by w[k] (w: the KL weights of this lane's k slots).
+template <typename T>
+__device__ __forceinline__ typename MM<T>::frag frag_scale(typename MM<T>::frag f, const float* w) {
+  if constexpr (MM<T>::KL == 1) {
+    return f * w[0];
+  } else {
+    typename MM<T>::frag r;
+#pragma unroll
+    for (int e = 0; e < MM<T>::KL; ++e) r[e] = static_cast<T>(static_cast<float>(f[e]) * w[e]);
+    return r;
+  }
+}
 
 // Segment walk.
 //   WALK_AGG:    zero initial state; writes the segment aggregate (a, kappa, b, U, V) to agg.
 //   WALK_FULL:   starts from seg_states[seg] (the segment scan folded the preceding aggregates),
-//                walks the chunks with the true state and writes y (and S_T, Z_T, the raw S_{T-1}).
-//   WALK_REWALK: starts from seg_states[seg] (chunk length may differ from the forward's) and
-//                writes the raw state at the start of every chunk of the segment to rw (the
-//                backward pass walks them in reverse); no y.
+//                walks the chunks with the true state and writes y (and S_T, Z_T, the raw S_{T-1}),
+//                and the raw state at every backward-chunk boundary to rw ([BH][ncb][2][D][D]):
+//                the chunk start and, when g.Lmid > 0, the state after token Lmid - 1.
 // The chunk coefficients (a, kappa, end weights, Ws[s, t-1]) come precomputed from k_chunk_coef
 // (coef: [BH][nc] records, wsh_all: [BH][nc][CH][SPM], full walk only) with the prefetch.
 // Wave roles per chunk: P1 all waves run G1 (and G2 for the full walk); P3 waves 0-3 run G3 (y)
@@ -200,7 +220,6 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
                                             const float* coef, const T* wsh_all, unsigned char* smem_raw) {
   constexpr bool AGG = MODE == WALK_AGG;
   constexpr bool FULL = MODE == WALK_FULL;
-  constexpr bool REWALK = MODE == WALK_REWALK;
   typedef SegFwdSmem<T, CH, D, FULL> Sm;
   Sm& sm = *reinterpret_cast<Sm*>(smem_raw);
   constexpr int SPM = Sm::SPM;
@@ -227,11 +246,6 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
 #pragma unroll
     for (int r = 0; r < 4; ++r) { Sr[n][r] = 0.f; Zr[n][r] = 0.f; }
   float seg_a = 1.f, seg_k = 0.f, seg_b = 1.f;   // aggregate transition (AGG)
-  float Sraw[NTD][4];                             // raw (pre-clamp) end state of the last chunk
-#pragma unroll
-  for (int n = 0; n < NTD; ++n)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Sraw[n][r] = 0.f;
 
   if constexpr (!AGG) {
     // segment-start state (written by the segment scan)
@@ -272,15 +286,17 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
     const int t1 = min(g.T, t0 + g.Lc);
     const int L = t1 - t0;
     const bool bufchunk = (c == 0) && g.has_buf;
-    if constexpr (REWALK) {
-      if (owns) {
-        float* dst = rw + (size_t)(c - c_begin) * 2 * D * D;
+    const int rb = g.Lmid > 0 ? 2 : 1;        // backward chunks per forward chunk
+    if constexpr (FULL) {
+      // the segment's start state (later chunk starts are written as the previous chunk ends)
+      if (owns && c == c_begin) {
+        float* dst = rw + ((size_t)bh * g.ncb + (size_t)c * rb) * 2 * D * D;
 #pragma unroll
         for (int n = 0; n < NTD; ++n)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
-            dst[(size_t)i * D + k] = c == c_begin ? Sr[n][r] : Sraw[n][r];
+            dst[(size_t)i * D + k] = Sr[n][r];
             dst[(size_t)D * D + (size_t)i * D + k] = Zr[n][r];
           }
       }
@@ -339,39 +355,23 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
     }
     __syncthreads();
 
-    // ---- P2: Q epilogue, scaled phi^T for G4 (all waves)
+    // ---- P2 (full walk): Q epilogue
     if constexpr (FULL) {
-      {
 #pragma unroll
-        for (int j = 0; j < PER2; ++j) {
-          const int tt = wave + NGW * j;
-          if (NT2 % NGW == 0 || tt < NT2) {
-            const int m0 = (tt / NTS) * 16, n0 = (tt % NTS) * 16;
-            const int s = n0 + (lane & 15);
+      for (int j = 0; j < PER2; ++j) {
+        const int tt = wave + NGW * j;
+        if (NT2 % NGW == 0 || tt < NT2) {
+          const int m0 = (tt / NTS) * 16, n0 = (tt % NTS) * 16;
+          const int s = n0 + (lane & 15);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int t = m0 + 4 * (lane >> 4) + r;
-              sm.Q[t][s] = from_f32<T>(kacc[j][r] * to_f32(sm.wsh[t][s]));
-            }
+          for (int r = 0; r < 4; ++r) {
+            const int t = m0 + 4 * (lane >> 4) + r;
+            sm.Q[t][s] = from_f32<T>(kacc[j][r] * to_f32(sm.wsh[t][s]));
           }
         }
       }
+      __syncthreads();
     }
-    {
-      // consecutive lanes take consecutive sources: conflict-free transposed stores
-      constexpr int NPT = (SPM * D + kSegThreads - 1) / kSegThreads;
-#pragma unroll
-      for (int j = 0; j < NPT; ++j) {
-        const int idx = tid + j * kSegThreads;
-        const int s = idx % SPM, k = idx / SPM;
-        if (k < D) {
-          const float x = to_f32(sm.phi[s][k]);
-          sm.phiTs[k][s] = from_f32<T>(sm.sc.wsend[s] * x);
-          sm.phiTz[k][s] = from_f32<T>(sm.sc.wzend[s] * x);
-        }
-      }
-    }
-    __syncthreads();
 
     // ---- P3: G3 (waves 0-3, full walk) | G4 + state update (waves 4-7)
     if (FULL && wave < 4) {
@@ -421,20 +421,71 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
         }
       }
     } else if (owns) {
+      // G4: U = -delta diag(Ws_end) phi^T, V = delta diag(Wz_end) phi^T, the end weights applied to the
+      // delta fragments in registers; the full walk also forms the state after token Lmid - 1.
       const float a_end = sm.sc.endc[0], k_end = sm.sc.endc[1], b_end = sm.sc.endc[2];
       const bool do_clamp = !AGG && clamp_after(g, t1);
+      const bool mid = FULL && g.Lmid > 0 && L > g.Lmid;
       const int m0 = mt * 16;
-      typename M::frag fa[SPM / M::KS];
+      constexpr int NKS = SPM / M::KS;
+      if constexpr (FULL) {
+        if (mid) {   // state after token Lmid - 1 (never a clamp point), from the chunk-start state
+          float* rw_mid = rw + ((size_t)bh * g.ncb + (size_t)c * rb + 1) * 2 * D * D;
+          typename M::frag fsm[NKS], fzm[NKS];
 #pragma unroll
-      for (int kk = 0; kk < SPM / M::KS; ++kk) fa[kk] = frag_ld_row<T>(&sm.delta[0][0], SPM + 8, m0, kk * M::KS);
-#pragma unroll 1
+          for (int kk = 0; kk < NKS; ++kk) {
+            const typename M::frag fd = frag_ld_row<T>(&sm.delta[0][0], SPM + 8, m0, kk * M::KS);
+            const int sb = kk * M::KS + (lane >> 4) * M::KL;
+            fsm[kk] = frag_scale<T>(fd, &sm.sc.wsmid[sb]);
+            fzm[kk] = frag_scale<T>(fd, &sm.sc.wzmid[sb]);
+          }
+#pragma unroll
+          for (int n = 0; n < NTD; ++n) {
+            const int n0 = n * 16;
+            f32x4 aum = zero4(), avm = zero4();
+#pragma unroll
+            for (int kk = 0; kk < NKS; ++kk) {
+              const typename M::frag fb = frag_ld_row<T>(&sm.phiT[0][0], SPM + 8, n0, kk * M::KS);
+              aum = M::mma(fsm[kk], fb, aum);
+              avm = M::mma(fzm[kk], fb, avm);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int i = m0 + 4 * (lane >> 4) + r, k = n0 + (lane & 15);
+              float Um = -aum[r], Vm = avm[r];
+              if (bufchunk) {
+                for (int s = 0; s < H; ++s) {
+                  const float b = a.buf_in[(((size_t)bh * H + s) * D + i) * D + k];
+                  Um -= sm.sc.wsmid[s] * b;
+                  Vm += sm.sc.wzmid[s] * b;
+                }
+              }
+              rw_mid[(size_t)i * D + k] = sm.sc.midc[0] * Sr[n][r] - sm.sc.midc[1] * Zr[n][r] + Um;
+              rw_mid[(size_t)D * D + (size_t)i * D + k] = g.momentum ? (sm.sc.midc[2] * Zr[n][r] + Vm) : 0.f;
+            }
+          }
+        }
+      }
+      typename M::frag fs[NKS], fz[NKS];
+#pragma unroll
+      for (int kk = 0; kk < NKS; ++kk) {
+        const typename M::frag fd = frag_ld_row<T>(&sm.delta[0][0], SPM + 8, m0, kk * M::KS);
+        const int sb = kk * M::KS + (lane >> 4) * M::KL;
+        fs[kk] = frag_scale<T>(fd, &sm.sc.wsend[sb]);
+        fz[kk] = frag_scale<T>(fd, &sm.sc.wzend[sb]);
+      }
+      // raw end state -> the next chunk's saved start state (within the segment: the next segment's
+      // workgroup writes its own start state, from the segment scan)
+      float* rw_next = (FULL && c + 1 < c_end) ? rw + ((size_t)bh * g.ncb + (size_t)(c + 1) * rb) * 2 * D * D : nullptr;
+#pragma unroll
       for (int n = 0; n < NTD; ++n) {
         const int n0 = n * 16;
         f32x4 au = zero4(), av = zero4();
 #pragma unroll
-        for (int kk = 0; kk < SPM / M::KS; ++kk) {
-          au = M::mma(fa[kk], frag_ld_row<T>(&sm.phiTs[0][0], SPM + 8, n0, kk * M::KS), au);
-          av = M::mma(fa[kk], frag_ld_row<T>(&sm.phiTz[0][0], SPM + 8, n0, kk * M::KS), av);
+        for (int kk = 0; kk < NKS; ++kk) {
+          const typename M::frag fb = frag_ld_row<T>(&sm.phiT[0][0], SPM + 8, n0, kk * M::KS);
+          au = M::mma(fs[kk], fb, au);
+          av = M::mma(fz[kk], fb, av);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -449,7 +500,10 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
           }
           const float Sn = a_end * Sr[n][r] - k_end * Zr[n][r] + U;
           const float Zn = g.momentum ? (b_end * Zr[n][r] + V) : 0.f;
-          Sraw[n][r] = Sn;
+          if (FULL && rw_next) {
+            rw_next[(size_t)i * D + k] = Sn;
+            rw_next[(size_t)D * D + (size_t)i * D + k] = Zn;
+          }
           Sr[n][r] = do_clamp ? clamp100(Sn) : Sn;
           Zr[n][r] = Zn;
         }

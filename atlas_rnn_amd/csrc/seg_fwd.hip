@@ -9,7 +9,8 @@
 //   k_fwd_seg_scan: one thread per state element (i, k) of a row folds the aggregates in segment
 //                   order from (S0, Z0), writing every segment-start state (kept for the backward).
 //   k_fwd_seg     : walk the segment's chunks again from its start state, producing y (and S_T,
-//                   Z_T in the last segment).
+//                   Z_T in the last segment) and the raw state at every backward-chunk boundary
+//                   (kept for the backward pass, which therefore never re-walks the forward).
 // With clamp_every > 0 the clamp at scan_chunk_len boundaries is not affine, so the caller uses a
 // single segment (an exact sequential walk over all chunks).
 //
@@ -67,15 +68,15 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg_scan(const Geom g, const f
 
 template <typename T, int CH, int D>
 __global__ __launch_bounds__(kSegThreads) void k_fwd_seg(const Geom g, const FwdPtrs<T> a, const SegGeom sg,
-                                                           const float* seg_states, float* final_raw,
+                                                           const float* seg_states, float* rw, float* final_raw,
                                                            const float* coef, const T* wsh) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  fwd_segment<T, CH, D, WALK_FULL>(g, a, sg, nullptr, seg_states, nullptr, final_raw, coef, wsh, smem_raw);
+  fwd_segment<T, CH, D, WALK_FULL>(g, a, sg, nullptr, seg_states, rw, final_raw, coef, wsh, smem_raw);
 }
 
 template <typename T, int CH, int D>
 hipError_t launch_fwd_seg(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg, float* agg, float* seg_states,
-                          float* final_raw, float* coef, T* wsh, hipStream_t stream) {
+                          float* rw, float* final_raw, float* coef, T* wsh, hipStream_t stream) {
   hipError_t err = launch_chunk_coef<T, CH>(g, a.decay, a.lr, a.beta, a.gate, coef, wsh, KID_FWD_COEF, stream);
   if (err != hipSuccess) return err;
   if (sg.nseg > 1) {
@@ -100,14 +101,14 @@ hipError_t launch_fwd_seg(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg,
   if (err != hipSuccess) return err;
   prof_begin(KID_FWD_WALK, stream);
   hipLaunchKernelGGL((k_fwd_seg<T, CH, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg,
-                     (const float*)seg_states, final_raw, (const float*)coef, (const T*)wsh);
+                     (const float*)seg_states, rw, final_raw, (const float*)coef, (const T*)wsh);
   prof_end(KID_FWD_WALK, stream);
   return hipGetLastError();
 }
 
 #define ATLAS_INST_FWD_SEG(T, CH, D) \
   template hipError_t launch_fwd_seg<T, CH, D>(const Geom&, const FwdPtrs<T>&, const SegGeom&, float*, float*, float*, \
-                                               float*, T*, hipStream_t);
+                                               float*, float*, T*, hipStream_t);
 
 ATLAS_INST_FWD_SEG(bf16, 64, 64)
 ATLAS_INST_FWD_SEG(float, 32, 64)

@@ -74,19 +74,18 @@ def test_sizes(lib):
     p = _prob()
     st = 64 * 64 * 4
     saved = lib.atlas_mem_saved_bytes(ctypes.byref(p))
-    # at least: segment-start (S, Z) of >= 1 segment per row, one aggregate (U, V) per segment, raw S_{T-1}
-    assert saved >= 32 * (2 * st + 2 * st + st)
-    # the saved buffer is per segment, not per chunk: far below one state per 64-token chunk
-    assert saved < 32 * (4096 // 64) * 2 * st
+    # the forward keeps the raw (S, Z) at every backward-chunk boundary (32 tokens for bf16) plus the
+    # segment states and the raw S_{T-1}
+    assert saved >= 32 * (4096 // 32) * 2 * st + 32 * st
     assert saved % 256 == 0
     ws = lib.atlas_mem_bwd_workspace_bytes(ctypes.byref(p))
     assert ws > 0 and ws % 256 == 0
-    pf = _prob(dtype=_lib.DT_F32)
-    assert lib.atlas_mem_saved_bytes(ctypes.byref(pf)) >= 32 * 5 * st
-    # clamping every 32 tokens forbids folding across clamps: one segment per row, one state per chunk
+    pf = _prob(dtype=_lib.DT_F32)   # fp32: 16-token backward chunks
+    assert lib.atlas_mem_saved_bytes(ctypes.byref(pf)) >= 32 * (4096 // 16) * 2 * st
+    # clamping every 32 tokens forbids folding across clamps: one segment per row
     pc = _prob(clamp_every=32)
     assert lib.atlas_mem_validate(ctypes.byref(pc)) == 0
-    assert lib.atlas_mem_saved_bytes(ctypes.byref(pc)) >= 32 * 2 * st
+    assert lib.atlas_mem_saved_bytes(ctypes.byref(pc)) >= 32 * (4096 // 32) * 2 * st
 
 
 def test_strerror(lib):

@@ -42,6 +42,9 @@ CASES = [
     Case("bf16_multiseg_short_chunk", BH=40, T=1100, d=32, e=16, gate='lag', momentum=True, buffer=True,
          states=0.1, dtype=BF16, seed=13),
     Case("fp32_multiseg", BH=40, T=300, d=32, e=5, gate='token', momentum=True, buffer=True, states=0.2, seed=14),
+    # the largest window (33) at d = 64: the backward's LDS footprint is at its maximum
+    Case("bf16_max_window_d64", BH=2, T=150, d=64, e=33, gate='lag', momentum=True, buffer=True, states=0.1,
+         dtype=BF16, seed=15),
 ]
 
 
