@@ -13,6 +13,17 @@ from .functional import (  # noqa: F401
     assoc_scan,
     AssocScan,
     window_sum,
+    affine_associative_scan,
+)
+from .rnn_memory import (  # noqa: F401
+    RNNMemState,
+    state_detach,
+    PolynomialFeatureMap,
+    MultiheadRMSNorm,
+    RNNMemoryCell,
+    OmegaRNNMemoryCell,
+    RNNMemory,
+    OmegaRNNMemory,
 )
 
 __all__ = [
@@ -23,4 +34,13 @@ __all__ = [
     "assoc_scan",
     "AssocScan",
     "window_sum",
+    "affine_associative_scan",
+    "RNNMemState",
+    "state_detach",
+    "PolynomialFeatureMap",
+    "MultiheadRMSNorm",
+    "RNNMemoryCell",
+    "OmegaRNNMemoryCell",
+    "RNNMemory",
+    "OmegaRNNMemory",
 ]

@@ -39,6 +39,8 @@ EXPORTED_SYMBOLS = (
     "atlas_scan_fwd",
     "atlas_scan_bwd",
     "atlas_window_sum",
+    "atlas_affine_scan_fwd",
+    "atlas_affine_scan_bwd",
     "atlas_mem_profile_enable",
     "atlas_mem_profile_read",
     "atlas_mem_kernel_name",
@@ -108,6 +110,10 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_scan_bwd.argtypes = [i32, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.atlas_window_sum.restype = i32
     lib.atlas_window_sum.argtypes = [i32, i64, i64, i64, i32, i32, vp, vp, vp]
+    lib.atlas_affine_scan_fwd.restype = i32
+    lib.atlas_affine_scan_fwd.argtypes = [i32, i32, i32, i32, vp, vp, vp, vp, vp]
+    lib.atlas_affine_scan_bwd.restype = i32
+    lib.atlas_affine_scan_bwd.argtypes = [i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.atlas_mem_profile_enable.restype = i32
     lib.atlas_mem_profile_enable.argtypes = [i32]
     lib.atlas_mem_profile_read.restype = i32

@@ -334,6 +334,48 @@ def window_sum(x: Tensor, window: int) -> Tensor:
     return _WindowSumFn.apply(x.to(dt).contiguous(), int(window))
 
 
+class _AffineScanFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, A, B, prev):
+        lib = _lib.load()
+        n, t, d = A.shape[0], A.shape[1], A.shape[2]
+        r = B.shape[2]
+        out = torch.empty_like(B)
+        _lib.check(lib.atlas_affine_scan_fwd(n, t, r, d, _ptr(A), _ptr(B), _ptr(prev), _ptr(out), _stream(A.device)),
+                   "atlas_affine_scan_fwd")
+        ctx.save_for_backward(A, out, prev)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        lib = _lib.load()
+        A, out, prev = ctx.saved_tensors
+        n, t, d = A.shape[0], A.shape[1], A.shape[2]
+        r = out.shape[2]
+        dout = dout.contiguous().float()
+        dA = torch.empty_like(A)
+        dB = torch.empty_like(out)
+        dprev = torch.empty_like(prev) if prev is not None else None
+        _lib.check(lib.atlas_affine_scan_bwd(n, t, r, d, _ptr(A), _ptr(out), _ptr(prev), _ptr(dout), _ptr(dA), _ptr(dB),
+                                             _ptr(dprev), _stream(A.device)), "atlas_affine_scan_bwd")
+        return dA, dB, dprev
+
+
+def affine_associative_scan(A: Tensor, B: Tensor, *, prev: Tensor | None = None, remove_prev: bool = False) -> Tensor:
+    """H_t = H_{t-1} A_t + B_t (atlas_pytorch/affine_scan.py:36-158): A [N,T,D,D], B [N,T,R,D],
+    prev [N,R,D]. Returns [N,T,R,D], or [N,T+1,R,D] led by prev when prev is given and not
+    remove_prev. Computed in fp32 (D, R <= 64); the result has B's dtype."""
+    _require_gpu(A, B, prev)
+    dt = B.dtype
+    A32 = A.float().contiguous()
+    B32 = B.float().contiguous()
+    p32 = prev.float().contiguous() if prev is not None else None
+    H = _AffineScanFn.apply(A32, B32, p32)
+    if prev is not None and not remove_prev:
+        H = torch.cat([p32[:, None], H], dim=1)
+    return H.to(dt)
+
+
 # ------------------------------------------------------------------------------------------
 # Preallocated plan: direct C-ABI calls for a fixed problem shape
 # ------------------------------------------------------------------------------------------
