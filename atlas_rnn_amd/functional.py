@@ -21,6 +21,7 @@ from torch import Tensor
 from . import _lib
 
 _DTYPES = {torch.float32: _lib.DT_F32, torch.bfloat16: _lib.DT_BF16}
+_KERNEL_DIMS = (32, 64)       # head dims the kernels are compiled for; smaller ones are zero-padded
 
 
 def _ptr(t: Tensor | None):
@@ -157,8 +158,9 @@ def memory_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor
                       S_ref: Tensor | None = None, S0: Tensor | None = None, Z0: Tensor | None = None,
                       buffer: Tensor | None = None, *, window: int = 1, map_mode: str = 'off',
                       map_degree: int = 1, clamp_every: int | None = None, clamp_final: bool = True):
-    """Memory-layer recurrence over [BH, T, d] inputs (see oracle/recurrence.py for the math).
+    """Memory-layer recurrence over [BH, T, d] inputs (atlas_pytorch/rnn_memory.py:605-730).
 
+    d_k == d_v <= 64; the kernels are built for 32 and 64, other head sizes are zero-padded.
     k, q: raw keys / queries [BH, T, d_k] (the elementwise polynomial map is applied inside);
     v [BH, T, d_v]; lr (eta), decay (alpha), beta [BH, T]; gate None | [BH, T] (per-token,
     reference omega_gate) | [BH, T, e] (per-lag); S_ref, S0, Z0 [BH, d_v, d_k];
@@ -173,6 +175,18 @@ def memory_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor
         S0 = torch.zeros(bh, dv, dk, device=dev, dtype=torch.float32)
     if S_ref is None:
         S_ref = S0
+    if dk == dv and dk < 64 and dk not in _KERNEL_DIMS:
+        # Zero feature columns leave the recurrence exact: the padded rows / columns of every
+        # state stay zero, the padded entries of y are zero and their gradients are dropped.
+        D = next(x for x in _KERNEL_DIMS if x > dk)
+        pad = D - dk
+        pv = lambda t: None if t is None else torch.nn.functional.pad(t, (0, pad))
+        pm = lambda t: None if t is None else torch.nn.functional.pad(t, (0, pad, 0, pad))
+        y, S_T, Z_T, B = memory_recurrence(pv(k), pv(q), pv(v), lr, decay, beta, gate, pm(S_ref), pm(S0), pm(Z0),
+                                           pm(buffer), window=window, map_mode=map_mode, map_degree=map_degree,
+                                           clamp_every=clamp_every, clamp_final=clamp_final)
+        return (y[..., :dk], S_T[..., :dk, :dk], None if Z_T is None else Z_T[..., :dk, :dk],
+                None if B is None else B[..., :dk, :dk])
     e = window
     cfg = RecurrenceConfig(window=e, map_mode=map_mode, map_degree=map_degree,
                            clamp_every=clamp_every, clamp_final=clamp_final)

@@ -45,6 +45,10 @@ CASES = [
     # the largest window (33) at d = 64: the backward's LDS footprint is at its maximum
     Case("bf16_max_window_d64", BH=2, T=150, d=64, e=33, gate='lag', momentum=True, buffer=True, states=0.1,
          dtype=BF16, seed=15),
+    # head sizes the kernels are not built for, zero-padded to 32 / 64 by the host wrapper
+    Case("fp32_d16_padded", BH=3, T=45, d=16, e=3, gate='token', momentum=True, buffer=True, states=0.2, seed=16),
+    Case("bf16_d48_padded", BH=2, T=70, d=48, e=2, gate='lag', momentum=True, buffer=True, states=0.1,
+         map_degree=2, dtype=BF16, seed=17),
 ]
 
 
