@@ -107,6 +107,37 @@ def cpu_baseline(x_cpu, sample_t=256, reps=3):
     return B * sample_t / med, cores, med
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_c3.md")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary (lines
+    `traffic: <kernel> <bytes>`, FETCH_SIZE + WRITE_SIZE scaled by the copy-kernel factor), or
+    None when the summary has no figure for it."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic:" and parts[1] == kernel:
+                    return int(parts[2])
+    except OSError:
+        return None
+    return None
+
+
+def calibrate_copy(nbytes=256 << 20, reps=5):
+    """A plain device-to-device copy of known size, for scaling the HBM counters
+    (FETCH_SIZE / WRITE_SIZE of this launch against nbytes read and nbytes written)."""
+    import torch
+    src = torch.empty(nbytes // 4, device="cuda", dtype=torch.float32).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "launches": reps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -114,7 +145,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-tokens", type=int, default=256)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a plain copy kernel of known size (HBM counter calibration)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the memory-layer recurrence shards over (batch, head) rows "
               "with no exchange, so there is no multi-GPU figure to report (use --gpus 1).", file=sys.stderr)
@@ -157,7 +193,7 @@ def main():
     dom_s = kernels[dom]["avg_us"] * 1e-6
     achieved = per_kernel[dom] / dom_s / 1e9
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": measured_traffic(dom),
                 "algorithmic_bytes_per_launch": per_kernel[dom], "avg_launch_us": round(kernels[dom]["avg_us"], 2)}
     step_gbs = step_bytes / (elapsed / args.steps) / 1e9
     out = {
