@@ -115,6 +115,45 @@ __device__ __forceinline__ typename MM<OT>::frag frag_ld_kscaled(const ST* p, in
   return f;
 }
 
+// Fragment of a matrix stored transposed in LDS: element (r, k) at p[k * ld + r].
+// bf16: two ds_read_b64_tr_b16 (gfx950 transpose loads) per lane instead of eight 2-byte reads.
+// Within each 16-lane group g = l >> 4, lane 16g + i supplies the address of the 4 elements
+// r0 + 4 (i % 4) .. +3 of row k0 + 8g + h + i / 4 (h = 0, then 4), and lane 16g + m receives
+// element m of the group's rows h + j, j < 4: A[r0 + m][k0 + 8g + h + j]. Reads exactly the
+// elements frag_ld(p, 1, ld, r0, k0) reads. Requires p in LDS, 8-byte aligned, ld % 4 == 0 and
+// r0 % 4 == 0. fp32: the plain strided load (one element per lane).
+template <typename OT>
+__device__ __forceinline__ typename MM<OT>::frag frag_ld_tr(const OT* p, int ld, int r0, int k0) {
+  if constexpr (MM<OT>::KL == 1) {
+    return frag_ld<OT>(p, 1, ld, r0, k0);
+  } else {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const int l = lane_id(), i = l & 15;
+    const OT* q = p + (k0 + 8 * (l >> 4) + (i >> 2)) * ld + r0 + 4 * (i & 3);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(q));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(q + 4 * ld));
+    const s16x8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(typename MM<OT>::frag, v);
+  }
+}
+
+// frag_ld_tr with each k value multiplied by s[k] (fp32) before rounding to OT.
+template <typename OT>
+__device__ __forceinline__ typename MM<OT>::frag frag_ld_tr_kscaled(const OT* p, int ld, int r0, int k0,
+                                                                   const float* s) {
+  typename MM<OT>::frag f = frag_ld_tr<OT>(p, ld, r0, k0);
+  const int kb = k0 + (lane_id() >> 4) * MM<OT>::KL;
+  if constexpr (MM<OT>::KL == 1) {
+    f = static_cast<OT>(to_f32(f) * s[kb]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < MM<OT>::KL; ++e) f[e] = static_cast<OT>(to_f32(f[e]) * s[kb + e]);
+  }
+  return f;
+}
+
 // Clamp of the reference (torch.clamp(-100, 100)) and its gradient mask (min <= x <= max).
 __device__ __forceinline__ float clamp100(float x) { return fminf(fmaxf(x, -100.f), 100.f); }
 __device__ __forceinline__ float clamp_mask(float x) { return (x >= -100.f && x <= 100.f) ? 1.f : 0.f; }

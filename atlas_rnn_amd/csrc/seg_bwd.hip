@@ -498,7 +498,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         }
 #pragma unroll
         for (int k0 = 0; k0 < CH; k0 += M::KS)
-          aq = M::mma(frag_ld<T>(&sm.dy[0][0], 1, D + 8, m0, k0), frag_ld_row<T>(&sm.u.g.QT[0][0], CH + 8, n0, k0), aq);
+          aq = M::mma(frag_ld_tr<T>(&sm.dy[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.u.g.QT[0][0], CH + 8, n0, k0), aq);
         if (valid) {
           const int s = n0 + (lane & 15);
           const float wz = sm.sc.wzend[s], ws = sm.sc.wsend[s];
@@ -544,7 +544,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
       f32x4 acc = zero4();
 #pragma unroll
       for (int k0 = 0; k0 < SPM; k0 += M::KS)
-        acc = M::mma(frag_ld_row<T>(&sm.u.g.dD[0][0], SPM + 8, m0, k0), frag_ld<T>(&sm.phi[0][0], 1, D + 8, n0, k0), acc);
+        acc = M::mma(frag_ld_row<T>(&sm.u.g.dD[0][0], SPM + 8, m0, k0), frag_ld_tr<T>(&sm.phi[0][0], D + 8, n0, k0), acc);
 #pragma unroll
       for (int r = 0; r < 4; ++r) dsr[j][r] += acc[r];
     }
@@ -560,8 +560,8 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         for (int k0 = 0; k0 < D; k0 += M::KS) {
           const typename M::frag fa = frag_ld_row<T>(&sm.dy[0][0], D + 8, m0, k0);
           if constexpr (SIL) {
-            as = M::mma(fa, frag_ld<T>(&sm.Sin[0][0], 1, D + 8, n0, k0), as);
-            az = M::mma(fa, frag_ld<T>(&sm.Zin[0][0], 1, D + 8, n0, k0), az);
+            as = M::mma(fa, frag_ld_tr<T>(&sm.Sin[0][0], D + 8, n0, k0), as);
+            az = M::mma(fa, frag_ld_tr<T>(&sm.Zin[0][0], D + 8, n0, k0), az);
           } else {
             typename M::frag fs;
             {
@@ -582,7 +582,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         }
 #pragma unroll
         for (int k0 = 0; k0 < SPM; k0 += M::KS)
-          aq = M::mma(frag_ld_row<T>(&sm.u.g.Qp[0][0], SPM + 8, m0, k0), frag_ld<T>(&sm.phi[0][0], 1, D + 8, n0, k0), aq);
+          aq = M::mma(frag_ld_row<T>(&sm.u.g.Qp[0][0], SPM + 8, m0, k0), frag_ld_tr<T>(&sm.phi[0][0], D + 8, n0, k0), aq);
         const int k = n0 + (lane & 15);
         f32x4 dpsi;
         float fsp[4], fzp[4];
@@ -647,7 +647,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
               for (int ee = 0; ee < M::KL; ++ee)
                 fa[ee] = static_cast<T>(to_f32(sm.dy[qb + ee][i]) * to_f32(sm.wsh[qb + ee][s]));
             }
-            acc = M::mma(fa, frag_ld<T>(&sm.psi[0][0], 1, D + 8, n0, k0), acc);
+            acc = M::mma(fa, frag_ld_tr<T>(&sm.psi[0][0], D + 8, n0, k0), acc);
           }
           if (valid) {
 #pragma unroll
@@ -674,13 +674,13 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
 #pragma unroll
         for (int k0 = 0; k0 < D; k0 += M::KS) {
           const typename M::frag fa = frag_ld_row<T>(&sm.deltaT[0][0], D + 8, m0, k0);
-          a1 = M::mma(fa, frag_ld<T>(&sm.dZe[0][0], 1, D + 8, n0, k0), a1);
-          a2 = M::mma(fa, frag_ld<T>(&sm.dSe[0][0], 1, D + 8, n0, k0), a2);
-          a4 = M::mma(frag_ld<T>(&sm.u.g.dD[0][0], 1, SPM + 8, m0, k0), frag_ld<T>(&sm.sref[0][0], 1, D + 8, n0, k0), a4);
+          a1 = M::mma(fa, frag_ld_tr<T>(&sm.dZe[0][0], D + 8, n0, k0), a1);
+          a2 = M::mma(fa, frag_ld_tr<T>(&sm.dSe[0][0], D + 8, n0, k0), a2);
+          a4 = M::mma(frag_ld_tr<T>(&sm.u.g.dD[0][0], SPM + 8, m0, k0), frag_ld_tr<T>(&sm.sref[0][0], D + 8, n0, k0), a4);
         }
 #pragma unroll
         for (int k0 = 0; k0 < CH; k0 += M::KS)
-          a3 = M::mma(frag_ld_row<T>(&sm.u.g.QpT[0][0], CH + 8, m0, k0), frag_ld<T>(&sm.psi[0][0], 1, D + 8, n0, k0), a3);
+          a3 = M::mma(frag_ld_row<T>(&sm.u.g.QpT[0][0], CH + 8, m0, k0), frag_ld_tr<T>(&sm.psi[0][0], D + 8, n0, k0), a3);
         if (valid) {
           const int k = n0 + (lane & 15);
 #pragma unroll
@@ -717,9 +717,9 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         f32x4 aa = zero4(), ak = zero4();
 #pragma unroll
         for (int k0 = 0; k0 < CH; k0 += M::KS) {
-          const typename M::frag fb = frag_ld<T>(&sm.psi[0][0], 1, D + 8, n0, k0);
-          aa = M::mma(frag_ld_kscaled<T>(&sm.dy[0][0], 1, D + 8, m0, k0, sm.sc.acoef), fb, aa);
-          ak = M::mma(frag_ld_kscaled<T>(&sm.dy[0][0], 1, D + 8, m0, k0, sm.sc.kcoef), fb, ak);
+          const typename M::frag fb = frag_ld_tr<T>(&sm.psi[0][0], D + 8, n0, k0);
+          aa = M::mma(frag_ld_tr_kscaled<T>(&sm.dy[0][0], D + 8, m0, k0, sm.sc.acoef), fb, aa);
+          ak = M::mma(frag_ld_tr_kscaled<T>(&sm.dy[0][0], D + 8, m0, k0, sm.sc.kcoef), fb, ak);
         }
         if (valid) {
 #pragma unroll
