@@ -118,11 +118,12 @@ struct BwdSegSmem {
   static constexpr int SPM = CH + kHaloPad;
   static constexpr int LWR = ((CH + 2 + 15) / 16) * 16;   // rows of the phase-F GEMM operand
   static constexpr bool kStatesInLds = sizeof(T) == 2;   // fp32 reads S_in / Z_in from the saved chunk states
-  T sref[D][D + 8];
-  T dSe[D][D + 8];
-  T dZe[D][D + 8];
-  T Sin[kStatesInLds ? D : 1][D + 8];
-  T Zin[kStatesInLds ? D : 1][D + 8];
+  // adjoint at the chunk end and the chunk-start state, transposed: X^T[k][i] = X[i][k]
+  alignas(16) T sref[D][D + 8];
+  alignas(16) T dSeT[D][D + 8];
+  alignas(16) T dZeT[D][D + 8];
+  alignas(16) T SinT[kStatesInLds ? D : 1][D + 8];
+  alignas(16) T ZinT[kStatesInLds ? D : 1][D + 8];
   T phi[SPM][D + 8];
   T psi[CH][D + 8];
   T dy[CH][D + 8];
@@ -132,7 +133,7 @@ struct BwdSegSmem {
       T QT[SPM][CH + 8];   // Q^T[s][q],  Q[q][s] = Ws[s, q-1] (psi_q . phi_s)
       T Qp[CH][SPM + 8];   // Q'[q][s] = Ws[s, q-1] (dy_q . delta_s)
       T QpT[SPM][CH + 8];
-      T dD[D][SPM + 8];    // dDelta[i][s]
+      alignas(16) T dDT[SPM][D + 8];   // dDelta^T[s][i]
     } g;
     struct {               // phase F
       float Lw[LWR][CH + 1];      // window-weighted Lm rows (q < CH), hS (row CH), hZ (row CH + 1)
@@ -374,18 +375,20 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
       for (int j = 0; j < NT2; ++j) {
         const int tile = wave + kSegWaves * j;
         if (tile >= NTD * NTD) continue;
+        const int i0 = (tile / NTD) * 16 + 4 * (lane >> 4), k = (tile % NTD) * 16 + (lane & 15);
+        float sv[4], zv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int i = (tile / NTD) * 16 + 4 * (lane >> 4) + r, k = (tile % NTD) * 16 + (lane & 15);
-          const float sv = clamp_in ? clamp100(pf.s_in[j][r]) : pf.s_in[j][r];
-          const float zv = g.momentum ? pf.z_in[j][r] : 0.f;
-          gss += dS[j][r] * sv; gsz += dS[j][r] * zv; gzz += dZ[j][r] * zv;
-          sm.dSe[i][k] = from_f32<T>(dS[j][r]);
-          sm.dZe[i][k] = from_f32<T>(dZ[j][r]);
-          if constexpr (SIL) {
-            sm.Sin[i][k] = from_f32<T>(sv);
-            sm.Zin[i][k] = from_f32<T>(zv);
-          }
+          sv[r] = clamp_in ? clamp100(pf.s_in[j][r]) : pf.s_in[j][r];
+          zv[r] = g.momentum ? pf.z_in[j][r] : 0.f;
+          gss += dS[j][r] * sv[r]; gsz += dS[j][r] * zv[r]; gzz += dZ[j][r] * zv[r];
+        }
+        // rows i0..i0+3 of column k are contiguous in the transposed copies
+        store4<T>(&sm.dSeT[k][i0], dS[j][0], dS[j][1], dS[j][2], dS[j][3]);
+        store4<T>(&sm.dZeT[k][i0], dZ[j][0], dZ[j][1], dZ[j][2], dZ[j][3]);
+        if constexpr (SIL) {
+          store4<T>(&sm.SinT[k][i0], sv[0], sv[1], sv[2], sv[3]);
+          store4<T>(&sm.ZinT[k][i0], zv[0], zv[1], zv[2], zv[3]);
         }
       }
       for (int off = 32; off > 0; off >>= 1) {
@@ -446,8 +449,8 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
           }
         }
       }
-    } else if (lane <= CH) {
-      decay_column<CH>(sm.tab, sm.sc, lane, sm.B1);
+    } else {
+      decay_columns_wave<CH>(sm.tab, sm.sc, sm.B1);
     }
     __syncthreads();
     // G2 / G3: Kmat = psi phi^T, K3 = dy delta -> Q^T, Q', Q'^T, Lm
@@ -493,8 +496,8 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
 #pragma unroll
         for (int k0 = 0; k0 < D; k0 += M::KS) {
           const typename M::frag fb = frag_ld_row<T>(&sm.phi[0][0], D + 8, n0, k0);
-          as = M::mma(frag_ld_row<T>(&sm.dSe[0][0], D + 8, m0, k0), fb, as);
-          az = M::mma(frag_ld_row<T>(&sm.dZe[0][0], D + 8, m0, k0), fb, az);
+          as = M::mma(frag_ld_tr<T>(&sm.dSeT[0][0], D + 8, m0, k0), fb, as);
+          az = M::mma(frag_ld_tr<T>(&sm.dZeT[0][0], D + 8, m0, k0), fb, az);
         }
 #pragma unroll
         for (int k0 = 0; k0 < CH; k0 += M::KS)
@@ -502,15 +505,16 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         if (valid) {
           const int s = n0 + (lane & 15);
           const float wz = sm.sc.wzend[s], ws = sm.sc.wsend[s];
-          float hs = 0.f, hz = 0.f;
+          float hs = 0.f, hz = 0.f, dd[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int i = m0 + 4 * (lane >> 4) + r;
             const float d = to_f32(sm.deltaT[s][i]);
             hs += d * as[r];
             hz += d * az[r];
-            sm.u.g.dD[i][s] = from_f32<T>(wz * az[r] - ws * as[r] - aq[r]);
+            dd[r] = wz * az[r] - ws * as[r] - aq[r];
           }
+          store4<T>(&sm.u.g.dDT[s][m0 + 4 * (lane >> 4)], dd[0], dd[1], dd[2], dd[3]);
           hs += __shfl_xor(hs, 16); hs += __shfl_xor(hs, 32);
           hz += __shfl_xor(hz, 16); hz += __shfl_xor(hz, 32);
           if (lane < 16) { atomicAdd(&sm.hS[s], hs); atomicAdd(&sm.hZ[s], hz); }
@@ -526,7 +530,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         const int s = idx / D, i = idx % D;
         const int pp = t0 - H + s;
         if (pp < 0) continue;
-        float val = -to_f32(sm.u.g.dD[i][s]);
+        float val = -to_f32(sm.u.g.dDT[s][i]);
         if (s < H) {
           if (first) { if (c > 0) p.halo_part[(((size_t)bh * sg.nseg + seg) * H + s) * (2 * D) + i] = val; }
           else cur_carry[s * 2 * D + i] = val;
@@ -544,7 +548,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
       f32x4 acc = zero4();
 #pragma unroll
       for (int k0 = 0; k0 < SPM; k0 += M::KS)
-        acc = M::mma(frag_ld_row<T>(&sm.u.g.dD[0][0], SPM + 8, m0, k0), frag_ld_tr<T>(&sm.phi[0][0], D + 8, n0, k0), acc);
+        acc = M::mma(frag_ld_tr<T>(&sm.u.g.dDT[0][0], D + 8, m0, k0), frag_ld_tr<T>(&sm.phi[0][0], D + 8, n0, k0), acc);
 #pragma unroll
       for (int r = 0; r < 4; ++r) dsr[j][r] += acc[r];
     }
@@ -560,8 +564,8 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         for (int k0 = 0; k0 < D; k0 += M::KS) {
           const typename M::frag fa = frag_ld_row<T>(&sm.dy[0][0], D + 8, m0, k0);
           if constexpr (SIL) {
-            as = M::mma(fa, frag_ld_tr<T>(&sm.Sin[0][0], D + 8, n0, k0), as);
-            az = M::mma(fa, frag_ld_tr<T>(&sm.Zin[0][0], D + 8, n0, k0), az);
+            as = M::mma(fa, frag_ld_row<T>(&sm.SinT[0][0], D + 8, n0, k0), as);
+            az = M::mma(fa, frag_ld_row<T>(&sm.ZinT[0][0], D + 8, n0, k0), az);
           } else {
             typename M::frag fs;
             {
@@ -674,9 +678,9 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
 #pragma unroll
         for (int k0 = 0; k0 < D; k0 += M::KS) {
           const typename M::frag fa = frag_ld_row<T>(&sm.deltaT[0][0], D + 8, m0, k0);
-          a1 = M::mma(fa, frag_ld_tr<T>(&sm.dZe[0][0], D + 8, n0, k0), a1);
-          a2 = M::mma(fa, frag_ld_tr<T>(&sm.dSe[0][0], D + 8, n0, k0), a2);
-          a4 = M::mma(frag_ld_tr<T>(&sm.u.g.dD[0][0], SPM + 8, m0, k0), frag_ld_tr<T>(&sm.sref[0][0], D + 8, n0, k0), a4);
+          a1 = M::mma(fa, frag_ld_row<T>(&sm.dZeT[0][0], D + 8, n0, k0), a1);
+          a2 = M::mma(fa, frag_ld_row<T>(&sm.dSeT[0][0], D + 8, n0, k0), a2);
+          a4 = M::mma(frag_ld_row<T>(&sm.u.g.dDT[0][0], D + 8, m0, k0), frag_ld_tr<T>(&sm.sref[0][0], D + 8, n0, k0), a4);
         }
 #pragma unroll
         for (int k0 = 0; k0 < CH; k0 += M::KS)

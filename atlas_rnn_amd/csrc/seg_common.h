@@ -66,6 +66,19 @@ struct Vec8 {
   }
 };
 
+// Four values rounded to T and stored contiguously (8 bytes for bf16, 16 for fp32; p aligned).
+template <typename T>
+__device__ __forceinline__ void store4(T* p, float a, float b, float c, float d) {
+  if constexpr (sizeof(T) == 2) {
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    t4 v;
+    v[0] = static_cast<T>(a); v[1] = static_cast<T>(b); v[2] = static_cast<T>(c); v[3] = static_cast<T>(d);
+    *reinterpret_cast<t4*>(p) = v;
+  } else {
+    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ Vec8<T> vec8_load(const T* p) {
   Vec8<T> r;
@@ -118,40 +131,45 @@ struct DecayTab {
   float A[CH + 1][CH + 1], B[CH + 1][CH + 1], C[CH + 1][CH + 1];
 };
 
-// Column c (0 <= c <= CH) of the decay tables; the thread of column 0 also writes the prefix
-// coefficients sc.acoef[t] = a_{t-1}, sc.kcoef[t] = kappa_{t-1}, sc.endc and B1[t] = b_{t-1}
-// (t = 0..CH, B1[0] = 1).
+// Lane t's value of x, in every lane (v_readlane; t is a wave-uniform constant).
+__device__ __forceinline__ float lane_bcast(float x, int t) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), t));
+}
+
+// Decay tables of a chunk, computed by one wave with one column per lane (lane c = 0..CH;
+// lanes above CH run the same chain and write nothing). Column c (tp = c - 1), for t >= tp:
+//   A[c][t] = prod_{r=c..t} alpha_r,  B[c][t] = prod_{r=c..t} beta_r,
+//   C[c][t] = alpha_t C[c][t-1] + eta_t B[c][t]   (C[c][tp] = eta_tp),
+// zero for t < tp. Lane 0 also writes B1[t] = b_{t-1} (t = 0..CH, B1[0] = 1). The step scalars
+// are read once into lane t's registers and broadcast with v_readlane, so the chains never wait
+// on LDS reads (the table writes are not waited on).
 template <int CH>
-__device__ __forceinline__ void decay_column(DecayTab<CH>& tab, ChunkScalars<CH>& sc, int c, float* B1) {
-  static_assert(CH % 8 == 0, "decay table groups");
-  const int tp = c - 1;
+__device__ __forceinline__ void decay_columns_wave(DecayTab<CH>& tab, const ChunkScalars<CH>& sc, float* B1) {
+  static_assert(CH < kWave, "one lane per column");
+  const int c = lane_id(), tp = c - 1;
+  const bool writer = c <= CH;
+  const int ts = c < CH ? c : 0;
+  const float al_v = sc.alpha[ts], et_v = sc.eta[ts], be_v = sc.beta[ts];
   float a = 1.f, b = 1.f, m = 0.f;
-  if (c == 0) { B1[0] = 1.f; sc.acoef[0] = 1.f; sc.kcoef[0] = 0.f; }
-  for (int t0 = 0; t0 < CH; t0 += 8) {
-    float al8[8], et8[8], be8[8];
+  if (c == 0) B1[0] = 1.f;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) { al8[u] = sc.alpha[t0 + u]; et8[u] = sc.eta[t0 + u]; be8[u] = sc.beta[t0 + u]; }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int t = t0 + u;
-      if (t == tp) {
-        m = et8[u];
-      } else if (t > tp) {
-        b = be8[u] * b;
-        a = al8[u] * a;
-        m = al8[u] * m + et8[u] * b;
-      }
-      const bool on = t >= tp;
+  for (int t = 0; t < CH; ++t) {
+    const float al = lane_bcast(al_v, t), et = lane_bcast(et_v, t), be = lane_bcast(be_v, t);
+    if (t == tp) {
+      m = et;
+    } else if (t > tp) {
+      b = be * b;
+      a = al * a;
+      m = al * m + et * b;
+    }
+    const bool on = t >= tp;
+    if (writer) {
       tab.A[c][t] = on ? a : 0.f;
       tab.B[c][t] = on ? b : 0.f;
       tab.C[c][t] = on ? m : 0.f;
-      if (c == 0) {
-        B1[t + 1] = b;
-        if (t + 1 < CH) { sc.acoef[t + 1] = a; sc.kcoef[t + 1] = m; }
-      }
     }
+    if (c == 0) B1[t + 1] = b;
   }
-  if (c == 0) { sc.endc[0] = a; sc.endc[1] = m; sc.endc[2] = b; }
 }
 
 // Coefficient recurrences of a chunk, run by 128 lanes (ci = 0..127):
