@@ -154,6 +154,19 @@ __device__ __forceinline__ typename MM<OT>::frag frag_ld_tr_kscaled(const OT* p,
   return f;
 }
 
+// Fragment f with its k values scaled by w[k] (w: the KL weights of this lane's k slots).
+template <typename T>
+__device__ __forceinline__ typename MM<T>::frag frag_scale(typename MM<T>::frag f, const float* w) {
+  if constexpr (MM<T>::KL == 1) {
+    return f * w[0];
+  } else {
+    typename MM<T>::frag r;
+#pragma unroll
+    for (int e = 0; e < MM<T>::KL; ++e) r[e] = static_cast<T>(static_cast<float>(f[e]) * w[e]);
+    return r;
+  }
+}
+
 // Clamp of the reference (torch.clamp(-100, 100)) and its gradient mask (min <= x <= max).
 __device__ __forceinline__ float clamp100(float x) { return fminf(fmaxf(x, -100.f), 100.f); }
 __device__ __forceinline__ float clamp_mask(float x) { return (x >= -100.f && x <= 100.f) ? 1.f : 0.f; }

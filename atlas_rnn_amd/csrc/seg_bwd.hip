@@ -29,11 +29,51 @@ hipError_t launch_chunk_coef(const Geom& g, const T* decay, const T* lr, const T
 // ---------------------------------------------------------------------------------------------
 template <typename T, int CH, int D>
 struct BwdAggSmem {
-  T psiT[D][CH + 8];
-  T dyT[D][CH + 8];
-  ChunkScalars<CH> sc;
+  alignas(16) T psi[CH][D + 8];
+  alignas(16) T dy[CH][D + 8];
+  alignas(16) float coef[2 * CH + 4];   // a_{t-1}, kappa_{t-1}, (a, kappa, b) of the chunk
 };
 
+// Register prefetch of one chunk for the adjoint aggregates: psi (threads 0 .. NV-1) or dy
+// (threads NV .. 2 NV-1) rows, 8 features per thread, and the head of the coefficient record.
+template <typename T, int CH, int D>
+struct BwdAggPrefetch {
+  static constexpr int NV = CH * D / 8;
+  static constexpr int NC4 = (2 * CH + 4) / 4;
+  static_assert(2 * NV <= kSegThreads && (2 * CH + 4) % 4 == 0, "one vector per thread");
+  Vec8<T> x;
+  float4 rc;
+  bool ok;
+  __device__ __forceinline__ void load(const Geom& g, const BwdPtrs<T>& a, const float* rec, size_t tb, int c,
+                                       int tid) {
+    const int t0 = c * g.Lc, L = min(g.T, t0 + g.Lc) - t0;
+    const int v = tid < NV ? tid : tid - NV;
+    const int t = v / (D / 8), c8 = v % (D / 8);
+    const T* src = (tid < NV || !a.dy) ? a.q : a.dy;
+    ok = tid < 2 * NV && t < L && (tid < NV || a.dy);
+    x = vec8_load(src + (tb + t0 + (ok ? t : 0)) * D + c8 * 8);
+    rc = reinterpret_cast<const float4*>(rec)[tid < NC4 ? tid : 0];
+  }
+  template <typename Sm>
+  __device__ __forceinline__ void store(const Geom& g, Sm& sm, int tid) const {
+    if (tid < 2 * NV) {
+      const int v = tid < NV ? tid : tid - NV;
+      const int t = v / (D / 8), c8 = v % (D / 8);
+      Vec8<T> y = x.masked(ok);
+      if (tid < NV) {
+        if (g.map_mode == MAP_ELEMENTWISE) y = y.mapped(g.map_deg);
+        y.store(&sm.psi[t][c8 * 8]);
+      } else {
+        y.store(&sm.dy[t][c8 * 8]);
+      }
+    }
+    if (tid < NC4) reinterpret_cast<float4*>(sm.coef)[tid] = rc;
+  }
+};
+
+// Adjoint aggregate of one segment: walks its chunks in reverse from a zero adjoint,
+//   lam <- a_end lam + sum_t a_{t-1} dy_t psi_t^T,   mu <- b_end mu - kappa_end lam - sum_t kappa_{t-1} dy_t psi_t^T,
+// with the next chunk's inputs prefetched into registers while the current one computes.
 template <typename T, int CH, int D>
 __global__ __launch_bounds__(kSegThreads) void k_bwd_seg_agg(const Geom g, const BwdPtrs<T> a, const SegGeom sg,
                                                                const BwdSegPtrs p) {
@@ -43,57 +83,54 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg_agg(const Geom g, const
   constexpr int NTD = D / 16;
   constexpr int NT2 = (NTD * NTD + kSegWaves - 1) / kSegWaves;   // state tiles per wave
   typedef MM<T> M;
-  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int seg = blockIdx.x, bh = blockIdx.y;
   const size_t tb = (size_t)bh * g.T;
   const int c_begin = seg * sg.G, c_end = min(g.nc, c_begin + sg.G);
+  const float* rec_row = p.coef + (size_t)bh * g.nc * CoefRec<CH>::SIZE;
   float lam[NT2][4], mu[NT2][4];
 #pragma unroll
   for (int j = 0; j < NT2; ++j)
 #pragma unroll
     for (int r = 0; r < 4; ++r) { lam[j][r] = 0.f; mu[j][r] = 0.f; }
   float pa = 1.f, pk = 0.f, pb = 1.f;
+  BwdAggPrefetch<T, CH, D> pf;
+  if (c_begin < c_end) pf.load(g, a, rec_row + (size_t)(c_end - 1) * CoefRec<CH>::SIZE, tb, c_end - 1, threadIdx.x);
   for (int c = c_end - 1; c >= c_begin; --c) {
-    const int t0 = c * g.Lc, t1 = min(g.T, t0 + g.Lc), L = t1 - t0;
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     __syncthreads();
-    for (int idx = tid; idx < CH * D; idx += kSegThreads) {
-      const int t = idx / D, k = idx % D;
-      float ps = 0.f, dv = 0.f;
-      if (t < L) {
-        ps = ld_map(a.q, (tb + t0 + t) * D + k, g.map_mode, g.map_deg);
-        dv = a.dy ? to_f32(a.dy[(tb + t0 + t) * D + k]) : 0.f;
-      }
-      sm.psiT[k][t] = from_f32<T>(ps);
-      sm.dyT[k][t] = from_f32<T>(dv);
-    }
-    {   // a_{t-1}, kappa_{t-1} and the chunk transition from the chunk's coefficient record
-      constexpr int REC4 = CoefRec<CH>::SIZE / 4;
-      const float4* rc = reinterpret_cast<const float4*>(p.coef + ((size_t)bh * g.nc + c) * CoefRec<CH>::SIZE);
-      if (tid < REC4) reinterpret_cast<float4*>(&sm.sc.acoef[0])[tid] = rc[tid];
-    }
+    pf.store(g, sm, tid);
     __syncthreads();
-    const float ae = sm.sc.endc[0], ke = sm.sc.endc[1], be = sm.sc.endc[2];
+    if (c - 1 >= c_begin) pf.load(g, a, rec_row + (size_t)(c - 1) * CoefRec<CH>::SIZE, tb, c - 1, tid);
+    const float ae = sm.coef[2 * CH], ke = sm.coef[2 * CH + 1], be = sm.coef[2 * CH + 2];
 #pragma unroll
     for (int j = 0; j < NT2; ++j) {
-      const int tile = wave + kSegWaves * j;
-      if (tile >= NTD * NTD) continue;
+      const int tile = min(wave + kSegWaves * j, NTD * NTD - 1);
+      const bool valid = (NTD * NTD) % kSegWaves == 0 || wave + kSegWaves * j < NTD * NTD;
       const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
       f32x4 aa = zero4(), ak = zero4();
-      for (int k0 = 0; k0 < CH; k0 += M::KS) {
-        const typename M::frag fb = frag_ld_row<T>(&sm.psiT[0][0], CH + 8, n0, k0);
-        aa = M::mma(frag_ld_kscaled<T>(&sm.dyT[0][0], CH + 8, 1, m0, k0, sm.sc.acoef), fb, aa);
-        ak = M::mma(frag_ld_kscaled<T>(&sm.dyT[0][0], CH + 8, 1, m0, k0, sm.sc.kcoef), fb, ak);
-      }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float l_out = lam[j][r];
-        lam[j][r] = ae * l_out + aa[r];
-        mu[j][r] = g.momentum ? (be * mu[j][r] - ke * l_out - ak[r]) : 0.f;
+      for (int k0 = 0; k0 < CH; k0 += M::KS) {
+        const typename M::frag fb = frag_ld_tr<T>(&sm.psi[0][0], D + 8, n0, k0);
+        const typename M::frag fd = frag_ld_tr<T>(&sm.dy[0][0], D + 8, m0, k0);
+        const int kb = k0 + (lane >> 4) * M::KL;
+        aa = M::mma(frag_scale<T>(fd, &sm.coef[kb]), fb, aa);
+        ak = M::mma(frag_scale<T>(fd, &sm.coef[CH + kb]), fb, ak);
+      }
+      if (valid) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float l_out = lam[j][r];
+          lam[j][r] = ae * l_out + aa[r];
+          mu[j][r] = g.momentum ? (be * mu[j][r] - ke * l_out - ak[r]) : 0.f;
+        }
       }
     }
     const float na = pa * ae, nk = pa * ke + pk * be;
     pb = pb * be; pa = na; pk = nk;
   }
+  const int lane = lane_id(), wave = wave_id();
   float* ag = p.adj_agg + ((size_t)bh * sg.nseg + seg) * sg.agg_stride;
 #pragma unroll
   for (int j = 0; j < NT2; ++j) {
@@ -107,7 +144,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg_agg(const Geom g, const
       ag[(size_t)D * D + (size_t)i * D + k] = mu[j][r];
     }
   }
-  if (tid == 0) { ag[2 * D * D] = pa; ag[2 * D * D + 1] = pk; ag[2 * D * D + 2] = pb; }
+  if (threadIdx.x == 0) { ag[2 * D * D] = pa; ag[2 * D * D + 1] = pk; ag[2 * D * D + 2] = pb; }
 }
 
 // ---------------------------------------------------------------------------------------------

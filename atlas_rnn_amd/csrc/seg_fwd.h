@@ -190,19 +190,6 @@ struct ChunkPrefetch {
 
 enum WalkMode { WALK_AGG = 0, WALK_FULL = 1 };
 
-// Fragment f with its k values scaled by w[k] (w: the KL weights of this lane's k slots).
-template <typename T>
-__device__ __forceinline__ typename MM<T>::frag frag_scale(typename MM<T>::frag f, const float* w) {
-  if constexpr (MM<T>::KL == 1) {
-    return f * w[0];
-  } else {
-    typename MM<T>::frag r;
-#pragma unroll
-    for (int e = 0; e < MM<T>::KL; ++e) r[e] = static_cast<T>(static_cast<float>(f[e]) * w[e]);
-    return r;
-  }
-}
-
 // Segment walk.
 //   WALK_AGG:    zero initial state; writes the segment aggregate (a, kappa, b, U, V) to agg.
 //   WALK_FULL:   starts from seg_states[seg] (the segment scan folded the preceding aggregates),
