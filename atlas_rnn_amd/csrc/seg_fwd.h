@@ -15,10 +15,9 @@ namespace atlas {
 template <typename T, int CH, int D, bool FULL>
 struct SegFwdSmem {
   static constexpr int SPM = CH + kHaloPad;
-  T phi[SPM][D + 8];         // phi[s][k]
-  T phiT[D][SPM + 8];        // phi^T[k][s] (G4's B operand)
-  T delta[D][SPM + 8];       // v staged by the loads as [i][s], then delta[i][s]
-  T sref[D][D + 8];
+  alignas(16) T phi[SPM][D + 8];   // phi[s][k]
+  alignas(16) T vd[SPM][D + 8];    // v[s][i] staged by the loads, then delta[s][i]
+  alignas(16) T sref[D][D + 8];
   ChunkScalars<CH> sc;
   // full walk only
   T psi[FULL ? CH : 1][D + 8];
@@ -43,14 +42,13 @@ struct ChunkPrefetch {
   static constexpr int NV_WSH = FULL ? (CH * SPM / 8 + kSegThreads - 1) / kSegThreads : 0;
   static_assert(REC4 <= kSegThreads && SPM % 8 == 0, "record / wsh prefetch");
   Vec8<T> phi[NV_PHI];
-  Vec8<T> kt[NV_PHI];        // k again with consecutive lanes on consecutive sources (phi^T store)
   Vec8<T> vv[NV_PHI];
   Vec8<T> psi[NV_PSI > 0 ? NV_PSI : 1];
   Vec8<T> wsv[NV_WSH > 0 ? NV_WSH : 1];
   float rc0, rc1, rc2, rc3;   // this thread's float4 of the coefficient record
   T alpha, eta, beta, ug;
   T wl[NWL];
-  unsigned ok_phi, ok_v, ok_psi, ok_wl;
+  unsigned ok_phi, ok_psi, ok_wl;
   bool ok_t, ok_ug, pad_ug;
 
   // rec_c / wsh_c: this chunk's coefficient record and Ws[s, t-1] block (k_chunk_coef)
@@ -58,7 +56,7 @@ struct ChunkPrefetch {
                                        const float* rec_c, const T* wsh_c) {
     const int tid = threadIdx.x, H = g.H;
     const size_t r0 = tb + t0;                          // always a valid token row
-    ok_phi = 0; ok_v = 0; ok_psi = 0; ok_wl = 0;
+    ok_phi = 0; ok_psi = 0; ok_wl = 0;
     {
       const float4 r4 = reinterpret_cast<const float4*>(rec_c)[tid < REC4 ? tid : 0];
       rc0 = r4.x; rc1 = r4.y; rc2 = r4.z; rc3 = r4.w;
@@ -73,22 +71,14 @@ struct ChunkPrefetch {
 #pragma unroll
     for (int j = 0; j < NV_PHI; ++j) {
       const int v = tid + j * kSegThreads;
-      {   // phi: 8 consecutive features of source s per lane
+      {   // phi and v: 8 consecutive features of source s per lane
         const int s = v / (D / 8), c8 = v % (D / 8);
         const int p = t0 - H + s;
         const bool ok = s < SPM && s < H + L && p >= 0;
-        phi[j] = vec8_load(a.k + (ok ? tb + p : r0) * D + c8 * 8);
-        ok_phi |= (ok ? 1u : 0u) << j;
-      }
-      {   // k (for phi^T) and v: consecutive lanes take consecutive sources (conflict-free
-          // transposed LDS stores)
-        const int s = v % SPM, c8 = v / SPM;
-        const int p = t0 - H + s;
-        const bool ok = c8 < D / 8 && s < H + L && p >= 0;
-        const size_t off = (ok ? tb + p : r0) * D + (ok ? c8 * 8 : 0);
-        kt[j] = vec8_load(a.k + off);
+        const size_t off = (ok ? tb + p : r0) * D + c8 * 8;
+        phi[j] = vec8_load(a.k + off);
         vv[j] = vec8_load(a.v + off);
-        ok_v |= (ok ? 1u : 0u) << j;
+        ok_phi |= (ok ? 1u : 0u) << j;
       }
     }
     if constexpr (FULL) {
@@ -129,27 +119,13 @@ struct ChunkPrefetch {
 #pragma unroll
     for (int j = 0; j < NV_PHI; ++j) {
       const int v = tid + j * kSegThreads;
-      {
-        const int s = v / (D / 8), c8 = v % (D / 8);
-        if (s < SPM) {
-          Vec8<T> x = phi[j].masked((ok_phi >> j) & 1u);
-          if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
-          x.store(&sm.phi[s][c8 * 8]);
-        }
-      }
-      {
-        const int s = v % SPM, c8 = v / SPM;
-        if (c8 < D / 8) {
-          const bool ok = (ok_v >> j) & 1u;
-          const Vec8<T> x = vv[j].masked(ok);
-          Vec8<T> y = kt[j].masked(ok);
-          if (g.map_mode == MAP_ELEMENTWISE) y = y.mapped(g.map_deg);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            sm.delta[c8 * 8 + e][s] = x.v[e];
-            sm.phiT[c8 * 8 + e][s] = y.v[e];
-          }
-        }
+      const int s = v / (D / 8), c8 = v % (D / 8);
+      if (s < SPM) {
+        const bool ok = (ok_phi >> j) & 1u;
+        Vec8<T> x = phi[j].masked(ok);
+        if (g.map_mode == MAP_ELEMENTWISE) x = x.mapped(g.map_deg);
+        x.store(&sm.phi[s][c8 * 8]);
+        vv[j].masked(ok).store(&sm.vd[s][c8 * 8]);
       }
     }
     if constexpr (FULL) {
@@ -298,7 +274,7 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
     }
 
     // ---- P1: G1 + G2 (all waves)
-    // G1: delta[i][s] = (S_ref phi_s)[i] - v_s[i];  G2 (full walk): Kmat[tau][s] = psi_tau . phi_s,
+    // G1: delta[s][i] = (S_ref phi_s)[i] - v_s[i];  G2 (full walk): Kmat[tau][s] = psi_tau . phi_s,
     // kept in registers (kacc) until the Q epilogue.
     constexpr int NGW = kSegWaves;
     constexpr int NT1 = NTS * NTD, PER1 = (NT1 + NGW - 1) / NGW;
@@ -311,20 +287,20 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
       for (int j = 0; j < PER1; ++j) {
         const int tile = min(wave + NGW * j, NT1 - 1);
         const bool valid = NT1 % NGW == 0 || wave + NGW * j < NT1;
-        const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;   // m: sources, n: rows i
+        const int m0 = (tile % NTD) * 16, n0 = (tile / NTD) * 16;   // m: rows i, n: sources
         f32x4 acc = zero4();
 #pragma unroll
         for (int k0 = 0; k0 < D; k0 += M::KS)
-          acc = M::mma(frag_ld_row<T>(&sm.phi[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.sref[0][0], D + 8, n0, k0), acc);
+          acc = M::mma(frag_ld_row<T>(&sm.sref[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.phi[0][0], D + 8, n0, k0), acc);
         if (valid) {
-          const int i = n0 + (lane & 15);
+          // rows i0..i0+3 of source s are contiguous in vd: v read and delta written in place
+          const int s = n0 + (lane & 15), i0 = m0 + 4 * (lane >> 4);
+          const int p = t0 - H + s;
+          const bool src_ok = s < H + L && p >= 0;
+          float d[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int s = m0 + 4 * (lane >> 4) + r;
-            const int p = t0 - H + s;
-            const float d = (s < H + L && p >= 0) ? acc[r] - to_f32(sm.delta[i][s]) : 0.f;
-            sm.delta[i][s] = from_f32<T>(d);
-          }
+          for (int r = 0; r < 4; ++r) d[r] = src_ok ? acc[r] - to_f32(sm.vd[s][i0 + r]) : 0.f;
+          store4<T>(&sm.vd[s][i0], d[0], d[1], d[2], d[3]);
         }
       }
       if constexpr (FULL) {
@@ -372,7 +348,7 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
           f32x4 aq = zero4(), as = zero4(), az = zero4();
 #pragma unroll
           for (int k0 = 0; k0 < SPM; k0 += M::KS)
-            aq = M::mma(frag_ld_row<T>(&sm.Q[0][0], SPM + 8, m0, k0), frag_ld_row<T>(&sm.delta[0][0], SPM + 8, n0, k0), aq);
+            aq = M::mma(frag_ld_row<T>(&sm.Q[0][0], SPM + 8, m0, k0), frag_ld_tr<T>(&sm.vd[0][0], D + 8, n0, k0), aq);
 #pragma unroll
           for (int k0 = 0; k0 < D; k0 += M::KS) {
             const typename M::frag fa = frag_ld_row<T>(&sm.psi[0][0], D + 8, m0, k0);
@@ -421,7 +397,7 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
           typename M::frag fsm[NKS], fzm[NKS];
 #pragma unroll
           for (int kk = 0; kk < NKS; ++kk) {
-            const typename M::frag fd = frag_ld_row<T>(&sm.delta[0][0], SPM + 8, m0, kk * M::KS);
+            const typename M::frag fd = frag_ld_tr<T>(&sm.vd[0][0], D + 8, m0, kk * M::KS);
             const int sb = kk * M::KS + (lane >> 4) * M::KL;
             fsm[kk] = frag_scale<T>(fd, &sm.sc.wsmid[sb]);
             fzm[kk] = frag_scale<T>(fd, &sm.sc.wzmid[sb]);
@@ -432,7 +408,7 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
             f32x4 aum = zero4(), avm = zero4();
 #pragma unroll
             for (int kk = 0; kk < NKS; ++kk) {
-              const typename M::frag fb = frag_ld_row<T>(&sm.phiT[0][0], SPM + 8, n0, kk * M::KS);
+              const typename M::frag fb = frag_ld_tr<T>(&sm.phi[0][0], D + 8, n0, kk * M::KS);
               aum = M::mma(fsm[kk], fb, aum);
               avm = M::mma(fzm[kk], fb, avm);
             }
@@ -456,7 +432,7 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
       typename M::frag fs[NKS], fz[NKS];
 #pragma unroll
       for (int kk = 0; kk < NKS; ++kk) {
-        const typename M::frag fd = frag_ld_row<T>(&sm.delta[0][0], SPM + 8, m0, kk * M::KS);
+        const typename M::frag fd = frag_ld_tr<T>(&sm.vd[0][0], D + 8, m0, kk * M::KS);
         const int sb = kk * M::KS + (lane >> 4) * M::KL;
         fs[kk] = frag_scale<T>(fd, &sm.sc.wsend[sb]);
         fz[kk] = frag_scale<T>(fd, &sm.sc.wzend[sb]);
@@ -470,7 +446,7 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
         f32x4 au = zero4(), av = zero4();
 #pragma unroll
         for (int kk = 0; kk < NKS; ++kk) {
-          const typename M::frag fb = frag_ld_row<T>(&sm.phiT[0][0], SPM + 8, n0, kk * M::KS);
+          const typename M::frag fb = frag_ld_tr<T>(&sm.phi[0][0], D + 8, n0, kk * M::KS);
           au = M::mma(fs[kk], fb, au);
           av = M::mma(fz[kk], fb, av);
         }
