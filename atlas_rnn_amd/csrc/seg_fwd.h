@@ -174,9 +174,10 @@ enum WalkMode { WALK_AGG = 0, WALK_FULL = 1 };
 //                the chunk start and, when g.Lmid > 0, the state after token Lmid - 1.
 // The chunk coefficients (a, kappa, end weights, Ws[s, t-1]) come precomputed from k_chunk_coef
 // (coef: [BH][nc] records, wsh_all: [BH][nc][CH][SPM], full walk only) with the prefetch.
-// Wave roles per chunk: P1 all waves run G1 (and G2 for the full walk); P3 waves 0-3 run G3 (y)
-// while waves 4-7 run G4 and update the states, which they hold in registers (wave 4 + m owns
-// state rows 16 m .. 16 m + 15).
+// Wave roles per chunk: P1 all waves run G1 (and G2 for the full walk); P3 of the full walk:
+// waves 0-3 run G3 (y) while waves 4-7 run G4 and update the states, which they hold in
+// registers (wave 4 + m owns state rows 16 m .. 16 m + 15); P3 of the aggregate pass: every
+// wave runs G4 on its share of the state tiles.
 template <typename T, int CH, int D, int MODE>
 __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg, float* agg,
                                             const float* seg_states, float* rw, float* final_raw,
@@ -199,15 +200,20 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
   // ---- S_ref (bf16/fp32 operand copy)
   for (int idx = tid; idx < D * D; idx += kSegThreads) sm.sref[idx / D][idx % D] = from_f32<T>(a.S_ref[sb + idx]);
 
-  // ---- state registers on waves 4..7: wave w owns row tile (w - 4) (for D = 32 only waves 4, 5)
-  const bool state_wave = wave >= 4;
-  const int mt = wave - 4;                        // row tile owned
-  const bool owns = state_wave && mt < NTD;
-  float Sr[NTD][4], Zr[NTD][4];
+  // ---- state registers. Full walk: wave 4 + m owns row tile m (all NTD column tiles) while
+  // waves 0-3 run G3. Aggregate pass: the NTD x NTD tiles are spread over all waves, NOWN tiles
+  // of one row tile per wave.
+  constexpr int NOWN = FULL ? NTD : (NTD * NTD < kSegWaves ? 1 : NTD * NTD / kSegWaves);
+  constexpr int OWNERS = FULL ? NTD : NTD * NTD / NOWN;
+  static_assert(FULL || NTD % NOWN == 0, "owned tiles share a row tile");
+  const bool owns = FULL ? (wave >= 4 && wave - 4 < NTD) : (wave < OWNERS);
+  const int otile0 = FULL ? (wave - 4) * NTD : wave * NOWN;   // first owned tile, row-major over (mt, n)
+  const int mt = otile0 / NTD, nt0 = otile0 % NTD;           // row tile, first column tile
+  float Sr[NOWN][4], Zr[NOWN][4];
 #pragma unroll
-  for (int n = 0; n < NTD; ++n)
+  for (int jn = 0; jn < NOWN; ++jn)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) { Sr[n][r] = 0.f; Zr[n][r] = 0.f; }
+    for (int r = 0; r < 4; ++r) { Sr[jn][r] = 0.f; Zr[jn][r] = 0.f; }
   float seg_a = 1.f, seg_k = 0.f, seg_b = 1.f;   // aggregate transition (AGG)
 
   if constexpr (!AGG) {
@@ -215,15 +221,15 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
     if (owns) {
       const float* ss = seg_states + ((size_t)bh * sg.nseg + seg) * 2 * D * D;
 #pragma unroll
-      for (int n = 0; n < NTD; ++n)
+      for (int jn = 0; jn < NOWN; ++jn)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
-          Sr[n][r] = ss[(size_t)i * D + k];
-          Zr[n][r] = ss[(size_t)D * D + (size_t)i * D + k];
+          const int i = mt * 16 + 4 * (lane >> 4) + r, k = (nt0 + jn) * 16 + (lane & 15);
+          Sr[jn][r] = ss[(size_t)i * D + k];
+          Zr[jn][r] = ss[(size_t)D * D + (size_t)i * D + k];
           if constexpr (FULL) {
-            sm.Sb[i][k] = from_f32<T>(Sr[n][r]);
-            sm.Zb[i][k] = from_f32<T>(Zr[n][r]);
+            sm.Sb[i][k] = from_f32<T>(Sr[jn][r]);
+            sm.Zb[i][k] = from_f32<T>(Zr[jn][r]);
           }
         }
     }
@@ -255,12 +261,12 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
       if (owns && c == c_begin) {
         float* dst = rw + ((size_t)bh * g.ncb + (size_t)c * rb) * 2 * D * D;
 #pragma unroll
-        for (int n = 0; n < NTD; ++n)
+        for (int jn = 0; jn < NOWN; ++jn)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
-            dst[(size_t)i * D + k] = Sr[n][r];
-            dst[(size_t)D * D + (size_t)i * D + k] = Zr[n][r];
+            const int i = mt * 16 + 4 * (lane >> 4) + r, k = (nt0 + jn) * 16 + (lane & 15);
+            dst[(size_t)i * D + k] = Sr[jn][r];
+            dst[(size_t)D * D + (size_t)i * D + k] = Zr[jn][r];
           }
       }
     }
@@ -403,8 +409,8 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
             fzm[kk] = frag_scale<T>(fd, &sm.sc.wzmid[sb]);
           }
 #pragma unroll
-          for (int n = 0; n < NTD; ++n) {
-            const int n0 = n * 16;
+          for (int jn = 0; jn < NOWN; ++jn) {
+            const int n0 = (nt0 + jn) * 16;
             f32x4 aum = zero4(), avm = zero4();
 #pragma unroll
             for (int kk = 0; kk < NKS; ++kk) {
@@ -423,8 +429,8 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
                   Vm += sm.sc.wzmid[s] * b;
                 }
               }
-              rw_mid[(size_t)i * D + k] = sm.sc.midc[0] * Sr[n][r] - sm.sc.midc[1] * Zr[n][r] + Um;
-              rw_mid[(size_t)D * D + (size_t)i * D + k] = g.momentum ? (sm.sc.midc[2] * Zr[n][r] + Vm) : 0.f;
+              rw_mid[(size_t)i * D + k] = sm.sc.midc[0] * Sr[jn][r] - sm.sc.midc[1] * Zr[jn][r] + Um;
+              rw_mid[(size_t)D * D + (size_t)i * D + k] = g.momentum ? (sm.sc.midc[2] * Zr[jn][r] + Vm) : 0.f;
             }
           }
         }
@@ -441,8 +447,8 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
       // workgroup writes its own start state, from the segment scan)
       float* rw_next = (FULL && c + 1 < c_end) ? rw + ((size_t)bh * g.ncb + (size_t)(c + 1) * rb) * 2 * D * D : nullptr;
 #pragma unroll
-      for (int n = 0; n < NTD; ++n) {
-        const int n0 = n * 16;
+      for (int jn = 0; jn < NOWN; ++jn) {
+        const int n0 = (nt0 + jn) * 16;
         f32x4 au = zero4(), av = zero4();
 #pragma unroll
         for (int kk = 0; kk < NKS; ++kk) {
@@ -461,14 +467,14 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
               V += sm.sc.wzend[s] * b;
             }
           }
-          const float Sn = a_end * Sr[n][r] - k_end * Zr[n][r] + U;
-          const float Zn = g.momentum ? (b_end * Zr[n][r] + V) : 0.f;
+          const float Sn = a_end * Sr[jn][r] - k_end * Zr[jn][r] + U;
+          const float Zn = g.momentum ? (b_end * Zr[jn][r] + V) : 0.f;
           if (FULL && rw_next) {
             rw_next[(size_t)i * D + k] = Sn;
             rw_next[(size_t)D * D + (size_t)i * D + k] = Zn;
           }
-          Sr[n][r] = do_clamp ? clamp100(Sn) : Sn;
-          Zr[n][r] = Zn;
+          Sr[jn][r] = do_clamp ? clamp100(Sn) : Sn;
+          Zr[jn][r] = Zn;
         }
       }
       if constexpr (AGG) {
@@ -483,12 +489,12 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
       __syncthreads();                    // G3 done reading Sb / Zb
       if (owns) {
 #pragma unroll
-        for (int n = 0; n < NTD; ++n)
+        for (int jn = 0; jn < NOWN; ++jn)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
-            sm.Sb[i][k] = from_f32<T>(Sr[n][r]);
-            sm.Zb[i][k] = from_f32<T>(Zr[n][r]);
+            const int i = mt * 16 + 4 * (lane >> 4) + r, k = (nt0 + jn) * 16 + (lane & 15);
+            sm.Sb[i][k] = from_f32<T>(Sr[jn][r]);
+            sm.Zb[i][k] = from_f32<T>(Zr[jn][r]);
           }
       }
     }
@@ -499,27 +505,27 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
     if constexpr (AGG) {
       float* ag = agg + ((size_t)bh * sg.nseg + seg) * sg.agg_stride;
 #pragma unroll
-      for (int n = 0; n < NTD; ++n)
+      for (int jn = 0; jn < NOWN; ++jn)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
-          ag[(size_t)i * D + k] = Sr[n][r];
-          ag[(size_t)D * D + (size_t)i * D + k] = Zr[n][r];
+          const int i = mt * 16 + 4 * (lane >> 4) + r, k = (nt0 + jn) * 16 + (lane & 15);
+          ag[(size_t)i * D + k] = Sr[jn][r];
+          ag[(size_t)D * D + (size_t)i * D + k] = Zr[jn][r];
         }
-      if (mt == 0 && lane == 0) {
+      if (otile0 == 0 && lane == 0) {
         ag[2 * D * D] = seg_a; ag[2 * D * D + 1] = seg_k; ag[2 * D * D + 2] = seg_b;
       }
     } else if (FULL && seg == sg.nseg - 1) {
       // Sr holds the raw S_{T-1} (the last chunk of the sequence is never a clamp point)
 #pragma unroll
-      for (int n = 0; n < NTD; ++n)
+      for (int jn = 0; jn < NOWN; ++jn)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int i = mt * 16 + 4 * (lane >> 4) + r, k = n * 16 + (lane & 15);
+          const int i = mt * 16 + 4 * (lane >> 4) + r, k = (nt0 + jn) * 16 + (lane & 15);
           const size_t off = sb + (size_t)i * D + k;
-          a.S_T[off] = g.clamp_final ? clamp100(Sr[n][r]) : Sr[n][r];
-          if (g.momentum) a.Z_T[off] = Zr[n][r];
-          if (final_raw) final_raw[off] = Sr[n][r];
+          a.S_T[off] = g.clamp_final ? clamp100(Sr[jn][r]) : Sr[jn][r];
+          if (g.momentum) a.Z_T[off] = Zr[jn][r];
+          if (final_raw) final_raw[off] = Sr[jn][r];
         }
     }
   }

@@ -34,8 +34,10 @@ template <typename T, int CH>
 hipError_t launch_chunk_coef(const Geom& g, const T* decay, const T* lr, const T* beta, const T* gate, float* rec,
                              T* wsh, int kid, hipStream_t stream);
 
+// Two workgroups per CU (16 waves, at most 128 VGPRs each) for the bf16 configurations, whose
+// aggregate-pass LDS fits twice in 160 KB.
 template <typename T, int CH, int D>
-__global__ __launch_bounds__(kSegThreads) void k_fwd_seg_agg(const Geom g, const FwdPtrs<T> a, const SegGeom sg,
+__global__ __launch_bounds__(kSegThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_fwd_seg_agg(const Geom g, const FwdPtrs<T> a, const SegGeom sg,
                                                                float* agg, const float* coef) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   fwd_segment<T, CH, D, WALK_AGG>(g, a, sg, agg, nullptr, nullptr, nullptr, coef, nullptr, smem_raw);
