@@ -47,7 +47,7 @@ EXPORTED_SYMBOLS = (
     "atlas_mem_mfma_selftest",
 )
 
-NKERNELS = 11
+NKERNELS = 12
 
 
 class Problem(ctypes.Structure):

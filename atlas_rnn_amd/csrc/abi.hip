@@ -72,7 +72,8 @@ struct Profiler {
 Profiler& prof() { static Profiler p; return p; }
 const char* kKernelNames[KID_COUNT] = {"k_fwd_seg_agg", "k_fwd_seg", "k_buffer_out", "k_bwd_seg_agg",
                                        "k_bwd_seg", "k_bwd_seg_fixup", "k_seg_reduce_dsref", "k_fwd_seg_scan",
-                                       "k_bwd_seg_scan", "k_chunk_coef_fwd", "k_chunk_coef_bwd"};
+                                       "k_bwd_seg_scan", "k_chunk_coef_fwd", "k_chunk_coef_bwd",
+                                       "k_bwd_scalar"};
 }  // namespace
 
 namespace atlas {
@@ -205,6 +206,9 @@ struct SavedLayout {
 // floats per chunk coefficient record (acoef, kcoef, endc, wsend, wzend, wsmid, wzmid, midc)
 size_t coef_rec_floats(int ch) { return (size_t)2 * ch + 8 + 4 * (ch + kHaloPad); }
 
+// floats per backward chunk of the scalar-gradient inputs (ScalarBlock: Lm, hS, hZ, fS, fZ, Grams)
+size_t scalar_block_floats(int ch) { return (size_t)ch * (ch + kHaloPad) + 2 * (ch + kHaloPad) + 2 * ch + 4; }
+
 SavedLayout saved_layout(const Plan& pl) {
   const Geom& g = pl.g;
   SavedLayout L{};
@@ -224,7 +228,7 @@ SavedLayout saved_layout(const Plan& pl) {
 // backward workspace: adjoint aggregates, re-walk chunk states, dS_ref partials, boundary partials,
 // token-gate (target, lag) gradients.
 struct BwdLayout {
-  size_t agg, segadj, dsref, tail, halo, dw, coef, wsh, total;
+  size_t agg, segadj, dsref, tail, halo, dw, coef, wsh, scal, total;
 };
 
 BwdLayout bwd_layout(const Plan& pl) {
@@ -241,6 +245,7 @@ BwdLayout bwd_layout(const Plan& pl) {
   L.dw = off; off += align256(g.gate_mode == ATLAS_GATE_TOKEN ? (size_t)g.BH * g.T * g.e * sizeof(float) : 0);
   L.coef = off; off += align256((size_t)g.BH * g.nc * coef_rec_floats(pl.CHB) * sizeof(float));
   L.wsh = off; off += align256((size_t)g.BH * g.nc * pl.CHB * (pl.CHB + kHaloPad) * pl.esize);
+  L.scal = off; off += align256((size_t)g.BH * g.nc * scalar_block_floats(pl.CHB) * sizeof(float));
   L.total = off;
   return L;
 }
@@ -302,6 +307,7 @@ int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, voi
   p.halo_part = gb.H > 0 ? reinterpret_cast<float*>(w + L.halo) : nullptr;
   p.dw = gb.gate_mode == ATLAS_GATE_TOKEN ? reinterpret_cast<float*>(w + L.dw) : nullptr;
   p.coef = reinterpret_cast<float*>(w + L.coef);
+  p.scal = reinterpret_cast<float*>(w + L.scal);
   p.wsh = w + L.wsh;
   hipError_t err = hipErrorInvalidValue;
   if (gb.DK == 64) {

@@ -23,6 +23,8 @@ namespace atlas {
 template <typename T, int CH>
 hipError_t launch_chunk_coef(const Geom& g, const T* decay, const T* lr, const T* beta, const T* gate, float* rec,
                              T* wsh, int kid, hipStream_t stream);
+template <typename T, int CH>
+hipError_t launch_bwd_scalar(const Geom& g, const BwdPtrs<T>& a, const BwdSegPtrs& p, hipStream_t stream);
 
 // ---------------------------------------------------------------------------------------------
 // adjoint aggregates
@@ -153,7 +155,6 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg_agg(const Geom g, const
 template <typename T, int CH, int D>
 struct BwdSegSmem {
   static constexpr int SPM = CH + kHaloPad;
-  static constexpr int LWR = ((CH + 2 + 15) / 16) * 16;   // rows of the phase-F GEMM operand
   static constexpr bool kStatesInLds = sizeof(T) == 2;   // fp32 reads S_in / Z_in from the saved chunk states
   // adjoint at the chunk end and the chunk-start state, transposed: X^T[k][i] = X[i][k]
   alignas(16) T sref[D][D + 8];
@@ -165,25 +166,16 @@ struct BwdSegSmem {
   T psi[CH][D + 8];
   T dy[CH][D + 8];
   T deltaT[SPM][D + 8];    // v_s staged by the loads, then delta^T[s][i]
-  union {
-    struct {               // phases A-D
-      T QT[SPM][CH + 8];   // Q^T[s][q],  Q[q][s] = Ws[s, q-1] (psi_q . phi_s)
-      T Qp[CH][SPM + 8];   // Q'[q][s] = Ws[s, q-1] (dy_q . delta_s)
-      T QpT[SPM][CH + 8];
-      alignas(16) T dDT[SPM][D + 8];   // dDelta^T[s][i]
-    } g;
-    struct {               // phase F
-      float Lw[LWR][CH + 1];      // window-weighted Lm rows (q < CH), hS (row CH), hZ (row CH + 1)
-      float LWs[CH + 2][CH + 1];  // Lw C^T: rows q; row CH = HWsS, row CH + 1 unused
-      float LWz[CH + 2][CH + 1];  // Lw B^T: rows q; row CH = HWzS, row CH + 1 = HWzZ
-    } f;
-  } u;
+  struct {
+    T QT[SPM][CH + 8];   // Q^T[s][q],  Q[q][s] = Ws[s, q-1] (psi_q . phi_s)
+    T Qp[CH][SPM + 8];   // Q'[q][s] = Ws[s, q-1] (dy_q . delta_s)
+    T QpT[SPM][CH + 8];
+    alignas(16) T dDT[SPM][D + 8];   // dDelta^T[s][i]
+  } g;
   T wsh[CH][SPM + 8];      // Ws[s, tau-1]
   float Lm[CH][SPM + 1];   // (dy_q . delta_s)(psi_q . phi_s)
   ChunkScalars<CH> sc;
-  DecayTab<CH> tab;
   float hS[SPM], hZ[SPM], fS[CH], fZ[CH];
-  float B1[CH + 1];        // b_{t-1}, t = 0..CH (a_{t-1}, kappa_{t-1} are sc.acoef / sc.kcoef)
   float gram[4];
   float red[kSegWaves][4];
   // followed by the halo carry: float carry[2][H][2 * D] (dynamic size)
@@ -200,24 +192,20 @@ struct BwdPrefetch {
   static constexpr int NT2 = (NTD * NTD + kSegWaves - 1) / kSegWaves;
   static constexpr int NVS = (SPM * (D / 8) + kSegThreads - 1) / kSegThreads;
   static constexpr int NVT = (CH * (D / 8) + kSegThreads - 1) / kSegThreads;
-  static constexpr int NWL = (CH * kMaxWindow + kSegThreads - 1) / kSegThreads;
   static constexpr int REC4 = CoefRec<CH>::SIZE / 4;
   static constexpr int NV_WSH = (CH * SPM / 8 + kSegThreads - 1) / kSegThreads;
   Vec8<T> rk[NVS], rv[NVS], rq[NVT], rd[NVT], wsv[NV_WSH];
   float rc0, rc1, rc2, rc3;
-  T x_al, x_et, x_be, x_ug;
-  T x_wl[NWL];
-  unsigned okS, okT, okW;
-  bool okt, okug, padug;
+  unsigned okS, okT;
   float s_in[NT2][4], z_in[NT2][4];   // raw chunk-start state (saved by the forward), this wave's tiles
 
   __device__ __forceinline__ void load(const Geom& g, const BwdPtrs<T>& a, const BwdSegPtrs& p, int bh, int c,
                                        const float* Sin_g, int tid, int lane, int wave) {
-    const int H = g.H, e = g.e;
+    const int H = g.H;
     const size_t tb = (size_t)bh * g.T;
     const int t0 = c * g.Lc, L = min(g.T, t0 + g.Lc) - t0;
     const size_t r0 = tb + t0;
-    okS = 0; okT = 0; okW = 0;
+    okS = 0; okT = 0;
 #pragma unroll
     for (int j = 0; j < NVS; ++j) {
       const int idx = tid + j * kSegThreads;
@@ -239,23 +227,6 @@ struct BwdPrefetch {
       rq[j] = vec8_load(a.q + row * D + c8 * 8);
       rd[j] = vec8_load(dyp + row * D + c8 * 8);
       okT |= (ok ? 1u : 0u) << j;
-    }
-    okt = tid < L;
-    const size_t rt = okt ? r0 + tid : r0;
-    x_al = a.decay[rt];
-    x_et = a.lr[rt];
-    x_be = ((g.momentum && a.beta) ? a.beta : a.decay)[rt];
-    const T* gp = a.gate ? a.gate : a.decay;
-    const int pg = t0 - H + tid;
-    okug = g.gate_mode == GATE_TOKEN && tid < SPM && tid < H + L && pg >= 0;
-    padug = g.gate_mode == GATE_TOKEN && tid < SPM && tid < H + L && pg < 0;
-    x_ug = gp[okug ? tb + pg : r0];
-#pragma unroll
-    for (int j = 0; j < NWL; ++j) {
-      const int idx = tid + j * kSegThreads;
-      const bool ok = g.gate_mode == GATE_LAG && idx < CH * e && idx / e < L;
-      x_wl[j] = gp[ok ? r0 * e + idx : r0];
-      okW |= (ok ? 1u : 0u) << j;
     }
     {
       const float4 r4 = reinterpret_cast<const float4*>(p.coef + ((size_t)bh * g.nc + c) * CoefRec<CH>::SIZE)[tid < REC4 ? tid : 0];
@@ -283,7 +254,6 @@ struct BwdPrefetch {
   // chunk inputs -> LDS (the states are consumed by the caller)
   template <typename Sm>
   __device__ __forceinline__ void store(const Geom& g, const BwdPtrs<T>& a, Sm& sm, int tid) {
-    const int e = g.e;
 #pragma unroll
     for (int j = 0; j < NVS; ++j) {
       const int idx = tid + j * kSegThreads;
@@ -314,28 +284,10 @@ struct BwdPrefetch {
       const int v = tid + j * kSegThreads;
       if (v < CH * SPM / 8) wsv[j].store(&sm.wsh[(v * 8) / SPM][(v * 8) % SPM]);
     }
-    if (tid < CH) {
-      sm.sc.alpha[tid] = okt ? to_f32(x_al) : 1.f;
-      sm.sc.eta[tid] = okt ? to_f32(x_et) : 0.f;
-      sm.sc.beta[tid] = okt ? (g.momentum ? to_f32(x_be) : 0.f) : 1.f;
-      sm.fS[tid] = 0.f; sm.fZ[tid] = 0.f;
-    }
+    if (tid < CH) { sm.fS[tid] = 0.f; sm.fZ[tid] = 0.f; }
     for (int s = tid; s < SPM; s += kSegThreads) { sm.hS[s] = 0.f; sm.hZ[s] = 0.f; }
-    if (g.gate_mode == GATE_TOKEN && tid < SPM) sm.sc.ug[tid] = okug ? to_f32(x_ug) : (padug ? 1.f : 0.f);
-    if (g.gate_mode == GATE_LAG) {
-#pragma unroll
-      for (int j = 0; j < NWL; ++j) {
-        const int idx = tid + j * kSegThreads;
-        if (idx < CH * e) sm.sc.wl[idx] = ((okW >> j) & 1u) ? to_f32(x_wl[j]) : 0.f;
-      }
-    }
   }
 };
-
-template <typename T>
-__device__ __forceinline__ float src_w(int gate_mode, float ug, const float* wl, int e, int t, int j) {
-  return gate_mode == GATE_TOKEN ? ug : (gate_mode == GATE_LAG ? wl[t * e + j] : 1.f);
-}
 
 template <typename T, int CH, int D>
 __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const BwdPtrs<T> a, const SegGeom sg,
@@ -461,33 +413,31 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
       }
     }
 
-    // ---- phase A: G1 delta^T (waves 0-6) | decay table columns (wave 7)
-    // Tile indices past the end of a tile list are clamped: the MFMAs stay unconditional and only
-    // the stores are guarded.
-    if (wave < 7) {
-      constexpr int NT1 = NTS * NTD, PER1 = (NT1 + 6) / 7;
+    // ---- phase A: G1 delta^T[s][i] = (S_ref phi_s)[i] - v_s[i] (all waves; the accumulator of lane
+    // (i0..i0+3, s) is contiguous in deltaT, so v is read and delta written in place with one
+    // 4-element access each). Tile indices past the end are clamped: the MFMAs stay unconditional
+    // and only the stores are guarded.
+    {
+      constexpr int NT1 = NTS * NTD, PER1 = (NT1 + kSegWaves - 1) / kSegWaves;
 #pragma unroll 1
       for (int j = 0; j < PER1; ++j) {
-        const int tile = min(wave + 7 * j, NT1 - 1);
-        const bool valid = NT1 % 7 == 0 || wave + 7 * j < NT1;
-        const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
+        const int tile = min(wave + kSegWaves * j, NT1 - 1);
+        const bool valid = NT1 % kSegWaves == 0 || wave + kSegWaves * j < NT1;
+        const int m0 = (tile % NTD) * 16, n0 = (tile / NTD) * 16;   // m: rows i, n: sources s
         f32x4 acc = zero4();
 #pragma unroll
         for (int k0 = 0; k0 < D; k0 += M::KS)
-          acc = M::mma(frag_ld_row<T>(&sm.phi[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.sref[0][0], D + 8, n0, k0), acc);
+          acc = M::mma(frag_ld_row<T>(&sm.sref[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.phi[0][0], D + 8, n0, k0), acc);
         if (valid) {
-          const int i = n0 + (lane & 15);
+          const int s = n0 + (lane & 15), i0 = m0 + 4 * (lane >> 4);
+          const int pp = t0 - H + s;
+          const bool src_ok = s < H + L && pp >= 0;
+          float d[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int s = m0 + 4 * (lane >> 4) + r;
-            const int pp = t0 - H + s;
-            const float d = (s < H + L && pp >= 0) ? acc[r] - to_f32(sm.deltaT[s][i]) : 0.f;
-            sm.deltaT[s][i] = from_f32<T>(d);
-          }
+          for (int r = 0; r < 4; ++r) d[r] = src_ok ? acc[r] - to_f32(sm.deltaT[s][i0 + r]) : 0.f;
+          store4<T>(&sm.deltaT[s][i0], d[0], d[1], d[2], d[3]);
         }
       }
-    } else {
-      decay_columns_wave<CH>(sm.tab, sm.sc, sm.B1);
     }
     __syncthreads();
     // G2 / G3: Kmat = psi phi^T, K3 = dy delta -> Q^T, Q', Q'^T, Lm
@@ -510,10 +460,10 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
           for (int r = 0; r < 4; ++r) {
             const int t = m0 + 4 * (lane >> 4) + r;
             const float w = to_f32(sm.wsh[t][s]);
-            sm.u.g.QT[s][t] = from_f32<T>(w * kk[r]);
+            sm.g.QT[s][t] = from_f32<T>(w * kk[r]);
             const T qp = from_f32<T>(w * k3[r]);
-            sm.u.g.Qp[t][s] = qp;
-            sm.u.g.QpT[s][t] = qp;
+            sm.g.Qp[t][s] = qp;
+            sm.g.QpT[s][t] = qp;
             sm.Lm[t][s] = kk[r] * k3[r];
           }
         }
@@ -538,7 +488,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         }
 #pragma unroll
         for (int k0 = 0; k0 < CH; k0 += M::KS)
-          aq = M::mma(frag_ld_tr<T>(&sm.dy[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.u.g.QT[0][0], CH + 8, n0, k0), aq);
+          aq = M::mma(frag_ld_tr<T>(&sm.dy[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.g.QT[0][0], CH + 8, n0, k0), aq);
         if (valid) {
           const int s = n0 + (lane & 15);
           const float wz = sm.sc.wzend[s], ws = sm.sc.wsend[s];
@@ -551,7 +501,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
             hz += d * az[r];
             dd[r] = wz * az[r] - ws * as[r] - aq[r];
           }
-          store4<T>(&sm.u.g.dDT[s][m0 + 4 * (lane >> 4)], dd[0], dd[1], dd[2], dd[3]);
+          store4<T>(&sm.g.dDT[s][m0 + 4 * (lane >> 4)], dd[0], dd[1], dd[2], dd[3]);
           hs += __shfl_xor(hs, 16); hs += __shfl_xor(hs, 32);
           hz += __shfl_xor(hz, 16); hz += __shfl_xor(hz, 32);
           if (lane < 16) { atomicAdd(&sm.hS[s], hs); atomicAdd(&sm.hZ[s], hz); }
@@ -567,7 +517,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         const int s = idx / D, i = idx % D;
         const int pp = t0 - H + s;
         if (pp < 0) continue;
-        float val = -to_f32(sm.u.g.dDT[s][i]);
+        float val = -to_f32(sm.g.dDT[s][i]);
         if (s < H) {
           if (first) { if (c > 0) p.halo_part[(((size_t)bh * sg.nseg + seg) * H + s) * (2 * D) + i] = val; }
           else cur_carry[s * 2 * D + i] = val;
@@ -585,7 +535,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
       f32x4 acc = zero4();
 #pragma unroll
       for (int k0 = 0; k0 < SPM; k0 += M::KS)
-        acc = M::mma(frag_ld_tr<T>(&sm.u.g.dDT[0][0], D + 8, m0, k0), frag_ld_tr<T>(&sm.phi[0][0], D + 8, n0, k0), acc);
+        acc = M::mma(frag_ld_tr<T>(&sm.g.dDT[0][0], D + 8, m0, k0), frag_ld_tr<T>(&sm.phi[0][0], D + 8, n0, k0), acc);
 #pragma unroll
       for (int r = 0; r < 4; ++r) dsr[j][r] += acc[r];
     }
@@ -623,7 +573,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         }
 #pragma unroll
         for (int k0 = 0; k0 < SPM; k0 += M::KS)
-          aq = M::mma(frag_ld_row<T>(&sm.u.g.Qp[0][0], SPM + 8, m0, k0), frag_ld_tr<T>(&sm.phi[0][0], D + 8, n0, k0), aq);
+          aq = M::mma(frag_ld_row<T>(&sm.g.Qp[0][0], SPM + 8, m0, k0), frag_ld_tr<T>(&sm.phi[0][0], D + 8, n0, k0), aq);
         const int k = n0 + (lane & 15);
         f32x4 dpsi;
         float fsp[4], fzp[4];
@@ -717,11 +667,11 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
           const typename M::frag fa = frag_ld_row<T>(&sm.deltaT[0][0], D + 8, m0, k0);
           a1 = M::mma(fa, frag_ld_row<T>(&sm.dZeT[0][0], D + 8, n0, k0), a1);
           a2 = M::mma(fa, frag_ld_row<T>(&sm.dSeT[0][0], D + 8, n0, k0), a2);
-          a4 = M::mma(frag_ld_row<T>(&sm.u.g.dDT[0][0], D + 8, m0, k0), frag_ld_tr<T>(&sm.sref[0][0], D + 8, n0, k0), a4);
+          a4 = M::mma(frag_ld_row<T>(&sm.g.dDT[0][0], D + 8, m0, k0), frag_ld_tr<T>(&sm.sref[0][0], D + 8, n0, k0), a4);
         }
 #pragma unroll
         for (int k0 = 0; k0 < CH; k0 += M::KS)
-          a3 = M::mma(frag_ld_row<T>(&sm.u.g.QpT[0][0], CH + 8, m0, k0), frag_ld_tr<T>(&sm.psi[0][0], D + 8, n0, k0), a3);
+          a3 = M::mma(frag_ld_row<T>(&sm.g.QpT[0][0], CH + 8, m0, k0), frag_ld_tr<T>(&sm.psi[0][0], D + 8, n0, k0), a3);
         if (valid) {
           const int k = n0 + (lane & 15);
 #pragma unroll
@@ -747,7 +697,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
       }
     }
 
-    // ---- phase E: chunk-start adjoint (the B1 step) -> carried (dS, dZ) for chunk c - 1
+    // ---- phase E: chunk-start adjoint (the transposed chunk transition) -> carried (dS, dZ) for chunk c - 1
     {
       const float ae = sm.sc.endc[0], ke = sm.sc.endc[1], be = sm.sc.endc[2];
 #pragma unroll
@@ -780,94 +730,15 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
       }
     }
 
-    // ---- phase F: scalar gradients
-    __syncthreads();   // phase D done with the union's GEMM operands
-    // F1: Lw[q][t'] = sum_j w(t', j) X_q[t' + H - j],  X_q = Lm[q] (q < CH), hS (q = CH), hZ (q = CH + 1)
-    for (int idx = tid; idx < (CH + 2) * CH; idx += kSegThreads) {
-      const int q = idx / CH, tq = idx % CH;
-      const float* X = q < CH ? &sm.Lm[q][0] : (q == CH ? sm.hS : sm.hZ);
-      float acc = 0.f;
-      if (tq < L) {
-        for (int j = 0; j < e; ++j) {
-          const int s = tq + H - j;
-          acc += src_w<T>(g.gate_mode, sm.sc.ug[s], sm.sc.wl, e, tq, j) * X[s];
-        }
-      }
-      sm.u.f.Lw[q][tq] = acc;
-    }
-    __syncthreads();
-    // F2: the window-weighted recurrences along the chunk as GEMMs with the decay tables:
-    //   LWz[q][t] = sum_t' B[t'+1][t] Lw[q][t'],   LWs[q][t] = sum_t' C[t'+1][t] Lw[q][t']
+    // ---- inputs of the scalar gradients (k_bwd_scalar) -> HBM
+    __syncthreads();   // hS, hZ, fS, fZ, Lm complete
     {
-      typedef MM<float> MF;
-      constexpr int NRT = Sm::LWR / 16, NCT = CH / 16;
-      for (int job = wave; job < 2 * NRT * NCT; job += kSegWaves) {
-        const int mat = job / (NRT * NCT), tile = job % (NRT * NCT);
-        const int m0 = (tile / NCT) * 16, n0 = (tile % NCT) * 16;
-        const float* tabp = mat == 0 ? &sm.tab.B[1][0] : &sm.tab.C[1][0];
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int k0 = 0; k0 < CH; k0 += MF::KS)
-          acc = MF::mma(frag_ld<float>(&sm.u.f.Lw[0][0], CH + 1, 1, m0, k0), frag_ld<float>(tabp, 1, CH + 1, n0, k0), acc);
-        float* dst = mat == 0 ? &sm.u.f.LWz[0][0] : &sm.u.f.LWs[0][0];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int q = m0 + 4 * (lane >> 4) + r;
-          if (q < CH + 2) dst[q * (CH + 1) + n0 + (lane & 15)] = acc[r];
-        }
-      }
-    }
-    __syncthreads();
-    // F3: one wave per term (0: dalpha, 1: deta, 2: dbeta, 3 + j: dw[t, j]); lane = (q part, target t).
-    //   The running products of the step-by-step adjoint are table entries: prod alpha = A[t+1][q-1],
-    //   prod beta = B[t+1][q-1], the eta-mixed term = C[t+1][q-1] (zero for q - 1 < t).
-    {
-      constexpr int NQ = kWave / CH;
-      constexpr int QPP = CH / NQ;
-      const int t = lane % CH, part = lane / CH;
-      const int nterm = 3 + (g.gate_mode != GATE_NONE ? e : 0);
-      const float gss = sm.gram[0], gsz = sm.gram[1], gzz = sm.gram[2];
-      const float am1 = sm.sc.acoef[t], km1 = sm.sc.kcoef[t], bm1 = sm.B1[t], b0 = sm.B1[t + 1];
-      const float Aend = sm.tab.A[t + 1][CH - 1], Bend = sm.tab.B[t + 1][CH - 1], Cend = sm.tab.C[t + 1][CH - 1];
-      for (int term = wave; term < nterm; term += kSegWaves) {
-        const float* W = term < 2 ? &sm.tab.A[t + 1][0] : &sm.tab.C[t + 1][0];
-        const int sj = term >= 3 ? t + H - (term - 3) : 0;
-        float acc = 0.f;
-#pragma unroll 4
-        for (int qq = 0; qq < QPP; ++qq) {
-          const int q = part * QPP + qq;
-          if (q >= 1) {
-            float v;
-            if (term == 0) v = am1 * sm.fS[q] - km1 * sm.fZ[q] - (t > 0 ? sm.u.f.LWs[q][t - 1] : 0.f);
-            else if (term == 1) v = b0 * sm.fZ[q] + sm.u.f.LWz[q][t];
-            else if (term == 2) v = bm1 * sm.fZ[q] + (t > 0 ? sm.u.f.LWz[q][t - 1] : 0.f);
-            else v = sm.Lm[q][sj];
-            acc += W[q - 1] * v;
-          }
-        }
-#pragma unroll
-        for (int off = CH; off < kWave; off <<= 1) acc += __shfl_xor(acc, off);
-        if (part == 0 && t < L) {
-          const size_t tt = tb + t0 + t;
-          if (term == 0) {
-            const float hss_m1 = t > 0 ? sm.u.f.LWs[CH][t - 1] : 0.f;
-            a.ddecay[tt] = from_f32<T>(acc + Aend * (am1 * gss - km1 * gsz - hss_m1));
-          } else if (term == 1) {
-            a.dlr[tt] = from_f32<T>(-(acc + Aend * (b0 * gsz + sm.u.f.LWz[CH][t])));
-          } else if (term == 2) {
-            if (g.momentum && a.dbeta) {
-              const float hzs_m1 = t > 0 ? sm.u.f.LWz[CH][t - 1] : 0.f;
-              const float hzz_m1 = t > 0 ? sm.u.f.LWz[CH + 1][t - 1] : 0.f;
-              a.dbeta[tt] = from_f32<T>(Bend * (bm1 * gzz + hzz_m1) - Cend * (bm1 * gsz + hzs_m1) - acc);
-            }
-          } else {
-            const int j = term - 3;
-            const float v = Bend * sm.hZ[sj] - Cend * sm.hS[sj] - acc;
-            if (g.gate_mode == GATE_LAG) a.dgate[tt * e + j] = from_f32<T>(v);
-            else p.dw[tt * e + j] = v;
-          }
-        }
-      }
+      typedef ScalarBlock<CH> SB;
+      float* blk = p.scal + ((size_t)bh * g.nc + c) * SB::SIZE;
+      for (int idx = tid; idx < CH * SPM; idx += kSegThreads) blk[SB::LM + idx] = sm.Lm[idx / SPM][idx % SPM];
+      for (int idx = tid; idx < SPM; idx += kSegThreads) { blk[SB::HS + idx] = sm.hS[idx]; blk[SB::HZ + idx] = sm.hZ[idx]; }
+      if (tid < CH) { blk[SB::FS + tid] = sm.fS[tid]; blk[SB::FZ + tid] = sm.fZ[tid]; }
+      if (tid < 4) blk[SB::GRAM + tid] = tid < 3 ? sm.gram[tid] : 0.f;
     }
   }
 
@@ -1047,6 +918,7 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
     prof_end(KID_BWD_CHUNK, stream);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
+  if ((err = launch_bwd_scalar<T, CH>(g, a, p, stream)) != hipSuccess) return err;
   prof_begin(KID_BWD_FIXUP, stream);
   hipLaunchKernelGGL((k_bwd_seg_fixup<T, D>), dim3(sg.nseg, g.BH), dim3(kThreads), 0, stream, g, a, sg, p);
   prof_end(KID_BWD_FIXUP, stream);

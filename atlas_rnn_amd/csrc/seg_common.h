@@ -28,7 +28,27 @@ struct BwdSegPtrs {
   float* dw;                 // [BH][T][e] per (target, lag) gradients (token gates)
   float* coef;               // [BH][nc][CoefRec] chunk coefficient records (k_chunk_coef)
   void* wsh;                 // [BH][nc][CH][SPM] Ws[s, t-1] of every chunk (input element type)
+  float* scal;               // [BH][nc][ScalarBlock] per-chunk inputs of the scalar gradients
 };
+
+// Per backward chunk, written by the reverse walk and read by k_bwd_scalar (fp32):
+//   Lm[q][s] = (dy_q . delta_s)(psi_q . phi_s)   [CH][SPM]
+//   hS[s] = <dS_end, delta_s phi_s^T>, hZ[s] = <dZ_end, delta_s phi_s^T>   (dense buffer sources: <., B_s>)
+//   fS[q] = psi_q . (S_in^T dy_q), fZ[q] = psi_q . (Z_in^T dy_q)
+//   gram = <dS_end, S_in>, <dS_end, Z_in>, <dZ_end, Z_in>
+template <int CH>
+struct ScalarBlock {
+  static constexpr int SPM = CH + kHaloPad;
+  static constexpr int LM = 0, HS = CH * SPM, HZ = HS + SPM, FS = HZ + SPM, FZ = FS + CH, GRAM = FZ + CH;
+  static constexpr int SIZE = GRAM + 4;
+  static_assert(SIZE % 4 == 0, "16-byte aligned blocks");
+};
+
+// Window weight of the source t - j for target t: the token gate of the source, the lag gate
+// w[t][j], or 1.
+__device__ __forceinline__ float src_w(int gate_mode, float ug, const float* wl, int e, int t, int j) {
+  return gate_mode == GATE_TOKEN ? ug : (gate_mode == GATE_LAG ? wl[t * e + j] : 1.f);
+}
 
 // Eight consecutive elements: one 16-byte (bf16) or two 16-byte (fp32) vector accesses.
 template <typename T>

@@ -178,7 +178,7 @@ int atlas_affine_scan_bwd(int n, int t, int r, int d, const float* A, const floa
 /* ---- diagnostics (no reference counterpart) ------------------------------------------------ */
 
 /* Number of kernels the timing hooks distinguish (index -> atlas_mem_kernel_name). */
-#define ATLAS_MEM_NKERNELS 11
+#define ATLAS_MEM_NKERNELS 12
 
 /* Opt-in timing: while enabled, each kernel launch of atlas_mem_fwd/atlas_mem_bwd is bracketed
  * by HIP events on its stream (adds two event records per launch). */
