@@ -772,16 +772,25 @@ __global__ __launch_bounds__(kThreads) void k_bwd_seg_scan(const Geom g, const f
   float dZ = (g.momentum && dZ_T) ? dZ_T[off] : 0.f;
   const float* ag = p.adj_agg + (size_t)bh * sg.nseg * sg.agg_stride;
   float* sa = p.seg_adj + (size_t)bh * sg.nseg * 2 * D * D;
-  for (int js = sg.nseg - 1; js >= 0; --js) {
-    sa[(size_t)js * 2 * D * D + idx] = dS;
-    sa[(size_t)js * 2 * D * D + D * D + idx] = dZ;
-    if (js > 0) {
-      const float* aj = ag + (size_t)js * sg.agg_stride;
-      const float ta = aj[2 * D * D], tk = aj[2 * D * D + 1], tbb = aj[2 * D * D + 2];
-      const float Lv = aj[idx], Kv = aj[D * D + idx];
-      const float s_out = dS;
-      dS = ta * s_out + Lv;
-      dZ = g.momentum ? (tbb * dZ - tk * s_out + Kv) : 0.f;
+  // aggregates are read kScanBatch segments at a time (one memory round trip per batch)
+  for (int j0 = sg.nseg - 1; j0 >= 0; j0 -= kScanBatch) {
+    float Lv[kScanBatch], Kv[kScanBatch], ta[kScanBatch], tk[kScanBatch], tbb[kScanBatch];
+#pragma unroll
+    for (int u = 0; u < kScanBatch; ++u) {
+      const float* aj = ag + (size_t)max(j0 - u, 0) * sg.agg_stride;
+      Lv[u] = aj[idx]; Kv[u] = aj[D * D + idx];
+      ta[u] = aj[2 * D * D]; tk[u] = aj[2 * D * D + 1]; tbb[u] = aj[2 * D * D + 2];
+    }
+#pragma unroll
+    for (int u = 0; u < kScanBatch; ++u) {
+      const int js = j0 - u;
+      if (js >= 0) {
+        sa[(size_t)js * 2 * D * D + idx] = dS;
+        sa[(size_t)js * 2 * D * D + D * D + idx] = dZ;
+        const float s_out = dS;
+        dS = ta[u] * s_out + Lv[u];
+        dZ = g.momentum ? (tbb[u] * dZ - tk[u] * s_out + Kv[u]) : 0.f;
+      }
     }
   }
 }

@@ -8,6 +8,7 @@ namespace atlas {
 
 constexpr int kSegThreads = 512;   // 8 waves per workgroup
 constexpr int kSegWaves = kSegThreads / kWave;
+constexpr int kScanBatch = 8;   // segment aggregates loaded per round trip by the segment scans
 
 struct SegGeom {
   int G;              // chunks per segment

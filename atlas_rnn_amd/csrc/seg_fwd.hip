@@ -54,16 +54,25 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg_scan(const Geom g, const f
   float Z = (g.momentum && Z0) ? Z0[(size_t)bh * D * D + idx] : 0.f;
   const float* ag = agg + (size_t)bh * sg.nseg * sg.agg_stride;
   float* ss = seg_states + (size_t)bh * sg.nseg * 2 * D * D;
-  for (int js = 0; js < sg.nseg; ++js) {
-    ss[(size_t)js * 2 * D * D + idx] = S;
-    ss[(size_t)js * 2 * D * D + D * D + idx] = Z;
-    if (js + 1 < sg.nseg) {
-      const float* aj = ag + (size_t)js * sg.agg_stride;
-      const float ta = aj[2 * D * D], tk = aj[2 * D * D + 1], tbb = aj[2 * D * D + 2];
-      const float U = aj[idx], V = aj[D * D + idx];
-      const float Sn = ta * S - tk * Z + U;
-      Z = g.momentum ? tbb * Z + V : 0.f;
-      S = Sn;
+  // aggregates are read kScanBatch segments at a time (one memory round trip per batch)
+  for (int j0 = 0; j0 < sg.nseg; j0 += kScanBatch) {
+    float U[kScanBatch], V[kScanBatch], ta[kScanBatch], tk[kScanBatch], tbb[kScanBatch];
+#pragma unroll
+    for (int u = 0; u < kScanBatch; ++u) {
+      const float* aj = ag + (size_t)min(j0 + u, sg.nseg - 1) * sg.agg_stride;
+      U[u] = aj[idx]; V[u] = aj[D * D + idx];
+      ta[u] = aj[2 * D * D]; tk[u] = aj[2 * D * D + 1]; tbb[u] = aj[2 * D * D + 2];
+    }
+#pragma unroll
+    for (int u = 0; u < kScanBatch; ++u) {
+      const int js = j0 + u;
+      if (js < sg.nseg) {
+        ss[(size_t)js * 2 * D * D + idx] = S;
+        ss[(size_t)js * 2 * D * D + D * D + idx] = Z;
+        const float Sn = ta[u] * S - tk[u] * Z + U[u];
+        Z = g.momentum ? tbb[u] * Z + V[u] : 0.f;
+        S = Sn;
+      }
     }
   }
 }
