@@ -174,10 +174,9 @@ enum WalkMode { WALK_AGG = 0, WALK_FULL = 1 };
 //                the chunk start and, when g.Lmid > 0, the state after token Lmid - 1.
 // The chunk coefficients (a, kappa, end weights, Ws[s, t-1]) come precomputed from k_chunk_coef
 // (coef: [BH][nc] records, wsh_all: [BH][nc][CH][SPM], full walk only) with the prefetch.
-// Wave roles per chunk: P1 all waves run G1 (and G2 for the full walk); P3 of the full walk:
-// waves 0-3 run G3 (y) while waves 4-7 run G4 and update the states, which they hold in
-// registers (wave 4 + m owns state rows 16 m .. 16 m + 15); P3 of the aggregate pass: every
-// wave runs G4 on its share of the state tiles.
+// Wave roles per chunk: P1 all waves run G1 (and G2 for the full walk); P3 all waves run G3 (y,
+// full walk), then G4 on the state tiles they own, updating the states, which they hold in
+// registers.
 template <typename T, int CH, int D, int MODE>
 __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg, float* agg,
                                             const float* seg_states, float* rw, float* final_raw,
@@ -200,14 +199,13 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
   // ---- S_ref (bf16/fp32 operand copy)
   for (int idx = tid; idx < D * D; idx += kSegThreads) sm.sref[idx / D][idx % D] = from_f32<T>(a.S_ref[sb + idx]);
 
-  // ---- state registers. Full walk: wave 4 + m owns row tile m (all NTD column tiles) while
-  // waves 0-3 run G3. Aggregate pass: the NTD x NTD tiles are spread over all waves, NOWN tiles
-  // of one row tile per wave.
-  constexpr int NOWN = FULL ? NTD : (NTD * NTD < kSegWaves ? 1 : NTD * NTD / kSegWaves);
-  constexpr int OWNERS = FULL ? NTD : NTD * NTD / NOWN;
-  static_assert(FULL || NTD % NOWN == 0, "owned tiles share a row tile");
-  const bool owns = FULL ? (wave >= 4 && wave - 4 < NTD) : (wave < OWNERS);
-  const int otile0 = FULL ? (wave - 4) * NTD : wave * NOWN;   // first owned tile, row-major over (mt, n)
+  // ---- state registers: the NTD x NTD state tiles are spread over the waves, NOWN tiles of one
+  // row tile per wave.
+  constexpr int NOWN = NTD * NTD < kSegWaves ? 1 : NTD * NTD / kSegWaves;
+  constexpr int OWNERS = NTD * NTD / NOWN;
+  static_assert(NTD % NOWN == 0, "owned tiles share a row tile");
+  const bool owns = wave < OWNERS;
+  const int otile0 = wave * NOWN;                             // first owned tile, row-major over (mt, n)
   const int mt = otile0 / NTD, nt0 = otile0 % NTD;           // row tile, first column tile
   float Sr[NOWN][4], Zr[NOWN][4];
 #pragma unroll
@@ -342,13 +340,14 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
       __syncthreads();
     }
 
-    // ---- P3: G3 (waves 0-3, full walk) | G4 + state update (waves 4-7)
-    if (FULL && wave < 4) {
-      constexpr int NT3 = (CH / 16) * NTD, PER3 = (NT3 + 3) / 4;
-      static_assert(!FULL || NT3 % 4 == 0, "G3 tiles split evenly over 4 waves");
+    // ---- P3: G3 (y, full walk), then G4 + state update on the owned state tiles (all waves)
+    if constexpr (FULL) {
+      constexpr int NT3 = (CH / 16) * NTD, PER3 = (NT3 + kSegWaves - 1) / kSegWaves;
 #pragma unroll 1
       for (int j = 0; j < PER3; ++j) {
-        const int tile = wave + 4 * j;
+        // past the end of the tile list the tile index is clamped (unconditional MFMAs, guarded stores)
+        const int tile = min(wave + kSegWaves * j, NT3 - 1);
+        const bool valid = NT3 % kSegWaves == 0 || wave + kSegWaves * j < NT3;
         {
           const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;   // m: tau, n: rows i
           f32x4 aq = zero4(), as = zero4(), az = zero4();
@@ -385,11 +384,12 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int t = m0 + 4 * (lane >> 4) + r;
-            if (t < L) a.y[(tb + t0 + t) * D + i] = from_f32<T>(yv[r]);
+            if (valid && t < L) a.y[(tb + t0 + t) * D + i] = from_f32<T>(yv[r]);
           }
         }
       }
-    } else if (owns) {
+    }
+    if (owns) {
       // G4: U = -delta diag(Ws_end) phi^T, V = delta diag(Wz_end) phi^T, the end weights applied to the
       // delta fragments in registers; the full walk also forms the state after token Lmid - 1.
       const float a_end = sm.sc.endc[0], k_end = sm.sc.endc[1], b_end = sm.sc.endc[2];
