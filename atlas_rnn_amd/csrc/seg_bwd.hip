@@ -332,7 +332,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
   }
 
   Sm& sm = *reinterpret_cast<Sm*>(smem_raw);
-  float* carry = reinterpret_cast<float*>(smem_raw + sizeof(Sm));   // [2][H][2D]
+  float* carry = reinterpret_cast<float*>(smem_raw + carry_offset<Sm>());   // [2][H][2D], 16-byte aligned
   for (int idx = tid; idx < D * D; idx += kSegThreads) sm.sref[idx / D][idx % D] = from_f32<T>(a.S_ref[sb + idx]);
   for (int idx = tid; idx < 2 * H * 2 * D; idx += kSegThreads) carry[idx] = 0.f;
 
@@ -511,21 +511,32 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
     __syncthreads();
 
     // ---- phase C: dv from dDelta; G6 dS_ref; G7 dpsi (+ fS, fZ); d buffer_in
-    {
+    {   // dv: 8 features of one source per lane
       const int tail0 = t1 - H;
-      for (int idx = tid; idx < (H + L) * D; idx += kSegThreads) {
-        const int s = idx / D, i = idx % D;
+      constexpr int NV = D / 8;
+      for (int idx = tid; idx < (H + L) * NV; idx += kSegThreads) {
+        const int s = idx / NV, i0 = (idx % NV) * 8;
         const int pp = t0 - H + s;
         if (pp < 0) continue;
-        float val = -to_f32(sm.g.dDT[s][i]);
+        const Vec8<T> x = vec8_load(&sm.g.dDT[s][i0]);
+        float val[8];
+#pragma unroll
+        for (int e8 = 0; e8 < 8; ++e8) val[e8] = -to_f32(x.v[e8]);
         if (s < H) {
-          if (first) { if (c > 0) p.halo_part[(((size_t)bh * sg.nseg + seg) * H + s) * (2 * D) + i] = val; }
-          else cur_carry[s * 2 * D + i] = val;
+          float* dst = first ? (c > 0 ? p.halo_part + (((size_t)bh * sg.nseg + seg) * H + s) * (2 * D) + i0 : nullptr)
+                             : cur_carry + s * 2 * D + i0;
+          if (dst) store8f(dst, val);
           continue;
         }
-        if (pp >= tail0) val += prev_carry[(pp - tail0) * 2 * D + i];
-        if (pp >= seg_tail0) p.tail_part[(((size_t)bh * sg.nseg + seg) * H + (pp - seg_tail0)) * (2 * D) + i] = val;
-        else a.dv[(tb + pp) * D + i] = from_f32<T>(val);
+        if (pp >= tail0) add8f(val, prev_carry + (pp - tail0) * 2 * D + i0);
+        if (pp >= seg_tail0) {
+          store8f(p.tail_part + (((size_t)bh * sg.nseg + seg) * H + (pp - seg_tail0)) * (2 * D) + i0, val);
+        } else {
+          Vec8<T> y;
+#pragma unroll
+          for (int e8 = 0; e8 < 8; ++e8) y.v[e8] = from_f32<T>(val[e8]);
+          y.store(a.dv + (tb + pp) * D + i0);
+        }
       }
     }
 #pragma unroll
@@ -539,25 +550,26 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
 #pragma unroll
       for (int r = 0; r < 4; ++r) dsr[j][r] += acc[r];
     }
-    {   // G7: dpsi[q, k] = a_{q-1} (dy_q S_in)[k] - kappa_{q-1} (dy_q Z_in)[k] - sum_s Q'[q, s] phi_s[k]
+    {   // G7: dpsi[q, k] = a_{q-1} (dy_q S_in)[k] - kappa_{q-1} (dy_q Z_in)[k] - sum_s Q'[q, s] phi_s[k],
+        // computed as transposed tiles: a lane holds features k0..k0+3 of one target q
       constexpr int NT7 = NTC * NTD, PER7 = (NT7 + kSegWaves - 1) / kSegWaves;
 #pragma unroll 1
       for (int j = 0; j < PER7; ++j) {
         const int tile = min(wave + kSegWaves * j, NT7 - 1);
         const bool valid = NT7 % kSegWaves == 0 || wave + kSegWaves * j < NT7;
-        const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
+        const int m0 = (tile % NTD) * 16, n0 = (tile / NTD) * 16;   // m: features k, n: targets q
         f32x4 as = zero4(), az = zero4(), aq = zero4();
 #pragma unroll
         for (int k0 = 0; k0 < D; k0 += M::KS) {
-          const typename M::frag fa = frag_ld_row<T>(&sm.dy[0][0], D + 8, m0, k0);
+          const typename M::frag fb = frag_ld_row<T>(&sm.dy[0][0], D + 8, n0, k0);
           if constexpr (SIL) {
-            as = M::mma(fa, frag_ld_row<T>(&sm.SinT[0][0], D + 8, n0, k0), as);
-            az = M::mma(fa, frag_ld_row<T>(&sm.ZinT[0][0], D + 8, n0, k0), az);
-          } else {
+            as = M::mma(frag_ld_row<T>(&sm.SinT[0][0], D + 8, m0, k0), fb, as);
+            az = M::mma(frag_ld_row<T>(&sm.ZinT[0][0], D + 8, m0, k0), fb, az);
+          } else {   // S_in[i][k] straight from the saved fp32 state (16 consecutive k per row i)
             typename M::frag fs;
             {
               const int kb = k0 + (lane >> 4) * M::KL;
-              const float* q = Sin_g + (size_t)kb * D + n0 + (lane & 15);
+              const float* q = Sin_g + (size_t)kb * D + m0 + (lane & 15);
               if constexpr (M::KL == 1) fs = static_cast<T>(clamp_in ? clamp100(q[0]) : q[0]);
               else {
 #pragma unroll
@@ -567,23 +579,22 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
                 }
               }
             }
-            as = M::mma(fa, fs, as);
-            az = M::mma(fa, frag_ld_or_zero<T>(g.momentum ? Zin_g : nullptr, 1, D, n0, k0), az);
+            as = M::mma(fs, fb, as);
+            az = M::mma(frag_ld_or_zero<T>(g.momentum ? Zin_g : nullptr, 1, D, m0, k0), fb, az);
           }
         }
 #pragma unroll
         for (int k0 = 0; k0 < SPM; k0 += M::KS)
-          aq = M::mma(frag_ld_row<T>(&sm.g.Qp[0][0], SPM + 8, m0, k0), frag_ld_tr<T>(&sm.phi[0][0], D + 8, n0, k0), aq);
-        const int k = n0 + (lane & 15);
-        f32x4 dpsi;
-        float fsp[4], fzp[4];
+          aq = M::mma(frag_ld_tr<T>(&sm.phi[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.g.Qp[0][0], SPM + 8, n0, k0), aq);
+        const int t = n0 + (lane & 15), kq = m0 + 4 * (lane >> 4);
+        const float ac = sm.sc.acoef[t], kc = sm.sc.kcoef[t];
+        float ps[4], dpsi[4], fsp = 0.f, fzp = 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int t = m0 + 4 * (lane >> 4) + r;
-          dpsi[r] = sm.sc.acoef[t] * as[r] - sm.sc.kcoef[t] * az[r] - aq[r];
-          const float ps = to_f32(sm.psi[t][k]);
-          fsp[r] = as[r] * ps;
-          fzp[r] = az[r] * ps;
+          ps[r] = to_f32(sm.psi[t][kq + r]);
+          dpsi[r] = ac * as[r] - kc * az[r] - aq[r];
+          fsp += as[r] * ps[r];
+          fzp += az[r] * ps[r];
         }
         if (bufchunk) {
           for (int s = 0; s < H; ++s) {
@@ -591,29 +602,30 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
             f32x4 ab = zero4();
 #pragma unroll
             for (int k0 = 0; k0 < D; k0 += M::KS)
-              ab = M::mma(frag_ld_row<T>(&sm.dy[0][0], D + 8, m0, k0), frag_ld<T>(Bs, 1, D, n0, k0), ab);
+              ab = M::mma(frag_ld<T>(Bs, 1, D, m0, k0), frag_ld_row<T>(&sm.dy[0][0], D + 8, n0, k0), ab);
+            const float w = to_f32(sm.wsh[t][s]);
+            float lm = 0.f;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const int t = m0 + 4 * (lane >> 4) + r;
-              dpsi[r] -= to_f32(sm.wsh[t][s]) * ab[r];
-              float lm = ab[r] * to_f32(sm.psi[t][k]);
-              for (int off = 8; off > 0; off >>= 1) lm += __shfl_xor(lm, off);
-              if (valid && (lane & 15) == 0) atomicAdd(&sm.Lm[t][s], lm);
+              dpsi[r] -= w * ab[r];
+              lm += ab[r] * ps[r];
             }
+            lm += __shfl_xor(lm, 16);
+            lm += __shfl_xor(lm, 32);
+            if (valid && lane < 16) atomicAdd(&sm.Lm[t][s], lm);
           }
         }
+        fsp += __shfl_xor(fsp, 16); fsp += __shfl_xor(fsp, 32);
+        fzp += __shfl_xor(fzp, 16); fzp += __shfl_xor(fzp, 32);
         if (valid) {
+          if (lane < 16) { atomicAdd(&sm.fS[t], fsp); atomicAdd(&sm.fZ[t], fzp); }
+          if (t < L) {
+            const size_t row = (tb + t0 + t) * D + kq;
+            if (g.map_mode == MAP_ELEMENTWISE) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int t = m0 + 4 * (lane >> 4) + r;
-            float fsv = fsp[r], fzv = fzp[r];
-            for (int off = 8; off > 0; off >>= 1) { fsv += __shfl_xor(fsv, off); fzv += __shfl_xor(fzv, off); }
-            if ((lane & 15) == 0) { atomicAdd(&sm.fS[t], fsv); atomicAdd(&sm.fZ[t], fzv); }
-            if (t < L) {
-              float outv = dpsi[r];
-              if (g.map_mode == MAP_ELEMENTWISE) outv *= poly_map_grad(to_f32(a.q[(tb + t0 + t) * D + k]), g.map_deg);
-              a.dq[(tb + t0 + t) * D + k] = from_f32<T>(outv);
+              for (int r = 0; r < 4; ++r) dpsi[r] *= poly_map_grad(to_f32(a.q[row + r]), g.map_deg);
             }
+            store4<T>(a.dq + row, dpsi[0], dpsi[1], dpsi[2], dpsi[3]);
           }
         }
       }
@@ -652,7 +664,8 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
     }
     __syncthreads();
 
-    // ---- phase D: G5  dphi[s, k] = Wz_end dZ_end^T delta_s - Ws_end dS_end^T delta_s - sum_q Q'[q, s] psi_q + S_ref^T dDelta_s
+    // ---- phase D: G5  dphi[s, k] = Wz_end dZ_end^T delta_s - Ws_end dS_end^T delta_s - sum_q Q'[q, s] psi_q + S_ref^T dDelta_s,
+    // as transposed tiles: a lane holds features k0..k0+3 of one source s
     {
       const int tail0 = t1 - H;
       constexpr int NT5 = NTS * NTD, PER5 = (NT5 + kSegWaves - 1) / kSegWaves;
@@ -660,37 +673,44 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
       for (int j = 0; j < PER5; ++j) {
         const int tile = min(wave + kSegWaves * j, NT5 - 1);
         const bool valid = NT5 % kSegWaves == 0 || wave + kSegWaves * j < NT5;
-        const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
+        const int m0 = (tile % NTD) * 16, n0 = (tile / NTD) * 16;   // m: features k, n: sources s
         f32x4 a1 = zero4(), a2 = zero4(), a3 = zero4(), a4 = zero4();
 #pragma unroll
         for (int k0 = 0; k0 < D; k0 += M::KS) {
-          const typename M::frag fa = frag_ld_row<T>(&sm.deltaT[0][0], D + 8, m0, k0);
-          a1 = M::mma(fa, frag_ld_row<T>(&sm.dZeT[0][0], D + 8, n0, k0), a1);
-          a2 = M::mma(fa, frag_ld_row<T>(&sm.dSeT[0][0], D + 8, n0, k0), a2);
-          a4 = M::mma(frag_ld_row<T>(&sm.g.dDT[0][0], D + 8, m0, k0), frag_ld_tr<T>(&sm.sref[0][0], D + 8, n0, k0), a4);
+          const typename M::frag fb = frag_ld_row<T>(&sm.deltaT[0][0], D + 8, n0, k0);
+          a1 = M::mma(frag_ld_row<T>(&sm.dZeT[0][0], D + 8, m0, k0), fb, a1);
+          a2 = M::mma(frag_ld_row<T>(&sm.dSeT[0][0], D + 8, m0, k0), fb, a2);
+          a4 = M::mma(frag_ld_tr<T>(&sm.sref[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.g.dDT[0][0], D + 8, n0, k0), a4);
         }
 #pragma unroll
         for (int k0 = 0; k0 < CH; k0 += M::KS)
-          a3 = M::mma(frag_ld_row<T>(&sm.g.QpT[0][0], CH + 8, m0, k0), frag_ld_tr<T>(&sm.psi[0][0], D + 8, n0, k0), a3);
-        if (valid) {
-          const int k = n0 + (lane & 15);
+          a3 = M::mma(frag_ld_tr<T>(&sm.psi[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.g.QpT[0][0], CH + 8, n0, k0), a3);
+        const int s = n0 + (lane & 15), kq = m0 + 4 * (lane >> 4);
+        const int pp = t0 - H + s;
+        if (valid && s < H + L && pp >= 0) {
+          const float wz = sm.sc.wzend[s], ws = sm.sc.wsend[s];
+          float val[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int s = m0 + 4 * (lane >> 4) + r;
-            const int pp = t0 - H + s;
-            if (s >= H + L || pp < 0) continue;
-            float val = sm.sc.wzend[s] * a1[r] - sm.sc.wsend[s] * a2[r] - a3[r] + a4[r];
-            if (s < H) {
-              if (first) { if (c > 0) p.halo_part[(((size_t)bh * sg.nseg + seg) * H + s) * (2 * D) + D + k] = val; }
-              else cur_carry[s * 2 * D + D + k] = val;
-              continue;
+          for (int r = 0; r < 4; ++r) val[r] = wz * a1[r] - ws * a2[r] - a3[r] + a4[r];
+          if (s < H) {
+            float* dst = first ? (c > 0 ? p.halo_part + (((size_t)bh * sg.nseg + seg) * H + s) * (2 * D) + D + kq : nullptr)
+                               : cur_carry + s * 2 * D + D + kq;
+            if (dst) store4<float>(dst, val[0], val[1], val[2], val[3]);
+          } else {
+            if (pp >= tail0) {
+              const float4 cv = *reinterpret_cast<const float4*>(prev_carry + (pp - tail0) * 2 * D + D + kq);
+              val[0] += cv.x; val[1] += cv.y; val[2] += cv.z; val[3] += cv.w;
             }
-            if (pp >= tail0) val += prev_carry[(pp - tail0) * 2 * D + D + k];
             if (pp >= seg_tail0) {
-              p.tail_part[(((size_t)bh * sg.nseg + seg) * H + (pp - seg_tail0)) * (2 * D) + D + k] = val;
+              store4<float>(p.tail_part + (((size_t)bh * sg.nseg + seg) * H + (pp - seg_tail0)) * (2 * D) + D + kq,
+                            val[0], val[1], val[2], val[3]);
             } else {
-              if (g.map_mode == MAP_ELEMENTWISE) val *= poly_map_grad(to_f32(a.k[(tb + pp) * D + k]), g.map_deg);
-              a.dk[(tb + pp) * D + k] = from_f32<T>(val);
+              const size_t row = (tb + pp) * D + kq;
+              if (g.map_mode == MAP_ELEMENTWISE) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) val[r] *= poly_map_grad(to_f32(a.k[row + r]), g.map_deg);
+              }
+              store4<T>(a.dk + row, val[0], val[1], val[2], val[3]);
             }
           }
         }
@@ -893,7 +913,7 @@ __global__ __launch_bounds__(kThreads) void k_seg_reduce_dsref(int nseg, int n, 
 
 template <typename T, int CH, int D>
 size_t bwd_seg_smem_bytes(int H) {
-  return sizeof(BwdSegSmem<T, CH, D>) + (size_t)2 * H * 2 * D * sizeof(float);
+  return carry_offset<BwdSegSmem<T, CH, D>>() + (size_t)2 * H * 2 * D * sizeof(float);
 }
 
 template <typename T, int CH, int D>

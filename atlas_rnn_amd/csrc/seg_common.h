@@ -100,6 +100,21 @@ __device__ __forceinline__ void store4(T* p, float a, float b, float c, float d)
   }
 }
 
+// Eight fp32 values to / from 16-byte aligned memory (two 16-byte accesses).
+__device__ __forceinline__ void store8f(float* p, const float* v) {
+  reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+  reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+__device__ __forceinline__ void add8f(float* v, const float* p) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+  v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
+  v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
+}
+
+// Byte offset of dynamic data placed after a shared-memory struct, rounded up to 16 bytes.
+template <typename Sm>
+constexpr size_t carry_offset() { return (sizeof(Sm) + 15) & ~(size_t)15; }
+
 template <typename T>
 __device__ __forceinline__ Vec8<T> vec8_load(const T* p) {
   Vec8<T> r;
