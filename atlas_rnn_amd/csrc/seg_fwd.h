@@ -279,11 +279,10 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
 
     // ---- P1: G1 + G2 (all waves)
     // G1: delta[s][i] = (S_ref phi_s)[i] - v_s[i];  G2 (full walk): Kmat[tau][s] = psi_tau . phi_s,
-    // kept in registers (kacc) until the Q epilogue.
+    // weighted into Q[tau][s] = Ws[s, tau-1] Kmat[tau][s] by the producing lane.
     constexpr int NGW = kSegWaves;
     constexpr int NT1 = NTS * NTD, PER1 = (NT1 + NGW - 1) / NGW;
     constexpr int NT2 = FULL ? (CH / 16) * NTS : 0, PER2 = (NT2 + NGW - 1) / NGW;
-    f32x4 kacc[PER2 > 0 ? PER2 : 1];
     static_assert(!FULL || NT2 > 0, "G2 tiles");
     {
       // tile indices past the end are clamped (MFMAs stay unconditional, only the stores are guarded)
@@ -308,37 +307,26 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
         }
       }
       if constexpr (FULL) {
+        // G2 as transposed tiles (a lane holds sources s0..s0+3 of one target tau), weighted by
+        // Ws[s, tau-1] into Q right away
 #pragma unroll
         for (int j = 0; j < PER2; ++j) {
           const int tt = min(wave + NGW * j, NT2 - 1);
-          const int m0 = (tt / NTS) * 16, n0 = (tt % NTS) * 16;
+          const bool valid = NT2 % NGW == 0 || wave + NGW * j < NT2;
+          const int m0 = (tt % NTS) * 16, n0 = (tt / NTS) * 16;   // m: sources s, n: targets tau
           f32x4 acc = zero4();
 #pragma unroll
           for (int k0 = 0; k0 < D; k0 += M::KS)
-            acc = M::mma(frag_ld_row<T>(&sm.psi[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.phi[0][0], D + 8, n0, k0), acc);
-          kacc[j] = acc;
+            acc = M::mma(frag_ld_row<T>(&sm.phi[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.psi[0][0], D + 8, n0, k0), acc);
+          if (valid) {
+            const int t = n0 + (lane & 15), s0 = m0 + 4 * (lane >> 4);
+            store4<T>(&sm.Q[t][s0], acc[0] * to_f32(sm.wsh[t][s0]), acc[1] * to_f32(sm.wsh[t][s0 + 1]),
+                      acc[2] * to_f32(sm.wsh[t][s0 + 2]), acc[3] * to_f32(sm.wsh[t][s0 + 3]));
+          }
         }
       }
     }
     __syncthreads();
-
-    // ---- P2 (full walk): Q epilogue
-    if constexpr (FULL) {
-#pragma unroll
-      for (int j = 0; j < PER2; ++j) {
-        const int tt = wave + NGW * j;
-        if (NT2 % NGW == 0 || tt < NT2) {
-          const int m0 = (tt / NTS) * 16, n0 = (tt % NTS) * 16;
-          const int s = n0 + (lane & 15);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int t = m0 + 4 * (lane >> 4) + r;
-            sm.Q[t][s] = from_f32<T>(kacc[j][r] * to_f32(sm.wsh[t][s]));
-          }
-        }
-      }
-      __syncthreads();
-    }
 
     // ---- P3: G3 (y, full walk), then G4 + state update on the owned state tiles (all waves)
     if constexpr (FULL) {
@@ -349,43 +337,36 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
         const int tile = min(wave + kSegWaves * j, NT3 - 1);
         const bool valid = NT3 % kSegWaves == 0 || wave + kSegWaves * j < NT3;
         {
-          const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;   // m: tau, n: rows i
+          const int m0 = (tile % NTD) * 16, n0 = (tile / NTD) * 16;   // m: rows i, n: targets tau
           f32x4 aq = zero4(), as = zero4(), az = zero4();
 #pragma unroll
           for (int k0 = 0; k0 < SPM; k0 += M::KS)
-            aq = M::mma(frag_ld_row<T>(&sm.Q[0][0], SPM + 8, m0, k0), frag_ld_tr<T>(&sm.vd[0][0], D + 8, n0, k0), aq);
+            aq = M::mma(frag_ld_tr<T>(&sm.vd[0][0], D + 8, m0, k0), frag_ld_row<T>(&sm.Q[0][0], SPM + 8, n0, k0), aq);
 #pragma unroll
           for (int k0 = 0; k0 < D; k0 += M::KS) {
-            const typename M::frag fa = frag_ld_row<T>(&sm.psi[0][0], D + 8, m0, k0);
-            as = M::mma(fa, frag_ld_row<T>(&sm.Sb[0][0], D + 8, n0, k0), as);
-            az = M::mma(fa, frag_ld_row<T>(&sm.Zb[0][0], D + 8, n0, k0), az);
+            const typename M::frag fb = frag_ld_row<T>(&sm.psi[0][0], D + 8, n0, k0);
+            as = M::mma(frag_ld_row<T>(&sm.Sb[0][0], D + 8, m0, k0), fb, as);
+            az = M::mma(frag_ld_row<T>(&sm.Zb[0][0], D + 8, m0, k0), fb, az);
           }
-          f32x4 yv;
+          // a lane holds rows i0..i0+3 of y for one target t
+          const int t = n0 + (lane & 15), i0 = m0 + 4 * (lane >> 4);
+          const float ac = sm.sc.acoef[t], kc = sm.sc.kcoef[t];
+          float yv[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int t = m0 + 4 * (lane >> 4) + r;
-            yv[r] = -aq[r] + sm.sc.acoef[t] * as[r] - sm.sc.kcoef[t] * az[r];
-          }
+          for (int r = 0; r < 4; ++r) yv[r] = -aq[r] + ac * as[r] - kc * az[r];
           if (bufchunk) {
             for (int s = 0; s < H; ++s) {
               const float* Bs = a.buf_in + ((size_t)bh * H + s) * D * D;
               f32x4 ab = zero4();
 #pragma unroll
               for (int k0 = 0; k0 < D; k0 += M::KS)
-                ab = M::mma(frag_ld_row<T>(&sm.psi[0][0], D + 8, m0, k0), frag_ld<T>(Bs, D, 1, n0, k0), ab);
+                ab = M::mma(frag_ld<T>(Bs, D, 1, m0, k0), frag_ld_row<T>(&sm.psi[0][0], D + 8, n0, k0), ab);
+              const float w = to_f32(sm.wsh[t][s]);
 #pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                const int t = m0 + 4 * (lane >> 4) + r;
-                yv[r] -= to_f32(sm.wsh[t][s]) * ab[r];
-              }
+              for (int r = 0; r < 4; ++r) yv[r] -= w * ab[r];
             }
           }
-          const int i = n0 + (lane & 15);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int t = m0 + 4 * (lane >> 4) + r;
-            if (valid && t < L) a.y[(tb + t0 + t) * D + i] = from_f32<T>(yv[r]);
-          }
+          if (valid && t < L) store4<T>(a.y + (tb + t0 + t) * D + i0, yv[0], yv[1], yv[2], yv[3]);
         }
       }
     }
