@@ -49,8 +49,10 @@ def algorithmic_bytes(bh=BH, t=T, d=D, e=E, s_in=2, s_st=4):
         "k_buffer_out": bh * (e - 1) * (2 * d * s_in + d * d * s_st),
         # adjoint aggregates: read q, dy, alpha/eta/beta
         "k_bwd_seg_agg": n * 2 * d * s_in + n * 3 * s_in,
-        # backward walk: read k, q, v, dy, scalars, S_ref, dS_T, dZ_T; write dk, dq, dv, scalar grads, dS0, dZ0
-        "k_bwd_seg": n * 4 * d * s_in + 2 * n * n_sc * s_in + n * 3 * d * s_in + 5 * st,
+        # backward walk: read k, q, v, dy, S_ref, dS_T, dZ_T; write dk, dq, dv, dS0, dZ0
+        "k_bwd_seg": n * 4 * d * s_in + n * 3 * d * s_in + 5 * st,
+        # scalar gradients: read the per-token scalars, write their gradients
+        "k_bwd_scalar": 2 * n * n_sc * s_in,
         "k_bwd_seg_fixup": 0,
         "k_seg_reduce_dsref": st,
         # segment scans and chunk-coefficient passes: intermediate data only; the coefficient
