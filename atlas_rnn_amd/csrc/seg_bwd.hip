@@ -508,48 +508,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         }
       }
     }
-    __syncthreads();
-
-    // ---- phase C: dv from dDelta; G6 dS_ref; G7 dpsi (+ fS, fZ); d buffer_in
-    {   // dv: 8 features of one source per lane
-      const int tail0 = t1 - H;
-      constexpr int NV = D / 8;
-      for (int idx = tid; idx < (H + L) * NV; idx += kSegThreads) {
-        const int s = idx / NV, i0 = (idx % NV) * 8;
-        const int pp = t0 - H + s;
-        if (pp < 0) continue;
-        const Vec8<T> x = vec8_load(&sm.g.dDT[s][i0]);
-        float val[8];
-#pragma unroll
-        for (int e8 = 0; e8 < 8; ++e8) val[e8] = -to_f32(x.v[e8]);
-        if (s < H) {
-          float* dst = first ? (c > 0 ? p.halo_part + (((size_t)bh * sg.nseg + seg) * H + s) * (2 * D) + i0 : nullptr)
-                             : cur_carry + s * 2 * D + i0;
-          if (dst) store8f(dst, val);
-          continue;
-        }
-        if (pp >= tail0) add8f(val, prev_carry + (pp - tail0) * 2 * D + i0);
-        if (pp >= seg_tail0) {
-          store8f(p.tail_part + (((size_t)bh * sg.nseg + seg) * H + (pp - seg_tail0)) * (2 * D) + i0, val);
-        } else {
-          Vec8<T> y;
-#pragma unroll
-          for (int e8 = 0; e8 < 8; ++e8) y.v[e8] = from_f32<T>(val[e8]);
-          y.store(a.dv + (tb + pp) * D + i0);
-        }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NT2; ++j) {   // G6: dS_ref[i, k] += sum_s dDelta[i, s] phi_s[k]
-      const int tile = min(wave + kSegWaves * j, NTD * NTD - 1);
-      const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
-      f32x4 acc = zero4();
-#pragma unroll
-      for (int k0 = 0; k0 < SPM; k0 += M::KS)
-        acc = M::mma(frag_ld_tr<T>(&sm.g.dDT[0][0], D + 8, m0, k0), frag_ld_tr<T>(&sm.phi[0][0], D + 8, n0, k0), acc);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dsr[j][r] += acc[r];
-    }
+    // G7 (independent of G4) in the same phase
     {   // G7: dpsi[q, k] = a_{q-1} (dy_q S_in)[k] - kappa_{q-1} (dy_q Z_in)[k] - sum_s Q'[q, s] phi_s[k],
         // computed as transposed tiles: a lane holds features k0..k0+3 of one target q
       constexpr int NT7 = NTC * NTD, PER7 = (NT7 + kSegWaves - 1) / kSegWaves;
@@ -630,6 +589,48 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         }
       }
     }
+    __syncthreads();
+
+    // ---- phase C: dv from dDelta; G6 dS_ref; d buffer_in; then G5 and the carried adjoint (no barrier between)
+    {   // dv: 8 features of one source per lane
+      const int tail0 = t1 - H;
+      constexpr int NV = D / 8;
+      for (int idx = tid; idx < (H + L) * NV; idx += kSegThreads) {
+        const int s = idx / NV, i0 = (idx % NV) * 8;
+        const int pp = t0 - H + s;
+        if (pp < 0) continue;
+        const Vec8<T> x = vec8_load(&sm.g.dDT[s][i0]);
+        float val[8];
+#pragma unroll
+        for (int e8 = 0; e8 < 8; ++e8) val[e8] = -to_f32(x.v[e8]);
+        if (s < H) {
+          float* dst = first ? (c > 0 ? p.halo_part + (((size_t)bh * sg.nseg + seg) * H + s) * (2 * D) + i0 : nullptr)
+                             : cur_carry + s * 2 * D + i0;
+          if (dst) store8f(dst, val);
+          continue;
+        }
+        if (pp >= tail0) add8f(val, prev_carry + (pp - tail0) * 2 * D + i0);
+        if (pp >= seg_tail0) {
+          store8f(p.tail_part + (((size_t)bh * sg.nseg + seg) * H + (pp - seg_tail0)) * (2 * D) + i0, val);
+        } else {
+          Vec8<T> y;
+#pragma unroll
+          for (int e8 = 0; e8 < 8; ++e8) y.v[e8] = from_f32<T>(val[e8]);
+          y.store(a.dv + (tb + pp) * D + i0);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NT2; ++j) {   // G6: dS_ref[i, k] += sum_s dDelta[i, s] phi_s[k]
+      const int tile = min(wave + kSegWaves * j, NTD * NTD - 1);
+      const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int k0 = 0; k0 < SPM; k0 += M::KS)
+        acc = M::mma(frag_ld_tr<T>(&sm.g.dDT[0][0], D + 8, m0, k0), frag_ld_tr<T>(&sm.phi[0][0], D + 8, n0, k0), acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dsr[j][r] += acc[r];
+    }
     if (bufchunk) {   // d buffer_in[s] = Wz_end[s] dZ_end - Ws_end[s] dS_end - sum_q Ws[s, q-1] dy_q psi_q^T
       for (int s = 0; s < H; ++s) {
         float* dst = a.dbuf_in + ((size_t)bh * H + s) * D * D;
@@ -662,8 +663,6 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
         }
       }
     }
-    __syncthreads();
-
     // ---- phase D: G5  dphi[s, k] = Wz_end dZ_end^T delta_s - Ws_end dS_end^T delta_s - sum_q Q'[q, s] psi_q + S_ref^T dDelta_s,
     // as transposed tiles: a lane holds features k0..k0+3 of one source s
     {
