@@ -167,6 +167,19 @@ __device__ __forceinline__ typename MM<T>::frag frag_scale(typename MM<T>::frag 
   }
 }
 
+// Sum over the 16 lanes of each row (lanes 16r .. 16r+15), returned in every lane of the row:
+// four DPP row rotations (row_ror 8, 4, 2, 1) on the VALU, no LDS traffic.
+__device__ __forceinline__ float row_sum16(float x) {
+#define ATLAS_ROR_ADD(n) \
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x120 + (n), 0xf, 0xf, false))
+  ATLAS_ROR_ADD(8);
+  ATLAS_ROR_ADD(4);
+  ATLAS_ROR_ADD(2);
+  ATLAS_ROR_ADD(1);
+#undef ATLAS_ROR_ADD
+  return x;
+}
+
 // Clamp of the reference (torch.clamp(-100, 100)) and its gradient mask (min <= x <= max).
 __device__ __forceinline__ float clamp100(float x) { return fminf(fmaxf(x, -100.f), 100.f); }
 __device__ __forceinline__ float clamp_mask(float x) { return (x >= -100.f && x <= 100.f) ? 1.f : 0.f; }

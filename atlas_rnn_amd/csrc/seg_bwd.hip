@@ -177,7 +177,7 @@ struct BwdSegSmem {
   ChunkScalars<CH> sc;
   float hS[SPM], hZ[SPM], fS[CH], fZ[CH];
   float gram[4];
-  float red[kSegWaves][4];
+  float red[kSegWaves][4][4];   // per wave and lane row: partial Grams
   // followed by the halo carry: float carry[2][H][2 * D] (dynamic size)
 };
 
@@ -380,17 +380,20 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
           store4<T>(&sm.ZinT[k][i0], zv[0], zv[1], zv[2], zv[3]);
         }
       }
-      for (int off = 32; off > 0; off >>= 1) {
-        gss += __shfl_xor(gss, off); gsz += __shfl_xor(gsz, off); gzz += __shfl_xor(gzz, off);
+      gss = row_sum16(gss); gsz = row_sum16(gsz); gzz = row_sum16(gzz);
+      if ((lane & 15) == 0) {
+        float* rd = sm.red[wave][lane >> 4];
+        rd[0] = gss; rd[1] = gsz; rd[2] = gzz;
       }
-      if (lane == 0) { sm.red[wave][0] = gss; sm.red[wave][1] = gsz; sm.red[wave][2] = gzz; }
       if (c - 1 >= c_begin) pf.load(g, a, p, bh, c - 1, rw + (size_t)(c - 1) * 2 * D * D, tid, lane, wave);
     }
     __syncthreads();
     if (tid < 3) {
       float sum = 0.f;
 #pragma unroll
-      for (int w = 0; w < kSegWaves; ++w) sum += sm.red[w][tid];
+      for (int w = 0; w < kSegWaves; ++w)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sum += sm.red[w][r][tid];
       sm.gram[tid] = sum;
     }
     if (bufchunk) {   // <dS_end, B_s>, <dZ_end, B_s> for the dense buffer sources
