@@ -18,6 +18,19 @@ hipError_t launch_fwd_seg(const Geom&, const FwdPtrs<T>&, const SegGeom&, float*
 template <typename T, int CH, int D>
 hipError_t launch_bwd_seg(const Geom&, const BwdPtrs<T>&, const SegGeom&, const BwdSegPtrs&, hipStream_t);
 template <typename T, int DK, int DV> hipError_t launch_buffer_out(const Geom&, const FwdPtrs<T>&, hipStream_t);
+bool walk_fwd_supported(const Geom& g);
+hipError_t launch_walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
+                           float* rw, float* final_raw, float* coef, bf16* wsh, hipStream_t stream);
+
+// ATLAS_MEM_GENERIC=1 routes every call through the general segment kernels (seg_fwd.hip /
+// seg_bwd.hip) instead of the specialised bf16, d = 64 walks; used by the tests to check both.
+static bool force_generic() {
+  static const bool v = [] {
+    const char* e = std::getenv("ATLAS_MEM_GENERIC");
+    return e && e[0] == '1';
+  }();
+  return v;
+}
 
 // Diagnostic tile product C = A B^T (16 x 64 inputs) through the same fragment helpers.
 template <typename T>
@@ -270,7 +283,12 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
   const Geom& g = pl.g;
   hipError_t err = hipErrorInvalidValue;
   if (g.DK == 64) {
-    if constexpr (sizeof(T) == 2) err = launch_fwd_seg<T, 64, 64>(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
+    if constexpr (sizeof(T) == 2) {
+      if (!force_generic() && walk_fwd_supported(g))
+        err = launch_walk_fwd(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
+      else
+        err = launch_fwd_seg<T, 64, 64>(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
+    }
     else err = launch_fwd_seg<T, 32, 64>(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
     if (err == hipSuccess) err = launch_buffer_out<T, 64, 64>(g, a, s);
   } else if (g.DK == 32) {

@@ -77,6 +77,20 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg_scan(const Geom g, const f
   }
 }
 
+template <int D>
+hipError_t launch_fwd_seg_scan(const Geom& g, const float* S0, const float* Z0, const SegGeom& sg, const float* agg,
+                               float* seg_states, hipStream_t stream) {
+  prof_begin(KID_FWD_SCAN, stream);
+  hipLaunchKernelGGL((k_fwd_seg_scan<D>), dim3((D * D + kThreads - 1) / kThreads, g.BH), dim3(kThreads), 0, stream,
+                     g, S0, Z0, sg, agg, seg_states);
+  prof_end(KID_FWD_SCAN, stream);
+  return hipGetLastError();
+}
+template hipError_t launch_fwd_seg_scan<64>(const Geom&, const float*, const float*, const SegGeom&, const float*,
+                                            float*, hipStream_t);
+template hipError_t launch_fwd_seg_scan<32>(const Geom&, const float*, const float*, const SegGeom&, const float*,
+                                            float*, hipStream_t);
+
 template <typename T, int CH, int D>
 __global__ __launch_bounds__(kSegThreads) void k_fwd_seg(const Geom g, const FwdPtrs<T> a, const SegGeom sg,
                                                            const float* seg_states, float* rw, float* final_raw,
@@ -101,11 +115,7 @@ hipError_t launch_fwd_seg(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg,
     prof_end(KID_FWD_SEG_AGG, stream);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
-  prof_begin(KID_FWD_SCAN, stream);
-  hipLaunchKernelGGL((k_fwd_seg_scan<D>), dim3((D * D + kThreads - 1) / kThreads, g.BH), dim3(kThreads), 0, stream,
-                     g, a.S0, a.Z0, sg, (const float*)agg, seg_states);
-  prof_end(KID_FWD_SCAN, stream);
-  if ((err = hipGetLastError()) != hipSuccess) return err;
+  if ((err = launch_fwd_seg_scan<D>(g, a.S0, a.Z0, sg, agg, seg_states, stream)) != hipSuccess) return err;
   const size_t smem = sizeof(SegFwdSmem<T, CH, D, true>);
   err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_seg<T, CH, D>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);

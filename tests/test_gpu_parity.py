@@ -49,6 +49,20 @@ CASES = [
     Case("fp32_d16_padded", BH=3, T=45, d=16, e=3, gate='token', momentum=True, buffer=True, states=0.2, seed=16),
     Case("bf16_d48_padded", BH=2, T=70, d=48, e=2, gate='lag', momentum=True, buffer=True, states=0.1,
          map_degree=2, dtype=BF16, seed=17),
+    # the specialised bf16, d = 64 walks (no carried buffer, no scan_chunk_len clamp): window at the
+    # halo limit (e = 17) and just past it (e = 18, general kernels), chunk-edge lengths, many segments
+    Case("bf16_walk_e16_token", BH=3, T=1000, d=64, e=16, gate='token', momentum=True, states=0.1, dtype=BF16,
+         seed=18),
+    Case("bf16_walk_e17_lag_nomom", BH=2, T=129, d=64, e=17, gate='lag', momentum=False, states=0.1, dtype=BF16,
+         seed=19),
+    Case("bf16_walk_e18_lag", BH=2, T=129, d=64, e=18, gate='lag', momentum=True, states=0.1, dtype=BF16, seed=20),
+    Case("bf16_walk_T1", BH=2, T=1, d=64, e=4, gate='lag', momentum=True, states=0.1, dtype=BF16, seed=21),
+    Case("bf16_walk_T64", BH=2, T=64, d=64, e=3, gate='token', momentum=True, states=0.1, dtype=BF16, seed=22),
+    Case("bf16_walk_T65", BH=2, T=65, d=64, e=3, gate=None, momentum=True, states=0.1, dtype=BF16, seed=23),
+    Case("bf16_walk_T97_titans", BH=3, T=97, d=64, e=1, gate=None, momentum=False, states=0.1, dtype=BF16, seed=24),
+    Case("bf16_walk_multiseg", BH=40, T=700, d=64, e=4, gate='lag', momentum=True, states=0.1, dtype=BF16, seed=25),
+    Case("bf16_walk_map3", BH=2, T=200, d=64, e=4, gate='lag', momentum=True, states=0.1, map_degree=3,
+         dtype=BF16, seed=26),
 ]
 
 
