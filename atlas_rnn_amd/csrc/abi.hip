@@ -16,7 +16,7 @@ template <typename T, int CH, int D>
 hipError_t launch_fwd_seg(const Geom&, const FwdPtrs<T>&, const SegGeom&, float*, float*, float*, float*, float*,
                           T*, hipStream_t);
 template <typename T, int CH, int D>
-hipError_t launch_bwd_seg(const Geom&, const BwdPtrs<T>&, const SegGeom&, const BwdSegPtrs&, hipStream_t);
+hipError_t launch_bwd_seg(const Geom&, const BwdPtrs<T>&, const SegGeom&, const BwdSegPtrs&, hipStream_t, bool);
 template <typename T, int DK, int DV> hipError_t launch_buffer_out(const Geom&, const FwdPtrs<T>&, hipStream_t);
 bool walk_fwd_supported(const Geom& g);
 hipError_t launch_walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
@@ -328,12 +328,14 @@ int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, voi
   p.scal = reinterpret_cast<float*>(w + L.scal);
   p.wsh = w + L.wsh;
   hipError_t err = hipErrorInvalidValue;
+  // the specialised walks run as a pair: the forward saved its states in their layout
+  const bool walk = sizeof(T) == 2 && !force_generic() && walk_fwd_supported(pl.g);
   if (gb.DK == 64) {
-    if constexpr (sizeof(T) == 2) err = launch_bwd_seg<T, 32, 64>(gb, a, pl.sgb, p, s);
-    else err = launch_bwd_seg<T, 16, 64>(gb, a, pl.sgb, p, s);
+    if constexpr (sizeof(T) == 2) err = launch_bwd_seg<T, 32, 64>(gb, a, pl.sgb, p, s, walk);
+    else err = launch_bwd_seg<T, 16, 64>(gb, a, pl.sgb, p, s, false);
   } else if (gb.DK == 32) {
-    if constexpr (sizeof(T) == 2) err = launch_bwd_seg<T, 32, 32>(gb, a, pl.sgb, p, s);
-    else err = launch_bwd_seg<T, 16, 32>(gb, a, pl.sgb, p, s);
+    if constexpr (sizeof(T) == 2) err = launch_bwd_seg<T, 32, 32>(gb, a, pl.sgb, p, s, false);
+    else err = launch_bwd_seg<T, 16, 32>(gb, a, pl.sgb, p, s, false);
   }
   return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
 }

@@ -918,9 +918,13 @@ size_t bwd_seg_smem_bytes(int H) {
   return carry_offset<BwdSegSmem<T, CH, D>>() + (size_t)2 * H * 2 * D * sizeof(float);
 }
 
+hipError_t launch_walk_bwd_kernel(const Geom& g, const BwdPtrs<bf16>& a, const SegGeom& sg, const BwdSegPtrs& p,
+                                  hipStream_t stream);
+
+// walk: run the specialised reverse walk (walk_bwd.hip, bf16 with d = 64 only) in place of k_bwd_seg
 template <typename T, int CH, int D>
 hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg, const BwdSegPtrs& p,
-                          hipStream_t stream) {
+                          hipStream_t stream, bool walk) {
   hipError_t err = launch_chunk_coef<T, CH>(g, a.decay, a.lr, a.beta, a.gate, p.coef, reinterpret_cast<T*>(p.wsh),
                                             KID_BWD_COEF, stream);
   if (err != hipSuccess) return err;
@@ -939,7 +943,15 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
                      g, a.dS_T, a.dZ_T, sg, p);
   prof_end(KID_BWD_SCAN, stream);
   if ((err = hipGetLastError()) != hipSuccess) return err;
-  {
+  if constexpr (sizeof(T) == 2 && CH == 32 && D == 64) {
+    if (walk) {
+      prof_begin(KID_BWD_CHUNK, stream);
+      err = launch_walk_bwd_kernel(g, a, sg, p, stream);
+      prof_end(KID_BWD_CHUNK, stream);
+      if (err != hipSuccess) return err;
+    }
+  }
+  if (!walk) {
     const size_t smem = bwd_seg_smem_bytes<T, CH, D>(g.H);
     err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bwd_seg<T, CH, D>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
@@ -963,7 +975,7 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
 
 #define ATLAS_INST_BWD_SEG(T, CH, D)                                                                  \
   template hipError_t launch_bwd_seg<T, CH, D>(const Geom&, const BwdPtrs<T>&, const SegGeom&,        \
-                                               const BwdSegPtrs&, hipStream_t);                       \
+                                               const BwdSegPtrs&, hipStream_t, bool);                 \
   template size_t bwd_seg_smem_bytes<T, CH, D>(int);
 
 ATLAS_INST_BWD_SEG(bf16, 32, 64)

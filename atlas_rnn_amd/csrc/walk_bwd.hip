@@ -1,0 +1,549 @@
+// walk_bwd.hip - specialised reverse walk of the backward pass for bf16 inputs with d_k = d_v = 64.
+//
+// Replaces k_bwd_seg (seg_bwd.hip) for the configurations the specialised forward walks cover; the
+// adjoint aggregates, the segment scan, the scalar gradients (k_bwd_scalar), the fixup and the
+// dS_ref reduction are shared with the general path and see the same per-chunk records.
+// Chunks of 32 tokens, sources s = 0 .. 47 (the e - 1 <= 16 halo tokens, then the chunk),
+// processed last to first within a segment, with three workgroup barriers per chunk:
+//   phase A  bf16 copies of the chunk-end adjoint for the matrix cores; delta = S_ref phi - v
+//            (-> LDS), K = psi phi^T (kept) and Q = Ws o K (-> LDS), the state term S_in^T dy of
+//            dpsi (kept), the Grams <dS_end, S_in> ..., and the chunk-start adjoint (the
+//            transposed chunk transition, in the owners' fp32 registers)
+//   phase B  P = dy delta^T, Q' = Ws o P (-> LDS) and Lm = K o P (scalar-gradient record);
+//            dDelta = Wz_end dZ_end phi - Ws_end dS_end phi - Q^T dy (-> LDS, dv) with hS, hZ
+//   phase C  dpsi (dq), dphi (dk), dS_ref += dDelta^T phi, the scalar records, staging of the
+//            previous chunk's inputs (double buffered)
+// The chunk-start states come from the forward walk in the fragment layout of walk_common.h and
+// feed the matrix cores without going through LDS.
+#include "mem_common.h"
+#include "mem_params.h"
+#include "seg_common.h"
+#include "walk_common.h"
+
+namespace atlas {
+
+namespace wb {
+
+constexpr int D = 64;
+constexpr int CH = 32;          // backward chunk length
+constexpr int SP = 48;          // source rows with data: halo (<= 16) + chunk
+constexpr int NST = SP / 16;    // 3 source tiles
+constexpr int SPR = 64;         // LDS rows of source-indexed matrices (rows SP.. stay zero: k = 32 steps)
+constexpr int PD = D + 8;       // pitch of 64-wide bf16 rows
+constexpr int SPM = CH + kHaloPad;   // 64: pitch of the per-source arrays in HBM (records, Ws, Lm)
+constexpr int WP = SP + 8;      // 56: LDS pitch of the Ws rows [tau][s]
+constexpr int QP = CH + 8;      // 40: LDS pitch of Q^T / Q'^T rows [s][tau]
+constexpr int REC = CoefRec<CH>::SIZE;   // 328
+constexpr int R_ACOEF = 0, R_KCOEF = CH, R_ENDC = 2 * CH, R_WSEND = 2 * CH + 4, R_WZEND = R_WSEND + SPM;
+constexpr int REC4 = REC / 4;   // 82
+constexpr int HMAX = 16;
+typedef ScalarBlock<CH> SB;
+static_assert(SB::SPM == SPM, "scalar record pitch");
+static_assert(R_WSEND % 4 == 0 && R_WZEND % 4 == 0 && REC % 4 == 0, "record alignment");
+
+struct Stage {
+  alignas(16) bf16 phi[SPR][PD];
+  alignas(16) bf16 psi[CH][PD];
+  alignas(16) bf16 dy[CH][PD];
+  alignas(16) bf16 wsh[CH][WP];
+  alignas(16) float rec[REC];
+};
+
+struct Smem {
+  Stage st[2];
+  alignas(16) bf16 dl[SPR][PD];    // delta[s][i]
+  alignas(16) bf16 dD[SPR][PD];    // dDelta[s][i]
+  alignas(16) bf16 QT[SPR][QP];    // Q^T[s][tau]
+  alignas(16) bf16 QpT[SPR][QP];   // Q'^T[s][tau]
+  alignas(16) bf16 dSeT[D][PD];    // chunk-end adjoint, transposed: dSeT[k][i] = dS_end[i][k]
+  alignas(16) bf16 dZeT[D][PD];
+  alignas(16) float carry[2][HMAX][2 * D];   // halo partials (dv | dphi) handed to the previous chunk
+  float hS[SPM], hZ[SPM], fS[CH], fZ[CH];
+  float red[kSegWaves][4];
+};
+
+struct Prefetch {
+  u32x4v phi, x;        // phi row vector (tid < 384); psi (tid < 256) or dy (tid >= 256) row vector
+  u32x4v wsh, rec;
+  u32x2v v[2];          // v of this wave's delta tiles (8 bytes per lane)
+  u32x4v sin[2], zin[2];   // chunk-start S, Z fragments (kt, q = 0, 1)
+};
+
+}  // namespace wb
+
+template <bool MAPE>
+__global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const BwdPtrs<bf16> a, const SegGeom sg,
+                                                            const BwdSegPtrs p) {
+  using namespace wb;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  Smem& sm = *reinterpret_cast<Smem*>(smem_raw);
+  const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
+  const int gq = lane >> 4, m = lane & 15;
+  const int seg = blockIdx.x, bh = blockIdx.y;
+  const int H = g.H;
+  const int c_begin = seg * sg.G, c_end = min(g.nc, c_begin + sg.G);
+  const size_t DD = (size_t)D * D;
+  const size_t sbase = (size_t)bh * DD;
+  const int seg_tail0 = min(g.T, c_end * CH) - H;
+  // roles
+  const int qw = w & 1, kt = w >> 1;            // owned adjoint tiles: rows 32 qw + 16 u, columns 16 kt
+  const int it1 = w & 3;                        // delta / dDelta tiles: rows 16 it1, sources st1(u)
+  const int nt1 = w < 4 ? 2 : 1;
+  auto st1 = [&](int u) { return w < 4 ? 2 * u : 1; };
+  const bool has_mp = w < 6;                    // K / P tile (tt, stm)
+  const int tt = w & 1, stm = w >> 1;
+  const int nt5 = qw == 0 ? 2 : 1;              // dphi tiles: columns 16 kt, sources st5(u)
+  auto st5 = [&](int u) { return u == 0 ? qw : 2; };
+
+  const uint32_t row_bytes = (uint32_t)g.T * (D * 2);
+  const rsrc_t rk = make_rsrc(a.k + (size_t)bh * g.T * D, row_bytes);
+  const rsrc_t rv = make_rsrc(a.v + (size_t)bh * g.T * D, row_bytes);
+  const rsrc_t rq = make_rsrc(a.q + (size_t)bh * g.T * D, row_bytes);
+  const rsrc_t rdy = make_rsrc(a.dy ? a.dy + (size_t)bh * g.T * D : a.q, a.dy ? row_bytes : 0u);
+  const rsrc_t rrec = make_rsrc(p.coef + (size_t)bh * g.nc * REC, (uint32_t)g.nc * (REC * 4));
+  const rsrc_t rwsh = make_rsrc(reinterpret_cast<const bf16*>(p.wsh) + (size_t)bh * g.nc * CH * SPM,
+                                (uint32_t)g.nc * (CH * SPM * 2));
+  const rsrc_t rdq = make_rsrc(a.dq + (size_t)bh * g.T * D, row_bytes);
+  const rsrc_t rdk = make_rsrc(a.dk + (size_t)bh * g.T * D, row_bytes);
+  const rsrc_t rdv = make_rsrc(a.dv + (size_t)bh * g.T * D, row_bytes);
+  const unsigned char* states = reinterpret_cast<const unsigned char*>(p.rw) + (size_t)bh * g.ncb * kStateBlk;
+
+  // per-thread staging offsets (relative to token t0 / chunk c)
+  const int sv_s = tid >> 3, sv_c8 = tid & 7;
+  const uint32_t o_phi = (tid < SP * 8 && sv_s < H + CH) ? (uint32_t)((sv_s - H) * (D * 2) + sv_c8 * 16) : kOob;
+  const int l_phi = tid < SP * 8 ? sv_s * PD + sv_c8 * 8 : -1;
+  const int xr = (tid & 255) >> 3;
+  const uint32_t o_x = (uint32_t)(xr * (D * 2) + sv_c8 * 16);
+  const int l_x = xr * PD + sv_c8 * 8;
+  const uint32_t o_wsh = tid < CH * (SP / 8) ? (uint32_t)((tid / (SP / 8)) * (SPM * 2) + (tid % (SP / 8)) * 16) : kOob;
+  const int l_wsh = tid < CH * (SP / 8) ? (tid / (SP / 8)) * WP + (tid % (SP / 8)) * 8 : -1;
+  const uint32_t o_rec = tid < REC4 ? (uint32_t)(tid * 16) : kOob;
+  uint32_t o_v[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int s = 16 * st1(u) + m;
+    o_v[u] = (u < nt1 && s < H + CH) ? (uint32_t)((s - H) * (D * 2) + (16 * it1 + 4 * gq) * 2) : kOob;
+  }
+
+  auto pf_load = [&](Prefetch& pf, int c) {
+    const int t0 = c * CH;
+    const uint32_t tb = (uint32_t)t0 * (D * 2);
+    pf.phi = bld16(rk, o_phi + tb);
+    pf.x = bld16(tid < 256 ? rq : rdy, o_x + tb);
+    pf.wsh = bld16(rwsh, o_wsh + (uint32_t)c * (CH * SPM * 2));
+    pf.rec = bld16(rrec, o_rec + (uint32_t)c * (REC * 4));
+#pragma unroll
+    for (int u = 0; u < 2; ++u) pf.v[u] = bld8(rv, o_v[u] + tb);
+    const unsigned char* blk = states + (size_t)c * kStateBlk;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      pf.sin[q] = *reinterpret_cast<const u32x4v*>(blk + frag_off(kt, q, lane));
+      pf.zin[q] = *reinterpret_cast<const u32x4v*>(blk + kStateBytes + frag_off(kt, q, lane));
+    }
+  };
+  auto pf_store = [&](const Prefetch& pf, Stage& st) {
+    if (l_phi >= 0) {
+      u32x4v x = pf.phi;
+      if constexpr (MAPE) x = map_bf16x8(x, g.map_deg);
+      *reinterpret_cast<u32x4v*>(&st.phi[0][0] + l_phi) = x;
+    }
+    if (tid < 256) {
+      u32x4v x = pf.x;
+      if constexpr (MAPE) x = map_bf16x8(x, g.map_deg);
+      *reinterpret_cast<u32x4v*>(&st.psi[0][0] + l_x) = x;
+    } else {
+      *reinterpret_cast<u32x4v*>(&st.dy[0][0] + l_x) = pf.x;
+    }
+    if (l_wsh >= 0) *reinterpret_cast<u32x4v*>(&st.wsh[0][0] + l_wsh) = pf.wsh;
+    if (tid < REC4) *reinterpret_cast<u32x4v*>(&st.rec[tid * 4]) = pf.rec;
+  };
+
+  // ---- constants: S_ref rows 16 it1 (A operand of delta) and S_ref^T columns 16 kt (A of S_ref^T dDelta)
+  bf16x8 sref_f[2], srefT_f[2];
+  {
+    const float* sr = a.S_ref + sbase;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float* r0 = sr + (size_t)(16 * it1 + m) * D + 32 * q + 8 * gq;
+      const float4 x0 = *reinterpret_cast<const float4*>(r0);
+      const float4 x1 = *reinterpret_cast<const float4*>(r0 + 4);
+      bf16x8 f;
+      f[0] = static_cast<bf16>(x0.x); f[1] = static_cast<bf16>(x0.y); f[2] = static_cast<bf16>(x0.z);
+      f[3] = static_cast<bf16>(x0.w); f[4] = static_cast<bf16>(x1.x); f[5] = static_cast<bf16>(x1.y);
+      f[6] = static_cast<bf16>(x1.z); f[7] = static_cast<bf16>(x1.w);
+      sref_f[q] = f;
+      bf16x8 ft;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ft[e] = static_cast<bf16>(sr[(size_t)(32 * q + 8 * gq + e) * D + 16 * kt + m]);
+      srefT_f[q] = ft;
+    }
+  }
+
+  // ---- adjoint at the segment end (owned tiles u: rows 32 qw + 16 u + 4 gq + r, column 16 kt + m)
+  float dS[2][4], dZ[2][4], dsr[2][4];
+  {
+    const float* sa = p.seg_adj + ((size_t)bh * sg.nseg + seg) * 2 * DD;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const size_t off = (size_t)(32 * qw + 16 * u + 4 * gq + r) * D + 16 * kt + m;
+        dS[u][r] = sa[off];
+        dZ[u][r] = sa[DD + off];
+        dsr[u][r] = 0.f;
+      }
+  }
+
+  // ---- zero the padding rows, the carries and the accumulators
+  for (int idx = tid; idx < (SPR - SP) * PD; idx += kSegThreads) {
+    const int rr = SP + idx / PD, cc = idx % PD;
+    sm.st[0].phi[rr][cc] = bf16(0.f);
+    sm.st[1].phi[rr][cc] = bf16(0.f);
+    sm.dl[rr][cc] = bf16(0.f);
+    sm.dD[rr][cc] = bf16(0.f);
+  }
+  for (int idx = tid; idx < (SPR - SP) * QP; idx += kSegThreads) {
+    const int rr = SP + idx / QP, cc = idx % QP;
+    sm.QT[rr][cc] = bf16(0.f);
+    sm.QpT[rr][cc] = bf16(0.f);
+  }
+  for (int idx = tid; idx < 2 * HMAX * 2 * D; idx += kSegThreads) (&sm.carry[0][0][0])[idx] = 0.f;
+  if (tid < SPM) { sm.hS[tid] = 0.f; sm.hZ[tid] = 0.f; }
+  if (tid < CH) { sm.fS[tid] = 0.f; sm.fZ[tid] = 0.f; }
+
+  // One register prefetch: the chunk's register operands (v, the saved states) are consumed in
+  // phase A, after which the previous chunk's loads are issued into the same registers and staged
+  // at the end of phase C.
+  Prefetch pf;
+  pf_load(pf, c_end - 1);
+  pf_store(pf, sm.st[0]);
+  __syncthreads();
+
+  for (int c = c_end - 1; c >= c_begin; --c) {
+    // per-lane indices laundered once per chunk (see walk_common.h)
+    const int ln = launder(lane);
+    const int gq = ln >> 4, m = ln & 15;
+    const int b = (c_end - 1 - c) & 1;
+    const Stage& st = sm.st[b];
+    const float* rec = st.rec;
+    const int t0 = c * CH, t1 = min(g.T, t0 + CH), L = t1 - t0;
+    const int tail0 = t1 - H;
+    const bool first = c == c_begin;
+    float* cur_carry = &sm.carry[c & 1][0][0];
+    const float* prev_carry = &sm.carry[(c + 1) & 1][0][0];
+
+    // Routes the (dv | dphi) values of source s, features f0 .. f0+3 (half 0: dv, 1: dphi): halo
+    // sources to the previous chunk's carry (or the segment's halo record), the chunk's last e-1
+    // tokens plus the next chunk's carry, the segment's last e-1 tokens to the tail record.
+    auto route = [&](int s, int f0, int half, float* val, const rsrc_t& dst, const u32x2v& raw) {
+      const int pp = t0 - H + s;
+      if (s >= H + L || pp < 0) return;
+      if (s < H) {
+        float* o = first ? p.halo_part + (((size_t)bh * sg.nseg + seg) * H + s) * (2 * D) : cur_carry + s * (2 * D);
+        *reinterpret_cast<float4*>(o + half * D + f0) = make_float4(val[0], val[1], val[2], val[3]);
+        return;
+      }
+      if (pp >= tail0) {
+        const float4 cv = *reinterpret_cast<const float4*>(prev_carry + (pp - tail0) * (2 * D) + half * D + f0);
+        val[0] += cv.x; val[1] += cv.y; val[2] += cv.z; val[3] += cv.w;
+      }
+      if (pp >= seg_tail0) {
+        float* o = p.tail_part + (((size_t)bh * sg.nseg + seg) * H + (pp - seg_tail0)) * (2 * D) + half * D + f0;
+        *reinterpret_cast<float4*>(o) = make_float4(val[0], val[1], val[2], val[3]);
+        return;
+      }
+      if constexpr (MAPE) {
+        if (half == 1) {
+          val[0] *= poly_map_grad(__builtin_bit_cast(float, raw[0] << 16), g.map_deg);
+          val[1] *= poly_map_grad(__builtin_bit_cast(float, raw[0] & 0xffff0000u), g.map_deg);
+          val[2] *= poly_map_grad(__builtin_bit_cast(float, raw[1] << 16), g.map_deg);
+          val[3] *= poly_map_grad(__builtin_bit_cast(float, raw[1] & 0xffff0000u), g.map_deg);
+        }
+      }
+      u32x2v o;
+      o[0] = pack_bf16x2(val[0], val[1]);
+      o[1] = pack_bf16x2(val[2], val[3]);
+      bst8(dst, (uint32_t)((pp * D + f0) * 2), o);
+    };
+
+    // raw q, k of this lane's dq / dk elements for the map derivative (elementwise map only)
+    u32x2v mq = {0u, 0u}, mk[2] = {{0u, 0u}, {0u, 0u}};
+    if constexpr (MAPE) {
+      mq = bld8(rq, (uint32_t)((t0 + 16 * qw + m) * (D * 2) + (16 * kt + 4 * gq) * 2));
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        mk[u] = bld8(rk, (uint32_t)((t0 - H + 16 * st5(u) + m) * (D * 2) + (16 * kt + 4 * gq) * 2));
+    }
+
+    // ================================ phase A ================================
+    // bf16 copies of the chunk-end adjoint (transposed)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i0 = 32 * qw + 16 * u + 4 * gq;
+      store4<bf16>(&sm.dSeT[16 * kt + m][i0], dS[u][0], dS[u][1], dS[u][2], dS[u][3]);
+      store4<bf16>(&sm.dZeT[16 * kt + m][i0], dZ[u][0], dZ[u][1], dZ[u][2], dZ[u][3]);
+    }
+    // delta tiles C[i][s]
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      if (u < nt1) {
+        const int s0 = 16 * st1(u);
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int q = 0; q < 2; ++q) acc = mma_bf16(sref_f[q], frag_row_l(&st.phi[0][0], PD, s0, 32 * q, ln), acc);
+        const u32x2v vv = pf.v[u];
+        acc[0] -= __builtin_bit_cast(float, vv[0] << 16);
+        acc[1] -= __builtin_bit_cast(float, vv[0] & 0xffff0000u);
+        acc[2] -= __builtin_bit_cast(float, vv[1] << 16);
+        acc[3] -= __builtin_bit_cast(float, vv[1] & 0xffff0000u);
+        store4<bf16>(&sm.dl[s0 + m][16 * it1 + 4 * gq], acc[0], acc[1], acc[2], acc[3]);
+      }
+    }
+    // K tile C[tau][s] and Q = Ws o K -> Q^T
+    f32x4 kmat = zero4(), wtile = zero4();
+    if (has_mp) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        kmat = mma_bf16(frag_row_l(&st.psi[0][0], PD, 16 * tt, 32 * q, ln), frag_row_l(&st.phi[0][0], PD, 16 * stm, 32 * q, ln), kmat);
+      const s16x4 wv = tr4_l(&st.wsh[0][0], WP, 16 * tt, 16 * stm, ln);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) wtile[r] = bf16_bits_to_f32((unsigned short)wv[r]);
+      store4<bf16>(&sm.QT[16 * stm + m][16 * tt + 4 * gq], wtile[0] * kmat[0], wtile[1] * kmat[1],
+                   wtile[2] * kmat[2], wtile[3] * kmat[3]);
+    }
+    // state term of dpsi: C[k][tau] = sum_i S_in[i][k] dy[tau][i] (k = 16 kt.., tau = 16 qw..); fS, fZ
+    f32x4 TS = zero4(), TZ = zero4();
+    {
+      const int tau = 16 * qw + m;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint2 lo = *reinterpret_cast<const uint2*>(&st.dy[tau][32 * q + 4 * gq]);
+        const uint2 hi = *reinterpret_cast<const uint2*>(&st.dy[tau][32 * q + 16 + 4 * gq]);
+        const u32x4v bv = {lo.x, lo.y, hi.x, hi.y};
+        const bf16x8 fb = __builtin_bit_cast(bf16x8, bv);
+        TS = mma_bf16(__builtin_bit_cast(bf16x8, pf.sin[q]), fb, TS);
+        TZ = mma_bf16(__builtin_bit_cast(bf16x8, pf.zin[q]), fb, TZ);
+      }
+      const float4 ps = lds_bf16x4(&st.psi[tau][16 * kt + 4 * gq]);
+      float fs = TS[0] * ps.x + TS[1] * ps.y + TS[2] * ps.z + TS[3] * ps.w;
+      float fz = TZ[0] * ps.x + TZ[1] * ps.y + TZ[2] * ps.z + TZ[3] * ps.w;
+      fs += __shfl_xor(fs, 16); fs += __shfl_xor(fs, 32);
+      fz += __shfl_xor(fz, 16); fz += __shfl_xor(fz, 32);
+      if (gq == 0) { atomicAdd(&sm.fS[tau], fs); atomicAdd(&sm.fZ[tau], fz); }
+    }
+    // Grams <dS_end, S_in>, <dS_end, Z_in>, <dZ_end, Z_in> (fragment (kt, qw) holds the owned elements)
+    {
+      // (selects, not a runtime index: an indexed register array would be placed in scratch)
+      const bf16x8 fs = __builtin_bit_cast(bf16x8, qw ? pf.sin[1] : pf.sin[0]);
+      const bf16x8 fz = __builtin_bit_cast(bf16x8, qw ? pf.zin[1] : pf.zin[0]);
+      float gss = 0.f, gsz = 0.f, gzz = 0.f;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float sv = static_cast<float>(fs[4 * u + r]), zv = static_cast<float>(fz[4 * u + r]);
+          gss += dS[u][r] * sv; gsz += dS[u][r] * zv; gzz += dZ[u][r] * zv;
+        }
+      gss = row_sum16(gss); gsz = row_sum16(gsz); gzz = row_sum16(gzz);
+      gss += __shfl_xor(gss, 16); gss += __shfl_xor(gss, 32);
+      gsz += __shfl_xor(gsz, 16); gsz += __shfl_xor(gsz, 32);
+      gzz += __shfl_xor(gzz, 16); gzz += __shfl_xor(gzz, 32);
+      if (lane == 0) { sm.red[w][0] = gss; sm.red[w][1] = gsz; sm.red[w][2] = gzz; }
+    }
+    // chunk-start adjoint on the owned tiles (the transposed chunk transition):
+    //   dS_in = a dS_end + sum_t a_{t-1} dy_t psi_t^T,  dZ_in = b dZ_end - kappa dS_end - sum_t kappa_{t-1} dy_t psi_t^T
+    // (the rest of the chunk reads the chunk-end adjoint from its bf16 copies)
+    {
+      const bf16x8 fpsi = frag_tr_l(&st.psi[0][0], PD, 16 * kt, 0, ln);
+      const float ae = rec[R_ENDC], ke = rec[R_ENDC + 1], be = rec[R_ENDC + 2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int r0 = 32 * qw + 16 * u;
+        const f32x4 xa = mma_bf16(frag_tr_scaled_l(&st.dy[0][0], PD, r0, 0, rec + R_ACOEF, ln), fpsi, zero4());
+        const f32x4 xk = mma_bf16(frag_tr_scaled_l(&st.dy[0][0], PD, r0, 0, rec + R_KCOEF, ln), fpsi, zero4());
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float lam = ae * dS[u][r] + xa[r];
+          const float mu = g.momentum ? (be * dZ[u][r] - ke * dS[u][r] - xk[r]) : 0.f;
+          dS[u][r] = lam;
+          dZ[u][r] = mu;
+        }
+      }
+      if (c == 0) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const size_t off = sbase + (size_t)(32 * qw + 16 * u + 4 * gq + r) * D + 16 * kt + m;
+            a.dS0[off] = dS[u][r];
+            if (g.momentum && a.dZ0) a.dZ0[off] = dZ[u][r];
+          }
+      }
+    }
+    // the register operands of this chunk are consumed: start loading the previous chunk
+    if (c - 1 >= c_begin) pf_load(pf, c - 1);
+    __syncthreads();
+
+    // ================================ phase B ================================
+    float* blk = p.scal + ((size_t)bh * g.nc + c) * SB::SIZE;
+    if (has_mp) {   // P tile, Lm = K o P, Q' = Ws o P -> Q'^T
+      f32x4 pm = zero4();
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        pm = mma_bf16(frag_row_l(&st.dy[0][0], PD, 16 * tt, 32 * q, ln), frag_row_l(&sm.dl[0][0], PD, 16 * stm, 32 * q, ln), pm);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) blk[SB::LM + (16 * tt + 4 * gq + r) * SPM + 16 * stm + m] = kmat[r] * pm[r];
+      store4<bf16>(&sm.QpT[16 * stm + m][16 * tt + 4 * gq], wtile[0] * pm[0], wtile[1] * pm[1], wtile[2] * pm[2],
+                   wtile[3] * pm[3]);
+    }
+    // dDelta tiles C[i][s] (same tiles as delta): hS, hZ, dv, dDelta -> LDS
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      if (u < nt1) {
+        const int s0 = 16 * st1(u), s = s0 + m, i0 = 16 * it1 + 4 * gq;
+        f32x4 as = zero4(), az = zero4(), aq = zero4();
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const bf16x8 fb = frag_row_l(&st.phi[0][0], PD, s0, 32 * q, ln);
+          as = mma_bf16(frag_tr_l(&sm.dSeT[0][0], PD, 16 * it1, 32 * q, ln), fb, as);
+          az = mma_bf16(frag_tr_l(&sm.dZeT[0][0], PD, 16 * it1, 32 * q, ln), fb, az);
+        }
+        aq = mma_bf16(frag_tr_l(&st.dy[0][0], PD, 16 * it1, 0, ln), frag_row_l(&sm.QT[0][0], QP, s0, 0, ln), aq);
+        const float wz = rec[R_WZEND + s], ws = rec[R_WSEND + s];
+        const float4 dl4 = lds_bf16x4(&sm.dl[s][i0]);
+        const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+        float dd[4], hs = 0.f, hz = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          dd[r] = wz * az[r] - ws * as[r] - aq[r];
+          hs += dlv[r] * as[r];
+          hz += dlv[r] * az[r];
+        }
+        hs += __shfl_xor(hs, 16); hs += __shfl_xor(hs, 32);
+        hz += __shfl_xor(hz, 16); hz += __shfl_xor(hz, 32);
+        if (gq == 0) { atomicAdd(&sm.hS[s], hs); atomicAdd(&sm.hZ[s], hz); }
+        store4<bf16>(&sm.dD[s][i0], dd[0], dd[1], dd[2], dd[3]);
+        float val[4] = {-dd[0], -dd[1], -dd[2], -dd[3]};
+        route(s, i0, 0, val, rdv, u32x2v{0u, 0u});
+      }
+    }
+    __syncthreads();
+
+    // ================================ phase C ================================
+    {   // dpsi tile C[k][tau] = a_{tau-1} S_in^T dy - kappa_{tau-1} Z_in^T dy - sum_s phi_s Q'[tau][s]
+      f32x4 aq = zero4();
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        aq = mma_bf16(frag_tr_l(&st.phi[0][0], PD, 16 * kt, 32 * q, ln),
+                      frag_tr_l(&sm.QpT[0][0], QP, 16 * qw, 32 * q, ln), aq);
+      const int tau = 16 * qw + m;
+      const float ac = rec[R_ACOEF + tau], kc = rec[R_KCOEF + tau];
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = ac * TS[r] - kc * TZ[r] - aq[r];
+      if constexpr (MAPE) {
+        v[0] *= poly_map_grad(__builtin_bit_cast(float, mq[0] << 16), g.map_deg);
+        v[1] *= poly_map_grad(__builtin_bit_cast(float, mq[0] & 0xffff0000u), g.map_deg);
+        v[2] *= poly_map_grad(__builtin_bit_cast(float, mq[1] << 16), g.map_deg);
+        v[3] *= poly_map_grad(__builtin_bit_cast(float, mq[1] & 0xffff0000u), g.map_deg);
+      }
+      u32x2v o;
+      o[0] = pack_bf16x2(v[0], v[1]);
+      o[1] = pack_bf16x2(v[2], v[3]);
+      bst8(rdq, (uint32_t)(((t0 + tau) * D + 16 * kt + 4 * gq) * 2), o);
+    }
+    // dphi tiles C[k][s] = Wz_end dZ_end^T delta - Ws_end dS_end^T delta - sum_tau psi Q' + S_ref^T dDelta
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      if (u < nt5) {
+        const int s0 = 16 * st5(u), s = s0 + m;
+        f32x4 a1 = zero4(), a2 = zero4(), a4 = zero4();
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const bf16x8 fb = frag_row_l(&sm.dl[0][0], PD, s0, 32 * q, ln);
+          a1 = mma_bf16(frag_row_l(&sm.dZeT[0][0], PD, 16 * kt, 32 * q, ln), fb, a1);
+          a2 = mma_bf16(frag_row_l(&sm.dSeT[0][0], PD, 16 * kt, 32 * q, ln), fb, a2);
+          a4 = mma_bf16(srefT_f[q], frag_row_l(&sm.dD[0][0], PD, s0, 32 * q, ln), a4);
+        }
+        const f32x4 a3 =
+            mma_bf16(frag_tr_l(&st.psi[0][0], PD, 16 * kt, 0, ln), frag_row_l(&sm.QpT[0][0], QP, s0, 0, ln), zero4());
+        const float wz = rec[R_WZEND + s], ws = rec[R_WSEND + s];
+        float val[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) val[r] = wz * a1[r] - ws * a2[r] - a3[r] + a4[r];
+        route(s, 16 * kt + 4 * gq, 1, val, rdk, mk[u]);
+      }
+    }
+    // dS_ref on the owned tiles: += sum_s dDelta[s][i] phi[s][k]
+    {
+      bf16x8 fb[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) fb[q] = frag_tr_l(&st.phi[0][0], PD, 16 * kt, 32 * q, ln);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int q = 0; q < 2; ++q) acc = mma_bf16(frag_tr_l(&sm.dD[0][0], PD, 32 * qw + 16 * u, 32 * q, ln), fb[q], acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dsr[u][r] += acc[r];
+      }
+    }
+    // scalar-gradient record of the chunk (hS, hZ after phase B; fS, fZ, Grams after phase A)
+    if (tid < CH * (SPM - SP) / 4) {   // Lm columns past the sources
+      const int rr = tid / ((SPM - SP) / 4), cc = SP + 4 * (tid % ((SPM - SP) / 4));
+      *reinterpret_cast<float4*>(blk + SB::LM + rr * SPM + cc) = make_float4(0.f, 0.f, 0.f, 0.f);
+    } else if (tid >= 256 && tid < 256 + SPM) {
+      const int s = tid - 256;
+      blk[SB::HS + s] = sm.hS[s];
+      blk[SB::HZ + s] = sm.hZ[s];
+      sm.hS[s] = 0.f;
+      sm.hZ[s] = 0.f;
+    } else if (tid >= 384 && tid < 384 + CH) {
+      const int t = tid - 384;
+      blk[SB::FS + t] = sm.fS[t];
+      blk[SB::FZ + t] = sm.fZ[t];
+      sm.fS[t] = 0.f;
+      sm.fZ[t] = 0.f;
+    } else if (tid >= 448 && tid < 452) {
+      const int j = tid - 448;
+      float sum = 0.f;
+      if (j < 3) {
+#pragma unroll
+        for (int ww = 0; ww < kSegWaves; ++ww) sum += sm.red[ww][j];
+      }
+      blk[SB::GRAM + j] = sum;
+    }
+    // stage the previous chunk (its loads were issued at the end of phase A)
+    if (c - 1 >= c_begin) pf_store(pf, sm.st[b ^ 1]);
+    __syncthreads();
+  }
+
+  // ---- segment output: dS_ref partial
+  float* dst = p.dsref_part + ((size_t)bh * sg.nseg + seg) * DD;
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[(size_t)(32 * qw + 16 * u + 4 * gq + r) * D + 16 * kt + m] = dsr[u][r];
+}
+
+size_t walk_bwd_smem_bytes() { return sizeof(wb::Smem); }
+
+hipError_t launch_walk_bwd_kernel(const Geom& g, const BwdPtrs<bf16>& a, const SegGeom& sg, const BwdSegPtrs& p,
+                                  hipStream_t stream) {
+  const size_t smem = sizeof(wb::Smem);
+  hipError_t err;
+  if (g.map_mode == MAP_ELEMENTWISE) {
+    err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_bwd<true>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL((k_walk_bwd<true>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, p);
+  } else {
+    err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_bwd<false>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL((k_walk_bwd<false>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, p);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace atlas

@@ -134,6 +134,47 @@ __device__ __forceinline__ bf16x8 frag_row(const bf16* p, int ld, int r0, int k0
   return *reinterpret_cast<const bf16x8*>(p + (r0 + (l & 15)) * ld + k0 + 8 * (l >> 4));
 }
 
+// The same fragment reads with the lane index passed in. Inside a chunk loop the caller passes a
+// lane index laundered through an empty asm statement once per chunk, so that the per-lane LDS
+// addresses are recomputed each chunk instead of being hoisted out of the loop and held in (or
+// spilled from) registers for the whole walk.
+__device__ __forceinline__ int launder(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+__device__ __forceinline__ bf16x8 frag_row_l(const bf16* p, int ld, int r0, int k0, int l) {
+  return *reinterpret_cast<const bf16x8*>(p + (r0 + (l & 15)) * ld + k0 + 8 * (l >> 4));
+}
+// lane (g, m) receives p[row0 + 4g + j][col0 + m], j < 4 (see tr4)
+__device__ __forceinline__ s16x4 tr4_l(const bf16* p, int ld, int row0, int col0, int l) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const int g = l >> 4, i = l & 15;
+  const bf16* q = p + (row0 + 4 * g + (i >> 2)) * ld + col0 + 4 * (i & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(q));
+}
+// Standard-order fragment of the transpose of a row-major p[k][r]: lane supplies
+// A[r0 + (l & 15)][k0 + 8 (l >> 4) + e] = p[k0 + 8 (l >> 4) + e][r0 + (l & 15)] (two transposing reads).
+__device__ __forceinline__ bf16x8 frag_tr_l(const bf16* p, int ld, int r0, int k0, int l) {
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  // tr4_l adds 4 (l >> 4) to the row base: rows k0 + 8 (l >> 4) + (0..3), then + 4 .. 7
+  const s16x4 lo = tr4_l(p, ld, k0 + 4 * (l >> 4), r0, l);
+  const s16x4 hi = tr4_l(p, ld, k0 + 4 * (l >> 4) + 4, r0, l);
+  const s16x8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, v);
+}
+// frag_tr_l with k value e scaled by s[k0 + 8 (l >> 4) + e] (fp32, LDS).
+__device__ __forceinline__ bf16x8 frag_tr_scaled_l(const bf16* p, int ld, int r0, int k0, const float* s, int l) {
+  const bf16x8 f = frag_tr_l(p, ld, r0, k0, l);
+  const float4 s0 = *reinterpret_cast<const float4*>(s + k0 + 8 * (l >> 4));
+  const float4 s1 = *reinterpret_cast<const float4*>(s + k0 + 8 * (l >> 4) + 4);
+  bf16x8 r;
+  r[0] = static_cast<__bf16>(static_cast<float>(f[0]) * s0.x); r[1] = static_cast<__bf16>(static_cast<float>(f[1]) * s0.y);
+  r[2] = static_cast<__bf16>(static_cast<float>(f[2]) * s0.z); r[3] = static_cast<__bf16>(static_cast<float>(f[3]) * s0.w);
+  r[4] = static_cast<__bf16>(static_cast<float>(f[4]) * s1.x); r[5] = static_cast<__bf16>(static_cast<float>(f[5]) * s1.y);
+  r[6] = static_cast<__bf16>(static_cast<float>(f[6]) * s1.z); r[7] = static_cast<__bf16>(static_cast<float>(f[7]) * s1.w);
+  return r;
+}
+
 // Elementwise polynomial map on eight bf16 values held as a 16-byte vector.
 __device__ __forceinline__ u32x4v map_bf16x8(u32x4v v, int deg) {
   u32x4v r;
@@ -144,6 +185,17 @@ __device__ __forceinline__ u32x4v map_bf16x8(u32x4v v, int deg) {
     r[w] = pack_bf16x2(a, b);
   }
   return r;
+}
+
+// Saved chunk-start states of the specialised walks (forward -> backward): per backward chunk,
+// S then Z, each 64 x 64 bf16 stored as eight 1 KB operand fragments (kt = 0..3, q = 0..1) in the
+// chained slot order: lane (g, m) of fragment (kt, q) holds X[32q + 4g + r][16kt + m] in slots r < 4
+// and X[32q + 16 + 4g + r][16kt + m] in slots 4 + r. The backward loads a fragment with one 16-byte
+// access per lane; the forward's state owners (16-row tile it, columns 16kt + m) write 8 bytes.
+constexpr int kStateBytes = 64 * 64 * 2;        // one state, bf16
+constexpr int kStateBlk = 2 * kStateBytes;      // S and Z of one backward chunk
+__device__ __forceinline__ uint32_t frag_off(int kt, int q, int lane) {
+  return (uint32_t)(((kt * 2 + q) * 64 + lane) * 16);
 }
 
 }  // namespace atlas

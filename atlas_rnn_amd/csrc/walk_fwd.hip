@@ -16,8 +16,9 @@
 // (window e <= 17); source s is token t0 - (e - 1) + s.
 //
 //   k_walk_agg  : zero initial state -> segment aggregate (a, kappa, b, U, V)       [WALK_AGG]
-//   k_walk_full : from the segment-start state: y, S_T / Z_T, the raw state at every backward-chunk
-//                 boundary (chunk start and token Lmid - 1) for the backward         [WALK_FULL]
+//   k_walk_full : from the segment-start state: y, S_T / Z_T, and the state at every backward-chunk
+//                 boundary (chunk start and token Lmid - 1) for the backward, in the bf16 fragment
+//                 layout of walk_common.h                                          [WALK_FULL]
 #include "mem_common.h"
 #include "mem_params.h"
 #include "seg_common.h"
@@ -205,11 +206,24 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
   float seg_a = 1.f, seg_k = 0.f, seg_b = 1.f;
   const int i0 = 16 * it + 4 * gq;
   const int rb = g.Lmid > 0 ? 2 : 1;
-  float* rw_row = FULL ? rw + (size_t)bh * g.ncb * 2 * DD : nullptr;
+  // saved states (walk_common.h layout): block of backward chunk cb at rw_row + cb * kStateBlk
+  unsigned char* rw_row = FULL ? reinterpret_cast<unsigned char*>(rw) + (size_t)bh * g.ncb * kStateBlk : nullptr;
+  // this lane's 8-byte half of the fragments of its tiles j = 0, 1
+  const uint32_t f2o[2] = {frag_off(2 * th, it >> 1, lane) + (it & 1) * 8,
+                           frag_off(2 * th + 1, it >> 1, lane) + (it & 1) * 8};
+  auto save_state = [&](int cb, const float (&Sv)[2][4], const float (&Zv)[2][4]) {
+    unsigned char* blk = rw_row + (size_t)cb * kStateBlk;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      *reinterpret_cast<uint2*>(blk + f2o[j]) =
+          make_uint2(pack_bf16x2(Sv[j][0], Sv[j][1]), pack_bf16x2(Sv[j][2], Sv[j][3]));
+      *reinterpret_cast<uint2*>(blk + kStateBytes + f2o[j]) =
+          make_uint2(pack_bf16x2(Zv[j][0], Zv[j][1]), pack_bf16x2(Zv[j][2], Zv[j][3]));
+    }
+  };
 
   if constexpr (FULL) {
     const float* ss = seg_states + ((size_t)bh * sg.nseg + seg) * 2 * DD;
-    float* dst = rw_row + (size_t)c_begin * rb * 2 * DD;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int k = 32 * th + 16 * j + m;
@@ -218,12 +232,11 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
         const size_t off = (size_t)(i0 + r) * D + k;
         Sr[j][r] = ss[off];
         Zr[j][r] = ss[DD + off];
-        dst[off] = Sr[j][r];
-        dst[DD + off] = Zr[j][r];
       }
       store4<bf16>(&sm.SbT[0][k][i0], Sr[j][0], Sr[j][1], Sr[j][2], Sr[j][3]);
       store4<bf16>(&sm.ZbT[0][k][i0], Zr[j][0], Zr[j][1], Zr[j][2], Zr[j][3]);
     }
+    save_state(c_begin * rb, Sr, Zr);
   }
 
   Prefetch<FULL> pf;
@@ -356,7 +369,7 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
             fzm[q] = pack_frag_scaled(dl[2 * q], lo, zhi, zlo);
           }
           const float ma = rec[R_MIDC], mk = rec[R_MIDC + 1], mb = rec[R_MIDC + 2];
-          float* dst = rw_row + ((size_t)c * rb + 1) * 2 * DD;
+          float Sm_[2][4], Zm_[2][4];
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
             f32x4 au = zero4(), av = zero4();
@@ -365,17 +378,15 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
               au = mma_bf16(fsm[q], fb[j][q], au);
               av = mma_bf16(fzm[q], fb[j][q], av);
             }
-            const int k = 32 * th + 16 * j + m;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const size_t off = (size_t)(i0 + r) * D + k;
-              dst[off] = ma * Sr[j][r] - mk * Zr[j][r] - au[r];
-              dst[DD + off] = g.momentum ? (mb * Zr[j][r] + av[r]) : 0.f;
+              Sm_[j][r] = ma * Sr[j][r] - mk * Zr[j][r] - au[r];
+              Zm_[j][r] = g.momentum ? (mb * Zr[j][r] + av[r]) : 0.f;
             }
           }
+          save_state(c * rb + 1, Sm_, Zm_);
         }
       }
-      float* rw_next = (FULL && c + 1 < c_end) ? rw_row + (size_t)(c + 1) * rb * 2 * DD : nullptr;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         f32x4 au = zero4(), av = zero4();
@@ -393,17 +404,12 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
           Zr[j][r] = Zn;
         }
         if constexpr (FULL) {
-          if (rw_next) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const size_t off = (size_t)(i0 + r) * D + k;
-              rw_next[off] = Sr[j][r];
-              rw_next[DD + off] = Zr[j][r];
-            }
-          }
           store4<bf16>(&sm.SbT[b ^ 1][k][i0], Sr[j][0], Sr[j][1], Sr[j][2], Sr[j][3]);
           store4<bf16>(&sm.ZbT[b ^ 1][k][i0], Zr[j][0], Zr[j][1], Zr[j][2], Zr[j][3]);
         }
+      }
+      if constexpr (FULL) {
+        if (c + 1 < c_end) save_state((c + 1) * rb, Sr, Zr);
       }
       if constexpr (!FULL) {
         const float na = a_end * seg_a;
