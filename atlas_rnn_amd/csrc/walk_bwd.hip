@@ -31,7 +31,7 @@ constexpr int NST = SP / 16;    // 3 source tiles
 constexpr int SPR = 64;         // LDS rows of source-indexed matrices (rows SP.. stay zero: k = 32 steps)
 constexpr int PD = D + 8;       // pitch of 64-wide bf16 rows
 constexpr int SPM = CH + kHaloPad;   // 64: pitch of the per-source arrays in HBM (records, Ws, Lm)
-constexpr int WP = SP + 8;      // 56: LDS pitch of the Ws rows [tau][s]
+constexpr int WP = SPR + 8;     // 72: LDS pitch of the Ws rows [tau][s] (columns SP.. stay zero)
 constexpr int QP = CH + 8;      // 40: LDS pitch of Q^T / Q'^T rows [s][tau]
 constexpr int REC = CoefRec<CH>::SIZE;   // 328
 constexpr int R_ACOEF = 0, R_KCOEF = CH, R_ENDC = 2 * CH, R_WSEND = 2 * CH + 4, R_WZEND = R_WSEND + SPM;
@@ -77,7 +77,8 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
   using namespace wb;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   Smem& sm = *reinterpret_cast<Smem*>(smem_raw);
-  const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
+  const int tid = threadIdx.x, lane = lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (scalar) wave index
   const int gq = lane >> 4, m = lane & 15;
   const int seg = blockIdx.x, bh = blockIdx.y;
   const int H = g.H;
@@ -85,15 +86,12 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
   const size_t DD = (size_t)D * D;
   const size_t sbase = (size_t)bh * DD;
   const int seg_tail0 = min(g.T, c_end * CH) - H;
-  // roles
-  const int qw = w & 1, kt = w >> 1;            // owned adjoint tiles: rows 32 qw + 16 u, columns 16 kt
-  const int it1 = w & 3;                        // delta / dDelta tiles: rows 16 it1, sources st1(u)
-  const int nt1 = w < 4 ? 2 : 1;
-  auto st1 = [&](int u) { return w < 4 ? 2 * u : 1; };
-  const bool has_mp = w < 6;                    // K / P tile (tt, stm)
-  const int tt = w & 1, stm = w >> 1;
-  const int nt5 = qw == 0 ? 2 : 1;              // dphi tiles: columns 16 kt, sources st5(u)
-  auto st5 = [&](int u) { return u == 0 ? qw : 2; };
+  // roles (every wave does the same work; source tile 3, s = 48 .. 63, is zero padding)
+  const int qw = w & 1, kt = w >> 1;     // owned adjoint tiles: rows 32 qw + 16 u, columns 16 kt
+  const int it1 = w & 3;                 // delta / dDelta tiles: rows 16 it1, sources 16 st1(u)
+  const int s1a = w >> 2;                // st1(u) = s1a + 2 u
+  const int tt = w & 1, stm = w >> 1;    // K / P tile: targets 16 tt, sources 16 stm
+  // dpsi tile: features 16 kt, targets 16 qw; dphi tiles: features 16 kt, sources 16 (qw + 2 u)
 
   const uint32_t row_bytes = (uint32_t)g.T * (D * 2);
   const rsrc_t rk = make_rsrc(a.k + (size_t)bh * g.T * D, row_bytes);
@@ -121,15 +119,15 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
   uint32_t o_v[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    const int s = 16 * st1(u) + m;
-    o_v[u] = (u < nt1 && s < H + CH) ? (uint32_t)((s - H) * (D * 2) + (16 * it1 + 4 * gq) * 2) : kOob;
+    const int s = 16 * (s1a + 2 * u) + m;
+    o_v[u] = s < H + CH ? (uint32_t)((s - H) * (D * 2) + (16 * it1 + 4 * gq) * 2) : kOob;
   }
 
   auto pf_load = [&](Prefetch& pf, int c) {
     const int t0 = c * CH;
     const uint32_t tb = (uint32_t)t0 * (D * 2);
     pf.phi = bld16(rk, o_phi + tb);
-    pf.x = bld16(tid < 256 ? rq : rdy, o_x + tb);
+    pf.x = bld16(w < 4 ? rq : rdy, o_x + tb);   // waves 0-3: psi rows, 4-7: dy rows
     pf.wsh = bld16(rwsh, o_wsh + (uint32_t)c * (CH * SPM * 2));
     pf.rec = bld16(rrec, o_rec + (uint32_t)c * (REC * 4));
 #pragma unroll
@@ -207,6 +205,11 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
     sm.QT[rr][cc] = bf16(0.f);
     sm.QpT[rr][cc] = bf16(0.f);
   }
+  for (int idx = tid; idx < CH * (WP - SP); idx += kSegThreads) {
+    const int rr = idx / (WP - SP), cc = SP + idx % (WP - SP);
+    sm.st[0].wsh[rr][cc] = bf16(0.f);
+    sm.st[1].wsh[rr][cc] = bf16(0.f);
+  }
   for (int idx = tid; idx < 2 * HMAX * 2 * D; idx += kSegThreads) (&sm.carry[0][0][0])[idx] = 0.f;
   if (tid < SPM) { sm.hS[tid] = 0.f; sm.hZ[tid] = 0.f; }
   if (tid < CH) { sm.fS[tid] = 0.f; sm.fZ[tid] = 0.f; }
@@ -272,68 +275,81 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
       mq = bld8(rq, (uint32_t)((t0 + 16 * qw + m) * (D * 2) + (16 * kt + 4 * gq) * 2));
 #pragma unroll
       for (int u = 0; u < 2; ++u)
-        mk[u] = bld8(rk, (uint32_t)((t0 - H + 16 * st5(u) + m) * (D * 2) + (16 * kt + 4 * gq) * 2));
+        mk[u] = bld8(rk, (uint32_t)((t0 - H + 16 * (qw + 2 * u) + m) * (D * 2) + (16 * kt + 4 * gq) * 2));
     }
 
     // ================================ phase A ================================
-    // bf16 copies of the chunk-end adjoint (transposed)
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int i0 = 32 * qw + 16 * u + 4 * gq;
-      store4<bf16>(&sm.dSeT[16 * kt + m][i0], dS[u][0], dS[u][1], dS[u][2], dS[u][3]);
-      store4<bf16>(&sm.dZeT[16 * kt + m][i0], dZ[u][0], dZ[u][1], dZ[u][2], dZ[u][3]);
-    }
-    // delta tiles C[i][s]
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      if (u < nt1) {
-        const int s0 = 16 * st1(u);
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int q = 0; q < 2; ++q) acc = mma_bf16(sref_f[q], frag_row_l(&st.phi[0][0], PD, s0, 32 * q, ln), acc);
-        const u32x2v vv = pf.v[u];
-        acc[0] -= __builtin_bit_cast(float, vv[0] << 16);
-        acc[1] -= __builtin_bit_cast(float, vv[0] & 0xffff0000u);
-        acc[2] -= __builtin_bit_cast(float, vv[1] << 16);
-        acc[3] -= __builtin_bit_cast(float, vv[1] & 0xffff0000u);
-        store4<bf16>(&sm.dl[s0 + m][16 * it1 + 4 * gq], acc[0], acc[1], acc[2], acc[3]);
-      }
-    }
-    // K tile C[tau][s] and Q = Ws o K -> Q^T
-    f32x4 kmat = zero4(), wtile = zero4();
-    if (has_mp) {
-#pragma unroll
-      for (int q = 0; q < 2; ++q)
-        kmat = mma_bf16(frag_row_l(&st.psi[0][0], PD, 16 * tt, 32 * q, ln), frag_row_l(&st.phi[0][0], PD, 16 * stm, 32 * q, ln), kmat);
-      const s16x4 wv = tr4_l(&st.wsh[0][0], WP, 16 * tt, 16 * stm, ln);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) wtile[r] = bf16_bits_to_f32((unsigned short)wv[r]);
-      store4<bf16>(&sm.QT[16 * stm + m][16 * tt + 4 * gq], wtile[0] * kmat[0], wtile[1] * kmat[1],
-                   wtile[2] * kmat[2], wtile[3] * kmat[3]);
-    }
-    // state term of dpsi: C[k][tau] = sum_i S_in[i][k] dy[tau][i] (k = 16 kt.., tau = 16 qw..); fS, fZ
-    f32x4 TS = zero4(), TZ = zero4();
+    // delta tiles C[i][s], K tile C[tau][s] (Q = Ws o K), the state term of dpsi C[k][tau] =
+    // sum_i S_in[i][k] dy[tau][i], the chunk transition terms, the Grams; operands first, then the
+    // matrix products, then the epilogues and LDS stores.
+    f32x4 dl_acc[2], kmat, TS, TZ, xa[2], xk[2];
+    float wt[4];
     {
-      const int tau = 16 * qw + m;
+      bf16x8 fphi[2][2], fpk[2], fps[2], fdy[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) fphi[u][q] = frag_row_l(&st.phi[0][0], PD, 16 * (s1a + 2 * u), 32 * q, ln);
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
+        fpk[q] = frag_row_l(&st.phi[0][0], PD, 16 * stm, 32 * q, ln);
+        fps[q] = frag_row_l(&st.psi[0][0], PD, 16 * tt, 32 * q, ln);
+        const int tau = 16 * qw + m;
         const uint2 lo = *reinterpret_cast<const uint2*>(&st.dy[tau][32 * q + 4 * gq]);
         const uint2 hi = *reinterpret_cast<const uint2*>(&st.dy[tau][32 * q + 16 + 4 * gq]);
         const u32x4v bv = {lo.x, lo.y, hi.x, hi.y};
-        const bf16x8 fb = __builtin_bit_cast(bf16x8, bv);
-        TS = mma_bf16(__builtin_bit_cast(bf16x8, pf.sin[q]), fb, TS);
-        TZ = mma_bf16(__builtin_bit_cast(bf16x8, pf.zin[q]), fb, TZ);
+        fdy[q] = __builtin_bit_cast(bf16x8, bv);
       }
+      const bf16x8 fpsiT = frag_tr_l(&st.psi[0][0], PD, 16 * kt, 0, ln);
+      bf16x8 fya[2], fyk[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        fya[u] = frag_tr_scaled_l(&st.dy[0][0], PD, 32 * qw + 16 * u, 0, rec + R_ACOEF, ln);
+        fyk[u] = frag_tr_scaled_l(&st.dy[0][0], PD, 32 * qw + 16 * u, 0, rec + R_KCOEF, ln);
+      }
+      const s16x4 wv = tr4_l(&st.wsh[0][0], WP, 16 * tt, 16 * stm, ln);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) wt[r] = bf16_bits_to_f32((unsigned short)wv[r]);
+
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        dl_acc[u] = mma_bf16(sref_f[0], fphi[u][0], zero4());
+        dl_acc[u] = mma_bf16(sref_f[1], fphi[u][1], dl_acc[u]);
+      }
+      kmat = mma_bf16(fps[0], fpk[0], zero4());
+      kmat = mma_bf16(fps[1], fpk[1], kmat);
+      TS = mma_bf16(__builtin_bit_cast(bf16x8, pf.sin[0]), fdy[0], zero4());
+      TZ = mma_bf16(__builtin_bit_cast(bf16x8, pf.zin[0]), fdy[0], zero4());
+      TS = mma_bf16(__builtin_bit_cast(bf16x8, pf.sin[1]), fdy[1], TS);
+      TZ = mma_bf16(__builtin_bit_cast(bf16x8, pf.zin[1]), fdy[1], TZ);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        xa[u] = mma_bf16(fya[u], fpsiT, zero4());
+        xk[u] = mma_bf16(fyk[u], fpsiT, zero4());
+      }
+    }
+    {   // delta = acc - v -> LDS
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const u32x2v vv = pf.v[u];
+        store4<bf16>(&sm.dl[16 * (s1a + 2 * u) + m][16 * it1 + 4 * gq],
+                     dl_acc[u][0] - __builtin_bit_cast(float, vv[0] << 16),
+                     dl_acc[u][1] - __builtin_bit_cast(float, vv[0] & 0xffff0000u),
+                     dl_acc[u][2] - __builtin_bit_cast(float, vv[1] << 16),
+                     dl_acc[u][3] - __builtin_bit_cast(float, vv[1] & 0xffff0000u));
+      }
+      store4<bf16>(&sm.QT[16 * stm + m][16 * tt + 4 * gq], wt[0] * kmat[0], wt[1] * kmat[1], wt[2] * kmat[2],
+                   wt[3] * kmat[3]);
+    }
+    {   // fS, fZ (partial over this wave's 16 features, summed over the rows)
+      const int tau = 16 * qw + m;
       const float4 ps = lds_bf16x4(&st.psi[tau][16 * kt + 4 * gq]);
-      float fs = TS[0] * ps.x + TS[1] * ps.y + TS[2] * ps.z + TS[3] * ps.w;
-      float fz = TZ[0] * ps.x + TZ[1] * ps.y + TZ[2] * ps.z + TZ[3] * ps.w;
-      fs += __shfl_xor(fs, 16); fs += __shfl_xor(fs, 32);
-      fz += __shfl_xor(fz, 16); fz += __shfl_xor(fz, 32);
+      const float fs = xsum_rows(TS[0] * ps.x + TS[1] * ps.y + TS[2] * ps.z + TS[3] * ps.w);
+      const float fz = xsum_rows(TZ[0] * ps.x + TZ[1] * ps.y + TZ[2] * ps.z + TZ[3] * ps.w);
       if (gq == 0) { atomicAdd(&sm.fS[tau], fs); atomicAdd(&sm.fZ[tau], fz); }
     }
-    // Grams <dS_end, S_in>, <dS_end, Z_in>, <dZ_end, Z_in> (fragment (kt, qw) holds the owned elements)
-    {
-      // (selects, not a runtime index: an indexed register array would be placed in scratch)
+    {   // Grams <dS_end, S_in>, <dS_end, Z_in>, <dZ_end, Z_in> (fragment (kt, qw) holds the owned elements;
+        // selects, not a runtime index, so that the prefetch registers stay registers)
       const bf16x8 fs = __builtin_bit_cast(bf16x8, qw ? pf.sin[1] : pf.sin[0]);
       const bf16x8 fz = __builtin_bit_cast(bf16x8, qw ? pf.zin[1] : pf.zin[0]);
       float gss = 0.f, gsz = 0.f, gzz = 0.f;
@@ -344,27 +360,21 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
           const float sv = static_cast<float>(fs[4 * u + r]), zv = static_cast<float>(fz[4 * u + r]);
           gss += dS[u][r] * sv; gsz += dS[u][r] * zv; gzz += dZ[u][r] * zv;
         }
-      gss = row_sum16(gss); gsz = row_sum16(gsz); gzz = row_sum16(gzz);
-      gss += __shfl_xor(gss, 16); gss += __shfl_xor(gss, 32);
-      gsz += __shfl_xor(gsz, 16); gsz += __shfl_xor(gsz, 32);
-      gzz += __shfl_xor(gzz, 16); gzz += __shfl_xor(gzz, 32);
-      if (lane == 0) { sm.red[w][0] = gss; sm.red[w][1] = gsz; sm.red[w][2] = gzz; }
+      gss = xsum_rows(row_sum16(gss)); gsz = xsum_rows(row_sum16(gsz)); gzz = xsum_rows(row_sum16(gzz));
+      if (ln == 0) { sm.red[w][0] = gss; sm.red[w][1] = gsz; sm.red[w][2] = gzz; }
     }
-    // chunk-start adjoint on the owned tiles (the transposed chunk transition):
-    //   dS_in = a dS_end + sum_t a_{t-1} dy_t psi_t^T,  dZ_in = b dZ_end - kappa dS_end - sum_t kappa_{t-1} dy_t psi_t^T
-    // (the rest of the chunk reads the chunk-end adjoint from its bf16 copies)
-    {
-      const bf16x8 fpsi = frag_tr_l(&st.psi[0][0], PD, 16 * kt, 0, ln);
+    {   // the chunk-end adjoint's bf16 copies (read by phases B, C), then the chunk-start adjoint:
+        //   dS_in = a dS_end + sum_t a_{t-1} dy_t psi_t^T,  dZ_in = b dZ_end - kappa dS_end - sum_t kappa_{t-1} dy_t psi_t^T
       const float ae = rec[R_ENDC], ke = rec[R_ENDC + 1], be = rec[R_ENDC + 2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int r0 = 32 * qw + 16 * u;
-        const f32x4 xa = mma_bf16(frag_tr_scaled_l(&st.dy[0][0], PD, r0, 0, rec + R_ACOEF, ln), fpsi, zero4());
-        const f32x4 xk = mma_bf16(frag_tr_scaled_l(&st.dy[0][0], PD, r0, 0, rec + R_KCOEF, ln), fpsi, zero4());
+        const int i0 = 32 * qw + 16 * u + 4 * gq;
+        store4<bf16>(&sm.dSeT[16 * kt + m][i0], dS[u][0], dS[u][1], dS[u][2], dS[u][3]);
+        store4<bf16>(&sm.dZeT[16 * kt + m][i0], dZ[u][0], dZ[u][1], dZ[u][2], dZ[u][3]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float lam = ae * dS[u][r] + xa[r];
-          const float mu = g.momentum ? (be * dZ[u][r] - ke * dS[u][r] - xk[r]) : 0.f;
+          const float lam = ae * dS[u][r] + xa[u][r];
+          const float mu = g.momentum ? (be * dZ[u][r] - ke * dS[u][r] - xk[u][r]) : 0.f;
           dS[u][r] = lam;
           dZ[u][r] = mu;
         }
@@ -385,42 +395,56 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
     __syncthreads();
 
     // ================================ phase B ================================
+    // P tile C[tau][s] = dy delta^T (Lm = K o P, Q' = Ws o P); dDelta tiles C[i][s] =
+    // Wz_end dZ_end phi - Ws_end dS_end phi - sum_tau dy Q (hS, hZ, dv)
     float* blk = p.scal + ((size_t)bh * g.nc + c) * SB::SIZE;
-    if (has_mp) {   // P tile, Lm = K o P, Q' = Ws o P -> Q'^T
-      f32x4 pm = zero4();
+    {
+      bf16x8 fy[2], fd[2], fp[2][2], fsT[2], fzT[2], fq[2];
 #pragma unroll
-      for (int q = 0; q < 2; ++q)
-        pm = mma_bf16(frag_row_l(&st.dy[0][0], PD, 16 * tt, 32 * q, ln), frag_row_l(&sm.dl[0][0], PD, 16 * stm, 32 * q, ln), pm);
+      for (int q = 0; q < 2; ++q) {
+        fy[q] = frag_row_l(&st.dy[0][0], PD, 16 * tt, 32 * q, ln);
+        fd[q] = frag_row_l(&sm.dl[0][0], PD, 16 * stm, 32 * q, ln);
+        fsT[q] = frag_tr_l(&sm.dSeT[0][0], PD, 16 * it1, 32 * q, ln);
+        fzT[q] = frag_tr_l(&sm.dZeT[0][0], PD, 16 * it1, 32 * q, ln);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) fp[u][q] = frag_row_l(&st.phi[0][0], PD, 16 * (s1a + 2 * u), 32 * q, ln);
+      }
+      const bf16x8 fyT = frag_tr_l(&st.dy[0][0], PD, 16 * it1, 0, ln);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) fq[u] = frag_row_l(&sm.QT[0][0], QP, 16 * (s1a + 2 * u), 0, ln);
+      float4 dlv[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) dlv[u] = lds_bf16x4(&sm.dl[16 * (s1a + 2 * u) + m][16 * it1 + 4 * gq]);
+
+      f32x4 pm = mma_bf16(fy[0], fd[0], zero4());
+      pm = mma_bf16(fy[1], fd[1], pm);
+      f32x4 as[2], az[2], aq[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        as[u] = mma_bf16(fsT[0], fp[u][0], zero4());
+        az[u] = mma_bf16(fzT[0], fp[u][0], zero4());
+        aq[u] = mma_bf16(fyT, fq[u], zero4());
+        as[u] = mma_bf16(fsT[1], fp[u][1], as[u]);
+        az[u] = mma_bf16(fzT[1], fp[u][1], az[u]);
+      }
+
 #pragma unroll
       for (int r = 0; r < 4; ++r) blk[SB::LM + (16 * tt + 4 * gq + r) * SPM + 16 * stm + m] = kmat[r] * pm[r];
-      store4<bf16>(&sm.QpT[16 * stm + m][16 * tt + 4 * gq], wtile[0] * pm[0], wtile[1] * pm[1], wtile[2] * pm[2],
-                   wtile[3] * pm[3]);
-    }
-    // dDelta tiles C[i][s] (same tiles as delta): hS, hZ, dv, dDelta -> LDS
+      store4<bf16>(&sm.QpT[16 * stm + m][16 * tt + 4 * gq], wt[0] * pm[0], wt[1] * pm[1], wt[2] * pm[2], wt[3] * pm[3]);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      if (u < nt1) {
-        const int s0 = 16 * st1(u), s = s0 + m, i0 = 16 * it1 + 4 * gq;
-        f32x4 as = zero4(), az = zero4(), aq = zero4();
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const bf16x8 fb = frag_row_l(&st.phi[0][0], PD, s0, 32 * q, ln);
-          as = mma_bf16(frag_tr_l(&sm.dSeT[0][0], PD, 16 * it1, 32 * q, ln), fb, as);
-          az = mma_bf16(frag_tr_l(&sm.dZeT[0][0], PD, 16 * it1, 32 * q, ln), fb, az);
-        }
-        aq = mma_bf16(frag_tr_l(&st.dy[0][0], PD, 16 * it1, 0, ln), frag_row_l(&sm.QT[0][0], QP, s0, 0, ln), aq);
+      for (int u = 0; u < 2; ++u) {
+        const int s = 16 * (s1a + 2 * u) + m, i0 = 16 * it1 + 4 * gq;
         const float wz = rec[R_WZEND + s], ws = rec[R_WSEND + s];
-        const float4 dl4 = lds_bf16x4(&sm.dl[s][i0]);
-        const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+        const float dlr[4] = {dlv[u].x, dlv[u].y, dlv[u].z, dlv[u].w};
         float dd[4], hs = 0.f, hz = 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          dd[r] = wz * az[r] - ws * as[r] - aq[r];
-          hs += dlv[r] * as[r];
-          hz += dlv[r] * az[r];
+          dd[r] = wz * az[u][r] - ws * as[u][r] - aq[u][r];
+          hs += dlr[r] * as[u][r];
+          hz += dlr[r] * az[u][r];
         }
-        hs += __shfl_xor(hs, 16); hs += __shfl_xor(hs, 32);
-        hz += __shfl_xor(hz, 16); hz += __shfl_xor(hz, 32);
+        hs = xsum_rows(hs);
+        hz = xsum_rows(hz);
         if (gq == 0) { atomicAdd(&sm.hS[s], hs); atomicAdd(&sm.hZ[s], hz); }
         store4<bf16>(&sm.dD[s][i0], dd[0], dd[1], dd[2], dd[3]);
         float val[4] = {-dd[0], -dd[1], -dd[2], -dd[3]};
@@ -430,69 +454,77 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
     __syncthreads();
 
     // ================================ phase C ================================
-    {   // dpsi tile C[k][tau] = a_{tau-1} S_in^T dy - kappa_{tau-1} Z_in^T dy - sum_s phi_s Q'[tau][s]
-      f32x4 aq = zero4();
+    // dpsi tile C[k][tau] = a_{tau-1} S_in^T dy - kappa_{tau-1} Z_in^T dy - sum_s phi_s Q'[tau][s];
+    // dphi tiles C[k][s] = Wz_end dZ_end^T delta - Ws_end dS_end^T delta - sum_tau psi Q' + S_ref^T dDelta;
+    // dS_ref += dDelta^T phi on the owned tiles
+    {
+      bf16x8 fphT[2], fqpT[2], fdl[2][2], fzE[2], fsE[2], fdd[2][2], fqp[2], fddT[2][2];
 #pragma unroll
-      for (int q = 0; q < 2; ++q)
-        aq = mma_bf16(frag_tr_l(&st.phi[0][0], PD, 16 * kt, 32 * q, ln),
-                      frag_tr_l(&sm.QpT[0][0], QP, 16 * qw, 32 * q, ln), aq);
-      const int tau = 16 * qw + m;
-      const float ac = rec[R_ACOEF + tau], kc = rec[R_KCOEF + tau];
-      float v[4];
+      for (int q = 0; q < 2; ++q) {
+        fphT[q] = frag_tr_l(&st.phi[0][0], PD, 16 * kt, 32 * q, ln);
+        fqpT[q] = frag_tr_l(&sm.QpT[0][0], QP, 16 * qw, 32 * q, ln);
+        fzE[q] = frag_row_l(&sm.dZeT[0][0], PD, 16 * kt, 32 * q, ln);
+        fsE[q] = frag_row_l(&sm.dSeT[0][0], PD, 16 * kt, 32 * q, ln);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = ac * TS[r] - kc * TZ[r] - aq[r];
-      if constexpr (MAPE) {
-        v[0] *= poly_map_grad(__builtin_bit_cast(float, mq[0] << 16), g.map_deg);
-        v[1] *= poly_map_grad(__builtin_bit_cast(float, mq[0] & 0xffff0000u), g.map_deg);
-        v[2] *= poly_map_grad(__builtin_bit_cast(float, mq[1] << 16), g.map_deg);
-        v[3] *= poly_map_grad(__builtin_bit_cast(float, mq[1] & 0xffff0000u), g.map_deg);
-      }
-      u32x2v o;
-      o[0] = pack_bf16x2(v[0], v[1]);
-      o[1] = pack_bf16x2(v[2], v[3]);
-      bst8(rdq, (uint32_t)(((t0 + tau) * D + 16 * kt + 4 * gq) * 2), o);
-    }
-    // dphi tiles C[k][s] = Wz_end dZ_end^T delta - Ws_end dS_end^T delta - sum_tau psi Q' + S_ref^T dDelta
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      if (u < nt5) {
-        const int s0 = 16 * st5(u), s = s0 + m;
-        f32x4 a1 = zero4(), a2 = zero4(), a4 = zero4();
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const bf16x8 fb = frag_row_l(&sm.dl[0][0], PD, s0, 32 * q, ln);
-          a1 = mma_bf16(frag_row_l(&sm.dZeT[0][0], PD, 16 * kt, 32 * q, ln), fb, a1);
-          a2 = mma_bf16(frag_row_l(&sm.dSeT[0][0], PD, 16 * kt, 32 * q, ln), fb, a2);
-          a4 = mma_bf16(srefT_f[q], frag_row_l(&sm.dD[0][0], PD, s0, 32 * q, ln), a4);
+        for (int u = 0; u < 2; ++u) {
+          fdl[u][q] = frag_row_l(&sm.dl[0][0], PD, 16 * (qw + 2 * u), 32 * q, ln);
+          fdd[u][q] = frag_row_l(&sm.dD[0][0], PD, 16 * (qw + 2 * u), 32 * q, ln);
+          fddT[u][q] = frag_tr_l(&sm.dD[0][0], PD, 32 * qw + 16 * u, 32 * q, ln);
         }
-        const f32x4 a3 =
-            mma_bf16(frag_tr_l(&st.psi[0][0], PD, 16 * kt, 0, ln), frag_row_l(&sm.QpT[0][0], QP, s0, 0, ln), zero4());
+      }
+      const bf16x8 fpsT = frag_tr_l(&st.psi[0][0], PD, 16 * kt, 0, ln);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) fqp[u] = frag_row_l(&sm.QpT[0][0], QP, 16 * (qw + 2 * u), 0, ln);
+
+      f32x4 a7 = mma_bf16(fphT[0], fqpT[0], zero4());
+      a7 = mma_bf16(fphT[1], fqpT[1], a7);
+      f32x4 a1[2], a2[2], a3[2], a4[2], a6[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        a1[u] = mma_bf16(fzE[0], fdl[u][0], zero4());
+        a2[u] = mma_bf16(fsE[0], fdl[u][0], zero4());
+        a4[u] = mma_bf16(srefT_f[0], fdd[u][0], zero4());
+        a6[u] = mma_bf16(fddT[u][0], fphT[0], zero4());
+        a3[u] = mma_bf16(fpsT, fqp[u], zero4());
+        a1[u] = mma_bf16(fzE[1], fdl[u][1], a1[u]);
+        a2[u] = mma_bf16(fsE[1], fdl[u][1], a2[u]);
+        a4[u] = mma_bf16(srefT_f[1], fdd[u][1], a4[u]);
+        a6[u] = mma_bf16(fddT[u][1], fphT[1], a6[u]);
+      }
+
+      {   // dq
+        const int tau = 16 * qw + m;
+        const float ac = rec[R_ACOEF + tau], kc = rec[R_KCOEF + tau];
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = ac * TS[r] - kc * TZ[r] - a7[r];
+        if constexpr (MAPE) {
+          v[0] *= poly_map_grad(__builtin_bit_cast(float, mq[0] << 16), g.map_deg);
+          v[1] *= poly_map_grad(__builtin_bit_cast(float, mq[0] & 0xffff0000u), g.map_deg);
+          v[2] *= poly_map_grad(__builtin_bit_cast(float, mq[1] << 16), g.map_deg);
+          v[3] *= poly_map_grad(__builtin_bit_cast(float, mq[1] & 0xffff0000u), g.map_deg);
+        }
+        u32x2v o;
+        o[0] = pack_bf16x2(v[0], v[1]);
+        o[1] = pack_bf16x2(v[2], v[3]);
+        bst8(rdq, (uint32_t)(((t0 + tau) * D + 16 * kt + 4 * gq) * 2), o);
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {   // dk
+        const int s = 16 * (qw + 2 * u) + m;
         const float wz = rec[R_WZEND + s], ws = rec[R_WSEND + s];
         float val[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) val[r] = wz * a1[r] - ws * a2[r] - a3[r] + a4[r];
+        for (int r = 0; r < 4; ++r) val[r] = wz * a1[u][r] - ws * a2[u][r] - a3[u][r] + a4[u][r];
         route(s, 16 * kt + 4 * gq, 1, val, rdk, mk[u]);
       }
-    }
-    // dS_ref on the owned tiles: += sum_s dDelta[s][i] phi[s][k]
-    {
-      bf16x8 fb[2];
 #pragma unroll
-      for (int q = 0; q < 2; ++q) fb[q] = frag_tr_l(&st.phi[0][0], PD, 16 * kt, 32 * q, ln);
+      for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int q = 0; q < 2; ++q) acc = mma_bf16(frag_tr_l(&sm.dD[0][0], PD, 32 * qw + 16 * u, 32 * q, ln), fb[q], acc);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dsr[u][r] += acc[r];
-      }
+        for (int r = 0; r < 4; ++r) dsr[u][r] += a6[u][r];
     }
     // scalar-gradient record of the chunk (hS, hZ after phase B; fS, fZ, Grams after phase A)
-    if (tid < CH * (SPM - SP) / 4) {   // Lm columns past the sources
-      const int rr = tid / ((SPM - SP) / 4), cc = SP + 4 * (tid % ((SPM - SP) / 4));
-      *reinterpret_cast<float4*>(blk + SB::LM + rr * SPM + cc) = make_float4(0.f, 0.f, 0.f, 0.f);
-    } else if (tid >= 256 && tid < 256 + SPM) {
+    if (tid >= 256 && tid < 256 + SPM) {
       const int s = tid - 256;
       blk[SB::HS + s] = sm.hS[s];
       blk[SB::HZ + s] = sm.hZ[s];

@@ -175,6 +175,29 @@ __device__ __forceinline__ bf16x8 frag_tr_scaled_l(const bf16* p, int ld, int r0
   return r;
 }
 
+template <bool LO = true>
+__device__ __forceinline__ bf16x8 tr_pair_l(const bf16* p, int ld, int q, int col0, int l) {
+  const s16x4 a = tr4_l(p, ld, 32 * q, col0, l);
+  s16x4 b = s16x4{0, 0, 0, 0};
+  if constexpr (LO) b = tr4_l(p, ld, 32 * q + 16, col0, l);
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 v = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// Sum of x over the four 16-lane rows of the wave (lanes m, m + 16, m + 32, m + 48), returned in
+// every lane: two gfx950 cross-row swaps (v_permlane32_swap, v_permlane16_swap) on the VALU
+// instead of LDS-routed lane shuffles. Written as inline assembly because the compiler's
+// two-result builtins were seen to drop the second result when both operands hold the same value;
+// the leading s_nop covers the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ float xsum_rows(float x) {
+  float a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  float c = a + b, d = c;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(c), "+v"(d));
+  return c + d;
+}
+
 // Elementwise polynomial map on eight bf16 values held as a 16-byte vector.
 __device__ __forceinline__ u32x4v map_bf16x8(u32x4v v, int deg) {
   u32x4v r;
