@@ -4,15 +4,17 @@
 // adjoint aggregates, the segment scan, the scalar gradients (k_bwd_scalar), the fixup and the
 // dS_ref reduction are shared with the general path and see the same per-chunk records.
 // Chunks of 32 tokens, sources s = 0 .. 47 (the e - 1 <= 16 halo tokens, then the chunk),
-// processed last to first within a segment, with three workgroup barriers per chunk:
+// processed last to first within a segment in three phases, software-pipelined so that phase C of
+// chunk c+1 and phase A of chunk c share one barrier interval (two barriers per chunk):
 //   phase A  bf16 copies of the chunk-end adjoint for the matrix cores; delta = S_ref phi - v
 //            (-> LDS), K = psi phi^T (kept) and Q = Ws o K (-> LDS), the state term S_in^T dy of
 //            dpsi (kept), the Grams <dS_end, S_in> ..., and the chunk-start adjoint (the
 //            transposed chunk transition, in the owners' fp32 registers)
 //   phase B  P = dy delta^T, Q' = Ws o P (-> LDS) and Lm = K o P (scalar-gradient record);
 //            dDelta = Wz_end dZ_end phi - Ws_end dS_end phi - Q^T dy (-> LDS, dv) with hS, hZ
-//   phase C  dpsi (dq), dphi (dk), dS_ref += dDelta^T phi, the scalar records, staging of the
-//            previous chunk's inputs (double buffered)
+//   phase C  dpsi (dq), dphi (dk), dS_ref += dDelta^T phi, the scalar records
+// The inputs of chunk c-1 are staged (double buffered by chunk parity) during phase B of chunk c;
+// delta, the adjoint copies and the phase-A reductions are double buffered by chunk parity too.
 // The chunk-start states come from the forward walk in the fragment layout of walk_common.h and
 // feed the matrix cores without going through LDS.
 #include "mem_common.h"
@@ -50,22 +52,28 @@ struct Stage {
 };
 
 struct Smem {
-  Stage st[2];
-  alignas(16) bf16 dl[SPR][PD];    // delta[s][i]
-  alignas(16) bf16 dD[SPR][PD];    // dDelta[s][i]
-  alignas(16) bf16 QT[SPR][QP];    // Q^T[s][tau]
-  alignas(16) bf16 QpT[SPR][QP];   // Q'^T[s][tau]
-  alignas(16) bf16 dSeT[D][PD];    // chunk-end adjoint, transposed: dSeT[k][i] = dS_end[i][k]
-  alignas(16) bf16 dZeT[D][PD];
+  Stage st[2];                        // staged inputs, by chunk parity
+  alignas(16) bf16 dl[2][SPR][PD];    // delta[s][i], by chunk parity
+  alignas(16) bf16 dD[SPR][PD];       // dDelta[s][i]
+  alignas(16) bf16 QT[SPR][QP];       // Q^T[s][tau]
+  alignas(16) bf16 QpT[SPR][QP];      // Q'^T[s][tau]
+  alignas(16) bf16 dSeT[2][D][PD];    // chunk-end adjoint, transposed (dSeT[k][i] = dS_end[i][k]), by parity
+  alignas(16) bf16 dZeT[2][D][PD];
   alignas(16) float carry[2][HMAX][2 * D];   // halo partials (dv | dphi) handed to the previous chunk
-  float hS[SPM], hZ[SPM], fS[CH], fZ[CH];
-  float red[kSegWaves][4];
+  float hS[SPM], hZ[SPM];
+  float fS[2][CH], fZ[2][CH];         // by chunk parity
+  float red[2][kSegWaves][4];         // Gram partials, by chunk parity
 };
+static_assert(sizeof(Smem) <= 160 * 1024, "one workgroup per CU: at most 160 KB of LDS");
 
-struct Prefetch {
-  u32x4v phi, x;        // phi row vector (tid < 384); psi (tid < 256) or dy (tid >= 256) row vector
+// Register prefetch: the staged inputs (loaded one chunk ahead of their staging) and the operands
+// consumed from registers in phase A (v of the wave's delta tiles, the saved chunk-start states).
+struct StagePf {
+  u32x4v phi, x;        // phi row vector (tid < 384); psi (waves 0-3) or dy (waves 4-7) row vector
   u32x4v wsh, rec;
-  u32x2v v[2];          // v of this wave's delta tiles (8 bytes per lane)
+};
+struct RegPf {
+  u32x2v v[2];
   u32x4v sin[2], zin[2];   // chunk-start S, Z fragments (kt, q = 0, 1)
 };
 
@@ -123,23 +131,14 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
     o_v[u] = s < H + CH ? (uint32_t)((s - H) * (D * 2) + (16 * it1 + 4 * gq) * 2) : kOob;
   }
 
-  auto pf_load = [&](Prefetch& pf, int c) {
-    const int t0 = c * CH;
-    const uint32_t tb = (uint32_t)t0 * (D * 2);
+  auto sp_load = [&](StagePf& pf, int c) {
+    const uint32_t tb = (uint32_t)(c * CH) * (D * 2);
     pf.phi = bld16(rk, o_phi + tb);
     pf.x = bld16(w < 4 ? rq : rdy, o_x + tb);   // waves 0-3: psi rows, 4-7: dy rows
     pf.wsh = bld16(rwsh, o_wsh + (uint32_t)c * (CH * SPM * 2));
     pf.rec = bld16(rrec, o_rec + (uint32_t)c * (REC * 4));
-#pragma unroll
-    for (int u = 0; u < 2; ++u) pf.v[u] = bld8(rv, o_v[u] + tb);
-    const unsigned char* blk = states + (size_t)c * kStateBlk;
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      pf.sin[q] = *reinterpret_cast<const u32x4v*>(blk + frag_off(kt, q, lane));
-      pf.zin[q] = *reinterpret_cast<const u32x4v*>(blk + kStateBytes + frag_off(kt, q, lane));
-    }
   };
-  auto pf_store = [&](const Prefetch& pf, Stage& st) {
+  auto sp_store = [&](const StagePf& pf, Stage& st) {
     if (l_phi >= 0) {
       u32x4v x = pf.phi;
       if constexpr (MAPE) x = map_bf16x8(x, g.map_deg);
@@ -154,6 +153,17 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
     }
     if (l_wsh >= 0) *reinterpret_cast<u32x4v*>(&st.wsh[0][0] + l_wsh) = pf.wsh;
     if (tid < REC4) *reinterpret_cast<u32x4v*>(&st.rec[tid * 4]) = pf.rec;
+  };
+  auto rp_load = [&](RegPf& pf, int c) {
+    const uint32_t tb = (uint32_t)(c * CH) * (D * 2);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) pf.v[u] = bld8(rv, o_v[u] + tb);
+    const unsigned char* blk = states + (size_t)c * kStateBlk;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      pf.sin[q] = *reinterpret_cast<const u32x4v*>(blk + frag_off(kt, q, lane));
+      pf.zin[q] = *reinterpret_cast<const u32x4v*>(blk + kStateBytes + frag_off(kt, q, lane));
+    }
   };
 
   // ---- constants: S_ref rows 16 it1 (A operand of delta) and S_ref^T columns 16 kt (A of S_ref^T dDelta)
@@ -197,7 +207,8 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
     const int rr = SP + idx / PD, cc = idx % PD;
     sm.st[0].phi[rr][cc] = bf16(0.f);
     sm.st[1].phi[rr][cc] = bf16(0.f);
-    sm.dl[rr][cc] = bf16(0.f);
+    sm.dl[0][rr][cc] = bf16(0.f);
+    sm.dl[1][rr][cc] = bf16(0.f);
     sm.dD[rr][cc] = bf16(0.f);
   }
   for (int idx = tid; idx < (SPR - SP) * QP; idx += kSegThreads) {
@@ -212,78 +223,85 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
   }
   for (int idx = tid; idx < 2 * HMAX * 2 * D; idx += kSegThreads) (&sm.carry[0][0][0])[idx] = 0.f;
   if (tid < SPM) { sm.hS[tid] = 0.f; sm.hZ[tid] = 0.f; }
-  if (tid < CH) { sm.fS[tid] = 0.f; sm.fZ[tid] = 0.f; }
+  if (tid < CH) { sm.fS[0][tid] = 0.f; sm.fZ[0][tid] = 0.f; sm.fS[1][tid] = 0.f; sm.fZ[1][tid] = 0.f; }
 
-  // One register prefetch: the chunk's register operands (v, the saved states) are consumed in
-  // phase A, after which the previous chunk's loads are issued into the same registers and staged
-  // at the end of phase C.
-  Prefetch pf;
-  pf_load(pf, c_end - 1);
-  pf_store(pf, sm.st[0]);
-  __syncthreads();
+  // Per-chunk context: token range, halo routing.
+  struct Ctx {
+    int c, t0, t1, L, tail0;
+    bool first;
+    float* cur_carry;
+    const float* prev_carry;
+  };
+  auto ctx = [&](int c) {
+    Ctx x;
+    x.c = c;
+    x.t0 = c * CH;
+    x.t1 = min(g.T, x.t0 + CH);
+    x.L = x.t1 - x.t0;
+    x.tail0 = x.t1 - H;
+    x.first = c == c_begin;
+    x.cur_carry = &sm.carry[c & 1][0][0];
+    x.prev_carry = &sm.carry[(c + 1) & 1][0][0];
+    return x;
+  };
+  // Routes the (dv | dphi) values of source s, features f0 .. f0+3 (half 0: dv, 1: dphi): halo
+  // sources to the previous chunk's carry (or the segment's halo record), the chunk's last e-1
+  // tokens plus the next chunk's carry, the segment's last e-1 tokens to the tail record.
+  auto route = [&](const Ctx& x, int s, int f0, int half, float* val, const rsrc_t& dst, const u32x2v& raw) {
+    const int pp = x.t0 - H + s;
+    if (s >= H + x.L || pp < 0) return;
+    if (s < H) {
+      float* o = x.first ? p.halo_part + (((size_t)bh * sg.nseg + seg) * H + s) * (2 * D) : x.cur_carry + s * (2 * D);
+      *reinterpret_cast<float4*>(o + half * D + f0) = make_float4(val[0], val[1], val[2], val[3]);
+      return;
+    }
+    if (pp >= x.tail0) {
+      const float4 cv = *reinterpret_cast<const float4*>(x.prev_carry + (pp - x.tail0) * (2 * D) + half * D + f0);
+      val[0] += cv.x; val[1] += cv.y; val[2] += cv.z; val[3] += cv.w;
+    }
+    if (pp >= seg_tail0) {
+      float* o = p.tail_part + (((size_t)bh * sg.nseg + seg) * H + (pp - seg_tail0)) * (2 * D) + half * D + f0;
+      *reinterpret_cast<float4*>(o) = make_float4(val[0], val[1], val[2], val[3]);
+      return;
+    }
+    if constexpr (MAPE) {
+      if (half == 1) {
+        val[0] *= poly_map_grad(__builtin_bit_cast(float, raw[0] << 16), g.map_deg);
+        val[1] *= poly_map_grad(__builtin_bit_cast(float, raw[0] & 0xffff0000u), g.map_deg);
+        val[2] *= poly_map_grad(__builtin_bit_cast(float, raw[1] << 16), g.map_deg);
+        val[3] *= poly_map_grad(__builtin_bit_cast(float, raw[1] & 0xffff0000u), g.map_deg);
+      }
+    }
+    u32x2v o;
+    o[0] = pack_bf16x2(val[0], val[1]);
+    o[1] = pack_bf16x2(val[2], val[3]);
+    bst8(dst, (uint32_t)((pp * D + f0) * 2), o);
+  };
 
-  for (int c = c_end - 1; c >= c_begin; --c) {
-    // per-lane indices laundered once per chunk (see walk_common.h)
+  // values handed from phase A of a chunk to its phases B and C
+  f32x4 kmat = zero4(), TS = zero4(), TZ = zero4();
+  float wt[4] = {0.f, 0.f, 0.f, 0.f};
+  u32x2v mq = {0u, 0u}, mk[2] = {{0u, 0u}, {0u, 0u}};
+  StagePf sp;
+  RegPf rp;
+
+  // ================================ phase A ================================
+  // delta tiles C[i][s], K tile C[tau][s] (Q = Ws o K), the state term of dpsi C[k][tau] =
+  // sum_i S_in[i][k] dy[tau][i], the chunk transition terms, the Grams; operands first, then the
+  // matrix products, then the epilogues and LDS stores. Ends by loading the registers of chunk c-1.
+  auto phaseA = [&](int c) {
     const int ln = launder(lane);
     const int gq = ln >> 4, m = ln & 15;
-    const int b = (c_end - 1 - c) & 1;
-    const Stage& st = sm.st[b];
+    const Stage& st = sm.st[c & 1];
     const float* rec = st.rec;
-    const int t0 = c * CH, t1 = min(g.T, t0 + CH), L = t1 - t0;
-    const int tail0 = t1 - H;
-    const bool first = c == c_begin;
-    float* cur_carry = &sm.carry[c & 1][0][0];
-    const float* prev_carry = &sm.carry[(c + 1) & 1][0][0];
-
-    // Routes the (dv | dphi) values of source s, features f0 .. f0+3 (half 0: dv, 1: dphi): halo
-    // sources to the previous chunk's carry (or the segment's halo record), the chunk's last e-1
-    // tokens plus the next chunk's carry, the segment's last e-1 tokens to the tail record.
-    auto route = [&](int s, int f0, int half, float* val, const rsrc_t& dst, const u32x2v& raw) {
-      const int pp = t0 - H + s;
-      if (s >= H + L || pp < 0) return;
-      if (s < H) {
-        float* o = first ? p.halo_part + (((size_t)bh * sg.nseg + seg) * H + s) * (2 * D) : cur_carry + s * (2 * D);
-        *reinterpret_cast<float4*>(o + half * D + f0) = make_float4(val[0], val[1], val[2], val[3]);
-        return;
-      }
-      if (pp >= tail0) {
-        const float4 cv = *reinterpret_cast<const float4*>(prev_carry + (pp - tail0) * (2 * D) + half * D + f0);
-        val[0] += cv.x; val[1] += cv.y; val[2] += cv.z; val[3] += cv.w;
-      }
-      if (pp >= seg_tail0) {
-        float* o = p.tail_part + (((size_t)bh * sg.nseg + seg) * H + (pp - seg_tail0)) * (2 * D) + half * D + f0;
-        *reinterpret_cast<float4*>(o) = make_float4(val[0], val[1], val[2], val[3]);
-        return;
-      }
-      if constexpr (MAPE) {
-        if (half == 1) {
-          val[0] *= poly_map_grad(__builtin_bit_cast(float, raw[0] << 16), g.map_deg);
-          val[1] *= poly_map_grad(__builtin_bit_cast(float, raw[0] & 0xffff0000u), g.map_deg);
-          val[2] *= poly_map_grad(__builtin_bit_cast(float, raw[1] << 16), g.map_deg);
-          val[3] *= poly_map_grad(__builtin_bit_cast(float, raw[1] & 0xffff0000u), g.map_deg);
-        }
-      }
-      u32x2v o;
-      o[0] = pack_bf16x2(val[0], val[1]);
-      o[1] = pack_bf16x2(val[2], val[3]);
-      bst8(dst, (uint32_t)((pp * D + f0) * 2), o);
-    };
-
-    // raw q, k of this lane's dq / dk elements for the map derivative (elementwise map only)
-    u32x2v mq = {0u, 0u}, mk[2] = {{0u, 0u}, {0u, 0u}};
-    if constexpr (MAPE) {
+    const int t0 = c * CH;
+    if constexpr (MAPE) {   // raw q, k of this lane's dq / dk elements for the map derivative
       mq = bld8(rq, (uint32_t)((t0 + 16 * qw + m) * (D * 2) + (16 * kt + 4 * gq) * 2));
 #pragma unroll
       for (int u = 0; u < 2; ++u)
         mk[u] = bld8(rk, (uint32_t)((t0 - H + 16 * (qw + 2 * u) + m) * (D * 2) + (16 * kt + 4 * gq) * 2));
     }
-
-    // ================================ phase A ================================
-    // delta tiles C[i][s], K tile C[tau][s] (Q = Ws o K), the state term of dpsi C[k][tau] =
-    // sum_i S_in[i][k] dy[tau][i], the chunk transition terms, the Grams; operands first, then the
-    // matrix products, then the epilogues and LDS stores.
-    f32x4 dl_acc[2], kmat, TS, TZ, xa[2], xk[2];
-    float wt[4];
+    f32x4 dl_acc[2], xa[2], xk[2];
     {
       bf16x8 fphi[2][2], fpk[2], fps[2], fdy[2];
 #pragma unroll
@@ -318,21 +336,21 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
       }
       kmat = mma_bf16(fps[0], fpk[0], zero4());
       kmat = mma_bf16(fps[1], fpk[1], kmat);
-      TS = mma_bf16(__builtin_bit_cast(bf16x8, pf.sin[0]), fdy[0], zero4());
-      TZ = mma_bf16(__builtin_bit_cast(bf16x8, pf.zin[0]), fdy[0], zero4());
-      TS = mma_bf16(__builtin_bit_cast(bf16x8, pf.sin[1]), fdy[1], TS);
-      TZ = mma_bf16(__builtin_bit_cast(bf16x8, pf.zin[1]), fdy[1], TZ);
+      TS = mma_bf16(__builtin_bit_cast(bf16x8, rp.sin[0]), fdy[0], zero4());
+      TZ = mma_bf16(__builtin_bit_cast(bf16x8, rp.zin[0]), fdy[0], zero4());
+      TS = mma_bf16(__builtin_bit_cast(bf16x8, rp.sin[1]), fdy[1], TS);
+      TZ = mma_bf16(__builtin_bit_cast(bf16x8, rp.zin[1]), fdy[1], TZ);
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         xa[u] = mma_bf16(fya[u], fpsiT, zero4());
         xk[u] = mma_bf16(fyk[u], fpsiT, zero4());
       }
     }
-    {   // delta = acc - v -> LDS
+    {   // delta = acc - v -> LDS; Q -> LDS
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const u32x2v vv = pf.v[u];
-        store4<bf16>(&sm.dl[16 * (s1a + 2 * u) + m][16 * it1 + 4 * gq],
+        const u32x2v vv = rp.v[u];
+        store4<bf16>(&sm.dl[c & 1][16 * (s1a + 2 * u) + m][16 * it1 + 4 * gq],
                      dl_acc[u][0] - __builtin_bit_cast(float, vv[0] << 16),
                      dl_acc[u][1] - __builtin_bit_cast(float, vv[0] & 0xffff0000u),
                      dl_acc[u][2] - __builtin_bit_cast(float, vv[1] << 16),
@@ -346,12 +364,12 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
       const float4 ps = lds_bf16x4(&st.psi[tau][16 * kt + 4 * gq]);
       const float fs = xsum_rows(TS[0] * ps.x + TS[1] * ps.y + TS[2] * ps.z + TS[3] * ps.w);
       const float fz = xsum_rows(TZ[0] * ps.x + TZ[1] * ps.y + TZ[2] * ps.z + TZ[3] * ps.w);
-      if (gq == 0) { atomicAdd(&sm.fS[tau], fs); atomicAdd(&sm.fZ[tau], fz); }
+      if (gq == 0) { atomicAdd(&sm.fS[c & 1][tau], fs); atomicAdd(&sm.fZ[c & 1][tau], fz); }
     }
     {   // Grams <dS_end, S_in>, <dS_end, Z_in>, <dZ_end, Z_in> (fragment (kt, qw) holds the owned elements;
         // selects, not a runtime index, so that the prefetch registers stay registers)
-      const bf16x8 fs = __builtin_bit_cast(bf16x8, qw ? pf.sin[1] : pf.sin[0]);
-      const bf16x8 fz = __builtin_bit_cast(bf16x8, qw ? pf.zin[1] : pf.zin[0]);
+      const bf16x8 fs = __builtin_bit_cast(bf16x8, qw ? rp.sin[1] : rp.sin[0]);
+      const bf16x8 fz = __builtin_bit_cast(bf16x8, qw ? rp.zin[1] : rp.zin[0]);
       float gss = 0.f, gsz = 0.f, gzz = 0.f;
 #pragma unroll
       for (int u = 0; u < 2; ++u)
@@ -361,7 +379,7 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
           gss += dS[u][r] * sv; gsz += dS[u][r] * zv; gzz += dZ[u][r] * zv;
         }
       gss = xsum_rows(row_sum16(gss)); gsz = xsum_rows(row_sum16(gsz)); gzz = xsum_rows(row_sum16(gzz));
-      if (ln == 0) { sm.red[w][0] = gss; sm.red[w][1] = gsz; sm.red[w][2] = gzz; }
+      if (ln == 0) { sm.red[c & 1][w][0] = gss; sm.red[c & 1][w][1] = gsz; sm.red[c & 1][w][2] = gzz; }
     }
     {   // the chunk-end adjoint's bf16 copies (read by phases B, C), then the chunk-start adjoint:
         //   dS_in = a dS_end + sum_t a_{t-1} dy_t psi_t^T,  dZ_in = b dZ_end - kappa dS_end - sum_t kappa_{t-1} dy_t psi_t^T
@@ -369,8 +387,8 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int i0 = 32 * qw + 16 * u + 4 * gq;
-        store4<bf16>(&sm.dSeT[16 * kt + m][i0], dS[u][0], dS[u][1], dS[u][2], dS[u][3]);
-        store4<bf16>(&sm.dZeT[16 * kt + m][i0], dZ[u][0], dZ[u][1], dZ[u][2], dZ[u][3]);
+        store4<bf16>(&sm.dSeT[c & 1][16 * kt + m][i0], dS[u][0], dS[u][1], dS[u][2], dS[u][3]);
+        store4<bf16>(&sm.dZeT[c & 1][16 * kt + m][i0], dZ[u][0], dZ[u][1], dZ[u][2], dZ[u][3]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float lam = ae * dS[u][r] + xa[u][r];
@@ -390,140 +408,150 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
           }
       }
     }
-    // the register operands of this chunk are consumed: start loading the previous chunk
-    if (c - 1 >= c_begin) pf_load(pf, c - 1);
-    __syncthreads();
+    // this chunk's register operands are consumed: load the previous chunk's
+    if (c - 1 >= c_begin) rp_load(rp, c - 1);
+  };
 
-    // ================================ phase B ================================
-    // P tile C[tau][s] = dy delta^T (Lm = K o P, Q' = Ws o P); dDelta tiles C[i][s] =
-    // Wz_end dZ_end phi - Ws_end dS_end phi - sum_tau dy Q (hS, hZ, dv)
+  // ================================ phase B ================================
+  // P tile C[tau][s] = dy delta^T (Lm = K o P, Q' = Ws o P); dDelta tiles C[i][s] =
+  // Wz_end dZ_end phi - Ws_end dS_end phi - sum_tau dy Q (hS, hZ, dv)
+  auto phaseB = [&](int c) {
+    const int ln = launder(lane);
+    const int gq = ln >> 4, m = ln & 15;
+    const Stage& st = sm.st[c & 1];
+    const float* rec = st.rec;
+    const Ctx x = ctx(c);
     float* blk = p.scal + ((size_t)bh * g.nc + c) * SB::SIZE;
-    {
-      bf16x8 fy[2], fd[2], fp[2][2], fsT[2], fzT[2], fq[2];
+    bf16x8 fy[2], fd[2], fp[2][2], fsT[2], fzT[2], fq[2];
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        fy[q] = frag_row_l(&st.dy[0][0], PD, 16 * tt, 32 * q, ln);
-        fd[q] = frag_row_l(&sm.dl[0][0], PD, 16 * stm, 32 * q, ln);
-        fsT[q] = frag_tr_l(&sm.dSeT[0][0], PD, 16 * it1, 32 * q, ln);
-        fzT[q] = frag_tr_l(&sm.dZeT[0][0], PD, 16 * it1, 32 * q, ln);
+    for (int q = 0; q < 2; ++q) {
+      fy[q] = frag_row_l(&st.dy[0][0], PD, 16 * tt, 32 * q, ln);
+      fd[q] = frag_row_l(&sm.dl[c & 1][0][0], PD, 16 * stm, 32 * q, ln);
+      fsT[q] = frag_tr_l(&sm.dSeT[c & 1][0][0], PD, 16 * it1, 32 * q, ln);
+      fzT[q] = frag_tr_l(&sm.dZeT[c & 1][0][0], PD, 16 * it1, 32 * q, ln);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) fp[u][q] = frag_row_l(&st.phi[0][0], PD, 16 * (s1a + 2 * u), 32 * q, ln);
-      }
-      const bf16x8 fyT = frag_tr_l(&st.dy[0][0], PD, 16 * it1, 0, ln);
+      for (int u = 0; u < 2; ++u) fp[u][q] = frag_row_l(&st.phi[0][0], PD, 16 * (s1a + 2 * u), 32 * q, ln);
+    }
+    const bf16x8 fyT = frag_tr_l(&st.dy[0][0], PD, 16 * it1, 0, ln);
 #pragma unroll
-      for (int u = 0; u < 2; ++u) fq[u] = frag_row_l(&sm.QT[0][0], QP, 16 * (s1a + 2 * u), 0, ln);
-      float4 dlv[2];
+    for (int u = 0; u < 2; ++u) fq[u] = frag_row_l(&sm.QT[0][0], QP, 16 * (s1a + 2 * u), 0, ln);
+    float4 dlv[2];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) dlv[u] = lds_bf16x4(&sm.dl[16 * (s1a + 2 * u) + m][16 * it1 + 4 * gq]);
+    for (int u = 0; u < 2; ++u) dlv[u] = lds_bf16x4(&sm.dl[c & 1][16 * (s1a + 2 * u) + m][16 * it1 + 4 * gq]);
 
-      f32x4 pm = mma_bf16(fy[0], fd[0], zero4());
-      pm = mma_bf16(fy[1], fd[1], pm);
-      f32x4 as[2], az[2], aq[2];
+    f32x4 pm = mma_bf16(fy[0], fd[0], zero4());
+    pm = mma_bf16(fy[1], fd[1], pm);
+    f32x4 as[2], az[2], aq[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      as[u] = mma_bf16(fsT[0], fp[u][0], zero4());
+      az[u] = mma_bf16(fzT[0], fp[u][0], zero4());
+      aq[u] = mma_bf16(fyT, fq[u], zero4());
+      as[u] = mma_bf16(fsT[1], fp[u][1], as[u]);
+      az[u] = mma_bf16(fzT[1], fp[u][1], az[u]);
+    }
+
+#pragma unroll
+    for (int r = 0; r < 4; ++r) blk[SB::LM + (16 * tt + 4 * gq + r) * SPM + 16 * stm + m] = kmat[r] * pm[r];
+    store4<bf16>(&sm.QpT[16 * stm + m][16 * tt + 4 * gq], wt[0] * pm[0], wt[1] * pm[1], wt[2] * pm[2], wt[3] * pm[3]);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int s = 16 * (s1a + 2 * u) + m, i0 = 16 * it1 + 4 * gq;
+      const float wz = rec[R_WZEND + s], ws = rec[R_WSEND + s];
+      const float dlr[4] = {dlv[u].x, dlv[u].y, dlv[u].z, dlv[u].w};
+      float dd[4], hs = 0.f, hz = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        dd[r] = wz * az[u][r] - ws * as[u][r] - aq[u][r];
+        hs += dlr[r] * as[u][r];
+        hz += dlr[r] * az[u][r];
+      }
+      hs = xsum_rows(hs);
+      hz = xsum_rows(hz);
+      if (gq == 0) { atomicAdd(&sm.hS[s], hs); atomicAdd(&sm.hZ[s], hz); }
+      store4<bf16>(&sm.dD[s][i0], dd[0], dd[1], dd[2], dd[3]);
+      float val[4] = {-dd[0], -dd[1], -dd[2], -dd[3]};
+      route(x, s, i0, 0, val, rdv, u32x2v{0u, 0u});
+    }
+  };
+
+  // ================================ phase C ================================
+  // dpsi tile C[k][tau] = a_{tau-1} S_in^T dy - kappa_{tau-1} Z_in^T dy - sum_s phi_s Q'[tau][s];
+  // dphi tiles C[k][s] = Wz_end dZ_end^T delta - Ws_end dS_end^T delta - sum_tau psi Q' + S_ref^T dDelta;
+  // dS_ref += dDelta^T phi on the owned tiles; the chunk's scalar-gradient record
+  auto phaseC = [&](int c) {
+    const int ln = launder(lane);
+    const int gq = ln >> 4, m = ln & 15;
+    const Stage& st = sm.st[c & 1];
+    const float* rec = st.rec;
+    const Ctx x = ctx(c);
+    bf16x8 fphT[2], fqpT[2], fdl[2][2], fzE[2], fsE[2], fdd[2][2], fqp[2], fddT[2][2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      fphT[q] = frag_tr_l(&st.phi[0][0], PD, 16 * kt, 32 * q, ln);
+      fqpT[q] = frag_tr_l(&sm.QpT[0][0], QP, 16 * qw, 32 * q, ln);
+      fzE[q] = frag_row_l(&sm.dZeT[c & 1][0][0], PD, 16 * kt, 32 * q, ln);
+      fsE[q] = frag_row_l(&sm.dSeT[c & 1][0][0], PD, 16 * kt, 32 * q, ln);
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        as[u] = mma_bf16(fsT[0], fp[u][0], zero4());
-        az[u] = mma_bf16(fzT[0], fp[u][0], zero4());
-        aq[u] = mma_bf16(fyT, fq[u], zero4());
-        as[u] = mma_bf16(fsT[1], fp[u][1], as[u]);
-        az[u] = mma_bf16(fzT[1], fp[u][1], az[u]);
-      }
-
-#pragma unroll
-      for (int r = 0; r < 4; ++r) blk[SB::LM + (16 * tt + 4 * gq + r) * SPM + 16 * stm + m] = kmat[r] * pm[r];
-      store4<bf16>(&sm.QpT[16 * stm + m][16 * tt + 4 * gq], wt[0] * pm[0], wt[1] * pm[1], wt[2] * pm[2], wt[3] * pm[3]);
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int s = 16 * (s1a + 2 * u) + m, i0 = 16 * it1 + 4 * gq;
-        const float wz = rec[R_WZEND + s], ws = rec[R_WSEND + s];
-        const float dlr[4] = {dlv[u].x, dlv[u].y, dlv[u].z, dlv[u].w};
-        float dd[4], hs = 0.f, hz = 0.f;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          dd[r] = wz * az[u][r] - ws * as[u][r] - aq[u][r];
-          hs += dlr[r] * as[u][r];
-          hz += dlr[r] * az[u][r];
-        }
-        hs = xsum_rows(hs);
-        hz = xsum_rows(hz);
-        if (gq == 0) { atomicAdd(&sm.hS[s], hs); atomicAdd(&sm.hZ[s], hz); }
-        store4<bf16>(&sm.dD[s][i0], dd[0], dd[1], dd[2], dd[3]);
-        float val[4] = {-dd[0], -dd[1], -dd[2], -dd[3]};
-        route(s, i0, 0, val, rdv, u32x2v{0u, 0u});
+        fdl[u][q] = frag_row_l(&sm.dl[c & 1][0][0], PD, 16 * (qw + 2 * u), 32 * q, ln);
+        fdd[u][q] = frag_row_l(&sm.dD[0][0], PD, 16 * (qw + 2 * u), 32 * q, ln);
+        fddT[u][q] = frag_tr_l(&sm.dD[0][0], PD, 32 * qw + 16 * u, 32 * q, ln);
       }
     }
-    __syncthreads();
+    const bf16x8 fpsT = frag_tr_l(&st.psi[0][0], PD, 16 * kt, 0, ln);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) fqp[u] = frag_row_l(&sm.QpT[0][0], QP, 16 * (qw + 2 * u), 0, ln);
 
-    // ================================ phase C ================================
-    // dpsi tile C[k][tau] = a_{tau-1} S_in^T dy - kappa_{tau-1} Z_in^T dy - sum_s phi_s Q'[tau][s];
-    // dphi tiles C[k][s] = Wz_end dZ_end^T delta - Ws_end dS_end^T delta - sum_tau psi Q' + S_ref^T dDelta;
-    // dS_ref += dDelta^T phi on the owned tiles
-    {
-      bf16x8 fphT[2], fqpT[2], fdl[2][2], fzE[2], fsE[2], fdd[2][2], fqp[2], fddT[2][2];
+    f32x4 a7 = mma_bf16(fphT[0], fqpT[0], zero4());
+    a7 = mma_bf16(fphT[1], fqpT[1], a7);
+    f32x4 a1[2], a2[2], a3[2], a4[2], a6[2];
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        fphT[q] = frag_tr_l(&st.phi[0][0], PD, 16 * kt, 32 * q, ln);
-        fqpT[q] = frag_tr_l(&sm.QpT[0][0], QP, 16 * qw, 32 * q, ln);
-        fzE[q] = frag_row_l(&sm.dZeT[0][0], PD, 16 * kt, 32 * q, ln);
-        fsE[q] = frag_row_l(&sm.dSeT[0][0], PD, 16 * kt, 32 * q, ln);
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          fdl[u][q] = frag_row_l(&sm.dl[0][0], PD, 16 * (qw + 2 * u), 32 * q, ln);
-          fdd[u][q] = frag_row_l(&sm.dD[0][0], PD, 16 * (qw + 2 * u), 32 * q, ln);
-          fddT[u][q] = frag_tr_l(&sm.dD[0][0], PD, 32 * qw + 16 * u, 32 * q, ln);
-        }
-      }
-      const bf16x8 fpsT = frag_tr_l(&st.psi[0][0], PD, 16 * kt, 0, ln);
-#pragma unroll
-      for (int u = 0; u < 2; ++u) fqp[u] = frag_row_l(&sm.QpT[0][0], QP, 16 * (qw + 2 * u), 0, ln);
-
-      f32x4 a7 = mma_bf16(fphT[0], fqpT[0], zero4());
-      a7 = mma_bf16(fphT[1], fqpT[1], a7);
-      f32x4 a1[2], a2[2], a3[2], a4[2], a6[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        a1[u] = mma_bf16(fzE[0], fdl[u][0], zero4());
-        a2[u] = mma_bf16(fsE[0], fdl[u][0], zero4());
-        a4[u] = mma_bf16(srefT_f[0], fdd[u][0], zero4());
-        a6[u] = mma_bf16(fddT[u][0], fphT[0], zero4());
-        a3[u] = mma_bf16(fpsT, fqp[u], zero4());
-        a1[u] = mma_bf16(fzE[1], fdl[u][1], a1[u]);
-        a2[u] = mma_bf16(fsE[1], fdl[u][1], a2[u]);
-        a4[u] = mma_bf16(srefT_f[1], fdd[u][1], a4[u]);
-        a6[u] = mma_bf16(fddT[u][1], fphT[1], a6[u]);
-      }
-
-      {   // dq
-        const int tau = 16 * qw + m;
-        const float ac = rec[R_ACOEF + tau], kc = rec[R_KCOEF + tau];
-        float v[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = ac * TS[r] - kc * TZ[r] - a7[r];
-        if constexpr (MAPE) {
-          v[0] *= poly_map_grad(__builtin_bit_cast(float, mq[0] << 16), g.map_deg);
-          v[1] *= poly_map_grad(__builtin_bit_cast(float, mq[0] & 0xffff0000u), g.map_deg);
-          v[2] *= poly_map_grad(__builtin_bit_cast(float, mq[1] << 16), g.map_deg);
-          v[3] *= poly_map_grad(__builtin_bit_cast(float, mq[1] & 0xffff0000u), g.map_deg);
-        }
-        u32x2v o;
-        o[0] = pack_bf16x2(v[0], v[1]);
-        o[1] = pack_bf16x2(v[2], v[3]);
-        bst8(rdq, (uint32_t)(((t0 + tau) * D + 16 * kt + 4 * gq) * 2), o);
-      }
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {   // dk
-        const int s = 16 * (qw + 2 * u) + m;
-        const float wz = rec[R_WZEND + s], ws = rec[R_WSEND + s];
-        float val[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) val[r] = wz * a1[u][r] - ws * a2[u][r] - a3[u][r] + a4[u][r];
-        route(s, 16 * kt + 4 * gq, 1, val, rdk, mk[u]);
-      }
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dsr[u][r] += a6[u][r];
+    for (int u = 0; u < 2; ++u) {
+      a1[u] = mma_bf16(fzE[0], fdl[u][0], zero4());
+      a2[u] = mma_bf16(fsE[0], fdl[u][0], zero4());
+      a4[u] = mma_bf16(srefT_f[0], fdd[u][0], zero4());
+      a6[u] = mma_bf16(fddT[u][0], fphT[0], zero4());
+      a3[u] = mma_bf16(fpsT, fqp[u], zero4());
+      a1[u] = mma_bf16(fzE[1], fdl[u][1], a1[u]);
+      a2[u] = mma_bf16(fsE[1], fdl[u][1], a2[u]);
+      a4[u] = mma_bf16(srefT_f[1], fdd[u][1], a4[u]);
+      a6[u] = mma_bf16(fddT[u][1], fphT[1], a6[u]);
     }
+
+    {   // dq
+      const int tau = 16 * qw + m;
+      const float ac = rec[R_ACOEF + tau], kc = rec[R_KCOEF + tau];
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = ac * TS[r] - kc * TZ[r] - a7[r];
+      if constexpr (MAPE) {
+        v[0] *= poly_map_grad(__builtin_bit_cast(float, mq[0] << 16), g.map_deg);
+        v[1] *= poly_map_grad(__builtin_bit_cast(float, mq[0] & 0xffff0000u), g.map_deg);
+        v[2] *= poly_map_grad(__builtin_bit_cast(float, mq[1] << 16), g.map_deg);
+        v[3] *= poly_map_grad(__builtin_bit_cast(float, mq[1] & 0xffff0000u), g.map_deg);
+      }
+      u32x2v o;
+      o[0] = pack_bf16x2(v[0], v[1]);
+      o[1] = pack_bf16x2(v[2], v[3]);
+      bst8(rdq, (uint32_t)(((x.t0 + tau) * D + 16 * kt + 4 * gq) * 2), o);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {   // dk
+      const int s = 16 * (qw + 2 * u) + m;
+      const float wz = rec[R_WZEND + s], ws = rec[R_WSEND + s];
+      float val[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) val[r] = wz * a1[u][r] - ws * a2[u][r] - a3[u][r] + a4[u][r];
+      route(x, s, 16 * kt + 4 * gq, 1, val, rdk, mk[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dsr[u][r] += a6[u][r];
+
     // scalar-gradient record of the chunk (hS, hZ after phase B; fS, fZ, Grams after phase A)
+    float* blk = p.scal + ((size_t)bh * g.nc + c) * SB::SIZE;
     if (tid >= 256 && tid < 256 + SPM) {
       const int s = tid - 256;
       blk[SB::HS + s] = sm.hS[s];
@@ -532,23 +560,48 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
       sm.hZ[s] = 0.f;
     } else if (tid >= 384 && tid < 384 + CH) {
       const int t = tid - 384;
-      blk[SB::FS + t] = sm.fS[t];
-      blk[SB::FZ + t] = sm.fZ[t];
-      sm.fS[t] = 0.f;
-      sm.fZ[t] = 0.f;
+      blk[SB::FS + t] = sm.fS[c & 1][t];
+      blk[SB::FZ + t] = sm.fZ[c & 1][t];
+      sm.fS[c & 1][t] = 0.f;
+      sm.fZ[c & 1][t] = 0.f;
     } else if (tid >= 448 && tid < 452) {
       const int j = tid - 448;
       float sum = 0.f;
       if (j < 3) {
 #pragma unroll
-        for (int ww = 0; ww < kSegWaves; ++ww) sum += sm.red[ww][j];
+        for (int ww = 0; ww < kSegWaves; ++ww) sum += sm.red[c & 1][ww][j];
       }
       blk[SB::GRAM + j] = sum;
     }
-    // stage the previous chunk (its loads were issued at the end of phase A)
-    if (c - 1 >= c_begin) pf_store(pf, sm.st[b ^ 1]);
+  };
+
+  // ---- software pipeline over the chunks (last to first), two barriers per chunk:
+  //   [phase C of chunk c+1 | phase A of chunk c] -> [phase B of chunk c | staging of chunk c-1]
+  sp_load(sp, c_end - 1);
+  sp_store(sp, sm.st[(c_end - 1) & 1]);
+  if (c_end - 2 >= c_begin) sp_load(sp, c_end - 2);
+  rp_load(rp, c_end - 1);
+  __syncthreads();
+  phaseA(c_end - 1);
+  __syncthreads();
+  phaseB(c_end - 1);
+  if (c_end - 2 >= c_begin) {
+    sp_store(sp, sm.st[(c_end - 2) & 1]);
+    if (c_end - 3 >= c_begin) sp_load(sp, c_end - 3);
+  }
+  __syncthreads();
+  for (int c = c_end - 2; c >= c_begin; --c) {
+    phaseC(c + 1);
+    phaseA(c);
+    __syncthreads();
+    phaseB(c);
+    if (c - 1 >= c_begin) {
+      sp_store(sp, sm.st[(c - 1) & 1]);
+      if (c - 2 >= c_begin) sp_load(sp, c - 2);
+    }
     __syncthreads();
   }
+  phaseC(c_begin);
 
   // ---- segment output: dS_ref partial
   float* dst = p.dsref_part + ((size_t)bh * sg.nseg + seg) * DD;
