@@ -920,6 +920,7 @@ size_t bwd_seg_smem_bytes(int H) {
 
 hipError_t launch_walk_bwd_kernel(const Geom& g, const BwdPtrs<bf16>& a, const SegGeom& sg, const BwdSegPtrs& p,
                                   hipStream_t stream);
+hipError_t launch_scalar_chain(const Geom& g, const BwdPtrs<bf16>& a, const BwdSegPtrs& p, hipStream_t stream);
 
 // walk: run the specialised reverse walk (walk_bwd.hip, bf16 with d = 64 only) in place of k_bwd_seg
 template <typename T, int CH, int D>
@@ -961,7 +962,15 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
     prof_end(KID_BWD_CHUNK, stream);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
-  if ((err = launch_bwd_scalar<T, CH>(g, a, p, stream)) != hipSuccess) return err;
+  if constexpr (sizeof(T) == 2 && CH == 32 && D == 64) {
+    if (walk) {
+      prof_begin(KID_BWD_SCALAR, stream);
+      err = launch_scalar_chain(g, a, p, stream);
+      prof_end(KID_BWD_SCALAR, stream);
+      if (err != hipSuccess) return err;
+    }
+  }
+  if (!walk && (err = launch_bwd_scalar<T, CH>(g, a, p, stream)) != hipSuccess) return err;
   prof_begin(KID_BWD_FIXUP, stream);
   hipLaunchKernelGGL((k_bwd_seg_fixup<T, D>), dim3(sg.nseg, g.BH), dim3(kThreads), 0, stream, g, a, sg, p);
   prof_end(KID_BWD_FIXUP, stream);

@@ -631,4 +631,200 @@ hipError_t launch_walk_bwd_kernel(const Geom& g, const BwdPtrs<bf16>& a, const S
   return hipGetLastError();
 }
 
+
+
+// ---------------------------------------------------------------------------------------------
+// Scalar gradients of the specialised path, one wave per 32-token chunk (two chunks per
+// workgroup), as the reverse-mode form of the chunk's coefficient recurrences. Lane s < 48 owns
+// source s and runs
+//   forward   Wz_t = beta_t Wz_{t-1} + w(s, t),   Ws_t = alpha_t Ws_{t-1} + eta_t Wz_t
+//   reverse   gWs_t = G_t + alpha_{t+1} gWs_{t+1},  gWz_t = Hz_t + eta_t gWs_t + beta_{t+1} gWz_{t+1}
+// with the direct terms G_t = -Lm[t+1][s] (t < 31), G_31 = -hS[s], Hz_31 = hZ[s] from the walk's
+// record; lane 48 runs the same pair for the chunk prefix (a_t, kappa_t, b_t) with the direct
+// terms fS, fZ and the Grams. Per step the lanes contribute
+//   dalpha_t += gWs_t Ws_{t-1},  deta_t += gWs_t Wz_t,  dbeta_t += gWz_t Wz_{t-1},  dw(s, t) = gWz_t
+// (prefix lane: dalpha_t += ga_t a_{t-1} + gkappa_t kappa_{t-1}, deta_t += gkappa_t b_t,
+// dbeta_t += gb_t b_{t-1}); the sums over the lanes go through LDS. The step scalars are the same
+// for every lane and are broadcast from lane t with v_readlane; all arithmetic is fp32.
+// ---------------------------------------------------------------------------------------------
+namespace wb {
+constexpr int kChainWaves = 2;
+constexpr int NSRC = SP;          // 48 source lanes; lane NSRC runs the prefix chain
+constexpr int RP = CH + 1;        // pitch of the window-weight rows
+constexpr int LP = 52;            // pitch of the contribution rows (49 lanes, 16-byte aligned)
+struct ChainSmem {   // static LDS: kChainWaves * 19.5 KB
+  union {
+    float W[NSRC][RP];            // window weights w(s, t) of the sources
+    alignas(16) float red[3][CH][LP];   // contributions (alpha, eta, beta) of step t from lane l at [t][l]
+  } u[kChainWaves];
+};
+}  // namespace wb
+
+__global__ __launch_bounds__(64 * wb::kChainWaves) void k_scalar_chain(const Geom g, const BwdPtrs<bf16> a,
+                                                                         const BwdSegPtrs p) {
+  using namespace wb;
+  __shared__ ChainSmem smc;
+  const int lane = lane_id();
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = blockIdx.x * kChainWaves + wv, bh = blockIdx.y;
+  if (c >= g.nc) return;   // wave-uniform: no barriers below
+  const int H = g.H, e = g.e;
+  const int t0 = c * CH, L = min(g.T, t0 + CH) - t0;
+  const size_t tb = (size_t)bh * g.T;
+  const float* blk = p.scal + ((size_t)bh * g.nc + c) * SB::SIZE;
+  auto& U = smc.u[wv];
+
+  // step scalars in lane t (padded steps: alpha = beta = 1, eta = 0; beta = 0 without momentum)
+  float al = 1.f, et = 0.f, be = 1.f;
+  if (lane < L) {
+    al = to_f32(a.decay[tb + t0 + lane]);
+    et = to_f32(a.lr[tb + t0 + lane]);
+    be = g.momentum ? to_f32(a.beta[tb + t0 + lane]) : 0.f;
+  }
+  // direct terms of this lane: Lm[t + 1][s] (source lanes), fS / fZ (prefix lane)
+  float dcol[CH];
+#pragma unroll
+  for (int t = 0; t < CH - 1; ++t) {
+    const int col = lane < NSRC ? lane : 0;
+    const float lm = blk[SB::LM + (t + 1) * SPM + col];
+    const float fs = blk[SB::FS + t + 1];
+    dcol[t] = lane < NSRC ? -lm : fs;
+  }
+  float fzc[CH];
+#pragma unroll
+  for (int t = 0; t < CH - 1; ++t) fzc[t] = -blk[SB::FZ + t + 1];
+  fzc[CH - 1] = 0.f;
+  const float hs = lane < NSRC ? blk[SB::HS + lane] : 0.f, hz = lane < NSRC ? blk[SB::HZ + lane] : 0.f;
+  const float gss = blk[SB::GRAM], gsz = blk[SB::GRAM + 1], gzz = blk[SB::GRAM + 2];
+
+  // window weights of the sources: W[s][t] = w(s, t) for j = t + H - s in [0, e)
+  for (int idx = lane; idx < NSRC * RP; idx += 64) (&U.W[0][0])[idx] = 0.f;
+  __builtin_amdgcn_wave_barrier();
+  if (g.gate_mode != GATE_NONE) {
+    for (int idx = lane; idx < CH * e; idx += 64) {
+      const int t = idx / e, j = idx % e, s = t + H - j;
+      float wgt = 0.f;
+      if (t < L) {
+        if (g.gate_mode == GATE_LAG) wgt = to_f32(a.gate[(tb + t0 + t) * e + j]);
+        else {
+          const int ps = t0 + t - j;   // source token
+          wgt = ps >= 0 ? to_f32(a.gate[tb + ps]) : 0.f;
+        }
+      }
+      if (s >= 0 && s < NSRC) U.W[s][t] = wgt;
+    }
+  } else {
+    for (int idx = lane; idx < CH * e; idx += 64) {
+      const int t = idx / e, j = idx % e, s = t + H - j;
+      if (s >= 0 && s < NSRC) U.W[s][t] = t < L ? 1.f : 0.f;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  float wrow[CH];
+  {
+    const int row = lane < NSRC ? lane : 0;
+#pragma unroll
+    for (int t = 0; t < CH; ++t) wrow[t] = lane < NSRC ? U.W[row][t] : 0.f;
+  }
+  __builtin_amdgcn_wave_barrier();
+
+  // forward: source lanes Wz, Ws; prefix lane b (in "wz"), a (in "ws"), kappa
+  const bool pre = lane == NSRC;
+  float wsp[CH], wzc[CH], wzp[CH], kap[CH];
+  {
+    float wz = pre ? 1.f : 0.f, ws = pre ? 1.f : 0.f, kp = 0.f;
+#pragma unroll
+    for (int t = 0; t < CH; ++t) {
+      const float A = lane_bcast(al, t), E = lane_bcast(et, t), B = lane_bcast(be, t);
+      wzp[t] = wz;
+      wsp[t] = ws;
+      kap[t] = kp;   // kappa_{t-1} (prefix lane)
+      if (pre) {
+        wz = B * wz;               // b_t
+        ws = A * ws;               // a_t
+        kp = A * kp + E * wz;      // kappa_t
+      } else {
+        wz = B * wz + wrow[t];
+        ws = A * ws + E * wz;
+      }
+      wzc[t] = wz;
+    }
+  }
+  // reverse
+  {
+    float gws = 0.f, gwz = 0.f, gk = 0.f;
+#pragma unroll
+    for (int t = CH - 1; t >= 0; --t) {
+      const float A1 = t + 1 < CH ? lane_bcast(al, t + 1) : 0.f;
+      const float B1 = t + 1 < CH ? lane_bcast(be, t + 1) : 0.f;
+      const float E = lane_bcast(et, t);
+      float ca, ce, cb;
+      if (pre) {
+        // ga (in gws), gkappa (gk), gb (gwz)
+        const float da = t < CH - 1 ? dcol[t] : gss;
+        const float dk = t < CH - 1 ? fzc[t] : -gsz;
+        const float db = t < CH - 1 ? 0.f : gzz;
+        gws = da + A1 * gws;
+        gk = dk + A1 * gk;
+        gwz = db + B1 * gwz + E * gk;
+        ca = gws * wsp[t] + gk * kap[t];   // ga_t a_{t-1} + gkappa_t kappa_{t-1}
+        ce = gk * wzc[t];                  // gkappa_t b_t
+        cb = gwz * wzp[t];                 // gb_t b_{t-1}
+      } else {
+        const float dws = t < CH - 1 ? dcol[t] : -hs;
+        const float dwz = t < CH - 1 ? 0.f : hz;
+        gws = dws + A1 * gws;
+        gwz = dwz + E * gws + B1 * gwz;
+        ca = gws * wsp[t];
+        ce = gws * wzc[t];
+        cb = gwz * wzp[t];
+        // window-weight gradient dw(s, t) = gWz_t for j = t + H - s in [0, e)
+        const int j = t + H - lane;
+        if (lane < NSRC && j >= 0 && j < e && t < L && g.gate_mode != GATE_NONE) {
+          if (g.gate_mode == GATE_LAG) a.dgate[(tb + t0 + t) * e + j] = from_f32<bf16>(gwz);
+          else p.dw[(tb + t0 + t) * e + j] = gwz;
+        }
+      }
+      if (lane < LP) {   // lanes past the prefix lane write zeros (the row sums read 52 entries)
+        const bool live = lane <= NSRC;
+        U.red[0][t][lane] = live ? ca : 0.f;
+        U.red[1][t][lane] = live ? ce : 0.f;
+        U.red[2][t][lane] = live ? cb : 0.f;
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  // sums over the lanes (16-byte row reads): lanes 0..31 alpha and eta of step t = lane, lanes
+  // 32..63 beta of step lane - 32
+  {
+    const int t = lane & (CH - 1);
+    auto row_sum = [&](int q) {
+      const float4* r = reinterpret_cast<const float4*>(&U.red[q][t][0]);
+      float4 acc = r[0];
+#pragma unroll
+      for (int i = 1; i < LP / 4; ++i) {
+        const float4 x = r[i];
+        acc.x += x.x; acc.y += x.y; acc.z += x.z; acc.w += x.w;
+      }
+      return (acc.x + acc.y) + (acc.z + acc.w);
+    };
+    if (lane < CH) {
+      const float s0 = row_sum(0), s1 = row_sum(1);
+      if (t < L) {
+        a.ddecay[tb + t0 + t] = from_f32<bf16>(s0);
+        a.dlr[tb + t0 + t] = from_f32<bf16>(s1);
+      }
+    } else {
+      const float s0 = row_sum(2);
+      if (t < L && g.momentum && a.dbeta) a.dbeta[tb + t0 + t] = from_f32<bf16>(s0);
+    }
+  }
+}
+
+hipError_t launch_scalar_chain(const Geom& g, const BwdPtrs<bf16>& a, const BwdSegPtrs& p, hipStream_t stream) {
+  hipLaunchKernelGGL(k_scalar_chain, dim3((g.nc + wb::kChainWaves - 1) / wb::kChainWaves, g.BH),
+                     dim3(64 * wb::kChainWaves), 0, stream, g, a, p);
+  return hipGetLastError();
+}
+
 }  // namespace atlas
