@@ -83,6 +83,8 @@ struct Profiler {
   }
 };
 Profiler& prof() { static Profiler p; return p; }
+// kernel launched last for each timed stage (the specialised and the general path launch different
+// kernels for the same stage; prof_name records which)
 const char* kKernelNames[KID_COUNT] = {"k_fwd_seg_agg", "k_fwd_seg", "k_buffer_out", "k_bwd_seg_agg",
                                        "k_bwd_seg", "k_bwd_seg_fixup", "k_seg_reduce_dsref", "k_fwd_seg_scan",
                                        "k_bwd_seg_scan", "k_chunk_coef_fwd", "k_chunk_coef_bwd",
@@ -90,6 +92,9 @@ const char* kKernelNames[KID_COUNT] = {"k_fwd_seg_agg", "k_fwd_seg", "k_buffer_o
 }  // namespace
 
 namespace atlas {
+void prof_name(int kid, const char* name) {
+  if (kid >= 0 && kid < KID_COUNT) kKernelNames[kid] = name;
+}
 void prof_begin(int kid, hipStream_t s) {
   Profiler& P = prof();
   if (!P.on) return;

@@ -267,6 +267,7 @@ __global__ __launch_bounds__(kScalarThreads) void k_bwd_scalar(const Geom g, con
 
 template <typename T, int CH>
 hipError_t launch_bwd_scalar(const Geom& g, const BwdPtrs<T>& a, const BwdSegPtrs& p, hipStream_t stream) {
+  prof_name(KID_BWD_SCALAR, "k_bwd_scalar");
   prof_begin(KID_BWD_SCALAR, stream);
   hipLaunchKernelGGL((k_bwd_scalar<T, CH>), dim3(g.nc, g.BH), dim3(kScalarThreads), 0, stream, g, a, p);
   prof_end(KID_BWD_SCALAR, stream);

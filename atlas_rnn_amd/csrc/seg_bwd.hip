@@ -946,6 +946,7 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
   if ((err = hipGetLastError()) != hipSuccess) return err;
   if constexpr (sizeof(T) == 2 && CH == 32 && D == 64) {
     if (walk) {
+      prof_name(KID_BWD_CHUNK, "k_walk_bwd");
       prof_begin(KID_BWD_CHUNK, stream);
       err = launch_walk_bwd_kernel(g, a, sg, p, stream);
       prof_end(KID_BWD_CHUNK, stream);
@@ -957,6 +958,7 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
     err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bwd_seg<T, CH, D>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (err != hipSuccess) return err;
+    prof_name(KID_BWD_CHUNK, "k_bwd_seg");
     prof_begin(KID_BWD_CHUNK, stream);
     hipLaunchKernelGGL((k_bwd_seg<T, CH, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, p);
     prof_end(KID_BWD_CHUNK, stream);
@@ -964,6 +966,7 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
   }
   if constexpr (sizeof(T) == 2 && CH == 32 && D == 64) {
     if (walk) {
+      prof_name(KID_BWD_SCALAR, "k_scalar_chain");
       prof_begin(KID_BWD_SCALAR, stream);
       err = launch_scalar_chain(g, a, p, stream);
       prof_end(KID_BWD_SCALAR, stream);

@@ -109,6 +109,7 @@ hipError_t launch_fwd_seg(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg,
     err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_seg_agg<T, CH, D>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (err != hipSuccess) return err;
+    prof_name(KID_FWD_SEG_AGG, "k_fwd_seg_agg");
     prof_begin(KID_FWD_SEG_AGG, stream);
     hipLaunchKernelGGL((k_fwd_seg_agg<T, CH, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, agg,
                        (const float*)coef);
@@ -120,6 +121,7 @@ hipError_t launch_fwd_seg(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg,
   err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_seg<T, CH, D>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (err != hipSuccess) return err;
+  prof_name(KID_FWD_WALK, "k_fwd_seg");
   prof_begin(KID_FWD_WALK, stream);
   hipLaunchKernelGGL((k_fwd_seg<T, CH, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg,
                      (const float*)seg_states, rw, final_raw, (const float*)coef, (const T*)wsh);

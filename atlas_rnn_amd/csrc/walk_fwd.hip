@@ -494,6 +494,7 @@ static hipError_t launch_walks(const Geom& g, const FwdPtrs<bf16>& a, const SegG
     err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_agg<MAPE>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (err != hipSuccess) return err;
+    prof_name(KID_FWD_SEG_AGG, "k_walk_agg");
     prof_begin(KID_FWD_SEG_AGG, stream);
     hipLaunchKernelGGL((k_walk_agg<MAPE>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, agg,
                        (const float*)coef);
@@ -505,6 +506,7 @@ static hipError_t launch_walks(const Geom& g, const FwdPtrs<bf16>& a, const SegG
   err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_full<MAPE>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (err != hipSuccess) return err;
+  prof_name(KID_FWD_WALK, "k_walk_full");
   prof_begin(KID_FWD_WALK, stream);
   hipLaunchKernelGGL((k_walk_full<MAPE>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg,
                      (const float*)seg_states, rw, final_raw, (const float*)coef, (const bf16*)wsh);

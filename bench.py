@@ -62,6 +62,10 @@ def algorithmic_bytes(bh=BH, t=T, d=D, e=E, s_in=2, s_st=4):
         "k_chunk_coef_fwd": n * n_sc * s_in,
         "k_chunk_coef_bwd": n * n_sc * s_in,
     }
+    # the specialised bf16 d = 64 path launches these kernels for the same stages
+    for spec, gen in (("k_walk_agg", "k_fwd_seg_agg"), ("k_walk_full", "k_fwd_seg"), ("k_walk_bwd", "k_bwd_seg"),
+                      ("k_scalar_chain", "k_bwd_scalar")):
+        per_kernel[spec] = per_kernel[gen]
     return fwd, bwd, per_kernel
 
 
