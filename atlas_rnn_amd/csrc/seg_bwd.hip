@@ -13,7 +13,8 @@
 //                   phase comments) while carrying (dS, dZ) and the halo gradients of the previous
 //                   chunk's last e-1 tokens.
 //   k_bwd_seg_fixup : merges the partial (dv, dphi) of tokens whose window crosses a segment boundary,
-//                   adds the d buffer_out terms, reduces token-gate gradients and dS_ref partials.
+//                   adds the d buffer_out terms, reduces token-gate gradients and (without d buffer_out)
+//                   the dS_ref partials; with d buffer_out k_seg_reduce_dsref reduces them afterwards.
 #include "mem_common.h"
 #include "mem_params.h"
 #include "seg_common.h"
@@ -820,9 +821,11 @@ __global__ __launch_bounds__(kThreads) void k_bwd_seg_scan(const Geom g, const f
 // ---------------------------------------------------------------------------------------------
 // segment-boundary fixup: grid (nseg, BH)
 // ---------------------------------------------------------------------------------------------
+// reduce_dsref: without d buffer_out terms (which add to the dS_ref partials here) the block of
+// segment seg also sums its share of the dS_ref partials over the segments (no separate launch).
 template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void k_bwd_seg_fixup(const Geom g, const BwdPtrs<T> a, const SegGeom sg,
-                                                              const BwdSegPtrs p) {
+                                                              const BwdSegPtrs p, int reduce_dsref) {
   __shared__ float sphi[D], sdel[D], sdd[D], sdb[D];
   const int seg = blockIdx.x, bh = blockIdx.y;
   const int H = g.H, e = g.e;
@@ -830,6 +833,22 @@ __global__ __launch_bounds__(kThreads) void k_bwd_seg_fixup(const Geom g, const 
   const int tok0 = c_begin * g.Lc, tok1 = min(g.T, c_end * g.Lc);
   const size_t tb = (size_t)bh * g.T;
   const int tid = threadIdx.x;
+  if (reduce_dsref) {
+    const int per = (D * D + sg.nseg - 1) / sg.nseg;
+    const int i0 = seg * per, i1 = min(D * D, i0 + per);
+    const float* part = p.dsref_part + (size_t)bh * sg.nseg * D * D;
+    for (int idx = i0 + tid; idx < i1; idx += kThreads) {
+      float acc = 0.f;
+      for (int s0 = 0; s0 < sg.nseg; s0 += 8) {   // eight partials per memory round trip
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = part[(size_t)min(s0 + u, sg.nseg - 1) * D * D + idx];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += s0 + u < sg.nseg ? v[u] : 0.f;
+      }
+      a.dS_ref[(size_t)bh * D * D + idx] = acc;
+    }
+  }
   // token-gate gradient du_p = sum_j dw[p + j, j] (the d buffer_out term is added below)
   if (g.gate_mode == GATE_TOKEN) {
     for (int pp = tok0 + tid; pp < tok1; pp += kThreads) {
@@ -974,10 +993,13 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
     }
   }
   if (!walk && (err = launch_bwd_scalar<T, CH>(g, a, p, stream)) != hipSuccess) return err;
+  const int fused_reduce = a.dbuf_out == nullptr;
   prof_begin(KID_BWD_FIXUP, stream);
-  hipLaunchKernelGGL((k_bwd_seg_fixup<T, D>), dim3(sg.nseg, g.BH), dim3(kThreads), 0, stream, g, a, sg, p);
+  hipLaunchKernelGGL((k_bwd_seg_fixup<T, D>), dim3(sg.nseg, g.BH), dim3(kThreads), 0, stream, g, a, sg, p,
+                     fused_reduce);
   prof_end(KID_BWD_FIXUP, stream);
   if ((err = hipGetLastError()) != hipSuccess) return err;
+  if (fused_reduce) return hipSuccess;
   prof_begin(KID_REDUCE_DSREF, stream);
   hipLaunchKernelGGL(k_seg_reduce_dsref, dim3((D * D + kThreads - 1) / kThreads, g.BH), dim3(kThreads), 0, stream,
                      sg.nseg, D * D, (const float*)p.dsref_part, a.dS_ref);
