@@ -634,30 +634,42 @@ hipError_t launch_walk_bwd_kernel(const Geom& g, const BwdPtrs<bf16>& a, const S
 
 
 // ---------------------------------------------------------------------------------------------
-// Scalar gradients of the specialised path, one wave per 32-token chunk (two chunks per
+// Scalar gradients of the specialised path, one wave per 32-token chunk (four chunks per
 // workgroup), as the reverse-mode form of the chunk's coefficient recurrences. Lane s < 48 owns
-// source s and runs
-//   forward   Wz_t = beta_t Wz_{t-1} + w(s, t),   Ws_t = alpha_t Ws_{t-1} + eta_t Wz_t
-//   reverse   gWs_t = G_t + alpha_{t+1} gWs_{t+1},  gWz_t = Hz_t + eta_t gWs_t + beta_{t+1} gWz_{t+1}
-// with the direct terms G_t = -Lm[t+1][s] (t < 31), G_31 = -hS[s], Hz_31 = hZ[s] from the walk's
-// record; lane 48 runs the same pair for the chunk prefix (a_t, kappa_t, b_t) with the direct
-// terms fS, fZ and the Grams. Per step the lanes contribute
-//   dalpha_t += gWs_t Ws_{t-1},  deta_t += gWs_t Wz_t,  dbeta_t += gWz_t Wz_{t-1},  dw(s, t) = gWz_t
-// (prefix lane: dalpha_t += ga_t a_{t-1} + gkappa_t kappa_{t-1}, deta_t += gkappa_t b_t,
-// dbeta_t += gb_t b_{t-1}); the sums over the lanes go through LDS. The step scalars are the same
-// for every lane and are broadcast from lane t with v_readlane; all arithmetic is fp32.
+// source s and lane 48 the chunk prefix; every lane runs the same branch-free code:
+//   forward   Wz_t = beta_t Wz_{t-1} + w(s, t),   Ws_t = alpha_t Ws_{t-1} + eta_t Wz_t,   a_t = alpha_t a_{t-1}
+//   reverse   gWs_t = G_t + alpha_{t+1} gWs_{t+1},  gWz_t = Hz_t + eta_t gWs_t + beta_{t+1} gWz_{t+1},
+//             ga_t = Ga_t + alpha_{t+1} ga_{t+1}
+// A source starts from Wz = Ws = 0 with the window weights as input and the direct terms
+// G_t = -Lm[t+1][s] (t < 31), G_31 = -hS[s], Hz_31 = hZ[s], Ga = 0 from the walk's record. The
+// prefix lane starts from Wz = 1 (so that Wz_t = b_t and Ws_t = kappa_t) with no input, and
+// G_t = -fZ[t+1], G_31 = -<dS_end, Z_in>, Hz_31 = <dZ_end, Z_in>, Ga_t = fS[t+1], Ga_31 = <dS_end, S_in>.
+// Per step a lane contributes
+//   dalpha_t += gWs_t Ws_{t-1} + ga_t a_{t-1},  deta_t += gWs_t Wz_t,  dbeta_t += gWz_t Wz_{t-1},
+// and a source's window-weight gradient is dw(s, t) = gWz_t. The contributions are summed over
+// lane quads with DPP, then over the quads through LDS. The step scalars are the same for every
+// lane and are broadcast from lane t with v_readlane; all arithmetic is fp32.
 // ---------------------------------------------------------------------------------------------
 namespace wb {
-constexpr int kChainWaves = 2;
+constexpr int kChainWaves = 4;
 constexpr int NSRC = SP;          // 48 source lanes; lane NSRC runs the prefix chain
 constexpr int RP = CH + 1;        // pitch of the window-weight rows
-constexpr int LP = 52;            // pitch of the contribution rows (49 lanes, 16-byte aligned)
-struct ChainSmem {   // static LDS: kChainWaves * 19.5 KB
+constexpr int NQD = 13;           // lane quads holding live lanes (0 .. 51)
+constexpr int QDP = 16;           // pitch of the per-step quad rows
+struct ChainSmem {   // static LDS: kChainWaves * 6.3 KB
   union {
-    float W[NSRC][RP];            // window weights w(s, t) of the sources
-    alignas(16) float red[3][CH][LP];   // contributions (alpha, eta, beta) of step t from lane l at [t][l]
+    float W[NSRC][RP];                  // window weights w(s, t) of the sources
+    struct {
+      alignas(16) float red[3][CH][QDP];   // quad sums of the alpha / eta / beta contributions of step t
+      float dw[CH * kMaxWindow + 1];       // window-weight gradients [t][j]; the last slot takes masked writes
+    } r;
   } u[kChainWaves];
 };
+__device__ __forceinline__ float quad_sum(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xf, 0xf, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xf, 0xf, false));
+  return x;
+}
 }  // namespace wb
 
 __global__ __launch_bounds__(64 * wb::kChainWaves) void k_scalar_chain(const Geom g, const BwdPtrs<bf16> a,
@@ -673,6 +685,7 @@ __global__ __launch_bounds__(64 * wb::kChainWaves) void k_scalar_chain(const Geo
   const size_t tb = (size_t)bh * g.T;
   const float* blk = p.scal + ((size_t)bh * g.nc + c) * SB::SIZE;
   auto& U = smc.u[wv];
+  const bool src = lane < NSRC, pre = lane == NSRC;
 
   // step scalars in lane t (padded steps: alpha = beta = 1, eta = 0; beta = 0 without momentum)
   float al = 1.f, et = 0.f, be = 1.f;
@@ -681,132 +694,101 @@ __global__ __launch_bounds__(64 * wb::kChainWaves) void k_scalar_chain(const Geo
     et = to_f32(a.lr[tb + t0 + lane]);
     be = g.momentum ? to_f32(a.beta[tb + t0 + lane]) : 0.f;
   }
-  // direct terms of this lane: Lm[t + 1][s] (source lanes), fS / fZ (prefix lane)
-  float dcol[CH];
+  // direct terms of this lane. Every lane issues the same loads (no load sits in a lane-dependent
+  // branch, so they are all in flight together); the prefix lane's terms come from lane broadcasts.
+  float dG[CH], dA[CH], hz_end;
+  {
+    const int col = src ? lane : 0;
+    float lmv[CH - 1];
 #pragma unroll
-  for (int t = 0; t < CH - 1; ++t) {
-    const int col = lane < NSRC ? lane : 0;
-    const float lm = blk[SB::LM + (t + 1) * SPM + col];
-    const float fs = blk[SB::FS + t + 1];
-    dcol[t] = lane < NSRC ? -lm : fs;
+    for (int t = 0; t < CH - 1; ++t) lmv[t] = blk[SB::LM + (t + 1) * SPM + col];
+    const float fsl = blk[SB::FS + (lane & (CH - 1))], fzl = blk[SB::FZ + (lane & (CH - 1))];
+    const float gram = blk[SB::GRAM + (lane & 3)];
+    const float hs = blk[SB::HS + col], hz = blk[SB::HZ + col];
+#pragma unroll
+    for (int t = 0; t < CH - 1; ++t) {
+      const float fs = lane_bcast(fsl, t + 1), fz = lane_bcast(fzl, t + 1);
+      dG[t] = src ? -lmv[t] : (pre ? -fz : 0.f);
+      dA[t] = pre ? fs : 0.f;
+    }
+    const float gss = lane_bcast(gram, 0), gsz = lane_bcast(gram, 1), gzz = lane_bcast(gram, 2);
+    dG[CH - 1] = src ? -hs : (pre ? -gsz : 0.f);
+    dA[CH - 1] = pre ? gss : 0.f;
+    hz_end = src ? hz : (pre ? gzz : 0.f);
   }
-  float fzc[CH];
-#pragma unroll
-  for (int t = 0; t < CH - 1; ++t) fzc[t] = -blk[SB::FZ + t + 1];
-  fzc[CH - 1] = 0.f;
-  const float hs = lane < NSRC ? blk[SB::HS + lane] : 0.f, hz = lane < NSRC ? blk[SB::HZ + lane] : 0.f;
-  const float gss = blk[SB::GRAM], gsz = blk[SB::GRAM + 1], gzz = blk[SB::GRAM + 2];
 
   // window weights of the sources: W[s][t] = w(s, t) for j = t + H - s in [0, e)
   for (int idx = lane; idx < NSRC * RP; idx += 64) (&U.W[0][0])[idx] = 0.f;
   __builtin_amdgcn_wave_barrier();
-  if (g.gate_mode != GATE_NONE) {
-    for (int idx = lane; idx < CH * e; idx += 64) {
-      const int t = idx / e, j = idx % e, s = t + H - j;
-      float wgt = 0.f;
-      if (t < L) {
-        if (g.gate_mode == GATE_LAG) wgt = to_f32(a.gate[(tb + t0 + t) * e + j]);
-        else {
-          const int ps = t0 + t - j;   // source token
-          wgt = ps >= 0 ? to_f32(a.gate[tb + ps]) : 0.f;
-        }
-      }
-      if (s >= 0 && s < NSRC) U.W[s][t] = wgt;
+  for (int idx = lane; idx < CH * e; idx += 64) {
+    const int t = idx / e, j = idx % e, s = t + H - j;
+    float wgt = 0.f;
+    if (t < L) {
+      if (g.gate_mode == GATE_LAG) wgt = to_f32(a.gate[(tb + t0 + t) * e + j]);
+      else if (g.gate_mode == GATE_TOKEN) wgt = t0 + t - j >= 0 ? to_f32(a.gate[tb + t0 + t - j]) : 0.f;
+      else wgt = 1.f;
     }
-  } else {
-    for (int idx = lane; idx < CH * e; idx += 64) {
-      const int t = idx / e, j = idx % e, s = t + H - j;
-      if (s >= 0 && s < NSRC) U.W[s][t] = t < L ? 1.f : 0.f;
-    }
+    if (s >= 0 && s < NSRC) U.W[s][t] = wgt;
   }
   __builtin_amdgcn_wave_barrier();
   float wrow[CH];
   {
-    const int row = lane < NSRC ? lane : 0;
+    const int row = src ? lane : 0;
 #pragma unroll
-    for (int t = 0; t < CH; ++t) wrow[t] = lane < NSRC ? U.W[row][t] : 0.f;
+    for (int t = 0; t < CH; ++t) wrow[t] = src ? U.W[row][t] : 0.f;
   }
   __builtin_amdgcn_wave_barrier();
 
-  // forward: source lanes Wz, Ws; prefix lane b (in "wz"), a (in "ws"), kappa
-  const bool pre = lane == NSRC;
-  float wsp[CH], wzc[CH], wzp[CH], kap[CH];
+  // forward
+  float wsp[CH], wzc[CH], wzp[CH], ap[CH];
   {
-    float wz = pre ? 1.f : 0.f, ws = pre ? 1.f : 0.f, kp = 0.f;
+    float wz = pre ? 1.f : 0.f, ws = 0.f, av = 1.f;
 #pragma unroll
     for (int t = 0; t < CH; ++t) {
       const float A = lane_bcast(al, t), E = lane_bcast(et, t), B = lane_bcast(be, t);
       wzp[t] = wz;
       wsp[t] = ws;
-      kap[t] = kp;   // kappa_{t-1} (prefix lane)
-      if (pre) {
-        wz = B * wz;               // b_t
-        ws = A * ws;               // a_t
-        kp = A * kp + E * wz;      // kappa_t
-      } else {
-        wz = B * wz + wrow[t];
-        ws = A * ws + E * wz;
-      }
+      ap[t] = av;
+      wz = B * wz + wrow[t];
+      ws = A * ws + E * wz;
+      av = A * av;
       wzc[t] = wz;
     }
   }
-  // reverse
+  // reverse (branch-free: masked stores go to a dummy slot)
   {
-    float gws = 0.f, gwz = 0.f, gk = 0.f;
+    const bool live = lane <= NSRC;
+    const bool quad_head = (lane & 3) == 0 && lane < 4 * NQD;
+    const int qrow = quad_head ? (lane >> 2) : QDP - 1;   // column QDP - 1 is never read
+    float gws = 0.f, gwz = 0.f, ga = 0.f;
 #pragma unroll
     for (int t = CH - 1; t >= 0; --t) {
       const float A1 = t + 1 < CH ? lane_bcast(al, t + 1) : 0.f;
       const float B1 = t + 1 < CH ? lane_bcast(be, t + 1) : 0.f;
       const float E = lane_bcast(et, t);
-      float ca, ce, cb;
-      if (pre) {
-        // ga (in gws), gkappa (gk), gb (gwz)
-        const float da = t < CH - 1 ? dcol[t] : gss;
-        const float dk = t < CH - 1 ? fzc[t] : -gsz;
-        const float db = t < CH - 1 ? 0.f : gzz;
-        gws = da + A1 * gws;
-        gk = dk + A1 * gk;
-        gwz = db + B1 * gwz + E * gk;
-        ca = gws * wsp[t] + gk * kap[t];   // ga_t a_{t-1} + gkappa_t kappa_{t-1}
-        ce = gk * wzc[t];                  // gkappa_t b_t
-        cb = gwz * wzp[t];                 // gb_t b_{t-1}
-      } else {
-        const float dws = t < CH - 1 ? dcol[t] : -hs;
-        const float dwz = t < CH - 1 ? 0.f : hz;
-        gws = dws + A1 * gws;
-        gwz = dwz + E * gws + B1 * gwz;
-        ca = gws * wsp[t];
-        ce = gws * wzc[t];
-        cb = gwz * wzp[t];
-        // window-weight gradient dw(s, t) = gWz_t for j = t + H - s in [0, e)
-        const int j = t + H - lane;
-        if (lane < NSRC && j >= 0 && j < e && t < L && g.gate_mode != GATE_NONE) {
-          if (g.gate_mode == GATE_LAG) a.dgate[(tb + t0 + t) * e + j] = from_f32<bf16>(gwz);
-          else p.dw[(tb + t0 + t) * e + j] = gwz;
-        }
-      }
-      if (lane < LP) {   // lanes past the prefix lane write zeros (the row sums read 52 entries)
-        const bool live = lane <= NSRC;
-        U.red[0][t][lane] = live ? ca : 0.f;
-        U.red[1][t][lane] = live ? ce : 0.f;
-        U.red[2][t][lane] = live ? cb : 0.f;
-      }
+      gws = dG[t] + A1 * gws;
+      gwz = (t == CH - 1 ? hz_end : 0.f) + E * gws + B1 * gwz;
+      ga = dA[t] + A1 * ga;
+      const float ca = quad_sum(live ? gws * wsp[t] + ga * ap[t] : 0.f);
+      const float ce = quad_sum(live ? gws * wzc[t] : 0.f);
+      const float cb = quad_sum(live ? gwz * wzp[t] : 0.f);
+      U.r.red[0][t][qrow] = ca;
+      U.r.red[1][t][qrow] = ce;
+      U.r.red[2][t][qrow] = cb;
+      const int j = t + H - lane;
+      const bool wv_ok = src && j >= 0 && j < e;
+      U.r.dw[wv_ok ? t * e + j : CH * kMaxWindow] = gwz;
     }
   }
   __builtin_amdgcn_wave_barrier();
-  // sums over the lanes (16-byte row reads): lanes 0..31 alpha and eta of step t = lane, lanes
-  // 32..63 beta of step lane - 32
+  // sums over the quads: lanes 0..31 alpha and eta of step t = lane, lanes 32..63 beta of step lane - 32
   {
     const int t = lane & (CH - 1);
     auto row_sum = [&](int q) {
-      const float4* r = reinterpret_cast<const float4*>(&U.red[q][t][0]);
-      float4 acc = r[0];
-#pragma unroll
-      for (int i = 1; i < LP / 4; ++i) {
-        const float4 x = r[i];
-        acc.x += x.x; acc.y += x.y; acc.z += x.z; acc.w += x.w;
-      }
-      return (acc.x + acc.y) + (acc.z + acc.w);
+      const float4* r = reinterpret_cast<const float4*>(&U.r.red[q][t][0]);
+      const float4 x0 = r[0], x1 = r[1], x2 = r[2];
+      const float x3 = U.r.red[q][t][12];
+      return ((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w)) + ((x2.x + x2.y) + (x2.z + x2.w)) + x3;
     };
     if (lane < CH) {
       const float s0 = row_sum(0), s1 = row_sum(1);
@@ -817,6 +799,16 @@ __global__ __launch_bounds__(64 * wb::kChainWaves) void k_scalar_chain(const Geo
     } else {
       const float s0 = row_sum(2);
       if (t < L && g.momentum && a.dbeta) a.dbeta[tb + t0 + t] = from_f32<bf16>(s0);
+    }
+  }
+  // window-weight gradients, written contiguously per chunk
+  if (g.gate_mode != GATE_NONE) {
+    for (int idx = lane; idx < CH * e; idx += 64) {
+      if (idx / e < L) {
+        const float v = U.r.dw[idx];
+        if (g.gate_mode == GATE_LAG) a.dgate[(tb + t0) * e + idx] = from_f32<bf16>(v);
+        else p.dw[(tb + t0) * e + idx] = v;
+      }
     }
   }
 }
