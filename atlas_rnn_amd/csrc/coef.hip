@@ -11,63 +11,250 @@
 #include "mem_common.h"
 #include "mem_params.h"
 #include "seg_common.h"
+#include "walk_common.h"
 
 namespace atlas {
 
-constexpr int kCoefThreads = 128;   // two waves: sources 0..127, prefix chain in lane 127
+// One lane per source (sources 0 .. SPM-1, SPM = CH + 32), rounded up to whole waves.
+template <int CH>
+constexpr int coef_threads() { return (CH + kHaloPad + 63) / 64 * 64; }
 
+template <int CH>
+struct CoefSmem {
+  static constexpr int SPM = CH + kHaloPad;
+  alignas(16) float alpha[CH];   // padded steps: alpha = beta = 1, eta = 0
+  alignas(16) float eta[CH];
+  alignas(16) float beta[CH];
+  // [t][s]: the window weight w(s, t) (zero outside the window) until lane s reads it, then
+  // Ws[s, t-1] (each lane reads and overwrites only its own column, in order)
+  alignas(16) float tab[CH][SPM];
+};
+
+// Record layout (floats): acoef[CH], kcoef[CH], endc[4], wsend[SPM], wzend[SPM], wsmid[SPM],
+// wzmid[SPM], midc[4].
+//   source s:   Wz[s,t] = beta_t Wz[s,t-1] + w(s,t),  Ws[s,t] = alpha_t Ws[s,t-1] + eta_t Wz[s,t]
+//               one lane per source, three VALU operations and two LDS accesses per step; Ws[s, t-1]
+//               goes to the table and from there, after the chains, to wsh[t][s] in 16-byte stores;
+//   prefix:     when H + CH <= SPM - 2 (e <= 31), the two last source lanes never see a window
+//               weight and run the same chain from Ws = 1 (lane SPM-2: Ws_t = a_t = prod alpha) and
+//               from Wz = 1 (lane SPM-1: Wz_t = b_t = prod beta, Ws_t = kappa_t); acoef and kcoef
+//               are their table columns. Otherwise inclusive scans across the last wave's lanes.
+//   mid values: after token Lmid - 1 (a multiple of 8) when Lmid > 0, else zero.
+// The inputs (step scalars, and the gates of windows up to 4 NT / CH) are loaded together, ahead
+// of the first barrier.
 template <typename T, int CH, bool WSH>
-__global__ __launch_bounds__(kCoefThreads) void k_chunk_coef(const Geom g, const T* __restrict__ decay,
-                                                               const T* __restrict__ lr, const T* __restrict__ beta,
-                                                               const T* __restrict__ gate, float* __restrict__ rec,
-                                                               T* __restrict__ wsh) {
-  constexpr int SPM = CH + kHaloPad;
-  constexpr int REC = CoefRec<CH>::SIZE;
-  __shared__ ChunkScalars<CH> sc;
-  const int c = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x;
+__global__ __launch_bounds__(coef_threads<CH>()) void k_chunk_coef(const Geom g, const T* __restrict__ decay,
+                                                                    const T* __restrict__ lr,
+                                                                    const T* __restrict__ beta,
+                                                                    const T* __restrict__ gate,
+                                                                    float* __restrict__ rec_all, T* __restrict__ wsh) {
+  constexpr int SPM = CH + kHaloPad, NT = coef_threads<CH>(), REC = CoefRec<CH>::SIZE;
+  constexpr int R_KCOEF = CH, R_ENDC = 2 * CH, R_WSEND = R_ENDC + 4, R_WZEND = R_WSEND + SPM,
+                R_WSMID = R_WZEND + SPM, R_WZMID = R_WSMID + SPM, R_MIDC = R_WZMID + SPM;
+  constexpr int GRP = NT / CH, JR = 4;   // threads per target; gates held per thread
+  constexpr int LA = SPM - 2, LK = SPM - 1;   // prefix lanes
+  static_assert(R_MIDC + 4 == REC, "record layout");
+  static_assert(CH <= 64 && (CH & (CH - 1)) == 0 && CH % 8 == 0 && NT % CH == 0 && SPM % 8 == 0, "lanes");
+  __shared__ CoefSmem<CH> sm;
+  const int c = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x, lane = lane_id();
   const int H = g.H, e = g.e;
   const int t0 = c * g.Lc, L = min(g.T, t0 + g.Lc) - t0;
   const size_t tb = (size_t)bh * g.T, r0 = tb + t0;
-  for (int t = tid; t < CH; t += kCoefThreads) {
-    const bool ok = t < L;
-    const size_t rt = ok ? r0 + t : r0;
-    const T x_al = decay[rt], x_et = lr[rt], x_be = (g.momentum && beta ? beta : decay)[rt];
-    sc.alpha[t] = ok ? to_f32(x_al) : 1.f;
-    sc.eta[t] = ok ? to_f32(x_et) : 0.f;
-    sc.beta[t] = ok ? (g.momentum ? to_f32(x_be) : 0.f) : 1.f;
+  float* rec = rec_all + ((size_t)bh * g.nc + c) * REC;
+  const bool scan_wave = tid >= NT - 64;            // wave-uniform
+  const bool lane_prefix = H + CH <= SPM - 2;       // uniform
+  const bool few_gates = e <= JR * GRP;             // uniform
+
+  // ---- inputs: step scalars (last wave, lane t), window weights of target tt, lags jg + GRP r
+  float al = 1.f, et = 0.f, be = 1.f;
+  {   // every lane loads (clamped index, no branch around the loads); the last wave's lanes t < L keep them
+    const size_t rt = r0 + min(lane, L - 1);
+    const T xa = decay[rt], xe = lr[rt], xb = (g.momentum && beta ? beta : decay)[rt];
+    const bool keep = scan_wave && lane < min(CH, L);
+    const float fa = to_f32(xa), fe = to_f32(xe), fb = g.momentum ? to_f32(xb) : 0.f;
+    al = keep ? fa : 1.f;
+    et = keep ? fe : 0.f;
+    be = keep ? fb : 1.f;
   }
-  if (g.gate_mode == GATE_TOKEN) {
-    for (int s = tid; s < SPM; s += kCoefThreads) {
-      const int p = t0 - H + s;
-      const bool in = s < H + L;
-      const T x = gate[(in && p >= 0) ? tb + p : r0];
-      sc.ug[s] = in ? (p >= 0 ? to_f32(x) : 1.f) : 0.f;
+  const int tt = tid % CH, jg = tid / CH;
+  auto weight = [&](int j) {   // w(tt + H - j, tt); the load is issued for any j, tt (clamped index)
+    const int tc = min(tt, L - 1), jc = min(j, e - 1);
+    if (g.gate_mode == GATE_LAG) return to_f32(gate[(r0 + tc) * e + jc]);
+    if (g.gate_mode == GATE_TOKEN) {
+      const int p = t0 + tc - jc;   // source token
+      const float x = to_f32(gate[tb + (p >= 0 ? p : 0)]);
+      return p >= 0 ? x : 1.f;
     }
-  } else if (g.gate_mode == GATE_LAG) {
-    for (int idx = tid; idx < CH * e; idx += kCoefThreads) {
-      const bool ok = idx / e < L;
-      const T x = gate[ok ? r0 * e + idx : r0];
-      sc.wl[idx] = ok ? to_f32(x) : 0.f;
+    return 1.f;
+  };
+  float gv[JR];
+  if (few_gates) {   // one uniform branch around all JR loads, so that they are in flight together
+    T raw[JR];
+    if (g.gate_mode == GATE_LAG) {
+#pragma unroll
+      for (int r = 0; r < JR; ++r) {
+        const int tc = min(tt, L - 1), jc = min(jg + GRP * r, e - 1);
+        raw[r] = gate[(r0 + tc) * e + jc];
+      }
+#pragma unroll
+      for (int r = 0; r < JR; ++r) gv[r] = to_f32(raw[r]);
+    } else if (g.gate_mode == GATE_TOKEN) {
+#pragma unroll
+      for (int r = 0; r < JR; ++r) {
+        const int p = t0 + min(tt, L - 1) - min(jg + GRP * r, e - 1);
+        raw[r] = gate[tb + (p >= 0 ? p : 0)];
+      }
+#pragma unroll
+      for (int r = 0; r < JR; ++r) {
+        const int p = t0 + min(tt, L - 1) - min(jg + GRP * r, e - 1);
+        gv[r] = p >= 0 ? to_f32(raw[r]) : 1.f;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < JR; ++r) gv[r] = 1.f;
+    }
+  }
+  for (int i = tid; i < CH * SPM / 4; i += NT)
+    reinterpret_cast<float4*>(&sm.tab[0][0])[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (scan_wave && lane < CH) {
+    sm.alpha[lane] = al;
+    sm.eta[lane] = et;
+    sm.beta[lane] = be;
+  }
+  __syncthreads();
+  if (tt < L) {   // target tt, lag j -> source s = tt + H - j (0 .. SPM-1 since H = e - 1 <= 32)
+    if (few_gates) {
+#pragma unroll
+      for (int r = 0; r < JR; ++r) {
+        const int j = jg + GRP * r;
+        if (j < e) sm.tab[tt][tt + H - j] = gv[r];
+      }
+    } else {
+      for (int j = jg; j < e; j += GRP) sm.tab[tt][tt + H - j] = weight(j);
     }
   }
   __syncthreads();
-  T* w = WSH ? wsh + ((size_t)bh * g.nc + c) * CH * SPM : nullptr;
-  chunk_coefficients<CH, WSH, true, T>(g, sc, L, tid, w, SPM);
+
+  if (!lane_prefix && scan_wave) {   // prefix coefficients by scans, lane t = step t
+    float b = be;
+#pragma unroll
+    for (int d = 1; d < CH; d <<= 1) {
+      const float o = __shfl_up(b, d, 64);
+      if (lane >= d) b *= o;
+    }
+    float A = al, K = et * b;   // (A, K) o (A', K') = (A A', A K' + K)
+#pragma unroll
+    for (int d = 1; d < CH; d <<= 1) {
+      const float oA = __shfl_up(A, d, 64), oK = __shfl_up(K, d, 64);
+      if (lane >= d) {
+        K = fmaf(A, oK, K);
+        A *= oA;
+      }
+    }
+    const float ap = __shfl_up(A, 1, 64), kp = __shfl_up(K, 1, 64);
+    if (lane < CH) {
+      rec[lane] = lane ? ap : 1.f;
+      rec[R_KCOEF + lane] = lane ? kp : 0.f;
+    }
+    if (lane == CH - 1) *reinterpret_cast<float4*>(rec + R_ENDC) = make_float4(A, K, b, 0.f);
+    if (g.Lmid > 0 ? lane == g.Lmid - 1 : lane == 0)
+      *reinterpret_cast<float4*>(rec + R_MIDC) = g.Lmid > 0 ? make_float4(A, K, b, 0.f) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+
+  if (tid < SPM) {   // chains
+    const int s = tid;
+    float ws = (lane_prefix && s == LA) ? 1.f : 0.f, wz = (lane_prefix && s == LK) ? 1.f : 0.f;
+    float wsm = 0.f, wzm = 0.f;
+#pragma unroll
+    for (int t8 = 0; t8 < CH; t8 += 8) {
+      float a8[8], e8[8], b8[8], w8[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float4 xa = *reinterpret_cast<const float4*>(&sm.alpha[t8 + 4 * h]);
+        const float4 xe = *reinterpret_cast<const float4*>(&sm.eta[t8 + 4 * h]);
+        const float4 xb = *reinterpret_cast<const float4*>(&sm.beta[t8 + 4 * h]);
+        a8[4 * h] = xa.x; a8[4 * h + 1] = xa.y; a8[4 * h + 2] = xa.z; a8[4 * h + 3] = xa.w;
+        e8[4 * h] = xe.x; e8[4 * h + 1] = xe.y; e8[4 * h + 2] = xe.z; e8[4 * h + 3] = xe.w;
+        b8[4 * h] = xb.x; b8[4 * h + 1] = xb.y; b8[4 * h + 2] = xb.z; b8[4 * h + 3] = xb.w;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) w8[u] = sm.tab[t8 + u][s];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        sm.tab[t8 + u][s] = ws;   // Ws[s, t-1]
+        wz = fmaf(b8[u], wz, w8[u]);
+        ws = fmaf(a8[u], ws, e8[u] * wz);
+      }
+      if (t8 + 8 == g.Lmid) {   // wave-uniform
+        wsm = ws;
+        wzm = wz;
+      }
+    }
+    const bool src = !(lane_prefix && s >= LA);
+    rec[R_WSEND + s] = src ? ws : 0.f;
+    rec[R_WZEND + s] = src ? wz : 0.f;
+    rec[R_WSMID + s] = src ? wsm : 0.f;
+    rec[R_WZMID + s] = src ? wzm : 0.f;
+    if (!src) {   // (a, kappa, b) at the end and after token Lmid - 1
+      if (s == LA) {
+        rec[R_ENDC] = ws;
+        rec[R_MIDC] = wsm;
+      } else {
+        rec[R_ENDC + 1] = ws;
+        rec[R_ENDC + 2] = wz;
+        rec[R_ENDC + 3] = 0.f;
+        rec[R_MIDC + 1] = wsm;
+        rec[R_MIDC + 2] = wzm;
+        rec[R_MIDC + 3] = 0.f;
+      }
+    }
+  }
   __syncthreads();
-  float4* dst = reinterpret_cast<float4*>(rec + ((size_t)bh * g.nc + c) * REC);
-  const float4* src = reinterpret_cast<const float4*>(&sc.acoef[0]);
-  for (int i = tid; i < REC / 4; i += kCoefThreads) dst[i] = src[i];
+
+  if (lane_prefix && tid < CH) {   // acoef = a_{t-1}, kcoef = kappa_{t-1}
+    rec[tid] = sm.tab[tid][LA];
+    rec[R_KCOEF + tid] = sm.tab[tid][LK];
+  }
+  if constexpr (WSH) {   // Ws[s, t-1] -> wsh[t][s], eight sources per store (prefix columns zeroed)
+    const rsrc_t rw = make_rsrc(wsh + ((size_t)bh * g.nc + c) * CH * SPM, (uint32_t)(CH * SPM * sizeof(T)));
+    constexpr int G8 = SPM / 8;
+    for (int i = tid; i < CH * G8; i += NT) {
+      const int t = i / G8, s0 = (i % G8) * 8;
+      float v[8];
+      const float4 x0 = *reinterpret_cast<const float4*>(&sm.tab[t][s0]);
+      const float4 x1 = *reinterpret_cast<const float4*>(&sm.tab[t][s0 + 4]);
+      v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+      if (lane_prefix && s0 == SPM - 8) { v[6] = 0.f; v[7] = 0.f; }
+      const uint32_t off = (uint32_t)((t * SPM + s0) * sizeof(T));
+      if constexpr (sizeof(T) == 2) {
+        u32x4v o;
+        o[0] = pack_bf16x2(v[0], v[1]);
+        o[1] = pack_bf16x2(v[2], v[3]);
+        o[2] = pack_bf16x2(v[4], v[5]);
+        o[3] = pack_bf16x2(v[6], v[7]);
+        bst16(rw, off, o);
+      } else {
+        const u32x4v o0 = {__builtin_bit_cast(unsigned, v[0]), __builtin_bit_cast(unsigned, v[1]),
+                           __builtin_bit_cast(unsigned, v[2]), __builtin_bit_cast(unsigned, v[3])};
+        const u32x4v o1 = {__builtin_bit_cast(unsigned, v[4]), __builtin_bit_cast(unsigned, v[5]),
+                           __builtin_bit_cast(unsigned, v[6]), __builtin_bit_cast(unsigned, v[7])};
+        bst16(rw, off, o0);
+        bst16(rw, off + 16, o1);
+      }
+    }
+  }
 }
 
 template <typename T, int CH>
 hipError_t launch_chunk_coef(const Geom& g, const T* decay, const T* lr, const T* beta, const T* gate, float* rec,
                              T* wsh, int kid, hipStream_t stream) {
+  if (g.Lmid % 8 != 0 || g.Lmid > CH) return hipErrorInvalidValue;   // mid values are taken per 8 steps
   prof_begin(kid, stream);
   if (wsh) {
-    hipLaunchKernelGGL((k_chunk_coef<T, CH, true>), dim3(g.nc, g.BH), dim3(kCoefThreads), 0, stream, g, decay, lr,
+    hipLaunchKernelGGL((k_chunk_coef<T, CH, true>), dim3(g.nc, g.BH), dim3(coef_threads<CH>()), 0, stream, g, decay, lr,
                        beta, gate, rec, wsh);
   } else {
-    hipLaunchKernelGGL((k_chunk_coef<T, CH, false>), dim3(g.nc, g.BH), dim3(kCoefThreads), 0, stream, g, decay, lr,
+    hipLaunchKernelGGL((k_chunk_coef<T, CH, false>), dim3(g.nc, g.BH), dim3(coef_threads<CH>()), 0, stream, g, decay, lr,
                        beta, gate, rec, wsh);
   }
   prof_end(kid, stream);

@@ -208,75 +208,4 @@ __device__ __forceinline__ void decay_columns_wave(DecayTab<CH>& tab, const Chun
   }
 }
 
-// Coefficient recurrences of a chunk, run by 128 lanes (ci = 0..127):
-//   source s (ci < SPM): Wz[s,t] = beta_t Wz[s,t-1] + w(s,t),  Ws[s,t] = alpha_t Ws[s,t-1] + eta_t Wz[s,t]
-//                        (w(s,t) = window weight of source s at target t), writing Ws[s, t-1] to
-//                        wsh[t * ldw + s] when WSH and the end values to wsend / wzend;
-//   ci == 127 (PREFIX):  b_t = beta_t b_{t-1}, a_t = alpha_t a_{t-1}, kappa_t = alpha_t kappa_{t-1} + eta_t b_t.
-// The values after token g.Lmid - 1 are also kept (wsmid, wzmid, midc) when g.Lmid > 0.
-// The scalars of 8 steps are read into registers before the 8 dependent steps run, so the chain
-// waits on LDS once per group instead of once per step.
-template <int CH, bool WSH, bool PREFIX = true, typename WT = float>
-__device__ __forceinline__ void chunk_coefficients(const Geom& g, ChunkScalars<CH>& sc, int L, int ci,
-                                                   WT* __restrict__ wsh, int ldw) {
-  constexpr int SPM = CH + kHaloPad;
-  static_assert(SPM <= 127 && CH % 8 == 0, "coefficient lanes");
-  const float* __restrict__ al = sc.alpha;
-  const float* __restrict__ et = sc.eta;
-  const float* __restrict__ be = sc.beta;
-  const float* __restrict__ wl = sc.wl;
-  const int H = g.H, e = g.e;
-  if (ci < SPM) {
-    const int s = ci;
-    const float us = g.gate_mode == GATE_TOKEN ? sc.ug[s] : 1.f;
-    const bool lag = g.gate_mode == GATE_LAG;
-    float ws = 0.f, wz = 0.f, wsm = 0.f, wzm = 0.f;
-    const int tm = g.Lmid - 1;
-    for (int t0 = 0; t0 < CH; t0 += 8) {
-      float al8[8], et8[8], be8[8], w8[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int t = t0 + u, j = t + H - s;
-        const bool on = j >= 0 && j < e && t < L;
-        const float wv = wl[on ? t * e + j : 0];
-        al8[u] = al[t]; et8[u] = et[t]; be8[u] = be[t];
-        w8[u] = on ? (lag ? wv : us) : 0.f;
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        if constexpr (WSH) wsh[(t0 + u) * ldw + s] = static_cast<WT>(ws);
-        wz = be8[u] * wz + w8[u];
-        ws = al8[u] * ws + et8[u] * wz;
-        wsm = (t0 + u == tm) ? ws : wsm;
-        wzm = (t0 + u == tm) ? wz : wzm;
-      }
-    }
-    sc.wsend[s] = ws;
-    sc.wzend[s] = wz;
-    sc.wsmid[s] = wsm;
-    sc.wzmid[s] = wzm;
-  } else if (PREFIX && ci == 127) {
-    float ac = 1.f, kc = 0.f, bc = 1.f, am = 0.f, km = 0.f, bm = 0.f;
-    const int tm = g.Lmid - 1;
-    for (int t0 = 0; t0 < CH; t0 += 8) {
-      float al8[8], et8[8], be8[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) { al8[u] = al[t0 + u]; et8[u] = et[t0 + u]; be8[u] = be[t0 + u]; }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        sc.acoef[t0 + u] = ac;
-        sc.kcoef[t0 + u] = kc;
-        bc = be8[u] * bc;
-        ac = al8[u] * ac;
-        kc = al8[u] * kc + et8[u] * bc;
-        am = (t0 + u == tm) ? ac : am;
-        km = (t0 + u == tm) ? kc : km;
-        bm = (t0 + u == tm) ? bc : bm;
-      }
-    }
-    sc.endc[0] = ac; sc.endc[1] = kc; sc.endc[2] = bc; sc.endc[3] = 0.f;
-    sc.midc[0] = am; sc.midc[1] = km; sc.midc[2] = bm; sc.midc[3] = 0.f;
-  }
-}
-
 }  // namespace atlas
