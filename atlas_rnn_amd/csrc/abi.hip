@@ -394,11 +394,11 @@ int atlas_mem_fwd(const atlas_mem_problem* prob, const atlas_mem_fwd_args* args,
   if ((p.gate_mode != ATLAS_GATE_NONE) != (args->gate != nullptr)) return ATLAS_MEM_ERR_ARG;
   if (p.has_buffer && !args->buffer_in) return ATLAS_MEM_ERR_NULL;
   if (p.window > 1 && !args->buffer_out) return ATLAS_MEM_ERR_NULL;
-  const size_t es = p.dtype == ATLAS_DT_BF16 ? 2 : 4;
+  // every pointer 16-byte aligned: the kernels move rows and states with 16-byte accesses
   const void* tp[] = {args->k, args->q, args->v, args->lr, args->decay, args->beta, args->gate, args->y};
-  for (const void* q : tp) if (misaligned(q, es)) return ATLAS_MEM_ERR_ALIGN;
+  for (const void* q : tp) if (misaligned(q, 16)) return ATLAS_MEM_ERR_ALIGN;
   const void* fp[] = {args->S_ref, args->S0, args->Z0, args->buffer_in, args->S_T, args->Z_T, args->buffer_out, saved};
-  for (const void* q : fp) if (misaligned(q, 4)) return ATLAS_MEM_ERR_ALIGN;
+  for (const void* q : fp) if (misaligned(q, 16)) return ATLAS_MEM_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
   return p.dtype == ATLAS_DT_BF16 ? run_fwd<bf16>(pl, args, saved, s) : run_fwd<float>(pl, args, saved, s);
 }
@@ -417,13 +417,12 @@ int atlas_mem_bwd(const atlas_mem_problem* prob, const atlas_mem_bwd_args* args,
   if ((p.gate_mode != ATLAS_GATE_NONE) != (args->gate != nullptr)) return ATLAS_MEM_ERR_ARG;
   if (p.gate_mode != ATLAS_GATE_NONE && !args->dgate) return ATLAS_MEM_ERR_NULL;
   if (p.has_buffer && (!args->buffer_in || !args->dbuffer_in)) return ATLAS_MEM_ERR_NULL;
-  const size_t es = p.dtype == ATLAS_DT_BF16 ? 2 : 4;
   const void* tp[] = {args->k, args->q, args->v, args->lr, args->decay, args->beta, args->gate, args->dy,
                       args->dk, args->dq, args->dv, args->dlr, args->ddecay, args->dbeta, args->dgate};
-  for (const void* q : tp) if (misaligned(q, es)) return ATLAS_MEM_ERR_ALIGN;
+  for (const void* q : tp) if (misaligned(q, 16)) return ATLAS_MEM_ERR_ALIGN;
   const void* fp[] = {args->S_ref, args->S0, args->Z0, args->buffer_in, args->dS_T, args->dZ_T, args->dbuffer_out,
                       args->dS_ref, args->dS0, args->dZ0, args->dbuffer_in, saved, workspace};
-  for (const void* q : fp) if (misaligned(q, 4)) return ATLAS_MEM_ERR_ALIGN;
+  for (const void* q : fp) if (misaligned(q, 16)) return ATLAS_MEM_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
   return p.dtype == ATLAS_DT_BF16 ? run_bwd<bf16>(pl, args, saved, workspace, s)
                                   : run_bwd<float>(pl, args, saved, workspace, s);

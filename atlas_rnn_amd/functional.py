@@ -120,10 +120,10 @@ class MemoryRecurrenceFn(torch.autograd.Function):
         bh, T, dk = k.shape
         dv_ = v.shape[-1]
         f32 = torch.float32
-        dy = dy.contiguous() if dy is not None else None
-        dS_T = dS_T.float().contiguous() if dS_T is not None else None
-        dZ_T = dZ_T.float().contiguous() if (dZ_T is not None and ctx.momentum and dZ_T.numel() > 0) else None
-        dbuf_out = dbuf_out.float().contiguous() if (dbuf_out is not None and dbuf_out.numel() > 0) else None
+        dy = _aligned(dy)
+        dS_T = _aligned(dS_T.float()) if dS_T is not None else None
+        dZ_T = _aligned(dZ_T.float()) if (dZ_T is not None and ctx.momentum and dZ_T.numel() > 0) else None
+        dbuf_out = _aligned(dbuf_out.float()) if (dbuf_out is not None and dbuf_out.numel() > 0) else None
         dk_ = torch.empty_like(k)
         dq_ = torch.empty_like(q)
         dv_t = torch.empty_like(v)
@@ -149,8 +149,16 @@ class MemoryRecurrenceFn(torch.autograd.Function):
                 dZ0 if Z0 is not None else None, dbuf_in, None)
 
 
+def _aligned(x: Tensor | None) -> Tensor | None:
+    """x contiguous with a 16-byte aligned start (the C ABI rejects other pointers)."""
+    if x is None:
+        return None
+    x = x.contiguous()
+    return x if x.data_ptr() % 16 == 0 else x.clone()
+
+
 def _canon(x: Tensor | None, dtype) -> Tensor | None:
-    return None if x is None else x.to(dtype).contiguous()
+    return None if x is None else _aligned(x.to(dtype))
 
 
 def memory_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,

@@ -106,6 +106,21 @@ def test_null_pointer_errors_before_launch(lib):
     assert lib.atlas_window_sum(0, 1, 4, 8, 0, 0, None, None, None) == 2
 
 
+def test_misaligned_pointers_error_before_launch(lib):
+    # validation happens before any HIP call: the (never dereferenced) addresses only have to be
+    # non-null; a pointer off a 16-byte boundary is rejected with ERR_ALIGN
+    p = _prob()
+    good, bad = 0x10000, 0x10008
+    fields = dict(k=good, q=good, v=good, lr=good, decay=good, beta=good, gate=good, S_ref=good, S0=good,
+                  Z0=good, y=good, S_T=good, Z_T=good, buffer_out=good)
+    for name in ("k", "lr", "S_ref", "S0", "buffer_out"):
+        f = dict(fields, **{name: bad})
+        args = _lib.FwdArgs(**{k: ctypes.c_void_p(v) for k, v in f.items()})
+        assert lib.atlas_mem_fwd(ctypes.byref(p), ctypes.byref(args), ctypes.c_void_p(good), None) == 5, name
+    args = _lib.FwdArgs(**{k: ctypes.c_void_p(v) for k, v in fields.items()})
+    assert lib.atlas_mem_fwd(ctypes.byref(p), ctypes.byref(args), ctypes.c_void_p(bad), None) == 5
+
+
 def test_cpu_tensors_are_rejected():
     torch = pytest.importorskip("torch")
     from atlas_rnn_amd.functional import memory_recurrence
