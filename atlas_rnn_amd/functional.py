@@ -161,6 +161,89 @@ def _canon(x: Tensor | None, dtype) -> Tensor | None:
     return None if x is None else _aligned(x.to(dtype))
 
 
+_BLOCK = 64    # block width of the decomposition for head sizes the kernels are not built for
+
+
+def _poly_map(x: Tensor, degree: int) -> Tensor:
+    """sum_{i=1..degree} x^i in (at least) fp32, rounded back to x's dtype (what the kernels apply
+    to each input element before its matrix products)."""
+    xf = x.to(torch.promote_types(x.dtype, torch.float32))
+    out, pw = xf, xf
+    for _ in range(2, degree + 1):
+        pw = pw * xf
+        out = out + pw
+    return out.to(x.dtype)
+
+
+def block_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
+                     beta: Tensor | None, gate: Tensor | None, S_ref: Tensor, S0: Tensor, Z0: Tensor | None,
+                     buffer: Tensor | None, *, window: int, map_mode: str, map_degree: int,
+                     clamp_every: int | None, clamp_final: bool, inner=None):
+    """The recurrence for head sizes above 64 or d_k != d_v, as 64 x 64 state blocks.
+
+    With the state split into blocks S[i, j] (rows 64 i .. of d_v, columns 64 j .. of d_k):
+      * delta_t = S_ref phi_t - v_t couples the column blocks only through delta, so delta is
+        formed once (one GEMM over all tokens) and every block runs the 64-wide recurrence with
+        S_ref = 0 and v = -delta[rows of i] (its own delta is then 0 . phi - v = delta);
+      * the block's update delta_i phi_j^T, decay, momentum, window and clamp are blockwise;
+      * y[rows of i] = sum_j S[i, j] psi_j.
+    The blocks are stacked along the head-batch axis ((i, j, bh) order) into ONE call of the
+    64-wide kernels; the per-token scalars are shared by all blocks. Gradients follow through the
+    stacking, the delta GEMM and the block sum (torch autograd). Head sizes that are not a multiple
+    of 64 are zero-padded (the padded rows / columns of every state stay zero).
+    `inner` runs the 64-wide recurrence (memory_recurrence by default).
+    """
+    inner = memory_recurrence if inner is None else inner
+    bh, T, dk = k.shape
+    dv = v.shape[-1]
+    nbk, nbv = -(-dk // _BLOCK), -(-dv // _BLOCK)
+    Dk, Dv = nbk * _BLOCK, nbv * _BLOCK
+    pad_k, pad_v = Dk - dk, Dv - dv
+    # the elementwise map is applied here (delta needs the mapped keys)
+    if map_mode == 'elementwise' and map_degree > 1:
+        k, q = _poly_map(k, map_degree), _poly_map(q, map_degree)
+    F = torch.nn.functional
+    phi, psi = F.pad(k, (0, pad_k)), F.pad(q, (0, pad_k))
+    vv = F.pad(v, (0, pad_v))
+    pst = lambda t: None if t is None else F.pad(t, (0, pad_k, 0, pad_v))
+    S_ref, S0, Z0, buffer = pst(S_ref), pst(S0), pst(Z0), pst(buffer)
+    # delta = S_ref phi - v (at least fp32), handed to every block as -v in the input dtype
+    acc = torch.promote_types(k.dtype, torch.float32)
+    delta = torch.matmul(phi.to(acc), S_ref.to(acc).transpose(-1, -2)) - vv.to(acc)
+    nv = (-delta).to(k.dtype)
+
+    def cols(x, j):            # [BH, T, Dk] -> feature block j
+        return x[..., j * _BLOCK:(j + 1) * _BLOCK]
+
+    def blk(x, i, j):          # [..., Dv, Dk] -> state block (i, j)
+        return x[..., i * _BLOCK:(i + 1) * _BLOCK, j * _BLOCK:(j + 1) * _BLOCK]
+
+    pairs = [(i, j) for i in range(nbv) for j in range(nbk)]
+    nb = len(pairs)
+    rep = lambda t: None if t is None else torch.cat([t] * nb, dim=0)
+    kb = torch.cat([cols(phi, j) for i, j in pairs], dim=0)
+    qb = torch.cat([cols(psi, j) for i, j in pairs], dim=0)
+    vb = torch.cat([nv[..., i * _BLOCK:(i + 1) * _BLOCK] for i, j in pairs], dim=0)
+    S0b = torch.cat([blk(S0, i, j) for i, j in pairs], dim=0)
+    Z0b = None if Z0 is None else torch.cat([blk(Z0, i, j) for i, j in pairs], dim=0)
+    Bb = None if buffer is None else torch.cat([blk(buffer, i, j) for i, j in pairs], dim=0)
+    Sref0 = torch.zeros_like(S0b)
+    y, S_T, Z_T, B = inner(kb, qb, vb, rep(lr), rep(decay), rep(beta), rep(gate), Sref0, S0b, Z0b, Bb,
+                           window=window, map_mode='off', map_degree=1, clamp_every=clamp_every,
+                           clamp_final=clamp_final)
+    # y: sum over the column blocks of each row block; states: blocks back in place
+    y = y.reshape(nbv, nbk, bh, T, _BLOCK).sum(dim=1).permute(1, 2, 0, 3).reshape(bh, T, Dv)
+
+    def unblock(x):            # [(i, j, bh), ..., 64, 64] -> [bh, ..., Dv, Dk]
+        if x is None:
+            return None
+        x = x.reshape(nbv, nbk, bh, *x.shape[1:])
+        x = torch.cat([torch.cat([x[i, j] for j in range(nbk)], dim=-1) for i in range(nbv)], dim=-2)
+        return x[..., :dv, :dk]
+
+    return y[..., :dv], unblock(S_T), unblock(Z_T), unblock(B)
+
+
 def memory_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
                       beta: Tensor | None = None, gate: Tensor | None = None,
                       S_ref: Tensor | None = None, S0: Tensor | None = None, Z0: Tensor | None = None,
@@ -168,7 +251,9 @@ def memory_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor
                       map_degree: int = 1, clamp_every: int | None = None, clamp_final: bool = True):
     """Memory-layer recurrence over [BH, T, d] inputs (atlas_pytorch/rnn_memory.py:605-730).
 
-    d_k == d_v <= 64; the kernels are built for 32 and 64, other head sizes are zero-padded.
+    The kernels are built for d_k == d_v in {32, 64}; smaller equal head sizes are zero-padded,
+    and larger or unequal ones (e.g. d_k = 128 after a tensor feature map, d_v = 64) run as
+    64 x 64 state blocks through `block_recurrence`.
     k, q: raw keys / queries [BH, T, d_k] (the elementwise polynomial map is applied inside);
     v [BH, T, d_v]; lr (eta), decay (alpha), beta [BH, T]; gate None | [BH, T] (per-token,
     reference omega_gate) | [BH, T, e] (per-lag); S_ref, S0, Z0 [BH, d_v, d_k];
@@ -183,6 +268,10 @@ def memory_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor
         S0 = torch.zeros(bh, dv, dk, device=dev, dtype=torch.float32)
     if S_ref is None:
         S_ref = S0
+    if dk != dv or dk > max(_KERNEL_DIMS):
+        return block_recurrence(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buffer, window=window,
+                                map_mode=map_mode, map_degree=map_degree, clamp_every=clamp_every,
+                                clamp_final=clamp_final)
     if dk == dv and dk < 64 and dk not in _KERNEL_DIMS:
         # Zero feature columns leave the recurrence exact: the padded rows / columns of every
         # state stay zero, the padded entries of y are zero and their gradients are dropped.

@@ -23,7 +23,7 @@ class Case:
     name: str
     BH: int
     T: int
-    d: int
+    d: int                           # d_k
     e: int = 1
     gate: str | None = None          # None | 'token' | 'lag'
     momentum: bool = True
@@ -36,6 +36,7 @@ class Case:
     seed: int = 0
     decay_shift: float = 2.0
     backward: bool = True
+    dv: int | None = None            # d_v (None: d_v = d_k)
     extra: dict = field(default_factory=dict)
 
 
@@ -43,9 +44,10 @@ def make_inputs(c: Case) -> dict:
     g = torch.Generator().manual_seed(1000 + c.seed)
     r = lambda *s: torch.randn(*s, generator=g, dtype=torch.float32)
     BH, T, d, e = c.BH, c.T, c.d, c.e
+    dv = c.dv or d
     k = r(BH, T, d)
     k = k / k.norm(dim=-1, keepdim=True)
-    p = dict(k=k, q=r(BH, T, d), v=r(BH, T, d),
+    p = dict(k=k, q=r(BH, T, d), v=r(BH, T, dv),
              decay=torch.sigmoid(r(BH, T) * 0.5 + c.decay_shift), lr=0.1 * torch.sigmoid(r(BH, T)))
     p["beta"] = torch.sigmoid(r(BH, T) * 0.5 + 1.0) if c.momentum else None
     if c.gate == 'token':
@@ -55,16 +57,16 @@ def make_inputs(c: Case) -> dict:
     else:
         p["gate"] = None
     s = c.states
-    z = lambda: torch.zeros(BH, d, d)
-    p["S_ref"] = s * r(BH, d, d) if s else z()
-    p["S0"] = s * r(BH, d, d) if s else z()
-    p["Z0"] = (s * r(BH, d, d) if s else z()) if c.momentum else None
-    p["buffer"] = (0.1 * r(BH, e - 1, d, d)) if (c.buffer and e > 1) else None
+    z = lambda: torch.zeros(BH, dv, d)
+    p["S_ref"] = s * r(BH, dv, d) if s else z()
+    p["S0"] = s * r(BH, dv, d) if s else z()
+    p["Z0"] = (s * r(BH, dv, d) if s else z()) if c.momentum else None
+    p["buffer"] = (0.1 * r(BH, e - 1, dv, d)) if (c.buffer and e > 1) else None
     # upstream gradients
-    p["gy"] = r(BH, T, d)
-    p["gS"] = r(BH, d, d)
-    p["gZ"] = r(BH, d, d) if c.momentum else None
-    p["gB"] = r(BH, e - 1, d, d) if e > 1 else None
+    p["gy"] = r(BH, T, dv)
+    p["gS"] = r(BH, dv, d)
+    p["gZ"] = r(BH, dv, d) if c.momentum else None
+    p["gB"] = r(BH, e - 1, dv, d) if e > 1 else None
     # round the dtype-carried tensors
     for key in ("k", "q", "v", "decay", "lr", "beta", "gate", "gy"):
         if p[key] is not None:

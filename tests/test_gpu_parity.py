@@ -63,6 +63,16 @@ CASES = [
     Case("bf16_walk_multiseg", BH=40, T=700, d=64, e=4, gate='lag', momentum=True, states=0.1, dtype=BF16, seed=25),
     Case("bf16_walk_map3", BH=2, T=200, d=64, e=4, gate='lag', momentum=True, states=0.1, map_degree=3,
          dtype=BF16, seed=26),
+    # head sizes above 64 / d_k != d_v (64 x 64 state blocks stacked along BH): the BASELINE C4 shape
+    # class (d_k = 128 after the tensor map, d_v = 64, e = 8, elementwise map of degree 3)
+    Case("c4_reduced_fp32_dk128_dv64", BH=4, T=300, d=128, dv=64, e=8, gate='lag', momentum=True, states=0.1,
+         map_degree=3, seed=27),
+    Case("c4_reduced_bf16_dk128_dv64", BH=4, T=300, d=128, dv=64, e=8, gate='lag', momentum=True, states=0.1,
+         map_degree=3, dtype=BF16, seed=28),
+    Case("bf16_dk96_dv80_buffer", BH=2, T=150, d=96, dv=80, e=4, gate='token', momentum=True, buffer=True,
+         states=0.1, dtype=BF16, seed=29),
+    Case("fp32_dk128_dv128_clamp", BH=2, T=96, d=128, e=2, gate='token', momentum=True, states=0.2,
+         clamp_every=32, seed=30),
 ]
 
 
@@ -92,7 +102,7 @@ def test_mfma_tile_layout():
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: c.name)
 def test_recurrence_parity(case):
-    _say(f"case {case.name}: BH={case.BH} T={case.T} d={case.d} e={case.e} gate={case.gate} "
+    _say(f"case {case.name}: BH={case.BH} T={case.T} d={case.d} dv={case.dv or case.d} e={case.e} gate={case.gate} "
          f"mom={case.momentum} buf={case.buffer} dtype={case.dtype}")
     p = make_inputs(case)
     ref_out, ref_grads = run_oracle(case, p)
