@@ -132,16 +132,19 @@ struct Plan {
   int status;
 };
 
-// Segments per head-batch row: enough (segment, bh) workgroups to cover the 256 CUs twice;
-// a single segment when S is clamped at scan_chunk_len boundaries (not affine).
+// Segments per head-batch row: enough (segment, bh) workgroups for one per CU (the walks hold a
+// CU's LDS, so a second round of workgroups would only queue behind the first); a single segment
+// when S is clamped at scan_chunk_len boundaries (not affine). The CU count is MI355X's, fixed so
+// that the saved / workspace sizes do not depend on the device queried.
 // ATLAS_MEM_SEG_CHUNKS overrides the chunks per segment (tuning).
+constexpr int kCUs = 256;
 SegGeom make_seg(const Geom& g) {
   SegGeom s{};
   int G;
   if (g.clamp_every > 0) {
     G = g.nc;
   } else {
-    const int want = g.BH >= 512 ? 1 : (512 + g.BH - 1) / g.BH;
+    const int want = g.BH >= kCUs ? 1 : (kCUs + g.BH - 1) / g.BH;
     G = (g.nc + want - 1) / want;
     if (const char* env = std::getenv("ATLAS_MEM_SEG_CHUNKS")) {
       const int v = std::atoi(env);
