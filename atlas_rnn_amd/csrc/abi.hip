@@ -12,6 +12,9 @@
 #include <cstdlib>
 
 namespace atlas {
+template <typename T, int CHF, int CHB>
+hipError_t launch_chunk_coef_pair(const Geom& gf, const Geom& gb, const T* decay, const T* lr, const T* beta,
+                                  const T* gate, float* rec_f, T* wsh_f, float* rec_b, T* wsh_b, hipStream_t stream);
 template <typename T, int CH, int D>
 hipError_t launch_fwd_seg(const Geom&, const FwdPtrs<T>&, const SegGeom&, float*, float*, float*, float*, float*,
                           T*, hipStream_t);
@@ -221,7 +224,7 @@ size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 // `saved` layout: segment-start states, segment aggregates (forward scratch), raw S_{T-1}, the raw
 // state at every backward-chunk boundary (written by the forward walk, read by the backward).
 struct SavedLayout {
-  size_t seg, agg, final_raw, rw, coef, wsh, total;
+  size_t seg, agg, final_raw, rw, coef, wsh, bcoef, bwsh, total;
 };
 
 // floats per chunk coefficient record (acoef, kcoef, endc, wsend, wzend, wsmid, wzmid, midc)
@@ -242,14 +245,17 @@ SavedLayout saved_layout(const Plan& pl) {
   // forward scratch: per-chunk coefficient records and Ws[s, t-1] blocks
   L.coef = off; off += align256((size_t)g.BH * g.nc * coef_rec_floats(pl.CH) * sizeof(float));
   L.wsh = off; off += align256((size_t)g.BH * g.nc * pl.CH * (pl.CH + kHaloPad) * pl.esize);
+  // the backward's chunk records (input-only: formed in the forward's coefficient launch)
+  L.bcoef = off; off += align256((size_t)g.BH * pl.gb.nc * coef_rec_floats(pl.CHB) * sizeof(float));
+  L.bwsh = off; off += align256((size_t)g.BH * pl.gb.nc * pl.CHB * (pl.CHB + kHaloPad) * pl.esize);
   L.total = off;
   return L;
 }
 
-// backward workspace: adjoint aggregates, re-walk chunk states, dS_ref partials, boundary partials,
-// token-gate (target, lag) gradients.
+// backward workspace: adjoint aggregates, segment-end adjoints, dS_ref partials, boundary partials,
+// token-gate (target, lag) gradients, the scalar-gradient inputs.
 struct BwdLayout {
-  size_t agg, segadj, dsref, tail, halo, dw, coef, wsh, scal, total;
+  size_t agg, segadj, dsref, tail, halo, dw, scal, total;
 };
 
 BwdLayout bwd_layout(const Plan& pl) {
@@ -264,8 +270,6 @@ BwdLayout bwd_layout(const Plan& pl) {
   L.tail = off; off += align256((size_t)g.BH * nseg * g.H * (g.DV + g.DK) * sizeof(float));
   L.halo = off; off += align256((size_t)g.BH * nseg * g.H * (g.DV + g.DK) * sizeof(float));
   L.dw = off; off += align256(g.gate_mode == ATLAS_GATE_TOKEN ? (size_t)g.BH * g.T * g.e * sizeof(float) : 0);
-  L.coef = off; off += align256((size_t)g.BH * g.nc * coef_rec_floats(pl.CHB) * sizeof(float));
-  L.wsh = off; off += align256((size_t)g.BH * g.nc * pl.CHB * (pl.CHB + kHaloPad) * pl.esize);
   L.scal = off; off += align256((size_t)g.BH * g.nc * scalar_block_floats(pl.CHB) * sizeof(float));
   L.total = off;
   return L;
@@ -289,7 +293,13 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
   float* coef = reinterpret_cast<float*>(sv + SL.coef);
   T* wsh = reinterpret_cast<T*>(sv + SL.wsh);
   const Geom& g = pl.g;
-  hipError_t err = hipErrorInvalidValue;
+  // chunk coefficient records of the forward and of the backward (one launch, inputs only)
+  constexpr int CHF = sizeof(T) == 2 ? 64 : 32, CHB = sizeof(T) == 2 ? 32 : 16;
+  hipError_t err = launch_chunk_coef_pair<T, CHF, CHB>(g, pl.gb, a.decay, a.lr, a.beta, a.gate, coef, wsh,
+                                                       reinterpret_cast<float*>(sv + SL.bcoef),
+                                                       reinterpret_cast<T*>(sv + SL.bwsh), s);
+  if (err != hipSuccess) return ATLAS_MEM_ERR_LAUNCH;
+  err = hipErrorInvalidValue;
   if (g.DK == 64) {
     if constexpr (sizeof(T) == 2) {
       if (!force_generic() && walk_fwd_supported(g))
@@ -332,9 +342,10 @@ int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, voi
   p.tail_part = gb.H > 0 ? reinterpret_cast<float*>(w + L.tail) : nullptr;
   p.halo_part = gb.H > 0 ? reinterpret_cast<float*>(w + L.halo) : nullptr;
   p.dw = gb.gate_mode == ATLAS_GATE_TOKEN ? reinterpret_cast<float*>(w + L.dw) : nullptr;
-  p.coef = reinterpret_cast<float*>(w + L.coef);
+  // formed by the forward (read only here)
+  p.coef = const_cast<float*>(reinterpret_cast<const float*>(sv + SL.bcoef));
+  p.wsh = const_cast<unsigned char*>(sv + SL.bwsh);
   p.scal = reinterpret_cast<float*>(w + L.scal);
-  p.wsh = w + L.wsh;
   hipError_t err = hipErrorInvalidValue;
   // the specialised walks run as a pair: the forward saved its states in their layout
   const bool walk = sizeof(T) == 2 && !force_generic() && walk_fwd_supported(pl.g);

@@ -1,9 +1,10 @@
 // coef.hip - per-chunk coefficients of the chunked closed form, for every chunk of every row.
 //
 // The coefficients of a chunk depend only on its decay / lr / beta / gate values, never on the
-// states, so they are formed here ahead of the segment walks, with one small workgroup per
+// states, so they are formed here ahead of the segment walks, with one small thread group per
 // (chunk, bh) and many workgroups per CU: the step-by-step recurrences that would otherwise sit on
-// a walk's critical path overlap across chunks. Per chunk:
+// a walk's critical path overlap across chunks. One launch in the forward forms the records of
+// the forward chunks and of the backward chunks (k_chunk_coef_pair). Per chunk:
 //   record (fp32): acoef[CH] = a_{t-1}, kcoef[CH] = kappa_{t-1}, endc = (a, kappa, b) of the chunk,
 //                  wsend[SPM] = Ws[s, end], wzend[SPM] = Wz[s, end]
 //   wsh (T):       Ws[s, t-1] as [CH][SPM] (optional)
@@ -42,12 +43,13 @@ struct CoefSmem {
 //   mid values: after token Lmid - 1 (a multiple of 8) when Lmid > 0, else zero.
 // The inputs (step scalars, and the gates of windows up to 4 NT / CH) are loaded together, ahead
 // of the first barrier.
+// Chunk c of row bh, by coef_threads<CH>() threads (tid) with the LDS block sm. Every thread of
+// the workgroup reaches the same barriers, whichever chunk (and chunk length) its group works on.
 template <typename T, int CH, bool WSH>
-__global__ __launch_bounds__(coef_threads<CH>()) void k_chunk_coef(const Geom g, const T* __restrict__ decay,
-                                                                    const T* __restrict__ lr,
-                                                                    const T* __restrict__ beta,
-                                                                    const T* __restrict__ gate,
-                                                                    float* __restrict__ rec_all, T* __restrict__ wsh) {
+__device__ __forceinline__ void chunk_coef(const Geom& g, const T* __restrict__ decay, const T* __restrict__ lr,
+                                           const T* __restrict__ beta, const T* __restrict__ gate,
+                                           float* __restrict__ rec_all, T* __restrict__ wsh, int c, int bh, int tid,
+                                           CoefSmem<CH>& sm) {
   constexpr int SPM = CH + kHaloPad, NT = coef_threads<CH>(), REC = CoefRec<CH>::SIZE;
   constexpr int R_KCOEF = CH, R_ENDC = 2 * CH, R_WSEND = R_ENDC + 4, R_WZEND = R_WSEND + SPM,
                 R_WSMID = R_WZEND + SPM, R_WZMID = R_WSMID + SPM, R_MIDC = R_WZMID + SPM;
@@ -55,8 +57,7 @@ __global__ __launch_bounds__(coef_threads<CH>()) void k_chunk_coef(const Geom g,
   constexpr int LA = SPM - 2, LK = SPM - 1;   // prefix lanes
   static_assert(R_MIDC + 4 == REC, "record layout");
   static_assert(CH <= 64 && (CH & (CH - 1)) == 0 && CH % 8 == 0 && NT % CH == 0 && SPM % 8 == 0, "lanes");
-  __shared__ CoefSmem<CH> sm;
-  const int c = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x, lane = lane_id();
+  const int lane = tid & 63;
   const int H = g.H, e = g.e;
   const int t0 = c * g.Lc, L = min(g.T, t0 + g.Lc) - t0;
   const size_t tb = (size_t)bh * g.T, r0 = tb + t0;
@@ -245,29 +246,47 @@ __global__ __launch_bounds__(coef_threads<CH>()) void k_chunk_coef(const Geom g,
   }
 }
 
-template <typename T, int CH>
-hipError_t launch_chunk_coef(const Geom& g, const T* decay, const T* lr, const T* beta, const T* gate, float* rec,
-                             T* wsh, int kid, hipStream_t stream) {
-  if (g.Lmid % 8 != 0 || g.Lmid > CH) return hipErrorInvalidValue;   // mid values are taken per 8 steps
-  prof_begin(kid, stream);
-  if (wsh) {
-    hipLaunchKernelGGL((k_chunk_coef<T, CH, true>), dim3(g.nc, g.BH), dim3(coef_threads<CH>()), 0, stream, g, decay, lr,
-                       beta, gate, rec, wsh);
+// Forward (CHF) and backward (CHB) chunk records in one launch: workgroups x < gf.nc form forward
+// chunks, the others PER backward chunks each (one thread group per chunk; a group past the last
+// chunk repeats it, writing the same values). Both depend only on the per-token scalars.
+template <typename T, int CHF, int CHB>
+__global__ __launch_bounds__(coef_threads<CHF>()) void k_chunk_coef_pair(
+    const Geom gf, const Geom gb, const T* __restrict__ decay, const T* __restrict__ lr, const T* __restrict__ beta,
+    const T* __restrict__ gate, float* __restrict__ rec_f, T* __restrict__ wsh_f, float* __restrict__ rec_b,
+    T* __restrict__ wsh_b) {
+  constexpr int NTB = coef_threads<CHB>(), PER = coef_threads<CHF>() / NTB;
+  static_assert(coef_threads<CHF>() % NTB == 0, "backward groups per workgroup");
+  __shared__ union U {
+    CoefSmem<CHF> f;
+    CoefSmem<CHB> b[PER];
+  } sm;
+  const int x = blockIdx.x, bh = blockIdx.y;
+  if (x < gf.nc) {
+    chunk_coef<T, CHF, true>(gf, decay, lr, beta, gate, rec_f, wsh_f, x, bh, threadIdx.x, sm.f);
   } else {
-    hipLaunchKernelGGL((k_chunk_coef<T, CH, false>), dim3(g.nc, g.BH), dim3(coef_threads<CH>()), 0, stream, g, decay, lr,
-                       beta, gate, rec, wsh);
+    const int j = threadIdx.x / NTB;
+    const int c = min((x - gf.nc) * PER + j, gb.nc - 1);
+    chunk_coef<T, CHB, true>(gb, decay, lr, beta, gate, rec_b, wsh_b, c, bh, threadIdx.x % NTB, sm.b[j]);
   }
-  prof_end(kid, stream);
+}
+
+template <typename T, int CHF, int CHB>
+hipError_t launch_chunk_coef_pair(const Geom& gf, const Geom& gb, const T* decay, const T* lr, const T* beta,
+                                  const T* gate, float* rec_f, T* wsh_f, float* rec_b, T* wsh_b, hipStream_t stream) {
+  if (gf.Lmid % 8 != 0 || gf.Lmid > CHF || gb.Lmid != 0) return hipErrorInvalidValue;
+  constexpr int PER = coef_threads<CHF>() / coef_threads<CHB>();
+  prof_name(KID_FWD_COEF, "k_chunk_coef_pair");
+  prof_begin(KID_FWD_COEF, stream);
+  hipLaunchKernelGGL((k_chunk_coef_pair<T, CHF, CHB>), dim3(gf.nc + (gb.nc + PER - 1) / PER, gf.BH),
+                     dim3(coef_threads<CHF>()), 0, stream, gf, gb, decay, lr, beta, gate, rec_f, wsh_f, rec_b, wsh_b);
+  prof_end(KID_FWD_COEF, stream);
   return hipGetLastError();
 }
 
-#define ATLAS_INST_COEF(T, CH)                                                                        \
-  template hipError_t launch_chunk_coef<T, CH>(const Geom&, const T*, const T*, const T*, const T*, float*, \
-                                               T*, int, hipStream_t);
-
-ATLAS_INST_COEF(bf16, 64)
-ATLAS_INST_COEF(float, 32)
-ATLAS_INST_COEF(bf16, 32)
-ATLAS_INST_COEF(float, 16)
+template hipError_t launch_chunk_coef_pair<bf16, 64, 32>(const Geom&, const Geom&, const bf16*, const bf16*, const bf16*,
+                                                         const bf16*, float*, bf16*, float*, bf16*, hipStream_t);
+template hipError_t launch_chunk_coef_pair<float, 32, 16>(const Geom&, const Geom&, const float*, const float*,
+                                                          const float*, const float*, float*, float*, float*, float*,
+                                                          hipStream_t);
 
 }  // namespace atlas

@@ -22,9 +22,6 @@
 namespace atlas {
 
 template <typename T, int CH>
-hipError_t launch_chunk_coef(const Geom& g, const T* decay, const T* lr, const T* beta, const T* gate, float* rec,
-                             T* wsh, int kid, hipStream_t stream);
-template <typename T, int CH>
 hipError_t launch_bwd_scalar(const Geom& g, const BwdPtrs<T>& a, const BwdSegPtrs& p, hipStream_t stream);
 
 // ---------------------------------------------------------------------------------------------
@@ -945,9 +942,8 @@ hipError_t launch_scalar_chain(const Geom& g, const BwdPtrs<bf16>& a, const BwdS
 template <typename T, int CH, int D>
 hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg, const BwdSegPtrs& p,
                           hipStream_t stream, bool walk) {
-  hipError_t err = launch_chunk_coef<T, CH>(g, a.decay, a.lr, a.beta, a.gate, p.coef, reinterpret_cast<T*>(p.wsh),
-                                            KID_BWD_COEF, stream);
-  if (err != hipSuccess) return err;
+  // the chunk coefficient records p.coef / p.wsh were formed by the forward (input-only)
+  hipError_t err = hipSuccess;
   if (sg.nseg > 1) {
     const size_t smem = sizeof(BwdAggSmem<T, CH, D>);
     err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bwd_seg_agg<T, CH, D>),

@@ -30,10 +30,6 @@
 
 namespace atlas {
 
-template <typename T, int CH>
-hipError_t launch_chunk_coef(const Geom& g, const T* decay, const T* lr, const T* beta, const T* gate, float* rec,
-                             T* wsh, int kid, hipStream_t stream);
-
 // Two workgroups per CU (16 waves, at most 128 VGPRs each) for the bf16 configurations, whose
 // aggregate-pass LDS fits twice in 160 KB.
 template <typename T, int CH, int D>
@@ -102,8 +98,8 @@ __global__ __launch_bounds__(kSegThreads) void k_fwd_seg(const Geom g, const Fwd
 template <typename T, int CH, int D>
 hipError_t launch_fwd_seg(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg, float* agg, float* seg_states,
                           float* rw, float* final_raw, float* coef, T* wsh, hipStream_t stream) {
-  hipError_t err = launch_chunk_coef<T, CH>(g, a.decay, a.lr, a.beta, a.gate, coef, wsh, KID_FWD_COEF, stream);
-  if (err != hipSuccess) return err;
+  // the chunk coefficient records (coef, wsh) are formed by the caller first
+  hipError_t err = hipSuccess;
   if (sg.nseg > 1) {
     const size_t smem = sizeof(SegFwdSmem<T, CH, D, false>);
     err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_seg_agg<T, CH, D>),

@@ -471,9 +471,6 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_full(const Geom g, const F
   walk_fwd<true, MAPE>(g, a, sg, nullptr, seg_states, rw, final_raw, coef, wsh, smem_raw);
 }
 
-template <typename T, int CH>
-hipError_t launch_chunk_coef(const Geom& g, const T* decay, const T* lr, const T* beta, const T* gate, float* rec,
-                             T* wsh, int kid, hipStream_t stream);
 template <int D>
 hipError_t launch_fwd_seg_scan(const Geom& g, const float* S0, const float* Z0, const SegGeom& sg, const float* agg,
                                float* seg_states, hipStream_t stream);
@@ -516,8 +513,7 @@ static hipError_t launch_walks(const Geom& g, const FwdPtrs<bf16>& a, const SegG
 
 hipError_t launch_walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
                            float* rw, float* final_raw, float* coef, bf16* wsh, hipStream_t stream) {
-  hipError_t err = launch_chunk_coef<bf16, wf::CH>(g, a.decay, a.lr, a.beta, a.gate, coef, wsh, KID_FWD_COEF, stream);
-  if (err != hipSuccess) return err;
+  // the chunk coefficient records (coef, wsh) are formed by the caller first
   return g.map_mode == MAP_ELEMENTWISE
              ? launch_walks<true>(g, a, sg, agg, seg_states, rw, final_raw, coef, wsh, stream)
              : launch_walks<false>(g, a, sg, agg, seg_states, rw, final_raw, coef, wsh, stream);

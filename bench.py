@@ -59,8 +59,8 @@ def algorithmic_bytes(bh=BH, t=T, d=D, e=E, s_in=2, s_st=4):
         # passes read the per-token scalars once
         "k_fwd_seg_scan": 0,
         "k_bwd_seg_scan": 0,
-        "k_chunk_coef_fwd": n * n_sc * s_in,
-        "k_chunk_coef_bwd": n * n_sc * s_in,
+        # forward and backward chunk records in one launch (reads the per-token scalars once)
+        "k_chunk_coef_pair": n * n_sc * s_in,
     }
     # the specialised bf16 d = 64 path launches these kernels for the same stages
     for spec, gen in (("k_walk_agg", "k_fwd_seg_agg"), ("k_walk_full", "k_fwd_seg"), ("k_walk_bwd", "k_bwd_seg"),
