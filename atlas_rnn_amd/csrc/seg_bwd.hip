@@ -18,6 +18,7 @@
 #include "mem_common.h"
 #include "mem_params.h"
 #include "seg_common.h"
+#include "seg_fixup.h"
 
 namespace atlas {
 
@@ -823,100 +824,8 @@ __global__ __launch_bounds__(kThreads) void k_bwd_seg_scan(const Geom g, const f
 template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void k_bwd_seg_fixup(const Geom g, const BwdPtrs<T> a, const SegGeom sg,
                                                               const BwdSegPtrs p, int reduce_dsref) {
-  __shared__ float sphi[D], sdel[D], sdd[D], sdb[D];
-  const int seg = blockIdx.x, bh = blockIdx.y;
-  const int H = g.H, e = g.e;
-  const int c_begin = seg * sg.G, c_end = min(g.nc, c_begin + sg.G);
-  const int tok0 = c_begin * g.Lc, tok1 = min(g.T, c_end * g.Lc);
-  const size_t tb = (size_t)bh * g.T;
-  const int tid = threadIdx.x;
-  if (reduce_dsref) {
-    const int per = (D * D + sg.nseg - 1) / sg.nseg;
-    const int i0 = seg * per, i1 = min(D * D, i0 + per);
-    const float* part = p.dsref_part + (size_t)bh * sg.nseg * D * D;
-    for (int idx = i0 + tid; idx < i1; idx += kThreads) {
-      float acc = 0.f;
-      for (int s0 = 0; s0 < sg.nseg; s0 += 8) {   // eight partials per memory round trip
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = part[(size_t)min(s0 + u, sg.nseg - 1) * D * D + idx];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) acc += s0 + u < sg.nseg ? v[u] : 0.f;
-      }
-      a.dS_ref[(size_t)bh * D * D + idx] = acc;
-    }
-  }
-  // token-gate gradient du_p = sum_j dw[p + j, j] (the d buffer_out term is added below)
-  if (g.gate_mode == GATE_TOKEN) {
-    for (int pp = tok0 + tid; pp < tok1; pp += kThreads) {
-      if (a.dbuf_out && pp >= g.T - H) continue;
-      float du = 0.f;
-      for (int j = 0; j < e && pp + j < g.T; ++j) du += p.dw[(tb + pp + j) * e + j];
-      a.dgate[tb + pp] = from_f32<T>(du);
-    }
-  }
-  if (H == 0) return;
-  const int tail0 = tok1 - H;
-  const bool has_next = seg + 1 < sg.nseg;
-  for (int h = 0; h < H; ++h) {
-    const int pp = tail0 + h;
-    if (pp < tok0) continue;                       // token of the previous segment (short last segment)
-    const size_t tp = (((size_t)bh * sg.nseg + seg) * H + h) * (2 * D);
-    const size_t hp = has_next ? (((size_t)bh * sg.nseg + seg + 1) * H + h) * (2 * D) : 0;
-    const bool outbuf = (a.dbuf_out != nullptr) && (pp >= g.T - H);
-    const int kb = pp - (g.T - H);
-    __syncthreads();
-    if (outbuf) {
-      for (int k = tid; k < D; k += kThreads) sphi[k] = ld_map(a.k, (tb + pp) * D + k, g.map_mode, g.map_deg);
-      __syncthreads();
-      const float cp = (g.gate_mode == GATE_TOKEN) ? to_f32(a.gate[tb + pp]) : 1.f;
-      const float* dB = a.dbuf_out + ((size_t)bh * H + kb) * D * D;
-      const float* Sr = a.S_ref + (size_t)bh * D * D;
-      for (int i = tid; i < D; i += kThreads) {
-        float acc = 0.f, accd = 0.f;
-        for (int k = 0; k < D; ++k) { acc += Sr[(size_t)i * D + k] * sphi[k]; accd += dB[(size_t)i * D + k] * sphi[k]; }
-        sdel[i] = acc - to_f32(a.v[(tb + pp) * D + i]);
-        sdb[i] = accd;
-        sdd[i] = cp * accd;
-      }
-      __syncthreads();
-      if (tid == 0 && g.gate_mode == GATE_TOKEN) {
-        float du = 0.f;
-        for (int i = 0; i < D; ++i) du += sdel[i] * sdb[i];
-        for (int j = 0; j < e && pp + j < g.T; ++j) du += p.dw[(tb + pp + j) * e + j];
-        a.dgate[tb + pp] = from_f32<T>(du);
-      }
-      float* dsr = p.dsref_part + ((size_t)bh * sg.nseg + seg) * D * D;
-      for (int idx = tid; idx < D * D; idx += kThreads) dsr[idx] += sdd[idx / D] * sphi[idx % D];
-    }
-    for (int i = tid; i < D; i += kThreads) {
-      float val = p.tail_part[tp + i] + (has_next ? p.halo_part[hp + i] : 0.f);
-      if (outbuf) val -= sdd[i];
-      a.dv[(tb + pp) * D + i] = from_f32<T>(val);
-    }
-    for (int k = tid; k < D; k += kThreads) {
-      float val = p.tail_part[tp + D + k] + (has_next ? p.halo_part[hp + D + k] : 0.f);
-      if (outbuf) {
-        const float cp = (g.gate_mode == GATE_TOKEN) ? to_f32(a.gate[tb + pp]) : 1.f;
-        const float* dB = a.dbuf_out + ((size_t)bh * H + kb) * D * D;
-        const float* Sr = a.S_ref + (size_t)bh * D * D;
-        float acc = 0.f;
-        for (int i = 0; i < D; ++i) acc += cp * dB[(size_t)i * D + k] * sdel[i] + Sr[(size_t)i * D + k] * sdd[i];
-        val += acc;
-      }
-      if (g.map_mode == MAP_ELEMENTWISE) val *= poly_map_grad(to_f32(a.k[(tb + pp) * D + k]), g.map_deg);
-      a.dk[(tb + pp) * D + k] = from_f32<T>(val);
-    }
-  }
-  // buffer pass-through when T < e - 1: buffer_out[k'] = buffer_in[T + k']
-  if (seg == 0 && a.dbuf_out && a.dbuf_in && g.T < H) {
-    __syncthreads();
-    for (int kq = 0; kq + g.T < H; ++kq) {
-      const float* src = a.dbuf_out + ((size_t)bh * H + kq) * D * D;
-      float* dstb = a.dbuf_in + ((size_t)bh * H + g.T + kq) * D * D;
-      for (int idx = tid; idx < D * D; idx += kThreads) dstb[idx] += src[idx];
-    }
-  }
+  if (a.dbuf_out) bwd_seg_fixup<T, D, true>(g, a, sg, p, reduce_dsref, blockIdx.x, blockIdx.y);
+  else bwd_seg_fixup<T, D, false>(g, a, sg, p, reduce_dsref, blockIdx.x, blockIdx.y);
 }
 
 // dS_ref = sum over segments of the partials.   grid (D*D/256, BH)
@@ -936,7 +845,8 @@ size_t bwd_seg_smem_bytes(int H) {
 
 hipError_t launch_walk_bwd_kernel(const Geom& g, const BwdPtrs<bf16>& a, const SegGeom& sg, const BwdSegPtrs& p,
                                   hipStream_t stream);
-hipError_t launch_scalar_chain(const Geom& g, const BwdPtrs<bf16>& a, const BwdSegPtrs& p, hipStream_t stream);
+hipError_t launch_scalar_chain(const Geom& g, const BwdPtrs<bf16>& a, const BwdSegPtrs& p, const SegGeom& sg,
+                               bool with_fixup, hipStream_t stream);
 
 // walk: run the specialised reverse walk (walk_bwd.hip, bf16 with d = 64 only) in place of k_bwd_seg
 template <typename T, int CH, int D>
@@ -979,17 +889,21 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
     prof_end(KID_BWD_CHUNK, stream);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
+  // the specialised path runs the fixup inside the scalar-chain launch when the two are independent
+  // (no token gates, whose gradients the fixup forms from the chains' output; no buffer_out gradient)
+  const int fused_reduce = a.dbuf_out == nullptr;
+  const bool fixup_in_chain = walk && fused_reduce && g.gate_mode != GATE_TOKEN;
   if constexpr (sizeof(T) == 2 && CH == 32 && D == 64) {
     if (walk) {
-      prof_name(KID_BWD_SCALAR, "k_scalar_chain");
+      prof_name(KID_BWD_SCALAR, fixup_in_chain ? "k_scalar_chain+fixup" : "k_scalar_chain");
       prof_begin(KID_BWD_SCALAR, stream);
-      err = launch_scalar_chain(g, a, p, stream);
+      err = launch_scalar_chain(g, a, p, sg, fixup_in_chain, stream);
       prof_end(KID_BWD_SCALAR, stream);
       if (err != hipSuccess) return err;
     }
   }
   if (!walk && (err = launch_bwd_scalar<T, CH>(g, a, p, stream)) != hipSuccess) return err;
-  const int fused_reduce = a.dbuf_out == nullptr;
+  if (fixup_in_chain) return hipSuccess;
   prof_begin(KID_BWD_FIXUP, stream);
   hipLaunchKernelGGL((k_bwd_seg_fixup<T, D>), dim3(sg.nseg, g.BH), dim3(kThreads), 0, stream, g, a, sg, p,
                      fused_reduce);

@@ -20,6 +20,7 @@
 #include "mem_common.h"
 #include "mem_params.h"
 #include "seg_common.h"
+#include "seg_fixup.h"
 #include "walk_common.h"
 
 namespace atlas {
@@ -672,9 +673,17 @@ __device__ __forceinline__ float quad_sum(float x) {
 }
 }  // namespace wb
 
+// Workgroups x >= nchain run the segment fixup of segment x - nchain instead (seg_fixup.h): both
+// read only what the reverse walk wrote, so one launch carries both.
+static_assert(64 * wb::kChainWaves == kThreads, "the fixup workgroups share the launch's block size");
 __global__ __launch_bounds__(64 * wb::kChainWaves) void k_scalar_chain(const Geom g, const BwdPtrs<bf16> a,
-                                                                         const BwdSegPtrs p) {
+                                                                         const BwdSegPtrs p, const SegGeom sg,
+                                                                         int nchain) {
   using namespace wb;
+  if ((int)blockIdx.x >= nchain) {   // workgroup-uniform
+    bwd_seg_fixup<bf16, D, false>(g, a, sg, p, 1, blockIdx.x - nchain, blockIdx.y);
+    return;
+  }
   __shared__ ChainSmem smc;
   const int lane = lane_id();
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -813,9 +822,13 @@ __global__ __launch_bounds__(64 * wb::kChainWaves) void k_scalar_chain(const Geo
   }
 }
 
-hipError_t launch_scalar_chain(const Geom& g, const BwdPtrs<bf16>& a, const BwdSegPtrs& p, hipStream_t stream) {
-  hipLaunchKernelGGL(k_scalar_chain, dim3((g.nc + wb::kChainWaves - 1) / wb::kChainWaves, g.BH),
-                     dim3(64 * wb::kChainWaves), 0, stream, g, a, p);
+// with_fixup: the launch also runs the segment fixup (valid without token gates, whose gradients
+// the fixup forms from the chains' output, and without a buffer_out gradient)
+hipError_t launch_scalar_chain(const Geom& g, const BwdPtrs<bf16>& a, const BwdSegPtrs& p, const SegGeom& sg,
+                               bool with_fixup, hipStream_t stream) {
+  const int nchain = (g.nc + wb::kChainWaves - 1) / wb::kChainWaves;
+  hipLaunchKernelGGL(k_scalar_chain, dim3(nchain + (with_fixup ? sg.nseg : 0), g.BH), dim3(64 * wb::kChainWaves), 0,
+                     stream, g, a, p, sg, nchain);
   return hipGetLastError();
 }
 

@@ -37,6 +37,7 @@ class Case:
     decay_shift: float = 2.0
     backward: bool = True
     dv: int | None = None            # d_v (None: d_v = d_k)
+    grad_buffer: bool = True         # the loss includes buffer_out (False: no buffer_out gradient)
     extra: dict = field(default_factory=dict)
 
 
@@ -67,6 +68,8 @@ def make_inputs(c: Case) -> dict:
     p["gS"] = r(BH, dv, d)
     p["gZ"] = r(BH, dv, d) if c.momentum else None
     p["gB"] = r(BH, e - 1, dv, d) if e > 1 else None
+    if not c.grad_buffer:
+        p["gB"] = None
     # round the dtype-carried tensors
     for key in ("k", "q", "v", "decay", "lr", "beta", "gate", "gy"):
         if p[key] is not None:
@@ -82,7 +85,7 @@ def _loss(out, p):
     loss = (y * p["gy"]).sum() + (S_T * p["gS"]).sum()
     if Z_T is not None:
         loss = loss + (Z_T * p["gZ"]).sum()
-    if B is not None:
+    if B is not None and p["gB"] is not None:
         loss = loss + (B * p["gB"]).sum()
     return loss
 

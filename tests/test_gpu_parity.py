@@ -63,6 +63,16 @@ CASES = [
     Case("bf16_walk_multiseg", BH=40, T=700, d=64, e=4, gate='lag', momentum=True, states=0.1, dtype=BF16, seed=25),
     Case("bf16_walk_map3", BH=2, T=200, d=64, e=4, gate='lag', momentum=True, states=0.1, map_degree=3,
          dtype=BF16, seed=26),
+    # no buffer_out gradient (the benchmark's case): the specialised backward runs the segment fixup
+    # inside the scalar-gradient launch (not with token gates)
+    Case("bf16_walk_c3_no_dbuf", BH=4, T=600, d=64, e=4, gate='lag', momentum=True, states=0.1, dtype=BF16,
+         grad_buffer=False, seed=31),
+    Case("bf16_walk_e16_none_no_dbuf", BH=3, T=500, d=64, e=16, gate=None, momentum=True, states=0.1, dtype=BF16,
+         grad_buffer=False, seed=32),
+    Case("bf16_walk_token_no_dbuf", BH=3, T=300, d=64, e=3, gate='token', momentum=True, states=0.1, dtype=BF16,
+         grad_buffer=False, seed=33),
+    Case("fp32_lag_no_dbuf", BH=3, T=200, d=64, e=4, gate='lag', momentum=True, states=0.1, grad_buffer=False,
+         seed=34),
     # head sizes above 64 / d_k != d_v (64 x 64 state blocks stacked along BH): the BASELINE C4 shape
     # class (d_k = 128 after the tensor map, d_v = 64, e = 8, elementwise map of degree 3)
     Case("c4_reduced_fp32_dk128_dv64", BH=4, T=300, d=128, dv=64, e=8, gate='lag', momentum=True, states=0.1,
