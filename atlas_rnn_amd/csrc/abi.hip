@@ -20,7 +20,6 @@ hipError_t launch_fwd_seg(const Geom&, const FwdPtrs<T>&, const SegGeom&, float*
                           T*, hipStream_t);
 template <typename T, int CH, int D>
 hipError_t launch_bwd_seg(const Geom&, const BwdPtrs<T>&, const SegGeom&, const BwdSegPtrs&, hipStream_t, bool);
-template <typename T, int DK, int DV> hipError_t launch_buffer_out(const Geom&, const FwdPtrs<T>&, hipStream_t);
 bool walk_fwd_supported(const Geom& g);
 hipError_t launch_walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
                            float* rw, float* final_raw, float* coef, bf16* wsh, hipStream_t stream);
@@ -308,11 +307,9 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
         err = launch_fwd_seg<T, 64, 64>(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
     }
     else err = launch_fwd_seg<T, 32, 64>(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
-    if (err == hipSuccess) err = launch_buffer_out<T, 64, 64>(g, a, s);
   } else if (g.DK == 32) {
     if constexpr (sizeof(T) == 2) err = launch_fwd_seg<T, 64, 32>(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
     else err = launch_fwd_seg<T, 32, 32>(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
-    if (err == hipSuccess) err = launch_buffer_out<T, 32, 32>(g, a, s);
   }
   return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
 }

@@ -26,6 +26,7 @@
 #include "mem_common.h"
 #include "mem_params.h"
 #include "seg_common.h"
+#include "buffer_out.h"
 #include "seg_fwd.h"
 
 namespace atlas {
@@ -39,11 +40,19 @@ __global__ __launch_bounds__(kSegThreads) __attribute__((amdgpu_waves_per_eu(4))
   fwd_segment<T, CH, D, WALK_AGG>(g, a, sg, agg, nullptr, nullptr, nullptr, coef, nullptr, smem_raw);
 }
 
-// grid (D * D / kThreads, BH): segment-start states  x_{j+1} = [[a_j, -kappa_j], [0, b_j]] x_j + [U_j; V_j]
-template <int D>
+// grid (D * D / kThreads + H', BH): segment-start states
+//   x_{j+1} = [[a_j, -kappa_j], [0, b_j]] x_j + [U_j; V_j],
+// and, in the H' = e - 1 workgroups x >= nscan when buffer_out is requested, buffer_out's slot
+// x - nscan (buffer_out.h: inputs only, so it rides along with this short launch).
+template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void k_fwd_seg_scan(const Geom g, const float* S0, const float* Z0,
-                                                             const SegGeom sg, const float* agg, float* seg_states) {
+                                                             const SegGeom sg, const float* agg, float* seg_states,
+                                                             const FwdPtrs<T> a, int nscan) {
   const int bh = blockIdx.y;
+  if ((int)blockIdx.x >= nscan) {   // workgroup-uniform
+    buffer_out_slot<T, D, D>(g, a, blockIdx.x - nscan, bh);
+    return;
+  }
   const int idx = blockIdx.x * kThreads + threadIdx.x;
   if (idx >= D * D) return;
   float S = S0[(size_t)bh * D * D + idx];
@@ -73,19 +82,20 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg_scan(const Geom g, const f
   }
 }
 
-template <int D>
-hipError_t launch_fwd_seg_scan(const Geom& g, const float* S0, const float* Z0, const SegGeom& sg, const float* agg,
+template <typename T, int D>
+hipError_t launch_fwd_seg_scan(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg, const float* agg,
                                float* seg_states, hipStream_t stream) {
+  const int nscan = (D * D + kThreads - 1) / kThreads;
+  const int nbuf = (g.H > 0 && a.buf_out) ? g.H : 0;
+  prof_name(KID_FWD_SCAN, nbuf ? "k_fwd_seg_scan+buffer_out" : "k_fwd_seg_scan");
   prof_begin(KID_FWD_SCAN, stream);
-  hipLaunchKernelGGL((k_fwd_seg_scan<D>), dim3((D * D + kThreads - 1) / kThreads, g.BH), dim3(kThreads), 0, stream,
-                     g, S0, Z0, sg, agg, seg_states);
+  hipLaunchKernelGGL((k_fwd_seg_scan<T, D>), dim3(nscan + nbuf, g.BH), dim3(kThreads), 0, stream, g, a.S0, a.Z0, sg,
+                     agg, seg_states, a, nscan);
   prof_end(KID_FWD_SCAN, stream);
   return hipGetLastError();
 }
-template hipError_t launch_fwd_seg_scan<64>(const Geom&, const float*, const float*, const SegGeom&, const float*,
-                                            float*, hipStream_t);
-template hipError_t launch_fwd_seg_scan<32>(const Geom&, const float*, const float*, const SegGeom&, const float*,
-                                            float*, hipStream_t);
+template hipError_t launch_fwd_seg_scan<bf16, 64>(const Geom&, const FwdPtrs<bf16>&, const SegGeom&, const float*,
+                                                  float*, hipStream_t);
 
 template <typename T, int CH, int D>
 __global__ __launch_bounds__(kSegThreads) void k_fwd_seg(const Geom g, const FwdPtrs<T> a, const SegGeom sg,
@@ -112,7 +122,7 @@ hipError_t launch_fwd_seg(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg,
     prof_end(KID_FWD_SEG_AGG, stream);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
-  if ((err = launch_fwd_seg_scan<D>(g, a.S0, a.Z0, sg, agg, seg_states, stream)) != hipSuccess) return err;
+  if ((err = launch_fwd_seg_scan<T, D>(g, a, sg, agg, seg_states, stream)) != hipSuccess) return err;
   const size_t smem = sizeof(SegFwdSmem<T, CH, D, true>);
   err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_seg<T, CH, D>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);

@@ -471,8 +471,8 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_full(const Geom g, const F
   walk_fwd<true, MAPE>(g, a, sg, nullptr, seg_states, rw, final_raw, coef, wsh, smem_raw);
 }
 
-template <int D>
-hipError_t launch_fwd_seg_scan(const Geom& g, const float* S0, const float* Z0, const SegGeom& sg, const float* agg,
+template <typename T, int D>
+hipError_t launch_fwd_seg_scan(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg, const float* agg,
                                float* seg_states, hipStream_t stream);
 
 // The specialised walks cover bf16, d = 64, window <= 17, no clamp at scan_chunk_len boundaries and
@@ -498,7 +498,7 @@ static hipError_t launch_walks(const Geom& g, const FwdPtrs<bf16>& a, const SegG
     prof_end(KID_FWD_SEG_AGG, stream);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
-  if ((err = launch_fwd_seg_scan<64>(g, a.S0, a.Z0, sg, agg, seg_states, stream)) != hipSuccess) return err;
+  if ((err = launch_fwd_seg_scan<bf16, 64>(g, a, sg, agg, seg_states, stream)) != hipSuccess) return err;
   const size_t smem = sizeof(wf::Smem<true>);
   err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_full<MAPE>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
