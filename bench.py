@@ -62,6 +62,9 @@ def algorithmic_bytes(bh=BH, t=T, d=D, e=E, s_in=2, s_st=4):
         # forward and backward chunk records in one launch (reads the per-token scalars once)
         "k_chunk_coef_pair": n * n_sc * s_in,
     }
+    # launches that carry a second, independent stage as extra workgroups
+    per_kernel["k_fwd_seg_scan+buffer_out"] = per_kernel["k_fwd_seg_scan"] + per_kernel["k_buffer_out"]
+    per_kernel["k_scalar_chain+fixup"] = per_kernel["k_bwd_scalar"] + per_kernel["k_bwd_seg_fixup"] + st
     # the specialised bf16 d = 64 path launches these kernels for the same stages
     for spec, gen in (("k_walk_agg", "k_fwd_seg_agg"), ("k_walk_full", "k_fwd_seg"), ("k_walk_bwd", "k_bwd_seg"),
                       ("k_scalar_chain", "k_bwd_scalar")):
