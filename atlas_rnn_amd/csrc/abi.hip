@@ -19,7 +19,8 @@ template <typename T, int CH, int D>
 hipError_t launch_fwd_seg(const Geom&, const FwdPtrs<T>&, const SegGeom&, float*, float*, float*, float*, float*,
                           T*, hipStream_t);
 template <typename T, int CH, int D>
-hipError_t launch_bwd_seg(const Geom&, const BwdPtrs<T>&, const SegGeom&, const BwdSegPtrs&, hipStream_t, bool);
+hipError_t launch_bwd_seg(const Geom&, const BwdPtrs<T>&, const SegGeom&, const BwdSegPtrs&, hipStream_t, bool,
+                          const AggOverFwd*);
 bool walk_fwd_supported(const Geom& g);
 hipError_t launch_walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
                            float* rw, float* final_raw, float* coef, bf16* wsh, hipStream_t stream);
@@ -346,12 +347,15 @@ int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, voi
   hipError_t err = hipErrorInvalidValue;
   // the specialised walks run as a pair: the forward saved its states in their layout
   const bool walk = sizeof(T) == 2 && !force_generic() && walk_fwd_supported(pl.g);
+  // the specialised path forms its adjoint aggregates over the forward's chunks and records
+  const AggOverFwd agf{pl.g, pl.sg, reinterpret_cast<const float*>(sv + SL.coef)};
+  const bool agg_fwd = walk && pl.g.Lc == 64;
   if (gb.DK == 64) {
-    if constexpr (sizeof(T) == 2) err = launch_bwd_seg<T, 32, 64>(gb, a, pl.sgb, p, s, walk);
-    else err = launch_bwd_seg<T, 16, 64>(gb, a, pl.sgb, p, s, false);
+    if constexpr (sizeof(T) == 2) err = launch_bwd_seg<T, 32, 64>(gb, a, pl.sgb, p, s, walk, agg_fwd ? &agf : nullptr);
+    else err = launch_bwd_seg<T, 16, 64>(gb, a, pl.sgb, p, s, false, nullptr);
   } else if (gb.DK == 32) {
-    if constexpr (sizeof(T) == 2) err = launch_bwd_seg<T, 32, 32>(gb, a, pl.sgb, p, s, false);
-    else err = launch_bwd_seg<T, 16, 32>(gb, a, pl.sgb, p, s, false);
+    if constexpr (sizeof(T) == 2) err = launch_bwd_seg<T, 32, 32>(gb, a, pl.sgb, p, s, false, nullptr);
+    else err = launch_bwd_seg<T, 16, 32>(gb, a, pl.sgb, p, s, false, nullptr);
   }
   return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
 }

@@ -35,37 +35,47 @@ struct BwdAggSmem {
   alignas(16) float coef[2 * CH + 4];   // a_{t-1}, kappa_{t-1}, (a, kappa, b) of the chunk
 };
 
-// Register prefetch of one chunk for the adjoint aggregates: psi (threads 0 .. NV-1) or dy
-// (threads NV .. 2 NV-1) rows, 8 features per thread, and the head of the coefficient record.
+// Register prefetch of one chunk for the adjoint aggregates: psi (vectors 0 .. NV-1) or dy
+// (vectors NV .. 2 NV-1) rows, 8 features per vector, NVT vectors per thread, and the head of the
+// coefficient record.
 template <typename T, int CH, int D>
 struct BwdAggPrefetch {
   static constexpr int NV = CH * D / 8;
+  static constexpr int NVT = (2 * NV + kSegThreads - 1) / kSegThreads;
   static constexpr int NC4 = (2 * CH + 4) / 4;
-  static_assert(2 * NV <= kSegThreads && (2 * CH + 4) % 4 == 0, "one vector per thread");
-  Vec8<T> x;
+  static_assert((2 * CH + 4) % 4 == 0 && NC4 <= kSegThreads, "record head");
+  Vec8<T> x[NVT];
   float4 rc;
-  bool ok;
+  bool ok[NVT];
   __device__ __forceinline__ void load(const Geom& g, const BwdPtrs<T>& a, const float* rec, size_t tb, int c,
                                        int tid) {
     const int t0 = c * g.Lc, L = min(g.T, t0 + g.Lc) - t0;
-    const int v = tid < NV ? tid : tid - NV;
-    const int t = v / (D / 8), c8 = v % (D / 8);
-    const T* src = (tid < NV || !a.dy) ? a.q : a.dy;
-    ok = tid < 2 * NV && t < L && (tid < NV || a.dy);
-    x = vec8_load(src + (tb + t0 + (ok ? t : 0)) * D + c8 * 8);
+#pragma unroll
+    for (int u = 0; u < NVT; ++u) {
+      const int vi = tid + u * kSegThreads;
+      const int v = vi < NV ? vi : vi - NV;
+      const int t = v / (D / 8), c8 = v % (D / 8);
+      const T* src = (vi < NV || !a.dy) ? a.q : a.dy;
+      ok[u] = vi < 2 * NV && t < L && (vi < NV || a.dy);
+      x[u] = vec8_load(src + (tb + t0 + (ok[u] ? t : 0)) * D + c8 * 8);
+    }
     rc = reinterpret_cast<const float4*>(rec)[tid < NC4 ? tid : 0];
   }
   template <typename Sm>
   __device__ __forceinline__ void store(const Geom& g, Sm& sm, int tid) const {
-    if (tid < 2 * NV) {
-      const int v = tid < NV ? tid : tid - NV;
-      const int t = v / (D / 8), c8 = v % (D / 8);
-      Vec8<T> y = x.masked(ok);
-      if (tid < NV) {
-        if (g.map_mode == MAP_ELEMENTWISE) y = y.mapped(g.map_deg);
-        y.store(&sm.psi[t][c8 * 8]);
-      } else {
-        y.store(&sm.dy[t][c8 * 8]);
+#pragma unroll
+    for (int u = 0; u < NVT; ++u) {
+      const int vi = tid + u * kSegThreads;
+      if (vi < 2 * NV) {
+        const int v = vi < NV ? vi : vi - NV;
+        const int t = v / (D / 8), c8 = v % (D / 8);
+        Vec8<T> y = x[u].masked(ok[u]);
+        if (vi < NV) {
+          if (g.map_mode == MAP_ELEMENTWISE) y = y.mapped(g.map_deg);
+          y.store(&sm.psi[t][c8 * 8]);
+        } else {
+          y.store(&sm.dy[t][c8 * 8]);
+        }
       }
     }
     if (tid < NC4) reinterpret_cast<float4*>(sm.coef)[tid] = rc;
@@ -849,20 +859,39 @@ hipError_t launch_scalar_chain(const Geom& g, const BwdPtrs<bf16>& a, const BwdS
                                bool with_fixup, hipStream_t stream);
 
 // walk: run the specialised reverse walk (walk_bwd.hip, bf16 with d = 64 only) in place of k_bwd_seg
+// ag (the specialised path): adjoint aggregates over the forward's chunks (seg_common.h).
 template <typename T, int CH, int D>
 hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg, const BwdSegPtrs& p,
-                          hipStream_t stream, bool walk) {
+                          hipStream_t stream, bool walk, const AggOverFwd* ag) {
   // the chunk coefficient records p.coef / p.wsh were formed by the forward (input-only)
   hipError_t err = hipSuccess;
   if (sg.nseg > 1) {
-    const size_t smem = sizeof(BwdAggSmem<T, CH, D>);
-    err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bwd_seg_agg<T, CH, D>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-    if (err != hipSuccess) return err;
-    prof_begin(KID_BWD_ADJOINT, stream);
-    hipLaunchKernelGGL((k_bwd_seg_agg<T, CH, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, p);
-    prof_end(KID_BWD_ADJOINT, stream);
-    if ((err = hipGetLastError()) != hipSuccess) return err;
+    if constexpr (sizeof(T) == 2 && CH == 32 && D == 64) {
+      if (ag) {
+        if (ag->sg.nseg != sg.nseg || ag->sg.agg_stride != sg.agg_stride) return hipErrorInvalidValue;
+        BwdSegPtrs pf = p;
+        pf.coef = const_cast<float*>(ag->coef);
+        const size_t smem = sizeof(BwdAggSmem<T, 64, D>);
+        err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bwd_seg_agg<T, 64, D>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        if (err != hipSuccess) return err;
+        prof_begin(KID_BWD_ADJOINT, stream);
+        hipLaunchKernelGGL((k_bwd_seg_agg<T, 64, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, ag->g, a,
+                           ag->sg, pf);
+        prof_end(KID_BWD_ADJOINT, stream);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+      }
+    }
+    if (!ag) {
+      const size_t smem = sizeof(BwdAggSmem<T, CH, D>);
+      err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bwd_seg_agg<T, CH, D>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      if (err != hipSuccess) return err;
+      prof_begin(KID_BWD_ADJOINT, stream);
+      hipLaunchKernelGGL((k_bwd_seg_agg<T, CH, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, p);
+      prof_end(KID_BWD_ADJOINT, stream);
+      if ((err = hipGetLastError()) != hipSuccess) return err;
+    }
   }
   prof_begin(KID_BWD_SCAN, stream);
   hipLaunchKernelGGL((k_bwd_seg_scan<D>), dim3((D * D + kThreads - 1) / kThreads, g.BH), dim3(kThreads), 0, stream,
@@ -919,7 +948,7 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
 
 #define ATLAS_INST_BWD_SEG(T, CH, D)                                                                  \
   template hipError_t launch_bwd_seg<T, CH, D>(const Geom&, const BwdPtrs<T>&, const SegGeom&,        \
-                                               const BwdSegPtrs&, hipStream_t, bool);                 \
+                                               const BwdSegPtrs&, hipStream_t, bool, const AggOverFwd*); \
   template size_t bwd_seg_smem_bytes<T, CH, D>(int);
 
 ATLAS_INST_BWD_SEG(bf16, 32, 64)

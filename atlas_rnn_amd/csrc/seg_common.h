@@ -16,6 +16,15 @@ struct SegGeom {
   int agg_stride;     // floats per segment aggregate: U, V (2 D^2) + a, kappa, b (padded to 16)
 };
 
+// The adjoint aggregates of the specialised backward are formed over the forward's 64-token
+// chunks (an aggregate does not depend on how its segment is chunked, so this halves the serial
+// steps), with the forward's coefficient records: the forward geometry, segments and records.
+struct AggOverFwd {
+  Geom g;
+  SegGeom sg;
+  const float* coef;
+};
+
 // Backward-pass buffers beyond the user-visible arguments.
 struct BwdSegPtrs {
   const float* seg_states;   // forward segment-start states [BH][nseg][2][D][D]

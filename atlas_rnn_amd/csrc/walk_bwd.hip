@@ -32,7 +32,7 @@ constexpr int CH = 32;          // backward chunk length
 constexpr int SP = 48;          // source rows with data: halo (<= 16) + chunk
 constexpr int NST = SP / 16;    // 3 source tiles
 constexpr int SPR = 64;         // LDS rows of source-indexed matrices (rows SP.. stay zero: k = 32 steps)
-constexpr int PD = D + 8;       // pitch of 64-wide bf16 rows
+constexpr int PD = D + 16;      // pitch of 64-wide bf16 rows
 constexpr int SPM = CH + kHaloPad;   // 64: pitch of the per-source arrays in HBM (records, Ws, Lm)
 constexpr int WP = SPR + 8;     // 72: LDS pitch of the Ws rows [tau][s] (columns SP.. stay zero)
 constexpr int QP = CH + 8;      // 40: LDS pitch of Q^T / Q'^T rows [s][tau]

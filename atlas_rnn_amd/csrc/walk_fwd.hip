@@ -32,7 +32,7 @@ constexpr int D = 64;          // head size (d_k = d_v)
 constexpr int CH = 64;         // chunk length
 constexpr int SP = 80;         // source rows: halo (<= 16) + chunk
 constexpr int NST = SP / 16;   // source tiles
-constexpr int PD = D + 8;      // LDS pitch of D-wide rows (bf16)
+constexpr int PD = D + 16;     // LDS pitch of D-wide rows (bf16)
 constexpr int SPM = CH + kHaloPad;   // pitch of the coefficient arrays and Ws blocks in HBM (96)
 constexpr int WP = SP + 8;     // LDS pitch of the Ws rows (88)
 constexpr int REC = CoefRec<CH>::SIZE;   // 520 floats
