@@ -45,11 +45,19 @@ struct CoefSmem {
 // of the first barrier.
 // Chunk c of row bh, by coef_threads<CH>() threads (tid) with the LDS block sm. Every thread of
 // the workgroup reaches the same barriers, whichever chunk (and chunk length) its group works on.
-template <typename T, int CH, bool WSH>
+// HALF: the chunk's first half is a backward chunk of its own (Lmid = CH / 2, the backward's
+// chunk); its record is the forward record's values at the mid point and its Ws block the first
+// CH / 2 rows of the forward table, written to rec_h / wsh_h (backward chunk 2c of geometry gh).
+// Used only when both prefix-lane conditions hold (see k_chunk_coef_pair).
+template <typename T, int CH, bool WSH, bool HALF = false>
 __device__ __forceinline__ void chunk_coef(const Geom& g, const T* __restrict__ decay, const T* __restrict__ lr,
                                            const T* __restrict__ beta, const T* __restrict__ gate,
                                            float* __restrict__ rec_all, T* __restrict__ wsh, int c, int bh, int tid,
-                                           CoefSmem<CH>& sm) {
+                                           CoefSmem<CH>& sm, const Geom* gh = nullptr,
+                                           float* __restrict__ rec_h_all = nullptr, T* __restrict__ wsh_h = nullptr) {
+  constexpr int CHH = CH / 2, SPMH = CHH + kHaloPad, RECH = CoefRec<CHH>::SIZE;
+  constexpr int H_KCOEF = CHH, H_ENDC = 2 * CHH, H_WSEND = H_ENDC + 4, H_WZEND = H_WSEND + SPMH,
+                H_WSMID = H_WZEND + SPMH, H_WZMID = H_WSMID + SPMH, H_MIDC = H_WZMID + SPMH;
   constexpr int SPM = CH + kHaloPad, NT = coef_threads<CH>(), REC = CoefRec<CH>::SIZE;
   constexpr int R_KCOEF = CH, R_ENDC = 2 * CH, R_WSEND = R_ENDC + 4, R_WZEND = R_WSEND + SPM,
                 R_WSMID = R_WZEND + SPM, R_WZMID = R_WSMID + SPM, R_MIDC = R_WZMID + SPM;
@@ -196,6 +204,19 @@ __device__ __forceinline__ void chunk_coef(const Geom& g, const T* __restrict__ 
     rec[R_WZEND + s] = src ? wz : 0.f;
     rec[R_WSMID + s] = src ? wsm : 0.f;
     rec[R_WZMID + s] = src ? wzm : 0.f;
+    if constexpr (HALF) {   // the half's sources are the first SPMH; its own prefix columns stay zero
+      float* rh = rec_h_all + ((size_t)bh * gh->nc + 2 * c) * RECH;
+      if (s < SPMH) {
+        const bool hs = s < SPMH - 2;
+        rh[H_WSEND + s] = hs ? wsm : 0.f;
+        rh[H_WZEND + s] = hs ? wzm : 0.f;
+        rh[H_WSMID + s] = 0.f;
+        rh[H_WZMID + s] = 0.f;
+      }
+      if (s == LA) *reinterpret_cast<float4*>(rh + H_MIDC) = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (s == LA) rh[H_ENDC] = wsm;
+      if (s == LK) { rh[H_ENDC + 1] = wsm; rh[H_ENDC + 2] = wzm; rh[H_ENDC + 3] = 0.f; }
+    }
     if (!src) {   // (a, kappa, b) at the end and after token Lmid - 1
       if (s == LA) {
         rec[R_ENDC] = ws;
@@ -215,6 +236,40 @@ __device__ __forceinline__ void chunk_coef(const Geom& g, const T* __restrict__ 
   if (lane_prefix && tid < CH) {   // acoef = a_{t-1}, kcoef = kappa_{t-1}
     rec[tid] = sm.tab[tid][LA];
     rec[R_KCOEF + tid] = sm.tab[tid][LK];
+  }
+  if constexpr (HALF) {
+    float* rh = rec_h_all + ((size_t)bh * gh->nc + 2 * c) * RECH;
+    if (tid < CHH) {
+      rh[tid] = sm.tab[tid][LA];
+      rh[H_KCOEF + tid] = sm.tab[tid][LK];
+    }
+    // Ws block of the half: table rows t < CHH, sources s < SPMH (its prefix columns zeroed)
+    const rsrc_t rw = make_rsrc(wsh_h + ((size_t)bh * gh->nc + 2 * c) * CHH * SPMH, (uint32_t)(CHH * SPMH * sizeof(T)));
+    constexpr int G8 = SPMH / 8;
+    for (int i = tid; i < CHH * G8; i += NT) {
+      const int t = i / G8, s0 = (i % G8) * 8;
+      float v[8];
+      const float4 x0 = *reinterpret_cast<const float4*>(&sm.tab[t][s0]);
+      const float4 x1 = *reinterpret_cast<const float4*>(&sm.tab[t][s0 + 4]);
+      v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+      if (s0 == SPMH - 8) { v[6] = 0.f; v[7] = 0.f; }
+      const uint32_t off = (uint32_t)((t * SPMH + s0) * sizeof(T));
+      if constexpr (sizeof(T) == 2) {
+        u32x4v o;
+        o[0] = pack_bf16x2(v[0], v[1]);
+        o[1] = pack_bf16x2(v[2], v[3]);
+        o[2] = pack_bf16x2(v[4], v[5]);
+        o[3] = pack_bf16x2(v[6], v[7]);
+        bst16(rw, off, o);
+      } else {
+        const u32x4v o0 = {__builtin_bit_cast(unsigned, v[0]), __builtin_bit_cast(unsigned, v[1]),
+                           __builtin_bit_cast(unsigned, v[2]), __builtin_bit_cast(unsigned, v[3])};
+        const u32x4v o1 = {__builtin_bit_cast(unsigned, v[4]), __builtin_bit_cast(unsigned, v[5]),
+                           __builtin_bit_cast(unsigned, v[6]), __builtin_bit_cast(unsigned, v[7])};
+        bst16(rw, off, o0);
+        bst16(rw, off + 16, o1);
+      }
+    }
   }
   if constexpr (WSH) {   // Ws[s, t-1] -> wsh[t][s], eight sources per store (prefix columns zeroed)
     const rsrc_t rw = make_rsrc(wsh + ((size_t)bh * g.nc + c) * CH * SPM, (uint32_t)(CH * SPM * sizeof(T)));
@@ -253,7 +308,7 @@ template <typename T, int CHF, int CHB>
 __global__ __launch_bounds__(coef_threads<CHF>()) void k_chunk_coef_pair(
     const Geom gf, const Geom gb, const T* __restrict__ decay, const T* __restrict__ lr, const T* __restrict__ beta,
     const T* __restrict__ gate, float* __restrict__ rec_f, T* __restrict__ wsh_f, float* __restrict__ rec_b,
-    T* __restrict__ wsh_b) {
+    T* __restrict__ wsh_b, int halves) {
   constexpr int NTB = coef_threads<CHB>(), PER = coef_threads<CHF>() / NTB;
   static_assert(coef_threads<CHF>() % NTB == 0, "backward groups per workgroup");
   __shared__ union U {
@@ -262,12 +317,24 @@ __global__ __launch_bounds__(coef_threads<CHF>()) void k_chunk_coef_pair(
   } sm;
   const int x = blockIdx.x, bh = blockIdx.y;
   if (x < gf.nc) {
-    chunk_coef<T, CHF, true>(gf, decay, lr, beta, gate, rec_f, wsh_f, x, bh, threadIdx.x, sm.f);
+    if (halves)
+      chunk_coef<T, CHF, true, true>(gf, decay, lr, beta, gate, rec_f, wsh_f, x, bh, threadIdx.x, sm.f, &gb, rec_b,
+                                     wsh_b);
+    else
+      chunk_coef<T, CHF, true>(gf, decay, lr, beta, gate, rec_f, wsh_f, x, bh, threadIdx.x, sm.f);
   } else {
     const int j = threadIdx.x / NTB;
-    const int c = min((x - gf.nc) * PER + j, gb.nc - 1);
+    const int i = (x - gf.nc) * PER + j;   // backward chunk i, or odd chunk 2 i + 1 when halves
+    const int c = halves ? min(2 * i + 1, gb.nc - 1 - (gb.nc % 2 == 1)) : min(i, gb.nc - 1);
     chunk_coef<T, CHB, true>(gb, decay, lr, beta, gate, rec_b, wsh_b, c, bh, threadIdx.x % NTB, sm.b[j]);
   }
+}
+
+// Whether the forward chunks' first halves give the even backward chunks (k_chunk_coef_pair).
+template <int CHF, int CHB>
+bool coef_halves(const Geom& gf, const Geom& gb) {
+  return CHF == 2 * CHB && gb.Lc == CHB && gf.Lc == CHF && gf.Lmid == CHB && gf.H + CHF <= CHF + kHaloPad - 2 &&
+         gb.H + CHB <= CHB + kHaloPad - 2;
 }
 
 template <typename T, int CHF, int CHB>
@@ -275,10 +342,13 @@ hipError_t launch_chunk_coef_pair(const Geom& gf, const Geom& gb, const T* decay
                                   const T* gate, float* rec_f, T* wsh_f, float* rec_b, T* wsh_b, hipStream_t stream) {
   if (gf.Lmid % 8 != 0 || gf.Lmid > CHF || gb.Lmid != 0) return hipErrorInvalidValue;
   constexpr int PER = coef_threads<CHF>() / coef_threads<CHB>();
+  const int halves = coef_halves<CHF, CHB>(gf, gb) ? 1 : 0;
+  const int nb = halves ? gb.nc / 2 : gb.nc;   // backward chunks formed by their own thread groups
   prof_name(KID_FWD_COEF, "k_chunk_coef_pair");
   prof_begin(KID_FWD_COEF, stream);
-  hipLaunchKernelGGL((k_chunk_coef_pair<T, CHF, CHB>), dim3(gf.nc + (gb.nc + PER - 1) / PER, gf.BH),
-                     dim3(coef_threads<CHF>()), 0, stream, gf, gb, decay, lr, beta, gate, rec_f, wsh_f, rec_b, wsh_b);
+  hipLaunchKernelGGL((k_chunk_coef_pair<T, CHF, CHB>), dim3(gf.nc + (nb + PER - 1) / PER, gf.BH),
+                     dim3(coef_threads<CHF>()), 0, stream, gf, gb, decay, lr, beta, gate, rec_f, wsh_f, rec_b, wsh_b,
+                     halves);
   prof_end(KID_FWD_COEF, stream);
   return hipGetLastError();
 }
