@@ -653,6 +653,7 @@ hipError_t launch_walk_bwd_kernel(const Geom& g, const BwdPtrs<bf16>& a, const S
 // ---------------------------------------------------------------------------------------------
 namespace wb {
 constexpr int kChainWaves = 4;
+constexpr int kWalkWindow = SP - CH + 1;   // 17: the largest window of the specialised path
 constexpr int NSRC = SP;          // 48 source lanes; lane NSRC runs the prefix chain
 constexpr int RP = CH + 1;        // pitch of the window-weight rows
 constexpr int NQD = 13;           // lane quads holding live lanes (0 .. 51)
@@ -662,7 +663,7 @@ struct ChainSmem {   // static LDS: kChainWaves * 6.3 KB
     float W[NSRC][RP];                  // window weights w(s, t) of the sources
     struct {
       alignas(16) float red[3][CH][QDP];   // quad sums of the alpha / eta / beta contributions of step t
-      float dw[CH * kMaxWindow + 1];       // window-weight gradients [t][j]; the last slot takes masked writes
+      float dw[CH * kWalkWindow + 1];      // window-weight gradients [t][j]; the last slot takes masked writes
     } r;
   } u[kChainWaves];
 };
@@ -786,7 +787,7 @@ __global__ __launch_bounds__(64 * wb::kChainWaves) void k_scalar_chain(const Geo
       U.r.red[2][t][qrow] = cb;
       const int j = t + H - lane;
       const bool wv_ok = src && j >= 0 && j < e;
-      U.r.dw[wv_ok ? t * e + j : CH * kMaxWindow] = gwz;
+      U.r.dw[wv_ok ? t * e + j : CH * kWalkWindow] = gwz;
     }
   }
   __builtin_amdgcn_wave_barrier();
