@@ -41,6 +41,8 @@ EXPORTED_SYMBOLS = (
     "atlas_window_sum",
     "atlas_affine_scan_fwd",
     "atlas_affine_scan_bwd",
+    "atlas_tensor_map_fwd",
+    "atlas_tensor_map_bwd",
     "atlas_mem_profile_enable",
     "atlas_mem_profile_read",
     "atlas_mem_kernel_name",
@@ -114,6 +116,10 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_affine_scan_fwd.argtypes = [i32, i32, i32, i32, vp, vp, vp, vp, vp]
     lib.atlas_affine_scan_bwd.restype = i32
     lib.atlas_affine_scan_bwd.argtypes = [i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.atlas_tensor_map_fwd.restype = i32
+    lib.atlas_tensor_map_fwd.argtypes = [i32, i64, i32, i32, vp, vp, vp, vp]
+    lib.atlas_tensor_map_bwd.restype = i32
+    lib.atlas_tensor_map_bwd.argtypes = [i32, i64, i32, i32, vp, vp, vp, vp, vp]
     lib.atlas_mem_profile_enable.restype = i32
     lib.atlas_mem_profile_enable.argtypes = [i32]
     lib.atlas_mem_profile_read.restype = i32

@@ -1,0 +1,372 @@
+// tmap.hip - the tensor polynomial feature map, fused (forward and backward), bf16 in / fp32 accumulate.
+//
+//   phi = [x; vec(x x^T)] P,   x [N, D],  P [D + D*D, M]        (rnn_memory.py:125-130, the 'tensor'
+//                                                                 mode of PolynomialFeatureMap)
+// Neither direction materialises the [N, D + D*D] Kronecker features:
+//
+// forward  (k_tmap_fwd): one GEMM over K = D + D*D in blocks of D: block 0 is x itself, block a + 1
+//   the row a of x x^T, i.e. x_a * x. The x-side MFMA operand of a block is formed in registers from
+//   the token's x values (x_a from LDS, x_b held per lane), the P-side operand (P^T staged in LDS,
+//   double buffered, one barrier per block) is shared by the waves. The accumulator is phi^T, so each
+//   lane stores four consecutive features of one token.
+//
+// backward (k_tmap_bwd): with G[n, a, b] = sum_j dphi[n, j] P[D + D a + b, j] (P's rows are the
+//   k operand; dphi stays in registers for the whole launch),
+//     dx[n, c] = sum_j dphi[n, j] P[c, j] + sum_b G[n, c, b] x[n, b] + sum_a G[n, a, c] x[n, a].
+//   The block of row a yields G[., a, .] as matrix-core tiles; the third term accumulates in the
+//   owning lanes (x[n, a] is one value per lane), the second is a sum over b across the tile (in lane
+//   and over the four lane rows) written to an LDS table t1[half][n][a] and added at the end.
+//
+// Token tiles of 128 rows; rows past N load zeros and their stores are dropped (buffer range checks).
+#include "mem_common.h"
+#include "walk_common.h"
+
+namespace atlas {
+
+namespace tm {
+constexpr int TN = 128;   // tokens per workgroup
+}
+
+// ---------------------------------------------------------------------------------------------
+// forward: waves = 4 (token groups of 32) x M / 32 (feature groups of 32); lane tile 2 x 2 of 16 x 16
+// ---------------------------------------------------------------------------------------------
+template <int D, int M>
+struct TmapFwdSmem {
+  alignas(16) bf16 xs[tm::TN][D + 8];
+  alignas(16) bf16 pt[2][M][D + 8];   // P^T columns of the current / next block
+};
+
+template <int D, int M>
+__global__ __launch_bounds__(64 * 4 * (M / 32)) void k_tmap_fwd(long n_tok, const bf16* __restrict__ x,
+                                                                   const bf16* __restrict__ pt,
+                                                                   bf16* __restrict__ out) {
+  constexpr int NW = 4 * (M / 32), NT = 64 * NW, K = D + D * D, NS = D / 32;
+  constexpr int PV = M * D / 8;   // 16-byte vectors of one P^T block
+  static_assert(PV % NT == 0 || NT % PV == 0, "block staging");
+  constexpr int PVT = (PV + NT - 1) / NT;
+  __shared__ TmapFwdSmem<D, M> sm;
+  const int tid = threadIdx.x, lane = lane_id(), w = threadIdx.x >> 6;
+  const int g = lane >> 4, i = lane & 15;
+  const int rg = w & 3, cg = w >> 2;     // tokens 32 rg .., features 32 cg ..
+  const long n0 = (long)blockIdx.x * tm::TN;
+  const uint32_t xbytes = (uint32_t)(min((long)tm::TN, n_tok - n0) * D * 2);
+  const rsrc_t rx = make_rsrc(x + n0 * D, xbytes);
+  const rsrc_t rp = make_rsrc(pt, (uint32_t)(M * K * 2));
+
+  // x tile -> LDS (rows past N read as zeros)
+  for (int v = tid; v < tm::TN * D / 8; v += NT) {
+    const int r = v / (D / 8), c8 = v % (D / 8);
+    *reinterpret_cast<u32x4v*>(&sm.xs[r][c8 * 8]) = bld16(rx, (uint32_t)((r * D + c8 * 8) * 2));
+  }
+  // P^T block kb: columns kb*D .. of every feature row j (vector v: row v / (D/8), 8 columns)
+  u32x4v pf[PVT];
+  auto p_load = [&](int kb) {
+#pragma unroll
+    for (int u = 0; u < PVT; ++u) {
+      const int v = tid + u * NT;
+      const int j = v / (D / 8), c8 = v % (D / 8);
+      pf[u] = bld16(rp, v < PV ? (uint32_t)((j * K + kb * D + c8 * 8) * 2) : kOob);
+    }
+  };
+  auto p_store = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < PVT; ++u) {
+      const int v = tid + u * NT;
+      if (v < PV) *reinterpret_cast<u32x4v*>(&sm.pt[buf][v / (D / 8)][(v % (D / 8)) * 8]) = pf[u];
+    }
+  };
+  p_load(0);
+  p_store(0);
+  p_load(1);
+  __syncthreads();
+
+  // x_b of this lane's k slots, per token tile: b = 32 s + 8 g + e
+  float xb[2][NS][8];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(&sm.xs[32 * rg + 16 * nt + i][32 * s + 8 * g]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xb[nt][s][e] = static_cast<float>(v[e]);
+    }
+
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) acc[jt][nt] = zero4();
+
+  for (int kb = 0; kb <= D; ++kb) {
+    const int buf = kb & 1;
+    float xa[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)   // x_a of the block's row a = kb - 1 (unused in block 0)
+      xa[nt] = static_cast<float>(sm.xs[32 * rg + 16 * nt + i][kb > 0 ? kb - 1 : 0]);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      bf16x8 fa[2], fb[2];
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt) fa[jt] = frag_row(&sm.pt[buf][0][0], D + 8, 32 * cg + 16 * jt, 32 * s);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        if (kb == 0) {   // workgroup-uniform: the linear block is x itself
+          fb[nt] = frag_row(&sm.xs[0][0], D + 8, 32 * rg + 16 * nt, 32 * s);
+        } else {         // x_a * x_b, rounded to bf16 like the materialised Kronecker features
+#pragma unroll
+          for (int e = 0; e < 8; ++e) fb[nt][e] = static_cast<bf16>(xa[nt] * xb[nt][s][e]);
+        }
+      }
+#pragma unroll
+      for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[jt][nt] = mma_bf16(fa[jt], fb[nt], acc[jt][nt]);
+    }
+    if (kb < D) {
+      p_store(buf ^ 1);
+      if (kb + 1 < D) p_load(kb + 2);
+    }
+    __syncthreads();
+  }
+
+  // phi^T tiles: lane (g, i) holds phi[token 32 rg + 16 nt + i][feature 32 cg + 16 jt + 4 g + r]
+  const rsrc_t ro = make_rsrc(out + n0 * M, (uint32_t)(min((long)tm::TN, n_tok - n0) * M * 2));
+#pragma unroll
+  for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int r = 32 * rg + 16 * nt + i, j = 32 * cg + 16 * jt + 4 * g;
+      u32x2v o;
+      o[0] = pack_bf16x2(acc[jt][nt][0], acc[jt][nt][1]);
+      o[1] = pack_bf16x2(acc[jt][nt][2], acc[jt][nt][3]);
+      bst8(ro, (uint32_t)((r * M + j) * 2), o);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// backward: waves = 4 (token groups of 32) x D / 32 (feature halves of 32); lane tile 2 x 2
+// ---------------------------------------------------------------------------------------------
+template <int D, int M>
+struct TmapBwdSmem {
+  alignas(16) bf16 xs[tm::TN][D + 8];
+  alignas(16) bf16 pb[2][D][M + 8];       // rows of P for the current / next block
+  float t1[D / 32][tm::TN][D + 1];        // sum over b of G[n, a, b] x[n, b], per feature half of b
+};
+
+template <int D, int M>
+__global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, const bf16* __restrict__ x,
+                                                                   const bf16* __restrict__ proj,
+                                                                   const bf16* __restrict__ dout,
+                                                                   bf16* __restrict__ dx) {
+  constexpr int NW = 4 * (D / 32), NT = 64 * NW, NK = M / 32;
+  constexpr int PV = D * M / 8;   // 16-byte vectors of one block of D rows of P
+  constexpr int PVT = (PV + NT - 1) / NT;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  TmapBwdSmem<D, M>& sm = *reinterpret_cast<TmapBwdSmem<D, M>*>(smem_raw);
+  const int tid = threadIdx.x, lane = lane_id(), w = threadIdx.x >> 6;
+  const int g = lane >> 4, i = lane & 15;
+  const int rg = w & 3, cb = w >> 2;     // tokens 32 rg .., features (b, c) 32 cb ..
+  const long n0 = (long)blockIdx.x * tm::TN;
+  const long nrow = min((long)tm::TN, n_tok - n0);
+  const rsrc_t rx = make_rsrc(x + n0 * D, (uint32_t)(nrow * D * 2));
+  const rsrc_t rd = make_rsrc(dout + n0 * M, (uint32_t)(nrow * M * 2));
+  const rsrc_t rp = make_rsrc(proj, (uint32_t)((D + D * D) * M * 2));
+
+  for (int v = tid; v < tm::TN * D / 8; v += NT) {
+    const int r = v / (D / 8), c8 = v % (D / 8);
+    *reinterpret_cast<u32x4v*>(&sm.xs[r][c8 * 8]) = bld16(rx, (uint32_t)((r * D + c8 * 8) * 2));
+  }
+  u32x4v pf[PVT];
+  auto p_load = [&](int kb) {   // P rows kb*D .. kb*D + D - 1 (kb 0: the linear rows, kb a + 1: row a of x x^T)
+#pragma unroll
+    for (int u = 0; u < PVT; ++u) {
+      const int v = tid + u * NT;
+      const int r = v / (M / 8), c8 = v % (M / 8);
+      pf[u] = bld16(rp, v < PV ? (uint32_t)(((kb * D + r) * M + c8 * 8) * 2) : kOob);
+    }
+  };
+  auto p_store = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < PVT; ++u) {
+      const int v = tid + u * NT;
+      if (v < PV) *reinterpret_cast<u32x4v*>(&sm.pb[buf][v / (M / 8)][(v % (M / 8)) * 8]) = pf[u];
+    }
+  };
+  // dphi of this lane's tokens as k operands over j (kept for the whole launch)
+  bf16x8 fd[2][NK];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks)
+      fd[nt][ks] = __builtin_bit_cast(bf16x8, bld16(rd, (uint32_t)(((32 * rg + 16 * nt + i) * M + 32 * ks + 8 * g) * 2)));
+  p_load(0);
+  p_store(0);
+  p_load(1);
+  __syncthreads();
+
+  // x[n, b] at this lane's tile positions: b = 32 cb + 16 bt + 4 g + r, n = 32 rg + 16 nt + i
+  float xc[2][2][4];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int bt = 0; bt < 2; ++bt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) xc[nt][bt][r] = static_cast<float>(sm.xs[32 * rg + 16 * nt + i][32 * cb + 16 * bt + 4 * g + r]);
+
+  f32x4 acc[2][2];   // [bt][nt]: dx^T tiles (linear term + third term)
+#pragma unroll
+  for (int bt = 0; bt < 2; ++bt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) acc[bt][nt] = zero4();
+
+  for (int kb = 0; kb <= D; ++kb) {
+    const int buf = kb & 1;
+    f32x4 gt[2][2];
+#pragma unroll
+    for (int bt = 0; bt < 2; ++bt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) gt[bt][nt] = zero4();
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) {
+      bf16x8 fp[2];
+#pragma unroll
+      for (int bt = 0; bt < 2; ++bt) fp[bt] = frag_row(&sm.pb[buf][0][0], M + 8, 32 * cb + 16 * bt, 32 * ks);
+#pragma unroll
+      for (int bt = 0; bt < 2; ++bt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) gt[bt][nt] = mma_bf16(fp[bt], fd[nt][ks], gt[bt][nt]);
+    }
+    if (kb == 0) {   // workgroup-uniform: the linear rows give dx directly
+#pragma unroll
+      for (int bt = 0; bt < 2; ++bt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[bt][nt] += gt[bt][nt];
+    } else {
+      const int a = kb - 1;
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int n = 32 * rg + 16 * nt + i;
+        const float xa = static_cast<float>(sm.xs[n][a]);
+        float part = 0.f;
+#pragma unroll
+        for (int bt = 0; bt < 2; ++bt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            acc[bt][nt][r] += gt[bt][nt][r] * xa;          // G[n, a, c] x[n, a] for c = b
+            part += gt[bt][nt][r] * xc[nt][bt][r];         // G[n, a, b] x[n, b]
+          }
+        part = xsum_rows(part);                             // over the four lane rows (all 32 b)
+        if (g == 0) sm.t1[cb][n][a] = part;
+      }
+    }
+    if (kb < D) {
+      p_store(buf ^ 1);
+      if (kb + 1 < D) p_load(kb + 2);
+    }
+    __syncthreads();
+  }
+
+  // dx[n, c] = acc (c = 32 cb + 16 bt + 4 g + r) + sum over the halves of t1[., n, c]
+  const rsrc_t ro = make_rsrc(dx + n0 * D, (uint32_t)(nrow * D * 2));
+#pragma unroll
+  for (int bt = 0; bt < 2; ++bt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int n = 32 * rg + 16 * nt + i, c = 32 * cb + 16 * bt + 4 * g;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float s = acc[bt][nt][r];
+#pragma unroll
+        for (int h = 0; h < D / 32; ++h) s += sm.t1[h][n][c + r];
+        v[r] = s;
+      }
+      u32x2v o;
+      o[0] = pack_bf16x2(v[0], v[1]);
+      o[1] = pack_bf16x2(v[2], v[3]);
+      bst8(ro, (uint32_t)((n * D + c) * 2), o);
+    }
+}
+
+template <int D, int M>
+hipError_t launch_tmap_fwd(long n, const bf16* x, const bf16* pt, bf16* out, hipStream_t s) {
+  const unsigned grid = (unsigned)((n + tm::TN - 1) / tm::TN);
+  hipLaunchKernelGGL((k_tmap_fwd<D, M>), dim3(grid), dim3(64 * 4 * (M / 32)), 0, s, n, x, pt, out);
+  return hipGetLastError();
+}
+
+template <int D, int M>
+hipError_t launch_tmap_bwd(long n, const bf16* x, const bf16* p, const bf16* dout, bf16* dx, hipStream_t s) {
+  const size_t smem = sizeof(TmapBwdSmem<D, M>);
+  hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_tmap_bwd<D, M>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (err != hipSuccess) return err;
+  const unsigned grid = (unsigned)((n + tm::TN - 1) / tm::TN);
+  hipLaunchKernelGGL((k_tmap_bwd<D, M>), dim3(grid), dim3(64 * 4 * (D / 32)), smem, s, n, x, p, dout, dx);
+  return hipGetLastError();
+}
+
+// d_in in {32, 64}, d_out in {32, 64, 128}
+hipError_t tmap_fwd(int d, int m, long n, const bf16* x, const bf16* pt, bf16* out, hipStream_t s) {
+  if (d == 64 && m == 128) return launch_tmap_fwd<64, 128>(n, x, pt, out, s);
+  if (d == 64 && m == 64) return launch_tmap_fwd<64, 64>(n, x, pt, out, s);
+  if (d == 64 && m == 32) return launch_tmap_fwd<64, 32>(n, x, pt, out, s);
+  if (d == 32 && m == 128) return launch_tmap_fwd<32, 128>(n, x, pt, out, s);
+  if (d == 32 && m == 64) return launch_tmap_fwd<32, 64>(n, x, pt, out, s);
+  if (d == 32 && m == 32) return launch_tmap_fwd<32, 32>(n, x, pt, out, s);
+  return hipErrorInvalidValue;
+}
+hipError_t tmap_bwd(int d, int m, long n, const bf16* x, const bf16* p, const bf16* dout, bf16* dx, hipStream_t s) {
+  if (d == 64 && m == 128) return launch_tmap_bwd<64, 128>(n, x, p, dout, dx, s);
+  if (d == 64 && m == 64) return launch_tmap_bwd<64, 64>(n, x, p, dout, dx, s);
+  if (d == 64 && m == 32) return launch_tmap_bwd<64, 32>(n, x, p, dout, dx, s);
+  if (d == 32 && m == 128) return launch_tmap_bwd<32, 128>(n, x, p, dout, dx, s);
+  if (d == 32 && m == 64) return launch_tmap_bwd<32, 64>(n, x, p, dout, dx, s);
+  if (d == 32 && m == 32) return launch_tmap_bwd<32, 32>(n, x, p, dout, dx, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace atlas
+
+// ---------------------------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------------------------
+#include "../../include/atlas_mem.h"
+
+namespace {
+bool tmap_dims_ok(int64_t n, int d_in, int d_out) {
+  return n >= 0 && n < ((int64_t)1 << 40) && (d_in == 32 || d_in == 64) && (d_out == 32 || d_out == 64 || d_out == 128);
+}
+bool tmap_misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
+}  // namespace
+
+extern "C" {
+
+int atlas_tensor_map_fwd(int dtype, int64_t n, int d_in, int d_out, const void* x, const void* proj_t, void* out,
+                         void* stream) {
+  if (dtype != ATLAS_DT_BF16) return ATLAS_MEM_ERR_DTYPE;
+  if (!tmap_dims_ok(n, d_in, d_out)) return ATLAS_MEM_ERR_SHAPE;
+  if (!x || !proj_t || !out) return ATLAS_MEM_ERR_NULL;
+  if (tmap_misaligned(x) || tmap_misaligned(proj_t) || tmap_misaligned(out)) return ATLAS_MEM_ERR_ALIGN;
+  if (n == 0) return ATLAS_MEM_OK;
+  const hipError_t err = atlas::tmap_fwd(d_in, d_out, (long)n, static_cast<const atlas::bf16*>(x),
+                                         static_cast<const atlas::bf16*>(proj_t), static_cast<atlas::bf16*>(out),
+                                         static_cast<hipStream_t>(stream));
+  return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
+}
+
+int atlas_tensor_map_bwd(int dtype, int64_t n, int d_in, int d_out, const void* x, const void* proj,
+                         const void* dout, void* dx, void* stream) {
+  if (dtype != ATLAS_DT_BF16) return ATLAS_MEM_ERR_DTYPE;
+  if (!tmap_dims_ok(n, d_in, d_out)) return ATLAS_MEM_ERR_SHAPE;
+  if (!x || !proj || !dout || !dx) return ATLAS_MEM_ERR_NULL;
+  if (tmap_misaligned(x) || tmap_misaligned(proj) || tmap_misaligned(dout) || tmap_misaligned(dx))
+    return ATLAS_MEM_ERR_ALIGN;
+  if (n == 0) return ATLAS_MEM_OK;
+  const hipError_t err = atlas::tmap_bwd(d_in, d_out, (long)n, static_cast<const atlas::bf16*>(x),
+                                         static_cast<const atlas::bf16*>(proj), static_cast<const atlas::bf16*>(dout),
+                                         static_cast<atlas::bf16*>(dx), static_cast<hipStream_t>(stream));
+  return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
+}
+
+}  // extern "C"

@@ -161,6 +161,68 @@ def _canon(x: Tensor | None, dtype) -> Tensor | None:
     return None if x is None else _aligned(x.to(dtype))
 
 
+# ---------------------------------------------------------------------------------------------
+# Tensor polynomial feature map (rnn_memory.py:125-130): [x; vec(x x^T)] @ P, fused on the GPU
+# ---------------------------------------------------------------------------------------------
+
+_TMAP_DIN = (32, 64)
+_TMAP_DOUT = (32, 64, 128)
+
+
+def _tensor_map_reference_form(x: Tensor, proj: Tensor) -> Tensor:
+    """The reference's tensor ops (materialises vec(x x^T)); used where the kernels do not apply."""
+    d = x.shape[-1]
+    outer = torch.einsum('...i,...j->...ij', x, x).reshape(*x.shape[:-1], d * d)
+    return torch.cat([x, outer], dim=-1) @ proj.to(x.device, x.dtype)
+
+
+class _TensorMapFn(torch.autograd.Function):
+    """atlas_tensor_map_fwd / _bwd: bf16 x [n, d] and P [d + d*d, m] -> phi [n, m]; P is a constant
+    (a registered buffer in the reference, so it has no gradient)."""
+
+    @staticmethod
+    def forward(ctx, x, proj):
+        dev = _require_gpu(x, proj)
+        lib = _lib.load()
+        lead, d, m = x.shape[:-1], x.shape[-1], proj.shape[-1]
+        x2 = _aligned(x.reshape(-1, d))
+        p = _aligned(proj.to(torch.bfloat16))
+        pt = _aligned(p.t())
+        n = x2.shape[0]
+        out = torch.empty(n, m, device=dev, dtype=torch.bfloat16)
+        _lib.check(lib.atlas_tensor_map_fwd(_lib.DT_BF16, n, d, m, _ptr(x2), _ptr(pt), _ptr(out), _stream(dev)),
+                   "atlas_tensor_map_fwd")
+        ctx.save_for_backward(x2, p)
+        ctx.lead = lead
+        return out.reshape(*lead, m)
+
+    @staticmethod
+    def backward(ctx, dout):
+        x2, p = ctx.saved_tensors
+        dev = x2.device
+        lib = _lib.load()
+        n, d = x2.shape
+        m = p.shape[-1]
+        g = _aligned(dout.reshape(-1, m).to(torch.bfloat16))
+        dx = torch.empty_like(x2)
+        _lib.check(lib.atlas_tensor_map_bwd(_lib.DT_BF16, n, d, m, _ptr(x2), _ptr(p), _ptr(g), _ptr(dx), _stream(dev)),
+                   "atlas_tensor_map_bwd")
+        return dx.reshape(*ctx.lead, d), None
+
+
+def tensor_feature_map(x: Tensor, proj: Tensor) -> Tensor:
+    """[x; vec(x x^T)] @ proj (rnn_memory.py:125-130). bf16 GPU inputs with d in (32, 64) and
+    proj [d + d*d, m], m in (32, 64, 128), and a constant proj run the fused kernels (the Kronecker
+    features are never materialised); other dtypes, sizes or a trainable proj use the reference's
+    tensor ops."""
+    d, m = x.shape[-1], proj.shape[-1]
+    fused = (x.is_cuda and x.dtype == torch.bfloat16 and d in _TMAP_DIN and m in _TMAP_DOUT
+             and proj.shape[0] == d + d * d and not proj.requires_grad)
+    if not fused:
+        return _tensor_map_reference_form(x, proj)
+    return _TensorMapFn.apply(x, proj)
+
+
 _BLOCK = 64    # block width of the decomposition for head sizes the kernels are not built for
 
 

@@ -34,7 +34,8 @@ from einops.layers.torch import Rearrange
 from torch import Tensor, nn
 from torch.nn import Conv1d, Linear, Module, Parameter
 
-from .functional import AssocScan, AtlasOmegaFunction, check_cuda_availability, memory_recurrence, window_sum
+from .functional import (AssocScan, AtlasOmegaFunction, check_cuda_availability, memory_recurrence,
+                         tensor_feature_map, window_sum)
 
 
 def exists(v):
@@ -99,10 +100,8 @@ class PolynomialFeatureMap(Module):
                 power = power * x
                 out = out + power
             return out
-        if self.mode == 'tensor':
-            d = x.shape[-1]
-            outer = torch.einsum('...i,...j->...ij', x, x).reshape(*x.shape[:-1], d * d)
-            return torch.cat([x, outer], dim=-1) @ self.proj.to(x.device, x.dtype)
+        if self.mode == 'tensor':   # fused kernels for bf16 GPU inputs (functional.tensor_feature_map)
+            return tensor_feature_map(x, self.proj.to(x.device, x.dtype))
         return x
 
 

@@ -149,6 +149,90 @@ def calibrate_copy(nbytes=256 << 20, reps=5):
     print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "launches": reps}), flush=True)
 
 
+# The other BASELINE configs (`--config c2|c4|c5`): one JSON line each, same keys; the default
+# run (no flag) is the C3 headline above. Tokens are (b, t) positions through one memory layer.
+OTHER_CONFIGS = {
+    # Titans-RNN with momentum, no window, no gate, bf16, B=4 H=8 T=2048 d=64
+    "c2": dict(B=4, H=8, T=2048, dk=64, dv=64, e=1, gate=None, seed=1002,
+               workload="C2 Titans-RNN memory layer: B=4 H=8 T=2048 d=64, momentum, bf16 inputs, fp32 state, "
+                        "chunk 64"),
+    # OmegaNet-RNN with the tensor feature map phi = elementwise_g3([k; vec(k k^T)] P), P: 4160 -> 128
+    # (Xavier-uniform), d_k = 128, d_v = 64, e = 8, lag gates; the map's GEMM is part of the step
+    "c4": dict(B=2, H=8, T=8192, dk=128, dv=64, e=8, gate="lag", seed=1004, tensor_map=True,
+               workload="C4 OmegaNet-RNN memory layer with the tensor feature map (64+4096 -> 128, then the "
+                        "elementwise map of degree 3): B=2 H=8 T=8192 d_k=128 d_v=64 e=8 lag gates, momentum, "
+                        "bf16 inputs, fp32 state"),
+    # the memory core of one layer of the byte-level RNN transformer: B=8 H=8 T=2048, e=4, per-token gates
+    "c5": dict(B=8, H=8, T=2048, dk=64, dv=64, e=4, gate="token", seed=1005,
+               workload="C5 memory core of one RNN-transformer layer: B=8 H=8 T=2048 d=64 e=4 per-token gates, "
+                        "momentum, bf16 inputs, fp32 state"),
+}
+
+
+def run_other_config(name, steps, warmup):
+    """fwd+bwd of config `name` through the autograd API (torch.autograd.grad of sum(y * g))."""
+    import torch
+    from atlas_rnn_amd.functional import memory_recurrence, tensor_feature_map
+    c = OTHER_CONFIGS[name]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    bh, t, dk, dv, e = c["B"] * c["H"], c["T"], c["dk"], c["dv"], c["e"]
+    g = torch.Generator().manual_seed(c["seed"])
+    r = lambda *sh: torch.randn(*sh, generator=g)
+    bf = lambda x: x.to(device=dev, dtype=torch.bfloat16).contiguous()
+    tensor_map = c.get("tensor_map", False)
+    kin = 64 if tensor_map else dk
+    k = r(bh, t, kin)
+    k = k / k.norm(dim=-1, keepdim=True)
+    q = r(bh, t, kin)
+    q = q / q.norm(dim=-1, keepdim=True) if tensor_map else q
+    gate = None
+    if c["gate"] == "lag":
+        gate = torch.softmax(r(bh, t, e), dim=-1)
+    elif c["gate"] == "token":
+        gate = torch.sigmoid(r(bh, t))
+    leaves = dict(k=bf(k), q=bf(q), v=bf(r(bh, t, dv)), lr=bf(0.1 * torch.sigmoid(r(bh, t))),
+                  decay=bf(torch.sigmoid(r(bh, t) * 0.5 + 2.0)), beta=bf(torch.sigmoid(r(bh, t) * 0.5 + 1.0)),
+                  gate=bf(gate) if gate is not None else None)
+    for v in leaves.values():
+        if v is not None:
+            v.requires_grad_(True)
+    P = None
+    if tensor_map:   # Xavier-uniform (64 + 4096) -> 128, seeded
+        bound = (6.0 / (kin + kin * kin + dk)) ** 0.5
+        P = bf((torch.rand(kin + kin * kin, dk, generator=g) * 2 - 1) * bound)
+    gy = bf(r(bh, t, dv))
+    zeros = torch.zeros(bh, dv, dk, device=dev)
+
+    def feat(x):   # fused tensor-map kernels (atlas_tensor_map_fwd / _bwd)
+        return tensor_feature_map(x, P) if tensor_map else x
+
+    def step():
+        y, S_T, Z_T, B_out = memory_recurrence(
+            feat(leaves["k"]), feat(leaves["q"]), leaves["v"], leaves["lr"], leaves["decay"], leaves["beta"],
+            leaves["gate"], zeros, zeros, zeros, None, window=e,
+            map_mode="elementwise" if tensor_map else "off", map_degree=3 if tensor_map else 1)
+        ins = [v for v in leaves.values() if v is not None]
+        torch.autograd.grad((y.float() * gy.float()).sum(), ins)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    tokens = c["B"] * t
+    out = {"metric": "memory-layer tokens/s fwd+bwd", "value": round(tokens * steps / el, 1), "unit": "tokens/s",
+           "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(1e3 * el / steps, 4),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic (seeded)", "config": {"workload": c["workload"], "global_batch": c["B"],
+                                                     "seq_len": t, "heads": c["H"], "d_k": dk, "d_v": dv,
+                                                     "window": e, "parallelism": "single GPU"}}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -158,9 +242,17 @@ def main():
     ap.add_argument("--cpu-sample-tokens", type=int, default=256)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (HBM counter calibration)")
+    ap.add_argument("--config", choices=["c3"] + sorted(OTHER_CONFIGS), default="c3",
+                    help="c3 (default): the headline; c2 / c4 / c5: the other BASELINE configs")
     args = ap.parse_args()
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.config != "c3":
+        if args.gpus != 1:
+            print("bench.py measures one GPU (use --gpus 1).", file=sys.stderr)
+            sys.exit(2)
+        run_other_config(args.config, args.steps, args.warmup)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the memory-layer recurrence shards over (batch, head) rows "

@@ -175,6 +175,21 @@ int atlas_affine_scan_fwd(int n, int t, int r, int d, const float* A, const floa
 int atlas_affine_scan_bwd(int n, int t, int r, int d, const float* A, const float* H, const float* prev,
                           const float* dout, float* dA, float* dB, float* dprev, void* stream);
 
+/* Tensor polynomial feature map, fused (replaces the 'tensor' mode of PolynomialFeatureMap,
+ * atlas_pytorch/rnn_memory.py:125-130, which materialises vec(x x^T) with einsum / cat / matmul):
+ *   out = [x; vec(x x^T)] P,  x [n, d_in] bf16, P [d_in + d_in^2, d_out] bf16 (row a*d_in + b of
+ *   the quadratic part multiplies x_a x_b), out [n, d_out] bf16, fp32 accumulation.
+ * The forward takes P transposed (proj_t [d_out, d_in + d_in^2]); d_in in {32, 64},
+ * d_out in {32, 64, 128}; bf16 only; every pointer 16-byte aligned. */
+int atlas_tensor_map_fwd(int dtype, int64_t n, int d_in, int d_out, const void* x, const void* proj_t, void* out,
+                         void* stream);
+
+/* Gradient of atlas_tensor_map_fwd with respect to x for the output gradient dout [n, d_out]
+ * (P is a fixed buffer in the reference: no gradient). Takes P itself (proj [d_in + d_in^2, d_out]);
+ * dx [n, d_in] bf16. */
+int atlas_tensor_map_bwd(int dtype, int64_t n, int d_in, int d_out, const void* x, const void* proj,
+                         const void* dout, void* dx, void* stream);
+
 /* ---- diagnostics (no reference counterpart) ------------------------------------------------ */
 
 /* Number of kernels the timing hooks distinguish (index -> atlas_mem_kernel_name). */

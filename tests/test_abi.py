@@ -121,6 +121,33 @@ def test_misaligned_pointers_error_before_launch(lib):
     assert lib.atlas_mem_fwd(ctypes.byref(p), ctypes.byref(args), ctypes.c_void_p(bad), None) == 5
 
 
+def test_tensor_map_errors_before_launch(lib):
+    good, bad = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x10008)
+    f = lib.atlas_tensor_map_fwd
+    b = lib.atlas_tensor_map_bwd
+    assert f(_lib.DT_F32, 8, 64, 128, good, good, good, None) == 3            # bf16 only
+    assert f(_lib.DT_BF16, 8, 48, 128, good, good, good, None) == 2           # d_in in (32, 64)
+    assert f(_lib.DT_BF16, 8, 64, 96, good, good, good, None) == 2            # d_out in (32, 64, 128)
+    assert f(_lib.DT_BF16, 8, 64, 128, None, good, good, None) == 4
+    assert f(_lib.DT_BF16, 8, 64, 128, good, bad, good, None) == 5
+    assert f(_lib.DT_BF16, 0, 64, 128, good, good, good, None) == 0           # empty: nothing launched
+    assert b(_lib.DT_BF16, 8, 64, 128, good, good, good, None, None) == 4
+    assert b(_lib.DT_BF16, 8, 64, 128, good, good, bad, good, None) == 5
+    assert b(_lib.DT_BF16, -1, 64, 128, good, good, good, good, None) == 2
+
+
+def test_tensor_feature_map_reference_form_off_gpu():
+    """On the CPU (and for shapes or dtypes the kernels do not take) the map is the reference's
+    tensor-op formulation, which the oracle restates."""
+    torch = pytest.importorskip("torch")
+    from atlas_rnn_amd.functional import tensor_feature_map
+    from oracle import poly_feature_map
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(5, 7, 16, generator=g, dtype=torch.float64)
+    P = torch.randn(16 + 256, 16, generator=g, dtype=torch.float64)
+    torch.testing.assert_close(tensor_feature_map(x, P), poly_feature_map(x, 2, 'tensor', P))
+
+
 def test_cpu_tensors_are_rejected():
     torch = pytest.importorskip("torch")
     from atlas_rnn_amd.functional import memory_recurrence

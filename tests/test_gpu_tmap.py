@@ -1,0 +1,97 @@
+"""GPU parity of the fused tensor feature map (atlas_tensor_map_fwd / _bwd) against the fp64
+oracle map `poly_feature_map(x, 2, 'tensor', proj)` (rnn_memory.py:125-130), on bf16-rounded inputs:
+the map's output and the gradient of x for a seeded upstream gradient, rtol 2e-2 with an atol floor
+of 2e-2 * max|ref| (bf16). Then the BASELINE C4 composition at a reduced size: the tensor map
+(64 + 4096 -> 128) into the d_k = 128 / d_v = 64 recurrence with the elementwise map of degree 3,
+window 8, lag gates and momentum, against the oracle end to end (outputs and every input gradient).
+"""
+
+import sys
+
+import pytest
+import torch
+
+from _cases import compare
+from oracle import memory_recurrence_vectorised, poly_feature_map
+
+pytestmark = pytest.mark.gpu
+
+F64 = torch.float64
+BF16 = torch.bfloat16
+TOL = 2e-2
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("n,d,m", [(300, 64, 128), (129, 64, 64), (77, 32, 32), (1, 32, 128), (256, 64, 32),
+                                   (1000, 32, 64)])
+def test_tensor_map_parity(n, d, m):
+    from atlas_rnn_amd.functional import _TensorMapFn
+    _say(f"tensor map n={n} d={d} m={m}")
+    g = torch.Generator().manual_seed(n * 7 + d + m)
+    x = torch.randn(n, d, generator=g)
+    x = (x / x.norm(dim=-1, keepdim=True)).to(BF16)
+    bound = (6.0 / (d + d * d + m)) ** 0.5
+    P = ((torch.rand(d + d * d, m, generator=g) * 2 - 1) * bound).to(BF16)
+    gy = torch.randn(n, m, generator=g).to(BF16)
+    # oracle
+    x64 = x.to(F64).requires_grad_(True)
+    ref = poly_feature_map(x64, 2, 'tensor', P.to(F64))
+    (dref,) = torch.autograd.grad((ref * gy.to(F64)).sum(), [x64])
+    # kernels (through the autograd function, no fallback)
+    xg = x.cuda().requires_grad_(True)
+    out = _TensorMapFn.apply(xg, P.cuda())
+    (dx,) = torch.autograd.grad((out.float() * gy.cuda().float()).sum(), [xg])
+    torch.cuda.synchronize()
+    compare("phi", out.detach().float().cpu(), ref.detach(), TOL)
+    compare("dx", dx.float().cpu(), dref, TOL)
+
+
+def test_c4_composition_reduced():
+    """tensor map -> d_k 128 / d_v 64 recurrence (block path, elementwise map g = 3), fwd + bwd."""
+    from atlas_rnn_amd.functional import memory_recurrence, tensor_feature_map
+    BH, T, d, dk, dv, e = 4, 160, 64, 128, 64, 8
+    _say(f"c4 composition BH={BH} T={T}")
+    g = torch.Generator().manual_seed(4004)
+    r = lambda *s: torch.randn(*s, generator=g)
+    k = r(BH, T, d)
+    k = k / k.norm(dim=-1, keepdim=True)
+    q = r(BH, T, d)
+    q = q / q.norm(dim=-1, keepdim=True)
+    bound = (6.0 / (d + d * d + dk)) ** 0.5
+    P = ((torch.rand(d + d * d, dk, generator=g) * 2 - 1) * bound).to(BF16)
+    x = dict(k=k, q=q, v=r(BH, T, dv), lr=0.1 * torch.sigmoid(r(BH, T)), decay=torch.sigmoid(r(BH, T) * 0.5 + 2.0),
+             beta=torch.sigmoid(r(BH, T) * 0.5 + 1.0), gate=torch.softmax(r(BH, T, e), -1))
+    x = {kk: v.to(BF16) for kk, v in x.items()}
+    S0 = 0.1 * r(BH, dv, dk)
+    gy = r(BH, T, dv).to(BF16)
+    gS = r(BH, dv, dk)
+    names = list(x)
+
+    # oracle: fp64 on the bf16 values; the map rounds its output to bf16 like the kernels' input
+    x64 = {kk: v.to(F64).requires_grad_(True) for kk, v in x.items()}
+    S064 = S0.to(F64)
+    pk = poly_feature_map(poly_feature_map(x64["k"], 2, 'tensor', P.to(F64)), 3, 'elementwise')
+    pq = poly_feature_map(poly_feature_map(x64["q"], 2, 'tensor', P.to(F64)), 3, 'elementwise')
+    y, S_T, Z_T, B = memory_recurrence_vectorised(pk, pq, x64["v"], x64["lr"], x64["decay"], x64["beta"], x64["gate"],
+                                                  S064, S064, torch.zeros_like(S064), None, window=e)
+    loss = (y * gy.to(F64)).sum() + (S_T * gS.to(F64)).sum()
+    ref_g = dict(zip(names, torch.autograd.grad(loss, [x64[kk] for kk in names])))
+
+    xg = {kk: v.cuda().requires_grad_(True) for kk, v in x.items()}
+    Sg = S0.cuda()
+    Pg = P.cuda()
+    fk = tensor_feature_map(xg["k"], Pg)
+    fq = tensor_feature_map(xg["q"], Pg)
+    yg, STg, ZTg, Bg = memory_recurrence(fk, fq, xg["v"], xg["lr"], xg["decay"], xg["beta"], xg["gate"], Sg, Sg,
+                                         torch.zeros_like(Sg), None, window=e, map_mode='elementwise', map_degree=3)
+    lg = (yg.float() * gy.cuda().float()).sum() + (STg * gS.cuda()).sum()
+    got_g = dict(zip(names, torch.autograd.grad(lg, [xg[kk] for kk in names])))
+    torch.cuda.synchronize()
+    compare("c4.y", yg.detach().float().cpu(), y.detach(), TOL)
+    compare("c4.S_T", STg.detach().float().cpu(), S_T.detach(), TOL)
+    for kk in names:
+        compare(f"c4.d{kk}", got_g[kk].float().cpu(), ref_g[kk], TOL)
