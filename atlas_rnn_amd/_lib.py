@@ -117,9 +117,9 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_affine_scan_bwd.restype = i32
     lib.atlas_affine_scan_bwd.argtypes = [i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.atlas_tensor_map_fwd.restype = i32
-    lib.atlas_tensor_map_fwd.argtypes = [i32, i64, i32, i32, vp, vp, vp, vp]
+    lib.atlas_tensor_map_fwd.argtypes = [i32, i64, i32, i32, i32, vp, vp, vp, vp, vp]
     lib.atlas_tensor_map_bwd.restype = i32
-    lib.atlas_tensor_map_bwd.argtypes = [i32, i64, i32, i32, vp, vp, vp, vp, vp]
+    lib.atlas_tensor_map_bwd.argtypes = [i32, i64, i32, i32, i32, vp, vp, vp, vp, vp, vp]
     lib.atlas_mem_profile_enable.restype = i32
     lib.atlas_mem_profile_enable.argtypes = [i32]
     lib.atlas_mem_profile_read.restype = i32

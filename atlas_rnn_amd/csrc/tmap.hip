@@ -17,6 +17,11 @@
 //   owning lanes (x[n, a] is one value per lane), the second is a sum over b across the tile (in lane
 //   and over the four lane rows) written to an LDS table t1[half][n][a] and added at the end.
 //
+// An elementwise polynomial of degree deg after the projection (phi -> sum_{i=1..deg} phi^i, the
+// BASELINE C4 composition) is applied in the forward's epilogue on the fp32 accumulator, which then
+// also stores the projection itself (pre); the backward scales dphi by the map's derivative at pre
+// as it loads dphi.
+//
 // Token tiles of 128 rows; rows past N load zeros and their stores are dropped (buffer range checks).
 #include "mem_common.h"
 #include "walk_common.h"
@@ -39,7 +44,8 @@ struct TmapFwdSmem {
 template <int D, int M>
 __global__ __launch_bounds__(64 * 4 * (M / 32)) void k_tmap_fwd(long n_tok, const bf16* __restrict__ x,
                                                                    const bf16* __restrict__ pt,
-                                                                   bf16* __restrict__ out) {
+                                                                   bf16* __restrict__ out, int deg,
+                                                                   bf16* __restrict__ pre) {
   constexpr int NW = 4 * (M / 32), NT = 64 * NW, K = D + D * D, NS = D / 32;
   constexpr int PV = M * D / 8;   // 16-byte vectors of one P^T block
   static_assert(PV % NT == 0 || NT % PV == 0, "block staging");
@@ -130,16 +136,30 @@ __global__ __launch_bounds__(64 * 4 * (M / 32)) void k_tmap_fwd(long n_tok, cons
   }
 
   // phi^T tiles: lane (g, i) holds phi[token 32 rg + 16 nt + i][feature 32 cg + 16 jt + 4 g + r]
-  const rsrc_t ro = make_rsrc(out + n0 * M, (uint32_t)(min((long)tm::TN, n_tok - n0) * M * 2));
+  const uint32_t obytes = (uint32_t)(min((long)tm::TN, n_tok - n0) * M * 2);
+  const rsrc_t ro = make_rsrc(out + n0 * M, obytes);
+  const rsrc_t rpre = make_rsrc(pre ? pre + n0 * M : out, pre ? obytes : 0u);
 #pragma unroll
   for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int r = 32 * rg + 16 * nt + i, j = 32 * cg + 16 * jt + 4 * g;
+      const uint32_t off = (uint32_t)((r * M + j) * 2);
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = acc[jt][nt][e];
+      if (deg > 1) {   // uniform
+        u32x2v p;
+        p[0] = pack_bf16x2(v[0], v[1]);
+        p[1] = pack_bf16x2(v[2], v[3]);
+        bst8(rpre, off, p);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = poly_map(v[e], deg);
+      }
       u32x2v o;
-      o[0] = pack_bf16x2(acc[jt][nt][0], acc[jt][nt][1]);
-      o[1] = pack_bf16x2(acc[jt][nt][2], acc[jt][nt][3]);
-      bst8(ro, (uint32_t)((r * M + j) * 2), o);
+      o[0] = pack_bf16x2(v[0], v[1]);
+      o[1] = pack_bf16x2(v[2], v[3]);
+      bst8(ro, off, o);
     }
 }
 
@@ -157,7 +177,8 @@ template <int D, int M>
 __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, const bf16* __restrict__ x,
                                                                    const bf16* __restrict__ proj,
                                                                    const bf16* __restrict__ dout,
-                                                                   bf16* __restrict__ dx) {
+                                                                   bf16* __restrict__ dx, int deg,
+                                                                   const bf16* __restrict__ pre) {
   constexpr int NW = 4 * (D / 32), NT = 64 * NW, NK = M / 32;
   constexpr int PV = D * M / 8;   // 16-byte vectors of one block of D rows of P
   constexpr int PVT = (PV + NT - 1) / NT;
@@ -192,13 +213,24 @@ __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, cons
       if (v < PV) *reinterpret_cast<u32x4v*>(&sm.pb[buf][v / (M / 8)][(v % (M / 8)) * 8]) = pf[u];
     }
   };
-  // dphi of this lane's tokens as k operands over j (kept for the whole launch)
+  // dphi of this lane's tokens as k operands over j (kept for the whole launch); with the
+  // elementwise map, dphi = dout * map'(pre)
+  const rsrc_t rpre = make_rsrc(pre ? pre + n0 * M : dout, pre ? (uint32_t)(nrow * M * 2) : 0u);
   bf16x8 fd[2][NK];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-    for (int ks = 0; ks < NK; ++ks)
-      fd[nt][ks] = __builtin_bit_cast(bf16x8, bld16(rd, (uint32_t)(((32 * rg + 16 * nt + i) * M + 32 * ks + 8 * g) * 2)));
+    for (int ks = 0; ks < NK; ++ks) {
+      const uint32_t off = (uint32_t)(((32 * rg + 16 * nt + i) * M + 32 * ks + 8 * g) * 2);
+      fd[nt][ks] = __builtin_bit_cast(bf16x8, bld16(rd, off));
+      if (deg > 1) {   // uniform
+        const bf16x8 pv = __builtin_bit_cast(bf16x8, bld16(rpre, off));
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          fd[nt][ks][e] = static_cast<bf16>(static_cast<float>(fd[nt][ks][e]) *
+                                            poly_map_grad(static_cast<float>(pv[e]), deg));
+      }
+    }
   p_load(0);
   p_store(0);
   p_load(1);
@@ -289,40 +321,42 @@ __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, cons
 }
 
 template <int D, int M>
-hipError_t launch_tmap_fwd(long n, const bf16* x, const bf16* pt, bf16* out, hipStream_t s) {
+hipError_t launch_tmap_fwd(long n, const bf16* x, const bf16* pt, bf16* out, int deg, bf16* pre, hipStream_t s) {
   const unsigned grid = (unsigned)((n + tm::TN - 1) / tm::TN);
-  hipLaunchKernelGGL((k_tmap_fwd<D, M>), dim3(grid), dim3(64 * 4 * (M / 32)), 0, s, n, x, pt, out);
+  hipLaunchKernelGGL((k_tmap_fwd<D, M>), dim3(grid), dim3(64 * 4 * (M / 32)), 0, s, n, x, pt, out, deg, pre);
   return hipGetLastError();
 }
 
 template <int D, int M>
-hipError_t launch_tmap_bwd(long n, const bf16* x, const bf16* p, const bf16* dout, bf16* dx, hipStream_t s) {
+hipError_t launch_tmap_bwd(long n, const bf16* x, const bf16* p, const bf16* dout, bf16* dx, int deg, const bf16* pre,
+                           hipStream_t s) {
   const size_t smem = sizeof(TmapBwdSmem<D, M>);
   hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_tmap_bwd<D, M>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (err != hipSuccess) return err;
   const unsigned grid = (unsigned)((n + tm::TN - 1) / tm::TN);
-  hipLaunchKernelGGL((k_tmap_bwd<D, M>), dim3(grid), dim3(64 * 4 * (D / 32)), smem, s, n, x, p, dout, dx);
+  hipLaunchKernelGGL((k_tmap_bwd<D, M>), dim3(grid), dim3(64 * 4 * (D / 32)), smem, s, n, x, p, dout, dx, deg, pre);
   return hipGetLastError();
 }
 
 // d_in in {32, 64}, d_out in {32, 64, 128}
-hipError_t tmap_fwd(int d, int m, long n, const bf16* x, const bf16* pt, bf16* out, hipStream_t s) {
-  if (d == 64 && m == 128) return launch_tmap_fwd<64, 128>(n, x, pt, out, s);
-  if (d == 64 && m == 64) return launch_tmap_fwd<64, 64>(n, x, pt, out, s);
-  if (d == 64 && m == 32) return launch_tmap_fwd<64, 32>(n, x, pt, out, s);
-  if (d == 32 && m == 128) return launch_tmap_fwd<32, 128>(n, x, pt, out, s);
-  if (d == 32 && m == 64) return launch_tmap_fwd<32, 64>(n, x, pt, out, s);
-  if (d == 32 && m == 32) return launch_tmap_fwd<32, 32>(n, x, pt, out, s);
+hipError_t tmap_fwd(int d, int m, long n, const bf16* x, const bf16* pt, bf16* out, int deg, bf16* pre, hipStream_t s) {
+  if (d == 64 && m == 128) return launch_tmap_fwd<64, 128>(n, x, pt, out, deg, pre, s);
+  if (d == 64 && m == 64) return launch_tmap_fwd<64, 64>(n, x, pt, out, deg, pre, s);
+  if (d == 64 && m == 32) return launch_tmap_fwd<64, 32>(n, x, pt, out, deg, pre, s);
+  if (d == 32 && m == 128) return launch_tmap_fwd<32, 128>(n, x, pt, out, deg, pre, s);
+  if (d == 32 && m == 64) return launch_tmap_fwd<32, 64>(n, x, pt, out, deg, pre, s);
+  if (d == 32 && m == 32) return launch_tmap_fwd<32, 32>(n, x, pt, out, deg, pre, s);
   return hipErrorInvalidValue;
 }
-hipError_t tmap_bwd(int d, int m, long n, const bf16* x, const bf16* p, const bf16* dout, bf16* dx, hipStream_t s) {
-  if (d == 64 && m == 128) return launch_tmap_bwd<64, 128>(n, x, p, dout, dx, s);
-  if (d == 64 && m == 64) return launch_tmap_bwd<64, 64>(n, x, p, dout, dx, s);
-  if (d == 64 && m == 32) return launch_tmap_bwd<64, 32>(n, x, p, dout, dx, s);
-  if (d == 32 && m == 128) return launch_tmap_bwd<32, 128>(n, x, p, dout, dx, s);
-  if (d == 32 && m == 64) return launch_tmap_bwd<32, 64>(n, x, p, dout, dx, s);
-  if (d == 32 && m == 32) return launch_tmap_bwd<32, 32>(n, x, p, dout, dx, s);
+hipError_t tmap_bwd(int d, int m, long n, const bf16* x, const bf16* p, const bf16* dout, bf16* dx, int deg,
+                    const bf16* pre, hipStream_t s) {
+  if (d == 64 && m == 128) return launch_tmap_bwd<64, 128>(n, x, p, dout, dx, deg, pre, s);
+  if (d == 64 && m == 64) return launch_tmap_bwd<64, 64>(n, x, p, dout, dx, deg, pre, s);
+  if (d == 64 && m == 32) return launch_tmap_bwd<64, 32>(n, x, p, dout, dx, deg, pre, s);
+  if (d == 32 && m == 128) return launch_tmap_bwd<32, 128>(n, x, p, dout, dx, deg, pre, s);
+  if (d == 32 && m == 64) return launch_tmap_bwd<32, 64>(n, x, p, dout, dx, deg, pre, s);
+  if (d == 32 && m == 32) return launch_tmap_bwd<32, 32>(n, x, p, dout, dx, deg, pre, s);
   return hipErrorInvalidValue;
 }
 
@@ -342,30 +376,35 @@ bool tmap_misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1
 
 extern "C" {
 
-int atlas_tensor_map_fwd(int dtype, int64_t n, int d_in, int d_out, const void* x, const void* proj_t, void* out,
-                         void* stream) {
+int atlas_tensor_map_fwd(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x, const void* proj_t,
+                         void* out, void* pre, void* stream) {
   if (dtype != ATLAS_DT_BF16) return ATLAS_MEM_ERR_DTYPE;
-  if (!tmap_dims_ok(n, d_in, d_out)) return ATLAS_MEM_ERR_SHAPE;
-  if (!x || !proj_t || !out) return ATLAS_MEM_ERR_NULL;
-  if (tmap_misaligned(x) || tmap_misaligned(proj_t) || tmap_misaligned(out)) return ATLAS_MEM_ERR_ALIGN;
+  if (!tmap_dims_ok(n, d_in, d_out) || degree < 1 || degree > 16) return ATLAS_MEM_ERR_SHAPE;
+  if (!x || !proj_t || !out || (degree > 1 && !pre)) return ATLAS_MEM_ERR_NULL;
+  if (tmap_misaligned(x) || tmap_misaligned(proj_t) || tmap_misaligned(out) || tmap_misaligned(pre))
+    return ATLAS_MEM_ERR_ALIGN;
   if (n == 0) return ATLAS_MEM_OK;
   const hipError_t err = atlas::tmap_fwd(d_in, d_out, (long)n, static_cast<const atlas::bf16*>(x),
                                          static_cast<const atlas::bf16*>(proj_t), static_cast<atlas::bf16*>(out),
+                                         degree, degree > 1 ? static_cast<atlas::bf16*>(pre) : nullptr,
                                          static_cast<hipStream_t>(stream));
   return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
 }
 
-int atlas_tensor_map_bwd(int dtype, int64_t n, int d_in, int d_out, const void* x, const void* proj,
-                         const void* dout, void* dx, void* stream) {
+int atlas_tensor_map_bwd(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x, const void* proj,
+                         const void* pre, const void* dout, void* dx, void* stream) {
   if (dtype != ATLAS_DT_BF16) return ATLAS_MEM_ERR_DTYPE;
-  if (!tmap_dims_ok(n, d_in, d_out)) return ATLAS_MEM_ERR_SHAPE;
-  if (!x || !proj || !dout || !dx) return ATLAS_MEM_ERR_NULL;
-  if (tmap_misaligned(x) || tmap_misaligned(proj) || tmap_misaligned(dout) || tmap_misaligned(dx))
+  if (!tmap_dims_ok(n, d_in, d_out) || degree < 1 || degree > 16) return ATLAS_MEM_ERR_SHAPE;
+  if (!x || !proj || !dout || !dx || (degree > 1 && !pre)) return ATLAS_MEM_ERR_NULL;
+  if (tmap_misaligned(x) || tmap_misaligned(proj) || tmap_misaligned(dout) || tmap_misaligned(dx) ||
+      tmap_misaligned(pre))
     return ATLAS_MEM_ERR_ALIGN;
   if (n == 0) return ATLAS_MEM_OK;
   const hipError_t err = atlas::tmap_bwd(d_in, d_out, (long)n, static_cast<const atlas::bf16*>(x),
                                          static_cast<const atlas::bf16*>(proj), static_cast<const atlas::bf16*>(dout),
-                                         static_cast<atlas::bf16*>(dx), static_cast<hipStream_t>(stream));
+                                         static_cast<atlas::bf16*>(dx), degree,
+                                         degree > 1 ? static_cast<const atlas::bf16*>(pre) : nullptr,
+                                         static_cast<hipStream_t>(stream));
   return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
 }
 

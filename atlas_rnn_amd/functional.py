@@ -84,6 +84,9 @@ class MemoryRecurrenceFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buf, cfg: RecurrenceConfig):
+        # outputs a loss does not use get no gradient tensor (the kernels treat a missing dS_T,
+        # dZ_T or buffer_out gradient as zero without reading one)
+        ctx.set_materialize_grads(False)
         lib = _lib.load()
         bh, T, dk = k.shape
         dv = v.shape[-1]
@@ -177,11 +180,12 @@ def _tensor_map_reference_form(x: Tensor, proj: Tensor) -> Tensor:
 
 
 class _TensorMapFn(torch.autograd.Function):
-    """atlas_tensor_map_fwd / _bwd: bf16 x [n, d] and P [d + d*d, m] -> phi [n, m]; P is a constant
-    (a registered buffer in the reference, so it has no gradient)."""
+    """atlas_tensor_map_fwd / _bwd: bf16 x [n, d] and P [d + d*d, m] -> phi [n, m], followed by the
+    elementwise polynomial of `degree` (1: none); P is a constant (a registered buffer in the
+    reference, so it has no gradient)."""
 
     @staticmethod
-    def forward(ctx, x, proj):
+    def forward(ctx, x, proj, degree):
         dev = _require_gpu(x, proj)
         lib = _lib.load()
         lead, d, m = x.shape[:-1], x.shape[-1], proj.shape[-1]
@@ -190,37 +194,47 @@ class _TensorMapFn(torch.autograd.Function):
         pt = _aligned(p.t())
         n = x2.shape[0]
         out = torch.empty(n, m, device=dev, dtype=torch.bfloat16)
-        _lib.check(lib.atlas_tensor_map_fwd(_lib.DT_BF16, n, d, m, _ptr(x2), _ptr(pt), _ptr(out), _stream(dev)),
-                   "atlas_tensor_map_fwd")
-        ctx.save_for_backward(x2, p)
+        pre = torch.empty(n, m, device=dev, dtype=torch.bfloat16) if degree > 1 else None
+        _lib.check(lib.atlas_tensor_map_fwd(_lib.DT_BF16, n, d, m, degree, _ptr(x2), _ptr(pt), _ptr(out), _ptr(pre),
+                                            _stream(dev)), "atlas_tensor_map_fwd")
+        ctx.save_for_backward(x2, p, pre)
         ctx.lead = lead
+        ctx.degree = degree
         return out.reshape(*lead, m)
 
     @staticmethod
     def backward(ctx, dout):
-        x2, p = ctx.saved_tensors
+        x2, p, pre = ctx.saved_tensors
         dev = x2.device
         lib = _lib.load()
         n, d = x2.shape
         m = p.shape[-1]
         g = _aligned(dout.reshape(-1, m).to(torch.bfloat16))
         dx = torch.empty_like(x2)
-        _lib.check(lib.atlas_tensor_map_bwd(_lib.DT_BF16, n, d, m, _ptr(x2), _ptr(p), _ptr(g), _ptr(dx), _stream(dev)),
-                   "atlas_tensor_map_bwd")
-        return dx.reshape(*ctx.lead, d), None
+        _lib.check(lib.atlas_tensor_map_bwd(_lib.DT_BF16, n, d, m, ctx.degree, _ptr(x2), _ptr(p), _ptr(pre), _ptr(g),
+                                            _ptr(dx), _stream(dev)), "atlas_tensor_map_bwd")
+        return dx.reshape(*ctx.lead, d), None, None
 
 
-def tensor_feature_map(x: Tensor, proj: Tensor) -> Tensor:
-    """[x; vec(x x^T)] @ proj (rnn_memory.py:125-130). bf16 GPU inputs with d in (32, 64) and
+def tensor_feature_map(x: Tensor, proj: Tensor, degree: int = 1) -> Tensor:
+    """[x; vec(x x^T)] @ proj (rnn_memory.py:125-130), then (degree > 1) the elementwise polynomial
+    sum_{i=1..degree} phi^i (BASELINE C4's composition). bf16 GPU inputs with d in (32, 64) and
     proj [d + d*d, m], m in (32, 64, 128), and a constant proj run the fused kernels (the Kronecker
-    features are never materialised); other dtypes, sizes or a trainable proj use the reference's
-    tensor ops."""
+    features are never materialised; the polynomial is applied on the fp32 accumulator); other
+    dtypes, sizes or a trainable proj use the reference's tensor ops."""
     d, m = x.shape[-1], proj.shape[-1]
     fused = (x.is_cuda and x.dtype == torch.bfloat16 and d in _TMAP_DIN and m in _TMAP_DOUT
-             and proj.shape[0] == d + d * d and not proj.requires_grad)
+             and proj.shape[0] == d + d * d and not proj.requires_grad and 1 <= degree <= 16)
     if not fused:
-        return _tensor_map_reference_form(x, proj)
-    return _TensorMapFn.apply(x, proj)
+        phi = _tensor_map_reference_form(x, proj)
+        if degree > 1:
+            out, pw = phi, phi
+            for _ in range(2, degree + 1):
+                pw = pw * phi
+                out = out + pw
+            phi = out
+        return phi
+    return _TensorMapFn.apply(x, proj, int(degree))
 
 
 _BLOCK = 64    # block width of the decomposition for head sizes the kernels are not built for

@@ -204,14 +204,13 @@ def run_other_config(name, steps, warmup):
     gy = bf(r(bh, t, dv))
     zeros = torch.zeros(bh, dv, dk, device=dev)
 
-    def feat(x):   # fused tensor-map kernels (atlas_tensor_map_fwd / _bwd)
-        return tensor_feature_map(x, P) if tensor_map else x
+    def feat(x):   # fused tensor-map kernels, elementwise map of degree 3 in their epilogue
+        return tensor_feature_map(x, P, degree=3) if tensor_map else x
 
     def step():
         y, S_T, Z_T, B_out = memory_recurrence(
             feat(leaves["k"]), feat(leaves["q"]), leaves["v"], leaves["lr"], leaves["decay"], leaves["beta"],
-            leaves["gate"], zeros, zeros, zeros, None, window=e,
-            map_mode="elementwise" if tensor_map else "off", map_degree=3 if tensor_map else 1)
+            leaves["gate"], zeros, zeros, zeros, None, window=e)
         ins = [v for v in leaves.values() if v is not None]
         torch.autograd.grad((y.float() * gy.float()).sum(), ins)
 

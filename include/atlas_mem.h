@@ -177,18 +177,20 @@ int atlas_affine_scan_bwd(int n, int t, int r, int d, const float* A, const floa
 
 /* Tensor polynomial feature map, fused (replaces the 'tensor' mode of PolynomialFeatureMap,
  * atlas_pytorch/rnn_memory.py:125-130, which materialises vec(x x^T) with einsum / cat / matmul):
- *   out = [x; vec(x x^T)] P,  x [n, d_in] bf16, P [d_in + d_in^2, d_out] bf16 (row a*d_in + b of
- *   the quadratic part multiplies x_a x_b), out [n, d_out] bf16, fp32 accumulation.
+ *   pre = [x; vec(x x^T)] P,  out = sum_{i=1..degree} pre^i  (degree 1: out = pre),
+ *   x [n, d_in] bf16, P [d_in + d_in^2, d_out] bf16 (row d_in + a*d_in + b multiplies x_a x_b),
+ *   out, pre [n, d_out] bf16 (pre written only for degree > 1, for the backward), fp32 accumulation.
+ * degree > 1 is the elementwise map after the projection (BASELINE config C4's composition).
  * The forward takes P transposed (proj_t [d_out, d_in + d_in^2]); d_in in {32, 64},
- * d_out in {32, 64, 128}; bf16 only; every pointer 16-byte aligned. */
-int atlas_tensor_map_fwd(int dtype, int64_t n, int d_in, int d_out, const void* x, const void* proj_t, void* out,
-                         void* stream);
+ * d_out in {32, 64, 128}, degree 1..16; bf16 only; every pointer 16-byte aligned. */
+int atlas_tensor_map_fwd(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x, const void* proj_t,
+                         void* out, void* pre, void* stream);
 
 /* Gradient of atlas_tensor_map_fwd with respect to x for the output gradient dout [n, d_out]
- * (P is a fixed buffer in the reference: no gradient). Takes P itself (proj [d_in + d_in^2, d_out]);
- * dx [n, d_in] bf16. */
-int atlas_tensor_map_bwd(int dtype, int64_t n, int d_in, int d_out, const void* x, const void* proj,
-                         const void* dout, void* dx, void* stream);
+ * (P is a fixed buffer in the reference: no gradient). Takes P itself (proj [d_in + d_in^2, d_out])
+ * and, for degree > 1, the forward's pre; dx [n, d_in] bf16. */
+int atlas_tensor_map_bwd(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x, const void* proj,
+                         const void* pre, const void* dout, void* dx, void* stream);
 
 /* ---- diagnostics (no reference counterpart) ------------------------------------------------ */
 

@@ -125,15 +125,18 @@ def test_tensor_map_errors_before_launch(lib):
     good, bad = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x10008)
     f = lib.atlas_tensor_map_fwd
     b = lib.atlas_tensor_map_bwd
-    assert f(_lib.DT_F32, 8, 64, 128, good, good, good, None) == 3            # bf16 only
-    assert f(_lib.DT_BF16, 8, 48, 128, good, good, good, None) == 2           # d_in in (32, 64)
-    assert f(_lib.DT_BF16, 8, 64, 96, good, good, good, None) == 2            # d_out in (32, 64, 128)
-    assert f(_lib.DT_BF16, 8, 64, 128, None, good, good, None) == 4
-    assert f(_lib.DT_BF16, 8, 64, 128, good, bad, good, None) == 5
-    assert f(_lib.DT_BF16, 0, 64, 128, good, good, good, None) == 0           # empty: nothing launched
-    assert b(_lib.DT_BF16, 8, 64, 128, good, good, good, None, None) == 4
-    assert b(_lib.DT_BF16, 8, 64, 128, good, good, bad, good, None) == 5
-    assert b(_lib.DT_BF16, -1, 64, 128, good, good, good, good, None) == 2
+    assert f(_lib.DT_F32, 8, 64, 128, 1, good, good, good, None, None) == 3         # bf16 only
+    assert f(_lib.DT_BF16, 8, 48, 128, 1, good, good, good, None, None) == 2        # d_in in (32, 64)
+    assert f(_lib.DT_BF16, 8, 64, 96, 1, good, good, good, None, None) == 2         # d_out in (32, 64, 128)
+    assert f(_lib.DT_BF16, 8, 64, 128, 0, good, good, good, None, None) == 2        # degree 1..16
+    assert f(_lib.DT_BF16, 8, 64, 128, 1, None, good, good, None, None) == 4
+    assert f(_lib.DT_BF16, 8, 64, 128, 3, good, good, good, None, None) == 4        # degree > 1 needs pre
+    assert f(_lib.DT_BF16, 8, 64, 128, 1, good, bad, good, None, None) == 5
+    assert f(_lib.DT_BF16, 0, 64, 128, 1, good, good, good, None, None) == 0        # empty: nothing launched
+    assert b(_lib.DT_BF16, 8, 64, 128, 1, good, good, None, good, None, None) == 4
+    assert b(_lib.DT_BF16, 8, 64, 128, 1, good, good, None, bad, good, None) == 5
+    assert b(_lib.DT_BF16, 8, 64, 128, 2, good, good, None, good, good, None) == 4  # degree > 1 needs pre
+    assert b(_lib.DT_BF16, -1, 64, 128, 1, good, good, None, good, good, None) == 2
 
 
 def test_tensor_feature_map_reference_form_off_gpu():
@@ -146,6 +149,8 @@ def test_tensor_feature_map_reference_form_off_gpu():
     x = torch.randn(5, 7, 16, generator=g, dtype=torch.float64)
     P = torch.randn(16 + 256, 16, generator=g, dtype=torch.float64)
     torch.testing.assert_close(tensor_feature_map(x, P), poly_feature_map(x, 2, 'tensor', P))
+    torch.testing.assert_close(tensor_feature_map(x, P, degree=3),
+                               poly_feature_map(poly_feature_map(x, 2, 'tensor', P), 3, 'elementwise'))
 
 
 def test_cpu_tensors_are_rejected():

@@ -26,11 +26,11 @@ def _say(msg):
     sys.stdout.flush()
 
 
-@pytest.mark.parametrize("n,d,m", [(300, 64, 128), (129, 64, 64), (77, 32, 32), (1, 32, 128), (256, 64, 32),
-                                   (1000, 32, 64)])
-def test_tensor_map_parity(n, d, m):
+@pytest.mark.parametrize("n,d,m,deg", [(300, 64, 128, 1), (129, 64, 64, 1), (77, 32, 32, 1), (1, 32, 128, 1),
+                                       (256, 64, 32, 1), (1000, 32, 64, 1), (300, 64, 128, 3), (65, 32, 64, 2)])
+def test_tensor_map_parity(n, d, m, deg):
     from atlas_rnn_amd.functional import _TensorMapFn
-    _say(f"tensor map n={n} d={d} m={m}")
+    _say(f"tensor map n={n} d={d} m={m} degree={deg}")
     g = torch.Generator().manual_seed(n * 7 + d + m)
     x = torch.randn(n, d, generator=g)
     x = (x / x.norm(dim=-1, keepdim=True)).to(BF16)
@@ -39,11 +39,11 @@ def test_tensor_map_parity(n, d, m):
     gy = torch.randn(n, m, generator=g).to(BF16)
     # oracle
     x64 = x.to(F64).requires_grad_(True)
-    ref = poly_feature_map(x64, 2, 'tensor', P.to(F64))
+    ref = poly_feature_map(poly_feature_map(x64, 2, 'tensor', P.to(F64)), deg, 'elementwise')
     (dref,) = torch.autograd.grad((ref * gy.to(F64)).sum(), [x64])
     # kernels (through the autograd function, no fallback)
     xg = x.cuda().requires_grad_(True)
-    out = _TensorMapFn.apply(xg, P.cuda())
+    out = _TensorMapFn.apply(xg, P.cuda(), deg)
     (dx,) = torch.autograd.grad((out.float() * gy.cuda().float()).sum(), [xg])
     torch.cuda.synchronize()
     compare("phi", out.detach().float().cpu(), ref.detach(), TOL)
@@ -84,10 +84,10 @@ def test_c4_composition_reduced():
     xg = {kk: v.cuda().requires_grad_(True) for kk, v in x.items()}
     Sg = S0.cuda()
     Pg = P.cuda()
-    fk = tensor_feature_map(xg["k"], Pg)
-    fq = tensor_feature_map(xg["q"], Pg)
+    fk = tensor_feature_map(xg["k"], Pg, degree=3)
+    fq = tensor_feature_map(xg["q"], Pg, degree=3)
     yg, STg, ZTg, Bg = memory_recurrence(fk, fq, xg["v"], xg["lr"], xg["decay"], xg["beta"], xg["gate"], Sg, Sg,
-                                         torch.zeros_like(Sg), None, window=e, map_mode='elementwise', map_degree=3)
+                                         torch.zeros_like(Sg), None, window=e)
     lg = (yg.float() * gy.cuda().float()).sum() + (STg * gS.cuda()).sum()
     got_g = dict(zip(names, torch.autograd.grad(lg, [xg[kk] for kk in names])))
     torch.cuda.synchronize()
