@@ -33,27 +33,33 @@ constexpr int TN = 128;   // tokens per workgroup
 }
 
 // ---------------------------------------------------------------------------------------------
-// forward: waves = 4 (token groups of 32) x M / 32 (feature groups of 32); lane tile 2 x 2 of 16 x 16
+// forward: waves = 4 (token groups of 32) x M / FG (feature groups of FG = min(M, 64)); lane tile
+// 2 token tiles x FG / 16 feature tiles, so each Kronecker operand built in registers feeds FG / 16
+// matrix products. P^T blocks are loaded two blocks ahead into registers (two stages), then staged in
+// LDS (double buffered).
 // ---------------------------------------------------------------------------------------------
+template <int M> constexpr int tmap_fg() { return M < 64 ? M : 64; }
+template <int M> constexpr int tmap_fwd_threads() { return 64 * 4 * (M / tmap_fg<M>()); }
+
 template <int D, int M>
 struct TmapFwdSmem {
   alignas(16) bf16 xs[tm::TN][D + 8];
   alignas(16) bf16 pt[2][M][D + 8];   // P^T columns of the current / next block
 };
 
+// Four waves per SIMD (at most 128 VGPRs): the few bytes of spill this costs at D = 64, M = 128 are
+// cheaper than the third wave's missing latency cover (measured).
 template <int D, int M>
-__global__ __launch_bounds__(64 * 4 * (M / 32)) void k_tmap_fwd(long n_tok, const bf16* __restrict__ x,
-                                                                   const bf16* __restrict__ pt,
-                                                                   bf16* __restrict__ out, int deg,
-                                                                   bf16* __restrict__ pre) {
-  constexpr int NW = 4 * (M / 32), NT = 64 * NW, K = D + D * D, NS = D / 32;
+__global__ __launch_bounds__(tmap_fwd_threads<M>()) __attribute__((amdgpu_waves_per_eu(4)))
+void k_tmap_fwd(long n_tok, const bf16* __restrict__ x, const bf16* __restrict__ pt, bf16* __restrict__ out,
+                int deg, bf16* __restrict__ pre) {
+  constexpr int FG = tmap_fg<M>(), JT = FG / 16, NT = tmap_fwd_threads<M>(), K = D + D * D, NS = D / 32;
   constexpr int PV = M * D / 8;   // 16-byte vectors of one P^T block
-  static_assert(PV % NT == 0 || NT % PV == 0, "block staging");
   constexpr int PVT = (PV + NT - 1) / NT;
   __shared__ TmapFwdSmem<D, M> sm;
   const int tid = threadIdx.x, lane = lane_id(), w = threadIdx.x >> 6;
   const int g = lane >> 4, i = lane & 15;
-  const int rg = w & 3, cg = w >> 2;     // tokens 32 rg .., features 32 cg ..
+  const int rg = w & 3, cg = w >> 2;     // tokens 32 rg .., features FG cg ..
   const long n0 = (long)blockIdx.x * tm::TN;
   const uint32_t xbytes = (uint32_t)(min((long)tm::TN, n_tok - n0) * D * 2);
   const rsrc_t rx = make_rsrc(x + n0 * D, xbytes);
@@ -65,25 +71,26 @@ __global__ __launch_bounds__(64 * 4 * (M / 32)) void k_tmap_fwd(long n_tok, cons
     *reinterpret_cast<u32x4v*>(&sm.xs[r][c8 * 8]) = bld16(rx, (uint32_t)((r * D + c8 * 8) * 2));
   }
   // P^T block kb: columns kb*D .. of every feature row j (vector v: row v / (D/8), 8 columns)
-  u32x4v pf[PVT];
-  auto p_load = [&](int kb) {
+  u32x4v pf0[PVT], pf1[PVT];
+  auto p_load = [&](u32x4v (&pf)[PVT], int kb) {
 #pragma unroll
     for (int u = 0; u < PVT; ++u) {
       const int v = tid + u * NT;
       const int j = v / (D / 8), c8 = v % (D / 8);
-      pf[u] = bld16(rp, v < PV ? (uint32_t)((j * K + kb * D + c8 * 8) * 2) : kOob);
+      pf[u] = bld16(rp, (v < PV && kb <= D) ? (uint32_t)((j * K + kb * D + c8 * 8) * 2) : kOob);
     }
   };
-  auto p_store = [&](int buf) {
+  auto p_store = [&](const u32x4v (&pf)[PVT], int buf) {
 #pragma unroll
     for (int u = 0; u < PVT; ++u) {
       const int v = tid + u * NT;
       if (v < PV) *reinterpret_cast<u32x4v*>(&sm.pt[buf][v / (D / 8)][(v % (D / 8)) * 8]) = pf[u];
     }
   };
-  p_load(0);
-  p_store(0);
-  p_load(1);
+  p_load(pf0, 0);
+  p_store(pf0, 0);
+  p_load(pf0, 1);
+  p_load(pf1, 2);
   __syncthreads();
 
   // x_b of this lane's k slots, per token tile: b = 32 s + 8 g + e
@@ -97,13 +104,15 @@ __global__ __launch_bounds__(64 * 4 * (M / 32)) void k_tmap_fwd(long n_tok, cons
       for (int e = 0; e < 8; ++e) xb[nt][s][e] = static_cast<float>(v[e]);
     }
 
-  f32x4 acc[2][2];
+  f32x4 acc[JT][2];
 #pragma unroll
-  for (int jt = 0; jt < 2; ++jt)
+  for (int jt = 0; jt < JT; ++jt)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) acc[jt][nt] = zero4();
 
-  for (int kb = 0; kb <= D; ++kb) {
+  // block kb from LDS buffer kb & 1; register stage `pf` holds block kb + 1 and is refilled with
+  // block kb + 3 after its store
+  auto block = [&](int kb, u32x4v (&pf)[PVT]) {
     const int buf = kb & 1;
     float xa[2];
 #pragma unroll
@@ -111,9 +120,7 @@ __global__ __launch_bounds__(64 * 4 * (M / 32)) void k_tmap_fwd(long n_tok, cons
       xa[nt] = static_cast<float>(sm.xs[32 * rg + 16 * nt + i][kb > 0 ? kb - 1 : 0]);
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      bf16x8 fa[2], fb[2];
-#pragma unroll
-      for (int jt = 0; jt < 2; ++jt) fa[jt] = frag_row(&sm.pt[buf][0][0], D + 8, 32 * cg + 16 * jt, 32 * s);
+      bf16x8 fb[2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         if (kb == 0) {   // workgroup-uniform: the linear block is x itself
@@ -124,26 +131,32 @@ __global__ __launch_bounds__(64 * 4 * (M / 32)) void k_tmap_fwd(long n_tok, cons
         }
       }
 #pragma unroll
-      for (int jt = 0; jt < 2; ++jt)
+      for (int jt = 0; jt < JT; ++jt) {
+        const bf16x8 fa = frag_row(&sm.pt[buf][0][0], D + 8, FG * cg + 16 * jt, 32 * s);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) acc[jt][nt] = mma_bf16(fa[jt], fb[nt], acc[jt][nt]);
+        for (int nt = 0; nt < 2; ++nt) acc[jt][nt] = mma_bf16(fa, fb[nt], acc[jt][nt]);
+      }
     }
     if (kb < D) {
-      p_store(buf ^ 1);
-      if (kb + 1 < D) p_load(kb + 2);
+      p_store(pf, buf ^ 1);
+      p_load(pf, kb + 3);   // past the last block: out-of-range loads (zeros), never stored
     }
     __syncthreads();
+  };
+  for (int kb = 0; kb <= D; kb += 2) {
+    block(kb, pf0);
+    if (kb + 1 <= D) block(kb + 1, pf1);
   }
 
-  // phi^T tiles: lane (g, i) holds phi[token 32 rg + 16 nt + i][feature 32 cg + 16 jt + 4 g + r]
+  // phi^T tiles: lane (g, i) holds phi[token 32 rg + 16 nt + i][feature FG cg + 16 jt + 4 g + r]
   const uint32_t obytes = (uint32_t)(min((long)tm::TN, n_tok - n0) * M * 2);
   const rsrc_t ro = make_rsrc(out + n0 * M, obytes);
   const rsrc_t rpre = make_rsrc(pre ? pre + n0 * M : out, pre ? obytes : 0u);
 #pragma unroll
-  for (int jt = 0; jt < 2; ++jt)
+  for (int jt = 0; jt < JT; ++jt)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      const int r = 32 * rg + 16 * nt + i, j = 32 * cg + 16 * jt + 4 * g;
+      const int r = 32 * rg + 16 * nt + i, j = FG * cg + 16 * jt + 4 * g;
       const uint32_t off = (uint32_t)((r * M + j) * 2);
       float v[4];
 #pragma unroll
@@ -197,16 +210,18 @@ __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, cons
     const int r = v / (D / 8), c8 = v % (D / 8);
     *reinterpret_cast<u32x4v*>(&sm.xs[r][c8 * 8]) = bld16(rx, (uint32_t)((r * D + c8 * 8) * 2));
   }
-  u32x4v pf[PVT];
-  auto p_load = [&](int kb) {   // P rows kb*D .. kb*D + D - 1 (kb 0: the linear rows, kb a + 1: row a of x x^T)
+  // P rows kb*D .. kb*D + D - 1 (kb 0: the linear rows, kb a + 1: row a of x x^T), loaded two
+  // blocks ahead into registers (two stages) and staged in LDS (double buffered)
+  u32x4v pf0[PVT], pf1[PVT];
+  auto p_load = [&](u32x4v (&pf)[PVT], int kb) {
 #pragma unroll
     for (int u = 0; u < PVT; ++u) {
       const int v = tid + u * NT;
       const int r = v / (M / 8), c8 = v % (M / 8);
-      pf[u] = bld16(rp, v < PV ? (uint32_t)(((kb * D + r) * M + c8 * 8) * 2) : kOob);
+      pf[u] = bld16(rp, (v < PV && kb <= D) ? (uint32_t)(((kb * D + r) * M + c8 * 8) * 2) : kOob);
     }
   };
-  auto p_store = [&](int buf) {
+  auto p_store = [&](const u32x4v (&pf)[PVT], int buf) {
 #pragma unroll
     for (int u = 0; u < PVT; ++u) {
       const int v = tid + u * NT;
@@ -231,9 +246,10 @@ __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, cons
                                             poly_map_grad(static_cast<float>(pv[e]), deg));
       }
     }
-  p_load(0);
-  p_store(0);
-  p_load(1);
+  p_load(pf0, 0);
+  p_store(pf0, 0);
+  p_load(pf0, 1);
+  p_load(pf1, 2);
   __syncthreads();
 
   // x[n, b] at this lane's tile positions: b = 32 cb + 16 bt + 4 g + r, n = 32 rg + 16 nt + i
@@ -251,7 +267,8 @@ __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, cons
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) acc[bt][nt] = zero4();
 
-  for (int kb = 0; kb <= D; ++kb) {
+  // block kb from LDS buffer kb & 1; register stage `pf` holds block kb + 1, refilled with kb + 3
+  auto block = [&](int kb, u32x4v (&pf)[PVT]) {
     const int buf = kb & 1;
     f32x4 gt[2][2];
 #pragma unroll
@@ -292,10 +309,14 @@ __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, cons
       }
     }
     if (kb < D) {
-      p_store(buf ^ 1);
-      if (kb + 1 < D) p_load(kb + 2);
+      p_store(pf, buf ^ 1);
+      p_load(pf, kb + 3);   // past the last block: out-of-range loads (zeros), never stored
     }
     __syncthreads();
+  };
+  for (int kb = 0; kb <= D; kb += 2) {
+    block(kb, pf0);
+    if (kb + 1 <= D) block(kb + 1, pf1);
   }
 
   // dx[n, c] = acc (c = 32 cb + 16 bt + 4 g + r) + sum over the halves of t1[., n, c]
@@ -323,7 +344,7 @@ __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, cons
 template <int D, int M>
 hipError_t launch_tmap_fwd(long n, const bf16* x, const bf16* pt, bf16* out, int deg, bf16* pre, hipStream_t s) {
   const unsigned grid = (unsigned)((n + tm::TN - 1) / tm::TN);
-  hipLaunchKernelGGL((k_tmap_fwd<D, M>), dim3(grid), dim3(64 * 4 * (M / 32)), 0, s, n, x, pt, out, deg, pre);
+  hipLaunchKernelGGL((k_tmap_fwd<D, M>), dim3(grid), dim3(tmap_fwd_threads<M>()), 0, s, n, x, pt, out, deg, pre);
   return hipGetLastError();
 }
 
