@@ -279,30 +279,38 @@ def block_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
     if map_mode == 'elementwise' and map_degree > 1:
         k, q = _poly_map(k, map_degree), _poly_map(q, map_degree)
     F = torch.nn.functional
-    phi, psi = F.pad(k, (0, pad_k)), F.pad(q, (0, pad_k))
-    vv = F.pad(v, (0, pad_v))
-    pst = lambda t: None if t is None else F.pad(t, (0, pad_k, 0, pad_v))
+    padf = lambda t, pads: t if t is None or not any(pads) else F.pad(t, pads)   # F.pad copies even at 0
+    phi, psi = padf(k, (0, pad_k)), padf(q, (0, pad_k))
+    vv = padf(v, (0, pad_v))
+    pst = lambda t: padf(t, (0, pad_k, 0, pad_v))
     S_ref, S0, Z0, buffer = pst(S_ref), pst(S0), pst(Z0), pst(buffer)
     # delta = S_ref phi - v (at least fp32), handed to every block as -v in the input dtype
     acc = torch.promote_types(k.dtype, torch.float32)
     delta = torch.matmul(phi.to(acc), S_ref.to(acc).transpose(-1, -2)) - vv.to(acc)
     nv = (-delta).to(k.dtype)
+    nb = nbv * nbk
 
-    def cols(x, j):            # [BH, T, Dk] -> feature block j
-        return x[..., j * _BLOCK:(j + 1) * _BLOCK]
+    # Stacking in (i, j, bh) order as one permuted copy per tensor (its gradient is one permuted
+    # copy back, plus a sum over the blocks that share the tensor).
+    def stack_cols(x, n_rep_outer, n_blk, n_rep_inner):   # [BH, T, n_blk * 64] -> [(o, blk, in, bh), T, 64]
+        x = x.reshape(bh, T, n_blk, _BLOCK).permute(2, 0, 1, 3).unsqueeze(1).unsqueeze(0)
+        x = x.expand(n_rep_outer, n_blk, n_rep_inner, bh, T, _BLOCK)
+        return x.reshape(n_rep_outer * n_blk * n_rep_inner * bh, T, _BLOCK)
 
-    def blk(x, i, j):          # [..., Dv, Dk] -> state block (i, j)
-        return x[..., i * _BLOCK:(i + 1) * _BLOCK, j * _BLOCK:(j + 1) * _BLOCK]
+    def stack_state(x):        # [BH, ..., Dv, Dk] -> [(i, j, bh), ..., 64, 64]
+        if x is None:
+            return None
+        mid = x.shape[1:-2]
+        x = x.reshape(bh, *mid, nbv, _BLOCK, nbk, _BLOCK)
+        m = len(mid)
+        x = x.permute(m + 1, m + 3, 0, *range(1, m + 1), m + 2, m + 4)
+        return x.reshape(nb * bh, *mid, _BLOCK, _BLOCK)
 
-    pairs = [(i, j) for i in range(nbv) for j in range(nbk)]
-    nb = len(pairs)
-    rep = lambda t: None if t is None else torch.cat([t] * nb, dim=0)
-    kb = torch.cat([cols(phi, j) for i, j in pairs], dim=0)
-    qb = torch.cat([cols(psi, j) for i, j in pairs], dim=0)
-    vb = torch.cat([nv[..., i * _BLOCK:(i + 1) * _BLOCK] for i, j in pairs], dim=0)
-    S0b = torch.cat([blk(S0, i, j) for i, j in pairs], dim=0)
-    Z0b = None if Z0 is None else torch.cat([blk(Z0, i, j) for i, j in pairs], dim=0)
-    Bb = None if buffer is None else torch.cat([blk(buffer, i, j) for i, j in pairs], dim=0)
+    rep = lambda t: None if t is None else t.unsqueeze(0).expand(nb, *t.shape).reshape(nb * bh, *t.shape[1:])
+    kb = stack_cols(phi, nbv, nbk, 1)
+    qb = stack_cols(psi, nbv, nbk, 1)
+    vb = stack_cols(nv, 1, nbv, nbk)
+    S0b, Z0b, Bb = stack_state(S0), stack_state(Z0), stack_state(buffer)
     Sref0 = torch.zeros_like(S0b)
     y, S_T, Z_T, B = inner(kb, qb, vb, rep(lr), rep(decay), rep(beta), rep(gate), Sref0, S0b, Z0b, Bb,
                            window=window, map_mode='off', map_degree=1, clamp_every=clamp_every,
@@ -313,8 +321,10 @@ def block_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
     def unblock(x):            # [(i, j, bh), ..., 64, 64] -> [bh, ..., Dv, Dk]
         if x is None:
             return None
-        x = x.reshape(nbv, nbk, bh, *x.shape[1:])
-        x = torch.cat([torch.cat([x[i, j] for j in range(nbk)], dim=-1) for i in range(nbv)], dim=-2)
+        mid = x.shape[1:-2]
+        m = len(mid)
+        x = x.reshape(nbv, nbk, bh, *mid, _BLOCK, _BLOCK)
+        x = x.permute(2, *range(3, m + 3), 0, m + 3, 1, m + 4).reshape(bh, *mid, Dv, Dk)
         return x[..., :dv, :dk]
 
     return y[..., :dv], unblock(S_T), unblock(Z_T), unblock(B)

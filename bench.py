@@ -170,7 +170,8 @@ OTHER_CONFIGS = {
 
 
 def run_other_config(name, steps, warmup):
-    """fwd+bwd of config `name` through the autograd API (torch.autograd.grad of sum(y * g))."""
+    """fwd+bwd of config `name` through the autograd API (torch.autograd.grad of y against a fixed
+    random output gradient, i.e. the gradient of sum(y * g))."""
     import torch
     from atlas_rnn_amd.functional import memory_recurrence, tensor_feature_map
     c = OTHER_CONFIGS[name]
@@ -212,7 +213,7 @@ def run_other_config(name, steps, warmup):
             feat(leaves["k"]), feat(leaves["q"]), leaves["v"], leaves["lr"], leaves["decay"], leaves["beta"],
             leaves["gate"], zeros, zeros, zeros, None, window=e)
         ins = [v for v in leaves.values() if v is not None]
-        torch.autograd.grad((y.float() * gy.float()).sum(), ins)
+        torch.autograd.grad(y, ins, grad_outputs=gy)
 
     for _ in range(warmup):
         step()
