@@ -267,10 +267,12 @@ __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, cons
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) acc[bt][nt] = zero4();
 
-  // block kb from LDS buffer kb & 1; register stage `pf` holds block kb + 1, refilled with kb + 3
-  auto block = [&](int kb, u32x4v (&pf)[PVT]) {
+  // Software pipeline over the blocks of K: step kb forms G's tiles of block kb (matrix cores,
+  // P block from LDS buffer kb & 1) while the vector units consume block kb - 1's tiles, which the
+  // previous step left in the other register set; one barrier per block. Register stage `pf`
+  // holds block kb + 1 and is refilled with kb + 3.
+  auto mma = [&](int kb, f32x4 (&gt)[2][2]) {
     const int buf = kb & 1;
-    f32x4 gt[2][2];
 #pragma unroll
     for (int bt = 0; bt < 2; ++bt)
 #pragma unroll
@@ -285,6 +287,8 @@ __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, cons
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) gt[bt][nt] = mma_bf16(fp[bt], fd[nt][ks], gt[bt][nt]);
     }
+  };
+  auto epi = [&](int kb, const f32x4 (&gt)[2][2]) {
     if (kb == 0) {   // workgroup-uniform: the linear rows give dx directly
 #pragma unroll
       for (int bt = 0; bt < 2; ++bt)
@@ -308,16 +312,22 @@ __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, cons
         if (g == 0) sm.t1[cb][n][a] = part;
       }
     }
+  };
+  auto step = [&](int kb, u32x4v (&pf)[PVT], f32x4 (&gcur)[2][2], const f32x4 (&gprev)[2][2]) {
+    mma(kb, gcur);
+    if (kb > 0) epi(kb - 1, gprev);
     if (kb < D) {
-      p_store(pf, buf ^ 1);
-      p_load(pf, kb + 3);   // past the last block: out-of-range loads (zeros), never stored
+      p_store(pf, (kb & 1) ^ 1);   // buffer of block kb - 1, whose reads ended before the last barrier
+      p_load(pf, kb + 3);          // past the last block: out-of-range loads (zeros), never stored
     }
     __syncthreads();
   };
+  f32x4 gA[2][2], gB[2][2];
   for (int kb = 0; kb <= D; kb += 2) {
-    block(kb, pf0);
-    if (kb + 1 <= D) block(kb + 1, pf1);
+    step(kb, pf0, gA, gB);
+    if (kb + 1 <= D) step(kb + 1, pf1, gB, gA);
   }
+  epi(D, gA);   // D is even: the last block's tiles are in gA
 
   // dx[n, c] = acc (c = 32 cb + 16 bt + 4 g + r) + sum over the halves of t1[., n, c]
   const rsrc_t ro = make_rsrc(dx + n0 * D, (uint32_t)(nrow * D * 2));
