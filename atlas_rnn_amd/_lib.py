@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "atlas_mem_bwd_workspace_bytes",
     "atlas_mem_fwd",
     "atlas_mem_bwd",
+    "atlas_mem_step",
     "atlas_scan_fwd",
     "atlas_scan_bwd",
     "atlas_window_sum",
@@ -104,6 +105,8 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_mem_bwd_workspace_bytes.argtypes = [P]
     lib.atlas_mem_fwd.restype = i32
     lib.atlas_mem_fwd.argtypes = [P, ctypes.POINTER(FwdArgs), vp, vp]
+    lib.atlas_mem_step.restype = i32
+    lib.atlas_mem_step.argtypes = [P, ctypes.POINTER(FwdArgs), vp]
     lib.atlas_mem_bwd.restype = i32
     lib.atlas_mem_bwd.argtypes = [P, ctypes.POINTER(BwdArgs), vp, vp, sz, vp]
     lib.atlas_scan_fwd.restype = i32

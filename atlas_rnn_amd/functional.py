@@ -330,6 +330,29 @@ def block_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
     return y[..., :dv], unblock(S_T), unblock(Z_T), unblock(B)
 
 
+def _memory_step(cfg: RecurrenceConfig, args, states):
+    """One token without autograd (atlas_mem_step): the generation step of
+    atlas_pytorch/rnn_transformer.py:863-900 through the cell's recurrence at T = 1."""
+    k, q, v, lr, decay, beta, gate = args
+    S_ref, S0, Z0, buf = states
+    lib = _lib.load()
+    bh, _, dk = k.shape
+    dv = v.shape[-1]
+    dev = k.device
+    momentum = beta is not None
+    e = cfg.window
+    prob = _problem(cfg, bh, 1, dk, dv, momentum, gate, buf is not None, k.dtype)
+    y = torch.empty(bh, 1, dv, device=dev, dtype=k.dtype)
+    S_T = torch.empty(bh, dv, dk, device=dev, dtype=torch.float32)
+    Z_T = torch.empty_like(S_T) if momentum else None
+    buf_out = torch.empty(bh, e - 1, dv, dk, device=dev, dtype=torch.float32) if e > 1 else None
+    a = _lib.FwdArgs(k=_ptr(k), q=_ptr(q), v=_ptr(v), lr=_ptr(lr), decay=_ptr(decay), beta=_ptr(beta),
+                     gate=_ptr(gate), S_ref=_ptr(S_ref), S0=_ptr(S0), Z0=_ptr(Z0), buffer_in=_ptr(buf),
+                     y=_ptr(y), S_T=_ptr(S_T), Z_T=_ptr(Z_T), buffer_out=_ptr(buf_out))
+    _lib.check(lib.atlas_mem_step(ctypes.byref(prob), ctypes.byref(a), _stream(dev)), "atlas_mem_step")
+    return y, S_T, Z_T, buf_out
+
+
 def memory_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
                       beta: Tensor | None = None, gate: Tensor | None = None,
                       S_ref: Tensor | None = None, S0: Tensor | None = None, Z0: Tensor | None = None,
@@ -376,6 +399,8 @@ def memory_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor
     args = [_canon(t, dt) for t in (k, q, v, lr, decay, beta, gate)]
     states = [_canon(t, torch.float32) for t in (S_ref, S0, Z0 if beta is not None else None,
                                                   buffer if e > 1 else None)]
+    if T == 1 and not (torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (*args, *states))):
+        return _memory_step(cfg, args, states)   # decode: one launch, no saved buffer
     # window - 1 longer than the chunk implied by clamp_every: run one call per scan chunk
     # (atlas_pytorch/rnn_memory.py:584-601), carrying S, Z and the buffer, S_ref fixed.
     lib = _lib.load()

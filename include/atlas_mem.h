@@ -137,6 +137,13 @@ size_t atlas_mem_bwd_workspace_bytes(const atlas_mem_problem* prob);
 int atlas_mem_fwd(const atlas_mem_problem* prob, const atlas_mem_fwd_args* args,
                   float* saved, void* stream);
 
+/* One token (seq_len == 1, forward only) without a saved buffer: the decode / streaming step of
+ * RNNMemoryTransformer.generate (atlas_pytorch/rnn_transformer.py:863-900), which runs the cell's
+ * recurrence (atlas_pytorch/rnn_memory.py:605-730) one token at a time. Same problem and argument
+ * structures and the same results as atlas_mem_fwd at T = 1; outputs may alias their inputs
+ * (S_T = S0, Z_T = Z0, buffer_out = buffer_in) for in-place state updates. One launch. */
+int atlas_mem_step(const atlas_mem_problem* prob, const atlas_mem_fwd_args* args, void* stream);
+
 /* Backward pass from the forward's `saved` states. Replaces backward_exact
  * (atlas_pytorch/cuda/atlas_omega.cpp:102-136) plus the PyTorch-side chain in
  * AtlasOmegaFunction.backward (atlas_pytorch/cuda/atlas_omega_autograd.py:156-204). */

@@ -121,6 +121,24 @@ def test_misaligned_pointers_error_before_launch(lib):
     assert lib.atlas_mem_fwd(ctypes.byref(p), ctypes.byref(args), ctypes.c_void_p(bad), None) == 5
 
 
+def test_step_errors_before_launch(lib):
+    # atlas_mem_step: one token only; null, inconsistent and misaligned arguments are rejected
+    # before any HIP call
+    good, bad = 0x10000, 0x10008
+    fields = dict(k=good, q=good, v=good, lr=good, decay=good, beta=good, gate=good, S_ref=good, S0=good,
+                  Z0=good, y=good, S_T=good, Z_T=good, buffer_out=good)
+    args = _lib.FwdArgs(**{k: ctypes.c_void_p(v) for k, v in fields.items()})
+    assert lib.atlas_mem_step(ctypes.byref(_prob(seq_len=4096)), ctypes.byref(args), None) == 2
+    assert lib.atlas_mem_step(ctypes.byref(_prob(seq_len=1)), None, None) == 4
+    assert lib.atlas_mem_step(None, ctypes.byref(args), None) == 4
+    assert lib.atlas_mem_step(ctypes.byref(_prob(seq_len=1)), ctypes.byref(_lib.FwdArgs()), None) == 4
+    assert lib.atlas_mem_step(ctypes.byref(_prob(seq_len=1, momentum=0)), ctypes.byref(args), None) == 9
+    assert lib.atlas_mem_step(ctypes.byref(_prob(seq_len=1, d_k=48)), ctypes.byref(args), None) == 2
+    for name in ("k", "gate", "S0", "buffer_out"):
+        a = _lib.FwdArgs(**{k: ctypes.c_void_p(v) for k, v in dict(fields, **{name: bad}).items()})
+        assert lib.atlas_mem_step(ctypes.byref(_prob(seq_len=1)), ctypes.byref(a), None) == 5, name
+
+
 def test_tensor_map_errors_before_launch(lib):
     good, bad = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x10008)
     f = lib.atlas_tensor_map_fwd
