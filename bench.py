@@ -233,6 +233,65 @@ def run_other_config(name, steps, warmup):
     print(json.dumps(out), flush=True)
 
 
+def run_decode(steps, warmup):
+    """Generation steps at the C3 head shape (B=4 H=8 d=64 e=4 lag gates, momentum, bf16 inputs,
+    fp32 state): atlas_mem_step through the C ABI with the state updated in place, the way a decode
+    loop carries it. One step = one token for every sequence of the batch; `value` counts those
+    (b) tokens per second. The kernel is timed with events on the stream it runs on; its
+    algorithmic bytes are the state read and written once (S_ref, S0, Z0, buffer in; S_T, Z_T,
+    buffer out) plus the token's vectors."""
+    import ctypes
+    import torch
+    from atlas_rnn_amd import _lib
+    from atlas_rnn_amd.functional import RecurrenceConfig, _problem, _ptr, _stream
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, H, d, e = 4, 8, 64, 4
+    bh = B * H
+    g = torch.Generator().manual_seed(1006)
+    r = lambda *sh: torch.randn(*sh, generator=g)
+    bf = lambda x: x.to(device=dev, dtype=torch.bfloat16).contiguous()
+    k = r(bh, 1, d)
+    x = dict(k=bf(k / k.norm(dim=-1, keepdim=True)), q=bf(r(bh, 1, d)), v=bf(r(bh, 1, d)),
+             lr=bf(0.1 * torch.sigmoid(r(bh, 1))), decay=bf(torch.sigmoid(r(bh, 1) * 0.5 + 2.0)),
+             beta=bf(torch.sigmoid(r(bh, 1) * 0.5 + 1.0)), gate=bf(torch.softmax(r(bh, 1, e), dim=-1)))
+    S_ref = (0.1 * r(bh, d, d)).to(dev)
+    S, Z, Bf = S_ref.clone(), (0.1 * r(bh, d, d)).to(dev), (0.1 * r(bh, e - 1, d, d)).to(dev)
+    y = torch.empty(bh, 1, d, device=dev, dtype=torch.bfloat16)
+    lib = _lib.load()
+    prob = _problem(RecurrenceConfig(window=e), bh, 1, d, d, True, x["gate"], True, torch.bfloat16)
+    a = _lib.FwdArgs(k=_ptr(x["k"]), q=_ptr(x["q"]), v=_ptr(x["v"]), lr=_ptr(x["lr"]), decay=_ptr(x["decay"]),
+                     beta=_ptr(x["beta"]), gate=_ptr(x["gate"]), S_ref=_ptr(S_ref), S0=_ptr(S), Z0=_ptr(Z),
+                     buffer_in=_ptr(Bf), y=_ptr(y), S_T=_ptr(S), Z_T=_ptr(Z), buffer_out=_ptr(Bf))
+    stream = _stream(dev)
+
+    def step():
+        _lib.check(lib.atlas_mem_step(ctypes.byref(prob), ctypes.byref(a), stream), "atlas_mem_step")
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    us = 1e3 * ev0.elapsed_time(ev1) / steps
+    state_bytes = bh * d * d * 4 * (3 + 2 + 2 * (e - 1))   # S_ref, S0, S_T; Z0, Z_T; buffer in / out
+    vec_bytes = bh * (3 * d + 3 + e) * 2 + bh * d * 2       # k, q, v, scalars, gates; y
+    alg = state_bytes + vec_bytes
+    out = {"metric": "decode tokens/s (one memory-layer step per token)", "value": round(B / (us * 1e-6), 1),
+           "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(us / 1e3, 6),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic (seeded)",
+           "config": {"workload": "decode step at the C3 head shape: B=4 H=8 d=64 e=4 lag gates, momentum, "
+                                  "state in place", "global_batch": B, "seq_len": 1, "parallelism": "single GPU"},
+           "roofline": {"bound": "hbm", "achieved": round(alg / (us * 1e-6) / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
+                        "frac": round(alg / (us * 1e-6) / 8e12, 4), "traffic": None}}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -242,8 +301,9 @@ def main():
     ap.add_argument("--cpu-sample-tokens", type=int, default=256)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (HBM counter calibration)")
-    ap.add_argument("--config", choices=["c3"] + sorted(OTHER_CONFIGS), default="c3",
-                    help="c3 (default): the headline; c2 / c4 / c5: the other BASELINE configs")
+    ap.add_argument("--config", choices=["c3"] + sorted(OTHER_CONFIGS) + ["decode"], default="c3",
+                    help="c3 (default): the headline; c2 / c4 / c5: the other BASELINE configs; decode: the "
+                         "one-token step")
     args = ap.parse_args()
     if args.calibrate_copy:
         calibrate_copy()
@@ -252,7 +312,10 @@ def main():
         if args.gpus != 1:
             print("bench.py measures one GPU (use --gpus 1).", file=sys.stderr)
             sys.exit(2)
-        run_other_config(args.config, args.steps, args.warmup)
+        if args.config == "decode":
+            run_decode(args.steps, args.warmup)
+        else:
+            run_other_config(args.config, args.steps, args.warmup)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the memory-layer recurrence shards over (batch, head) rows "
