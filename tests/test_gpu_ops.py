@@ -293,3 +293,37 @@ def test_cell_parity(name, spec, T, kernel_dt):
     names = ["x"] + [n for n, _ in gcell.named_parameters()]
     for n, a, b in zip(names, grads, grads_r):
         compare(f"{name}.d{n}", a.float().cpu(), b, tol)
+
+
+@pytest.mark.parametrize("name,spec", [CELLS[0][:2], CELLS[2][:2]], ids=[CELLS[0][0], CELLS[2][0]])
+def test_cell_decode_steps(name, spec):
+    """Generation: the cell called one token at a time without autograd (the decode step kernel)
+    carries its state like the reference cell called the same way."""
+    _say(f"cell decode {name}: {spec}")
+    torch.manual_seed(33)
+    cell = _make_cell(spec)
+    with torch.no_grad():
+        for p in cell.parameters():
+            if p.ndim == 2 and p.shape[0] == cell.heads:
+                p.normal_(0, 0.2)
+    batch, steps = 2, 6
+    g = torch.Generator().manual_seed(34)
+    x = torch.randn(batch, steps, cell.dim, generator=g)
+    ref_cell = copy.deepcopy(cell).double()
+    gcell = copy.deepcopy(cell).cuda()
+    st_r = ref_cell.init_state(batch)
+    st_r = am.RNNMemState(st_r.seq_index, *[t.to(F64) if t is not None else None for t in st_r[1:]])
+    st_d = gcell.init_state(batch)
+    st_d = am.RNNMemState(st_d.seq_index, *[t.cuda() if t is not None else None for t in st_d[1:]])
+    with torch.no_grad():
+        for t in range(steps):
+            out_r, (S_r, Z_r, B_r) = _reference_cell_forward(ref_cell, x[:, t:t + 1].to(F64), st_r)
+            st_r = am.RNNMemState(st_r.seq_index + 1, S_r, Z_r, B_r)
+            out, st_d = gcell(x[:, t:t + 1].cuda(), st_d)
+            compare(f"{name}.out[{t}]", out.float().cpu(), out_r, 1e-4)
+    torch.cuda.synchronize()
+    compare(f"{name}.S", st_d.S.float().cpu(), st_r.S, 1e-4)
+    if st_r.Z is not None:
+        compare(f"{name}.Z", st_d.Z.float().cpu(), st_r.Z, 1e-4)
+    if st_r.omega_buffer is not None:
+        compare(f"{name}.buffer", st_d.omega_buffer.float().cpu(), st_r.omega_buffer, 1e-4)
