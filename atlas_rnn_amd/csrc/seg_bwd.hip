@@ -15,6 +15,8 @@
 //   k_bwd_seg_fixup : merges the partial (dv, dphi) of tokens whose window crosses a segment boundary,
 //                   adds the d buffer_out terms, reduces token-gate gradients and (without d buffer_out)
 //                   the dS_ref partials; with d buffer_out k_seg_reduce_dsref reduces them afterwards.
+#include <type_traits>
+
 #include "mem_common.h"
 #include "mem_params.h"
 #include "seg_common.h"
@@ -30,16 +32,35 @@ hipError_t launch_bwd_scalar(const Geom& g, const BwdPtrs<T>& a, const BwdSegPtr
 // ---------------------------------------------------------------------------------------------
 template <typename T, int CH, int D>
 struct BwdAggSmem {
+  // The aggregates over the forward's 64-token chunks (the specialised path) stage dy pre-scaled
+  // by both coefficients, once per chunk, instead of scaling every fragment as it is used (four
+  // waves share each dy fragment); the general path's chunk lengths keep the per-fragment scaling.
+  static constexpr bool kPre = CH == 64;
+  struct PreDy {
+    alignas(16) T a[CH][D + 8];   // a_{t-1} dy_t, rounded to T
+    alignas(16) T k[CH][D + 8];   // kappa_{t-1} dy_t, rounded to T
+  };
+  struct NoDy {};
   alignas(16) T psi[CH][D + 8];
-  alignas(16) T dy[CH][D + 8];
-  alignas(16) float coef[2 * CH + 4];   // a_{t-1}, kappa_{t-1}, (a, kappa, b) of the chunk
+  alignas(16) T dy[CH][D + 8];                 // unscaled (per-fragment scaling)
+  alignas(16) float coef[2 * CH + 4];          // a_{t-1}, kappa_{t-1}, (a, kappa, b) of the chunk
+  typename std::conditional<kPre, PreDy, NoDy>::type pre;
 };
 
 // Register prefetch of one chunk for the adjoint aggregates: psi (vectors 0 .. NV-1) or dy
-// (vectors NV .. 2 NV-1) rows, 8 features per vector, NVT vectors per thread, and the head of the
-// coefficient record.
+// (vectors NV .. 2 NV-1) rows, 8 features per vector, NVT vectors per thread, the coefficients
+// a_{t-1}, kappa_{t-1} of each dy vector's token, and the head of the coefficient record. The dy
+// rows are stored scaled by both coefficients (once per chunk, instead of once per fragment use).
+template <int N>
+struct AggPreW {   // coefficients of the dy vectors (pre-scaled staging only)
+  float a[N], k[N];
+};
+struct AggNoW {};
+
 template <typename T, int CH, int D>
-struct BwdAggPrefetch {
+struct BwdAggPrefetch
+    : std::conditional<BwdAggSmem<T, CH, D>::kPre, AggPreW<(2 * (CH * D / 8) + kSegThreads - 1) / kSegThreads>,
+                       AggNoW>::type {
   static constexpr int NV = CH * D / 8;
   static constexpr int NVT = (2 * NV + kSegThreads - 1) / kSegThreads;
   static constexpr int NC4 = (2 * CH + 4) / 4;
@@ -58,6 +79,11 @@ struct BwdAggPrefetch {
       const T* src = (vi < NV || !a.dy) ? a.q : a.dy;
       ok[u] = vi < 2 * NV && t < L && (vi < NV || a.dy);
       x[u] = vec8_load(src + (tb + t0 + (ok[u] ? t : 0)) * D + c8 * 8);
+      if constexpr (BwdAggSmem<T, CH, D>::kPre) {
+        const int tc = t < CH ? t : 0;
+        this->a[u] = rec[tc];
+        this->k[u] = rec[CH + tc];
+      }
     }
     rc = reinterpret_cast<const float4*>(rec)[tid < NC4 ? tid : 0];
   }
@@ -74,7 +100,12 @@ struct BwdAggPrefetch {
           if (g.map_mode == MAP_ELEMENTWISE) y = y.mapped(g.map_deg);
           y.store(&sm.psi[t][c8 * 8]);
         } else {
-          y.store(&sm.dy[t][c8 * 8]);
+          if constexpr (Sm::kPre) {
+            y.store_scaled(&sm.pre.a[t][c8 * 8], this->a[u]);
+            y.store_scaled(&sm.pre.k[t][c8 * 8], this->k[u]);
+          } else {
+            y.store(&sm.dy[t][c8 * 8]);
+          }
         }
       }
     }
@@ -124,10 +155,15 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg_agg(const Geom g, const
 #pragma unroll
       for (int k0 = 0; k0 < CH; k0 += M::KS) {
         const typename M::frag fb = frag_ld_tr<T>(&sm.psi[0][0], D + 8, n0, k0);
-        const typename M::frag fd = frag_ld_tr<T>(&sm.dy[0][0], D + 8, m0, k0);
-        const int kb = k0 + (lane >> 4) * M::KL;
-        aa = M::mma(frag_scale<T>(fd, &sm.coef[kb]), fb, aa);
-        ak = M::mma(frag_scale<T>(fd, &sm.coef[CH + kb]), fb, ak);
+        if constexpr (Sm::kPre) {
+          aa = M::mma(frag_ld_tr<T>(&sm.pre.a[0][0], D + 8, m0, k0), fb, aa);
+          ak = M::mma(frag_ld_tr<T>(&sm.pre.k[0][0], D + 8, m0, k0), fb, ak);
+        } else {
+          const typename M::frag fd = frag_ld_tr<T>(&sm.dy[0][0], D + 8, m0, k0);
+          const int kb = k0 + (lane >> 4) * M::KL;
+          aa = M::mma(frag_scale<T>(fd, &sm.coef[kb]), fb, aa);
+          ak = M::mma(frag_scale<T>(fd, &sm.coef[CH + kb]), fb, ak);
+        }
       }
       if (valid) {
 #pragma unroll

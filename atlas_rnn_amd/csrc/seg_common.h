@@ -76,6 +76,23 @@ struct Vec8 {
     for (int e = 0; e < 8; ++e) r.v[e] = static_cast<T>(poly_map(to_f32(v[e]), deg));
     return r;
   }
+  // every element times w, rounded to T, stored to 16-byte aligned p (built as words, so no
+  // aggregate temporary goes through scratch)
+  __device__ __forceinline__ void store_scaled(T* p, float w) const {
+    if constexpr (sizeof(T) == 2) {
+      unsigned wd[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const unsigned lo = __builtin_bit_cast(unsigned short, static_cast<T>(to_f32(v[2 * h]) * w));
+        const unsigned hi = __builtin_bit_cast(unsigned short, static_cast<T>(to_f32(v[2 * h + 1]) * w));
+        wd[h] = lo | (hi << 16);
+      }
+      *reinterpret_cast<uint4*>(p) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+    } else {
+      reinterpret_cast<float4*>(p)[0] = make_float4(to_f32(v[0]) * w, to_f32(v[1]) * w, to_f32(v[2]) * w, to_f32(v[3]) * w);
+      reinterpret_cast<float4*>(p)[1] = make_float4(to_f32(v[4]) * w, to_f32(v[5]) * w, to_f32(v[6]) * w, to_f32(v[7]) * w);
+    }
+  }
   // this vector if ok, zeros otherwise (word-wise selects, no aggregate temporaries)
   __device__ __forceinline__ Vec8 masked(bool ok) const {
     Vec8 r;
