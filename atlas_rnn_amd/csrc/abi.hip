@@ -163,6 +163,7 @@ SegGeom make_seg(const Geom& g) {
 }
 
 int chunk_cap(int dtype) { return dtype == ATLAS_DT_BF16 ? 64 : 32; }
+constexpr int kMinClampChunk = 8;   // shortest backward chunk accepted under clamp_every
 int bwd_chunk_cap(int dtype) { return dtype == ATLAS_DT_BF16 ? 32 : 16; }
 int largest_divisor_at_most(int n, int cap) {
   for (int d = cap; d >= 1; --d)
@@ -194,6 +195,10 @@ Plan make_plan(const atlas_mem_problem* p) {
   if (Lc / Lb > 2) Lc = Lb;
   const int H = p->window - 1;
   if (Lb < H) { pl.status = ATLAS_MEM_ERR_UNSUPPORTED; return pl; }
+  // clamp_every with no divisor of at least kMinClampChunk in range (37, 74, ...) would walk the
+  // row in chunks of a few tokens with a state saved after each: the caller splits such calls at
+  // clamp_every instead (one unclamped call per scan chunk, state carried)
+  if (p->clamp_every > 0 && Lb < kMinClampChunk) { pl.status = ATLAS_MEM_ERR_UNSUPPORTED; return pl; }
   Geom& g = pl.g;
   g.BH = p->bh; g.T = p->seq_len; g.DK = p->d_k; g.DV = p->d_v;
   g.e = p->window; g.H = H; g.Lc = Lc; g.nc = (p->seq_len + Lc - 1) / Lc;
@@ -374,7 +379,7 @@ const char* atlas_mem_strerror(int status) {
     case ATLAS_MEM_ERR_DTYPE: return "unknown dtype code (ATLAS_DT_F32 or ATLAS_DT_BF16)";
     case ATLAS_MEM_ERR_NULL: return "a required pointer is NULL";
     case ATLAS_MEM_ERR_ALIGN: return "a pointer is not aligned to its element size";
-    case ATLAS_MEM_ERR_UNSUPPORTED: return "window - 1 exceeds the chunk length implied by clamp_every; split the call at clamp_every";
+    case ATLAS_MEM_ERR_UNSUPPORTED: return "the chunk length implied by clamp_every is below 8 tokens or shorter than window - 1; split the call at clamp_every";
     case ATLAS_MEM_ERR_WORKSPACE: return "workspace smaller than atlas_mem_bwd_workspace_bytes()";
     case ATLAS_MEM_ERR_LAUNCH: return "a HIP kernel launch or runtime call failed";
     case ATLAS_MEM_ERR_ARG: return "inconsistent flags (momentum/gate/map/buffer/clamp)";

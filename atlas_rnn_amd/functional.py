@@ -46,6 +46,51 @@ def _require_gpu(*ts: Tensor | None) -> torch.device:
     return dev
 
 
+def check_operands(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buffer, *, window: int,
+                   dtype: torch.dtype | None = None, contiguous: bool = False) -> None:
+    """Raises ValueError unless the recurrence operands have consistent shapes, one device and
+    (when given) the input dtype, before any pointer reaches the C ABI:
+    k, q [BH, T, d_k]; v [BH, T, d_v]; lr, decay, beta [BH, T]; gate [BH, T] (per token) or
+    [BH, T, window] (per lag); S_ref, S0, Z0 [BH, d_v, d_k]; buffer [BH, window - 1, d_v, d_k]
+    (fp32 states). contiguous=True also requires row-major storage (the raw-pointer calls)."""
+    if k.dim() != 3:
+        raise ValueError(f"k must be [BH, T, d_k], got shape {tuple(k.shape)}")
+    bh, T, dk = k.shape
+    if v.dim() != 3 or v.shape[:2] != (bh, T):
+        raise ValueError(f"v must be [BH={bh}, T={T}, d_v], got {tuple(v.shape)}")
+    dv = v.shape[2]
+    if tuple(q.shape) != (bh, T, dk):
+        raise ValueError(f"q must have k's shape {(bh, T, dk)}, got {tuple(q.shape)}")
+    if not 1 <= window:
+        raise ValueError(f"window must be >= 1, got {window}")
+    expect = {"lr": (lr, (bh, T)), "decay": (decay, (bh, T)), "beta": (beta, (bh, T)),
+              "S_ref": (S_ref, (bh, dv, dk)), "S0": (S0, (bh, dv, dk)), "Z0": (Z0, (bh, dv, dk)),
+              "buffer": (buffer if window > 1 else None, (bh, window - 1, dv, dk))}
+    if gate is not None:
+        if gate.dim() == 2:
+            expect["gate"] = (gate, (bh, T))
+        elif gate.dim() == 3:
+            expect["gate"] = (gate, (bh, T, window))
+        else:
+            raise ValueError(f"gate must be [BH, T] (per token) or [BH, T, window] (per lag), got {tuple(gate.shape)}")
+    for name, (t, shape) in expect.items():
+        if t is not None and tuple(t.shape) != shape:
+            raise ValueError(f"{name} must have shape {shape}, got {tuple(t.shape)}")
+    dev = k.device
+    named = dict(k=k, q=q, v=v, lr=lr, decay=decay, beta=beta, gate=gate, S_ref=S_ref, S0=S0, Z0=Z0, buffer=buffer)
+    for name, t in named.items():
+        if t is None:
+            continue
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, k on {dev}")
+        if contiguous and not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+        if dtype is not None:
+            want = dtype if name in ("k", "q", "v", "lr", "decay", "beta", "gate") else torch.float32
+            if t.dtype != want:
+                raise ValueError(f"{name} must be {want}, got {t.dtype}")
+
+
 @dataclass(frozen=True)
 class RecurrenceConfig:
     window: int = 1
@@ -88,6 +133,8 @@ class MemoryRecurrenceFn(torch.autograd.Function):
         # dZ_T or buffer_out gradient as zero without reading one)
         ctx.set_materialize_grads(False)
         lib = _lib.load()
+        check_operands(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buf, window=cfg.window, dtype=k.dtype,
+                       contiguous=True)
         bh, T, dk = k.shape
         dv = v.shape[-1]
         momentum = beta is not None
@@ -123,7 +170,7 @@ class MemoryRecurrenceFn(torch.autograd.Function):
         bh, T, dk = k.shape
         dv_ = v.shape[-1]
         f32 = torch.float32
-        dy = _aligned(dy)
+        dy = _aligned(dy.to(k.dtype)) if dy is not None else None
         dS_T = _aligned(dS_T.float()) if dS_T is not None else None
         dZ_T = _aligned(dZ_T.float()) if (dZ_T is not None and ctx.momentum and dZ_T.numel() > 0) else None
         dbuf_out = _aligned(dbuf_out.float()) if (dbuf_out is not None and dbuf_out.numel() > 0) else None
@@ -371,12 +418,15 @@ def memory_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor
     """
     dev = _require_gpu(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buffer)
     dt = k.dtype if k.dtype in _DTYPES else torch.float32
+    if k.dim() != 3 or v.dim() != 3:
+        raise ValueError(f"k and v must be [BH, T, d], got {tuple(k.shape)} and {tuple(v.shape)}")
     bh, T, dk = k.shape
     dv = v.shape[-1]
     if S0 is None:
         S0 = torch.zeros(bh, dv, dk, device=dev, dtype=torch.float32)
     if S_ref is None:
         S_ref = S0
+    check_operands(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buffer, window=window)
     if dk != dv or dk > max(_KERNEL_DIMS):
         return block_recurrence(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buffer, window=window,
                                 map_mode=map_mode, map_degree=map_degree, clamp_every=clamp_every,
@@ -394,6 +444,8 @@ def memory_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor
         return (y[..., :dk], S_T[..., :dk, :dk], None if Z_T is None else Z_T[..., :dk, :dk],
                 None if B is None else B[..., :dk, :dk])
     e = window
+    if clamp_every is not None and clamp_every >= T:
+        clamp_every = None        # no clamp point before the last token (the final clamp is clamp_final's)
     cfg = RecurrenceConfig(window=e, map_mode=map_mode, map_degree=map_degree,
                            clamp_every=clamp_every, clamp_final=clamp_final)
     args = [_canon(t, dt) for t in (k, q, v, lr, decay, beta, gate)]
@@ -401,8 +453,9 @@ def memory_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor
                                                   buffer if e > 1 else None)]
     if T == 1 and not (torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (*args, *states))):
         return _memory_step(cfg, args, states)   # decode: one launch, no saved buffer
-    # window - 1 longer than the chunk implied by clamp_every: run one call per scan chunk
-    # (atlas_pytorch/rnn_memory.py:584-601), carrying S, Z and the buffer, S_ref fixed.
+    # window - 1 longer than the chunk implied by clamp_every, or clamp_every without a divisor
+    # usable as a chunk: run one call per scan chunk (atlas_pytorch/rnn_memory.py:584-601),
+    # carrying S, Z and the buffer, S_ref fixed.
     lib = _lib.load()
     prob = _problem(cfg, bh, T, dk, dv, beta is not None, gate, states[3] is not None, dt)
     status = lib.atlas_mem_validate(ctypes.byref(prob))
@@ -639,7 +692,25 @@ class RecurrencePlan:
         self.grads = None
         self._inputs = None
 
+    def _check(self, k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buffer):
+        check_operands(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buffer, window=self.window,
+                       dtype=self.dtype, contiguous=True)
+        if tuple(k.shape) != self.shape or tuple(v.shape) != self.shape:
+            raise ValueError(f"the plan is for k, v of shape {self.shape}, got {tuple(k.shape)}, {tuple(v.shape)}")
+        if k.device != self.device and not (self.device.index is None and k.device.type == self.device.type):
+            raise ValueError(f"the plan runs on {self.device}, inputs are on {k.device}")
+        if (beta is not None) != self.momentum:
+            raise ValueError("beta must be given iff the plan has momentum")
+        gmode = _lib.GATE_NONE if gate is None else (_lib.GATE_TOKEN if gate.dim() == 2 else _lib.GATE_LAG)
+        if gmode != self.prob.gate_mode:
+            raise ValueError(f"gate layout {None if gate is None else tuple(gate.shape)} does not match the plan's gate mode")
+        if (buffer is not None) != bool(self.prob.has_buffer):
+            raise ValueError("buffer must be given iff the plan was made with has_buffer=True")
+        if S_ref is None or S0 is None:
+            raise ValueError("S_ref and S0 are required")
+
     def forward(self, k, q, v, lr, decay, beta=None, gate=None, S_ref=None, S0=None, Z0=None, buffer=None):
+        self._check(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buffer)
         self._inputs = (k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buffer)
         a = _lib.FwdArgs(k=_ptr(k), q=_ptr(q), v=_ptr(v), lr=_ptr(lr), decay=_ptr(decay), beta=_ptr(beta),
                          gate=_ptr(gate), S_ref=_ptr(S_ref), S0=_ptr(S0), Z0=_ptr(Z0), buffer_in=_ptr(buffer),
@@ -652,6 +723,22 @@ class RecurrencePlan:
         if self._inputs is None:
             raise RuntimeError("RecurrencePlan.backward before forward")
         k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buf = self._inputs
+        bh, T, d = self.shape
+        state = (bh, d, d)
+        for name, t, shape, dt in (("dy", dy, self.shape, self.dtype), ("dS_T", dS_T, state, torch.float32),
+                                   ("dZ_T", dZ_T, state, torch.float32),
+                                   ("dbuffer_out", dbuffer_out, (bh, self.window - 1, d, d), torch.float32)):
+            if t is None:
+                if name == "dy":
+                    raise ValueError("dy is required")
+                continue
+            if tuple(t.shape) != shape or t.dtype != dt or not t.is_contiguous() or t.device != k.device:
+                raise ValueError(f"{name} must be a contiguous {dt} tensor of shape {shape} on {k.device}, "
+                                 f"got {t.dtype} {tuple(t.shape)} on {t.device}")
+        if dZ_T is not None and not self.momentum:
+            raise ValueError("dZ_T given to a plan without momentum")
+        if dbuffer_out is not None and self.window < 2:
+            raise ValueError("dbuffer_out given to a plan with window 1")
         if self.grads is None:
             f32 = torch.float32
             bh, T, d = self.shape

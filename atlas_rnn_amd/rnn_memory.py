@@ -301,7 +301,9 @@ class OmegaRNNMemoryCell(_CellBase):
 
     def _forward_cuda(self, x: Tensor, state: RNNMemState | None) -> tuple[Tensor, RNNMemState]:
         """rnn_memory.py:732-814, inside the scan_chunk_len loop of rnn_memory.py:584-601: every
-        chunk is one call with S_ref = the call-start state and an empty window."""
+        chunk is one call with S_ref = the call-start state and an empty window. The chunk's Z_T
+        becomes the next chunk's Z0 only with momentum: without it the reference's next state has
+        Z = None (rnn_memory.py:810), so every chunk starts from Z0 = 0 (:781) with beta = 1."""
         batch, seq_len, _ = x.shape
         if not exists(state):
             state = self.init_state(batch, x.device, x.dtype)
@@ -319,7 +321,8 @@ class OmegaRNNMemoryCell(_CellBase):
         bf = torch.bfloat16
         S_ref = state.S.to(bf).float()
         S = state.S if exists(state.S) else k.new_zeros((BH, d, d))
-        Z = state.Z if exists(state.Z) else k.new_zeros((BH, d, d))
+        zeros = k.new_zeros((BH, d, d))
+        Z = state.Z if (self.use_momentum and exists(state.Z)) else zeros
         chunk = self.scan_chunk_len if (exists(self.scan_chunk_len) and seq_len > self.scan_chunk_len) else seq_len
         ys = []
         for start in range(0, seq_len, chunk):
@@ -329,7 +332,7 @@ class OmegaRNNMemoryCell(_CellBase):
                 beta[:, sl].to(bf), gate[:, sl].to(bf), S.to(bf).float(), Z.to(bf).float())
             ys.append(y.to(x.dtype))
             S = S_T.to(x.dtype)
-            Z = Z_T.to(x.dtype)
+            Z = Z_T.to(x.dtype) if self.use_momentum else zeros
         y = torch.cat(ys, dim=1) if len(ys) > 1 else ys[0]
         y = rearrange(y, '(b h) t d -> b h t d', b=batch, h=self.heads)
         out = self.to_out(self.merge_heads(y))

@@ -38,6 +38,7 @@ class Case:
     backward: bool = True
     dv: int | None = None            # d_v (None: d_v = d_k)
     grad_buffer: bool = True         # the loss includes buffer_out (False: no buffer_out gradient)
+    buffer_scale: float = 0.1        # carried buffer ~ buffer_scale * N(0, 1) (0: a zero buffer, as the cells pass)
     extra: dict = field(default_factory=dict)
 
 
@@ -62,7 +63,7 @@ def make_inputs(c: Case) -> dict:
     p["S_ref"] = s * r(BH, dv, d) if s else z()
     p["S0"] = s * r(BH, dv, d) if s else z()
     p["Z0"] = (s * r(BH, dv, d) if s else z()) if c.momentum else None
-    p["buffer"] = (0.1 * r(BH, e - 1, dv, d)) if (c.buffer and e > 1) else None
+    p["buffer"] = (c.buffer_scale * r(BH, e - 1, dv, d)) if (c.buffer and e > 1) else None
     # upstream gradients
     p["gy"] = r(BH, T, dv)
     p["gS"] = r(BH, dv, d)
@@ -136,16 +137,67 @@ def run_gpu(c: Case, p: dict, device="cuda"):
             {kk: v.float().cpu() for kk, v in grads.items()})
 
 
+def run_oracle_rows(c: Case, p: dict, rows, block: int = 256):
+    """fp64 oracle outputs and gradients for the head-batch rows `rows` only (rows are independent,
+    so these equal the same rows of the full problem's). The sequence runs in blocks of `block`
+    tokens carrying (S, Z, buffer), unclamped until the last block: the same recurrence as one call
+    (the oracle's chunk invariance), with a fraction of the memory at long T. No clamp_every."""
+    assert c.clamp_every is None
+    idx = torch.tensor(list(rows))
+    sub = {kk: (v[idx] if v is not None else None) for kk, v in p.items()}
+    x = {kk: (sub[kk].to(F64).clone().requires_grad_(c.backward) if sub[kk] is not None else None)
+         for kk in TENSOR_INPUTS}
+    mode = 'elementwise' if c.map_degree > 1 else 'off'
+    phi_k = poly_feature_map(x["k"], c.map_degree, mode)
+    phi_q = poly_feature_map(x["q"], c.map_degree, mode)
+    ys, S, Z, B = [], x["S0"], x["Z0"], x["buffer"]
+    for s0 in range(0, c.T, block):
+        sl = slice(s0, min(c.T, s0 + block))
+        sl_or_none = lambda t: t[:, sl] if t is not None else None
+        y, S, Z, B = memory_recurrence_vectorised(
+            phi_k[:, sl], phi_q[:, sl], x["v"][:, sl], x["lr"][:, sl], x["decay"][:, sl], sl_or_none(x["beta"]),
+            sl_or_none(x["gate"]), x["S_ref"], S, Z, B, window=c.e,
+            clamp_final=c.clamp_final and s0 + block >= c.T)
+        ys.append(y)
+    out = [torch.cat(ys, dim=1), S, Z, B]
+    grads = {}
+    if c.backward:
+        q64 = {kk: (v.to(F64) if v is not None else None) for kk, v in sub.items() if kk.startswith("g")}
+        loss = _loss(out, q64)
+        leaves = [kk for kk in TENSOR_INPUTS if x[kk] is not None]
+        gs = torch.autograd.grad(loss, [x[kk] for kk in leaves], allow_unused=True)
+        grads = {kk: (gg if gg is not None else torch.zeros_like(x[kk])) for kk, gg in zip(leaves, gs)}
+    return [o.detach() if o is not None else None for o in out], grads
+
+
 def tol_for(c: Case) -> float:
     return 1e-4 if c.dtype == torch.float32 else 2e-2
 
 
-def compare(name: str, got: torch.Tensor, ref: torch.Tensor, tol: float):
-    """Elementwise |got - ref| <= tol * |ref| + tol * max|ref| (rtol with an atol floor scaled
-    by the tensor's largest magnitude)."""
+# (name, normwise relative error, tol) of every compare() call in this process: the margin report
+NORMWISE: list[tuple[str, float, float]] = []
+
+
+def normwise_error(got: torch.Tensor, ref: torch.Tensor) -> float:
+    """||got - ref||_F / ||ref||_F in fp64 (0 when both are zero)."""
+    ref = ref.to(torch.float64)
+    got = got.to(torch.float64)
+    den = ref.norm().item()
+    num = (got - ref).norm().item()
+    return num / den if den > 0 else (0.0 if num == 0 else float("inf"))
+
+
+def compare(name: str, got: torch.Tensor, ref: torch.Tensor, tol: float, normwise: bool = True):
+    """Two checks: the normwise relative error ||got - ref|| / ||ref|| <= tol (normwise=True), and
+    elementwise |got - ref| <= tol * |ref| + tol * max|ref| (rtol with an atol floor scaled by the
+    tensor's largest magnitude). The normwise error is recorded in NORMWISE."""
     ref = ref.to(torch.float64)
     got = got.to(torch.float64)
     assert got.shape == ref.shape, f"{name}: shape {tuple(got.shape)} vs {tuple(ref.shape)}"
+    nw = normwise_error(got, ref)
+    NORMWISE.append((name, nw, tol))
+    if normwise:
+        assert nw <= tol, f"{name}: normwise relative error {nw:.3e} > {tol}"
     scale = ref.abs().max().item()
     atol = tol * max(scale, 1e-30)
     err = (got - ref).abs()

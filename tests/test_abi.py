@@ -70,6 +70,24 @@ def test_window_longer_than_clamp_chunk_is_unsupported(lib):
     assert lib.atlas_mem_validate(ctypes.byref(_prob(window=8, clamp_every=4))) == _lib.ERR_UNSUPPORTED
 
 
+@pytest.mark.parametrize("every", [37, 41, 47, 53, 59, 61, 74])
+def test_clamp_every_without_a_usable_chunk_is_split_by_the_caller(lib, every):
+    # no divisor >= 8 usable as a chunk: the library refuses (the host splits the call at
+    # clamp_every) instead of walking 1-token chunks with a state saved after each token
+    p = _prob(clamp_every=every)
+    assert lib.atlas_mem_validate(ctypes.byref(p)) == _lib.ERR_UNSUPPORTED
+    assert lib.atlas_mem_saved_bytes(ctypes.byref(p)) == 0
+
+
+@pytest.mark.parametrize("every", [32, 48, 64, 96, 100, 128])
+def test_clamp_every_saved_bytes_stay_bounded(lib, every):
+    # usable clamp chunks keep the saved states at backward-chunk granularity (<= 1 per 8 tokens)
+    st = 64 * 64 * 4
+    p = _prob(clamp_every=every)
+    assert lib.atlas_mem_validate(ctypes.byref(p)) == 0
+    assert lib.atlas_mem_saved_bytes(ctypes.byref(p)) <= 32 * (4096 // 8) * 2 * st + 64 * 2 ** 20
+
+
 def test_sizes(lib):
     p = _prob()
     st = 64 * 64 * 4

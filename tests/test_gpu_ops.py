@@ -196,15 +196,21 @@ def _reference_cell_forward(cell, x, state):
         gate = gate if gate is not None else torch.ones_like(lr)
         ops = [_ste_bf16(t) for t in (phi_k, phi_q, v, lr, decay, beta, gate)]
         S_ref = _ste_bf16(state.S)
-        S, Z = state.S, state.Z
+        # the next chunk starts from the returned Z only with momentum; otherwise the reference's
+        # state carries Z = None and each chunk starts from zeros (rnn_memory.py:781, :810)
+        zeros = torch.zeros_like(state.S)
+        S = state.S
+        Z = state.Z if (cell.use_momentum and state.Z is not None) else zeros
         ys = []
         step = chunk or T
         for s0 in range(0, T, step):
             sl = slice(s0, min(T, s0 + step))
-            y, S, Z, _ = memory_recurrence_vectorised(*[o[:, sl] for o in ops], S_ref, _ste_bf16(S), _ste_bf16(Z),
-                                                      None, window=16, clamp_final=False)
+            y, S, Z_T, _ = memory_recurrence_vectorised(*[o[:, sl] for o in ops], S_ref, _ste_bf16(S),
+                                                        _ste_bf16(Z), None, window=16, clamp_final=False)
+            Z = Z_T if cell.use_momentum else zeros
             ys.append(y)
         y = torch.cat(ys, dim=1)
+        Z = Z if cell.use_momentum else None
         buf = None
     else:
         Z0 = state.Z if cell.use_momentum else None
@@ -228,6 +234,9 @@ CELLS = [
                                      qkv_conv_kernel=None), 40, None),
     ("omega_cuda_w16_chunk32", dict(kind="omega", dim=64, dim_head=64, heads=1, omega_window=16, use_cuda=True,
                                     scan_chunk_len=32), 80, BF16),
+    # without momentum every scan chunk of the window-16 path starts from Z = 0
+    ("omega_cuda_w16_nomom_chunk32", dict(kind="omega", dim=64, dim_head=64, heads=1, omega_window=16,
+                                          use_cuda=True, use_momentum=False, scan_chunk_len=32), 80, BF16),
 ]
 
 
