@@ -16,6 +16,7 @@ ABI_VERSION = 1
 
 OK = 0
 ERR_UNSUPPORTED = 6
+ERR_SCRATCH = 10
 
 DT_F32 = 0
 DT_BF16 = 1
@@ -36,6 +37,8 @@ EXPORTED_SYMBOLS = (
     "atlas_mem_bwd_workspace_bytes",
     "atlas_mem_fwd",
     "atlas_mem_bwd",
+    "atlas_mem_bwd_noalloc",
+    "atlas_mem_noalloc_scratch_bytes",
     "atlas_mem_step",
     "atlas_scan_fwd",
     "atlas_scan_bwd",
@@ -109,6 +112,10 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_mem_step.argtypes = [P, ctypes.POINTER(FwdArgs), vp]
     lib.atlas_mem_bwd.restype = i32
     lib.atlas_mem_bwd.argtypes = [P, ctypes.POINTER(BwdArgs), vp, vp, sz, vp]
+    lib.atlas_mem_bwd_noalloc.restype = i32
+    lib.atlas_mem_bwd_noalloc.argtypes = [P, ctypes.POINTER(BwdArgs), vp, vp]
+    lib.atlas_mem_noalloc_scratch_bytes.restype = sz
+    lib.atlas_mem_noalloc_scratch_bytes.argtypes = []
     lib.atlas_scan_fwd.restype = i32
     lib.atlas_scan_fwd.argtypes = [i32, i64, i64, i64, vp, vp, vp, vp, vp]
     lib.atlas_scan_bwd.restype = i32

@@ -365,6 +365,34 @@ int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, voi
   return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
 }
 
+int check_bwd_args(const atlas_mem_problem& p, const atlas_mem_bwd_args* args, const float* saved,
+                   const void* workspace);
+
+// Scratch of atlas_mem_bwd_noalloc: the backward workspace as a file-scope device array (each GPU
+// holds its own copy for the life of the process). In host code `scratch` names a host-side
+// stand-in, never the device memory: its per-device address comes from hipGetSymbolAddress, looked
+// up once per device with that device current (the entry point's first call there) and kept in
+// scratch_dev. Calls that overlap on one GPU share the array and race; every call overwrites what
+// it reads (the backward never relies on zeroed workspace), so nothing has to be cleared.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_dev[kMaxDevices] = {};
+
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return ATLAS_MEM_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lk(scratch_mu);
+  if (!scratch_dev[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return ATLAS_MEM_ERR_LAUNCH;
+    scratch_dev[dev] = p;
+  }
+  *out = scratch_dev[dev];
+  return ATLAS_MEM_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -383,6 +411,7 @@ const char* atlas_mem_strerror(int status) {
     case ATLAS_MEM_ERR_WORKSPACE: return "workspace smaller than atlas_mem_bwd_workspace_bytes()";
     case ATLAS_MEM_ERR_LAUNCH: return "a HIP kernel launch or runtime call failed";
     case ATLAS_MEM_ERR_ARG: return "inconsistent flags (momentum/gate/map/buffer/clamp)";
+    case ATLAS_MEM_ERR_SCRATCH: return "the backward workspace exceeds the 64 MiB static scratch of atlas_mem_bwd_noalloc; use atlas_mem_bwd";
     default: return "unknown atlas_mem status";
   }
 }
@@ -428,8 +457,37 @@ int atlas_mem_bwd(const atlas_mem_problem* prob, const atlas_mem_bwd_args* args,
   const Plan pl = make_plan(prob);
   if (!pl.ok) return pl.status;
   if (!args || !saved || !workspace) return ATLAS_MEM_ERR_NULL;
-  const atlas_mem_problem& p = *prob;
   if (workspace_bytes < bwd_layout(pl).total) return ATLAS_MEM_ERR_WORKSPACE;
+  const int st = check_bwd_args(*prob, args, saved, workspace);
+  if (st != ATLAS_MEM_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return prob->dtype == ATLAS_DT_BF16 ? run_bwd<bf16>(pl, args, saved, workspace, s)
+                                      : run_bwd<float>(pl, args, saved, workspace, s);
+}
+
+int atlas_mem_bwd_noalloc(const atlas_mem_problem* prob, const atlas_mem_bwd_args* args, const float* saved,
+                          void* stream) {
+  const Plan pl = make_plan(prob);
+  if (!pl.ok) return pl.status;
+  if (!args || !saved) return ATLAS_MEM_ERR_NULL;
+  if (bwd_layout(pl).total > kNoAllocScratchBytes) return ATLAS_MEM_ERR_SCRATCH;
+  void* ws = nullptr;
+  const int ss = scratch_on_current_device(&ws);
+  if (ss != ATLAS_MEM_OK) return ss;
+  const int st = check_bwd_args(*prob, args, saved, ws);
+  if (st != ATLAS_MEM_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return prob->dtype == ATLAS_DT_BF16 ? run_bwd<bf16>(pl, args, saved, ws, s) : run_bwd<float>(pl, args, saved, ws, s);
+}
+
+size_t atlas_mem_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+}  // extern "C"
+
+namespace {
+// Pointer and alignment checks shared by atlas_mem_bwd and atlas_mem_bwd_noalloc (no HIP call).
+int check_bwd_args(const atlas_mem_problem& p, const atlas_mem_bwd_args* args, const float* saved,
+                   const void* workspace) {
   if (!args->k || !args->q || !args->v || !args->lr || !args->decay || !args->S_ref || !args->S0 ||
       !args->dk || !args->dq || !args->dv || !args->dlr || !args->ddecay || !args->dS_ref || !args->dS0)
     return ATLAS_MEM_ERR_NULL;
@@ -443,10 +501,11 @@ int atlas_mem_bwd(const atlas_mem_problem* prob, const atlas_mem_bwd_args* args,
   const void* fp[] = {args->S_ref, args->S0, args->Z0, args->buffer_in, args->dS_T, args->dZ_T, args->dbuffer_out,
                       args->dS_ref, args->dS0, args->dZ0, args->dbuffer_in, saved, workspace};
   for (const void* q : fp) if (misaligned(q, 16)) return ATLAS_MEM_ERR_ALIGN;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  return p.dtype == ATLAS_DT_BF16 ? run_bwd<bf16>(pl, args, saved, workspace, s)
-                                  : run_bwd<float>(pl, args, saved, workspace, s);
+  return ATLAS_MEM_OK;
 }
+}  // namespace
+
+extern "C" {
 
 int atlas_mem_profile_enable(int on) {
   Profiler& P = prof();

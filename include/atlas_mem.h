@@ -51,7 +51,8 @@ enum atlas_mem_status {
   ATLAS_MEM_ERR_UNSUPPORTED = 6,  /* valid request this build does not implement */
   ATLAS_MEM_ERR_WORKSPACE = 7,    /* workspace too small */
   ATLAS_MEM_ERR_LAUNCH = 8,       /* a HIP launch or runtime call failed */
-  ATLAS_MEM_ERR_ARG = 9           /* inconsistent flags */
+  ATLAS_MEM_ERR_ARG = 9,          /* inconsistent flags */
+  ATLAS_MEM_ERR_SCRATCH = 10      /* atlas_mem_bwd_noalloc: workspace above its static scratch */
 };
 
 enum atlas_mem_dtype { ATLAS_DT_F32 = 0, ATLAS_DT_BF16 = 1 };
@@ -149,6 +150,21 @@ int atlas_mem_step(const atlas_mem_problem* prob, const atlas_mem_fwd_args* args
  * AtlasOmegaFunction.backward (atlas_pytorch/cuda/atlas_omega_autograd.py:156-204). */
 int atlas_mem_bwd(const atlas_mem_problem* prob, const atlas_mem_bwd_args* args,
                   const float* saved, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Allocation-free backward. No counterpart in the reference: for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight training loops, harnesses that forbid
+ * hipMalloc). Same problem, arguments, kernels and results as atlas_mem_bwd, with the workspace
+ * taken from a static device array of atlas_mem_noalloc_scratch_bytes() (64 MiB) that each GPU
+ * holds for the life of the process; the library allocates nothing. Problems whose
+ * atlas_mem_bwd_workspace_bytes exceeds it return ATLAS_MEM_ERR_SCRATCH (the C2, C3 and C5
+ * headline shapes need 38-58 MiB). The first call on a device looks the array up with that device
+ * current (make a first call outside graph capture). Calls that overlap on one GPU share the array
+ * and race: serialise them (one stream, or events). */
+int atlas_mem_bwd_noalloc(const atlas_mem_problem* prob, const atlas_mem_bwd_args* args,
+                          const float* saved, void* stream);
+
+/* Size of the static scratch array of atlas_mem_bwd_noalloc, in bytes. */
+size_t atlas_mem_noalloc_scratch_bytes(void);
 
 /* ---- scan primitives (row-major [n, t, d] buffers of `dtype`, gates [n, t]) -------------- */
 

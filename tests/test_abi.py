@@ -106,8 +106,25 @@ def test_sizes(lib):
     assert lib.atlas_mem_saved_bytes(ctypes.byref(pc)) >= 32 * (4096 // 32) * 2 * st
 
 
+def test_noalloc_backward_host_checks(lib):
+    # the static scratch is 64 MiB: the headline shapes fit, a larger workspace is refused before any
+    # HIP call, as are missing pointers
+    assert lib.atlas_mem_noalloc_scratch_bytes() == 64 << 20
+    assert lib.atlas_mem_bwd_workspace_bytes(ctypes.byref(_prob())) <= 64 << 20          # C3
+    assert lib.atlas_mem_bwd_workspace_bytes(ctypes.byref(_prob(bh=64, seq_len=2048, gate_mode=_lib.GATE_TOKEN))) <= 64 << 20
+    good = ctypes.c_void_p(0x10000)
+    args = _lib.BwdArgs()
+    big = _prob(bh=256)
+    assert lib.atlas_mem_bwd_workspace_bytes(ctypes.byref(big)) > 64 << 20
+    assert lib.atlas_mem_bwd_noalloc(ctypes.byref(big), ctypes.byref(args), good, None) == _lib.ERR_SCRATCH
+    assert lib.atlas_mem_bwd_noalloc(ctypes.byref(_prob()), None, good, None) == 4
+    assert lib.atlas_mem_bwd_noalloc(ctypes.byref(_prob()), ctypes.byref(args), None, None) == 4
+    assert lib.atlas_mem_bwd_noalloc(ctypes.byref(_prob(d_k=48)), ctypes.byref(args), good, None) == 2
+    assert b"64 MiB" in lib.atlas_mem_strerror(_lib.ERR_SCRATCH)
+
+
 def test_strerror(lib):
-    for code in range(0, 10):
+    for code in range(0, 11):
         assert len(lib.atlas_mem_strerror(code)) > 0
     assert b"unknown" in lib.atlas_mem_strerror(99)
 
