@@ -2,16 +2,20 @@
 
 Workload (the metric's shape): B=4, H=8 (BH=32), T=4096, d_k=d_v=64,
 Omega window e=4 with per-lag softmax gates, momentum, bf16 inputs, fp32 state, chunk 64,
-S0 = S_ref = Z0 = 0, zero buffer; dy ~ N(0,1) (loss = sum y * g). Inputs are synthetic, seeded,
-and resident in HBM before the timed region. One step = one forward + one backward of the
-recurrence over the whole batch (libatlas_mem.so through its C ABI, preallocated buffers).
+S0 = S_ref = Z0 = 0; dy ~ N(0,1) (loss = sum y * g). Inputs are synthetic, seeded, and resident in
+HBM before the timed region. One step = one forward + one backward of the recurrence over the
+whole batch (libatlas_mem.so through its C ABI, preallocated buffers).
 
 Prints ONE JSON line (rank 0). `value` and `ms_per_step` come from K plain steps. `roofline`
 covers the kernel with the largest share of the step: the same K steps are run again with the
 library's HIP events recorded around every launch on the launch stream (the records between
 launches lengthen that pass, reported as `profiled_ms_per_step`, so it gives kernel durations only);
-`cpu_baseline` times the CPU oracle (the fp32 torch restatement of the reference op sequence,
-forward + backward through autograd) on a bounded sample of the same workload.
+`mfma` is the step's matrix-product work against the bf16 peak; `cpu_baseline` times the CPU oracle
+(the fp32 torch restatement of the reference op sequence, forward + backward through autograd) on a
+bounded sample of the same workload.
+
+`--config c2|c5` runs the other HBM-bound BASELINE configs the same way; `--config c4` the tensor
+feature map configuration (MFMA-bound; autograd path); `--config decode` the one-token step.
 """
 
 from __future__ import annotations
@@ -27,16 +31,37 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, TFLOP/s
 B, H, T, D, E = 4, 8, 4096, 64, 4
 BH = B * H
 TOKENS = B * T               # (b, t) positions through one memory layer, all heads
 
+# The configurations run through the preplanned native path (RecurrencePlan: the C ABI with every
+# buffer allocated up front). C3 is the headline (the default run); c2 / c5 are the other HBM-bound
+# BASELINE configs. Tokens are (b, t) positions through one memory layer.
+PLAN_CONFIGS = {
+    "c3": dict(B=4, H=8, T=4096, d=64, e=4, gate="lag", seed=1003, cpu_sample_t=1024,
+               workload="C3 OmegaNet-RNN memory layer: B=4 H=8 T=4096 d=64 e=4 lag gates, momentum, "
+                        "bf16 inputs, fp32 state, chunk 64"),
+    "c2": dict(B=4, H=8, T=2048, d=64, e=1, gate=None, seed=1002, cpu_sample_t=1024,
+               workload="C2 Titans-RNN memory layer: B=4 H=8 T=2048 d=64, momentum, bf16 inputs, fp32 state, "
+                        "chunk 64"),
+    "c5": dict(B=8, H=8, T=2048, d=64, e=4, gate="token", seed=1005, cpu_sample_t=512,
+               workload="C5 memory core of one RNN-transformer layer: B=8 H=8 T=2048 d=64 e=4 per-token gates, "
+                        "momentum, bf16 inputs, fp32 state"),
+}
 
-def algorithmic_bytes(bh=BH, t=T, d=D, e=E, s_in=2, s_st=4):
+
+def n_scalars(e, gate):
+    """Per-token-head scalars: eta, alpha, beta, plus e lag gates or one token gate."""
+    return 3 + (e if gate == "lag" else 1 if gate == "token" else 0)
+
+
+def algorithmic_bytes(bh=BH, t=T, d=D, e=E, n_sc=None, s_in=2, s_st=4):
     """Compulsory HBM bytes (each input read once, each output written once) per kernel and per
-    step. Scalars per token-head: eta, alpha, beta and e lag gates."""
+    step. n_sc: scalars per token-head (default: eta, alpha, beta and e lag gates)."""
     n = bh * t
-    n_sc = 3 + e
+    n_sc = 3 + e if n_sc is None else n_sc
     st = bh * d * d * s_st
     buf = 2 * bh * (e - 1) * d * d * s_st
     fwd = n * 3 * d * s_in + n * n_sc * s_in + n * d * s_in + 5 * st + buf
@@ -72,42 +97,98 @@ def algorithmic_bytes(bh=BH, t=T, d=D, e=E, s_in=2, s_st=4):
     return fwd, bwd, per_kernel
 
 
-def make_inputs(device):
+def flops_per_step(bh, t, d=D, momentum=True, bwd_factor=2.0, chunk=64):
+    """Matrix-core work of one step (the chunked form's products, per token-head): delta = S_ref phi
+    (2 d^2), the intra-chunk psi phi^T and its product with delta (2 * 2 C d), the chunk-start
+    state's contribution psi S (and psi Z) (2 d^2 each) and the end-state update delta^T W phi per
+    chunk (2 d^2 per token for S, and for Z); the backward does about twice the forward's. At d = 64,
+    C = 64 with momentum: 57,344 flop per token-head forward."""
+    ns = 2 if momentum else 1
+    fwd = 2 * d * d + 2 * 2 * chunk * d + ns * 2 * d * d + ns * 2 * d * d
+    return bh * t * fwd * (1.0 + bwd_factor)
+
+
+def cpu_threads():
+    """Host threads for the CPU baseline: every core of this process's affinity mask, limited to
+    the box's CPU share where the environment states one (OMP_NUM_THREADS)."""
+    aff = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS")
+    n = min(aff, int(cap)) if cap and cap.isdigit() and int(cap) > 0 else aff
+    return max(1, n), aff
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def make_inputs(device, cfg=None):
+    """Seeded synthetic inputs of a PLAN_CONFIGS entry (default C3) on `device` (bf16 operands, fp32
+    zero states) and their fp32 CPU originals."""
     import torch
-    g = torch.Generator().manual_seed(1003)       # seed = 1000 + config number
+    cfg = PLAN_CONFIGS["c3"] if cfg is None else cfg
+    bh, t, d, e = cfg["B"] * cfg["H"], cfg["T"], cfg["d"], cfg["e"]
+    g = torch.Generator().manual_seed(cfg["seed"])       # seed = 1000 + config number
     r = lambda *s: torch.randn(*s, generator=g)
-    k = r(BH, T, D)
+    k = r(bh, t, d)
     k = k / k.norm(dim=-1, keepdim=True)
-    x = dict(k=k, q=r(BH, T, D), v=r(BH, T, D),
-             lr=0.1 * torch.sigmoid(r(BH, T)), decay=torch.sigmoid(r(BH, T) * 0.5 + 2.0),
-             beta=torch.sigmoid(r(BH, T) * 0.5 + 1.0), gate=torch.softmax(r(BH, T, E), dim=-1),
-             dy=r(BH, T, D))
+    x = dict(k=k, q=r(bh, t, d), v=r(bh, t, d),
+             lr=0.1 * torch.sigmoid(r(bh, t)), decay=torch.sigmoid(r(bh, t) * 0.5 + 2.0),
+             beta=torch.sigmoid(r(bh, t) * 0.5 + 1.0))
+    if cfg["gate"] == "lag":
+        x["gate"] = torch.softmax(r(bh, t, e), dim=-1)
+    elif cfg["gate"] == "token":
+        x["gate"] = torch.sigmoid(r(bh, t))
+    x["dy"] = r(bh, t, d)
     out = {kk: v.to(device=device, dtype=torch.bfloat16).contiguous() for kk, v in x.items()}
-    zeros = torch.zeros(BH, D, D, device=device, dtype=torch.float32)
+    out.setdefault("gate", None)
+    x.setdefault("gate", None)
+    zeros = torch.zeros(bh, d, d, device=device, dtype=torch.float32)
     out.update(S_ref=zeros, S0=zeros, Z0=zeros)
     return out, x
 
 
-def cpu_baseline(x_cpu, sample_t=256, reps=3):
-    """Oracle (fp32, autograd) on the first `sample_t` tokens of every (b, h): 1 warmup, median
-    of `reps`. Returns tokens/s of the sample and the thread count."""
+def cpu_baseline(x_cpu, cfg=None, sample_t=256, reps=3, proj=None, map_degree=1):
+    """The CPU oracle (fp32 torch restatement of the reference op sequence, forward + backward
+    through autograd) on the first `sample_t` tokens of every (b, h) row: 1 warmup, median of
+    `reps`. The oracle's work per token does not grow with T (its scans are linear-work), so the
+    sample's tokens/s stands for the full sequence. With `proj`, k and q first go through the tensor
+    feature map (and the elementwise map of `map_degree`). Returns (tokens/s, threads, affinity
+    cores, median seconds)."""
     import torch
-    from oracle import memory_recurrence_vectorised
-    cores = max(1, min(16, len(os.sched_getaffinity(0))))
-    torch.set_num_threads(cores)
+    from oracle import memory_recurrence_vectorised, poly_feature_map
+    cfg = PLAN_CONFIGS["c3"] if cfg is None else cfg
+    threads, aff = cpu_threads()
+    torch.set_num_threads(threads)
+    bh, e = cfg["B"] * cfg["H"], cfg["e"]
     sl = slice(0, sample_t)
     f32 = torch.float32
-    leaves = {kk: x_cpu[kk][:, sl].to(torch.bfloat16).to(f32).clone().requires_grad_(True)
-              for kk in ("k", "q", "v", "lr", "decay", "beta", "gate")}
+    names = ("k", "q", "v", "lr", "decay", "beta") + (("gate",) if x_cpu.get("gate") is not None else ())
+    leaves = {kk: x_cpu[kk][:, sl].to(torch.bfloat16).to(f32).clone().requires_grad_(True) for kk in names}
     dy = x_cpu["dy"][:, sl].to(torch.bfloat16).to(f32)
-    S0 = torch.zeros(BH, D, D, requires_grad=True)
-    Z0 = torch.zeros(BH, D, D, requires_grad=True)
+    dk = proj.shape[1] if proj is not None else leaves["k"].shape[-1]
+    dv = leaves["v"].shape[-1]
+    S0 = torch.zeros(bh, dv, dk, requires_grad=True)
+    Z0 = torch.zeros(bh, dv, dk, requires_grad=True)
+    P = proj.to(f32) if proj is not None else None
+
+    def feat(x):
+        if P is None:
+            return x
+        return poly_feature_map(poly_feature_map(x, 2, 'tensor', P), map_degree, 'elementwise')
+
     times = []
     for i in range(reps + 1):
         t0 = time.perf_counter()
         y, S_T, Z_T, buf = memory_recurrence_vectorised(
-            leaves["k"], leaves["q"], leaves["v"], leaves["lr"], leaves["decay"], leaves["beta"], leaves["gate"],
-            S0, S0, Z0, None, window=E)
+            feat(leaves["k"]), feat(leaves["q"]), leaves["v"], leaves["lr"], leaves["decay"], leaves["beta"],
+            leaves.get("gate"), S0, S0, Z0, None, window=e)
         (y * dy).sum().backward()
         dt = time.perf_counter() - t0
         if i > 0:
@@ -115,18 +196,29 @@ def cpu_baseline(x_cpu, sample_t=256, reps=3):
         for t in list(leaves.values()) + [S0, Z0]:
             t.grad = None
     med = statistics.median(times)
-    return B * sample_t / med, cores, med
+    return cfg["B"] * sample_t / med, threads, aff, med
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_c3.md")
+def cpu_baseline_record(x_cpu, cfg, sample_t, **kw):
+    tps, threads, aff, med = cpu_baseline(x_cpu, cfg, sample_t=sample_t, **kw)
+    bh = cfg["B"] * cfg["H"]
+    return {"value": round(tps, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle fp32 fwd+bwd (autograd) on tokens 0..{sample_t - 1} of all {bh} (b,h) rows, "
+                       f"median of 3 = {med:.2f} s; linear-work scans, so the rate stands for T = {cfg['T']}"),
+            "cpu_model": cpu_model(), "affinity_cores": aff,
+            "threads_note": "threads = affinity cores, capped at the box's CPU share (OMP_NUM_THREADS)"}
 
 
-def measured_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary (lines
-    `traffic: <kernel> <bytes>`, FETCH_SIZE + WRITE_SIZE scaled by the copy-kernel factor), or
-    None when the summary has no figure for it."""
+def traffic_file(name):
+    return os.path.join(ROOT, "profiles", f"hbm_traffic_{name}.md")
+
+
+def measured_traffic(kernel, name="c3"):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary of config
+    `name` (lines `traffic: <kernel> <bytes>`, FETCH_SIZE + WRITE_SIZE scaled by the copy-kernel
+    factor), or None when there is no summary or no figure for it."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(traffic_file(name)) as f:
             for line in f:
                 parts = line.split()
                 if len(parts) == 3 and parts[0] == "traffic:" and parts[1] == kernel:
@@ -149,71 +241,56 @@ def calibrate_copy(nbytes=256 << 20, reps=5):
     print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "launches": reps}), flush=True)
 
 
-# The other BASELINE configs (`--config c2|c4|c5`): one JSON line each, same keys; the default
-# run (no flag) is the C3 headline above. Tokens are (b, t) positions through one memory layer.
-OTHER_CONFIGS = {
-    # Titans-RNN with momentum, no window, no gate, bf16, B=4 H=8 T=2048 d=64
-    "c2": dict(B=4, H=8, T=2048, dk=64, dv=64, e=1, gate=None, seed=1002,
-               workload="C2 Titans-RNN memory layer: B=4 H=8 T=2048 d=64, momentum, bf16 inputs, fp32 state, "
-                        "chunk 64"),
-    # OmegaNet-RNN with the tensor feature map phi = elementwise_g3([k; vec(k k^T)] P), P: 4160 -> 128
-    # (Xavier-uniform), d_k = 128, d_v = 64, e = 8, lag gates; the map's GEMM is part of the step
-    "c4": dict(B=2, H=8, T=8192, dk=128, dv=64, e=8, gate="lag", seed=1004, tensor_map=True,
-               workload="C4 OmegaNet-RNN memory layer with the tensor feature map (64+4096 -> 128, then the "
-                        "elementwise map of degree 3): B=2 H=8 T=8192 d_k=128 d_v=64 e=8 lag gates, momentum, "
-                        "bf16 inputs, fp32 state"),
-    # the memory core of one layer of the byte-level RNN transformer: B=8 H=8 T=2048, e=4, per-token gates
-    "c5": dict(B=8, H=8, T=2048, dk=64, dv=64, e=4, gate="token", seed=1005,
-               workload="C5 memory core of one RNN-transformer layer: B=8 H=8 T=2048 d=64 e=4 per-token gates, "
-                        "momentum, bf16 inputs, fp32 state"),
-}
+# C4 (`--config c4`): OmegaNet-RNN with the tensor feature map phi = elementwise_g3([k; vec(k k^T)] P),
+# P: 4160 -> 128 (Xavier-uniform), d_k = 128, d_v = 64, e = 8, lag gates. The map is a GEMM with
+# K = 4160 (MFMA-bound); the step runs through the autograd API (the map's fused kernels, then the
+# recurrence on 64 x 64 state blocks).
+C4 = dict(B=2, H=8, T=8192, dk=128, dv=64, e=8, gate="lag", seed=1004, d_in=64, degree=3,
+          workload="C4 OmegaNet-RNN memory layer with the tensor feature map (64+4096 -> 128, then the "
+                   "elementwise map of degree 3): B=2 H=8 T=8192 d_k=128 d_v=64 e=8 lag gates, momentum, "
+                   "bf16 inputs, fp32 state")
 
 
-def run_other_config(name, steps, warmup):
-    """fwd+bwd of config `name` through the autograd API (torch.autograd.grad of y against a fixed
-    random output gradient, i.e. the gradient of sum(y * g))."""
+def run_c4(steps, warmup, cpu=True, cpu_sample_t=128):
+    """C4 fwd+bwd through the autograd API (torch.autograd.grad of y against a fixed random output
+    gradient, i.e. the gradient of sum(y * g)). The roofline is the matrix-core one of the dominant
+    kernel, the fused tensor map's backward or forward, timed with HIP events on the stream it is
+    launched on (direct C-ABI calls on preallocated buffers, the same launches the step makes)."""
+    import ctypes
     import torch
-    from atlas_rnn_amd.functional import memory_recurrence, tensor_feature_map
-    c = OTHER_CONFIGS[name]
+    from atlas_rnn_amd import _lib
+    from atlas_rnn_amd.functional import memory_recurrence, tensor_feature_map, _ptr, _stream
+    c = C4
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    bh, t, dk, dv, e = c["B"] * c["H"], c["T"], c["dk"], c["dv"], c["e"]
+    bh, t, dk, dv, e, kin, deg = c["B"] * c["H"], c["T"], c["dk"], c["dv"], c["e"], c["d_in"], c["degree"]
     g = torch.Generator().manual_seed(c["seed"])
     r = lambda *sh: torch.randn(*sh, generator=g)
     bf = lambda x: x.to(device=dev, dtype=torch.bfloat16).contiguous()
-    tensor_map = c.get("tensor_map", False)
-    kin = 64 if tensor_map else dk
     k = r(bh, t, kin)
     k = k / k.norm(dim=-1, keepdim=True)
     q = r(bh, t, kin)
-    q = q / q.norm(dim=-1, keepdim=True) if tensor_map else q
-    gate = None
-    if c["gate"] == "lag":
-        gate = torch.softmax(r(bh, t, e), dim=-1)
-    elif c["gate"] == "token":
-        gate = torch.sigmoid(r(bh, t))
-    leaves = dict(k=bf(k), q=bf(q), v=bf(r(bh, t, dv)), lr=bf(0.1 * torch.sigmoid(r(bh, t))),
-                  decay=bf(torch.sigmoid(r(bh, t) * 0.5 + 2.0)), beta=bf(torch.sigmoid(r(bh, t) * 0.5 + 1.0)),
-                  gate=bf(gate) if gate is not None else None)
-    for v in leaves.values():
-        if v is not None:
-            v.requires_grad_(True)
-    P = None
-    if tensor_map:   # Xavier-uniform (64 + 4096) -> 128, seeded
-        bound = (6.0 / (kin + kin * kin + dk)) ** 0.5
-        P = bf((torch.rand(kin + kin * kin, dk, generator=g) * 2 - 1) * bound)
-    gy = bf(r(bh, t, dv))
+    q = q / q.norm(dim=-1, keepdim=True)
+    x_cpu = dict(k=k, q=q, v=r(bh, t, dv), lr=0.1 * torch.sigmoid(r(bh, t)),
+                 decay=torch.sigmoid(r(bh, t) * 0.5 + 2.0), beta=torch.sigmoid(r(bh, t) * 0.5 + 1.0),
+                 gate=torch.softmax(r(bh, t, e), dim=-1))
+    leaves = {kk: bf(v).requires_grad_(True) for kk, v in x_cpu.items()}
+    bound = (6.0 / (kin + kin * kin + dk)) ** 0.5
+    P_cpu = (torch.rand(kin + kin * kin, dk, generator=g) * 2 - 1) * bound
+    P = bf(P_cpu)
+    dy_cpu = r(bh, t, dv)
+    x_cpu["dy"] = dy_cpu
+    gy = bf(dy_cpu)
     zeros = torch.zeros(bh, dv, dk, device=dev)
 
     def feat(x):   # fused tensor-map kernels, elementwise map of degree 3 in their epilogue
-        return tensor_feature_map(x, P, degree=3) if tensor_map else x
+        return tensor_feature_map(x, P, degree=deg)
 
     def step():
         y, S_T, Z_T, B_out = memory_recurrence(
             feat(leaves["k"]), feat(leaves["q"]), leaves["v"], leaves["lr"], leaves["decay"], leaves["beta"],
             leaves["gate"], zeros, zeros, zeros, None, window=e)
-        ins = [v for v in leaves.values() if v is not None]
-        torch.autograd.grad(y, ins, grad_outputs=gy)
+        torch.autograd.grad(y, list(leaves.values()), grad_outputs=gy)
 
     for _ in range(warmup):
         step()
@@ -223,14 +300,59 @@ def run_other_config(name, steps, warmup):
         step()
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
+
+    # the map's kernels alone, on preallocated buffers: n = BH * T tokens per call (k or q)
+    lib = _lib.load()
+    n = bh * t
+    xk = leaves["k"].detach().reshape(n, kin).contiguous()
+    pt = P.t().contiguous()
+    out = torch.empty(n, dk, device=dev, dtype=torch.bfloat16)
+    pre = torch.empty_like(out)
+    dout = bf(r(n, dk))
+    dx = torch.empty_like(xk)
+    stream = _stream(dev)
+    fwd_call = lambda: _lib.check(lib.atlas_tensor_map_fwd(_lib.DT_BF16, n, kin, dk, deg, _ptr(xk), _ptr(pt),
+                                                           _ptr(out), _ptr(pre), stream), "atlas_tensor_map_fwd")
+    bwd_call = lambda: _lib.check(lib.atlas_tensor_map_bwd(_lib.DT_BF16, n, kin, dk, deg, _ptr(xk), _ptr(P),
+                                                           _ptr(pre), _ptr(dout), _ptr(dx), stream),
+                                  "atlas_tensor_map_bwd")
+    kern = {}
+    for name, call in (("k_tmap_fwd", fwd_call), ("k_tmap_bwd", bwd_call)):
+        for _ in range(3):
+            call()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(torch.cuda.current_stream(dev))
+        for _ in range(steps):
+            call()
+        ev1.record(torch.cuda.current_stream(dev))
+        torch.cuda.synchronize()
+        kern[name] = 1e3 * ev0.elapsed_time(ev1) / steps   # microseconds per launch
+    map_flops = 2.0 * (kin + kin * kin) * dk * n          # one call: [n, 4160] x [4160, 128]
+    # per step: 2 forward and 2 backward map calls + the recurrence on 2 state blocks (d = 64)
+    step_flops = 4 * map_flops + 2 * flops_per_step(bh, t, 64)
+    dom = max(kern, key=kern.get)
+    ach = map_flops / (kern[dom] * 1e-6) / 1e12
     tokens = c["B"] * t
-    out = {"metric": "memory-layer tokens/s fwd+bwd", "value": round(tokens * steps / el, 1), "unit": "tokens/s",
-           "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(1e3 * el / steps, 4),
-           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-           "data": "synthetic (seeded)", "config": {"workload": c["workload"], "global_batch": c["B"],
-                                                     "seq_len": t, "heads": c["H"], "d_k": dk, "d_v": dv,
-                                                     "window": e, "parallelism": "single GPU"}}
-    print(json.dumps(out), flush=True)
+    ms = 1e3 * el / steps
+    line = {"metric": "memory-layer tokens/s fwd+bwd", "value": round(tokens * steps / el, 1), "unit": "tokens/s",
+            "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded)",
+            "config": {"workload": c["workload"], "global_batch": c["B"], "seq_len": t, "heads": c["H"], "d_k": dk,
+                       "d_v": dv, "window": e, "parallelism": "single GPU"},
+            "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                         "algorithmic_flops_per_launch": map_flops, "avg_launch_us": round(kern[dom], 2)},
+            "kernels": {kk: {"avg_us": round(v, 2)} for kk, v in kern.items()},
+            "mfma": {"flops_per_step": step_flops, "achieved_tflops": round(step_flops / (ms * 1e-3) / 1e12, 1),
+                     "peak_tflops": BF16_PEAK_TFLOPS,
+                     "frac": round(step_flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}}
+    if cpu:
+        line["cpu_baseline"] = cpu_baseline_record(x_cpu, dict(B=c["B"], H=c["H"], T=t, e=e), cpu_sample_t,
+                                                   proj=P_cpu.to(torch.bfloat16).float(), map_degree=deg)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
 
 
 def run_decode(steps, warmup):
@@ -292,54 +414,29 @@ def run_decode(steps, warmup):
     print(json.dumps(out), flush=True)
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-tokens", type=int, default=256)
-    ap.add_argument("--calibrate-copy", action="store_true",
-                    help="run only a plain copy kernel of known size (HBM counter calibration)")
-    ap.add_argument("--config", choices=["c3"] + sorted(OTHER_CONFIGS) + ["decode"], default="c3",
-                    help="c3 (default): the headline; c2 / c4 / c5: the other BASELINE configs; decode: the "
-                         "one-token step")
-    args = ap.parse_args()
-    if args.calibrate_copy:
-        calibrate_copy()
-        return
-    if args.config != "c3":
-        if args.gpus != 1:
-            print("bench.py measures one GPU (use --gpus 1).", file=sys.stderr)
-            sys.exit(2)
-        if args.config == "decode":
-            run_decode(args.steps, args.warmup)
-        else:
-            run_other_config(args.config, args.steps, args.warmup)
-        return
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: the memory-layer recurrence shards over (batch, head) rows "
-              "with no exchange, so there is no multi-GPU figure to report (use --gpus 1).", file=sys.stderr)
-        sys.exit(2)
-
+def bench_plan(name, steps, warmup, cpu=True, cpu_sample_t=256):
+    """fwd+bwd of PLAN_CONFIGS[name] through the preplanned native path: K plain steps timed
+    (value, ms_per_step); the same K steps again with the library's HIP events around every launch
+    on its stream (per-kernel durations for the roofline); then the CPU oracle on a sample."""
     import torch
     from atlas_rnn_amd.functional import RecurrencePlan, profile_enable, profile_read
-
+    cfg = PLAN_CONFIGS[name]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    x, x_cpu = make_inputs(dev)
-    plan = RecurrencePlan(BH, T, D, window=E, momentum=True, gate_mode='lag', dtype=torch.bfloat16, device=dev)
+    bh, t, d, e = cfg["B"] * cfg["H"], cfg["T"], cfg["d"], cfg["e"]
+    x, x_cpu = make_inputs(dev, cfg)
+    plan = RecurrencePlan(bh, t, d, window=e, momentum=True, gate_mode=cfg["gate"], dtype=torch.bfloat16, device=dev)
 
     def step():
         plan.forward(x["k"], x["q"], x["v"], x["lr"], x["decay"], x["beta"], x["gate"], x["S_ref"], x["S0"], x["Z0"])
         plan.backward(x["dy"])
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     # timed region: K steps, nothing else on the stream
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
@@ -349,7 +446,7 @@ def main():
     profile_read(reset=True)
     torch.cuda.synchronize()
     tp0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     torch.cuda.synchronize()
     tp1 = time.perf_counter()
@@ -357,48 +454,80 @@ def main():
     profile_enable(False)
 
     elapsed = t1 - t0
-    ms_per_step = 1e3 * elapsed / args.steps
-    value = TOKENS * args.steps / elapsed
-    fwd_b, bwd_b, per_kernel = algorithmic_bytes()
+    ms_per_step = 1e3 * elapsed / steps
+    tokens = cfg["B"] * t
+    value = tokens * steps / elapsed
+    fwd_b, bwd_b, per_kernel = algorithmic_bytes(bh, t, d, e, n_scalars(e, cfg["gate"]))
     step_bytes = fwd_b + bwd_b
-    kernels = {name: {"avg_us": 1e3 * ms / max(n, 1), "launches": n} for name, (ms, n) in prof.items() if n}
+    kernels = {kk: {"avg_us": 1e3 * ms / max(n, 1), "launches": n} for kk, (ms, n) in prof.items() if n}
     dom = max(kernels, key=lambda kk: kernels[kk]["avg_us"] * kernels[kk]["launches"])
     dom_s = kernels[dom]["avg_us"] * 1e-6
     achieved = per_kernel[dom] / dom_s / 1e9
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": measured_traffic(dom),
+                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": measured_traffic(dom, name),
                 "algorithmic_bytes_per_launch": per_kernel[dom], "avg_launch_us": round(kernels[dom]["avg_us"], 2)}
-    step_gbs = step_bytes / (elapsed / args.steps) / 1e9
+    step_gbs = step_bytes / (elapsed / steps) / 1e9
+    flops = flops_per_step(bh, t, d)
+    tflops = flops / (elapsed / steps) / 1e12
     out = {
-        "metric": "memory-layer tokens/s fwd+bwd at H=8,d=64,T=4096; % HBM/MFMA roofline",
+        "metric": "memory-layer tokens/s fwd+bwd at H=8,d=64,T=4096; % HBM/MFMA roofline" if name == "c3"
+        else "memory-layer tokens/s fwd+bwd",
         "value": round(value, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) q/k/v with L2-normalised keys, sigmoid gates, softmax lag gates)",
-        "config": {"workload": "C3 OmegaNet-RNN memory layer: B=4 H=8 T=4096 d=64 e=4 lag gates, momentum, "
-                               "bf16 inputs, fp32 state, chunk 64", "global_batch": B, "seq_len": T,
-                   "heads": H, "d": D, "window": E, "parallelism": "single GPU"},
+        "data": "synthetic (seeded N(0,1) q/k/v with L2-normalised keys, sigmoid gates"
+                + (", softmax lag gates)" if cfg["gate"] == "lag" else ")"),
+        "config": {"workload": cfg["workload"], "global_batch": cfg["B"], "seq_len": t,
+                   "heads": cfg["H"], "d": d, "window": e, "parallelism": "single GPU"},
         "roofline": roofline,
         "step_roofline": {"bytes_per_step": step_bytes, "achieved_gbs": round(step_gbs, 2),
                           "frac": round(step_gbs / HBM_PEAK_GBS, 5)},
+        "mfma": {"flops_per_step": flops, "achieved_tflops": round(tflops, 2), "peak_tflops": BF16_PEAK_TFLOPS,
+                 "frac": round(tflops / BF16_PEAK_TFLOPS, 5),
+                 "note": "the chunked form's matrix products (bf16 in, fp32 accumulate) per step"},
         "kernels": {kk: {"avg_us": round(v["avg_us"], 2), "launches": v["launches"]} for kk, v in kernels.items()},
-        "profiled_ms_per_step": round(1e3 * (tp1 - tp0) / args.steps, 4),
+        "profiled_ms_per_step": round(1e3 * (tp1 - tp0) / steps, 4),
     }
-    if not args.no_cpu_baseline:
-        cpu_tps, cores, med = cpu_baseline(x_cpu, sample_t=args.cpu_sample_tokens)
-        out["cpu_baseline"] = {"value": round(cpu_tps, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
-                               "sample": f"oracle fp32 fwd+bwd (autograd) on tokens 0..{args.cpu_sample_tokens - 1} "
-                                         f"of all {BH} (b,h) rows, median of 3 = {med:.2f} s"}
-    else:
-        out["cpu_baseline"] = None
+    out["cpu_baseline"] = cpu_baseline_record(x_cpu, cfg, cpu_sample_t) if cpu else None
     print(json.dumps(out), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-tokens", type=int, default=None,
+                    help="tokens per row of the CPU baseline sample (default: 1024 c2/c3, 512 c5, 128 c4)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a plain copy kernel of known size (HBM counter calibration)")
+    ap.add_argument("--config", choices=sorted(PLAN_CONFIGS) + ["c4", "decode"], default="c3",
+                    help="c3 (default): the headline; c2 / c4 / c5: the other BASELINE configs; decode: the "
+                         "one-token step")
+    args = ap.parse_args()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the memory-layer recurrence shards over (batch, head) rows "
+              "with no exchange, so there is no multi-GPU figure to report (use --gpus 1).", file=sys.stderr)
+        sys.exit(2)
+    cpu = not args.no_cpu_baseline
+    if args.config == "decode":
+        run_decode(args.steps, args.warmup)
+    elif args.config == "c4":
+        run_c4(args.steps, args.warmup, cpu=cpu, cpu_sample_t=args.cpu_sample_tokens or 128)
+    else:
+        bench_plan(args.config, args.steps, args.warmup, cpu=cpu,
+                   cpu_sample_t=args.cpu_sample_tokens or PLAN_CONFIGS[args.config]["cpu_sample_t"])
 
 
 if __name__ == "__main__":
