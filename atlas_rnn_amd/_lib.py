@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "atlas_window_sum",
     "atlas_affine_scan_fwd",
     "atlas_affine_scan_bwd",
+    "atlas_affine_scan_workspace_bytes",
     "atlas_tensor_map_fwd",
     "atlas_tensor_map_bwd",
     "atlas_mem_profile_enable",
@@ -123,9 +124,11 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_window_sum.restype = i32
     lib.atlas_window_sum.argtypes = [i32, i64, i64, i64, i32, i32, vp, vp, vp]
     lib.atlas_affine_scan_fwd.restype = i32
-    lib.atlas_affine_scan_fwd.argtypes = [i32, i32, i32, i32, vp, vp, vp, vp, vp]
+    lib.atlas_affine_scan_fwd.argtypes = [i32, i32, i32, i32, vp, vp, vp, vp, vp, sz, vp]
     lib.atlas_affine_scan_bwd.restype = i32
-    lib.atlas_affine_scan_bwd.argtypes = [i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.atlas_affine_scan_bwd.argtypes = [i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
+    lib.atlas_affine_scan_workspace_bytes.restype = sz
+    lib.atlas_affine_scan_workspace_bytes.argtypes = [i32, i32, i32, i32]
     lib.atlas_tensor_map_fwd.restype = i32
     lib.atlas_tensor_map_fwd.argtypes = [i32, i64, i32, i32, i32, vp, vp, vp, vp, vp]
     lib.atlas_tensor_map_bwd.restype = i32

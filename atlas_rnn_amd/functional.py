@@ -609,6 +609,11 @@ def window_sum(x: Tensor, window: int) -> Tensor:
     return _WindowSumFn.apply(x.to(dt).contiguous(), int(window))
 
 
+def _affine_workspace(lib, n, t, r, d, device) -> tuple[Tensor, int]:
+    nbytes = lib.atlas_affine_scan_workspace_bytes(n, t, r, d)
+    return torch.empty((nbytes + 3) // 4, device=device, dtype=torch.float32), nbytes
+
+
 class _AffineScanFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, A, B, prev):
@@ -616,8 +621,9 @@ class _AffineScanFn(torch.autograd.Function):
         n, t, d = A.shape[0], A.shape[1], A.shape[2]
         r = B.shape[2]
         out = torch.empty_like(B)
-        _lib.check(lib.atlas_affine_scan_fwd(n, t, r, d, _ptr(A), _ptr(B), _ptr(prev), _ptr(out), _stream(A.device)),
-                   "atlas_affine_scan_fwd")
+        ws, nbytes = _affine_workspace(lib, n, t, r, d, A.device)
+        _lib.check(lib.atlas_affine_scan_fwd(n, t, r, d, _ptr(A), _ptr(B), _ptr(prev), _ptr(out), _ptr(ws), nbytes,
+                                             _stream(A.device)), "atlas_affine_scan_fwd")
         ctx.save_for_backward(A, out, prev)
         return out
 
@@ -631,16 +637,21 @@ class _AffineScanFn(torch.autograd.Function):
         dA = torch.empty_like(A)
         dB = torch.empty_like(out)
         dprev = torch.empty_like(prev) if prev is not None else None
+        ws, nbytes = _affine_workspace(lib, n, t, r, d, A.device)
         _lib.check(lib.atlas_affine_scan_bwd(n, t, r, d, _ptr(A), _ptr(out), _ptr(prev), _ptr(dout), _ptr(dA), _ptr(dB),
-                                             _ptr(dprev), _stream(A.device)), "atlas_affine_scan_bwd")
+                                             _ptr(dprev), _ptr(ws), nbytes, _stream(A.device)), "atlas_affine_scan_bwd")
         return dA, dB, dprev
 
 
 def affine_associative_scan(A: Tensor, B: Tensor, *, prev: Tensor | None = None, remove_prev: bool = False) -> Tensor:
     """H_t = H_{t-1} A_t + B_t (atlas_pytorch/affine_scan.py:36-158): A [N,T,D,D], B [N,T,R,D],
     prev [N,R,D]. Returns [N,T,R,D], or [N,T+1,R,D] led by prev when prev is given and not
-    remove_prev. Computed in fp32 (D, R <= 64); the result has B's dtype."""
+    remove_prev. Computed in fp32 on the matrix cores, chunked (D, R <= 64); the result has B's dtype."""
     _require_gpu(A, B, prev)
+    if A.dim() != 4 or A.shape[2] != A.shape[3] or B.dim() != 4 or B.shape[:2] != A.shape[:2] or B.shape[3] != A.shape[2]:
+        raise ValueError(f"A must be [N, T, D, D] and B [N, T, R, D], got {tuple(A.shape)} and {tuple(B.shape)}")
+    if prev is not None and tuple(prev.shape) != (B.shape[0], B.shape[2], B.shape[3]):
+        raise ValueError(f"prev must be [N, R, D] = {(B.shape[0], B.shape[2], B.shape[3])}, got {tuple(prev.shape)}")
     dt = B.dtype
     A32 = A.float().contiguous()
     B32 = B.float().contiguous()

@@ -355,6 +355,85 @@ def run_c4(steps, warmup, cpu=True, cpu_sample_t=128):
     print(json.dumps(line), flush=True)
 
 
+def run_affine(steps, warmup, n=32, t=1024, d=64, r=64, cpu=True):
+    """The right-affine scan (affine_scan.py:36-158) at D = R = 64, T = 1024, N = 32, forward + backward
+    on the chunked fp32 matrix-core kernels, each pass timed with HIP events on its stream. HBM
+    roofline: A and B read once, H written once (forward); A, H, dout read once, dA, dB written once
+    (backward). `mfma` counts the sequential scan's products (2 N T R D^2 per pass, twice that for dA
+    and the adjoint) against the fp32 matrix peak."""
+    import ctypes
+    import torch
+    from atlas_rnn_amd import _lib
+    from atlas_rnn_amd.functional import _ptr, _stream
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator().manual_seed(1007)
+    A_cpu = 0.95 * torch.eye(d) + 0.3 * torch.randn(n, t, d, d, generator=g) / d ** 0.5
+    B_cpu = torch.randn(n, t, r, d, generator=g)
+    A, B = A_cpu.to(dev), B_cpu.to(dev)
+    prev = torch.randn(n, r, d, generator=g).to(dev)
+    H = torch.empty_like(B)
+    dout = torch.randn(n, t, r, d, generator=g).to(dev)
+    dA, dB, dprev = torch.empty_like(A), torch.empty_like(B), torch.empty_like(prev)
+    lib = _lib.load()
+    nb = lib.atlas_affine_scan_workspace_bytes(n, t, r, d)
+    ws = torch.empty((nb + 3) // 4, device=dev)
+    st = _stream(dev)
+    fwd = lambda: _lib.check(lib.atlas_affine_scan_fwd(n, t, r, d, _ptr(A), _ptr(B), _ptr(prev), _ptr(H), _ptr(ws),
+                                                       nb, st), "atlas_affine_scan_fwd")
+    bwd = lambda: _lib.check(lib.atlas_affine_scan_bwd(n, t, r, d, _ptr(A), _ptr(H), _ptr(prev), _ptr(dout), _ptr(dA),
+                                                       _ptr(dB), _ptr(dprev), _ptr(ws), nb, st), "atlas_affine_scan_bwd")
+    us = {}
+    for name, call in (("fwd", fwd), ("bwd", bwd)):
+        for _ in range(warmup):
+            call()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(torch.cuda.current_stream(dev))
+        for _ in range(steps):
+            call()
+        ev1.record(torch.cuda.current_stream(dev))
+        torch.cuda.synchronize()
+        us[name] = 1e3 * ev0.elapsed_time(ev1) / steps
+    a_b, bh_b = n * t * d * d * 4, n * t * r * d * 4
+    alg = {"fwd": a_b + 2 * bh_b, "bwd": 2 * a_b + 3 * bh_b}
+    flops = 2.0 * n * t * r * d * d * 3          # forward scan, adjoint scan, dA
+    step_us = us["fwd"] + us["bwd"]
+    dom = max(us, key=us.get)
+    ach = alg[dom] / (us[dom] * 1e-6) / 1e9
+    line = {"metric": "affine-scan steps/s fwd+bwd (H_t = H_{t-1} A_t + B_t)", "value": round(n * t / (step_us * 1e-6), 1),
+            "unit": "steps/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(step_us / 1e3, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded)",
+            "config": {"workload": f"affine_associative_scan N={n} T={t} R={r} D={d}, fp32, with prev",
+                       "parallelism": "single GPU"},
+            "roofline": {"bound": "hbm", "kernel": f"affine scan {dom} pass", "achieved": round(ach, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "algorithmic_bytes_per_launch": alg[dom], "avg_launch_us": round(us[dom], 2)},
+            "passes_us": {kk: round(v, 2) for kk, v in us.items()},
+            "mfma": {"flops_per_step": flops, "achieved_tflops": round(flops / (step_us * 1e-6) / 1e12, 2),
+                     "peak_tflops": 157.3, "frac": round(flops / (step_us * 1e-6) / 1e12 / 157.3, 4)}}
+    if cpu:
+        from oracle import affine_scan_sequential
+        threads, aff = cpu_threads()
+        torch.set_num_threads(threads)
+        ts = 64
+        Ac = A_cpu[:, :ts].clone().requires_grad_()
+        Bc = B_cpu[:, :ts].clone().requires_grad_()
+        pc = prev.cpu().clone().requires_grad_()
+        times = []
+        for i in range(4):
+            t0 = time.perf_counter()
+            out = affine_scan_sequential(Ac, Bc, pc, remove_prev=True)
+            (out * dout[:, :ts].cpu()).sum().backward()
+            if i:
+                times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        line["cpu_baseline"] = {"value": round(n * ts / med, 1), "unit": "steps/s", "cores": threads, "kind": "port",
+                                "sample": f"oracle sequential matmul loop fwd+bwd (autograd, fp32) on steps 0..{ts - 1} "
+                                          f"of all {n} scans, median of 3 = {med:.2f} s; linear in T",
+                                "cpu_model": cpu_model(), "affinity_cores": aff}
+    print(json.dumps(line), flush=True)
+
+
 def run_decode(steps, warmup):
     """Generation steps at the C3 head shape (B=4 H=8 d=64 e=4 lag gates, momentum, bf16 inputs,
     fp32 state): atlas_mem_step through the C ABI with the state updated in place, the way a decode
@@ -509,7 +588,7 @@ def main():
                     help="tokens per row of the CPU baseline sample (default: 1024 c2/c3, 512 c5, 128 c4)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (HBM counter calibration)")
-    ap.add_argument("--config", choices=sorted(PLAN_CONFIGS) + ["c4", "decode"], default="c3",
+    ap.add_argument("--config", choices=sorted(PLAN_CONFIGS) + ["c4", "decode", "affine"], default="c3",
                     help="c3 (default): the headline; c2 / c4 / c5: the other BASELINE configs; decode: the "
                          "one-token step")
     args = ap.parse_args()
@@ -523,6 +602,8 @@ def main():
     cpu = not args.no_cpu_baseline
     if args.config == "decode":
         run_decode(args.steps, args.warmup)
+    elif args.config == "affine":
+        run_affine(args.steps, args.warmup, cpu=cpu)
     elif args.config == "c4":
         run_c4(args.steps, args.warmup, cpu=cpu, cpu_sample_t=args.cpu_sample_tokens or 128)
     else:

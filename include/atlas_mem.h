@@ -187,16 +187,23 @@ int atlas_scan_bwd(int dtype, int64_t n, int64_t t, int64_t d, const void* gates
 int atlas_window_sum(int dtype, int64_t n, int64_t t, int64_t d, int window, int reverse,
                      const void* x, void* y, void* stream);
 
-/* Right-affine scan H_t = H_{t-1} A_t + B_t over t = 1..T, fp32 (replaces
- * affine_associative_scan, atlas_pytorch/affine_scan.py:36-158): A [n,t,d,d], B [n,t,r,d],
- * prev = H_0 [n,r,d] (NULL: zero), out = H_1..H_T [n,t,r,d]; r, d <= 64. */
+/* Right-affine scan H_t = H_{t-1} A_t + B_t over t = 1..T, fp32 (replaces affine_associative_scan,
+ * atlas_pytorch/affine_scan.py:36-158): A [n,t,d,d], B [n,t,r,d], prev = H_0 [n,r,d] (NULL: zero),
+ * out = H_1..H_T [n,t,r,d]; r, d <= 64. Chunked on the fp32 matrix cores: the chunks' composed maps,
+ * a chain over chunks, then every chunk's states. `workspace` (atlas_affine_scan_workspace_bytes) is
+ * caller-owned scratch; pointers 4-byte aligned. */
 int atlas_affine_scan_fwd(int n, int t, int r, int d, const float* A, const float* B, const float* prev,
-                          float* out, void* stream);
+                          float* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Gradients of atlas_affine_scan_fwd given its output H (= out): dA [n,t,d,d], dB [n,t,r,d] and
- * dprev [n,r,d] (may be NULL) for the output gradient dout [n,t,r,d]. */
+ * dprev [n,r,d] (may be NULL) for the output gradient dout [n,t,r,d]. The adjoint is the same chunked
+ * scan run backwards over A^T; same workspace size as the forward. */
 int atlas_affine_scan_bwd(int n, int t, int r, int d, const float* A, const float* H, const float* prev,
-                          const float* dout, float* dA, float* dB, float* dprev, void* stream);
+                          const float* dout, float* dA, float* dB, float* dprev, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace the affine scan (either direction) needs; 0 for invalid sizes. */
+size_t atlas_affine_scan_workspace_bytes(int n, int t, int r, int d);
 
 /* Tensor polynomial feature map, fused (replaces the 'tensor' mode of PolynomialFeatureMap,
  * atlas_pytorch/rnn_memory.py:125-130, which materialises vec(x x^T) with einsum / cat / matmul):

@@ -123,6 +123,17 @@ def test_noalloc_backward_host_checks(lib):
     assert b"64 MiB" in lib.atlas_mem_strerror(_lib.ERR_SCRATCH)
 
 
+def test_affine_scan_host_checks(lib):
+    good = ctypes.c_void_p(0x10000)
+    assert lib.atlas_affine_scan_workspace_bytes(2, 1024, 64, 64) > 0
+    assert lib.atlas_affine_scan_workspace_bytes(2, 1024, 65, 64) == 0
+    assert lib.atlas_affine_scan_fwd(2, 16, 8, 8, good, good, None, good, None, 0, None) == 4       # no workspace
+    ws = lib.atlas_affine_scan_workspace_bytes(2, 16, 8, 8)
+    assert lib.atlas_affine_scan_fwd(2, 16, 8, 8, good, good, None, good, good, ws - 1, None) == 7  # too small
+    assert lib.atlas_affine_scan_fwd(2, 16, 8, 8, ctypes.c_void_p(0x10002), good, None, good, good, ws, None) == 5
+    assert lib.atlas_affine_scan_bwd(2, 16, 70, 8, good, good, None, good, good, good, None, good, ws, None) == 2
+
+
 def test_strerror(lib):
     for code in range(0, 11):
         assert len(lib.atlas_mem_strerror(code)) > 0

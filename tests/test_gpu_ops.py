@@ -134,6 +134,10 @@ def test_window_sum_parity(dt, window):
     (2, 33, 64, 64, True, True),
     (4, 1, 5, 7, False, False),
     (1, 129, 1, 64, True, False),
+    # chunks of 64 steps, 16 chunks: the compose / chain / apply passes at full tile size
+    (2, 1024, 64, 64, True, False),
+    # sizes off the 16-wide tiles, a ragged last chunk, no prev
+    (3, 301, 20, 50, False, False),
 ])
 def test_affine_scan_parity(N, T, R, D, with_prev, remove_prev):
     _say(f"affine scan N={N} T={T} R={R} D={D} prev={with_prev} remove_prev={remove_prev}")
