@@ -48,6 +48,11 @@ EXPORTED_SYMBOLS = (
     "atlas_affine_scan_workspace_bytes",
     "atlas_tensor_map_fwd",
     "atlas_tensor_map_bwd",
+    "atlas_prologue_num_workgroups",
+    "atlas_prologue_fwd",
+    "atlas_prologue_bwd",
+    "atlas_heads_fwd",
+    "atlas_heads_bwd",
     "atlas_mem_profile_enable",
     "atlas_mem_profile_read",
     "atlas_mem_kernel_name",
@@ -133,6 +138,17 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_tensor_map_fwd.argtypes = [i32, i64, i32, i32, i32, vp, vp, vp, vp, vp]
     lib.atlas_tensor_map_bwd.restype = i32
     lib.atlas_tensor_map_bwd.argtypes = [i32, i64, i32, i32, i32, vp, vp, vp, vp, vp, vp]
+    f32 = ctypes.c_float
+    lib.atlas_prologue_num_workgroups.restype = i32
+    lib.atlas_prologue_num_workgroups.argtypes = [i32, i32]
+    lib.atlas_prologue_fwd.restype = i32
+    lib.atlas_prologue_fwd.argtypes = [i32, i32, i32, i32, i32, f32] + [vp] * 11
+    lib.atlas_prologue_bwd.restype = i32
+    lib.atlas_prologue_bwd.argtypes = [i32, i32, i32, i32, i32] + [vp] * 14
+    lib.atlas_heads_fwd.restype = i32
+    lib.atlas_heads_fwd.argtypes = [i32] * 6 + [vp] * 12
+    lib.atlas_heads_bwd.restype = i32
+    lib.atlas_heads_bwd.argtypes = [i32] * 6 + [vp] * 17
     lib.atlas_mem_profile_enable.restype = i32
     lib.atlas_mem_profile_enable.argtypes = [i32]
     lib.atlas_mem_profile_read.restype = i32

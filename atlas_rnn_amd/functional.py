@@ -663,6 +663,166 @@ def affine_associative_scan(A: Tensor, B: Tensor, *, prev: Tensor | None = None,
 
 
 # ------------------------------------------------------------------------------------------
+# Cell prologue (rnn_memory.py:567-653): fused kernels around the projection GEMMs
+# ------------------------------------------------------------------------------------------
+
+def _dt_code(t: Tensor) -> int:
+    if t.dtype not in _DTYPES:
+        raise ValueError(f"the fused prologue takes fp32 or bf16 tensors, got {t.dtype}")
+    return _DTYPES[t.dtype]
+
+
+class _PrologueFn(torch.autograd.Function):
+    """xn = RMSNorm(x) and the three depthwise convolutions of xn (atlas_prologue_fwd / _bwd)."""
+
+    @staticmethod
+    def forward(ctx, x, norm_w, wq, wk, wv, conv_k, eps):
+        lib = _lib.load()
+        B, T, dim = x.shape
+        x = _aligned(x)
+        conv = conv_k > 1
+        xn = torch.empty_like(x)
+        qi = torch.empty_like(x) if conv else None
+        ki = torch.empty_like(x) if conv else None
+        vi = torch.empty_like(x) if conv else None
+        inv = torch.empty(B, T, device=x.device, dtype=torch.float32)
+        taps = [_aligned(w.reshape(dim, conv_k)) if conv else None for w in (wq, wk, wv)]
+        _lib.check(lib.atlas_prologue_fwd(_dt_code(x), B, T, dim, conv_k, float(eps), _ptr(x), _ptr(norm_w),
+                                          _ptr(taps[0]), _ptr(taps[1]), _ptr(taps[2]), _ptr(xn), _ptr(qi), _ptr(ki),
+                                          _ptr(vi), _ptr(inv), _stream(x.device)), "atlas_prologue_fwd")
+        ctx.save_for_backward(x, norm_w, *(t if t is not None else torch.empty(0) for t in taps), inv)
+        ctx.conv_k = conv_k
+        ctx.wshape = tuple(wq.shape) if conv else None
+        if not conv:
+            return xn          # the caller uses xn for q_in, k_in and v_in
+        return xn, qi, ki, vi
+
+    @staticmethod
+    def backward(ctx, dxn, *dconv):
+        lib = _lib.load()
+        x, norm_w, tq, tk, tv, inv = ctx.saved_tensors
+        B, T, dim = x.shape
+        K = ctx.conv_k
+        conv = K > 1
+        z = lambda t: torch.zeros_like(x) if t is None else _aligned(t.to(x.dtype))
+        dxn = z(dxn)
+        dqi, dki, dvi = (z(g) for g in dconv) if conv else (None, None, None)
+        nwg = lib.atlas_prologue_num_workgroups(B, T)
+        dx = torch.empty_like(x)
+        dnw = torch.empty(nwg, dim, device=x.device, dtype=torch.float32)
+        dcv = torch.empty(nwg, 3, dim, K, device=x.device, dtype=torch.float32) if conv else None
+        _lib.check(lib.atlas_prologue_bwd(_dt_code(x), B, T, dim, K, _ptr(x), _ptr(norm_w),
+                                          _ptr(tq if conv else None), _ptr(tk if conv else None),
+                                          _ptr(tv if conv else None), _ptr(inv), _ptr(dxn), _ptr(dqi), _ptr(dki),
+                                          _ptr(dvi), _ptr(dx), _ptr(dnw), _ptr(dcv), _stream(x.device)),
+                   "atlas_prologue_bwd")
+        dnorm = dnw.sum(dim=0).to(norm_w.dtype)
+        if not conv:
+            return dx, dnorm, None, None, None, None, None
+        dtaps = dcv.sum(dim=0).to(x.dtype)
+        return (dx, dnorm, dtaps[0].reshape(ctx.wshape), dtaps[1].reshape(ctx.wshape), dtaps[2].reshape(ctx.wshape),
+                None, None)
+
+
+class _HeadsFn(torch.autograd.Function):
+    """Head split, MultiheadRMSNorm of q / k and the gate sigmoids (atlas_heads_fwd / _bwd)."""
+
+    @staticmethod
+    def forward(ctx, ql, kl, vl, zl, q_gamma, k_gamma, bias, heads, d):
+        lib = _lib.load()
+        B, T, _ = ql.shape
+        nG = bias.numel() // heads if bias is not None else 0
+        dev = ql.device
+        ql, kl, vl = _aligned(ql), _aligned(kl), _aligned(vl)
+        zl = _aligned(zl) if nG else None
+        qg = _aligned(q_gamma.reshape(heads, d)) if q_gamma is not None else None
+        kg = _aligned(k_gamma.reshape(heads, d)) if k_gamma is not None else None
+        q = torch.empty(B * heads, T, d, device=dev, dtype=ql.dtype)
+        k = torch.empty_like(q)
+        v = torch.empty_like(q)
+        gates = torch.empty(nG, B * heads, T, device=dev, dtype=ql.dtype) if nG else None
+        _lib.check(lib.atlas_heads_fwd(_dt_code(ql), B, T, heads, d, nG, _ptr(ql), _ptr(kl), _ptr(vl), _ptr(zl),
+                                       _ptr(qg), _ptr(kg), _ptr(bias), _ptr(q), _ptr(k), _ptr(v), _ptr(gates),
+                                       _stream(dev)), "atlas_heads_fwd")
+        e0 = torch.empty(0, device=dev)
+        ctx.save_for_backward(ql, kl, qg if qg is not None else e0, kg if kg is not None else e0,
+                              gates if gates is not None else e0)
+        ctx.meta = (heads, d, nG, q_gamma is not None, None if q_gamma is None else tuple(q_gamma.shape),
+                    None if bias is None else bias.dtype)
+        if nG:
+            return (q, k, v, *gates.unbind(0))
+        return q, k, v
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv, *dgates):
+        lib = _lib.load()
+        ql, kl, qg, kg, gates = ctx.saved_tensors
+        heads, d, nG, norm, gshape, bdt = ctx.meta
+        B, T, _ = ql.shape
+        dev = ql.device
+        z = lambda t: torch.zeros(B * heads, T, d, device=dev, dtype=ql.dtype) if t is None else _aligned(t.to(ql.dtype))
+        dq, dk, dv = z(dq), z(dk), z(dv)
+        dg = None
+        if nG:
+            dg = torch.stack([g.to(ql.dtype) if g is not None else torch.zeros(B * heads, T, device=dev, dtype=ql.dtype)
+                              for g in dgates])
+        nwg = lib.atlas_prologue_num_workgroups(B, T)
+        dql, dkl, dvl = torch.empty_like(ql), torch.empty_like(kl), torch.empty_like(ql)
+        dzl = torch.empty(B, T, nG * heads, device=dev, dtype=ql.dtype) if nG else None
+        dqg = torch.empty(nwg, heads, d, device=dev, dtype=torch.float32) if norm else None
+        dkg = torch.empty_like(dqg) if norm else None
+        dbias = torch.empty(nwg, nG * heads, device=dev, dtype=torch.float32) if nG else None
+        _lib.check(lib.atlas_heads_bwd(_dt_code(ql), B, T, heads, d, nG, _ptr(ql), _ptr(kl),
+                                       _ptr(qg if norm else None), _ptr(kg if norm else None),
+                                       _ptr(gates if nG else None), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(dql),
+                                       _ptr(dkl), _ptr(dvl), _ptr(dzl), _ptr(dqg), _ptr(dkg), _ptr(dbias), _stream(dev)),
+                   "atlas_heads_bwd")
+        dqgam = dqg.sum(dim=0).reshape(gshape).to(qg.dtype) if norm else None
+        dkgam = dkg.sum(dim=0).reshape(gshape).to(kg.dtype) if norm else None
+        db = dbias.sum(dim=0).to(bdt) if nG else None
+        return dql, dkl, dvl, dzl, dqgam, dkgam, db, None, None
+
+
+def cell_prologue(x: Tensor, norm_weight: Tensor, eps: float, conv_weights, proj_weights, gate_weights, gate_biases,
+                  q_gamma: Tensor | None, k_gamma: Tensor | None, heads: int, dim_head: int):
+    """The memory cell's prologue (rnn_memory.py:567-653) on the fused kernels:
+
+        xn = RMSNorm(x);  q_in, k_in, v_in = depthwise convs of xn (or xn itself)
+        ql, kl, vl = q_in Wq^T, k_in Wk^T, v_in Wv^T;  zl = xn [W_g1; W_g2; ...]^T     (GEMMs, hipBLASLt)
+        q, k = MultiheadRMSNorm of the heads of ql, kl; v = the heads of vl;  gate_i = sigmoid(zl_i + b_i)
+
+    x [B, T, dim]; conv_weights (wq, wk, wv) [dim, 1, K] or None; proj_weights (Wq, Wk, Wv) [H d, dim];
+    gate_weights / gate_biases: lists of [H, dim] / [H] (the to_lr, to_decay, [to_momentum],
+    [to_omega_gate] heads); q_gamma, k_gamma [H, 1, d] or None (no q/k norm). Every tensor in x's
+    dtype (fp32 or bf16; parameters are cast). Returns (xn, q, k, v [(B H), T, d], [gate_i
+    [(B H), T]]), all differentiable."""
+    _require_gpu(x, norm_weight)
+    if x.dim() != 3:
+        raise ValueError(f"x must be [B, T, dim], got {tuple(x.shape)}")
+    dt = x.dtype
+    cast = lambda t: None if t is None else t.to(dt)
+    conv_k = 0
+    if conv_weights is not None:
+        conv_k = conv_weights[0].shape[-1]
+        if conv_k > 8:
+            raise ValueError("the fused prologue supports depthwise convolutions of up to 8 taps")
+    wq, wk, wv = (cast(w) for w in conv_weights) if conv_weights is not None else (None, None, None)
+    if conv_k > 1:
+        xn, qi, ki, vi = _PrologueFn.apply(x, norm_weight.to(dt).contiguous(), wq, wk, wv, conv_k, eps)
+    else:
+        xn = _PrologueFn.apply(x, norm_weight.to(dt).contiguous(), None, None, None, 0, eps)
+        qi = ki = vi = xn
+    F = torch.nn.functional
+    ql = F.linear(qi, cast(proj_weights[0]))
+    kl = F.linear(ki, cast(proj_weights[1]))
+    vl = F.linear(vi, cast(proj_weights[2]))
+    zl = F.linear(xn, torch.cat([cast(w) for w in gate_weights], dim=0)) if gate_weights else None
+    bias = torch.cat([cast(b) for b in gate_biases]).contiguous() if gate_weights else None
+    out = _HeadsFn.apply(ql, kl, vl, zl, cast(q_gamma), cast(k_gamma), bias, heads, dim_head)
+    return xn, out[0], out[1], out[2], list(out[3:])
+
+
+# ------------------------------------------------------------------------------------------
 # Preallocated plan: direct C-ABI calls for a fixed problem shape
 # ------------------------------------------------------------------------------------------
 

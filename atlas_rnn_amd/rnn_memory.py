@@ -10,12 +10,14 @@ reference, so checkpoints load with `load_state_dict` and callers switch by chan
 * `OmegaRNNMemoryCell`                                (rnn_memory.py:415-814)
 * `RNNMemory`, `OmegaRNNMemory`                       (rnn_memory.py:821-885)
 
-The prologue (pre-norm, depthwise convs, q/k/v projections, q/k norms, gate heads) stays in
-PyTorch as in the reference. The memory recurrence itself - delta, the gated window of outer
-products, the momentum and decay scans, the clamp, the retrieval and all their gradients - runs
-in libatlas_mem.so (`functional.memory_recurrence`) on ROCm tensors; on CPU tensors the cells
-raise, there is no CPU implementation of the recurrence in this package. The elementwise
-feature map is applied inside the kernels; the tensor map's projection stays a GEMM in PyTorch.
+The prologue runs in fused kernels around the projection GEMMs (`functional.cell_prologue`:
+pre-norm RMSNorm and the depthwise convs in one kernel; the head split, q/k MultiheadRMSNorm and
+the gate sigmoids in another; both with hand-written backwards). The memory recurrence itself -
+delta, the gated window of outer products, the momentum and decay scans, the clamp, the retrieval
+and all their gradients - runs in libatlas_mem.so (`functional.memory_recurrence`) on ROCm
+tensors; on CPU tensors the cells raise, there is no CPU implementation in this package. The
+elementwise feature map is applied inside the recurrence kernels, the tensor map in its own fused
+kernels.
 
 `scan_chunk_len` keeps the reference semantics (S_ref = the call-start state for every chunk,
 each chunk's end state clamped to +-100) through the kernels' clamp_every option.
@@ -34,8 +36,8 @@ from einops.layers.torch import Rearrange
 from torch import Tensor, nn
 from torch.nn import Conv1d, Linear, Module, Parameter
 
-from .functional import (AssocScan, AtlasOmegaFunction, check_cuda_availability, memory_recurrence,
-                         tensor_feature_map, window_sum)
+from .functional import (AssocScan, AtlasOmegaFunction, cell_prologue, check_cuda_availability,
+                         memory_recurrence, tensor_feature_map, window_sum)
 
 
 def exists(v):
@@ -177,44 +179,42 @@ class _CellBase(Module):
                               device=device, dtype=dtype)
         return RNNMemState(seq_index=0, S=S, Z=Z, omega_buffer=buf)
 
-    def _prologue(self, x: Tensor):
-        """Pre-norm, depthwise convs on the whole sequence (rnn_memory.py:267-277, 572-582)."""
-        x_act = self.activation(self.pre_norm(x))
-        q_in = k_in = v_in = x_act
-        if exists(self.q_conv):
-            q_in = self.q_conv(q_in.transpose(1, 2)).transpose(1, 2)
-        if exists(self.k_conv):
-            k_in = self.k_conv(k_in.transpose(1, 2)).transpose(1, 2)
-        if exists(self.v_conv):
-            v_in = self.v_conv(v_in.transpose(1, 2)).transpose(1, 2)
-        return x_act, q_in, k_in, v_in
+    def _gate_heads(self):
+        """The sigmoid gate heads in the order the fused prologue computes them."""
+        heads = [self.to_lr, self.to_decay]
+        if self.use_momentum:
+            heads.append(self.to_momentum)
+        if getattr(self, 'to_omega_gate', None) is not None:
+            heads.append(self.to_omega_gate)
+        return heads
 
-    def _heads(self, x_act, q_in, k_in, v_in):
-        """Projections, q/k norms and the feature map -> [BH, T, d] operands (rnn_memory.py:314-337)."""
-        batch, seq_len, _ = x_act.shape
-        q = self.split_heads(self.to_q(q_in))[:, :, :seq_len]
-        k = self.split_heads(self.to_k(k_in))[:, :, :seq_len]
-        v = self.split_heads(self.to_v(v_in))[:, :, :seq_len]
-        q = self.q_norm(q)
-        k = self.k_norm(k)
-        k = rearrange(k, 'b h n d -> (b h) n d')
-        q = rearrange(q, 'b h n d -> (b h) n d')
+    def _inputs(self, x: Tensor):
+        """Pre-norm, the depthwise convs, the projections, the q / k norms, the gate heads and the
+        feature map (rnn_memory.py:267-337, :572-653) -> the recurrence's operands
+        k, q, v [BH, T, d] and lr, decay, beta, omega gate [BH, T]. The norms, convs, head split
+        and gate sigmoids run in the fused prologue kernels (functional.cell_prologue); the
+        projections are GEMMs."""
+        heads = self._gate_heads()
+        convs = (self.q_conv.weight, self.k_conv.weight, self.v_conv.weight) if exists(self.q_conv) else None
+        qg = self.q_norm.gamma if isinstance(self.q_norm, MultiheadRMSNorm) else None
+        kg = self.k_norm.gamma if isinstance(self.k_norm, MultiheadRMSNorm) else None
+        eps = self.pre_norm.eps if self.pre_norm.eps is not None else torch.finfo(x.dtype).eps
+        _, q, k, v, gates = cell_prologue(
+            x, self.pre_norm.weight, eps, convs, (self.to_q.weight, self.to_k.weight, self.to_v.weight),
+            [h[0].weight for h in heads], [h[0].bias for h in heads], qg, kg, self.heads, self.dim_head)
         if not self.phi.fused_elementwise:
             k = self.phi(k)
             q = self.phi(q)
-        v = rearrange(v, 'b h n d -> (b h) n d')
-        lr = rearrange(self.to_lr(x_act), 'b n h -> (b h) n')
-        decay = rearrange(self.to_decay(x_act), 'b n h -> (b h) n')
-        beta = rearrange(self.to_momentum(x_act), 'b n h -> (b h) n') if self.use_momentum else None
-        return k, q, v, lr, decay, beta
+        lr, decay = gates[0], gates[1]
+        beta = gates[2] if self.use_momentum else None
+        gate = gates[-1] if getattr(self, 'to_omega_gate', None) is not None else None
+        return k, q, v, lr, decay, beta, gate
 
-    def _memory(self, x, state, window, gate_fn) -> tuple[Tensor, RNNMemState]:
+    def _memory(self, x, state, window) -> tuple[Tensor, RNNMemState]:
         batch, seq_len, _ = x.shape
         if not exists(state):
             state = self.init_state(batch, x.device, x.dtype)
-        x_act, q_in, k_in, v_in = self._prologue(x)
-        k, q, v, lr, decay, beta = self._heads(x_act, q_in, k_in, v_in)
-        gate = gate_fn(x_act)
+        k, q, v, lr, decay, beta, gate = self._inputs(x)
         S0 = state.S
         Z0 = state.Z if (self.use_momentum and exists(state.Z)) else None
         if self.use_momentum and Z0 is None:
@@ -251,7 +251,7 @@ class RNNMemoryCell(_CellBase):
                     use_accelerated_scan, scan_chunk_len, omega_window=1, use_omega_gate=None)
 
     def forward(self, x: Tensor, state: RNNMemState | None = None) -> tuple[Tensor, RNNMemState]:
-        return self._memory(x, state, 1, lambda x_act: None)
+        return self._memory(x, state, 1)
 
 
 class OmegaRNNMemoryCell(_CellBase):
@@ -289,15 +289,10 @@ class OmegaRNNMemoryCell(_CellBase):
         if self.use_cuda and self.cuda_available:
             self.assoc_scan = None
 
-    def _gate(self, x_act: Tensor) -> Tensor | None:
-        if not self.use_omega_gate:
-            return None
-        return rearrange(self.to_omega_gate(x_act), 'b n h -> (b h) n')
-
     def forward(self, x: Tensor, state: RNNMemState | None = None) -> tuple[Tensor, RNNMemState]:
         if self.use_cuda and self.cuda_available:
             return self._forward_cuda(x, state)
-        return self._memory(x, state, self.omega_window, self._gate)
+        return self._memory(x, state, self.omega_window)
 
     def _forward_cuda(self, x: Tensor, state: RNNMemState | None) -> tuple[Tensor, RNNMemState]:
         """rnn_memory.py:732-814, inside the scan_chunk_len loop of rnn_memory.py:584-601: every
@@ -307,14 +302,12 @@ class OmegaRNNMemoryCell(_CellBase):
         batch, seq_len, _ = x.shape
         if not exists(state):
             state = self.init_state(batch, x.device, x.dtype)
-        x_act, q_in, k_in, v_in = self._prologue(x)
-        k, q, v, lr, decay, beta = self._heads(x_act, q_in, k_in, v_in)
+        k, q, v, lr, decay, beta, gate = self._inputs(x)
         if self.phi.fused_elementwise:
             k = self.phi(k)
             q = self.phi(q)
         if beta is None:
             beta = torch.ones_like(lr)
-        gate = self._gate(x_act)
         if gate is None:
             gate = torch.ones_like(lr)
         BH, d = k.shape[0], self.dim_head

@@ -434,6 +434,119 @@ def run_affine(steps, warmup, n=32, t=1024, d=64, r=64, cpu=True):
     print(json.dumps(line), flush=True)
 
 
+def run_prologue(steps, warmup, B=8, T=2048, dim=512, heads=8, d=64, conv_k=4, n_gates=4):
+    """The cell prologue at C5's layer shape (B=8 T=2048 dim=512, 8 heads of 64, conv 4, four gate
+    heads), bf16: forward + backward of functional.cell_prologue (fused kernels + the projection
+    GEMMs), timed with HIP events on the stream; the same composition of unfused torch ops (the
+    reference's sequence) timed beside it. HBM roofline of the fused kernels alone: the prologue
+    kernel reads x and writes xn, q_in, k_in, v_in; the heads kernel reads ql, kl, vl and the gate
+    logits and writes q, k, v and the gates (forward), the backward moves twice as much."""
+    import torch
+    from atlas_rnn_amd.functional import cell_prologue
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator().manual_seed(1008)
+    bf = lambda t: t.to(dev, torch.bfloat16).requires_grad_()
+    r = lambda *sh: torch.randn(*sh, generator=g)
+    x = bf(r(B, T, dim))
+    p = dict(nw=bf(1 + 0.1 * r(dim)), wq=bf(0.5 * r(dim, 1, conv_k)), wk=bf(0.5 * r(dim, 1, conv_k)),
+             wv=bf(0.5 * r(dim, 1, conv_k)), Wq=bf(r(heads * d, dim) / dim ** 0.5), Wk=bf(r(heads * d, dim) / dim ** 0.5),
+             Wv=bf(r(heads * d, dim) / dim ** 0.5), qg=bf(torch.ones(heads, 1, d)), kg=bf(torch.ones(heads, 1, d)))
+    G = [bf(0.1 * r(heads, dim) / dim ** 0.5) for _ in range(n_gates)]
+    bias = [bf(r(heads)) for _ in range(n_gates)]
+    eps = torch.finfo(torch.bfloat16).eps
+    F = torch.nn.functional
+
+    def fused():
+        xn, q, k, v, gates = cell_prologue(x, p["nw"], eps, (p["wq"], p["wk"], p["wv"]), (p["Wq"], p["Wk"], p["Wv"]),
+                                           G, bias, p["qg"], p["kg"], heads, d)
+        return [q, k, v, *gates]
+
+    def unfused():   # rnn_memory.py:567-653 as torch ops
+        xn = F.rms_norm(x, (dim,), p["nw"], eps)
+        outs = []
+        for w, W, gam in (("wq", "Wq", "qg"), ("wk", "Wk", "kg"), ("wv", "Wv", None)):
+            xi = F.conv1d(xn.transpose(1, 2), p[w], padding=conv_k // 2, groups=dim).transpose(1, 2)
+            y = F.linear(xi, p[W]).reshape(B, T + 1, heads, d).permute(0, 2, 1, 3)[:, :, :T]
+            if gam:
+                y = y / (y.norm(dim=-1, keepdim=True) * d ** -0.5).clamp(min=1e-8) * p[gam]
+            outs.append(y.reshape(B * heads, T, d))
+        outs += [torch.sigmoid(F.linear(xn, G[i], bias[i])).permute(0, 2, 1).reshape(B * heads, T)
+                 for i in range(n_gates)]
+        return outs
+
+    leaves = [x, *p.values(), *G, *bias]
+    grads_out = None
+    us = {}
+    for name, fn in (("fused", fused), ("torch", unfused)):
+        def step():
+            outs = fn()
+            torch.autograd.grad(outs, leaves, grad_outputs=[torch.ones_like(o) for o in outs])
+        for _ in range(warmup):
+            step()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(steps):
+            step()
+        ev1.record()
+        torch.cuda.synchronize()
+        us[name] = 1e3 * ev0.elapsed_time(ev1) / steps
+    # the two forward kernels alone, on preallocated buffers (direct C-ABI calls)
+    import ctypes
+    from atlas_rnn_amd import _lib
+    from atlas_rnn_amd.functional import _ptr, _stream
+    lib = _lib.load()
+    st = _stream(dev)
+    xd = x.detach()
+    taps = [p[w].detach().reshape(dim, conv_k).contiguous() for w in ("wq", "wk", "wv")]
+    xn_, qi_, ki_, vi_ = (torch.empty_like(xd) for _ in range(4))
+    inv_ = torch.empty(B, T, device=dev)
+    ql_ = torch.empty(B, T, heads * d, device=dev, dtype=torch.bfloat16)
+    zl_ = torch.empty(B, T, n_gates * heads, device=dev, dtype=torch.bfloat16)
+    q_, k_, v_ = (torch.empty(B * heads, T, d, device=dev, dtype=torch.bfloat16) for _ in range(3))
+    gt_ = torch.empty(n_gates, B * heads, T, device=dev, dtype=torch.bfloat16)
+    bcat = torch.cat([b.detach() for b in bias])
+    calls = {
+        "k_pro_fwd": lambda: _lib.check(lib.atlas_prologue_fwd(
+            _lib.DT_BF16, B, T, dim, conv_k, eps, _ptr(xd), _ptr(p["nw"].detach()), _ptr(taps[0]), _ptr(taps[1]),
+            _ptr(taps[2]), _ptr(xn_), _ptr(qi_), _ptr(ki_), _ptr(vi_), _ptr(inv_), st), "atlas_prologue_fwd"),
+        "k_heads_fwd": lambda: _lib.check(lib.atlas_heads_fwd(
+            _lib.DT_BF16, B, T, heads, d, n_gates, _ptr(ql_), _ptr(ql_), _ptr(ql_), _ptr(zl_),
+            _ptr(p["qg"].detach()), _ptr(p["kg"].detach()), _ptr(bcat), _ptr(q_), _ptr(k_), _ptr(v_), _ptr(gt_), st),
+            "atlas_heads_fwd")}
+    kus = {}
+    for name, call in calls.items():
+        for _ in range(3):
+            call()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(steps):
+            call()
+        ev1.record()
+        torch.cuda.synchronize()
+        kus[name] = 1e3 * ev0.elapsed_time(ev1) / steps
+    n_tok = B * T
+    e = 2
+    kbytes = {"k_pro_fwd": n_tok * dim * e * 5 + n_tok * 4,
+              "k_heads_fwd": n_tok * heads * d * e * 6 + n_tok * heads * n_gates * e * 2}
+    kern_bytes_fwd = sum(kbytes.values())
+    line = {"metric": "cell-prologue tokens/s fwd+bwd (norms, convs, projections, head split, gates)",
+            "value": round(n_tok / (us["fused"] * 1e-6), 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": round(us["fused"] / 1e3, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded)",
+            "config": {"workload": f"memory-cell prologue at C5's layer shape: B={B} T={T} dim={dim} heads={heads} d={d} "
+                                   f"conv {conv_k} gate heads {n_gates}, bf16", "parallelism": "single GPU"},
+            "torch_unfused_ms_per_step": round(us["torch"] / 1e3, 4),
+            "speedup_vs_torch": round(us["torch"] / us["fused"], 2),
+            "kernels": {kk: {"avg_us": round(v, 2), "gbs": round(kbytes[kk] / (v * 1e-6) / 1e9, 1)} for kk, v in kus.items()}}
+    dom = max(kus, key=kus.get)
+    ach = kbytes[dom] / (kus[dom] * 1e-6) / 1e9
+    line["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                        "algorithmic_bytes_per_launch": kbytes[dom], "avg_launch_us": round(kus[dom], 2)}
+    print(json.dumps(line), flush=True)
+
+
 def run_decode(steps, warmup):
     """Generation steps at the C3 head shape (B=4 H=8 d=64 e=4 lag gates, momentum, bf16 inputs,
     fp32 state): atlas_mem_step through the C ABI with the state updated in place, the way a decode
@@ -588,7 +701,7 @@ def main():
                     help="tokens per row of the CPU baseline sample (default: 1024 c2/c3, 512 c5, 128 c4)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (HBM counter calibration)")
-    ap.add_argument("--config", choices=sorted(PLAN_CONFIGS) + ["c4", "decode", "affine"], default="c3",
+    ap.add_argument("--config", choices=sorted(PLAN_CONFIGS) + ["c4", "decode", "affine", "prologue"], default="c3",
                     help="c3 (default): the headline; c2 / c4 / c5: the other BASELINE configs; decode: the "
                          "one-token step")
     args = ap.parse_args()
@@ -602,6 +715,8 @@ def main():
     cpu = not args.no_cpu_baseline
     if args.config == "decode":
         run_decode(args.steps, args.warmup)
+    elif args.config == "prologue":
+        run_prologue(args.steps, args.warmup)
     elif args.config == "affine":
         run_affine(args.steps, args.warmup, cpu=cpu)
     elif args.config == "c4":

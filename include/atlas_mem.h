@@ -222,6 +222,50 @@ int atlas_tensor_map_fwd(int dtype, int64_t n, int d_in, int d_out, int degree, 
 int atlas_tensor_map_bwd(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x, const void* proj,
                          const void* pre, const void* dout, void* dx, void* stream);
 
+/* ---- cell prologue (atlas_pytorch/rnn_memory.py:567-653, MultiheadRMSNorm :139-147) --------
+ * Fused around the cell's projections, which stay plain GEMMs (hipBLASLt): dtype is ATLAS_DT_F32 or
+ * ATLAS_DT_BF16 for every tensor argument except inv_rms and the *_part partial sums (fp32).
+ * Parameter gradients come back as per-workgroup partials [atlas_prologue_num_workgroups, ...] that
+ * the caller sums over their first axis. */
+
+/* Workgroups of atlas_prologue_* / atlas_heads_* for (batch, seq_len): the first axis of every
+ * *_part buffer. */
+int atlas_prologue_num_workgroups(int batch, int seq_len);
+
+/* xn = RMSNorm(x) = x rsqrt(mean_c x^2 + eps) norm_w (nn.RMSNorm(dim), the cell's pre_norm) and, when
+ * conv_k > 1, the three depthwise convolutions over time of xn (Conv1d(dim, dim, conv_k, padding =
+ * conv_k / 2, groups = dim, bias = False) truncated to seq_len: q_in[t] = sum_j wq[c][j] xn[t + j - conv_k/2]).
+ * x, xn, q_in, k_in, v_in [batch, seq_len, dim]; norm_w [dim]; wq, wk, wv [dim][conv_k] (the conv
+ * weights [dim, 1, conv_k]); inv_rms [batch, seq_len] fp32 out (kept for the backward). conv_k <= 8;
+ * conv_k <= 1: no convolution (wq .. v_in unused). */
+int atlas_prologue_fwd(int dtype, int batch, int seq_len, int dim, int conv_k, float eps, const void* x,
+                       const void* norm_w, const void* wq, const void* wk, const void* wv, void* xn, void* q_in,
+                       void* k_in, void* v_in, float* inv_rms, void* stream);
+
+/* Adjoint of atlas_prologue_fwd: dxn (the gradient reaching xn directly) and dq_in / dk_in / dv_in
+ * -> dx, dnorm_w_part [nwg][dim] and dconv_part [nwg][3][dim][conv_k] (q, k, v taps). */
+int atlas_prologue_bwd(int dtype, int batch, int seq_len, int dim, int conv_k, const void* x, const void* norm_w,
+                       const void* wq, const void* wk, const void* wv, const float* inv_rms, const void* dxn,
+                       const void* dq_in, const void* dk_in, const void* dv_in, void* dx, float* dnorm_w_part,
+                       float* dconv_part, void* stream);
+
+/* The head split of the projections ql, kl, vl [batch, seq_len, heads * d] into [(batch heads), seq_len, d],
+ * MultiheadRMSNorm of q and k (x / max(|x| d^-1/2, 1e-8) * gamma[h]; q_gamma, k_gamma [heads][d], both
+ * NULL: no norm), and n_gates sigmoid gate heads from the logits zl [batch, seq_len, n_gates * heads]
+ * plus gate_bias [n_gates * heads] into gates [n_gates][(batch heads), seq_len]. d <= 128. */
+int atlas_heads_fwd(int dtype, int batch, int seq_len, int heads, int d, int n_gates, const void* ql, const void* kl,
+                    const void* vl, const void* zl, const void* q_gamma, const void* k_gamma, const void* gate_bias,
+                    void* q, void* k, void* v, void* gates, void* stream);
+
+/* Adjoint of atlas_heads_fwd given its gates: dq, dk, dv [(batch heads), seq_len, d], dgates
+ * [n_gates][(batch heads), seq_len] (NULL: zero) -> dql, dkl, dvl [batch, seq_len, heads * d],
+ * dzl [batch, seq_len, n_gates * heads], dq_gamma_part, dk_gamma_part [nwg][heads][d], dbias_part
+ * [nwg][n_gates * heads]. */
+int atlas_heads_bwd(int dtype, int batch, int seq_len, int heads, int d, int n_gates, const void* ql, const void* kl,
+                    const void* q_gamma, const void* k_gamma, const void* gates, const void* dq, const void* dk,
+                    const void* dv, const void* dgates, void* dql, void* dkl, void* dvl, void* dzl,
+                    float* dq_gamma_part, float* dk_gamma_part, float* dbias_part, void* stream);
+
 /* ---- diagnostics (no reference counterpart) ------------------------------------------------ */
 
 /* Number of kernels the timing hooks distinguish (index -> atlas_mem_kernel_name). */

@@ -1,0 +1,99 @@
+"""GPU parity of the fused cell prologue (functional.cell_prologue: atlas_prologue_* and atlas_heads_*
+kernels around the projection GEMMs) against the reference's op sequence (rnn_memory.py:567-653:
+nn.RMSNorm pre-norm, non-causal depthwise Conv1d truncated to T, Linear projections, head split,
+MultiheadRMSNorm :139-147, Linear + Sigmoid gate heads) composed in float64 on the CPU with torch's
+own layers. Outputs and the gradients of x and of every parameter; fp32 rtol 1e-4, bf16 rtol 2e-2
+(normwise and elementwise, tests/_cases.compare)."""
+
+import sys
+
+import pytest
+import torch
+from einops import rearrange
+
+from _cases import compare
+from atlas_rnn_amd.functional import cell_prologue
+
+pytestmark = pytest.mark.gpu
+
+F64 = torch.float64
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _reference(x, p, conv_k, heads, d, eps, n_gates, qk_norm):
+    """rnn_memory.py:567-653 with torch layers' functional forms, float64."""
+    F = torch.nn.functional
+    B, T, dim = x.shape
+    xn = F.rms_norm(x, (dim,), p["norm_w"], eps)
+    if conv_k > 1:
+        pad = conv_k // 2
+        ins = [F.conv1d(xn.transpose(1, 2), p[w], padding=pad, groups=dim).transpose(1, 2)
+               for w in ("wq", "wk", "wv")]
+    else:
+        ins = [xn, xn, xn]
+    outs = []
+    for w, xin, gam in zip(("Wq", "Wk", "Wv"), ins, ("qg", "kg", None)):
+        y = rearrange(F.linear(xin, p[w]), 'b n (h d) -> b h n d', h=heads)[:, :, :T]
+        if gam is not None and qk_norm:
+            rms = y.norm(dim=-1, keepdim=True) * d ** -0.5
+            y = (y / rms.clamp(min=1e-8)) * p[gam]
+        outs.append(rearrange(y, 'b h n d -> (b h) n d'))
+    gates = [rearrange(torch.sigmoid(F.linear(xn, p[f"G{i}"], p[f"b{i}"])), 'b n h -> (b h) n') for i in range(n_gates)]
+    return [xn, *outs, *gates]
+
+
+CASES = [
+    # (name, B, T, dim, heads, d, conv_k, n_gates, qk_norm, dtype)
+    ("fp32_k4_mom_gate", 2, 70, 64, 2, 32, 4, 4, True, torch.float32),
+    ("fp32_k3_nomom", 2, 33, 48, 3, 16, 3, 2, True, torch.float32),
+    ("fp32_noconv_nonorm", 3, 17, 32, 1, 32, 0, 3, False, torch.float32),
+    ("fp32_d128_k2", 1, 40, 64, 2, 128, 2, 2, True, torch.float32),
+    ("bf16_k4_c5_head", 2, 50, 512, 8, 64, 4, 4, True, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_cell_prologue_parity(case):
+    name, B, T, dim, heads, d, conv_k, n_gates, qk_norm, dt = case
+    _say(f"prologue {name}")
+    g = torch.Generator().manual_seed(sum(map(ord, name)))
+    r = lambda *s: torch.randn(*s, generator=g)
+    p = {"norm_w": 1 + 0.1 * r(dim), "Wq": r(heads * d, dim) / dim ** 0.5, "Wk": r(heads * d, dim) / dim ** 0.5,
+         "Wv": r(heads * d, dim) / dim ** 0.5, "qg": 1 + 0.1 * r(heads, 1, d), "kg": 1 + 0.1 * r(heads, 1, d)}
+    if conv_k > 1:
+        for w in ("wq", "wk", "wv"):
+            p[w] = 0.5 * r(dim, 1, conv_k)
+    for i in range(n_gates):
+        p[f"G{i}"] = 0.2 * r(heads, dim) / dim ** 0.5
+        p[f"b{i}"] = r(heads)
+    x = r(B, T, dim)
+    p = {k: v.to(dt).float() for k, v in p.items()}
+    x = x.to(dt).float()
+    eps = torch.finfo(dt).eps
+    pr = {k: v.to(F64).requires_grad_() for k, v in p.items()}
+    xr = x.to(F64).requires_grad_()
+    ref = _reference(xr, pr, conv_k, heads, d, eps, n_gates, qk_norm)
+    pd = {k: v.to("cuda", dt).requires_grad_() for k, v in p.items()}
+    xd = x.to("cuda", dt).requires_grad_()
+    xn, q, k, v, gates = cell_prologue(
+        xd, pd["norm_w"], eps, (pd["wq"], pd["wk"], pd["wv"]) if conv_k > 1 else None, (pd["Wq"], pd["Wk"], pd["Wv"]),
+        [pd[f"G{i}"] for i in range(n_gates)], [pd[f"b{i}"] for i in range(n_gates)],
+        pd["qg"] if qk_norm else None, pd["kg"] if qk_norm else None, heads, d)
+    got = [xn, q, k, v, *gates]
+    wts = [torch.randn(t.shape, generator=g, dtype=F64) for t in ref]
+    names = ["x"] + [kk for kk in p if (kk not in ("qg", "kg") or qk_norm)]
+    lr_ = sum((t * w).sum() for t, w in zip(ref, wts))
+    ld_ = sum((t.float() * w.to("cuda", torch.float32)).sum() for t, w in zip(got, wts))
+    gr = torch.autograd.grad(lr_, [xr] + [pr[kk] for kk in names[1:]])
+    gd = torch.autograd.grad(ld_, [xd] + [pd[kk] for kk in names[1:]])
+    torch.cuda.synchronize()
+    tol = 1e-4 if dt == torch.float32 else 2e-2
+    for nm, a, b in zip(["xn", "q", "k", "v"] + [f"gate{i}" for i in range(n_gates)], got, ref):
+        assert a.shape == b.shape, nm
+        compare(f"{name}.{nm}", a.detach().float().cpu(), b.detach(), tol)
+    for nm, a, b in zip(names, gd, gr):
+        compare(f"{name}.d{nm}", a.float().cpu(), b, tol)
