@@ -1,6 +1,7 @@
 // abi.hip - extern "C" entry points of libatlas_mem.so (declared in include/atlas_mem.h).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -133,6 +134,10 @@ struct Plan {
   int esize;   // bytes per input element
   bool ok;
   int status;
+  // scan_chunk_len clamps at chunk ends: the segment-parallel sequence (this plan, unclamped, checking
+  // the clamp points) runs first and the exact one-segment-per-row sequence (make_plan(p, true))
+  // runs behind it only when some clamp point's |S| exceeds 100 (the clamp is the identity otherwise)
+  bool dual;
 };
 
 // Segments per head-batch row: enough (segment, bh) workgroups for one per CU (the walks hold a
@@ -171,7 +176,7 @@ int largest_divisor_at_most(int n, int cap) {
   return 1;
 }
 
-Plan make_plan(const atlas_mem_problem* p) {
+Plan make_plan(const atlas_mem_problem* p, bool serial_clamp = false) {
   Plan pl{};
   pl.ok = false;
   pl.status = ATLAS_MEM_ERR_ARG;
@@ -207,6 +212,10 @@ Plan make_plan(const atlas_mem_problem* p) {
   g.momentum = p->momentum; g.gate_mode = p->gate_mode; g.map_mode = p->map_mode;
   g.map_deg = p->map_mode == ATLAS_MAP_ELEMENTWISE ? p->map_degree : 1;
   g.has_buf = p->has_buffer; g.clamp_every = p->clamp_every; g.clamp_final = p->clamp_final;
+  g.flag = nullptr; g.flag_run = -1; g.flag_reset = 0; g.clamp_check = 0;
+  // clamp points on forward-chunk ends: segment-parallel with the clamp points checked (dual)
+  pl.dual = !serial_clamp && p->clamp_every > 0 && p->clamp_every % CH == 0 && p->clamp_every < p->seq_len;
+  if (pl.dual) g.clamp_every = 0;
   pl.sg = make_seg(g);
   // backward: same segments, chunks of Lb
   Geom& gb = pl.gb;
@@ -278,6 +287,37 @@ BwdLayout bwd_layout(const Plan& pl) {
   L.scal = off; off += align256((size_t)g.BH * g.nc * scalar_block_floats(pl.CHB) * sizeof(float));
   L.total = off;
   return L;
+}
+
+// `saved` of a dual plan: the flag (256 bytes), then the segment-parallel sequence's layout, then the
+// exact sequence's.
+struct DualLayout {
+  size_t fast, exact, total;
+};
+DualLayout dual_layout(const Plan& fast, const Plan& exact) {
+  DualLayout D{};
+  D.fast = 256;
+  D.exact = D.fast + saved_layout(fast).total;
+  D.total = D.exact + saved_layout(exact).total;
+  return D;
+}
+
+size_t saved_bytes(const atlas_mem_problem* p, const Plan& pl) {
+  if (!pl.dual) return saved_layout(pl).total;
+  return dual_layout(pl, make_plan(p, true)).total;
+}
+size_t bwd_ws_bytes(const atlas_mem_problem* p, const Plan& pl) {
+  if (!pl.dual) return bwd_layout(pl).total;
+  return std::max(bwd_layout(pl).total, bwd_layout(make_plan(p, true)).total);
+}
+
+// The two sequences of a dual plan, flag-selected: the fast one always runs in the forward (and
+// clears / sets the flag), the exact one only when the flag is set; the backward runs the one the
+// forward's flag selected.
+void set_flag(Plan& pl, const int* flag, int run, int reset, int check) {
+  for (Geom* g : {&pl.g, &pl.gb}) {
+    g->flag = flag; g->flag_run = run; g->flag_reset = reset; g->clamp_check = check;
+  }
 }
 
 bool misaligned(const void* p, size_t a) { return p && (reinterpret_cast<uintptr_t>(p) % a) != 0; }
@@ -368,6 +408,24 @@ int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, voi
 int check_bwd_args(const atlas_mem_problem& p, const atlas_mem_bwd_args* args, const float* saved,
                    const void* workspace);
 
+// The backward of a plan (of both flag-selected sequences for a dual plan).
+int run_bwd_plan(const atlas_mem_problem* prob, const Plan& pl, const atlas_mem_bwd_args* args, const float* saved,
+                 void* ws, hipStream_t s) {
+  auto one = [&](const Plan& q, const float* sv) {
+    return prob->dtype == ATLAS_DT_BF16 ? run_bwd<bf16>(q, args, sv, ws, s) : run_bwd<float>(q, args, sv, ws, s);
+  };
+  if (!pl.dual) return one(pl, saved);
+  Plan fast = pl, exact = make_plan(prob, true);
+  const unsigned char* sv = reinterpret_cast<const unsigned char*>(saved);
+  const DualLayout D = dual_layout(fast, exact);
+  const int* flag = reinterpret_cast<const int*>(sv);
+  set_flag(fast, flag, 0, 0, 0);
+  set_flag(exact, flag, 1, 0, 0);
+  const int st = one(fast, reinterpret_cast<const float*>(sv + D.fast));
+  if (st != ATLAS_MEM_OK) return st;
+  return one(exact, reinterpret_cast<const float*>(sv + D.exact));
+}
+
 // Scratch of atlas_mem_bwd_noalloc: the backward workspace as a file-scope device array (each GPU
 // holds its own copy for the life of the process). In host code `scratch` names a host-side
 // stand-in, never the device memory: its per-device address comes from hipGetSymbolAddress, looked
@@ -421,13 +479,13 @@ int atlas_mem_validate(const atlas_mem_problem* prob) { return make_plan(prob).s
 size_t atlas_mem_saved_bytes(const atlas_mem_problem* prob) {
   const Plan pl = make_plan(prob);
   if (!pl.ok) return 0;
-  return saved_layout(pl).total;
+  return saved_bytes(prob, pl);
 }
 
 size_t atlas_mem_bwd_workspace_bytes(const atlas_mem_problem* prob) {
   const Plan pl = make_plan(prob);
   if (!pl.ok) return 0;
-  return bwd_layout(pl).total;
+  return bwd_ws_bytes(prob, pl);
 }
 
 int atlas_mem_fwd(const atlas_mem_problem* prob, const atlas_mem_fwd_args* args, float* saved, void* stream) {
@@ -449,7 +507,19 @@ int atlas_mem_fwd(const atlas_mem_problem* prob, const atlas_mem_fwd_args* args,
   const void* fp[] = {args->S_ref, args->S0, args->Z0, args->buffer_in, args->S_T, args->Z_T, args->buffer_out, saved};
   for (const void* q : fp) if (misaligned(q, 16)) return ATLAS_MEM_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return p.dtype == ATLAS_DT_BF16 ? run_fwd<bf16>(pl, args, saved, s) : run_fwd<float>(pl, args, saved, s);
+  auto one = [&](const Plan& q, float* sv) {
+    return p.dtype == ATLAS_DT_BF16 ? run_fwd<bf16>(q, args, sv, s) : run_fwd<float>(q, args, sv, s);
+  };
+  if (!pl.dual) return one(pl, saved);
+  Plan fast = pl, exact = make_plan(prob, true);
+  unsigned char* sv = reinterpret_cast<unsigned char*>(saved);
+  const DualLayout D = dual_layout(fast, exact);
+  const int* flag = reinterpret_cast<const int*>(sv);
+  set_flag(fast, flag, -1, 1, p.clamp_every);
+  set_flag(exact, flag, 1, 0, 0);
+  const int st = one(fast, reinterpret_cast<float*>(sv + D.fast));
+  if (st != ATLAS_MEM_OK) return st;
+  return one(exact, reinterpret_cast<float*>(sv + D.exact));
 }
 
 int atlas_mem_bwd(const atlas_mem_problem* prob, const atlas_mem_bwd_args* args, const float* saved,
@@ -457,12 +527,10 @@ int atlas_mem_bwd(const atlas_mem_problem* prob, const atlas_mem_bwd_args* args,
   const Plan pl = make_plan(prob);
   if (!pl.ok) return pl.status;
   if (!args || !saved || !workspace) return ATLAS_MEM_ERR_NULL;
-  if (workspace_bytes < bwd_layout(pl).total) return ATLAS_MEM_ERR_WORKSPACE;
+  if (workspace_bytes < bwd_ws_bytes(prob, pl)) return ATLAS_MEM_ERR_WORKSPACE;
   const int st = check_bwd_args(*prob, args, saved, workspace);
   if (st != ATLAS_MEM_OK) return st;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  return prob->dtype == ATLAS_DT_BF16 ? run_bwd<bf16>(pl, args, saved, workspace, s)
-                                      : run_bwd<float>(pl, args, saved, workspace, s);
+  return run_bwd_plan(prob, pl, args, saved, workspace, static_cast<hipStream_t>(stream));
 }
 
 int atlas_mem_bwd_noalloc(const atlas_mem_problem* prob, const atlas_mem_bwd_args* args, const float* saved,
@@ -470,14 +538,13 @@ int atlas_mem_bwd_noalloc(const atlas_mem_problem* prob, const atlas_mem_bwd_arg
   const Plan pl = make_plan(prob);
   if (!pl.ok) return pl.status;
   if (!args || !saved) return ATLAS_MEM_ERR_NULL;
-  if (bwd_layout(pl).total > kNoAllocScratchBytes) return ATLAS_MEM_ERR_SCRATCH;
+  if (bwd_ws_bytes(prob, pl) > kNoAllocScratchBytes) return ATLAS_MEM_ERR_SCRATCH;
   void* ws = nullptr;
   const int ss = scratch_on_current_device(&ws);
   if (ss != ATLAS_MEM_OK) return ss;
   const int st = check_bwd_args(*prob, args, saved, ws);
   if (st != ATLAS_MEM_OK) return st;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  return prob->dtype == ATLAS_DT_BF16 ? run_bwd<bf16>(pl, args, saved, ws, s) : run_bwd<float>(pl, args, saved, ws, s);
+  return run_bwd_plan(prob, pl, args, saved, ws, static_cast<hipStream_t>(stream));
 }
 
 size_t atlas_mem_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }

@@ -61,6 +61,7 @@ __device__ __forceinline__ f32x4 tile_gemm_f32(const float* a, int lda, const fl
 template <typename T, int CH>
 __global__ __launch_bounds__(kScalarThreads) void k_bwd_scalar(const Geom g, const BwdPtrs<T> a,
                                                                  const BwdSegPtrs p) {
+  if (geom_skip(g)) return;
   typedef BwdScalarSmem<CH> Sm;
   typedef ScalarBlock<CH> SB;
   constexpr int SPM = Sm::SPM, LWR = Sm::LWR;

@@ -309,6 +309,8 @@ __global__ __launch_bounds__(coef_threads<CHF>()) void k_chunk_coef_pair(
     const Geom gf, const Geom gb, const T* __restrict__ decay, const T* __restrict__ lr, const T* __restrict__ beta,
     const T* __restrict__ gate, float* __restrict__ rec_f, T* __restrict__ wsh_f, float* __restrict__ rec_b,
     T* __restrict__ wsh_b, int halves) {
+  if (geom_skip(gf)) return;
+  if (gf.flag_reset && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *const_cast<int*>(gf.flag) = 0;
   constexpr int NTB = coef_threads<CHB>(), PER = coef_threads<CHF>() / NTB;
   static_assert(coef_threads<CHF>() % NTB == 0, "backward groups per workgroup");
   __shared__ union U {

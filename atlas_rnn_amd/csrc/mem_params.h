@@ -24,7 +24,29 @@ struct Geom {
   int ncb;          // forward walk: number of backward chunks (rows of the saved chunk-start states)
   int nc;           // number of chunks = ceil(T / Lc)
   int momentum, gate_mode, map_mode, map_deg, has_buf, clamp_every, clamp_final;
+  // Two launch sequences for one call (scan_chunk_len clamps, see abi.hip): `flag` (device int)
+  // selects which one runs. flag_run -1: always run; 0: run only while *flag == 0; 1: only when set.
+  // flag_reset: the launch clears *flag first (workgroup 0). clamp_check > 0: set *flag when the
+  // unclamped S exceeds 100 in magnitude at a clamp point (every clamp_check tokens, not the last).
+  const int* flag;
+  int flag_run, flag_reset, clamp_check;
 };
+
+// Early exit of a launch whose sequence is not the one the flag selected (a wave-uniform read).
+__device__ __forceinline__ bool geom_skip(const Geom& g) {
+  if (g.flag_run < 0) return false;
+  const int f = *reinterpret_cast<const volatile int*>(g.flag);
+  return (f != 0) != (g.flag_run != 0);
+}
+
+// The clamp check of the segment-parallel sequence: t1 is a chunk end (the state after token
+// t1 - 1); any owned |S| > 100 there means the clamp would change S, so the exact sequence runs.
+__device__ __forceinline__ bool clamp_point(const Geom& g, int t1) {
+  return g.clamp_check > 0 && t1 < g.T && (t1 % g.clamp_check) == 0;
+}
+__device__ __forceinline__ void flag_if_clamped(const Geom& g, bool over) {
+  if (over) atomicOr(const_cast<int*>(g.flag), 1);
+}
 
 // The end of chunk c (token t1 - 1) is a clamp point inside the sequence.
 __host__ __device__ inline bool clamp_after(const Geom& g, int t1) {

@@ -119,6 +119,7 @@ struct BwdAggPrefetch
 template <typename T, int CH, int D>
 __global__ __launch_bounds__(kSegThreads) void k_bwd_seg_agg(const Geom g, const BwdPtrs<T> a, const SegGeom sg,
                                                                const BwdSegPtrs p) {
+  if (geom_skip(g)) return;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   typedef BwdAggSmem<T, CH, D> Sm;
   Sm& sm = *reinterpret_cast<Sm*>(smem_raw);
@@ -337,6 +338,7 @@ struct BwdPrefetch {
 template <typename T, int CH, int D>
 __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const BwdPtrs<T> a, const SegGeom sg,
                                                            const BwdSegPtrs p) {
+  if (geom_skip(g)) return;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   typedef BwdSegSmem<T, CH, D> Sm;
   constexpr int SPM = Sm::SPM;
@@ -830,6 +832,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg(const Geom g, const Bwd
 template <int D>
 __global__ __launch_bounds__(kThreads) void k_bwd_seg_scan(const Geom g, const float* dS_T, const float* dZ_T,
                                                              const SegGeom sg, const BwdSegPtrs p) {
+  if (geom_skip(g)) return;
   const int bh = blockIdx.y;
   const int idx = blockIdx.x * kThreads + threadIdx.x;
   if (idx >= D * D) return;
@@ -870,12 +873,15 @@ __global__ __launch_bounds__(kThreads) void k_bwd_seg_scan(const Geom g, const f
 template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void k_bwd_seg_fixup(const Geom g, const BwdPtrs<T> a, const SegGeom sg,
                                                               const BwdSegPtrs p, int reduce_dsref) {
+  if (geom_skip(g)) return;
   if (a.dbuf_out) bwd_seg_fixup<T, D, true>(g, a, sg, p, reduce_dsref, blockIdx.x, blockIdx.y);
   else bwd_seg_fixup<T, D, false>(g, a, sg, p, reduce_dsref, blockIdx.x, blockIdx.y);
 }
 
 // dS_ref = sum over segments of the partials.   grid (D*D/256, BH)
-__global__ __launch_bounds__(kThreads) void k_seg_reduce_dsref(int nseg, int n, const float* part, float* out) {
+__global__ __launch_bounds__(kThreads) void k_seg_reduce_dsref(const Geom g, int nseg, int n, const float* part,
+                                                                float* out) {
+  if (geom_skip(g)) return;
   const int bh = blockIdx.y;
   const int idx = blockIdx.x * kThreads + threadIdx.x;
   if (idx >= n) return;
@@ -977,7 +983,7 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
   if (fused_reduce) return hipSuccess;
   prof_begin(KID_REDUCE_DSREF, stream);
   hipLaunchKernelGGL(k_seg_reduce_dsref, dim3((D * D + kThreads - 1) / kThreads, g.BH), dim3(kThreads), 0, stream,
-                     sg.nseg, D * D, (const float*)p.dsref_part, a.dS_ref);
+                     g, sg.nseg, D * D, (const float*)p.dsref_part, a.dS_ref);
   prof_end(KID_REDUCE_DSREF, stream);
   return hipGetLastError();
 }

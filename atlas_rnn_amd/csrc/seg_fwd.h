@@ -458,6 +458,14 @@ __device__ __forceinline__ void fwd_segment(const Geom& g, const FwdPtrs<T>& a, 
           Zr[jn][r] = Zn;
         }
       }
+      if (FULL && clamp_point(g, t1)) {
+        bool over = false;
+#pragma unroll
+        for (int jn = 0; jn < NOWN; ++jn)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) over |= fabsf(Sr[jn][r]) > 100.f;
+        flag_if_clamped(g, over);
+      }
       if constexpr (AGG) {
         const float na = a_end * seg_a;
         const float nk = a_end * seg_k + k_end * seg_b;

@@ -36,6 +36,7 @@ namespace atlas {
 template <typename T, int CH, int D>
 __global__ __launch_bounds__(kSegThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_fwd_seg_agg(const Geom g, const FwdPtrs<T> a, const SegGeom sg,
                                                                float* agg, const float* coef) {
+  if (geom_skip(g)) return;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   fwd_segment<T, CH, D, WALK_AGG>(g, a, sg, agg, nullptr, nullptr, nullptr, coef, nullptr, smem_raw);
 }
@@ -48,6 +49,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void k_fwd_seg_scan(const Geom g, const float* S0, const float* Z0,
                                                              const SegGeom sg, const float* agg, float* seg_states,
                                                              const FwdPtrs<T> a, int nscan) {
+  if (geom_skip(g)) return;
   const int bh = blockIdx.y;
   if ((int)blockIdx.x >= nscan) {   // workgroup-uniform
     buffer_out_slot<T, D, D>(g, a, blockIdx.x - nscan, bh);
@@ -101,6 +103,7 @@ template <typename T, int CH, int D>
 __global__ __launch_bounds__(kSegThreads) void k_fwd_seg(const Geom g, const FwdPtrs<T> a, const SegGeom sg,
                                                            const float* seg_states, float* rw, float* final_raw,
                                                            const float* coef, const T* wsh) {
+  if (geom_skip(g)) return;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   fwd_segment<T, CH, D, WALK_FULL>(g, a, sg, nullptr, seg_states, rw, final_raw, coef, wsh, smem_raw);
 }

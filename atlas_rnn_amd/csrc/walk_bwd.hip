@@ -84,6 +84,7 @@ template <bool MAPE>
 __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const BwdPtrs<bf16> a, const SegGeom sg,
                                                             const BwdSegPtrs p) {
   using namespace wb;
+  if (geom_skip(g)) return;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   Smem& sm = *reinterpret_cast<Smem*>(smem_raw);
   const int tid = threadIdx.x, lane = lane_id();
@@ -681,6 +682,7 @@ __global__ __launch_bounds__(64 * wb::kChainWaves) void k_scalar_chain(const Geo
                                                                          const BwdSegPtrs p, const SegGeom sg,
                                                                          int nchain) {
   using namespace wb;
+  if (geom_skip(g)) return;
   if ((int)blockIdx.x >= nchain) {   // workgroup-uniform
     bwd_seg_fixup<bf16, D, false>(g, a, sg, p, 1, blockIdx.x - nchain, blockIdx.y);
     return;

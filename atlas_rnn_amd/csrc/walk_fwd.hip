@@ -409,6 +409,16 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
         }
       }
       if constexpr (FULL) {
+        if (clamp_point(g, t0 + L)) {
+          bool over = false;
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) over |= fabsf(Sr[j][r]) > 100.f;
+          flag_if_clamped(g, over);
+        }
+      }
+      if constexpr (FULL) {
         if (c + 1 < c_end) save_state((c + 1) * rb, Sr, Zr);
       }
       if constexpr (!FULL) {
@@ -459,6 +469,7 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
 template <bool MAPE>
 __global__ __launch_bounds__(kSegThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_walk_agg(
     const Geom g, const FwdPtrs<bf16> a, const SegGeom sg, float* agg, const float* coef) {
+  if (geom_skip(g)) return;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   walk_fwd<false, MAPE>(g, a, sg, agg, nullptr, nullptr, nullptr, coef, nullptr, smem_raw);
 }
@@ -467,6 +478,7 @@ template <bool MAPE>
 __global__ __launch_bounds__(kSegThreads) void k_walk_full(const Geom g, const FwdPtrs<bf16> a, const SegGeom sg,
                                                              const float* seg_states, float* rw, float* final_raw,
                                                              const float* coef, const bf16* wsh) {
+  if (geom_skip(g)) return;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   walk_fwd<true, MAPE>(g, a, sg, nullptr, seg_states, rw, final_raw, coef, wsh, smem_raw);
 }

@@ -606,7 +606,7 @@ def run_decode(steps, warmup):
     print(json.dumps(out), flush=True)
 
 
-def bench_plan(name, steps, warmup, cpu=True, cpu_sample_t=256):
+def bench_plan(name, steps, warmup, cpu=True, cpu_sample_t=256, with_buffer=False, clamp_every=None):
     """fwd+bwd of PLAN_CONFIGS[name] through the preplanned native path: K plain steps timed
     (value, ms_per_step); the same K steps again with the library's HIP events around every launch
     on its stream (per-kernel durations for the roofline); then the CPU oracle on a sample."""
@@ -617,10 +617,13 @@ def bench_plan(name, steps, warmup, cpu=True, cpu_sample_t=256):
     torch.cuda.set_device(dev)
     bh, t, d, e = cfg["B"] * cfg["H"], cfg["T"], cfg["d"], cfg["e"]
     x, x_cpu = make_inputs(dev, cfg)
-    plan = RecurrencePlan(bh, t, d, window=e, momentum=True, gate_mode=cfg["gate"], dtype=torch.bfloat16, device=dev)
+    buf = torch.zeros(bh, e - 1, d, d, device=dev) if (with_buffer and e > 1) else None
+    plan = RecurrencePlan(bh, t, d, window=e, momentum=True, gate_mode=cfg["gate"], dtype=torch.bfloat16, device=dev,
+                          has_buffer=buf is not None, clamp_every=clamp_every)
 
     def step():
-        plan.forward(x["k"], x["q"], x["v"], x["lr"], x["decay"], x["beta"], x["gate"], x["S_ref"], x["S0"], x["Z0"])
+        plan.forward(x["k"], x["q"], x["v"], x["lr"], x["decay"], x["beta"], x["gate"], x["S_ref"], x["S0"], x["Z0"],
+                     buf)
         plan.backward(x["dy"])
 
     for _ in range(warmup):
@@ -676,8 +679,10 @@ def bench_plan(name, steps, warmup, cpu=True, cpu_sample_t=256):
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) q/k/v with L2-normalised keys, sigmoid gates"
                 + (", softmax lag gates)" if cfg["gate"] == "lag" else ")"),
-        "config": {"workload": cfg["workload"], "global_batch": cfg["B"], "seq_len": t,
-                   "heads": cfg["H"], "d": d, "window": e, "parallelism": "single GPU"},
+        "config": {"workload": cfg["workload"] + (", carried (zero) buffer" if buf is not None else "")
+                   + (f", S clamped every {clamp_every} tokens (scan_chunk_len)" if clamp_every else ""),
+                   "global_batch": cfg["B"], "seq_len": t, "heads": cfg["H"], "d": d, "window": e,
+                   "parallelism": "single GPU"},
         "roofline": roofline,
         "step_roofline": {"bytes_per_step": step_bytes, "achieved_gbs": round(step_gbs, 2),
                           "frac": round(step_gbs / HBM_PEAK_GBS, 5)},
@@ -699,6 +704,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-tokens", type=int, default=None,
                     help="tokens per row of the CPU baseline sample (default: 1024 c2/c3, 512 c5, 128 c4)")
+    ap.add_argument("--with-buffer", action="store_true",
+                    help="c2/c3/c5: pass a carried (zero) omega buffer, as the drop-in cells do")
+    ap.add_argument("--clamp-every", type=int, default=None,
+                    help="c2/c3/c5: clamp S every N tokens (the cells' scan_chunk_len)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (HBM counter calibration)")
     ap.add_argument("--config", choices=sorted(PLAN_CONFIGS) + ["c4", "decode", "affine", "prologue"], default="c3",
@@ -723,7 +732,8 @@ def main():
         run_c4(args.steps, args.warmup, cpu=cpu, cpu_sample_t=args.cpu_sample_tokens or 128)
     else:
         bench_plan(args.config, args.steps, args.warmup, cpu=cpu,
-                   cpu_sample_t=args.cpu_sample_tokens or PLAN_CONFIGS[args.config]["cpu_sample_t"])
+                   cpu_sample_t=args.cpu_sample_tokens or PLAN_CONFIGS[args.config]["cpu_sample_t"],
+                   with_buffer=args.with_buffer, clamp_every=args.clamp_every)
 
 
 if __name__ == "__main__":

@@ -141,8 +141,9 @@ def run_oracle_rows(c: Case, p: dict, rows, block: int = 256):
     """fp64 oracle outputs and gradients for the head-batch rows `rows` only (rows are independent,
     so these equal the same rows of the full problem's). The sequence runs in blocks of `block`
     tokens carrying (S, Z, buffer), unclamped until the last block: the same recurrence as one call
-    (the oracle's chunk invariance), with a fraction of the memory at long T. No clamp_every."""
-    assert c.clamp_every is None
+    (the oracle's chunk invariance), with a fraction of the memory at long T. With clamp_every, the
+    block length must be a multiple of it (every block end is then a clamp point)."""
+    assert c.clamp_every is None or block % c.clamp_every == 0
     idx = torch.tensor(list(rows))
     sub = {kk: (v[idx] if v is not None else None) for kk, v in p.items()}
     x = {kk: (sub[kk].to(F64).clone().requires_grad_(c.backward) if sub[kk] is not None else None)
@@ -154,10 +155,11 @@ def run_oracle_rows(c: Case, p: dict, rows, block: int = 256):
     for s0 in range(0, c.T, block):
         sl = slice(s0, min(c.T, s0 + block))
         sl_or_none = lambda t: t[:, sl] if t is not None else None
+        last = s0 + block >= c.T
         y, S, Z, B = memory_recurrence_vectorised(
             phi_k[:, sl], phi_q[:, sl], x["v"][:, sl], x["lr"][:, sl], x["decay"][:, sl], sl_or_none(x["beta"]),
-            sl_or_none(x["gate"]), x["S_ref"], S, Z, B, window=c.e,
-            clamp_final=c.clamp_final and s0 + block >= c.T)
+            sl_or_none(x["gate"]), x["S_ref"], S, Z, B, window=c.e, clamp_every=c.clamp_every,
+            clamp_final=c.clamp_final if last else c.clamp_every is not None)
         ys.append(y)
     out = [torch.cat(ys, dim=1), S, Z, B]
     grads = {}

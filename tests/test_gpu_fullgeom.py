@@ -30,6 +30,10 @@ CASES = [
     # C3 as the drop-in cell calls it: a carried (zero) buffer
     (Case("c3_full_zero_buffer", BH=32, T=4096, d=64, e=4, gate='lag', momentum=True, buffer=True,
           buffer_scale=0.0, dtype=BF16, seed=103), (0, 15, 31)),
+    # C3 with scan_chunk_len = 64, as the drop-in cell runs it ("chunk 64"): segment-parallel with the
+    # clamp points checked on the device
+    (Case("c3_full_clamp64", BH=32, T=4096, d=64, e=4, gate='lag', momentum=True, clamp_every=64, dtype=BF16,
+          seed=107), (0, 15, 31)),
     # C2: Titans with momentum, B=4 H=8 T=2048
     (Case("c2_full", BH=32, T=2048, d=64, e=1, gate=None, momentum=True, dtype=BF16, seed=104), (0, 15, 31)),
     # C5's memory core: B=8 H=8 T=2048, e=4 per-token gates (the cell's omega gate), momentum;

@@ -83,6 +83,21 @@ CASES = [
          states=0.1, dtype=BF16, seed=29),
     Case("fp32_dk128_dv128_clamp", BH=2, T=96, d=128, e=2, gate='token', momentum=True, states=0.2,
          clamp_every=32, seed=30),
+    # scan_chunk_len clamps on chunk ends run segment-parallel with the clamp points checked on the
+    # device; the exact one-segment-per-row sequence runs only when a clamp would change S
+    Case("bf16_walk_clamp64_quiet", BH=4, T=600, d=64, e=4, gate='lag', momentum=True, states=0.1, clamp_every=64,
+         dtype=BF16, seed=35),
+    # forward only in bf16: once the clamp fires, its gradient mask (|S| <= 100) flips for elements that
+    # bf16 operand rounding moves across the bound (gradients ~3e-2 off in either direction of the
+    # bound; fp32 with firing clamps matches to 2e-7, fp32_clamp64_fires_late checks the gradients)
+    Case("bf16_walk_clamp64_fires", BH=3, T=300, d=64, e=4, gate='lag', momentum=True, states=150.0, clamp_every=64,
+         decay_shift=7.0, dtype=BF16, backward=False, seed=36),
+    Case("bf16_buffer_clamp64_quiet", BH=3, T=400, d=64, e=3, gate='token', momentum=True, buffer=True, states=0.1,
+         clamp_every=64, dtype=BF16, seed=37),
+    Case("fp32_clamp64_multiseg_quiet", BH=40, T=300, d=32, e=2, gate=None, momentum=True, states=0.2, clamp_every=64,
+         seed=38),
+    Case("fp32_clamp64_fires_late", BH=2, T=200, d=32, e=2, gate='token', momentum=False, states=60.0, clamp_every=64,
+         decay_shift=9.0, seed=39),
 ]
 
 
