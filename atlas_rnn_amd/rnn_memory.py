@@ -212,16 +212,15 @@ class _CellBase(Module):
 
     def _memory(self, x, state, window) -> tuple[Tensor, RNNMemState]:
         batch, seq_len, _ = x.shape
-        if not exists(state):
+        # a state the cell creates itself has Z = 0 and an all-zero omega buffer: they are passed as
+        # absent (the kernels read absent as zeros), which keeps the call on the specialised walks
+        fresh = not exists(state)
+        if fresh:
             state = self.init_state(batch, x.device, x.dtype)
         k, q, v, lr, decay, beta, gate = self._inputs(x)
         S0 = state.S
-        Z0 = state.Z if (self.use_momentum and exists(state.Z)) else None
-        if self.use_momentum and Z0 is None:
-            Z0 = torch.zeros_like(S0)
-        buf = state.omega_buffer if window > 1 else None
-        if window > 1 and buf is None:
-            buf = S0.new_zeros((S0.shape[0], window - 1, *S0.shape[1:]))
+        Z0 = state.Z if (self.use_momentum and exists(state.Z) and not fresh) else None
+        buf = state.omega_buffer if (window > 1 and not fresh) else None
         chunk = self.scan_chunk_len if (exists(self.scan_chunk_len) and seq_len > self.scan_chunk_len) else None
         y, S_T, Z_T, buf_out = memory_recurrence(
             k, q, v, lr, decay, beta, gate, S_ref=S0, S0=S0, Z0=Z0, buffer=buf, window=window,

@@ -547,6 +547,92 @@ def run_prologue(steps, warmup, B=8, T=2048, dim=512, heads=8, d=64, conv_k=4, n
     print(json.dumps(line), flush=True)
 
 
+def run_module(steps, warmup, B=4, T=4096, heads=8, d=64, e=4, chunk=64):
+    """The drop-in cell at the C3 shape: OmegaRNNMemoryCell(dim=512, 8 heads of 64, omega_window=4,
+    per-token omega gate, momentum, scan_chunk_len=64) in bf16, forward + backward of every parameter
+    (loss = sum out * g), called with a fresh state (state=None: a new sequence) and with a carried
+    state (the previous call's S, Z and omega buffer). The library's recurrence kernels inside the
+    cell step are timed with its HIP events and set against the same recurrence through the
+    preplanned path (RecurrencePlan, token gates, clamp_every=64)."""
+    import torch
+    import atlas_rnn_amd as am
+    from atlas_rnn_amd.functional import RecurrencePlan, profile_enable, profile_read
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    torch.manual_seed(1009)
+    dim = heads * d
+    cell = am.OmegaRNNMemoryCell(dim=dim, dim_head=d, heads=heads, omega_window=e, use_omega_gate=True,
+                                 use_momentum=True, scan_chunk_len=chunk).to(dev, torch.bfloat16)
+    with torch.no_grad():   # non-trivial gate heads (zero-initialised weights give constant gates)
+        for pp in cell.parameters():
+            if pp.ndim == 2 and pp.shape[0] == heads:
+                pp.normal_(0, 0.02)
+    g = torch.Generator().manual_seed(1010)
+    x = torch.randn(B, T, dim, generator=g).to(dev, torch.bfloat16)
+    gy = torch.randn(B, T, dim, generator=g).to(dev, torch.bfloat16)
+    params = list(cell.parameters())
+    with torch.no_grad():
+        _, st0 = cell(x)
+    st0 = am.state_detach(st0)
+
+    def step(state):
+        out, _ = cell(x, state)
+        torch.autograd.grad(out, params, grad_outputs=gy)
+
+    res = {}
+    for name, state in (("fresh_state", None), ("carried_state", st0)):
+        for _ in range(warmup):
+            step(state)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step(state)
+        torch.cuda.synchronize()
+        ms = 1e3 * (time.perf_counter() - t0) / steps
+        profile_enable(True)
+        profile_read(reset=True)
+        for _ in range(steps):
+            step(state)
+        torch.cuda.synchronize()
+        prof = profile_read(reset=True)
+        profile_enable(False)
+        rec_ms = sum(v for v, n in prof.values()) / steps
+        res[name] = {"ms_per_step": round(ms, 4), "recurrence_kernels_ms": round(rec_ms, 4),
+                     "kernels": {kk: round(1e3 * v / steps, 2) for kk, (v, n) in prof.items() if n}}
+    # the same recurrence through the preplanned path
+    bh = B * heads
+    xin, _ = make_inputs(dev, dict(B=B, H=heads, T=T, d=d, e=e, gate="token", seed=1003))
+    plan = RecurrencePlan(bh, T, d, window=e, momentum=True, gate_mode='token', dtype=torch.bfloat16, device=dev,
+                          clamp_every=chunk)
+
+    def pstep():
+        plan.forward(xin["k"], xin["q"], xin["v"], xin["lr"], xin["decay"], xin["beta"], xin["gate"], xin["S_ref"],
+                     xin["S0"], None)
+        plan.backward(xin["dy"])
+
+    for _ in range(warmup):
+        pstep()
+    profile_enable(True)
+    profile_read(reset=True)
+    for _ in range(steps):
+        pstep()
+    torch.cuda.synchronize()
+    prof = profile_read(reset=True)
+    profile_enable(False)
+    plan_ms = sum(v for v, n in prof.values()) / steps
+    ms = res["fresh_state"]["ms_per_step"]
+    line = {"metric": "memory-cell tokens/s fwd+bwd (prologue, recurrence, output projection, every parameter gradient)",
+            "value": round(B * T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded), random-init cell",
+            "config": {"workload": f"OmegaRNNMemoryCell(dim={dim}, dim_head={d}, heads={heads}, omega_window={e}, "
+                                   f"use_omega_gate=True, use_momentum=True, scan_chunk_len={chunk}), x [{B}, {T}, {dim}]",
+                       "parallelism": "single GPU"},
+            "module": res, "plan_recurrence_kernels_ms": round(plan_ms, 4),
+            "module_vs_plan_recurrence": round(res["fresh_state"]["recurrence_kernels_ms"] / plan_ms, 3)}
+    print(json.dumps(line), flush=True)
+
+
 def run_decode(steps, warmup):
     """Generation steps at the C3 head shape (B=4 H=8 d=64 e=4 lag gates, momentum, bf16 inputs,
     fp32 state): atlas_mem_step through the C ABI with the state updated in place, the way a decode
@@ -710,7 +796,8 @@ def main():
                     help="c2/c3/c5: clamp S every N tokens (the cells' scan_chunk_len)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (HBM counter calibration)")
-    ap.add_argument("--config", choices=sorted(PLAN_CONFIGS) + ["c4", "decode", "affine", "prologue"], default="c3",
+    ap.add_argument("--config", choices=sorted(PLAN_CONFIGS) + ["c4", "decode", "affine", "prologue", "module"],
+                    default="c3",
                     help="c3 (default): the headline; c2 / c4 / c5: the other BASELINE configs; decode: the "
                          "one-token step")
     args = ap.parse_args()
@@ -724,6 +811,8 @@ def main():
     cpu = not args.no_cpu_baseline
     if args.config == "decode":
         run_decode(args.steps, args.warmup)
+    elif args.config == "module":
+        run_module(args.steps, args.warmup)
     elif args.config == "prologue":
         run_prologue(args.steps, args.warmup)
     elif args.config == "affine":

@@ -340,3 +340,38 @@ def test_cell_decode_steps(name, spec):
         compare(f"{name}.Z", st_d.Z.float().cpu(), st_r.Z, 1e-4)
     if st_r.omega_buffer is not None:
         compare(f"{name}.buffer", st_d.omega_buffer.float().cpu(), st_r.omega_buffer, 1e-4)
+
+
+@pytest.mark.parametrize("spec", [dict(kind="omega", dim=128, dim_head=64, heads=2, omega_window=4, scan_chunk_len=64),
+                                  dict(kind="titans", dim=64, dim_head=32, heads=2)],
+                         ids=["omega_w4_chunk64", "titans"])
+def test_cell_fresh_state_matches_explicit_zero_state(spec):
+    """cell(x) with no state passes its zero Z and omega buffer as absent (the specialised walks);
+    cell(x, cell.init_state(b)) passes them as tensors (the general kernels). Outputs, next states
+    and parameter gradients agree (fp32: rtol 1e-4; the explicit zero-state path is the one the
+    oracle pins in test_cell_parity)."""
+    _say(f"cell fresh state vs zero state: {spec}")
+    torch.manual_seed(41)
+    cell = _make_cell(spec).cuda()
+    with torch.no_grad():
+        for p in cell.parameters():
+            if p.ndim == 2 and p.shape[0] == cell.heads:
+                p.normal_(0, 0.2)
+    g = torch.Generator().manual_seed(42)
+    x = torch.randn(2, 300, cell.dim, generator=g).cuda()
+    gy = torch.randn(2, 300, cell.dim, generator=g).cuda()
+    res = []
+    for state in (None, cell.init_state(2)):
+        out, st = cell(x, state)
+        grads = torch.autograd.grad((out * gy).sum(), list(cell.parameters()))
+        res.append((out, st, grads))
+    torch.cuda.synchronize()
+    (o1, s1, g1), (o2, s2, g2) = res
+    compare("fresh.out", o1.detach().cpu(), o2.detach().cpu().double(), 1e-4)
+    for a, b in zip(s1[1:], s2[1:]):
+        if a is None:
+            assert b is None
+            continue
+        compare("fresh.state", a.cpu(), b.cpu().double(), 1e-4)
+    for (n, _), a, b in zip(cell.named_parameters(), g1, g2):
+        compare(f"fresh.d{n}", a.cpu(), b.cpu().double(), 1e-4)
