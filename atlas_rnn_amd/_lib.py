@@ -48,6 +48,9 @@ EXPORTED_SYMBOLS = (
     "atlas_affine_scan_workspace_bytes",
     "atlas_tensor_map_fwd",
     "atlas_tensor_map_bwd",
+    "atlas_block_split",
+    "atlas_block_merge",
+    "atlas_block_parts",
     "atlas_prologue_num_workgroups",
     "atlas_prologue_fwd",
     "atlas_prologue_bwd",
@@ -138,6 +141,12 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_tensor_map_fwd.argtypes = [i32, i64, i32, i32, i32, vp, vp, vp, vp, vp]
     lib.atlas_tensor_map_bwd.restype = i32
     lib.atlas_tensor_map_bwd.argtypes = [i32, i64, i32, i32, i32, vp, vp, vp, vp, vp, vp]
+    lib.atlas_block_split.restype = i32
+    lib.atlas_block_split.argtypes = [i32] * 5 + [vp] * 8
+    lib.atlas_block_merge.restype = i32
+    lib.atlas_block_merge.argtypes = [i32] * 5 + [vp] * 10
+    lib.atlas_block_parts.restype = i32
+    lib.atlas_block_parts.argtypes = [i32]
     f32 = ctypes.c_float
     lib.atlas_prologue_num_workgroups.restype = i32
     lib.atlas_prologue_num_workgroups.argtypes = [i32, i32]

@@ -298,30 +298,70 @@ def _poly_map(x: Tensor, degree: int) -> Tensor:
     return out.to(x.dtype)
 
 
+class _BlockSplitFn(torch.autograd.Function):
+    """phi, psi [BH, T, Dk], v [BH, T, Dv], S_ref [BH, Dv, Dk] -> the stacked 64-wide operands of the
+    state blocks (atlas_block_split / atlas_block_merge): phi_b, psi_b, nv_b [NB BH, T, 64] with
+    nv = v - S_ref phi, block r = (i * Dk/64 + j) * BH + bh."""
+
+    @staticmethod
+    def forward(ctx, phi, psi, v, S_ref):
+        lib = _lib.load()
+        bh, T, dk = phi.shape
+        dv = v.shape[-1]
+        nb = (dk // _BLOCK) * (dv // _BLOCK)
+        phi, psi, v, S_ref = _aligned(phi), _aligned(psi), _aligned(v), _aligned(S_ref.float())
+        out = [torch.empty(nb * bh, T, _BLOCK, device=phi.device, dtype=phi.dtype) for _ in range(3)]
+        _lib.check(lib.atlas_block_split(_dt_code(phi), bh, T, dk, dv, _ptr(phi), _ptr(psi), _ptr(v), _ptr(S_ref),
+                                         _ptr(out[0]), _ptr(out[1]), _ptr(out[2]), _stream(phi.device)),
+                   "atlas_block_split")
+        ctx.save_for_backward(phi, S_ref)
+        ctx.dv = dv
+        return tuple(out)
+
+    @staticmethod
+    def backward(ctx, dphi_b, dpsi_b, dnv_b):
+        lib = _lib.load()
+        phi, S_ref = ctx.saved_tensors
+        bh, T, dk = phi.shape
+        dv = ctx.dv
+        z = lambda g: torch.zeros(dk // _BLOCK * (dv // _BLOCK) * bh, T, _BLOCK, device=phi.device,
+                                  dtype=phi.dtype) if g is None else _aligned(g.to(phi.dtype))
+        dphi_b, dpsi_b, dnv_b = z(dphi_b), z(dpsi_b), z(dnv_b)
+        dphi = torch.empty_like(phi)
+        dpsi = torch.empty_like(phi)
+        dvv = torch.empty(bh, T, dv, device=phi.device, dtype=phi.dtype)
+        parts = torch.empty(bh, lib.atlas_block_parts(T), dv, dk, device=phi.device, dtype=torch.float32)
+        _lib.check(lib.atlas_block_merge(_dt_code(phi), bh, T, dk, dv, _ptr(phi), _ptr(S_ref), _ptr(dphi_b),
+                                         _ptr(dpsi_b), _ptr(dnv_b), _ptr(dphi), _ptr(dpsi), _ptr(dvv), _ptr(parts),
+                                         _stream(phi.device)), "atlas_block_merge")
+        return dphi, dpsi, dvv, parts.sum(dim=1)
+
+
 def block_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
                      beta: Tensor | None, gate: Tensor | None, S_ref: Tensor, S0: Tensor, Z0: Tensor | None,
                      buffer: Tensor | None, *, window: int, map_mode: str, map_degree: int,
-                     clamp_every: int | None, clamp_final: bool, inner=None):
+                     clamp_every: int | None, clamp_final: bool):
     """The recurrence for head sizes above 64 or d_k != d_v, as 64 x 64 state blocks.
 
     With the state split into blocks S[i, j] (rows 64 i .. of d_v, columns 64 j .. of d_k):
       * delta_t = S_ref phi_t - v_t couples the column blocks only through delta, so delta is
-        formed once (one GEMM over all tokens) and every block runs the 64-wide recurrence with
-        S_ref = 0 and v = -delta[rows of i] (its own delta is then 0 . phi - v = delta);
+        formed once and every block runs the 64-wide recurrence with S_ref = 0 and
+        v = -delta[rows of i] (its own delta is then 0 . phi - v = delta);
       * the block's update delta_i phi_j^T, decay, momentum, window and clamp are blockwise;
       * y[rows of i] = sum_j S[i, j] psi_j.
     The blocks are stacked along the head-batch axis ((i, j, bh) order) into ONE call of the
-    64-wide kernels; the per-token scalars are shared by all blocks. Gradients follow through the
-    stacking, the delta GEMM and the block sum (torch autograd). Head sizes that are not a multiple
-    of 64 are zero-padded (the padded rows / columns of every state stay zero).
-    `inner` runs the 64-wide recurrence (memory_recurrence by default).
+    64-wide kernels; the per-token scalars are shared by all blocks. The column / row blocks of
+    phi, psi and v - S_ref phi are formed in one pass by atlas_block_split (its adjoint
+    atlas_block_merge); the states and scalars are stacked by small copies. Head sizes that are not
+    a multiple of 64 are zero-padded (the padded rows / columns of every state stay zero).
     """
-    inner = memory_recurrence if inner is None else inner
     bh, T, dk = k.shape
     dv = v.shape[-1]
     nbk, nbv = -(-dk // _BLOCK), -(-dv // _BLOCK)
     Dk, Dv = nbk * _BLOCK, nbv * _BLOCK
     pad_k, pad_v = Dk - dk, Dv - dv
+    if Dk > 256 or Dv > 256:
+        raise ValueError(f"head sizes up to 256 are supported (got d_k={dk}, d_v={dv})")
     # the elementwise map is applied here (delta needs the mapped keys)
     if map_mode == 'elementwise' and map_degree > 1:
         k, q = _poly_map(k, map_degree), _poly_map(q, map_degree)
@@ -331,18 +371,8 @@ def block_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
     vv = padf(v, (0, pad_v))
     pst = lambda t: padf(t, (0, pad_k, 0, pad_v))
     S_ref, S0, Z0, buffer = pst(S_ref), pst(S0), pst(Z0), pst(buffer)
-    # delta = S_ref phi - v (at least fp32), handed to every block as -v in the input dtype
-    acc = torch.promote_types(k.dtype, torch.float32)
-    delta = torch.matmul(phi.to(acc), S_ref.to(acc).transpose(-1, -2)) - vv.to(acc)
-    nv = (-delta).to(k.dtype)
     nb = nbv * nbk
-
-    # Stacking in (i, j, bh) order as one permuted copy per tensor (its gradient is one permuted
-    # copy back, plus a sum over the blocks that share the tensor).
-    def stack_cols(x, n_rep_outer, n_blk, n_rep_inner):   # [BH, T, n_blk * 64] -> [(o, blk, in, bh), T, 64]
-        x = x.reshape(bh, T, n_blk, _BLOCK).permute(2, 0, 1, 3).unsqueeze(1).unsqueeze(0)
-        x = x.expand(n_rep_outer, n_blk, n_rep_inner, bh, T, _BLOCK)
-        return x.reshape(n_rep_outer * n_blk * n_rep_inner * bh, T, _BLOCK)
+    kb, qb, vb = _BlockSplitFn.apply(phi, psi, vv, S_ref)
 
     def stack_state(x):        # [BH, ..., Dv, Dk] -> [(i, j, bh), ..., 64, 64]
         if x is None:
@@ -354,14 +384,11 @@ def block_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
         return x.reshape(nb * bh, *mid, _BLOCK, _BLOCK)
 
     rep = lambda t: None if t is None else t.unsqueeze(0).expand(nb, *t.shape).reshape(nb * bh, *t.shape[1:])
-    kb = stack_cols(phi, nbv, nbk, 1)
-    qb = stack_cols(psi, nbv, nbk, 1)
-    vb = stack_cols(nv, 1, nbv, nbk)
     S0b, Z0b, Bb = stack_state(S0), stack_state(Z0), stack_state(buffer)
     Sref0 = torch.zeros_like(S0b)
-    y, S_T, Z_T, B = inner(kb, qb, vb, rep(lr), rep(decay), rep(beta), rep(gate), Sref0, S0b, Z0b, Bb,
-                           window=window, map_mode='off', map_degree=1, clamp_every=clamp_every,
-                           clamp_final=clamp_final)
+    y, S_T, Z_T, B = memory_recurrence(kb, qb, vb, rep(lr), rep(decay), rep(beta), rep(gate), Sref0, S0b, Z0b, Bb,
+                                       window=window, map_mode='off', map_degree=1, clamp_every=clamp_every,
+                                       clamp_final=clamp_final)
     # y: sum over the column blocks of each row block; states: blocks back in place
     y = y.reshape(nbv, nbk, bh, T, _BLOCK).sum(dim=1).permute(1, 2, 0, 3).reshape(bh, T, Dv)
 

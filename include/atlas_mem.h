@@ -222,6 +222,26 @@ int atlas_tensor_map_fwd(int dtype, int64_t n, int d_in, int d_out, int degree, 
 int atlas_tensor_map_bwd(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x, const void* proj,
                          const void* pre, const void* dout, void* dx, void* stream);
 
+/* ---- state blocks for head sizes above 64 (BASELINE C4: d_k = 128, d_v = 64) ----------------
+ * The recurrence with S [d_v, d_k] runs as 64 x 64 blocks S[i, j] stacked along the row axis
+ * (r = (i * d_k/64 + j) * bh + b), each with S_ref = 0 and v = -delta[rows of block i], where
+ * delta = S_ref phi - v couples the column blocks (replaces the full-state einsum of
+ * atlas_pytorch/rnn_memory.py:659-660 for such sizes). d_k, d_v multiples of 64, <= 256. */
+
+/* phi, psi [bh, T, d_k], v [bh, T, d_v], S_ref [bh, d_v, d_k] fp32 -> phi_b, psi_b, nv_b [NB bh, T, 64]
+ * (NB = d_v/64 * d_k/64): the column blocks of phi and psi and the row blocks of v - S_ref phi. */
+int atlas_block_split(int dtype, int bh, int seq_len, int d_k, int d_v, const void* phi, const void* psi, const void* v,
+                      const float* S_ref, void* phi_b, void* psi_b, void* nv_b, void* stream);
+
+/* Adjoint of atlas_block_split: dphi_b, dpsi_b, dnv_b -> dphi, dpsi [bh, T, d_k], dv [bh, T, d_v] and
+ * dsref_part [bh][atlas_block_parts(T)][d_v][d_k] fp32 (sum over the second axis: dS_ref). */
+int atlas_block_merge(int dtype, int bh, int seq_len, int d_k, int d_v, const void* phi, const float* S_ref,
+                      const void* dphi_b, const void* dpsi_b, const void* dnv_b, void* dphi, void* dpsi, void* dv,
+                      float* dsref_part, void* stream);
+
+/* Number of dS_ref partials atlas_block_merge writes per row for seq_len tokens. */
+int atlas_block_parts(int seq_len);
+
 /* ---- cell prologue (atlas_pytorch/rnn_memory.py:567-653, MultiheadRMSNorm :139-147) --------
  * Fused around the cell's projections, which stay plain GEMMs (hipBLASLt): dtype is ATLAS_DT_F32 or
  * ATLAS_DT_BF16 for every tensor argument except inv_rms and the *_part partial sums (fp32).

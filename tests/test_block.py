@@ -1,17 +1,74 @@
-"""Block decomposition for head sizes the kernels are not built for (d_k = 128 after a tensor
-feature map with d_v = 64 is BASELINE config C4), checked on the CPU: `block_recurrence` with the
-fp64 oracle as its 64-wide inner recurrence must equal the oracle run on the full state, outputs
-and every input gradient (the decomposition is exact algebra, so the bar is fp64 round-off)."""
+"""The state-block decomposition for head sizes the kernels are not built for (d_k = 128 after a
+tensor feature map with d_v = 64 is BASELINE config C4), checked on the CPU as algebra: the
+decomposition `functional.block_recurrence` runs on the GPU (64 x 64 blocks S[i, j] stacked along
+the row axis, each with S_ref = 0 and v = -delta[rows of i], y = sum_j of the blocks' outputs) is
+restated here with torch ops around the fp64 oracle as the 64-wide recurrence, and must equal the
+oracle run on the full state, outputs and every input gradient (exact algebra: the bar is fp64
+round-off). The GPU kernels of the split (atlas_block_split / _merge) are checked end to end
+against the oracle in tests/test_gpu_parity.py (the c4_reduced and d_k != d_v cases)."""
 
 from __future__ import annotations
 
 import pytest
 import torch
 
-from atlas_rnn_amd.functional import block_recurrence
 from oracle import memory_recurrence_vectorised, poly_feature_map
 
 F64 = torch.float64
+BLK = 64
+
+
+def block_decomposition(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buffer, *, window, map_mode, map_degree,
+                        clamp_every, clamp_final, inner):
+    """The block algebra of functional.block_recurrence with torch ops (fp64 reference)."""
+    bh, T, dk = k.shape
+    dv = v.shape[-1]
+    nbk, nbv = -(-dk // BLK), -(-dv // BLK)
+    Dk, Dv = nbk * BLK, nbv * BLK
+    F = torch.nn.functional
+    padf = lambda t, pads: t if t is None or not any(pads) else F.pad(t, pads)
+    if map_mode == 'elementwise' and map_degree > 1:
+        k, q = poly_feature_map(k, map_degree, 'elementwise'), poly_feature_map(q, map_degree, 'elementwise')
+    phi, psi, vv = padf(k, (0, Dk - dk)), padf(q, (0, Dk - dk)), padf(v, (0, Dv - dv))
+    pst = lambda t: padf(t, (0, Dk - dk, 0, Dv - dv))
+    S_ref, S0, Z0, buffer = pst(S_ref), pst(S0), pst(Z0), pst(buffer)
+    nv = vv - torch.matmul(phi, S_ref.transpose(-1, -2))       # v - S_ref phi = -delta
+    nb = nbv * nbk
+
+    def cols(x, i_major):   # [BH, T, n*64] -> [(i, j, bh), T, 64]
+        n = x.shape[-1] // BLK
+        x = x.reshape(bh, T, n, BLK).permute(2, 0, 1, 3)
+        if i_major:   # row blocks i of nv, the same for every j
+            x = x.unsqueeze(1).expand(nbv, nbk, bh, T, BLK)
+        else:         # column blocks j of phi / psi, the same for every i
+            x = x.unsqueeze(0).expand(nbv, nbk, bh, T, BLK)
+        return x.reshape(nb * bh, T, BLK)
+
+    def stack_state(x):
+        if x is None:
+            return None
+        mid = x.shape[1:-2]
+        x = x.reshape(bh, *mid, nbv, BLK, nbk, BLK)
+        m = len(mid)
+        return x.permute(m + 1, m + 3, 0, *range(1, m + 1), m + 2, m + 4).reshape(nb * bh, *mid, BLK, BLK)
+
+    rep = lambda t: None if t is None else t.unsqueeze(0).expand(nb, *t.shape).reshape(nb * bh, *t.shape[1:])
+    S0b = stack_state(S0)
+    y, S_T, Z_T, B = inner(cols(phi, False), cols(psi, False), cols(nv, True), rep(lr), rep(decay), rep(beta),
+                           rep(gate), torch.zeros_like(S0b), S0b, stack_state(Z0), stack_state(buffer),
+                           window=window, map_mode='off', map_degree=1, clamp_every=clamp_every,
+                           clamp_final=clamp_final)
+    y = y.reshape(nbv, nbk, bh, T, BLK).sum(dim=1).permute(1, 2, 0, 3).reshape(bh, T, Dv)
+
+    def unblock(x):
+        if x is None:
+            return None
+        mid = x.shape[1:-2]
+        m = len(mid)
+        x = x.reshape(nbv, nbk, bh, *mid, BLK, BLK)
+        return x.permute(2, *range(3, m + 3), 0, m + 3, 1, m + 4).reshape(bh, *mid, Dv, Dk)[..., :dv, :dk]
+
+    return y[..., :dv], unblock(S_T), unblock(Z_T), unblock(B)
 
 
 def _oracle_inner(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, buffer, *, window, map_mode, map_degree,
@@ -73,7 +130,7 @@ def test_block_recurrence_matches_full_oracle(dk, dv, e, gate, momentum, degree,
         poly_feature_map(a["k"], degree, mode), poly_feature_map(a["q"], degree, mode), a["v"], a["lr"],
         a["decay"], a["beta"], a["gate"], a["S_ref"], a["S0"], a["Z0"], a["buffer"], window=e,
         clamp_every=clamp_every, clamp_final=True))
-    got_out, got_g = run(lambda a: block_recurrence(
+    got_out, got_g = run(lambda a: block_decomposition(
         a["k"], a["q"], a["v"], a["lr"], a["decay"], a["beta"], a["gate"], a["S_ref"], a["S0"], a["Z0"],
         a["buffer"], window=e, map_mode=mode, map_degree=degree, clamp_every=clamp_every, clamp_final=True,
         inner=_oracle_inner))
