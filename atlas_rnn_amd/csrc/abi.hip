@@ -26,16 +26,6 @@ bool walk_fwd_supported(const Geom& g);
 hipError_t launch_walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
                            float* rw, float* final_raw, float* coef, bf16* wsh, hipStream_t stream);
 
-// ATLAS_MEM_GENERIC=1 routes every call through the general segment kernels (seg_fwd.hip /
-// seg_bwd.hip) instead of the specialised bf16, d = 64 walks; used by the tests to check both.
-static bool force_generic() {
-  static const bool v = [] {
-    const char* e = std::getenv("ATLAS_MEM_GENERIC");
-    return e && e[0] == '1';
-  }();
-  return v;
-}
-
 // Diagnostic tile product C = A B^T (16 x 64 inputs) through the same fragment helpers.
 template <typename T>
 __global__ __launch_bounds__(64) void k_mfma_selftest(const T* A, const T* B, float* C) {
@@ -144,7 +134,6 @@ struct Plan {
 // CU's LDS, so a second round of workgroups would only queue behind the first); a single segment
 // when S is clamped at scan_chunk_len boundaries (not affine). The CU count is MI355X's, fixed so
 // that the saved / workspace sizes do not depend on the device queried.
-// ATLAS_MEM_SEG_CHUNKS overrides the chunks per segment (tuning).
 constexpr int kCUs = 256;
 SegGeom make_seg(const Geom& g) {
   SegGeom s{};
@@ -154,10 +143,6 @@ SegGeom make_seg(const Geom& g) {
   } else {
     const int want = g.BH >= kCUs ? 1 : (kCUs + g.BH - 1) / g.BH;
     G = (g.nc + want - 1) / want;
-    if (const char* env = std::getenv("ATLAS_MEM_SEG_CHUNKS")) {
-      const int v = std::atoi(env);
-      if (v > 0) G = v;
-    }
   }
   if (G < 1) G = 1;
   if (G > g.nc) G = g.nc;
@@ -347,7 +332,7 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
   err = hipErrorInvalidValue;
   if (g.DK == 64) {
     if constexpr (sizeof(T) == 2) {
-      if (!force_generic() && walk_fwd_supported(g))
+      if (walk_fwd_supported(g))
         err = launch_walk_fwd(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
       else
         err = launch_fwd_seg<T, 64, 64>(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
@@ -391,7 +376,7 @@ int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, voi
   p.scal = reinterpret_cast<float*>(w + L.scal);
   hipError_t err = hipErrorInvalidValue;
   // the specialised walks run as a pair: the forward saved its states in their layout
-  const bool walk = sizeof(T) == 2 && !force_generic() && walk_fwd_supported(pl.g);
+  const bool walk = sizeof(T) == 2 && walk_fwd_supported(pl.g);
   // the specialised path forms its adjoint aggregates over the forward's chunks and records
   const AggOverFwd agf{pl.g, pl.sg, reinterpret_cast<const float*>(sv + SL.coef)};
   const bool agg_fwd = walk && pl.g.Lc == 64;

@@ -370,8 +370,249 @@ hipError_t launch_tmap_bwd(long n, const bf16* x, const bf16* p, const bf16* dou
   return hipGetLastError();
 }
 
-// d_in in {32, 64}, d_out in {32, 64, 128}
+// ---------------------------------------------------------------------------------------------
+// General kernels: fp32 inputs (fp32 operands on v_mfma_f32_16x16x4f32, fp32 accumulate: the
+// map in x.dtype as the reference runs it) and bf16 inputs at the sizes the kernels above are not
+// built for. d_in in {16, 32, 64}, d_out a multiple of 16 up to 128. One workgroup (4 waves) per 64
+// tokens, wave w owning tokens 16 w .. 16 w + 15; P's blocks of d_in rows (block 0 the linear
+// rows, block a + 1 the rows that multiply x_a x) are staged in LDS as fp32 pb[b][o], one block at
+// a time, with the next block prefetched into registers while the current one is consumed.
+//   forward   phi[n, o] = sum_blk sum_b A_blk[n, b] pb_blk[b, o],  A_0 = x,  A_{a+1} = x_a x
+//   backward  G_blk[n, b] = sum_o dphi[n, o] pb_blk[b, o]; dx[n, b] += G_0[n, b] + x[n, a] G_{a+1}[n, b]
+//             and dx[n, a] += sum_b G_{a+1}[n, b] x[n, b] (a 16-lane sum, collected in an LDS table)
+// ---------------------------------------------------------------------------------------------
+namespace tg {
+constexpr int TN = 64;      // tokens per workgroup
+constexpr int NT = 256;     // threads
+constexpr int MMAX = 128;   // largest d_out
+}
+
+// Four consecutive elements as fp32 (8-byte aligned bf16 or 16-byte aligned fp32).
+__device__ __forceinline__ float4 ld4f(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 ld4f(const bf16* p) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  return make_float4(__builtin_bit_cast(float, u.x << 16), __builtin_bit_cast(float, u.x & 0xffff0000u),
+                     __builtin_bit_cast(float, u.y << 16), __builtin_bit_cast(float, u.y & 0xffff0000u));
+}
+
+template <int D, int PITCH>
+struct TgSmem {
+  float xs[tg::TN][D + 1];                // x of the workgroup's tokens (zero past n_tok)
+  alignas(16) float pb[D][PITCH];         // the current P block, pb[b][o]
+  float t1[tg::TN][D + 1];   // backward: the row term sum_b G_{a+1}[n, b] x[n, b] at [n][a]
+};
+
+// x rows n0 .. n0 + 63 into xs (fp32, zeros past n_tok)
+template <typename T, int D, int PITCH>
+__device__ __forceinline__ void tg_load_x(TgSmem<D, PITCH>& sm, const T* x, long n0, long n_tok) {
+  for (int u = threadIdx.x; u < tg::TN * D / 4; u += tg::NT) {
+    const int r = u / (D / 4), c = (u % (D / 4)) * 4;
+    const float4 v = n0 + r < n_tok ? ld4f(x + (n0 + r) * D + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    sm.xs[r][c] = v.x; sm.xs[r][c + 1] = v.y; sm.xs[r][c + 2] = v.z; sm.xs[r][c + 3] = v.w;
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(tg::NT) void k_tmap_gen_fwd(long n_tok, int M, const T* __restrict__ x,
+                                                         const T* __restrict__ pt, T* __restrict__ out, int deg,
+                                                         T* __restrict__ pre) {
+  constexpr int KK = D / 4, K = D + D * D;
+  constexpr int VPT = tg::MMAX * D / 4 / tg::NT;   // P^T vectors per thread and block (at M = 128)
+  __shared__ TgSmem<D, tg::MMAX + 16> sm;          // pitch: 4 k rows x 16 columns hit 64 banks
+  const int tid = threadIdx.x, l = lane_id(), w = wave_id();
+  const int row = l & 15, kq = l >> 4;
+  const long n0 = (long)blockIdx.x * tg::TN;
+  const int JT = M / 16, nvec = M * D / 4;
+  tg_load_x<T, D>(sm, x, n0, n_tok);
+  // P block blk from P^T [M][K]: pb[b][o] = P^T[o][blk D + b], four b per vector
+  float4 pf[VPT];
+  auto pload = [&](int blk) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int v = tid + i * tg::NT;
+      if (v < nvec) pf[i] = ld4f(pt + (size_t)(v / KK) * K + blk * D + (v % KK) * 4);
+    }
+  };
+  auto pstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int v = tid + i * tg::NT;
+      if (v < nvec) {
+        const int o = v / KK, b = (v % KK) * 4;
+        sm.pb[b][o] = pf[i].x; sm.pb[b + 1][o] = pf[i].y; sm.pb[b + 2][o] = pf[i].z; sm.pb[b + 3][o] = pf[i].w;
+      }
+    }
+  };
+  pload(0);
+  __syncthreads();
+  float xv[KK];   // x[n][4 kk + kq] of this lane's token row
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) xv[kk] = sm.xs[16 * w + row][4 * kk + kq];
+  f32x4 acc[tg::MMAX / 16];
+#pragma unroll
+  for (int j = 0; j < tg::MMAX / 16; ++j) acc[j] = zero4();
+  for (int blk = 0; blk <= D; ++blk) {
+    __syncthreads();   // every wave is done with the previous block
+    pstore();
+    __syncthreads();
+    if (blk < D) pload(blk + 1);
+    const float xa = blk == 0 ? 1.f : sm.xs[16 * w + row][blk - 1];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const float av = xa * xv[kk];
+#pragma unroll
+      for (int j = 0; j < tg::MMAX / 16; ++j)
+        if (j < JT) acc[j] = MM<float>::mma(av, sm.pb[4 * kk + kq][16 * j + row], acc[j]);
+    }
+  }
+  // acc[j][r] = phi[token 16 w + 4 kq + r][feature 16 j + row]
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const long n = n0 + 16 * w + 4 * kq + r;
+    if (n >= n_tok) continue;
+#pragma unroll
+    for (int j = 0; j < tg::MMAX / 16; ++j) {
+      if (j >= JT) continue;
+      const size_t o = (size_t)n * M + 16 * j + row;
+      const float v = acc[j][r];
+      if (deg > 1) {
+        pre[o] = from_f32<T>(v);
+        out[o] = from_f32<T>(poly_map(v, deg));
+      } else {
+        out[o] = from_f32<T>(v);
+      }
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(tg::NT) void k_tmap_gen_bwd(long n_tok, int M, const T* __restrict__ x,
+                                                         const T* __restrict__ p, const T* __restrict__ dout,
+                                                         T* __restrict__ dx, int deg, const T* __restrict__ pre) {
+  constexpr int JD = D / 16, KO = tg::MMAX / 4;
+  constexpr int VPT = tg::MMAX * D / 4 / tg::NT;
+  __shared__ TgSmem<D, tg::MMAX + 4> sm;   // pitch: 16 rows x 4 k columns hit 64 banks
+  const int tid = threadIdx.x, l = lane_id(), w = wave_id();
+  const int row = l & 15, kq = l >> 4;
+  const long n0 = (long)blockIdx.x * tg::TN;
+  const int MQ = M / 4, nvec = M * D / 4;
+  tg_load_x<T, D>(sm, x, n0, n_tok);
+  for (int u = tid; u < tg::TN * (D + 1); u += tg::NT) (&sm.t1[0][0])[u] = 0.f;
+  // P block blk from P [K][M]: pb[b][o] = P[blk D + b][o], four o per vector
+  float4 pf[VPT];
+  auto pload = [&](int blk) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int v = tid + i * tg::NT;
+      if (v < nvec) pf[i] = ld4f(p + (size_t)(blk * D + v / MQ) * M + (v % MQ) * 4);
+    }
+  };
+  auto pstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int v = tid + i * tg::NT;
+      if (v < nvec) *reinterpret_cast<float4*>(&sm.pb[v / MQ][(v % MQ) * 4]) = pf[i];
+    }
+  };
+  pload(0);
+  // dphi (scaled by the map's derivative at pre) of this lane's token row, k = 4 kk + kq
+  float dp[KO];
+  {
+    const long n = n0 + 16 * w + row;
+#pragma unroll
+    for (int kk = 0; kk < KO; ++kk) {
+      float v = 0.f;
+      if (kk < MQ && n < n_tok) {
+        const size_t o = (size_t)n * M + 4 * kk + kq;
+        v = to_f32(dout[o]);
+        if (deg > 1) v *= poly_map_grad(to_f32(pre[o]), deg);
+      }
+      dp[kk] = v;
+    }
+  }
+  __syncthreads();
+  float xc[JD][4], dxc[JD][4];   // x and dx at [token 16 w + 4 kq + r][16 jd + row]
+#pragma unroll
+  for (int jd = 0; jd < JD; ++jd)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      xc[jd][r] = sm.xs[16 * w + 4 * kq + r][16 * jd + row];
+      dxc[jd][r] = 0.f;
+    }
+  for (int blk = 0; blk <= D; ++blk) {
+    __syncthreads();
+    pstore();
+    __syncthreads();
+    if (blk < D) pload(blk + 1);
+    f32x4 G[JD];
+#pragma unroll
+    for (int jd = 0; jd < JD; ++jd) G[jd] = zero4();
+#pragma unroll
+    for (int kk = 0; kk < KO; ++kk) {
+      if (kk >= MQ) break;
+#pragma unroll
+      for (int jd = 0; jd < JD; ++jd) G[jd] = MM<float>::mma(dp[kk], sm.pb[16 * jd + row][4 * kk + kq], G[jd]);
+    }
+    // G[jd][r] = G_blk[token 16 w + 4 kq + r][b = 16 jd + row]
+    if (blk == 0) {
+#pragma unroll
+      for (int jd = 0; jd < JD; ++jd)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dxc[jd][r] += G[jd][r];
+    } else {
+      const int a = blk - 1;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float xa = sm.xs[16 * w + 4 * kq + r][a];
+        float rs = 0.f;
+#pragma unroll
+        for (int jd = 0; jd < JD; ++jd) {
+          dxc[jd][r] += xa * G[jd][r];
+          rs += G[jd][r] * xc[jd][r];
+        }
+        rs = row_sum16(rs);
+        if (row == 0) sm.t1[16 * w + 4 * kq + r][a] = rs;   // rows of this wave only
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const long n = n0 + 16 * w + 4 * kq + r;
+    if (n >= n_tok) continue;
+#pragma unroll
+    for (int jd = 0; jd < JD; ++jd) {
+      const int c = 16 * jd + row;
+      dx[(size_t)n * D + c] = from_f32<T>(dxc[jd][r] + sm.t1[16 * w + 4 * kq + r][c]);
+    }
+  }
+}
+
+template <typename T>
+hipError_t tmap_gen_fwd(int d, int m, long n, const T* x, const T* pt, T* out, int deg, T* pre, hipStream_t s) {
+  const dim3 grid((unsigned)((n + tg::TN - 1) / tg::TN)), block(tg::NT);
+  if (d == 16) hipLaunchKernelGGL((k_tmap_gen_fwd<T, 16>), grid, block, 0, s, n, m, x, pt, out, deg, pre);
+  else if (d == 32) hipLaunchKernelGGL((k_tmap_gen_fwd<T, 32>), grid, block, 0, s, n, m, x, pt, out, deg, pre);
+  else if (d == 64) hipLaunchKernelGGL((k_tmap_gen_fwd<T, 64>), grid, block, 0, s, n, m, x, pt, out, deg, pre);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+template <typename T>
+hipError_t tmap_gen_bwd(int d, int m, long n, const T* x, const T* p, const T* dout, T* dx, int deg, const T* pre,
+                        hipStream_t s) {
+  const dim3 grid((unsigned)((n + tg::TN - 1) / tg::TN)), block(tg::NT);
+  if (d == 16) hipLaunchKernelGGL((k_tmap_gen_bwd<T, 16>), grid, block, 0, s, n, m, x, p, dout, dx, deg, pre);
+  else if (d == 32) hipLaunchKernelGGL((k_tmap_gen_bwd<T, 32>), grid, block, 0, s, n, m, x, p, dout, dx, deg, pre);
+  else if (d == 64) hipLaunchKernelGGL((k_tmap_gen_bwd<T, 64>), grid, block, 0, s, n, m, x, p, dout, dx, deg, pre);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+bool tmap_fast(int d, int m) { return (d == 32 || d == 64) && (m == 32 || m == 64 || m == 128); }
+
+// bf16: d_in in {32, 64}, d_out in {32, 64, 128} on the kernels above, other sizes on the general ones
 hipError_t tmap_fwd(int d, int m, long n, const bf16* x, const bf16* pt, bf16* out, int deg, bf16* pre, hipStream_t s) {
+  if (!tmap_fast(d, m)) return tmap_gen_fwd<bf16>(d, m, n, x, pt, out, deg, pre, s);
   if (d == 64 && m == 128) return launch_tmap_fwd<64, 128>(n, x, pt, out, deg, pre, s);
   if (d == 64 && m == 64) return launch_tmap_fwd<64, 64>(n, x, pt, out, deg, pre, s);
   if (d == 64 && m == 32) return launch_tmap_fwd<64, 32>(n, x, pt, out, deg, pre, s);
@@ -382,6 +623,7 @@ hipError_t tmap_fwd(int d, int m, long n, const bf16* x, const bf16* pt, bf16* o
 }
 hipError_t tmap_bwd(int d, int m, long n, const bf16* x, const bf16* p, const bf16* dout, bf16* dx, int deg,
                     const bf16* pre, hipStream_t s) {
+  if (!tmap_fast(d, m)) return tmap_gen_bwd<bf16>(d, m, n, x, p, dout, dx, deg, pre, s);
   if (d == 64 && m == 128) return launch_tmap_bwd<64, 128>(n, x, p, dout, dx, deg, pre, s);
   if (d == 64 && m == 64) return launch_tmap_bwd<64, 64>(n, x, p, dout, dx, deg, pre, s);
   if (d == 64 && m == 32) return launch_tmap_bwd<64, 32>(n, x, p, dout, dx, deg, pre, s);
@@ -400,7 +642,8 @@ hipError_t tmap_bwd(int d, int m, long n, const bf16* x, const bf16* p, const bf
 
 namespace {
 bool tmap_dims_ok(int64_t n, int d_in, int d_out) {
-  return n >= 0 && n < ((int64_t)1 << 40) && (d_in == 32 || d_in == 64) && (d_out == 32 || d_out == 64 || d_out == 128);
+  return n >= 0 && n < ((int64_t)1 << 40) && (d_in == 16 || d_in == 32 || d_in == 64) && d_out >= 16 &&
+         d_out <= 128 && d_out % 16 == 0;
 }
 bool tmap_misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
 }  // namespace
@@ -409,12 +652,19 @@ extern "C" {
 
 int atlas_tensor_map_fwd(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x, const void* proj_t,
                          void* out, void* pre, void* stream) {
-  if (dtype != ATLAS_DT_BF16) return ATLAS_MEM_ERR_DTYPE;
+  if (dtype != ATLAS_DT_BF16 && dtype != ATLAS_DT_F32) return ATLAS_MEM_ERR_DTYPE;
   if (!tmap_dims_ok(n, d_in, d_out) || degree < 1 || degree > 16) return ATLAS_MEM_ERR_SHAPE;
   if (!x || !proj_t || !out || (degree > 1 && !pre)) return ATLAS_MEM_ERR_NULL;
   if (tmap_misaligned(x) || tmap_misaligned(proj_t) || tmap_misaligned(out) || tmap_misaligned(pre))
     return ATLAS_MEM_ERR_ALIGN;
   if (n == 0) return ATLAS_MEM_OK;
+  if (dtype == ATLAS_DT_F32) {
+    const hipError_t err = atlas::tmap_gen_fwd<float>(d_in, d_out, (long)n, static_cast<const float*>(x),
+                                                      static_cast<const float*>(proj_t), static_cast<float*>(out),
+                                                      degree, degree > 1 ? static_cast<float*>(pre) : nullptr,
+                                                      static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
+  }
   const hipError_t err = atlas::tmap_fwd(d_in, d_out, (long)n, static_cast<const atlas::bf16*>(x),
                                          static_cast<const atlas::bf16*>(proj_t), static_cast<atlas::bf16*>(out),
                                          degree, degree > 1 ? static_cast<atlas::bf16*>(pre) : nullptr,
@@ -424,13 +674,21 @@ int atlas_tensor_map_fwd(int dtype, int64_t n, int d_in, int d_out, int degree, 
 
 int atlas_tensor_map_bwd(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x, const void* proj,
                          const void* pre, const void* dout, void* dx, void* stream) {
-  if (dtype != ATLAS_DT_BF16) return ATLAS_MEM_ERR_DTYPE;
+  if (dtype != ATLAS_DT_BF16 && dtype != ATLAS_DT_F32) return ATLAS_MEM_ERR_DTYPE;
   if (!tmap_dims_ok(n, d_in, d_out) || degree < 1 || degree > 16) return ATLAS_MEM_ERR_SHAPE;
   if (!x || !proj || !dout || !dx || (degree > 1 && !pre)) return ATLAS_MEM_ERR_NULL;
   if (tmap_misaligned(x) || tmap_misaligned(proj) || tmap_misaligned(dout) || tmap_misaligned(dx) ||
       tmap_misaligned(pre))
     return ATLAS_MEM_ERR_ALIGN;
   if (n == 0) return ATLAS_MEM_OK;
+  if (dtype == ATLAS_DT_F32) {
+    const hipError_t err = atlas::tmap_gen_bwd<float>(d_in, d_out, (long)n, static_cast<const float*>(x),
+                                                      static_cast<const float*>(proj), static_cast<const float*>(dout),
+                                                      static_cast<float*>(dx), degree,
+                                                      degree > 1 ? static_cast<const float*>(pre) : nullptr,
+                                                      static_cast<hipStream_t>(stream));
+    return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
+  }
   const hipError_t err = atlas::tmap_bwd(d_in, d_out, (long)n, static_cast<const atlas::bf16*>(x),
                                          static_cast<const atlas::bf16*>(proj), static_cast<const atlas::bf16*>(dout),
                                          static_cast<atlas::bf16*>(dx), degree,

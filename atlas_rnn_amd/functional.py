@@ -215,21 +215,31 @@ def _canon(x: Tensor | None, dtype) -> Tensor | None:
 # Tensor polynomial feature map (rnn_memory.py:125-130): [x; vec(x x^T)] @ P, fused on the GPU
 # ---------------------------------------------------------------------------------------------
 
-_TMAP_DIN = (32, 64)
-_TMAP_DOUT = (32, 64, 128)
+_TMAP_DIN = (16, 32, 64)
+_TMAP_DOUT = tuple(range(16, 129, 16))
 
 
-def _tensor_map_reference_form(x: Tensor, proj: Tensor) -> Tensor:
-    """The reference's tensor ops (materialises vec(x x^T)); used where the kernels do not apply."""
-    d = x.shape[-1]
-    outer = torch.einsum('...i,...j->...ij', x, x).reshape(*x.shape[:-1], d * d)
-    return torch.cat([x, outer], dim=-1) @ proj.to(x.device, x.dtype)
+def _tmap_check(x: Tensor, proj: Tensor, degree: int) -> None:
+    """Raises for operands the kernels do not take (no other implementation exists)."""
+    d, m = x.shape[-1], proj.shape[-1]
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"tensor_feature_map: dtype {x.dtype} (the kernels take bfloat16 or float32)")
+    if d not in _TMAP_DIN or m not in _TMAP_DOUT:
+        raise ValueError(f"tensor_feature_map: d_in {d} / d_out {m} (the kernels take d_in in {_TMAP_DIN}, "
+                         "d_out a multiple of 16 up to 128)")
+    if tuple(proj.shape) != (d + d * d, m):
+        raise ValueError(f"tensor_feature_map: proj {tuple(proj.shape)}, expected ({d + d * d}, {m})")
+    if proj.requires_grad:
+        raise NotImplementedError("tensor_feature_map: proj is a constant (a registered buffer in the reference); "
+                                  "the kernels form no gradient for it")
+    if not 1 <= int(degree) <= 16:
+        raise ValueError(f"tensor_feature_map: degree {degree} (1 .. 16)")
 
 
 class _TensorMapFn(torch.autograd.Function):
-    """atlas_tensor_map_fwd / _bwd: bf16 x [n, d] and P [d + d*d, m] -> phi [n, m], followed by the
-    elementwise polynomial of `degree` (1: none); P is a constant (a registered buffer in the
-    reference, so it has no gradient)."""
+    """atlas_tensor_map_fwd / _bwd: x [n, d] and P [d + d*d, m] (bf16 or fp32, P in x's dtype as the
+    reference casts it) -> phi [n, m], followed by the elementwise polynomial of `degree` (1: none);
+    P is a constant (a registered buffer in the reference, so it has no gradient)."""
 
     @staticmethod
     def forward(ctx, x, proj, degree):
@@ -237,12 +247,12 @@ class _TensorMapFn(torch.autograd.Function):
         lib = _lib.load()
         lead, d, m = x.shape[:-1], x.shape[-1], proj.shape[-1]
         x2 = _aligned(x.reshape(-1, d))
-        p = _aligned(proj.to(torch.bfloat16))
+        p = _aligned(proj.to(x.dtype))
         pt = _aligned(p.t())
         n = x2.shape[0]
-        out = torch.empty(n, m, device=dev, dtype=torch.bfloat16)
-        pre = torch.empty(n, m, device=dev, dtype=torch.bfloat16) if degree > 1 else None
-        _lib.check(lib.atlas_tensor_map_fwd(_lib.DT_BF16, n, d, m, degree, _ptr(x2), _ptr(pt), _ptr(out), _ptr(pre),
+        out = torch.empty(n, m, device=dev, dtype=x.dtype)
+        pre = torch.empty(n, m, device=dev, dtype=x.dtype) if degree > 1 else None
+        _lib.check(lib.atlas_tensor_map_fwd(_dt_code(x2), n, d, m, degree, _ptr(x2), _ptr(pt), _ptr(out), _ptr(pre),
                                             _stream(dev)), "atlas_tensor_map_fwd")
         ctx.save_for_backward(x2, p, pre)
         ctx.lead = lead
@@ -256,31 +266,20 @@ class _TensorMapFn(torch.autograd.Function):
         lib = _lib.load()
         n, d = x2.shape
         m = p.shape[-1]
-        g = _aligned(dout.reshape(-1, m).to(torch.bfloat16))
+        g = _aligned(dout.reshape(-1, m).to(x2.dtype))
         dx = torch.empty_like(x2)
-        _lib.check(lib.atlas_tensor_map_bwd(_lib.DT_BF16, n, d, m, ctx.degree, _ptr(x2), _ptr(p), _ptr(pre), _ptr(g),
+        _lib.check(lib.atlas_tensor_map_bwd(_dt_code(x2), n, d, m, ctx.degree, _ptr(x2), _ptr(p), _ptr(pre), _ptr(g),
                                             _ptr(dx), _stream(dev)), "atlas_tensor_map_bwd")
         return dx.reshape(*ctx.lead, d), None, None
 
 
 def tensor_feature_map(x: Tensor, proj: Tensor, degree: int = 1) -> Tensor:
-    """[x; vec(x x^T)] @ proj (rnn_memory.py:125-130), then (degree > 1) the elementwise polynomial
-    sum_{i=1..degree} phi^i (BASELINE C4's composition). bf16 GPU inputs with d in (32, 64) and
-    proj [d + d*d, m], m in (32, 64, 128), and a constant proj run the fused kernels (the Kronecker
-    features are never materialised; the polynomial is applied on the fp32 accumulator); other
-    dtypes, sizes or a trainable proj use the reference's tensor ops."""
-    d, m = x.shape[-1], proj.shape[-1]
-    fused = (x.is_cuda and x.dtype == torch.bfloat16 and d in _TMAP_DIN and m in _TMAP_DOUT
-             and proj.shape[0] == d + d * d and not proj.requires_grad and 1 <= degree <= 16)
-    if not fused:
-        phi = _tensor_map_reference_form(x, proj)
-        if degree > 1:
-            out, pw = phi, phi
-            for _ in range(2, degree + 1):
-                pw = pw * phi
-                out = out + pw
-            phi = out
-        return phi
+    """[x; vec(x x^T)] @ proj (rnn_memory.py:125-130) in x's dtype, then (degree > 1) the elementwise
+    polynomial sum_{i=1..degree} phi^i (BASELINE C4's composition), on the fused kernels: the
+    Kronecker features are never materialised and the polynomial is applied on the fp32 accumulator.
+    x: bf16 or fp32 GPU tensor [..., d], d in (16, 32, 64); proj [d + d*d, m], m a multiple of 16 up
+    to 128, constant. Anything else raises (CPU tensors included)."""
+    _tmap_check(x, proj, degree)
     return _TensorMapFn.apply(x, proj, int(degree))
 
 

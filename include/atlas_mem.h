@@ -208,17 +208,20 @@ size_t atlas_affine_scan_workspace_bytes(int n, int t, int r, int d);
 /* Tensor polynomial feature map, fused (replaces the 'tensor' mode of PolynomialFeatureMap,
  * atlas_pytorch/rnn_memory.py:125-130, which materialises vec(x x^T) with einsum / cat / matmul):
  *   pre = [x; vec(x x^T)] P,  out = sum_{i=1..degree} pre^i  (degree 1: out = pre),
- *   x [n, d_in] bf16, P [d_in + d_in^2, d_out] bf16 (row d_in + a*d_in + b multiplies x_a x_b),
- *   out, pre [n, d_out] bf16 (pre written only for degree > 1, for the backward), fp32 accumulation.
+ *   x [n, d_in], P [d_in + d_in^2, d_out] (row d_in + a*d_in + b multiplies x_a x_b),
+ *   out, pre [n, d_out] (pre written only for degree > 1, for the backward), all of one dtype:
+ *   ATLAS_DT_BF16 (bf16 matrix cores, fp32 accumulation) or ATLAS_DT_F32 (fp32 operands on the fp32
+ *   matrix cores, as the reference runs the map in x.dtype).
  * degree > 1 is the elementwise map after the projection (BASELINE config C4's composition).
- * The forward takes P transposed (proj_t [d_out, d_in + d_in^2]); d_in in {32, 64},
- * d_out in {32, 64, 128}, degree 1..16; bf16 only; every pointer 16-byte aligned. */
+ * The forward takes P transposed (proj_t [d_out, d_in + d_in^2]); d_in in {16, 32, 64}, d_out a
+ * multiple of 16 up to 128 (bf16 at d_in {32, 64} x d_out {32, 64, 128} runs the fast kernels),
+ * degree 1..16; every pointer 16-byte aligned. */
 int atlas_tensor_map_fwd(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x, const void* proj_t,
                          void* out, void* pre, void* stream);
 
 /* Gradient of atlas_tensor_map_fwd with respect to x for the output gradient dout [n, d_out]
  * (P is a fixed buffer in the reference: no gradient). Takes P itself (proj [d_in + d_in^2, d_out])
- * and, for degree > 1, the forward's pre; dx [n, d_in] bf16. */
+ * and, for degree > 1, the forward's pre; dx [n, d_in] in the same dtype. */
 int atlas_tensor_map_bwd(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x, const void* proj,
                          const void* pre, const void* dout, void* dx, void* stream);
 

@@ -189,9 +189,12 @@ def test_tensor_map_errors_before_launch(lib):
     good, bad = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x10008)
     f = lib.atlas_tensor_map_fwd
     b = lib.atlas_tensor_map_bwd
-    assert f(_lib.DT_F32, 8, 64, 128, 1, good, good, good, None, None) == 3         # bf16 only
-    assert f(_lib.DT_BF16, 8, 48, 128, 1, good, good, good, None, None) == 2        # d_in in (32, 64)
-    assert f(_lib.DT_BF16, 8, 64, 96, 1, good, good, good, None, None) == 2         # d_out in (32, 64, 128)
+    assert f(2, 8, 64, 128, 1, good, good, good, None, None) == 3                   # bf16 or fp32
+    assert f(_lib.DT_F32, 8, 48, 128, 1, good, good, good, None, None) == 2         # d_in in (16, 32, 64)
+    assert f(_lib.DT_BF16, 8, 128, 128, 1, good, good, good, None, None) == 2
+    assert f(_lib.DT_BF16, 8, 64, 72, 1, good, good, good, None, None) == 2         # d_out % 16 == 0
+    assert f(_lib.DT_F32, 8, 64, 144, 1, good, good, good, None, None) == 2         # d_out <= 128
+    assert f(_lib.DT_F32, 8, 16, 16, 1, good, bad, good, None, None) == 5
     assert f(_lib.DT_BF16, 8, 64, 128, 0, good, good, good, None, None) == 2        # degree 1..16
     assert f(_lib.DT_BF16, 8, 64, 128, 1, None, good, good, None, None) == 4
     assert f(_lib.DT_BF16, 8, 64, 128, 3, good, good, good, None, None) == 4        # degree > 1 needs pre
@@ -203,18 +206,27 @@ def test_tensor_map_errors_before_launch(lib):
     assert b(_lib.DT_BF16, -1, 64, 128, 1, good, good, None, good, good, None) == 2
 
 
-def test_tensor_feature_map_reference_form_off_gpu():
-    """On the CPU (and for shapes or dtypes the kernels do not take) the map is the reference's
-    tensor-op formulation, which the oracle restates."""
+def test_tensor_feature_map_raises_off_kernel():
+    """The map has one implementation, the kernels: CPU tensors and operands they do not take raise
+    before anything is launched (no tensor-op formulation to fall back to)."""
     torch = pytest.importorskip("torch")
     from atlas_rnn_amd.functional import tensor_feature_map
-    from oracle import poly_feature_map
-    g = torch.Generator().manual_seed(3)
-    x = torch.randn(5, 7, 16, generator=g, dtype=torch.float64)
-    P = torch.randn(16 + 256, 16, generator=g, dtype=torch.float64)
-    torch.testing.assert_close(tensor_feature_map(x, P), poly_feature_map(x, 2, 'tensor', P))
-    torch.testing.assert_close(tensor_feature_map(x, P, degree=3),
-                               poly_feature_map(poly_feature_map(x, 2, 'tensor', P), 3, 'elementwise'))
+    x = torch.randn(5, 7, 16)
+    P = torch.randn(16 + 256, 16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        tensor_feature_map(x, P)
+    with pytest.raises(TypeError, match="dtype"):
+        tensor_feature_map(x.double(), P.double())
+    with pytest.raises(ValueError, match="d_in"):
+        tensor_feature_map(torch.randn(3, 24), torch.randn(24 + 576, 16))
+    with pytest.raises(ValueError, match="d_out"):
+        tensor_feature_map(x, torch.randn(16 + 256, 24))
+    with pytest.raises(ValueError, match="proj"):
+        tensor_feature_map(x, torch.randn(16 + 255, 16))
+    with pytest.raises(NotImplementedError, match="constant"):
+        tensor_feature_map(x, P.requires_grad_(True))
+    with pytest.raises(ValueError, match="degree"):
+        tensor_feature_map(x, P.detach(), degree=0)
 
 
 def test_cpu_tensors_are_rejected():

@@ -97,7 +97,8 @@ def test_omega_gate_short_circuit_on_device():
     compare("short_circuit.buf", buf.cpu(), ref_buf, 1e-5)
 
 
-@pytest.mark.parametrize("mode,degree,dt", [("elementwise", 3, torch.float32), ("tensor", 2, BF16)])
+@pytest.mark.parametrize("mode,degree,dt", [("elementwise", 3, torch.float32), ("tensor", 2, BF16),
+                                            ("tensor", 2, torch.float32)])
 def test_omega_poly_features(mode, degree, dt):
     """omega.py:90-118 on the GPU: the elementwise polynomial, and the tensor map with the cached
     projection (the fused kernel) against the oracle's closed form with the same projection."""

@@ -24,8 +24,8 @@ from einops import rearrange
 
 import atlas_rnn_amd as am
 from _cases import compare
-from oracle import (affine_scan_sequential, memory_recurrence_vectorised, scalar_assoc_scan_sequential,
-                    sliding_sum_along_time)
+from oracle import (affine_scan_sequential, memory_recurrence_vectorised, poly_feature_map,
+                    scalar_assoc_scan_sequential, sliding_sum_along_time)
 
 pytestmark = pytest.mark.gpu
 
@@ -181,9 +181,11 @@ def _reference_cell_forward(cell, x, state):
     k = cell.split_heads(cell.to_k(k_in))[:, :, :T]
     v = cell.split_heads(cell.to_v(v_in))[:, :, :T]
     q, k = cell.q_norm(q), cell.k_norm(k)
-    phi_k = rearrange(cell.phi(rearrange(k, 'b h n d -> (b h n) d')), '(b h n) d -> (b h) n d', b=batch,
+    fm = cell.phi   # the oracle's feature map with the cell's own projection buffer
+    phi = lambda t: poly_feature_map(t, fm.degree, fm.mode, getattr(fm, 'proj', None))
+    phi_k = rearrange(phi(rearrange(k, 'b h n d -> (b h n) d')), '(b h n) d -> (b h) n d', b=batch,
                       h=cell.heads, n=T)
-    phi_q = rearrange(cell.phi(rearrange(q, 'b h n d -> (b h n) d')), '(b h n) d -> (b h) n d', b=batch,
+    phi_q = rearrange(phi(rearrange(q, 'b h n d -> (b h n) d')), '(b h n) d -> (b h) n d', b=batch,
                       h=cell.heads, n=T)
     v = rearrange(v, 'b h n d -> (b h) n d')
     lr = rearrange(cell.to_lr(x_act), 'b n h -> (b h) n')

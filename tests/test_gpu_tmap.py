@@ -1,7 +1,9 @@
 """GPU parity of the fused tensor feature map (atlas_tensor_map_fwd / _bwd) against the fp64
-oracle map `poly_feature_map(x, 2, 'tensor', proj)` (rnn_memory.py:125-130), on bf16-rounded inputs:
-the map's output and the gradient of x for a seeded upstream gradient, rtol 2e-2 with an atol floor
-of 2e-2 * max|ref| (bf16). Then the BASELINE C4 composition at a reduced size: the tensor map
+oracle map `poly_feature_map(x, 2, 'tensor', proj)` (rnn_memory.py:125-130), on inputs rounded to
+the kernel's dtype: the map's output and the gradient of x for a seeded upstream gradient, bf16
+rtol 2e-2 and fp32 rtol 1e-4 (normwise and elementwise, tests/_cases.compare). bf16 at the fast
+kernels' sizes (d_in 32 / 64, d_out 32 / 64 / 128) and at others (the general kernels, which also
+run every fp32 size). Then the BASELINE C4 composition at a reduced size: the tensor map
 (64 + 4096 -> 128) into the d_k = 128 / d_v = 64 recurrence with the elementwise map of degree 3,
 window 8, lag gates and momentum, against the oracle end to end (outputs and every input gradient).
 """
@@ -18,6 +20,7 @@ pytestmark = pytest.mark.gpu
 
 F64 = torch.float64
 BF16 = torch.bfloat16
+F32 = torch.float32
 TOL = 2e-2
 
 
@@ -26,28 +29,41 @@ def _say(msg):
     sys.stdout.flush()
 
 
-@pytest.mark.parametrize("n,d,m,deg", [(300, 64, 128, 1), (129, 64, 64, 1), (77, 32, 32, 1), (1, 32, 128, 1),
-                                       (256, 64, 32, 1), (1000, 32, 64, 1), (300, 64, 128, 3), (65, 32, 64, 2)])
-def test_tensor_map_parity(n, d, m, deg):
+MAP_CASES = [
+    # (n, d_in, d_out, degree, dtype): the fast bf16 kernels
+    (300, 64, 128, 1, BF16), (129, 64, 64, 1, BF16), (77, 32, 32, 1, BF16), (1, 32, 128, 1, BF16),
+    (256, 64, 32, 1, BF16), (1000, 32, 64, 1, BF16), (300, 64, 128, 3, BF16), (65, 32, 64, 2, BF16),
+    # the general kernels: bf16 at other sizes, fp32 at every size
+    (70, 16, 16, 1, BF16), (129, 64, 48, 2, BF16), (33, 32, 112, 1, BF16),
+    (300, 64, 128, 1, F32), (129, 64, 64, 3, F32), (77, 32, 32, 1, F32), (40, 16, 16, 2, F32),
+    (1, 16, 128, 1, F32), (200, 32, 80, 1, F32),
+]
+
+
+@pytest.mark.parametrize("n,d,m,deg,dt", MAP_CASES, ids=[f"{c[4]}-{c[0]}x{c[1]}-{c[2]}-g{c[3]}".replace("torch.", "")
+                                                          for c in MAP_CASES])
+def test_tensor_map_parity(n, d, m, deg, dt):
     from atlas_rnn_amd.functional import _TensorMapFn
-    _say(f"tensor map n={n} d={d} m={m} degree={deg}")
+    _say(f"tensor map n={n} d={d} m={m} degree={deg} {dt}")
     g = torch.Generator().manual_seed(n * 7 + d + m)
     x = torch.randn(n, d, generator=g)
-    x = (x / x.norm(dim=-1, keepdim=True)).to(BF16)
+    x = (x / x.norm(dim=-1, keepdim=True)).to(dt)
     bound = (6.0 / (d + d * d + m)) ** 0.5
-    P = ((torch.rand(d + d * d, m, generator=g) * 2 - 1) * bound).to(BF16)
-    gy = torch.randn(n, m, generator=g).to(BF16)
+    P = ((torch.rand(d + d * d, m, generator=g) * 2 - 1) * bound).to(dt)
+    gy = torch.randn(n, m, generator=g).to(dt)
     # oracle
     x64 = x.to(F64).requires_grad_(True)
     ref = poly_feature_map(poly_feature_map(x64, 2, 'tensor', P.to(F64)), deg, 'elementwise')
     (dref,) = torch.autograd.grad((ref * gy.to(F64)).sum(), [x64])
-    # kernels (through the autograd function, no fallback)
+    # kernels (through the autograd function)
     xg = x.cuda().requires_grad_(True)
     out = _TensorMapFn.apply(xg, P.cuda(), deg)
+    assert out.dtype == dt
     (dx,) = torch.autograd.grad((out.float() * gy.cuda().float()).sum(), [xg])
     torch.cuda.synchronize()
-    compare("phi", out.detach().float().cpu(), ref.detach(), TOL)
-    compare("dx", dx.float().cpu(), dref, TOL)
+    tol = TOL if dt == BF16 else 1e-4
+    compare("phi", out.detach().float().cpu(), ref.detach(), tol)
+    compare("dx", dx.float().cpu(), dref, tol)
 
 
 def test_c4_composition_reduced():

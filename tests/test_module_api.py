@@ -93,9 +93,10 @@ def test_polynomial_feature_map_closed_forms():
     # sum_{i=1..3} x^i
     want = torch.tensor([[0.5 + 0.25 + 0.125, -2.0 + 4.0 - 8.0, 3.0 + 9.0 + 27.0]], dtype=torch.float64)
     assert torch.allclose(am.PolynomialFeatureMap(3, 3, 'elementwise')(x), want)
-    m = am.PolynomialFeatureMap(3, 2, 'tensor').double()
-    feats = torch.cat([x[0], torch.outer(x[0], x[0]).reshape(-1)])
-    assert torch.allclose(m(x)[0], feats @ m.proj)
+    m = am.PolynomialFeatureMap(16, 2, 'tensor')   # the tensor map runs on its kernels only
+    assert m.proj.shape == (16 + 256, 16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        m(torch.randn(2, 16))
     assert am.PolynomialFeatureMap(3, 2, 'elementwise').fused_elementwise
     assert not am.PolynomialFeatureMap(3, 2, 'tensor').fused_elementwise
 
