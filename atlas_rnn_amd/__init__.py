@@ -7,6 +7,9 @@ include/atlas_mem.h. Module classes mirror atlas_pytorch.rnn_memory / omega / af
 
 from .functional import (  # noqa: F401
     memory_recurrence,
+    memory_step_factored,
+    buffer_factors,
+    expand_buffer_factors,
     AtlasOmegaFunction,
     atlas_omega_forward,
     check_cuda_availability,
@@ -28,6 +31,9 @@ from .rnn_memory import (  # noqa: F401
 
 __all__ = [
     "memory_recurrence",
+    "memory_step_factored",
+    "buffer_factors",
+    "expand_buffer_factors",
     "AtlasOmegaFunction",
     "atlas_omega_forward",
     "check_cuda_availability",

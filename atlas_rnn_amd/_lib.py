@@ -40,6 +40,9 @@ EXPORTED_SYMBOLS = (
     "atlas_mem_bwd_noalloc",
     "atlas_mem_noalloc_scratch_bytes",
     "atlas_mem_step",
+    "atlas_mem_step_factored",
+    "atlas_buffer_factors",
+    "atlas_buffer_expand",
     "atlas_scan_fwd",
     "atlas_scan_bwd",
     "atlas_window_sum",
@@ -119,6 +122,12 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_mem_fwd.argtypes = [P, ctypes.POINTER(FwdArgs), vp, vp]
     lib.atlas_mem_step.restype = i32
     lib.atlas_mem_step.argtypes = [P, ctypes.POINTER(FwdArgs), vp]
+    lib.atlas_mem_step_factored.restype = i32
+    lib.atlas_mem_step_factored.argtypes = [P, ctypes.POINTER(FwdArgs), vp, vp, vp]
+    lib.atlas_buffer_factors.restype = i32
+    lib.atlas_buffer_factors.argtypes = [P] + [vp] * 7
+    lib.atlas_buffer_expand.restype = i32
+    lib.atlas_buffer_expand.argtypes = [i32] * 4 + [vp] * 3
     lib.atlas_mem_bwd.restype = i32
     lib.atlas_mem_bwd.argtypes = [P, ctypes.POINTER(BwdArgs), vp, vp, sz, vp]
     lib.atlas_mem_bwd_noalloc.restype = i32

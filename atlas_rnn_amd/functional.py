@@ -426,6 +426,111 @@ def _memory_step(cfg: RecurrenceConfig, args, states):
     return y, S_T, Z_T, buf_out
 
 
+# ---------------------------------------------------------------------------------------------
+# The carried buffer as rank-1 factors (decode): factors [BH, e-1, d_v + d_k] fp32, slot m =
+# (g delta | phi) of the token whose product g delta phi^T the dense slot holds
+# ---------------------------------------------------------------------------------------------
+
+def _factor_dims(k: Tensor, v: Tensor) -> tuple[int, int, int]:
+    if k.dim() != 3 or v.dim() != 3:
+        raise ValueError(f"k and v must be [BH, T, d], got {tuple(k.shape)} and {tuple(v.shape)}")
+    bh, _, dk = k.shape
+    dv = v.shape[-1]
+    if dk != dv or dk not in _KERNEL_DIMS:
+        raise ValueError(f"the factored buffer takes d_k == d_v in {_KERNEL_DIMS}, got {dk} / {dv}")
+    return bh, dk, dv
+
+
+def _check_factors(factors: Tensor | None, bh: int, window: int, d: int, name: str) -> None:
+    if factors is None:
+        return
+    want = (bh, window - 1, 2 * d)
+    if tuple(factors.shape) != want or factors.dtype != torch.float32:
+        raise ValueError(f"{name} must be fp32 {want}, got {factors.dtype} {tuple(factors.shape)}")
+
+
+def memory_step_factored(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
+                         beta: Tensor | None = None, gate: Tensor | None = None,
+                         S_ref: Tensor | None = None, S0: Tensor | None = None, Z0: Tensor | None = None,
+                         factors: Tensor | None = None, *, window: int = 1, map_mode: str = 'off',
+                         map_degree: int = 1, clamp_final: bool = True):
+    """One decode token (T = 1, no autograd) with the carried buffer as rank-1 factors
+    (atlas_mem_step_factored): the recurrence step of memory_recurrence at T = 1
+    (rnn_memory.py:659-728, the generation loop of rnn_transformer.py:863-900), reading and writing
+    factors [BH, e-1, 2d] instead of the dense [BH, e-1, d, d]. Returns (y [BH, 1, d], S_T,
+    Z_T or None, factors_out or None); expand_buffer_factors(factors_out) is the dense buffer_out."""
+    dev = _require_gpu(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, factors)
+    bh, dk, dv = _factor_dims(k, v)
+    if k.shape[1] != 1:
+        raise ValueError(f"memory_step_factored takes one token, got T = {k.shape[1]}")
+    dt = k.dtype if k.dtype in _DTYPES else torch.float32
+    if S0 is None:
+        S0 = torch.zeros(bh, dv, dk, device=dev, dtype=torch.float32)
+    if S_ref is None:
+        S_ref = S0
+    check_operands(k, q, v, lr, decay, beta, gate, S_ref, S0, Z0, None, window=window)
+    _check_factors(factors, bh, window, dk, "factors")
+    e = window
+    cfg = RecurrenceConfig(window=e, map_mode=map_mode, map_degree=map_degree, clamp_final=clamp_final)
+    kk, qq, vv, lr_, dc, bt, gt = [_canon(t, dt) for t in (k, q, v, lr, decay, beta, gate)]
+    S_ref_, S0_ = _canon(S_ref, torch.float32), _canon(S0, torch.float32)
+    Z0_ = _canon(Z0, torch.float32) if beta is not None else None
+    f_in = _canon(factors, torch.float32) if e > 1 else None
+    lib = _lib.load()
+    prob = _problem(cfg, bh, 1, dk, dv, beta is not None, gt, f_in is not None, dt)
+    y = torch.empty(bh, 1, dv, device=dev, dtype=dt)
+    S_T = torch.empty(bh, dv, dk, device=dev, dtype=torch.float32)
+    Z_T = torch.empty_like(S_T) if beta is not None else None
+    f_out = torch.empty(bh, e - 1, dv + dk, device=dev, dtype=torch.float32) if e > 1 else None
+    a = _lib.FwdArgs(k=_ptr(kk), q=_ptr(qq), v=_ptr(vv), lr=_ptr(lr_), decay=_ptr(dc), beta=_ptr(bt), gate=_ptr(gt),
+                     S_ref=_ptr(S_ref_), S0=_ptr(S0_), Z0=_ptr(Z0_), y=_ptr(y), S_T=_ptr(S_T), Z_T=_ptr(Z_T))
+    _lib.check(lib.atlas_mem_step_factored(ctypes.byref(prob), ctypes.byref(a), _ptr(f_in), _ptr(f_out),
+                                           _stream(dev)), "atlas_mem_step_factored")
+    return y, S_T, Z_T, f_out
+
+
+def buffer_factors(k: Tensor, v: Tensor, gate: Tensor | None, S_ref: Tensor, factors: Tensor | None = None, *,
+                   window: int, map_mode: str = 'off', map_degree: int = 1) -> Tensor:
+    """The factored form of the buffer memory_recurrence returns after these T tokens (the last
+    e-1 of [factors; tokens], atlas_buffer_factors): prefill -> factored decode state."""
+    dev = _require_gpu(k, v, gate, S_ref, factors)
+    bh, dk, dv = _factor_dims(k, v)
+    if window < 2:
+        raise ValueError("the buffer exists for window >= 2")
+    T = k.shape[1]
+    dt = k.dtype if k.dtype in _DTYPES else torch.float32
+    check_operands(k, k, v, v[..., 0], v[..., 0], None, gate, S_ref, S_ref, None, None, window=window)
+    _check_factors(factors, bh, window, dk, "factors")
+    cfg = RecurrenceConfig(window=window, map_mode=map_mode, map_degree=map_degree)
+    kk, vv, gt = [_canon(t, dt) for t in (k, v, gate)]
+    S_ref_ = _canon(S_ref, torch.float32)
+    f_in = _canon(factors, torch.float32)
+    prob = _problem(cfg, bh, T, dk, dv, False, gt, f_in is not None, dt)
+    out = torch.empty(bh, window - 1, dv + dk, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    _lib.check(lib.atlas_buffer_factors(ctypes.byref(prob), _ptr(kk), _ptr(vv), _ptr(gt), _ptr(S_ref_), _ptr(f_in),
+                                        _ptr(out), _stream(dev)), "atlas_buffer_factors")
+    return out
+
+
+def expand_buffer_factors(factors: Tensor, d_v: int | None = None) -> Tensor:
+    """factors [BH, e-1, d_v + d_k] -> the dense buffer [BH, e-1, d_v, d_k] (atlas_buffer_expand), the
+    RNNMemState.omega_buffer / memory_recurrence buffer format. d_v defaults to half the width."""
+    dev = _require_gpu(factors)
+    if factors.dim() != 3 or factors.dtype != torch.float32:
+        raise ValueError(f"factors must be fp32 [BH, e-1, d_v + d_k], got {factors.dtype} {tuple(factors.shape)}")
+    bh, slots, width = factors.shape
+    dv = width // 2 if d_v is None else d_v
+    dk = width - dv
+    if dv < 1 or dk < 1:
+        raise ValueError(f"d_v {dv} does not split width {width}")
+    f = _aligned(factors)
+    out = torch.empty(bh, slots, dv, dk, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    _lib.check(lib.atlas_buffer_expand(bh, slots, dv, dk, _ptr(f), _ptr(out), _stream(dev)), "atlas_buffer_expand")
+    return out
+
+
 def memory_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
                       beta: Tensor | None = None, gate: Tensor | None = None,
                       S_ref: Tensor | None = None, S0: Tensor | None = None, Z0: Tensor | None = None,

@@ -633,13 +633,15 @@ def run_module(steps, warmup, B=4, T=4096, heads=8, d=64, e=4, chunk=64):
     print(json.dumps(line), flush=True)
 
 
-def run_decode(steps, warmup):
+def run_decode(steps, warmup, factored=False):
     """Generation steps at the C3 head shape (B=4 H=8 d=64 e=4 lag gates, momentum, bf16 inputs,
     fp32 state): atlas_mem_step through the C ABI with the state updated in place, the way a decode
     loop carries it. One step = one token for every sequence of the batch; `value` counts those
-    (b) tokens per second. The kernel is timed with events on the stream it runs on; its
+    (b) tokens per second, timed on a HIP graph of the steps (the eager per-call rate, host-bound,
+    is reported beside it). The kernel is timed with events on the stream it runs on; its
     algorithmic bytes are the state read and written once (S_ref, S0, Z0, buffer in; S_T, Z_T,
-    buffer out) plus the token's vectors."""
+    buffer out) plus the token's vectors. factored: the buffer carried as rank-1 factors
+    [bh, e-1, 2d] (atlas_mem_step_factored, two factor buffers used in turn)."""
     import ctypes
     import torch
     from atlas_rnn_amd import _lib
@@ -663,30 +665,60 @@ def run_decode(steps, warmup):
     a = _lib.FwdArgs(k=_ptr(x["k"]), q=_ptr(x["q"]), v=_ptr(x["v"]), lr=_ptr(x["lr"]), decay=_ptr(x["decay"]),
                      beta=_ptr(x["beta"]), gate=_ptr(x["gate"]), S_ref=_ptr(S_ref), S0=_ptr(S), Z0=_ptr(Z),
                      buffer_in=_ptr(Bf), y=_ptr(y), S_T=_ptr(S), Z_T=_ptr(Z), buffer_out=_ptr(Bf))
+    fac = [(0.1 * r(bh, e - 1, 2 * d)).to(dev), torch.empty(bh, e - 1, 2 * d, device=dev)]
+    fp = [_ptr(f) for f in fac]
+    af = _lib.FwdArgs(k=_ptr(x["k"]), q=_ptr(x["q"]), v=_ptr(x["v"]), lr=_ptr(x["lr"]), decay=_ptr(x["decay"]),
+                      beta=_ptr(x["beta"]), gate=_ptr(x["gate"]), S_ref=_ptr(S_ref), S0=_ptr(S), Z0=_ptr(Z),
+                      y=_ptr(y), S_T=_ptr(S), Z_T=_ptr(Z))
+
+    def step(i, st):   # token i (the factor buffers alternate with its parity)
+        if factored:
+            _lib.check(lib.atlas_mem_step_factored(ctypes.byref(prob), ctypes.byref(af), fp[i & 1], fp[(i & 1) ^ 1],
+                                                   st), "atlas_mem_step_factored")
+        else:
+            _lib.check(lib.atlas_mem_step(ctypes.byref(prob), ctypes.byref(a), st), "atlas_mem_step")
+
     stream = _stream(dev)
-
-    def step():
-        _lib.check(lib.atlas_mem_step(ctypes.byref(prob), ctypes.byref(a), stream), "atlas_mem_step")
-
-    for _ in range(warmup):
-        step()
+    for i in range(warmup):
+        step(i, stream)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record()
-    for _ in range(steps):
-        step()
+    for i in range(steps):
+        step(i, stream)
     ev1.record()
     torch.cuda.synchronize()
-    us = 1e3 * ev0.elapsed_time(ev1) / steps
-    state_bytes = bh * d * d * 4 * (3 + 2 + 2 * (e - 1))   # S_ref, S0, S_T; Z0, Z_T; buffer in / out
+    eager_us = 1e3 * ev0.elapsed_time(ev1) / steps
+    # the same steps replayed from a HIP graph of G launches (no host work between tokens): the
+    # kernel-bound rate a captured generation loop sees; this is `value`
+    G = 64
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cap = _stream(dev)   # the capturing stream
+        for i in range(G):
+            step(i, cap)
+    torch.cuda.synchronize()
+    reps = max(1, steps // G)
+    graph.replay()
+    torch.cuda.synchronize()
+    ev0.record()
+    for _ in range(reps):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    us = 1e3 * ev0.elapsed_time(ev1) / (reps * G)
+    state_bytes = bh * d * d * 4 * (3 + 2)                  # S_ref, S0, S_T; Z0, Z_T
+    state_bytes += bh * (e - 1) * 4 * (2 * 2 * d if factored else 2 * d * d)   # buffer in / out
     vec_bytes = bh * (3 * d + 3 + e) * 2 + bh * d * 2       # k, q, v, scalars, gates; y
     alg = state_bytes + vec_bytes
     out = {"metric": "decode tokens/s (one memory-layer step per token)", "value": round(B / (us * 1e-6), 1),
            "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(us / 1e3, 6),
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-           "data": "synthetic (seeded)",
+           "data": "synthetic (seeded)", "timing": f"HIP graph of {G} steps replayed {reps} times",
+           "eager_us_per_step": round(eager_us, 3),
            "config": {"workload": "decode step at the C3 head shape: B=4 H=8 d=64 e=4 lag gates, momentum, "
-                                  "state in place", "global_batch": B, "seq_len": 1, "parallelism": "single GPU"},
+                                  "state in place" + (", buffer as rank-1 factors" if factored else ""),
+                      "global_batch": B, "seq_len": 1, "parallelism": "single GPU"},
            "roofline": {"bound": "hbm", "achieved": round(alg / (us * 1e-6) / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
                         "frac": round(alg / (us * 1e-6) / 8e12, 4), "traffic": None}}
     print(json.dumps(out), flush=True)
@@ -794,6 +826,8 @@ def main():
                     help="c2/c3/c5: pass a carried (zero) omega buffer, as the drop-in cells do")
     ap.add_argument("--clamp-every", type=int, default=None,
                     help="c2/c3/c5: clamp S every N tokens (the cells' scan_chunk_len)")
+    ap.add_argument("--factored", action="store_true",
+                    help="--config decode: carry the buffer as rank-1 factors (atlas_mem_step_factored)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (HBM counter calibration)")
     ap.add_argument("--config", choices=sorted(PLAN_CONFIGS) + ["c4", "decode", "affine", "prologue", "module"],
@@ -810,7 +844,7 @@ def main():
         sys.exit(2)
     cpu = not args.no_cpu_baseline
     if args.config == "decode":
-        run_decode(args.steps, args.warmup)
+        run_decode(args.steps, args.warmup, factored=args.factored)
     elif args.config == "module":
         run_module(args.steps, args.warmup)
     elif args.config == "prologue":

@@ -145,6 +145,29 @@ int atlas_mem_fwd(const atlas_mem_problem* prob, const atlas_mem_fwd_args* args,
  * (S_T = S0, Z_T = Z0, buffer_out = buffer_in) for in-place state updates. One launch. */
 int atlas_mem_step(const atlas_mem_problem* prob, const atlas_mem_fwd_args* args, void* stream);
 
+/* The carried Omega buffer as rank-1 factors (the on-device RNNMemState format, dense or factored,
+ * of atlas_pytorch/rnn_transformer.py:863-900's generation loop). Every dense slot the forward
+ * carries is one outer product g_p delta_p phi_p^T (rnn_memory.py:673-687); the factored form holds
+ *   factors [bh, e-1, d_v + d_k] fp32, slot m = (g_p delta_p [d_v] | phi_p [d_k]), slot 0 the oldest,
+ * (d_v + d_k) / (d_v d_k) of the dense bytes. */
+
+/* atlas_mem_step with the window sum over factored slots: args->buffer_in / buffer_out must be NULL;
+ * factors_in (iff prob->has_buffer) -> factors_out (iff window > 1), which must not overlap
+ * (callers alternate two buffers). S_T = S0 and Z_T = Z0 may alias as in atlas_mem_step. */
+int atlas_mem_step_factored(const atlas_mem_problem* prob, const atlas_mem_fwd_args* args, const float* factors_in,
+                            float* factors_out, void* stream);
+
+/* The factors the buffer holds after prob->seq_len tokens: the last e-1 of [factors_in; tokens],
+ * i.e. the factored form of atlas_mem_fwd's buffer_out (k [bh, T, d_k], v [bh, T, d_v], gate as
+ * in atlas_mem_fwd_args, S_ref [bh, d_v, d_k]); window >= 2; factors_in iff has_buffer, not
+ * overlapping factors_out. */
+int atlas_buffer_factors(const atlas_mem_problem* prob, const void* k, const void* v, const void* gate,
+                         const float* S_ref, const float* factors_in, float* factors_out, void* stream);
+
+/* factors [bh, slots, d_v + d_k] -> dense [bh, slots, d_v, d_k] (the buffer_in of atlas_mem_fwd and
+ * RNNMemState.omega_buffer). */
+int atlas_buffer_expand(int bh, int slots, int d_v, int d_k, const float* factors, float* dense, void* stream);
+
 /* Backward pass from the forward's `saved` states. Replaces backward_exact
  * (atlas_pytorch/cuda/atlas_omega.cpp:102-136) plus the PyTorch-side chain in
  * AtlasOmegaFunction.backward (atlas_pytorch/cuda/atlas_omega_autograd.py:156-204). */

@@ -185,6 +185,37 @@ def test_step_errors_before_launch(lib):
         assert lib.atlas_mem_step(ctypes.byref(_prob(seq_len=1)), ctypes.byref(a), None) == 5, name
 
 
+def test_factored_buffer_errors_before_launch(lib):
+    # atlas_mem_step_factored / atlas_buffer_factors / atlas_buffer_expand: null, inconsistent,
+    # overlapping and misaligned arguments are rejected before any HIP call
+    good, bad = 0x10000, 0x10008
+    fields = dict(k=good, q=good, v=good, lr=good, decay=good, beta=good, gate=good, S_ref=good, S0=good,
+                  Z0=good, y=good, S_T=good, Z_T=good)
+    args = _lib.FwdArgs(**{k: ctypes.c_void_p(v) for k, v in fields.items()})
+    st = lib.atlas_mem_step_factored
+    p1 = _prob(seq_len=1, has_buffer=1)           # window 4, d 64, bh 32
+    f_in, f_out = ctypes.c_void_p(0x100000), ctypes.c_void_p(0x200000)
+    assert st(ctypes.byref(_prob(seq_len=2)), ctypes.byref(args), f_in, f_out, None) == 2
+    assert st(ctypes.byref(p1), ctypes.byref(args), None, f_out, None) == 4          # has_buffer needs factors_in
+    assert st(ctypes.byref(p1), ctypes.byref(args), f_in, None, None) == 4           # window > 1 needs factors_out
+    assert st(ctypes.byref(p1), ctypes.byref(args), f_in, ctypes.c_void_p(0x100000 + 4096), None) == 9   # overlap
+    assert st(ctypes.byref(p1), ctypes.byref(args), ctypes.c_void_p(bad), f_out, None) == 5
+    dense = _lib.FwdArgs(**{k: ctypes.c_void_p(v) for k, v in dict(fields, buffer_out=good).items()})
+    assert st(ctypes.byref(p1), ctypes.byref(dense), f_in, f_out, None) == 9          # no dense buffer here
+    bf = lib.atlas_buffer_factors
+    k = ctypes.c_void_p(good)
+    assert bf(ctypes.byref(_prob(window=1, has_buffer=0)), k, k, None, k, None, f_out, None) == 2
+    pb = _prob(has_buffer=1)
+    assert bf(ctypes.byref(pb), k, k, k, k, None, f_out, None) == 4                    # has_buffer needs factors_in
+    assert bf(ctypes.byref(pb), k, k, None, k, f_in, f_out, None) == 9                 # lag gates need the gate
+    assert bf(ctypes.byref(pb), k, k, k, k, f_in, f_in, None) == 9                     # in place
+    ex = lib.atlas_buffer_expand
+    assert ex(0, 3, 64, 64, k, k, None) == 2
+    assert ex(2, 0, 64, 64, None, None, None) == 0                                    # nothing to expand
+    assert ex(2, 3, 64, 64, None, k, None) == 4
+    assert ex(2, 3, 64, 64, k, ctypes.c_void_p(bad), None) == 5
+
+
 def test_tensor_map_errors_before_launch(lib):
     good, bad = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x10008)
     f = lib.atlas_tensor_map_fwd
