@@ -80,7 +80,7 @@ struct RegPf {
 
 }  // namespace wb
 
-template <bool MAPE>
+template <bool MAPE, int HC>
 __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const BwdPtrs<bf16> a, const SegGeom sg,
                                                             const BwdSegPtrs p) {
   using namespace wb;
@@ -91,7 +91,7 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (scalar) wave index
   const int gq = lane >> 4, m = lane & 15;
   const int seg = blockIdx.x, bh = blockIdx.y;
-  const int H = g.H;
+  const int H = HC >= 0 ? HC : g.H;
   const int c_begin = seg * sg.G, c_end = min(g.nc, c_begin + sg.G);
   const size_t DD = (size_t)D * D;
   const size_t sbase = (size_t)bh * DD;
@@ -292,7 +292,7 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
   // sum_i S_in[i][k] dy[tau][i], the chunk transition terms, the Grams; operands first, then the
   // matrix products, then the epilogues and LDS stores. Ends by loading the registers of chunk c-1.
   auto phaseA = [&](int c) {
-    const int ln = launder(lane);
+    const int ln = launder(lane) & 63;
     const int gq = ln >> 4, m = ln & 15;
     const Stage& st = sm.st[c & 1];
     const float* rec = st.rec;
@@ -418,7 +418,7 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
   // P tile C[tau][s] = dy delta^T (Lm = K o P, Q' = Ws o P); dDelta tiles C[i][s] =
   // Wz_end dZ_end phi - Ws_end dS_end phi - sum_tau dy Q (hS, hZ, dv)
   auto phaseB = [&](int c) {
-    const int ln = launder(lane);
+    const int ln = launder(lane) & 63;
     const int gq = ln >> 4, m = ln & 15;
     const Stage& st = sm.st[c & 1];
     const float* rec = st.rec;
@@ -453,8 +453,11 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
       az[u] = mma_bf16(fzT[1], fp[u][1], az[u]);
     }
 
+    {
+      float* lp = blk + (unsigned)(SB::LM + (16 * tt + 4 * gq) * SPM + 16 * stm + m);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) blk[SB::LM + (16 * tt + 4 * gq + r) * SPM + 16 * stm + m] = kmat[r] * pm[r];
+      for (int r = 0; r < 4; ++r) lp[r * SPM] = kmat[r] * pm[r];
+    }
     store4<bf16>(&sm.QpT[16 * stm + m][16 * tt + 4 * gq], wt[0] * pm[0], wt[1] * pm[1], wt[2] * pm[2], wt[3] * pm[3]);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -482,7 +485,7 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
   // dphi tiles C[k][s] = Wz_end dZ_end^T delta - Ws_end dS_end^T delta - sum_tau psi Q' + S_ref^T dDelta;
   // dS_ref += dDelta^T phi on the owned tiles; the chunk's scalar-gradient record
   auto phaseC = [&](int c) {
-    const int ln = launder(lane);
+    const int ln = launder(lane) & 63;
     const int gq = ln >> 4, m = ln & 15;
     const Stage& st = sm.st[c & 1];
     const float* rec = st.rec;
@@ -615,25 +618,31 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
 
 size_t walk_bwd_smem_bytes() { return sizeof(wb::Smem); }
 
-hipError_t launch_walk_bwd_kernel(const Geom& g, const BwdPtrs<bf16>& a, const SegGeom& sg, const BwdSegPtrs& p,
-                                  hipStream_t stream) {
+template <bool MAPE, int HC>
+hipError_t launch_walk_bwd_h(const Geom& g, const BwdPtrs<bf16>& a, const SegGeom& sg, const BwdSegPtrs& p,
+                             hipStream_t stream) {
   const size_t smem = sizeof(wb::Smem);
-  hipError_t err;
-  if (g.map_mode == MAP_ELEMENTWISE) {
-    err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_bwd<true>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-    if (err != hipSuccess) return err;
-    hipLaunchKernelGGL((k_walk_bwd<true>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, p);
-  } else {
-    err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_bwd<false>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-    if (err != hipSuccess) return err;
-    hipLaunchKernelGGL((k_walk_bwd<false>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, p);
-  }
+  const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_bwd<MAPE, HC>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL((k_walk_bwd<MAPE, HC>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, p);
   return hipGetLastError();
 }
-
-
+template <bool MAPE>
+hipError_t launch_walk_bwd_m(const Geom& g, const BwdPtrs<bf16>& a, const SegGeom& sg, const BwdSegPtrs& p,
+                             hipStream_t stream) {
+  switch (g.H) {
+    case 0: return launch_walk_bwd_h<MAPE, 0>(g, a, sg, p, stream);
+    case 3: return launch_walk_bwd_h<MAPE, 3>(g, a, sg, p, stream);
+    case 7: return launch_walk_bwd_h<MAPE, 7>(g, a, sg, p, stream);
+    default: return launch_walk_bwd_h<MAPE, -1>(g, a, sg, p, stream);
+  }
+}
+hipError_t launch_walk_bwd_kernel(const Geom& g, const BwdPtrs<bf16>& a, const SegGeom& sg, const BwdSegPtrs& p,
+                                  hipStream_t stream) {
+  return g.map_mode == MAP_ELEMENTWISE ? launch_walk_bwd_m<true>(g, a, sg, p, stream)
+                                       : launch_walk_bwd_m<false>(g, a, sg, p, stream);
+}
 
 // ---------------------------------------------------------------------------------------------
 // Scalar gradients of the specialised path, one wave per 32-token chunk (four chunks per
@@ -707,27 +716,15 @@ __global__ __launch_bounds__(64 * wb::kChainWaves) void k_scalar_chain(const Geo
     be = g.momentum ? to_f32(a.beta[tb + t0 + lane]) : 0.f;
   }
   // direct terms of this lane. Every lane issues the same loads (no load sits in a lane-dependent
-  // branch, so they are all in flight together); the prefix lane's terms come from lane broadcasts.
-  float dG[CH], dA[CH], hz_end;
-  {
-    const int col = src ? lane : 0;
-    float lmv[CH - 1];
+  // branch, so they are all in flight together); the prefix lane's terms come from lane broadcasts
+  // in the reverse loop.
+  const int col = src ? lane : 0;
+  float lmv[CH - 1];
 #pragma unroll
-    for (int t = 0; t < CH - 1; ++t) lmv[t] = blk[SB::LM + (t + 1) * SPM + col];
-    const float fsl = blk[SB::FS + (lane & (CH - 1))], fzl = blk[SB::FZ + (lane & (CH - 1))];
-    const float gram = blk[SB::GRAM + (lane & 3)];
-    const float hs = blk[SB::HS + col], hz = blk[SB::HZ + col];
-#pragma unroll
-    for (int t = 0; t < CH - 1; ++t) {
-      const float fs = lane_bcast(fsl, t + 1), fz = lane_bcast(fzl, t + 1);
-      dG[t] = src ? -lmv[t] : (pre ? -fz : 0.f);
-      dA[t] = pre ? fs : 0.f;
-    }
-    const float gss = lane_bcast(gram, 0), gsz = lane_bcast(gram, 1), gzz = lane_bcast(gram, 2);
-    dG[CH - 1] = src ? -hs : (pre ? -gsz : 0.f);
-    dA[CH - 1] = pre ? gss : 0.f;
-    hz_end = src ? hz : (pre ? gzz : 0.f);
-  }
+  for (int t = 0; t < CH - 1; ++t) lmv[t] = blk[SB::LM + (t + 1) * SPM + col];
+  const float fsl = blk[SB::FS + (lane & (CH - 1))], fzl = blk[SB::FZ + (lane & (CH - 1))];
+  const float gram = blk[SB::GRAM + (lane & 3)];
+  const float hs = blk[SB::HS + col], hz = blk[SB::HZ + col];
 
   // window weights of the sources: W[s][t] = w(s, t) for j = t + H - s in [0, e)
   for (int idx = lane; idx < NSRC * RP; idx += 64) (&U.W[0][0])[idx] = 0.f;
@@ -752,36 +749,61 @@ __global__ __launch_bounds__(64 * wb::kChainWaves) void k_scalar_chain(const Geo
   __builtin_amdgcn_wave_barrier();
 
   // forward
-  float wsp[CH], wzc[CH], wzp[CH], ap[CH];
+  float wsp[CH], wzc[CH], wzp[CH];
   {
-    float wz = pre ? 1.f : 0.f, ws = 0.f, av = 1.f;
+    float wz = pre ? 1.f : 0.f, ws = 0.f;
 #pragma unroll
     for (int t = 0; t < CH; ++t) {
       const float A = lane_bcast(al, t), E = lane_bcast(et, t), B = lane_bcast(be, t);
       wzp[t] = wz;
       wsp[t] = ws;
-      ap[t] = av;
       wz = B * wz + wrow[t];
       ws = A * ws + E * wz;
-      av = A * av;
       wzc[t] = wz;
     }
   }
-  // reverse (branch-free: masked stores go to a dummy slot)
+  // a_{t-1} = prod_{tau < t} alpha_tau in lane t (an exclusive product scan over the lanes; it is the
+  // same for every source, so it is broadcast per step instead of held in 32 registers per lane)
+  float apl = al;
+#pragma unroll
+  for (int d = 1; d < CH; d <<= 1) {
+    const float y = __shfl_up(apl, d, 64);
+    if (lane >= d) apl *= y;
+  }
   {
+    const float sh = __shfl_up(apl, 1, 64);
+    apl = lane == 0 ? 1.f : sh;
+  }
+  // reverse (branch-free: masked stores go to a dummy slot). The step scalars are broadcast again
+  // from laundered copies, so that the forward loop's broadcasts are not held in scalar registers
+  // across both loops; the direct terms G_t, Ga_t are formed per step.
+  {
+    const float alr = launder_f(al), ber = launder_f(be), etr = launder_f(et);
+    const float gss = lane_bcast(gram, 0), gsz = lane_bcast(gram, 1), gzz = lane_bcast(gram, 2);
+    const float hz_end = src ? hz : (pre ? gzz : 0.f);
     const bool live = lane <= NSRC;
     const bool quad_head = (lane & 3) == 0 && lane < 4 * NQD;
     const int qrow = quad_head ? (lane >> 2) : QDP - 1;   // column QDP - 1 is never read
     float gws = 0.f, gwz = 0.f, ga = 0.f;
 #pragma unroll
     for (int t = CH - 1; t >= 0; --t) {
-      const float A1 = t + 1 < CH ? lane_bcast(al, t + 1) : 0.f;
-      const float B1 = t + 1 < CH ? lane_bcast(be, t + 1) : 0.f;
-      const float E = lane_bcast(et, t);
-      gws = dG[t] + A1 * gws;
+      const float A1 = t + 1 < CH ? lane_bcast(alr, t + 1) : 0.f;
+      const float B1 = t + 1 < CH ? lane_bcast(ber, t + 1) : 0.f;
+      const float E = lane_bcast(etr, t);
+      float dG, dA;
+      if (t < CH - 1) {   // compile-time branch; the broadcasts stay outside lane-dependent selects
+        const float fs = lane_bcast(fsl, t + 1), fz = lane_bcast(fzl, t + 1);
+        dG = src ? -lmv[t] : (pre ? -fz : 0.f);
+        dA = pre ? fs : 0.f;
+      } else {
+        dG = src ? -hs : (pre ? -gsz : 0.f);
+        dA = pre ? gss : 0.f;
+      }
+      gws = dG + A1 * gws;
       gwz = (t == CH - 1 ? hz_end : 0.f) + E * gws + B1 * gwz;
-      ga = dA[t] + A1 * ga;
-      const float ca = quad_sum(live ? gws * wsp[t] + ga * ap[t] : 0.f);
+      ga = dA + A1 * ga;
+      const float apt = lane_bcast(apl, t);
+      const float ca = quad_sum(live ? gws * wsp[t] + ga * apt : 0.f);
       const float ce = quad_sum(live ? gws * wzc[t] : 0.f);
       const float cb = quad_sum(live ? gwz * wzp[t] : 0.f);
       U.r.red[0][t][qrow] = ca;

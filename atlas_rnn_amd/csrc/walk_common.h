@@ -142,6 +142,10 @@ __device__ __forceinline__ int launder(int x) {
   asm volatile("" : "+v"(x));
   return x;
 }
+__device__ __forceinline__ float launder_f(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 __device__ __forceinline__ bf16x8 frag_row_l(const bf16* p, int ld, int r0, int k0, int l) {
   return *reinterpret_cast<const bf16x8*>(p + (r0 + (l & 15)) * ld + k0 + 8 * (l >> 4));
 }
