@@ -9,8 +9,9 @@
 //                   nv_b[r] = (v - S_ref phi)[:, 64 i ..], the product on the fp32 matrix cores
 //   k_block_merge : its adjoint per token: dphi = sum_i dphi_b[(i, j)] | ... - S_ref^T dnv, dpsi likewise,
 //                   dv = dnv = sum_j dnv_b[(i, j)]
-//   k_block_dsref : per-512-token partials of dS_ref = -sum_t dnv_t phi_t^T
-// One workgroup (256 threads) per 64 tokens of one row (dS_ref: per 512); rows move in 16-byte vectors.
+//   k_block_dsref : per-256-token partials of dS_ref = -sum_t dnv_t phi_t^T, one workgroup per 64 x 64 block
+// One workgroup (256 threads) per 64 tokens of one row (dS_ref: per 256 tokens and block); rows move in
+// 16-byte vectors; LDS is sized by the blocks present (the merge's S_ref^T dnv reuses the S_ref tile).
 #include <hip/hip_runtime.h>
 
 #include "../../include/atlas_mem.h"
@@ -22,7 +23,7 @@ namespace blk {
 constexpr int kThreads = 256;
 constexpr int TT = 64;            // tokens per tile
 constexpr int B = 64;             // block width
-constexpr int kPartTiles = 8;     // tiles per dS_ref partial (512 tokens)
+constexpr int kPartTiles = 4;     // tiles per dS_ref partial (256 tokens)
 constexpr int MaxD = 256;         // d_k, d_v <= 256
 constexpr int P = B + 4;          // LDS pitch (fp32), 16-byte aligned rows
 typedef MM<float> M;
@@ -85,9 +86,9 @@ __global__ __launch_bounds__(blk::kThreads) void k_block_split(int BH, int Tn, i
                                                                const float* __restrict__ S_ref, T* __restrict__ phi_b,
                                                                T* __restrict__ psi_b, T* __restrict__ nv_b) {
   using namespace blk;
-  __shared__ __align__(16) float sx[TT][P];   // phi columns 64 kb .. of the tile
+  __shared__ __align__(16) float sx[TT][P];   // phi columns 64 kb .. of the tile; then S_ref phi of block i
   __shared__ __align__(16) float sr[B][P];    // S_ref rows 64 i .., columns 64 kb ..
-  __shared__ __align__(16) float sy[TT][P];   // nv block i of the tile
+  float (*sy)[P] = sx;
   const int t0 = blockIdx.x * TT, bh = blockIdx.y, tid = threadIdx.x, l = lane_id(), w = wave_id();
   const int nt = min(TT, Tn - t0);
   const int nbk = dk / B, nbv = dv / B;
@@ -120,6 +121,7 @@ __global__ __launch_bounds__(blk::kThreads) void k_block_split(int BH, int Tn, i
         for (int k0 = 0; k0 < B; k0 += 4)
           acc[n] = M::mma(sx[16 * w + (l & 15)][k0 + (l >> 4)], sr[16 * n + (l & 15)][k0 + (l >> 4)], acc[n]);
     }
+    __syncthreads();   // sy aliases sx
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
@@ -145,12 +147,15 @@ __global__ __launch_bounds__(blk::kThreads) void k_block_merge(int BH, int Tn, i
                                                                const T* __restrict__ dnv_b, T* __restrict__ dphi,
                                                                T* __restrict__ dpsi, T* __restrict__ dv_out) {
   using namespace blk;
-  __shared__ __align__(16) float sd[MaxD / B][TT][P];   // dnv of the tile, every value block i
-  __shared__ __align__(16) float sr[B][P];              // S_ref block (i, kb)
-  __shared__ __align__(16) float sk[TT][P];             // (S_ref^T dnv)[t][kb block]
+  // dynamic LDS: sd[nbv][TT][P] (dnv of the tile, every value block i), then sr[B][P] (S_ref block
+  // (i, kb)), which sk[TT][P] ((S_ref^T dnv)[t][kb block]) reuses once the block's products are done
+  extern __shared__ __align__(16) float blk_smem[];
   const int t0 = blockIdx.x * TT, bh = blockIdx.y, tid = threadIdx.x, l = lane_id(), w = wave_id();
   const int nt = min(TT, Tn - t0);
   const int nbk = dk / B, nbv = dv / B;
+  float (*sd)[TT][P] = reinterpret_cast<float (*)[TT][P]>(blk_smem);
+  float (*sr)[P] = reinterpret_cast<float (*)[P]>(blk_smem + (size_t)nbv * TT * P);
+  float (*sk)[P] = sr;
   auto row = [&](int i, int j, int t) { return (((size_t)(i * nbk + j) * BH + bh) * Tn + t0 + t) * B; };
   for (int i = 0; i < nbv; ++i)
     for (int u = tid; u < TT * (B / 8); u += blk::kThreads) {
@@ -193,6 +198,7 @@ __global__ __launch_bounds__(blk::kThreads) void k_block_merge(int BH, int Tn, i
         for (int k0 = 0; k0 < B; k0 += 4)
           acc[n] = M::mma(sd[i][16 * w + (l & 15)][k0 + (l >> 4)], sr[k0 + (l >> 4)][16 * n + (l & 15)], acc[n]);
     }
+    __syncthreads();   // sk aliases sr
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
@@ -214,8 +220,8 @@ __global__ __launch_bounds__(blk::kThreads) void k_block_merge(int BH, int Tn, i
   }
 }
 
-// dS_ref partials: part p of row bh covers tokens [512 p, 512 p + 512): out[a][c] = -sum_t dv[t][a] phi[t][c]
-// (dv: the merged dnv). Wave w owns value tile 16 w .. of each 64 x 64 (i, kb) block.
+// dS_ref partials: part p of row bh covers tokens [256 p, 256 p + 256): out[a][c] = -sum_t dv[t][a] phi[t][c]
+// (dv: the merged dnv) for the 64 x 64 block (i, kb) = blockIdx.z; wave w owns value rows 16 w ..
 template <typename T>
 __global__ __launch_bounds__(blk::kThreads) void k_block_dsref(int BH, int Tn, int dk, int dv, const T* __restrict__ phi,
                                                                const T* __restrict__ dvv, float* __restrict__ part) {
@@ -223,32 +229,30 @@ __global__ __launch_bounds__(blk::kThreads) void k_block_dsref(int BH, int Tn, i
   __shared__ __align__(16) float sd[TT][P];
   __shared__ __align__(16) float sx[TT][P];
   const int p = blockIdx.x, bh = blockIdx.y, l = lane_id(), w = wave_id();
-  const int nbk = dk / B, nbv = dv / B, n_parts = gridDim.x;
-  for (int i = 0; i < nbv; ++i)
-    for (int kb = 0; kb < nbk; ++kb) {
-      f32x4 acc[4];
+  const int nbk = dk / B, n_parts = gridDim.x;
+  const int i = blockIdx.z / nbk, kb = blockIdx.z % nbk;
+  f32x4 acc[4];
 #pragma unroll
-      for (int n = 0; n < 4; ++n) acc[n] = zero4();
-      for (int tile = 0; tile < kPartTiles; ++tile) {
-        const int t0 = (p * kPartTiles + tile) * TT;
-        if (t0 >= Tn) break;   // workgroup-uniform
-        const int nt = min(TT, Tn - t0);
-        __syncthreads();
-        tile_in(sd, dvv + ((size_t)bh * Tn + t0) * dv + i * B, dv, TT, nt);
-        tile_in(sx, phi + ((size_t)bh * Tn + t0) * dk + kb * B, dk, TT, nt);
-        __syncthreads();
+  for (int n = 0; n < 4; ++n) acc[n] = zero4();
+  for (int tile = 0; tile < kPartTiles; ++tile) {
+    const int t0 = (p * kPartTiles + tile) * TT;
+    if (t0 >= Tn) break;   // workgroup-uniform
+    const int nt = min(TT, Tn - t0);
+    __syncthreads();
+    tile_in(sd, dvv + ((size_t)bh * Tn + t0) * dv + i * B, dv, TT, nt);
+    tile_in(sx, phi + ((size_t)bh * Tn + t0) * dk + kb * B, dk, TT, nt);
+    __syncthreads();
 #pragma unroll
-        for (int n = 0; n < 4; ++n)
-          for (int k0 = 0; k0 < TT; k0 += 4)
-            acc[n] = M::mma(sd[k0 + (l >> 4)][16 * w + (l & 15)], sx[k0 + (l >> 4)][16 * n + (l & 15)], acc[n]);
-      }
-      float* dst = part + ((size_t)bh * n_parts + p) * dv * dk;
+    for (int n = 0; n < 4; ++n)
+      for (int k0 = 0; k0 < TT; k0 += 4)
+        acc[n] = M::mma(sd[k0 + (l >> 4)][16 * w + (l & 15)], sx[k0 + (l >> 4)][16 * n + (l & 15)], acc[n]);
+  }
+  float* dst = part + ((size_t)bh * n_parts + p) * dv * dk;
 #pragma unroll
-      for (int n = 0; n < 4; ++n)
+  for (int n = 0; n < 4; ++n)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          dst[(size_t)(i * B + 16 * w + 4 * (l >> 4) + q) * dk + kb * B + 16 * n + (l & 15)] = -acc[n][q];
-    }
+    for (int q = 0; q < 4; ++q)
+      dst[(size_t)(i * B + 16 * w + 4 * (l >> 4) + q) * dk + kb * B + 16 * n + (l & 15)] = -acc[n][q];
 }
 
 }  // namespace atlas
@@ -296,16 +300,21 @@ int atlas_block_merge(int dtype, int bh, int seq_len, int d_k, int d_v, const vo
   for (const void* p : {phi, (const void*)S_ref, dphi_b, dpsi_b, dnv_b, (const void*)dphi, (const void*)dpsi,
                         (const void*)dv, (const void*)dsref_part})
     if (blk_misaligned(p)) return ATLAS_MEM_ERR_ALIGN;
-  const dim3 grid((seq_len + blk::TT - 1) / blk::TT, bh), pgrid(atlas_block_parts(seq_len), bh);
+  const dim3 grid((seq_len + blk::TT - 1) / blk::TT, bh), pgrid(atlas_block_parts(seq_len), bh, (d_v / blk::B) * (d_k / blk::B));
+  const size_t smem = ((size_t)(d_v / blk::B) * blk::TT + blk::B) * blk::P * sizeof(float);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const void* mk = dtype == ATLAS_DT_BF16 ? reinterpret_cast<const void*>(&k_block_merge<bf16>)
+                                          : reinterpret_cast<const void*>(&k_block_merge<float>);
+  if (hipFuncSetAttribute(mk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+    return ATLAS_MEM_ERR_LAUNCH;
   if (dtype == ATLAS_DT_BF16) {
-    hipLaunchKernelGGL(k_block_merge<bf16>, grid, dim3(blk::kThreads), 0, s, bh, seq_len, d_k, d_v, S_ref,
+    hipLaunchKernelGGL(k_block_merge<bf16>, grid, dim3(blk::kThreads), smem, s, bh, seq_len, d_k, d_v, S_ref,
                        (const bf16*)dphi_b, (const bf16*)dpsi_b, (const bf16*)dnv_b, (bf16*)dphi, (bf16*)dpsi,
                        (bf16*)dv);
     hipLaunchKernelGGL(k_block_dsref<bf16>, pgrid, dim3(blk::kThreads), 0, s, bh, seq_len, d_k, d_v,
                        (const bf16*)phi, (const bf16*)dv, dsref_part);
   } else {
-    hipLaunchKernelGGL(k_block_merge<float>, grid, dim3(blk::kThreads), 0, s, bh, seq_len, d_k, d_v, S_ref,
+    hipLaunchKernelGGL(k_block_merge<float>, grid, dim3(blk::kThreads), smem, s, bh, seq_len, d_k, d_v, S_ref,
                        (const float*)dphi_b, (const float*)dpsi_b, (const float*)dnv_b, (float*)dphi, (float*)dpsi,
                        (float*)dv);
     hipLaunchKernelGGL(k_block_dsref<float>, pgrid, dim3(blk::kThreads), 0, s, bh, seq_len, d_k, d_v,
