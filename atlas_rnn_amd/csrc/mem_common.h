@@ -180,6 +180,41 @@ __device__ __forceinline__ float row_sum16(float x) {
   return x;
 }
 
+// Eight consecutive values as fp32 (16 bytes of bf16 or 32 of fp32; 16-byte aligned p).
+template <typename T>
+__device__ __forceinline__ void ld8(const T* p, float* v) {
+  if constexpr (sizeof(T) == 2) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const unsigned w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      v[2 * h] = __builtin_bit_cast(float, w[h] << 16);
+      v[2 * h + 1] = __builtin_bit_cast(float, w[h] & 0xffff0000u);
+    }
+  } else {
+    const float4 x = reinterpret_cast<const float4*>(p)[0], y = reinterpret_cast<const float4*>(p)[1];
+    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w; v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+  }
+}
+template <typename T>
+__device__ __forceinline__ void st8(T* p, const float* v) {
+  if constexpr (sizeof(T) == 2) {
+    typedef __bf16 bf16x2_ __attribute__((ext_vector_type(2)));
+    unsigned w[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      bf16x2_ b;
+      b[0] = static_cast<__bf16>(v[2 * h]);
+      b[1] = static_cast<__bf16>(v[2 * h + 1]);
+      w[h] = __builtin_bit_cast(unsigned, b);
+    }
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
 // Clamp of the reference (torch.clamp(-100, 100)) and its gradient mask (min <= x <= max).
 __device__ __forceinline__ float clamp100(float x) { return fminf(fmaxf(x, -100.f), 100.f); }
 __device__ __forceinline__ float clamp_mask(float x) { return (x >= -100.f && x <= 100.f) ? 1.f : 0.f; }

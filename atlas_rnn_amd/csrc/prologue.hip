@@ -17,6 +17,8 @@
 // reductions (RMS over dim, the RMSNorm adjoint's dot product) go through LDS.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "../../include/atlas_mem.h"
 #include "mem_common.h"
 
@@ -35,79 +37,109 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// inverse RMS of x[b, t, :] for t in [tb, te) into sinv[t - tb] (one wave per token).
+// inverse RMS of x[b, t, :] for t in [tb, te) into sinv[t - tb]: one wave per token, eight channels
+// (one 16-byte vector of bf16) per lane.
 template <typename T>
 __device__ __forceinline__ void token_inv_rms(const T* xb, int dim, float eps, int tb, int te, float* sinv) {
   const int lane = lane_id(), w = wave_id();
   for (int t = tb + w; t < te; t += pro::kThreads / 64) {
     const T* row = xb + (size_t)t * dim;
     float s = 0.f;
-    for (int c = lane; c < dim; c += 64) {
-      const float v = to_f32(row[c]);
-      s += v * v;
+    for (int c8 = lane * 8; c8 < dim; c8 += 512) {
+      float v[8];
+      ld8(row + c8, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += v[e] * v[e];
     }
     s = wave_sum(s);
     if (lane == 0) sinv[t - tb] = rsqrtf(s / (float)dim + eps);
   }
 }
 
-// Forward of RMSNorm + the three depthwise convolutions. wq / wk / wv: [dim][K] (null: no conv,
-// then only xn is written). inv_rms [B][T] is saved for the backward.
-template <typename T>
-__global__ __launch_bounds__(pro::kThreads) void k_pro_fwd(int Tn, int dim, int K, int pad, float eps,
-                                                           const T* __restrict__ x, const T* __restrict__ wn,
-                                                           const T* __restrict__ wq, const T* __restrict__ wk,
-                                                           const T* __restrict__ wv, T* __restrict__ xn,
-                                                           T* __restrict__ qi, T* __restrict__ ki, T* __restrict__ vi,
+// the K taps of eight channels c8 .. c8 + 7 of a [dim][K] tap array, as tap[j][e]
+template <typename T, int KT>
+__device__ __forceinline__ void load_taps(const T* w, int c8, float (&tap)[KT > 0 ? KT : 1][8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int j = 0; j < KT; ++j) tap[j][e] = to_f32(w[(size_t)(c8 + e) * KT + j]);
+}
+
+// Forward of RMSNorm + the three depthwise convolutions (KT taps, 0: no conv, then only xn is
+// written). inv_rms [B][T] is saved for the backward. Workgroup: 16 tokens of one batch row; lane l
+// of wave w handles channels 8 l .. (every 512 channels) of tokens w, w + 4, ... with 16-byte accesses.
+template <typename T, int KT>
+__global__ __launch_bounds__(pro::kThreads) void k_pro_fwd(int Tn, int dim, float eps, const T* __restrict__ x,
+                                                           const T* __restrict__ wn, const T* __restrict__ wq,
+                                                           const T* __restrict__ wk, const T* __restrict__ wv,
+                                                           T* __restrict__ xn, T* __restrict__ qi,
+                                                           T* __restrict__ ki, T* __restrict__ vi,
                                                            float* __restrict__ inv_rms) {
+  constexpr int pad = KT / 2;
   __shared__ float sinv[pro::kTok + 2 * pro::kHalo];
-  const int t0 = blockIdx.x * pro::kTok, b = blockIdx.y, tid = threadIdx.x;
+  const int t0 = blockIdx.x * pro::kTok, b = blockIdx.y, tid = threadIdx.x, lane = lane_id(), w = wave_id();
   const int t1 = min(Tn, t0 + pro::kTok);
-  const bool conv = wq != nullptr;
   // tokens whose normalised values this tile reads: [t0 - pad, t1 - 1 + K - 1 - pad]
-  const int hb = conv ? max(0, t0 - pad) : t0, he = conv ? min(Tn, t1 + K - 1 - pad) : t1;
+  const int hb = KT ? max(0, t0 - pad) : t0, he = KT ? min(Tn, t1 + KT - 1 - pad) : t1;
   const int base = t0 - pro::kHalo;   // sinv index = t - base
   const T* xb = x + (size_t)b * Tn * dim;
   token_inv_rms(xb, dim, eps, hb, he, sinv + (hb - base));
   __syncthreads();
   for (int t = t0 + tid; t < t1; t += pro::kThreads) inv_rms[(size_t)b * Tn + t] = sinv[t - base];
   const size_t ob = (size_t)b * Tn * dim;
-  for (int c = tid; c < dim; c += pro::kThreads) {
-    const float w = to_f32(wn[c]);
-    float tq[pro::kMaxK], tk[pro::kMaxK], tv[pro::kMaxK];
-    if (conv) {
-      for (int j = 0; j < K; ++j) {
-        tq[j] = to_f32(wq[c * K + j]);
-        tk[j] = to_f32(wk[c * K + j]);
-        tv[j] = to_f32(wv[c * K + j]);
-      }
+  for (int c8 = lane * 8; c8 < dim; c8 += 512) {
+    float wv8[8];
+    ld8(wn + c8, wv8);
+    float tq[KT > 0 ? KT : 1][8], tk[KT > 0 ? KT : 1][8], tv[KT > 0 ? KT : 1][8];
+    if constexpr (KT > 0) {
+      load_taps<T, KT>(wq, c8, tq);
+      load_taps<T, KT>(wk, c8, tk);
+      load_taps<T, KT>(wv, c8, tv);
     }
-    for (int t = t0; t < t1; ++t) {
-      xn[ob + (size_t)t * dim + c] = from_f32<T>(to_f32(xb[(size_t)t * dim + c]) * sinv[t - base] * w);
-      if (!conv) continue;
-      float aq = 0.f, ak = 0.f, av = 0.f;
-      for (int j = 0; j < K; ++j) {
-        const int s = t + j - pad;
-        if (s < 0 || s >= Tn) continue;
-        const float v = to_f32(xb[(size_t)s * dim + c]) * sinv[s - base] * w;
-        aq += tq[j] * v;
-        ak += tk[j] * v;
-        av += tv[j] * v;
+    for (int t = t0 + w; t < t1; t += pro::kThreads / 64) {
+      float xv[8];
+      ld8(xb + (size_t)t * dim + c8, xv);
+      const float it = sinv[t - base];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[e] *= it * wv8[e];
+      st8(xn + ob + (size_t)t * dim + c8, xv);
+      if constexpr (KT > 0) {
+        float aq[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, ak[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f},
+              av[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < KT; ++j) {
+          const int s = t + j - pad;
+          if (s < 0 || s >= Tn) continue;
+          float xs[8];
+          ld8(xb + (size_t)s * dim + c8, xs);
+          const float is = sinv[s - base];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float v = xs[e] * is * wv8[e];
+            aq[e] += tq[j][e] * v;
+            ak[e] += tk[j][e] * v;
+            av[e] += tv[j][e] * v;
+          }
+        }
+        st8(qi + ob + (size_t)t * dim + c8, aq);
+        st8(ki + ob + (size_t)t * dim + c8, ak);
+        st8(vi + ob + (size_t)t * dim + c8, av);
       }
-      qi[ob + (size_t)t * dim + c] = from_f32<T>(aq);
-      ki[ob + (size_t)t * dim + c] = from_f32<T>(ak);
-      vi[ob + (size_t)t * dim + c] = from_f32<T>(av);
     }
   }
 }
 
 // Adjoint of k_pro_fwd. dxn: gradient reaching xn directly (the gate heads; with no conv also the
 // projections); dqi / dki / dvi: gradients of the conv outputs (null without conv). Writes dx and
-// per-workgroup partials dwn_part [nwg][dim], dwc_part [nwg][3][dim][K] (nwg = gridDim.x * gridDim.y).
+// partials dwn_part [nwg][dim], dwc_part [nwg][3][dim][K], nwg = B * ceil(T / 16): workgroup = 64
+// tokens of one batch row, wave w owns the 16-token block 4 blockIdx.x + w (partial row
+// b * ceil(T / 16) + block) and all channels, eight per lane.
 //   u[t, c]  = w[c] * g[t, c],  g = dxn + sum_j taps[c][j] dconv[t - j + pad]   (the conv's transpose)
 //   dx[t, c] = inv_t u[t, c] - x[t, c] inv_t^3 (sum_c' u[t, c'] x[t, c']) / dim
-template <typename T>
-__global__ __launch_bounds__(pro::kThreads) void k_pro_bwd(int Tn, int dim, int K, int pad, const T* __restrict__ x,
+// Three passes over the block: A (g: the dot products and the norm-weight partials), B (g again: dx),
+// C (the tap partials), so that taps and tap partials are never live together.
+template <typename T, int KT>
+__global__ __launch_bounds__(pro::kThreads) void k_pro_bwd(int Tn, int dim, const T* __restrict__ x,
                                                            const T* __restrict__ wn, const T* __restrict__ wq,
                                                            const T* __restrict__ wk, const T* __restrict__ wv,
                                                            const float* __restrict__ inv_rms,
@@ -115,220 +147,282 @@ __global__ __launch_bounds__(pro::kThreads) void k_pro_bwd(int Tn, int dim, int 
                                                            const T* __restrict__ dki, const T* __restrict__ dvi,
                                                            T* __restrict__ dx, float* __restrict__ dwn_part,
                                                            float* __restrict__ dwc_part) {
-  __shared__ float sdot[pro::kThreads / 64][pro::kTok];
-  const int t0 = blockIdx.x * pro::kTok, b = blockIdx.y, tid = threadIdx.x, lane = lane_id(), wv_ = wave_id();
-  const int t1 = min(Tn, t0 + pro::kTok), nt = t1 - t0;
-  const int wg = blockIdx.y * gridDim.x + blockIdx.x;
-  const bool conv = wq != nullptr;
-  const size_t ob = (size_t)b * Tn * dim;
+  constexpr int pad = KT / 2, KA = KT > 0 ? KT : 1;
+  const int lane = lane_id(), w = wave_id();
+  const int b = blockIdx.y, ntb = (Tn + pro::kTok - 1) / pro::kTok;
+  const int blk = blockIdx.x * (pro::kThreads / 64) + w;
+  if (blk >= ntb) return;   // wave-uniform; no barriers in this kernel
+  const int t0 = blk * pro::kTok, t1 = min(Tn, t0 + pro::kTok);
+  const size_t ob = (size_t)b * Tn * dim, prow = (size_t)b * ntb + blk;
   const float* inv = inv_rms + (size_t)b * Tn;
+  const T* xb = x + ob;
+  // g[t, c8 .. c8 + 7] = dxn + the conv's transpose
+  auto gvec = [&](int t, int c8, const float (&tq)[KA][8], const float (&tk)[KA][8], const float (&tv)[KA][8],
+                  float (&g)[8]) {
+    ld8(dxn + ob + (size_t)t * dim + c8, g);
+    if constexpr (KT > 0) {
+#pragma unroll
+      for (int j = 0; j < KT; ++j) {
+        const int u = t - j + pad;   // xn[t] feeds output u
+        if (u < 0 || u >= Tn) continue;
+        float a[8], c[8], d[8];
+        const size_t ou = ob + (size_t)u * dim + c8;
+        ld8(dqi + ou, a);
+        ld8(dki + ou, c);
+        ld8(dvi + ou, d);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) g[e] += tq[j][e] * a[e] + tk[j][e] * c[e] + tv[j][e] * d[e];
+      }
+    }
+  };
   float dot[pro::kTok];
 #pragma unroll
   for (int i = 0; i < pro::kTok; ++i) dot[i] = 0.f;
-  // pass A: dot products, norm-weight and tap partials
-  for (int c = tid; c < dim; c += pro::kThreads) {
-    const float w = to_f32(wn[c]);
-    float tq[pro::kMaxK], tk[pro::kMaxK], tv[pro::kMaxK], gq[pro::kMaxK], gk[pro::kMaxK], gv[pro::kMaxK];
-    for (int j = 0; j < K; ++j) {
-      tq[j] = conv ? to_f32(wq[c * K + j]) : 0.f;
-      tk[j] = conv ? to_f32(wk[c * K + j]) : 0.f;
-      tv[j] = conv ? to_f32(wv[c * K + j]) : 0.f;
-      gq[j] = gk[j] = gv[j] = 0.f;
+  // pass A
+  for (int c8 = lane * 8; c8 < dim; c8 += 512) {
+    float wv8[8], tq[KA][8], tk[KA][8], tv[KA][8], dw[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    ld8(wn + c8, wv8);
+    if constexpr (KT > 0) {
+      load_taps<T, KT>(wq, c8, tq);
+      load_taps<T, KT>(wk, c8, tk);
+      load_taps<T, KT>(wv, c8, tv);
     }
-    float dw = 0.f;
 #pragma unroll
     for (int i = 0; i < pro::kTok; ++i) {
       const int t = t0 + i;
       if (t >= t1) break;
-      const size_t o = ob + (size_t)t * dim + c;
-      const float xv = to_f32(x[o]);
-      float g = to_f32(dxn[o]);
-      if (conv) {
-        const float dq = to_f32(dqi[o]), dk = to_f32(dki[o]), dv = to_f32(dvi[o]);
-        for (int j = 0; j < K; ++j) {
-          // the conv's transpose: xn[t] feeds outputs u = t - j + pad
-          const int u = t - j + pad;
-          if (u >= 0 && u < Tn) {
-            const size_t ou = ob + (size_t)u * dim + c;
-            g += tq[j] * to_f32(dqi[ou]) + tk[j] * to_f32(dki[ou]) + tv[j] * to_f32(dvi[ou]);
-          }
-          // taps: output t reads xn[t + j - pad]
-          const int s = t + j - pad;
-          if (s >= 0 && s < Tn) {
-            const float xs = to_f32(x[ob + (size_t)s * dim + c]) * inv[s] * w;
-            gq[j] += dq * xs;
-            gk[j] += dk * xs;
-            gv[j] += dv * xs;
-          }
-        }
-      }
-      dw += g * xv * inv[t];
-      dot[i] += w * g * xv;
-    }
-    dwn_part[(size_t)wg * dim + c] = dw;
-    if (conv) {
-      float* p = dwc_part + (size_t)wg * 3 * dim * K;
-      for (int j = 0; j < K; ++j) {
-        p[(size_t)c * K + j] = gq[j];
-        p[(size_t)(dim + c) * K + j] = gk[j];
-        p[(size_t)(2 * dim + c) * K + j] = gv[j];
+      float g[8], xv[8];
+      gvec(t, c8, tq, tk, tv, g);
+      ld8(xb + (size_t)t * dim + c8, xv);
+      const float it = inv[t];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        dw[e] += g[e] * xv[e] * it;
+        dot[i] += wv8[e] * g[e] * xv[e];
       }
     }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dwn_part[prow * dim + c8 + e] = dw[e];
   }
 #pragma unroll
-  for (int i = 0; i < pro::kTok; ++i) {
-    const float s = wave_sum(dot[i]);
-    if (lane == 0) sdot[wv_][i] = s;
-  }
-  __syncthreads();
-  // pass B: dx (recomputing u)
-  for (int c = tid; c < dim; c += pro::kThreads) {
-    const float w = to_f32(wn[c]);
-    float tq[pro::kMaxK], tk[pro::kMaxK], tv[pro::kMaxK];
-    for (int j = 0; j < K; ++j) {
-      tq[j] = conv ? to_f32(wq[c * K + j]) : 0.f;
-      tk[j] = conv ? to_f32(wk[c * K + j]) : 0.f;
-      tv[j] = conv ? to_f32(wv[c * K + j]) : 0.f;
+  for (int i = 0; i < pro::kTok; ++i) dot[i] = wave_sum(dot[i]);
+  // pass B: dx
+  for (int c8 = lane * 8; c8 < dim; c8 += 512) {
+    float wv8[8], tq[KA][8], tk[KA][8], tv[KA][8];
+    ld8(wn + c8, wv8);
+    if constexpr (KT > 0) {
+      load_taps<T, KT>(wq, c8, tq);
+      load_taps<T, KT>(wk, c8, tk);
+      load_taps<T, KT>(wv, c8, tv);
     }
-    for (int i = 0; i < nt; ++i) {
+#pragma unroll
+    for (int i = 0; i < pro::kTok; ++i) {
       const int t = t0 + i;
-      const size_t o = ob + (size_t)t * dim + c;
-      float g = to_f32(dxn[o]);
-      if (conv) {
-        for (int j = 0; j < K; ++j) {
-          const int u = t - j + pad;
-          if (u >= 0 && u < Tn) {
-            const size_t ou = ob + (size_t)u * dim + c;
-            g += tq[j] * to_f32(dqi[ou]) + tk[j] * to_f32(dki[ou]) + tv[j] * to_f32(dvi[ou]);
+      if (t >= t1) break;
+      float g[8], xv[8];
+      gvec(t, c8, tq, tk, tv, g);
+      ld8(xb + (size_t)t * dim + c8, xv);
+      const float it = inv[t], c3 = it * it * it * dot[i] / (float)dim;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g[e] = it * wv8[e] * g[e] - xv[e] * c3;
+      st8(dx + ob + (size_t)t * dim + c8, g);
+    }
+  }
+  // pass C: tap partials, output t reads xn[t + j - pad]
+  if constexpr (KT > 0) {
+    for (int c8 = lane * 8; c8 < dim; c8 += 512) {
+      float wv8[8], gq[KT][8], gk[KT][8], gv[KT][8];
+      ld8(wn + c8, wv8);
+#pragma unroll
+      for (int j = 0; j < KT; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gq[j][e] = gk[j][e] = gv[j][e] = 0.f;
+      for (int t = t0; t < t1; ++t) {
+        float dq[8], dk[8], dv[8];
+        const size_t o = ob + (size_t)t * dim + c8;
+        ld8(dqi + o, dq);
+        ld8(dki + o, dk);
+        ld8(dvi + o, dv);
+#pragma unroll
+        for (int j = 0; j < KT; ++j) {
+          const int s = t + j - pad;
+          if (s < 0 || s >= Tn) continue;
+          float xs[8];
+          ld8(xb + (size_t)s * dim + c8, xs);
+          const float is = inv[s];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float v = xs[e] * is * wv8[e];
+            gq[j][e] += dq[e] * v;
+            gk[j][e] += dk[e] * v;
+            gv[j][e] += dv[e] * v;
           }
         }
       }
-      const float it = inv[t];
-      const float d = sdot[0][i] + sdot[1][i] + sdot[2][i] + sdot[3][i];
-      dx[o] = from_f32<T>(it * w * g - to_f32(x[o]) * it * it * it * d / (float)dim);
+      float* p = dwc_part + prow * 3 * dim * KT;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int j = 0; j < KT; ++j) {
+          p[(size_t)(c8 + e) * KT + j] = gq[j][e];
+          p[(size_t)(dim + c8 + e) * KT + j] = gk[j][e];
+          p[(size_t)(2 * dim + c8 + e) * KT + j] = gv[j][e];
+        }
     }
   }
 }
 
 // Head split + q / k MultiheadRMSNorm + gate sigmoids. ql, kl, vl [B, T, H d]; zl [B, T, nG H] gate
 // logits (no bias); qg, kg [H][d] (null: no norm); bias [nG H]. Outputs q, k, v [(b h), T, d] and
-// gates [nG][(b h), T]. One wave per (t, h) row of d <= 128 elements.
+// gates [nG][(b h), T]. Workgroup (16 tokens, (b, h)): heads_row_threads(d) threads per token row,
+// eight elements (one 16-byte vector of bf16) per thread; the row's RMS is a shuffle sum.
+// Threads per head row: d / 8 rounded up to a power of two (the extra threads hold zeros), so that
+// a row's sums are xor shuffles within an aligned lane group.
+__host__ __device__ __forceinline__ int heads_row_threads(int d) {
+  int rl = 1;
+  while (rl * 8 < d) rl <<= 1;
+  return rl;
+}
 template <typename T>
-__global__ __launch_bounds__(pro::kThreads) void k_heads_fwd(int Tn, int H, int d, int nG, const T* __restrict__ ql,
-                                                             const T* __restrict__ kl, const T* __restrict__ vl,
-                                                             const T* __restrict__ zl, const T* __restrict__ qg,
-                                                             const T* __restrict__ kg, const T* __restrict__ bias,
-                                                             T* __restrict__ q, T* __restrict__ k, T* __restrict__ v,
-                                                             T* __restrict__ gates) {
-  const int t0 = blockIdx.x * pro::kTok, b = blockIdx.y, tid = threadIdx.x, lane = lane_id(), w = wave_id();
-  const int t1 = min(Tn, t0 + pro::kTok);
-  const int HD = H * d, BH = gridDim.y * H;
+__device__ __forceinline__ float row_sum8(float v, int rl) {   // sum over the rl threads of a row
+  for (int m = rl >> 1; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_heads_fwd(int Tn, int H, int d, int nG, const T* __restrict__ ql,
+                                                   const T* __restrict__ kl, const T* __restrict__ vl,
+                                                   const T* __restrict__ zl, const T* __restrict__ qg,
+                                                   const T* __restrict__ kg, const T* __restrict__ bias,
+                                                   T* __restrict__ q, T* __restrict__ k, T* __restrict__ v,
+                                                   T* __restrict__ gates) {
+  const int tb = blockIdx.x, bh = blockIdx.y, H_ = H, b = bh / H_, h = bh % H_, tid = threadIdx.x;
+  const int rl = heads_row_threads(d), r = tid / rl, c8 = (tid % rl) * 8;
+  const int t = tb * pro::kTok + r;
+  const bool valid = t < Tn && c8 < d;
+  const int HD = H * d, BH = gridDim.y;
   const float rs = rsqrtf((float)d);
-  for (int r = w; r < (t1 - t0) * H; r += pro::kThreads / 64) {
-    const int t = t0 + r / H, h = r % H;
-    const size_t src = ((size_t)b * Tn + t) * HD + (size_t)h * d;
-    const size_t dst = (((size_t)b * H + h) * Tn + t) * d;
-    for (int which = 0; which < 3; ++which) {
-      const T* in = which == 0 ? ql : (which == 1 ? kl : vl);
-      T* out = which == 0 ? q : (which == 1 ? k : v);
-      const T* gam = which == 0 ? qg : (which == 1 ? kg : nullptr);
-      const float v0 = lane < d ? to_f32(in[src + lane]) : 0.f;
-      const float v1 = lane + 64 < d ? to_f32(in[src + lane + 64]) : 0.f;
-      float scale = 1.f;
-      if (gam) {
-        const float ss = wave_sum(v0 * v0 + v1 * v1);
-        scale = 1.f / fmaxf(sqrtf(ss) * rs, 1e-8f);
-      }
-      if (lane < d) out[dst + lane] = from_f32<T>(v0 * scale * (gam ? to_f32(gam[h * d + lane]) : 1.f));
-      if (lane + 64 < d) out[dst + lane + 64] = from_f32<T>(v1 * scale * (gam ? to_f32(gam[h * d + lane + 64]) : 1.f));
+  const size_t src = ((size_t)b * Tn + t) * HD + (size_t)h * d + c8;
+  const size_t dst = ((size_t)bh * Tn + t) * d + c8;
+#pragma unroll
+  for (int which = 0; which < 3; ++which) {
+    const T* in = which == 0 ? ql : (which == 1 ? kl : vl);
+    T* out = which == 0 ? q : (which == 1 ? k : v);
+    const T* gam = which == 0 ? qg : (which == 1 ? kg : nullptr);
+    float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (valid) ld8(in + src, x);
+    if (gam) {   // uniform
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+      ss = row_sum8<T>(ss, rl);
+      const float scale = 1.f / fmaxf(sqrtf(ss) * rs, 1e-8f);
+      float g[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (c8 < d) ld8(gam + (size_t)h * d + c8, g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] *= scale * g[e];
     }
+    if (valid) st8(out + dst, x);
   }
-  // gates: one thread per (t, g, h)
-  const int ng = (t1 - t0) * nG * H;
-  for (int i = tid; i < ng; i += pro::kThreads) {
-    const int t = t0 + i / (nG * H), gh = i % (nG * H), g = gh / H, h = gh % H;
-    const float z = to_f32(zl[((size_t)b * Tn + t) * nG * H + gh]) + to_f32(bias[gh]);
-    gates[((size_t)g * BH + (size_t)b * H + h) * Tn + t] = from_f32<T>(1.f / (1.f + __expf(-z)));
+  // gates of this head: item i < nG * 16 -> gate i / 16, token i % 16
+  for (int i = tid; i < nG * pro::kTok; i += blockDim.x) {
+    const int g = i / pro::kTok, tt = tb * pro::kTok + i % pro::kTok;
+    if (tt < Tn) {
+      const float z = to_f32(zl[((size_t)b * Tn + tt) * nG * H + g * H + h]) + to_f32(bias[g * H + h]);
+      gates[((size_t)g * BH + bh) * Tn + tt] = from_f32<T>(1.f / (1.f + __expf(-z)));
+    }
   }
 }
 
 // Adjoint of k_heads_fwd: dq, dk, dv [(b h), T, d], dgates [nG][(b h), T] (null: zero) and the forward's
 // gates -> dql, dkl, dvl [B, T, H d], dzl [B, T, nG H]; partials dqg_part, dkg_part [nwg][H][d] (when
-// the norms exist) and dbias_part [nwg][nG H].
+// the norms exist) and dbias_part [nwg][nG H], nwg = B * ceil(T / 16): workgroup (token block tb,
+// (b, h)) writes row b * ceil(T / 16) + tb, columns of head h.
 //   y = x s gamma, s = 1 / max(r, 1e-8), r = |x| / sqrt(d):  dx = s gamma dy - x s^3 (x . gamma dy) / d  (r > 1e-8)
 template <typename T>
-__global__ __launch_bounds__(pro::kThreads) void k_heads_bwd(int Tn, int H, int d, int nG, const T* __restrict__ ql,
-                                                             const T* __restrict__ kl, const T* __restrict__ qg,
-                                                             const T* __restrict__ kg, const T* __restrict__ gates,
-                                                             const T* __restrict__ dq, const T* __restrict__ dk,
-                                                             const T* __restrict__ dv, const T* __restrict__ dgates,
-                                                             T* __restrict__ dql, T* __restrict__ dkl,
-                                                             T* __restrict__ dvl, T* __restrict__ dzl,
-                                                             float* __restrict__ dqg_part, float* __restrict__ dkg_part,
-                                                             float* __restrict__ dbias_part) {
-  extern __shared__ float sgam[];   // [2][H][d] gamma partials of this workgroup, then [nG H] bias partials
-  const int t0 = blockIdx.x * pro::kTok, b = blockIdx.y, tid = threadIdx.x, lane = lane_id(), w = wave_id();
-  const int t1 = min(Tn, t0 + pro::kTok);
-  const int HD = H * d, BH = gridDim.y * H;
-  const int wg = blockIdx.y * gridDim.x + blockIdx.x;
+__global__ __launch_bounds__(256) void k_heads_bwd(int Tn, int H, int d, int nG, const T* __restrict__ ql,
+                                                   const T* __restrict__ kl, const T* __restrict__ qg,
+                                                   const T* __restrict__ kg, const T* __restrict__ gates,
+                                                   const T* __restrict__ dq, const T* __restrict__ dk,
+                                                   const T* __restrict__ dv, const T* __restrict__ dgates,
+                                                   T* __restrict__ dql, T* __restrict__ dkl, T* __restrict__ dvl,
+                                                   T* __restrict__ dzl, float* __restrict__ dqg_part,
+                                                   float* __restrict__ dkg_part, float* __restrict__ dbias_part) {
+  __shared__ float sgp[2][pro::kTok][128 + 1];   // gamma-gradient terms per token row, q and k
+  __shared__ float sbp[8][pro::kTok];            // bias-gradient terms per gate and token
+  const int tb = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H, tid = threadIdx.x;
+  const int rl = heads_row_threads(d), r = tid / rl, c8 = (tid % rl) * 8;
+  const int t = tb * pro::kTok + r;
+  const bool valid = t < Tn && c8 < d;
+  const int HD = H * d, BH = gridDim.y, ntb = gridDim.x;
   const float rs = rsqrtf((float)d);
   const bool norm = qg != nullptr;
-  float* sb = sgam + 2 * HD;
-  for (int i = tid; i < 2 * HD + nG * H; i += pro::kThreads) sgam[i] = 0.f;
-  __syncthreads();
-  for (int r = w; r < (t1 - t0) * H; r += pro::kThreads / 64) {
-    const int t = t0 + r / H, h = r % H;
-    const size_t xo = ((size_t)b * Tn + t) * HD + (size_t)h * d;
-    const size_t yo = (((size_t)b * H + h) * Tn + t) * d;
-    for (int which = 0; which < 3; ++which) {
-      const T* dy = which == 0 ? dq : (which == 1 ? dk : dv);
-      T* dxo = which == 0 ? dql : (which == 1 ? dkl : dvl);
-      const float g0 = lane < d ? to_f32(dy[yo + lane]) : 0.f;
-      const float g1 = lane + 64 < d ? to_f32(dy[yo + lane + 64]) : 0.f;
-      if (which == 2 || !norm) {
-        if (lane < d) dxo[xo + lane] = from_f32<T>(g0);
-        if (lane + 64 < d) dxo[xo + lane + 64] = from_f32<T>(g1);
-        continue;
-      }
-      const T* in = which == 0 ? ql : kl;
-      const T* gam = which == 0 ? qg : kg;
-      const float x0 = lane < d ? to_f32(in[xo + lane]) : 0.f;
-      const float x1 = lane + 64 < d ? to_f32(in[xo + lane + 64]) : 0.f;
-      const float gm0 = lane < d ? to_f32(gam[h * d + lane]) : 0.f;
-      const float gm1 = lane + 64 < d ? to_f32(gam[h * d + lane + 64]) : 0.f;
-      const float ss = wave_sum(x0 * x0 + x1 * x1);
-      const float r_ = sqrtf(ss) * rs;
-      const bool live = r_ > 1e-8f;
-      const float s = 1.f / fmaxf(r_, 1e-8f);
-      const float u0 = gm0 * g0, u1 = gm1 * g1;
-      const float xu = wave_sum(x0 * u0 + x1 * u1);
-      const float c3 = live ? s * s * s * xu / (float)d : 0.f;
-      if (lane < d) dxo[xo + lane] = from_f32<T>(s * u0 - x0 * c3);
-      if (lane + 64 < d) dxo[xo + lane + 64] = from_f32<T>(s * u1 - x1 * c3);
-      float* sg = sgam + which * HD + h * d;
-      if (lane < d) atomicAdd(&sg[lane], g0 * x0 * s);
-      if (lane + 64 < d) atomicAdd(&sg[lane + 64], g1 * x1 * s);
+  const size_t xo = ((size_t)b * Tn + t) * HD + (size_t)h * d + c8;
+  const size_t yo = ((size_t)bh * Tn + t) * d + c8;
+#pragma unroll
+  for (int which = 0; which < 3; ++which) {
+    const T* dy = which == 0 ? dq : (which == 1 ? dk : dv);
+    T* dxo = which == 0 ? dql : (which == 1 ? dkl : dvl);
+    float gv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (valid) ld8(dy + yo, gv);
+    if (which == 2 || !norm) {
+      if (valid) st8(dxo + xo, gv);
+      continue;
     }
+    const T* in = which == 0 ? ql : kl;
+    const T* gam = which == 0 ? qg : kg;
+    float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, gm[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (valid) ld8(in + xo, x);
+    if (c8 < d) ld8(gam + (size_t)h * d + c8, gm);
+    float ss = 0.f, xu = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ss += x[e] * x[e];
+      xu += x[e] * gm[e] * gv[e];
+    }
+    ss = row_sum8<T>(ss, rl);
+    xu = row_sum8<T>(xu, rl);
+    const float r_ = sqrtf(ss) * rs;
+    const float sc = 1.f / fmaxf(r_, 1e-8f);
+    const float c3 = r_ > 1e-8f ? sc * sc * sc * xu / (float)d : 0.f;
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      o[e] = sc * gm[e] * gv[e] - x[e] * c3;
+      if (c8 < d) sgp[which][r][c8 + e] = gv[e] * x[e] * sc;   // 0 for rows past T (x = 0)
+    }
+    if (valid) st8(dxo + xo, o);
   }
   // gates: dz = dg s (1 - s)
-  const int ng = (t1 - t0) * nG * H;
-  for (int i = tid; i < ng; i += pro::kThreads) {
-    const int t = t0 + i / (nG * H), gh = i % (nG * H), g = gh / H, h = gh % H;
-    const size_t go = ((size_t)g * BH + (size_t)b * H + h) * Tn + t;
-    const float s = to_f32(gates[go]);
-    const float dg = dgates ? to_f32(dgates[go]) : 0.f;
-    const float dz = dg * s * (1.f - s);
-    dzl[((size_t)b * Tn + t) * nG * H + gh] = from_f32<T>(dz);
-    atomicAdd(&sb[gh], dz);
+  for (int i = tid; i < nG * pro::kTok; i += blockDim.x) {
+    const int g = i / pro::kTok, rr = i % pro::kTok, tt = tb * pro::kTok + rr;
+    float dz = 0.f;
+    if (tt < Tn) {
+      const size_t go = ((size_t)g * BH + bh) * Tn + tt;
+      const float sg = to_f32(gates[go]);
+      const float dg = dgates ? to_f32(dgates[go]) : 0.f;
+      dz = dg * sg * (1.f - sg);
+      dzl[((size_t)b * Tn + tt) * nG * H + g * H + h] = from_f32<T>(dz);
+    }
+    sbp[g][rr] = dz;
   }
   __syncthreads();
+  const size_t prow = (size_t)b * ntb + tb;
   if (norm) {
-    for (int i = tid; i < HD; i += pro::kThreads) {
-      dqg_part[(size_t)wg * HD + i] = sgam[i];
-      dkg_part[(size_t)wg * HD + i] = sgam[HD + i];
+    for (int i = tid; i < 2 * d; i += blockDim.x) {
+      const int which = i / d, c = i % d;
+      float acc = 0.f;
+#pragma unroll
+      for (int rr = 0; rr < pro::kTok; ++rr) acc += sgp[which][rr][c];
+      (which ? dkg_part : dqg_part)[prow * HD + (size_t)h * d + c] = acc;
     }
   }
-  for (int i = tid; i < nG * H; i += pro::kThreads) dbias_part[(size_t)wg * nG * H + i] = sb[i];
+  for (int g = tid; g < nG; g += blockDim.x) {
+    float acc = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < pro::kTok; ++rr) acc += sbp[g][rr];
+    dbias_part[prow * nG * H + g * H + h] = acc;
+  }
 }
 
 }  // namespace atlas
@@ -337,11 +431,12 @@ using namespace atlas;
 
 namespace {
 bool pro_shapes_ok(int B, int Tn, int dim, int K) {
-  return B >= 1 && B <= 65535 && Tn >= 1 && dim >= 1 && dim <= (1 << 16) && K >= 0 && K <= pro::kMaxK;
+  return B >= 1 && B <= 65535 && Tn >= 1 && dim >= 8 && dim <= (1 << 16) && dim % 8 == 0 && K >= 0 &&
+         K <= pro::kMaxK;
 }
 bool heads_shapes_ok(int B, int Tn, int H, int d, int nG) {
-  return B >= 1 && B <= 65535 && Tn >= 1 && H >= 1 && d >= 1 && d <= 128 && nG >= 0 && nG <= 8 &&
-         (size_t)(2 * H * d + nG * H) * 4 <= 64 * 1024;
+  return B >= 1 && Tn >= 1 && H >= 1 && (int64_t)B * H <= 65535 && d >= 8 && d <= 128 && d % 8 == 0 && nG >= 0 &&
+         nG <= 8;
 }
 }  // namespace
 
@@ -360,17 +455,31 @@ int atlas_prologue_fwd(int dtype, int batch, int seq_len, int dim, int conv_k, f
   const bool conv = conv_k > 1;
   if (!x || !norm_w || !xn || !inv_rms) return ATLAS_MEM_ERR_NULL;
   if (conv && (!wq || !wk || !wv || !q_in || !k_in || !v_in)) return ATLAS_MEM_ERR_NULL;
-  const dim3 grid((seq_len + pro::kTok - 1) / pro::kTok, batch);
-  const int K = conv ? conv_k : 0, pad = conv_k / 2;
+  for (const void* p : {x, norm_w, (const void*)xn, (const void*)q_in, (const void*)k_in, (const void*)v_in})
+    if (reinterpret_cast<uintptr_t>(p) & 15) return ATLAS_MEM_ERR_ALIGN;
+  const dim3 grid((seq_len + pro::kTok - 1) / pro::kTok, batch), block(pro::kThreads);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == ATLAS_DT_BF16)
-    hipLaunchKernelGGL(k_pro_fwd<bf16>, grid, dim3(pro::kThreads), 0, s, seq_len, dim, K, pad, eps, (const bf16*)x,
-                       (const bf16*)norm_w, conv ? (const bf16*)wq : nullptr, (const bf16*)wk, (const bf16*)wv,
-                       (bf16*)xn, (bf16*)q_in, (bf16*)k_in, (bf16*)v_in, inv_rms);
-  else
-    hipLaunchKernelGGL(k_pro_fwd<float>, grid, dim3(pro::kThreads), 0, s, seq_len, dim, K, pad, eps, (const float*)x,
-                       (const float*)norm_w, conv ? (const float*)wq : nullptr, (const float*)wk, (const float*)wv,
-                       (float*)xn, (float*)q_in, (float*)k_in, (float*)v_in, inv_rms);
+  const int K = conv ? conv_k : 0;
+  auto go = [&](auto tag, auto kt) {
+    using T = decltype(tag);
+    constexpr int KT = decltype(kt)::value;
+    hipLaunchKernelGGL((k_pro_fwd<T, KT>), grid, block, 0, s, seq_len, dim, eps, (const T*)x, (const T*)norm_w,
+                       (const T*)wq, (const T*)wk, (const T*)wv, (T*)xn, (T*)q_in, (T*)k_in, (T*)v_in, inv_rms);
+  };
+  auto by_k = [&](auto tag) {
+    switch (K) {
+      case 0: go(tag, std::integral_constant<int, 0>{}); break;
+      case 2: go(tag, std::integral_constant<int, 2>{}); break;
+      case 3: go(tag, std::integral_constant<int, 3>{}); break;
+      case 4: go(tag, std::integral_constant<int, 4>{}); break;
+      case 5: go(tag, std::integral_constant<int, 5>{}); break;
+      case 6: go(tag, std::integral_constant<int, 6>{}); break;
+      case 7: go(tag, std::integral_constant<int, 7>{}); break;
+      default: go(tag, std::integral_constant<int, 8>{}); break;
+    }
+  };
+  if (dtype == ATLAS_DT_BF16) by_k(bf16{});
+  else by_k(float{});
   return hipGetLastError() == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
 }
 
@@ -383,19 +492,33 @@ int atlas_prologue_bwd(int dtype, int batch, int seq_len, int dim, int conv_k, c
   const bool conv = conv_k > 1;
   if (!x || !norm_w || !inv_rms || !dxn || !dx || !dnorm_w_part) return ATLAS_MEM_ERR_NULL;
   if (conv && (!wq || !wk || !wv || !dq_in || !dk_in || !dv_in || !dconv_part)) return ATLAS_MEM_ERR_NULL;
-  const dim3 grid((seq_len + pro::kTok - 1) / pro::kTok, batch);
-  const int K = conv ? conv_k : 0, pad = conv_k / 2;
+  for (const void* p : {x, norm_w, dxn, dq_in, dk_in, dv_in, (const void*)dx})
+    if (reinterpret_cast<uintptr_t>(p) & 15) return ATLAS_MEM_ERR_ALIGN;
+  const int ntb = (seq_len + pro::kTok - 1) / pro::kTok, wpb = pro::kThreads / 64;
+  const dim3 grid((ntb + wpb - 1) / wpb, batch), block(pro::kThreads);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == ATLAS_DT_BF16)
-    hipLaunchKernelGGL(k_pro_bwd<bf16>, grid, dim3(pro::kThreads), 0, s, seq_len, dim, K, pad, (const bf16*)x,
-                       (const bf16*)norm_w, conv ? (const bf16*)wq : nullptr, (const bf16*)wk, (const bf16*)wv, inv_rms,
-                       (const bf16*)dxn, (const bf16*)dq_in, (const bf16*)dk_in, (const bf16*)dv_in, (bf16*)dx,
-                       dnorm_w_part, dconv_part);
-  else
-    hipLaunchKernelGGL(k_pro_bwd<float>, grid, dim3(pro::kThreads), 0, s, seq_len, dim, K, pad, (const float*)x,
-                       (const float*)norm_w, conv ? (const float*)wq : nullptr, (const float*)wk, (const float*)wv,
-                       inv_rms, (const float*)dxn, (const float*)dq_in, (const float*)dk_in, (const float*)dv_in,
-                       (float*)dx, dnorm_w_part, dconv_part);
+  const int K = conv ? conv_k : 0;
+  auto go = [&](auto tag, auto kt) {
+    using T = decltype(tag);
+    constexpr int KT = decltype(kt)::value;
+    hipLaunchKernelGGL((k_pro_bwd<T, KT>), grid, block, 0, s, seq_len, dim, (const T*)x, (const T*)norm_w,
+                       (const T*)wq, (const T*)wk, (const T*)wv, inv_rms, (const T*)dxn, (const T*)dq_in,
+                       (const T*)dk_in, (const T*)dv_in, (T*)dx, dnorm_w_part, dconv_part);
+  };
+  auto by_k = [&](auto tag) {
+    switch (K) {
+      case 0: go(tag, std::integral_constant<int, 0>{}); break;
+      case 2: go(tag, std::integral_constant<int, 2>{}); break;
+      case 3: go(tag, std::integral_constant<int, 3>{}); break;
+      case 4: go(tag, std::integral_constant<int, 4>{}); break;
+      case 5: go(tag, std::integral_constant<int, 5>{}); break;
+      case 6: go(tag, std::integral_constant<int, 6>{}); break;
+      case 7: go(tag, std::integral_constant<int, 7>{}); break;
+      default: go(tag, std::integral_constant<int, 8>{}); break;
+    }
+  };
+  if (dtype == ATLAS_DT_BF16) by_k(bf16{});
+  else by_k(float{});
   return hipGetLastError() == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
 }
 
@@ -407,14 +530,16 @@ int atlas_heads_fwd(int dtype, int batch, int seq_len, int heads, int d, int n_g
   if (!ql || !kl || !vl || !q || !k || !v) return ATLAS_MEM_ERR_NULL;
   if ((q_gamma == nullptr) != (k_gamma == nullptr)) return ATLAS_MEM_ERR_ARG;
   if (n_gates > 0 && (!zl || !gate_bias || !gates)) return ATLAS_MEM_ERR_NULL;
-  const dim3 grid((seq_len + pro::kTok - 1) / pro::kTok, batch);
+  for (const void* p : {ql, kl, vl, q_gamma, k_gamma, (const void*)q, (const void*)k, (const void*)v})
+    if (reinterpret_cast<uintptr_t>(p) & 15) return ATLAS_MEM_ERR_ALIGN;
+  const dim3 grid((seq_len + pro::kTok - 1) / pro::kTok, batch * heads), block(pro::kTok * heads_row_threads(d));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == ATLAS_DT_BF16)
-    hipLaunchKernelGGL(k_heads_fwd<bf16>, grid, dim3(pro::kThreads), 0, s, seq_len, heads, d, n_gates, (const bf16*)ql,
+    hipLaunchKernelGGL(k_heads_fwd<bf16>, grid, block, 0, s, seq_len, heads, d, n_gates, (const bf16*)ql,
                        (const bf16*)kl, (const bf16*)vl, (const bf16*)zl, (const bf16*)q_gamma, (const bf16*)k_gamma,
                        (const bf16*)gate_bias, (bf16*)q, (bf16*)k, (bf16*)v, (bf16*)gates);
   else
-    hipLaunchKernelGGL(k_heads_fwd<float>, grid, dim3(pro::kThreads), 0, s, seq_len, heads, d, n_gates,
+    hipLaunchKernelGGL(k_heads_fwd<float>, grid, block, 0, s, seq_len, heads, d, n_gates,
                        (const float*)ql, (const float*)kl, (const float*)vl, (const float*)zl, (const float*)q_gamma,
                        (const float*)k_gamma, (const float*)gate_bias, (float*)q, (float*)k, (float*)v, (float*)gates);
   return hipGetLastError() == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
@@ -430,16 +555,17 @@ int atlas_heads_bwd(int dtype, int batch, int seq_len, int heads, int d, int n_g
   if ((q_gamma == nullptr) != (k_gamma == nullptr)) return ATLAS_MEM_ERR_ARG;
   if (q_gamma && (!dq_gamma_part || !dk_gamma_part)) return ATLAS_MEM_ERR_NULL;
   if (n_gates > 0 && (!gates || !dzl || !dbias_part)) return ATLAS_MEM_ERR_NULL;
-  const dim3 grid((seq_len + pro::kTok - 1) / pro::kTok, batch);
-  const size_t smem = (size_t)(2 * heads * d + n_gates * heads) * sizeof(float);
+  for (const void* p : {ql, kl, q_gamma, k_gamma, dq, dk, dv, (const void*)dql, (const void*)dkl, (const void*)dvl})
+    if (reinterpret_cast<uintptr_t>(p) & 15) return ATLAS_MEM_ERR_ALIGN;
+  const dim3 grid((seq_len + pro::kTok - 1) / pro::kTok, batch * heads), block(pro::kTok * heads_row_threads(d));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == ATLAS_DT_BF16)
-    hipLaunchKernelGGL(k_heads_bwd<bf16>, grid, dim3(pro::kThreads), smem, s, seq_len, heads, d, n_gates,
+    hipLaunchKernelGGL(k_heads_bwd<bf16>, grid, block, 0, s, seq_len, heads, d, n_gates,
                        (const bf16*)ql, (const bf16*)kl, (const bf16*)q_gamma, (const bf16*)k_gamma,
                        (const bf16*)gates, (const bf16*)dq, (const bf16*)dk, (const bf16*)dv, (const bf16*)dgates,
                        (bf16*)dql, (bf16*)dkl, (bf16*)dvl, (bf16*)dzl, dq_gamma_part, dk_gamma_part, dbias_part);
   else
-    hipLaunchKernelGGL(k_heads_bwd<float>, grid, dim3(pro::kThreads), smem, s, seq_len, heads, d, n_gates,
+    hipLaunchKernelGGL(k_heads_bwd<float>, grid, block, 0, s, seq_len, heads, d, n_gates,
                        (const float*)ql, (const float*)kl, (const float*)q_gamma, (const float*)k_gamma,
                        (const float*)gates, (const float*)dq, (const float*)dk, (const float*)dv, (const float*)dgates,
                        (float*)dql, (float*)dkl, (float*)dvl, (float*)dzl, dq_gamma_part, dk_gamma_part, dbias_part);

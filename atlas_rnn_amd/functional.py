@@ -914,6 +914,97 @@ class _HeadsFn(torch.autograd.Function):
         return dql, dkl, dvl, dzl, dqgam, dkgam, db, None, None
 
 
+def _wgrad(dy: Tensor, x: Tensor, dtype) -> Tensor:
+    """dW = dy^T x over every leading axis of dy [..., o] and x [..., i], split over the tokens:
+    one batched product of S token slices, summed in fp32. With K = tokens in the thousands and a
+    d x d output, the plain product runs on few output tiles (measured 105 us for 16384 tokens x
+    512 x 512 on MI355X, 66 us split eight ways)."""
+    o, i = dy.shape[-1], x.shape[-1]
+    dy2, x2 = dy.reshape(-1, o), x.reshape(-1, i)
+    n = dy2.shape[0]
+    S = next((c for c in (8, 4, 2) if n % c == 0 and n // c >= 1024), 1)
+    if S == 1:
+        return (dy2.t() @ x2).to(dtype)
+    a = dy2.view(S, n // S, o).transpose(1, 2).contiguous()   # both operands row-major (no transposed views)
+    return torch.bmm(a, x2.view(S, n // S, i).contiguous()).float().sum(0).to(dtype)
+
+
+class _LinearFn(torch.autograd.Function):
+    """y = x W^T (hipBLASLt) with the token-split weight gradient of _wgrad."""
+
+    @staticmethod
+    def forward(ctx, x, w):
+        ctx.save_for_backward(x, w)
+        return torch.nn.functional.linear(x, w)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dx = dy @ w if ctx.needs_input_grad[0] else None
+        dw = _wgrad(dy, x, w.dtype) if ctx.needs_input_grad[1] else None
+        return dx, dw
+
+
+def linear(x: Tensor, w: Tensor) -> Tensor:
+    """x W^T without bias, with the token-split weight gradient of _LinearFn."""
+    return _LinearFn.apply(x, w)
+
+
+class _HandCtx:
+    """Stands in for autograd's ctx where one Function composes other Functions' forward and
+    backward by hand."""
+
+    def set_materialize_grads(self, value):
+        pass
+
+    def save_for_backward(self, *tensors):
+        self.saved_tensors = tensors
+
+
+class _CellPrologueFn(torch.autograd.Function):
+    """The whole prologue as ONE autograd node: the RMSNorm / conv kernel, the four projections
+    (hipBLASLt), the head-split kernel, and in the backward their adjoints in reverse order with the
+    token-split weight gradients. One node instead of seven keeps the host's per-step work (the
+    prologue is host-bound at C5's layer shape: ~1.1 ms of issue time against less GPU time)."""
+
+    @staticmethod
+    def forward(ctx, x, norm_w, wq, wk, wv, Wq, Wk, Wv, Wg, bg, qg, kg, conv_k, eps, heads, d):
+        F = torch.nn.functional
+        cp, ch = _HandCtx(), _HandCtx()
+        conv = conv_k > 1
+        if conv:
+            xn, qi, ki, vi = _PrologueFn.forward(cp, x, norm_w, wq, wk, wv, conv_k, eps)
+        else:
+            xn = _PrologueFn.forward(cp, x, norm_w, None, None, None, 0, eps)
+            qi = ki = vi = xn
+        ql, kl, vl = F.linear(qi, Wq), F.linear(ki, Wk), F.linear(vi, Wv)
+        zl = F.linear(xn, Wg) if Wg is not None else None
+        outs = _HeadsFn.forward(ch, ql, kl, vl, zl, qg, kg, bg, heads, d)
+        e0 = torch.empty(0, device=x.device)
+        ctx.save_for_backward(qi, ki, vi, xn, Wq, Wk, Wv, Wg if Wg is not None else e0)
+        ctx.cp, ctx.ch, ctx.conv, ctx.has_g = cp, ch, conv, Wg is not None
+        return (xn, *outs)
+
+    @staticmethod
+    def backward(ctx, dxn, dq, dk, dv, *dgates):
+        qi, ki, vi, xn, Wq, Wk, Wv, Wg = ctx.saved_tensors
+        dql, dkl, dvl, dzl, dqg, dkg, db, _, _ = _HeadsFn.backward(ctx.ch, dq, dk, dv, *dgates)
+        dqi, dki, dvi = dql @ Wq, dkl @ Wk, dvl @ Wv
+        dWq, dWk, dWv = _wgrad(dql, qi, Wq.dtype), _wgrad(dkl, ki, Wk.dtype), _wgrad(dvl, vi, Wv.dtype)
+        dWg = None
+        dsum = dxn
+        if ctx.has_g:
+            dWg = _wgrad(dzl, xn, Wg.dtype)
+            dxg = dzl @ Wg
+            dsum = dxg if dsum is None else dsum + dxg
+        if ctx.conv:
+            dx, dnorm, dtq, dtk, dtv, _, _ = _PrologueFn.backward(ctx.cp, dsum, dqi, dki, dvi)
+        else:
+            dsum = dqi + dki + dvi + (dsum if dsum is not None else 0)
+            dx, dnorm, dtq, dtk, dtv, _, _ = _PrologueFn.backward(ctx.cp, dsum)
+        return (dx, dnorm, dtq, dtk, dtv, dWq, dWk, dWv, dWg, db, dqg, dkg, None, None, None, None)
+
+
 def cell_prologue(x: Tensor, norm_weight: Tensor, eps: float, conv_weights, proj_weights, gate_weights, gate_biases,
                   q_gamma: Tensor | None, k_gamma: Tensor | None, heads: int, dim_head: int):
     """The memory cell's prologue (rnn_memory.py:567-653) on the fused kernels:
@@ -938,19 +1029,14 @@ def cell_prologue(x: Tensor, norm_weight: Tensor, eps: float, conv_weights, proj
         if conv_k > 8:
             raise ValueError("the fused prologue supports depthwise convolutions of up to 8 taps")
     wq, wk, wv = (cast(w) for w in conv_weights) if conv_weights is not None else (None, None, None)
-    if conv_k > 1:
-        xn, qi, ki, vi = _PrologueFn.apply(x, norm_weight.to(dt).contiguous(), wq, wk, wv, conv_k, eps)
-    else:
-        xn = _PrologueFn.apply(x, norm_weight.to(dt).contiguous(), None, None, None, 0, eps)
-        qi = ki = vi = xn
-    F = torch.nn.functional
-    ql = F.linear(qi, cast(proj_weights[0]))
-    kl = F.linear(ki, cast(proj_weights[1]))
-    vl = F.linear(vi, cast(proj_weights[2]))
-    zl = F.linear(xn, torch.cat([cast(w) for w in gate_weights], dim=0)) if gate_weights else None
+    if conv_k <= 1:
+        wq = wk = wv = None
+    Wg = torch.cat([cast(w) for w in gate_weights], dim=0) if gate_weights else None
     bias = torch.cat([cast(b) for b in gate_biases]).contiguous() if gate_weights else None
-    out = _HeadsFn.apply(ql, kl, vl, zl, cast(q_gamma), cast(k_gamma), bias, heads, dim_head)
-    return xn, out[0], out[1], out[2], list(out[3:])
+    out = _CellPrologueFn.apply(x, norm_weight.to(dt).contiguous(), wq, wk, wv, cast(proj_weights[0]),
+                                cast(proj_weights[1]), cast(proj_weights[2]), Wg, bias, cast(q_gamma), cast(k_gamma),
+                                conv_k if conv_k > 1 else 0, eps, heads, dim_head)
+    return out[0], out[1], out[2], out[3], list(out[4:])
 
 
 # ------------------------------------------------------------------------------------------

@@ -36,7 +36,7 @@ from einops.layers.torch import Rearrange
 from torch import Tensor, nn
 from torch.nn import Conv1d, Linear, Module, Parameter
 
-from .functional import (AssocScan, AtlasOmegaFunction, cell_prologue, check_cuda_availability,
+from .functional import (AssocScan, AtlasOmegaFunction, cell_prologue, check_cuda_availability, linear,
                          memory_recurrence, tensor_feature_map, window_sum)
 
 
@@ -227,7 +227,7 @@ class _CellBase(Module):
             map_mode='elementwise' if self.phi.fused_elementwise else 'off', map_degree=self.phi.degree,
             clamp_every=chunk, clamp_final=True)
         y = rearrange(y.to(x.dtype), '(b h) t d -> b h t d', b=batch, h=self.heads)
-        out = self.to_out(self.merge_heads(y))
+        out = linear(self.merge_heads(y), self.to_out.weight)   # to_out, token-split weight gradient
         dt = S0.dtype
         next_state = RNNMemState(
             seq_index=state.seq_index + seq_len,
@@ -327,7 +327,7 @@ class OmegaRNNMemoryCell(_CellBase):
             Z = Z_T.to(x.dtype) if self.use_momentum else zeros
         y = torch.cat(ys, dim=1) if len(ys) > 1 else ys[0]
         y = rearrange(y, '(b h) t d -> b h t d', b=batch, h=self.heads)
-        out = self.to_out(self.merge_heads(y))
+        out = linear(self.merge_heads(y), self.to_out.weight)   # to_out, token-split weight gradient
         next_state = RNNMemState(seq_index=state.seq_index + seq_len, S=S,
                                  Z=Z if self.use_momentum else None, omega_buffer=None)
         return out, next_state

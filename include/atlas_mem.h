@@ -298,7 +298,8 @@ int atlas_prologue_bwd(int dtype, int batch, int seq_len, int dim, int conv_k, c
 /* The head split of the projections ql, kl, vl [batch, seq_len, heads * d] into [(batch heads), seq_len, d],
  * MultiheadRMSNorm of q and k (x / max(|x| d^-1/2, 1e-8) * gamma[h]; q_gamma, k_gamma [heads][d], both
  * NULL: no norm), and n_gates sigmoid gate heads from the logits zl [batch, seq_len, n_gates * heads]
- * plus gate_bias [n_gates * heads] into gates [n_gates][(batch heads), seq_len]. d <= 128. */
+ * plus gate_bias [n_gates * heads] into gates [n_gates][(batch heads), seq_len]. d a multiple of 8 up to
+ * 128, batch * heads <= 65535, n_gates <= 8; the row tensors and gammas 16-byte aligned. */
 int atlas_heads_fwd(int dtype, int batch, int seq_len, int heads, int d, int n_gates, const void* ql, const void* kl,
                     const void* vl, const void* zl, const void* q_gamma, const void* k_gamma, const void* gate_bias,
                     void* q, void* k, void* v, void* gates, void* stream);
@@ -306,7 +307,8 @@ int atlas_heads_fwd(int dtype, int batch, int seq_len, int heads, int d, int n_g
 /* Adjoint of atlas_heads_fwd given its gates: dq, dk, dv [(batch heads), seq_len, d], dgates
  * [n_gates][(batch heads), seq_len] (NULL: zero) -> dql, dkl, dvl [batch, seq_len, heads * d],
  * dzl [batch, seq_len, n_gates * heads], dq_gamma_part, dk_gamma_part [nwg][heads][d], dbias_part
- * [nwg][n_gates * heads]. */
+ * [nwg][n_gates * heads] with nwg = atlas_prologue_num_workgroups(batch, seq_len) (every entry written;
+ * the gradients are the sums over nwg). */
 int atlas_heads_bwd(int dtype, int batch, int seq_len, int heads, int d, int n_gates, const void* ql, const void* kl,
                     const void* q_gamma, const void* k_gamma, const void* gates, const void* dq, const void* dk,
                     const void* dv, const void* dgates, void* dql, void* dkl, void* dvl, void* dzl,

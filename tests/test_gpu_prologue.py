@@ -53,6 +53,9 @@ CASES = [
     ("fp32_noconv_nonorm", 3, 17, 32, 1, 32, 0, 3, False, torch.float32),
     ("fp32_d128_k2", 1, 40, 64, 2, 128, 2, 2, True, torch.float32),
     ("bf16_k4_c5_head", 2, 50, 512, 8, 64, 4, 4, True, torch.bfloat16),
+    # head sizes whose rows do not fill a power-of-two thread group (padded lanes)
+    ("fp32_d48_k4", 2, 37, 96, 2, 48, 4, 3, True, torch.float32),
+    ("bf16_d24_k2_nonorm", 1, 20, 48, 2, 24, 2, 2, False, torch.bfloat16),
 ]
 
 
