@@ -131,13 +131,14 @@ __global__ __launch_bounds__(pro::kThreads) void k_pro_fwd(int Tn, int dim, floa
 
 // Adjoint of k_pro_fwd. dxn: gradient reaching xn directly (the gate heads; with no conv also the
 // projections); dqi / dki / dvi: gradients of the conv outputs (null without conv). Writes dx and
-// partials dwn_part [nwg][dim], dwc_part [nwg][3][dim][K], nwg = B * ceil(T / 16): workgroup = 64
-// tokens of one batch row, wave w owns the 16-token block 4 blockIdx.x + w (partial row
-// b * ceil(T / 16) + block) and all channels, eight per lane.
+// partials dwn_part [nwg][dim], dwc_part [nwg][3][dim][K], nwg = B * ceil(T / 16): one workgroup per
+// 16-token block of one batch row (partial row b * ceil(T / 16) + block); wave w owns tokens
+// 4 w .. 4 w + 3 of the block and every channel, eight per lane.
 //   u[t, c]  = w[c] * g[t, c],  g = dxn + sum_j taps[c][j] dconv[t - j + pad]   (the conv's transpose)
 //   dx[t, c] = inv_t u[t, c] - x[t, c] inv_t^3 (sum_c' u[t, c'] x[t, c']) / dim
-// Three passes over the block: A (g: the dot products and the norm-weight partials), B (g again: dx),
-// C (the tap partials), so that taps and tap partials are never live together.
+// Three passes: A (g: the dot products and the norm-weight partials), B (g again: dx), C (the tap
+// partials), so that taps and tap partials are never live together; the four waves' partials are
+// summed through LDS, 512 channels at a time.
 template <typename T, int KT>
 __global__ __launch_bounds__(pro::kThreads) void k_pro_bwd(int Tn, int dim, const T* __restrict__ x,
                                                            const T* __restrict__ wn, const T* __restrict__ wq,
@@ -147,12 +148,11 @@ __global__ __launch_bounds__(pro::kThreads) void k_pro_bwd(int Tn, int dim, cons
                                                            const T* __restrict__ dki, const T* __restrict__ dvi,
                                                            T* __restrict__ dx, float* __restrict__ dwn_part,
                                                            float* __restrict__ dwc_part) {
-  constexpr int pad = KT / 2, KA = KT > 0 ? KT : 1;
-  const int lane = lane_id(), w = wave_id();
-  const int b = blockIdx.y, ntb = (Tn + pro::kTok - 1) / pro::kTok;
-  const int blk = blockIdx.x * (pro::kThreads / 64) + w;
-  if (blk >= ntb) return;   // wave-uniform; no barriers in this kernel
-  const int t0 = blk * pro::kTok, t1 = min(Tn, t0 + pro::kTok);
+  constexpr int pad = KT / 2, KA = KT > 0 ? KT : 1, NW = pro::kThreads / 64, TW = pro::kTok / NW;
+  __shared__ float sred[NW][512 * KA];   // per-wave partials of 512 channels (x K taps)
+  const int lane = lane_id(), w = wave_id(), tid = threadIdx.x;
+  const int b = blockIdx.y, ntb = gridDim.x, blk = blockIdx.x;
+  const int t0 = blk * pro::kTok + w * TW, t1 = min(Tn, t0 + TW);   // this wave's tokens (may be none)
   const size_t ob = (size_t)b * Tn * dim, prow = (size_t)b * ntb + blk;
   const float* inv = inv_rms + (size_t)b * Tn;
   const T* xb = x + ob;
@@ -175,37 +175,54 @@ __global__ __launch_bounds__(pro::kThreads) void k_pro_bwd(int Tn, int dim, cons
       }
     }
   };
-  float dot[pro::kTok];
+  // sums sred[*][0 .. n) over the waves into dst (n = 8 * 64 * per-lane values of this 512-channel chunk)
+  auto wave_reduce_store = [&](float* dst, int n) {
+    __syncthreads();
+    for (int i = tid; i < n; i += pro::kThreads) {
+      float acc = 0.f;
 #pragma unroll
-  for (int i = 0; i < pro::kTok; ++i) dot[i] = 0.f;
-  // pass A
-  for (int c8 = lane * 8; c8 < dim; c8 += 512) {
-    float wv8[8], tq[KA][8], tk[KA][8], tv[KA][8], dw[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    ld8(wn + c8, wv8);
-    if constexpr (KT > 0) {
-      load_taps<T, KT>(wq, c8, tq);
-      load_taps<T, KT>(wk, c8, tk);
-      load_taps<T, KT>(wv, c8, tv);
+      for (int ww = 0; ww < NW; ++ww) acc += sred[ww][i];
+      dst[i] = acc;
     }
+    __syncthreads();
+  };
+  float dot[TW];
 #pragma unroll
-    for (int i = 0; i < pro::kTok; ++i) {
-      const int t = t0 + i;
-      if (t >= t1) break;
-      float g[8], xv[8];
-      gvec(t, c8, tq, tk, tv, g);
-      ld8(xb + (size_t)t * dim + c8, xv);
-      const float it = inv[t];
+  for (int i = 0; i < TW; ++i) dot[i] = 0.f;
+  // pass A
+  for (int cb = 0; cb < dim; cb += 512) {
+    const int c8 = cb + lane * 8;
+    const bool on = c8 < dim;
+    float dw[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (on) {
+      float wv8[8], tq[KA][8], tk[KA][8], tv[KA][8];
+      ld8(wn + c8, wv8);
+      if constexpr (KT > 0) {
+        load_taps<T, KT>(wq, c8, tq);
+        load_taps<T, KT>(wk, c8, tk);
+        load_taps<T, KT>(wv, c8, tv);
+      }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        dw[e] += g[e] * xv[e] * it;
-        dot[i] += wv8[e] * g[e] * xv[e];
+      for (int i = 0; i < TW; ++i) {
+        const int t = t0 + i;
+        if (t >= t1) break;
+        float g[8], xv[8];
+        gvec(t, c8, tq, tk, tv, g);
+        ld8(xb + (size_t)t * dim + c8, xv);
+        const float it = inv[t];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          dw[e] += g[e] * xv[e] * it;
+          dot[i] += wv8[e] * g[e] * xv[e];
+        }
       }
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) dwn_part[prow * dim + c8 + e] = dw[e];
+    for (int e = 0; e < 8; ++e) sred[w][lane * 8 + e] = dw[e];
+    wave_reduce_store(dwn_part + prow * dim + cb, min(512, dim - cb));
   }
 #pragma unroll
-  for (int i = 0; i < pro::kTok; ++i) dot[i] = wave_sum(dot[i]);
+  for (int i = 0; i < TW; ++i) dot[i] = wave_sum(dot[i]);
   // pass B: dx
   for (int c8 = lane * 8; c8 < dim; c8 += 512) {
     float wv8[8], tq[KA][8], tk[KA][8], tv[KA][8];
@@ -216,7 +233,7 @@ __global__ __launch_bounds__(pro::kThreads) void k_pro_bwd(int Tn, int dim, cons
       load_taps<T, KT>(wv, c8, tv);
     }
 #pragma unroll
-    for (int i = 0; i < pro::kTok; ++i) {
+    for (int i = 0; i < TW; ++i) {
       const int t = t0 + i;
       if (t >= t1) break;
       float g[8], xv[8];
@@ -228,54 +245,48 @@ __global__ __launch_bounds__(pro::kThreads) void k_pro_bwd(int Tn, int dim, cons
       st8(dx + ob + (size_t)t * dim + c8, g);
     }
   }
-  // pass C: tap partials, output t reads xn[t + j - pad]
+  // pass C: tap partials, output t reads xn[t + j - pad]; one conv at a time through LDS
   if constexpr (KT > 0) {
-    for (int c8 = lane * 8; c8 < dim; c8 += 512) {
-      float wv8[8], gq[KT][8], gk[KT][8], gv[KT][8];
-      ld8(wn + c8, wv8);
+    for (int cb = 0; cb < dim; cb += 512) {
+      const int c8 = cb + lane * 8;
+      const bool on = c8 < dim;
+      float wv8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (on) ld8(wn + c8, wv8);
 #pragma unroll
-      for (int j = 0; j < KT; ++j)
+      for (int which = 0; which < 3; ++which) {
+        const T* dc = which == 0 ? dqi : (which == 1 ? dki : dvi);
+        float gt[KT][8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) gq[j][e] = gk[j][e] = gv[j][e] = 0.f;
-      for (int t = t0; t < t1; ++t) {
-        float dq[8], dk[8], dv[8];
-        const size_t o = ob + (size_t)t * dim + c8;
-        ld8(dqi + o, dq);
-        ld8(dki + o, dk);
-        ld8(dvi + o, dv);
+        for (int j = 0; j < KT; ++j)
 #pragma unroll
-        for (int j = 0; j < KT; ++j) {
-          const int s = t + j - pad;
-          if (s < 0 || s >= Tn) continue;
-          float xs[8];
-          ld8(xb + (size_t)s * dim + c8, xs);
-          const float is = inv[s];
+          for (int e = 0; e < 8; ++e) gt[j][e] = 0.f;
+        if (on) {
+          for (int t = t0; t < t1; ++t) {
+            float dd[8];
+            ld8(dc + ob + (size_t)t * dim + c8, dd);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float v = xs[e] * is * wv8[e];
-            gq[j][e] += dq[e] * v;
-            gk[j][e] += dk[e] * v;
-            gv[j][e] += dv[e] * v;
+            for (int j = 0; j < KT; ++j) {
+              const int s_ = t + j - pad;
+              if (s_ < 0 || s_ >= Tn) continue;
+              float xs[8];
+              ld8(xb + (size_t)s_ * dim + c8, xs);
+              const float is = inv[s_];
+#pragma unroll
+              for (int e = 0; e < 8; ++e) gt[j][e] += dd[e] * xs[e] * is * wv8[e];
+            }
           }
         }
+        // layout of a conv's partial: [dim][K] -> this chunk is 512 K contiguous values
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+          for (int j = 0; j < KT; ++j) sred[w][(lane * 8 + e) * KT + j] = gt[j][e];
+        wave_reduce_store(dwc_part + (prow * 3 + which) * dim * KT + (size_t)cb * KT, min(512, dim - cb) * KT);
       }
-      float* p = dwc_part + prow * 3 * dim * KT;
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-#pragma unroll
-        for (int j = 0; j < KT; ++j) {
-          p[(size_t)(c8 + e) * KT + j] = gq[j][e];
-          p[(size_t)(dim + c8 + e) * KT + j] = gk[j][e];
-          p[(size_t)(2 * dim + c8 + e) * KT + j] = gv[j][e];
-        }
     }
   }
 }
 
-// Head split + q / k MultiheadRMSNorm + gate sigmoids. ql, kl, vl [B, T, H d]; zl [B, T, nG H] gate
-// logits (no bias); qg, kg [H][d] (null: no norm); bias [nG H]. Outputs q, k, v [(b h), T, d] and
-// gates [nG][(b h), T]. Workgroup (16 tokens, (b, h)): heads_row_threads(d) threads per token row,
-// eight elements (one 16-byte vector of bf16) per thread; the row's RMS is a shuffle sum.
 // Threads per head row: d / 8 rounded up to a power of two (the extra threads hold zeros), so that
 // a row's sums are xor shuffles within an aligned lane group.
 __host__ __device__ __forceinline__ int heads_row_threads(int d) {
@@ -494,8 +505,7 @@ int atlas_prologue_bwd(int dtype, int batch, int seq_len, int dim, int conv_k, c
   if (conv && (!wq || !wk || !wv || !dq_in || !dk_in || !dv_in || !dconv_part)) return ATLAS_MEM_ERR_NULL;
   for (const void* p : {x, norm_w, dxn, dq_in, dk_in, dv_in, (const void*)dx})
     if (reinterpret_cast<uintptr_t>(p) & 15) return ATLAS_MEM_ERR_ALIGN;
-  const int ntb = (seq_len + pro::kTok - 1) / pro::kTok, wpb = pro::kThreads / 64;
-  const dim3 grid((ntb + wpb - 1) / wpb, batch), block(pro::kThreads);
+  const dim3 grid((seq_len + pro::kTok - 1) / pro::kTok, batch), block(pro::kThreads);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int K = conv ? conv_k : 0;
   auto go = [&](auto tag, auto kt) {
