@@ -23,6 +23,8 @@ template <typename T, int CH, int D>
 hipError_t launch_bwd_seg(const Geom&, const BwdPtrs<T>&, const SegGeom&, const BwdSegPtrs&, hipStream_t, bool,
                           const AggOverFwd*);
 bool walk_fwd_supported(const Geom& g);
+hipError_t launch_buf_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, const float* coef, const bf16* wsh,
+                          float* corr, hipStream_t stream);
 hipError_t launch_walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
                            float* rw, float* final_raw, float* coef, bf16* wsh, hipStream_t stream);
 
@@ -223,8 +225,11 @@ size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 // `saved` layout: segment-start states, segment aggregates (forward scratch), raw S_{T-1}, the raw
 // state at every backward-chunk boundary (written by the forward walk, read by the backward).
 struct SavedLayout {
-  size_t seg, agg, final_raw, rw, coef, wsh, bcoef, bwsh, total;
+  size_t seg, agg, final_raw, rw, coef, wsh, bcoef, bwsh, bufc, total;
 };
+
+// the specialised walks with a carried buffer take its first-chunk terms from bufwalk.hip
+bool walk_with_buffer(const Plan& pl) { return pl.esize == 2 && pl.g.has_buf && walk_fwd_supported(pl.g); }
 
 // floats per chunk coefficient record (acoef, kcoef, endc, wsend, wzend, wsmid, wzmid, midc)
 size_t coef_rec_floats(int ch) { return (size_t)2 * ch + 8 + 4 * (ch + kHaloPad); }
@@ -247,6 +252,7 @@ SavedLayout saved_layout(const Plan& pl) {
   // the backward's chunk records (input-only: formed in the forward's coefficient launch)
   L.bcoef = off; off += align256((size_t)g.BH * pl.gb.nc * coef_rec_floats(pl.CHB) * sizeof(float));
   L.bwsh = off; off += align256((size_t)g.BH * pl.gb.nc * pl.CHB * (pl.CHB + kHaloPad) * pl.esize);
+  L.bufc = off; off += align256(walk_with_buffer(pl) ? (size_t)g.BH * bufw::kCorrFloats * sizeof(float) : 0);
   L.total = off;
   return L;
 }
@@ -254,7 +260,7 @@ SavedLayout saved_layout(const Plan& pl) {
 // backward workspace: adjoint aggregates, segment-end adjoints, dS_ref partials, boundary partials,
 // token-gate (target, lag) gradients, the scalar-gradient inputs.
 struct BwdLayout {
-  size_t agg, segadj, dsref, tail, halo, dw, scal, total;
+  size_t agg, segadj, dsref, tail, halo, dw, scal, badj, total;
 };
 
 BwdLayout bwd_layout(const Plan& pl) {
@@ -270,6 +276,7 @@ BwdLayout bwd_layout(const Plan& pl) {
   L.halo = off; off += align256((size_t)g.BH * nseg * g.H * (g.DV + g.DK) * sizeof(float));
   L.dw = off; off += align256(g.gate_mode == ATLAS_GATE_TOKEN ? (size_t)g.BH * g.T * g.e * sizeof(float) : 0);
   L.scal = off; off += align256((size_t)g.BH * g.nc * scalar_block_floats(pl.CHB) * sizeof(float));
+  L.badj = off; off += align256(walk_with_buffer(pl) ? (size_t)g.BH * bufw::kAdjFloats * sizeof(float) : 0);
   L.total = off;
   return L;
 }
@@ -316,6 +323,7 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
   const SavedLayout SL = saved_layout(pl);
   unsigned char* sv = reinterpret_cast<unsigned char*>(saved);
   a.y = (T*)x->y; a.S_T = x->S_T; a.Z_T = x->Z_T; a.buf_out = x->buffer_out;
+  a.buf_corr = nullptr;
   float* seg_states = reinterpret_cast<float*>(sv + SL.seg);
   float* agg = reinterpret_cast<float*>(sv + SL.agg);
   float* final_raw = reinterpret_cast<float*>(sv + SL.final_raw);
@@ -332,8 +340,15 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
   err = hipErrorInvalidValue;
   if (g.DK == 64) {
     if constexpr (sizeof(T) == 2) {
-      if (walk_fwd_supported(g))
-        err = launch_walk_fwd(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
+      if (walk_fwd_supported(g)) {
+        err = hipSuccess;
+        if (walk_with_buffer(pl)) {
+          float* corr = reinterpret_cast<float*>(sv + SL.bufc);
+          err = launch_buf_fwd(g, a, pl.sg, coef, wsh, corr, s);
+          a.buf_corr = corr;
+        }
+        if (err == hipSuccess) err = launch_walk_fwd(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
+      }
       else
         err = launch_fwd_seg<T, 64, 64>(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
     }
@@ -374,6 +389,7 @@ int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, voi
   p.coef = const_cast<float*>(reinterpret_cast<const float*>(sv + SL.bcoef));
   p.wsh = const_cast<unsigned char*>(sv + SL.bwsh);
   p.scal = reinterpret_cast<float*>(w + L.scal);
+  p.buf_adj = walk_with_buffer(pl) ? reinterpret_cast<float*>(w + L.badj) : nullptr;
   hipError_t err = hipErrorInvalidValue;
   // the specialised walks run as a pair: the forward saved its states in their layout
   const bool walk = sizeof(T) == 2 && walk_fwd_supported(pl.g);

@@ -59,6 +59,8 @@ struct FwdPtrs {
   const T* lr; const T* decay; const T* beta; const T* gate;
   const float* S_ref; const float* S0; const float* Z0; const float* buf_in;
   T* y; float* S_T; float* Z_T; float* buf_out;
+  // the specialised walks with a carried buffer: its first-chunk terms (bufwalk.hip), else null
+  const float* buf_corr;
 };
 
 template <typename T>

@@ -899,6 +899,7 @@ hipError_t launch_walk_bwd_kernel(const Geom& g, const BwdPtrs<bf16>& a, const S
                                   hipStream_t stream);
 hipError_t launch_scalar_chain(const Geom& g, const BwdPtrs<bf16>& a, const BwdSegPtrs& p, const SegGeom& sg,
                                bool with_fixup, hipStream_t stream);
+hipError_t launch_buf_bwd(const Geom& g, const BwdPtrs<bf16>& a, const BwdSegPtrs& p, hipStream_t stream);
 
 // walk: run the specialised reverse walk (walk_bwd.hip, bf16 with d = 64 only) in place of k_bwd_seg
 // ag (the specialised path): adjoint aggregates over the forward's chunks (seg_common.h).
@@ -947,6 +948,8 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
       err = launch_walk_bwd_kernel(g, a, sg, p, stream);
       prof_end(KID_BWD_CHUNK, stream);
       if (err != hipSuccess) return err;
+      // a carried buffer: its first-chunk terms, before the scalar chain reads chunk 0's record
+      if (p.buf_adj && (err = launch_buf_bwd(g, a, p, stream)) != hipSuccess) return err;
     }
   }
   if (!walk) {

@@ -39,7 +39,19 @@ struct BwdSegPtrs {
   float* coef;               // [BH][nc][CoefRec] chunk coefficient records (k_chunk_coef)
   void* wsh;                 // [BH][nc][CH][SPM] Ws[s, t-1] of every chunk (input element type)
   float* scal;               // [BH][nc][ScalarBlock] per-chunk inputs of the scalar gradients
+  float* buf_adj;            // [BH][2][D][D] first chunk's end adjoint (specialised walk with a carried buffer)
 };
+
+// The carried buffer on the specialised walks (bufwalk.hip, d = 64). Per row, its first-chunk terms:
+// the state corrections after the forward chunk's last token (end) and after token Lmid - 1 (mid),
+// the same end terms carried to the end of segment 0 (added to its aggregate by the segment scan),
+// and the y corrections of the first forward chunk's targets.
+namespace bufw {
+constexpr int D = 64, CHF = 64, CHB = 32;
+constexpr int SE = 0, ZE = D * D, SM = 2 * D * D, ZM = 3 * D * D, AU = 4 * D * D, AV = 5 * D * D, Y = 6 * D * D;
+constexpr int kCorrFloats = 6 * D * D + CHF * D;
+constexpr int kAdjFloats = 2 * D * D;
+}
 
 // Per backward chunk, written by the reverse walk and read by k_bwd_scalar (fp32):
 //   Lm[q][s] = (dy_q . delta_s)(psi_q . phi_s)   [CH][SPM]

@@ -70,6 +70,11 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg_scan(const Geom g, const f
       U[u] = aj[idx]; V[u] = aj[D * D + idx];
       ta[u] = aj[2 * D * D]; tk[u] = aj[2 * D * D + 1]; tbb[u] = aj[2 * D * D + 2];
     }
+    if (j0 == 0 && a.buf_corr) {   // the specialised walks' carried buffer: its terms at segment 0's end
+      const float* bc = a.buf_corr + (size_t)bh * bufw::kCorrFloats;
+      U[0] += bc[bufw::AU + idx];
+      V[0] += bc[bufw::AV + idx];
+    }
 #pragma unroll
     for (int u = 0; u < kScanBatch; ++u) {
       const int js = j0 + u;

@@ -80,7 +80,7 @@ struct RegPf {
 
 }  // namespace wb
 
-template <bool MAPE, int HC>
+template <bool MAPE, int HC, bool BUF>
 __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const BwdPtrs<bf16> a, const SegGeom sg,
                                                             const BwdSegPtrs p) {
   using namespace wb;
@@ -386,6 +386,17 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
     {   // the chunk-end adjoint's bf16 copies (read by phases B, C), then the chunk-start adjoint:
         //   dS_in = a dS_end + sum_t a_{t-1} dy_t psi_t^T,  dZ_in = b dZ_end - kappa dS_end - sum_t kappa_{t-1} dy_t psi_t^T
       const float ae = rec[R_ENDC], ke = rec[R_ENDC + 1], be = rec[R_ENDC + 2];
+      if (BUF && c == 0) {   // chunk 0's end adjoint, for the carried buffer's terms (bufwalk.hip)
+        float* ba = p.buf_adj + (size_t)bh * bufw::kAdjFloats;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int off = (32 * qw + 16 * u + 4 * gq + r) * D + 16 * kt + m;
+            ba[off] = dS[u][r];
+            ba[DD + off] = dZ[u][r];
+          }
+      }
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int i0 = 32 * qw + 16 * u + 4 * gq;
@@ -618,19 +629,21 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
 
 size_t walk_bwd_smem_bytes() { return sizeof(wb::Smem); }
 
-template <bool MAPE, int HC>
+template <bool MAPE, int HC, bool BUF = false>
 hipError_t launch_walk_bwd_h(const Geom& g, const BwdPtrs<bf16>& a, const SegGeom& sg, const BwdSegPtrs& p,
                              hipStream_t stream) {
   const size_t smem = sizeof(wb::Smem);
-  const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_bwd<MAPE, HC>),
+  const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_bwd<MAPE, HC, BUF>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL((k_walk_bwd<MAPE, HC>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, p);
+  hipLaunchKernelGGL((k_walk_bwd<MAPE, HC, BUF>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, p);
   return hipGetLastError();
 }
 template <bool MAPE>
 hipError_t launch_walk_bwd_m(const Geom& g, const BwdPtrs<bf16>& a, const SegGeom& sg, const BwdSegPtrs& p,
                              hipStream_t stream) {
+  // a carried buffer (window > 1): the generic-halo kernel that also leaves chunk 0's end adjoint
+  if (p.buf_adj) return launch_walk_bwd_h<MAPE, -1, true>(g, a, sg, p, stream);
   switch (g.H) {
     case 0: return launch_walk_bwd_h<MAPE, 0>(g, a, sg, p, stream);
     case 3: return launch_walk_bwd_h<MAPE, 3>(g, a, sg, p, stream);
@@ -734,7 +747,8 @@ __global__ __launch_bounds__(64 * wb::kChainWaves) void k_scalar_chain(const Geo
     float wgt = 0.f;
     if (t < L) {
       if (g.gate_mode == GATE_LAG) wgt = to_f32(a.gate[(tb + t0 + t) * e + j]);
-      else if (g.gate_mode == GATE_TOKEN) wgt = t0 + t - j >= 0 ? to_f32(a.gate[tb + t0 + t - j]) : 0.f;
+      else if (g.gate_mode == GATE_TOKEN)   // a buffer source carries its gate inside B: weight 1
+        wgt = t0 + t - j >= 0 ? to_f32(a.gate[tb + t0 + t - j]) : (g.has_buf ? 1.f : 0.f);
       else wgt = 1.f;
     }
     if (s >= 0 && s < NSRC) U.W[s][t] = wgt;

@@ -11,7 +11,9 @@
 //    MFMAs (walk_common.h: chained operands), so only the staged inputs and the state copy go
 //    through LDS;
 //  * rows are read through per-row buffer resources: the halo before the first token and the
-//    rows past T read as zeros, and y rows past T are dropped by the range check.
+//    rows past T read as zeros, and y rows past T are dropped by the range check;
+//  * a carried buffer (BUF): its sources are chunk 0's halo; their terms (bufwalk.hip) are added to
+//    chunk 0's y and to the states after it.
 // Sources of a chunk are the e - 1 halo tokens followed by the chunk's 64 tokens, s = 0 .. 79
 // (window e <= 17); source s is token t0 - (e - 1) + s.
 //
@@ -155,7 +157,7 @@ __device__ __forceinline__ f32x4 tile_or_zero(const f32x4 (&a)[N], int idx) {
 }  // namespace wf
 
 // One segment of one row. FULL = false: aggregate pass; FULL = true: full walk.
-template <bool FULL, bool MAPE>
+template <bool FULL, bool MAPE, bool BUF>
 __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg,
                                          const float* seg_states, float* rw, float* final_raw, const float* coef,
                                          const bf16* wsh_all, unsigned char* smem_raw) {
@@ -286,6 +288,8 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
     }
 
     const float* rec = st.rec;
+    // the carried buffer's first-chunk terms (bufwalk.hip), chunk 0 of a call with a buffer only
+    const float* bufc = (BUF && c == 0) ? a.buf_corr + (size_t)bh * bufw::kCorrFloats : nullptr;
     // chained operands over the source slots of k-step q: tiles 2q (slots 0..3) and 2q+1 (4..7)
     constexpr int NQ = (NST + 1) / 2;   // 3
     bf16x8 fws[NQ], fwz[NQ];
@@ -334,9 +338,16 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
         }
         const int tau = 16 * tt + m;
         const float ac = rec[R_ACOEF + tau], kc = rec[R_KCOEF + tau];
+        float yv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yv[r] = -aq[r] + ac * as[r] - kc * az[r];
+        if (BUF && bufc) {   // the carried buffer's sources (chunk 0 only)
+          const float4 yc = *reinterpret_cast<const float4*>(bufc + bufw::Y + tau * D + i0);
+          yv[0] += yc.x; yv[1] += yc.y; yv[2] += yc.z; yv[3] += yc.w;
+        }
         u32x2v out;
-        out[0] = pack_bf16x2(-aq[0] + ac * as[0] - kc * az[0], -aq[1] + ac * as[1] - kc * az[1]);
-        out[1] = pack_bf16x2(-aq[2] + ac * as[2] - kc * az[2], -aq[3] + ac * as[3] - kc * az[3]);
+        out[0] = pack_bf16x2(yv[0], yv[1]);
+        out[1] = pack_bf16x2(yv[2], yv[3]);
         bst8(ry, (uint32_t)(((t0 + tau) * D + i0) * 2), out);
       }
     }
@@ -378,10 +389,15 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
               au = mma_bf16(fsm[q], fb[j][q], au);
               av = mma_bf16(fzm[q], fb[j][q], av);
             }
+            const int kk = 32 * th + 16 * j + m;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               Sm_[j][r] = ma * Sr[j][r] - mk * Zr[j][r] - au[r];
               Zm_[j][r] = g.momentum ? (mb * Zr[j][r] + av[r]) : 0.f;
+              if (BUF && bufc) {
+                Sm_[j][r] += bufc[bufw::SM + (i0 + r) * D + kk];
+                Zm_[j][r] += bufc[bufw::ZM + (i0 + r) * D + kk];
+              }
             }
           }
           save_state(c * rb + 1, Sm_, Zm_);
@@ -406,6 +422,23 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
         if constexpr (FULL) {
           store4<bf16>(&sm.SbT[b ^ 1][k][i0], Sr[j][0], Sr[j][1], Sr[j][2], Sr[j][3]);
           store4<bf16>(&sm.ZbT[b ^ 1][k][i0], Zr[j][0], Zr[j][1], Zr[j][2], Zr[j][3]);
+        }
+      }
+      if constexpr (BUF) {
+        if (bufc) {   // chunk 0: the buffer sources' terms of the end state (and its bf16 copy again)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int k = 32 * th + 16 * j + m;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              Sr[j][r] += bufc[bufw::SE + (i0 + r) * D + k];
+              Zr[j][r] += bufc[bufw::ZE + (i0 + r) * D + k];
+            }
+            if constexpr (FULL) {
+              store4<bf16>(&sm.SbT[b ^ 1][k][i0], Sr[j][0], Sr[j][1], Sr[j][2], Sr[j][3]);
+              store4<bf16>(&sm.ZbT[b ^ 1][k][i0], Zr[j][0], Zr[j][1], Zr[j][2], Zr[j][3]);
+            }
+          }
         }
       }
       if constexpr (FULL) {
@@ -466,34 +499,36 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
   }
 }
 
+// (a carried buffer's terms reach segment 0's aggregate in the segment scan, not here)
 template <bool MAPE>
 __global__ __launch_bounds__(kSegThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_walk_agg(
     const Geom g, const FwdPtrs<bf16> a, const SegGeom sg, float* agg, const float* coef) {
   if (geom_skip(g)) return;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  walk_fwd<false, MAPE>(g, a, sg, agg, nullptr, nullptr, nullptr, coef, nullptr, smem_raw);
+  walk_fwd<false, MAPE, false>(g, a, sg, agg, nullptr, nullptr, nullptr, coef, nullptr, smem_raw);
 }
 
-template <bool MAPE>
+template <bool MAPE, bool BUF>
 __global__ __launch_bounds__(kSegThreads) void k_walk_full(const Geom g, const FwdPtrs<bf16> a, const SegGeom sg,
                                                              const float* seg_states, float* rw, float* final_raw,
                                                              const float* coef, const bf16* wsh) {
   if (geom_skip(g)) return;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  walk_fwd<true, MAPE>(g, a, sg, nullptr, seg_states, rw, final_raw, coef, wsh, smem_raw);
+  walk_fwd<true, MAPE, BUF>(g, a, sg, nullptr, seg_states, rw, final_raw, coef, wsh, smem_raw);
 }
 
 template <typename T, int D>
 hipError_t launch_fwd_seg_scan(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg, const float* agg,
                                float* seg_states, hipStream_t stream);
 
-// The specialised walks cover bf16, d = 64, window <= 17, no clamp at scan_chunk_len boundaries and
-// no carried buffer; everything else runs through seg_fwd.hip.
+// The specialised walks cover bf16, d = 64, window <= 17 and no clamp at scan_chunk_len boundaries
+// (a carried buffer enters through bufwalk.hip's first-chunk terms); everything else runs through
+// seg_fwd.hip.
 bool walk_fwd_supported(const Geom& g) {
-  return g.DK == 64 && g.DV == 64 && g.Lc == wf::CH && g.H <= wf::SP - wf::CH && g.clamp_every == 0 && !g.has_buf;
+  return g.DK == 64 && g.DV == 64 && g.Lc == wf::CH && g.H <= wf::SP - wf::CH && g.clamp_every == 0;
 }
 
-template <bool MAPE>
+template <bool MAPE, bool BUF>
 static hipError_t launch_walks(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg,
                                float* seg_states, float* rw, float* final_raw, float* coef, bf16* wsh,
                                hipStream_t stream) {
@@ -512,12 +547,12 @@ static hipError_t launch_walks(const Geom& g, const FwdPtrs<bf16>& a, const SegG
   }
   if ((err = launch_fwd_seg_scan<bf16, 64>(g, a, sg, agg, seg_states, stream)) != hipSuccess) return err;
   const size_t smem = sizeof(wf::Smem<true>);
-  err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_full<MAPE>),
+  err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_full<MAPE, BUF>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (err != hipSuccess) return err;
   prof_name(KID_FWD_WALK, "k_walk_full");
   prof_begin(KID_FWD_WALK, stream);
-  hipLaunchKernelGGL((k_walk_full<MAPE>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg,
+  hipLaunchKernelGGL((k_walk_full<MAPE, BUF>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg,
                      (const float*)seg_states, rw, final_raw, (const float*)coef, (const bf16*)wsh);
   prof_end(KID_FWD_WALK, stream);
   return hipGetLastError();
@@ -526,9 +561,12 @@ static hipError_t launch_walks(const Geom& g, const FwdPtrs<bf16>& a, const SegG
 hipError_t launch_walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
                            float* rw, float* final_raw, float* coef, bf16* wsh, hipStream_t stream) {
   // the chunk coefficient records (coef, wsh) are formed by the caller first
-  return g.map_mode == MAP_ELEMENTWISE
-             ? launch_walks<true>(g, a, sg, agg, seg_states, rw, final_raw, coef, wsh, stream)
-             : launch_walks<false>(g, a, sg, agg, seg_states, rw, final_raw, coef, wsh, stream);
+  const bool mape = g.map_mode == MAP_ELEMENTWISE, buf = a.buf_corr != nullptr;
+  if (buf)
+    return mape ? launch_walks<true, true>(g, a, sg, agg, seg_states, rw, final_raw, coef, wsh, stream)
+                : launch_walks<false, true>(g, a, sg, agg, seg_states, rw, final_raw, coef, wsh, stream);
+  return mape ? launch_walks<true, false>(g, a, sg, agg, seg_states, rw, final_raw, coef, wsh, stream)
+              : launch_walks<false, false>(g, a, sg, agg, seg_states, rw, final_raw, coef, wsh, stream);
 }
 
 }  // namespace atlas

@@ -30,6 +30,9 @@ CASES = [
     # C3 as the drop-in cell calls it: a carried (zero) buffer
     (Case("c3_full_zero_buffer", BH=32, T=4096, d=64, e=4, gate='lag', momentum=True, buffer=True,
           buffer_scale=0.0, dtype=BF16, seed=103), (0, 15, 31)),
+    # C3 with a carried nonzero buffer (a state from a previous call): the walks with its first-chunk terms
+    (Case("c3_full_buffer", BH=32, T=4096, d=64, e=4, gate='lag', momentum=True, buffer=True, states=0.1,
+          dtype=BF16, seed=108), (0, 31)),
     # C3 with scan_chunk_len = 64, as the drop-in cell runs it ("chunk 64"): segment-parallel with the
     # clamp points checked on the device
     (Case("c3_full_clamp64", BH=32, T=4096, d=64, e=4, gate='lag', momentum=True, clamp_every=64, dtype=BF16,

@@ -49,7 +49,7 @@ CASES = [
     Case("fp32_d16_padded", BH=3, T=45, d=16, e=3, gate='token', momentum=True, buffer=True, states=0.2, seed=16),
     Case("bf16_d48_padded", BH=2, T=70, d=48, e=2, gate='lag', momentum=True, buffer=True, states=0.1,
          map_degree=2, dtype=BF16, seed=17),
-    # the specialised bf16, d = 64 walks (no carried buffer, no scan_chunk_len clamp): window at the
+    # the specialised bf16, d = 64 walks (no scan_chunk_len clamp): window at the
     # halo limit (e = 17) and just past it (e = 18, general kernels), chunk-edge lengths, many segments
     Case("bf16_walk_e16_token", BH=3, T=1000, d=64, e=16, gate='token', momentum=True, states=0.1, dtype=BF16,
          seed=18),
@@ -94,6 +94,28 @@ CASES = [
          decay_shift=7.0, dtype=BF16, backward=False, seed=36),
     Case("bf16_buffer_clamp64_quiet", BH=3, T=400, d=64, e=3, gate='token', momentum=True, buffer=True, states=0.1,
          clamp_every=64, dtype=BF16, seed=37),
+    # a carried buffer on the specialised walks: its sources are chunk 0's halo (first-chunk terms
+    # from bufwalk.hip), one chunk per segment, segment 0 of several chunks (its aggregate carries
+    # the terms through them), the largest walk window, rows shorter than a backward chunk and than
+    # the halo, an elementwise map, and with no buffer_out gradient (fixup inside the scalar launch)
+    Case("bf16_walk_buf_lag", BH=3, T=300, d=64, e=4, gate='lag', momentum=True, buffer=True, states=0.1,
+         dtype=BF16, seed=40),
+    Case("bf16_walk_buf_multiseg_token", BH=64, T=1100, d=64, e=4, gate='token', momentum=True, buffer=True,
+         states=0.1, dtype=BF16, seed=41),
+    Case("bf16_walk_buf_none_nomom_map2", BH=2, T=100, d=64, e=3, gate=None, momentum=False, buffer=True,
+         states=0.1, map_degree=2, dtype=BF16, seed=42),
+    Case("bf16_walk_buf_e17_lag_nomom", BH=2, T=129, d=64, e=17, gate='lag', momentum=False, buffer=True,
+         states=0.1, dtype=BF16, seed=43),
+    Case("bf16_walk_buf_T20_token", BH=2, T=20, d=64, e=5, gate='token', momentum=True, buffer=True, states=0.1,
+         dtype=BF16, seed=44),
+    Case("bf16_walk_buf_T3_lt_halo", BH=2, T=3, d=64, e=6, gate='lag', momentum=True, buffer=True, states=0.1,
+         dtype=BF16, seed=45),
+    Case("bf16_walk_buf_T33_map3", BH=2, T=33, d=64, e=4, gate='lag', momentum=True, buffer=True, states=0.1,
+         map_degree=3, dtype=BF16, seed=46),
+    Case("bf16_walk_buf_lag_no_dbuf", BH=40, T=700, d=64, e=4, gate='lag', momentum=True, buffer=True, states=0.1,
+         grad_buffer=False, dtype=BF16, seed=47),
+    Case("bf16_walk_buf_token_no_dbuf", BH=3, T=300, d=64, e=3, gate='token', momentum=True, buffer=True,
+         states=0.1, grad_buffer=False, dtype=BF16, seed=48),
     Case("fp32_clamp64_multiseg_quiet", BH=40, T=300, d=32, e=2, gate=None, momentum=True, states=0.2, clamp_every=64,
          seed=38),
     Case("fp32_clamp64_fires_late", BH=2, T=200, d=32, e=2, gate='token', momentum=False, states=60.0, clamp_every=64,
