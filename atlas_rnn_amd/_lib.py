@@ -65,7 +65,7 @@ EXPORTED_SYMBOLS = (
     "atlas_mem_mfma_selftest",
 )
 
-NKERNELS = 12
+NKERNELS = 14
 
 
 class Problem(ctypes.Structure):

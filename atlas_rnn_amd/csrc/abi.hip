@@ -23,8 +23,9 @@ template <typename T, int CH, int D>
 hipError_t launch_bwd_seg(const Geom&, const BwdPtrs<T>&, const SegGeom&, const BwdSegPtrs&, hipStream_t, bool,
                           const AggOverFwd*);
 bool walk_fwd_supported(const Geom& g);
-hipError_t launch_buf_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, const float* coef, const bf16* wsh,
-                          float* corr, hipStream_t stream);
+hipError_t launch_buf_state(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, const float* coef, float* corr,
+                            hipStream_t stream);
+hipError_t launch_buf_y(const Geom& g, const FwdPtrs<bf16>& a, const bf16* wsh, hipStream_t stream);
 hipError_t launch_walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
                            float* rw, float* final_raw, float* coef, bf16* wsh, hipStream_t stream);
 
@@ -84,7 +85,7 @@ Profiler& prof() { static Profiler p; return p; }
 const char* kKernelNames[KID_COUNT] = {"k_fwd_seg_agg", "k_fwd_seg", "k_buffer_out", "k_bwd_seg_agg",
                                        "k_bwd_seg", "k_bwd_seg_fixup", "k_seg_reduce_dsref", "k_fwd_seg_scan",
                                        "k_bwd_seg_scan", "k_chunk_coef_fwd", "k_chunk_coef_bwd",
-                                       "k_bwd_scalar"};
+                                       "k_bwd_scalar", "k_buf_fwd", "k_buf_bwd"};
 }  // namespace
 
 namespace atlas {
@@ -344,10 +345,11 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
         err = hipSuccess;
         if (walk_with_buffer(pl)) {
           float* corr = reinterpret_cast<float*>(sv + SL.bufc);
-          err = launch_buf_fwd(g, a, pl.sg, coef, wsh, corr, s);
+          err = launch_buf_state(g, a, pl.sg, coef, corr, s);
           a.buf_corr = corr;
         }
         if (err == hipSuccess) err = launch_walk_fwd(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);
+        if (err == hipSuccess && a.buf_corr) err = launch_buf_y(g, a, wsh, s);
       }
       else
         err = launch_fwd_seg<T, 64, 64>(g, a, pl.sg, agg, seg_states, rw, final_raw, coef, wsh, s);

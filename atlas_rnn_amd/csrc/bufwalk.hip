@@ -5,22 +5,23 @@
 // the window over [__omega_buf; gated]). Source slot s of the first chunk is token s - (e - 1), so
 // the buffer sources are the halo slots s < e - 1 of chunk 0, whose token rows the walks read as
 // zeros. Every buffer term is linear in B and lies in chunk 0 (the later chunks see it through the
-// state), so the walks keep their chunk code and take these terms from two small launches:
+// state), so the walks keep their chunk code and take these terms from three small launches:
 //
-//   k_buf_fwd (before the walks), with the forward chunk's coefficient record and Ws block:
-//     y corrections     yc[t] = -sum_s Ws[s, t-1] B_s psi_t                      (t < 64)
-//     state corrections dS_end = -sum_s Ws[s, end] B_s,  dZ_end = sum_s Wz[s, end] B_s, and the same
-//                       after token Lmid - 1 (the saved backward-chunk boundary); Z terms only with
-//                       momentum. k_walk_full adds them at the end of chunk 0 and to the y of chunk
-//                       0's targets; carried through segment 0's later chunks (their end scalars a,
-//                       kappa, b), the end terms are added to segment 0's aggregate by the segment scan.
+//   k_buf_state (before the walks), from the forward chunk's coefficient record:
+//     dS_end = -sum_s Ws[s, end] B_s,  dZ_end = sum_s Wz[s, end] B_s, the same after token Lmid - 1
+//     (the saved backward-chunk boundary), Z terms only with momentum. k_walk_full adds them to the
+//     states after chunk 0; carried through segment 0's later chunks (their end scalars a, kappa, b)
+//     the end terms are added to segment 0's aggregate by the segment scan.
+//   k_buf_y (after k_walk_full), with the forward chunk's Ws block:
+//     y_t += -sum_s Ws[s, t-1] B_s psi_t                                             (t < 64)
 //   k_buf_bwd (after k_walk_bwd, before the scalar chain), with the backward chunk's records and the
 //   chunk-0 end adjoint (dS_e, dZ_e) the reverse walk leaves in buf_adj:
 //     d buffer_in[s] = Wz[s, end] dZ_e - Ws[s, end] dS_e - sum_q Ws[s, q-1] dy_q psi_q^T
 //     records of chunk 0: hS[s] += <dS_e, B_s>, hZ[s] += <dZ_e, B_s>, Lm[q][s] += dy_q^T B_s psi_q
 //     dq[q] += -(sum_s Ws[s, q-1] B_s^T dy_q) * map'(q)                             (q < 32)
 //   (the same terms as the general kernels' first-chunk buffer code, seg_fwd.h / seg_bwd.hip).
-// Workgroups of 256 threads; fp32 arithmetic on the fp32 buffer.
+// The products run on fp32 matrix cores (v_mfma_f32_16x16x4_f32, mem_common.h's NT convention) with
+// the operands staged in LDS as fp32; y and dq are read, corrected and rounded to bf16 again.
 #include "mem_common.h"
 #include "mem_params.h"
 #include "seg_common.h"
@@ -33,6 +34,9 @@ namespace {
 
 constexpr int kBwThreads = 256;
 constexpr int D = bufw::D;
+constexpr int P = D + 1;   // LDS pitch of the fp32 operand rows
+
+typedef MM<float> MF;
 
 template <int CH>
 struct RecOff {
@@ -43,90 +47,147 @@ struct RecOff {
 
 __device__ __forceinline__ float bf16f(bf16 x) { return static_cast<float>(x); }
 
-// one buffer slot [D][D] fp32 -> LDS (pitch D + 1)
-__device__ __forceinline__ void stage_slot(float (*sB)[D + 1], const float* Bs) {
-  for (int v = threadIdx.x; v < D * D / 4; v += kBwThreads) {
-    const float4 x = reinterpret_cast<const float4*>(Bs)[v];
-    const int i = (4 * v) / D, k = (4 * v) % D;
-    sB[i][k] = x.x; sB[i][k + 1] = x.y; sB[i][k + 2] = x.z; sB[i][k + 3] = x.w;
+// rows [0, n) of D bf16 values (row r at src + r * D) -> dst[r][*] fp32, mapped; rows n .. nr - 1 zero
+__device__ __forceinline__ void stage_rows(float (*dst)[P], const bf16* src, int n, int nr, int map_mode, int deg) {
+  for (int v = threadIdx.x; v < nr * (D / 8); v += kBwThreads) {
+    const int r = v / (D / 8), c = (v % (D / 8)) * 8;
+    float x[8];
+    if (r < n) {
+      const uint4 w = *reinterpret_cast<const uint4*>(src + (size_t)r * D + c);
+      const unsigned u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        x[2 * h] = __builtin_bit_cast(float, u[h] << 16);
+        x[2 * h + 1] = __builtin_bit_cast(float, u[h] & 0xffff0000u);
+      }
+      if (map_mode == MAP_ELEMENTWISE) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = poly_map(x[e], deg);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dst[r][c + e] = x[e];
   }
 }
 
-// grid (CHF / 16, BH): workgroup x forms the y corrections of tokens 16 x .. 16 x + 15 and a quarter
-// of the state corrections (elements 1024 x ..). G0: the chunks of segment 0 when there are several
-// segments (the end terms are carried through its chunks 1 .. G0 - 1 for its aggregate), else 0.
-__global__ __launch_bounds__(kBwThreads) void k_buf_fwd(const Geom g, const FwdPtrs<bf16> a, const float* __restrict__ coef,
-                                                        const bf16* __restrict__ wsh, float* __restrict__ corr, int G0) {
+// one buffer slot [D][D] fp32 -> dst (pitch P)
+__device__ __forceinline__ void stage_slot(float (*dst)[P], const float* Bs) {
+  for (int v = threadIdx.x; v < D * D / 4; v += kBwThreads) {
+    const float4 x = reinterpret_cast<const float4*>(Bs)[v];
+    const int i = (4 * v) / D, k = (4 * v) % D;
+    dst[i][k] = x.x; dst[i][k + 1] = x.y; dst[i][k + 2] = x.z; dst[i][k + 3] = x.w;
+  }
+}
+
+// A product's k order is free as long as both operands follow it: the products below give lane
+// group kq = lane >> 4 the k values 16 kq + j at step j (16 steps over D = 64), so that a lane's
+// operand values are 16 consecutive floats of one row.
+
+// The end scalars (a, kappa, b) of a run of chunks composed in order, later o earlier:
+// (a2 a1, a2 k1 + k2 b1, b2 b1).
+struct Akb {
+  float a, k, b;
+};
+__device__ __forceinline__ Akb compose(const Akb& later, const Akb& earlier) {
+  return Akb{later.a * earlier.a, later.a * earlier.k + later.k * earlier.b, later.b * earlier.b};
+}
+
+// grid (D * D / kBwThreads, BH), one state element per thread. G0: the chunks of segment 0 when
+// there are several segments (its aggregate gets the end terms carried through chunks 1 .. G0 - 1),
+// else 0.
+__global__ __launch_bounds__(kBwThreads) void k_buf_state(const Geom g, const FwdPtrs<bf16> a,
+                                                          const float* __restrict__ coef, float* __restrict__ corr,
+                                                          int G0) {
+  if (geom_skip(g)) return;
+  constexpr int CH = bufw::CHF;
+  using R = RecOff<CH>;
+  __shared__ Akb part[kBwThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, bh = blockIdx.y;
+  const int idx = blockIdx.x * kBwThreads + tid;
+  const int H = g.H;
+  const float* rec = coef + (size_t)bh * g.nc * CoefRec<CH>::SIZE;   // chunk 0
+  float* out = corr + (size_t)bh * bufw::kCorrFloats;
+  const float* Bb = a.buf_in + (size_t)bh * H * D * D + idx;
+  float se = 0.f, ze = 0.f, sm = 0.f, zm = 0.f;
+  for (int s = 0; s < H; ++s) {
+    const float b = Bb[(size_t)s * D * D];
+    se -= rec[R::WSEND + s] * b;
+    ze += rec[R::WZEND + s] * b;
+    sm -= rec[R::WSMID + s] * b;
+    zm += rec[R::WZMID + s] * b;
+  }
+  const float zk = g.momentum ? 1.f : 0.f;
+  // chunks 1 .. G0 - 1 with no input: each thread composes its run, then each wave its lanes' (a
+  // tree in chunk order) and one thread the four waves'
+  const int nrun = G0 > 1 ? (G0 - 1 + kBwThreads - 1) / kBwThreads : 0;
+  Akb x{1.f, 0.f, 1.f};
+  for (int j = 0; j < nrun; ++j) {
+    const int c = 1 + tid * nrun + j;
+    if (c < G0) {
+      const float* rc = rec + (size_t)c * CoefRec<CH>::SIZE;
+      x = compose(Akb{rc[R::ENDC], rc[R::ENDC + 1], zk * rc[R::ENDC + 2]}, x);
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const Akb y{__shfl_down(x.a, o, 64), __shfl_down(x.k, o, 64), __shfl_down(x.b, o, 64)};
+    if ((lane & (2 * o - 1)) == 0 && lane + o < 64) x = compose(y, x);
+  }
+  if (lane == 0) part[tid >> 6] = x;
+  __syncthreads();
+  Akb t = part[0];
+#pragma unroll
+  for (int w = 1; w < kBwThreads / 64; ++w) t = compose(part[w], t);
+  out[bufw::SE + idx] = se;
+  out[bufw::ZE + idx] = zk * ze;
+  out[bufw::SM + idx] = sm;
+  out[bufw::ZM + idx] = zk * zm;
+  out[bufw::AU + idx] = t.a * se - t.k * zk * ze;
+  out[bufw::AV + idx] = zk * t.b * ze;
+}
+
+// grid (CHF / 16, BH): workgroup x corrects y of tokens 16 x .. 16 x + 15, wave w rows 16 w ..:
+//   Y[i][t] = -sum_s sum_k B_s[i][k] (Ws[s, t-1] psi_t[k])   (one product over K = (e-1) * D)
+__global__ __launch_bounds__(kBwThreads) void k_buf_y(const Geom g, const FwdPtrs<bf16> a, const bf16* __restrict__ wsh) {
   if (geom_skip(g)) return;
   constexpr int CH = bufw::CHF, TG = 16;
   using R = RecOff<CH>;
-  __shared__ float sB[D][D + 1];
-  __shared__ float sp[TG][D + 1];
-  const int tid = threadIdx.x, bh = blockIdx.y, xg = blockIdx.x;
+  __shared__ float sps[TG][P];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, bh = blockIdx.y, t0 = blockIdx.x * TG;
   const int H = g.H, L = min(g.T, CH);
-  const float* rec = coef + (size_t)bh * g.nc * CoefRec<CH>::SIZE;       // chunk 0
-  const bf16* w0 = wsh + (size_t)bh * g.nc * CH * R::SPM;                 // chunk 0: Ws rows [t][s]
-  float* out = corr + (size_t)bh * bufw::kCorrFloats;
-  for (int idx = tid; idx < TG * D; idx += kBwThreads) {
-    const int t = TG * xg + idx / D, k = idx % D;
-    sp[idx / D][k] = t < L ? ld_map(a.q, ((size_t)bh * g.T + t) * D + k, g.map_mode, g.map_deg) : 0.f;
-  }
-  const int tt = tid >> 4, il = tid & 15, t = TG * xg + tt;   // y rows il + 16 r of token t
-  const int eb = xg * (D * D / 4) + 4 * tid;                   // state elements eb .. eb + 3
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  float se[4] = {0.f, 0.f, 0.f, 0.f}, ze[4] = {0.f, 0.f, 0.f, 0.f};
-  float sm[4] = {0.f, 0.f, 0.f, 0.f}, zm[4] = {0.f, 0.f, 0.f, 0.f};
-  const float* Bb = a.buf_in + (size_t)bh * H * D * D;
+  if (t0 >= L) return;   // workgroup-uniform
+  const bf16* w0 = wsh + (size_t)bh * g.nc * CH * R::SPM;   // chunk 0: Ws rows [t][s]
+  stage_rows(sps, a.q + ((size_t)bh * g.T + t0) * D, min(TG, L - t0), TG, g.map_mode, g.map_deg);
+  __syncthreads();
+  const int tl = lane & 15, kq = lane >> 4;
+  // A = B_s rows 16 w + tl straight from memory: 16 consecutive k per lane
+  const float* Brow = a.buf_in + ((size_t)bh * H * D + 16 * w + tl) * D + 16 * kq;
+  f32x4 acc = zero4();
   for (int s = 0; s < H; ++s) {
-    const float* Bs = Bb + (size_t)s * D * D;
-    __syncthreads();   // the previous slot's readers are done
-    stage_slot(sB, Bs);
-    __syncthreads();
-    const float w = t < L ? bf16f(w0[(size_t)t * R::SPM + s]) : 0.f;
+    float4 bv[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = il + 16 * r;
-      float dot = 0.f;
-#pragma unroll 16
-      for (int k = 0; k < D; ++k) dot += sB[i][k] * sp[tt][k];
-      acc[r] -= w * dot;
-    }
-    const float4 b = *reinterpret_cast<const float4*>(Bs + eb);
-    const float bv[4] = {b.x, b.y, b.z, b.w};
-    const float ws = rec[R::WSEND + s], wz = rec[R::WZEND + s], wsm = rec[R::WSMID + s], wzm = rec[R::WZMID + s];
+    for (int v = 0; v < 4; ++v) bv[v] = reinterpret_cast<const float4*>(Brow + (size_t)s * D * D)[v];
+    const float wt = t0 + tl < L ? bf16f(w0[(size_t)(t0 + tl) * R::SPM + s]) : 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      se[r] -= ws * bv[r];
-      ze[r] += wz * bv[r];
-      sm[r] -= wsm * bv[r];
-      zm[r] += wzm * bv[r];
+    for (int v = 0; v < 4; ++v) {
+      const float bb[4] = {bv[v].x, bv[v].y, bv[v].z, bv[v].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = MF::mma(bb[e], wt * sps[tl][16 * kq + 4 * v + e], acc);
     }
   }
+  // the accumulator is read after the loop's exit: one unconditional (zero) product first, so that
+  // the read never follows a join directly after an MFMA that was issued conditionally
+  acc = MF::mma(0.f, 0.f, acc);
+  // lane: rows 16 w + 4 kq + r of token t0 + tl
+  const int t = t0 + tl;
+  if (t < L) {
+    bf16* yp = a.y + ((size_t)bh * g.T + t) * D + 16 * w + 4 * kq;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) out[bufw::Y + t * D + il + 16 * r] = acc[r];   // zero past L
-  const float zk = g.momentum ? 1.f : 0.f;
-  // through chunks 1 .. G0 - 1 with no input: dS <- a dS - kappa dZ, dZ <- b dZ, i.e. at segment 0's
-  // end dS_A = pa dS - pk dZ, dZ_A = pb dZ
-  float pa = 1.f, pk = 0.f, pb = zk;
-  for (int c = 1; c < G0; ++c) {
-    const float* rc = rec + (size_t)c * CoefRec<CH>::SIZE;
-    const float ca = rc[R::ENDC], ck = rc[R::ENDC + 1], cb = rc[R::ENDC + 2];
-    pk = ca * pk + ck * pb;
-    pa = ca * pa;
-    pb = zk * cb * pb;
+    for (int r = 0; r < 4; ++r) yp[r] = from_f32<bf16>(bf16f(yp[r]) - acc[r]);
   }
-  *reinterpret_cast<float4*>(out + bufw::SE + eb) = make_float4(se[0], se[1], se[2], se[3]);
-  *reinterpret_cast<float4*>(out + bufw::ZE + eb) = make_float4(zk * ze[0], zk * ze[1], zk * ze[2], zk * ze[3]);
-  *reinterpret_cast<float4*>(out + bufw::SM + eb) = make_float4(sm[0], sm[1], sm[2], sm[3]);
-  *reinterpret_cast<float4*>(out + bufw::ZM + eb) = make_float4(zk * zm[0], zk * zm[1], zk * zm[2], zk * zm[3]);
-  float au[4], av[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    au[r] = pa * se[r] - pk * zk * ze[r];
-    av[r] = pb * ze[r];
-  }
-  *reinterpret_cast<float4*>(out + bufw::AU + eb) = make_float4(au[0], au[1], au[2], au[3]);
-  *reinterpret_cast<float4*>(out + bufw::AV + eb) = make_float4(av[0], av[1], av[2], av[3]);
 }
 
 // grid (e, BH): workgroup s < e - 1 forms d buffer_in[s] and slot s's record terms; workgroup e - 1
@@ -136,115 +197,116 @@ __global__ __launch_bounds__(kBwThreads) void k_buf_bwd(const Geom g, const BwdP
   constexpr int CH = bufw::CHB;
   using R = RecOff<CH>;
   using SB = ScalarBlock<CH>;
-  __shared__ float sB[D][D + 1];
-  __shared__ float sdy[CH][D + 1];
-  __shared__ float sps[CH][D + 1];
+  __shared__ float sB[D][P];
+  __shared__ float sdy[CH][P];
+  __shared__ float sps[CH][P];
   __shared__ float sw[CH];
   __shared__ float sred[2][kBwThreads / 64];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, bh = blockIdx.y, s = blockIdx.x;
+  __shared__ float slm[2][CH];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, bh = blockIdx.y, s = blockIdx.x;
+  const int tl = lane & 15, kq = lane >> 4;
   const int H = g.H, Lq = min(g.T, CH);
   const size_t tb = (size_t)bh * g.T;
   const float* rec = p.coef + (size_t)bh * g.nc * CoefRec<CH>::SIZE;                       // chunk 0
   const bf16* w0 = reinterpret_cast<const bf16*>(p.wsh) + (size_t)bh * g.nc * CH * R::SPM;  // chunk 0
   float* blk = p.scal + (size_t)bh * g.nc * SB::SIZE;                                       // chunk 0
   const float* Bb = a.buf_in + (size_t)bh * H * D * D;
-  for (int idx = tid; idx < CH * D; idx += kBwThreads) {
-    const int q = idx / D, k = idx % D;
-    sdy[q][k] = q < Lq ? bf16f(a.dy[(tb + q) * D + k]) : 0.f;
-    if (s < H) sps[q][k] = q < Lq ? ld_map(a.q, (tb + q) * D + k, g.map_mode, g.map_deg) : 0.f;
-  }
-  if (s == H) {   // dq[q][k] += -(sum_s w(q, s) sum_i B_s[i][k] dy_q[i]) map'(q[q][k]); lane: q, columns k
-    const int q = tid >> 3, kl = tid & 7;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  stage_rows(sdy, a.dy + tb * D, Lq, CH, MAP_OFF, 1);
+  if (s == H) {
+    // dq: C[k][q] = sum_s sum_i B_s[i][k] (w(q, s) dy_q[i]); wave w: features 16 w .., both token
+    // tiles; A[k][i] = B_s[i][k] straight from memory (lane: column 16 w + tl, rows 16 kq + j)
+    __syncthreads();   // dy staged
+    f32x4 acc[2] = {zero4(), zero4()};
+    const float* Bcol = Bb + (size_t)(16 * kq) * D + 16 * w + tl;
     for (int sl = 0; sl < H; ++sl) {
-      __syncthreads();
-      stage_slot(sB, Bb + (size_t)sl * D * D);
-      __syncthreads();
-      const float w = q < Lq ? bf16f(w0[(size_t)q * R::SPM + sl]) : 0.f;
+      float bc[16];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const int k = kl + 8 * r;
-        float dot = 0.f;
-#pragma unroll 16
-        for (int i = 0; i < D; ++i) dot += sB[i][k] * sdy[q][i];
-        acc[r] -= w * dot;
-      }
+      for (int j = 0; j < 16; ++j) bc[j] = Bcol[(size_t)sl * D * D + j * D];
+      float wq[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) wq[u] = 16 * u + tl < Lq ? bf16f(w0[(size_t)(16 * u + tl) * R::SPM + sl]) : 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) acc[u] = MF::mma(bc[j], wq[u] * sdy[16 * u + tl][16 * kq + j], acc[u]);
     }
-    if (q < Lq) {
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const int k = kl + 8 * r;
-        const size_t o = (tb + q) * D + k;
-        const float mg = g.map_mode == MAP_ELEMENTWISE ? poly_map_grad(bf16f(a.q[o]), g.map_deg) : 1.f;
-        a.dq[o] = from_f32<bf16>(bf16f(a.dq[o]) + acc[r] * mg);
+    for (int u = 0; u < 2; ++u) acc[u] = MF::mma(0.f, 0.f, acc[u]);   // as in k_buf_y: after the loop's exit
+    // lane: features 16 w + 4 kq + r of token 16 u + tl
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int q = 16 * u + tl;
+      if (q < Lq) {
+        const size_t o = (tb + q) * D + 16 * w + 4 * kq;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float mg = g.map_mode == MAP_ELEMENTWISE ? poly_map_grad(bf16f(a.q[o + r]), g.map_deg) : 1.f;
+          a.dq[o + r] = from_f32<bf16>(bf16f(a.dq[o + r]) - acc[u][r] * mg);
+        }
       }
     }
     return;   // workgroup-uniform
   }
-  // slot s: B_s, the weights w(q, s)
+  // slot s: B_s, psi of the chunk's tokens, the weights w(q, s)
   stage_slot(sB, Bb + (size_t)s * D * D);
+  stage_rows(sps, a.q + tb * D, Lq, CH, g.map_mode, g.map_deg);
   if (tid < CH) sw[tid] = tid < Lq ? bf16f(w0[(size_t)tid * R::SPM + s]) : 0.f;
   __syncthreads();
-  // d buffer_in[s] and <dS_e, B_s>, <dZ_e, B_s>; thread: row i, columns kb .. kb + 15
-  {
-    const int i = tid >> 2, kb = (tid & 3) * 16;
+  {   // d buffer_in[s] tiles (rows 16 w .., columns 16 j ..): A[i][q] = w(q, s) dy_q[i], Bt[k][q] = psi_q[k]
     const float* dSe = p.buf_adj + (size_t)bh * bufw::kAdjFloats;
     const float* dZe = dSe + D * D;
     const float ws = rec[R::WSEND + s], wz = rec[R::WZEND + s];
-    float acc[16];
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) acc[kk] = 0.f;
-    for (int q = 0; q < CH; ++q) {
-      const float x = sw[q] * sdy[q][i];
-#pragma unroll
-      for (int kk = 0; kk < 16; ++kk) acc[kk] += x * sps[q][kb + kk];
-    }
     float hs = 0.f, hz = 0.f;
-    float* dst = a.dbuf_in + (((size_t)bh * H + s) * D + i) * D + kb;
 #pragma unroll
-    for (int k4 = 0; k4 < 4; ++k4) {
-      const float4 es = *reinterpret_cast<const float4*>(dSe + i * D + kb + 4 * k4);
-      const float4 ez = *reinterpret_cast<const float4*>(dZe + i * D + kb + 4 * k4);
-      const float vs[4] = {es.x, es.y, es.z, es.w}, vz[4] = {ez.x, ez.y, ez.z, ez.w};
-      float o[4];
+    for (int j = 0; j < 4; ++j) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int jq = 0; jq < CH / 4; ++jq) {   // token q = 8 kq + jq at step jq
+        const int q = (CH / 4) * kq + jq;
+        acc = MF::mma(sw[q] * sdy[q][16 * w + tl], sps[q][16 * j + tl], acc);
+      }
+      // lane: rows i = 16 w + 4 kq + r, column k = 16 j + tl
+      const int k = 16 * j + tl;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float b = sB[i][kb + 4 * k4 + r];
-        hs += vs[r] * b;
-        hz += vz[r] * b;
-        o[r] = wz * vz[r] - ws * vs[r] - acc[4 * k4 + r];
+        const int i = 16 * w + 4 * kq + r;
+        const float es = dSe[i * D + k], ez = dZe[i * D + k], b = sB[i][k];
+        hs += es * b;
+        hz += ez * b;
+        a.dbuf_in[(((size_t)bh * H + s) * D + i) * D + k] = wz * ez - ws * es - acc[r];
       }
-      *reinterpret_cast<float4*>(dst + 4 * k4) = make_float4(o[0], o[1], o[2], o[3]);
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
       hs += __shfl_xor(hs, off, 64);
       hz += __shfl_xor(hz, off, 64);
     }
-    if (lane == 0) { sred[0][wv] = hs; sred[1][wv] = hz; }
+    if (lane == 0) { sred[0][w] = hs; sred[1][w] = hz; }
   }
-  // Lm[q][s] += dy_q^T B_s psi_q; thread: token q, rows il + 8 r
-  {
-    const int q = tid >> 3, il = tid & 7;
-    float v = 0.f;
+  {   // Lm[q][s] += sum_i dy_q[i] V[i][q], V = B_s psi^T: wave w rows 32 (w >> 1) .. +31, tokens 16 (w & 1) ..
+    const int q = 16 * (w & 1) + tl;
+    float lm = 0.f;
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const int i = il + 8 * r;
-      float dot = 0.f;
-#pragma unroll 16
-      for (int k = 0; k < D; ++k) dot += sB[i][k] * sps[q][k];
-      v += sdy[q][i] * dot;
+    for (int h = 0; h < 2; ++h) {
+      const int m0 = 32 * (w >> 1) + 16 * h;
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc = MF::mma(sB[m0 + tl][16 * kq + j], sps[q][16 * kq + j], acc);
+      // lane: rows m0 + 4 kq + r of token q
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lm += sdy[q][m0 + 4 * kq + r] * acc[r];
     }
-    v += __shfl_xor(v, 1, 64);
-    v += __shfl_xor(v, 2, 64);
-    v += __shfl_xor(v, 4, 64);
-    if (il == 0 && q < Lq) blk[SB::LM + q * SB::SPM + s] += v;
+    lm += __shfl_xor(lm, 16, 64);
+    lm += __shfl_xor(lm, 32, 64);
+    if (kq == 0) slm[w >> 1][q] = lm;
   }
   __syncthreads();
-  if (tid == 0) {
+  if (tid < CH) {
+    if (tid < Lq) blk[SB::LM + tid * SB::SPM + s] += slm[0][tid] + slm[1][tid];
+  } else if (tid == CH) {
     float hs = 0.f, hz = 0.f;
 #pragma unroll
-    for (int w = 0; w < kBwThreads / 64; ++w) { hs += sred[0][w]; hz += sred[1][w]; }
+    for (int ww = 0; ww < kBwThreads / 64; ++ww) { hs += sred[0][ww]; hz += sred[1][ww]; }
     blk[SB::HS + s] += hs;
     blk[SB::HZ + s] += hz;
   }
@@ -252,15 +314,28 @@ __global__ __launch_bounds__(kBwThreads) void k_buf_bwd(const Geom g, const BwdP
 
 }  // namespace
 
-hipError_t launch_buf_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, const float* coef, const bf16* wsh,
-                          float* corr, hipStream_t stream) {
+hipError_t launch_buf_state(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, const float* coef, float* corr,
+                            hipStream_t stream) {
   const int G0 = sg.nseg > 1 ? std::min(sg.G, g.nc) : 0;
-  hipLaunchKernelGGL(k_buf_fwd, dim3(bufw::CHF / 16, g.BH), dim3(kBwThreads), 0, stream, g, a, coef, wsh, corr, G0);
+  prof_name(KID_BUF_FWD, "k_buf_state+k_buf_y");
+  prof_begin(KID_BUF_FWD, stream);
+  hipLaunchKernelGGL(k_buf_state, dim3(D * D / kBwThreads, g.BH), dim3(kBwThreads), 0, stream, g, a, coef, corr, G0);
+  prof_end(KID_BUF_FWD, stream);
+  return hipGetLastError();
+}
+
+hipError_t launch_buf_y(const Geom& g, const FwdPtrs<bf16>& a, const bf16* wsh, hipStream_t stream) {
+  prof_begin(KID_BUF_FWD, stream);
+  hipLaunchKernelGGL(k_buf_y, dim3(bufw::CHF / 16, g.BH), dim3(kBwThreads), 0, stream, g, a, wsh);
+  prof_end(KID_BUF_FWD, stream);
   return hipGetLastError();
 }
 
 hipError_t launch_buf_bwd(const Geom& g, const BwdPtrs<bf16>& a, const BwdSegPtrs& p, hipStream_t stream) {
+  prof_name(KID_BUF_BWD, "k_buf_bwd");
+  prof_begin(KID_BUF_BWD, stream);
   hipLaunchKernelGGL(k_buf_bwd, dim3(g.e, g.BH), dim3(kBwThreads), 0, stream, g, a, p);
+  prof_end(KID_BUF_BWD, stream);
   return hipGetLastError();
 }
 

@@ -76,7 +76,8 @@ struct BwdPtrs {
 // Opt-in per-kernel timing (atlas_mem_profile_*): brackets each launch with HIP events.
 enum KernelId {
   KID_FWD_SEG_AGG = 0, KID_FWD_WALK, KID_BUFFER_OUT, KID_BWD_ADJOINT, KID_BWD_CHUNK, KID_BWD_FIXUP,
-  KID_REDUCE_DSREF, KID_FWD_SCAN, KID_BWD_SCAN, KID_FWD_COEF, KID_BWD_COEF, KID_BWD_SCALAR, KID_COUNT
+  KID_REDUCE_DSREF, KID_FWD_SCAN, KID_BWD_SCAN, KID_FWD_COEF, KID_BWD_COEF, KID_BWD_SCALAR, KID_BUF_FWD,
+  KID_BUF_BWD, KID_COUNT
 };
 void prof_name(int kid, const char* name);   // records the kernel a stage launches (timing labels)
 void prof_begin(int kid, hipStream_t s);

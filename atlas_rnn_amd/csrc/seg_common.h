@@ -44,12 +44,11 @@ struct BwdSegPtrs {
 
 // The carried buffer on the specialised walks (bufwalk.hip, d = 64). Per row, its first-chunk terms:
 // the state corrections after the forward chunk's last token (end) and after token Lmid - 1 (mid),
-// the same end terms carried to the end of segment 0 (added to its aggregate by the segment scan),
-// and the y corrections of the first forward chunk's targets.
+// and the same end terms carried to the end of segment 0 (added to its aggregate by the segment scan).
 namespace bufw {
 constexpr int D = 64, CHF = 64, CHB = 32;
-constexpr int SE = 0, ZE = D * D, SM = 2 * D * D, ZM = 3 * D * D, AU = 4 * D * D, AV = 5 * D * D, Y = 6 * D * D;
-constexpr int kCorrFloats = 6 * D * D + CHF * D;
+constexpr int SE = 0, ZE = D * D, SM = 2 * D * D, ZM = 3 * D * D, AU = 4 * D * D, AV = 5 * D * D;
+constexpr int kCorrFloats = 6 * D * D;
 constexpr int kAdjFloats = 2 * D * D;
 }
 

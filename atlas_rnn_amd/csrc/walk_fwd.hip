@@ -12,8 +12,8 @@
 //    through LDS;
 //  * rows are read through per-row buffer resources: the halo before the first token and the
 //    rows past T read as zeros, and y rows past T are dropped by the range check;
-//  * a carried buffer (BUF): its sources are chunk 0's halo; their terms (bufwalk.hip) are added to
-//    chunk 0's y and to the states after it.
+//  * a carried buffer (BUF): its sources are chunk 0's halo; their state terms (bufwalk.hip) are
+//    added to the states after chunk 0 (its y terms are added after the walk).
 // Sources of a chunk are the e - 1 halo tokens followed by the chunk's 64 tokens, s = 0 .. 79
 // (window e <= 17); source s is token t0 - (e - 1) + s.
 //
@@ -338,16 +338,9 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
         }
         const int tau = 16 * tt + m;
         const float ac = rec[R_ACOEF + tau], kc = rec[R_KCOEF + tau];
-        float yv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) yv[r] = -aq[r] + ac * as[r] - kc * az[r];
-        if (BUF && bufc) {   // the carried buffer's sources (chunk 0 only)
-          const float4 yc = *reinterpret_cast<const float4*>(bufc + bufw::Y + tau * D + i0);
-          yv[0] += yc.x; yv[1] += yc.y; yv[2] += yc.z; yv[3] += yc.w;
-        }
         u32x2v out;
-        out[0] = pack_bf16x2(yv[0], yv[1]);
-        out[1] = pack_bf16x2(yv[2], yv[3]);
+        out[0] = pack_bf16x2(-aq[0] + ac * as[0] - kc * az[0], -aq[1] + ac * as[1] - kc * az[1]);
+        out[1] = pack_bf16x2(-aq[2] + ac * as[2] - kc * az[2], -aq[3] + ac * as[3] - kc * az[3]);
         bst8(ry, (uint32_t)(((t0 + tau) * D + i0) * 2), out);
       }
     }

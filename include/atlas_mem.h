@@ -317,7 +317,7 @@ int atlas_heads_bwd(int dtype, int batch, int seq_len, int heads, int d, int n_g
 /* ---- diagnostics (no reference counterpart) ------------------------------------------------ */
 
 /* Number of kernels the timing hooks distinguish (index -> atlas_mem_kernel_name). */
-#define ATLAS_MEM_NKERNELS 12
+#define ATLAS_MEM_NKERNELS 14
 
 /* Opt-in timing: while enabled, each kernel launch of atlas_mem_fwd/atlas_mem_bwd is bracketed
  * by HIP events on its stream (adds two event records per launch). */
