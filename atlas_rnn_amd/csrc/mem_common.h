@@ -28,6 +28,15 @@ constexpr int kWave = 64;
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 
+// Workgroup barrier that orders LDS only: waits for this wave's LDS operations (lgkmcnt) but not for
+// its global loads, so loads issued ahead (register prefetch) stay in flight across it. For use where
+// no other thread reads, after the barrier, global memory this thread wrote before it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
