@@ -4,8 +4,9 @@
 
 `affine_associative_scan(A, B, *, prev=None, remove_prev=False)` returns [N, T, R, D] (or
 [N, T+1, R, D] starting with prev when prev is given and remove_prev is False), with gradients
-for A, B and prev. The scan runs in fp32 in libatlas_mem.so (atlas_affine_scan_fwd / _bwd,
-one workgroup per n, D, R <= 64); other dtypes are computed in fp32 and cast back.
+for A, B and prev. The scan runs in fp32 in libatlas_mem.so (atlas_affine_scan_fwd / _bwd:
+chunked compose / chain / apply passes on the fp32 matrix cores, D, R <= 64); other dtypes are
+computed in fp32 and cast back.
 """
 
 from __future__ import annotations

@@ -424,9 +424,11 @@ int run_bwd_plan(const atlas_mem_problem* prob, const Plan& pl, const atlas_mem_
   const int* flag = reinterpret_cast<const int*>(sv);
   set_flag(fast, flag, 0, 0, 0);
   set_flag(exact, flag, 1, 0, 0);
-  const int st = one(fast, reinterpret_cast<const float*>(sv + D.fast));
+  // either order: the flag is only read here; the exact sequence first, so that the per-kernel
+  // timing labels name the segment-parallel kernels that normally run
+  const int st = one(exact, reinterpret_cast<const float*>(sv + D.exact));
   if (st != ATLAS_MEM_OK) return st;
-  return one(exact, reinterpret_cast<const float*>(sv + D.exact));
+  return one(fast, reinterpret_cast<const float*>(sv + D.fast));
 }
 
 // Scratch of atlas_mem_bwd_noalloc: the backward workspace as a file-scope device array (each GPU

@@ -774,11 +774,13 @@ def bench_plan(name, steps, warmup, cpu=True, cpu_sample_t=256, with_buffer=Fals
     step_bytes = fwd_b + bwd_b
     kernels = {kk: {"avg_us": 1e3 * ms / max(n, 1), "launches": n} for kk, (ms, n) in prof.items() if n}
     dom = max(kernels, key=lambda kk: kernels[kk]["avg_us"] * kernels[kk]["launches"])
-    dom_s = kernels[dom]["avg_us"] * 1e-6
+    # the stage's time per step: under scan_chunk_len clamps both flag-selected sequences are
+    # launched every step and the unselected one returns at once, so launches != steps there
+    dom_s = kernels[dom]["avg_us"] * kernels[dom]["launches"] / steps * 1e-6
     achieved = per_kernel[dom] / dom_s / 1e9
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": measured_traffic(dom, name),
-                "algorithmic_bytes_per_launch": per_kernel[dom], "avg_launch_us": round(kernels[dom]["avg_us"], 2)}
+                "algorithmic_bytes_per_launch": per_kernel[dom], "avg_launch_us": round(dom_s * 1e6, 2)}
     step_gbs = step_bytes / (elapsed / steps) / 1e9
     flops = flops_per_step(bh, t, d)
     tflops = flops / (elapsed / steps) / 1e12
