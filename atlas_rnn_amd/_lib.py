@@ -51,6 +51,8 @@ EXPORTED_SYMBOLS = (
     "atlas_affine_scan_workspace_bytes",
     "atlas_tensor_map_fwd",
     "atlas_tensor_map_bwd",
+    "atlas_tensor_map_symmetrize",
+    "atlas_tensor_map_fwd_sym",
     "atlas_block_split",
     "atlas_block_merge",
     "atlas_block_parts",
@@ -150,6 +152,10 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_tensor_map_fwd.argtypes = [i32, i64, i32, i32, i32, vp, vp, vp, vp, vp]
     lib.atlas_tensor_map_bwd.restype = i32
     lib.atlas_tensor_map_bwd.argtypes = [i32, i64, i32, i32, i32, vp, vp, vp, vp, vp, vp]
+    lib.atlas_tensor_map_symmetrize.restype = i32
+    lib.atlas_tensor_map_symmetrize.argtypes = [i32, i32, i32, vp, vp, vp, vp]
+    lib.atlas_tensor_map_fwd_sym.restype = i32
+    lib.atlas_tensor_map_fwd_sym.argtypes = [i32, i64, i32, i32, i32, vp, vp, vp, vp, vp]
     lib.atlas_block_split.restype = i32
     lib.atlas_block_split.argtypes = [i32] * 5 + [vp] * 8
     lib.atlas_block_merge.restype = i32

@@ -23,6 +23,8 @@
 // as it loads dphi.
 //
 // Token tiles of 128 rows; rows past N load zeros and their stores are dropped (buffer range checks).
+#include <type_traits>
+
 #include "mem_common.h"
 #include "walk_common.h"
 
@@ -49,7 +51,9 @@ struct TmapFwdSmem {
 
 // Four waves per SIMD (at most 128 VGPRs): the few bytes of spill this costs at D = 64, M = 128 are
 // cheaper than the third wave's missing latency cover (measured).
-template <int D, int M>
+// SYM: pt is a symmetrised table (atlas_tensor_map_symmetrize: P[a][b] + P[b][a] on b > a, zero on
+// b < a), so the blocks of rows a >= D / 2 skip their products over the zero columns b < D / 2.
+template <int D, int M, bool SYM>
 __global__ __launch_bounds__(tmap_fwd_threads<M>()) __attribute__((amdgpu_waves_per_eu(4)))
 void k_tmap_fwd(long n_tok, const bf16* __restrict__ x, const bf16* __restrict__ pt, bf16* __restrict__ out,
                 int deg, bf16* __restrict__ pre) {
@@ -111,15 +115,16 @@ void k_tmap_fwd(long n_tok, const bf16* __restrict__ x, const bf16* __restrict__
     for (int nt = 0; nt < 2; ++nt) acc[jt][nt] = zero4();
 
   // block kb from LDS buffer kb & 1; register stage `pf` holds block kb + 1 and is refilled with
-  // block kb + 3 after its store
-  auto block = [&](int kb, u32x4v (&pf)[PVT]) {
+  // block kb + 3 after its store; the products start at column tile S0 (compile time)
+  auto block = [&](int kb, u32x4v (&pf)[PVT], auto s0c) {
+    constexpr int S0 = decltype(s0c)::value;
     const int buf = kb & 1;
     float xa[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)   // x_a of the block's row a = kb - 1 (unused in block 0)
       xa[nt] = static_cast<float>(sm.xs[32 * rg + 16 * nt + i][kb > 0 ? kb - 1 : 0]);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
+    for (int s = S0; s < NS; ++s) {
       bf16x8 fb[2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
@@ -143,9 +148,24 @@ void k_tmap_fwd(long n_tok, const bf16* __restrict__ x, const bf16* __restrict__
     }
     __syncthreads();
   };
-  for (int kb = 0; kb <= D; kb += 2) {
-    block(kb, pf0);
-    if (kb + 1 <= D) block(kb + 1, pf1);
+  // blocks 0 .. KS - 1 over every column tile, then (SYM) the blocks of rows a >= D / 2 from tile
+  // NS / 2 on; even blocks take register stage pf0, odd ones pf1
+  using all_t = std::integral_constant<int, 0>;
+  using hi_t = std::integral_constant<int, NS / 2>;
+  constexpr int KS = (SYM && NS > 1) ? D / 2 + 1 : D + 1;
+  static_assert(KS % 2 == 1 && D % 2 == 0, "block parity");
+  for (int kb = 0; kb + 1 < KS; kb += 2) {
+    block(kb, pf0, all_t{});
+    block(kb + 1, pf1, all_t{});
+  }
+  block(KS - 1, pf0, all_t{});
+  if constexpr (KS <= D) {
+    block(KS, pf1, hi_t{});
+    for (int kb = KS + 1; kb + 1 <= D; kb += 2) {
+      block(kb, pf0, hi_t{});
+      block(kb + 1, pf1, hi_t{});
+    }
+    block(D, pf0, hi_t{});
   }
 
   // phi^T tiles: lane (g, i) holds phi[token 32 rg + 16 nt + i][feature FG cg + 16 jt + 4 g + r]
@@ -351,11 +371,33 @@ __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, cons
     }
 }
 
-template <int D, int M>
+template <int D, int M, bool SYM = false>
 hipError_t launch_tmap_fwd(long n, const bf16* x, const bf16* pt, bf16* out, int deg, bf16* pre, hipStream_t s) {
   const unsigned grid = (unsigned)((n + tm::TN - 1) / tm::TN);
-  hipLaunchKernelGGL((k_tmap_fwd<D, M>), dim3(grid), dim3(tmap_fwd_threads<M>()), 0, s, n, x, pt, out, deg, pre);
+  hipLaunchKernelGGL((k_tmap_fwd<D, M, SYM>), dim3(grid), dim3(tmap_fwd_threads<M>()), 0, s, n, x, pt, out, deg, pre);
   return hipGetLastError();
+}
+
+// The symmetrised projection (both layouts): x x^T is symmetric, so its projection keeps only
+// a <= b: ps[D + a D + b] = P[D + a D + b] + P[D + b D + a] (b > a), P[D + a D + a] (b = a), 0 (b < a);
+// the linear rows are copied. ps [K][M] (the backward's layout) and pst [M][K] (the forward's).
+template <typename T>
+__global__ __launch_bounds__(256) void k_tmap_symmetrize(int D, int M, const T* __restrict__ p, T* __restrict__ ps,
+                                                         T* __restrict__ pst) {
+  const int K = D + D * D;
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)K * M) return;
+  const int r = (int)(idx / M), j = (int)(idx % M);
+  float v;
+  if (r < D) {
+    v = static_cast<float>(p[idx]);
+  } else {
+    const int a = (r - D) / D, b = (r - D) % D;
+    v = b < a ? 0.f : static_cast<float>(p[idx]);
+    if (b > a) v += static_cast<float>(p[(long)(D + b * D + a) * M + j]);
+  }
+  ps[idx] = static_cast<T>(v);
+  pst[(long)j * K + r] = static_cast<T>(v);
 }
 
 template <int D, int M>
@@ -621,6 +663,14 @@ hipError_t tmap_fwd(int d, int m, long n, const bf16* x, const bf16* pt, bf16* o
   if (d == 32 && m == 32) return launch_tmap_fwd<32, 32>(n, x, pt, out, deg, pre, s);
   return hipErrorInvalidValue;
 }
+// The same with a symmetrised table: the d_in = 64 kernels skip its zero lower triangle.
+hipError_t tmap_fwd_sym(int d, int m, long n, const bf16* x, const bf16* pt, bf16* out, int deg, bf16* pre,
+                        hipStream_t s) {
+  if (d == 64 && m == 128) return launch_tmap_fwd<64, 128, true>(n, x, pt, out, deg, pre, s);
+  if (d == 64 && m == 64) return launch_tmap_fwd<64, 64, true>(n, x, pt, out, deg, pre, s);
+  if (d == 64 && m == 32) return launch_tmap_fwd<64, 32, true>(n, x, pt, out, deg, pre, s);
+  return tmap_fwd(d, m, n, x, pt, out, deg, pre, s);
+}
 hipError_t tmap_bwd(int d, int m, long n, const bf16* x, const bf16* p, const bf16* dout, bf16* dx, int deg,
                     const bf16* pre, hipStream_t s) {
   if (!tmap_fast(d, m)) return tmap_gen_bwd<bf16>(d, m, n, x, p, dout, dx, deg, pre, s);
@@ -669,6 +719,40 @@ int atlas_tensor_map_fwd(int dtype, int64_t n, int d_in, int d_out, int degree, 
                                          static_cast<const atlas::bf16*>(proj_t), static_cast<atlas::bf16*>(out),
                                          degree, degree > 1 ? static_cast<atlas::bf16*>(pre) : nullptr,
                                          static_cast<hipStream_t>(stream));
+  return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
+}
+
+int atlas_tensor_map_symmetrize(int dtype, int d_in, int d_out, const void* proj, void* proj_sym, void* proj_sym_t,
+                                void* stream) {
+  if (dtype != ATLAS_DT_BF16 && dtype != ATLAS_DT_F32) return ATLAS_MEM_ERR_DTYPE;
+  if (!tmap_dims_ok(0, d_in, d_out)) return ATLAS_MEM_ERR_SHAPE;
+  if (!proj || !proj_sym || !proj_sym_t) return ATLAS_MEM_ERR_NULL;
+  if (tmap_misaligned(proj) || tmap_misaligned(proj_sym) || tmap_misaligned(proj_sym_t)) return ATLAS_MEM_ERR_ALIGN;
+  const long total = (long)(d_in + d_in * d_in) * d_out;
+  const unsigned grid = (unsigned)((total + 255) / 256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == ATLAS_DT_F32)
+    hipLaunchKernelGGL(atlas::k_tmap_symmetrize<float>, dim3(grid), dim3(256), 0, s, d_in, d_out,
+                       static_cast<const float*>(proj), static_cast<float*>(proj_sym), static_cast<float*>(proj_sym_t));
+  else
+    hipLaunchKernelGGL(atlas::k_tmap_symmetrize<atlas::bf16>, dim3(grid), dim3(256), 0, s, d_in, d_out,
+                       static_cast<const atlas::bf16*>(proj), static_cast<atlas::bf16*>(proj_sym),
+                       static_cast<atlas::bf16*>(proj_sym_t));
+  return hipGetLastError() == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
+}
+
+int atlas_tensor_map_fwd_sym(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x,
+                             const void* proj_sym_t, void* out, void* pre, void* stream) {
+  if (dtype != ATLAS_DT_BF16) return atlas_tensor_map_fwd(dtype, n, d_in, d_out, degree, x, proj_sym_t, out, pre, stream);
+  if (!tmap_dims_ok(n, d_in, d_out) || degree < 1 || degree > 16) return ATLAS_MEM_ERR_SHAPE;
+  if (!x || !proj_sym_t || !out || (degree > 1 && !pre)) return ATLAS_MEM_ERR_NULL;
+  if (tmap_misaligned(x) || tmap_misaligned(proj_sym_t) || tmap_misaligned(out) || tmap_misaligned(pre))
+    return ATLAS_MEM_ERR_ALIGN;
+  if (n == 0) return ATLAS_MEM_OK;
+  const hipError_t err = atlas::tmap_fwd_sym(d_in, d_out, (long)n, static_cast<const atlas::bf16*>(x),
+                                             static_cast<const atlas::bf16*>(proj_sym_t), static_cast<atlas::bf16*>(out),
+                                             degree, degree > 1 ? static_cast<atlas::bf16*>(pre) : nullptr,
+                                             static_cast<hipStream_t>(stream));
   return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
 }
 

@@ -248,12 +248,18 @@ class _TensorMapFn(torch.autograd.Function):
         lead, d, m = x.shape[:-1], x.shape[-1], proj.shape[-1]
         x2 = _aligned(x.reshape(-1, d))
         p = _aligned(proj.to(x.dtype))
-        pt = _aligned(p.t())
+        # the symmetrised table in both layouts (one launch in place of a transposition): the forward
+        # skips its zero lower triangle, the backward gives the same dx from it as from P
+        ps = torch.empty_like(p)
+        pst = torch.empty(m, p.shape[0], device=dev, dtype=p.dtype)
+        _lib.check(lib.atlas_tensor_map_symmetrize(_dt_code(p), d, m, _ptr(p), _ptr(ps), _ptr(pst), _stream(dev)),
+                   "atlas_tensor_map_symmetrize")
         n = x2.shape[0]
         out = torch.empty(n, m, device=dev, dtype=x.dtype)
         pre = torch.empty(n, m, device=dev, dtype=x.dtype) if degree > 1 else None
-        _lib.check(lib.atlas_tensor_map_fwd(_dt_code(x2), n, d, m, degree, _ptr(x2), _ptr(pt), _ptr(out), _ptr(pre),
-                                            _stream(dev)), "atlas_tensor_map_fwd")
+        _lib.check(lib.atlas_tensor_map_fwd_sym(_dt_code(x2), n, d, m, degree, _ptr(x2), _ptr(pst), _ptr(out),
+                                                _ptr(pre), _stream(dev)), "atlas_tensor_map_fwd_sym")
+        p = ps
         ctx.save_for_backward(x2, p, pre)
         ctx.lead = lead
         ctx.degree = degree

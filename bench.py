@@ -305,15 +305,18 @@ def run_c4(steps, warmup, cpu=True, cpu_sample_t=128):
     lib = _lib.load()
     n = bh * t
     xk = leaves["k"].detach().reshape(n, kin).contiguous()
-    pt = P.t().contiguous()
+    stream = _stream(dev)
+    ps = torch.empty_like(P)                          # the symmetrised table the step uses
+    pst = torch.empty(dk, P.shape[0], device=dev, dtype=P.dtype)
+    _lib.check(lib.atlas_tensor_map_symmetrize(_lib.DT_BF16, kin, dk, _ptr(P), _ptr(ps), _ptr(pst), stream),
+               "atlas_tensor_map_symmetrize")
     out = torch.empty(n, dk, device=dev, dtype=torch.bfloat16)
     pre = torch.empty_like(out)
     dout = bf(r(n, dk))
     dx = torch.empty_like(xk)
-    stream = _stream(dev)
-    fwd_call = lambda: _lib.check(lib.atlas_tensor_map_fwd(_lib.DT_BF16, n, kin, dk, deg, _ptr(xk), _ptr(pt),
-                                                           _ptr(out), _ptr(pre), stream), "atlas_tensor_map_fwd")
-    bwd_call = lambda: _lib.check(lib.atlas_tensor_map_bwd(_lib.DT_BF16, n, kin, dk, deg, _ptr(xk), _ptr(P),
+    fwd_call = lambda: _lib.check(lib.atlas_tensor_map_fwd_sym(_lib.DT_BF16, n, kin, dk, deg, _ptr(xk), _ptr(pst),
+                                                               _ptr(out), _ptr(pre), stream), "atlas_tensor_map_fwd_sym")
+    bwd_call = lambda: _lib.check(lib.atlas_tensor_map_bwd(_lib.DT_BF16, n, kin, dk, deg, _ptr(xk), _ptr(ps),
                                                            _ptr(pre), _ptr(dout), _ptr(dx), stream),
                                   "atlas_tensor_map_bwd")
     kern = {}

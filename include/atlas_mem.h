@@ -248,6 +248,22 @@ int atlas_tensor_map_fwd(int dtype, int64_t n, int d_in, int d_out, int degree, 
 int atlas_tensor_map_bwd(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x, const void* proj,
                          const void* pre, const void* dout, void* dx, void* stream);
 
+/* The projection of the symmetric x x^T needs only its upper triangle: proj_sym [d_in + d_in^2, d_out]
+ * holds P's linear rows and, for the quadratic rows a*d_in + b, P[a][b] + P[b][a] (b > a), P[a][a]
+ * (b = a), 0 (b < a), so that [x; vec(x x^T)] proj_sym = [x; vec(x x^T)] P; proj_sym_t is its
+ * transpose [d_out, d_in + d_in^2]. Same dtype, sizes and alignment as atlas_tensor_map_fwd.
+ * Internal to this library (no counterpart in the reference: a preparation step of the two calls
+ * below, in place of the forward's transposition of P). */
+int atlas_tensor_map_symmetrize(int dtype, int d_in, int d_out, const void* proj, void* proj_sym, void* proj_sym_t,
+                                void* stream);
+
+/* atlas_tensor_map_fwd on a table from atlas_tensor_map_symmetrize (proj_sym_t in place of proj_t;
+ * any other table gives wrong results): the bf16 d_in = 64 kernels skip the products over its zero
+ * lower triangle (a quarter of the quadratic block's matrix-core work). The backward takes either
+ * table (atlas_tensor_map_bwd with proj_sym gives the same dx). */
+int atlas_tensor_map_fwd_sym(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x,
+                             const void* proj_sym_t, void* out, void* pre, void* stream);
+
 /* ---- state blocks for head sizes above 64 (BASELINE C4: d_k = 128, d_v = 64) ----------------
  * The recurrence with S [d_v, d_k] runs as 64 x 64 blocks S[i, j] stacked along the row axis
  * (r = (i * d_k/64 + j) * bh + b), each with S_ref = 0 and v = -delta[rows of block i], where

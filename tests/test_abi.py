@@ -235,6 +235,18 @@ def test_tensor_map_errors_before_launch(lib):
     assert b(_lib.DT_BF16, 8, 64, 128, 1, good, good, None, bad, good, None) == 5
     assert b(_lib.DT_BF16, 8, 64, 128, 2, good, good, None, good, good, None) == 4  # degree > 1 needs pre
     assert b(_lib.DT_BF16, -1, 64, 128, 1, good, good, None, good, good, None) == 2
+    sy = lib.atlas_tensor_map_symmetrize
+    fs = lib.atlas_tensor_map_fwd_sym
+    assert sy(2, 64, 128, good, good, good, None) == 3
+    assert sy(_lib.DT_BF16, 48, 128, good, good, good, None) == 2
+    assert sy(_lib.DT_BF16, 64, 72, good, good, good, None) == 2
+    assert sy(_lib.DT_BF16, 64, 128, good, None, good, None) == 4
+    assert sy(_lib.DT_F32, 64, 128, good, good, bad, None) == 5
+    assert fs(_lib.DT_BF16, 8, 64, 128, 3, good, good, good, None, None) == 4       # degree > 1 needs pre
+    assert fs(_lib.DT_BF16, 8, 64, 128, 1, good, bad, good, None, None) == 5
+    assert fs(_lib.DT_BF16, 8, 64, 136, 1, good, good, good, None, None) == 2
+    assert fs(_lib.DT_F32, 8, 48, 128, 1, good, good, good, None, None) == 2         # fp32 takes the plain checks
+    assert fs(_lib.DT_BF16, 0, 64, 128, 1, good, good, good, None, None) == 0
 
 
 def test_tensor_feature_map_raises_off_kernel():

@@ -66,6 +66,48 @@ def test_tensor_map_parity(n, d, m, deg, dt):
     compare("dx", dx.float().cpu(), dref, tol)
 
 
+@pytest.mark.parametrize("dt", [BF16, F32], ids=["bf16", "fp32"])
+def test_symmetrized_table_and_both_forwards(dt):
+    """atlas_tensor_map_symmetrize against the table formed on the CPU (P's linear rows, then
+    P[a][b] + P[b][a] above the diagonal, P[a][a] on it, zeros below; bit-exact after rounding the
+    fp32 sum to the dtype) and its transpose; then atlas_tensor_map_fwd on P^T and
+    atlas_tensor_map_fwd_sym on the symmetrised table against the oracle map."""
+    from atlas_rnn_amd import _lib
+    from atlas_rnn_amd.functional import _ptr, _stream
+    d, m, n = 64, 128, 257
+    _say(f"symmetrised tensor-map table {dt}")
+    g = torch.Generator().manual_seed(777)
+    bound = (6.0 / (d + d * d + m)) ** 0.5
+    P = ((torch.rand(d + d * d, m, generator=g) * 2 - 1) * bound).to(dt)
+    Pq = P[d:].float().reshape(d, d, m)
+    ref_q = Pq + Pq.transpose(0, 1)
+    a = torch.arange(d).view(d, 1)
+    b = torch.arange(d).view(1, d)
+    ref_q = torch.where((b > a).unsqueeze(-1), ref_q, torch.where((b == a).unsqueeze(-1), Pq, torch.zeros_like(Pq)))
+    ref = torch.cat([P[:d].float(), ref_q.reshape(d * d, m)]).to(dt)
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    code = _lib.DT_BF16 if dt == BF16 else _lib.DT_F32
+    Pd = P.to(dev)
+    ps = torch.empty_like(Pd)
+    pst = torch.empty(m, d + d * d, device=dev, dtype=dt)
+    _lib.check(lib.atlas_tensor_map_symmetrize(code, d, m, _ptr(Pd), _ptr(ps), _ptr(pst), _stream(dev)), "symmetrize")
+    torch.cuda.synchronize()
+    assert torch.equal(ps.cpu(), ref)
+    assert torch.equal(pst.cpu(), ref.t().contiguous())
+    x = torch.randn(n, d, generator=g)
+    x = (x / x.norm(dim=-1, keepdim=True)).to(dt)
+    oracle = poly_feature_map(x.to(F64), 2, 'tensor', P.to(F64))
+    xd = x.to(dev)
+    pt = Pd.t().contiguous()
+    tol = TOL if dt == BF16 else 1e-4
+    for name, fn, table in (("fwd", lib.atlas_tensor_map_fwd, pt), ("fwd_sym", lib.atlas_tensor_map_fwd_sym, pst)):
+        out = torch.empty(n, m, device=dev, dtype=dt)
+        _lib.check(fn(code, n, d, m, 1, _ptr(xd), _ptr(table), _ptr(out), None, _stream(dev)), name)
+        torch.cuda.synchronize()
+        compare(f"tmap.{name}", out.float().cpu(), oracle, tol)
+
+
 def test_c4_composition_reduced():
     """tensor map -> d_k 128 / d_v 64 recurrence (block path, elementwise map g = 3), fwd + bwd."""
     from atlas_rnn_amd.functional import memory_recurrence, tensor_feature_map
