@@ -61,6 +61,8 @@ EXPORTED_SYMBOLS = (
     "atlas_prologue_bwd",
     "atlas_heads_fwd",
     "atlas_heads_bwd",
+    "atlas_linear_wgrad_workspace_bytes",
+    "atlas_linear_wgrad",
     "atlas_mem_profile_enable",
     "atlas_mem_profile_read",
     "atlas_mem_kernel_name",
@@ -173,6 +175,10 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_heads_fwd.argtypes = [i32] * 6 + [vp] * 12
     lib.atlas_heads_bwd.restype = i32
     lib.atlas_heads_bwd.argtypes = [i32] * 6 + [vp] * 17
+    lib.atlas_linear_wgrad_workspace_bytes.restype = i64
+    lib.atlas_linear_wgrad_workspace_bytes.argtypes = [i64, i32, i32]
+    lib.atlas_linear_wgrad.restype = i32
+    lib.atlas_linear_wgrad.argtypes = [i32, i64, i32, i32, vp, vp, vp, vp, i64, vp]
     lib.atlas_mem_profile_enable.restype = i32
     lib.atlas_mem_profile_enable.argtypes = [i32]
     lib.atlas_mem_profile_read.restype = i32

@@ -921,13 +921,25 @@ class _HeadsFn(torch.autograd.Function):
 
 
 def _wgrad(dy: Tensor, x: Tensor, dtype) -> Tensor:
-    """dW = dy^T x over every leading axis of dy [..., o] and x [..., i], split over the tokens:
-    one batched product of S token slices, summed in fp32. With K = tokens in the thousands and a
-    d x d output, the plain product runs on few output tiles (measured 105 us for 16384 tokens x
-    512 x 512 on MI355X, 66 us split eight ways)."""
+    """dW = dy^T x over every leading axis of dy [..., o] and x [..., i]. bf16 operands go to
+    atlas_linear_wgrad (both read as stored, the token axis split over the matrix cores, fp32
+    partials summed in a fixed order): 16384 tokens x 512 x 512 took 67 us through a transposed copy
+    and a batched hipBLASLt product, whose plain form (one product with K = 16384 on few output
+    tiles) took 100 us. fp32 operands keep torch's product over token slices."""
     o, i = dy.shape[-1], x.shape[-1]
     dy2, x2 = dy.reshape(-1, o), x.reshape(-1, i)
     n = dy2.shape[0]
+    if dy2.dtype == torch.bfloat16 and x2.dtype == torch.bfloat16 and o % 8 == 0 and i % 8 == 0 \
+            and dtype in (torch.bfloat16, torch.float32):
+        lib = _lib.load()
+        dy2, x2 = _aligned(dy2), _aligned(x2)
+        dev = dy2.device
+        ws_bytes = lib.atlas_linear_wgrad_workspace_bytes(n, o, i)
+        ws = torch.empty(max(ws_bytes, 16) // 4, device=dev, dtype=torch.float32)
+        dw = torch.empty(o, i, device=dev, dtype=dtype)
+        _lib.check(lib.atlas_linear_wgrad(_DTYPES[dtype], n, o, i, _ptr(dy2), _ptr(x2), _ptr(dw), _ptr(ws), ws_bytes,
+                                          _stream(dev)), "atlas_linear_wgrad")
+        return dw
     S = next((c for c in (8, 4, 2) if n % c == 0 and n // c >= 1024), 1)
     if S == 1:
         return (dy2.t() @ x2).to(dtype)

@@ -330,6 +330,18 @@ int atlas_heads_bwd(int dtype, int batch, int seq_len, int heads, int d, int n_g
                     const void* dv, const void* dgates, void* dql, void* dkl, void* dvl, void* dzl,
                     float* dq_gamma_part, float* dk_gamma_part, float* dbias_part, void* stream);
 
+/* Weight gradient of a bias-free linear layer y = x W^T over n tokens: dW [out_features][in_features]
+ * = sum_t dy[t]^T x[t], from dy [n][out_features] and x [n][in_features] as stored (bf16, row-major,
+ * 16-byte aligned). Replaces the weight gradient autograd forms for the cell's projections
+ * (nn.Linear / LinearNoBias to_q, to_k, to_v, to_out and the gate heads, rnn_memory.py:486-489,
+ * :503-520). Feature counts multiples of 8; fp32 accumulation; dW in out_dtype (ATLAS_DT_BF16 or
+ * ATLAS_DT_F32). The token axis is split over workgroups whose fp32 partial tiles go to workspace
+ * (at least atlas_linear_wgrad_workspace_bytes) and are summed in a fixed order (deterministic).
+ * n = 0 writes zeros (dy, x and workspace may then be NULL). */
+int64_t atlas_linear_wgrad_workspace_bytes(int64_t n, int out_features, int in_features);
+int atlas_linear_wgrad(int out_dtype, int64_t n, int out_features, int in_features, const void* dy, const void* x,
+                       void* dw, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---- diagnostics (no reference counterpart) ------------------------------------------------ */
 
 /* Number of kernels the timing hooks distinguish (index -> atlas_mem_kernel_name). */

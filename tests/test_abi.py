@@ -249,6 +249,23 @@ def test_tensor_map_errors_before_launch(lib):
     assert fs(_lib.DT_BF16, 0, 64, 128, 1, good, good, good, None, None) == 0
 
 
+def test_linear_wgrad_errors_before_launch(lib):
+    good, bad = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x10008)
+    ws = lib.atlas_linear_wgrad_workspace_bytes
+    g = lib.atlas_linear_wgrad
+    assert ws(16384, 512, 512) == 16 * 16 * 128 * 128 * 4          # 16 token splits x 16 tiles of 128 x 128
+    assert ws(1000, 32, 512) == 4 * 4 * 128 * 128 * 4              # 256-token splits on 4 tiles
+    assert ws(0, 512, 512) == 0
+    assert ws(100, 12, 512) == -1 and ws(-1, 64, 64) == -1           # features % 8 == 0; n >= 0
+    need = ws(1000, 32, 512)
+    assert g(2, 1000, 32, 512, good, good, good, good, need, None) == 3          # dW bf16 or fp32
+    assert g(_lib.DT_BF16, 1000, 36, 512, good, good, good, good, need, None) == 2
+    assert g(_lib.DT_BF16, 1000, 32, 512, None, good, good, good, need, None) == 4
+    assert g(_lib.DT_BF16, 1000, 32, 512, good, good, good, None, need, None) == 4   # n > 0 needs workspace
+    assert g(_lib.DT_BF16, 1000, 32, 512, good, bad, good, good, need, None) == 5
+    assert g(_lib.DT_F32, 1000, 32, 512, good, good, good, good, need - 4, None) == 7
+
+
 def test_tensor_feature_map_raises_off_kernel():
     """The map has one implementation, the kernels: CPU tensors and operands they do not take raise
     before anything is launched (no tensor-op formulation to fall back to)."""
