@@ -21,6 +21,7 @@
 
 #include "../../include/atlas_mem.h"
 #include "mem_common.h"
+#include "walk_common.h"
 
 namespace atlas {
 
@@ -287,6 +288,215 @@ __global__ __launch_bounds__(pro::kThreads) void k_pro_bwd(int Tn, int dim, cons
   }
 }
 
+// The same adjoint in one pass over the tokens, for dim <= 512 and conv_k <= 4 (the cell's shapes):
+// a workgroup of two waves per 16-token block, lane l of wave w owning channels c = 4 (64 w + l) ..
+// c + 3. The conv's transpose is scattered as each row u of dq_in / dk_in / dv_in arrives: it adds
+// taps[j] * dconv[u] to g of token u + j - pad, so that g of token u - pad is complete after row u;
+// that token is then finished at once (the RMSNorm adjoint's dot product summed over the lanes and
+// the two waves, dx, the norm-weight partial), and row u also feeds the tap partials with the x rows
+// u - pad .. u - pad + K - 1 held in a register window. Every input row is read once per block
+// (plus the K - 1 halo rows), with the loads of step u + 2 in flight during step u; rows outside
+// [0, T) read as zeros through the buffer range check (the convs' zero padding). Same partial layout
+// as k_pro_bwd (one row per 16-token block).
+namespace pw {
+constexpr int kWaves = 2, kThreads = 64 * kWaves, kCh = 4;   // channels per lane
+constexpr int kMaxDim = kThreads * kCh;                      // 512
+}
+
+// Four consecutive elements through a buffer resource, as fp32. The fp32 form converts the whole
+// 16-byte vector at once: hipcc 7.2 narrows a raw buffer load whose vector elements are bit-cast to
+// float one by one to a single dword (the other three elements then hold stale registers).
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+template <typename T>
+__device__ __forceinline__ float4 ld4_rs(rsrc_t r, uint32_t off) {
+  if constexpr (sizeof(T) == 2) {
+    const u32x2v u = bld8(r, off);
+    return make_float4(__builtin_bit_cast(float, u[0] << 16), __builtin_bit_cast(float, u[0] & 0xffff0000u),
+                       __builtin_bit_cast(float, u[1] << 16), __builtin_bit_cast(float, u[1] & 0xffff0000u));
+  } else {
+    const f32x4v v = __builtin_bit_cast(f32x4v, bld16(r, off));
+    return make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void st4_rs(rsrc_t r, uint32_t off, const float (&v)[4]) {
+  if constexpr (sizeof(T) == 2) {
+    u32x2v u;
+    u[0] = pack_bf16x2(v[0], v[1]);
+    u[1] = pack_bf16x2(v[2], v[3]);
+    bst8(r, off, u);
+  } else {
+    const f32x4v f = {v[0], v[1], v[2], v[3]};
+    bst16(r, off, __builtin_bit_cast(u32x4v, f));
+  }
+}
+
+template <typename T, int KT>
+__global__ __launch_bounds__(pw::kThreads) void k_pro_bwd_win(int Tn, int dim, const T* __restrict__ x,
+                                                              const T* __restrict__ wn, const T* __restrict__ wq,
+                                                              const T* __restrict__ wk, const T* __restrict__ wv,
+                                                              const float* __restrict__ inv_rms,
+                                                              const T* __restrict__ dxn, const T* __restrict__ dqi,
+                                                              const T* __restrict__ dki, const T* __restrict__ dvi,
+                                                              T* __restrict__ dx, float* __restrict__ dwn_part,
+                                                              float* __restrict__ dwc_part) {
+  constexpr int pad = KT / 2, KA = KT > 0 ? KT : 1, E = (int)sizeof(T);
+  __shared__ float sdot[2][pw::kWaves];   // per-wave partial dot products, by step parity
+  const int lane = lane_id(), w = wave_id();
+  const int b = blockIdx.y, blk = blockIdx.x, ntb = gridDim.x;
+  const int t0 = blk * pro::kTok, t1 = min(Tn, t0 + pro::kTok);
+  const int c = pw::kCh * (64 * w + lane);
+  const bool on = c < dim;
+  const size_t ob = (size_t)b * Tn * dim, prow = (size_t)b * ntb + blk;
+  const uint32_t nbytes = (uint32_t)((size_t)Tn * dim * E);
+  const float* inv = inv_rms + (size_t)b * Tn;
+  const rsrc_t rx = make_rsrc(x + ob, nbytes), rdxn = make_rsrc(dxn + ob, nbytes), rdx = make_rsrc(dx + ob, nbytes);
+  const rsrc_t rq = make_rsrc(KT ? dqi + ob : x, KT ? nbytes : 0u), rk = make_rsrc(KT ? dki + ob : x, KT ? nbytes : 0u),
+               rv = make_rsrc(KT ? dvi + ob : x, KT ? nbytes : 0u);
+  // byte offset of this lane's channels in row r (rows < 0 wrap past the range and read zeros)
+  auto roff = [&](int r) { return on ? (uint32_t)((r * dim + c) * E) : kOob; };
+  auto inv_at = [&](int r) { return (r >= 0 && r < Tn) ? inv[r] : 0.f; };
+
+  float wn4[4] = {0.f, 0.f, 0.f, 0.f}, tap[3][KA][4];
+  if (on) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wn4[e] = to_f32(wn[c + e]);
+  }
+#pragma unroll
+  for (int h = 0; h < 3; ++h)
+#pragma unroll
+    for (int j = 0; j < KA; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const T* tw = h == 0 ? wq : (h == 1 ? wk : wv);
+        tap[h][j][e] = (KT > 0 && on) ? to_f32(tw[(size_t)(c + e) * KT + j]) : 0.f;
+      }
+  float gt[3][KA][4], dw4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int h = 0; h < 3; ++h)
+#pragma unroll
+    for (int j = 0; j < KA; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) gt[h][j][e] = 0.f;
+  // windows: gw[m] = g of token u - pad + m (scatter targets), xw[m] / iw[m] = x row u - pad + m
+  float gw[KA][4], xw[KA][4], iw[KA];
+#pragma unroll
+  for (int m = 0; m < KA; ++m) {
+    iw[m] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) gw[m][e] = xw[m][e] = 0.f;
+  }
+  // steps u in [ub, ue]: conv rows (KT > 0) or tokens (KT = 0)
+  const int ub = KT ? t0 + pad - KT + 1 : t0, ue = KT ? t1 - 1 + pad : t1 - 1;
+  if constexpr (KT > 0) {   // x rows ub - pad .. ub - pad + KT - 2 (the last window row comes with step ub)
+#pragma unroll
+    for (int m = 0; m + 1 < KT; ++m) {
+      const float4 v = ld4_rs<T>(rx, roff(ub - pad + m));
+      xw[m][0] = v.x; xw[m][1] = v.y; xw[m][2] = v.z; xw[m][3] = v.w;
+      iw[m] = inv_at(ub - pad + m);
+    }
+  }
+  // inputs of one step: conv rows u, x row u - pad + K - 1 (its inverse RMS), dxn of token u - pad
+  struct Stage {
+    float4 q, k, v, x, d;
+    float i;
+  };
+  auto sload = [&](Stage& st, int u) {
+    const int xr = u - pad + KA - 1, tk = u - pad;
+    if constexpr (KT > 0) {
+      st.q = ld4_rs<T>(rq, roff(u));
+      st.k = ld4_rs<T>(rk, roff(u));
+      st.v = ld4_rs<T>(rv, roff(u));
+    }
+    st.x = ld4_rs<T>(rx, roff(xr));
+    st.i = inv_at(xr);
+    st.d = ld4_rs<T>(rdxn, roff(tk));
+  };
+  auto step = [&](int u, Stage& st) {
+    const int tk = u - pad;
+    {   // newest window row
+      xw[KA - 1][0] = st.x.x; xw[KA - 1][1] = st.x.y; xw[KA - 1][2] = st.x.z; xw[KA - 1][3] = st.x.w;
+      iw[KA - 1] = st.i;
+    }
+    if constexpr (KT > 0) {
+      const float dq[4] = {st.q.x, st.q.y, st.q.z, st.q.w}, dk[4] = {st.k.x, st.k.y, st.k.z, st.k.w},
+                  dv[4] = {st.v.x, st.v.y, st.v.z, st.v.w};
+#pragma unroll
+      for (int j = 0; j < KT; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gw[j][e] += tap[0][j][e] * dq[e] + tap[1][j][e] * dk[e] + tap[2][j][e] * dv[e];
+      if (u >= t0 && u < t1) {   // tap partials of output row u: xn rows u - pad + j
+#pragma unroll
+        for (int j = 0; j < KT; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float xn = xw[j][e] * iw[j] * wn4[e];
+            gt[0][j][e] += dq[e] * xn;
+            gt[1][j][e] += dk[e] * xn;
+            gt[2][j][e] += dv[e] * xn;
+          }
+      }
+    }
+    if (tk >= t0 && tk < t1) {   // token tk is complete: finish it (uniform over the workgroup)
+      const float dd[4] = {st.d.x, st.d.y, st.d.z, st.d.w};
+      float g[4], pd = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        g[e] = gw[0][e] + dd[e];
+        pd += wn4[e] * g[e] * xw[0][e];
+      }
+      pd = wave_sum(pd);
+      const int par = tk & 1;
+      if (lane == 0) sdot[par][w] = pd;
+      __syncthreads();
+      float dot = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < pw::kWaves; ++ww) dot += sdot[par][ww];
+      const float it = iw[0], c3 = it * it * it * dot / (float)dim;
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        dw4[e] += g[e] * xw[0][e] * it;
+        o[e] = it * wn4[e] * g[e] - xw[0][e] * c3;
+      }
+      if (on) st4_rs<T>(rdx, roff(tk), o);
+    }
+    // shift the windows by one token
+#pragma unroll
+    for (int m = 0; m + 1 < KA; ++m) {
+      iw[m] = iw[m + 1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        gw[m][e] = gw[m + 1][e];
+        xw[m][e] = xw[m + 1][e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) gw[KA - 1][e] = 0.f;
+    sload(st, u + 2);   // past ue: rows of the next block or past T (zeros), never used
+  };
+  Stage sa, sb;
+  sload(sa, ub);
+  sload(sb, ub + 1);
+  for (int u = ub; u <= ue; u += 2) {
+    step(u, sa);
+    if (u + 1 <= ue) step(u + 1, sb);
+  }
+  if (on) {
+    *reinterpret_cast<float4*>(dwn_part + prow * dim + c) = make_float4(dw4[0], dw4[1], dw4[2], dw4[3]);
+    if constexpr (KT > 0) {   // [3][dim][K]: this lane's 4 K consecutive values per conv
+#pragma unroll
+      for (int h = 0; h < 3; ++h) {
+        float* dst = dwc_part + ((prow * 3 + h) * dim + c) * KT;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int j = 0; j < KT; ++j) dst[e * KT + j] = gt[h][j][e];
+      }
+    }
+  }
+}
+
 // Threads per head row: d / 8 rounded up to a power of two (the extra threads hold zeros), so that
 // a row's sums are xor shuffles within an aligned lane group.
 __host__ __device__ __forceinline__ int heads_row_threads(int d) {
@@ -508,9 +718,20 @@ int atlas_prologue_bwd(int dtype, int batch, int seq_len, int dim, int conv_k, c
   const dim3 grid((seq_len + pro::kTok - 1) / pro::kTok, batch), block(pro::kThreads);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int K = conv ? conv_k : 0;
+  const size_t esize = dtype == ATLAS_DT_BF16 ? 2 : 4;
+  // one pass over the tokens where the per-lane windows fit (dim <= 512, conv_k <= 4)
+  const bool win = dim <= pw::kMaxDim && K <= 4 && (size_t)seq_len * dim * esize < ((size_t)1 << 31);
   auto go = [&](auto tag, auto kt) {
     using T = decltype(tag);
     constexpr int KT = decltype(kt)::value;
+    if constexpr (KT <= 4) {
+      if (win) {
+        hipLaunchKernelGGL((k_pro_bwd_win<T, KT>), grid, dim3(pw::kThreads), 0, s, seq_len, dim, (const T*)x,
+                           (const T*)norm_w, (const T*)wq, (const T*)wk, (const T*)wv, inv_rms, (const T*)dxn,
+                           (const T*)dq_in, (const T*)dk_in, (const T*)dv_in, (T*)dx, dnorm_w_part, dconv_part);
+        return;
+      }
+    }
     hipLaunchKernelGGL((k_pro_bwd<T, KT>), grid, block, 0, s, seq_len, dim, (const T*)x, (const T*)norm_w,
                        (const T*)wq, (const T*)wk, (const T*)wv, inv_rms, (const T*)dxn, (const T*)dq_in,
                        (const T*)dk_in, (const T*)dv_in, (T*)dx, dnorm_w_part, dconv_part);

@@ -56,6 +56,11 @@ CASES = [
     # head sizes whose rows do not fill a power-of-two thread group (padded lanes)
     ("fp32_d48_k4", 2, 37, 96, 2, 48, 4, 3, True, torch.float32),
     ("bf16_d24_k2_nonorm", 1, 20, 48, 2, 24, 2, 2, False, torch.bfloat16),
+    # the one-pass backward covers dim <= 512 and conv_k <= 4; these take the three-pass kernel
+    ("fp32_dim640_k6", 1, 40, 640, 5, 128, 6, 2, True, torch.float32),
+    ("bf16_k8", 2, 30, 64, 2, 32, 8, 2, True, torch.bfloat16),
+    # fewer tokens than one 16-token block, every token inside the conv halo
+    ("bf16_t5_k4", 2, 5, 128, 2, 64, 4, 4, True, torch.bfloat16),
 ]
 
 
