@@ -53,6 +53,7 @@ EXPORTED_SYMBOLS = (
     "atlas_tensor_map_bwd",
     "atlas_tensor_map_symmetrize",
     "atlas_tensor_map_fwd_sym",
+    "atlas_tensor_map_bwd_sym",
     "atlas_block_split",
     "atlas_block_merge",
     "atlas_block_parts",
@@ -158,6 +159,8 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_tensor_map_symmetrize.argtypes = [i32, i32, i32, vp, vp, vp, vp]
     lib.atlas_tensor_map_fwd_sym.restype = i32
     lib.atlas_tensor_map_fwd_sym.argtypes = [i32, i64, i32, i32, i32, vp, vp, vp, vp, vp]
+    lib.atlas_tensor_map_bwd_sym.restype = i32
+    lib.atlas_tensor_map_bwd_sym.argtypes = [i32, i64, i32, i32, i32, vp, vp, vp, vp, vp, vp]
     lib.atlas_block_split.restype = i32
     lib.atlas_block_split.argtypes = [i32] * 5 + [vp] * 8
     lib.atlas_block_merge.restype = i32

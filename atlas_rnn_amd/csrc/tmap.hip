@@ -206,7 +206,12 @@ struct TmapBwdSmem {
   float t1[D / 32][tm::TN][D + 1];        // sum over b of G[n, a, b] x[n, b], per feature half of b
 };
 
-template <int D, int M>
+// SYM: proj is the symmetrised table (zero where b < a), so the blocks of rows a >= D / 2 only have
+// products over b >= D / 2: there the two feature-half waves of a token group split its two token
+// tiles instead of the feature halves (half the matrix-core work), the third term of a wave whose
+// b half is the lower one is handed over through t1[0][n][b >= D / 2], which no block writes
+// otherwise, and the second term lands whole in t1[1][n][a].
+template <int D, int M, bool SYM = false>
 __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, const bf16* __restrict__ x,
                                                                    const bf16* __restrict__ proj,
                                                                    const bf16* __restrict__ dout,
@@ -343,11 +348,93 @@ __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, cons
     __syncthreads();
   };
   f32x4 gA[2][2], gB[2][2];
-  for (int kb = 0; kb <= D; kb += 2) {
-    step(kb, pf0, gA, gB);
-    if (kb + 1 <= D) step(kb + 1, pf1, gB, gA);
+  if constexpr (!SYM || D != 64) {
+    for (int kb = 0; kb <= D; kb += 2) {
+      step(kb, pf0, gA, gB);
+      if (kb + 1 <= D) step(kb + 1, pf1, gB, gA);
+    }
+    epi(D, gA);   // D is even: the last block's tiles are in gA
+  } else {
+    // blocks 0 .. D / 2 (the linear rows and a < D / 2) as above
+    for (int kb = 0; kb < D / 2; kb += 2) {
+      step(kb, pf0, gA, gB);
+      step(kb + 1, pf1, gB, gA);
+    }
+    step(D / 2, pf0, gA, gB);
+    // blocks a + 1 with a >= D / 2: tiles b = D / 2 + 16 bt, tokens 32 rg + 16 cb (token tile nt = cb)
+    bf16x8 fdh[NK];
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) fdh[ks] = cb ? fd[1][ks] : fd[0][ks];
+    const int nh = 32 * rg + 16 * cb + i;
+    float xh[2][4];
+    f32x4 accH[2];
+#pragma unroll
+    for (int bt = 0; bt < 2; ++bt) {
+      accH[bt] = zero4();
+#pragma unroll
+      for (int r = 0; r < 4; ++r) xh[bt][r] = static_cast<float>(sm.xs[nh][D / 2 + 16 * bt + 4 * g + r]);
+    }
+    auto mma_h = [&](int kb, f32x4 (&gt)[2]) {
+      const int buf = kb & 1;
+#pragma unroll
+      for (int bt = 0; bt < 2; ++bt) gt[bt] = zero4();
+#pragma unroll
+      for (int ks = 0; ks < NK; ++ks) {
+#pragma unroll
+        for (int bt = 0; bt < 2; ++bt)
+          gt[bt] = mma_bf16(frag_row(&sm.pb[buf][0][0], M + 8, D / 2 + 16 * bt, 32 * ks), fdh[ks], gt[bt]);
+      }
+    };
+    auto epi_h = [&](int kb, const f32x4 (&gt)[2]) {
+      const int a = kb - 1;
+      const float xa = static_cast<float>(sm.xs[nh][a]);
+      float part = 0.f;
+#pragma unroll
+      for (int bt = 0; bt < 2; ++bt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          accH[bt][r] += gt[bt][r] * xa;
+          part += gt[bt][r] * xh[bt][r];
+        }
+      part = xsum_rows(part);
+      if (g == 0) sm.t1[1][nh][a] = part;
+    };
+    auto step_h = [&](int kb, u32x4v (&pf)[PVT], f32x4 (&gcur)[2], const f32x4 (&gprev)[2]) {
+      mma_h(kb, gcur);
+      epi_h(kb - 1, gprev);
+      if (kb < D) {
+        p_store(pf, (kb & 1) ^ 1);
+        p_load(pf, kb + 3);
+      }
+      __syncthreads();
+    };
+    f32x4 hA[2], hB[2];
+    mma_h(D / 2 + 1, hA);   // block D / 2 + 1, with the epilogue of block D / 2 (full tiles)
+    epi(D / 2, gA);
+    p_store(pf1, ((D / 2 + 1) & 1) ^ 1);
+    p_load(pf1, D / 2 + 4);
+    __syncthreads();
+    for (int kb = D / 2 + 2; kb <= D; kb += 2) {
+      step_h(kb, pf0, hB, hA);
+      if (kb + 1 <= D) step_h(kb + 1, pf1, hA, hB);
+    }
+    epi_h(D, hB);   // D is even: the last block's tiles are in hB
+    // the third term of the upper feature half: a wave of the upper half keeps its own token tile's,
+    // a wave of the lower half hands its tile's over (t1[0][n][c >= D / 2] holds only this)
+#pragma unroll
+    for (int bt = 0; bt < 2; ++bt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int cc = D / 2 + 16 * bt + 4 * g + r;
+        if (cb) {
+          acc[bt][1][r] += accH[bt][r];
+          sm.t1[0][nh][cc] = 0.f;
+        } else {
+          sm.t1[0][nh][cc] = accH[bt][r];
+        }
+      }
   }
-  epi(D, gA);   // D is even: the last block's tiles are in gA
+  __syncthreads();   // t1 written by the other feature half's waves
 
   // dx[n, c] = acc (c = 32 cb + 16 bt + 4 g + r) + sum over the halves of t1[., n, c]
   const rsrc_t ro = make_rsrc(dx + n0 * D, (uint32_t)(nrow * D * 2));
@@ -400,15 +487,16 @@ __global__ __launch_bounds__(256) void k_tmap_symmetrize(int D, int M, const T* 
   pst[(long)j * K + r] = static_cast<T>(v);
 }
 
-template <int D, int M>
+template <int D, int M, bool SYM = false>
 hipError_t launch_tmap_bwd(long n, const bf16* x, const bf16* p, const bf16* dout, bf16* dx, int deg, const bf16* pre,
                            hipStream_t s) {
   const size_t smem = sizeof(TmapBwdSmem<D, M>);
-  hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_tmap_bwd<D, M>),
+  hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_tmap_bwd<D, M, SYM>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (err != hipSuccess) return err;
   const unsigned grid = (unsigned)((n + tm::TN - 1) / tm::TN);
-  hipLaunchKernelGGL((k_tmap_bwd<D, M>), dim3(grid), dim3(64 * 4 * (D / 32)), smem, s, n, x, p, dout, dx, deg, pre);
+  hipLaunchKernelGGL((k_tmap_bwd<D, M, SYM>), dim3(grid), dim3(64 * 4 * (D / 32)), smem, s, n, x, p, dout, dx, deg,
+                     pre);
   return hipGetLastError();
 }
 
@@ -682,6 +770,14 @@ hipError_t tmap_bwd(int d, int m, long n, const bf16* x, const bf16* p, const bf
   if (d == 32 && m == 32) return launch_tmap_bwd<32, 32>(n, x, p, dout, dx, deg, pre, s);
   return hipErrorInvalidValue;
 }
+// The same with a symmetrised table: the d_in = 64 kernels skip its zero lower triangle.
+hipError_t tmap_bwd_sym(int d, int m, long n, const bf16* x, const bf16* ps, const bf16* dout, bf16* dx, int deg,
+                        const bf16* pre, hipStream_t s) {
+  if (d == 64 && m == 128) return launch_tmap_bwd<64, 128, true>(n, x, ps, dout, dx, deg, pre, s);
+  if (d == 64 && m == 64) return launch_tmap_bwd<64, 64, true>(n, x, ps, dout, dx, deg, pre, s);
+  if (d == 64 && m == 32) return launch_tmap_bwd<64, 32, true>(n, x, ps, dout, dx, deg, pre, s);
+  return tmap_bwd(d, m, n, x, ps, dout, dx, deg, pre, s);
+}
 
 }  // namespace atlas
 
@@ -778,6 +874,24 @@ int atlas_tensor_map_bwd(int dtype, int64_t n, int d_in, int d_out, int degree, 
                                          static_cast<atlas::bf16*>(dx), degree,
                                          degree > 1 ? static_cast<const atlas::bf16*>(pre) : nullptr,
                                          static_cast<hipStream_t>(stream));
+  return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
+}
+
+int atlas_tensor_map_bwd_sym(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x,
+                             const void* proj_sym, const void* pre, const void* dout, void* dx, void* stream) {
+  if (dtype != ATLAS_DT_BF16)
+    return atlas_tensor_map_bwd(dtype, n, d_in, d_out, degree, x, proj_sym, pre, dout, dx, stream);
+  if (!tmap_dims_ok(n, d_in, d_out) || degree < 1 || degree > 16) return ATLAS_MEM_ERR_SHAPE;
+  if (!x || !proj_sym || !dout || !dx || (degree > 1 && !pre)) return ATLAS_MEM_ERR_NULL;
+  if (tmap_misaligned(x) || tmap_misaligned(proj_sym) || tmap_misaligned(dout) || tmap_misaligned(dx) ||
+      tmap_misaligned(pre))
+    return ATLAS_MEM_ERR_ALIGN;
+  if (n == 0) return ATLAS_MEM_OK;
+  const hipError_t err = atlas::tmap_bwd_sym(d_in, d_out, (long)n, static_cast<const atlas::bf16*>(x),
+                                             static_cast<const atlas::bf16*>(proj_sym),
+                                             static_cast<const atlas::bf16*>(dout), static_cast<atlas::bf16*>(dx),
+                                             degree, degree > 1 ? static_cast<const atlas::bf16*>(pre) : nullptr,
+                                             static_cast<hipStream_t>(stream));
   return err == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
 }
 

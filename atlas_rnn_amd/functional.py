@@ -249,7 +249,7 @@ class _TensorMapFn(torch.autograd.Function):
         x2 = _aligned(x.reshape(-1, d))
         p = _aligned(proj.to(x.dtype))
         # the symmetrised table in both layouts (one launch in place of a transposition): the forward
-        # skips its zero lower triangle, the backward gives the same dx from it as from P
+        # and the backward skip the products over its zero lower triangle
         ps = torch.empty_like(p)
         pst = torch.empty(m, p.shape[0], device=dev, dtype=p.dtype)
         _lib.check(lib.atlas_tensor_map_symmetrize(_dt_code(p), d, m, _ptr(p), _ptr(ps), _ptr(pst), _stream(dev)),
@@ -274,8 +274,8 @@ class _TensorMapFn(torch.autograd.Function):
         m = p.shape[-1]
         g = _aligned(dout.reshape(-1, m).to(x2.dtype))
         dx = torch.empty_like(x2)
-        _lib.check(lib.atlas_tensor_map_bwd(_dt_code(x2), n, d, m, ctx.degree, _ptr(x2), _ptr(p), _ptr(pre), _ptr(g),
-                                            _ptr(dx), _stream(dev)), "atlas_tensor_map_bwd")
+        _lib.check(lib.atlas_tensor_map_bwd_sym(_dt_code(x2), n, d, m, ctx.degree, _ptr(x2), _ptr(p), _ptr(pre),
+                                                _ptr(g), _ptr(dx), _stream(dev)), "atlas_tensor_map_bwd_sym")
         return dx.reshape(*ctx.lead, d), None, None
 
 

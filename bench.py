@@ -316,9 +316,9 @@ def run_c4(steps, warmup, cpu=True, cpu_sample_t=128):
     dx = torch.empty_like(xk)
     fwd_call = lambda: _lib.check(lib.atlas_tensor_map_fwd_sym(_lib.DT_BF16, n, kin, dk, deg, _ptr(xk), _ptr(pst),
                                                                _ptr(out), _ptr(pre), stream), "atlas_tensor_map_fwd_sym")
-    bwd_call = lambda: _lib.check(lib.atlas_tensor_map_bwd(_lib.DT_BF16, n, kin, dk, deg, _ptr(xk), _ptr(ps),
-                                                           _ptr(pre), _ptr(dout), _ptr(dx), stream),
-                                  "atlas_tensor_map_bwd")
+    bwd_call = lambda: _lib.check(lib.atlas_tensor_map_bwd_sym(_lib.DT_BF16, n, kin, dk, deg, _ptr(xk), _ptr(ps),
+                                                               _ptr(pre), _ptr(dout), _ptr(dx), stream),
+                                  "atlas_tensor_map_bwd_sym")
     kern = {}
     for name, call in (("k_tmap_fwd", fwd_call), ("k_tmap_bwd", bwd_call)):
         for _ in range(3):

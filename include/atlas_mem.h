@@ -264,6 +264,13 @@ int atlas_tensor_map_symmetrize(int dtype, int d_in, int d_out, const void* proj
 int atlas_tensor_map_fwd_sym(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x,
                              const void* proj_sym_t, void* out, void* pre, void* stream);
 
+/* atlas_tensor_map_bwd on the symmetrised table proj_sym [d_in + d_in^2][d_out] (internal, no
+ * reference counterpart; requires the table of atlas_tensor_map_symmetrize, any other table gives
+ * wrong results): the bf16 d_in = 64 kernel halves the matrix-core work of the blocks of rows
+ * a >= d_in / 2. Same arguments and results as atlas_tensor_map_bwd given proj_sym. */
+int atlas_tensor_map_bwd_sym(int dtype, int64_t n, int d_in, int d_out, int degree, const void* x,
+                             const void* proj_sym, const void* pre, const void* dout, void* dx, void* stream);
+
 /* ---- state blocks for head sizes above 64 (BASELINE C4: d_k = 128, d_v = 64) ----------------
  * The recurrence with S [d_v, d_k] runs as 64 x 64 blocks S[i, j] stacked along the row axis
  * (r = (i * d_k/64 + j) * bh + b), each with S_ref = 0 and v = -delta[rows of block i], where

@@ -247,6 +247,13 @@ def test_tensor_map_errors_before_launch(lib):
     assert fs(_lib.DT_BF16, 8, 64, 136, 1, good, good, good, None, None) == 2
     assert fs(_lib.DT_F32, 8, 48, 128, 1, good, good, good, None, None) == 2         # fp32 takes the plain checks
     assert fs(_lib.DT_BF16, 0, 64, 128, 1, good, good, good, None, None) == 0
+    bs = lib.atlas_tensor_map_bwd_sym
+    assert bs(_lib.DT_BF16, 8, 64, 128, 1, good, good, None, good, None, None) == 4
+    assert bs(_lib.DT_BF16, 8, 64, 128, 1, good, good, None, bad, good, None) == 5
+    assert bs(_lib.DT_BF16, 8, 64, 128, 2, good, good, None, good, good, None) == 4   # degree > 1 needs pre
+    assert bs(_lib.DT_BF16, 8, 64, 136, 1, good, good, None, good, good, None) == 2
+    assert bs(_lib.DT_F32, 8, 48, 128, 1, good, good, None, good, good, None) == 2     # fp32 takes the plain checks
+    assert bs(_lib.DT_BF16, 0, 64, 128, 1, good, good, None, good, good, None) == 0
 
 
 def test_linear_wgrad_errors_before_launch(lib):

@@ -71,7 +71,9 @@ def test_symmetrized_table_and_both_forwards(dt):
     """atlas_tensor_map_symmetrize against the table formed on the CPU (P's linear rows, then
     P[a][b] + P[b][a] above the diagonal, P[a][a] on it, zeros below; bit-exact after rounding the
     fp32 sum to the dtype) and its transpose; then atlas_tensor_map_fwd on P^T and
-    atlas_tensor_map_fwd_sym on the symmetrised table against the oracle map."""
+    atlas_tensor_map_fwd_sym on the symmetrised table against the oracle map, and the gradient of x
+    from atlas_tensor_map_bwd on P and atlas_tensor_map_bwd_sym on the symmetrised table against the
+    oracle's (fp64 autograd)."""
     from atlas_rnn_amd import _lib
     from atlas_rnn_amd.functional import _ptr, _stream
     d, m, n = 64, 128, 257
@@ -106,6 +108,16 @@ def test_symmetrized_table_and_both_forwards(dt):
         _lib.check(fn(code, n, d, m, 1, _ptr(xd), _ptr(table), _ptr(out), None, _stream(dev)), name)
         torch.cuda.synchronize()
         compare(f"tmap.{name}", out.float().cpu(), oracle, tol)
+    # backward: atlas_tensor_map_bwd on P and atlas_tensor_map_bwd_sym on the symmetrised table
+    dout = torch.randn(n, m, generator=g).to(dt)
+    xo = x.to(F64).requires_grad_()
+    (poly_feature_map(xo, 2, 'tensor', P.to(F64)) * dout.to(F64)).sum().backward()
+    dd = dout.to(dev)
+    for name, fn, table in (("bwd", lib.atlas_tensor_map_bwd, Pd), ("bwd_sym", lib.atlas_tensor_map_bwd_sym, ps)):
+        dx = torch.empty(n, d, device=dev, dtype=dt)
+        _lib.check(fn(code, n, d, m, 1, _ptr(xd), _ptr(table), None, _ptr(dd), _ptr(dx), _stream(dev)), name)
+        torch.cuda.synchronize()
+        compare(f"tmap.{name}", dx.float().cpu(), xo.grad, tol)
 
 
 def test_c4_composition_reduced():
