@@ -62,6 +62,7 @@ EXPORTED_SYMBOLS = (
     "atlas_prologue_bwd",
     "atlas_heads_fwd",
     "atlas_heads_bwd",
+    "atlas_linear_batch",
     "atlas_linear_wgrad_workspace_bytes",
     "atlas_linear_wgrad",
     "atlas_mem_profile_enable",
@@ -178,6 +179,9 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_heads_fwd.argtypes = [i32] * 6 + [vp] * 12
     lib.atlas_heads_bwd.restype = i32
     lib.atlas_heads_bwd.argtypes = [i32] * 6 + [vp] * 17
+    lib.atlas_linear_batch.restype = i32
+    lib.atlas_linear_batch.argtypes = [i32, i32, i64, ctypes.POINTER(i32), ctypes.POINTER(i32),
+                                       ctypes.POINTER(vp), ctypes.POINTER(vp), ctypes.POINTER(vp), vp]
     lib.atlas_linear_wgrad_workspace_bytes.restype = i64
     lib.atlas_linear_wgrad_workspace_bytes.argtypes = [i64, i32, i32]
     lib.atlas_linear_wgrad.restype = i32

@@ -947,18 +947,48 @@ def _wgrad(dy: Tensor, x: Tensor, dtype) -> Tensor:
     return torch.bmm(a, x2.view(S, n // S, i).contiguous()).float().sum(0).to(dtype)
 
 
+_GEMM_NT, _GEMM_NN = 0, 1
+
+
+def _products(layout: int, acts, weights):
+    """atlas_linear_batch: up to four bf16 products in one launch. NT: acts[i] [..., k] x
+    weights[i] [n, k] -> [..., n] (y = x W^T); NN: acts[i] [..., k] x weights[i] [k, n] -> [..., n]
+    (dx = dy W). Falls back to torch for other dtypes or sizes that are not multiples of 8."""
+    ok = all(a.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and a.shape[-1] % 8 == 0
+             and w.shape[0] % 8 == 0 and w.shape[1] % 8 == 0 for a, w in zip(acts, weights))
+    m = acts[0].numel() // acts[0].shape[-1]
+    if not ok or any(a.numel() // a.shape[-1] != m for a in acts):
+        if layout == _GEMM_NT:
+            return [torch.nn.functional.linear(a, w) for a, w in zip(acts, weights)]
+        return [a @ w for a, w in zip(acts, weights)]
+    lib = _lib.load()
+    dev = acts[0].device
+    a2 = [_aligned(a.reshape(m, a.shape[-1])) for a in acts]
+    w2 = [_aligned(w) for w in weights]
+    ns = [w.shape[0] if layout == _GEMM_NT else w.shape[1] for w in w2]
+    ks = [a.shape[-1] for a in a2]
+    outs = [torch.empty(m, nn, device=dev, dtype=torch.bfloat16) for nn in ns]
+    cnt = len(a2)
+    I32 = ctypes.c_int * cnt
+    VP = ctypes.c_void_p * cnt
+    _lib.check(lib.atlas_linear_batch(layout, cnt, m, I32(*ns), I32(*ks), VP(*[a.data_ptr() for a in a2]),
+                                      VP(*[w.data_ptr() for w in w2]), VP(*[o.data_ptr() for o in outs]),
+                                      _stream(dev)), "atlas_linear_batch")
+    return [o.reshape(*a.shape[:-1], nn) for o, a, nn in zip(outs, acts, ns)]
+
+
 class _LinearFn(torch.autograd.Function):
-    """y = x W^T (hipBLASLt) with the token-split weight gradient of _wgrad."""
+    """y = x W^T with its input gradient on atlas_linear_batch and the weight gradient of _wgrad."""
 
     @staticmethod
     def forward(ctx, x, w):
         ctx.save_for_backward(x, w)
-        return torch.nn.functional.linear(x, w)
+        return _products(_GEMM_NT, [x], [w])[0]
 
     @staticmethod
     def backward(ctx, dy):
         x, w = ctx.saved_tensors
-        dx = dy @ w if ctx.needs_input_grad[0] else None
+        dx = _products(_GEMM_NN, [dy], [w])[0] if ctx.needs_input_grad[0] else None
         dw = _wgrad(dy, x, w.dtype) if ctx.needs_input_grad[1] else None
         return dx, dw
 
@@ -981,13 +1011,13 @@ class _HandCtx:
 
 class _CellPrologueFn(torch.autograd.Function):
     """The whole prologue as ONE autograd node: the RMSNorm / conv kernel, the four projections
-    (hipBLASLt), the head-split kernel, and in the backward their adjoints in reverse order with the
-    token-split weight gradients. One node instead of seven keeps the host's per-step work (the
-    prologue is host-bound at C5's layer shape: ~1.1 ms of issue time against less GPU time)."""
+    (one atlas_linear_batch launch), the head-split kernel, and in the backward their adjoints in
+    reverse order (the four input gradients in one launch) with the weight gradients of _wgrad.
+    One node and batched products keep the host's per-step work down (the prologue is bound by
+    host issue at C5's layer shape, not by its kernels)."""
 
     @staticmethod
     def forward(ctx, x, norm_w, wq, wk, wv, Wq, Wk, Wv, Wg, bg, qg, kg, conv_k, eps, heads, d):
-        F = torch.nn.functional
         cp, ch = _HandCtx(), _HandCtx()
         conv = conv_k > 1
         if conv:
@@ -995,8 +1025,10 @@ class _CellPrologueFn(torch.autograd.Function):
         else:
             xn = _PrologueFn.forward(cp, x, norm_w, None, None, None, 0, eps)
             qi = ki = vi = xn
-        ql, kl, vl = F.linear(qi, Wq), F.linear(ki, Wk), F.linear(vi, Wv)
-        zl = F.linear(xn, Wg) if Wg is not None else None
+        if Wg is not None:
+            ql, kl, vl, zl = _products(_GEMM_NT, [qi, ki, vi, xn], [Wq, Wk, Wv, Wg])
+        else:
+            (ql, kl, vl), zl = _products(_GEMM_NT, [qi, ki, vi], [Wq, Wk, Wv]), None
         outs = _HeadsFn.forward(ch, ql, kl, vl, zl, qg, kg, bg, heads, d)
         e0 = torch.empty(0, device=x.device)
         ctx.save_for_backward(qi, ki, vi, xn, Wq, Wk, Wv, Wg if Wg is not None else e0)
@@ -1007,13 +1039,15 @@ class _CellPrologueFn(torch.autograd.Function):
     def backward(ctx, dxn, dq, dk, dv, *dgates):
         qi, ki, vi, xn, Wq, Wk, Wv, Wg = ctx.saved_tensors
         dql, dkl, dvl, dzl, dqg, dkg, db, _, _ = _HeadsFn.backward(ctx.ch, dq, dk, dv, *dgates)
-        dqi, dki, dvi = dql @ Wq, dkl @ Wk, dvl @ Wv
+        if ctx.has_g:
+            dqi, dki, dvi, dxg = _products(_GEMM_NN, [dql, dkl, dvl, dzl], [Wq, Wk, Wv, Wg])
+        else:
+            dqi, dki, dvi = _products(_GEMM_NN, [dql, dkl, dvl], [Wq, Wk, Wv])
         dWq, dWk, dWv = _wgrad(dql, qi, Wq.dtype), _wgrad(dkl, ki, Wk.dtype), _wgrad(dvl, vi, Wv.dtype)
         dWg = None
         dsum = dxn
         if ctx.has_g:
             dWg = _wgrad(dzl, xn, Wg.dtype)
-            dxg = dzl @ Wg
             dsum = dxg if dsum is None else dsum + dxg
         if ctx.conv:
             dx, dnorm, dtq, dtk, dtv, _, _ = _PrologueFn.backward(ctx.cp, dsum, dqi, dki, dvi)

@@ -337,6 +337,18 @@ int atlas_heads_bwd(int dtype, int batch, int seq_len, int heads, int d, int n_g
                     const void* dv, const void* dgates, void* dql, void* dkl, void* dvl, void* dzl,
                     float* dq_gamma_part, float* dk_gamma_part, float* dbias_part, void* stream);
 
+/* The linear layers' products in bf16 (fp32 accumulation), up to four independent problems per
+ * launch sharing m: for problem z, with A [m][k[z]] row-major,
+ *   ATLAS_GEMM_NT:  C [m][n[z]] = A B^T, B [n[z]][k[z]]   (y = x W^T, the layer's forward)
+ *   ATLAS_GEMM_NN:  C [m][n[z]] = A B,   B [k[z]][n[z]]   (dx = dy W, its input gradient)
+ * Replaces the products autograd forms for the cell's LinearNoBias to_q / to_k / to_v / to_out and
+ * its gate heads (rnn_memory.py:486-489, :503-520); the prologue's four projections and their four
+ * input gradients are one launch each. n, k multiples of 8; every pointer 16-byte aligned; a, b, c
+ * are host arrays of count device pointers. */
+enum atlas_gemm_layout { ATLAS_GEMM_NT = 0, ATLAS_GEMM_NN = 1 };
+int atlas_linear_batch(int b_layout, int count, int64_t m, const int* n, const int* k, const void* const* a,
+                       const void* const* b, void* const* c, void* stream);
+
 /* Weight gradient of a bias-free linear layer y = x W^T over n tokens: dW [out_features][in_features]
  * = sum_t dy[t]^T x[t], from dy [n][out_features] and x [n][in_features] as stored (bf16, row-major,
  * 16-byte aligned). Replaces the weight gradient autograd forms for the cell's projections

@@ -303,3 +303,19 @@ def test_cpu_tensors_are_rejected():
     s = torch.zeros(1, 4)
     with pytest.raises(RuntimeError, match="GPU"):
         memory_recurrence(x, x, x, s, s)
+
+
+def test_linear_batch_errors_before_launch(lib):
+    good, bad = 0x10000, 0x10008
+    I32, VP = ctypes.c_int * 2, ctypes.c_void_p * 2
+    f = lib.atlas_linear_batch
+    ok = dict(n=I32(64, 32), k=I32(64, 64), a=VP(good, good), b=VP(good, good), c=VP(good, good))
+    call = lambda layout=0, count=2, m=100, **kw: f(layout, count, m, *[kw.get(x, ok[x]) for x in ("n", "k", "a", "b", "c")],
+                                                    None)
+    assert call(layout=2) == 9                                   # NT or NN
+    assert call(count=0) == 2 and call(count=5) == 2              # one to four problems
+    assert call(n=I32(64, 36)) == 2 and call(k=I32(4, 64)) == 2   # multiples of 8
+    assert call(m=-1) == 2
+    assert call(a=VP(good, None)) == 4
+    assert call(c=VP(good, bad)) == 5
+    assert call(m=0, a=VP(None, None), c=VP(None, None)) == 0    # m = 0: nothing launched
