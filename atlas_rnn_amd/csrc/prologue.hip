@@ -497,6 +497,54 @@ __global__ __launch_bounds__(pw::kThreads) void k_pro_bwd_win(int Tn, int dim, c
   }
 }
 
+// Sums of per-workgroup partials over their rows (the parameter gradients of the prologue and head
+// kernels), several arrays in one launch: problem z is parts[z] [rows][cols[z]] fp32 -> outs[z]
+// [cols[z]] in bf16 or fp32. Workgroup: 16 columns x 16 row groups; thread (group q, column c) sums
+// rows q, q + 16, ... with four accumulators in a fixed pattern, and the sixteen group sums are
+// added in order through LDS, so the result does not depend on scheduling (deterministic).
+namespace ps {
+constexpr int kMax = 8, kCols = 16, kGroups = 16;
+struct List {
+  const float* part[kMax];
+  void* out[kMax];
+  int cols[kMax];
+  int off[kMax + 1];   // first flat column of each problem
+  int bf16[kMax];
+  int count;
+};
+}
+__global__ __launch_bounds__(256) void k_partials_sum(int rows, ps::List L) {
+  __shared__ float red[ps::kGroups][ps::kCols + 1];
+  const int cl = threadIdx.x & (ps::kCols - 1), q = threadIdx.x / ps::kCols;
+  const int fc = blockIdx.x * ps::kCols + cl;   // flat column
+  int z = 0;
+  while (z + 1 < L.count && fc >= L.off[z + 1]) ++z;
+  const bool live = fc < L.off[L.count];
+  const int c = fc - L.off[z];
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  if (live) {
+    const float* p = L.part[z] + c;
+    const size_t st = (size_t)L.cols[z];
+    int r = q;
+    for (; r + 3 * ps::kGroups < rows; r += 4 * ps::kGroups) {
+      a0 += p[(size_t)r * st];
+      a1 += p[(size_t)(r + ps::kGroups) * st];
+      a2 += p[(size_t)(r + 2 * ps::kGroups) * st];
+      a3 += p[(size_t)(r + 3 * ps::kGroups) * st];
+    }
+    for (; r < rows; r += ps::kGroups) a0 += p[(size_t)r * st];
+  }
+  red[q][cl] = (a0 + a1) + (a2 + a3);
+  __syncthreads();
+  if (q == 0 && live) {
+    float sum = 0.f;
+#pragma unroll
+    for (int g = 0; g < ps::kGroups; ++g) sum += red[g][cl];
+    if (L.bf16[z]) static_cast<bf16*>(L.out[z])[c] = static_cast<bf16>(sum);
+    else static_cast<float*>(L.out[z])[c] = sum;
+  }
+}
+
 // Threads per head row: d / 8 rounded up to a power of two (the extra threads hold zeros), so that
 // a row's sums are xor shuffles within an aligned lane group.
 __host__ __device__ __forceinline__ int heads_row_threads(int d) {
@@ -662,6 +710,32 @@ bool heads_shapes_ok(int B, int Tn, int H, int d, int nG) {
 }  // namespace
 
 extern "C" {
+
+int atlas_partials_sum(int count, int rows, const int* cols, const float* const* parts, void* const* outs,
+                       const int* out_dtypes, void* stream) {
+  using namespace atlas;
+  if (count < 1 || count > ps::kMax || rows < 0) return ATLAS_MEM_ERR_SHAPE;
+  if (!cols || !parts || !outs || !out_dtypes) return ATLAS_MEM_ERR_NULL;
+  ps::List L = {};
+  L.count = count;
+  int64_t total = 0;
+  for (int z = 0; z < count; ++z) {
+    if (cols[z] < 1) return ATLAS_MEM_ERR_SHAPE;
+    if (out_dtypes[z] != ATLAS_DT_BF16 && out_dtypes[z] != ATLAS_DT_F32) return ATLAS_MEM_ERR_DTYPE;
+    if (!outs[z] || (rows > 0 && !parts[z])) return ATLAS_MEM_ERR_NULL;
+    L.part[z] = parts[z];
+    L.out[z] = outs[z];
+    L.cols[z] = cols[z];
+    L.bf16[z] = out_dtypes[z] == ATLAS_DT_BF16;
+    L.off[z] = (int)total;
+    total += cols[z];
+    if (total >= ((int64_t)1 << 30)) return ATLAS_MEM_ERR_SHAPE;
+  }
+  L.off[count] = (int)total;
+  const unsigned grid = (unsigned)((total + ps::kCols - 1) / ps::kCols);
+  hipLaunchKernelGGL(k_partials_sum, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), rows, L);
+  return hipGetLastError() == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
+}
 
 int atlas_prologue_num_workgroups(int batch, int seq_len) {
   if (batch < 1 || seq_len < 1) return 0;

@@ -809,8 +809,25 @@ def _dt_code(t: Tensor) -> int:
     return _DTYPES[t.dtype]
 
 
-class _PrologueFn(torch.autograd.Function):
-    """xn = RMSNorm(x) and the three depthwise convolutions of xn (atlas_prologue_fwd / _bwd)."""
+def _sum_partials(items):
+    """atlas_partials_sum: items of (partials [rows, ...] fp32, out dtype, out shape) -> the sums over
+    the rows, one launch for all of them (deterministic order)."""
+    lib = _lib.load()
+    parts = [_aligned(p.reshape(p.shape[0], -1)) for p, _, _ in items]
+    outs = [torch.empty(p.shape[1], device=p.device, dtype=dt) for p, (_, dt, _) in zip(parts, items)]
+    cnt = len(parts)
+    I32, VP = ctypes.c_int * cnt, ctypes.c_void_p * cnt
+    _lib.check(lib.atlas_partials_sum(cnt, parts[0].shape[0], I32(*[p.shape[1] for p in parts]),
+                                      VP(*[p.data_ptr() for p in parts]), VP(*[o.data_ptr() for o in outs]),
+                                      I32(*[_DTYPES[o.dtype] for o in outs]), _stream(parts[0].device)),
+               "atlas_partials_sum")
+    return [o.reshape(shape) for o, (_, _, shape) in zip(outs, items)]
+
+
+class _PrologueFn:
+    """xn = RMSNorm(x) and the three depthwise convolutions of xn (atlas_prologue_fwd / _bwd), called
+    by hand from _CellPrologueFn (ctx is a _HandCtx); the backward returns its parameter gradients as
+    per-workgroup partials for one _sum_partials call."""
 
     @staticmethod
     def forward(ctx, x, norm_w, wq, wk, wv, conv_k, eps):
@@ -853,16 +870,15 @@ class _PrologueFn(torch.autograd.Function):
                                           _ptr(tv if conv else None), _ptr(inv), _ptr(dxn), _ptr(dqi), _ptr(dki),
                                           _ptr(dvi), _ptr(dx), _ptr(dnw), _ptr(dcv), _stream(x.device)),
                    "atlas_prologue_bwd")
-        dnorm = dnw.sum(dim=0).to(norm_w.dtype)
-        if not conv:
-            return dx, dnorm, None, None, None, None, None
-        dtaps = dcv.sum(dim=0).to(x.dtype)
-        return (dx, dnorm, dtaps[0].reshape(ctx.wshape), dtaps[1].reshape(ctx.wshape), dtaps[2].reshape(ctx.wshape),
-                None, None)
+        parts = [(dnw, norm_w.dtype, tuple(norm_w.shape))]
+        if conv:
+            parts.append((dcv, x.dtype, (3, *ctx.wshape)))
+        return dx, parts
 
 
-class _HeadsFn(torch.autograd.Function):
-    """Head split, MultiheadRMSNorm of q / k and the gate sigmoids (atlas_heads_fwd / _bwd)."""
+class _HeadsFn:
+    """Head split, MultiheadRMSNorm of q / k and the gate sigmoids (atlas_heads_fwd / _bwd), called by
+    hand from _CellPrologueFn; the backward returns its parameter gradients as partials."""
 
     @staticmethod
     def forward(ctx, ql, kl, vl, zl, q_gamma, k_gamma, bias, heads, d):
@@ -914,10 +930,13 @@ class _HeadsFn(torch.autograd.Function):
                                        _ptr(gates if nG else None), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(dql),
                                        _ptr(dkl), _ptr(dvl), _ptr(dzl), _ptr(dqg), _ptr(dkg), _ptr(dbias), _stream(dev)),
                    "atlas_heads_bwd")
-        dqgam = dqg.sum(dim=0).reshape(gshape).to(qg.dtype) if norm else None
-        dkgam = dkg.sum(dim=0).reshape(gshape).to(kg.dtype) if norm else None
-        db = dbias.sum(dim=0).to(bdt) if nG else None
-        return dql, dkl, dvl, dzl, dqgam, dkgam, db, None, None
+        parts = {}
+        if norm:
+            parts["qg"] = (dqg, qg.dtype, gshape)
+            parts["kg"] = (dkg, kg.dtype, gshape)
+        if nG:
+            parts["b"] = (dbias, bdt, (nG * heads,))
+        return dql, dkl, dvl, dzl, parts
 
 
 def _wgrad(dy: Tensor, x: Tensor, dtype) -> Tensor:
@@ -1038,7 +1057,7 @@ class _CellPrologueFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dxn, dq, dk, dv, *dgates):
         qi, ki, vi, xn, Wq, Wk, Wv, Wg = ctx.saved_tensors
-        dql, dkl, dvl, dzl, dqg, dkg, db, _, _ = _HeadsFn.backward(ctx.ch, dq, dk, dv, *dgates)
+        dql, dkl, dvl, dzl, hparts = _HeadsFn.backward(ctx.ch, dq, dk, dv, *dgates)
         if ctx.has_g:
             dqi, dki, dvi, dxg = _products(_GEMM_NN, [dql, dkl, dvl, dzl], [Wq, Wk, Wv, Wg])
         else:
@@ -1050,11 +1069,20 @@ class _CellPrologueFn(torch.autograd.Function):
             dWg = _wgrad(dzl, xn, Wg.dtype)
             dsum = dxg if dsum is None else dsum + dxg
         if ctx.conv:
-            dx, dnorm, dtq, dtk, dtv, _, _ = _PrologueFn.backward(ctx.cp, dsum, dqi, dki, dvi)
+            dx, pparts = _PrologueFn.backward(ctx.cp, dsum, dqi, dki, dvi)
         else:
             dsum = dqi + dki + dvi + (dsum if dsum is not None else 0)
-            dx, dnorm, dtq, dtk, dtv, _, _ = _PrologueFn.backward(ctx.cp, dsum)
-        return (dx, dnorm, dtq, dtk, dtv, dWq, dWk, dWv, dWg, db, dqg, dkg, None, None, None, None)
+            dx, pparts = _PrologueFn.backward(ctx.cp, dsum)
+        # every parameter gradient of the two kernels from their partials, in one launch
+        names = [n for n in ("qg", "kg", "b") if n in hparts]
+        sums = _sum_partials(pparts + [hparts[n] for n in names])
+        dnorm = sums[0]
+        dtq = dtk = dtv = None
+        if ctx.conv:
+            dtq, dtk, dtv = sums[1].unbind(0)
+        got = dict(zip(names, sums[len(pparts):]))
+        return (dx, dnorm, dtq, dtk, dtv, dWq, dWk, dWv, dWg, got.get("b"), got.get("qg"), got.get("kg"),
+                None, None, None, None)
 
 
 def cell_prologue(x: Tensor, norm_weight: Tensor, eps: float, conv_weights, proj_weights, gate_weights, gate_biases,

@@ -301,6 +301,13 @@ int atlas_block_parts(int seq_len);
  * *_part buffer. */
 int atlas_prologue_num_workgroups(int batch, int seq_len);
 
+/* Sums over rows of fp32 partials (the *_part buffers of the kernels below), up to eight arrays in
+ * one launch: outs[z] [cols[z]] = sum_r parts[z][r][:] in out_dtypes[z] (ATLAS_DT_BF16 or
+ * ATLAS_DT_F32), summed in a fixed order (deterministic). parts, outs, cols and out_dtypes are host
+ * arrays of count entries; rows = 0 writes zeros. */
+int atlas_partials_sum(int count, int rows, const int* cols, const float* const* parts, void* const* outs,
+                       const int* out_dtypes, void* stream);
+
 /* xn = RMSNorm(x) = x rsqrt(mean_c x^2 + eps) norm_w (nn.RMSNorm(dim), the cell's pre_norm) and, when
  * conv_k > 1, the three depthwise convolutions over time of xn (Conv1d(dim, dim, conv_k, padding =
  * conv_k / 2, groups = dim, bias = False) truncated to seq_len: q_in[t] = sum_j wq[c][j] xn[t + j - conv_k/2]).

@@ -319,3 +319,16 @@ def test_linear_batch_errors_before_launch(lib):
     assert call(a=VP(good, None)) == 4
     assert call(c=VP(good, bad)) == 5
     assert call(m=0, a=VP(None, None), c=VP(None, None)) == 0    # m = 0: nothing launched
+
+
+def test_partials_sum_errors_before_launch(lib):
+    good = 0x10000
+    I32, VP = ctypes.c_int * 2, ctypes.c_void_p * 2
+    f = lib.atlas_partials_sum
+    assert f(0, 4, I32(8, 8), VP(good, good), VP(good, good), I32(1, 1), None) == 2      # one to eight arrays
+    assert f(9, 4, I32(8, 8), VP(good, good), VP(good, good), I32(1, 1), None) == 2
+    assert f(2, -1, I32(8, 8), VP(good, good), VP(good, good), I32(1, 1), None) == 2
+    assert f(2, 4, I32(8, 0), VP(good, good), VP(good, good), I32(1, 1), None) == 2
+    assert f(2, 4, I32(8, 8), VP(good, good), VP(good, good), I32(1, 2), None) == 3      # bf16 or fp32 out
+    assert f(2, 4, I32(8, 8), VP(good, None), VP(good, good), I32(1, 0), None) == 4
+    assert f(2, 4, I32(8, 8), VP(good, good), VP(None, good), I32(1, 0), None) == 4
