@@ -66,6 +66,8 @@ EXPORTED_SYMBOLS = (
     "atlas_linear_batch",
     "atlas_linear_wgrad_workspace_bytes",
     "atlas_linear_wgrad",
+    "atlas_linear_wgrad_batch_workspace_bytes",
+    "atlas_linear_wgrad_batch",
     "atlas_mem_profile_enable",
     "atlas_mem_profile_read",
     "atlas_mem_kernel_name",
@@ -190,6 +192,11 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_linear_wgrad_workspace_bytes.argtypes = [i64, i32, i32]
     lib.atlas_linear_wgrad.restype = i32
     lib.atlas_linear_wgrad.argtypes = [i32, i64, i32, i32, vp, vp, vp, vp, i64, vp]
+    lib.atlas_linear_wgrad_batch_workspace_bytes.restype = i64
+    lib.atlas_linear_wgrad_batch_workspace_bytes.argtypes = [i32, i64, ctypes.POINTER(i32), ctypes.POINTER(i32)]
+    lib.atlas_linear_wgrad_batch.restype = i32
+    lib.atlas_linear_wgrad_batch.argtypes = [i32, i32, i64, ctypes.POINTER(i32), ctypes.POINTER(i32),
+                                             ctypes.POINTER(vp), ctypes.POINTER(vp), ctypes.POINTER(vp), vp, i64, vp]
     lib.atlas_mem_profile_enable.restype = i32
     lib.atlas_mem_profile_enable.argtypes = [i32]
     lib.atlas_mem_profile_read.restype = i32

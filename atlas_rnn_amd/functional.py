@@ -939,31 +939,46 @@ class _HeadsFn:
         return dql, dkl, dvl, dzl, parts
 
 
-def _wgrad(dy: Tensor, x: Tensor, dtype) -> Tensor:
-    """dW = dy^T x over every leading axis of dy [..., o] and x [..., i]. bf16 operands go to
-    atlas_linear_wgrad (both read as stored, the token axis split over the matrix cores, fp32
-    partials summed in a fixed order): 16384 tokens x 512 x 512 took 67 us through a transposed copy
-    and a batched hipBLASLt product, whose plain form (one product with K = 16384 on few output
-    tiles) took 100 us. fp32 operands keep torch's product over token slices."""
-    o, i = dy.shape[-1], x.shape[-1]
-    dy2, x2 = dy.reshape(-1, o), x.reshape(-1, i)
-    n = dy2.shape[0]
-    if dy2.dtype == torch.bfloat16 and x2.dtype == torch.bfloat16 and o % 8 == 0 and i % 8 == 0 \
-            and dtype in (torch.bfloat16, torch.float32):
+def _wgrads(pairs, dtype) -> list:
+    """dW = dy^T x over every leading axis of dy [..., o] and x [..., i], for each (dy, x) of pairs
+    (the same token count). bf16 operands go to atlas_linear_wgrad_batch, all layers in one launch
+    (both activations read as stored, the token axis split over the matrix cores, fp32 partials
+    summed in a fixed order): 16384 tokens x 512 x 512 took 67 us through a transposed copy and a
+    batched hipBLASLt product, whose plain form (one product with K = 16384 on few output tiles)
+    took 100 us. fp32 operands keep torch's product over token slices."""
+    dys = [dy.reshape(-1, dy.shape[-1]) for dy, _ in pairs]
+    xs = [x.reshape(-1, x.shape[-1]) for _, x in pairs]
+    n = dys[0].shape[0]
+    if all(d.dtype == torch.bfloat16 and x.dtype == torch.bfloat16 and d.shape[-1] % 8 == 0 and x.shape[-1] % 8 == 0
+           and d.shape[0] == n and x.shape[0] == n for d, x in zip(dys, xs)) and dtype in _DTYPES:
         lib = _lib.load()
-        dy2, x2 = _aligned(dy2), _aligned(x2)
-        dev = dy2.device
-        ws_bytes = lib.atlas_linear_wgrad_workspace_bytes(n, o, i)
+        dys, xs = [_aligned(d) for d in dys], [_aligned(x) for x in xs]
+        dev = dys[0].device
+        cnt = len(dys)
+        I32, VP = ctypes.c_int * cnt, ctypes.c_void_p * cnt
+        os_, is_ = I32(*[d.shape[1] for d in dys]), I32(*[x.shape[1] for x in xs])
+        ws_bytes = lib.atlas_linear_wgrad_batch_workspace_bytes(cnt, n, os_, is_)
         ws = torch.empty(max(ws_bytes, 16) // 4, device=dev, dtype=torch.float32)
-        dw = torch.empty(o, i, device=dev, dtype=dtype)
-        _lib.check(lib.atlas_linear_wgrad(_DTYPES[dtype], n, o, i, _ptr(dy2), _ptr(x2), _ptr(dw), _ptr(ws), ws_bytes,
-                                          _stream(dev)), "atlas_linear_wgrad")
-        return dw
-    S = next((c for c in (8, 4, 2) if n % c == 0 and n // c >= 1024), 1)
-    if S == 1:
-        return (dy2.t() @ x2).to(dtype)
-    a = dy2.view(S, n // S, o).transpose(1, 2).contiguous()   # both operands row-major (no transposed views)
-    return torch.bmm(a, x2.view(S, n // S, i).contiguous()).float().sum(0).to(dtype)
+        dws = [torch.empty(d.shape[1], x.shape[1], device=dev, dtype=dtype) for d, x in zip(dys, xs)]
+        _lib.check(lib.atlas_linear_wgrad_batch(_DTYPES[dtype], cnt, n, os_, is_, VP(*[d.data_ptr() for d in dys]),
+                                                VP(*[x.data_ptr() for x in xs]), VP(*[w.data_ptr() for w in dws]),
+                                                _ptr(ws), ws_bytes, _stream(dev)), "atlas_linear_wgrad_batch")
+        return dws
+    out = []
+    for dy2, x2 in zip(dys, xs):
+        o, i = dy2.shape[-1], x2.shape[-1]
+        S = next((c for c in (8, 4, 2) if n % c == 0 and n // c >= 1024), 1)
+        if S == 1:
+            out.append((dy2.t() @ x2).to(dtype))
+            continue
+        a = dy2.view(S, n // S, o).transpose(1, 2).contiguous()   # both operands row-major (no transposed views)
+        out.append(torch.bmm(a, x2.view(S, n // S, i).contiguous()).float().sum(0).to(dtype))
+    return out
+
+
+def _wgrad(dy: Tensor, x: Tensor, dtype) -> Tensor:
+    """One layer's weight gradient (_wgrads)."""
+    return _wgrads([(dy, x)], dtype)[0]
 
 
 _GEMM_NT, _GEMM_NN = 0, 1
@@ -1062,11 +1077,12 @@ class _CellPrologueFn(torch.autograd.Function):
             dqi, dki, dvi, dxg = _products(_GEMM_NN, [dql, dkl, dvl, dzl], [Wq, Wk, Wv, Wg])
         else:
             dqi, dki, dvi = _products(_GEMM_NN, [dql, dkl, dvl], [Wq, Wk, Wv])
-        dWq, dWk, dWv = _wgrad(dql, qi, Wq.dtype), _wgrad(dkl, ki, Wk.dtype), _wgrad(dvl, vi, Wv.dtype)
-        dWg = None
+        pairs = [(dql, qi), (dkl, ki), (dvl, vi)] + ([(dzl, xn)] if ctx.has_g else [])
+        dws = _wgrads(pairs, Wq.dtype)
+        dWq, dWk, dWv = dws[:3]
+        dWg = dws[3] if ctx.has_g else None
         dsum = dxn
         if ctx.has_g:
-            dWg = _wgrad(dzl, xn, Wg.dtype)
             dsum = dxg if dsum is None else dsum + dxg
         if ctx.conv:
             dx, pparts = _PrologueFn.backward(ctx.cp, dsum, dqi, dki, dvi)

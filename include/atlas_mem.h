@@ -368,6 +368,16 @@ int64_t atlas_linear_wgrad_workspace_bytes(int64_t n, int out_features, int in_f
 int atlas_linear_wgrad(int out_dtype, int64_t n, int out_features, int in_features, const void* dy, const void* x,
                        void* dw, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The same for up to four layers over the same n tokens in one launch (the prologue's q / k / v /
+ * gate weights): out_features, in_features, dy, x and dw are host arrays of count entries, the
+ * workspace (atlas_linear_wgrad_batch_workspace_bytes, -1 for invalid sizes) holds every layer's
+ * partials. */
+int64_t atlas_linear_wgrad_batch_workspace_bytes(int count, int64_t n, const int* out_features,
+                                                 const int* in_features);
+int atlas_linear_wgrad_batch(int out_dtype, int count, int64_t n, const int* out_features, const int* in_features,
+                             const void* const* dy, const void* const* x, void* const* dw, void* workspace,
+                             int64_t workspace_bytes, void* stream);
+
 /* ---- diagnostics (no reference counterpart) ------------------------------------------------ */
 
 /* Number of kernels the timing hooks distinguish (index -> atlas_mem_kernel_name). */

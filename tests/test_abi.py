@@ -271,6 +271,21 @@ def test_linear_wgrad_errors_before_launch(lib):
     assert g(_lib.DT_BF16, 1000, 32, 512, good, good, good, None, need, None) == 4   # n > 0 needs workspace
     assert g(_lib.DT_BF16, 1000, 32, 512, good, bad, good, good, need, None) == 5
     assert g(_lib.DT_F32, 1000, 32, 512, good, good, good, good, need - 4, None) == 7
+    I32, VP = ctypes.c_int * 2, ctypes.c_void_p * 2
+    bws = lib.atlas_linear_wgrad_batch_workspace_bytes
+    gb = lib.atlas_linear_wgrad_batch
+    # a batch shares the token splits: 16384 tokens over 16 + 4 tiles -> 25 splits of 672 tokens
+    assert bws(2, 16384, I32(512, 32), I32(512, 512)) == 25 * (16 + 4) * 128 * 128 * 4
+    assert bws(0, 100, I32(8, 8), I32(8, 8)) == -1 and bws(5, 100, I32(8, 8), I32(8, 8)) == -1
+    need2 = bws(2, 1000, I32(64, 32), I32(64, 512))
+    assert gb(_lib.DT_BF16, 2, 1000, I32(64, 36), I32(64, 512), VP(good, good), VP(good, good), VP(good, good),
+              good, need2, None) == 2
+    assert gb(_lib.DT_BF16, 2, 1000, I32(64, 32), I32(64, 512), VP(good, None), VP(good, good), VP(good, good),
+              good, need2, None) == 4
+    assert gb(_lib.DT_BF16, 2, 1000, I32(64, 32), I32(64, 512), VP(good, good), VP(good, bad.value), VP(good, good),
+              good, need2, None) == 5
+    assert gb(_lib.DT_BF16, 2, 1000, I32(64, 32), I32(64, 512), VP(good, good), VP(good, good), VP(good, good),
+              good, need2 - 4, None) == 7
 
 
 def test_tensor_feature_map_raises_off_kernel():

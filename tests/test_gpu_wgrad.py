@@ -115,3 +115,19 @@ def test_wgrad_through_the_linear_helper():
     torch.cuda.synchronize()
     assert dw.dtype == torch.bfloat16 and dw.shape == (96, 40)
     _check(dw, dy.reshape(-1, 96), x.reshape(-1, 40), torch.bfloat16)
+
+
+def test_wgrad_batch_of_the_prologue_layers():
+    """atlas_linear_wgrad_batch through functional._wgrads: the prologue's q / k / v (512 x 512) and
+    gate-head (32 x 512) weights over the same 16384 tokens in one launch, each against fp64."""
+    from atlas_rnn_amd.functional import _wgrads
+    _say("wgrad batch of four layers")
+    g = torch.Generator(device="cpu").manual_seed(13)
+    n = 16384
+    pairs = [(torch.randn(n, o, generator=g).to(DEV, torch.bfloat16), torch.randn(n, 512, generator=g).to(DEV, torch.bfloat16))
+             for o in (512, 512, 512, 32)]
+    dws = _wgrads(pairs, torch.bfloat16)
+    torch.cuda.synchronize()
+    for dw, (dy, x) in zip(dws, pairs):
+        assert dw.shape == (dy.shape[1], 512)
+        _check(dw, dy, x, torch.bfloat16)
