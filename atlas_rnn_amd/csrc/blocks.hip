@@ -271,7 +271,7 @@ int atlas_block_merge(int dtype, int bh, int seq_len, int d_k, int d_v, const vo
   hipStream_t s = static_cast<hipStream_t>(stream);
   const void* mk = dtype == ATLAS_DT_BF16 ? reinterpret_cast<const void*>(&k_block_merge<bf16>)
                                           : reinterpret_cast<const void*>(&k_block_merge<float>);
-  if (hipFuncSetAttribute(mk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+  if (set_dyn_smem(mk, smem) != hipSuccess)
     return ATLAS_MEM_ERR_LAUNCH;
   if (dtype == ATLAS_DT_BF16) {
     hipLaunchKernelGGL(k_block_merge<bf16>, grid, dim3(blk::kThreads), smem, s, bh, seq_len, d_k, d_v, S_ref,

@@ -18,7 +18,28 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+#include <set>
+#include <tuple>
+
 namespace atlas {
+
+// hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per kernel, device and size: the attribute
+// stays set, and the runtime call otherwise costs host time on every launch.
+inline hipError_t set_dyn_smem(const void* fn, size_t bytes) {
+  static std::mutex mu;
+  static std::set<std::tuple<const void*, int, size_t>> done;
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  const auto key = std::make_tuple(fn, dev, bytes);
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count(key)) return hipSuccess;
+  err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (err == hipSuccess) done.insert(key);
+  return err;
+}
+
 
 typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

@@ -915,8 +915,7 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
         BwdSegPtrs pf = p;
         pf.coef = const_cast<float*>(ag->coef);
         const size_t smem = sizeof(BwdAggSmem<T, 64, D>);
-        err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bwd_seg_agg<T, 64, D>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        err = set_dyn_smem(reinterpret_cast<const void*>(&k_bwd_seg_agg<T, 64, D>), smem);
         if (err != hipSuccess) return err;
         prof_begin(KID_BWD_ADJOINT, stream);
         hipLaunchKernelGGL((k_bwd_seg_agg<T, 64, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, ag->g, a,
@@ -927,8 +926,7 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
     }
     if (!ag) {
       const size_t smem = sizeof(BwdAggSmem<T, CH, D>);
-      err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bwd_seg_agg<T, CH, D>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      err = set_dyn_smem(reinterpret_cast<const void*>(&k_bwd_seg_agg<T, CH, D>), smem);
       if (err != hipSuccess) return err;
       prof_begin(KID_BWD_ADJOINT, stream);
       hipLaunchKernelGGL((k_bwd_seg_agg<T, CH, D>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, p);
@@ -954,8 +952,7 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
   }
   if (!walk) {
     const size_t smem = bwd_seg_smem_bytes<T, CH, D>(g.H);
-    err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bwd_seg<T, CH, D>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    err = set_dyn_smem(reinterpret_cast<const void*>(&k_bwd_seg<T, CH, D>), smem);
     if (err != hipSuccess) return err;
     prof_name(KID_BWD_CHUNK, "k_bwd_seg");
     prof_begin(KID_BWD_CHUNK, stream);

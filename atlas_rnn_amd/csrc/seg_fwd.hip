@@ -120,8 +120,7 @@ hipError_t launch_fwd_seg(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg,
   hipError_t err = hipSuccess;
   if (sg.nseg > 1) {
     const size_t smem = sizeof(SegFwdSmem<T, CH, D, false>);
-    err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_seg_agg<T, CH, D>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    err = set_dyn_smem(reinterpret_cast<const void*>(&k_fwd_seg_agg<T, CH, D>), smem);
     if (err != hipSuccess) return err;
     prof_name(KID_FWD_SEG_AGG, "k_fwd_seg_agg");
     prof_begin(KID_FWD_SEG_AGG, stream);
@@ -132,8 +131,7 @@ hipError_t launch_fwd_seg(const Geom& g, const FwdPtrs<T>& a, const SegGeom& sg,
   }
   if ((err = launch_fwd_seg_scan<T, D>(g, a, sg, agg, seg_states, stream)) != hipSuccess) return err;
   const size_t smem = sizeof(SegFwdSmem<T, CH, D, true>);
-  err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_seg<T, CH, D>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  err = set_dyn_smem(reinterpret_cast<const void*>(&k_fwd_seg<T, CH, D>), smem);
   if (err != hipSuccess) return err;
   prof_name(KID_FWD_WALK, "k_fwd_seg");
   prof_begin(KID_FWD_WALK, stream);

@@ -491,8 +491,7 @@ template <int D, int M, bool SYM = false>
 hipError_t launch_tmap_bwd(long n, const bf16* x, const bf16* p, const bf16* dout, bf16* dx, int deg, const bf16* pre,
                            hipStream_t s) {
   const size_t smem = sizeof(TmapBwdSmem<D, M>);
-  hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_tmap_bwd<D, M, SYM>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  hipError_t err = set_dyn_smem(reinterpret_cast<const void*>(&k_tmap_bwd<D, M, SYM>), smem);
   if (err != hipSuccess) return err;
   const unsigned grid = (unsigned)((n + tm::TN - 1) / tm::TN);
   hipLaunchKernelGGL((k_tmap_bwd<D, M, SYM>), dim3(grid), dim3(64 * 4 * (D / 32)), smem, s, n, x, p, dout, dx, deg,

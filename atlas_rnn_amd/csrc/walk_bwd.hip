@@ -633,8 +633,7 @@ template <bool MAPE, int HC, bool BUF = false>
 hipError_t launch_walk_bwd_h(const Geom& g, const BwdPtrs<bf16>& a, const SegGeom& sg, const BwdSegPtrs& p,
                              hipStream_t stream) {
   const size_t smem = sizeof(wb::Smem);
-  const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_bwd<MAPE, HC, BUF>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  const hipError_t err = set_dyn_smem(reinterpret_cast<const void*>(&k_walk_bwd<MAPE, HC, BUF>), smem);
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL((k_walk_bwd<MAPE, HC, BUF>), dim3(sg.nseg, g.BH), dim3(kSegThreads), smem, stream, g, a, sg, p);
   return hipGetLastError();

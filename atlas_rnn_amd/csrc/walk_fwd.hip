@@ -528,8 +528,7 @@ static hipError_t launch_walks(const Geom& g, const FwdPtrs<bf16>& a, const SegG
   hipError_t err;
   if (sg.nseg > 1) {
     const size_t smem = sizeof(wf::Smem<false>);
-    err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_agg<MAPE>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    err = set_dyn_smem(reinterpret_cast<const void*>(&k_walk_agg<MAPE>), smem);
     if (err != hipSuccess) return err;
     prof_name(KID_FWD_SEG_AGG, "k_walk_agg");
     prof_begin(KID_FWD_SEG_AGG, stream);
@@ -540,8 +539,7 @@ static hipError_t launch_walks(const Geom& g, const FwdPtrs<bf16>& a, const SegG
   }
   if ((err = launch_fwd_seg_scan<bf16, 64>(g, a, sg, agg, seg_states, stream)) != hipSuccess) return err;
   const size_t smem = sizeof(wf::Smem<true>);
-  err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_walk_full<MAPE, BUF>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  err = set_dyn_smem(reinterpret_cast<const void*>(&k_walk_full<MAPE, BUF>), smem);
   if (err != hipSuccess) return err;
   prof_name(KID_FWD_WALK, "k_walk_full");
   prof_begin(KID_FWD_WALK, stream);
