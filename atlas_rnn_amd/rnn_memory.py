@@ -212,14 +212,13 @@ class _CellBase(Module):
 
     def _memory(self, x, state, window) -> tuple[Tensor, RNNMemState]:
         batch, seq_len, _ = x.shape
-        # a state the cell creates itself has Z = 0 and an all-zero omega buffer: they are passed as
-        # absent (the kernels read absent as zeros), which keeps the call on the specialised walks
+        # a state the cell creates itself (init_state) is all zeros: S0 is passed as absent (one fp32
+        # zero state, also S_ref) and Z and the omega buffer as absent (the kernels read absent as
+        # zeros), which keeps the call on the specialised walks without materialising the zeros
         fresh = not exists(state)
-        if fresh:
-            state = self.init_state(batch, x.device, x.dtype)
         k, q, v, lr, decay, beta, gate = self._inputs(x)
-        S0 = state.S
-        Z0 = state.Z if (self.use_momentum and exists(state.Z) and not fresh) else None
+        S0 = None if fresh else state.S
+        Z0 = state.Z if (self.use_momentum and not fresh and exists(state.Z)) else None
         buf = state.omega_buffer if (window > 1 and not fresh) else None
         chunk = self.scan_chunk_len if (exists(self.scan_chunk_len) and seq_len > self.scan_chunk_len) else None
         y, S_T, Z_T, buf_out = memory_recurrence(
@@ -227,10 +226,10 @@ class _CellBase(Module):
             map_mode='elementwise' if self.phi.fused_elementwise else 'off', map_degree=self.phi.degree,
             clamp_every=chunk, clamp_final=True)
         y = rearrange(y.to(x.dtype), '(b h) t d -> b h t d', b=batch, h=self.heads)
-        out = linear(self.merge_heads(y), self.to_out.weight)   # to_out, token-split weight gradient
-        dt = S0.dtype
+        out = linear(self.merge_heads(y), self.to_out.weight)   # to_out on the library's bf16 products
+        dt = x.dtype if fresh else S0.dtype   # init_state's dtype for a fresh state
         next_state = RNNMemState(
-            seq_index=state.seq_index + seq_len,
+            seq_index=(0 if fresh else state.seq_index) + seq_len,
             S=S_T.to(dt),
             Z=Z_T.to(dt) if (self.use_momentum and exists(Z_T)) else None,
             omega_buffer=buf_out.to(dt) if exists(buf_out) else None,
@@ -327,7 +326,7 @@ class OmegaRNNMemoryCell(_CellBase):
             Z = Z_T.to(x.dtype) if self.use_momentum else zeros
         y = torch.cat(ys, dim=1) if len(ys) > 1 else ys[0]
         y = rearrange(y, '(b h) t d -> b h t d', b=batch, h=self.heads)
-        out = linear(self.merge_heads(y), self.to_out.weight)   # to_out, token-split weight gradient
+        out = linear(self.merge_heads(y), self.to_out.weight)   # to_out on the library's bf16 products
         next_state = RNNMemState(seq_index=state.seq_index + seq_len, S=S,
                                  Z=Z if self.use_momentum else None, omega_buffer=None)
         return out, next_state
