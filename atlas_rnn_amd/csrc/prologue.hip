@@ -1,12 +1,12 @@
 // prologue.hip - the memory cell's prologue around its projections (atlas_pytorch/rnn_memory.py:567-653,
-// MultiheadRMSNorm :139-147), fused into two kernels on each side of the GEMMs (which stay on
-// hipBLASLt):
+// MultiheadRMSNorm :139-147), fused into two kernels on each side of the products (gemm.hip,
+// weight gradients wgrad.hip):
 //
 //   k_pro_fwd   : xn = RMSNorm(x) (nn.RMSNorm(dim): x * rsqrt(mean(x^2) + eps) * w), and the three
 //                 depthwise convolutions over time of xn (Conv1d(dim, dim, K, padding = K / 2,
 //                 groups = dim, no bias), truncated to T: out[t] = sum_j w[c][j] xn[t + j - K/2], so
 //                 for K = 4 token t sees t + 1) -> xn, q_in, k_in, v_in [B, T, dim]
-//   (q_in, k_in, v_in, xn) @ (Wq, Wk, Wv, Wgates)^T on hipBLASLt
+//   (q_in, k_in, v_in, xn) @ (Wq, Wk, Wv, Wgates)^T as one batched launch (gemm.hip)
 //   k_heads_fwd : per (b, t, h) row the head split to the recurrence's [(b h), T, d] layout,
 //                 MultiheadRMSNorm of q and k (x / max(|x| d^-1/2, 1e-8) * gamma[h]), and the gate heads'
 //                 bias + sigmoid -> q, k, v [(b h), T, d], gates [nG][(b h), T]

@@ -1113,7 +1113,7 @@ def cell_prologue(x: Tensor, norm_weight: Tensor, eps: float, conv_weights, proj
     """The memory cell's prologue (rnn_memory.py:567-653) on the fused kernels:
 
         xn = RMSNorm(x);  q_in, k_in, v_in = depthwise convs of xn (or xn itself)
-        ql, kl, vl = q_in Wq^T, k_in Wk^T, v_in Wv^T;  zl = xn [W_g1; W_g2; ...]^T     (GEMMs, hipBLASLt)
+        ql, kl, vl = q_in Wq^T, k_in Wk^T, v_in Wv^T;  zl = xn [W_g1; W_g2; ...]^T     (one batched launch)
         q, k = MultiheadRMSNorm of the heads of ql, kl; v = the heads of vl;  gate_i = sigmoid(zl_i + b_i)
 
     x [B, T, dim]; conv_weights (wq, wk, wv) [dim, 1, K] or None; proj_weights (Wq, Wk, Wv) [H d, dim];
