@@ -243,6 +243,34 @@ def _tmap_check(x: Tensor, proj: Tensor, degree: int) -> None:
         raise ValueError(f"tensor_feature_map: degree {degree} (1 .. 16)")
 
 
+_SYM_CACHE: dict = {}
+
+
+def _symmetrized(proj: Tensor, d: int, dtype) -> tuple[Tensor, Tensor]:
+    """The symmetrised table of proj [d + d*d, m] in both layouts (atlas_tensor_map_symmetrize: one
+    launch in place of a transposition; the forward and the backward skip the products over its
+    zero lower triangle). proj is a constant (a registered buffer in the reference), so the tables
+    are kept per (storage, version, dtype) and a map over k and q, or the next step, reuses them;
+    an in-place change of proj bumps its version and forms them again. The entry holds proj itself,
+    so that its storage cannot be freed and reused by another tensor while the entry exists."""
+    key = (proj.data_ptr(), proj._version, tuple(proj.shape), proj.dtype, dtype, proj.device)
+    hit = _SYM_CACHE.get(key)
+    if hit is not None and hit[0] is proj:
+        return hit[1], hit[2]
+    lib = _lib.load()
+    dev = proj.device
+    m = proj.shape[1]
+    p = _aligned(proj.detach().to(dtype))
+    ps = torch.empty_like(p)
+    pst = torch.empty(m, p.shape[0], device=dev, dtype=p.dtype)
+    _lib.check(lib.atlas_tensor_map_symmetrize(_dt_code(p), d, m, _ptr(p), _ptr(ps), _ptr(pst), _stream(dev)),
+               "atlas_tensor_map_symmetrize")
+    if len(_SYM_CACHE) >= 8:
+        _SYM_CACHE.clear()
+    _SYM_CACHE[key] = (proj, ps, pst)
+    return ps, pst
+
+
 class _TensorMapFn(torch.autograd.Function):
     """atlas_tensor_map_fwd / _bwd: x [n, d] and P [d + d*d, m] (bf16 or fp32, P in x's dtype as the
     reference casts it) -> phi [n, m], followed by the elementwise polynomial of `degree` (1: none);
@@ -254,13 +282,7 @@ class _TensorMapFn(torch.autograd.Function):
         lib = _lib.load()
         lead, d, m = x.shape[:-1], x.shape[-1], proj.shape[-1]
         x2 = _aligned(x.reshape(-1, d))
-        p = _aligned(proj.to(x.dtype))
-        # the symmetrised table in both layouts (one launch in place of a transposition): the forward
-        # and the backward skip the products over its zero lower triangle
-        ps = torch.empty_like(p)
-        pst = torch.empty(m, p.shape[0], device=dev, dtype=p.dtype)
-        _lib.check(lib.atlas_tensor_map_symmetrize(_dt_code(p), d, m, _ptr(p), _ptr(ps), _ptr(pst), _stream(dev)),
-                   "atlas_tensor_map_symmetrize")
+        ps, pst = _symmetrized(proj, d, x.dtype)
         n = x2.shape[0]
         out = torch.empty(n, m, device=dev, dtype=x.dtype)
         pre = torch.empty(n, m, device=dev, dtype=x.dtype) if degree > 1 else None

@@ -165,3 +165,26 @@ def test_c4_composition_reduced():
     compare("c4.S_T", STg.detach().float().cpu(), S_T.detach(), TOL)
     for kk in names:
         compare(f"c4.d{kk}", got_g[kk].float().cpu(), ref_g[kk], TOL)
+
+
+def test_symmetrised_tables_follow_in_place_changes_of_proj():
+    """The symmetrised tables are kept per projection; an in-place change of proj (its version)
+    forms them again, so the map always uses the current proj."""
+    from atlas_rnn_amd.functional import tensor_feature_map
+    _say("tensor map after an in-place change of proj")
+    g = torch.Generator().manual_seed(778)
+    d, m, n = 64, 128, 200
+    bound = (6.0 / (d + d * d + m)) ** 0.5
+    P = ((torch.rand(d + d * d, m, generator=g) * 2 - 1) * bound).to(BF16)
+    x = torch.randn(n, d, generator=g)
+    x = (x / x.norm(dim=-1, keepdim=True)).to(BF16)
+    dev = torch.device("cuda:0")
+    Pd, xd = P.to(dev), x.to(dev)
+    out1 = tensor_feature_map(xd, Pd, 1)
+    out2 = tensor_feature_map(xd, Pd, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+    Pd.mul_(2.0)   # exact in bf16
+    out3 = tensor_feature_map(xd, Pd, 1)
+    torch.cuda.synchronize()
+    compare("tmap.after_inplace", out3.float().cpu(), poly_feature_map(x.to(F64), 2, 'tensor', 2.0 * P.to(F64)), TOL)
