@@ -556,7 +556,8 @@ def run_module(steps, warmup, B=4, T=4096, heads=8, d=64, e=4, chunk=64):
     (loss = sum out * g), called with a fresh state (state=None: a new sequence) and with a carried
     state (the previous call's S, Z and omega buffer). The library's recurrence kernels inside the
     cell step are timed with its HIP events and set against the same recurrence through the
-    preplanned path (RecurrencePlan, token gates, clamp_every=64)."""
+    preplanned path (RecurrencePlan, token gates, clamp_every=64). The same step captured in a HIP
+    graph (torch.cuda.CUDAGraph) is timed too: `value` stays the eager call a drop-in user makes."""
     import torch
     import atlas_rnn_amd as am
     from atlas_rnn_amd.functional import RecurrencePlan, profile_enable, profile_read
@@ -600,7 +601,27 @@ def run_module(steps, warmup, B=4, T=4096, heads=8, d=64, e=4, chunk=64):
         prof = profile_read(reset=True)
         profile_enable(False)
         rec_ms = sum(v for v, n in prof.values()) / steps
-        res[name] = {"ms_per_step": round(ms, 4), "recurrence_kernels_ms": round(rec_ms, 4),
+        # the same step captured in a HIP graph and replayed (no Python, autograd or launch cost)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                step(state)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step(state)
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        graph_ms = 1e3 * (time.perf_counter() - t0) / steps
+        del graph
+        res[name] = {"ms_per_step": round(ms, 4), "graph_replay_ms_per_step": round(graph_ms, 4),
+                     "recurrence_kernels_ms": round(rec_ms, 4),
                      "kernels": {kk: round(1e3 * v / steps, 2) for kk, (v, n) in prof.items() if n}}
     # the same recurrence through the preplanned path
     bh = B * heads
