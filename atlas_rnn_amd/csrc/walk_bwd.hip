@@ -61,8 +61,10 @@ struct Smem {
   alignas(16) bf16 dSeT[2][D][PD];    // chunk-end adjoint, transposed (dSeT[k][i] = dS_end[i][k]), by parity
   alignas(16) bf16 dZeT[2][D][PD];
   alignas(16) float carry[2][HMAX][2 * D];   // halo partials (dv | dphi) handed to the previous chunk
-  float hS[SPM], hZ[SPM];
-  float fS[2][CH], fZ[2][CH];         // by chunk parity
+  // scalar-gradient sums, one slot per contributing wave (summed in a fixed order when the chunk's
+  // record is written, so the result does not depend on the order the waves finish in)
+  float hS[4][SPM], hZ[4][SPM];       // [it1][s]
+  float fS[2][4][CH], fZ[2][4][CH];   // [chunk parity][kt][tau]
   float red[2][kSegWaves][4];         // Gram partials, by chunk parity
 };
 static_assert(sizeof(Smem) <= 160 * 1024, "one workgroup per CU: at most 160 KB of LDS");
@@ -224,8 +226,8 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
     sm.st[1].wsh[rr][cc] = bf16(0.f);
   }
   for (int idx = tid; idx < 2 * HMAX * 2 * D; idx += kSegThreads) (&sm.carry[0][0][0])[idx] = 0.f;
-  if (tid < SPM) { sm.hS[tid] = 0.f; sm.hZ[tid] = 0.f; }
-  if (tid < CH) { sm.fS[0][tid] = 0.f; sm.fZ[0][tid] = 0.f; sm.fS[1][tid] = 0.f; sm.fZ[1][tid] = 0.f; }
+  for (int idx = tid; idx < 4 * SPM; idx += kSegThreads) { (&sm.hS[0][0])[idx] = 0.f; (&sm.hZ[0][0])[idx] = 0.f; }
+  for (int idx = tid; idx < 8 * CH; idx += kSegThreads) { (&sm.fS[0][0][0])[idx] = 0.f; (&sm.fZ[0][0][0])[idx] = 0.f; }
 
   // Per-chunk context: token range, halo routing.
   struct Ctx {
@@ -366,7 +368,7 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
       const float4 ps = lds_bf16x4(&st.psi[tau][16 * kt + 4 * gq]);
       const float fs = xsum_rows(TS[0] * ps.x + TS[1] * ps.y + TS[2] * ps.z + TS[3] * ps.w);
       const float fz = xsum_rows(TZ[0] * ps.x + TZ[1] * ps.y + TZ[2] * ps.z + TZ[3] * ps.w);
-      if (gq == 0) { atomicAdd(&sm.fS[c & 1][tau], fs); atomicAdd(&sm.fZ[c & 1][tau], fz); }
+      if (gq == 0) { sm.fS[c & 1][kt][tau] = fs; sm.fZ[c & 1][kt][tau] = fz; }
     }
     {   // Grams <dS_end, S_in>, <dS_end, Z_in>, <dZ_end, Z_in> (fragment (kt, qw) holds the owned elements;
         // selects, not a runtime index, so that the prefetch registers stay registers)
@@ -484,7 +486,7 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
       }
       hs = xsum_rows(hs);
       hz = xsum_rows(hz);
-      if (gq == 0) { atomicAdd(&sm.hS[s], hs); atomicAdd(&sm.hZ[s], hz); }
+      if (gq == 0) { sm.hS[it1][s] = hs; sm.hZ[it1][s] = hz; }
       store4<bf16>(&sm.dD[s][i0], dd[0], dd[1], dd[2], dd[3]);
       float val[4] = {-dd[0], -dd[1], -dd[2], -dd[3]};
       route(x, s, i0, 0, val, rdv, u32x2v{0u, 0u});
@@ -570,16 +572,14 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_bwd(const Geom g, const Bw
     float* blk = p.scal + ((size_t)bh * g.nc + c) * SB::SIZE;
     if (tid >= 256 && tid < 256 + SPM) {
       const int s = tid - 256;
-      blk[SB::HS + s] = sm.hS[s];
-      blk[SB::HZ + s] = sm.hZ[s];
-      sm.hS[s] = 0.f;
-      sm.hZ[s] = 0.f;
+      blk[SB::HS + s] = (sm.hS[0][s] + sm.hS[1][s]) + (sm.hS[2][s] + sm.hS[3][s]);
+      blk[SB::HZ + s] = (sm.hZ[0][s] + sm.hZ[1][s]) + (sm.hZ[2][s] + sm.hZ[3][s]);
     } else if (tid >= 384 && tid < 384 + CH) {
       const int t = tid - 384;
-      blk[SB::FS + t] = sm.fS[c & 1][t];
-      blk[SB::FZ + t] = sm.fZ[c & 1][t];
-      sm.fS[c & 1][t] = 0.f;
-      sm.fZ[c & 1][t] = 0.f;
+      const float(&fs)[4][CH] = sm.fS[c & 1];
+      const float(&fz)[4][CH] = sm.fZ[c & 1];
+      blk[SB::FS + t] = (fs[0][t] + fs[1][t]) + (fs[2][t] + fs[3][t]);
+      blk[SB::FZ + t] = (fz[0][t] + fz[1][t]) + (fz[2][t] + fz[3][t]);
     } else if (tid >= 448 && tid < 452) {
       const int j = tid - 448;
       float sum = 0.f;

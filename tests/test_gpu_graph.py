@@ -4,11 +4,10 @@ The library makes no host synchronisation, allocation or memset on this path (ev
 from torch's allocator, every launch goes to the current stream), so a caller can capture the whole
 training step of OmegaRNNMemoryCell (rnn_memory.py:556-603 and the prologue :567-653) and replay
 it. Each replay follows eager work of the same step and a synchronisation, and is checked against
-the eager result: the output and the final state bit for bit (the forward is deterministic), every
-parameter gradient to a normwise relative error of 2e-3 (the backward walks sum the scalar-gradient
-terms of their waves with LDS float atomics, whose order varies from run to run by a few fp32
-units; a stale or skipped node would be off by O(1)). Fresh and carried states, scan_chunk_len
-set (the two launch sequences chosen on the device by the clamp flag).
+the eager result bit for bit: the output, the final state and every parameter gradient (the bf16
+d = 64 kernels this cell runs sum in a fixed order, so the step is reproducible; a stale or
+skipped node would be off by O(1)). Fresh and carried states, scan_chunk_len set (the two launch
+sequences chosen on the device by the clamp flag).
 """
 
 import sys
@@ -21,7 +20,6 @@ import atlas_rnn_amd as am
 pytestmark = pytest.mark.gpu
 
 DEV = torch.device("cuda:0")
-GRAD_TOL = 2e-3
 
 
 def _say(msg):
@@ -82,9 +80,6 @@ def test_cell_step_graph_replays_match_eager(carried):
         torch.cuda.synchronize()
         for name, got, want in zip(names, static, ref):
             assert torch.isfinite(got.double()).all(), f"replay {r}: {name} not finite"
-            if name in ("out", "S"):
-                assert torch.equal(got, want), f"replay {r}: {name} differs from the eager step"
-            else:
-                err = _normwise(got, want)
-                assert err <= GRAD_TOL, f"replay {r}: grad {name} normwise error {err:.3e} > {GRAD_TOL}"
+            assert torch.equal(got, want), \
+                f"replay {r}: {name} differs from the eager step (normwise {_normwise(got, want):.3e})"
     del graph
