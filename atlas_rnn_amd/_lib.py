@@ -58,6 +58,7 @@ EXPORTED_SYMBOLS = (
     "atlas_block_merge",
     "atlas_block_parts",
     "atlas_partials_sum",
+    "atlas_replicas",
     "atlas_prologue_num_workgroups",
     "atlas_prologue_fwd",
     "atlas_prologue_bwd",
@@ -175,6 +176,9 @@ def load(path: str | None = None) -> ctypes.CDLL:
     lib.atlas_partials_sum.restype = i32
     lib.atlas_partials_sum.argtypes = [i32, i32, ctypes.POINTER(i32), ctypes.POINTER(vp), ctypes.POINTER(vp),
                                        ctypes.POINTER(i32), vp]
+    lib.atlas_replicas.restype = i32
+    lib.atlas_replicas.argtypes = [i32, i32, i32, i32, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(vp),
+                                   ctypes.POINTER(vp), vp]
     lib.atlas_prologue_num_workgroups.restype = i32
     lib.atlas_prologue_num_workgroups.argtypes = [i32, i32]
     lib.atlas_prologue_fwd.restype = i32

@@ -221,6 +221,75 @@ __global__ __launch_bounds__(blk::kThreads) void k_block_dsref(int BH, int Tn, i
       dst[(size_t)(i * B + 16 * w + 4 * (l >> 4) + q) * dk + kb * B + 16 * n + (l & 15)] = -acc[n][q];
 }
 
+// The per-token scalars shared by every block, replicated along the stacked row axis, and the
+// adjoint: the sum over the replicas. Up to four arrays per launch, 8 elements per thread (16-byte
+// accesses when the array allows them), fp32 sums in replica order 0, 1, ... (deterministic).
+namespace rep {
+constexpr int kMax = 4, kThreads = 256, kVec = 8;
+struct List {
+  const void* src[kMax];
+  void* dst[kMax];
+  long n[kMax];
+  long off[kMax + 1];   // first thread of each array (n / 8 rounded up)
+  int vec[kMax];        // both arrays 16-byte aligned, n % 8 == 0: vector accesses
+  int count, nrep;
+};
+}  // namespace rep
+
+template <typename T, bool SUM>
+__global__ __launch_bounds__(rep::kThreads) void k_replicas(rep::List L) {
+  const long v = (long)blockIdx.x * rep::kThreads + threadIdx.x;
+  if (v >= L.off[L.count]) return;
+  int z = 0;
+  while (z + 1 < L.count && v >= L.off[z + 1]) ++z;
+  const long i0 = (v - L.off[z]) * rep::kVec, n = L.n[z];
+  const T* src = static_cast<const T*>(L.src[z]);
+  T* dst = static_cast<T*>(L.dst[z]);
+  constexpr int PER16 = 16 / sizeof(T);   // elements per 16-byte access
+  struct alignas(16) V { T e[PER16]; };   // one 16-byte access, moved as a whole vector
+  if (L.vec[z]) {
+    typedef float f32x4v __attribute__((ext_vector_type(4)));
+    if constexpr (SUM) {
+      float acc[rep::kVec] = {};
+      for (int r = 0; r < L.nrep; ++r) {
+#pragma unroll
+        for (int h = 0; h < rep::kVec / PER16; ++h) {
+          const V x = __builtin_bit_cast(V, *reinterpret_cast<const f32x4v*>(src + (size_t)r * n + i0 + h * PER16));
+#pragma unroll
+          for (int u = 0; u < PER16; ++u) acc[h * PER16 + u] += to_f32(x.e[u]);
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < rep::kVec / PER16; ++h) {
+        V o;
+#pragma unroll
+        for (int u = 0; u < PER16; ++u) o.e[u] = from_f32<T>(acc[h * PER16 + u]);
+        *reinterpret_cast<f32x4v*>(dst + i0 + h * PER16) = __builtin_bit_cast(f32x4v, o);
+      }
+    } else {
+      f32x4v x[rep::kVec / PER16];
+#pragma unroll
+      for (int h = 0; h < rep::kVec / PER16; ++h) x[h] = *reinterpret_cast<const f32x4v*>(src + i0 + h * PER16);
+      for (int r = 0; r < L.nrep; ++r)
+#pragma unroll
+        for (int h = 0; h < rep::kVec / PER16; ++h)
+          *reinterpret_cast<f32x4v*>(dst + (size_t)r * n + i0 + h * PER16) = x[h];
+    }
+    return;
+  }
+  const long i1 = n < i0 + rep::kVec ? n : i0 + rep::kVec;
+  for (long i = i0; i < i1; ++i) {
+    if constexpr (SUM) {
+      float acc = 0.f;
+      for (int r = 0; r < L.nrep; ++r) acc += to_f32(src[(size_t)r * n + i]);
+      dst[i] = from_f32<T>(acc);
+    } else {
+      const T x = src[i];
+      for (int r = 0; r < L.nrep; ++r) dst[(size_t)r * n + i] = x;
+    }
+  }
+}
+
 }  // namespace atlas
 
 using namespace atlas;
@@ -285,6 +354,44 @@ int atlas_block_merge(int dtype, int bh, int seq_len, int d_k, int d_v, const vo
                        (float*)dv);
     hipLaunchKernelGGL(k_block_dsref<float>, pgrid, dim3(blk::kThreads), 0, s, bh, seq_len, d_k, d_v,
                        (const float*)phi, (const float*)dv, dsref_part);
+  }
+  return hipGetLastError() == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
+}
+
+int atlas_replicas(int op, int dtype, int count, int nrep, const int64_t* n, const void* const* src,
+                   void* const* dst, void* stream) {
+  using namespace atlas;
+  if (op != ATLAS_REPLICATE && op != ATLAS_REPLICA_SUM) return ATLAS_MEM_ERR_ARG;
+  if (dtype != ATLAS_DT_F32 && dtype != ATLAS_DT_BF16) return ATLAS_MEM_ERR_DTYPE;
+  if (count < 1 || count > rep::kMax || nrep < 1 || nrep > 64) return ATLAS_MEM_ERR_SHAPE;
+  if (!n || !src || !dst) return ATLAS_MEM_ERR_NULL;
+  rep::List L = {};
+  L.count = count;
+  L.nrep = nrep;
+  const int esize = dtype == ATLAS_DT_BF16 ? 2 : 4;
+  long total = 0;
+  for (int z = 0; z < count; ++z) {
+    if (n[z] < 0 || n[z] * nrep >= ((int64_t)1 << 40)) return ATLAS_MEM_ERR_SHAPE;
+    if (n[z] > 0 && (!src[z] || !dst[z])) return ATLAS_MEM_ERR_NULL;
+    if ((reinterpret_cast<uintptr_t>(src[z]) | reinterpret_cast<uintptr_t>(dst[z])) % esize) return ATLAS_MEM_ERR_ALIGN;
+    L.src[z] = src[z];
+    L.dst[z] = dst[z];
+    L.n[z] = (long)n[z];
+    L.vec[z] = n[z] % rep::kVec == 0 && !blk_misaligned(src[z]) && !blk_misaligned(dst[z]);
+    L.off[z] = total;
+    total += (n[z] + rep::kVec - 1) / rep::kVec;
+  }
+  L.off[count] = total;
+  if (total == 0) return ATLAS_MEM_OK;
+  if ((total + rep::kThreads - 1) / rep::kThreads >= ((int64_t)1 << 31)) return ATLAS_MEM_ERR_SHAPE;
+  const dim3 grid((unsigned)((total + rep::kThreads - 1) / rep::kThreads));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == ATLAS_DT_BF16) {
+    if (op == ATLAS_REPLICA_SUM) hipLaunchKernelGGL((atlas::k_replicas<bf16, true>), grid, dim3(rep::kThreads), 0, s, L);
+    else hipLaunchKernelGGL((atlas::k_replicas<bf16, false>), grid, dim3(rep::kThreads), 0, s, L);
+  } else {
+    if (op == ATLAS_REPLICA_SUM) hipLaunchKernelGGL((atlas::k_replicas<float, true>), grid, dim3(rep::kThreads), 0, s, L);
+    else hipLaunchKernelGGL((atlas::k_replicas<float, false>), grid, dim3(rep::kThreads), 0, s, L);
   }
   return hipGetLastError() == hipSuccess ? ATLAS_MEM_OK : ATLAS_MEM_ERR_LAUNCH;
 }

@@ -371,6 +371,56 @@ class _BlockSplitFn(torch.autograd.Function):
         return dphi, dpsi, dvv, parts.sum(dim=1)
 
 
+_REPLICATE, _REPLICA_SUM = 0, 1
+
+
+def _replicas(op: int, nrep: int, xs):
+    """atlas_replicas over a list of tensors (one launch per dtype, up to four arrays each):
+    _REPLICATE gives [nrep * x.shape[0], ...] (x repeated along the first axis), _REPLICA_SUM the
+    sum of the nrep replicas stacked along the first axis of x."""
+    lib = _lib.load()
+    xs = [x.contiguous() for x in xs]
+    outs = [torch.empty(((nrep * x.shape[0]) if op == _REPLICATE else (x.shape[0] // nrep),) + tuple(x.shape[1:]),
+                        device=x.device, dtype=x.dtype) for x in xs]
+    for dt in {x.dtype for x in xs}:
+        idx = [i for i, x in enumerate(xs) if x.dtype == dt]
+        for c0 in range(0, len(idx), 4):
+            grp = idx[c0:c0 + 4]
+            cnt = len(grp)
+            n64 = (ctypes.c_int64 * cnt)(*[(xs[i] if op == _REPLICATE else outs[i]).numel() for i in grp])
+            vp = ctypes.c_void_p * cnt
+            _lib.check(lib.atlas_replicas(op, _DTYPES[dt], cnt, nrep, n64, vp(*[xs[i].data_ptr() for i in grp]),
+                                          vp(*[outs[i].data_ptr() for i in grp]), _stream(xs[0].device)),
+                       "atlas_replicas")
+    return outs
+
+
+class _ReplicateFn(torch.autograd.Function):
+    """Each tensor repeated nrep times along its first axis; the adjoint sums the replicas."""
+
+    @staticmethod
+    def forward(ctx, nrep, *xs):
+        ctx.nrep = nrep
+        return tuple(_replicas(_REPLICATE, nrep, xs))
+
+    @staticmethod
+    def backward(ctx, *gs):
+        return (None,) + tuple(_replicas(_REPLICA_SUM, ctx.nrep, gs))
+
+
+class _ReplicaSumFn(torch.autograd.Function):
+    """The sum of the nrep replicas stacked along each tensor's first axis; the adjoint repeats."""
+
+    @staticmethod
+    def forward(ctx, nrep, *xs):
+        ctx.nrep = nrep
+        return tuple(_replicas(_REPLICA_SUM, nrep, xs))
+
+    @staticmethod
+    def backward(ctx, *gs):
+        return (None,) + tuple(_replicas(_REPLICATE, ctx.nrep, gs))
+
+
 def block_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
                      beta: Tensor | None, gate: Tensor | None, S_ref: Tensor, S0: Tensor, Z0: Tensor | None,
                      buffer: Tensor | None, *, window: int, map_mode: str, map_degree: int,
@@ -386,7 +436,8 @@ def block_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
     The blocks are stacked along the head-batch axis ((i, j, bh) order) into ONE call of the
     64-wide kernels; the per-token scalars are shared by all blocks. The column / row blocks of
     phi, psi and v - S_ref phi are formed in one pass by atlas_block_split (its adjoint
-    atlas_block_merge); the states and scalars are stacked by small copies. Head sizes that are not
+    atlas_block_merge); the states are stacked by small copies, the scalars by one launch of
+    atlas_replicas (and y summed over the column blocks by another). Head sizes that are not
     a multiple of 64 are zero-padded (the padded rows / columns of every state stay zero).
     """
     bh, T, dk = k.shape
@@ -417,14 +468,21 @@ def block_recurrence(k: Tensor, q: Tensor, v: Tensor, lr: Tensor, decay: Tensor,
         x = x.permute(m + 1, m + 3, 0, *range(1, m + 1), m + 2, m + 4)
         return x.reshape(nb * bh, *mid, _BLOCK, _BLOCK)
 
-    rep = lambda t: None if t is None else t.unsqueeze(0).expand(nb, *t.shape).reshape(nb * bh, *t.shape[1:])
+    # the per-token scalars of every block: one replicating launch (its adjoint: one summing launch)
+    scal = [t for t in (lr, decay, beta, gate) if t is not None]
+    reps = iter(_ReplicateFn.apply(nb, *scal))
+    lr_b, decay_b, beta_b, gate_b = [None if t is None else next(reps) for t in (lr, decay, beta, gate)]
     S0b, Z0b, Bb = stack_state(S0), stack_state(Z0), stack_state(buffer)
     Sref0 = torch.zeros_like(S0b)
-    y, S_T, Z_T, B = memory_recurrence(kb, qb, vb, rep(lr), rep(decay), rep(beta), rep(gate), Sref0, S0b, Z0b, Bb,
+    y, S_T, Z_T, B = memory_recurrence(kb, qb, vb, lr_b, decay_b, beta_b, gate_b, Sref0, S0b, Z0b, Bb,
                                        window=window, map_mode='off', map_degree=1, clamp_every=clamp_every,
                                        clamp_final=clamp_final)
-    # y: sum over the column blocks of each row block; states: blocks back in place
-    y = y.reshape(nbv, nbk, bh, T, _BLOCK).sum(dim=1).permute(1, 2, 0, 3).reshape(bh, T, Dv)
+    # y: sum over the column blocks of each row block (one launch); states: blocks back in place
+    if nbv == 1:   # a plain view, so that the adjoint hands the replicated gradient over without a copy
+        (y,) = _ReplicaSumFn.apply(nbk, y)
+    else:
+        yr = _ReplicaSumFn.apply(nbk, *y.reshape(nbv, nbk * bh, T, _BLOCK).unbind(0))
+        y = torch.stack(yr, dim=2).reshape(bh, T, Dv)
 
     def unblock(x):            # [(i, j, bh), ..., 64, 64] -> [bh, ..., Dv, Dk]
         if x is None:

@@ -291,6 +291,17 @@ int atlas_block_merge(int dtype, int bh, int seq_len, int d_k, int d_v, const vo
 /* Number of dS_ref partials atlas_block_merge writes per row for seq_len tokens. */
 int atlas_block_parts(int seq_len);
 
+/* The per-token scalars (lr, decay, beta, gate) shared by every block, copied along the stacked row
+ * axis, and the adjoint (replaces the expand / reshape copies and their gradient sums of the block
+ * stacking, and the sum of y over the column blocks). For each of count <= 4 arrays of n[z]
+ * elements of dtype:
+ *   ATLAS_REPLICATE:   dst[z][r n + i] = src[z][i],                 r < nrep
+ *   ATLAS_REPLICA_SUM: dst[z][i] = sum_{r < nrep} src[z][r n + i]   (fp32, in order r = 0, 1, ...)
+ * nrep <= 64. Arrays with n % 8 == 0 and 16-byte aligned pointers move in 16-byte accesses. */
+enum { ATLAS_REPLICATE = 0, ATLAS_REPLICA_SUM = 1 };
+int atlas_replicas(int op, int dtype, int count, int nrep, const int64_t* n, const void* const* src,
+                   void* const* dst, void* stream);
+
 /* ---- cell prologue (atlas_pytorch/rnn_memory.py:567-653, MultiheadRMSNorm :139-147) --------
  * Fused around the cell's projections, which stay plain GEMMs (hipBLASLt): dtype is ATLAS_DT_F32 or
  * ATLAS_DT_BF16 for every tensor argument except inv_rms and the *_part partial sums (fp32).

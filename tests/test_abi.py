@@ -347,3 +347,20 @@ def test_partials_sum_errors_before_launch(lib):
     assert f(2, 4, I32(8, 8), VP(good, good), VP(good, good), I32(1, 2), None) == 3      # bf16 or fp32 out
     assert f(2, 4, I32(8, 8), VP(good, None), VP(good, good), I32(1, 0), None) == 4
     assert f(2, 4, I32(8, 8), VP(good, good), VP(None, good), I32(1, 0), None) == 4
+
+
+def test_replicas_errors_before_launch(lib):
+    good, odd = 0x10000, 0x10001
+    I64, VP = ctypes.c_int64 * 2, ctypes.c_void_p * 2
+    f = lib.atlas_replicas
+    assert f(2, 1, 2, 2, I64(8, 8), VP(good, good), VP(good, good), None) == 9        # op
+    assert f(0, 2, 2, 2, I64(8, 8), VP(good, good), VP(good, good), None) == 3                      # dtype
+    assert f(0, 1, 0, 2, I64(8, 8), VP(good, good), VP(good, good), None) == 2                      # 1-4 arrays
+    assert f(0, 1, 5, 2, I64(8, 8), VP(good, good), VP(good, good), None) == 2
+    assert f(1, 1, 2, 0, I64(8, 8), VP(good, good), VP(good, good), None) == 2                      # 1-64 replicas
+    assert f(1, 1, 2, 65, I64(8, 8), VP(good, good), VP(good, good), None) == 2
+    assert f(0, 1, 2, 2, I64(8, -1), VP(good, good), VP(good, good), None) == 2
+    assert f(0, 1, 2, 2, I64(8, 8), VP(good, None), VP(good, good), None) == 4
+    assert f(0, 1, 2, 2, None, VP(good, good), VP(good, good), None) == 4
+    assert f(0, 1, 2, 2, I64(8, 8), VP(good, odd), VP(good, good), None) == 5                     # element alignment
+    assert f(0, 1, 2, 2, I64(0, 0), VP(None, None), VP(None, None), None) == 0                    # nothing to do
