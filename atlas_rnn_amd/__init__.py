@@ -13,6 +13,7 @@ from .functional import (  # noqa: F401
     AtlasOmegaFunction,
     atlas_omega_forward,
     check_cuda_availability,
+    get_cuda_status,
     assoc_scan,
     AssocScan,
     window_sum,
@@ -37,6 +38,7 @@ __all__ = [
     "AtlasOmegaFunction",
     "atlas_omega_forward",
     "check_cuda_availability",
+    "get_cuda_status",
     "assoc_scan",
     "AssocScan",
     "window_sum",

@@ -18,25 +18,28 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <map>
 #include <mutex>
-#include <set>
-#include <tuple>
+#include <utility>
 
 namespace atlas {
 
-// hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per kernel, device and size: the attribute
-// stays set, and the runtime call otherwise costs host time on every launch.
+// hipFuncSetAttribute(MaxDynamicSharedMemorySize) per kernel and device only when a launch needs
+// more than the largest value set so far: the attribute is a maximum, so it is raised and never
+// lowered (a launch with fewer bytes after one with more keeps working), and the runtime call does
+// not cost host time on every launch.
 inline hipError_t set_dyn_smem(const void* fn, size_t bytes) {
   static std::mutex mu;
-  static std::set<std::tuple<const void*, int, size_t>> done;
+  static std::map<std::pair<const void*, int>, size_t> raised;
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return err;
-  const auto key = std::make_tuple(fn, dev, bytes);
+  const auto key = std::make_pair(fn, dev);
   std::lock_guard<std::mutex> lock(mu);
-  if (done.count(key)) return hipSuccess;
+  const auto it = raised.find(key);
+  if (it != raised.end() && it->second >= bytes) return hipSuccess;
   err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-  if (err == hipSuccess) done.insert(key);
+  if (err == hipSuccess) raised[key] = bytes;
   return err;
 }
 

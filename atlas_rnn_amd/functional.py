@@ -243,20 +243,13 @@ def _tmap_check(x: Tensor, proj: Tensor, degree: int) -> None:
         raise ValueError(f"tensor_feature_map: degree {degree} (1 .. 16)")
 
 
-_SYM_CACHE: dict = {}
-
-
-def _symmetrized(proj: Tensor, d: int, dtype) -> tuple[Tensor, Tensor]:
-    """The symmetrised table of proj [d + d*d, m] in both layouts (atlas_tensor_map_symmetrize: one
-    launch in place of a transposition; the forward and the backward skip the products over its
-    zero lower triangle). proj is a constant (a registered buffer in the reference), so the tables
-    are kept per (storage, version, dtype) and a map over k and q, or the next step, reuses them;
-    an in-place change of proj bumps its version and forms them again. The entry holds proj itself,
-    so that its storage cannot be freed and reused by another tensor while the entry exists."""
-    key = (proj.data_ptr(), proj._version, tuple(proj.shape), proj.dtype, dtype, proj.device)
-    hit = _SYM_CACHE.get(key)
-    if hit is not None and hit[0] is proj:
-        return hit[1], hit[2]
+def symmetrized_tables(proj: Tensor, d: int, dtype) -> tuple[Tensor, Tensor]:
+    """The symmetrised table of proj [d + d*d, m] in both layouts, in `dtype`
+    (atlas_tensor_map_symmetrize: one launch in place of a transposition; the forward and the
+    backward skip the products over its zero lower triangle). x x^T is symmetric, so
+    [x; vec(x x^T)] proj = [x; vec(x x^T)] P' with P'[a][b] = proj[a][b] + proj[b][a] above the
+    diagonal, proj[a][a] on it and zeros below. Nothing is cached here: the owner of proj keeps the
+    tables (PolynomialFeatureMap does, per dtype and device) and passes them to tensor_feature_map."""
     lib = _lib.load()
     dev = proj.device
     m = proj.shape[1]
@@ -265,9 +258,6 @@ def _symmetrized(proj: Tensor, d: int, dtype) -> tuple[Tensor, Tensor]:
     pst = torch.empty(m, p.shape[0], device=dev, dtype=p.dtype)
     _lib.check(lib.atlas_tensor_map_symmetrize(_dt_code(p), d, m, _ptr(p), _ptr(ps), _ptr(pst), _stream(dev)),
                "atlas_tensor_map_symmetrize")
-    if len(_SYM_CACHE) >= 8:
-        _SYM_CACHE.clear()
-    _SYM_CACHE[key] = (proj, ps, pst)
     return ps, pst
 
 
@@ -277,12 +267,12 @@ class _TensorMapFn(torch.autograd.Function):
     P is a constant (a registered buffer in the reference, so it has no gradient)."""
 
     @staticmethod
-    def forward(ctx, x, proj, degree):
+    def forward(ctx, x, proj, degree, tables):
         dev = _require_gpu(x, proj)
         lib = _lib.load()
         lead, d, m = x.shape[:-1], x.shape[-1], proj.shape[-1]
         x2 = _aligned(x.reshape(-1, d))
-        ps, pst = _symmetrized(proj, d, x.dtype)
+        ps, pst = tables if tables is not None else symmetrized_tables(proj, d, x.dtype)
         n = x2.shape[0]
         out = torch.empty(n, m, device=dev, dtype=x.dtype)
         pre = torch.empty(n, m, device=dev, dtype=x.dtype) if degree > 1 else None
@@ -305,17 +295,30 @@ class _TensorMapFn(torch.autograd.Function):
         dx = torch.empty_like(x2)
         _lib.check(lib.atlas_tensor_map_bwd_sym(_dt_code(x2), n, d, m, ctx.degree, _ptr(x2), _ptr(p), _ptr(pre),
                                                 _ptr(g), _ptr(dx), _stream(dev)), "atlas_tensor_map_bwd_sym")
-        return dx.reshape(*ctx.lead, d), None, None
+        return dx.reshape(*ctx.lead, d), None, None, None
 
 
-def tensor_feature_map(x: Tensor, proj: Tensor, degree: int = 1) -> Tensor:
+def _tables_ok(tables, proj: Tensor, dtype) -> bool:
+    ps, pst = tables
+    m = proj.shape[-1]
+    return (ps.dtype == dtype and pst.dtype == dtype and ps.device == proj.device and pst.device == proj.device
+            and tuple(ps.shape) == tuple(proj.shape) and tuple(pst.shape) == (m, proj.shape[0])
+            and ps.is_contiguous() and pst.is_contiguous())
+
+
+def tensor_feature_map(x: Tensor, proj: Tensor, degree: int = 1,
+                       tables: tuple[Tensor, Tensor] | None = None) -> Tensor:
     """[x; vec(x x^T)] @ proj (rnn_memory.py:125-130) in x's dtype, then (degree > 1) the elementwise
     polynomial sum_{i=1..degree} phi^i (BASELINE C4's composition), on the fused kernels: the
     Kronecker features are never materialised and the polynomial is applied on the fp32 accumulator.
     x: bf16 or fp32 GPU tensor [..., d], d in (16, 32, 64); proj [d + d*d, m], m a multiple of 16 up
-    to 128, constant. Anything else raises (CPU tensors included)."""
+    to 128, constant. Anything else raises (CPU tensors included).
+    tables: proj's symmetrised tables in x's dtype (`symmetrized_tables`), when the caller keeps
+    them across calls; formed by this call otherwise (one extra launch)."""
     _tmap_check(x, proj, degree)
-    return _TensorMapFn.apply(x, proj, int(degree))
+    if tables is not None and not _tables_ok(tables, proj, x.dtype):
+        raise ValueError("tensor_feature_map: tables do not match proj (shape, dtype, device) and x's dtype")
+    return _TensorMapFn.apply(x, proj, int(degree), tables)
 
 
 _BLOCK = 64    # block width of the decomposition for head sizes the kernels are not built for
@@ -380,6 +383,10 @@ def _replicas(op: int, nrep: int, xs):
     sum of the nrep replicas stacked along the first axis of x."""
     lib = _lib.load()
     xs = [x.contiguous() for x in xs]
+    if op == _REPLICA_SUM:
+        for x in xs:
+            if x.shape[0] % nrep != 0:
+                raise ValueError(f"replica sum: first axis {x.shape[0]} is not a multiple of {nrep} replicas")
     outs = [torch.empty(((nrep * x.shape[0]) if op == _REPLICATE else (x.shape[0] // nrep),) + tuple(x.shape[1:]),
                         device=x.device, dtype=x.dtype) for x in xs]
     for dt in {x.dtype for x in xs}:
@@ -735,6 +742,18 @@ def check_cuda_availability():
         return False, f"libatlas_mem.so not loaded: {exc}"
     props = torch.cuda.get_device_properties(0)
     return True, f"atlas_rnn_amd ready (GPU: {props.name}, library: {_lib.LIB_PATH})"
+
+
+def get_cuda_status() -> dict:
+    """atlas_pytorch/cuda/atlas_omega_autograd.py:16-22: the backend's load status for logging, with
+    the reference's keys. `available`: libatlas_mem.so is loaded (its ABI version checked);
+    `loaded_via`: the library's path, or "none"; `error`: why it could not be loaded ("" when
+    available). Touches no GPU (it loads the library only)."""
+    try:
+        _lib.load()
+    except Exception as exc:  # noqa: BLE001
+        return {"available": False, "loaded_via": "none", "error": str(exc)}
+    return {"available": True, "loaded_via": _lib.LIB_PATH, "error": ""}
 
 
 # ------------------------------------------------------------------------------------------

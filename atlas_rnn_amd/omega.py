@@ -16,6 +16,7 @@ feature map `apply_poly_features` (omega.py:90-118).
 from __future__ import annotations
 
 import math
+from typing import Callable
 
 import torch
 from torch import Tensor
@@ -23,7 +24,7 @@ from torch import Tensor
 from .functional import AssocScan, assoc_scan, tensor_feature_map, window_sum
 
 __all__ = ["_sliding_sum_along_n", "assoc_scan", "AssocScan", "omega_store_chain", "apply_poly_features",
-           "OmegaPolyFeatures", "OMEGA_GATE_OFF"]
+           "OmegaPolyFeatures", "OMEGA_GATE_OFF", "newtonschulz5"]
 
 OMEGA_GATE_OFF = 1e-3   # every gate below this (over the whole batch): the chunk's updates are zero (omega.py:311)
 
@@ -39,10 +40,43 @@ def _bcast(g: Tensor, like: Tensor) -> Tensor:
     return g
 
 
+def newtonschulz5(t: Tensor, steps: int = 5, eps: float = 1e-7,
+                  coefs: tuple[float, float, float] = (3.4445, -4.7750, 2.0315)) -> Tensor:
+    """Quintic Newton-Schulz orthogonalisation of the trailing two dims (the published Muon
+    iteration that NeuralMemory's `newtonschulz5`, neural_memory.py:158-186, computes): tensors with
+    at most 3 dims are returned unchanged; otherwise each matrix X (transposed first when it has
+    more rows than columns) is scaled to unit Frobenius norm (at least eps) and iterated
+    `steps` times as A = X X^T, X <- a X + (b A + c A A) X. Runs in fp32 on torch's matrix
+    products (both operands contiguous) and returns t's dtype. A default for the orthogonaliser
+    arguments of `omega_store_chain`."""
+    if t.ndim <= 3:
+        return t
+    dt = t.dtype
+    x = t.float()
+    transpose = x.shape[-2] > x.shape[-1]
+    if transpose:
+        x = x.transpose(-1, -2)
+    lead = x.shape[:-2]
+    x = x.reshape(-1, *x.shape[-2:]).contiguous()
+    x = x / x.norm(dim=(-1, -2), keepdim=True).clamp(min=eps)
+    a, b, c = coefs
+    for _ in range(steps):
+        A = torch.matmul(x, x.transpose(-1, -2).contiguous())
+        B = b * A + c * torch.matmul(A, A)
+        x = a * x + torch.matmul(B, x)
+    x = x.reshape(*lead, *x.shape[-2:])
+    if transpose:
+        x = x.transpose(-1, -2)
+    return x.contiguous().to(dt)
+
+
 def omega_store_chain(surprise: Tensor, decay_factor: Tensor, last_update: Tensor, *,
                       adaptive_momentum: Tensor | None = None, last_momentum: Tensor | None = None,
                       combine_momentums: Tensor | None = None, omega_gate: Tensor | None = None,
-                      omega_window: int = 1, omega_buf: Tensor | None = None):
+                      omega_window: int = 1, omega_buf: Tensor | None = None,
+                      spectral_norm: Callable[[Tensor], Tensor] | None = None,
+                      muon: Callable[[Tensor], Tensor] | None = None,
+                      reference_shapes: bool = False):
     """The loop body of omega.py:254-322 for one parameter, on ROCm tensors.
 
     surprise [BH, n, *p] (the negated per-chunk gradients); decay_factor [BH, n] or [BH, n, 1];
@@ -57,6 +91,13 @@ def omega_store_chain(surprise: Tensor, decay_factor: Tensor, last_update: Tenso
     When every gate of the batch is below 1e-3 the updates are zero (omega.py:311-313), chosen on
     the device (no host synchronisation); the result keeps the scanned branch's n + 1 steps (the
     reference's zero branch has n) and next_last_update is zero as in the reference.
+    reference_shapes=True takes the reference's choice on the host instead (one synchronisation)
+    and returns its n zero steps in that branch.
+
+    The two Newton-Schulz points of the reference are caller-supplied orthogonalisers (for
+    example `newtonschulz5`): spectral_norm (the memory's `spectral_norm_surprises`) is applied to
+    the windowed update before the scan (omega.py:304-305); muon (`use_muon_optimizer`) to the
+    scanned result (omega.py:317-318), before next_last_update is taken from it.
     """
     if surprise.dim() < 2:
         raise ValueError(f"surprise must be [BH, n, ...], got {tuple(surprise.shape)}")
@@ -99,8 +140,15 @@ def omega_store_chain(surprise: Tensor, decay_factor: Tensor, last_update: Tenso
         next_buf = ext[:, -(e - 1):]
     else:
         update = gated
+    if spectral_norm is not None:                                      # omega.py:304-305
+        update = spectral_norm(update)
+    if reference_shapes and gate is not None and bool(torch.all(gate.amax(dim=1) < OMEGA_GATE_OFF)):
+        zero = torch.zeros_like(update)                                # omega.py:311-313: n zero steps
+        return zero, zero[:, -1], next_lm, next_buf
     scanned = assoc_scan(1.0 - decay_factor.reshape(BH, n), update, prev=last_update, remove_prev=False)   # :315
-    if gate is not None:                                               # omega.py:311-313, on the device
+    if muon is not None:                                               # omega.py:317-318
+        scanned = muon(scanned)
+    if gate is not None and not reference_shapes:                      # omega.py:311-313, on the device
         off = torch.all(gate.amax(dim=1) < OMEGA_GATE_OFF)
         scanned = torch.where(off, torch.zeros_like(scanned), scanned)
     return scanned, scanned[:, -1], next_lm, next_buf

@@ -27,6 +27,7 @@ from __future__ import annotations
 
 import math
 import warnings
+import weakref
 from functools import partial
 from typing import NamedTuple
 
@@ -38,6 +39,7 @@ from torch.nn import Conv1d, Linear, Module, Parameter
 
 from .functional import (AssocScan, AtlasOmegaFunction, cell_prologue, check_cuda_availability, linear,
                          memory_recurrence, tensor_feature_map, window_sum)
+from .functional import symmetrized_tables as functional_symmetrized_tables
 
 
 def exists(v):
@@ -83,9 +85,50 @@ class PolynomialFeatureMap(Module):
         self.dim = dim
         self.degree = degree
         self.mode = mode
+        # symmetrised tables of proj for the fused map, per (dtype, device):
+        # (ps, pst, weak reference to proj, proj version, event recorded after forming them, stream)
+        self._tables: dict = {}
         if mode == 'tensor':
             feat_dim = dim + dim * dim
             self.register_buffer('proj', torch.randn(feat_dim, dim) / math.sqrt(feat_dim))
+
+    def refresh_tables(self) -> None:
+        """Drops the cached tables of proj. Moves (`.to`, `.cuda`, ...), `load_state_dict` and
+        in-place operations that bump proj's version are seen by the cache itself; a write that
+        bypasses the version counter (through `proj.data`) must be followed by this call."""
+        self._tables.clear()
+
+    def _apply(self, fn, *args, **kwargs):
+        self._tables.clear()
+        return super()._apply(fn, *args, **kwargs)
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        self._tables.clear()
+        return super()._load_from_state_dict(*args, **kwargs)
+
+    def _tensor_tables(self, x: Tensor):
+        """proj's symmetrised tables in x's dtype, formed once per (dtype, device, proj version) and
+        reused by the k and q maps and by later steps. Under HIP graph capture they are formed
+        inside the graph on every call (the graph then owns them). Used on another stream than the
+        one that formed them, the current stream waits for them and keeps them alive."""
+        proj = self.proj
+        if torch.cuda.is_current_stream_capturing():
+            return functional_symmetrized_tables(proj, self.dim, x.dtype)
+        key = (x.dtype, x.device)
+        hit = self._tables.get(key)
+        cur = torch.cuda.current_stream(x.device)
+        if hit is not None and hit[2]() is proj and hit[3] == proj._version:
+            ps, pst, _, _, ev, stream = hit
+            if stream != cur:
+                cur.wait_event(ev)
+                ps.record_stream(cur)
+                pst.record_stream(cur)
+            return ps, pst
+        ps, pst = functional_symmetrized_tables(proj, self.dim, x.dtype)
+        ev = torch.cuda.Event()
+        ev.record(cur)
+        self._tables[key] = (ps, pst, weakref.ref(proj), proj._version, ev, cur)
+        return ps, pst
 
     @property
     def fused_elementwise(self) -> bool:
@@ -102,8 +145,10 @@ class PolynomialFeatureMap(Module):
                 power = power * x
                 out = out + power
             return out
-        if self.mode == 'tensor':   # fused kernels for bf16 GPU inputs (functional.tensor_feature_map)
-            return tensor_feature_map(x, self.proj.to(x.device, x.dtype))
+        if self.mode == 'tensor':   # fused kernels (functional.tensor_feature_map), proj cast to x's dtype
+            if not x.is_cuda or self.proj.device != x.device:   # the reference moves proj to x's device
+                return tensor_feature_map(x, self.proj.to(x.device))    # (raises for CPU tensors)
+            return tensor_feature_map(x, self.proj, tables=self._tensor_tables(x))
         return x
 
 

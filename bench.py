@@ -836,8 +836,41 @@ def bench_plan(name, steps, warmup, cpu=True, cpu_sample_t=256, with_buffer=Fals
         "kernels": {kk: {"avg_us": round(v["avg_us"], 2), "launches": v["launches"]} for kk, v in kernels.items()},
         "profiled_ms_per_step": round(1e3 * (tp1 - tp0) / steps, 4),
     }
+    if name == "c3" and clamp_every is None and buf is None:
+        out["scan_chunk_len_64"] = time_clamp_variant(x, cfg, steps, warmup, 64)
     out["cpu_baseline"] = cpu_baseline_record(x_cpu, cfg, cpu_sample_t) if cpu else None
     print(json.dumps(out), flush=True)
+
+
+def time_clamp_variant(x, cfg, steps, warmup, clamp_every):
+    """The same fwd+bwd step as the drop-in cell runs it for scan_chunk_len = clamp_every (S clamped
+    to +-100 at every clamp_every-token boundary, rnn_memory.py:584-601): the library's dual plan
+    (the segment-parallel sequence with the clamp points checked on the device, the exact sequence
+    launched behind it and skipped unless a clamp fires). Same inputs, K steps timed after W warmup."""
+    import torch
+    from atlas_rnn_amd.functional import RecurrencePlan
+    dev = x["k"].device
+    bh, t, d, e = cfg["B"] * cfg["H"], cfg["T"], cfg["d"], cfg["e"]
+    plan = RecurrencePlan(bh, t, d, window=e, momentum=True, gate_mode=cfg["gate"], dtype=torch.bfloat16, device=dev,
+                          has_buffer=False, clamp_every=clamp_every)
+
+    def step():
+        plan.forward(x["k"], x["q"], x["v"], x["lr"], x["decay"], x["beta"], x["gate"], x["S_ref"], x["S0"], x["Z0"],
+                     None)
+        plan.backward(x["dy"])
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    return {"clamp_every": clamp_every, "ms_per_step": round(1e3 * elapsed / steps, 4),
+            "value": round(cfg["B"] * t * steps / elapsed, 1), "unit": "tokens/s",
+            "note": "the same step with S clamped every 64 tokens (OmegaRNNMemoryCell(scan_chunk_len=64)); "
+                    "value stays on the unclamped plan"}
 
 
 def main():

@@ -23,7 +23,13 @@ the gate-below-1e-3 short-circuit; the window's known answers (tests/golden).
 
 The reference's short-circuit branch returns n zero steps while its scanned branch returns n + 1;
 both forms here return n + 1 zero steps (the product's shape, which needs no host sync to choose),
-with next_last_update = 0 as in the reference.
+with next_last_update = 0 as in the reference; reference_shapes=True returns the reference's n.
+
+The Newton-Schulz points (omega.py:304-305 `spectral_norm_surprises`, :317-318
+`use_muon_optimizer`) take an orthogonaliser; `newtonschulz5` restates the published quintic
+iteration NeuralMemory uses (neural_memory.py:158-186). It is pinned by its action on singular
+values (tests/test_oracle_omega.py): the iteration maps X = U diag(s) V^T to
+U diag(p^5(s / ||s||)) V^T with p(x) = a x + b x^3 + c x^5.
 """
 
 from __future__ import annotations
@@ -40,10 +46,28 @@ def _bcast(g: Tensor, like: Tensor) -> Tensor:
     return g
 
 
+def newtonschulz5(t: Tensor, steps: int = 5, eps: float = 1e-7, coefs=(3.4445, -4.7750, 2.0315)) -> Tensor:
+    """neural_memory.py:158-186: tensors of at most 3 dims unchanged; otherwise per matrix over the
+    trailing two dims (transposed when rows > cols): X / max(||X||_F, eps), then `steps` times
+    A = X X^T, B = b A + c A A, X = a X + B X."""
+    if t.ndim <= 3:
+        return t
+    transpose = t.shape[-2] > t.shape[-1]
+    x = t.transpose(-1, -2) if transpose else t
+    x = x / x.norm(dim=(-1, -2), keepdim=True).clamp(min=eps)
+    a, b, c = coefs
+    for _ in range(steps):
+        A = x @ x.transpose(-1, -2)
+        B = b * A + c * A @ A
+        x = a * x + B @ x
+    return x.transpose(-1, -2) if transpose else x
+
+
 def omega_store_chain(surprise: Tensor, decay_factor: Tensor, last_update: Tensor, *,
                       adaptive_momentum: Tensor | None = None, last_momentum: Tensor | None = None,
                       combine_momentums: Tensor | None = None, omega_gate: Tensor | None = None,
-                      omega_window: int = 1, omega_buf: Tensor | None = None):
+                      omega_window: int = 1, omega_buf: Tensor | None = None,
+                      spectral_norm=None, muon=None, reference_shapes: bool = False):
     """surprise [BH, n, *p]; decay_factor [BH, n] (or [BH, n, 1]); last_update [BH, *p];
     adaptive_momentum [O, BH, n] with last_momentum [O, BH, *p] (momentum on); combine_momentums
     [O, BH, n]; omega_gate [BH, n]; omega_buf [BH, e-1, *p]. Returns (update [BH, n+1, *p],
@@ -73,11 +97,18 @@ def omega_store_chain(surprise: Tensor, decay_factor: Tensor, last_update: Tenso
         next_buf = ext[:, -(e - 1):]
     else:
         update = gated
+    if spectral_norm is not None:                                      # :304-305
+        update = spectral_norm(update)
+    off = omega_gate is not None and bool(torch.all(omega_gate.reshape(BH, n).amax(dim=1) < 1e-3))   # :311
+    if off and reference_shapes:
+        zero = torch.zeros_like(update)
+        return zero, zero[:, -1], next_lm, next_buf
     decay = decay_factor.reshape(BH, n)
     scanned = scalar_assoc_scan_sequential(1.0 - decay, update, prev=last_update, remove_prev=False)   # :315
-    if omega_gate is not None:                                         # :311-313
-        off = torch.all(omega_gate.reshape(BH, n).amax(dim=1) < 1e-3)
-        scanned = torch.where(off, torch.zeros_like(scanned), scanned)
+    if muon is not None:                                               # :317-318
+        scanned = muon(scanned)
+    if off:                                                            # :311-313
+        scanned = torch.zeros_like(scanned)
     return scanned, scanned[:, -1], next_lm, next_buf
 
 

@@ -116,3 +116,55 @@ def test_omega_poly_features(mode, degree, dt):
     else:
         ref = poly_feature_map(x.double(), degree, 'elementwise')
     compare(f"omega_poly.{mode}", out.float().cpu(), ref, 1e-4 if dt == torch.float32 else 2e-2)
+
+
+@pytest.mark.parametrize("point", ["spectral_norm", "muon", "both"])
+def test_omega_newton_schulz_points(point):
+    """The reference's two Newton-Schulz points (omega.py:304-305, :317-318) with the library's
+    newtonschulz5 on the GPU against the oracle's fp64 restatement at the same points: every output
+    and every input gradient (fp32, rtol 1e-4 on outputs; gradients through five NS steps 1e-3)."""
+    from atlas_rnn_amd.omega import newtonschulz5
+    from oracle.omega import newtonschulz5 as ns_ref
+    _say(f"omega chain with Newton-Schulz at {point}")
+    BH, n, p, e = 4, 10, (8, 12), 3
+    x = _inputs(BH, n, p, 1, False, True, e, True, seed=91, dt=torch.float32)
+    kw_r = dict(spectral_norm=ns_ref if point in ("spectral_norm", "both") else None,
+                muon=ns_ref if point in ("muon", "both") else None)
+    kw_d = dict(spectral_norm=newtonschulz5 if point in ("spectral_norm", "both") else None,
+                muon=newtonschulz5 if point in ("muon", "both") else None)
+    xr = {k: v.to(F64).requires_grad_() for k, v in x.items()}
+    ref = oracle_chain(**xr, omega_window=e, **kw_r)
+    xd = {k: v.to("cuda").requires_grad_() for k, v in x.items()}
+    got = omega_store_chain(**xd, omega_window=e, **kw_d)
+    g = torch.Generator().manual_seed(8)
+    weights = [torch.randn(r.shape, generator=g, dtype=F64) for r in ref]
+    loss_r = sum((r * w).sum() for r, w in zip(ref, weights))
+    loss_d = sum((o.float() * w.to("cuda", torch.float32)).sum() for o, w in zip(got, weights))
+    names = sorted(x)
+    gr = torch.autograd.grad(loss_r, [xr[k] for k in names])
+    gd = torch.autograd.grad(loss_d, [xd[k] for k in names])
+    torch.cuda.synchronize()
+    for nm, o, r in zip(("update", "next_last_update", "next_last_momentum", "next_buf"), got, ref):
+        compare(f"ns_{point}.{nm}", o.detach().float().cpu(), r.detach(), 1e-4)
+    for k, a, b in zip(names, gd, gr):
+        compare(f"ns_{point}.d{k}", a.float().cpu(), b, 1e-3)
+
+
+def test_omega_reference_shapes_zero_branch():
+    """reference_shapes=True: with every gate below 1e-3 the reference's n zero steps (a host
+    decision, as omega.py:311-313 makes it); otherwise the scanned n + 1 steps as by default."""
+    _say("omega chain with the reference's zero-branch shape")
+    BH, n, p = 3, 5, (4, 4)
+    g = torch.Generator().manual_seed(9)
+    s = torch.randn(BH, n, *p, generator=g).cuda()
+    dec = torch.full((BH, n), 0.1).cuda()
+    last = torch.randn(BH, *p, generator=g).cuda()
+    upd, nl, _, _ = omega_store_chain(s, dec, last, omega_gate=torch.full((BH, n), 5e-4).cuda(), omega_window=2,
+                                      reference_shapes=True)
+    assert upd.shape == (BH, n, *p) and torch.count_nonzero(upd).item() == 0
+    assert torch.count_nonzero(nl).item() == 0
+    gate = torch.full((BH, n), 0.5).cuda()
+    a = omega_store_chain(s, dec, last, omega_gate=gate, omega_window=2, reference_shapes=True)
+    b = omega_store_chain(s, dec, last, omega_gate=gate, omega_window=2)
+    assert a[0].shape == (BH, n + 1, *p)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])

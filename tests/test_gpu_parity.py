@@ -83,6 +83,12 @@ CASES = [
          states=0.1, dtype=BF16, seed=29),
     Case("fp32_dk128_dv128_clamp", BH=2, T=96, d=128, e=2, gate='token', momentum=True, states=0.2,
          clamp_every=32, seed=30),
+    # d_k = 64 < d_v: one column block, two and three row blocks (y summed over nothing, the
+    # per-token scalars replicated over the row blocks)
+    Case("bf16_dk64_dv128_block", BH=3, T=200, d=64, dv=128, e=4, gate='lag', momentum=True, states=0.1,
+         dtype=BF16, seed=49),
+    Case("fp32_dk64_dv192_block_buffer", BH=2, T=150, d=64, dv=192, e=3, gate='token', momentum=True, buffer=True,
+         states=0.1, seed=50),
     # scan_chunk_len clamps on chunk ends run segment-parallel with the clamp points checked on the
     # device; the exact one-segment-per-row sequence runs only when a clamp would change S
     Case("bf16_walk_clamp64_quiet", BH=4, T=600, d=64, e=4, gate='lag', momentum=True, states=0.1, clamp_every=64,

@@ -147,3 +147,34 @@ def test_module_aliases():
     assert affine_scan.affine_associative_scan is am.affine_associative_scan
     assert omega.AssocScan is am.AssocScan
     assert rm._sliding_sum_along_time is not None and math.isfinite(1.0)
+
+
+def test_get_cuda_status_keys():
+    """atlas_omega_autograd.py:16-22: get_cuda_status() reports available / loaded_via / error; here
+    the backend is libatlas_mem.so (built in-tree), loaded without touching a GPU."""
+    st = am.get_cuda_status()
+    assert set(st) == {"available", "loaded_via", "error"}
+    assert isinstance(st["available"], bool) and isinstance(st["loaded_via"], str) and isinstance(st["error"], str)
+    if st["available"]:
+        assert st["loaded_via"].endswith("libatlas_mem.so") and st["error"] == ""
+    else:
+        assert st["loaded_via"] == "none" and st["error"]
+    from atlas_rnn_amd import functional
+    assert functional.get_cuda_status is am.get_cuda_status
+
+
+def test_tensor_map_tables_are_kept_by_the_module_and_dropped_on_moves():
+    """PolynomialFeatureMap keeps proj's symmetrised tables itself (not in a process-wide cache):
+    moves and load_state_dict drop them, refresh_tables() too."""
+    fm = am.PolynomialFeatureMap(16, 2, 'tensor')
+    fm._tables[("sentinel",)] = object()
+    fm.double()
+    assert not fm._tables
+    fm._tables[("sentinel",)] = object()
+    fm.load_state_dict(fm.state_dict())
+    assert not fm._tables
+    fm._tables[("sentinel",)] = object()
+    fm.refresh_tables()
+    assert not fm._tables
+    from atlas_rnn_amd import functional
+    assert not hasattr(functional, "_SYM_CACHE")

@@ -128,3 +128,42 @@ def test_gate_short_circuit():
     x["omega_gate"][1, 2] = 2e-3                                # one gate above the threshold: no short-circuit
     upd, _, _, _ = omega_store_chain(**x)
     assert torch.count_nonzero(upd) > 0
+
+
+def test_newtonschulz5_acts_on_singular_values():
+    """The quintic iteration maps X = U diag(s) V^T to U diag(p^5(s / ||s||)) V^T with
+    p(x) = a x + b x^3 + c x^5 (the SVD closed form of the published iteration), for wide and tall
+    matrices (tall ones are transposed and back); at most 3 dims pass through unchanged."""
+    from oracle.omega import newtonschulz5
+    g = torch.Generator().manual_seed(77)
+    a, b, c = 3.4445, -4.7750, 2.0315
+    for shape in [(2, 3, 6, 9), (2, 3, 9, 6), (1, 1, 5, 5)]:
+        x = torch.randn(*shape, generator=g, dtype=F64)
+        U, s, Vh = torch.linalg.svd(x, full_matrices=False)
+        sn = s / s.norm(dim=-1, keepdim=True)
+        for _ in range(5):
+            sn = a * sn + b * sn ** 3 + c * sn ** 5
+        want = U @ torch.diag_embed(sn) @ Vh
+        torch.testing.assert_close(newtonschulz5(x), want, rtol=1e-9, atol=1e-9)
+    y = torch.randn(3, 4, 5, generator=g, dtype=F64)
+    assert newtonschulz5(y) is y
+
+
+def test_newton_schulz_points_and_reference_shapes():
+    """spectral_norm acts on the windowed update before the scan, muon on the scanned result;
+    with every gate below 1e-3 reference_shapes gives the reference's n zero steps."""
+    from oracle.omega import newtonschulz5
+    x = _inputs(p=(4, 6))
+    base = omega_store_chain(**x)
+    sn = omega_store_chain(**x, spectral_norm=newtonschulz5)
+    mu = omega_store_chain(**x, muon=newtonschulz5)
+    # muon: the scanned result orthogonalised (next_last_update taken after it)
+    torch.testing.assert_close(mu[0], newtonschulz5(base[0]))
+    torch.testing.assert_close(mu[1], newtonschulz5(base[0])[:, -1])
+    # spectral_norm: the scan over orthogonalised updates, differs from the plain chain
+    assert not torch.allclose(sn[0], base[0])
+    xo = dict(x, omega_gate=torch.full_like(x["omega_gate"], 5e-4))
+    z = omega_store_chain(**xo, reference_shapes=True)
+    assert z[0].shape[1] == x["surprise"].shape[1] and not z[0].any() and not z[1].any()
+    z2 = omega_store_chain(**xo)
+    assert z2[0].shape[1] == x["surprise"].shape[1] + 1 and not z2[0].any()
