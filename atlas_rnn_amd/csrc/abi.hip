@@ -28,6 +28,10 @@ hipError_t launch_buf_state(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom
 hipError_t launch_buf_y(const Geom& g, const FwdPtrs<bf16>& a, const bf16* wsh, hipStream_t stream);
 hipError_t launch_walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
                            float* rw, float* final_raw, float* coef, bf16* wsh, hipStream_t stream);
+bool chunk_path_supported(const Geom& g);
+SegGeom chunk_seg(const Geom& g);
+hipError_t launch_chunk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
+                            float* final_raw, hipStream_t stream);
 
 // Diagnostic tile product C = A B^T (16 x 64 inputs) through the same fragment helpers.
 template <typename T>
@@ -131,7 +135,14 @@ struct Plan {
   // the clamp points) runs first and the exact one-segment-per-row sequence (make_plan(p, true))
   // runs behind it only when some clamp point's |S| exceeds 100 (the clamp is the identity otherwise)
   bool dual;
+  // the chunk-parallel path (chunk_fwd.hip, chunk_bwd.hip): bf16, d = 64, window <= 17, no clamp at
+  // scan_chunk_len boundaries, no carried buffer; sg is then its segment layout (chunk_seg)
+  bool chunk;
 };
+
+#ifndef ATLAS_CHUNK_PATH
+#define ATLAS_CHUNK_PATH 0
+#endif
 
 // Segments per head-batch row: enough (segment, bh) workgroups for one per CU (the walks hold a
 // CU's LDS, so a second round of workgroups would only queue behind the first); a single segment
@@ -204,7 +215,8 @@ Plan make_plan(const atlas_mem_problem* p, bool serial_clamp = false) {
   // clamp points on forward-chunk ends: segment-parallel with the clamp points checked (dual)
   pl.dual = !serial_clamp && p->clamp_every > 0 && p->clamp_every % CH == 0 && p->clamp_every < p->seq_len;
   if (pl.dual) g.clamp_every = 0;
-  pl.sg = make_seg(g);
+  pl.chunk = ATLAS_CHUNK_PATH && p->dtype == ATLAS_DT_BF16 && !pl.dual && chunk_path_supported(g);
+  pl.sg = pl.chunk ? chunk_seg(g) : make_seg(g);
   // backward: same segments, chunks of Lb
   Geom& gb = pl.gb;
   gb = g;
@@ -246,13 +258,15 @@ SavedLayout saved_layout(const Plan& pl) {
   L.seg = off; off += align256((size_t)g.BH * pl.sg.nseg * 2 * st);
   L.agg = off; off += align256((size_t)g.BH * pl.sg.nseg * pl.sg.agg_stride * sizeof(float));
   L.final_raw = off; off += align256((size_t)g.BH * st);
-  L.rw = off; off += align256((size_t)g.BH * g.ncb * 2 * st);
+  // the chunk-parallel path keeps nothing per chunk: the regions below are empty for it
+  const bool walk = !pl.chunk;
+  L.rw = off; off += align256(walk ? (size_t)g.BH * g.ncb * 2 * st : 0);
   // forward scratch: per-chunk coefficient records and Ws[s, t-1] blocks
-  L.coef = off; off += align256((size_t)g.BH * g.nc * coef_rec_floats(pl.CH) * sizeof(float));
-  L.wsh = off; off += align256((size_t)g.BH * g.nc * pl.CH * (pl.CH + kHaloPad) * pl.esize);
+  L.coef = off; off += align256(walk ? (size_t)g.BH * g.nc * coef_rec_floats(pl.CH) * sizeof(float) : 0);
+  L.wsh = off; off += align256(walk ? (size_t)g.BH * g.nc * pl.CH * (pl.CH + kHaloPad) * pl.esize : 0);
   // the backward's chunk records (input-only: formed in the forward's coefficient launch)
-  L.bcoef = off; off += align256((size_t)g.BH * pl.gb.nc * coef_rec_floats(pl.CHB) * sizeof(float));
-  L.bwsh = off; off += align256((size_t)g.BH * pl.gb.nc * pl.CHB * (pl.CHB + kHaloPad) * pl.esize);
+  L.bcoef = off; off += align256(walk ? (size_t)g.BH * pl.gb.nc * coef_rec_floats(pl.CHB) * sizeof(float) : 0);
+  L.bwsh = off; off += align256(walk ? (size_t)g.BH * pl.gb.nc * pl.CHB * (pl.CHB + kHaloPad) * pl.esize : 0);
   L.bufc = off; off += align256(walk_with_buffer(pl) ? (size_t)g.BH * bufw::kCorrFloats * sizeof(float) : 0);
   L.total = off;
   return L;
@@ -332,6 +346,11 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
   float* coef = reinterpret_cast<float*>(sv + SL.coef);
   T* wsh = reinterpret_cast<T*>(sv + SL.wsh);
   const Geom& g = pl.g;
+  if constexpr (sizeof(T) == 2) {
+    if (pl.chunk)
+      return launch_chunk_fwd(g, a, pl.sg, agg, seg_states, final_raw, s) == hipSuccess ? ATLAS_MEM_OK
+                                                                                        : ATLAS_MEM_ERR_LAUNCH;
+  }
   // chunk coefficient records of the forward and of the backward (one launch, inputs only)
   constexpr int CHF = sizeof(T) == 2 ? 64 : 32, CHB = sizeof(T) == 2 ? 32 : 16;
   hipError_t err = launch_chunk_coef_pair<T, CHF, CHB>(g, pl.gb, a.decay, a.lr, a.beta, a.gate, coef, wsh,
@@ -365,6 +384,7 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
 template <typename T>
 int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, void* ws, hipStream_t s) {
   const Geom& gb = pl.gb;
+  if (pl.chunk) return ATLAS_MEM_ERR_UNSUPPORTED;
   const BwdLayout L = bwd_layout(pl);
   const SavedLayout SL = saved_layout(pl);
   unsigned char* w = static_cast<unsigned char*>(ws);

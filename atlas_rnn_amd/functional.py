@@ -267,7 +267,7 @@ class _TensorMapFn(torch.autograd.Function):
     P is a constant (a registered buffer in the reference, so it has no gradient)."""
 
     @staticmethod
-    def forward(ctx, x, proj, degree, tables):
+    def forward(ctx, x, proj, degree, tables=None):
         dev = _require_gpu(x, proj)
         lib = _lib.load()
         lead, d, m = x.shape[:-1], x.shape[-1], proj.shape[-1]

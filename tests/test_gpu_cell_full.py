@@ -10,8 +10,11 @@ state of its 8 heads); then every parameter gradient is row 0's, and the referen
 Reference: the cell's own layers in fp64 on the same (bf16-valued) parameters, composed as
 rnn_memory.py:556-730 with the fp64 oracle recurrence (in 256-token blocks carrying the state). The
 bf16 tensors the GPU materialises between layers (the convolved inputs, the projections, the
-normalised q / k, the gates, y, the output) are rounded to bf16 in the reference's forward with an
-identity backward (as the GPU's casts are), so the comparison measures the kernels' arithmetic.
+normalised q / k, the gate heads' products and sigmoids, y, the output) are rounded to bf16 in the
+reference, as are the gradients flowing back through them (bf16 tensors have bf16 gradients), and a
+gate sigmoid's backward uses its stored bf16 output as torch's bf16 sigmoid does (s (1 - s) with s
+near 1 is where bf16 storage matters most), so the comparison measures the kernels' arithmetic
+rather than the storage format.
 Tolerance: 2e-2 (bf16 inputs), normwise and elementwise with an atol floor (`_cases.compare`).
 """
 
@@ -40,9 +43,37 @@ def _say(msg):
     sys.stdout.flush()
 
 
+class _Bf16Point(torch.autograd.Function):
+    """A tensor the GPU holds in bf16: its value is rounded to bf16, and so is the gradient that
+    flows back through it (autograd keeps a bf16 tensor's gradient in bf16)."""
+
+    @staticmethod
+    def forward(ctx, t):
+        return t.to(BF16).to(t.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(BF16).to(g.dtype)
+
+
 def _r(t):
-    """bf16 rounding in the forward, identity in the backward."""
-    return t + (t.to(BF16).to(t.dtype) - t).detach()
+    return _Bf16Point.apply(t)
+
+
+class _GateSigmoid(torch.autograd.Function):
+    """A gate head's sigmoid as the GPU (and torch's own bf16 sigmoid) computes it: the output is
+    stored in bf16 and the backward forms dz = dg s (1 - s) from that stored s, in bf16."""
+
+    @staticmethod
+    def forward(ctx, z):
+        s = torch.sigmoid(z).to(BF16).to(z.dtype)
+        ctx.save_for_backward(s)
+        return s
+
+    @staticmethod
+    def backward(ctx, g):
+        (s,) = ctx.saved_tensors
+        return (g.to(BF16).to(g.dtype) * s * (1 - s)).to(BF16).to(g.dtype)
 
 
 def _reference_row(cell, x, state):
@@ -58,7 +89,9 @@ def _reference_row(cell, x, state):
     q, k = _r(cell.q_norm(q)), _r(cell.k_norm(k))
     flat = lambda t: rearrange(t, 'b h n d -> (b h) n d')
     k, q, v = flat(k), flat(q), flat(v)
-    heads = lambda lin: rearrange(_r(lin(x_act)), 'b n h -> (b h) n')
+    # a gate head: the product (bf16), its bias, the sigmoid stored in bf16
+    heads = lambda lin: rearrange(_GateSigmoid.apply(_r(x_act @ lin[0].weight.t()) + lin[0].bias),
+                                  'b n h -> (b h) n')
     lr, decay, beta, gate = (heads(cell.to_lr), heads(cell.to_decay), heads(cell.to_momentum),
                              heads(cell.to_omega_gate))
     S_ref, S, Z, B = state.S, state.S, state.Z, state.omega_buffer
