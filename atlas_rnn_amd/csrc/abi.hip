@@ -29,6 +29,8 @@ hipError_t launch_buf_y(const Geom& g, const FwdPtrs<bf16>& a, const bf16* wsh, 
 hipError_t launch_walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
                            float* rw, float* final_raw, float* coef, bf16* wsh, hipStream_t stream);
 bool chunk_path_supported(const Geom& g);
+bool chunk_bwd_supported(const Geom& g, const SegGeom& sg);
+size_t chunk_bwd_xsave_bytes(const Geom& g, const SegGeom& sg);
 SegGeom chunk_seg(const Geom& g);
 hipError_t launch_chunk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
                             float* final_raw, hipStream_t stream);
@@ -138,10 +140,17 @@ struct Plan {
   // the chunk-parallel path (chunk_fwd.hip, chunk_bwd.hip): bf16, d = 64, window <= 17, no clamp at
   // scan_chunk_len boundaries, no carried buffer; sg is then its segment layout (chunk_seg)
   bool chunk;
+  // the specialised forward walk with the backward of chunk_bwd.hip (bf16, d = 64, window <= 17, no
+  // clamp, no carried buffer): the forward saves no boundary states and no backward records, and
+  // its chunks have no mid point (Lmid = 0)
+  bool cbwd;
 };
 
 #ifndef ATLAS_CHUNK_PATH
 #define ATLAS_CHUNK_PATH 0
+#endif
+#ifndef ATLAS_CHUNK_BWD
+#define ATLAS_CHUNK_BWD 1
 #endif
 
 // Segments per head-batch row: enough (segment, bh) workgroups for one per CU (the walks hold a
@@ -217,6 +226,9 @@ Plan make_plan(const atlas_mem_problem* p, bool serial_clamp = false) {
   if (pl.dual) g.clamp_every = 0;
   pl.chunk = ATLAS_CHUNK_PATH && p->dtype == ATLAS_DT_BF16 && !pl.dual && chunk_path_supported(g);
   pl.sg = pl.chunk ? chunk_seg(g) : make_seg(g);
+  pl.cbwd = ATLAS_CHUNK_BWD && p->dtype == ATLAS_DT_BF16 && !pl.dual && !pl.chunk && walk_fwd_supported(g) &&
+            chunk_bwd_supported(g, pl.sg);
+  if (pl.cbwd) g.Lmid = 0;
   // backward: same segments, chunks of Lb
   Geom& gb = pl.gb;
   gb = g;
@@ -258,24 +270,27 @@ SavedLayout saved_layout(const Plan& pl) {
   L.seg = off; off += align256((size_t)g.BH * pl.sg.nseg * 2 * st);
   L.agg = off; off += align256((size_t)g.BH * pl.sg.nseg * pl.sg.agg_stride * sizeof(float));
   L.final_raw = off; off += align256((size_t)g.BH * st);
-  // the chunk-parallel path keeps nothing per chunk: the regions below are empty for it
+  // the chunk-parallel path keeps nothing per chunk: the regions below are empty for it; with the
+  // backward of chunk_bwd.hip only the forward's own records remain
   const bool walk = !pl.chunk;
-  L.rw = off; off += align256(walk ? (size_t)g.BH * g.ncb * 2 * st : 0);
+  const bool brec = walk && !pl.cbwd;
+  L.rw = off; off += align256(brec ? (size_t)g.BH * g.ncb * 2 * st : 0);
   // forward scratch: per-chunk coefficient records and Ws[s, t-1] blocks
   L.coef = off; off += align256(walk ? (size_t)g.BH * g.nc * coef_rec_floats(pl.CH) * sizeof(float) : 0);
   L.wsh = off; off += align256(walk ? (size_t)g.BH * g.nc * pl.CH * (pl.CH + kHaloPad) * pl.esize : 0);
   // the backward's chunk records (input-only: formed in the forward's coefficient launch)
-  L.bcoef = off; off += align256(walk ? (size_t)g.BH * pl.gb.nc * coef_rec_floats(pl.CHB) * sizeof(float) : 0);
-  L.bwsh = off; off += align256(walk ? (size_t)g.BH * pl.gb.nc * pl.CHB * (pl.CHB + kHaloPad) * pl.esize : 0);
+  L.bcoef = off; off += align256(brec ? (size_t)g.BH * pl.gb.nc * coef_rec_floats(pl.CHB) * sizeof(float) : 0);
+  L.bwsh = off; off += align256(brec ? (size_t)g.BH * pl.gb.nc * pl.CHB * (pl.CHB + kHaloPad) * pl.esize : 0);
   L.bufc = off; off += align256(walk_with_buffer(pl) ? (size_t)g.BH * bufw::kCorrFloats * sizeof(float) : 0);
   L.total = off;
   return L;
 }
 
 // backward workspace: adjoint aggregates, segment-end adjoints, dS_ref partials, boundary partials,
-// token-gate (target, lag) gradients, the scalar-gradient inputs.
+// token-gate (target, lag) gradients, the scalar-gradient inputs (or, for the backward of
+// chunk_bwd.hip, its per-chunk start states and records).
 struct BwdLayout {
-  size_t agg, segadj, dsref, tail, halo, dw, scal, badj, total;
+  size_t agg, segadj, dsref, tail, halo, dw, scal, badj, xsave, total;
 };
 
 BwdLayout bwd_layout(const Plan& pl) {
@@ -290,8 +305,9 @@ BwdLayout bwd_layout(const Plan& pl) {
   L.tail = off; off += align256((size_t)g.BH * nseg * g.H * (g.DV + g.DK) * sizeof(float));
   L.halo = off; off += align256((size_t)g.BH * nseg * g.H * (g.DV + g.DK) * sizeof(float));
   L.dw = off; off += align256(g.gate_mode == ATLAS_GATE_TOKEN ? (size_t)g.BH * g.T * g.e * sizeof(float) : 0);
-  L.scal = off; off += align256((size_t)g.BH * g.nc * scalar_block_floats(pl.CHB) * sizeof(float));
+  L.scal = off; off += align256(pl.cbwd ? 0 : (size_t)g.BH * g.nc * scalar_block_floats(pl.CHB) * sizeof(float));
   L.badj = off; off += align256(walk_with_buffer(pl) ? (size_t)g.BH * bufw::kAdjFloats * sizeof(float) : 0);
+  L.xsave = off; off += align256(pl.cbwd ? chunk_bwd_xsave_bytes(pl.g, pl.sg) : 0);
   L.total = off;
   return L;
 }
@@ -353,9 +369,10 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
   }
   // chunk coefficient records of the forward and of the backward (one launch, inputs only)
   constexpr int CHF = sizeof(T) == 2 ? 64 : 32, CHB = sizeof(T) == 2 ? 32 : 16;
-  hipError_t err = launch_chunk_coef_pair<T, CHF, CHB>(g, pl.gb, a.decay, a.lr, a.beta, a.gate, coef, wsh,
-                                                       reinterpret_cast<float*>(sv + SL.bcoef),
-                                                       reinterpret_cast<T*>(sv + SL.bwsh), s);
+  hipError_t err = launch_chunk_coef_pair<T, CHF, CHB>(
+      g, pl.gb, a.decay, a.lr, a.beta, a.gate, coef, wsh, pl.cbwd ? nullptr : reinterpret_cast<float*>(sv + SL.bcoef),
+      pl.cbwd ? nullptr : reinterpret_cast<T*>(sv + SL.bwsh), s);
+  if (pl.cbwd) rw = nullptr;
   if (err != hipSuccess) return ATLAS_MEM_ERR_LAUNCH;
   err = hipErrorInvalidValue;
   if (g.DK == 64) {
@@ -412,11 +429,12 @@ int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, voi
   p.wsh = const_cast<unsigned char*>(sv + SL.bwsh);
   p.scal = reinterpret_cast<float*>(w + L.scal);
   p.buf_adj = walk_with_buffer(pl) ? reinterpret_cast<float*>(w + L.badj) : nullptr;
+  p.xsave = pl.cbwd ? static_cast<void*>(w + L.xsave) : nullptr;
   hipError_t err = hipErrorInvalidValue;
   // the specialised walks run as a pair: the forward saved its states in their layout
   const bool walk = sizeof(T) == 2 && walk_fwd_supported(pl.g);
   // the specialised path forms its adjoint aggregates over the forward's chunks and records
-  const AggOverFwd agf{pl.g, pl.sg, reinterpret_cast<const float*>(sv + SL.coef)};
+  const AggOverFwd agf{pl.g, pl.sg, reinterpret_cast<const float*>(sv + SL.coef), pl.cbwd};
   const bool agg_fwd = walk && pl.g.Lc == 64;
   if (gb.DK == 64) {
     if constexpr (sizeof(T) == 2) err = launch_bwd_seg<T, 32, 64>(gb, a, pl.sgb, p, s, walk, agg_fwd ? &agf : nullptr);

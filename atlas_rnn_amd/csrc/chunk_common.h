@@ -49,8 +49,7 @@ __device__ __forceinline__ Tri tri_shfl_up(const Tri& x, int off) {
 // Inclusive scan over the 64 lanes of a wave. LATER_LEFT: lane j gets X_j X_{j-1} ... X_0 (the
 // product of a forward recurrence); otherwise X_0 X_1 ... X_j.
 template <bool LATER_LEFT>
-__device__ __forceinline__ Tri wave_scan(Tri v) {
-  const int lane = lane_id();
+__device__ __forceinline__ Tri wave_scan(Tri v, int lane) {
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
     const Tri u = tri_shfl_up(v, off);
@@ -60,8 +59,7 @@ __device__ __forceinline__ Tri wave_scan(Tri v) {
 }
 
 // Inclusive sum over the 64 lanes of a wave.
-__device__ __forceinline__ float wave_prefix_sum(float v) {
-  const int lane = lane_id();
+__device__ __forceinline__ float wave_prefix_sum(float v, int lane) {
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
     const float u = __shfl_up(v, off, 64);
@@ -128,7 +126,7 @@ __device__ __forceinline__ void range_coefs(const Geom& g, const TokScal& sc, in
   const bool in = j < n;
   const Tri x{sc.al, -sc.et * sc.be, sc.be};
   // X_{n-1} X_{n-2} ... : earlier j on the left
-  Tri v = wave_scan<false>(x);
+  Tri v = wave_scan<false>(x, lane);
   if (lane == 63) rs.tot[w] = v;
   __syncthreads();
   Tri pre = tri_id();
@@ -297,6 +295,53 @@ __device__ __forceinline__ void state_blocks(const SrcBlocks<NB>& sb, int nsrc, 
         for (int r = 0; r < 4; ++r) { Sacc[kt][r] += sa[kt][r]; Zacc[kt][r] += za[kt][r]; }
     }
   }
+}
+
+// Operand generators (row = lane & 15 of the tile, k slots natural: k = 32 q + 8 gq + e; lane passed in).
+// B_eta[r][u] = -eta_u B(r -> u) for u >= r (r, u chunk-local targets).
+template <bool MOM>
+__device__ __forceinline__ bf16x8 gen_beta_eta(const float* lb, const float* eta, int r, int q, int lane) {
+  const int gq = lane >> 4;
+  const float lbr = MOM ? lb[r] : 0.f;
+  bf16x8 f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int u = 32 * q + 8 * gq + e;
+    float v = 0.f;
+    if (MOM) v = u >= r ? -eta[u] * __builtin_amdgcn_exp2f(lb[u] - lbr) : 0.f;
+    else v = u == r ? -eta[u] : 0.f;
+    f[e] = static_cast<bf16>(v);
+  }
+  return f;
+}
+// A'[t][u] = A(u -> t - 1) = exp2(LA[t-1] - LA[u]) for u <= t - 1 (t, u chunk-local).
+__device__ __forceinline__ bf16x8 gen_decay_to(const float* la, int t, int q, int lane) {
+  const int gq = lane >> 4;
+  const float lat = t > 0 ? la[t - 1] : 0.f;
+  bf16x8 f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int u = 32 * q + 8 * gq + e;
+    f[e] = static_cast<bf16>(u <= t - 1 ? __builtin_amdgcn_exp2f(lat - la[u]) : 0.f);
+  }
+  return f;
+}
+// Window weights Wg[s][r] = w(r, r - s) for 0 <= r - s < e, chained k order over the targets r
+// (slot e < 4: r = 32 q + 4 gq + e; e >= 4: r = 32 q + 16 + 4 gq + e - 4); s = row - HT.
+__device__ __forceinline__ bf16x8 gen_wgate(const Geom& g, const float* wl, const float* ug, int t0, int srow, int q,
+                                            int lane) {
+  const int gq = lane >> 4;
+  const int s = srow - HT;
+  bf16x8 f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int r = 32 * q + (e < 4 ? 4 * gq + e : 16 + 4 * gq + e - 4);
+    const int j = r - s;
+    float v = 0.f;
+    if (j >= 0 && j < g.e) v = win_w(g, wl, t0, ug, t0 - HT, t0 + r, j);
+    f[e] = static_cast<bf16>(v);
+  }
+  return f;
 }
 
 }  // namespace cp

@@ -42,52 +42,6 @@ __host__ __device__ inline int gate_floats(int gate_mode, int e, int n) {
   return gate_mode == GATE_LAG ? n * e : (gate_mode == GATE_TOKEN ? n + HT : 0);
 }
 
-// Operand generators (row = lane & 15 of the tile, k slots natural: k = 32 q + 8 gq + e).
-// B_eta[r][u] = -eta_u B(r -> u) for u >= r (r, u chunk-local targets).
-template <bool MOM>
-__device__ __forceinline__ bf16x8 gen_beta_eta(const float* lb, const float* eta, int r, int q) {
-  const int gq = lane_id() >> 4;
-  const float lbr = MOM ? lb[r] : 0.f;
-  bf16x8 f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int u = 32 * q + 8 * gq + e;
-    float v = 0.f;
-    if (MOM) v = u >= r ? -eta[u] * __builtin_amdgcn_exp2f(lb[u] - lbr) : 0.f;
-    else v = u == r ? -eta[u] : 0.f;
-    f[e] = static_cast<bf16>(v);
-  }
-  return f;
-}
-// A'[t][u] = A(u -> t - 1) = exp2(LA[t-1] - LA[u]) for u <= t - 1 (t, u chunk-local).
-__device__ __forceinline__ bf16x8 gen_decay_to(const float* la, int t, int q) {
-  const int gq = lane_id() >> 4;
-  const float lat = t > 0 ? la[t - 1] : 0.f;
-  bf16x8 f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int u = 32 * q + 8 * gq + e;
-    f[e] = static_cast<bf16>(u <= t - 1 ? __builtin_amdgcn_exp2f(lat - la[u]) : 0.f);
-  }
-  return f;
-}
-// Window weights Wg[s][r] = w(r, r - s) for 0 <= r - s < e, chained k order over the targets r
-// (slot e < 4: r = 32 q + 4 gq + e; e >= 4: r = 32 q + 16 + 4 gq + e - 4); s = row - HT.
-__device__ __forceinline__ bf16x8 gen_wgate(const Geom& g, const float* wl, const float* ug, int t0, int srow, int q) {
-  const int gq = lane_id() >> 4;
-  const int s = srow - HT;
-  bf16x8 f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int r = 32 * q + (e < 4 ? 4 * gq + e : 16 + 4 * gq + e - 4);
-    const int j = r - s;
-    float v = 0.f;
-    if (j >= 0 && j < g.e) v = win_w(g, wl, t0, ug, t0 - HT, t0 + r, j);
-    f[e] = static_cast<bf16>(v);
-  }
-  return f;
-}
-
 }  // namespace cp
 
 using namespace cp;
@@ -243,12 +197,12 @@ __global__ __launch_bounds__(NTH) void k_cp_out(const Geom g, const FwdPtrs<bf16
   stage_gates(g, a.gate, rowbase, st0, nr + CL, gates, gates);
   if (w == 0) {
     const TokScal sc = tok_scalars(g, a.decay, a.lr, a.beta, rowbase, t0 + lane);
-    const float la = wave_prefix_sum(fmaxf(__log2f(sc.al), kLogFloor));
+    const float la = wave_prefix_sum(fmaxf(__log2f(sc.al), kLogFloor), lane);
     sm.la[lane] = la;
     sm.eta[lane] = sc.et;
-    if (MOM) sm.lb[lane] = wave_prefix_sum(fmaxf(__log2f(sc.be), kLogFloor));
+    if (MOM) sm.lb[lane] = wave_prefix_sum(fmaxf(__log2f(sc.be), kLogFloor), lane);
     // (At, Kt): first row of M_{t-1} ... M_0
-    const Tri inc = wave_scan<true>(Tri{sc.al, -sc.et * sc.be, sc.be});
+    const Tri inc = wave_scan<true>(Tri{sc.al, -sc.et * sc.be, sc.be}, lane);
     Tri ex = tri_shfl_up(inc, 1);
     if (lane == 0) ex = tri_id();
     sm.At[lane] = ex.a;
@@ -320,12 +274,12 @@ __global__ __launch_bounds__(NTH) void k_cp_out(const Geom g, const FwdPtrs<bf16
   // ---- this wave's 16 targets t = 16 w + m: C', Wy, K^T, Q
   const int tt = w;
   f32x4 cpr[4];
-  const bf16x8 fdec[2] = {gen_decay_to(sm.la, 16 * tt + m, 0), gen_decay_to(sm.la, 16 * tt + m, 1)};
+  const bf16x8 fdec[2] = {gen_decay_to(sm.la, 16 * tt + m, 0, lane), gen_decay_to(sm.la, 16 * tt + m, 1, lane)};
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt) {
     cpr[rt] = zero4();
 #pragma unroll
-    for (int q = 0; q < 2; ++q) cpr[rt] = mma_bf16(gen_beta_eta<MOM>(sm.lb, sm.eta, 16 * rt + m, q), fdec[q], cpr[rt]);
+    for (int q = 0; q < 2; ++q) cpr[rt] = mma_bf16(gen_beta_eta<MOM>(sm.lb, sm.eta, 16 * rt + m, q, lane), fdec[q], cpr[rt]);
   }
   const float* wl_own = gates + (size_t)nr * g.e;   // lag gates of targets t0 ..
   const float* ug_own = gates + nr;                 // token gates of sources t0 - 16 ..
@@ -336,8 +290,8 @@ __global__ __launch_bounds__(NTH) void k_cp_out(const Geom g, const FwdPtrs<bf16
 #pragma unroll
     for (int st = 0; st < SRC / 16; ++st) {
       f32x4 wy = zero4(), kq = zero4();
-      wy = mma_bf16(gen_wgate(g, wl_own, ug_own, t0, 16 * st + m, 0), fc0, wy);
-      wy = mma_bf16(gen_wgate(g, wl_own, ug_own, t0, 16 * st + m, 1), fc1, wy);
+      wy = mma_bf16(gen_wgate(g, wl_own, ug_own, t0, 16 * st + m, 0, lane), fc0, wy);
+      wy = mma_bf16(gen_wgate(g, wl_own, ug_own, t0, 16 * st + m, 1, lane), fc1, wy);
 #pragma unroll
       for (int q = 0; q < 2; ++q)
         kq = mma_bf16(frag_row(&sm.phi[0][0], PD, 16 * st, 32 * q), frag_row(&sm.psi[0][0], PD, 16 * tt, 32 * q), kq);

@@ -344,8 +344,9 @@ hipError_t launch_chunk_coef_pair(const Geom& gf, const Geom& gb, const T* decay
                                   const T* gate, float* rec_f, T* wsh_f, float* rec_b, T* wsh_b, hipStream_t stream) {
   if (gf.Lmid % 8 != 0 || gf.Lmid > CHF || gb.Lmid != 0) return hipErrorInvalidValue;
   constexpr int PER = coef_threads<CHF>() / coef_threads<CHB>();
-  const int halves = coef_halves<CHF, CHB>(gf, gb) ? 1 : 0;
-  const int nb = halves ? gb.nc / 2 : gb.nc;   // backward chunks formed by their own thread groups
+  // rec_b null: the forward records only (a backward that forms its coefficients itself)
+  const int halves = rec_b && coef_halves<CHF, CHB>(gf, gb) ? 1 : 0;
+  const int nb = !rec_b ? 0 : halves ? gb.nc / 2 : gb.nc;   // backward chunks formed by their own thread groups
   prof_name(KID_FWD_COEF, "k_chunk_coef_pair");
   prof_begin(KID_FWD_COEF, stream);
   hipLaunchKernelGGL((k_chunk_coef_pair<T, CHF, CHB>), dim3(gf.nc + (nb + PER - 1) / PER, gf.BH),

@@ -900,6 +900,8 @@ hipError_t launch_walk_bwd_kernel(const Geom& g, const BwdPtrs<bf16>& a, const S
 hipError_t launch_scalar_chain(const Geom& g, const BwdPtrs<bf16>& a, const BwdSegPtrs& p, const SegGeom& sg,
                                bool with_fixup, hipStream_t stream);
 hipError_t launch_buf_bwd(const Geom& g, const BwdPtrs<bf16>& a, const BwdSegPtrs& p, hipStream_t stream);
+hipError_t launch_chunk_bwd(const Geom& g, const BwdPtrs<bf16>& a, const SegGeom& sg, const BwdSegPtrs& p,
+                            hipStream_t stream);
 
 // walk: run the specialised reverse walk (walk_bwd.hip, bf16 with d = 64 only) in place of k_bwd_seg
 // ag (the specialised path): adjoint aggregates over the forward's chunks (seg_common.h).
@@ -940,6 +942,7 @@ hipError_t launch_bwd_seg(const Geom& g, const BwdPtrs<T>& a, const SegGeom& sg,
   prof_end(KID_BWD_SCAN, stream);
   if ((err = hipGetLastError()) != hipSuccess) return err;
   if constexpr (sizeof(T) == 2 && CH == 32 && D == 64) {
+    if (ag && ag->chunk_bwd) return launch_chunk_bwd(ag->g, a, ag->sg, p, stream);
     if (walk) {
       prof_name(KID_BWD_CHUNK, "k_walk_bwd");
       prof_begin(KID_BWD_CHUNK, stream);

@@ -19,10 +19,14 @@ struct SegGeom {
 // The adjoint aggregates of the specialised backward are formed over the forward's 64-token
 // chunks (an aggregate does not depend on how its segment is chunked, so this halves the serial
 // steps), with the forward's coefficient records: the forward geometry, segments and records.
+// chunk_bwd: the reverse walk is k_cp_bwd (chunk_bwd.hip) over the forward's chunks and segments,
+// with its coefficients formed in the kernel (no backward records, saved boundary states or
+// scalar-gradient inputs), followed by its own fixup.
 struct AggOverFwd {
   Geom g;
   SegGeom sg;
   const float* coef;
+  bool chunk_bwd;
 };
 
 // Backward-pass buffers beyond the user-visible arguments.
@@ -40,6 +44,7 @@ struct BwdSegPtrs {
   void* wsh;                 // [BH][nc][CH][SPM] Ws[s, t-1] of every chunk (input element type)
   float* scal;               // [BH][nc][ScalarBlock] per-chunk inputs of the scalar gradients
   float* buf_adj;            // [BH][2][D][D] first chunk's end adjoint (specialised walk with a carried buffer)
+  void* xsave;               // chunk-parallel backward: per chunk its start state and coefficient record
 };
 
 // The carried buffer on the specialised walks (bufwalk.hip, d = 64). Per row, its first-chunk terms:

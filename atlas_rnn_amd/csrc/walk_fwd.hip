@@ -214,6 +214,7 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
   const uint32_t f2o[2] = {frag_off(2 * th, it >> 1, lane) + (it & 1) * 8,
                            frag_off(2 * th + 1, it >> 1, lane) + (it & 1) * 8};
   auto save_state = [&](int cb, const float (&Sv)[2][4], const float (&Zv)[2][4]) {
+    if (rw == nullptr) return;   // a backward that recomputes its states (chunk_bwd.hip)
     unsigned char* blk = rw_row + (size_t)cb * kStateBlk;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
