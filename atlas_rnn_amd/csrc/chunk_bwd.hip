@@ -47,7 +47,6 @@ constexpr int NWB = NTB / 64;
 constexpr int PB = 72;    // LDS pitch (bf16 elements) of 64-wide rows
 constexpr int QP = 88;    // pitch of the Q^T / R^T rows [t][s] (80 sources + 8)
 constexpr int MP = 104;   // pitch of the Gram rows [q][s'] (96 state bases + 8)
-constexpr int CPP = 68;   // pitch of the C' rows (fp32): targets 0 .. 63 and the chunk end (64)
 constexpr int EMAX = 17;  // window
 // chunk coefficient record (floats): cs, cz (sources), cgS, cgZ (targets), the chunk transition
 constexpr int R_CS = 0, R_CZ = SRC, R_GS = 2 * SRC, R_GZ = 2 * SRC + CL, R_TR = 2 * SRC + 2 * CL;
@@ -68,13 +67,15 @@ struct BwSm {
   alignas(16) bf16 Qt[CL][QP];       // Q[s][t] stored [t][s]
   alignas(16) bf16 Rt[CL][QP];
   alignas(16) bf16 Mt[CL][MP];       // Gram M[q][s'] (q: adjoint basis E_q; s' < 80: G_s, 80: S_c, 81: Z_c)
-  alignas(16) float Cp[CL][CPP];     // C'[r][t]: of g_r in S_{t-1}; column 64: in S at the chunk end
+  alignas(16) bf16 Cb[CL][PB];       // C'[r][t]: of g_r in S_{t-1} (r, t chunk-local targets)
   alignas(16) float co[REC];
   alignas(16) float la[CL], lb[CL], eta[CL], At[CL], Kt[CL], B1[CL], be[CL];
   float hp[2][4][SRC];               // hS / hZ partials by column tile
   float gram[NWB][4];
-  float wl[CL * EMAX];               // lag gates [t][j]
-  float ug[SRC];                     // token gates of the sources
+  // the window band Bd[s][r] = w(r, r + HT - s) (0 <= r + HT - s < e; zero elsewhere): the weight of
+  // source s in the window of target r, i.e. of lag j = r + HT - s (w: the lag gate, the token gate
+  // of the source, or 1; zero for targets past T)
+  alignas(16) bf16 Bd[SRC][PB];
   // end terms of ddelta / dphi (waves 4-7), bf16 pairs in the accumulator layout: [ct][st][pair][lane]
   unsigned ed[4][SRC / 16][2][64], ef[4][SRC / 16][2][64];
 };
@@ -131,6 +132,11 @@ __device__ __forceinline__ void rows_store(const RowPf<NWL>& pf, BwSm& sm, int d
   }
 }
 
+// the (segment, row) block of a boundary-partial buffer [BH][nseg][H][2D]
+__device__ __forceinline__ float* part_row(float* base, int bh, int nseg, int seg, int H) {
+  return base + ((size_t)bh * nseg + seg) * H * (2 * D);
+}
+
 // the chunk's scalars (wave 0: lane = target) and gates (raw bf16 bits)
 struct ScalPf {
   unsigned short al, et, be;
@@ -145,16 +151,21 @@ __device__ __forceinline__ void scal_load(ScalPf& p, const Geom& g, const BwdPtr
     p.et = __builtin_bit_cast(unsigned short, a.lr[o]);
     p.be = g.momentum ? __builtin_bit_cast(unsigned short, a.beta[o]) : (unsigned short)0;
   }
+  // window weight w(r, j) of target r, lag j: the lag gate, the gate of the source token t0 + r - j,
+  // or 1; zero for targets past T
 #pragma unroll
   for (int u = 0; u < 3; ++u) {
     p.gt[u] = 0;
     const int i = tid + NTB * u;
-    if (g.gate_mode == GATE_LAG) {
-      const int t = i / g.e;
-      if (t < CL && t0 + t < g.T) p.gt[u] = __builtin_bit_cast(unsigned short, a.gate[(rowbase + t0 + t) * g.e + i % g.e]);
-    } else if (g.gate_mode == GATE_TOKEN && u == 0) {
-      const int s = t0 - HT + i;
-      if (i < SRC && s >= 0 && s < g.T) p.gt[u] = __builtin_bit_cast(unsigned short, a.gate[rowbase + s]);
+    const int r = i / g.e, j = i - r * g.e;
+    if (r < CL && t0 + r < g.T) {
+      if (g.gate_mode == GATE_LAG) {
+        p.gt[u] = __builtin_bit_cast(unsigned short, a.gate[(rowbase + t0 + r) * g.e + j]);
+      } else if (g.gate_mode == GATE_TOKEN) {
+        if (t0 + r - j >= 0) p.gt[u] = __builtin_bit_cast(unsigned short, a.gate[rowbase + t0 + r - j]);
+      } else {
+        p.gt[u] = 0x3f80;
+      }
     }
   }
 }
@@ -163,16 +174,26 @@ __device__ __forceinline__ void gates_store(const ScalPf& p, const Geom& g, BwSm
 #pragma unroll
   for (int u = 0; u < 3; ++u) {
     const int i = tid + NTB * u;
-    if (g.gate_mode == GATE_LAG && i < CL * g.e) sm.wl[i] = bf(p.gt[u]);
-    if (g.gate_mode == GATE_TOKEN && u == 0 && i < SRC) sm.ug[i] = bf(p.gt[u]);
+    if (i < CL * g.e) {
+      const int r = i / g.e, j = i - r * g.e;
+      sm.Bd[r + HT - j][r] = __builtin_bit_cast(bf16, p.gt[u]);
+    }
   }
 }
 
-// window weight of lag j for chunk target r (the chunk's staged gates)
-__device__ __forceinline__ float cw(const Geom& g, const BwSm& sm, int r, int j) {
-  if (g.gate_mode == GATE_LAG) return sm.wl[r * g.e + j];
-  if (g.gate_mode == GATE_TOKEN) return sm.ug[r - j + HT];
-  return 1.f;
+// window weight of lag j for chunk target r (the chunk's staged band)
+__device__ __forceinline__ float cw(const BwSm& sm, int r, int j) { return static_cast<float>(sm.Bd[r + HT - j][r]); }
+
+// B'[u][t] = the coefficient of g_u in Z_{t-1}: B(u -> t - 1) = exp2(LB[t-1] - LB[u]) for u <= t - 1
+// with momentum, [u == t - 1] without. Operand rows t (lane & 15), k slots natural over u.
+template <bool MOM>
+__device__ __forceinline__ bf16x8 gen_zcoef(const float* lb, int t, int q, int lane) {
+  if constexpr (MOM) return gen_decay_to(lb, t, q, lane);
+  const int gq = lane >> 4;
+  bf16x8 f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = static_cast<bf16>(32 * q + 8 * gq + e == t - 1 ? 1.f : 0.f);
+  return f;
 }
 
 // wave 0: the chunk's end coefficients (cgS, cgZ per target; the transition) from its scalars
@@ -183,7 +204,7 @@ __device__ __forceinline__ void chunk_end_scan(const Geom& g, const ScalPf& p, i
               be = __shfl(bf(p.be), 63 - lane, 64);
   const Tri x{al, -et * be, be};
   const Tri inc = wave_scan<false>(x, lane);
-  Tri ex = tri_shfl_up(inc, 1);
+  Tri ex = tri_prev_lane(inc);
   if (lane == 0) ex = tri_id();
   const int r = 63 - lane;
   const bool real = t0 + r < g.T;
@@ -199,7 +220,7 @@ __device__ __forceinline__ void chunk_end_sources(const Geom& g, BwSm& sm) {
     for (int j = 0; j < g.e; ++j) {
       const int r = s - HT + j;
       if (r >= 0 && r < CL) {
-        const float wgt = cw(g, sm, r, j);
+        const float wgt = cw(sm, r, j);
         cs += wgt * sm.co[R_GS + r];
         cz += wgt * sm.co[R_GZ + r];
       }
@@ -219,20 +240,23 @@ __device__ __forceinline__ void chunk_prefix(const ScalPf& p, BwSm& sm) {
   sm.eta[lane] = et;
   sm.be[lane] = be;
   const Tri inc = wave_scan<true>(Tri{al, -et * be, be}, lane);
-  Tri ex = tri_shfl_up(inc, 1);
+  Tri ex = tri_prev_lane(inc);
   if (lane == 0) ex = tri_id();
   sm.At[lane] = ex.a;
   sm.Kt[lane] = ex.k;
   sm.B1[lane] = ex.b;
 }
 
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
-  return x;
-}
+// Sum over the 64 lanes, in every lane (DPP row sums, then the cross-row swaps).
+__device__ __forceinline__ float wave_sum(float x) { return xsum_rows(row_sum16(x)); }
 
 __device__ __forceinline__ unsigned pk(float a, float b) { return pack_bf16x2(a, b); }
+// v stored at byte offset off (32-bit) from a uniform base: one store with a scalar base and a 32-bit
+// vector offset instead of per-lane 64-bit address arithmetic
+template <typename T>
+__device__ __forceinline__ void st_at(T* base, uint32_t off, T v) {
+  *reinterpret_cast<T*>(reinterpret_cast<unsigned char*>(base) + off) = v;
+}
 __device__ __forceinline__ float lo16(unsigned u) { return __builtin_bit_cast(float, u << 16); }
 __device__ __forceinline__ float hi16(unsigned u) { return __builtin_bit_cast(float, u & 0xffff0000u); }
 
@@ -276,6 +300,9 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
     sreft[q] = f;
   }
 
+  // the band's entries off the window stay zero; its window entries are rewritten for every chunk
+  for (int i = tid; i < SRC * PB / 2; i += NTB) reinterpret_cast<unsigned*>(&sm.Bd[0][0])[i] = 0u;
+  __syncthreads();
   // ---------------------------------------------------------------- forward pass over the segment
   float xS[2][4], xZ[2][4];
   {
@@ -457,7 +484,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
     }
     __syncthreads();
 
-    // ---- R1: delta (in place of v), C', the end column of C'
+    // ---- R1: delta (in place of v), C'
     {
       CPB_FRESH_LANE
       const int st0 = hf == 0 ? 0 : 3, nst = hf == 0 ? 3 : 2;
@@ -478,9 +505,8 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
         for (int q = 0; q < 2; ++q)
           acc = mma_bf16(gen_beta_eta<MOM>(sm.lb, sm.eta, 16 * q4 + m, q, lane), gen_decay_to(sm.la, 16 * tt + m, q, lane), acc);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sm.Cp[16 * q4 + 4 * gq + r][16 * tt + m] = acc[r];
+        for (int r = 0; r < 4; ++r) sm.Cb[16 * q4 + 4 * gq + r][16 * tt + m] = static_cast<bf16>(acc[r]);
       }
-      if (tid < CL) sm.Cp[tid][CL] = sm.co[R_GS + tid];
     }
     __syncthreads();
 
@@ -489,26 +515,27 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
       CPB_FRESH_LANE
       const int tt = q4;
       const int t = 16 * tt + m;
+      // C' as the k-major operand over the targets r (lane row t): shared by every source tile
+      const bf16x8 fcb0 = frag_tr_l(&sm.Cb[0][0], PB, 16 * tt, 0, lane);
+      const bf16x8 fcb1 = frag_tr_l(&sm.Cb[0][0], PB, 16 * tt, 32, lane);
       f32x4 Rr[SRC / 16];
 #pragma unroll
       for (int st = 0; st < SRC / 16; ++st) {
-        f32x4 kq = zero4(), dd = zero4();
+        f32x4 kq = zero4(), dd = zero4(), wy = zero4();
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           kq = mma_bf16(frag_row_l(&sm.phi[0][0], PB, 16 * st, 32 * q, lane), frag_row_l(&sm.psi[0][0], PB, 16 * tt, 32 * q, lane), kq);
           dd = mma_bf16(frag_row_l(&sm.vd[0][0], PB, 16 * st, 32 * q, lane), frag_row_l(&sm.dy[0][0], PB, 16 * tt, 32 * q, lane), dd);
         }
+        // Wy[s][t] = sum_r Band[s][r] C'[r][t]: the band of source tile st meets targets
+        // 16 st - 16 .. 16 st + e - 2 only (e <= 17): k half 0 for st <= 2, half 1 for st >= 2
+        if (st <= 2) wy = mma_bf16(frag_row_l(&sm.Bd[0][0], PB, 16 * st, 0, lane), fcb0, wy);
+        if (st >= 2) wy = mma_bf16(frag_row_l(&sm.Bd[0][0], PB, 16 * st, 32, lane), fcb1, wy);
         float qv[4], rv_[4], mv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int s = 16 * st + 4 * gq + r;
-          float wy = 0.f;
-          for (int j = 0; j < g.e; ++j) {
-            const int rr = s - HT + j;
-            if (rr >= 0 && rr < CL) wy += cw(g, sm, rr, j) * sm.Cp[rr][t];
-          }
-          qv[r] = kq[r] * wy;
-          rv_[r] = dd[r] * wy;
+          qv[r] = kq[r] * wy[r];
+          rv_[r] = dd[r] * wy[r];
           mv[r] = kq[r] * dd[r];
           Rr[st][r] = rv_[r];
         }
@@ -617,16 +644,16 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
           if (st == 0) {   // halo rows: partial for the previous chunk (or the previous segment)
             if (seg_first) {
               if (seg > 0 && s >= HT - H)
-                p.halo_part[(((size_t)bh * sg.nseg + seg) * H + (s - (HT - H))) * (2 * D) + col] = -dd;
+                st_at(part_row(p.halo_part, bh, sg.nseg, seg, H), (uint32_t)(((s - (HT - H)) * (2 * D) + col) * 4), -dd);
             } else {
               cdv[r] = -dd;
             }
           } else if (pp < g.T) {
             float val = -dd + (st == SRC / 16 - 1 && !seg_last ? cin[r] : 0.f);
             if (pp >= tail0)
-              p.tail_part[(((size_t)bh * sg.nseg + seg) * H + (pp - tail0)) * (2 * D) + col] = val;
+              st_at(part_row(p.tail_part, bh, sg.nseg, seg, H), (uint32_t)(((pp - tail0) * (2 * D) + col) * 4), val);
             else
-              a.dv[(rowbase + pp) * D + col] = static_cast<bf16>(val);
+              st_at(a.dv + rowbase * D, (uint32_t)((pp * D + col) * 2), static_cast<bf16>(val));
           }
         }
       }
@@ -643,8 +670,10 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
                         sm.gram[6][2] + sm.gram[7][2];
       const float gZZ = sm.gram[0][3] + sm.gram[1][3] + sm.gram[2][3] + sm.gram[3][3] + sm.gram[4][3] + sm.gram[5][3] +
                         sm.gram[6][3] + sm.gram[7][3];
-      // adjoint-coefficient operands (rows t = 16 tt + m, k = q natural): Am (decay) and Km (C')
-      bf16x8 fam[2], fkm[2];
+      // adjoint-coefficient operands (rows t = 16 tt + m, k = q natural): Am (decay), Km (C'); the
+      // state-coefficient operands over the targets r (rows t): C'^T (of G_s in S_{t-1} through the
+      // window: Wy = Band C'), B'^T (in Z_{t-1}: Wzy = Band B')
+      bf16x8 fam[2], fzT[2];
       {
         const int t = 16 * tt + m;
         const float lat = sm.la[t];
@@ -653,66 +682,71 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const int qq = 32 * q + 8 * gq + e;
-            fam[q][e] = static_cast<bf16>(qq > t ? __builtin_amdgcn_exp2f(sm.la[qq - 1] - lat) : 0.f);
-            fkm[q][e] = static_cast<bf16>(sm.Cp[t][qq]);
+            const float x = __builtin_amdgcn_exp2f(sm.la[qq > 0 ? qq - 1 : 0] - lat);
+            fam[q][e] = static_cast<bf16>(qq > t ? x : 0.f);
           }
+          fzT[q] = gen_zcoef<MOM>(sm.lb, t, q, lane);
         }
       }
+      // per target row r of this lane: the end terms' coefficients (A(t -> 63); cgS, cgZ from the record)
+      float aend[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) aend[r] = __builtin_amdgcn_exp2f(sm.la[CL - 1] - sm.la[16 * tt + 4 * gq + r]);
+      // state bases s' = 16 sp2 + m: the products G_s (s' < 80), then S_c (80), Z_c (81)
 #pragma unroll 1
-      for (int sp2 = 0; sp2 < 6; ++sp2) {
-        f32x4 ra = zero4(), rz = zero4();
+      for (int sp2 = 0; sp2 < SRC / 16; ++sp2) {
+        f32x4 ra = zero4(), rz = zero4(), wy = zero4(), wz = zero4();
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           const bf16x8 fm = frag_tr_l(&sm.Mt[0][0], MP, 16 * sp2, 32 * q, lane);
           ra = mma_bf16(fam[q], fm, ra);
-          rz = mma_bf16(fkm[q], fm, rz);
+          rz = mma_bf16(frag_row_l(&sm.Cb[0][0], PB, 16 * tt, 32 * q, lane), fm, rz);
+          const bf16x8 fb = frag_row_l(&sm.Bd[0][0], PB, 16 * sp2, 32 * q, lane);
+          wy = mma_bf16(frag_tr_l(&sm.Cb[0][0], PB, 16 * tt, 32 * q, lane), fb, wy);
+          wz = mma_bf16(fzT[q], fb, wz);
         }
-        const int sq = 16 * sp2 + m;   // state basis index
-        float hs = 0.f, hz = 0.f;
-        if (sq < SRC) {
-          hs = sm.hp[0][0][sq] + sm.hp[0][1][sq] + sm.hp[0][2][sq] + sm.hp[0][3][sq];
-          hz = sm.hp[1][0][sq] + sm.hp[1][1][sq] + sm.hp[1][2][sq] + sm.hp[1][3][sq];
-        } else if (sq == SRC) {
-          hs = gSS; hz = gZS;
-        } else if (sq == SRC + 1) {
-          hs = gSZ; hz = gZZ;
-        }
+        const int sq = 16 * sp2 + m;
+        const float hs = sm.hp[0][0][sq] + sm.hp[0][1][sq] + sm.hp[0][2][sq] + sm.hp[0][3][sq];
+        const float hz = sm.hp[1][0][sq] + sm.hp[1][1][sq] + sm.hp[1][2][sq] + sm.hp[1][3][sq];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 16 * tt + 4 * gq + r;
-          const float aend = __builtin_amdgcn_exp2f(sm.la[CL - 1] - sm.la[t]);
-          const float Rs = ra[r] + aend * hs;
-          const float Rz = rz[r] + sm.Cp[t][CL] * hs + sm.co[R_GZ + t] * hz;
-          float wy = 0.f, wzy = 0.f;
-          if (sq < SRC) {
-            for (int j = 0; j < g.e; ++j) {
-              const int rr = sq - HT + j;
-              if (rr >= 0 && rr < CL) {
-                const float wgt = cw(g, sm, rr, j);
-                wy += wgt * sm.Cp[rr][t];
-                float bz = 0.f;
-                if (MOM) bz = rr <= t - 1 ? __builtin_amdgcn_exp2f(sm.lb[t - 1] - sm.lb[rr]) : 0.f;
-                else bz = rr == t - 1 ? 1.f : 0.f;
-                wzy += wgt * bz;
-              }
-            }
-            const int jb = t + HT - sq;   // band: the source of lag jb of target t
-            if (jb >= 0 && jb < g.e) {
-              eb[r] += cw(g, sm, t, jb) * Rs;
-              if (t0 + t < g.T) {
-                if (g.gate_mode == GATE_LAG) a.dgate[(rowbase + t0 + t) * g.e + jb] = static_cast<bf16>(Rz);
-                else if (g.gate_mode == GATE_TOKEN) p.dw[(rowbase + t0 + t) * g.e + jb] = Rz;
-              }
-            }
-          } else if (sq == SRC) {
-            wy = sm.At[t];
-          } else if (sq == SRC + 1) {
-            wy = sm.Kt[t];
-            wzy = sm.B1[t];
+          const float Rs = ra[r] + aend[r] * hs;
+          const float Rz = rz[r] + sm.co[R_GS + t] * hs + sm.co[R_GZ + t] * hz;
+          al[r] += wy[r] * Rs;
+          ea[r] += wz[r] * Rs;
+          bt[r] += wz[r] * Rz;
+          const int jb = t + HT - sq;   // band: the source of lag jb of target t
+          const bool inb = jb >= 0 && jb < g.e;
+          eb[r] += static_cast<float>(sm.Bd[sq][t]) * Rs;   // zero off the band
+          if (inb && t0 + t < g.T) {
+            const uint32_t o = (uint32_t)((t0 + t) * g.e + jb);
+            if (g.gate_mode == GATE_LAG) st_at(a.dgate + rowbase * g.e, o * 2, static_cast<bf16>(Rz));
+            else if (g.gate_mode == GATE_TOKEN) st_at(p.dw + rowbase * g.e, o * 4, Rz);
           }
+        }
+      }
+      {   // s' = 80 (S_c: in S_{t-1} with At), 81 (Z_c: in S_{t-1} with Kt, in Z_{t-1} with B1)
+        f32x4 ra = zero4(), rz = zero4();
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const bf16x8 fm = frag_tr_l(&sm.Mt[0][0], MP, SRC, 32 * q, lane);
+          ra = mma_bf16(fam[q], fm, ra);
+          rz = mma_bf16(frag_row_l(&sm.Cb[0][0], PB, 16 * tt, 32 * q, lane), fm, rz);
+        }
+        const bool bs = m == 0, bz = m == 1;
+        const float hs = bs ? gSS : bz ? gSZ : 0.f;
+        const float hz = bs ? gZS : bz ? gZZ : 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * tt + 4 * gq + r;
+          const float Rs = ra[r] + aend[r] * hs;
+          const float Rz = rz[r] + sm.co[R_GS + t] * hs + sm.co[R_GZ + t] * hz;
+          const float wy = bs ? sm.At[t] : bz ? sm.Kt[t] : 0.f;
+          const float wz = bz ? sm.B1[t] : 0.f;
           al[r] += wy * Rs;
-          ea[r] += wzy * Rs;
-          bt[r] += wzy * Rz;
+          ea[r] += wz * Rs;
+          bt[r] += wz * Rz;
         }
       }
 #pragma unroll
@@ -720,9 +754,10 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
         const float va = row_sum16(al[r]), vea = row_sum16(ea[r]), veb = row_sum16(eb[r]), vb = row_sum16(bt[r]);
         const int t = 16 * tt + 4 * gq + r;
         if (m == 0 && t0 + t < g.T) {
-          a.ddecay[rowbase + t0 + t] = static_cast<bf16>(va);
-          a.dlr[rowbase + t0 + t] = static_cast<bf16>(-(sm.be[t] * vea + veb));
-          if (MOM) a.dbeta[rowbase + t0 + t] = static_cast<bf16>(vb);
+          const uint32_t o = (uint32_t)(t0 + t) * 2;
+          st_at(a.ddecay + rowbase, o, static_cast<bf16>(va));
+          st_at(a.dlr + rowbase, o, static_cast<bf16>(-(sm.be[t] * vea + veb)));
+          if (MOM) st_at(a.dbeta + rowbase, o, static_cast<bf16>(vb));
         }
       }
     }
@@ -765,17 +800,17 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
           if (st == 0) {
             if (seg_first) {
               if (seg > 0 && s >= HT - H)
-                p.halo_part[(((size_t)bh * sg.nseg + seg) * H + (s - (HT - H))) * (2 * D) + D + col] = df;
+                st_at(part_row(p.halo_part, bh, sg.nseg, seg, H), (uint32_t)(((s - (HT - H)) * (2 * D) + D + col) * 4), df);
             } else {
               cdk[r] = df;
             }
           } else if (pp < g.T) {
             float val = df + (st == SRC / 16 - 1 && !seg_last ? cin[r] : 0.f);
             if (pp >= tail0) {
-              p.tail_part[(((size_t)bh * sg.nseg + seg) * H + (pp - tail0)) * (2 * D) + D + col] = val;
+              st_at(part_row(p.tail_part, bh, sg.nseg, seg, H), (uint32_t)(((pp - tail0) * (2 * D) + D + col) * 4), val);
             } else {
               if constexpr (MAPE) val *= poly_map_grad(bf(bld2(rkk, (uint32_t)((pp * D + col) * 2))), g.map_deg);
-              a.dk[(rowbase + pp) * D + col] = static_cast<bf16>(val);
+              st_at(a.dk + rowbase * D, (uint32_t)((pp * D + col) * 2), static_cast<bf16>(val));
             }
           }
         }

@@ -42,29 +42,52 @@ __device__ __forceinline__ Tri tri_id() { return Tri{1.f, 0.f, 1.f}; }
 __device__ __forceinline__ Tri tri_mul(const Tri& L, const Tri& R) {
   return Tri{L.a * R.a, L.a * R.k + L.k * R.b, L.b * R.b};
 }
-__device__ __forceinline__ Tri tri_shfl_up(const Tri& x, int off) {
-  return Tri{__shfl_up(x.a, off, 64), __shfl_up(x.k, off, 64), __shfl_up(x.b, off, 64)};
+// Lane moves on the VALU (DPP) for the wave-wide scans: `old` where the source lane is outside the
+// pattern or its row is masked off. Controls: row_shr:n = 0x110 + n (within 16-lane rows),
+// wave_shr:1 = 0x138, row_bcast:15 = 0x142 (lane 15 of a row to the next row), row_bcast:31 = 0x143
+// (lane 31 to rows 2 and 3).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_f(float old, float src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, src),
+                                                               CTRL, ROWS, 0xf, false));
 }
+template <int CTRL, int ROWS>
+__device__ __forceinline__ Tri dpp_tri(const Tri& x) {
+  return Tri{dpp_f<CTRL, ROWS>(1.f, x.a), dpp_f<CTRL, ROWS>(0.f, x.k), dpp_f<CTRL, ROWS>(1.f, x.b)};
+}
+// The previous lane's value (lane 0: the identity).
+__device__ __forceinline__ Tri tri_prev_lane(const Tri& x) { return dpp_tri<0x138, 0xf>(x); }
 
-// Inclusive scan over the 64 lanes of a wave. LATER_LEFT: lane j gets X_j X_{j-1} ... X_0 (the
-// product of a forward recurrence); otherwise X_0 X_1 ... X_j.
+// Inclusive scan over the 64 lanes of a wave (row shifts 1, 2, 4, 8, then the row broadcasts).
+// LATER_LEFT: lane j gets X_j X_{j-1} ... X_0 (the product of a forward recurrence); otherwise
+// X_0 X_1 ... X_j.
 template <bool LATER_LEFT>
 __device__ __forceinline__ Tri wave_scan(Tri v, int lane) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const Tri u = tri_shfl_up(v, off);
-    if (lane >= off) v = LATER_LEFT ? tri_mul(v, u) : tri_mul(u, v);
+  (void)lane;
+#define ATLAS_TRI_STEP(C, R)                         \
+  {                                                  \
+    const Tri u = dpp_tri<C, R>(v);                  \
+    v = LATER_LEFT ? tri_mul(v, u) : tri_mul(u, v);  \
   }
+  ATLAS_TRI_STEP(0x111, 0xf)
+  ATLAS_TRI_STEP(0x112, 0xf)
+  ATLAS_TRI_STEP(0x114, 0xf)
+  ATLAS_TRI_STEP(0x118, 0xf)
+  ATLAS_TRI_STEP(0x142, 0xa)
+  ATLAS_TRI_STEP(0x143, 0xc)
+#undef ATLAS_TRI_STEP
   return v;
 }
 
 // Inclusive sum over the 64 lanes of a wave.
 __device__ __forceinline__ float wave_prefix_sum(float v, int lane) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float u = __shfl_up(v, off, 64);
-    if (lane >= off) v += u;
-  }
+  (void)lane;
+  v += dpp_f<0x111, 0xf>(0.f, v);
+  v += dpp_f<0x112, 0xf>(0.f, v);
+  v += dpp_f<0x114, 0xf>(0.f, v);
+  v += dpp_f<0x118, 0xf>(0.f, v);
+  v += dpp_f<0x142, 0xa>(0.f, v);
+  v += dpp_f<0x143, 0xc>(0.f, v);
   return v;
 }
 
@@ -132,7 +155,7 @@ __device__ __forceinline__ void range_coefs(const Geom& g, const TokScal& sc, in
   Tri pre = tri_id();
   for (int u = 0; u < w; ++u) pre = tri_mul(pre, rs.tot[u]);
   v = tri_mul(pre, v);
-  Tri ex = tri_shfl_up(v, 1);
+  Tri ex = tri_prev_lane(v);
   if (lane == 0) ex = pre;
   if (tid == 0) {
     Tri all = tri_id();
@@ -301,15 +324,21 @@ __device__ __forceinline__ void state_blocks(const SrcBlocks<NB>& sb, int nsrc, 
 // B_eta[r][u] = -eta_u B(r -> u) for u >= r (r, u chunk-local targets).
 template <bool MOM>
 __device__ __forceinline__ bf16x8 gen_beta_eta(const float* lb, const float* eta, int r, int q, int lane) {
+  // loads unconditional (every index in range), the triangle applied by selects: no branches
   const int gq = lane >> 4;
   const float lbr = MOM ? lb[r] : 0.f;
   bf16x8 f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int u = 32 * q + 8 * gq + e;
-    float v = 0.f;
-    if (MOM) v = u >= r ? -eta[u] * __builtin_amdgcn_exp2f(lb[u] - lbr) : 0.f;
-    else v = u == r ? -eta[u] : 0.f;
+    const float et = eta[u];
+    float v;
+    if (MOM) {
+      const float x = -et * __builtin_amdgcn_exp2f(lb[u] - lbr);
+      v = u >= r ? x : 0.f;
+    } else {
+      v = u == r ? -et : 0.f;
+    }
     f[e] = static_cast<bf16>(v);
   }
   return f;
@@ -317,12 +346,13 @@ __device__ __forceinline__ bf16x8 gen_beta_eta(const float* lb, const float* eta
 // A'[t][u] = A(u -> t - 1) = exp2(LA[t-1] - LA[u]) for u <= t - 1 (t, u chunk-local).
 __device__ __forceinline__ bf16x8 gen_decay_to(const float* la, int t, int q, int lane) {
   const int gq = lane >> 4;
-  const float lat = t > 0 ? la[t - 1] : 0.f;
+  const float lat = la[t > 0 ? t - 1 : 0];
   bf16x8 f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int u = 32 * q + 8 * gq + e;
-    f[e] = static_cast<bf16>(u <= t - 1 ? __builtin_amdgcn_exp2f(lat - la[u]) : 0.f);
+    const float x = __builtin_amdgcn_exp2f(lat - la[u]);
+    f[e] = static_cast<bf16>(u <= t - 1 ? x : 0.f);
   }
   return f;
 }

@@ -203,7 +203,7 @@ __global__ __launch_bounds__(NTH) void k_cp_out(const Geom g, const FwdPtrs<bf16
     if (MOM) sm.lb[lane] = wave_prefix_sum(fmaxf(__log2f(sc.be), kLogFloor), lane);
     // (At, Kt): first row of M_{t-1} ... M_0
     const Tri inc = wave_scan<true>(Tri{sc.al, -sc.et * sc.be, sc.be}, lane);
-    Tri ex = tri_shfl_up(inc, 1);
+    Tri ex = tri_prev_lane(inc);
     if (lane == 0) ex = tri_id();
     sm.At[lane] = ex.a;
     sm.Kt[lane] = ex.k;

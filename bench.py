@@ -94,6 +94,10 @@ def algorithmic_bytes(bh=BH, t=T, d=D, e=E, n_sc=None, s_in=2, s_st=4):
     for spec, gen in (("k_walk_agg", "k_fwd_seg_agg"), ("k_walk_full", "k_fwd_seg"), ("k_walk_bwd", "k_bwd_seg"),
                       ("k_scalar_chain", "k_bwd_scalar")):
         per_kernel[spec] = per_kernel[gen]
+    # the backward walk with in-kernel coefficients (chunk_bwd.hip): the walk's reads and writes plus
+    # the per-token scalars read and their gradients written; its fixup writes dS_ref once
+    per_kernel["k_cp_bwd"] = per_kernel["k_bwd_seg"] + per_kernel["k_bwd_scalar"]
+    per_kernel["k_cp_fixup"] = st
     return fwd, bwd, per_kernel
 
 
