@@ -30,7 +30,7 @@ hipError_t launch_walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom&
                            float* rw, float* final_raw, float* coef, bf16* wsh, hipStream_t stream);
 bool chunk_path_supported(const Geom& g);
 bool chunk_bwd_supported(const Geom& g, const SegGeom& sg);
-size_t chunk_bwd_xsave_bytes(const Geom& g, const SegGeom& sg);
+size_t chunk_bwd_states_bytes(const Geom& g);
 SegGeom chunk_seg(const Geom& g);
 hipError_t launch_chunk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
                             float* final_raw, hipStream_t stream);
@@ -270,11 +270,11 @@ SavedLayout saved_layout(const Plan& pl) {
   L.seg = off; off += align256((size_t)g.BH * pl.sg.nseg * 2 * st);
   L.agg = off; off += align256((size_t)g.BH * pl.sg.nseg * pl.sg.agg_stride * sizeof(float));
   L.final_raw = off; off += align256((size_t)g.BH * st);
-  // the chunk-parallel path keeps nothing per chunk: the regions below are empty for it; with the
-  // backward of chunk_bwd.hip only the forward's own records remain
+  // the chunk-parallel path keeps nothing per chunk: the regions below are empty for it; the
+  // backward of chunk_bwd.hip takes the states at the 64-token chunk starts and forms its own records
   const bool walk = !pl.chunk;
   const bool brec = walk && !pl.cbwd;
-  L.rw = off; off += align256(brec ? (size_t)g.BH * g.ncb * 2 * st : 0);
+  L.rw = off; off += align256(brec ? (size_t)g.BH * g.ncb * 2 * st : pl.cbwd ? chunk_bwd_states_bytes(g) : 0);
   // forward scratch: per-chunk coefficient records and Ws[s, t-1] blocks
   L.coef = off; off += align256(walk ? (size_t)g.BH * g.nc * coef_rec_floats(pl.CH) * sizeof(float) : 0);
   L.wsh = off; off += align256(walk ? (size_t)g.BH * g.nc * pl.CH * (pl.CH + kHaloPad) * pl.esize : 0);
@@ -287,10 +287,10 @@ SavedLayout saved_layout(const Plan& pl) {
 }
 
 // backward workspace: adjoint aggregates, segment-end adjoints, dS_ref partials, boundary partials,
-// token-gate (target, lag) gradients, the scalar-gradient inputs (or, for the backward of
-// chunk_bwd.hip, its per-chunk start states and records).
+// token-gate (target, lag) gradients, the scalar-gradient inputs (none for the backward of
+// chunk_bwd.hip, which forms its scalar gradients in the walk).
 struct BwdLayout {
-  size_t agg, segadj, dsref, tail, halo, dw, scal, badj, xsave, total;
+  size_t agg, segadj, dsref, tail, halo, dw, scal, badj, total;
 };
 
 BwdLayout bwd_layout(const Plan& pl) {
@@ -307,7 +307,6 @@ BwdLayout bwd_layout(const Plan& pl) {
   L.dw = off; off += align256(g.gate_mode == ATLAS_GATE_TOKEN ? (size_t)g.BH * g.T * g.e * sizeof(float) : 0);
   L.scal = off; off += align256(pl.cbwd ? 0 : (size_t)g.BH * g.nc * scalar_block_floats(pl.CHB) * sizeof(float));
   L.badj = off; off += align256(walk_with_buffer(pl) ? (size_t)g.BH * bufw::kAdjFloats * sizeof(float) : 0);
-  L.xsave = off; off += align256(pl.cbwd ? chunk_bwd_xsave_bytes(pl.g, pl.sg) : 0);
   L.total = off;
   return L;
 }
@@ -372,7 +371,6 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
   hipError_t err = launch_chunk_coef_pair<T, CHF, CHB>(
       g, pl.gb, a.decay, a.lr, a.beta, a.gate, coef, wsh, pl.cbwd ? nullptr : reinterpret_cast<float*>(sv + SL.bcoef),
       pl.cbwd ? nullptr : reinterpret_cast<T*>(sv + SL.bwsh), s);
-  if (pl.cbwd) rw = nullptr;
   if (err != hipSuccess) return ATLAS_MEM_ERR_LAUNCH;
   err = hipErrorInvalidValue;
   if (g.DK == 64) {
@@ -429,7 +427,6 @@ int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, voi
   p.wsh = const_cast<unsigned char*>(sv + SL.bwsh);
   p.scal = reinterpret_cast<float*>(w + L.scal);
   p.buf_adj = walk_with_buffer(pl) ? reinterpret_cast<float*>(w + L.badj) : nullptr;
-  p.xsave = pl.cbwd ? static_cast<void*>(w + L.xsave) : nullptr;
   hipError_t err = hipErrorInvalidValue;
   // the specialised walks run as a pair: the forward saved its states in their layout
   const bool walk = sizeof(T) == 2 && walk_fwd_supported(pl.g);

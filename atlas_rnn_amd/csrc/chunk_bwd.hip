@@ -1,28 +1,25 @@
-// chunk_bwd.hip - reverse walk of the backward pass with every coefficient formed in the kernel
-// (bf16 inputs, d_k = d_v = 64, window <= 17, no scan_chunk_len clamp, no carried buffer).
+// chunk_bwd.hip - reverse walk of the backward pass with every coefficient and the scalar gradients
+// formed in the kernel (bf16 inputs, d_k = d_v = 64, window <= 17, no scan_chunk_len clamp, no
+// carried buffer).
 //
 // One workgroup of 8 waves per (segment, row); the segments are the forward's (G chunks of 64
 // tokens). The adjoint at each segment end comes from the adjoint aggregates and their scan
-// (seg_bwd.hip); the boundary merge and the dS_ref sum are the shared fixup (seg_fixup.h).
+// (seg_bwd.hip); the boundary merge and the dS_ref sum are the shared fixup (seg_fixup.h). The
+// chunk-start states X_c = (S_c, Z_c) are the forward walk's (bf16, one block per chunk).
 //
-//   forward pass over the segment: the chunk-start states X_c = (S_c, Z_c) from the segment-start
-//     state (X_{c+1} = T_c X_c + (U_c, V_c)), kept in the workspace as bf16 (16 KB per chunk, read
-//     back by the same workgroup) with each chunk's end coefficients (a record of 292 floats);
-//   reverse pass, chunk c (targets t = 0 .. 63, sources s = 0 .. 79 at tokens t0 - 16 + s), with
-//   Lam = (lamS, lamZ) the adjoint of (S, Z) after the chunk's last token:
-//     dpsi_t  = S_{t-1}^T dy_t = At S_c^T dy_t + Kt Z_c^T dy_t + sum_s R[s][t] phi_s
-//     ddelta_s = sum_t Q[s][t] dy_t + cs_s lamS phi_s + cz_s lamZ phi_s
-//     dphi_s  = sum_t R[s][t] psi_t + cs_s lamS^T delta_s + cz_s lamZ^T delta_s + S_ref^T ddelta_s
-//     with K[s][t] = phi_s . psi_t, Dd[s][t] = delta_s . dy_t, Wy[s][t] the coefficient of
-//     G_s = delta_s phi_s^T in S_{t-1}, Q = K o Wy, R = Dd o Wy;
-//   the scalar gradients are inner products of the adjoint at t with the state at t - 1. Both are
-//     combinations of a few bases: adjoint bases E_q = dy_q psi_q^T (q > t), lamS, lamZ; state
-//     bases G_s, S_c, Z_c. Their Gram matrix M (M[q][s] = K[s][q] Dd[s][q]; fS, fZ; hS, hZ; the
-//     four state-adjoint Grams) is contracted on the matrix cores with the adjoint coefficients
-//     (Am[t][q] = A(t -> q-1) for lamS_t; C'[t][q] for the total lamZ_t = d/dg_t) and then with
-//     the state coefficients (Wy; Wzy: of G_s in Z_{t-1}):
-//       dalpha_t = <lamS_t, S_{t-1}>,  deta_t = -<lamS_t, Z_t> = -(beta_t <lamS_t, Z_{t-1}> + <lamS_t, g_t>),
-//       dbeta_t = <lamZ_t, Z_{t-1}>,   dw[t][j] = <lamZ_t, G_{t-j}>;
+// Reverse pass, chunk c (targets t = 0 .. 63, sources s = 0 .. 79 at tokens t0 - 16 + s), with
+// Lam = (lamS, lamZ) the adjoint of (S, Z) after the chunk's last token:
+//   dpsi_t  = S_{t-1}^T dy_t = At S_c^T dy_t + Kt Z_c^T dy_t + sum_s R[s][t] phi_s
+//   ddelta_s = sum_t Q[s][t] dy_t + cs_s lamS phi_s + cz_s lamZ phi_s
+//   dphi_s  = sum_t R[s][t] psi_t + cs_s lamS^T delta_s + cz_s lamZ^T delta_s + S_ref^T ddelta_s
+//   with K[s][t] = phi_s . psi_t, Dd[s][t] = delta_s . dy_t, Wy[s][t] the coefficient of
+//   G_s = delta_s phi_s^T in S_{t-1} (the window band times C', C'[r][t] the coefficient of g_r in
+//   S_{t-1}), Q = K o Wy, R = Dd o Wy, cs / cz the coefficients of G_s in S / Z at the chunk end;
+// the scalar gradients are inner products of the adjoint at t with the state at t - 1, both
+//   combinations of a few bases: adjoint bases E_q = dy_q psi_q^T (q > t) and the end adjoint;
+//   state bases G_s, S_c, Z_c. With their Gram matrix M on the matrix cores:
+//     dalpha_t = <lamS_t, S_{t-1}>,  deta_t = -(beta_t <lamS_t, Z_{t-1}> + <lamS_t, g_t>),
+//     dbeta_t = <lamZ_t, Z_{t-1}>,   dw[t][j] = <lamZ_t, G_{t-j}>;
 //   then Lam <- T_c^T Lam + sum_t (At, Kt) E_t.
 // The halo sources of chunk c are the last 16 tokens of chunk c - 1: their partial gradients stay
 // in the registers of the lanes that hold those tokens' rows in the next step.
@@ -44,17 +41,17 @@ __device__ __forceinline__ int fresh_tid() { return launder((int)threadIdx.x); }
   const int tid = fresh_tid(), lane = tid & 63, gq = lane >> 4, m = lane & 15; \
   (void)tid; (void)lane; (void)gq; (void)m;
 constexpr int NWB = NTB / 64;
-constexpr int PB = 72;    // LDS pitch (bf16 elements) of 64-wide rows
+constexpr int PB = 72;    // LDS pitch (bf16 elements) of 64-wide rows (16-byte aligned rows)
 constexpr int QP = 88;    // pitch of the Q^T / R^T rows [t][s] (80 sources + 8)
-constexpr int MP = 104;   // pitch of the Gram rows [q][s'] (96 state bases + 8)
+// pitch of the Gram rows [q][s'] (96 state bases: 80 products, S_c, Z_c, zeros; + 8: 52 dwords, so
+// that the rows of 16 lanes fall on distinct banks)
+constexpr int MQ = 104;
+constexpr int QX = CL + 16;   // Gram rows: 64 adjoint bases E_q, then the chunk-end adjoint's partials
 constexpr int EMAX = 17;  // window
 // chunk coefficient record (floats): cs, cz (sources), cgS, cgZ (targets), the chunk transition
 constexpr int R_CS = 0, R_CZ = SRC, R_GS = 2 * SRC, R_GZ = 2 * SRC + CL, R_TR = 2 * SRC + 2 * CL;
 constexpr int REC = R_TR + 4;   // 292
 static_assert(REC <= NTB, "one record element per thread");
-// workspace per chunk between the passes: S_c^T, Z_c^T (bf16) and the coefficient record
-constexpr size_t kXsStates = (size_t)2 * D * D * 2;
-constexpr size_t kXsBytes = kXsStates + ((REC * 4 + 255) / 256) * 256;
 
 struct BwSm;
 struct BwSm {
@@ -66,18 +63,19 @@ struct BwSm {
   alignas(16) bf16 XL[2][D][PB];     // lamS^T, lamZ^T ([k][i])
   alignas(16) bf16 Qt[CL][QP];       // Q[s][t] stored [t][s]
   alignas(16) bf16 Rt[CL][QP];
-  alignas(16) bf16 Mt[CL][MP];       // Gram M[q][s'] (q: adjoint basis E_q; s' < 80: G_s, 80: S_c, 81: Z_c)
+  // Gram M[q][s'] of adjoint bases q and state bases s' (s' < 80: G_s; 80: S_c; 81: Z_c; rest zero).
+  // Rows q < 64: E_q = dy_q psi_q^T. Rows 64 + ct / 68 + ct: lamS / lamZ (the adjoint after the
+  // chunk) restricted to the state columns of tile ct (partials summed by the products that read
+  // them), their S_c / Z_c entries in rows 64 / 68 only. Rows 72 .. 79 zero.
+  alignas(16) bf16 Mt[QX][MQ];
   alignas(16) bf16 Cb[CL][PB];       // C'[r][t]: of g_r in S_{t-1} (r, t chunk-local targets)
   alignas(16) float co[REC];
   alignas(16) float la[CL], lb[CL], eta[CL], At[CL], Kt[CL], B1[CL], be[CL];
-  float hp[2][4][SRC];               // hS / hZ partials by column tile
   float gram[NWB][4];
   // the window band Bd[s][r] = w(r, r + HT - s) (0 <= r + HT - s < e; zero elsewhere): the weight of
   // source s in the window of target r, i.e. of lag j = r + HT - s (w: the lag gate, the token gate
   // of the source, or 1; zero for targets past T)
   alignas(16) bf16 Bd[SRC][PB];
-  // end terms of ddelta / dphi (waves 4-7), bf16 pairs in the accumulator layout: [ct][st][pair][lane]
-  unsigned ed[4][SRC / 16][2][64], ef[4][SRC / 16][2][64];
 };
 
 static_assert(sizeof(BwSm) <= 160 * 1024, "one workgroup per CU: at most 160 KB of LDS");
@@ -86,8 +84,7 @@ static_assert(sizeof(BwSm) <= 160 * 1024, "one workgroup per CU: at most 160 KB 
 // = w + 8 u of wave w. j < 10: phi rows t0 - 16 + 8 j ..; < 20: v rows; < 28: psi rows t0 + ..; < 36:
 // dy rows. The kind of a wave-load is uniform over the wave (scalar branches; the rows before token
 // 0 read as zeros: their offsets lie outside the buffer resource).
-constexpr int WL_F = 2 * SRC / 8;            // 20: phi, v [forward pass]
-constexpr int WL_R = WL_F + 2 * CL / 8;      // 36: + psi, dy [reverse pass]
+constexpr int WL_R = 2 * SRC / 8 + 2 * CL / 8;   // 36: phi, v, psi, dy
 template <int NWL>
 struct RowPf { u32x4v v[(NWL + NWB - 1) / NWB]; };
 
@@ -137,16 +134,17 @@ __device__ __forceinline__ float* part_row(float* base, int bh, int nseg, int se
   return base + ((size_t)bh * nseg + seg) * H * (2 * D);
 }
 
-// the chunk's scalars (wave 0: lane = target) and gates (raw bf16 bits)
+// the chunk's scalars (waves 0, 1: lane = target) and gates (raw bf16 bits)
 struct ScalPf {
   unsigned short al, et, be;
   unsigned short gt[3];
 };
 __device__ __forceinline__ void scal_load(ScalPf& p, const Geom& g, const BwdPtrs<bf16>& a, size_t rowbase, int t0) {
   const int tid = fresh_tid();
+  // waves 0 and 1 (lane = target): the prefix arrays and the end record are formed from them
   p.al = 0x3f80; p.et = 0; p.be = 0x3f80;   // 1, 0, 1 (the identity past T)
-  if (tid < 64 && t0 + tid < g.T) {
-    const size_t o = rowbase + t0 + tid;
+  if (tid < 128 && t0 + (tid & 63) < g.T) {
+    const size_t o = rowbase + t0 + (tid & 63);
     p.al = __builtin_bit_cast(unsigned short, a.decay[o]);
     p.et = __builtin_bit_cast(unsigned short, a.lr[o]);
     p.be = g.momentum ? __builtin_bit_cast(unsigned short, a.beta[o]) : (unsigned short)0;
@@ -213,20 +211,22 @@ __device__ __forceinline__ void chunk_end_scan(const Geom& g, const ScalPf& p, i
   if (lane == 63) { sm.co[R_TR] = inc.a; sm.co[R_TR + 1] = inc.k; sm.co[R_TR + 2] = inc.b; sm.co[R_TR + 3] = 0.f; }
 }
 // threads < 80: the per-source end coefficients from cgS / cgZ (needs chunk_end_scan's output)
-__device__ __forceinline__ void chunk_end_sources(const Geom& g, BwSm& sm) {
-  const int s = fresh_tid();
-  if (s < SRC) {
-    float cs = 0.f, cz = 0.f;
-    for (int j = 0; j < g.e; ++j) {
+__device__ __forceinline__ void chunk_end_sources(const Geom& g, BwSm& sm, int i) {
+  // i < 80: cs of source s = i (through cgS); 80 <= i < 160: cz of source s = i - 80 (through cgZ).
+  // cs_s = sum_j w(s - HT + j, j) cgS[s - HT + j] = sum over the band row Bd[s][r] (zero off the
+  // window): the 17 targets r = s - 16 .. s, loads unconditional (clamped), no branches
+  if (i >= 0 && i < 2 * SRC) {
+    const int zc = i >= SRC, s = zc ? i - SRC : i;
+    const float* cg = &sm.co[zc ? R_GZ : R_GS];
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < EMAX; ++j) {
       const int r = s - HT + j;
-      if (r >= 0 && r < CL) {
-        const float wgt = cw(sm, r, j);
-        cs += wgt * sm.co[R_GS + r];
-        cz += wgt * sm.co[R_GZ + r];
-      }
+      const int rc = min(max(r, 0), CL - 1);
+      const float x = static_cast<float>(sm.Bd[s][rc]) * cg[rc];
+      acc += (r >= 0 && r < CL) ? x : 0.f;
     }
-    sm.co[R_CS + s] = cs;
-    sm.co[R_CZ + s] = cz;
+    sm.co[(zc ? R_CZ : R_CS) + s] = acc;
   }
 }
 
@@ -253,9 +253,9 @@ __device__ __forceinline__ float wave_sum(float x) { return xsum_rows(row_sum16(
 __device__ __forceinline__ unsigned pk(float a, float b) { return pack_bf16x2(a, b); }
 // v stored at byte offset off (32-bit) from a uniform base: one store with a scalar base and a 32-bit
 // vector offset instead of per-lane 64-bit address arithmetic
-template <typename T>
-__device__ __forceinline__ void st_at(T* base, uint32_t off, T v) {
-  *reinterpret_cast<T*>(reinterpret_cast<unsigned char*>(base) + off) = v;
+template <typename B, typename V>
+__device__ __forceinline__ void st_at(B* base, uint32_t off, V v) {
+  *reinterpret_cast<V*>(reinterpret_cast<unsigned char*>(base) + off) = v;
 }
 __device__ __forceinline__ float lo16(unsigned u) { return __builtin_bit_cast(float, u << 16); }
 __device__ __forceinline__ float hi16(unsigned u) { return __builtin_bit_cast(float, u & 0xffff0000u); }
@@ -302,106 +302,25 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
 
   // the band's entries off the window stay zero; its window entries are rewritten for every chunk
   for (int i = tid; i < SRC * PB / 2; i += NTB) reinterpret_cast<unsigned*>(&sm.Bd[0][0])[i] = 0u;
+  // the Gram's entries that are never written stay zero
+  for (int i = tid; i < QX * MQ / 2; i += NTB) reinterpret_cast<unsigned*>(&sm.Mt[0][0])[i] = 0u;
   __syncthreads();
-  // ---------------------------------------------------------------- forward pass over the segment
-  float xS[2][4], xZ[2][4];
-  {
-    const float* ss = p.seg_states + ((size_t)bh * sg.nseg + seg) * 2 * DD;
+  // chunk-start states saved by the forward walk (walk_common.h fragment layout), one block per
+  // 64-token chunk of the row: this lane's slice X[16 q4 + 4 gq + r][16 kt + m] (kt = 2 hf + j) is
+  // one 8-byte half of fragment (kt, q4 >> 1)
+  const unsigned char* xrow = reinterpret_cast<const unsigned char*>(p.rw) + (size_t)bh * g.nc * kStateBlk;
+  auto xs_load = [&](int c, unsigned (&xv)[8]) {
+    const unsigned char* blk = xrow + (size_t)c * kStateBlk;
+    const int ln = fresh_tid() & 63;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int off = (16 * q4 + 4 * gq + r) * D + 16 * (2 * hf + j) + m;
-        xS[j][r] = ss[off];
-        xZ[j][r] = MOM ? ss[DD + off] : 0.f;
-      }
-  }
-  // per chunk of the segment: its chunk-start state (S_c^T, Z_c^T as bf16 [k][i], the LDS layout of
-  // XS) and its coefficient record, kept in the workspace between the two passes
-  unsigned char* xs_seg = reinterpret_cast<unsigned char*>(p.xsave) + ((size_t)bh * sg.nseg + seg) * sg.G * kXsBytes;
-  {
-    RowPf<WL_F> pf;
-    ScalPf sp;
-    rows_load<WL_F>(pf, rk, rv, rq, rdy, c_begin * CL, w);
-    scal_load(sp, g, a, rowbase, c_begin * CL);
-#pragma unroll 1
-    for (int cc = 0; cc < c_end - c_begin; ++cc) {
-      const int c = c_begin + cc;
-      {
-        CPB_FRESH_LANE
-        const int t0 = c * CL;
-        if (cc > 0) __syncthreads();
-        rows_store<MAPE, WL_F>(pf, sm, g.map_deg, w);
-        gates_store(sp, g, sm);
-        const ScalPf spc = sp;
-        if (c + 1 < c_end) {
-          rows_load<WL_F>(pf, rk, rv, rq, rdy, t0 + CL, w);
-          scal_load(sp, g, a, rowbase, t0 + CL);
-        } else {
-          pf = RowPf<WL_F>{};
-          sp = ScalPf{};
-        }
-        __syncthreads();
-        if (w == 0) chunk_end_scan(g, spc, t0, sm);
-        // delta[s][i] for this wave's rows i (tiles of 16 sources)
-        f32x4 dl[SRC / 16];
-#pragma unroll
-        for (int st = 0; st < SRC / 16; ++st) {
-          dl[st] = zero4();
-#pragma unroll
-          for (int q = 0; q < 2; ++q) dl[st] = mma_bf16(frag_row_l(&sm.phi[0][0], PB, 16 * st, 32 * q, lane), sref[q], dl[st]);
-          const s16x4 vt = tr4_l(&sm.vd[0][0], PB, 16 * st, 16 * q4, lane);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) dl[st][r] -= bf((unsigned short)vt[r]);
-        }
-        __syncthreads();
-        chunk_end_sources(g, sm);
-        __syncthreads();
-        unsigned char* xsc = xs_seg + (size_t)cc * kXsBytes;
-        if (tid < REC) reinterpret_cast<float*>(xsc + kXsStates)[tid] = sm.co[tid];
-        f32x4 U[2], V[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) { U[j] = zero4(); V[j] = zero4(); }
-#pragma unroll
-        for (int q = 0; q < 3; ++q) {
-          const float4 chi = *reinterpret_cast<const float4*>(&sm.co[R_CS + 32 * q + 4 * gq]);
-          const float4 zhi = *reinterpret_cast<const float4*>(&sm.co[R_CZ + 32 * q + 4 * gq]);
-          float4 clo = make_float4(0.f, 0.f, 0.f, 0.f), zlo = clo;
-          if (q < 2) {
-            clo = *reinterpret_cast<const float4*>(&sm.co[R_CS + 32 * q + 16 + 4 * gq]);
-            zlo = *reinterpret_cast<const float4*>(&sm.co[R_CZ + 32 * q + 16 + 4 * gq]);
-          }
-          const f32x4 lo = q < 2 ? dl[2 * q + 1] : zero4();
-          const bf16x8 fs = pack_frag_scaled(dl[2 * q], lo, chi, clo);
-          const bf16x8 fz = pack_frag_scaled(dl[2 * q], lo, zhi, zlo);
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int kt = 2 * hf + j;
-            const bf16x8 fb = q < 2 ? tr_pair_l<true>(&sm.phi[0][0], PB, q, 16 * kt, lane) : tr_pair_l<false>(&sm.phi[0][0], PB, q, 16 * kt, lane);
-            U[j] = mma_bf16(fs, fb, U[j]);
-            V[j] = mma_bf16(fz, fb, V[j]);
-          }
-        }
-        const float ta = sm.co[R_TR], tk = sm.co[R_TR + 1], tb = sm.co[R_TR + 2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int kt = 2 * hf + j;
-          const size_t o = ((size_t)(16 * kt + m) * D + 16 * q4 + 4 * gq) * 2;
-          *reinterpret_cast<uint2*>(xsc + o) = make_uint2(pk(xS[j][0], xS[j][1]), pk(xS[j][2], xS[j][3]));
-          *reinterpret_cast<uint2*>(xsc + DD * 2 + o) = make_uint2(pk(xZ[j][0], xZ[j][1]), pk(xZ[j][2], xZ[j][3]));
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float sn = ta * xS[j][r] + tk * xZ[j][r] + U[j][r];
-            xZ[j][r] = MOM ? tb * xZ[j][r] + V[j][r] : 0.f;
-            xS[j][r] = sn;
-          }
-        }
-      }
+    for (int jj = 0; jj < 2; ++jj) {
+      const uint32_t o = frag_off(2 * hf + jj, q4 >> 1, ln) + (q4 & 1) * 8;
+      const uint2 s2 = *reinterpret_cast<const uint2*>(blk + o);
+      const uint2 z2 = *reinterpret_cast<const uint2*>(blk + kStateBytes + o);
+      xv[4 * jj + 0] = s2.x; xv[4 * jj + 1] = s2.y;
+      xv[4 * jj + 2] = MOM ? z2.x : 0u; xv[4 * jj + 3] = MOM ? z2.y : 0u;
     }
-  }
+  };
 
   // ---------------------------------------------------------------- reverse pass
   float lS[2][4], lZ[2][4];
@@ -422,37 +341,30 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
   f32x4 dsr[4];             // dS_ref partial (waves 0-3: rows 16 q4 .., column tiles kt)
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt) dsr[kt] = zero4();
-  // Gram columns 82 .. 103 stay zero
-  for (int i = tid; i < CL * (MP - 82); i += NTB) sm.Mt[i / (MP - 82)][82 + i % (MP - 82)] = static_cast<bf16>(0.f);
 
   RowPf<WL_R> pf;
   ScalPf sp;
+  unsigned xn[8];   // the next chunk's state slice, in flight with its rows
   rows_load<WL_R>(pf, rk, rv, rq, rdy, (c_end - 1) * CL, w);
   scal_load(sp, g, a, rowbase, (c_end - 1) * CL);
+  xs_load(c_end - 1, xn);
 #pragma unroll 1
   for (int cr = c_end - c_begin - 1; cr >= 0; --cr) {
     CPB_FRESH_LANE
     const int c = c_begin + cr;
     const int t0 = c * CL;
-    const unsigned char* xsc = xs_seg + (size_t)cr * kXsBytes;
-    // this wave's slice of X_c (for the Grams) and the record
+    // this wave's slice of X_c (for the Grams and the LDS copy)
     unsigned xc[8];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int kt = 2 * hf + j;
-      const size_t o = ((size_t)(16 * kt + m) * D + 16 * q4 + 4 * gq) * 2;
-      const uint2 a0 = *reinterpret_cast<const uint2*>(xsc + o);
-      const uint2 a1 = *reinterpret_cast<const uint2*>(xsc + DD * 2 + o);
-      xc[4 * j + 0] = a0.x; xc[4 * j + 1] = a0.y; xc[4 * j + 2] = a1.x; xc[4 * j + 3] = a1.y;
-    }
-    const float rc = tid < REC ? reinterpret_cast<const float*>(xsc + kXsStates)[tid] : 0.f;
+    for (int v = 0; v < 8; ++v) xc[v] = xn[v];
     const bool seg_last = c == c_end - 1, seg_first = c == c_begin;
+    const bool interior = !seg_last && !seg_first;   // uniform: the stores take no per-row tests
     // ---- R0: stage the chunk
     __syncthreads();
     rows_store<MAPE, WL_R>(pf, sm, g.map_deg, w);
     gates_store(sp, g, sm);
     if (w == 0) chunk_prefix(sp, sm);
-    if (tid < REC) sm.co[tid] = rc;
+    if (w == 1) chunk_end_scan(g, sp, t0, sm);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int kt = 2 * hf + j;
@@ -507,10 +419,19 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
 #pragma unroll
         for (int r = 0; r < 4; ++r) sm.Cb[16 * q4 + 4 * gq + r][16 * tt + m] = static_cast<bf16>(acc[r]);
       }
+      chunk_end_sources(g, sm, tid - 256);   // threads 256 .. 415: cs, cz of the chunk's sources
+      if (tid < 4) {   // <lamS, S_c>, <lamS, Z_c>, <lamZ, S_c>, <lamZ, Z_c> into the end rows
+        float gsum = 0.f;
+#pragma unroll
+        for (int u = 0; u < NWB; ++u) gsum += sm.gram[u][tid];
+        sm.Mt[tid < 2 ? CL : CL + 4][SRC + (tid & 1)] = static_cast<bf16>(gsum);
+      }
     }
     __syncthreads();
 
     // ---- R2: t-phase (waves 0-3) | end terms of ddelta / dphi (waves 4-7)
+    // the end terms (waves 4-7), bf16 pairs in the accumulator layout, used in R3 / R4
+    unsigned edr[SRC / 16][2], efr[SRC / 16][2];
     if (hf == 0) {
       CPB_FRESH_LANE
       const int tt = q4;
@@ -583,36 +504,41 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
       }
     } else {
       CPB_FRESH_LANE
+      // transposed tiles: rows i (or k) = 16 ct + 4 gq + r, columns s = 16 st + m
       const int ct = q4;
+      bf16x8 ones;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ones[e] = static_cast<bf16>(1.f);
 #pragma unroll
       for (int st = 0; st < SRC / 16; ++st) {
         f32x4 es = zero4(), ez = zero4(), fs = zero4(), fz = zero4();
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           const bf16x8 fp = frag_row_l(&sm.phi[0][0], PB, 16 * st, 32 * q, lane);
-          es = mma_bf16(fp, frag_tr_l(&sm.XL[0][0][0], PB, 16 * ct, 32 * q, lane), es);
-          ez = mma_bf16(fp, frag_tr_l(&sm.XL[1][0][0], PB, 16 * ct, 32 * q, lane), ez);
+          es = mma_bf16(frag_tr_l(&sm.XL[0][0][0], PB, 16 * ct, 32 * q, lane), fp, es);   // (lamS phi_s)[i]
+          ez = mma_bf16(frag_tr_l(&sm.XL[1][0][0], PB, 16 * ct, 32 * q, lane), fp, ez);
           const bf16x8 fd = frag_row_l(&sm.vd[0][0], PB, 16 * st, 32 * q, lane);
-          fs = mma_bf16(fd, frag_row_l(&sm.XL[0][0][0], PB, 16 * ct, 32 * q, lane), fs);
-          fz = mma_bf16(fd, frag_row_l(&sm.XL[1][0][0], PB, 16 * ct, 32 * q, lane), fz);
+          fs = mma_bf16(frag_row_l(&sm.XL[0][0][0], PB, 16 * ct, 32 * q, lane), fd, fs);   // (lamS^T delta_s)[k]
+          fz = mma_bf16(frag_row_l(&sm.XL[1][0][0], PB, 16 * ct, 32 * q, lane), fd, fz);
         }
-        const s16x4 dt = tr4_l(&sm.vd[0][0], PB, 16 * st, 16 * ct, lane);
-        const float4 cs4 = *reinterpret_cast<const float4*>(&sm.co[R_CS + 16 * st + 4 * gq]);
-        const float4 cz4 = *reinterpret_cast<const float4*>(&sm.co[R_CZ + 16 * st + 4 * gq]);
-        const float csv[4] = {cs4.x, cs4.y, cs4.z, cs4.w}, czv[4] = {cz4.x, cz4.y, cz4.z, cz4.w};
-        float ev[4], fv[4];
+        // hS[s] = delta_s . (lamS phi_s): this wave's 16 rows i summed on the matrix cores (every
+        // output row holds the column sums); the four column tiles are the Gram's end-row partials
+        const float4 dl = lds_bf16x4(&sm.vd[16 * st + m][16 * ct + 4 * gq]);
+        const float dv4[4] = {dl.x, dl.y, dl.z, dl.w};
+        f32x4 ps, pz;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float dv = bf((unsigned short)dt[r]);
-          const float hs = row_sum16(dv * es[r]), hz = row_sum16(dv * ez[r]);
-          if (m == 0) { sm.hp[0][ct][16 * st + 4 * gq + r] = hs; sm.hp[1][ct][16 * st + 4 * gq + r] = hz; }
-          ev[r] = csv[r] * es[r] + czv[r] * ez[r];
-          fv[r] = csv[r] * fs[r] + czv[r] * fz[r];
+        for (int r = 0; r < 4; ++r) { ps[r] = dv4[r] * es[r]; pz[r] = dv4[r] * ez[r]; }
+        const f32x4 hs = mma_bf16(ones, pack_frag(ps, zero4()), zero4());
+        const f32x4 hz = mma_bf16(ones, pack_frag(pz, zero4()), zero4());
+        if (gq == 0) {
+          sm.Mt[CL + ct][16 * st + m] = static_cast<bf16>(hs[0]);
+          sm.Mt[CL + 4 + ct][16 * st + m] = static_cast<bf16>(hz[0]);
         }
-        sm.ed[ct][st][0][lane] = pk(ev[0], ev[1]);
-        sm.ed[ct][st][1][lane] = pk(ev[2], ev[3]);
-        sm.ef[ct][st][0][lane] = pk(fv[0], fv[1]);
-        sm.ef[ct][st][1][lane] = pk(fv[2], fv[3]);
+        const float cs = sm.co[R_CS + 16 * st + m], cz = sm.co[R_CZ + 16 * st + m];
+        edr[st][0] = pk(cs * es[0] + cz * ez[0], cs * es[1] + cz * ez[1]);
+        edr[st][1] = pk(cs * es[2] + cz * ez[2], cs * es[3] + cz * ez[3]);
+        efr[st][0] = pk(cs * fs[0] + cz * fz[0], cs * fs[1] + cz * fz[1]);
+        efr[st][1] = pk(cs * fs[2] + cz * fz[2], cs * fs[3] + cz * fz[3]);
       }
     }
     __syncthreads();
@@ -628,137 +554,192 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
       for (int st = 0; st < SRC / 16; ++st) {
         f32x4 acc;
         {
-          const unsigned e0 = sm.ed[ct][st][0][lane], e1 = sm.ed[ct][st][1][lane];
+          const unsigned e0 = edr[st][0], e1 = edr[st][1];
           acc[0] = lo16(e0); acc[1] = hi16(e0); acc[2] = lo16(e1); acc[3] = hi16(e1);
         }
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
-          acc = mma_bf16(frag_tr_l(&sm.Qt[0][0], QP, 16 * st, 32 * q, lane),
-                         frag_tr_l(&sm.dy[0][0], PB, 16 * ct, 32 * q, lane), acc);
+        for (int q = 0; q < 2; ++q)   // ddelta^T[i][s] = sum_t dy[t][i] Q[s][t] (+ the end terms)
+          acc = mma_bf16(frag_tr_l(&sm.dy[0][0], PB, 16 * ct, 32 * q, lane),
+                         frag_tr_l(&sm.Qt[0][0], QP, 16 * st, 32 * q, lane), acc);
+        // this lane: source s = 16 st + m, columns col0 .. col0 + 3
+        const int s = 16 * st + m, pp = t0 - HT + s, col0 = 16 * ct + 4 * gq;
+        store4<bf16>(&sm.vd[s][col0], acc[0], acc[1], acc[2], acc[3]);
+        float val[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int s = 16 * st + 4 * gq + r;
-          const float dd = acc[r];   // ddelta
-          sm.vd[s][16 * ct + m] = static_cast<bf16>(dd);
-          const int pp = t0 - HT + s, col = 16 * ct + m;
-          if (st == 0) {   // halo rows: partial for the previous chunk (or the previous segment)
-            if (seg_first) {
-              if (seg > 0 && s >= HT - H)
-                st_at(part_row(p.halo_part, bh, sg.nseg, seg, H), (uint32_t)(((s - (HT - H)) * (2 * D) + col) * 4), -dd);
-            } else {
-              cdv[r] = -dd;
+        for (int r = 0; r < 4; ++r) val[r] = -acc[r];
+        if (interior) {   // no segment boundary, no tail rows, every row < T
+          if (st == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cdv[r] = val[r];
+          } else {
+            if (st == SRC / 16 - 1)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) val[r] += cin[r];
+            st_at(a.dv + rowbase * D, (uint32_t)((pp * D + col0) * 2), make_uint2(pk(val[0], val[1]), pk(val[2], val[3])));
+          }
+        } else if (st == 0) {   // halo rows: partial for the previous chunk (or the previous segment)
+          if (seg_first) {
+            if (seg > 0 && s >= HT - H)
+              st_at(part_row(p.halo_part, bh, sg.nseg, seg, H), (uint32_t)(((s - (HT - H)) * (2 * D) + col0) * 4),
+                    make_float4(val[0], val[1], val[2], val[3]));
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cdv[r] = val[r];
+          }
+        } else if (pp < g.T) {
+          if (st == SRC / 16 - 1 && !seg_last)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) val[r] += cin[r];
+          if (pp >= tail0)
+            st_at(part_row(p.tail_part, bh, sg.nseg, seg, H), (uint32_t)(((pp - tail0) * (2 * D) + col0) * 4),
+                  make_float4(val[0], val[1], val[2], val[3]));
+          else
+            st_at(a.dv + rowbase * D, (uint32_t)((pp * D + col0) * 2), make_uint2(pk(val[0], val[1]), pk(val[2], val[3])));
+        }
+      }
+      // the window gradients dw[t][j] = <lamZ_t, G_{t-j}> = (Km M)[t][t + HT - j] (this half's
+      // share of the scalar phase): the state-base tiles tt and tt + 1 hold the band of the
+      // targets t = 16 tt + 4 gq + r
+      if (g.gate_mode != GATE_NONE) {
+        const int tt = q4, tl = 16 * tt + m;
+        const float cgs = sm.co[R_GS + tl], cgz = sm.co[R_GZ + tl];
+        bf16x8 kme;   // Km over the end rows (k = 64 + 8 gq + e): cgS on the lamS partials, cgZ on lamZ's
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kme[e] = static_cast<bf16>(gq == 0 ? (e < 4 ? cgs : cgz) : 0.f);
+        const bf16x8 km0 = frag_row_l(&sm.Cb[0][0], PB, 16 * tt, 0, lane);
+        const bf16x8 km1 = frag_row_l(&sm.Cb[0][0], PB, 16 * tt, 32, lane);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int sp = tt + h;
+          f32x4 rz = zero4();
+          rz = mma_bf16(km0, frag_tr_l(&sm.Mt[0][0], MQ, 16 * sp, 0, lane), rz);
+          rz = mma_bf16(km1, frag_tr_l(&sm.Mt[0][0], MQ, 16 * sp, 32, lane), rz);
+          // rows 64 .. 79 only (lanes 0 .. 31 address them; the others' k slots carry zero weights)
+          const bf16x8 me = frag_tr_l(&sm.Mt[0][0], MQ, 16 * sp, 64 - 16 * (gq >> 1), lane);
+          rz = mma_bf16(kme, gq < 2 ? me : zero_frag(), rz);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = 16 * tt + 4 * gq + r, sq = 16 * sp + m;
+            const int jb = t + HT - sq;
+            if (jb >= 0 && jb < g.e && t0 + t < g.T) {
+              const uint32_t o = (uint32_t)((t0 + t) * g.e + jb);
+              if (g.gate_mode == GATE_LAG) st_at(a.dgate + rowbase * g.e, o * 2, static_cast<bf16>(rz[r]));
+              else st_at(p.dw + rowbase * g.e, o * 4, rz[r]);
             }
-          } else if (pp < g.T) {
-            float val = -dd + (st == SRC / 16 - 1 && !seg_last ? cin[r] : 0.f);
-            if (pp >= tail0)
-              st_at(part_row(p.tail_part, bh, sg.nseg, seg, H), (uint32_t)(((pp - tail0) * (2 * D) + col) * 4), val);
-            else
-              st_at(a.dv + rowbase * D, (uint32_t)((pp * D + col) * 2), static_cast<bf16>(val));
           }
         }
       }
     } else {
       CPB_FRESH_LANE
       const int tt = q4;
-      float al[4] = {0.f, 0.f, 0.f, 0.f}, ea[4] = {0.f, 0.f, 0.f, 0.f}, eb[4] = {0.f, 0.f, 0.f, 0.f},
-            bt[4] = {0.f, 0.f, 0.f, 0.f};
-      const float gSS = sm.gram[0][0] + sm.gram[1][0] + sm.gram[2][0] + sm.gram[3][0] + sm.gram[4][0] + sm.gram[5][0] +
-                        sm.gram[6][0] + sm.gram[7][0];
-      const float gSZ = sm.gram[0][1] + sm.gram[1][1] + sm.gram[2][1] + sm.gram[3][1] + sm.gram[4][1] + sm.gram[5][1] +
-                        sm.gram[6][1] + sm.gram[7][1];
-      const float gZS = sm.gram[0][2] + sm.gram[1][2] + sm.gram[2][2] + sm.gram[3][2] + sm.gram[4][2] + sm.gram[5][2] +
-                        sm.gram[6][2] + sm.gram[7][2];
-      const float gZZ = sm.gram[0][3] + sm.gram[1][3] + sm.gram[2][3] + sm.gram[3][3] + sm.gram[4][3] + sm.gram[5][3] +
-                        sm.gram[6][3] + sm.gram[7][3];
-      // adjoint-coefficient operands (rows t = 16 tt + m, k = q natural): Am (decay), Km (C'); the
-      // state-coefficient operands over the targets r (rows t): C'^T (of G_s in S_{t-1} through the
-      // window: Wy = Band C'), B'^T (in Z_{t-1}: Wzy = Band B')
-      bf16x8 fam[2], fzT[2];
+      // The scalar gradients of target t = 16 tt + (lane & 15):
+      //   dalpha_t = <lamS_t, S_{t-1}>, deta_t = -(beta_t <lamS_t, Z_{t-1}> + <lamS_t, g_t>),
+      //   dbeta_t = <lamZ_t, Z_{t-1}>, dw[t][j] = <lamZ_t, G_{t-j}>,
+      // with lamS_t = sum_q Am[t][q] E_q (q over the adjoint bases, the end rows included) and the
+      // total lamZ_t = sum_q Km[t][q] E_q; S_{t-1} = sum_s' Wy~[s'][t] X_s', Z_{t-1} = sum_s' Wz~[s'][t] X_s'
+      // over the state bases X_s'. So dalpha_t = sum_q Am[t][q] (M Wy~)[q][t]: the products M Wy~,
+      // M Wz~ and M Band (for <lamS_t, g_t>) on the matrix cores, then one weighted sum over q.
+      const bf16x8 fcb0 = frag_tr_l(&sm.Cb[0][0], PB, 16 * tt, 0, lane);
+      const bf16x8 fcb1 = frag_tr_l(&sm.Cb[0][0], PB, 16 * tt, 32, lane);
+      // Wy~ = Band C' (+ At, Kt in rows 80, 81) and Wz~ = Band B' (+ B1 in row 81): tiles of 16 state
+      // bases (rows) by this wave's targets (columns), packed in pairs as the k-chained operands
+      bf16x8 wyp[3], wzp[3];
       {
-        const int t = 16 * tt + m;
-        const float lat = sm.la[t];
+        const bf16x8 fz0 = gen_zcoef<MOM>(sm.lb, 16 * tt + m, 0, lane);
+        const bf16x8 fz1 = gen_zcoef<MOM>(sm.lb, 16 * tt + m, 1, lane);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int i = 0; i < 3; ++i) {
+          f32x4 y[2], z[2];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int qq = 32 * q + 8 * gq + e;
-            const float x = __builtin_amdgcn_exp2f(sm.la[qq > 0 ? qq - 1 : 0] - lat);
-            fam[q][e] = static_cast<bf16>(qq > t ? x : 0.f);
+          for (int h = 0; h < 2; ++h) {
+            const int st = 2 * i + h;
+            y[h] = zero4();
+            z[h] = zero4();
+            // the band of source tile st meets k half 0 for st <= 2, half 1 for 2 <= st <= 4
+            if (st <= 2) {
+              const bf16x8 fb = frag_row_l(&sm.Bd[0][0], PB, 16 * st, 0, lane);
+              y[h] = mma_bf16(fb, fcb0, y[h]);
+              z[h] = mma_bf16(fb, fz0, z[h]);
+            }
+            if (st >= 2 && st <= 4) {
+              const bf16x8 fb = frag_row_l(&sm.Bd[0][0], PB, 16 * st, 32, lane);
+              y[h] = mma_bf16(fb, fcb1, y[h]);
+              z[h] = mma_bf16(fb, fz1, z[h]);
+            }
           }
-          fzT[q] = gen_zcoef<MOM>(sm.lb, t, q, lane);
+          if (i == 2 && gq == 0) {   // rows 80 (S_c), 81 (Z_c) of tile 5
+            const int t = 16 * tt + m;
+            y[1][0] = sm.At[t];
+            y[1][1] = sm.Kt[t];
+            z[1][1] = sm.B1[t];
+          }
+          wyp[i] = pack_frag(y[0], y[1]);
+          wzp[i] = pack_frag(z[0], z[1]);
         }
       }
-      // per target row r of this lane: the end terms' coefficients (A(t -> 63); cgS, cgZ from the record)
-      float aend[4];
+      // Band as the k-chained operand over the state bases (rows 80 .. 95 zero)
+      const bf16x8 bdp0 = tr_pair_l<true>(&sm.Bd[0][0], PB, 0, 16 * tt, lane);
+      const bf16x8 bdp1 = tr_pair_l<true>(&sm.Bd[0][0], PB, 1, 16 * tt, lane);
+      const bf16x8 bdp2 = tr_pair_l<false>(&sm.Bd[0][0], PB, 2, 16 * tt, lane);
+      const int tl = 16 * tt + m;   // this lane's target (accumulator column)
+      const float lat = sm.la[tl];
+      const float aend = __builtin_amdgcn_exp2f(sm.la[CL - 1] - lat);
+      const float cgs = sm.co[R_GS + tl], cgz = sm.co[R_GZ + tl];
+      float al = 0.f, ea = 0.f, eb = 0.f, bt = 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) aend[r] = __builtin_amdgcn_exp2f(sm.la[CL - 1] - sm.la[16 * tt + 4 * gq + r]);
-      // state bases s' = 16 sp2 + m: the products G_s (s' < 80), then S_c (80), Z_c (81)
-#pragma unroll 1
-      for (int sp2 = 0; sp2 < SRC / 16; ++sp2) {
-        f32x4 ra = zero4(), rz = zero4(), wy = zero4(), wz = zero4();
+      for (int qt = 0; qt < QX / 16; ++qt) {
+        // M rows q = 16 qt + (lane & 15) as the k-chained A operand over s'
+        bf16x8 mf[3];
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const bf16x8 fm = frag_tr_l(&sm.Mt[0][0], MP, 16 * sp2, 32 * q, lane);
-          ra = mma_bf16(fam[q], fm, ra);
-          rz = mma_bf16(frag_row_l(&sm.Cb[0][0], PB, 16 * tt, 32 * q, lane), fm, rz);
-          const bf16x8 fb = frag_row_l(&sm.Bd[0][0], PB, 16 * sp2, 32 * q, lane);
-          wy = mma_bf16(frag_tr_l(&sm.Cb[0][0], PB, 16 * tt, 32 * q, lane), fb, wy);
-          wz = mma_bf16(fzT[q], fb, wz);
+        for (int i = 0; i < 3; ++i) {
+          const bf16* mrow = &sm.Mt[16 * qt + m][32 * i + 4 * gq];
+          const uint2 lo = *reinterpret_cast<const uint2*>(mrow);
+          const uint2 hi = *reinterpret_cast<const uint2*>(mrow + 16);
+          mf[i] = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
         }
-        const int sq = 16 * sp2 + m;
-        const float hs = sm.hp[0][0][sq] + sm.hp[0][1][sq] + sm.hp[0][2][sq] + sm.hp[0][3][sq];
-        const float hz = sm.hp[1][0][sq] + sm.hp[1][1][sq] + sm.hp[1][2][sq] + sm.hp[1][3][sq];
+        f32x4 py = zero4(), pz = zero4(), mb = zero4();
+        py = mma_bf16(mf[0], wyp[0], py); py = mma_bf16(mf[1], wyp[1], py); py = mma_bf16(mf[2], wyp[2], py);
+        pz = mma_bf16(mf[0], wzp[0], pz); pz = mma_bf16(mf[1], wzp[1], pz); pz = mma_bf16(mf[2], wzp[2], pz);
+        mb = mma_bf16(mf[0], bdp0, mb); mb = mma_bf16(mf[1], bdp1, mb); mb = mma_bf16(mf[2], bdp2, mb);
+        // adjoint coefficients of the rows q = 16 qt + 4 gq + r for target tl
+        float am[4], km[4];
+        if (qt < CL / 16) {
+          const int q0 = 16 * qt + 4 * gq;
+          const float4 lq = *reinterpret_cast<const float4*>(&sm.la[q0]);   // LA[q0 .. q0 + 3]
+          const float lqm = sm.la[q0 > 0 ? q0 - 1 : 0];
+          const float lv[4] = {lqm, lq.x, lq.y, lq.z};                     // LA[q - 1]
+          const float4 kq = lds_bf16x4(&sm.Cb[tl][q0]);
+          const float kv[4] = {kq.x, kq.y, kq.z, kq.w};
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float x = __builtin_amdgcn_exp2f(lv[r] - lat);
+            am[r] = q0 + r > tl ? x : 0.f;
+            km[r] = kv[r];
+          }
+        } else {   // the end rows: lamS partials (64 .. 67), lamZ partials (68 .. 71)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            am[r] = gq == 0 ? aend : 0.f;
+            km[r] = gq == 0 ? cgs : (gq == 1 ? cgz : 0.f);
+          }
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int t = 16 * tt + 4 * gq + r;
-          const float Rs = ra[r] + aend[r] * hs;
-          const float Rz = rz[r] + sm.co[R_GS + t] * hs + sm.co[R_GZ + t] * hz;
-          al[r] += wy[r] * Rs;
-          ea[r] += wz[r] * Rs;
-          bt[r] += wz[r] * Rz;
-          const int jb = t + HT - sq;   // band: the source of lag jb of target t
-          const bool inb = jb >= 0 && jb < g.e;
-          eb[r] += static_cast<float>(sm.Bd[sq][t]) * Rs;   // zero off the band
-          if (inb && t0 + t < g.T) {
-            const uint32_t o = (uint32_t)((t0 + t) * g.e + jb);
-            if (g.gate_mode == GATE_LAG) st_at(a.dgate + rowbase * g.e, o * 2, static_cast<bf16>(Rz));
-            else if (g.gate_mode == GATE_TOKEN) st_at(p.dw + rowbase * g.e, o * 4, Rz);
-          }
+          al += am[r] * py[r];
+          ea += am[r] * pz[r];
+          eb += am[r] * mb[r];
+          bt += km[r] * pz[r];
         }
       }
-      {   // s' = 80 (S_c: in S_{t-1} with At), 81 (Z_c: in S_{t-1} with Kt, in Z_{t-1} with B1)
-        f32x4 ra = zero4(), rz = zero4();
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const bf16x8 fm = frag_tr_l(&sm.Mt[0][0], MP, SRC, 32 * q, lane);
-          ra = mma_bf16(fam[q], fm, ra);
-          rz = mma_bf16(frag_row_l(&sm.Cb[0][0], PB, 16 * tt, 32 * q, lane), fm, rz);
-        }
-        const bool bs = m == 0, bz = m == 1;
-        const float hs = bs ? gSS : bz ? gSZ : 0.f;
-        const float hz = bs ? gZS : bz ? gZZ : 0.f;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = 16 * tt + 4 * gq + r;
-          const float Rs = ra[r] + aend[r] * hs;
-          const float Rz = rz[r] + sm.co[R_GS + t] * hs + sm.co[R_GZ + t] * hz;
-          const float wy = bs ? sm.At[t] : bz ? sm.Kt[t] : 0.f;
-          const float wz = bz ? sm.B1[t] : 0.f;
-          al[r] += wy * Rs;
-          ea[r] += wz * Rs;
-          bt[r] += wz * Rz;
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float va = row_sum16(al[r]), vea = row_sum16(ea[r]), veb = row_sum16(eb[r]), vb = row_sum16(bt[r]);
-        const int t = 16 * tt + 4 * gq + r;
-        if (m == 0 && t0 + t < g.T) {
-          const uint32_t o = (uint32_t)(t0 + t) * 2;
-          st_at(a.ddecay + rowbase, o, static_cast<bf16>(va));
-          st_at(a.dlr + rowbase, o, static_cast<bf16>(-(sm.be[t] * vea + veb)));
-          if (MOM) st_at(a.dbeta + rowbase, o, static_cast<bf16>(vb));
-        }
+      al = xsum_rows(al);
+      ea = xsum_rows(ea);
+      eb = xsum_rows(eb);
+      bt = xsum_rows(bt);
+      if (gq == 0 && t0 + tl < g.T) {
+        const uint32_t o = (uint32_t)(t0 + tl) * 2;
+        st_at(a.ddecay + rowbase, o, static_cast<bf16>(al));
+        st_at(a.dlr + rowbase, o, static_cast<bf16>(-(sm.be[tl] * ea + eb)));
+        if (MOM) st_at(a.dbeta + rowbase, o, static_cast<bf16>(bt));
       }
     }
     __syncthreads();
@@ -768,9 +749,12 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
     if (c > c_begin) {
       rows_load<WL_R>(pf, rk, rv, rq, rdy, t0 - CL, w);
       scal_load(sp, g, a, rowbase, t0 - CL);
+      xs_load(c - 1, xn);
     } else {
       pf = RowPf<WL_R>{};
       sp = ScalPf{};
+#pragma unroll
+      for (int v = 0; v < 8; ++v) xn[v] = 0u;
     }
     if (hf == 1) {
       CPB_FRESH_LANE
@@ -783,36 +767,55 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
       for (int st = 0; st < SRC / 16; ++st) {
         f32x4 acc;
         {
-          const unsigned e0 = sm.ef[ct][st][0][lane], e1 = sm.ef[ct][st][1][lane];
+          const unsigned e0 = efr[st][0], e1 = efr[st][1];
           acc[0] = lo16(e0); acc[1] = hi16(e0); acc[2] = lo16(e1); acc[3] = hi16(e1);
         }
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          acc = mma_bf16(frag_tr_l(&sm.Rt[0][0], QP, 16 * st, 32 * q, lane),
-                         frag_tr_l(&sm.psi[0][0], PB, 16 * ct, 32 * q, lane), acc);
-          acc = mma_bf16(frag_row_l(&sm.vd[0][0], PB, 16 * st, 32 * q, lane), sreft[q], acc);
+        for (int q = 0; q < 2; ++q) {   // dphi^T[k][s] = sum_t psi[t][k] R[s][t] + (S_ref^T ddelta_s)[k] (+ end terms)
+          acc = mma_bf16(frag_tr_l(&sm.psi[0][0], PB, 16 * ct, 32 * q, lane),
+                         frag_tr_l(&sm.Rt[0][0], QP, 16 * st, 32 * q, lane), acc);
+          acc = mma_bf16(sreft[q], frag_row_l(&sm.vd[0][0], PB, 16 * st, 32 * q, lane), acc);
         }
+        const int s = 16 * st + m, pp = t0 - HT + s, col0 = 16 * ct + 4 * gq;
+        float val[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int s = 16 * st + 4 * gq + r;
-          const float df = acc[r];
-          const int pp = t0 - HT + s, col = 16 * ct + m;
-          if (st == 0) {
-            if (seg_first) {
-              if (seg > 0 && s >= HT - H)
-                st_at(part_row(p.halo_part, bh, sg.nseg, seg, H), (uint32_t)(((s - (HT - H)) * (2 * D) + D + col) * 4), df);
-            } else {
-              cdk[r] = df;
-            }
-          } else if (pp < g.T) {
-            float val = df + (st == SRC / 16 - 1 && !seg_last ? cin[r] : 0.f);
-            if (pp >= tail0) {
-              st_at(part_row(p.tail_part, bh, sg.nseg, seg, H), (uint32_t)(((pp - tail0) * (2 * D) + D + col) * 4), val);
-            } else {
-              if constexpr (MAPE) val *= poly_map_grad(bf(bld2(rkk, (uint32_t)((pp * D + col) * 2))), g.map_deg);
-              st_at(a.dk + rowbase * D, (uint32_t)((pp * D + col) * 2), static_cast<bf16>(val));
-            }
+        for (int r = 0; r < 4; ++r) val[r] = acc[r];
+        auto store_dk = [&](float (&v)[4]) {
+          if constexpr (MAPE) {
+            const u32x2v raw = bld8(rkk, (uint32_t)((pp * D + col0) * 2));
+            v[0] *= poly_map_grad(lo16(raw[0]), g.map_deg); v[1] *= poly_map_grad(hi16(raw[0]), g.map_deg);
+            v[2] *= poly_map_grad(lo16(raw[1]), g.map_deg); v[3] *= poly_map_grad(hi16(raw[1]), g.map_deg);
           }
+          st_at(a.dk + rowbase * D, (uint32_t)((pp * D + col0) * 2), make_uint2(pk(v[0], v[1]), pk(v[2], v[3])));
+        };
+        if (interior) {
+          if (st == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cdk[r] = val[r];
+          } else {
+            if (st == SRC / 16 - 1)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) val[r] += cin[r];
+            store_dk(val);
+          }
+        } else if (st == 0) {
+          if (seg_first) {
+            if (seg > 0 && s >= HT - H)
+              st_at(part_row(p.halo_part, bh, sg.nseg, seg, H), (uint32_t)(((s - (HT - H)) * (2 * D) + D + col0) * 4),
+                    make_float4(val[0], val[1], val[2], val[3]));
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cdk[r] = val[r];
+          }
+        } else if (pp < g.T) {
+          if (st == SRC / 16 - 1 && !seg_last)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) val[r] += cin[r];
+          if (pp >= tail0)
+            st_at(part_row(p.tail_part, bh, sg.nseg, seg, H), (uint32_t)(((pp - tail0) * (2 * D) + D + col0) * 4),
+                  make_float4(val[0], val[1], val[2], val[3]));
+          else
+            store_dk(val);
         }
       }
     } else {
@@ -905,10 +908,9 @@ bool chunk_bwd_supported(const Geom& g, const SegGeom& sg) {
          !g.has_buf && g.flag == nullptr && sg.G >= 1;
 }
 
-// Workspace of k_cp_bwd: per chunk its start state (bf16) and coefficient record.
-size_t chunk_bwd_xsave_bytes(const Geom& g, const SegGeom& sg) {
-  return (size_t)g.BH * sg.nseg * sg.G * kXsBytes;
-}
+// The chunk-start states k_cp_bwd reads: saved by the forward walk (walk_fwd.hip), one block per
+// 64-token chunk of every row.
+size_t chunk_bwd_states_bytes(const Geom& g) { return (size_t)g.BH * g.nc * kStateBlk; }
 
 // g, sg: the forward's chunks (64 tokens) and segments. p.seg_adj must hold the adjoint at every
 // segment end (k_bwd_seg_agg / k_bwd_seg_scan); p.tail_part / halo_part / dw / dsref_part are the

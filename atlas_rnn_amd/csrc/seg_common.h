@@ -44,7 +44,6 @@ struct BwdSegPtrs {
   void* wsh;                 // [BH][nc][CH][SPM] Ws[s, t-1] of every chunk (input element type)
   float* scal;               // [BH][nc][ScalarBlock] per-chunk inputs of the scalar gradients
   float* buf_adj;            // [BH][2][D][D] first chunk's end adjoint (specialised walk with a carried buffer)
-  void* xsave;               // chunk-parallel backward: per chunk its start state and coefficient record
 };
 
 // The carried buffer on the specialised walks (bufwalk.hip, d = 64). Per row, its first-chunk terms:

@@ -209,12 +209,13 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
   const int i0 = 16 * it + 4 * gq;
   const int rb = g.Lmid > 0 ? 2 : 1;
   // saved states (walk_common.h layout): block of backward chunk cb at rw_row + cb * kStateBlk
-  unsigned char* rw_row = FULL ? reinterpret_cast<unsigned char*>(rw) + (size_t)bh * g.ncb * kStateBlk : nullptr;
+  // (rows of g.ncb blocks with mid points; of g.nc blocks, one per chunk, without)
+  unsigned char* rw_row =
+      FULL ? reinterpret_cast<unsigned char*>(rw) + (size_t)bh * (rb == 2 ? g.ncb : g.nc) * kStateBlk : nullptr;
   // this lane's 8-byte half of the fragments of its tiles j = 0, 1
   const uint32_t f2o[2] = {frag_off(2 * th, it >> 1, lane) + (it & 1) * 8,
                            frag_off(2 * th + 1, it >> 1, lane) + (it & 1) * 8};
   auto save_state = [&](int cb, const float (&Sv)[2][4], const float (&Zv)[2][4]) {
-    if (rw == nullptr) return;   // a backward that recomputes its states (chunk_bwd.hip)
     unsigned char* blk = rw_row + (size_t)cb * kStateBlk;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {

@@ -92,10 +92,10 @@ def test_sizes(lib):
     p = _prob()
     st = 64 * 64 * 4
     saved = lib.atlas_mem_saved_bytes(ctypes.byref(p))
-    # bf16, d = 64, no clamp: the backward recomputes its chunk-start states (chunk_bwd.hip), so the
-    # forward keeps the segment states, the raw S_{T-1} and its own chunk records only: less than
-    # the raw (S, Z) at every 32-token boundary that the other backward reads
-    assert 32 * st <= saved < 32 * (4096 // 32) * 2 * st
+    # bf16, d = 64, no clamp: the backward of chunk_bwd.hip reads the chunk-start (S, Z) in bf16 at
+    # every 64-token boundary and forms its own records: at least those states, less than the raw
+    # (S, Z) at every 32-token boundary that the other backward reads
+    assert 32 * (4096 // 64) * 64 * 64 * 2 * 2 <= saved < 32 * (4096 // 32) * 2 * st
     assert saved % 256 == 0
     ws = lib.atlas_mem_bwd_workspace_bytes(ctypes.byref(p))
     assert ws > 0 and ws % 256 == 0
@@ -118,7 +118,7 @@ def test_noalloc_backward_host_checks(lib):
     assert lib.atlas_mem_bwd_workspace_bytes(ctypes.byref(_prob(bh=64, seq_len=2048, gate_mode=_lib.GATE_TOKEN))) <= 64 << 20
     good = ctypes.c_void_p(0x10000)
     args = _lib.BwdArgs()
-    big = _prob(bh=256)
+    big = _prob(bh=4096)
     assert lib.atlas_mem_bwd_workspace_bytes(ctypes.byref(big)) > 64 << 20
     assert lib.atlas_mem_bwd_noalloc(ctypes.byref(big), ctypes.byref(args), good, None) == _lib.ERR_SCRATCH
     assert lib.atlas_mem_bwd_noalloc(ctypes.byref(_prob()), None, good, None) == 4
