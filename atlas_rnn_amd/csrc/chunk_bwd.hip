@@ -69,6 +69,8 @@ struct BwSm {
   // them), their S_c / Z_c entries in rows 64 / 68 only. Rows 72 .. 79 zero.
   alignas(16) bf16 Mt[QX][MQ];
   alignas(16) bf16 Cb[CL][PB];       // C'[r][t]: of g_r in S_{t-1} (r, t chunk-local targets)
+  alignas(16) bf16 DA[CL][PB];       // DA[t][u] = A(u -> t - 1): the decay from token u + 1 to t - 1 (u < t)
+  alignas(16) bf16 BE[CL][PB];       // BE[r][u] = -eta_u B(r -> u) (u >= r): g_r in Z_u, into S_u
   alignas(16) float co[REC];
   alignas(16) float la[CL], lb[CL], eta[CL], At[CL], Kt[CL], B1[CL], be[CL];
   float gram[NWB][4];
@@ -210,24 +212,54 @@ __device__ __forceinline__ void chunk_end_scan(const Geom& g, const ScalPf& p, i
   sm.co[R_GZ + r] = real ? ex.b : 0.f;
   if (lane == 63) { sm.co[R_TR] = inc.a; sm.co[R_TR + 1] = inc.k; sm.co[R_TR + 2] = inc.b; sm.co[R_TR + 3] = 0.f; }
 }
-// threads < 80: the per-source end coefficients from cgS / cgZ (needs chunk_end_scan's output)
-__device__ __forceinline__ void chunk_end_sources(const Geom& g, BwSm& sm, int i) {
-  // i < 80: cs of source s = i (through cgS); 80 <= i < 160: cz of source s = i - 80 (through cgZ).
-  // cs_s = sum_j w(s - HT + j, j) cgS[s - HT + j] = sum over the band row Bd[s][r] (zero off the
-  // window): the 17 targets r = s - 16 .. s, loads unconditional (clamped), no branches
-  if (i >= 0 && i < 2 * SRC) {
-    const int zc = i >= SRC, s = zc ? i - SRC : i;
-    const float* cg = &sm.co[zc ? R_GZ : R_GS];
-    float acc = 0.f;
-#pragma unroll
-    for (int j = 0; j < EMAX; ++j) {
+// threads s < 80: the per-source end coefficients from cgS / cgZ (needs chunk_end_scan's output
+// and the band): cs_s = sum_j w(s - HT + j, j) cgS[s - HT + j], cz_s likewise with cgZ
+__device__ __forceinline__ void chunk_end_sources(const Geom& g, BwSm& sm, int s) {
+  if (s >= 0 && s < SRC) {
+    float cs = 0.f, cz = 0.f;
+    for (int j = 0; j < g.e; ++j) {
       const int r = s - HT + j;
-      const int rc = min(max(r, 0), CL - 1);
-      const float x = static_cast<float>(sm.Bd[s][rc]) * cg[rc];
-      acc += (r >= 0 && r < CL) ? x : 0.f;
+      if (r >= 0 && r < CL) {
+        const float wgt = cw(sm, r, j);
+        cs += wgt * sm.co[R_GS + r];
+        cz += wgt * sm.co[R_GZ + r];
+      }
     }
-    sm.co[(zc ? R_CZ : R_CS) + s] = acc;
+    sm.co[R_CS + s] = cs;
+    sm.co[R_CZ + s] = cz;
   }
+}
+
+// The two factors of C' = BE DA^T from the prefix arrays, one row segment per thread (512 threads:
+// row i >> 3, columns 8 (i & 7) .. +7): loads unconditional, the triangles applied by selects.
+template <bool MOM>
+__device__ __forceinline__ void gen_tables(BwSm& sm, int i) {
+  const int row = i >> 3, u0 = (i & 7) * 8;
+  const float4 a0 = *reinterpret_cast<const float4*>(&sm.la[u0]), a1 = *reinterpret_cast<const float4*>(&sm.la[u0 + 4]);
+  const float lau[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+  const float lat = sm.la[row > 0 ? row - 1 : 0];
+  const float4 e0 = *reinterpret_cast<const float4*>(&sm.eta[u0]), e1 = *reinterpret_cast<const float4*>(&sm.eta[u0 + 4]);
+  const float etu[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+  const float4 b0 = *reinterpret_cast<const float4*>(&sm.lb[u0]), b1 = *reinterpret_cast<const float4*>(&sm.lb[u0 + 4]);
+  const float lbu[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+  const float lbr = sm.lb[row];
+  bf16x8 da, be;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int u = u0 + e;
+    const float x = __builtin_amdgcn_exp2f(lat - lau[e]);
+    da[e] = static_cast<bf16>(u <= row - 1 ? x : 0.f);
+    float v;
+    if (MOM) {
+      const float y = -etu[e] * __builtin_amdgcn_exp2f(lbu[e] - lbr);
+      v = u >= row ? y : 0.f;
+    } else {
+      v = u == row ? -etu[e] : 0.f;
+    }
+    be[e] = static_cast<bf16>(v);
+  }
+  *reinterpret_cast<bf16x8*>(&sm.DA[row][u0]) = da;
+  *reinterpret_cast<bf16x8*>(&sm.BE[row][u0]) = be;
 }
 
 // wave 0: the chunk's prefix arrays: LA, LB (log2 prefix sums), eta, beta, and the coefficients of
@@ -396,7 +428,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
     }
     __syncthreads();
 
-    // ---- R1: delta (in place of v), C'
+    // ---- R1: delta (in place of v), the factors of C', the end coefficients, the Grams' end rows
     {
       CPB_FRESH_LANE
       const int st0 = hf == 0 ? 0 : 3, nst = hf == 0 ? 3 : 2;
@@ -409,22 +441,28 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
         const float4 vv = lds_bf16x4(pv);
         store4<bf16>(pv, acc[0] - vv.x, acc[1] - vv.y, acc[2] - vv.z, acc[3] - vv.w);
       }
+      gen_tables<MOM>(sm, tid);
+      chunk_end_sources(g, sm, tid - 256);   // threads 256 .. 335: cs, cz of the chunk's sources
+      if (tid < 4) {   // <lamS, S_c>, <lamS, Z_c>, <lamZ, S_c>, <lamZ, Z_c> into the end rows
+        float gsum = 0.f;
+#pragma unroll
+        for (int u = 0; u < NWB; ++u) gsum += sm.gram[u][tid];
+        sm.Mt[tid < 2 ? CL : CL + 4][SRC + (tid & 1)] = static_cast<bf16>(gsum);
+      }
+    }
+    __syncthreads();
+    // C'[r][t] = sum_u BE[r][u] DA[t][u]: tiles (q4, 2 hf + j)
+    {
+      CPB_FRESH_LANE
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int tt = 2 * hf + j;
         f32x4 acc = zero4();
 #pragma unroll
         for (int q = 0; q < 2; ++q)
-          acc = mma_bf16(gen_beta_eta<MOM>(sm.lb, sm.eta, 16 * q4 + m, q, lane), gen_decay_to(sm.la, 16 * tt + m, q, lane), acc);
+          acc = mma_bf16(frag_row_l(&sm.BE[0][0], PB, 16 * q4, 32 * q, lane), frag_row_l(&sm.DA[0][0], PB, 16 * tt, 32 * q, lane), acc);
 #pragma unroll
         for (int r = 0; r < 4; ++r) sm.Cb[16 * q4 + 4 * gq + r][16 * tt + m] = static_cast<bf16>(acc[r]);
-      }
-      chunk_end_sources(g, sm, tid - 256);   // threads 256 .. 415: cs, cz of the chunk's sources
-      if (tid < 4) {   // <lamS, S_c>, <lamS, Z_c>, <lamZ, S_c>, <lamZ, Z_c> into the end rows
-        float gsum = 0.f;
-#pragma unroll
-        for (int u = 0; u < NWB; ++u) gsum += sm.gram[u][tid];
-        sm.Mt[tid < 2 ? CL : CL + 4][SRC + (tid & 1)] = static_cast<bf16>(gsum);
       }
     }
     __syncthreads();
@@ -705,15 +743,13 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
         float am[4], km[4];
         if (qt < CL / 16) {
           const int q0 = 16 * qt + 4 * gq;
-          const float4 lq = *reinterpret_cast<const float4*>(&sm.la[q0]);   // LA[q0 .. q0 + 3]
-          const float lqm = sm.la[q0 > 0 ? q0 - 1 : 0];
-          const float lv[4] = {lqm, lq.x, lq.y, lq.z};                     // LA[q - 1]
+          // Am[t][q] = A(t -> q - 1) = DA[q][t] (zero for q <= t): rows q0 .. q0 + 3 of column tl
+          const s16x4 av = tr4_l(&sm.DA[0][0], PB, 16 * qt, 16 * tt, lane);
           const float4 kq = lds_bf16x4(&sm.Cb[tl][q0]);
           const float kv[4] = {kq.x, kq.y, kq.z, kq.w};
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float x = __builtin_amdgcn_exp2f(lv[r] - lat);
-            am[r] = q0 + r > tl ? x : 0.f;
+            am[r] = bf((unsigned short)av[r]);
             km[r] = kv[r];
           }
         } else {   // the end rows: lamS partials (64 .. 67), lamZ partials (68 .. 71)
