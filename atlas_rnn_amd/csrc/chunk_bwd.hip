@@ -53,6 +53,12 @@ constexpr int R_CS = 0, R_CZ = SRC, R_GS = 2 * SRC, R_GZ = 2 * SRC + CL, R_TR = 
 constexpr int REC = R_TR + 4;   // 292
 static_assert(REC <= NTB, "one record element per thread");
 
+// Per chunk: the end record (cs, cz, cgS, cgZ, transition) and the prefix arrays (LA, LB, eta,
+// beta; the coefficients At, Kt of (S_c, Z_c) in S_{t-1} and B1 of Z_c in Z_{t-1}).
+struct ChunkCoef {
+  alignas(16) float co[REC];
+  alignas(16) float la[CL], lb[CL], eta[CL], At[CL], Kt[CL], B1[CL], be[CL];
+};
 struct BwSm;
 struct BwSm {
   alignas(16) bf16 phi[SRC][PB];     // sources (mapped)
@@ -71,8 +77,7 @@ struct BwSm {
   alignas(16) bf16 Cb[CL][PB];       // C'[r][t]: of g_r in S_{t-1} (r, t chunk-local targets)
   alignas(16) bf16 DA[CL][PB];       // DA[t][u] = A(u -> t - 1): the decay from token u + 1 to t - 1 (u < t)
   alignas(16) bf16 BE[CL][PB];       // BE[r][u] = -eta_u B(r -> u) (u >= r): g_r in Z_u, into S_u
-  alignas(16) float co[REC];
-  alignas(16) float la[CL], lb[CL], eta[CL], At[CL], Kt[CL], B1[CL], be[CL];
+  ChunkCoef cc[2];                   // by chunk parity: the chunk in flight and the next one
   float gram[NWB][4];
   // the window band Bd[s][r] = w(r, r + HT - s) (0 <= r + HT - s < e; zero elsewhere): the weight of
   // source s in the window of target r, i.e. of lag j = r + HT - s (w: the lag gate, the token gate
@@ -197,7 +202,7 @@ __device__ __forceinline__ bf16x8 gen_zcoef(const float* lb, int t, int q, int l
 }
 
 // wave 0: the chunk's end coefficients (cgS, cgZ per target; the transition) from its scalars
-__device__ __forceinline__ void chunk_end_scan(const Geom& g, const ScalPf& p, int t0, BwSm& sm) {
+__device__ __forceinline__ void chunk_end_scan(const Geom& g, const ScalPf& p, int t0, ChunkCoef& sm) {
   const int lane = fresh_tid() & 63;
   // lane j holds target r = 63 - j (the chunk read backwards); targets past T are the identity
   const float al = __shfl(bf(p.al), 63 - lane, 64), et = __shfl(bf(p.et), 63 - lane, 64),
@@ -214,35 +219,35 @@ __device__ __forceinline__ void chunk_end_scan(const Geom& g, const ScalPf& p, i
 }
 // threads s < 80: the per-source end coefficients from cgS / cgZ (needs chunk_end_scan's output
 // and the band): cs_s = sum_j w(s - HT + j, j) cgS[s - HT + j], cz_s likewise with cgZ
-__device__ __forceinline__ void chunk_end_sources(const Geom& g, BwSm& sm, int s) {
+__device__ __forceinline__ void chunk_end_sources(const Geom& g, const BwSm& sm, ChunkCoef& kc, int s) {
   if (s >= 0 && s < SRC) {
     float cs = 0.f, cz = 0.f;
     for (int j = 0; j < g.e; ++j) {
       const int r = s - HT + j;
       if (r >= 0 && r < CL) {
         const float wgt = cw(sm, r, j);
-        cs += wgt * sm.co[R_GS + r];
-        cz += wgt * sm.co[R_GZ + r];
+        cs += wgt * kc.co[R_GS + r];
+        cz += wgt * kc.co[R_GZ + r];
       }
     }
-    sm.co[R_CS + s] = cs;
-    sm.co[R_CZ + s] = cz;
+    kc.co[R_CS + s] = cs;
+    kc.co[R_CZ + s] = cz;
   }
 }
 
 // The two factors of C' = BE DA^T from the prefix arrays, one row segment per thread (512 threads:
 // row i >> 3, columns 8 (i & 7) .. +7): loads unconditional, the triangles applied by selects.
 template <bool MOM>
-__device__ __forceinline__ void gen_tables(BwSm& sm, int i) {
+__device__ __forceinline__ void gen_tables(BwSm& sm, const ChunkCoef& kc, int i) {
   const int row = i >> 3, u0 = (i & 7) * 8;
-  const float4 a0 = *reinterpret_cast<const float4*>(&sm.la[u0]), a1 = *reinterpret_cast<const float4*>(&sm.la[u0 + 4]);
+  const float4 a0 = *reinterpret_cast<const float4*>(&kc.la[u0]), a1 = *reinterpret_cast<const float4*>(&kc.la[u0 + 4]);
   const float lau[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-  const float lat = sm.la[row > 0 ? row - 1 : 0];
-  const float4 e0 = *reinterpret_cast<const float4*>(&sm.eta[u0]), e1 = *reinterpret_cast<const float4*>(&sm.eta[u0 + 4]);
+  const float lat = kc.la[row > 0 ? row - 1 : 0];
+  const float4 e0 = *reinterpret_cast<const float4*>(&kc.eta[u0]), e1 = *reinterpret_cast<const float4*>(&kc.eta[u0 + 4]);
   const float etu[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
-  const float4 b0 = *reinterpret_cast<const float4*>(&sm.lb[u0]), b1 = *reinterpret_cast<const float4*>(&sm.lb[u0 + 4]);
+  const float4 b0 = *reinterpret_cast<const float4*>(&kc.lb[u0]), b1 = *reinterpret_cast<const float4*>(&kc.lb[u0 + 4]);
   const float lbu[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-  const float lbr = sm.lb[row];
+  const float lbr = kc.lb[row];
   bf16x8 da, be;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -264,7 +269,7 @@ __device__ __forceinline__ void gen_tables(BwSm& sm, int i) {
 
 // wave 0: the chunk's prefix arrays: LA, LB (log2 prefix sums), eta, beta, and the coefficients of
 // (S_c, Z_c) in S_{t-1} (At, Kt) and of Z_c in Z_{t-1} (B1)
-__device__ __forceinline__ void chunk_prefix(const ScalPf& p, BwSm& sm) {
+__device__ __forceinline__ void chunk_prefix(const ScalPf& p, ChunkCoef& sm) {
   const int lane = fresh_tid() & 63;
   const float al = bf(p.al), et = bf(p.et), be = bf(p.be);
   sm.la[lane] = wave_prefix_sum(fmaxf(__log2f(al), kLogFloor), lane);
@@ -377,12 +382,16 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
   RowPf<WL_R> pf;
   ScalPf sp;
   unsigned xn[8];   // the next chunk's state slice, in flight with its rows
-  rows_load<WL_R>(pf, rk, rv, rq, rdy, (c_end - 1) * CL, w);
   scal_load(sp, g, a, rowbase, (c_end - 1) * CL);
+  rows_load<WL_R>(pf, rk, rv, rq, rdy, (c_end - 1) * CL, w);
   xs_load(c_end - 1, xn);
+  // the last chunk's record and prefix arrays (every later chunk's are formed one step ahead)
+  if (w == 0) chunk_prefix(sp, sm.cc[(c_end - c_begin - 1) & 1]);
+  if (w == 1) chunk_end_scan(g, sp, (c_end - 1) * CL, sm.cc[(c_end - c_begin - 1) & 1]);
 #pragma unroll 1
   for (int cr = c_end - c_begin - 1; cr >= 0; --cr) {
     CPB_FRESH_LANE
+    ChunkCoef& kc = sm.cc[cr & 1];   // this chunk's record and prefix arrays (formed one step ahead)
     const int c = c_begin + cr;
     const int t0 = c * CL;
     // this wave's slice of X_c (for the Grams and the LDS copy)
@@ -395,8 +404,10 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
     __syncthreads();
     rows_store<MAPE, WL_R>(pf, sm, g.map_deg, w);
     gates_store(sp, g, sm);
-    if (w == 0) chunk_prefix(sp, sm);
-    if (w == 1) chunk_end_scan(g, sp, t0, sm);
+    gen_tables<MOM>(sm, kc, tid);
+    // the next chunk's scalars, early: waves 0, 1 form its record and prefix arrays at the end of R4
+    if (c > c_begin) scal_load(sp, g, a, rowbase, t0 - CL);
+    else sp = ScalPf{};
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int kt = 2 * hf + j;
@@ -441,21 +452,8 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
         const float4 vv = lds_bf16x4(pv);
         store4<bf16>(pv, acc[0] - vv.x, acc[1] - vv.y, acc[2] - vv.z, acc[3] - vv.w);
       }
-      gen_tables<MOM>(sm, tid);
-      chunk_end_sources(g, sm, tid - 256);   // threads 256 .. 335: cs, cz of the chunk's sources
-      if (tid < 4) {   // <lamS, S_c>, <lamS, Z_c>, <lamZ, S_c>, <lamZ, Z_c> into the end rows
-        float gsum = 0.f;
 #pragma unroll
-        for (int u = 0; u < NWB; ++u) gsum += sm.gram[u][tid];
-        sm.Mt[tid < 2 ? CL : CL + 4][SRC + (tid & 1)] = static_cast<bf16>(gsum);
-      }
-    }
-    __syncthreads();
-    // C'[r][t] = sum_u BE[r][u] DA[t][u]: tiles (q4, 2 hf + j)
-    {
-      CPB_FRESH_LANE
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < 2; ++j) {   // C'[r][t] = sum_u BE[r][u] DA[t][u]: tiles (q4, 2 hf + j)
         const int tt = 2 * hf + j;
         f32x4 acc = zero4();
 #pragma unroll
@@ -464,9 +462,15 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
 #pragma unroll
         for (int r = 0; r < 4; ++r) sm.Cb[16 * q4 + 4 * gq + r][16 * tt + m] = static_cast<bf16>(acc[r]);
       }
+      chunk_end_sources(g, sm, kc, tid - 256);   // threads 256 .. 335: cs, cz of the chunk's sources
+      if (tid < 4) {   // <lamS, S_c>, <lamS, Z_c>, <lamZ, S_c>, <lamZ, Z_c> into the end rows
+        float gsum = 0.f;
+#pragma unroll
+        for (int u = 0; u < NWB; ++u) gsum += sm.gram[u][tid];
+        sm.Mt[tid < 2 ? CL : CL + 4][SRC + (tid & 1)] = static_cast<bf16>(gsum);
+      }
     }
     __syncthreads();
-
     // ---- R2: t-phase (waves 0-3) | end terms of ddelta / dphi (waves 4-7)
     // the end terms (waves 4-7), bf16 pairs in the accumulator layout, used in R3 / R4
     unsigned edr[SRC / 16][2], efr[SRC / 16][2];
@@ -504,7 +508,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
       }
       // dpsi^T[k][t]: intra-chunk sources, then the chunk-start state
       const bf16x8 fr0 = pack_frag(Rr[0], Rr[1]), fr1 = pack_frag(Rr[2], Rr[3]), fr2 = pack_frag(Rr[4], zero4());
-      const float At = sm.At[t], Kt = sm.Kt[t];
+      const float At = kc.At[t], Kt = kc.Kt[t];
       float fS = 0.f, fZ = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
@@ -572,7 +576,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
           sm.Mt[CL + ct][16 * st + m] = static_cast<bf16>(hs[0]);
           sm.Mt[CL + 4 + ct][16 * st + m] = static_cast<bf16>(hz[0]);
         }
-        const float cs = sm.co[R_CS + 16 * st + m], cz = sm.co[R_CZ + 16 * st + m];
+        const float cs = kc.co[R_CS + 16 * st + m], cz = kc.co[R_CZ + 16 * st + m];
         edr[st][0] = pk(cs * es[0] + cz * ez[0], cs * es[1] + cz * ez[1]);
         edr[st][1] = pk(cs * es[2] + cz * ez[2], cs * es[3] + cz * ez[3]);
         efr[st][0] = pk(cs * fs[0] + cz * fz[0], cs * fs[1] + cz * fz[1]);
@@ -640,7 +644,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
       // targets t = 16 tt + 4 gq + r
       if (g.gate_mode != GATE_NONE) {
         const int tt = q4, tl = 16 * tt + m;
-        const float cgs = sm.co[R_GS + tl], cgz = sm.co[R_GZ + tl];
+        const float cgs = kc.co[R_GS + tl], cgz = kc.co[R_GZ + tl];
         bf16x8 kme;   // Km over the end rows (k = 64 + 8 gq + e): cgS on the lamS partials, cgZ on lamZ's
 #pragma unroll
         for (int e = 0; e < 8; ++e) kme[e] = static_cast<bf16>(gq == 0 ? (e < 4 ? cgs : cgz) : 0.f);
@@ -683,8 +687,8 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
       // bases (rows) by this wave's targets (columns), packed in pairs as the k-chained operands
       bf16x8 wyp[3], wzp[3];
       {
-        const bf16x8 fz0 = gen_zcoef<MOM>(sm.lb, 16 * tt + m, 0, lane);
-        const bf16x8 fz1 = gen_zcoef<MOM>(sm.lb, 16 * tt + m, 1, lane);
+        const bf16x8 fz0 = gen_zcoef<MOM>(kc.lb, 16 * tt + m, 0, lane);
+        const bf16x8 fz1 = gen_zcoef<MOM>(kc.lb, 16 * tt + m, 1, lane);
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
           f32x4 y[2], z[2];
@@ -707,9 +711,9 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
           }
           if (i == 2 && gq == 0) {   // rows 80 (S_c), 81 (Z_c) of tile 5
             const int t = 16 * tt + m;
-            y[1][0] = sm.At[t];
-            y[1][1] = sm.Kt[t];
-            z[1][1] = sm.B1[t];
+            y[1][0] = kc.At[t];
+            y[1][1] = kc.Kt[t];
+            z[1][1] = kc.B1[t];
           }
           wyp[i] = pack_frag(y[0], y[1]);
           wzp[i] = pack_frag(z[0], z[1]);
@@ -720,9 +724,9 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
       const bf16x8 bdp1 = tr_pair_l<true>(&sm.Bd[0][0], PB, 1, 16 * tt, lane);
       const bf16x8 bdp2 = tr_pair_l<false>(&sm.Bd[0][0], PB, 2, 16 * tt, lane);
       const int tl = 16 * tt + m;   // this lane's target (accumulator column)
-      const float lat = sm.la[tl];
-      const float aend = __builtin_amdgcn_exp2f(sm.la[CL - 1] - lat);
-      const float cgs = sm.co[R_GS + tl], cgz = sm.co[R_GZ + tl];
+      const float lat = kc.la[tl];
+      const float aend = __builtin_amdgcn_exp2f(kc.la[CL - 1] - lat);
+      const float cgs = kc.co[R_GS + tl], cgz = kc.co[R_GZ + tl];
       float al = 0.f, ea = 0.f, eb = 0.f, bt = 0.f;
 #pragma unroll
       for (int qt = 0; qt < QX / 16; ++qt) {
@@ -774,7 +778,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
       if (gq == 0 && t0 + tl < g.T) {
         const uint32_t o = (uint32_t)(t0 + tl) * 2;
         st_at(a.ddecay + rowbase, o, static_cast<bf16>(al));
-        st_at(a.dlr + rowbase, o, static_cast<bf16>(-(sm.be[tl] * ea + eb)));
+        st_at(a.dlr + rowbase, o, static_cast<bf16>(-(kc.be[tl] * ea + eb)));
         if (MOM) st_at(a.dbeta + rowbase, o, static_cast<bf16>(bt));
       }
     }
@@ -784,11 +788,9 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
     // (the last chunk clears the registers instead: the values just staged are dead from here on)
     if (c > c_begin) {
       rows_load<WL_R>(pf, rk, rv, rq, rdy, t0 - CL, w);
-      scal_load(sp, g, a, rowbase, t0 - CL);
       xs_load(c - 1, xn);
     } else {
       pf = RowPf<WL_R>{};
-      sp = ScalPf{};
 #pragma unroll
       for (int v = 0; v < 8; ++v) xn[v] = 0u;
     }
@@ -865,22 +867,28 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
 #pragma unroll
         for (int r = 0; r < 4; ++r) dsr[kt][r] += acc[r];
       }
+      // the next chunk's record and prefix arrays, from the scalars just fetched (the other buffer:
+      // this chunk's is still read below)
+      if (c > c_begin) {
+        if (w == 0) chunk_prefix(sp, sm.cc[(cr - 1) & 1]);
+        if (w == 1) chunk_end_scan(g, sp, t0 - CL, sm.cc[(cr - 1) & 1]);
+      }
     }
 
     // ---- R5: the adjoint at the chunk start
     {
       CPB_FRESH_LANE
-      const float ta = sm.co[R_TR], tk = sm.co[R_TR + 1], tb = sm.co[R_TR + 2];
+      const float ta = kc.co[R_TR], tk = kc.co[R_TR + 1], tb = kc.co[R_TR + 2];
       f32x4 dS[2], dZ[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) { dS[j] = zero4(); dZ[j] = zero4(); }
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const bf16x8 fy = tr_pair_l<true>(&sm.dy[0][0], PB, q, 16 * q4, lane);
-        const float4 ahi = *reinterpret_cast<const float4*>(&sm.At[32 * q + 4 * gq]);
-        const float4 alo = *reinterpret_cast<const float4*>(&sm.At[32 * q + 16 + 4 * gq]);
-        const float4 khi = *reinterpret_cast<const float4*>(&sm.Kt[32 * q + 4 * gq]);
-        const float4 klo = *reinterpret_cast<const float4*>(&sm.Kt[32 * q + 16 + 4 * gq]);
+        const float4 ahi = *reinterpret_cast<const float4*>(&kc.At[32 * q + 4 * gq]);
+        const float4 alo = *reinterpret_cast<const float4*>(&kc.At[32 * q + 16 + 4 * gq]);
+        const float4 khi = *reinterpret_cast<const float4*>(&kc.Kt[32 * q + 4 * gq]);
+        const float4 klo = *reinterpret_cast<const float4*>(&kc.Kt[32 * q + 16 + 4 * gq]);
         f32x4 yh, yl;
 #pragma unroll
         for (int e = 0; e < 4; ++e) { yh[e] = static_cast<float>(fy[e]); yl[e] = static_cast<float>(fy[4 + e]); }
