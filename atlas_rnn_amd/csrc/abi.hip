@@ -28,12 +28,8 @@ hipError_t launch_buf_state(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom
 hipError_t launch_buf_y(const Geom& g, const FwdPtrs<bf16>& a, const bf16* wsh, hipStream_t stream);
 hipError_t launch_walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
                            float* rw, float* final_raw, float* coef, bf16* wsh, hipStream_t stream);
-bool chunk_path_supported(const Geom& g);
 bool chunk_bwd_supported(const Geom& g, const SegGeom& sg);
 size_t chunk_bwd_states_bytes(const Geom& g);
-SegGeom chunk_seg(const Geom& g);
-hipError_t launch_chunk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg, float* seg_states,
-                            float* final_raw, hipStream_t stream);
 
 // Diagnostic tile product C = A B^T (16 x 64 inputs) through the same fragment helpers.
 template <typename T>
@@ -137,18 +133,12 @@ struct Plan {
   // the clamp points) runs first and the exact one-segment-per-row sequence (make_plan(p, true))
   // runs behind it only when some clamp point's |S| exceeds 100 (the clamp is the identity otherwise)
   bool dual;
-  // the chunk-parallel path (chunk_fwd.hip, chunk_bwd.hip): bf16, d = 64, window <= 17, no clamp at
-  // scan_chunk_len boundaries, no carried buffer; sg is then its segment layout (chunk_seg)
-  bool chunk;
   // the specialised forward walk with the backward of chunk_bwd.hip (bf16, d = 64, window <= 17, no
   // clamp, no carried buffer): the forward saves no boundary states and no backward records, and
   // its chunks have no mid point (Lmid = 0)
   bool cbwd;
 };
 
-#ifndef ATLAS_CHUNK_PATH
-#define ATLAS_CHUNK_PATH 0
-#endif
 #ifndef ATLAS_CHUNK_BWD
 #define ATLAS_CHUNK_BWD 1
 #endif
@@ -224,9 +214,8 @@ Plan make_plan(const atlas_mem_problem* p, bool serial_clamp = false) {
   // clamp points on forward-chunk ends: segment-parallel with the clamp points checked (dual)
   pl.dual = !serial_clamp && p->clamp_every > 0 && p->clamp_every % CH == 0 && p->clamp_every < p->seq_len;
   if (pl.dual) g.clamp_every = 0;
-  pl.chunk = ATLAS_CHUNK_PATH && p->dtype == ATLAS_DT_BF16 && !pl.dual && chunk_path_supported(g);
-  pl.sg = pl.chunk ? chunk_seg(g) : make_seg(g);
-  pl.cbwd = ATLAS_CHUNK_BWD && p->dtype == ATLAS_DT_BF16 && !pl.dual && !pl.chunk && walk_fwd_supported(g) &&
+  pl.sg = make_seg(g);
+  pl.cbwd = ATLAS_CHUNK_BWD && p->dtype == ATLAS_DT_BF16 && !pl.dual && walk_fwd_supported(g) &&
             chunk_bwd_supported(g, pl.sg);
   if (pl.cbwd) g.Lmid = 0;
   // backward: same segments, chunks of Lb
@@ -270,14 +259,13 @@ SavedLayout saved_layout(const Plan& pl) {
   L.seg = off; off += align256((size_t)g.BH * pl.sg.nseg * 2 * st);
   L.agg = off; off += align256((size_t)g.BH * pl.sg.nseg * pl.sg.agg_stride * sizeof(float));
   L.final_raw = off; off += align256((size_t)g.BH * st);
-  // the chunk-parallel path keeps nothing per chunk: the regions below are empty for it; the
-  // backward of chunk_bwd.hip takes the states at the 64-token chunk starts and forms its own records
-  const bool walk = !pl.chunk;
-  const bool brec = walk && !pl.cbwd;
-  L.rw = off; off += align256(brec ? (size_t)g.BH * g.ncb * 2 * st : pl.cbwd ? chunk_bwd_states_bytes(g) : 0);
+  // the backward of chunk_bwd.hip takes the states at the 64-token chunk starts and forms its own
+  // records; the earlier backward, the states at every backward-chunk boundary and its records
+  const bool brec = !pl.cbwd;
+  L.rw = off; off += align256(brec ? (size_t)g.BH * g.ncb * 2 * st : chunk_bwd_states_bytes(g));
   // forward scratch: per-chunk coefficient records and Ws[s, t-1] blocks
-  L.coef = off; off += align256(walk ? (size_t)g.BH * g.nc * coef_rec_floats(pl.CH) * sizeof(float) : 0);
-  L.wsh = off; off += align256(walk ? (size_t)g.BH * g.nc * pl.CH * (pl.CH + kHaloPad) * pl.esize : 0);
+  L.coef = off; off += align256((size_t)g.BH * g.nc * coef_rec_floats(pl.CH) * sizeof(float));
+  L.wsh = off; off += align256((size_t)g.BH * g.nc * pl.CH * (pl.CH + kHaloPad) * pl.esize);
   // the backward's chunk records (input-only: formed in the forward's coefficient launch)
   L.bcoef = off; off += align256(brec ? (size_t)g.BH * pl.gb.nc * coef_rec_floats(pl.CHB) * sizeof(float) : 0);
   L.bwsh = off; off += align256(brec ? (size_t)g.BH * pl.gb.nc * pl.CHB * (pl.CHB + kHaloPad) * pl.esize : 0);
@@ -361,11 +349,6 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
   float* coef = reinterpret_cast<float*>(sv + SL.coef);
   T* wsh = reinterpret_cast<T*>(sv + SL.wsh);
   const Geom& g = pl.g;
-  if constexpr (sizeof(T) == 2) {
-    if (pl.chunk)
-      return launch_chunk_fwd(g, a, pl.sg, agg, seg_states, final_raw, s) == hipSuccess ? ATLAS_MEM_OK
-                                                                                        : ATLAS_MEM_ERR_LAUNCH;
-  }
   // chunk coefficient records of the forward and of the backward (one launch, inputs only)
   constexpr int CHF = sizeof(T) == 2 ? 64 : 32, CHB = sizeof(T) == 2 ? 32 : 16;
   hipError_t err = launch_chunk_coef_pair<T, CHF, CHB>(
@@ -399,7 +382,6 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
 template <typename T>
 int run_bwd(const Plan& pl, const atlas_mem_bwd_args* x, const float* saved, void* ws, hipStream_t s) {
   const Geom& gb = pl.gb;
-  if (pl.chunk) return ATLAS_MEM_ERR_UNSUPPORTED;
   const BwdLayout L = bwd_layout(pl);
   const SavedLayout SL = saved_layout(pl);
   unsigned char* w = static_cast<unsigned char*>(ws);
