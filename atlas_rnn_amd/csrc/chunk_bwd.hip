@@ -41,24 +41,11 @@ __device__ __forceinline__ int fresh_tid() { return launder((int)threadIdx.x); }
   const int tid = fresh_tid(), lane = tid & 63, gq = lane >> 4, m = lane & 15; \
   (void)tid; (void)lane; (void)gq; (void)m;
 constexpr int NWB = NTB / 64;
-constexpr int PB = 72;    // LDS pitch (bf16 elements) of 64-wide rows (16-byte aligned rows)
 constexpr int QP = 88;    // pitch of the Q^T / R^T rows [t][s] (80 sources + 8)
 // pitch of the Gram rows [q][s'] (96 state bases: 80 products, S_c, Z_c, zeros; + 8: 52 dwords, so
 // that the rows of 16 lanes fall on distinct banks)
 constexpr int MQ = 104;
 constexpr int QX = CL + 16;   // Gram rows: 64 adjoint bases E_q, then the chunk-end adjoint's partials
-constexpr int EMAX = 17;  // window
-// chunk coefficient record (floats): cs, cz (sources), cgS, cgZ (targets), the chunk transition
-constexpr int R_CS = 0, R_CZ = SRC, R_GS = 2 * SRC, R_GZ = 2 * SRC + CL, R_TR = 2 * SRC + 2 * CL;
-constexpr int REC = R_TR + 4;   // 292
-static_assert(REC <= NTB, "one record element per thread");
-
-// Per chunk: the end record (cs, cz, cgS, cgZ, transition) and the prefix arrays (LA, LB, eta,
-// beta; the coefficients At, Kt of (S_c, Z_c) in S_{t-1} and B1 of Z_c in Z_{t-1}).
-struct ChunkCoef {
-  alignas(16) float co[REC];
-  alignas(16) float la[CL], lb[CL], eta[CL], At[CL], Kt[CL], B1[CL], be[CL];
-};
 struct BwSm;
 struct BwSm {
   alignas(16) bf16 phi[SRC][PB];     // sources (mapped)
@@ -75,14 +62,14 @@ struct BwSm {
   // them), their S_c / Z_c entries in rows 64 / 68 only. Rows 72 .. 79 zero.
   alignas(16) bf16 Mt[QX][MQ];
   alignas(16) bf16 Cb[CL][PB];       // C'[r][t]: of g_r in S_{t-1} (r, t chunk-local targets)
-  alignas(16) bf16 DA[CL][PB];       // DA[t][u] = A(u -> t - 1): the decay from token u + 1 to t - 1 (u < t)
-  alignas(16) bf16 BE[CL][PB];       // BE[r][u] = -eta_u B(r -> u) (u >= r): g_r in Z_u, into S_u
+  alignas(16) Rows64 DA;              // DA[t][u] = A(u -> t - 1): the decay from token u + 1 to t - 1 (u < t)
+  alignas(16) Rows64 BE;              // BE[r][u] = -eta_u B(r -> u) (u >= r): g_r in Z_u, into S_u
   ChunkCoef cc[2];                   // by chunk parity: the chunk in flight and the next one
   float gram[NWB][4];
   // the window band Bd[s][r] = w(r, r + HT - s) (0 <= r + HT - s < e; zero elsewhere): the weight of
   // source s in the window of target r, i.e. of lag j = r + HT - s (w: the lag gate, the token gate
   // of the source, or 1; zero for targets past T)
-  alignas(16) bf16 Bd[SRC][PB];
+  alignas(16) BandRows Bd;
 };
 
 static_assert(sizeof(BwSm) <= 160 * 1024, "one workgroup per CU: at most 160 KB of LDS");
@@ -186,9 +173,6 @@ __device__ __forceinline__ void gates_store(const ScalPf& p, const Geom& g, BwSm
   }
 }
 
-// window weight of lag j for chunk target r (the chunk's staged band)
-__device__ __forceinline__ float cw(const BwSm& sm, int r, int j) { return static_cast<float>(sm.Bd[r + HT - j][r]); }
-
 // B'[u][t] = the coefficient of g_u in Z_{t-1}: B(u -> t - 1) = exp2(LB[t-1] - LB[u]) for u <= t - 1
 // with momentum, [u == t - 1] without. Operand rows t (lane & 15), k slots natural over u.
 template <bool MOM>
@@ -199,89 +183,6 @@ __device__ __forceinline__ bf16x8 gen_zcoef(const float* lb, int t, int q, int l
 #pragma unroll
   for (int e = 0; e < 8; ++e) f[e] = static_cast<bf16>(32 * q + 8 * gq + e == t - 1 ? 1.f : 0.f);
   return f;
-}
-
-// wave 0: the chunk's end coefficients (cgS, cgZ per target; the transition) from its scalars
-__device__ __forceinline__ void chunk_end_scan(const Geom& g, const ScalPf& p, int t0, ChunkCoef& sm) {
-  const int lane = fresh_tid() & 63;
-  // lane j holds target r = 63 - j (the chunk read backwards); targets past T are the identity
-  const float al = __shfl(bf(p.al), 63 - lane, 64), et = __shfl(bf(p.et), 63 - lane, 64),
-              be = __shfl(bf(p.be), 63 - lane, 64);
-  const Tri x{al, -et * be, be};
-  const Tri inc = wave_scan<false>(x, lane);
-  Tri ex = tri_prev_lane(inc);
-  if (lane == 0) ex = tri_id();
-  const int r = 63 - lane;
-  const bool real = t0 + r < g.T;
-  sm.co[R_GS + r] = real ? ex.k - et * ex.a : 0.f;
-  sm.co[R_GZ + r] = real ? ex.b : 0.f;
-  if (lane == 63) { sm.co[R_TR] = inc.a; sm.co[R_TR + 1] = inc.k; sm.co[R_TR + 2] = inc.b; sm.co[R_TR + 3] = 0.f; }
-}
-// threads s < 80: the per-source end coefficients from cgS / cgZ (needs chunk_end_scan's output
-// and the band): cs_s = sum_j w(s - HT + j, j) cgS[s - HT + j], cz_s likewise with cgZ
-__device__ __forceinline__ void chunk_end_sources(const Geom& g, const BwSm& sm, ChunkCoef& kc, int s) {
-  if (s >= 0 && s < SRC) {
-    float cs = 0.f, cz = 0.f;
-    for (int j = 0; j < g.e; ++j) {
-      const int r = s - HT + j;
-      if (r >= 0 && r < CL) {
-        const float wgt = cw(sm, r, j);
-        cs += wgt * kc.co[R_GS + r];
-        cz += wgt * kc.co[R_GZ + r];
-      }
-    }
-    kc.co[R_CS + s] = cs;
-    kc.co[R_CZ + s] = cz;
-  }
-}
-
-// The two factors of C' = BE DA^T from the prefix arrays, one row segment per thread (512 threads:
-// row i >> 3, columns 8 (i & 7) .. +7): loads unconditional, the triangles applied by selects.
-template <bool MOM>
-__device__ __forceinline__ void gen_tables(BwSm& sm, const ChunkCoef& kc, int i) {
-  const int row = i >> 3, u0 = (i & 7) * 8;
-  const float4 a0 = *reinterpret_cast<const float4*>(&kc.la[u0]), a1 = *reinterpret_cast<const float4*>(&kc.la[u0 + 4]);
-  const float lau[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-  const float lat = kc.la[row > 0 ? row - 1 : 0];
-  const float4 e0 = *reinterpret_cast<const float4*>(&kc.eta[u0]), e1 = *reinterpret_cast<const float4*>(&kc.eta[u0 + 4]);
-  const float etu[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
-  const float4 b0 = *reinterpret_cast<const float4*>(&kc.lb[u0]), b1 = *reinterpret_cast<const float4*>(&kc.lb[u0 + 4]);
-  const float lbu[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-  const float lbr = kc.lb[row];
-  bf16x8 da, be;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int u = u0 + e;
-    const float x = __builtin_amdgcn_exp2f(lat - lau[e]);
-    da[e] = static_cast<bf16>(u <= row - 1 ? x : 0.f);
-    float v;
-    if (MOM) {
-      const float y = -etu[e] * __builtin_amdgcn_exp2f(lbu[e] - lbr);
-      v = u >= row ? y : 0.f;
-    } else {
-      v = u == row ? -etu[e] : 0.f;
-    }
-    be[e] = static_cast<bf16>(v);
-  }
-  *reinterpret_cast<bf16x8*>(&sm.DA[row][u0]) = da;
-  *reinterpret_cast<bf16x8*>(&sm.BE[row][u0]) = be;
-}
-
-// wave 0: the chunk's prefix arrays: LA, LB (log2 prefix sums), eta, beta, and the coefficients of
-// (S_c, Z_c) in S_{t-1} (At, Kt) and of Z_c in Z_{t-1} (B1)
-__device__ __forceinline__ void chunk_prefix(const ScalPf& p, ChunkCoef& sm) {
-  const int lane = fresh_tid() & 63;
-  const float al = bf(p.al), et = bf(p.et), be = bf(p.be);
-  sm.la[lane] = wave_prefix_sum(fmaxf(__log2f(al), kLogFloor), lane);
-  sm.lb[lane] = wave_prefix_sum(fmaxf(__log2f(be), kLogFloor), lane);
-  sm.eta[lane] = et;
-  sm.be[lane] = be;
-  const Tri inc = wave_scan<true>(Tri{al, -et * be, be}, lane);
-  Tri ex = tri_prev_lane(inc);
-  if (lane == 0) ex = tri_id();
-  sm.At[lane] = ex.a;
-  sm.Kt[lane] = ex.k;
-  sm.B1[lane] = ex.b;
 }
 
 // Sum over the 64 lanes, in every lane (DPP row sums, then the cross-row swaps).
@@ -386,8 +287,8 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
   rows_load<WL_R>(pf, rk, rv, rq, rdy, (c_end - 1) * CL, w);
   xs_load(c_end - 1, xn);
   // the last chunk's record and prefix arrays (every later chunk's are formed one step ahead)
-  if (w == 0) chunk_prefix(sp, sm.cc[(c_end - c_begin - 1) & 1]);
-  if (w == 1) chunk_end_scan(g, sp, (c_end - 1) * CL, sm.cc[(c_end - c_begin - 1) & 1]);
+  if (w == 0) chunk_prefix(bf(sp.al), bf(sp.et), bf(sp.be), lane, sm.cc[(c_end - c_begin - 1) & 1]);
+  if (w == 1) chunk_end_scan(g, bf(sp.al), bf(sp.et), bf(sp.be), (c_end - 1) * CL, lane, sm.cc[(c_end - c_begin - 1) & 1]);
 #pragma unroll 1
   for (int cr = c_end - c_begin - 1; cr >= 0; --cr) {
     CPB_FRESH_LANE
@@ -404,7 +305,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
     __syncthreads();
     rows_store<MAPE, WL_R>(pf, sm, g.map_deg, w);
     gates_store(sp, g, sm);
-    gen_tables<MOM>(sm, kc, tid);
+    gen_tables<MOM>(kc, sm.DA, sm.BE, tid);
     // the next chunk's scalars, early: waves 0, 1 form its record and prefix arrays at the end of R4
     if (c > c_begin) scal_load(sp, g, a, rowbase, t0 - CL);
     else sp = ScalPf{};
@@ -462,7 +363,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
 #pragma unroll
         for (int r = 0; r < 4; ++r) sm.Cb[16 * q4 + 4 * gq + r][16 * tt + m] = static_cast<bf16>(acc[r]);
       }
-      chunk_end_sources(g, sm, kc, tid - 256);   // threads 256 .. 335: cs, cz of the chunk's sources
+      chunk_end_sources(g, sm.Bd, kc, tid - 256);   // threads 256 .. 335: cs, cz of the chunk's sources
       if (tid < 4) {   // <lamS, S_c>, <lamS, Z_c>, <lamZ, S_c>, <lamZ, Z_c> into the end rows
         float gsum = 0.f;
 #pragma unroll
@@ -870,8 +771,8 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
       // the next chunk's record and prefix arrays, from the scalars just fetched (the other buffer:
       // this chunk's is still read below)
       if (c > c_begin) {
-        if (w == 0) chunk_prefix(sp, sm.cc[(cr - 1) & 1]);
-        if (w == 1) chunk_end_scan(g, sp, t0 - CL, sm.cc[(cr - 1) & 1]);
+        if (w == 0) chunk_prefix(bf(sp.al), bf(sp.et), bf(sp.be), lane, sm.cc[(cr - 1) & 1]);
+        if (w == 1) chunk_end_scan(g, bf(sp.al), bf(sp.et), bf(sp.be), t0 - CL, lane, sm.cc[(cr - 1) & 1]);
       }
     }
 

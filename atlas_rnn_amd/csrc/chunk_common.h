@@ -110,5 +110,109 @@ __device__ __forceinline__ bf16x8 gen_decay_to(const float* la, int t, int q, in
   }
   return f;
 }
+
+constexpr int PB = 72;     // LDS pitch (bf16 elements) of 64-wide rows (16-byte aligned rows)
+constexpr int EMAX = 17;   // longest window
+// chunk coefficient record (floats): cs, cz (sources: coefficients of G_s in S, Z at the chunk end),
+// cgS, cgZ (targets: of g_r in S, Z at the chunk end), the chunk transition (a, k, b, 0)
+constexpr int R_CS = 0, R_CZ = SRC, R_GS = 2 * SRC, R_GZ = 2 * SRC + CL, R_TR = 2 * SRC + 2 * CL;
+constexpr int REC = R_TR + 4;   // 292
+
+// Per chunk: the end record and the prefix arrays (LA, LB, eta, beta; the coefficients At, Kt of
+// (S_c, Z_c) in S_{t-1} and B1 of Z_c in Z_{t-1}).
+struct ChunkCoef {
+  alignas(16) float co[REC];
+  alignas(16) float la[CL], lb[CL], eta[CL], At[CL], Kt[CL], B1[CL], be[CL];
+};
+// the window band of a chunk: Bd[s][r] = w(r, r + HT - s) for 0 <= r + HT - s < e (zero elsewhere),
+// the weight of source s in the window of target r (w: the lag gate, the token gate of the source,
+// or 1; zero for targets past T)
+typedef bf16 BandRows[SRC][PB];
+typedef bf16 Rows64[CL][PB];
+
+// window weight of lag j for chunk target r (from the staged band)
+__device__ __forceinline__ float cw(const BandRows& Bd, int r, int j) { return static_cast<float>(Bd[r + HT - j][r]); }
+
+// One wave (lane = target r, its scalars al, et, be; the identity past T): the chunk's end
+// coefficients cgS, cgZ of every target and the chunk transition.
+__device__ __forceinline__ void chunk_end_scan(const Geom& g, float al0, float et0, float be0, int t0, int lane,
+                                               ChunkCoef& kc) {
+  // lane j holds target r = 63 - j (the chunk read backwards)
+  const float al = __shfl(al0, 63 - lane, 64), et = __shfl(et0, 63 - lane, 64), be = __shfl(be0, 63 - lane, 64);
+  const Tri x{al, -et * be, be};
+  const Tri inc = wave_scan<false>(x, lane);
+  Tri ex = tri_prev_lane(inc);
+  if (lane == 0) ex = tri_id();
+  const int r = 63 - lane;
+  const bool real = t0 + r < g.T;
+  kc.co[R_GS + r] = real ? ex.k - et * ex.a : 0.f;
+  kc.co[R_GZ + r] = real ? ex.b : 0.f;
+  if (lane == 63) { kc.co[R_TR] = inc.a; kc.co[R_TR + 1] = inc.k; kc.co[R_TR + 2] = inc.b; kc.co[R_TR + 3] = 0.f; }
+}
+// Thread s < 80: the per-source end coefficients from cgS / cgZ (after chunk_end_scan and the band):
+// cs_s = sum_j w(s - HT + j, j) cgS[s - HT + j], cz_s likewise with cgZ.
+__device__ __forceinline__ void chunk_end_sources(const Geom& g, const BandRows& Bd, ChunkCoef& kc, int s) {
+  if (s >= 0 && s < SRC) {
+    float cs = 0.f, cz = 0.f;
+    for (int j = 0; j < g.e; ++j) {
+      const int r = s - HT + j;
+      if (r >= 0 && r < CL) {
+        const float wgt = cw(Bd, r, j);
+        cs += wgt * kc.co[R_GS + r];
+        cz += wgt * kc.co[R_GZ + r];
+      }
+    }
+    kc.co[R_CS + s] = cs;
+    kc.co[R_CZ + s] = cz;
+  }
+}
+// The two factors of C' = BE DA^T (C'[r][t]: the coefficient of g_r in S_{t-1}) from the prefix
+// arrays: DA[t][u] = A(u -> t - 1) (u < t), BE[r][u] = -eta_u B(r -> u) (u >= r; without momentum
+// -eta_r at u = r). Item i < 512: row i >> 3, columns 8 (i & 7) .. +7; loads unconditional, the
+// triangles applied by selects.
+template <bool MOM>
+__device__ __forceinline__ void gen_tables(const ChunkCoef& kc, Rows64& DA, Rows64& BE, int i) {
+  const int row = i >> 3, u0 = (i & 7) * 8;
+  const float4 a0 = *reinterpret_cast<const float4*>(&kc.la[u0]), a1 = *reinterpret_cast<const float4*>(&kc.la[u0 + 4]);
+  const float lau[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+  const float lat = kc.la[row > 0 ? row - 1 : 0];
+  const float4 e0 = *reinterpret_cast<const float4*>(&kc.eta[u0]), e1 = *reinterpret_cast<const float4*>(&kc.eta[u0 + 4]);
+  const float etu[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+  const float4 b0 = *reinterpret_cast<const float4*>(&kc.lb[u0]), b1 = *reinterpret_cast<const float4*>(&kc.lb[u0 + 4]);
+  const float lbu[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+  const float lbr = kc.lb[row];
+  bf16x8 da, be;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int u = u0 + e;
+    const float x = __builtin_amdgcn_exp2f(lat - lau[e]);
+    da[e] = static_cast<bf16>(u <= row - 1 ? x : 0.f);
+    float v;
+    if (MOM) {
+      const float y = -etu[e] * __builtin_amdgcn_exp2f(lbu[e] - lbr);
+      v = u >= row ? y : 0.f;
+    } else {
+      v = u == row ? -etu[e] : 0.f;
+    }
+    be[e] = static_cast<bf16>(v);
+  }
+  *reinterpret_cast<bf16x8*>(&DA[row][u0]) = da;
+  *reinterpret_cast<bf16x8*>(&BE[row][u0]) = be;
+}
+// One wave (lane = target, its scalars): the chunk's prefix arrays LA, LB (log2 prefix sums, floored),
+// eta, beta, and At, Kt, B1.
+__device__ __forceinline__ void chunk_prefix(float al, float et, float be, int lane, ChunkCoef& kc) {
+  kc.la[lane] = wave_prefix_sum(fmaxf(__log2f(al), kLogFloor), lane);
+  kc.lb[lane] = wave_prefix_sum(fmaxf(__log2f(be), kLogFloor), lane);
+  kc.eta[lane] = et;
+  kc.be[lane] = be;
+  const Tri inc = wave_scan<true>(Tri{al, -et * be, be}, lane);
+  Tri ex = tri_prev_lane(inc);
+  if (lane == 0) ex = tri_id();
+  kc.At[lane] = ex.a;
+  kc.Kt[lane] = ex.k;
+  kc.B1[lane] = ex.b;
+}
+
 }  // namespace cp
 }  // namespace atlas
