@@ -19,7 +19,7 @@ ROOT = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libatlas_mem.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["abi.hip", "coef.hip", "seg_fwd.hip", "seg_bwd.hip", "scan.hip", "affine.hip", "bwd_scalar.hip", "walk_fwd.hip", "walk_bwd.hip", "tmap.hip", "step.hip", "prologue.hip", "blocks.hip", "factors.hip", "bufwalk.hip", "wgrad.hip", "gemm.hip", "chunk_bwd.hip"]
+SOURCES = ["abi.hip", "coef.hip", "seg_fwd.hip", "seg_bwd.hip", "scan.hip", "affine.hip", "bwd_scalar.hip", "walk_fwd.hip", "walk_bwd.hip", "tmap.hip", "step.hip", "prologue.hip", "blocks.hip", "factors.hip", "bufwalk.hip", "wgrad.hip", "gemm.hip", "chunk_bwd.hip", "chunk_coef.hip"]
 ARCH = os.environ.get("ATLAS_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

@@ -23,6 +23,9 @@ template <typename T, int CH, int D>
 hipError_t launch_bwd_seg(const Geom&, const BwdPtrs<T>&, const SegGeom&, const BwdSegPtrs&, hipStream_t, bool,
                           const AggOverFwd*);
 bool walk_fwd_supported(const Geom& g);
+bool chunk_coef_fwd_supported(const Geom& g);
+hipError_t launch_chunk_coef_fwd(const Geom& g, const bf16* decay, const bf16* lr, const bf16* beta, const bf16* gate,
+                                 float* coef, bf16* wsh, hipStream_t stream);
 hipError_t launch_buf_state(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, const float* coef, float* corr,
                             hipStream_t stream);
 hipError_t launch_buf_y(const Geom& g, const FwdPtrs<bf16>& a, const bf16* wsh, hipStream_t stream);
@@ -137,10 +140,16 @@ struct Plan {
   // clamp, no carried buffer): the forward saves no boundary states and no backward records, and
   // its chunks have no mid point (Lmid = 0)
   bool cbwd;
+  // cbwd plans: the forward records formed on the matrix cores (chunk_coef.hip) instead of by the
+  // per-source chains (coef.hip)
+  bool ccoef;
 };
 
 #ifndef ATLAS_CHUNK_BWD
 #define ATLAS_CHUNK_BWD 1
+#endif
+#ifndef ATLAS_CHUNK_COEF
+#define ATLAS_CHUNK_COEF 1
 #endif
 
 // Segments per head-batch row: enough (segment, bh) workgroups for one per CU (the walks hold a
@@ -218,6 +227,7 @@ Plan make_plan(const atlas_mem_problem* p, bool serial_clamp = false) {
   pl.cbwd = ATLAS_CHUNK_BWD && p->dtype == ATLAS_DT_BF16 && !pl.dual && walk_fwd_supported(g) &&
             chunk_bwd_supported(g, pl.sg);
   if (pl.cbwd) g.Lmid = 0;
+  pl.ccoef = ATLAS_CHUNK_COEF && pl.cbwd && chunk_coef_fwd_supported(g);
   // backward: same segments, chunks of Lb
   Geom& gb = pl.gb;
   gb = g;
@@ -351,9 +361,15 @@ int run_fwd(const Plan& pl, const atlas_mem_fwd_args* x, float* saved, hipStream
   const Geom& g = pl.g;
   // chunk coefficient records of the forward and of the backward (one launch, inputs only)
   constexpr int CHF = sizeof(T) == 2 ? 64 : 32, CHB = sizeof(T) == 2 ? 32 : 16;
-  hipError_t err = launch_chunk_coef_pair<T, CHF, CHB>(
-      g, pl.gb, a.decay, a.lr, a.beta, a.gate, coef, wsh, pl.cbwd ? nullptr : reinterpret_cast<float*>(sv + SL.bcoef),
-      pl.cbwd ? nullptr : reinterpret_cast<T*>(sv + SL.bwsh), s);
+  hipError_t err = hipErrorInvalidValue;
+  if constexpr (sizeof(T) == 2) {
+    if (pl.ccoef)
+      err = launch_chunk_coef_fwd(g, a.decay, a.lr, a.beta, a.gate, coef, wsh, s);
+  }
+  if (!pl.ccoef)
+    err = launch_chunk_coef_pair<T, CHF, CHB>(
+        g, pl.gb, a.decay, a.lr, a.beta, a.gate, coef, wsh, pl.cbwd ? nullptr : reinterpret_cast<float*>(sv + SL.bcoef),
+        pl.cbwd ? nullptr : reinterpret_cast<T*>(sv + SL.bwsh), s);
   if (err != hipSuccess) return ATLAS_MEM_ERR_LAUNCH;
   err = hipErrorInvalidValue;
   if (g.DK == 64) {

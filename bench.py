@@ -86,6 +86,8 @@ def algorithmic_bytes(bh=BH, t=T, d=D, e=E, n_sc=None, s_in=2, s_st=4):
         "k_bwd_seg_scan": 0,
         # forward and backward chunk records in one launch (reads the per-token scalars once)
         "k_chunk_coef_pair": n * n_sc * s_in,
+        # forward chunk records only, on the matrix cores (plans whose backward forms its own)
+        "k_chunk_coef_fwd": n * n_sc * s_in,
     }
     # launches that carry a second, independent stage as extra workgroups
     per_kernel["k_fwd_seg_scan+buffer_out"] = per_kernel["k_fwd_seg_scan"] + per_kernel["k_buffer_out"]
