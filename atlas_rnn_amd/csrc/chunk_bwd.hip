@@ -33,6 +33,23 @@ using namespace cp;
 
 constexpr int NTB = 512;
 
+// The walk's arguments, re-read from the kernarg segment where the chunk loop uses them (scalar
+// loads through a laundered pointer) instead of being held in scalar registers for the whole walk:
+// the loop needs more uniform values than there are scalar registers, and those held would be
+// spilled to vector-register lanes and read back with v_readlane on every chunk.
+struct CpArgs {
+  Geom g;
+  BwdPtrs<bf16> a;
+  SegGeom sg;
+  BwdSegPtrs p;
+};
+typedef const __attribute__((address_space(4))) CpArgs* CpK;
+__device__ __forceinline__ CpK kargs() {
+  CpK k = (CpK)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(k));
+  return k;
+}
+
 // The thread index through an empty asm: values derived from it inside the walk's loops are
 // recomputed where they are used instead of being hoisted out of the loop and held in registers
 // for its whole length.
@@ -83,8 +100,13 @@ template <int NWL>
 struct RowPf { u32x4v v[(NWL + NWB - 1) / NWB]; };
 
 template <int NWL>
-__device__ __forceinline__ void rows_load(RowPf<NWL>& pf, rsrc_t rk, rsrc_t rv, rsrc_t rq, rsrc_t rdy, int t0, int w) {
+__device__ __forceinline__ void rows_load(RowPf<NWL>& pf, int t0, int w) {
   const int lane = fresh_tid() & 63;
+  const CpK K = kargs();
+  const size_t rb = (size_t)blockIdx.y * K->g.T * D;
+  const uint32_t nb = (uint32_t)K->g.T * (D * 2);
+  const rsrc_t rk = make_rsrc(K->a.k + rb, nb), rv = make_rsrc(K->a.v + rb, nb);
+  const rsrc_t rq = make_rsrc(K->a.q + rb, nb), rdy = make_rsrc(K->a.dy + rb, nb);
   const uint32_t lo = (uint32_t)((lane >> 3) * (D * 2) + (lane & 7) * 16);
 #pragma unroll
   for (int u = 0; u < (NWL + NWB - 1) / NWB; ++u) {
@@ -133,15 +155,18 @@ struct ScalPf {
   unsigned short al, et, be;
   unsigned short gt[3];
 };
-__device__ __forceinline__ void scal_load(ScalPf& p, const Geom& g, const BwdPtrs<bf16>& a, size_t rowbase, int t0) {
+__device__ __forceinline__ void scal_load(ScalPf& p, int t0) {
   const int tid = fresh_tid();
+  const CpK K = kargs();
+  const int T = K->g.T, e = K->g.e, gm = K->g.gate_mode;
+  const size_t rowbase = (size_t)blockIdx.y * T;
   // waves 0 and 1 (lane = target): the prefix arrays and the end record are formed from them
   p.al = 0x3f80; p.et = 0; p.be = 0x3f80;   // 1, 0, 1 (the identity past T)
-  if (tid < 128 && t0 + (tid & 63) < g.T) {
+  if (tid < 128 && t0 + (tid & 63) < T) {
     const size_t o = rowbase + t0 + (tid & 63);
-    p.al = __builtin_bit_cast(unsigned short, a.decay[o]);
-    p.et = __builtin_bit_cast(unsigned short, a.lr[o]);
-    p.be = g.momentum ? __builtin_bit_cast(unsigned short, a.beta[o]) : (unsigned short)0;
+    p.al = __builtin_bit_cast(unsigned short, K->a.decay[o]);
+    p.et = __builtin_bit_cast(unsigned short, K->a.lr[o]);
+    p.be = K->g.momentum ? __builtin_bit_cast(unsigned short, K->a.beta[o]) : (unsigned short)0;
   }
   // window weight w(r, j) of target r, lag j: the lag gate, the gate of the source token t0 + r - j,
   // or 1; zero for targets past T
@@ -149,25 +174,25 @@ __device__ __forceinline__ void scal_load(ScalPf& p, const Geom& g, const BwdPtr
   for (int u = 0; u < 3; ++u) {
     p.gt[u] = 0;
     const int i = tid + NTB * u;
-    const int r = i / g.e, j = i - r * g.e;
-    if (r < CL && t0 + r < g.T) {
-      if (g.gate_mode == GATE_LAG) {
-        p.gt[u] = __builtin_bit_cast(unsigned short, a.gate[(rowbase + t0 + r) * g.e + j]);
-      } else if (g.gate_mode == GATE_TOKEN) {
-        if (t0 + r - j >= 0) p.gt[u] = __builtin_bit_cast(unsigned short, a.gate[rowbase + t0 + r - j]);
+    const int r = i / e, j = i - r * e;
+    if (r < CL && t0 + r < T) {
+      if (gm == GATE_LAG) {
+        p.gt[u] = __builtin_bit_cast(unsigned short, K->a.gate[(rowbase + t0 + r) * e + j]);
+      } else if (gm == GATE_TOKEN) {
+        if (t0 + r - j >= 0) p.gt[u] = __builtin_bit_cast(unsigned short, K->a.gate[rowbase + t0 + r - j]);
       } else {
         p.gt[u] = 0x3f80;
       }
     }
   }
 }
-__device__ __forceinline__ void gates_store(const ScalPf& p, const Geom& g, BwSm& sm) {
+__device__ __forceinline__ void gates_store(const ScalPf& p, int e, BwSm& sm) {
   const int tid = fresh_tid();
 #pragma unroll
   for (int u = 0; u < 3; ++u) {
     const int i = tid + NTB * u;
-    if (i < CL * g.e) {
-      const int r = i / g.e, j = i - r * g.e;
+    if (i < CL * e) {
+      const int r = i / e, j = i - r * e;
       sm.Bd[r + HT - j][r] = __builtin_bit_cast(bf16, p.gt[u]);
     }
   }
@@ -203,8 +228,11 @@ __device__ __forceinline__ float hi16(unsigned u) { return __builtin_bit_cast(fl
 using namespace cpb;
 
 template <bool MAPE, bool MOM>
-__global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16> a, const SegGeom sg,
-                                                 const BwdSegPtrs p) {
+__global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
+  const Geom& g = A.g;
+  const BwdPtrs<bf16>& a = A.a;
+  const SegGeom& sg = A.sg;
+  const BwdSegPtrs& p = A.p;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   BwSm& sm = *reinterpret_cast<BwSm*>(smem_raw);
   const int tid = threadIdx.x, lane = lane_id();
@@ -216,14 +244,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
   const int tok0 = c_begin * CL, tok1 = min(g.T, c_end * CL);
   const int H = g.H;
   const int tail0 = tok1 - H;   // the segment's last H tokens: partial results for the fixup
-  const size_t rowbase = (size_t)bh * g.T;
   const size_t DD = (size_t)D * D;
-  const uint32_t row_bytes = (uint32_t)g.T * (D * 2);
-  const rsrc_t rk = make_rsrc(a.k + rowbase * D, row_bytes);
-  const rsrc_t rv = make_rsrc(a.v + rowbase * D, row_bytes);
-  const rsrc_t rq = make_rsrc(a.q + rowbase * D, row_bytes);
-  const rsrc_t rdy = make_rsrc(a.dy + rowbase * D, row_bytes);
-  const rsrc_t rdq = make_rsrc(a.dq + rowbase * D, row_bytes);
 
   bf16x8 sref[2];
   load_sref(a.S_ref + (size_t)bh * DD, q4, sref);
@@ -246,9 +267,9 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
   // chunk-start states saved by the forward walk (walk_common.h fragment layout), one block per
   // 64-token chunk of the row: this lane's slice X[16 q4 + 4 gq + r][16 kt + m] (kt = 2 hf + j) is
   // one 8-byte half of fragment (kt, q4 >> 1)
-  const unsigned char* xrow = reinterpret_cast<const unsigned char*>(p.rw) + (size_t)bh * g.nc * kStateBlk;
   auto xs_load = [&](int c, unsigned (&xv)[8]) {
-    const unsigned char* blk = xrow + (size_t)c * kStateBlk;
+    const CpK K = kargs();
+    const unsigned char* blk = reinterpret_cast<const unsigned char*>(K->p.rw) + ((size_t)bh * K->g.nc + c) * kStateBlk;
     const int ln = fresh_tid() & 63;
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
@@ -283,15 +304,16 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
   RowPf<WL_R> pf;
   ScalPf sp;
   unsigned xn[8];   // the next chunk's state slice, in flight with its rows
-  scal_load(sp, g, a, rowbase, (c_end - 1) * CL);
-  rows_load<WL_R>(pf, rk, rv, rq, rdy, (c_end - 1) * CL, w);
+  scal_load(sp, (c_end - 1) * CL);
+  rows_load<WL_R>(pf, (c_end - 1) * CL, w);
   xs_load(c_end - 1, xn);
   // the last chunk's record and prefix arrays (every later chunk's are formed one step ahead)
   if (w == 0) chunk_prefix(bf(sp.al), bf(sp.et), bf(sp.be), lane, sm.cc[(c_end - c_begin - 1) & 1]);
-  if (w == 1) chunk_end_scan(g, bf(sp.al), bf(sp.et), bf(sp.be), (c_end - 1) * CL, lane, sm.cc[(c_end - c_begin - 1) & 1]);
+  if (w == 1) chunk_end_scan(g.T, bf(sp.al), bf(sp.et), bf(sp.be), (c_end - 1) * CL, lane, sm.cc[(c_end - c_begin - 1) & 1]);
 #pragma unroll 1
   for (int cr = c_end - c_begin - 1; cr >= 0; --cr) {
     CPB_FRESH_LANE
+    // the wave's role, recomputed each chunk (conditions derived from it are not held across the loop)
     ChunkCoef& kc = sm.cc[cr & 1];   // this chunk's record and prefix arrays (formed one step ahead)
     const int c = c_begin + cr;
     const int t0 = c * CL;
@@ -304,10 +326,10 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
     // ---- R0: stage the chunk
     __syncthreads();
     rows_store<MAPE, WL_R>(pf, sm, g.map_deg, w);
-    gates_store(sp, g, sm);
+    gates_store(sp, kargs()->g.e, sm);
     gen_tables<MOM>(kc, sm.DA, sm.BE, tid);
     // the next chunk's scalars, early: waves 0, 1 form its record and prefix arrays at the end of R4
-    if (c > c_begin) scal_load(sp, g, a, rowbase, t0 - CL);
+    if (c > c_begin) scal_load(sp, t0 - CL);
     else sp = ScalPf{};
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -379,6 +401,10 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
       CPB_FRESH_LANE
       const int tt = q4;
       const int t = 16 * tt + m;
+      const CpK K = kargs();
+      const size_t rb = (size_t)bh * K->g.T * D;
+      const uint32_t nb = (uint32_t)K->g.T * (D * 2);
+      const rsrc_t rdq = make_rsrc(K->a.dq + rb, nb);
       // C' as the k-major operand over the targets r (lane row t): shared by every source tile
       const bf16x8 fcb0 = frag_tr_l(&sm.Cb[0][0], PB, 16 * tt, 0, lane);
       const bf16x8 fcb1 = frag_tr_l(&sm.Cb[0][0], PB, 16 * tt, 32, lane);
@@ -430,9 +456,10 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] = di[r] + At * ds[r] + Kt * dz[r];
         if constexpr (MAPE) {
-          const u32x2v raw = bld8(rq, (uint32_t)(((t0 + t) * D + 16 * kt + 4 * gq) * 2));
-          o[0] *= poly_map_grad(lo16(raw[0]), g.map_deg); o[1] *= poly_map_grad(hi16(raw[0]), g.map_deg);
-          o[2] *= poly_map_grad(lo16(raw[1]), g.map_deg); o[3] *= poly_map_grad(hi16(raw[1]), g.map_deg);
+          const u32x2v raw = bld8(make_rsrc(K->a.q + rb, nb), (uint32_t)(((t0 + t) * D + 16 * kt + 4 * gq) * 2));
+          const int deg = K->g.map_deg;
+          o[0] *= poly_map_grad(lo16(raw[0]), deg); o[1] *= poly_map_grad(hi16(raw[0]), deg);
+          o[2] *= poly_map_grad(lo16(raw[1]), deg); o[3] *= poly_map_grad(hi16(raw[1]), deg);
         }
         u32x2v out;
         out[0] = pk(o[0], o[1]);
@@ -490,6 +517,8 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
     if (hf == 1) {
       CPB_FRESH_LANE
       const int ct = q4;
+      const CpK K = kargs();
+      const size_t rowbase = (size_t)bh * K->g.T;
       float cin[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) cin[r] = cdv[r];
@@ -518,32 +547,32 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
             if (st == SRC / 16 - 1)
 #pragma unroll
               for (int r = 0; r < 4; ++r) val[r] += cin[r];
-            st_at(a.dv + rowbase * D, (uint32_t)((pp * D + col0) * 2), make_uint2(pk(val[0], val[1]), pk(val[2], val[3])));
+            st_at(K->a.dv + rowbase * D, (uint32_t)((pp * D + col0) * 2), make_uint2(pk(val[0], val[1]), pk(val[2], val[3])));
           }
         } else if (st == 0) {   // halo rows: partial for the previous chunk (or the previous segment)
           if (seg_first) {
             if (seg > 0 && s >= HT - H)
-              st_at(part_row(p.halo_part, bh, sg.nseg, seg, H), (uint32_t)(((s - (HT - H)) * (2 * D) + col0) * 4),
+              st_at(part_row(K->p.halo_part, bh, K->sg.nseg, seg, H), (uint32_t)(((s - (HT - H)) * (2 * D) + col0) * 4),
                     make_float4(val[0], val[1], val[2], val[3]));
           } else {
 #pragma unroll
             for (int r = 0; r < 4; ++r) cdv[r] = val[r];
           }
-        } else if (pp < g.T) {
+        } else if (pp < K->g.T) {
           if (st == SRC / 16 - 1 && !seg_last)
 #pragma unroll
             for (int r = 0; r < 4; ++r) val[r] += cin[r];
           if (pp >= tail0)
-            st_at(part_row(p.tail_part, bh, sg.nseg, seg, H), (uint32_t)(((pp - tail0) * (2 * D) + col0) * 4),
+            st_at(part_row(K->p.tail_part, bh, K->sg.nseg, seg, H), (uint32_t)(((pp - tail0) * (2 * D) + col0) * 4),
                   make_float4(val[0], val[1], val[2], val[3]));
           else
-            st_at(a.dv + rowbase * D, (uint32_t)((pp * D + col0) * 2), make_uint2(pk(val[0], val[1]), pk(val[2], val[3])));
+            st_at(K->a.dv + rowbase * D, (uint32_t)((pp * D + col0) * 2), make_uint2(pk(val[0], val[1]), pk(val[2], val[3])));
         }
       }
       // the window gradients dw[t][j] = <lamZ_t, G_{t-j}> = (Km M)[t][t + HT - j] (this half's
       // share of the scalar phase): the state-base tiles tt and tt + 1 hold the band of the
       // targets t = 16 tt + 4 gq + r
-      if (g.gate_mode != GATE_NONE) {
+      if (K->g.gate_mode != GATE_NONE) {
         const int tt = q4, tl = 16 * tt + m;
         const float cgs = kc.co[R_GS + tl], cgz = kc.co[R_GZ + tl];
         bf16x8 kme;   // Km over the end rows (k = 64 + 8 gq + e): cgS on the lamS partials, cgZ on lamZ's
@@ -564,10 +593,11 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
           for (int r = 0; r < 4; ++r) {
             const int t = 16 * tt + 4 * gq + r, sq = 16 * sp + m;
             const int jb = t + HT - sq;
-            if (jb >= 0 && jb < g.e && t0 + t < g.T) {
-              const uint32_t o = (uint32_t)((t0 + t) * g.e + jb);
-              if (g.gate_mode == GATE_LAG) st_at(a.dgate + rowbase * g.e, o * 2, static_cast<bf16>(rz[r]));
-              else st_at(p.dw + rowbase * g.e, o * 4, rz[r]);
+            const int e = K->g.e;
+            if (jb >= 0 && jb < e && t0 + t < K->g.T) {
+              const uint32_t o = (uint32_t)((t0 + t) * e + jb);
+              if (K->g.gate_mode == GATE_LAG) st_at(K->a.dgate + rowbase * e, o * 2, static_cast<bf16>(rz[r]));
+              else st_at(K->p.dw + rowbase * e, o * 4, rz[r]);
             }
           }
         }
@@ -676,11 +706,13 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
       ea = xsum_rows(ea);
       eb = xsum_rows(eb);
       bt = xsum_rows(bt);
-      if (gq == 0 && t0 + tl < g.T) {
+      const CpK K = kargs();
+      if (gq == 0 && t0 + tl < K->g.T) {
         const uint32_t o = (uint32_t)(t0 + tl) * 2;
-        st_at(a.ddecay + rowbase, o, static_cast<bf16>(al));
-        st_at(a.dlr + rowbase, o, static_cast<bf16>(-(kc.be[tl] * ea + eb)));
-        if (MOM) st_at(a.dbeta + rowbase, o, static_cast<bf16>(bt));
+        const size_t rowbase = (size_t)bh * K->g.T;
+        st_at(K->a.ddecay + rowbase, o, static_cast<bf16>(al));
+        st_at(K->a.dlr + rowbase, o, static_cast<bf16>(-(kc.be[tl] * ea + eb)));
+        if (MOM) st_at(K->a.dbeta + rowbase, o, static_cast<bf16>(bt));
       }
     }
     __syncthreads();
@@ -688,7 +720,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
     // ---- R4: dphi, dk (waves 4-7) | dS_ref partial (waves 0-3); the next chunk's rows in flight
     // (the last chunk clears the registers instead: the values just staged are dead from here on)
     if (c > c_begin) {
-      rows_load<WL_R>(pf, rk, rv, rq, rdy, t0 - CL, w);
+      rows_load<WL_R>(pf, t0 - CL, w);
       xs_load(c - 1, xn);
     } else {
       pf = RowPf<WL_R>{};
@@ -698,7 +730,8 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
     if (hf == 1) {
       CPB_FRESH_LANE
       const int ct = q4;
-      const rsrc_t rkk = rk;
+      const CpK K = kargs();
+      const size_t rowbase = (size_t)bh * K->g.T;
       float cin[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) cin[r] = cdk[r];
@@ -721,11 +754,13 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
         for (int r = 0; r < 4; ++r) val[r] = acc[r];
         auto store_dk = [&](float (&v)[4]) {
           if constexpr (MAPE) {
-            const u32x2v raw = bld8(rkk, (uint32_t)((pp * D + col0) * 2));
-            v[0] *= poly_map_grad(lo16(raw[0]), g.map_deg); v[1] *= poly_map_grad(hi16(raw[0]), g.map_deg);
-            v[2] *= poly_map_grad(lo16(raw[1]), g.map_deg); v[3] *= poly_map_grad(hi16(raw[1]), g.map_deg);
+            const u32x2v raw =
+                bld8(make_rsrc(K->a.k + rowbase * D, (uint32_t)K->g.T * (D * 2)), (uint32_t)((pp * D + col0) * 2));
+            const int deg = K->g.map_deg;
+            v[0] *= poly_map_grad(lo16(raw[0]), deg); v[1] *= poly_map_grad(hi16(raw[0]), deg);
+            v[2] *= poly_map_grad(lo16(raw[1]), deg); v[3] *= poly_map_grad(hi16(raw[1]), deg);
           }
-          st_at(a.dk + rowbase * D, (uint32_t)((pp * D + col0) * 2), make_uint2(pk(v[0], v[1]), pk(v[2], v[3])));
+          st_at(K->a.dk + rowbase * D, (uint32_t)((pp * D + col0) * 2), make_uint2(pk(v[0], v[1]), pk(v[2], v[3])));
         };
         if (interior) {
           if (st == 0) {
@@ -740,18 +775,18 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
         } else if (st == 0) {
           if (seg_first) {
             if (seg > 0 && s >= HT - H)
-              st_at(part_row(p.halo_part, bh, sg.nseg, seg, H), (uint32_t)(((s - (HT - H)) * (2 * D) + D + col0) * 4),
+              st_at(part_row(K->p.halo_part, bh, K->sg.nseg, seg, H), (uint32_t)(((s - (HT - H)) * (2 * D) + D + col0) * 4),
                     make_float4(val[0], val[1], val[2], val[3]));
           } else {
 #pragma unroll
             for (int r = 0; r < 4; ++r) cdk[r] = val[r];
           }
-        } else if (pp < g.T) {
+        } else if (pp < K->g.T) {
           if (st == SRC / 16 - 1 && !seg_last)
 #pragma unroll
             for (int r = 0; r < 4; ++r) val[r] += cin[r];
           if (pp >= tail0)
-            st_at(part_row(p.tail_part, bh, sg.nseg, seg, H), (uint32_t)(((pp - tail0) * (2 * D) + D + col0) * 4),
+            st_at(part_row(K->p.tail_part, bh, K->sg.nseg, seg, H), (uint32_t)(((pp - tail0) * (2 * D) + D + col0) * 4),
                   make_float4(val[0], val[1], val[2], val[3]));
           else
             store_dk(val);
@@ -772,7 +807,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const Geom g, const BwdPtrs<bf16
       // this chunk's is still read below)
       if (c > c_begin) {
         if (w == 0) chunk_prefix(bf(sp.al), bf(sp.et), bf(sp.be), lane, sm.cc[(cr - 1) & 1]);
-        if (w == 1) chunk_end_scan(g, bf(sp.al), bf(sp.et), bf(sp.be), t0 - CL, lane, sm.cc[(cr - 1) & 1]);
+        if (w == 1) chunk_end_scan(kargs()->g.T, bf(sp.al), bf(sp.et), bf(sp.be), t0 - CL, lane, sm.cc[(cr - 1) & 1]);
       }
     }
 
@@ -873,12 +908,13 @@ hipError_t launch_chunk_bwd(const Geom& g, const BwdPtrs<bf16>& a, const SegGeom
   prof_name(KID_BWD_CHUNK, "k_cp_bwd");
   prof_begin(KID_BWD_CHUNK, stream);
   const dim3 grid(sg.nseg, g.BH);
+  const CpArgs A{g, a, sg, p};
   if (mape) {
-    if (g.momentum) hipLaunchKernelGGL((k_cp_bwd<true, true>), grid, dim3(NTB), smem, stream, g, a, sg, p);
-    else hipLaunchKernelGGL((k_cp_bwd<true, false>), grid, dim3(NTB), smem, stream, g, a, sg, p);
+    if (g.momentum) hipLaunchKernelGGL((k_cp_bwd<true, true>), grid, dim3(NTB), smem, stream, A);
+    else hipLaunchKernelGGL((k_cp_bwd<true, false>), grid, dim3(NTB), smem, stream, A);
   } else {
-    if (g.momentum) hipLaunchKernelGGL((k_cp_bwd<false, true>), grid, dim3(NTB), smem, stream, g, a, sg, p);
-    else hipLaunchKernelGGL((k_cp_bwd<false, false>), grid, dim3(NTB), smem, stream, g, a, sg, p);
+    if (g.momentum) hipLaunchKernelGGL((k_cp_bwd<false, true>), grid, dim3(NTB), smem, stream, A);
+    else hipLaunchKernelGGL((k_cp_bwd<false, false>), grid, dim3(NTB), smem, stream, A);
   }
   prof_end(KID_BWD_CHUNK, stream);
   if ((err = hipGetLastError()) != hipSuccess) return err;

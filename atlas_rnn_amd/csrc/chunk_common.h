@@ -135,7 +135,7 @@ __device__ __forceinline__ float cw(const BandRows& Bd, int r, int j) { return s
 
 // One wave (lane = target r, its scalars al, et, be; the identity past T): the chunk's end
 // coefficients cgS, cgZ of every target and the chunk transition.
-__device__ __forceinline__ void chunk_end_scan(const Geom& g, float al0, float et0, float be0, int t0, int lane,
+__device__ __forceinline__ void chunk_end_scan(int T, float al0, float et0, float be0, int t0, int lane,
                                                ChunkCoef& kc) {
   // lane j holds target r = 63 - j (the chunk read backwards)
   const float al = __shfl(al0, 63 - lane, 64), et = __shfl(et0, 63 - lane, 64), be = __shfl(be0, 63 - lane, 64);
@@ -144,7 +144,7 @@ __device__ __forceinline__ void chunk_end_scan(const Geom& g, float al0, float e
   Tri ex = tri_prev_lane(inc);
   if (lane == 0) ex = tri_id();
   const int r = 63 - lane;
-  const bool real = t0 + r < g.T;
+  const bool real = t0 + r < T;
   kc.co[R_GS + r] = real ? ex.k - et * ex.a : 0.f;
   kc.co[R_GZ + r] = real ? ex.b : 0.f;
   if (lane == 63) { kc.co[R_TR] = inc.a; kc.co[R_TR + 1] = inc.k; kc.co[R_TR + 2] = inc.b; kc.co[R_TR + 3] = 0.f; }
