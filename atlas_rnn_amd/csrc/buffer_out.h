@@ -28,11 +28,25 @@ __device__ __forceinline__ void buffer_out_slot(const Geom& g, const FwdPtrs<T>&
   for (int k = tid; k < DK; k += kThreads) sphi[k] = ld_map(a.k, (tb + p) * DK + k, g.map_mode, g.map_deg);
   __syncthreads();
   const float gp = (g.gate_mode == GATE_TOKEN) ? to_f32(a.gate[tb + p]) : 1.f;
-  for (int i = tid; i < DV; i += kThreads) {
-    const float* sr = a.S_ref + ((size_t)bh * DV + i) * DK;
+  // delta = S_ref phi - v: NP threads per row i, each over DK / NP columns in 16-byte loads, summed
+  // across the NP lanes
+  constexpr int NP = kThreads / DV, KP = DK / NP;
+  static_assert(kThreads % DV == 0 && DK % (4 * NP) == 0 && (NP & (NP - 1)) == 0, "row split");
+  {
+    const int i = tid / NP, kp = tid % NP;
+    const float4* sr = reinterpret_cast<const float4*>(a.S_ref + ((size_t)bh * DV + i) * DK + kp * KP);
+    float4 x[KP / 4];
+#pragma unroll
+    for (int u = 0; u < KP / 4; ++u) x[u] = sr[u];
     float acc = 0.f;
-    for (int k = 0; k < DK; ++k) acc += sr[k] * sphi[k];
-    sdel[i] = gp * (acc - to_f32(a.v[(tb + p) * DV + i]));
+#pragma unroll
+    for (int u = 0; u < KP / 4; ++u) {
+      const int k = kp * KP + 4 * u;
+      acc += x[u].x * sphi[k] + x[u].y * sphi[k + 1] + x[u].z * sphi[k + 2] + x[u].w * sphi[k + 3];
+    }
+#pragma unroll
+    for (int o = NP / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+    if (kp == 0) sdel[i] = gp * (acc - to_f32(a.v[(tb + p) * DV + i]));
   }
   __syncthreads();
   for (int idx = tid; idx < DV * DK; idx += kThreads) out[idx] = sdel[idx / DK] * sphi[idx % DK];

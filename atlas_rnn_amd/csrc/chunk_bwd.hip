@@ -572,7 +572,12 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
       // the window gradients dw[t][j] = <lamZ_t, G_{t-j}> = (Km M)[t][t + HT - j] (this half's
       // share of the scalar phase): the state-base tiles tt and tt + 1 hold the band of the
       // targets t = 16 tt + 4 gq + r
-      if (K->g.gate_mode != GATE_NONE) {
+      const CpK Kw = kargs();
+      const int gm = Kw->g.gate_mode, ne = Kw->g.e, T = Kw->g.T;
+      if (gm != GATE_NONE) {
+        // outputs of row bh: lag gates bf16 [T][e], or the per-(target, lag) fp32 terms of token gates
+        bf16* const dg_row = Kw->a.dgate + (size_t)bh * T * ne;
+        float* const dw_row = Kw->p.dw + (size_t)bh * T * ne;
         const int tt = q4, tl = 16 * tt + m;
         const float cgs = kc.co[R_GS + tl], cgz = kc.co[R_GZ + tl];
         bf16x8 kme;   // Km over the end rows (k = 64 + 8 gq + e): cgS on the lamS partials, cgZ on lamZ's
@@ -593,11 +598,10 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
           for (int r = 0; r < 4; ++r) {
             const int t = 16 * tt + 4 * gq + r, sq = 16 * sp + m;
             const int jb = t + HT - sq;
-            const int e = K->g.e;
-            if (jb >= 0 && jb < e && t0 + t < K->g.T) {
-              const uint32_t o = (uint32_t)((t0 + t) * e + jb);
-              if (K->g.gate_mode == GATE_LAG) st_at(K->a.dgate + rowbase * e, o * 2, static_cast<bf16>(rz[r]));
-              else st_at(K->p.dw + rowbase * e, o * 4, rz[r]);
+            if (jb >= 0 && jb < ne && t0 + t < T) {
+              const uint32_t o = (uint32_t)((t0 + t) * ne + jb);
+              if (gm == GATE_LAG) st_at(dg_row, o * 2, static_cast<bf16>(rz[r]));
+              else st_at(dw_row, o * 4, rz[r]);
             }
           }
         }

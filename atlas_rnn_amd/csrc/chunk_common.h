@@ -149,19 +149,38 @@ __device__ __forceinline__ void chunk_end_scan(int T, float al0, float et0, floa
   kc.co[R_GZ + r] = real ? ex.b : 0.f;
   if (lane == 63) { kc.co[R_TR] = inc.a; kc.co[R_TR + 1] = inc.k; kc.co[R_TR + 2] = inc.b; kc.co[R_TR + 3] = 0.f; }
 }
+// cs_s, cz_s over NJ >= e lags, branch-free: every read issued first (clamped, none predicated),
+// then the masked sums.
+template <int NJ>
+__device__ __forceinline__ void end_sources_nj(const BandRows& Bd, const ChunkCoef& kc, int s, int e, float& cs,
+                                               float& cz) {
+  bf16 wv[NJ];
+  float gv[NJ], zv[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int rc = min(max(s - HT + j, 0), CL - 1);
+    wv[j] = Bd[s][rc];
+    gv[j] = kc.co[R_GS + rc];
+    zv[j] = kc.co[R_GZ + rc];
+  }
+  cs = 0.f;
+  cz = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int r = s - HT + j;
+    const float wgt = static_cast<float>(wv[j]) * (j < e && r >= 0 && r < CL ? 1.f : 0.f);
+    cs += wgt * gv[j];
+    cz += wgt * zv[j];
+  }
+}
 // Thread s < 80: the per-source end coefficients from cgS / cgZ (after chunk_end_scan and the band):
-// cs_s = sum_j w(s - HT + j, j) cgS[s - HT + j], cz_s likewise with cgZ.
+// cs_s = sum_j w(s - HT + j, j) cgS[s - HT + j], cz_s likewise with cgZ (Bd[s][r] = w(r, j)).
 __device__ __forceinline__ void chunk_end_sources(const Geom& g, const BandRows& Bd, ChunkCoef& kc, int s) {
   if (s >= 0 && s < SRC) {
-    float cs = 0.f, cz = 0.f;
-    for (int j = 0; j < g.e; ++j) {
-      const int r = s - HT + j;
-      if (r >= 0 && r < CL) {
-        const float wgt = cw(Bd, r, j);
-        cs += wgt * kc.co[R_GS + r];
-        cz += wgt * kc.co[R_GZ + r];
-      }
-    }
+    float cs, cz;
+    if (g.e <= 4) end_sources_nj<4>(Bd, kc, s, g.e, cs, cz);
+    else if (g.e <= 8) end_sources_nj<8>(Bd, kc, s, g.e, cs, cz);
+    else end_sources_nj<EMAX>(Bd, kc, s, g.e, cs, cz);
     kc.co[R_CS + s] = cs;
     kc.co[R_CZ + s] = cz;
   }
