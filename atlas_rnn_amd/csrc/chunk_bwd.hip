@@ -513,47 +513,46 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
     }
     __syncthreads();
 
+    // The window gradients dw[t][j] = <lamZ_t, G_{t-j}> = (Km M)[t][t + HT - j] of the wave's
+    // targets t = 16 q4 + 4 gq + r over state-base tile q4 + h (the band of t spans tiles q4 and
+    // q4 + 1): tile 0 in R3 by waves 4-7, ahead of their ddelta (so that its LDS reads do not queue
+    // behind the ddelta stores), tile 1 in R4 by waves 0-3 (Mt, Cb and the record stay unchanged
+    // until the next chunk's R0).
+    auto dw_tile = [&](int h) {
+      CPB_FRESH_LANE
+      const CpK Kw = kargs();
+      const int gm = Kw->g.gate_mode, ne = Kw->g.e, T = Kw->g.T;
+      if (gm == GATE_NONE) return;
+      // outputs of row bh: lag gates bf16 [T][e], or the per-(target, lag) fp32 terms of token gates
+      bf16* const dg_row = Kw->a.dgate + (size_t)bh * T * ne;
+      float* const dw_row = Kw->p.dw + (size_t)bh * T * ne;
+      const int tt = q4, tl = 16 * tt + m, sp = tt + h;
+      const float cgs = kc.co[R_GS + tl], cgz = kc.co[R_GZ + tl];
+      bf16x8 kme;   // Km over the end rows (k = 64 + 8 gq + e): cgS on the lamS partials, cgZ on lamZ's
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kme[e] = static_cast<bf16>(gq == 0 ? (e < 4 ? cgs : cgz) : 0.f);
+      f32x4 rz = zero4();
+      rz = mma_bf16(frag_row_l(&sm.Cb[0][0], PB, 16 * tt, 0, lane), frag_tr_l(&sm.Mt[0][0], MQ, 16 * sp, 0, lane), rz);
+      rz = mma_bf16(frag_row_l(&sm.Cb[0][0], PB, 16 * tt, 32, lane), frag_tr_l(&sm.Mt[0][0], MQ, 16 * sp, 32, lane), rz);
+      // rows 64 .. 79 only (lanes 0 .. 31 address them; the others' k slots carry zero weights)
+      const bf16x8 me = frag_tr_l(&sm.Mt[0][0], MQ, 16 * sp, 64 - 16 * (gq >> 1), lane);
+      rz = mma_bf16(kme, gq < 2 ? me : zero_frag(), rz);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * tt + 4 * gq + r, sq = 16 * sp + m;
+        const int jb = t + HT - sq;
+        if (jb >= 0 && jb < ne && t0 + t < T) {
+          const uint32_t o = (uint32_t)((t0 + t) * ne + jb);
+          if (gm == GATE_LAG) st_at(dg_row, o * 2, static_cast<bf16>(rz[r]));
+          else st_at(dw_row, o * 4, rz[r]);
+        }
+      }
+    };
+
     // ---- R3: ddelta, dv (waves 4-7) | scalar gradients (waves 0-3)
     if (hf == 1) {
       CPB_FRESH_LANE
-      // the window gradients dw[t][j] = <lamZ_t, G_{t-j}> = (Km M)[t][t + HT - j] (this half's
-      // share of the scalar phase, ahead of ddelta so that its LDS reads do not queue behind the
-      // ddelta stores): the state-base tiles tt and tt + 1 hold the band of the targets
-      // t = 16 tt + 4 gq + r
-      const CpK Kw = kargs();
-      const int gm = Kw->g.gate_mode, ne = Kw->g.e, T = Kw->g.T;
-      if (gm != GATE_NONE) {
-        // outputs of row bh: lag gates bf16 [T][e], or the per-(target, lag) fp32 terms of token gates
-        bf16* const dg_row = Kw->a.dgate + (size_t)bh * T * ne;
-        float* const dw_row = Kw->p.dw + (size_t)bh * T * ne;
-        const int tt = q4, tl = 16 * tt + m;
-        const float cgs = kc.co[R_GS + tl], cgz = kc.co[R_GZ + tl];
-        bf16x8 kme;   // Km over the end rows (k = 64 + 8 gq + e): cgS on the lamS partials, cgZ on lamZ's
-#pragma unroll
-        for (int e = 0; e < 8; ++e) kme[e] = static_cast<bf16>(gq == 0 ? (e < 4 ? cgs : cgz) : 0.f);
-        const bf16x8 km0 = frag_row_l(&sm.Cb[0][0], PB, 16 * tt, 0, lane);
-        const bf16x8 km1 = frag_row_l(&sm.Cb[0][0], PB, 16 * tt, 32, lane);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int sp = tt + h;
-          f32x4 rz = zero4();
-          rz = mma_bf16(km0, frag_tr_l(&sm.Mt[0][0], MQ, 16 * sp, 0, lane), rz);
-          rz = mma_bf16(km1, frag_tr_l(&sm.Mt[0][0], MQ, 16 * sp, 32, lane), rz);
-          // rows 64 .. 79 only (lanes 0 .. 31 address them; the others' k slots carry zero weights)
-          const bf16x8 me = frag_tr_l(&sm.Mt[0][0], MQ, 16 * sp, 64 - 16 * (gq >> 1), lane);
-          rz = mma_bf16(kme, gq < 2 ? me : zero_frag(), rz);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int t = 16 * tt + 4 * gq + r, sq = 16 * sp + m;
-            const int jb = t + HT - sq;
-            if (jb >= 0 && jb < ne && t0 + t < T) {
-              const uint32_t o = (uint32_t)((t0 + t) * ne + jb);
-              if (gm == GATE_LAG) st_at(dg_row, o * 2, static_cast<bf16>(rz[r]));
-              else st_at(dw_row, o * 4, rz[r]);
-            }
-          }
-        }
-      }
+      dw_tile(0);
       const int ct = q4;
       const CpK K = kargs();
       const size_t rowbase = (size_t)bh * K->g.T;
@@ -808,6 +807,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) dsr[kt][r] += acc[r];
       }
+      dw_tile(1);
       // the next chunk's record and prefix arrays, from the scalars just fetched (the other buffer:
       // this chunk's is still read below)
       if (c > c_begin) {
