@@ -408,14 +408,21 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
       // C' as the k-major operand over the targets r (lane row t): shared by every source tile
       const bf16x8 fcb0 = frag_tr_l(&sm.Cb[0][0], PB, 16 * tt, 0, lane);
       const bf16x8 fcb1 = frag_tr_l(&sm.Cb[0][0], PB, 16 * tt, 32, lane);
+      // the targets' psi and dy rows, read once for every source tile and the dpsi products
+      bf16x8 fps[2], fdy[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        fps[q] = frag_row_l(&sm.psi[0][0], PB, 16 * tt, 32 * q, lane);
+        fdy[q] = frag_row_l(&sm.dy[0][0], PB, 16 * tt, 32 * q, lane);
+      }
       f32x4 Rr[SRC / 16];
 #pragma unroll
       for (int st = 0; st < SRC / 16; ++st) {
         f32x4 kq = zero4(), dd = zero4(), wy = zero4();
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-          kq = mma_bf16(frag_row_l(&sm.phi[0][0], PB, 16 * st, 32 * q, lane), frag_row_l(&sm.psi[0][0], PB, 16 * tt, 32 * q, lane), kq);
-          dd = mma_bf16(frag_row_l(&sm.vd[0][0], PB, 16 * st, 32 * q, lane), frag_row_l(&sm.dy[0][0], PB, 16 * tt, 32 * q, lane), dd);
+          kq = mma_bf16(frag_row_l(&sm.phi[0][0], PB, 16 * st, 32 * q, lane), fps[q], kq);
+          dd = mma_bf16(frag_row_l(&sm.vd[0][0], PB, 16 * st, 32 * q, lane), fdy[q], dd);
         }
         // Wy[s][t] = sum_r Band[s][r] C'[r][t]: the band of source tile st meets targets
         // 16 st - 16 .. 16 st + e - 2 only (e <= 17): k half 0 for st <= 2, half 1 for st >= 2
@@ -445,9 +452,8 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
         di = mma_bf16(tr_pair_l<false>(&sm.phi[0][0], PB, 2, 16 * kt, lane), fr2, di);
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-          const bf16x8 fdy = frag_row_l(&sm.dy[0][0], PB, 16 * tt, 32 * q, lane);
-          ds = mma_bf16(frag_row_l(&sm.XS[0][0][0], PB, 16 * kt, 32 * q, lane), fdy, ds);
-          dz = mma_bf16(frag_row_l(&sm.XS[1][0][0], PB, 16 * kt, 32 * q, lane), fdy, dz);
+          ds = mma_bf16(frag_row_l(&sm.XS[0][0][0], PB, 16 * kt, 32 * q, lane), fdy[q], ds);
+          dz = mma_bf16(frag_row_l(&sm.XS[1][0][0], PB, 16 * kt, 32 * q, lane), fdy[q], dz);
         }
         const float4 ps = lds_bf16x4(&sm.psi[t][16 * kt + 4 * gq]);
         fS += ps.x * ds[0] + ps.y * ds[1] + ps.z * ds[2] + ps.w * ds[3];
@@ -479,17 +485,26 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
       bf16x8 ones;
 #pragma unroll
       for (int e = 0; e < 8; ++e) ones[e] = static_cast<bf16>(1.f);
+      // the adjoint's operands of this wave's rows / columns, read once for every source tile
+      bf16x8 fls[2], flz[2], fks[2], fkz[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        fls[q] = frag_tr_l(&sm.XL[0][0][0], PB, 16 * ct, 32 * q, lane);
+        flz[q] = frag_tr_l(&sm.XL[1][0][0], PB, 16 * ct, 32 * q, lane);
+        fks[q] = frag_row_l(&sm.XL[0][0][0], PB, 16 * ct, 32 * q, lane);
+        fkz[q] = frag_row_l(&sm.XL[1][0][0], PB, 16 * ct, 32 * q, lane);
+      }
 #pragma unroll
       for (int st = 0; st < SRC / 16; ++st) {
         f32x4 es = zero4(), ez = zero4(), fs = zero4(), fz = zero4();
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           const bf16x8 fp = frag_row_l(&sm.phi[0][0], PB, 16 * st, 32 * q, lane);
-          es = mma_bf16(frag_tr_l(&sm.XL[0][0][0], PB, 16 * ct, 32 * q, lane), fp, es);   // (lamS phi_s)[i]
-          ez = mma_bf16(frag_tr_l(&sm.XL[1][0][0], PB, 16 * ct, 32 * q, lane), fp, ez);
+          es = mma_bf16(fls[q], fp, es);   // (lamS phi_s)[i]
+          ez = mma_bf16(flz[q], fp, ez);
           const bf16x8 fd = frag_row_l(&sm.vd[0][0], PB, 16 * st, 32 * q, lane);
-          fs = mma_bf16(frag_row_l(&sm.XL[0][0][0], PB, 16 * ct, 32 * q, lane), fd, fs);   // (lamS^T delta_s)[k]
-          fz = mma_bf16(frag_row_l(&sm.XL[1][0][0], PB, 16 * ct, 32 * q, lane), fd, fz);
+          fs = mma_bf16(fks[q], fd, fs);   // (lamS^T delta_s)[k]
+          fz = mma_bf16(fkz[q], fd, fz);
         }
         // hS[s] = delta_s . (lamS phi_s): this wave's 16 rows i summed on the matrix cores (every
         // output row holds the column sums); the four column tiles are the Gram's end-row partials
@@ -559,6 +574,9 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
       float cin[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) cin[r] = cdv[r];
+      bf16x8 fdt[2];   // dy^T rows of this wave's columns, read once for every source tile
+#pragma unroll
+      for (int q = 0; q < 2; ++q) fdt[q] = frag_tr_l(&sm.dy[0][0], PB, 16 * ct, 32 * q, lane);
 #pragma unroll
       for (int st = 0; st < SRC / 16; ++st) {
         f32x4 acc;
@@ -568,8 +586,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
         }
 #pragma unroll
         for (int q = 0; q < 2; ++q)   // ddelta^T[i][s] = sum_t dy[t][i] Q[s][t] (+ the end terms)
-          acc = mma_bf16(frag_tr_l(&sm.dy[0][0], PB, 16 * ct, 32 * q, lane),
-                         frag_tr_l(&sm.Qt[0][0], QP, 16 * st, 32 * q, lane), acc);
+          acc = mma_bf16(fdt[q], frag_tr_l(&sm.Qt[0][0], QP, 16 * st, 32 * q, lane), acc);
         // this lane: source s = 16 st + m, columns col0 .. col0 + 3
         const int s = 16 * st + m, pp = t0 - HT + s, col0 = 16 * ct + 4 * gq;
         store4<bf16>(&sm.vd[s][col0], acc[0], acc[1], acc[2], acc[3]);
@@ -739,6 +756,9 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
       float cin[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) cin[r] = cdk[r];
+      bf16x8 fpt[2];   // psi^T rows of this wave's columns, read once for every source tile
+#pragma unroll
+      for (int q = 0; q < 2; ++q) fpt[q] = frag_tr_l(&sm.psi[0][0], PB, 16 * ct, 32 * q, lane);
 #pragma unroll
       for (int st = 0; st < SRC / 16; ++st) {
         f32x4 acc;
@@ -748,8 +768,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
         }
 #pragma unroll
         for (int q = 0; q < 2; ++q) {   // dphi^T[k][s] = sum_t psi[t][k] R[s][t] + (S_ref^T ddelta_s)[k] (+ end terms)
-          acc = mma_bf16(frag_tr_l(&sm.psi[0][0], PB, 16 * ct, 32 * q, lane),
-                         frag_tr_l(&sm.Rt[0][0], QP, 16 * st, 32 * q, lane), acc);
+          acc = mma_bf16(fpt[q], frag_tr_l(&sm.Rt[0][0], QP, 16 * st, 32 * q, lane), acc);
           acc = mma_bf16(sreft[q], frag_row_l(&sm.vd[0][0], PB, 16 * st, 32 * q, lane), acc);
         }
         const int s = 16 * st + m, pp = t0 - HT + s, col0 = 16 * ct + 4 * gq;
