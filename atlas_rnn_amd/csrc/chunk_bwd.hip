@@ -375,13 +375,14 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
         const float4 vv = lds_bf16x4(pv);
         store4<bf16>(pv, acc[0] - vv.x, acc[1] - vv.y, acc[2] - vv.z, acc[3] - vv.w);
       }
+      const bf16x8 fbe0 = frag_row_l(&sm.BE[0][0], PB, 16 * q4, 0, lane);
+      const bf16x8 fbe1 = frag_row_l(&sm.BE[0][0], PB, 16 * q4, 32, lane);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {   // C'[r][t] = sum_u BE[r][u] DA[t][u]: tiles (q4, 2 hf + j)
         const int tt = 2 * hf + j;
         f32x4 acc = zero4();
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-          acc = mma_bf16(frag_row_l(&sm.BE[0][0], PB, 16 * q4, 32 * q, lane), frag_row_l(&sm.DA[0][0], PB, 16 * tt, 32 * q, lane), acc);
+        acc = mma_bf16(fbe0, frag_row_l(&sm.DA[0][0], PB, 16 * tt, 0, lane), acc);
+        acc = mma_bf16(fbe1, frag_row_l(&sm.DA[0][0], PB, 16 * tt, 32, lane), acc);
 #pragma unroll
         for (int r = 0; r < 4; ++r) sm.Cb[16 * q4 + 4 * gq + r][16 * tt + m] = static_cast<bf16>(acc[r]);
       }
@@ -817,12 +818,16 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
       }
     } else {
       CPB_FRESH_LANE
+      // ddelta^T of this wave's rows over the source slots, read once for the four column tiles
+      const bf16x8 fv0 = tr_pair_l<true>(&sm.vd[0][0], PB, 0, 16 * q4, lane);
+      const bf16x8 fv1 = tr_pair_l<true>(&sm.vd[0][0], PB, 1, 16 * q4, lane);
+      const bf16x8 fv2 = tr_pair_l<false>(&sm.vd[0][0], PB, 2, 16 * q4, lane);
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         f32x4 acc = zero4();
-        acc = mma_bf16(tr_pair_l<true>(&sm.vd[0][0], PB, 0, 16 * q4, lane), tr_pair_l<true>(&sm.phi[0][0], PB, 0, 16 * kt, lane), acc);
-        acc = mma_bf16(tr_pair_l<true>(&sm.vd[0][0], PB, 1, 16 * q4, lane), tr_pair_l<true>(&sm.phi[0][0], PB, 1, 16 * kt, lane), acc);
-        acc = mma_bf16(tr_pair_l<false>(&sm.vd[0][0], PB, 2, 16 * q4, lane), tr_pair_l<false>(&sm.phi[0][0], PB, 2, 16 * kt, lane), acc);
+        acc = mma_bf16(fv0, tr_pair_l<true>(&sm.phi[0][0], PB, 0, 16 * kt, lane), acc);
+        acc = mma_bf16(fv1, tr_pair_l<true>(&sm.phi[0][0], PB, 1, 16 * kt, lane), acc);
+        acc = mma_bf16(fv2, tr_pair_l<false>(&sm.phi[0][0], PB, 2, 16 * kt, lane), acc);
 #pragma unroll
         for (int r = 0; r < 4; ++r) dsr[kt][r] += acc[r];
       }
