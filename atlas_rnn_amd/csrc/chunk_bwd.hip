@@ -105,18 +105,19 @@ __device__ __forceinline__ void rows_load(RowPf<NWL>& pf, int t0, int w) {
   const CpK K = kargs();
   const size_t rb = (size_t)blockIdx.y * K->g.T * D;
   const uint32_t nb = (uint32_t)K->g.T * (D * 2);
-  const rsrc_t rk = make_rsrc(K->a.k + rb, nb), rv = make_rsrc(K->a.v + rb, nb);
-  const rsrc_t rq = make_rsrc(K->a.q + rb, nb), rdy = make_rsrc(K->a.dy + rb, nb);
   const uint32_t lo = (uint32_t)((lane >> 3) * (D * 2) + (lane & 7) * 16);
+  // One load per wave-load with the row tensor chosen by uniform selects: no branches, so the loads
+  // are all in flight together (loads in alternative branches writing the same registers would each
+  // wait for every load issued before them). Wave-loads past NWL read zeros (an offset out of range).
 #pragma unroll
   for (int u = 0; u < (NWL + NWB - 1) / NWB; ++u) {
     const int j = w + NWB * u;
-    if (j < NWL) {
-      if (j < SRC / 8) pf.v[u] = bld16(rk, (uint32_t)((t0 - HT + 8 * j) * (D * 2)) + lo);
-      else if (j < 2 * SRC / 8) pf.v[u] = bld16(rv, (uint32_t)((t0 - HT + 8 * (j - SRC / 8)) * (D * 2)) + lo);
-      else if (j < 2 * SRC / 8 + CL / 8) pf.v[u] = bld16(rq, (uint32_t)((t0 + 8 * (j - 2 * SRC / 8)) * (D * 2)) + lo);
-      else pf.v[u] = bld16(rdy, (uint32_t)((t0 + 8 * (j - 2 * SRC / 8 - CL / 8)) * (D * 2)) + lo);
-    }
+    const bool is_k = j < SRC / 8, is_v = j < 2 * SRC / 8, is_q = j < 2 * SRC / 8 + CL / 8;
+    const bf16* base = is_k ? K->a.k : is_v ? K->a.v : is_q ? K->a.q : K->a.dy;
+    const int row0 = is_k ? t0 - HT + 8 * j
+                   : is_v ? t0 - HT + 8 * (j - SRC / 8)
+                   : is_q ? t0 + 8 * (j - 2 * SRC / 8) : t0 + 8 * (j - 2 * SRC / 8 - CL / 8);
+    pf.v[u] = bld16(make_rsrc(base + rb, nb), j < NWL ? (uint32_t)(row0 * (D * 2)) + lo : kOob);
   }
 }
 template <bool MAPE, int NWL>
@@ -160,31 +161,38 @@ __device__ __forceinline__ void scal_load(ScalPf& p, int t0) {
   const CpK K = kargs();
   const int T = K->g.T, e = K->g.e, gm = K->g.gate_mode;
   const size_t rowbase = (size_t)blockIdx.y * T;
+  // Every load is unconditional (clamped index, a valid pointer for absent tensors) and the values
+  // are selected afterwards, so that the loads are in flight together (a load under a condition
+  // would wait for every load before it).
   // waves 0 and 1 (lane = target): the prefix arrays and the end record are formed from them
-  p.al = 0x3f80; p.et = 0; p.be = 0x3f80;   // 1, 0, 1 (the identity past T)
-  if (tid < 128 && t0 + (tid & 63) < T) {
-    const size_t o = rowbase + t0 + (tid & 63);
-    p.al = __builtin_bit_cast(unsigned short, K->a.decay[o]);
-    p.et = __builtin_bit_cast(unsigned short, K->a.lr[o]);
-    p.be = K->g.momentum ? __builtin_bit_cast(unsigned short, K->a.beta[o]) : (unsigned short)0;
-  }
+  const int ts = t0 + (tid & 63);
+  const size_t o = rowbase + min(ts, T - 1);
+  const bf16* bsrc = K->g.momentum ? K->a.beta : K->a.decay;
+  const unsigned short xa = __builtin_bit_cast(unsigned short, K->a.decay[o]);
+  const unsigned short xe = __builtin_bit_cast(unsigned short, K->a.lr[o]);
+  const unsigned short xb = __builtin_bit_cast(unsigned short, bsrc[o]);
   // window weight w(r, j) of target r, lag j: the lag gate, the gate of the source token t0 + r - j,
   // or 1; zero for targets past T
+  const bf16* gsrc = gm == GATE_NONE ? K->a.decay : K->a.gate;
+  unsigned short xg[3];
+  bool gok[3];
 #pragma unroll
   for (int u = 0; u < 3; ++u) {
-    p.gt[u] = 0;
     const int i = tid + NTB * u;
     const int r = i / e, j = i - r * e;
-    if (r < CL && t0 + r < T) {
-      if (gm == GATE_LAG) {
-        p.gt[u] = __builtin_bit_cast(unsigned short, K->a.gate[(rowbase + t0 + r) * e + j]);
-      } else if (gm == GATE_TOKEN) {
-        if (t0 + r - j >= 0) p.gt[u] = __builtin_bit_cast(unsigned short, K->a.gate[rowbase + t0 + r - j]);
-      } else {
-        p.gt[u] = 0x3f80;
-      }
-    }
+    const int tr = t0 + min(r, CL - 1);   // the target token (clamped)
+    size_t gi;
+    if (gm == GATE_LAG) gi = (rowbase + min(tr, T - 1)) * e + j;
+    else gi = rowbase + min(max(tr - j, 0), T - 1);
+    xg[u] = __builtin_bit_cast(unsigned short, gsrc[gi]);
+    gok[u] = r < CL && tr < T && (gm != GATE_TOKEN || tr - j >= 0);
   }
+  const bool sok = tid < 128 && ts < T;
+  p.al = sok ? xa : (unsigned short)0x3f80;   // 1, 0, 1: the identity past T
+  p.et = sok ? xe : (unsigned short)0;
+  p.be = sok ? (K->g.momentum ? xb : (unsigned short)0) : (unsigned short)0x3f80;
+#pragma unroll
+  for (int u = 0; u < 3; ++u) p.gt[u] = gok[u] ? (gm == GATE_NONE ? (unsigned short)0x3f80 : xg[u]) : (unsigned short)0;
 }
 __device__ __forceinline__ void gates_store(const ScalPf& p, int e, BwSm& sm) {
   const int tid = fresh_tid();
