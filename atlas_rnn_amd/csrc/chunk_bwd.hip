@@ -403,16 +403,6 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
       }
     }
     __syncthreads();
-    // the next chunk's rows and state slice in flight from here to its R0 (the last chunk clears
-    // the registers instead: the values staged in R0 are dead from here on)
-    if (c > c_begin) {
-      rows_load<WL_R>(pf, t0 - CL, w);
-      xs_load(c - 1, xn);
-    } else {
-      pf = RowPf<WL_R>{};
-#pragma unroll
-      for (int v = 0; v < 8; ++v) xn[v] = 0u;
-    }
     // ---- R2: t-phase (waves 0-3) | end terms of ddelta / dphi (waves 4-7)
     // the end terms (waves 4-7), bf16 pairs in the accumulator layout, used in R3 / R4
     unsigned edr[SRC / 16][2], efr[SRC / 16][2];
@@ -583,6 +573,16 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
       }
     };
 
+    // the next chunk's rows and state slice in flight from here to its R0 (the last chunk clears
+    // the registers instead: the values staged in R0 are dead from here on)
+    if (c > c_begin) {
+      rows_load<WL_R>(pf, t0 - CL, w);
+      xs_load(c - 1, xn);
+    } else {
+      pf = RowPf<WL_R>{};
+#pragma unroll
+      for (int v = 0; v < 8; ++v) xn[v] = 0u;
+    }
     // ---- R3: ddelta, dv (waves 4-7) | scalar gradients (waves 0-3)
     if (hf == 1) {
       CPB_FRESH_LANE
