@@ -318,6 +318,8 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
   // the last chunk's record and prefix arrays (every later chunk's are formed one step ahead)
   if (w == 0) chunk_prefix(bf(sp.al), bf(sp.et), bf(sp.be), lane, sm.cc[(c_end - c_begin - 1) & 1]);
   if (w == 1) chunk_end_scan(g.T, bf(sp.al), bf(sp.et), bf(sp.be), (c_end - 1) * CL, lane, sm.cc[(c_end - c_begin - 1) & 1]);
+  __syncthreads();
+  gen_tables<MOM>(sm.cc[(c_end - c_begin - 1) & 1], sm.DA, sm.BE, tid);   // (every later chunk's: in R4 before it)
 #pragma unroll 1
   for (int cr = c_end - c_begin - 1; cr >= 0; --cr) {
     CPB_FRESH_LANE
@@ -335,7 +337,6 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
     __syncthreads();
     rows_store<MAPE, WL_R>(pf, sm, g.map_deg, w);
     gates_store(sp, kargs()->g.e, sm);
-    gen_tables<MOM>(kc, sm.DA, sm.BE, tid);
     // the next chunk's scalars, early: waves 0, 1 form its record and prefix arrays at the end of R4
     if (c > c_begin) scal_load(sp, t0 - CL);
     else sp = ScalPf{};
@@ -754,6 +755,12 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
         st_at(K->a.dlr + rowbase, o, static_cast<bf16>(-(kc.be[tl] * ea + eb)));
         if (MOM) st_at(K->a.dbeta + rowbase, o, static_cast<bf16>(bt));
       }
+      // the next chunk's record and prefix arrays, from the scalars fetched in R0 (the other buffer:
+      // this chunk's is still read in R4 and R5)
+      if (c > c_begin) {
+        if (w == 0) chunk_prefix(bf(sp.al), bf(sp.et), bf(sp.be), lane, sm.cc[(cr - 1) & 1]);
+        if (w == 1) chunk_end_scan(K->g.T, bf(sp.al), bf(sp.et), bf(sp.be), t0 - CL, lane, sm.cc[(cr - 1) & 1]);
+      }
     }
     __syncthreads();
 
@@ -841,13 +848,10 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
         for (int r = 0; r < 4; ++r) dsr[kt][r] += acc[r];
       }
       dw_tile(1);
-      // the next chunk's record and prefix arrays, from the scalars just fetched (the other buffer:
-      // this chunk's is still read below)
-      if (c > c_begin) {
-        if (w == 0) chunk_prefix(bf(sp.al), bf(sp.et), bf(sp.be), lane, sm.cc[(cr - 1) & 1]);
-        if (w == 1) chunk_end_scan(kargs()->g.T, bf(sp.al), bf(sp.et), bf(sp.be), t0 - CL, lane, sm.cc[(cr - 1) & 1]);
-      }
     }
+    // the next chunk's C' factors, from its prefix arrays (formed in R3; this chunk's tables were last
+    // read in R3)
+    if (c > c_begin) gen_tables<MOM>(sm.cc[(cr - 1) & 1], sm.DA, sm.BE, fresh_tid());
 
     // ---- R5: the adjoint at the chunk start
     {
