@@ -6,7 +6,9 @@
 //    buffered in LDS, the next chunk's inputs are staged while the current one is computed, and the
 //    chunk after that is already in flight in registers;
 //  * wave w owns the state rows i in [16 (w & 3), +16) and, for the state update, the columns
-//    k in [32 (w >> 2), +32), and computes y for the targets tau in [32 (w >> 2), +32);
+//    k in [32 (w >> 2), +32), and computes y for the target tiles tau in [16 h, +16) and
+//    [16 (3 - h), +16), h = w >> 2 (an early and a late tile: the products over sources are
+//    formed on the causally nonzero source tiles only, so both halves do the same work);
 //  * delta = S_ref phi - v and the weighted target/source products stay in registers between their
 //    MFMAs (walk_common.h: chained operands), so only the staged inputs and the state copy go
 //    through LDS;
@@ -157,7 +159,12 @@ __device__ __forceinline__ f32x4 tile_or_zero(const f32x4 (&a)[N], int idx) {
 }  // namespace wf
 
 // One segment of one row. FULL = false: aggregate pass; FULL = true: full walk.
-template <bool FULL, bool MAPE, bool BUF>
+// TH = 0, 1 (full walks): the wave's column half as a constant, target tiles TH and 3 - TH, and
+// products over the source tiles that reach them only (y_tau takes sources s <= tau + H - 1, that
+// is tiles S <= T + 1 of target tile T); TH = 2: the half at run time, target tiles 2 h, 2 h + 1
+// and every source tile (the carried-buffer walks, whose registers have no room for the pruned
+// bodies).
+template <bool FULL, bool MAPE, bool BUF, int TH = 2>
 __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, const SegGeom& sg, float* agg,
                                          const float* seg_states, float* rw, float* final_raw, const float* coef,
                                          const bf16* wsh_all, unsigned char* smem_raw) {
@@ -166,7 +173,9 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
   Sm& sm = *reinterpret_cast<Sm*>(smem_raw);
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int gq = lane >> 4, m = lane & 15;
-  const int it = wave & 3, th = wave >> 2;     // state rows 16 it ..; target / column half th
+  const int it = wave & 3, th = TH < 2 ? TH : wave >> 2;   // state rows 16 it ..; column half th
+  const int TT[2] = {TH < 2 ? TH : 2 * th, TH < 2 ? 3 - TH : 2 * th + 1};   // target tiles
+  constexpr int NK[2] = {TH == 0 ? 2 : TH == 1 ? 3 : NST, TH == 0 ? NST : TH == 1 ? 4 : NST};
   const int seg = blockIdx.x, bh = blockIdx.y;
   const int H = g.H;
   const int c_begin = seg * sg.G, c_end = min(g.nc, c_begin + sg.G);
@@ -265,7 +274,7 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int q = 0; q < 2; ++q) psf[u][q] = frag_row(&st.psi[0][0], PD, 16 * (2 * th + u), 32 * q);
+        for (int q = 0; q < 2; ++q) psf[u][q] = frag_row(&st.psi[0][0], PD, 16 * TT[u], 32 * q);
     }
 #pragma unroll
     for (int s4 = 0; s4 < NST; ++s4) {
@@ -276,8 +285,8 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
         const bf16x8 fa = frag_row(&st.phi[0][0], PD, 16 * s4, 32 * q);
         dl[s4] = mma_bf16(fa, sref_f[q], dl[s4]);
         if constexpr (FULL) {
-          kq[0][s4] = mma_bf16(fa, psf[0][q], kq[0][s4]);
-          kq[1][s4] = mma_bf16(fa, psf[1][q], kq[1][s4]);
+          if (s4 < NK[0]) kq[0][s4] = mma_bf16(fa, psf[0][q], kq[0][s4]);
+          if (s4 < NK[1]) kq[1][s4] = mma_bf16(fa, psf[1][q], kq[1][s4]);
         }
       }
     }
@@ -320,19 +329,23 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
       }
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int tt = 2 * th + u;
+        const int tt = TT[u];
         // Q[tau][s] = Ws[s, tau-1] K[tau][s]; lane: tau = 16 tt + m, sources 16 s4 + 4 gq + r
         f32x4 qv[NST];
 #pragma unroll
         for (int s4 = 0; s4 < NST; ++s4) {
-          const float4 w = lds_bf16x4(&st.wsh[16 * tt + m][16 * s4 + 4 * gq]);
-          qv[s4][0] = kq[u][s4][0] * w.x; qv[s4][1] = kq[u][s4][1] * w.y;
-          qv[s4][2] = kq[u][s4][2] * w.z; qv[s4][3] = kq[u][s4][3] * w.w;
+          if (s4 < NK[u]) {
+            const float4 w = lds_bf16x4(&st.wsh[16 * tt + m][16 * s4 + 4 * gq]);
+            qv[s4][0] = kq[u][s4][0] * w.x; qv[s4][1] = kq[u][s4][1] * w.y;
+            qv[s4][2] = kq[u][s4][2] * w.z; qv[s4][3] = kq[u][s4][3] * w.w;
+          } else {
+            qv[s4] = zero4();
+          }
         }
         f32x4 aq = zero4(), as = zero4(), az = zero4();
 #pragma unroll
         for (int q = 0; q < NQ; ++q)
-          aq = mma_bf16(fdl[q], pack_frag(qv[2 * q], tile_or_zero(qv, 2 * q + 1)), aq);
+          if (2 * q < NK[u]) aq = mma_bf16(fdl[q], pack_frag(qv[2 * q], tile_or_zero(qv, 2 * q + 1)), aq);
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           as = mma_bf16(fS[q], psf[u][q], as);
@@ -509,7 +522,12 @@ __global__ __launch_bounds__(kSegThreads) void k_walk_full(const Geom g, const F
                                                              const float* coef, const bf16* wsh) {
   if (geom_skip(g)) return;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  walk_fwd<true, MAPE, BUF>(g, a, sg, nullptr, seg_states, rw, final_raw, coef, wsh, smem_raw);
+  if constexpr (BUF)
+    walk_fwd<true, MAPE, BUF>(g, a, sg, nullptr, seg_states, rw, final_raw, coef, wsh, smem_raw);
+  else if (__builtin_amdgcn_readfirstlane(wave_id() >> 2) == 0)
+    walk_fwd<true, MAPE, BUF, 0>(g, a, sg, nullptr, seg_states, rw, final_raw, coef, wsh, smem_raw);
+  else
+    walk_fwd<true, MAPE, BUF, 1>(g, a, sg, nullptr, seg_states, rw, final_raw, coef, wsh, smem_raw);
 }
 
 template <typename T, int D>
