@@ -192,6 +192,11 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
   const StageOffs so = stage_offsets(H, tid);
   const rsrc_t ry = make_rsrc(FULL ? a.y + (size_t)bh * g.T * D : nullptr, FULL ? row_bytes : 0u);
 
+  // the first chunk's loads go out before those of S_ref and the segment-start state, so that the
+  // walk's start waits for one round trip to memory instead of two
+  Prefetch<FULL> pf;
+  if (c_begin < c_end) pf_load<FULL>(pf, rr, so, c_begin * CH, c_begin);
+
   // S_ref rows 16 it .. +15 as the B operand of delta^T = phi S_ref^T (k = 32 q + 8 gq + e)
   bf16x8 sref_f[2];
   {
@@ -252,9 +257,7 @@ __device__ __forceinline__ void walk_fwd(const Geom& g, const FwdPtrs<bf16>& a, 
     save_state(c_begin * rb, Sr, Zr);
   }
 
-  Prefetch<FULL> pf;
   if (c_begin < c_end) {
-    pf_load<FULL>(pf, rr, so, c_begin * CH, c_begin);
     pf_store<FULL, MAPE>(pf, sm.st[0], so, tid, g.map_deg);
     if (c_begin + 1 < c_end) pf_load<FULL>(pf, rr, so, (c_begin + 1) * CH, c_begin + 1);
   }
