@@ -23,7 +23,8 @@ __device__ __forceinline__ void bwd_seg_fixup(const Geom& g, const BwdPtrs<T>& a
   const int tok0 = c_begin * g.Lc, tok1 = min(g.T, c_end * g.Lc);
   const size_t tb = (size_t)bh * g.T;
   const int tid = threadIdx.x;
-  if (reduce_dsref) {
+  auto reduce = [&]() {
+    if (!reduce_dsref) return;
     const int per = (D * D + sg.nseg - 1) / sg.nseg;
     const int i0 = seg * per, i1 = min(D * D, i0 + per);
     const float* part = p.dsref_part + (size_t)bh * sg.nseg * D * D;
@@ -38,7 +39,10 @@ __device__ __forceinline__ void bwd_seg_fixup(const Geom& g, const BwdPtrs<T>& a
       }
       a.dS_ref[(size_t)bh * D * D + idx] = acc;
     }
-  }
+  };
+  constexpr int HF = 16;   // tail tokens of the single-round-trip pass
+  const bool fast = (!OUTBUF || a.dbuf_out == nullptr) && g.H > 0 && g.H <= HF;
+  if (!fast) reduce();
   // token-gate gradient du_p = sum_j dw[p + j, j] (the d buffer_out term is added below)
   if (g.gate_mode == GATE_TOKEN) {
     for (int pp = tok0 + tid; pp < tok1; pp += kThreads) {
@@ -51,6 +55,42 @@ __device__ __forceinline__ void bwd_seg_fixup(const Geom& g, const BwdPtrs<T>& a
   if (H == 0) return;
   const int tail0 = tok1 - H;
   const bool has_next = seg + 1 < sg.nseg;
+  if (fast) {
+    // no buffer_out terms: the 2 D values of each tail token are independent sums of two partials;
+    // their loads are issued before the dS_ref sum's, so that the launch waits for one round trip
+    constexpr int NV = (2 * HF * D + kThreads - 1) / kThreads;
+    float val[NV];
+    int dst[NV];
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      dst[u] = -1;
+      val[u] = 0.f;
+      if (u * kThreads >= H * 2 * D) continue;   // uniform
+      const int idx = tid + u * kThreads;
+      const int h = idx / (2 * D), col = idx % (2 * D);
+      const int pp = tail0 + h;
+      const bool ok = h < H && pp >= tok0;   // (a token before tok0 belongs to the previous segment)
+      const size_t tp = (((size_t)bh * sg.nseg + seg) * H + (ok ? h : 0)) * (2 * D);
+      const size_t hp = (((size_t)bh * sg.nseg + seg + (has_next ? 1 : 0)) * H + (ok ? h : 0)) * (2 * D);
+      const float tv = p.tail_part[tp + col], hv = p.halo_part[hp + col];   // in range for every lane
+      val[u] = ok ? tv + (has_next ? hv : 0.f) : 0.f;
+      dst[u] = ok ? col : -1;
+    }
+    reduce();
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      if (dst[u] < 0) continue;
+      const int idx = tid + u * kThreads, pp = tail0 + idx / (2 * D), col = dst[u];
+      if (col < D) {
+        a.dv[(tb + pp) * D + col] = from_f32<T>(val[u]);
+      } else {
+        float v = val[u];
+        if (g.map_mode == MAP_ELEMENTWISE) v *= poly_map_grad(to_f32(a.k[(tb + pp) * D + col - D]), g.map_deg);
+        a.dk[(tb + pp) * D + col - D] = from_f32<T>(v);
+      }
+    }
+    return;
+  }
   for (int h = 0; h < H; ++h) {
     const int pp = tail0 + h;
     if (pp < tok0) continue;                       // token of the previous segment (short last segment)
