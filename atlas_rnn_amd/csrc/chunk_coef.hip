@@ -16,12 +16,16 @@
 //
 // Operands (v_mfma_f32_16x16x32_bf16; lane l: gq = l >> 4, m = l & 15):
 //   C' tile (rb, tb) = sum_q BE(rb, q) DA(tb, q), k = u = 32 q + 8 gq + e (natural order), the
-//     operands generated in registers from LA, LB, eta (exp2 of differences <= 0); tiles rb > tb
+//     operands generated in registers: one product of separable factors per entry (exp2(LA[t-1])
+//     exp2(-LA[u]), eta_u exp2(LB[u]) exp2(-LB[r]), formed once per token) where the chunk's
+//     summed log2 decays stay above -120, else exp2 of the differences (<= 0); tiles rb > tb
 //     and the k-steps outside u in [16 rb, 16 tb + 14] are zero and skipped;
 //   Wy tile (sb, tb) = sum_q Band(sb, q) C'(q, tb), k = r in the chained order of the accumulator
 //     tiles (slots e < 4: r = 32 q + 4 gq + e; e >= 4: r = 32 q + 16 + 4 gq + e - 4), so the C'
 //     accumulators are the B operand as they stand (pack_frag); the band slots are read from the
 //     wave's gate table. Band(sb, q) is zero unless 16 sb - 16 <= 32 q + 31 and 32 q <= 16 sb + 15.
+#include <type_traits>
+
 #include "chunk_common.h"
 
 namespace atlas {
@@ -39,6 +43,9 @@ static_assert(R_WSMID + 2 * SPM + 4 == REC && R_WSMID % 4 == 0, "record layout")
 // per wave: the prefix arrays, the end coefficients of the targets and the window band
 struct WvSm {
   alignas(16) float la[CL], lb[CL], eta[CL], gs[CL], gz[CL];
+  // separable factors (chunks whose total log2 decays stay above -kSepRange): A(u -> t - 1) =
+  // qa[t] pa[u], -eta_u B(r -> u) = pb[u] qb[r]
+  alignas(16) float qa[CL], pa[CL], pb[CL], qb[CL];
   // Bd[s][r] = w(r, j), s = r + H - j: the weight of source s in the window of target r (zero
   // outside the window and past T)
   alignas(16) BandRows Bd;
@@ -72,6 +79,33 @@ __device__ __forceinline__ bf16x8 gen_be(const WvSm& ws, int r, int q, int gq) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) f[e] = static_cast<bf16>(u0 + e == r ? -etu[e] : 0.f);
   }
+  return f;
+}
+// The same fragments from the separable factors (one product per entry instead of an exp2).
+template <bool MOM, bool MASK>
+__device__ __forceinline__ bf16x8 gen_be_sep(const WvSm& ws, int r, int q, int gq) {
+  const int u0 = 32 * q + 8 * gq;
+  bf16x8 f;
+  if constexpr (MOM) {
+    const float4 b0 = *reinterpret_cast<const float4*>(&ws.pb[u0]), b1 = *reinterpret_cast<const float4*>(&ws.pb[u0 + 4]);
+    const float pbu[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    const float qbr = ws.qb[r];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = static_cast<bf16>(!MASK || u0 + e >= r ? pbu[e] * qbr : 0.f);
+  } else {
+    f = gen_be<false, MASK>(ws, r, q, gq);
+  }
+  return f;
+}
+template <bool MASK>
+__device__ __forceinline__ bf16x8 gen_da_sep(const WvSm& ws, int t, int q, int gq) {
+  const int u0 = 32 * q + 8 * gq;
+  const float4 a0 = *reinterpret_cast<const float4*>(&ws.pa[u0]), a1 = *reinterpret_cast<const float4*>(&ws.pa[u0 + 4]);
+  const float pau[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+  const float qat = ws.qa[t];
+  bf16x8 f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = static_cast<bf16>(!MASK || u0 + e <= t - 1 ? qat * pau[e] : 0.f);
   return f;
 }
 // DA(tb, q) as the B operand: lane supplies DA[t = 16 tb + m][u = 32 q + 8 gq + e] = A(u -> t - 1)
@@ -175,9 +209,22 @@ __global__ __launch_bounds__(NT) void k_chunk_coef_fwd(const Geom g, const bf16*
   const float be = real ? static_cast<float>(xb) : 1.f;
 
   // ---- prefix arrays (LA, LB, eta), the coefficients of S_c, Z_c in S_{t-1}, the end coefficients
-  ws.la[lane] = wave_prefix_sum(fmaxf(__log2f(al), kLogFloor), lane);
-  ws.lb[lane] = wave_prefix_sum(fmaxf(__log2f(be), kLogFloor), lane);
+  const float lav = wave_prefix_sum(fmaxf(__log2f(al), kLogFloor), lane);
+  const float lbv = wave_prefix_sum(fmaxf(__log2f(be), kLogFloor), lane);
+  ws.la[lane] = lav;
+  ws.lb[lane] = lbv;
   ws.eta[lane] = et;
+  // separable factors (chunk_common.h): the prefix sums only decrease, so lane 63 holds the lowest
+  const bool sep = __shfl(lav, 63, 64) >= -kSepRange && (!MOM || __shfl(lbv, 63, 64) >= -kSepRange);
+  if (sep) {   // wave-uniform
+    const float lap = __shfl(lav, lane > 0 ? lane - 1 : 0, 64);
+    ws.qa[lane] = lane > 0 ? __builtin_amdgcn_exp2f(lap) : 1.f;
+    ws.pa[lane] = __builtin_amdgcn_exp2f(-lav);
+    if (MOM) {
+      ws.pb[lane] = -et * __builtin_amdgcn_exp2f(lbv);
+      ws.qb[lane] = __builtin_amdgcn_exp2f(-lbv);
+    }
+  }
   for (int i = lane; i < (int)(sizeof(BandRows) / 16); i += 64)
     reinterpret_cast<u32x4v*>(&ws.Bd[0][0])[i] = u32x4v{0u, 0u, 0u, 0u};
   wave_sync();
@@ -220,32 +267,43 @@ __global__ __launch_bounds__(NT) void k_chunk_coef_fwd(const Geom g, const bf16*
     }
   }
 
-  // ---- C' = BE DA^T (tiles rb <= tb)
+  // ---- C' = BE DA^T (tiles rb <= tb); the operands from the separable factors where they exist
   f32x4 cpt[4][4];
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) cpt[rb][tb] = zero4();
+  auto cprime = [&](auto sepc) {
+    constexpr bool SEP = decltype(sepc)::value;
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    bf16x8 fda[4];
+    for (int q = 0; q < 2; ++q) {
+      bf16x8 fda[4];
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb)
-      if (c_step(0, tb, q))
-        fda[tb] = 32 * q + 32 > 16 * tb ? gen_da<true>(ws, 16 * tb + m, q, gq) : gen_da<false>(ws, 16 * tb + m, q, gq);
+      for (int tb = 0; tb < 4; ++tb) {
+        if (!c_step(0, tb, q)) continue;
+        const int t = 16 * tb + m;
+        if (32 * q + 32 > 16 * tb) fda[tb] = SEP ? gen_da_sep<true>(ws, t, q, gq) : gen_da<true>(ws, t, q, gq);
+        else fda[tb] = SEP ? gen_da_sep<false>(ws, t, q, gq) : gen_da<false>(ws, t, q, gq);
+      }
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      if (!c_step(rb, 3, q)) continue;
-      const bf16x8 fbe =
-          32 * q < 16 * rb + 15 ? gen_be<MOM, true>(ws, 16 * rb + m, q, gq) : gen_be<MOM, false>(ws, 16 * rb + m, q, gq);
+      for (int rb = 0; rb < 4; ++rb) {
+        if (!c_step(rb, 3, q)) continue;
+        const int r = 16 * rb + m;
+        bf16x8 fbe;
+        if (32 * q < 16 * rb + 15) fbe = SEP ? gen_be_sep<MOM, true>(ws, r, q, gq) : gen_be<MOM, true>(ws, r, q, gq);
+        else fbe = SEP ? gen_be_sep<MOM, false>(ws, r, q, gq) : gen_be<MOM, false>(ws, r, q, gq);
 #pragma unroll
-      for (int tb = rb; tb < 4; ++tb)
-        if (c_step(rb, tb, q)) cpt[rb][tb] = mma_bf16(fbe, fda[tb], cpt[rb][tb]);
+        for (int tb = rb; tb < 4; ++tb)
+          if (c_step(rb, tb, q)) cpt[rb][tb] = mma_bf16(fbe, fda[tb], cpt[rb][tb]);
+      }
     }
-  }
+  };
+  if (sep) cprime(std::true_type{});
+  else cprime(std::false_type{});
 
   // ---- Wy = Band C', stored as wsh[t][s] = -Wy[s][t] (lane: sources 16 sb + 4 gq + i of target
-  // 16 tb + m; 8-byte stores; source slots 80 .. 95 zero; 0 - x keeps the empty slots +0)
+  // 16 tb + m; 8-byte stores; 0 - x keeps the empty slots +0). Only the source tiles sb <= tb + 1
+  // are stored: Ws[s, t - 1] is zero past s = t + H - 1 (H <= 16), and the walks read no more.
   const rsrc_t rw = make_rsrc(wsh_all + ((size_t)bh * g.nc + c) * CL * SPM, (uint32_t)(CL * SPM * sizeof(bf16)));
   bf16x8 fband[5][2];
 #pragma unroll
@@ -262,6 +320,7 @@ __global__ __launch_bounds__(NT) void k_chunk_coef_fwd(const Geom g, const bf16*
     const uint32_t row = (uint32_t)(((16 * tb + m) * SPM + 4 * gq) * sizeof(bf16));
 #pragma unroll
     for (int sb = 0; sb < 6; ++sb) {
+      if (sb > tb + 1) continue;   // Ws[s, t - 1] = 0 for s > t + H - 1: never stored, never read
       f32x4 acc = zero4();
 #pragma unroll
       for (int q = 0; q < 2; ++q)

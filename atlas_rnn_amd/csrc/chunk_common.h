@@ -23,6 +23,9 @@ constexpr int CL = 64;              // chunk length
 constexpr int HT = 16;              // halo rows staged before a chunk's first token (window halo <= 16)
 constexpr int SRC = CL + HT;        // source rows of a chunk
 constexpr float kLogFloor = -100.f;
+// A chunk whose prefix sums LA, LB end above -kSepRange has separable decay factors: exp2(LA[t] -
+// LA[u]) = exp2(LA[t]) exp2(-LA[u]) with both factors fp32 normal numbers (within 2^(+-120)).
+constexpr float kSepRange = 120.f;
 
 struct Tri { float a, k, b; };
 __device__ __forceinline__ Tri tri_id() { return Tri{1.f, 0.f, 1.f}; }

@@ -103,7 +103,10 @@ __device__ __forceinline__ StageOffs stage_offsets(int H, int tid) {
   for (int j = 0; j < 2; ++j) {
     const int v = tid + j * NTH;
     const int t = v / (SP / 8), sv = v % (SP / 8);
-    o.wsh[j] = v < NV_WSH ? (uint32_t)(t * SPM * 2 + sv * 16) : kOob;
+    // Ws[s, t - 1] is zero for s > t + H - 1, that is past source tile (t >> 4) + 1 (H <= 16):
+    // those vectors read as zeros (nothing is stored there)
+    const bool nz = sv < 2 * ((t >> 4) + 2);
+    o.wsh[j] = v < NV_WSH && nz ? (uint32_t)(t * SPM * 2 + sv * 16) : kOob;
     o.lwsh[j] = v < NV_WSH ? t * WP + sv * 8 : -1;
   }
   o.rec = tid < REC4 ? (uint32_t)(tid * 16) : kOob;

@@ -35,6 +35,7 @@ class Case:
     dtype: torch.dtype = torch.float32
     seed: int = 0
     decay_shift: float = 2.0
+    beta_shift: float = 1.0          # momentum decay beta = sigmoid(N(0, 1) / 2 + beta_shift)
     backward: bool = True
     dv: int | None = None            # d_v (None: d_v = d_k)
     grad_buffer: bool = True         # the loss includes buffer_out (False: no buffer_out gradient)
@@ -51,7 +52,7 @@ def make_inputs(c: Case) -> dict:
     k = k / k.norm(dim=-1, keepdim=True)
     p = dict(k=k, q=r(BH, T, d), v=r(BH, T, dv),
              decay=torch.sigmoid(r(BH, T) * 0.5 + c.decay_shift), lr=0.1 * torch.sigmoid(r(BH, T)))
-    p["beta"] = torch.sigmoid(r(BH, T) * 0.5 + 1.0) if c.momentum else None
+    p["beta"] = torch.sigmoid(r(BH, T) * 0.5 + c.beta_shift) if c.momentum else None
     if c.gate == 'token':
         p["gate"] = torch.sigmoid(r(BH, T))
     elif c.gate == 'lag':

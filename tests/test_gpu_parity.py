@@ -122,6 +122,15 @@ CASES = [
          grad_buffer=False, dtype=BF16, seed=47),
     Case("bf16_walk_buf_token_no_dbuf", BH=3, T=300, d=64, e=3, gate='token', momentum=True, buffer=True,
          states=0.1, grad_buffer=False, dtype=BF16, seed=48),
+    # fast decays: the chunk coefficients' decay products come from separable exp2 factors only where
+    # a chunk's summed log2 decays stay above -120 (within fp32's range); with decay and beta near
+    # sigmoid(-0.9) 25 of the 40 chunks pass (seed 51), near sigmoid(-6) none does
+    Case("bf16_walk_fast_decay_mixed", BH=4, T=640, d=64, e=4, gate='lag', momentum=True, states=0.1,
+         decay_shift=-0.9, beta_shift=-0.9, dtype=BF16, grad_buffer=False, seed=51),
+    Case("bf16_walk_vanishing_decay", BH=3, T=300, d=64, e=4, gate='lag', momentum=True, states=0.1,
+         decay_shift=-6.0, beta_shift=-6.0, dtype=BF16, grad_buffer=False, seed=52),
+    Case("bf16_walk_fast_decay_nomom", BH=3, T=400, d=64, e=3, gate='token', momentum=False, states=0.1,
+         decay_shift=-0.9, dtype=BF16, grad_buffer=False, seed=53),   # 15 of 18 full chunks pass
     Case("fp32_clamp64_multiseg_quiet", BH=40, T=300, d=32, e=2, gate=None, momentum=True, states=0.2, clamp_every=64,
          seed=38),
     Case("fp32_clamp64_fires_late", BH=2, T=200, d=32, e=2, gate='token', momentum=False, states=60.0, clamp_every=64,
