@@ -125,6 +125,8 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg_agg(const Geom g, const
   Sm& sm = *reinterpret_cast<Sm*>(smem_raw);
   constexpr int NTD = D / 16;
   constexpr int NT2 = (NTD * NTD + kSegWaves - 1) / kSegWaves;   // state tiles per wave
+  // pre-scaled dy with two tiles per wave: wave w owns row tile w >> 1, column tiles 2 (w & 1) + j
+  constexpr bool kPair = Sm::kPre && NTD * NTD == 2 * kSegWaves;
   typedef MM<T> M;
   const int seg = blockIdx.x, bh = blockIdx.y;
   const size_t tb = (size_t)bh * g.T;
@@ -147,8 +149,34 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg_agg(const Geom g, const
     __syncthreads();
     if (c - 1 >= c_begin) pf.load(g, a, rec_row + (size_t)(c - 1) * CoefRec<CH>::SIZE, tb, c - 1, tid);
     const float ae = sm.coef[2 * CH], ke = sm.coef[2 * CH + 1], be = sm.coef[2 * CH + 2];
+    if constexpr (kPair) {
+      // the wave's two tiles share their rows: the scaled dy fragments are read once per k-step
+      const int m0 = (wave >> 1) * 16;
+      f32x4 aa[2], ak[2];
 #pragma unroll
-    for (int j = 0; j < NT2; ++j) {
+      for (int j = 0; j < 2; ++j) { aa[j] = zero4(); ak[j] = zero4(); }
+#pragma unroll
+      for (int k0 = 0; k0 < CH; k0 += M::KS) {
+        const typename M::frag fa = frag_ld_tr<T>(&sm.pre.a[0][0], D + 8, m0, k0);
+        const typename M::frag fk = frag_ld_tr<T>(&sm.pre.k[0][0], D + 8, m0, k0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const typename M::frag fb = frag_ld_tr<T>(&sm.psi[0][0], D + 8, 16 * (2 * (wave & 1) + j), k0);
+          aa[j] = M::mma(fa, fb, aa[j]);
+          ak[j] = M::mma(fk, fb, ak[j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float l_out = lam[j][r];
+          lam[j][r] = ae * l_out + aa[j][r];
+          mu[j][r] = g.momentum ? (be * mu[j][r] - ke * l_out - ak[j][r]) : 0.f;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < (kPair ? 0 : NT2); ++j) {
       const int tile = min(wave + kSegWaves * j, NTD * NTD - 1);
       const bool valid = (NTD * NTD) % kSegWaves == 0 || wave + kSegWaves * j < NTD * NTD;
       const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
@@ -182,7 +210,7 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg_agg(const Geom g, const
   float* ag = p.adj_agg + ((size_t)bh * sg.nseg + seg) * sg.agg_stride;
 #pragma unroll
   for (int j = 0; j < NT2; ++j) {
-    const int tile = wave + kSegWaves * j;
+    const int tile = kPair ? (wave >> 1) * NTD + 2 * (wave & 1) + j : wave + kSegWaves * j;
     if (tile >= NTD * NTD) continue;
     const int m0 = (tile / NTD) * 16, n0 = (tile % NTD) * 16;
 #pragma unroll
