@@ -113,6 +113,52 @@ struct BwdAggPrefetch
   }
 };
 
+// The same staging for the forward's 64-token chunks at d = 64 (pre-scaled dy, one psi and one dy
+// vector per thread: psi row tid >> 3, dy row tid >> 3, 8 features at 8 (tid & 7)), with the
+// per-thread row pointers and offsets formed once per launch instead of once per chunk.
+template <typename T, int CH, int D>
+struct BwdAggFastPf {
+  static constexpr int NC4 = (2 * CH + 4) / 4;
+  Vec8<T> xq, xd;
+  float wa, wk;
+  float4 rc;
+  bool okq, okd;
+  const T* pq;   // psi row t of chunk 0 (rows past T read the sequence's first row, masked)
+  const T* pd;
+  const T* pq0;
+  const T* pd0;
+  int t;
+  __device__ __forceinline__ void init(const BwdPtrs<T>& a, size_t tb, int tid) {
+    t = tid >> 3;
+    const int c8 = tid & 7;
+    pq0 = a.q + tb * D + c8 * 8;
+    pd0 = (a.dy ? a.dy : a.q) + tb * D + c8 * 8;
+    pq = pq0 + (size_t)t * D;
+    pd = pd0 + (size_t)t * D;
+  }
+  __device__ __forceinline__ void load(const Geom& g, const BwdPtrs<T>& a, const float* rec, size_t, int c, int tid) {
+    const int t0 = c * CH, L = min(g.T, t0 + CH) - t0;
+    okq = t < L;
+    okd = okq && a.dy != nullptr;
+    xq = vec8_load(okq ? pq + (size_t)t0 * D : pq0);
+    xd = vec8_load(okd ? pd + (size_t)t0 * D : pd0);
+    wa = rec[t];
+    wk = rec[CH + t];
+    rc = reinterpret_cast<const float4*>(rec)[tid < NC4 ? tid : 0];
+  }
+  template <typename Sm>
+  __device__ __forceinline__ void store(const Geom& g, Sm& sm, int tid) const {
+    const int c8 = tid & 7;
+    Vec8<T> y = xq.masked(okq);
+    if (g.map_mode == MAP_ELEMENTWISE) y = y.mapped(g.map_deg);
+    y.store(&sm.psi[t][c8 * 8]);
+    const Vec8<T> z = xd.masked(okd);
+    z.store_scaled(&sm.pre.a[t][c8 * 8], wa);
+    z.store_scaled(&sm.pre.k[t][c8 * 8], wk);
+    if (tid < NC4) reinterpret_cast<float4*>(sm.coef)[tid] = rc;
+  }
+};
+
 // Adjoint aggregate of one segment: walks its chunks in reverse from a zero adjoint,
 //   lam <- a_end lam + sum_t a_{t-1} dy_t psi_t^T,   mu <- b_end mu - kappa_end lam - sum_t kappa_{t-1} dy_t psi_t^T,
 // with the next chunk's inputs prefetched into registers while the current one computes.
@@ -138,7 +184,9 @@ __global__ __launch_bounds__(kSegThreads) void k_bwd_seg_agg(const Geom g, const
 #pragma unroll
     for (int r = 0; r < 4; ++r) { lam[j][r] = 0.f; mu[j][r] = 0.f; }
   float pa = 1.f, pk = 0.f, pb = 1.f;
-  BwdAggPrefetch<T, CH, D> pf;
+  constexpr bool kFast = Sm::kPre && D == 64 && CH * D / 8 == kSegThreads;
+  typename std::conditional<kFast, BwdAggFastPf<T, CH, D>, BwdAggPrefetch<T, CH, D>>::type pf;
+  if constexpr (kFast) pf.init(a, tb, threadIdx.x);
   if (c_begin < c_end) pf.load(g, a, rec_row + (size_t)(c_end - 1) * CoefRec<CH>::SIZE, tb, c_end - 1, threadIdx.x);
   for (int c = c_end - 1; c >= c_begin; --c) {
     int tid = threadIdx.x;
