@@ -25,19 +25,21 @@ __device__ __forceinline__ void buffer_out_slot(const Geom& g, const FwdPtrs<T>&
   }
   const int p = ext - H;
   const size_t tb = (size_t)bh * g.T;
-  for (int k = tid; k < DK; k += kThreads) sphi[k] = ld_map(a.k, (tb + p) * DK + k, g.map_mode, g.map_deg);
-  __syncthreads();
-  const float gp = (g.gate_mode == GATE_TOKEN) ? to_f32(a.gate[tb + p]) : 1.f;
   // delta = S_ref phi - v: NP threads per row i, each over DK / NP columns in 16-byte loads, summed
-  // across the NP lanes
+  // across the NP lanes. Every global load (S_ref, v, the gate, phi) is issued before the barrier
+  // that publishes phi, so the slot waits for one memory round trip.
   constexpr int NP = kThreads / DV, KP = DK / NP;
   static_assert(kThreads % DV == 0 && DK % (4 * NP) == 0 && (NP & (NP - 1)) == 0, "row split");
-  {
-    const int i = tid / NP, kp = tid % NP;
-    const float4* sr = reinterpret_cast<const float4*>(a.S_ref + ((size_t)bh * DV + i) * DK + kp * KP);
-    float4 x[KP / 4];
+  const int i = tid / NP, kp = tid % NP;
+  const float4* sr = reinterpret_cast<const float4*>(a.S_ref + ((size_t)bh * DV + i) * DK + kp * KP);
+  float4 x[KP / 4];
 #pragma unroll
-    for (int u = 0; u < KP / 4; ++u) x[u] = sr[u];
+  for (int u = 0; u < KP / 4; ++u) x[u] = sr[u];
+  const float vp = to_f32(a.v[(tb + p) * DV + i]);
+  const float gp = (g.gate_mode == GATE_TOKEN) ? to_f32(a.gate[tb + p]) : 1.f;
+  for (int k = tid; k < DK; k += kThreads) sphi[k] = ld_map(a.k, (tb + p) * DK + k, g.map_mode, g.map_deg);
+  __syncthreads();
+  {
     float acc = 0.f;
 #pragma unroll
     for (int u = 0; u < KP / 4; ++u) {
@@ -46,7 +48,7 @@ __device__ __forceinline__ void buffer_out_slot(const Geom& g, const FwdPtrs<T>&
     }
 #pragma unroll
     for (int o = NP / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
-    if (kp == 0) sdel[i] = gp * (acc - to_f32(a.v[(tb + p) * DV + i]));
+    if (kp == 0) sdel[i] = gp * (acc - vp);
   }
   __syncthreads();
   for (int idx = tid; idx < DV * DK; idx += kThreads) out[idx] = sdel[idx / DK] * sphi[idx % DK];
