@@ -338,8 +338,7 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
     rows_store<MAPE, WL_R>(pf, sm, g.map_deg, w);
     gates_store(sp, kargs()->g.e, sm);
     // the next chunk's scalars, early: waves 0, 1 form its record and prefix arrays at the end of R4
-    if (c > c_begin) scal_load(sp, t0 - CL);
-    else sp = ScalPf{};
+    scal_load(sp, c > c_begin ? t0 - CL : t0);   // unconditional (see the rows' prefetch in R3)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int kt = 2 * hf + j;
@@ -574,15 +573,13 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
       }
     };
 
-    // the next chunk's rows and state slice in flight from here to its R0 (the last chunk clears
-    // the registers instead: the values staged in R0 are dead from here on)
-    if (c > c_begin) {
-      rows_load<WL_R>(pf, t0 - CL, w);
-      xs_load(c - 1, xn);
-    } else {
-      pf = RowPf<WL_R>{};
-#pragma unroll
-      for (int v = 0; v < 8; ++v) xn[v] = 0u;
+    // the next chunk's rows and state slice in flight from here to its R0. Unconditional (the
+    // segment's first chunk loads itself again, never used): a load under a condition would make
+    // the next wait on any earlier load wait for every load issued so far.
+    {
+      const int cn = c > c_begin ? c - 1 : c;
+      rows_load<WL_R>(pf, cn * CL, w);
+      xs_load(cn, xn);
     }
     // ---- R3: ddelta, dv (waves 4-7) | scalar gradients (waves 0-3)
     if (hf == 1) {
