@@ -156,7 +156,25 @@ struct ScalPf {
   unsigned short al, et, be;
   unsigned short gt[3];
 };
-__device__ __forceinline__ void scal_load(ScalPf& p, int t0) {
+// The thread's three window slots i = tid + NTB u (target r = i / e, lag j = i - r e), formed once per
+// launch: bits 0-10 rc e + j (rc = min(r, CL - 1)), 11-16 rc, 17-21 j, 22 r < CL. Per chunk the
+// gate loads then need no division and no multiply.
+struct GateIdx {
+  unsigned v[3];
+};
+__device__ __forceinline__ GateIdx gate_idx(int tid, int e) {
+  GateIdx gx;
+#pragma unroll
+  for (int u = 0; u < 3; ++u) {
+    const int i = tid + NTB * u;
+    const int r = i / e, j = i - r * e, rc = min(r, CL - 1);
+    gx.v[u] = (unsigned)(rc * e + j) | ((unsigned)rc << 11) | ((unsigned)j << 17) | ((r < CL ? 1u : 0u) << 22);
+  }
+  return gx;
+}
+static_assert((CL - 1) * EMAX + EMAX - 1 < (1 << 11) && CL <= 64 && EMAX <= 32, "GateIdx fields");
+
+__device__ __forceinline__ void scal_load(ScalPf& p, int t0, const GateIdx& gx) {
   const int tid = fresh_tid();
   const CpK K = kargs();
   const int T = K->g.T, e = K->g.e, gm = K->g.gate_mode;
@@ -173,19 +191,20 @@ __device__ __forceinline__ void scal_load(ScalPf& p, int t0) {
   const unsigned short xb = __builtin_bit_cast(unsigned short, bsrc[o]);
   // window weight w(r, j) of target r, lag j: the lag gate, the gate of the source token t0 + r - j,
   // or 1; zero for targets past T
-  const bf16* gsrc = gm == GATE_NONE ? K->a.decay : K->a.gate;
+  // the row's gates: [T][e] (lag) or [T] (token; none: any valid tensor)
+  const bf16* grow = gm == GATE_NONE ? K->a.decay + rowbase : gm == GATE_LAG ? K->a.gate + rowbase * e : K->a.gate + rowbase;
   unsigned short xg[3];
   bool gok[3];
 #pragma unroll
   for (int u = 0; u < 3; ++u) {
-    const int i = tid + NTB * u;
-    const int r = i / e, j = i - r * e;
-    const int tr = t0 + min(r, CL - 1);   // the target token (clamped)
-    size_t gi;
-    if (gm == GATE_LAG) gi = (rowbase + min(tr, T - 1)) * e + j;
-    else gi = rowbase + min(max(tr - j, 0), T - 1);
-    xg[u] = __builtin_bit_cast(unsigned short, gsrc[gi]);
-    gok[u] = r < CL && tr < T && (gm != GATE_TOKEN || tr - j >= 0);
+    const unsigned pk = gx.v[u];
+    const int rce = (int)(pk & 0x7ffu), rc = (int)((pk >> 11) & 63u), j = (int)((pk >> 17) & 31u);
+    const int tr = t0 + rc;   // the target token (clamped row)
+    // lag: (tr, j) = element tr e + j, clamped into the row (a target past T is masked below);
+    // token: the gate of source tr - j, clamped into the row
+    const int gi = gm == GATE_LAG ? min(t0 * e + rce, T * e - 1) : min(max(tr - j, 0), T - 1);
+    xg[u] = __builtin_bit_cast(unsigned short, grow[gi]);
+    gok[u] = (pk >> 22) != 0u && tr < T && (gm != GATE_TOKEN || tr - j >= 0);
   }
   const bool sok = tid < 128 && ts < T;
   p.al = sok ? xa : (unsigned short)0x3f80;   // 1, 0, 1: the identity past T
@@ -194,13 +213,12 @@ __device__ __forceinline__ void scal_load(ScalPf& p, int t0) {
 #pragma unroll
   for (int u = 0; u < 3; ++u) p.gt[u] = gok[u] ? (gm == GATE_NONE ? (unsigned short)0x3f80 : xg[u]) : (unsigned short)0;
 }
-__device__ __forceinline__ void gates_store(const ScalPf& p, int e, BwSm& sm) {
-  const int tid = fresh_tid();
+__device__ __forceinline__ void gates_store(const ScalPf& p, const GateIdx& gx, BwSm& sm) {
 #pragma unroll
   for (int u = 0; u < 3; ++u) {
-    const int i = tid + NTB * u;
-    if (i < CL * e) {
-      const int r = i / e, j = i - r * e;
+    const unsigned pk = gx.v[u];
+    if ((pk >> 22) != 0u) {   // r < CL (then r = rc)
+      const int r = (int)((pk >> 11) & 63u), j = (int)((pk >> 17) & 31u);
       sm.Bd[r + HT - j][r] = __builtin_bit_cast(bf16, p.gt[u]);
     }
   }
@@ -312,7 +330,8 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
   RowPf<WL_R> pf;
   ScalPf sp;
   unsigned xn[8];   // the next chunk's state slice, in flight with its rows
-  scal_load(sp, (c_end - 1) * CL);
+  const GateIdx gxi = gate_idx(tid, g.e);
+  scal_load(sp, (c_end - 1) * CL, gxi);
   rows_load<WL_R>(pf, (c_end - 1) * CL, w);
   xs_load(c_end - 1, xn);
   // the last chunk's record and prefix arrays (every later chunk's are formed one step ahead)
@@ -336,9 +355,9 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
     // ---- R0: stage the chunk
     __syncthreads();
     rows_store<MAPE, WL_R>(pf, sm, g.map_deg, w);
-    gates_store(sp, kargs()->g.e, sm);
+    gates_store(sp, gxi, sm);
     // the next chunk's scalars, early: waves 0, 1 form its record and prefix arrays at the end of R4
-    scal_load(sp, c > c_begin ? t0 - CL : t0);   // unconditional (see the rows' prefetch in R3)
+    scal_load(sp, c > c_begin ? t0 - CL : t0, gxi);   // unconditional (see the rows' prefetch in R3)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int kt = 2 * hf + j;
