@@ -272,6 +272,33 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
   const int tail0 = tok1 - H;   // the segment's last H tokens: partial results for the fixup
   const size_t DD = (size_t)D * D;
 
+  // chunk-start states saved by the forward walk (walk_common.h fragment layout), one block per
+  // 64-token chunk of the row: this lane's slice X[16 q4 + 4 gq + r][16 kt + m] (kt = 2 hf + j) is
+  // one 8-byte half of fragment (kt, q4 >> 1)
+  auto xs_load = [&](int c, unsigned (&xv)[8]) {
+    const CpK K = kargs();
+    const unsigned char* blk = reinterpret_cast<const unsigned char*>(K->p.rw) + ((size_t)bh * K->g.nc + c) * kStateBlk;
+    const int ln = fresh_tid() & 63;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const uint32_t o = frag_off(2 * hf + jj, q4 >> 1, ln) + (q4 & 1) * 8;
+      const uint2 s2 = *reinterpret_cast<const uint2*>(blk + o);
+      const uint2 z2 = *reinterpret_cast<const uint2*>(blk + kStateBytes + o);
+      xv[4 * jj + 0] = s2.x; xv[4 * jj + 1] = s2.y;
+      xv[4 * jj + 2] = MOM ? z2.x : 0u; xv[4 * jj + 3] = MOM ? z2.y : 0u;
+    }
+  };
+
+  // the last chunk's loads go out first: its scalars, rows and state slice are in flight while
+  // S_ref, the segment-end adjoint and the zeroed LDS tables are set up
+  RowPf<WL_R> pf;
+  ScalPf sp;
+  unsigned xn[8];   // the next chunk's state slice, in flight with its rows
+  const GateIdx gxi = gate_idx(tid, g.e);
+  scal_load(sp, (c_end - 1) * CL, gxi);
+  rows_load<WL_R>(pf, (c_end - 1) * CL, w);
+  xs_load(c_end - 1, xn);
+
   bf16x8 sref[2];
   load_sref(a.S_ref + (size_t)bh * DD, q4, sref);
   // S_ref^T operand of dphi (waves 4-7, column tile q4): Bt[k = 16 q4 + m][i = 32 q + 8 gq + e]
@@ -290,22 +317,6 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
   // the Gram's entries that are never written stay zero
   for (int i = tid; i < QX * MQ / 2; i += NTB) reinterpret_cast<unsigned*>(&sm.Mt[0][0])[i] = 0u;
   __syncthreads();
-  // chunk-start states saved by the forward walk (walk_common.h fragment layout), one block per
-  // 64-token chunk of the row: this lane's slice X[16 q4 + 4 gq + r][16 kt + m] (kt = 2 hf + j) is
-  // one 8-byte half of fragment (kt, q4 >> 1)
-  auto xs_load = [&](int c, unsigned (&xv)[8]) {
-    const CpK K = kargs();
-    const unsigned char* blk = reinterpret_cast<const unsigned char*>(K->p.rw) + ((size_t)bh * K->g.nc + c) * kStateBlk;
-    const int ln = fresh_tid() & 63;
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const uint32_t o = frag_off(2 * hf + jj, q4 >> 1, ln) + (q4 & 1) * 8;
-      const uint2 s2 = *reinterpret_cast<const uint2*>(blk + o);
-      const uint2 z2 = *reinterpret_cast<const uint2*>(blk + kStateBytes + o);
-      xv[4 * jj + 0] = s2.x; xv[4 * jj + 1] = s2.y;
-      xv[4 * jj + 2] = MOM ? z2.x : 0u; xv[4 * jj + 3] = MOM ? z2.y : 0u;
-    }
-  };
 
   // ---------------------------------------------------------------- reverse pass
   float lS[2][4], lZ[2][4];
@@ -327,13 +338,6 @@ __global__ __launch_bounds__(NTB) void k_cp_bwd(const CpArgs A) {
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt) dsr[kt] = zero4();
 
-  RowPf<WL_R> pf;
-  ScalPf sp;
-  unsigned xn[8];   // the next chunk's state slice, in flight with its rows
-  const GateIdx gxi = gate_idx(tid, g.e);
-  scal_load(sp, (c_end - 1) * CL, gxi);
-  rows_load<WL_R>(pf, (c_end - 1) * CL, w);
-  xs_load(c_end - 1, xn);
   // the last chunk's record and prefix arrays (every later chunk's are formed one step ahead)
   if (w == 0) chunk_prefix(bf(sp.al), bf(sp.et), bf(sp.be), lane, sm.cc[(c_end - c_begin - 1) & 1]);
   if (w == 1) chunk_end_scan(g.T, bf(sp.al), bf(sp.et), bf(sp.be), (c_end - 1) * CL, lane, sm.cc[(c_end - c_begin - 1) & 1]);
