@@ -265,7 +265,7 @@ def run_c4(steps, warmup, cpu=True, cpu_sample_t=128):
     import ctypes
     import torch
     from atlas_rnn_amd import _lib
-    from atlas_rnn_amd.functional import memory_recurrence, tensor_feature_map, _ptr, _stream
+    from atlas_rnn_amd.functional import memory_recurrence, tensor_feature_map, symmetrized_tables, _ptr, _stream
     c = C4
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -289,8 +289,12 @@ def run_c4(steps, warmup, cpu=True, cpu_sample_t=128):
     gy = bf(dy_cpu)
     zeros = torch.zeros(bh, dv, dk, device=dev)
 
+    # P is a constant projection: its symmetrised tables are formed once and kept, as
+    # PolynomialFeatureMap keeps them for its buffer (one launch per dtype and device)
+    tables = symmetrized_tables(P, kin, torch.bfloat16)
+
     def feat(x):   # fused tensor-map kernels, elementwise map of degree 3 in their epilogue
-        return tensor_feature_map(x, P, degree=deg)
+        return tensor_feature_map(x, P, degree=deg, tables=tables)
 
     def step():
         y, S_T, Z_T, B_out = memory_recurrence(
