@@ -32,6 +32,14 @@ namespace atlas {
 
 namespace tm {
 constexpr int TN = 128;   // tokens per workgroup
+// Packed order of the symmetrised table's blocks at d = 64 (zero where b < a), by 32-wide k-steps:
+// blocks 0 .. 16 (the linear rows, rows a = 0 .. 15) over both k-steps b in [0, 64); blocks 17 .. 48
+// (rows 16 .. 47) over the upper k-step b in [32, 64); then eight quads kPackQuad + q, each four
+// 16-column pieces of rows a0 .. a0 + 3 (two per k-step): b in [16, 32) of rows 16 .. 31 (q < 4) and
+// b in [48, 64) of rows 48 .. 63 (q >= 4), a0 = 16 + 4 q or 48 + 4 (q - 4). 82 k-steps in all
+// instead of 98 with whole upper k-steps for rows 32 .. 63.
+constexpr int kPackQuad = 49;
+constexpr int kNPack = kPackQuad + 8;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -76,12 +84,23 @@ void k_tmap_fwd(long n_tok, const bf16* __restrict__ x, const bf16* __restrict__
   }
   // P^T block kb: columns kb*D .. of every feature row j (vector v: row v / (D/8), 8 columns)
   u32x4v pf0[PVT], pf1[PVT];
+  // PACK (the symmetrised table at d = 64): the packed block order of tm::kPackQuad; otherwise block
+  // kb is row kb - 1 of x x^T (kb 0: the linear rows). Blocks past the last read as zeros.
+  constexpr bool PACK = SYM && D == 64 && NS == 2;
+  constexpr int NBLK = PACK ? tm::kNPack : D + 1;
   auto p_load = [&](u32x4v (&pf)[PVT], int kb) {
 #pragma unroll
     for (int u = 0; u < PVT; ++u) {
       const int v = tid + u * NT;
       const int j = v / (D / 8), c8 = v % (D / 8);
-      pf[u] = bld16(rp, (v < PV && kb <= D) ? (uint32_t)((j * K + kb * D + c8 * 8) * 2) : kOob);
+      int col = kb * D + c8 * 8;
+      if constexpr (PACK) {
+        if (kb >= tm::kPackQuad) {   // four 16-column pieces: rows a0 + (c8 >> 1), columns lo + 8 (c8 & 1)
+          const int qv = kb - tm::kPackQuad, lo = qv < 4 ? 16 : 48, a0 = lo + 4 * (qv & 3);
+          col = (a0 + (c8 >> 1) + 1) * D + lo + 8 * (c8 & 1);
+        }
+      }
+      pf[u] = bld16(rp, (v < PV && kb < NBLK) ? (uint32_t)((j * K + col) * 2) : kOob);
     }
   };
   auto p_store = [&](const u32x4v (&pf)[PVT], int buf) {
@@ -119,6 +138,7 @@ void k_tmap_fwd(long n_tok, const bf16* __restrict__ x, const bf16* __restrict__
   auto block = [&](int kb, u32x4v (&pf)[PVT], auto s0c) {
     constexpr int S0 = decltype(s0c)::value;
     const int buf = kb & 1;
+
     float xa[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)   // x_a of the block's row a = kb - 1 (unused in block 0)
@@ -142,16 +162,62 @@ void k_tmap_fwd(long n_tok, const bf16* __restrict__ x, const bf16* __restrict__
         for (int nt = 0; nt < 2; ++nt) acc[jt][nt] = mma_bf16(fa, fb[nt], acc[jt][nt]);
       }
     }
-    if (kb < D) {
+    if (kb + 1 < NBLK) {
       p_store(pf, buf ^ 1);
       p_load(pf, kb + 3);   // past the last block: out-of-range loads (zeros), never stored
     }
     __syncthreads();
   };
-  // blocks 0 .. KS - 1 over every column tile, then (SYM) the blocks of rows a >= D / 2 from tile
-  // NS / 2 on; even blocks take register stage pf0, odd ones pf1
+  // a quad of the packed order: four half-rows, two per k-step
+  auto quad = [&](int kb, u32x4v (&pf)[PVT]) {
+    const int buf = kb & 1;
+    const int qv = kb - tm::kPackQuad, lo = qv < 4 ? 16 : 48, a0 = lo + 4 * (qv & 3);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      bf16x8 fb[2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int tok = 32 * rg + 16 * nt + i;
+        const float xa = static_cast<float>(sm.xs[tok][a0 + 2 * s + (g >> 1)]);
+        const bf16x8 xv = *reinterpret_cast<const bf16x8*>(&sm.xs[tok][lo + 8 * (g & 1)]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) fb[nt][e] = static_cast<bf16>(xa * static_cast<float>(xv[e]));
+      }
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt) {
+        const bf16x8 fa = frag_row(&sm.pt[buf][0][0], D + 8, FG * cg + 16 * jt, 32 * s);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[jt][nt] = mma_bf16(fa, fb[nt], acc[jt][nt]);
+      }
+    }
+    if (kb + 1 < NBLK) {
+      p_store(pf, buf ^ 1);
+      p_load(pf, kb + 3);
+    }
+    __syncthreads();
+  };
   using all_t = std::integral_constant<int, 0>;
   using hi_t = std::integral_constant<int, NS / 2>;
+  if constexpr (PACK) {
+    // blocks 0 .. 16 over both k-steps, 17 .. 48 (rows 16 .. 47) over the upper one, then the quads;
+    // even blocks take register stage pf0, odd ones pf1
+    static_assert(tm::kPackQuad % 2 == 1 && (NBLK - tm::kPackQuad) % 2 == 0, "block parity");
+    for (int kb = 0; kb < 16; kb += 2) {
+      block(kb, pf0, all_t{});
+      block(kb + 1, pf1, all_t{});
+    }
+    block(16, pf0, all_t{});
+    for (int kb = 17; kb < tm::kPackQuad; kb += 2) {
+      block(kb, pf1, hi_t{});
+      block(kb + 1, pf0, hi_t{});
+    }
+    for (int kb = tm::kPackQuad; kb + 1 < NBLK; kb += 2) {
+      quad(kb, pf1);
+      quad(kb + 1, pf0);
+    }
+  } else {
+  // blocks 0 .. KS - 1 over every column tile, then (SYM) the blocks of rows a >= D / 2 from tile
+  // NS / 2 on; even blocks take register stage pf0, odd ones pf1
   constexpr int KS = (SYM && NS > 1) ? D / 2 + 1 : D + 1;
   static_assert(KS % 2 == 1 && D % 2 == 0, "block parity");
   for (int kb = 0; kb + 1 < KS; kb += 2) {
@@ -166,6 +232,7 @@ void k_tmap_fwd(long n_tok, const bf16* __restrict__ x, const bf16* __restrict__
       block(kb + 1, pf1, hi_t{});
     }
     block(D, pf0, hi_t{});
+  }
   }
 
   // phi^T tiles: lane (g, i) holds phi[token 32 rg + 16 nt + i][feature FG cg + 16 jt + 4 g + r]

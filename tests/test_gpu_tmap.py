@@ -66,8 +66,9 @@ def test_tensor_map_parity(n, d, m, deg, dt):
     compare("dx", dx.float().cpu(), dref, tol)
 
 
-@pytest.mark.parametrize("dt", [BF16, F32], ids=["bf16", "fp32"])
-def test_symmetrized_table_and_both_forwards(dt):
+@pytest.mark.parametrize("dt,m", [(BF16, 128), (F32, 128), (BF16, 64), (BF16, 32)],
+                         ids=["bf16_m128", "fp32_m128", "bf16_m64", "bf16_m32"])
+def test_symmetrized_table_and_both_forwards(dt, m):
     """atlas_tensor_map_symmetrize against the table formed on the CPU (P's linear rows, then
     P[a][b] + P[b][a] above the diagonal, P[a][a] on it, zeros below; bit-exact after rounding the
     fp32 sum to the dtype) and its transpose; then atlas_tensor_map_fwd on P^T and
@@ -76,8 +77,8 @@ def test_symmetrized_table_and_both_forwards(dt):
     oracle's (fp64 autograd)."""
     from atlas_rnn_amd import _lib
     from atlas_rnn_amd.functional import _ptr, _stream
-    d, m, n = 64, 128, 257
-    _say(f"symmetrised tensor-map table {dt}")
+    d, n = 64, 257
+    _say(f"symmetrised tensor-map table {dt} m={m}")
     g = torch.Generator().manual_seed(777)
     bound = (6.0 / (d + d * d + m)) ** 0.5
     P = ((torch.rand(d + d * d, m, generator=g) * 2 - 1) * bound).to(dt)
