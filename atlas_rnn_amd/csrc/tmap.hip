@@ -369,6 +369,16 @@ __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, cons
     for (int bt = 0; bt < 2; ++bt)
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) gt[bt][nt] = zero4();
+    // SYM at d = 64: rows a in [16, 32) are zero for b < 16, the first tile of the lower feature half
+    if (SYM && D == 64 && cb == 0 && kb > D / 4 && kb <= D / 2) {   // wave-uniform
+#pragma unroll
+      for (int ks = 0; ks < NK; ++ks) {
+        const bf16x8 fp1 = frag_row(&sm.pb[buf][0][0], M + 8, 16, 32 * ks);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) gt[1][nt] = mma_bf16(fp1, fd[nt][ks], gt[1][nt]);
+      }
+      return;
+    }
 #pragma unroll
     for (int ks = 0; ks < NK; ++ks) {
       bf16x8 fp[2];
@@ -445,6 +455,12 @@ __global__ __launch_bounds__(64 * 4 * (D / 32)) void k_tmap_bwd(long n_tok, cons
       const int buf = kb & 1;
 #pragma unroll
       for (int bt = 0; bt < 2; ++bt) gt[bt] = zero4();
+      if (kb > 3 * D / 4) {   // rows a >= 48: zero for b < 48, the first tile of the upper half
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks)
+          gt[1] = mma_bf16(frag_row(&sm.pb[buf][0][0], M + 8, D / 2 + 16, 32 * ks), fdh[ks], gt[1]);
+        return;
+      }
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks) {
 #pragma unroll
