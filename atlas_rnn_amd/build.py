@@ -36,12 +36,15 @@ HIPCC_FLAGS = [
 ]
 
 
-# Per-source options. The ILP-first machine scheduler keeps more independent LDS reads and matrix
-# products in flight in the reverse chunk walk (k_cp_bwd, bound by latency at two waves per SIMD:
-# -1.5 to -2.4 % in same-box measurements). Kernels measured slower with it keep the default
-# (k_tmap_fwd +40 % with spills, k_tmap_bwd +3 %, k_walk_full +2 %, k_bwd_seg_agg +1 %).
-_ILP_SCHED = ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]
-SOURCE_FLAGS = {"chunk_bwd.hip": _ILP_SCHED}
+# Per-source options. The ILP-first machine schedulers keep more independent LDS reads and matrix
+# products in flight in two kernels bound by latency at two waves per SIMD: the reverse chunk walk
+# (k_cp_bwd, iterative ILP: -1.5 to -2.4 % in same-box measurements) and the adjoint aggregates
+# (k_bwd_seg_agg, max ILP: -2 to -5 %). Kernels measured slower with either keep the default (k_tmap_fwd,
+# k_tmap_bwd, k_walk_full, k_walk_agg).
+SOURCE_FLAGS = {
+    "chunk_bwd.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+    "seg_bwd.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+}
 
 
 def _hipcc() -> str:
